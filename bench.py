@@ -1,0 +1,261 @@
+"""Benchmark of the equivariant edge step on one MI355X.
+
+Workload: 50,000 atoms uniform in a periodic cube at
+0.1 atoms/A^3 (L = 79.37 A), directed cell list at rc = 5 A (E ~ 2.62 M edges,
+built by this package's HIP neighbor list), node features 128 x (0e+1o+2e+3o)
+~ N(0,1) fp32 in ir_mul layout, real harmonics l <= 3 of the edge vectors and
+per-edge weights from 8 Bessel functions x cosine cutoff -> 64 -> 64 -> 2944
+SiLU MLP (random init, seeded).  One step = forward (harmonics, radial basis,
+MLP, channelwise TP + scatter-sum to receivers) and backward with respect to
+node features and edge vectors.  Metric: M edges/s = E * steps / time.
+
+Prints one JSON line (the driver's contract) with a ``roofline`` object for the
+dominant HIP kernel (timed with HIP events on the stream it runs on) and a
+``cpu_baseline`` (the fp64 NumPy oracle on a bounded sample, rank 0, N=1).
+
+    python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu-baseline]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import platform
+import sys
+import time
+
+import numpy as np
+import torch
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, GB/s
+
+
+def parse():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=10)
+    p.add_argument("--warmup", type=int, default=3)
+    p.add_argument("--atoms", type=int, default=50_000)
+    p.add_argument("--channels", type=int, default=128)
+    p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--unsorted", action="store_true", help="keep atoms in random order (no spatial sort)")
+    p.add_argument("--seed", type=int, default=0)
+    return p.parse_args()
+
+
+def bessel_cutoff(r: torch.Tensor, rc: float, n: int, mu: torch.Tensor, sigma: torch.Tensor) -> torch.Tensor:
+    """8-Bessel basis with the reference's shift/scale (radial.py:117-147) times the cosine cutoff
+    (cutoff.py:56-75), as combined in MACE's EmbeddingBlock (mace.py:180-182)."""
+    freqs = torch.arange(1, n + 1, device=r.device, dtype=r.dtype) * (math.pi / rc)
+    rr = r.unsqueeze(-1)
+    phi = math.sqrt(2.0 / rc) * torch.sin(rr * freqs) / (rr + 1e-8)
+    phi = (phi - mu) / sigma
+    cut = 0.5 * (torch.cos(math.pi * r / rc) + 1.0) * (r < rc)
+    return phi * cut.unsqueeze(-1)
+
+
+def bessel_stats(rc: float, n: int):
+    r = torch.linspace(1e-8, rc, 4096, dtype=torch.float32)
+    freqs = torch.arange(1, n + 1, dtype=torch.float32) * (math.pi / rc)
+    phi = math.sqrt(2.0 / rc) * torch.sin(r[:, None] * freqs) / (r[:, None] + 1e-8)
+    return phi.mean(0), phi.std(0).clamp(min=1e-8)
+
+
+def make_system(n_atoms: int, seed: int, sort: bool, dev):
+    import molnex_amd.kernels  # noqa: F401
+
+    L = (n_atoms / 0.1) ** (1.0 / 3.0)
+    g = torch.Generator().manual_seed(seed)
+    pos = torch.rand((n_atoms, 3), generator=g, dtype=torch.float32) * L
+    if sort:
+        # spatial (cell) order, as MD codes and data pipelines keep atoms
+        cell = torch.floor(pos / (L / 16)).long().clamp(max=15)
+        key = (cell[:, 2] * 16 + cell[:, 1]) * 16 + cell[:, 0]
+        pos = pos[torch.argsort(key, stable=True)]
+    pos = pos.to(dev)
+    box = torch.eye(3, device=dev) * L
+    i, j, shifts, deltas, dist = torch.ops.molix.neighbor_list(pos, 5.0, box, True)
+    # edge (sender j -> receiver i); bond vector pos[receiver] - image(pos[sender]) = deltas
+    edge_index = torch.stack([j.long(), i.long()], dim=1)
+    return pos, box, edge_index, deltas.contiguous(), L
+
+
+class EdgeStep:
+    """forward + backward of SH x radial-MLP x channelwise TP + scatter (config 3)."""
+
+    def __init__(self, n_atoms, edge_index, vec, C, seed, dev):
+        from molnex_amd import kernels as K
+
+        self.K = K
+        self.N, self.E, self.C = n_atoms, edge_index.shape[0], C
+        self.config = K.tp_config_id([0, 1, 2, 3], [0, 1, 2, 3], [0, 1, 2, 3])
+        self.num_paths, self.nx, self.ny, self.no = K.tp_config_info(self.config)
+        g = torch.Generator(device="cpu").manual_seed(seed + 1)
+        self.x = torch.randn((n_atoms, self.nx * C), generator=g).to(dev).requires_grad_(True)
+        self.vec = vec.detach().clone().requires_grad_(True)
+        self.edge_index = edge_index
+        torch.manual_seed(seed + 2)
+        self.mlp = torch.nn.Sequential(
+            torch.nn.Linear(8, 64), torch.nn.SiLU(), torch.nn.Linear(64, 64), torch.nn.SiLU(),
+            torch.nn.Linear(64, self.num_paths * C)).to(dev)
+        for p in self.mlp.parameters():
+            p.requires_grad_(False)
+        self.mu, self.sigma = (t.to(dev) for t in bessel_stats(5.0, 8))
+        self.gout = torch.randn((n_atoms, self.no * C), generator=g).to(dev)
+
+    def step(self):
+        ops = torch.ops.molix
+        row_ptr, perm, snd = ops.edge_csr(self.edge_index, self.N)
+        Y = ops.spherical_harmonics(self.vec, 3)
+        r = torch.linalg.vector_norm(self.vec, dim=-1)
+        w = self.mlp(bessel_cutoff(r, 5.0, 8, self.mu, self.sigma))
+        out = ops.tp_scatter(self.x, Y, w, row_ptr, perm, snd, self.config, self.C)
+        self.x.grad = None
+        self.vec.grad = None
+        out.backward(self.gout)
+        return out
+
+
+def time_tp_kernels(step: EdgeStep, reps: int = 5):
+    """Average duration of the TP forward and backward launches (HIP events on the
+    current stream, which is the stream the kernels are enqueued on)."""
+    ops = torch.ops.molix
+    K = step.K
+    row_ptr, perm, snd = ops.edge_csr(step.edge_index, step.N)
+    with torch.no_grad():
+        Y = ops.spherical_harmonics(step.vec, 3)
+        r = torch.linalg.vector_norm(step.vec, dim=-1)
+        w = step.mlp(bessel_cutoff(r, 5.0, 8, step.mu, step.sigma))
+    x = step.x.detach()
+    fwd, bwd = [], []
+    for _ in range(reps):
+        e = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
+        e[0].record()
+        ops.tp_scatter(x, Y, w, row_ptr, perm, snd, step.config, step.C)
+        e[1].record()
+        e[2].record()
+        K.tp_scatter_backward(step.gout, x, Y, w, row_ptr, perm, snd, step.config, step.C, True, True, True)
+        e[3].record()
+        fwd.append(e[:2])
+        bwd.append(e[2:])
+    torch.cuda.synchronize()
+    tf = sum(a.elapsed_time(b) for a, b in fwd) / reps
+    tb = sum(a.elapsed_time(b) for a, b in bwd) / reps
+    return tf, tb
+
+
+def tp_bytes(N, E, C, P=23, NX=16, NY=16, NO=99):
+    """Algorithmic HBM bytes (each tensor once at its width; fp32, int32 CSR)."""
+    csr = E * 8 + (N + 1) * 4
+    fwd = 4 * (E * P * C + N * NO * C + N * NX * C + E * NY) + csr
+    bwd = 4 * (2 * E * P * C + N * NO * C + 2 * N * NX * C + 2 * E * NY) + csr
+    return fwd, bwd
+
+
+def cpu_baseline(edge_index, vec, x, C, mlp, mu, sigma, gout, target_s=15.0, max_edges=120_000):
+    """fp64 NumPy oracle (oracle/equivariant.py) on a bounded sample: the edges of the
+    first receivers (in CSR order), fwd + bwd, in chunks until ~target_s of CPU work."""
+    from threadpoolctl import threadpool_limits
+
+    from oracle import equivariant as O
+
+    irr = "0e+1o+2e+3o"
+    tp = O.ChannelwiseTP("+".join(f"{C}x{t}" for t in irr.split("+")), irr, irr, C)
+    order = torch.argsort(edge_index[:, 1], stable=True)[:max_edges]
+    with torch.no_grad():
+        v = vec.detach()[order]
+        Ys = O.sh(range(4), v.cpu().double().numpy())
+        ws = mlp(bessel_cutoff(torch.linalg.vector_norm(v, dim=-1), 5.0, 8, mu, sigma)).cpu().double().numpy()
+    ei = edge_index[order].cpu().numpy()
+    recv, ei[:, 1] = np.unique(ei[:, 1], return_inverse=True)
+    xn = x.detach().cpu().double().numpy()
+    gn = gout[torch.from_numpy(recv).to(gout.device)].cpu().double().numpy()
+    done, t_used, chunk = 0, 0.0, 4000
+    with threadpool_limits(1):
+        while t_used < target_s and done < len(ei):
+            sl = slice(done, done + chunk)
+            t0 = time.perf_counter()
+            tp.forward(xn, Ys[sl], ws[sl], ei[sl], len(recv))
+            tp.backward(xn, Ys[sl], ws[sl], ei[sl], gn)
+            t_used += time.perf_counter() - t0
+            done += len(Ys[sl])
+    return {
+        "value": round(done / t_used / 1e6, 6),
+        "unit": "M edges/s",
+        "cores": 1,
+        "kind": "port",
+        "sample": f"{done} edges of the config-3 graph (receiver-ordered prefix), channelwise TP + scatter "
+                  f"forward and backward in fp64 NumPy (oracle/equivariant.py), {t_used:.1f} s on 1 core; "
+                  f"harmonics and MLP weights precomputed",
+    }
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU; --gpus > 1 is not supported (see DESIGN.md, "
+                                   "'More than one GPU')"}))
+        sys.exit(2)
+    if not torch.cuda.is_available():
+        print(json.dumps({"error": "no GPU visible"}))
+        sys.exit(1)
+    dev = torch.device("cuda:0")
+    torch.backends.cuda.matmul.allow_tf32 = False
+    pos, box, edge_index, vec, L = make_system(args.atoms, args.seed, not args.unsorted, dev)
+    N, E = pos.shape[0], edge_index.shape[0]
+    step = EdgeStep(N, edge_index, vec, args.channels, args.seed, dev)
+    for _ in range(args.warmup):
+        step.step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step.step()
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    ms = dt / args.steps * 1e3
+    value = E * args.steps / dt / 1e6
+
+    tf, tb = time_tp_kernels(step)
+    bf, bb = tp_bytes(N, E, args.channels)
+    dom_t, dom_b, dom_name = (tb, bb, "tp_scatter_bwd") if tb >= tf else (tf, bf, "tp_scatter_fwd")
+    achieved = dom_b / (dom_t * 1e-3) / 1e9
+    roof = {
+        "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+        "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None, "kernel": dom_name,
+        "kernel_ms": round(dom_t, 3), "algorithmic_bytes": dom_b,
+        "other": {"tp_scatter_fwd_ms": round(tf, 3), "tp_scatter_fwd_GBs": round(bf / (tf * 1e-3) / 1e9, 1),
+                  "tp_scatter_bwd_ms": round(tb, 3), "tp_scatter_bwd_GBs": round(bb / (tb * 1e-3) / 1e9, 1)},
+    }
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = cpu_baseline(edge_index, step.vec, step.x, args.channels, step.mlp, step.mu, step.sigma, step.gout)
+        cpu["cpu_model"] = platform.processor() or platform.machine()
+    line = {
+        "metric": "M edges/s TP+scatter (fwd+bwd wrt node features and edge vectors)",
+        "value": round(value, 3),
+        "unit": "M edges/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp32",
+        "data": "synthetic (seeded uniform periodic box, random-init MLP weights, N(0,1) node features)",
+        "config": {"workload": "config 3: edge TP + scatter, 50k atoms, rc 5 A, 128 ch, l<=3, fwd+bwd",
+                   "atoms": N, "edges": E, "channels": args.channels, "box_A": round(L, 3),
+                   "spatially_sorted": not args.unsorted},
+        "roofline": roof,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,160 @@
+/*
+ * molnex C ABI — MI355X (gfx950) kernels for MolNex's equivariant message-passing
+ * hot path.  Plain pointers and sizes only: every tensor argument is a device
+ * pointer to contiguous row-major memory, every call is enqueued on the given
+ * HIP stream, returns an MNX_* status and never allocates memory the caller
+ * sees.  Scratch memory comes in through `workspace` (size from the matching
+ * *_workspace_bytes query).  mnx_last_error() gives the message of the last
+ * failing call on this thread.
+ *
+ * The reference exposes this path as torch custom ops (TORCH_LIBRARY(molix),
+ * src/molix/op/src/molix_library.cpp:16-43) plus the cuequivariance-backed
+ * modules of molrep; each entry point below names the reference interface it
+ * replaces.
+ */
+#ifndef MOLNEX_H
+#define MOLNEX_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ihipStream_t* mnx_stream_t; /* == hipStream_t */
+
+#define MNX_OK 0
+#define MNX_ERR_INVALID 1     /* bad argument (shape, size, null pointer) */
+#define MNX_ERR_UNSUPPORTED 2 /* configuration without a compiled kernel */
+#define MNX_ERR_HIP 3         /* HIP runtime error */
+#define MNX_ERR_WORKSPACE 4   /* workspace smaller than the query returned */
+
+const char* mnx_last_error(void);
+int mnx_abi_version(void);
+
+/* ------------------------------------------------------------------------ */
+/* Neighbor list (cell list).                                                */
+/*                                                                            */
+/* Replaces torch.ops.molix.get_neighbor_pairs                                */
+/* (molix_library.cpp:22-26; CPU get_neighbor_pairs.cpp:28-77, CUDA           */
+/* get_neighbor_pairs.cu:29-79,104-151) and the pair enumeration behind       */
+/* molix.data.tasks.NeighborList (src/molix/data/tasks/neighbor_list.py:67-103).
+ * Pair predicate and geometry are the reference CPU path's, bit for bit:     */
+/*   d = pos[i] - pos[j]; for k = 2,1,0: d -= rint(d[k] / box[k][k]) * box[k] */
+/*   dist = sqrt(fma(d2, d2, fma(d1, d1, d0 * d0)));                          */
+/*   keep if dist <= cutoff && dist > 0.                                      */
+/* box: device pointer to a 3x3 row-major lower-triangular cell (rows a, b, c */
+/* as in the reference), or NULL for open boundaries.                          */
+/* ------------------------------------------------------------------------ */
+
+#define MNX_NLIST_HALF 0 /* unordered pairs, i > j (reference half list) */
+#define MNX_NLIST_FULL 1 /* ordered pairs, i != j */
+
+#define MNX_NLIST_COMPACT 0    /* pairs sorted by (i, j) at slots 0..total-1 */
+#define MNX_NLIST_TRIANGULAR 1 /* HALF only: pair (i, j) at slot i*(i-1)/2 + j
+                                  (reference max_num_pairs == -1 layout) */
+
+size_t mnx_nlist_workspace_bytes(int64_t num_atoms);
+
+/* Stage 1: bin atoms into cells and count pairs.  Writes the total pair count
+ * to *d_total (device int64).  The workspace keeps the bins for stage 2. */
+int mnx_nlist_count_f32(const float* pos, int64_t num_atoms, double cutoff, const float* box,
+                        int32_t mode, void* workspace, size_t workspace_bytes, int64_t* d_total,
+                        mnx_stream_t stream);
+int mnx_nlist_count_f64(const double* pos, int64_t num_atoms, double cutoff, const double* box,
+                        int32_t mode, void* workspace, size_t workspace_bytes, int64_t* d_total,
+                        mnx_stream_t stream);
+
+/* Stage 2: write pairs sorted by (i, j) into slots [0, capacity); slots past
+ * the pair count get i = j = -1 and NaN geometry (the reference padding).
+ * idx_i / idx_j: int32 [capacity]; deltas (d above) [capacity][3];
+ * distances [capacity]; shifts [capacity][3] = image offset added to pos[j]
+ * (d = pos[i] - (pos[j] + shift)).  Any output pointer may be NULL. */
+int mnx_nlist_emit_f32(const float* pos, int64_t num_atoms, double cutoff, const float* box,
+                       int32_t mode, int32_t layout, const void* workspace, size_t workspace_bytes,
+                       int64_t capacity, int32_t* idx_i, int32_t* idx_j, float* deltas,
+                       float* distances, float* shifts, mnx_stream_t stream);
+int mnx_nlist_emit_f64(const double* pos, int64_t num_atoms, double cutoff, const double* box,
+                       int32_t mode, int32_t layout, const void* workspace, size_t workspace_bytes,
+                       int64_t capacity, int32_t* idx_i, int32_t* idx_j, double* deltas,
+                       double* distances, double* shifts, mnx_stream_t stream);
+
+/* Reverse-mode of get_neighbor_pairs w.r.t. positions (get_neighbor_pairs.cu:81-102):
+ * grad_pos[i] += g_d + d/dist * g_dist, grad_pos[j] -= the same, over valid slots
+ * (idx_i >= 0).  grad_pos must be zeroed by the caller. */
+int mnx_nlist_backward_f32(const int32_t* idx_i, const int32_t* idx_j, const float* deltas,
+                           const float* distances, const float* grad_deltas,
+                           const float* grad_distances, int64_t num_slots, int64_t num_atoms,
+                           float* grad_pos, mnx_stream_t stream);
+int mnx_nlist_backward_f64(const int32_t* idx_i, const int32_t* idx_j, const double* deltas,
+                           const double* distances, const double* grad_deltas,
+                           const double* grad_distances, int64_t num_slots, int64_t num_atoms,
+                           double* grad_pos, mnx_stream_t stream);
+
+/* ------------------------------------------------------------------------ */
+/* Receiver CSR of an edge list (the gather/scatter index behind ConvTP's     */
+/* indices_1 / indices_out, tensor_product.py:101-111).                       */
+/* edge_index: int64 [E][2], column 0 = sender, column 1 = receiver.          */
+/* row_ptr: int32 [N+1]; perm: int32 [E] = edge ids grouped by receiver, in   */
+/* ascending edge id within a receiver (deterministic); senders_sorted: int32 */
+/* [E] = sender of perm[k].  Edges with an index outside [0, N) are left out  */
+/* and counted in *d_invalid (device int32, may be NULL); the kernels below   */
+/* then leave their grad_Y / grad_w rows untouched, so callers must reject    */
+/* such edge lists.                                                           */
+/* ------------------------------------------------------------------------ */
+size_t mnx_csr_workspace_bytes(int64_t num_nodes, int64_t num_edges);
+int mnx_csr_build(const int64_t* edge_index, int64_t num_edges, int64_t num_nodes, int32_t* row_ptr,
+                  int32_t* perm, int32_t* senders_sorted, int32_t* d_invalid, void* workspace,
+                  size_t workspace_bytes, mnx_stream_t stream);
+
+/* ------------------------------------------------------------------------ */
+/* Real spherical harmonics, component normalisation, l <= 3, input vectors   */
+/* normalised inside (replaces cuet.SphericalHarmonics(ls, normalize=True),   */
+/* src/molrep/embedding/angular.py:89,104).  Output [n][(l_max+1)^2].         */
+/* ------------------------------------------------------------------------ */
+int mnx_sh_fwd_f32(const float* vec, int64_t n, int32_t l_max, float* out, mnx_stream_t stream);
+/* grad_vec[n][3] = d<grad_out, Y(vec)>/d vec (overwritten). */
+int mnx_sh_bwd_f32(const float* vec, const float* grad_out, int64_t n, int32_t l_max,
+                   float* grad_vec, mnx_stream_t stream);
+
+/* ------------------------------------------------------------------------ */
+/* Channelwise tensor product fused with gather/scatter (replaces             */
+/* cuet.ChannelWiseTensorProduct(..., layout=ir_mul, shared_weights=False,    */
+/* internal_weights=False) called with indices_1 / indices_out / size_out,    */
+/* src/molrep/interaction/tensor_product.py:72-79,104-111).                   */
+/*                                                                            */
+/*   out[r] = sum_{e: recv(e)=r} TP(x[send(e)], Y[e]; w[e])                   */
+/*                                                                            */
+/* A configuration is the set of l's in irreps_in1 (uniform multiplicity C,   */
+/* natural parity), in irreps_in2 (the harmonics) and in the output filter,   */
+/* each given as a bit mask over l = 0..3.  mnx_tp_config returns its id or   */
+/* -1 when no kernel was compiled for it.  Layouts (ir_mul):                  */
+/*   x   [N][sum_l1 (2l1+1) * C]        Y [E][sum_l2 (2l2+1)]                 */
+/*   w   [E][num_paths * C]  (path-major)  out [N][sum_paths (2l3+1) * C]     */
+/* ------------------------------------------------------------------------ */
+int mnx_tp_config(int32_t in_mask, int32_t sh_mask, int32_t out_mask);
+/* info[0] = num_paths, info[1] = x comps per channel, info[2] = Y comps,
+ * info[3] = out comps per channel. */
+int mnx_tp_config_info(int32_t config, int32_t* info);
+
+int mnx_tp_fwd_f32(int32_t config, int32_t channels, const float* x, const float* Y,
+                   const float* w, const int32_t* row_ptr, const int32_t* perm,
+                   const int32_t* senders_sorted, int64_t num_nodes, int64_t num_edges, float* out,
+                   mnx_stream_t stream);
+
+/* Gradients of <grad_out, out> w.r.t. x, Y and w.  grad_x is accumulated with
+ * atomics and must be zeroed by the caller; grad_Y and grad_w are overwritten.
+ * Any of grad_x / grad_Y / grad_w may be NULL when not needed. */
+size_t mnx_tp_bwd_workspace_bytes(int32_t config, int32_t channels, int64_t num_edges);
+int mnx_tp_bwd_f32(int32_t config, int32_t channels, const float* x, const float* Y,
+                   const float* w, const float* grad_out, const int32_t* row_ptr,
+                   const int32_t* perm, const int32_t* senders_sorted, int64_t num_nodes,
+                   int64_t num_edges, float* grad_x, float* grad_Y, float* grad_w,
+                   void* workspace, size_t workspace_bytes, mnx_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MOLNEX_H */

@@ -1,0 +1,127 @@
+// Receiver CSR of an (E, 2) int64 edge list [sender, receiver] -- the index
+// structure behind ConvTP's gather (indices_1) and scatter-sum (indices_out),
+// src/molrep/interaction/tensor_product.py:101-111.  Counting sort by receiver
+// (atomic slot claims), then each receiver's segment is sorted by edge id so
+// the result is deterministic.  Edges whose sender or receiver lies outside
+// [0, N) are left out and counted in *d_invalid.
+
+#include "common.h"
+#include "scan.h"
+
+namespace mnx {
+namespace {
+
+struct CsrWs {
+    int32_t* counts;
+    int32_t* fill;
+    int32_t* tiles;
+    int32_t* invalid;
+};
+
+CsrWs carve_csr(void* base, size_t bytes, int64_t N, size_t* used) {
+    Workspace ws{static_cast<char*>(base), bytes};
+    CsrWs w;
+    w.counts = ws.take<int32_t>(N + 1);
+    w.fill = ws.take<int32_t>(N + 1);
+    w.tiles = ws.take<int32_t>(scan_workspace_elems(N + 1));
+    w.invalid = ws.take<int32_t>(1);
+    *used = ws.used;
+    return w;
+}
+
+__device__ __forceinline__ bool edge_ok(const int64_t* ei, int64_t e, int64_t N) {
+    const int64_t s = ei[2 * e], r = ei[2 * e + 1];
+    return s >= 0 && s < N && r >= 0 && r < N;
+}
+
+__global__ void k_count_recv(const int64_t* __restrict__ ei, int64_t E, int64_t N, int32_t* __restrict__ counts,
+                             int32_t* __restrict__ invalid) {
+    const int64_t e = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (e >= E) return;
+    if (!edge_ok(ei, e, N)) {
+        atomicAdd(invalid, 1);
+        return;
+    }
+    atomicAdd(&counts[ei[2 * e + 1]], 1);
+}
+
+__global__ void k_place_edges(const int64_t* __restrict__ ei, int64_t E, int64_t N, const int32_t* __restrict__ row_ptr,
+                              int32_t* __restrict__ fill, int32_t* __restrict__ perm) {
+    const int64_t e = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (e >= E || !edge_ok(ei, e, N)) return;
+    const int64_t r = ei[2 * e + 1];
+    perm[row_ptr[r] + atomicAdd(&fill[r], 1)] = int32_t(e);
+}
+
+__global__ void k_sort_segments(const int64_t* __restrict__ ei, int64_t N, const int32_t* __restrict__ row_ptr,
+                                int32_t* __restrict__ perm, int32_t* __restrict__ snd) {
+    const int64_t r = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (r >= N) return;
+    const int b = row_ptr[r], e = row_ptr[r + 1];
+    for (int k = b + 1; k < e; ++k) {
+        const int v = perm[k];
+        int q = k - 1;
+        while (q >= b && perm[q] > v) {
+            perm[q + 1] = perm[q];
+            --q;
+        }
+        perm[q + 1] = v;
+    }
+    if (snd)
+        for (int k = b; k < e; ++k) snd[k] = int32_t(ei[2 * int64_t(perm[k])]);
+}
+
+__global__ void k_copy_invalid(const int32_t* __restrict__ src, int32_t* __restrict__ dst) { *dst = *src; }
+
+}  // namespace
+}  // namespace mnx
+
+using namespace mnx;
+
+extern "C" {
+
+size_t mnx_csr_workspace_bytes(int64_t N, int64_t E) {
+    (void)E;
+    size_t used = 0;
+    carve_csr(nullptr, 0, N < 0 ? 0 : N, &used);
+    return used + 256;
+}
+
+int mnx_csr_build(const int64_t* edge_index, int64_t E, int64_t N, int32_t* row_ptr, int32_t* perm,
+                  int32_t* senders_sorted, int32_t* d_invalid, void* workspace, size_t ws_bytes,
+                  mnx_stream_t stream_) {
+    clear_error();
+    hipStream_t stream = (hipStream_t)stream_;
+    MNX_REQUIRE(N >= 0 && N < (int64_t(1) << 31) && E >= 0 && E < (int64_t(1) << 31), "sizes out of range");
+    MNX_REQUIRE(row_ptr && (E == 0 || (edge_index && perm)), "null pointer argument");
+    size_t need = 0;
+    CsrWs w = carve_csr(workspace, ws_bytes, N, &need);
+    if (!workspace || ws_bytes < need) return set_error(MNX_ERR_WORKSPACE, "workspace %zu < %zu bytes", ws_bytes, need);
+    MNX_HIP_TRY(hipMemsetAsync(w.counts, 0, sizeof(int32_t) * (N + 1), stream));
+    MNX_HIP_TRY(hipMemsetAsync(w.fill, 0, sizeof(int32_t) * (N + 1), stream));
+    MNX_HIP_TRY(hipMemsetAsync(w.invalid, 0, sizeof(int32_t), stream));
+    const int tb = 256;
+    if (E > 0) {
+        hipLaunchKernelGGL(k_count_recv, dim3(ceil_div(E, tb)), dim3(tb), 0, stream, edge_index, E, N, w.counts,
+                           w.invalid);
+        MNX_CHECK_LAUNCH();
+    }
+    // row_ptr[0..N] = exclusive scan of counts[0..N] (counts[N] == 0, so row_ptr[N] = valid edges)
+    int rc = exclusive_scan<int32_t, int32_t>(w.counts, N + 1, row_ptr, w.tiles, (int32_t*)nullptr, stream);
+    if (rc) return rc;
+    if (E > 0 && N > 0) {
+        hipLaunchKernelGGL(k_place_edges, dim3(ceil_div(E, tb)), dim3(tb), 0, stream, edge_index, E, N, row_ptr,
+                           w.fill, perm);
+        MNX_CHECK_LAUNCH();
+        hipLaunchKernelGGL(k_sort_segments, dim3(ceil_div(N, tb)), dim3(tb), 0, stream, edge_index, N, row_ptr,
+                           perm, senders_sorted);
+        MNX_CHECK_LAUNCH();
+    }
+    if (d_invalid) {
+        hipLaunchKernelGGL(k_copy_invalid, dim3(1), dim3(1), 0, stream, w.invalid, d_invalid);
+        MNX_CHECK_LAUNCH();
+    }
+    return MNX_OK;
+}
+
+}  // extern "C"

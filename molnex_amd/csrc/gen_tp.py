@@ -1,0 +1,359 @@
+"""Generate the channelwise tensor-product kernels (``tp_gen.inc``).
+
+Each supported configuration (the l's of irreps_in1, of the harmonics and of
+the output filter) becomes straight-line HIP code with the real coupling
+coefficients of ``molnex_amd.irreps`` baked in as constants, so every register
+index is static.  Paths are split into groups by the l of irreps_in1; each
+group is one wavefront kernel per (receiver, channel block).
+
+Forward (per edge, per channel):   out_p[m3] += w_p * sum_m1 M_p[m3][m1] x[m1]
+  with the uniform matrix M_p[m3][m1] = sum_m2 c_p[m1,m2,m3] Y[m2].
+Backward (per receiver, per channel), with v_p[m1][m2] = sum_m3 c_p g_p[m3]
+computed once per receiver:
+  u_p[m1] = sum_m2 Y[m2] v_p[m1][m2]      -> grad_x[m1] += w_p u_p[m1]
+  s_p[m2] = sum_m1 x[m1] v_p[m1][m2]      -> grad_w_p = sum_m2 Y[m2] s_p[m2]
+                                           -> grad_Y[m2] += w_p s_p[m2] (summed over channels)
+
+Run as ``python -m molnex_amd.csrc.gen_tp`` (``build()`` does this).
+"""
+
+from __future__ import annotations
+
+import math
+import os
+import sys
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.dirname(os.path.dirname(HERE)))
+
+from molnex_amd.irreps import ChannelwiseTPDescriptor, coupling  # noqa: E402
+
+EPS = 1e-12
+
+
+def _irreps(ls, mul=1):
+    return " + ".join(f"{mul}x{l}{'e' if l % 2 == 0 else 'o'}" for l in ls)
+
+
+def _mask(ls):
+    m = 0
+    for l in ls:
+        m |= 1 << l
+    return m
+
+
+def _ls(mask):
+    return [l for l in range(4) if mask >> l & 1]
+
+
+# (in1 l's, harmonics l's, output filter l's)
+def config_list():
+    cfgs = []
+    for L in range(4):  # MACE as coded: hidden = C x (0..L), harmonics 0..L
+        cfgs.append((list(range(L + 1)), list(range(L + 1)), list(range(L + 1))))
+    for ins in ([0], [0, 1]):  # MACE with hidden 0e+1o, harmonics l <= 3
+        for outs in ([0, 1, 2, 3], [0, 1]):
+            cfgs.append((ins, [0, 1, 2, 3], outs))
+    # small shapes used by the reference's module tests
+    cfgs += [
+        ([0], [0, 1], [0]),
+        ([1], [0, 1], [1]),
+        ([0], [0, 1, 2], [0]),
+        ([0], [0, 1], [0, 1]),
+        ([0, 1], [0, 1, 2, 3], [0, 1, 2, 3]),
+    ]
+    seen, out = set(), []
+    for c in cfgs:
+        key = (_mask(c[0]), _mask(c[1]), _mask(c[2]))
+        if key not in seen:
+            seen.add(key)
+            out.append(c)
+    return out
+
+
+def f32(v: float) -> str:
+    return f"{float(np.float32(v)):.9e}f"
+
+
+class Cfg:
+    def __init__(self, idx, in_ls, sh_ls, out_ls):
+        self.idx = idx
+        self.in_ls, self.sh_ls, self.out_ls = in_ls, sh_ls, out_ls
+        d = ChannelwiseTPDescriptor(_irreps(in_ls), _irreps(sh_ls), _irreps(out_ls))
+        self.d = d
+        self.NX = sum(2 * l + 1 for l in in_ls)
+        self.NY = sum(2 * l + 1 for l in sh_ls)
+        self.NO = sum(b.ir.dim for b in d.irreps_out)
+        self.NP = d.num_paths
+        off1 = np.cumsum([0] + [2 * l + 1 for l in in_ls])
+        off2 = np.cumsum([0] + [2 * l + 1 for l in sh_ls])
+        off3 = np.cumsum([0] + [b.ir.dim for b in d.irreps_out])
+        self.paths = []
+        for k, p in enumerate(d.paths):
+            coef = math.sqrt(2 * p.l3 + 1) * coupling(p.l1, p.l2, p.l3)
+            self.paths.append(
+                dict(k=k, l1=p.l1, l2=p.l2, l3=p.l3, o1=int(off1[p.i1]), o2=int(off2[p.i2]),
+                     o3=int(off3[p.out_block]), c=coef)
+            )
+        self.groups = []
+        for l1 in in_ls:
+            ps = [p for p in self.paths if p["l1"] == l1]
+            if ps:
+                self.groups.append(ps)
+
+    @property
+    def masks(self):
+        return _mask(self.in_ls), _mask(self.sh_ls), _mask(self.out_ls)
+
+
+def _uniq(seq):
+    out = []
+    for s in seq:
+        if s not in out:
+            out.append(s)
+    return out
+
+
+def gen_fwd(cfg: Cfg, g: int) -> str:
+    ps = cfg.groups[g]
+    xs = _uniq([p["o1"] + m for p in ps for m in range(2 * p["l1"] + 1)])
+    ys = _uniq([p["o2"] + m for p in ps for m in range(2 * p["l2"] + 1)])
+    outs = [p["o3"] + m for p in ps for m in range(2 * p["l3"] + 1)]
+    xi = {c: i for i, c in enumerate(xs)}
+    oi = {c: i for i, c in enumerate(outs)}
+    L = []
+    a = L.append
+    name = f"tp_fwd_c{cfg.idx}_g{g}"
+    a(f"template <int CPL>\n__global__ void __launch_bounds__(64) {name}(const float* __restrict__ x, "
+      "const float* __restrict__ Y, const float* __restrict__ w, const int32_t* __restrict__ row_ptr, "
+      "const int32_t* __restrict__ perm, const int32_t* __restrict__ snd, int64_t N, int C, "
+      "float* __restrict__ out) {")
+    a("  const int64_t n = xcd_node(blockIdx.x, gridDim.x);")
+    a("  if (n >= N) return;")
+    a("  const int lane = threadIdx.x;")
+    a("  int cc[CPL]; bool ok[CPL];")
+    a("#pragma unroll")
+    a("  for (int k = 0; k < CPL; ++k) { cc[k] = blockIdx.y * (64 * CPL) + 64 * k + lane; ok[k] = cc[k] < C; }")
+    a(f"  float acc[CPL][{len(outs)}];")
+    a("#pragma unroll")
+    a(f"  for (int k = 0; k < CPL; ++k)\n#pragma unroll\n    for (int i = 0; i < {len(outs)}; ++i) acc[k][i] = 0.f;")
+    a(f"  const int64_t XS = int64_t({cfg.NX}) * C, WS = int64_t({cfg.NP}) * C;")
+    a("  const int beg = row_ptr[n], end = row_ptr[n + 1];")
+    a("  for (int t = beg; t < end; ++t) {")
+    a("    const int e = perm[t], s = snd[t];")
+    a(f"    const float* __restrict__ Ye = Y + int64_t(e) * {cfg.NY};")
+    for c in ys:
+        a(f"    const float y{c} = Ye[{c}];")
+    a("    const float* __restrict__ xs = x + int64_t(s) * XS;")
+    a("    const float* __restrict__ we = w + int64_t(e) * WS;")
+    a(f"    float xv[CPL][{len(xs)}], wv[CPL][{len(ps)}];")
+    a("#pragma unroll")
+    a("    for (int k = 0; k < CPL; ++k) {")
+    for c in xs:
+        a(f"      xv[k][{xi[c]}] = ok[k] ? xs[{c} * C + cc[k]] : 0.f;")
+    for j, p in enumerate(ps):
+        a(f"      wv[k][{j}] = ok[k] ? __builtin_nontemporal_load(we + {p['k']} * C + cc[k]) : 0.f;")
+    a("    }")
+    # uniform coupling matrices M_p[m3][m1]
+    for j, p in enumerate(ps):
+        c = p["c"]
+        for m3 in range(2 * p["l3"] + 1):
+            for m1 in range(2 * p["l1"] + 1):
+                terms = [(m2, c[m1, m2, m3]) for m2 in range(2 * p["l2"] + 1) if abs(c[m1, m2, m3]) > EPS]
+                if not terms:
+                    continue
+                expr = f"{f32(terms[0][1])} * y{p['o2'] + terms[0][0]}"
+                for m2, v in terms[1:]:
+                    expr = f"fmaf({f32(v)}, y{p['o2'] + m2}, {expr})"
+                a(f"    const float M{j}_{m3}_{m1} = {expr};")
+    a("#pragma unroll")
+    a("    for (int k = 0; k < CPL; ++k) {")
+    for j, p in enumerate(ps):
+        c = p["c"]
+        for m3 in range(2 * p["l3"] + 1):
+            m1s = [m1 for m1 in range(2 * p["l1"] + 1)
+                   if any(abs(c[m1, m2, m3]) > EPS for m2 in range(2 * p["l2"] + 1))]
+            if not m1s:
+                continue
+            expr = f"M{j}_{m3}_{m1s[0]} * xv[k][{xi[p['o1'] + m1s[0]]}]"
+            for m1 in m1s[1:]:
+                expr = f"fmaf(M{j}_{m3}_{m1}, xv[k][{xi[p['o1'] + m1]}], {expr})"
+            o = oi[p["o3"] + m3]
+            a(f"      acc[k][{o}] = fmaf(wv[k][{j}], {expr}, acc[k][{o}]);")
+    a("    }")
+    a("  }")
+    a(f"  float* __restrict__ on = out + n * int64_t({cfg.NO}) * C;")
+    a("#pragma unroll")
+    a("  for (int k = 0; k < CPL; ++k) {")
+    a("    if (!ok[k]) continue;")
+    for c in outs:
+        a(f"    on[{c} * C + cc[k]] = acc[k][{oi[c]}];")
+    a("  }")
+    a("}")
+    return "\n".join(L)
+
+
+def gen_bwd(cfg: Cfg, g: int) -> str:
+    ps = cfg.groups[g]
+    xs = _uniq([p["o1"] + m for p in ps for m in range(2 * p["l1"] + 1)])
+    ys = _uniq([p["o2"] + m for p in ps for m in range(2 * p["l2"] + 1)])
+    outs = [p["o3"] + m for p in ps for m in range(2 * p["l3"] + 1)]
+    xi = {c: i for i, c in enumerate(xs)}
+    oi = {c: i for i, c in enumerate(outs)}
+    V = 1
+    while V < cfg.NY:
+        V *= 2
+    L = []
+    a = L.append
+    name = f"tp_bwd_c{cfg.idx}_g{g}"
+    a(f"template <int CPL>\n__global__ void __launch_bounds__(64) {name}(const float* __restrict__ x, "
+      "const float* __restrict__ Y, const float* __restrict__ w, const float* __restrict__ gout, "
+      "const int32_t* __restrict__ row_ptr, const int32_t* __restrict__ perm, const int32_t* __restrict__ snd, "
+      "int64_t N, int C, float* __restrict__ gx, float* __restrict__ gw, float* __restrict__ gyp, int npart) {")
+    a("  const int64_t n = xcd_node(blockIdx.x, gridDim.x);")
+    a("  if (n >= N) return;")
+    a("  const int lane = threadIdx.x;")
+    a("  int cc[CPL]; bool ok[CPL];")
+    a("#pragma unroll")
+    a("  for (int k = 0; k < CPL; ++k) { cc[k] = blockIdx.y * (64 * CPL) + 64 * k + lane; ok[k] = cc[k] < C; }")
+    a(f"  const int pidx = {g} * gridDim.y + blockIdx.y;")
+    a(f"  const int64_t XS = int64_t({cfg.NX}) * C, WS = int64_t({cfg.NP}) * C;")
+    a(f"  const float* __restrict__ gn = gout + n * int64_t({cfg.NO}) * C;")
+    # v_p[m1][m2] per channel, from g
+    vnames = {}
+    a(f"  float v[CPL][{sum(1 for p in ps for m1 in range(2*p['l1']+1) for m2 in range(2*p['l2']+1) if np.any(np.abs(p['c'][m1, m2, :]) > EPS))}];")
+    a("#pragma unroll")
+    a("  for (int k = 0; k < CPL; ++k) {")
+    a(f"    float gv[{len(outs)}];")
+    for c in outs:
+        a(f"    gv[{oi[c]}] = ok[k] ? gn[{c} * C + cc[k]] : 0.f;")
+    vi = 0
+    for j, p in enumerate(ps):
+        c = p["c"]
+        for m1 in range(2 * p["l1"] + 1):
+            for m2 in range(2 * p["l2"] + 1):
+                terms = [(m3, c[m1, m2, m3]) for m3 in range(2 * p["l3"] + 1) if abs(c[m1, m2, m3]) > EPS]
+                if not terms:
+                    continue
+                expr = f"{f32(terms[0][1])} * gv[{oi[p['o3'] + terms[0][0]]}]"
+                for m3, val in terms[1:]:
+                    expr = f"fmaf({f32(val)}, gv[{oi[p['o3'] + m3]}], {expr})"
+                a(f"    v[k][{vi}] = {expr};")
+                vnames[(j, m1, m2)] = vi
+                vi += 1
+    a("  }")
+    a("  const int beg = row_ptr[n], end = row_ptr[n + 1];")
+    a("  for (int t = beg; t < end; ++t) {")
+    a("    const int e = perm[t], s = snd[t];")
+    a(f"    const float* __restrict__ Ye = Y + int64_t(e) * {cfg.NY};")
+    for c in ys:
+        a(f"    const float y{c} = Ye[{c}];")
+    a("    const float* __restrict__ xs = x + int64_t(s) * XS;")
+    a("    float* __restrict__ gwe = gw ? gw + int64_t(e) * WS : nullptr;")
+    a("    const float* __restrict__ we = w + int64_t(e) * WS;")
+    a(f"    float gy[{V}];")
+    a("#pragma unroll")
+    a(f"    for (int i = 0; i < {V}; ++i) gy[i] = 0.f;")
+    a("#pragma unroll")
+    a("    for (int k = 0; k < CPL; ++k) {")
+    a(f"      float xv[{len(xs)}], wv[{len(ps)}], gxl[{len(xs)}];")
+    for c in xs:
+        a(f"      xv[{xi[c]}] = ok[k] ? xs[{c} * C + cc[k]] : 0.f;")
+        a(f"      gxl[{xi[c]}] = 0.f;")
+    for j, p in enumerate(ps):
+        a(f"      wv[{j}] = ok[k] ? __builtin_nontemporal_load(we + {p['k']} * C + cc[k]) : 0.f;")
+    for j, p in enumerate(ps):
+        n1, n2 = 2 * p["l1"] + 1, 2 * p["l2"] + 1
+        # u[m1] = sum_m2 y v ; s[m2] = sum_m1 x v
+        for m1 in range(n1):
+            ts = [m2 for m2 in range(n2) if (j, m1, m2) in vnames]
+            if not ts:
+                continue
+            expr = f"y{p['o2'] + ts[0]} * v[k][{vnames[(j, m1, ts[0])]}]"
+            for m2 in ts[1:]:
+                expr = f"fmaf(y{p['o2'] + m2}, v[k][{vnames[(j, m1, m2)]}], {expr})"
+            a(f"      const float u{j}_{m1} = {expr};")
+            a(f"      gxl[{xi[p['o1'] + m1]}] = fmaf(wv[{j}], u{j}_{m1}, gxl[{xi[p['o1'] + m1]}]);")
+        svals = []
+        for m2 in range(n2):
+            ts = [m1 for m1 in range(n1) if (j, m1, m2) in vnames]
+            if not ts:
+                continue
+            expr = f"xv[{xi[p['o1'] + ts[0]]}] * v[k][{vnames[(j, ts[0], m2)]}]"
+            for m1 in ts[1:]:
+                expr = f"fmaf(xv[{xi[p['o1'] + m1]}], v[k][{vnames[(j, m1, m2)]}], {expr})"
+            a(f"      const float s{j}_{m2} = {expr};")
+            a(f"      gy[{p['o2'] + m2}] = fmaf(wv[{j}], s{j}_{m2}, gy[{p['o2'] + m2}]);")
+            svals.append(m2)
+        if svals:
+            expr = f"y{p['o2'] + svals[0]} * s{j}_{svals[0]}"
+            for m2 in svals[1:]:
+                expr = f"fmaf(y{p['o2'] + m2}, s{j}_{m2}, {expr})"
+        else:
+            expr = "0.f"
+        a(f"      if (gwe && ok[k]) __builtin_nontemporal_store({expr}, gwe + {p['k']} * C + cc[k]);")
+    a("      if (gx && ok[k]) {")
+    a("        float* __restrict__ gxs = gx + int64_t(s) * XS;")
+    for c in xs:
+        a(f"        atomicAdd(gxs + {c} * C + cc[k], gxl[{xi[c]}]);")
+    a("      }")
+    a("    }")
+    a("    if (gyp) {")
+    a(f"      float r = wave_reduce_scatter<{V}>(gy, lane);")
+    a(f"      const int comp = reduce_scatter_index<{V}>(lane);")
+    a(f"      if ((lane & (64 / {V} - 1)) == 0 && comp < {cfg.NY}) gyp[(int64_t(e) * npart + pidx) * {cfg.NY} + comp] = r;")
+    a("    }")
+    a("  }")
+    a("}")
+    return "\n".join(L)
+
+
+def generate() -> str:
+    cfgs = [Cfg(i, *c) for i, c in enumerate(config_list())]
+    out = ["// Generated by gen_tp.py -- do not edit.", "// clang-format off", ""]
+    for cfg in cfgs:
+        im, sm, om = cfg.masks
+        out.append(f"// config {cfg.idx}: in l={cfg.in_ls} sh l={cfg.sh_ls} out l={cfg.out_ls}; "
+                   f"{cfg.NP} paths, NX={cfg.NX} NY={cfg.NY} NO={cfg.NO}")
+        for g in range(len(cfg.groups)):
+            out.append(gen_fwd(cfg, g))
+            out.append("")
+            out.append(gen_bwd(cfg, g))
+            out.append("")
+    # dispatch tables
+    out.append("static const TPConfigInfo kTPConfigs[] = {")
+    for cfg in cfgs:
+        im, sm, om = cfg.masks
+        out.append(f"  {{{im}, {sm}, {om}, {cfg.NP}, {cfg.NX}, {cfg.NY}, {cfg.NO}, {len(cfg.groups)}}},")
+    out.append("};")
+    out.append(f"static constexpr int kNumTPConfigs = {len(cfgs)};")
+    for cpl in (1, 2):
+        out.append(f"static const TPFwdFn kTPFwd{cpl}[][4] = {{")
+        for cfg in cfgs:
+            fns = [f"tp_fwd_c{cfg.idx}_g{g}<{cpl}>" for g in range(len(cfg.groups))]
+            fns += ["nullptr"] * (4 - len(fns))
+            out.append("  {" + ", ".join(fns) + "},")
+        out.append("};")
+        out.append(f"static const TPBwdFn kTPBwd{cpl}[][4] = {{")
+        for cfg in cfgs:
+            fns = [f"tp_bwd_c{cfg.idx}_g{g}<{cpl}>" for g in range(len(cfg.groups))]
+            fns += ["nullptr"] * (4 - len(fns))
+            out.append("  {" + ", ".join(fns) + "},")
+        out.append("};")
+    return "\n".join(out) + "\n"
+
+
+def main():
+    path = os.path.join(HERE, "tp_gen.inc")
+    text = generate()
+    old = open(path).read() if os.path.exists(path) else None
+    if old != text:
+        with open(path, "w") as f:
+            f.write(text)
+    return path
+
+
+if __name__ == "__main__":
+    print(main())

@@ -1,0 +1,602 @@
+// Cell-list neighbor list for gfx950.
+//
+// Replaces the O(N^2) pair enumeration of torch.ops.molix.get_neighbor_pairs
+// (reference CPU src/molix/op/src/neighbors/get_neighbor_pairs.cpp:28-77, CUDA
+// get_neighbor_pairs.cu:29-79) with a cell list, while keeping the reference
+// CPU path's pair predicate and geometry bit for bit:
+//   d = pos[i] - pos[j]                                      (.cpp:44)
+//   for k = 2, 1, 0: d -= rint(d[k] / box[k][k]) * box[k]   (.cpp:45-49; torch::round is
+//                                                             round-half-even)
+//   dist = sqrt(fma(d2, d2, fma(d1, d1, d0 * d0)))            (linalg_vector_norm, .cpp:50)
+//   keep iff dist <= cutoff && dist > 0                       (.cpp:52)
+// Output is sorted by (i, j) like the CPU enumeration order (.cpp:38-43), which
+// the CUDA reference does not guarantee (atomicAdd slots, .cu:69).
+//
+// Layout of the work: atoms are binned into cells whose slab widths exceed the
+// cutoff (fractional coordinates for periodic cells), one wavefront per atom
+// scans the 27 neighbouring cells, compacts the accepted j with a ballot into
+// LDS, bitonic-sorts them there and writes its segment with coalesced stores.
+// This translation unit is compiled with -ffp-contract=off.
+
+#include <math.h>
+
+#include <algorithm>
+
+#include "common.h"
+#include "scan.h"
+
+namespace mnx {
+namespace {
+
+constexpr int kNlCap = 4096;  // max neighbours of one atom (LDS list per wave)
+constexpr float kCellMargin = 1.0001f;
+
+struct NlGrid {
+    int32_t brute;  // 1: all-pairs scan (periodic axis with < 3 cells)
+    int32_t periodic;
+    int32_t n[3];
+    int32_t ncells;
+    int32_t overflow;  // set when an atom has more than kNlCap neighbours
+    int32_t pad;
+    double lo[3];
+    double inv_w[3];
+    double rinv[6];  // inverse of the lower-triangular cell: f_c = z*r5, ...
+};
+
+struct NlWs {
+    NlGrid* grid;
+    int32_t* cell_of;
+    int32_t* cell_count;
+    int32_t* cell_start;
+    int32_t* cell_fill;
+    int32_t* atoms_sorted;
+    int32_t* counts;
+    int64_t* offsets;
+    int64_t* total;
+    int64_t* tiles64;
+    int32_t* tiles32;
+    int64_t max_cells;
+};
+
+int64_t max_cells_for(int64_t n) { return 2 * n + 64; }
+
+NlWs carve(void* base, size_t bytes, int64_t n, size_t* used) {
+    Workspace ws{static_cast<char*>(base), bytes};
+    NlWs w;
+    w.max_cells = max_cells_for(n);
+    w.grid = ws.take<NlGrid>(1);
+    w.cell_of = ws.take<int32_t>(n > 0 ? n : 1);
+    w.cell_count = ws.take<int32_t>(w.max_cells);
+    w.cell_start = ws.take<int32_t>(w.max_cells + 1);
+    w.cell_fill = ws.take<int32_t>(w.max_cells);
+    w.atoms_sorted = ws.take<int32_t>(n > 0 ? n : 1);
+    w.counts = ws.take<int32_t>(n > 0 ? n : 1);
+    w.offsets = ws.take<int64_t>(n + 1);
+    w.total = ws.take<int64_t>(1);
+    w.tiles64 = ws.take<int64_t>(scan_workspace_elems(n));
+    w.tiles32 = ws.take<int32_t>(scan_workspace_elems(w.max_cells));
+    *used = ws.used;
+    return w;
+}
+
+// ---------------------------------------------------------------------------
+// Exact reference geometry
+// ---------------------------------------------------------------------------
+
+template <typename T>
+struct Geo {
+    T d[3];
+    T dist;
+    T shift[3];
+};
+
+__device__ __forceinline__ float fma_(float a, float b, float c) { return fmaf(a, b, c); }
+__device__ __forceinline__ double fma_(double a, double b, double c) { return fma(a, b, c); }
+__device__ __forceinline__ float rint_(float a) { return rintf(a); }
+__device__ __forceinline__ double rint_(double a) { return rint(a); }
+__device__ __forceinline__ float sqrt_(float a) { return sqrtf(a); }
+__device__ __forceinline__ double sqrt_(double a) { return sqrt(a); }
+
+// Geometry of the pair (hi, lo) with hi > lo, in the reference's orientation.
+template <typename T>
+__device__ __forceinline__ void pair_geo(const T* __restrict__ pos, const T* __restrict__ box, int hi, int lo,
+                                         bool periodic, bool want_shift, Geo<T>& g) {
+    T d0 = pos[3 * hi + 0] - pos[3 * lo + 0];
+    T d1 = pos[3 * hi + 1] - pos[3 * lo + 1];
+    T d2 = pos[3 * hi + 2] - pos[3 * lo + 2];
+    T s0 = 0, s1 = 0, s2 = 0;
+    if (periodic) {
+#pragma unroll
+        for (int k = 2; k >= 0; --k) {
+            const T dk = k == 2 ? d2 : (k == 1 ? d1 : d0);
+            const T s = rint_(dk / box[4 * k]);
+            const T b0 = s * box[3 * k + 0], b1 = s * box[3 * k + 1], b2 = s * box[3 * k + 2];
+            d0 = d0 - b0;
+            d1 = d1 - b1;
+            d2 = d2 - b2;
+            if (want_shift) {
+                s0 = s0 + b0;
+                s1 = s1 + b1;
+                s2 = s2 + b2;
+            }
+        }
+    }
+    g.d[0] = d0;
+    g.d[1] = d1;
+    g.d[2] = d2;
+    g.dist = sqrt_(fma_(d2, d2, fma_(d1, d1, d0 * d0)));
+    g.shift[0] = s0;
+    g.shift[1] = s1;
+    g.shift[2] = s2;
+}
+
+template <typename T>
+__device__ __forceinline__ bool accept(const T* pos, const T* box, int i, int j, bool periodic, T cutoff) {
+    Geo<T> g;
+    pair_geo<T>(pos, box, i > j ? i : j, i > j ? j : i, periodic, false, g);
+    return g.dist <= cutoff && g.dist > T(0);
+}
+
+// ---------------------------------------------------------------------------
+// Grid set-up and binning
+// ---------------------------------------------------------------------------
+
+template <typename T>
+__global__ void __launch_bounds__(1024) k_grid_setup(const T* __restrict__ pos, int64_t n, const T* __restrict__ box,
+                                                     double cutoff, int64_t max_cells, NlGrid* __restrict__ grid) {
+    __shared__ double smin[3][1024], smax[3][1024];
+    const int t = threadIdx.x;
+    double mn[3] = {1e300, 1e300, 1e300}, mx[3] = {-1e300, -1e300, -1e300};
+    if (!box) {
+        for (int64_t i = t; i < n; i += 1024)
+            for (int k = 0; k < 3; ++k) {
+                double v = double(pos[3 * i + k]);
+                mn[k] = fmin(mn[k], v);
+                mx[k] = fmax(mx[k], v);
+            }
+    }
+    for (int k = 0; k < 3; ++k) {
+        smin[k][t] = mn[k];
+        smax[k][t] = mx[k];
+    }
+    __syncthreads();
+    for (int off = 512; off > 0; off >>= 1) {
+        if (t < off)
+            for (int k = 0; k < 3; ++k) {
+                smin[k][t] = fmin(smin[k][t], smin[k][t + off]);
+                smax[k][t] = fmax(smax[k][t], smax[k][t + off]);
+            }
+        __syncthreads();
+    }
+    if (t != 0) return;
+    NlGrid g{};
+    const double cw = cutoff * double(kCellMargin) + 1e-12;
+    if (box) {
+        const double ax = box[0], bx = box[3], by = box[4], cx = box[6], cy = box[7], cz = box[8];
+        // perpendicular slab widths of the lower-triangular cell
+        const double vol = fabs(ax * by * cz);
+        const double bxc = sqrt((by * cz) * (by * cz) + (bx * cz) * (bx * cz) + (bx * cy - by * cx) * (bx * cy - by * cx));
+        const double axc = sqrt((ax * cz) * (ax * cz) + (ax * cy) * (ax * cy));
+        const double h[3] = {vol / bxc, vol / axc, fabs(cz)};
+        g.periodic = 1;
+        for (int k = 0; k < 3; ++k) {
+            double m = floor(h[k] / cw);
+            g.n[k] = m < 1 ? 1 : (m > 1024 ? 1024 : int(m));
+        }
+        g.rinv[0] = 1.0 / ax;
+        g.rinv[1] = bx;
+        g.rinv[2] = 1.0 / by;
+        g.rinv[3] = cx;
+        g.rinv[4] = cy;
+        g.rinv[5] = 1.0 / cz;
+        while (int64_t(g.n[0]) * g.n[1] * g.n[2] > max_cells) {
+            int kmax = g.n[0] >= g.n[1] ? (g.n[0] >= g.n[2] ? 0 : 2) : (g.n[1] >= g.n[2] ? 1 : 2);
+            g.n[kmax] = (g.n[kmax] + 1) / 2;
+        }
+        g.brute = (g.n[0] < 3 || g.n[1] < 3 || g.n[2] < 3) ? 1 : 0;
+    } else {
+        g.periodic = 0;
+        for (int k = 0; k < 3; ++k) {
+            double lo = n > 0 ? smin[k][0] : 0.0, hi = n > 0 ? smax[k][0] : 0.0;
+            double ext = hi - lo;
+            double m = floor(ext / cw);
+            g.n[k] = m < 1 ? 1 : (m > 1024 ? 1024 : int(m));
+            g.lo[k] = lo;
+        }
+        while (int64_t(g.n[0]) * g.n[1] * g.n[2] > max_cells) {
+            int kmax = g.n[0] >= g.n[1] ? (g.n[0] >= g.n[2] ? 0 : 2) : (g.n[1] >= g.n[2] ? 1 : 2);
+            g.n[kmax] = (g.n[kmax] + 1) / 2;
+        }
+        for (int k = 0; k < 3; ++k) {
+            double ext = (n > 0 ? smax[k][0] : 0.0) - g.lo[k];
+            g.inv_w[k] = ext > 0 ? double(g.n[k]) / ext : 0.0;
+        }
+        g.brute = 0;
+    }
+    g.ncells = g.brute ? 1 : g.n[0] * g.n[1] * g.n[2];
+    *grid = g;
+}
+
+template <typename T>
+__device__ __forceinline__ void cell_coords(const T* pos, int64_t i, const NlGrid& g, int c[3]) {
+    const double x = pos[3 * i], y = pos[3 * i + 1], z = pos[3 * i + 2];
+    if (g.periodic) {
+        double f[3];
+        f[2] = z * g.rinv[5];
+        f[1] = (y - f[2] * g.rinv[4]) * g.rinv[2];
+        f[0] = (x - f[1] * g.rinv[1] - f[2] * g.rinv[3]) * g.rinv[0];
+        for (int k = 0; k < 3; ++k) {
+            double fk = f[k] - floor(f[k]);
+            int ck = int(fk * g.n[k]);
+            c[k] = ck < 0 ? 0 : (ck >= g.n[k] ? g.n[k] - 1 : ck);
+        }
+    } else {
+        const double v[3] = {x, y, z};
+        for (int k = 0; k < 3; ++k) {
+            int ck = int((v[k] - g.lo[k]) * g.inv_w[k]);
+            c[k] = ck < 0 ? 0 : (ck >= g.n[k] ? g.n[k] - 1 : ck);
+        }
+    }
+}
+
+template <typename T>
+__global__ void k_bin(const T* __restrict__ pos, int64_t n, const NlGrid* __restrict__ gp, int32_t* __restrict__ cell_of,
+                      int32_t* __restrict__ cell_count) {
+    const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const NlGrid g = *gp;
+    int cid = 0;
+    if (!g.brute) {
+        int c[3];
+        cell_coords<T>(pos, i, g, c);
+        cid = (c[2] * g.n[1] + c[1]) * g.n[0] + c[0];
+    }
+    cell_of[i] = cid;
+    atomicAdd(&cell_count[cid], 1);
+}
+
+__global__ void k_place(int64_t n, const int32_t* __restrict__ cell_of, const int32_t* __restrict__ cell_start,
+                        int32_t* __restrict__ cell_fill, int32_t* __restrict__ atoms_sorted) {
+    const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const int cid = cell_of[i];
+    const int slot = cell_start[cid] + atomicAdd(&cell_fill[cid], 1);
+    atoms_sorted[slot] = int32_t(i);
+}
+
+// Sort each cell's atom list ascending (deterministic order after atomic placement).
+__global__ void k_sort_cells(const NlGrid* __restrict__ gp, const int32_t* __restrict__ cell_start,
+                             int32_t* __restrict__ atoms_sorted) {
+    const int64_t c = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (c >= gp->ncells) return;
+    const int b = cell_start[c], e = cell_start[c + 1];
+    for (int k = b + 1; k < e; ++k) {
+        int v = atoms_sorted[k];
+        int q = k - 1;
+        while (q >= b && atoms_sorted[q] > v) {
+            atoms_sorted[q + 1] = atoms_sorted[q];
+            --q;
+        }
+        atoms_sorted[q + 1] = v;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Candidate scan: one wavefront per atom
+// ---------------------------------------------------------------------------
+
+// Calls f(j) for every candidate j of atom i (each j at most once), lanes in parallel.
+template <typename T, typename F>
+__device__ __forceinline__ void for_candidates(const T* pos, int i, int64_t n, const NlGrid& g,
+                                               const int32_t* __restrict__ cell_start,
+                                               const int32_t* __restrict__ atoms_sorted, int mode, F&& f) {
+    const int lane = threadIdx.x & (kWave - 1);
+    if (g.brute) {
+        const int64_t end = mode == MNX_NLIST_HALF ? i : n;
+        for (int64_t base = 0; base < end; base += kWave) {
+            const int64_t j = base + lane;
+            f(j < end && j != i ? int(j) : -1);
+        }
+        return;
+    }
+    int c[3];
+    cell_coords<T>(pos, i, g, c);
+    for (int dz = -1; dz <= 1; ++dz) {
+        int z = c[2] + dz;
+        if (g.periodic) z = (z + g.n[2]) % g.n[2];
+        else if (z < 0 || z >= g.n[2]) continue;
+        for (int dy = -1; dy <= 1; ++dy) {
+            int y = c[1] + dy;
+            if (g.periodic) y = (y + g.n[1]) % g.n[1];
+            else if (y < 0 || y >= g.n[1]) continue;
+            for (int dx = -1; dx <= 1; ++dx) {
+                int x = c[0] + dx;
+                if (g.periodic) x = (x + g.n[0]) % g.n[0];
+                else if (x < 0 || x >= g.n[0]) continue;
+                const int cid = (z * g.n[1] + y) * g.n[0] + x;
+                const int b = cell_start[cid], e = cell_start[cid + 1];
+                for (int base = b; base < e; base += kWave) {
+                    const int k = base + lane;
+                    int j = k < e ? atoms_sorted[k] : -1;
+                    if (mode == MNX_NLIST_HALF ? j >= i : j == i) j = -1;
+                    f(j);
+                }
+            }
+        }
+    }
+}
+
+template <typename T>
+__global__ void __launch_bounds__(kWave) k_count(const T* __restrict__ pos, int64_t n, const T* __restrict__ box,
+                                                 T cutoff, int mode, NlGrid* __restrict__ gp,
+                                                 const int32_t* __restrict__ cell_start,
+                                                 const int32_t* __restrict__ atoms_sorted,
+                                                 int32_t* __restrict__ counts) {
+    const int i = blockIdx.x;
+    if (i >= n) return;
+    const NlGrid g = *gp;
+    const bool periodic = g.periodic;
+    int count = 0;
+    for_candidates<T>(pos, i, n, g, cell_start, atoms_sorted, mode, [&](int j) {
+        const bool ok = j >= 0 && accept<T>(pos, box, i, j, periodic, cutoff);
+        count += __popcll(__ballot(ok));
+    });
+    if (threadIdx.x == 0) {
+        counts[i] = count;
+        if (count > kNlCap) atomicExch(&gp->overflow, 1);
+    }
+}
+
+// Bitonic sort of `len` ints in LDS (len <= kNlCap), ascending; pads with INT_MAX.
+__device__ void lds_sort(int32_t* buf, int len) {
+    int m = 1;
+    while (m < len) m <<= 1;
+    const int lane = threadIdx.x;
+    for (int k = len + lane; k < m; k += kWave) buf[k] = 0x7fffffff;
+    __syncthreads();
+    for (int size = 2; size <= m; size <<= 1) {
+        for (int stride = size >> 1; stride > 0; stride >>= 1) {
+            for (int t = lane; t < (m >> 1); t += kWave) {
+                const int lo = 2 * t - (t & (stride - 1));
+                const int hi = lo + stride;
+                const bool up = (lo & size) == 0;
+                const int a = buf[lo], b = buf[hi];
+                if ((a > b) == up) {
+                    buf[lo] = b;
+                    buf[hi] = a;
+                }
+            }
+            __syncthreads();
+        }
+    }
+}
+
+template <typename T>
+__global__ void __launch_bounds__(kWave) k_emit(const T* __restrict__ pos, int64_t n, const T* __restrict__ box,
+                                                T cutoff, int mode, int layout, const NlGrid* __restrict__ gp,
+                                                const int32_t* __restrict__ cell_start,
+                                                const int32_t* __restrict__ atoms_sorted,
+                                                const int64_t* __restrict__ offsets, int64_t capacity,
+                                                int32_t* __restrict__ idx_i, int32_t* __restrict__ idx_j,
+                                                T* __restrict__ deltas, T* __restrict__ dist,
+                                                T* __restrict__ shifts) {
+    __shared__ int32_t buf[kNlCap];
+    const int i = blockIdx.x;
+    if (i >= n) return;
+    const NlGrid g = *gp;
+    const bool periodic = g.periodic;
+    const int lane = threadIdx.x;
+    int count = 0;
+    for_candidates<T>(pos, i, n, g, cell_start, atoms_sorted, mode, [&](int j) {
+        const bool ok = j >= 0 && accept<T>(pos, box, i, j, periodic, cutoff);
+        const uint64_t m = __ballot(ok);
+        const int before = __popcll(m & ((uint64_t(1) << lane) - 1));
+        if (ok && count + before < kNlCap) buf[count + before] = j;
+        count += __popcll(m);
+    });
+    if (count > kNlCap) count = kNlCap;  // flagged by k_count; host reports the error
+    __syncthreads();
+    lds_sort(buf, count);
+    const int64_t base = layout == MNX_NLIST_TRIANGULAR ? 0 : offsets[i];
+    for (int k = lane; k < count; k += kWave) {
+        const int j = buf[k];
+        const int64_t slot = layout == MNX_NLIST_TRIANGULAR ? int64_t(i) * (i - 1) / 2 + j : base + k;
+        if (slot >= capacity) continue;
+        Geo<T> gg;
+        const bool flip = i < j;
+        pair_geo<T>(pos, box, flip ? j : i, flip ? i : j, periodic, shifts != nullptr, gg);
+        if (idx_i) idx_i[slot] = i;
+        if (idx_j) idx_j[slot] = j;
+        if (deltas) {
+            deltas[3 * slot + 0] = flip ? -gg.d[0] : gg.d[0];
+            deltas[3 * slot + 1] = flip ? -gg.d[1] : gg.d[1];
+            deltas[3 * slot + 2] = flip ? -gg.d[2] : gg.d[2];
+        }
+        if (dist) dist[slot] = gg.dist;
+        if (shifts) {
+            shifts[3 * slot + 0] = flip ? -gg.shift[0] : gg.shift[0];
+            shifts[3 * slot + 1] = flip ? -gg.shift[1] : gg.shift[1];
+            shifts[3 * slot + 2] = flip ? -gg.shift[2] : gg.shift[2];
+        }
+    }
+}
+
+// Reference padding (-1 / NaN) for slots [from, capacity); `from` read from device when from_dev != null.
+template <typename T>
+__global__ void k_pad(int64_t from_host, const int64_t* __restrict__ from_dev, int64_t capacity,
+                      int32_t* __restrict__ idx_i, int32_t* __restrict__ idx_j, T* __restrict__ deltas,
+                      T* __restrict__ dist, T* __restrict__ shifts) {
+    const int64_t from = from_dev ? *from_dev : from_host;
+    const T nan = T(NAN);
+    for (int64_t s = from + int64_t(blockIdx.x) * blockDim.x + threadIdx.x; s < capacity;
+         s += int64_t(gridDim.x) * blockDim.x) {
+        if (s < 0) continue;
+        if (idx_i) idx_i[s] = -1;
+        if (idx_j) idx_j[s] = -1;
+        if (deltas) deltas[3 * s] = deltas[3 * s + 1] = deltas[3 * s + 2] = nan;
+        if (dist) dist[s] = nan;
+        if (shifts) shifts[3 * s] = shifts[3 * s + 1] = shifts[3 * s + 2] = nan;
+    }
+}
+
+// *d_total = pair count, or -1 when some atom exceeded kNlCap neighbours.
+__global__ void k_report_total(const NlGrid* __restrict__ gp, const int64_t* __restrict__ total,
+                               int64_t* __restrict__ d_total) {
+    *d_total = gp->overflow ? int64_t(-1) : *total;
+}
+
+template <typename T>
+int nlist_count(const T* pos, int64_t n, double cutoff, const T* box, int mode, void* ws, size_t ws_bytes,
+                int64_t* d_total, hipStream_t stream) {
+    clear_error();
+    MNX_REQUIRE(n >= 0 && n < (int64_t(1) << 31), "num_atoms out of range: %lld", (long long)n);
+    MNX_REQUIRE(mode == MNX_NLIST_HALF || mode == MNX_NLIST_FULL, "bad mode %d", mode);
+    MNX_REQUIRE(n == 0 || pos, "positions is null");
+    MNX_REQUIRE(cutoff > 0, "cutoff must be positive");
+    size_t need = 0;
+    NlWs w = carve(ws, ws_bytes, n, &need);
+    if (ws_bytes < need || !ws) return set_error(MNX_ERR_WORKSPACE, "workspace %zu < %zu bytes", ws_bytes, need);
+    MNX_HIP_TRY(hipMemsetAsync(w.cell_count, 0, sizeof(int32_t) * w.max_cells, stream));
+    MNX_HIP_TRY(hipMemsetAsync(w.cell_fill, 0, sizeof(int32_t) * w.max_cells, stream));
+    MNX_HIP_TRY(hipMemsetAsync(w.grid, 0, sizeof(NlGrid), stream));
+    hipLaunchKernelGGL((k_grid_setup<T>), dim3(1), dim3(1024), 0, stream, pos, n, box, cutoff, w.max_cells, w.grid);
+    MNX_CHECK_LAUNCH();
+    if (n > 0) {
+        const int tb = 256;
+        hipLaunchKernelGGL((k_bin<T>), dim3(ceil_div(n, tb)), dim3(tb), 0, stream, pos, n, w.grid, w.cell_of, w.cell_count);
+        MNX_CHECK_LAUNCH();
+    }
+    int rc = exclusive_scan<int32_t, int32_t>(w.cell_count, w.max_cells, w.cell_start, w.tiles32,
+                                              w.cell_start + w.max_cells, stream);
+    if (rc) return rc;
+    if (n > 0) {
+        const int tb = 256;
+        hipLaunchKernelGGL(k_place, dim3(ceil_div(n, tb)), dim3(tb), 0, stream, n, w.cell_of, w.cell_start,
+                           w.cell_fill, w.atoms_sorted);
+        MNX_CHECK_LAUNCH();
+        hipLaunchKernelGGL(k_sort_cells, dim3(ceil_div(w.max_cells, tb)), dim3(tb), 0, stream, w.grid,
+                           w.cell_start, w.atoms_sorted);
+        MNX_CHECK_LAUNCH();
+        hipLaunchKernelGGL((k_count<T>), dim3(n), dim3(kWave), 0, stream, pos, n, box, T(cutoff), mode, w.grid,
+                           w.cell_start, w.atoms_sorted, w.counts);
+        MNX_CHECK_LAUNCH();
+    }
+    rc = exclusive_scan<int32_t, int64_t>(w.counts, n, w.offsets, w.tiles64, w.total, stream);
+    if (rc) return rc;
+    if (d_total) {
+        hipLaunchKernelGGL(k_report_total, dim3(1), dim3(1), 0, stream, w.grid, w.total, d_total);
+        MNX_CHECK_LAUNCH();
+    }
+    return MNX_OK;
+}
+
+template <typename T>
+int nlist_emit(const T* pos, int64_t n, double cutoff, const T* box, int mode, int layout, const void* ws,
+               size_t ws_bytes, int64_t capacity, int32_t* idx_i, int32_t* idx_j, T* deltas, T* dist, T* shifts,
+               hipStream_t stream) {
+    clear_error();
+    MNX_REQUIRE(capacity >= 0, "capacity must be >= 0");
+    MNX_REQUIRE(layout == MNX_NLIST_COMPACT || (layout == MNX_NLIST_TRIANGULAR && mode == MNX_NLIST_HALF),
+                "triangular layout needs the half list");
+    size_t need = 0;
+    NlWs w = carve(const_cast<void*>(ws), ws_bytes, n, &need);
+    if (ws_bytes < need || !ws) return set_error(MNX_ERR_WORKSPACE, "workspace %zu < %zu bytes", ws_bytes, need);
+    if (capacity == 0) return MNX_OK;
+    const int tb = 256;
+    const int64_t pad_blocks = std::min<int64_t>(ceil_div(capacity, tb), 65536);
+    if (layout == MNX_NLIST_TRIANGULAR) {
+        hipLaunchKernelGGL((k_pad<T>), dim3(pad_blocks), dim3(tb), 0, stream, int64_t(0), (const int64_t*)nullptr,
+                           capacity, idx_i, idx_j, deltas, dist, shifts);
+        MNX_CHECK_LAUNCH();
+    } else {
+        hipLaunchKernelGGL((k_pad<T>), dim3(pad_blocks), dim3(tb), 0, stream, int64_t(0), (const int64_t*)w.total,
+                           capacity, idx_i, idx_j, deltas, dist, shifts);
+        MNX_CHECK_LAUNCH();
+    }
+    if (n > 0) {
+        hipLaunchKernelGGL((k_emit<T>), dim3(n), dim3(kWave), 0, stream, pos, n, box, T(cutoff), mode, layout,
+                           w.grid, w.cell_start, w.atoms_sorted, w.offsets, capacity, idx_i, idx_j, deltas, dist,
+                           shifts);
+        MNX_CHECK_LAUNCH();
+    }
+    return MNX_OK;
+}
+
+template <typename T>
+__global__ void k_nl_backward(const int32_t* __restrict__ ii, const int32_t* __restrict__ jj,
+                              const T* __restrict__ d, const T* __restrict__ dist, const T* __restrict__ gd,
+                              const T* __restrict__ gdist, int64_t slots, T* __restrict__ gpos) {
+    const int64_t s = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (s >= slots) return;
+    const int i = ii[s], j = jj[s];
+    if (i < 0 || j < 0) return;
+    const T inv = T(1) / dist[s];
+    const T gds = gdist ? gdist[s] : T(0);
+    for (int k = 0; k < 3; ++k) {
+        T g = (gd ? gd[3 * s + k] : T(0)) + d[3 * s + k] * inv * gds;
+        atomicAdd(&gpos[3 * i + k], g);
+        atomicAdd(&gpos[3 * j + k], -g);
+    }
+}
+
+}  // namespace
+}  // namespace mnx
+
+using namespace mnx;
+
+extern "C" {
+
+size_t mnx_nlist_workspace_bytes(int64_t num_atoms) {
+    size_t used = 0;
+    carve(nullptr, 0, num_atoms < 0 ? 0 : num_atoms, &used);
+    return used + 256;
+}
+
+int mnx_nlist_count_f32(const float* pos, int64_t n, double cutoff, const float* box, int32_t mode, void* ws,
+                        size_t ws_bytes, int64_t* d_total, mnx_stream_t stream) {
+    return nlist_count<float>(pos, n, cutoff, box, mode, ws, ws_bytes, d_total, (hipStream_t)stream);
+}
+int mnx_nlist_count_f64(const double* pos, int64_t n, double cutoff, const double* box, int32_t mode, void* ws,
+                        size_t ws_bytes, int64_t* d_total, mnx_stream_t stream) {
+    return nlist_count<double>(pos, n, cutoff, box, mode, ws, ws_bytes, d_total, (hipStream_t)stream);
+}
+int mnx_nlist_emit_f32(const float* pos, int64_t n, double cutoff, const float* box, int32_t mode, int32_t layout,
+                       const void* ws, size_t ws_bytes, int64_t capacity, int32_t* idx_i, int32_t* idx_j,
+                       float* deltas, float* distances, float* shifts, mnx_stream_t stream) {
+    return nlist_emit<float>(pos, n, cutoff, box, mode, layout, ws, ws_bytes, capacity, idx_i, idx_j, deltas,
+                             distances, shifts, (hipStream_t)stream);
+}
+int mnx_nlist_emit_f64(const double* pos, int64_t n, double cutoff, const double* box, int32_t mode,
+                       int32_t layout, const void* ws, size_t ws_bytes, int64_t capacity, int32_t* idx_i,
+                       int32_t* idx_j, double* deltas, double* distances, double* shifts, mnx_stream_t stream) {
+    return nlist_emit<double>(pos, n, cutoff, box, mode, layout, ws, ws_bytes, capacity, idx_i, idx_j, deltas,
+                              distances, shifts, (hipStream_t)stream);
+}
+
+int mnx_nlist_backward_f32(const int32_t* idx_i, const int32_t* idx_j, const float* deltas, const float* distances,
+                           const float* grad_deltas, const float* grad_distances, int64_t num_slots,
+                           int64_t num_atoms, float* grad_pos, mnx_stream_t stream) {
+    clear_error();
+    (void)num_atoms;
+    if (num_slots <= 0) return MNX_OK;
+    const int tb = 256;
+    hipLaunchKernelGGL((k_nl_backward<float>), dim3(ceil_div(num_slots, tb)), dim3(tb), 0, (hipStream_t)stream,
+                       idx_i, idx_j, deltas, distances, grad_deltas, grad_distances, num_slots, grad_pos);
+    MNX_CHECK_LAUNCH();
+    return MNX_OK;
+}
+
+int mnx_nlist_backward_f64(const int32_t* idx_i, const int32_t* idx_j, const double* deltas, const double* distances,
+                           const double* grad_deltas, const double* grad_distances, int64_t num_slots,
+                           int64_t num_atoms, double* grad_pos, mnx_stream_t stream) {
+    clear_error();
+    (void)num_atoms;
+    if (num_slots <= 0) return MNX_OK;
+    const int tb = 256;
+    hipLaunchKernelGGL((k_nl_backward<double>), dim3(ceil_div(num_slots, tb)), dim3(tb), 0, (hipStream_t)stream,
+                       idx_i, idx_j, deltas, distances, grad_deltas, grad_distances, num_slots, grad_pos);
+    MNX_CHECK_LAUNCH();
+    return MNX_OK;
+}
+
+}  // extern "C"

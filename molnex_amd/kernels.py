@@ -1,0 +1,380 @@
+"""Torch custom ops (namespace ``molix``) over the molnex C ABI.
+
+Every op here runs the HIP kernels of ``lib/libmolnex_hip.so`` on the current
+stream; there are no CPU implementations (a CPU tensor raises).  Fake (meta)
+implementations and autograd formulas are registered so the ops trace under
+``torch.compile`` / ``torch.export`` like the reference's ops
+(``src/molix/op/src/molix_meta.cpp:19-70``).
+
+Ops
+---
+``molix::get_neighbor_pairs``   reference schema, verbatim (``molix_library.cpp:22-26``)
+``molix::neighbor_list``        directed / half cell list, exact size, sorted (i, j)
+``molix::spherical_harmonics``  real SH l <= 3 (``cuet.SphericalHarmonics``)
+``molix::edge_csr``             receiver CSR of an (E, 2) edge list
+``molix::tp_scatter``           channelwise TP + scatter-sum (``cuet.ChannelWiseTensorProduct``)
+"""
+
+from __future__ import annotations
+
+import ctypes as C
+
+import torch
+from torch import Tensor
+
+from . import _lib
+from ._lib import check, ptr
+
+MNX_NLIST_HALF, MNX_NLIST_FULL = 0, 1
+MNX_NLIST_COMPACT, MNX_NLIST_TRIANGULAR = 0, 1
+
+
+def _stream(t: Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def _require_gpu(name: str, *ts: Tensor) -> None:
+    for t in ts:
+        if t is not None and t.numel() > 0 and t.device.type != "cuda":
+            raise RuntimeError(f"molix::{name} runs on the GPU only (got a {t.device} tensor)")
+
+
+def _ws(nbytes: int, device) -> Tensor:
+    return torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=device)
+
+
+# ---------------------------------------------------------------------------
+# Neighbor list
+# ---------------------------------------------------------------------------
+
+
+def _nlist_run(positions: Tensor, cutoff: float, box: Tensor | None, mode: int):
+    """Stage 1 of the cell list; returns (workspace, total pair count on host)."""
+    lib = _lib.load()
+    n = positions.shape[0]
+    f64 = positions.dtype == torch.float64
+    ws = _ws(lib.mnx_nlist_workspace_bytes(n), positions.device)
+    total = torch.empty(1, dtype=torch.int64, device=positions.device)
+    fn = lib.mnx_nlist_count_f64 if f64 else lib.mnx_nlist_count_f32
+    check(fn(ptr(positions), n, float(cutoff), ptr(box), mode, ptr(ws), ws.numel(), ptr(total),
+             _stream(positions)), "neighbor list count")
+    t = int(total.item())
+    if t < 0:
+        raise _lib.MolnexError("neighbor list: an atom has more than 4096 neighbours within the cutoff")
+    return ws, t
+
+
+def _nlist_emit(positions, cutoff, box, mode, layout, ws, capacity, idx_i, idx_j, deltas, dist, shifts):
+    lib = _lib.load()
+    f64 = positions.dtype == torch.float64
+    fn = lib.mnx_nlist_emit_f64 if f64 else lib.mnx_nlist_emit_f32
+    check(fn(ptr(positions), positions.shape[0], float(cutoff), ptr(box), mode, layout, ptr(ws), ws.numel(),
+             capacity, ptr(idx_i), ptr(idx_j), ptr(deltas), ptr(dist), ptr(shifts), _stream(positions)),
+          "neighbor list emit")
+
+
+def _prep_positions(positions: Tensor, box_vectors: Tensor):
+    if positions.dtype not in (torch.float32, torch.float64):
+        raise TypeError("positions must be float32 or float64")
+    pos = positions.detach().contiguous()
+    box = None
+    if box_vectors is not None and box_vectors.numel() != 0:
+        if tuple(box_vectors.shape) != (3, 3):
+            raise ValueError("box_vectors must be (3, 3) or empty")
+        box = box_vectors.detach().to(device=pos.device, dtype=pos.dtype).contiguous()
+    return pos, box
+
+
+@torch.library.custom_op(
+    "molix::get_neighbor_pairs",
+    mutates_args=(),
+    device_types="cuda",
+    schema="(Tensor positions, Scalar cutoff, Scalar max_num_pairs, Tensor box_vectors) -> "
+    "(Tensor neighbors, Tensor deltas, Tensor distances, Tensor num_pairs)",
+)
+def get_neighbor_pairs(positions, cutoff, max_num_pairs, box_vectors):
+    """Half pair list within ``cutoff`` (reference ``get_neighbor_pairs.cpp:28-77``).
+
+    ``max_num_pairs == -1``: width ``N(N-1)/2``, pair (i, j) at slot
+    ``i(i-1)/2 + j``; otherwise width ``max_num_pairs`` with the pairs sorted by
+    (i, j) first (the first ``max_num_pairs`` of them when there are more,
+    like the CUDA/meta widths, ``molix_meta.cpp:25-27``).  Padding is -1 / NaN.
+    """
+    _require_gpu("get_neighbor_pairs", positions, box_vectors)
+    pos, box = _prep_positions(positions, box_vectors)
+    n = pos.shape[0]
+    mnp = int(max_num_pairs)
+    width = n * (n - 1) // 2 if mnp == -1 else mnp
+    layout = MNX_NLIST_TRIANGULAR if mnp == -1 else MNX_NLIST_COMPACT
+    neighbors = torch.empty((2, width), dtype=torch.int32, device=pos.device)
+    deltas = torch.empty((width, 3), dtype=pos.dtype, device=pos.device)
+    distances = torch.empty((width,), dtype=pos.dtype, device=pos.device)
+    ws, total = _nlist_run(pos, float(cutoff), box, MNX_NLIST_HALF)
+    _nlist_emit(pos, float(cutoff), box, MNX_NLIST_HALF, layout, ws, width, neighbors[0], neighbors[1], deltas,
+                distances, None)
+    num_pairs = torch.full((1,), total, dtype=torch.int32, device=pos.device)
+    return neighbors, deltas, distances, num_pairs
+
+
+@get_neighbor_pairs.register_fake
+def _(positions, cutoff, max_num_pairs, box_vectors):
+    n = positions.shape[0]
+    mnp = int(max_num_pairs)
+    width = n * (n - 1) // 2 if mnp == -1 else mnp
+    return (
+        positions.new_empty((2, width), dtype=torch.int32),
+        positions.new_empty((width, 3)),
+        positions.new_empty((width,)),
+        positions.new_empty((1,), dtype=torch.int32),
+    )
+
+
+@torch.library.custom_op("molix::get_neighbor_pairs_backward", mutates_args=(), device_types="cuda")
+def get_neighbor_pairs_backward(neighbors: Tensor, deltas: Tensor, distances: Tensor, grad_deltas: Tensor,
+                                grad_distances: Tensor, num_atoms: int) -> Tensor:
+    """d/d positions of <g_deltas, deltas> + <g_dist, distances> (``get_neighbor_pairs.cu:81-102``)."""
+    lib = _lib.load()
+    gpos = torch.zeros((num_atoms, 3), dtype=deltas.dtype, device=deltas.device)
+    width = neighbors.shape[1]
+    nb = neighbors.contiguous()
+    fn = lib.mnx_nlist_backward_f64 if deltas.dtype == torch.float64 else lib.mnx_nlist_backward_f32
+    check(fn(ptr(nb[0]), ptr(nb[1]), ptr(deltas.contiguous()), ptr(distances.contiguous()),
+             ptr(grad_deltas.contiguous()), ptr(grad_distances.contiguous()), width, num_atoms, ptr(gpos),
+             _stream(deltas)), "get_neighbor_pairs backward")
+    return gpos
+
+
+@get_neighbor_pairs_backward.register_fake
+def _(neighbors, deltas, distances, grad_deltas, grad_distances, num_atoms):
+    return deltas.new_empty((num_atoms, 3))
+
+
+def _gnp_setup(ctx, inputs, output):
+    positions = inputs[0]
+    neighbors, deltas, distances, _ = output
+    ctx.save_for_backward(neighbors, deltas, distances)
+    ctx.num_atoms = positions.shape[0]
+
+
+def _gnp_backward(ctx, g_neighbors, g_deltas, g_distances, g_num):
+    neighbors, deltas, distances = ctx.saved_tensors
+    if g_deltas is None:
+        g_deltas = torch.zeros_like(deltas)
+    if g_distances is None:
+        g_distances = torch.zeros_like(distances)
+    gpos = get_neighbor_pairs_backward(neighbors, deltas, distances, g_deltas, g_distances, ctx.num_atoms)
+    return gpos, None, None, None
+
+
+get_neighbor_pairs.register_autograd(_gnp_backward, setup_context=_gnp_setup)
+
+
+@torch.library.custom_op("molix::neighbor_list", mutates_args=(), device_types="cuda")
+def neighbor_list(positions: Tensor, cutoff: float, box_vectors: Tensor, full: bool) -> tuple[
+        Tensor, Tensor, Tensor, Tensor, Tensor]:
+    """Exact-size cell list sorted by (i, j): ``full`` gives all ordered pairs i != j,
+    otherwise the reference half list (i > j).
+
+    Returns ``(i, j, shifts, deltas, distances)``: int32 ``i``/``j``; ``deltas``
+    = the reference's minimum-image ``pos[i] - pos[j]`` (bit-exact), ``shifts``
+    the image offset with ``deltas = pos[i] - (pos[j] + shifts)``.
+    """
+    _require_gpu("neighbor_list", positions, box_vectors)
+    pos, box = _prep_positions(positions, box_vectors)
+    mode = MNX_NLIST_FULL if full else MNX_NLIST_HALF
+    ws, total = _nlist_run(pos, cutoff, box, mode)
+    dev, dt = pos.device, pos.dtype
+    ii = torch.empty(total, dtype=torch.int32, device=dev)
+    jj = torch.empty(total, dtype=torch.int32, device=dev)
+    sh = torch.empty((total, 3), dtype=dt, device=dev)
+    dd = torch.empty((total, 3), dtype=dt, device=dev)
+    dist = torch.empty(total, dtype=dt, device=dev)
+    _nlist_emit(pos, cutoff, box, mode, MNX_NLIST_COMPACT, ws, total, ii, jj, dd, dist, sh)
+    return ii, jj, sh, dd, dist
+
+
+@neighbor_list.register_fake
+def _(positions, cutoff, box_vectors, full):
+    ctx = torch.library.get_ctx()
+    e = ctx.new_dynamic_size()
+    return (positions.new_empty((e,), dtype=torch.int32), positions.new_empty((e,), dtype=torch.int32),
+            positions.new_empty((e, 3)), positions.new_empty((e, 3)), positions.new_empty((e,)))
+
+
+# ---------------------------------------------------------------------------
+# Spherical harmonics
+# ---------------------------------------------------------------------------
+
+
+def _f32_rows(t: Tensor, width: int, what: str) -> Tensor:
+    if t.dtype != torch.float32:
+        raise TypeError(f"{what} must be float32 (the HIP kernels compute in fp32), got {t.dtype}")
+    return t.reshape(-1, width).contiguous()
+
+
+@torch.library.custom_op("molix::spherical_harmonics", mutates_args=(), device_types="cuda")
+def spherical_harmonics(vectors: Tensor, l_max: int) -> Tensor:
+    """Real harmonics ``[Y^0 .. Y^l_max]`` of normalised ``vectors`` (..., 3)."""
+    _require_gpu("spherical_harmonics", vectors)
+    v = _f32_rows(vectors, 3, "vectors")
+    d = (l_max + 1) ** 2
+    out = torch.empty((v.shape[0], d), dtype=torch.float32, device=v.device)
+    check(_lib.load().mnx_sh_fwd_f32(ptr(v), v.shape[0], l_max, ptr(out), _stream(v)), "spherical_harmonics")
+    return out.reshape(*vectors.shape[:-1], d)
+
+
+@spherical_harmonics.register_fake
+def _(vectors, l_max):
+    return vectors.new_empty((*vectors.shape[:-1], (l_max + 1) ** 2))
+
+
+@torch.library.custom_op("molix::spherical_harmonics_backward", mutates_args=(), device_types="cuda")
+def spherical_harmonics_backward(vectors: Tensor, grad: Tensor, l_max: int) -> Tensor:
+    v = _f32_rows(vectors, 3, "vectors")
+    d = (l_max + 1) ** 2
+    g = _f32_rows(grad, d, "grad")
+    gv = torch.empty_like(v)
+    check(_lib.load().mnx_sh_bwd_f32(ptr(v), ptr(g), v.shape[0], l_max, ptr(gv), _stream(v)),
+          "spherical_harmonics backward")
+    return gv.reshape(vectors.shape)
+
+
+@spherical_harmonics_backward.register_fake
+def _(vectors, grad, l_max):
+    return torch.empty_like(vectors)
+
+
+def _sh_setup(ctx, inputs, output):
+    ctx.save_for_backward(inputs[0])
+    ctx.l_max = inputs[1]
+
+
+def _sh_backward(ctx, grad):
+    (v,) = ctx.saved_tensors
+    return spherical_harmonics_backward(v, grad, ctx.l_max), None
+
+
+spherical_harmonics.register_autograd(_sh_backward, setup_context=_sh_setup)
+
+
+# ---------------------------------------------------------------------------
+# Receiver CSR and the channelwise tensor product
+# ---------------------------------------------------------------------------
+
+
+@torch.library.custom_op("molix::edge_csr", mutates_args=(), device_types="cuda")
+def edge_csr(edge_index: Tensor, num_nodes: int) -> tuple[Tensor, Tensor, Tensor]:
+    """Receiver CSR of ``edge_index`` (E, 2) = [sender, receiver]: ``(row_ptr, perm, senders)``.
+
+    Raises if an index lies outside ``[0, num_nodes)``.
+    """
+    _require_gpu("edge_csr", edge_index)
+    if edge_index.ndim != 2 or edge_index.shape[1] != 2:
+        raise ValueError(f"edge_index must be (E, 2), got {tuple(edge_index.shape)}")
+    lib = _lib.load()
+    ei = edge_index.to(torch.int64).contiguous()
+    E = ei.shape[0]
+    dev = ei.device
+    row_ptr = torch.empty(num_nodes + 1, dtype=torch.int32, device=dev)
+    perm = torch.empty(E, dtype=torch.int32, device=dev)
+    snd = torch.empty(E, dtype=torch.int32, device=dev)
+    invalid = torch.zeros(1, dtype=torch.int32, device=dev)
+    ws = _ws(lib.mnx_csr_workspace_bytes(num_nodes, E), dev)
+    check(lib.mnx_csr_build(ptr(ei), E, num_nodes, ptr(row_ptr), ptr(perm), ptr(snd), ptr(invalid), ptr(ws),
+                            ws.numel(), _stream(ei)), "edge_csr")
+    if E > 0 and int(invalid.item()) != 0:
+        raise ValueError(f"edge_index has {int(invalid.item())} edges with a node index outside [0, {num_nodes})")
+    return row_ptr, perm, snd
+
+
+@edge_csr.register_fake
+def _(edge_index, num_nodes):
+    E = edge_index.shape[0]
+    return (edge_index.new_empty((num_nodes + 1,), dtype=torch.int32),
+            edge_index.new_empty((E,), dtype=torch.int32), edge_index.new_empty((E,), dtype=torch.int32))
+
+
+def tp_config_id(in_ls, sh_ls, out_ls) -> int:
+    mask = lambda ls: sum(1 << l for l in ls)  # noqa: E731
+    return int(_lib.load().mnx_tp_config(mask(in_ls), mask(sh_ls), mask(out_ls)))
+
+
+def tp_config_info(config: int) -> tuple[int, int, int, int]:
+    info = (C.c_int32 * 4)()
+    check(_lib.load().mnx_tp_config_info(config, info), "tp_config_info")
+    return tuple(info)
+
+
+@torch.library.custom_op("molix::tp_scatter", mutates_args=(), device_types="cuda")
+def tp_scatter(x: Tensor, Y: Tensor, w: Tensor, row_ptr: Tensor, perm: Tensor, senders: Tensor, config: int,
+               channels: int) -> Tensor:
+    """``out[r] = sum_{e -> r} TP(x[send(e)], Y[e]; w[e])`` for a compiled configuration."""
+    _require_gpu("tp_scatter", x, Y, w, row_ptr)
+    num_paths, nx, ny, no = tp_config_info(config)
+    N = row_ptr.shape[0] - 1
+    E = Y.shape[0]
+    xs = _f32_rows(x, nx * channels, "x")
+    Ys = _f32_rows(Y, ny, "Y")
+    ws_ = _f32_rows(w, num_paths * channels, "w")
+    if xs.shape[0] != N or ws_.shape[0] != E or perm.shape[0] != E:
+        raise ValueError("tp_scatter: inconsistent sizes of x / Y / w / CSR")
+    out = torch.empty((N, no * channels), dtype=torch.float32, device=xs.device)
+    check(_lib.load().mnx_tp_fwd_f32(config, channels, ptr(xs), ptr(Ys), ptr(ws_), ptr(row_ptr), ptr(perm),
+                                     ptr(senders), N, E, ptr(out), _stream(xs)), "tp_scatter")
+    return out
+
+
+@tp_scatter.register_fake
+def _(x, Y, w, row_ptr, perm, senders, config, channels):
+    num_paths, nx, ny, no = tp_config_info(config)
+    return x.new_empty((row_ptr.shape[0] - 1, no * channels))
+
+
+@torch.library.custom_op("molix::tp_scatter_backward", mutates_args=(), device_types="cuda")
+def tp_scatter_backward(grad_out: Tensor, x: Tensor, Y: Tensor, w: Tensor, row_ptr: Tensor, perm: Tensor,
+                        senders: Tensor, config: int, channels: int, need_x: bool, need_Y: bool,
+                        need_w: bool) -> tuple[Tensor, Tensor, Tensor]:
+    """Gradients of ``<grad_out, tp_scatter(...)>`` w.r.t. x, Y, w (empty when not needed)."""
+    lib = _lib.load()
+    num_paths, nx, ny, no = tp_config_info(config)
+    N = row_ptr.shape[0] - 1
+    E = Y.shape[0]
+    xs = _f32_rows(x, nx * channels, "x")
+    Ys = _f32_rows(Y, ny, "Y")
+    wss = _f32_rows(w, num_paths * channels, "w")
+    go = _f32_rows(grad_out, no * channels, "grad_out")
+    dev = xs.device
+    gx = torch.zeros_like(xs) if need_x else xs.new_empty(0)
+    gY = torch.empty_like(Ys) if need_Y else Ys.new_empty(0)
+    gw = torch.empty_like(wss) if need_w else wss.new_empty(0)
+    ws = _ws(lib.mnx_tp_bwd_workspace_bytes(config, channels, E) if need_Y else 1, dev)
+    check(lib.mnx_tp_bwd_f32(config, channels, ptr(xs), ptr(Ys), ptr(wss), ptr(go), ptr(row_ptr), ptr(perm),
+                             ptr(senders), N, E, ptr(gx), ptr(gY), ptr(gw), ptr(ws), ws.numel(), _stream(xs)),
+          "tp_scatter backward")
+    if E == 0:
+        gY.zero_() if need_Y else None
+    return gx, gY, gw
+
+
+@tp_scatter_backward.register_fake
+def _(grad_out, x, Y, w, row_ptr, perm, senders, config, channels, need_x, need_Y, need_w):
+    return (torch.empty_like(x) if need_x else x.new_empty(0), torch.empty_like(Y) if need_Y else Y.new_empty(0),
+            torch.empty_like(w) if need_w else w.new_empty(0))
+
+
+def _tp_setup(ctx, inputs, output):
+    x, Y, w, row_ptr, perm, senders, config, channels = inputs
+    ctx.save_for_backward(x, Y, w, row_ptr, perm, senders)
+    ctx.config, ctx.channels = config, channels
+
+
+def _tp_backward(ctx, grad_out):
+    x, Y, w, row_ptr, perm, senders = ctx.saved_tensors
+    nx, nY, nw = ctx.needs_input_grad[:3]
+    gx, gY, gw = tp_scatter_backward(grad_out.contiguous(), x, Y, w, row_ptr, perm, senders, ctx.config,
+                                     ctx.channels, nx, nY, nw)
+    return (gx.reshape(x.shape) if nx else None, gY.reshape(Y.shape) if nY else None,
+            gw.reshape(w.shape) if nw else None, None, None, None, None, None)
+
+
+tp_scatter.register_autograd(_tp_backward, setup_context=_tp_setup)
