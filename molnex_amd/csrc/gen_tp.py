@@ -116,11 +116,68 @@ def _uniq(seq):
     return out
 
 
-def gen_fwd(cfg: Cfg, g: int) -> str:
-    ps = cfg.groups[g]
+def _group_layout(ps):
     xs = _uniq([p["o1"] + m for p in ps for m in range(2 * p["l1"] + 1)])
     ys = _uniq([p["o2"] + m for p in ps for m in range(2 * p["l2"] + 1)])
     outs = [p["o3"] + m for p in ps for m in range(2 * p["l3"] + 1)]
+    return xs, ys, outs
+
+
+def _v_count(ps):
+    return sum(1 for p in ps for m1 in range(2 * p["l1"] + 1) for m2 in range(2 * p["l2"] + 1)
+               if np.any(np.abs(p["c"][m1, m2, :]) > EPS))
+
+
+def bwd_cpl(ps) -> int:
+    """Channels per lane for a backward group: 2 when the per-channel register
+    state (folded gradient v, x, w, partial sums) stays small, else 1."""
+    xs, ys, outs = _group_layout(ps)
+    per_channel = _v_count(ps) + 2 * (len(xs) + len(ps)) + len(xs)
+    return 2 if per_channel <= 60 else 1
+
+
+def _emit_prefetch(a, cfg, ps, xs, ys, xi, indent, t_expr, cpl_expr="CPL"):
+    """Load edge t_expr's ids, harmonics, sender row and weights into n* registers."""
+    a(f"{indent}{{")
+    a(f"{indent}  ne = perm[{t_expr}]; ns = snd[{t_expr}];")
+    a(f"{indent}  const float* __restrict__ Yn = Y + int64_t(ne) * {cfg.NY};")
+    for c in ys:
+        a(f"{indent}  ny{c} = Yn[{c}];")
+    a(f"{indent}  const float* __restrict__ xn = x + int64_t(ns) * XS;")
+    a(f"{indent}  const float* __restrict__ wn = w + int64_t(ne) * WS;")
+    a("#pragma unroll")
+    a(f"{indent}  for (int k = 0; k < {cpl_expr}; ++k) {{")
+    for c in xs:
+        a(f"{indent}    nxv[k][{xi[c]}] = ok[k] ? xn[{c} * C + cc[k]] : 0.f;")
+    for j, p in enumerate(ps):
+        a(f"{indent}    nwv[k][{j}] = ok[k] ? __builtin_nontemporal_load(wn + {p['k']} * C + cc[k]) : 0.f;")
+    a(f"{indent}  }}")
+    a(f"{indent}}}")
+
+
+def _emit_edge_loop_head(a, cfg, ps, xs, ys, xi):
+    a("  const int beg = row_ptr[n], end = row_ptr[n + 1];")
+    a("  int ne = 0, ns = 0;")
+    a("  " + " ".join(f"float ny{c} = 0.f;" for c in ys))
+    a(f"  float nxv[CPL][{len(xs)}], nwv[CPL][{len(ps)}];")
+    a("  if (beg < end)")
+    _emit_prefetch(a, cfg, ps, xs, ys, xi, "  ", "beg")
+    a("  for (int t = beg; t < end; ++t) {")
+    a("    const int e = ne, s = ns;")
+    a("    " + " ".join(f"const float y{c} = ny{c};" for c in ys))
+    a(f"    float xv[CPL][{len(xs)}], wv[CPL][{len(ps)}];")
+    a("#pragma unroll")
+    a("    for (int k = 0; k < CPL; ++k) {")
+    a(f"#pragma unroll\n      for (int i = 0; i < {len(xs)}; ++i) xv[k][i] = nxv[k][i];")
+    a(f"#pragma unroll\n      for (int i = 0; i < {len(ps)}; ++i) wv[k][i] = nwv[k][i];")
+    a("    }")
+    a("    if (t + 1 < end)")
+    _emit_prefetch(a, cfg, ps, xs, ys, xi, "    ", "t + 1")
+
+
+def gen_fwd(cfg: Cfg, g: int) -> str:
+    ps = cfg.groups[g]
+    xs, ys, outs = _group_layout(ps)
     xi = {c: i for i, c in enumerate(xs)}
     oi = {c: i for i, c in enumerate(outs)}
     L = []
@@ -140,22 +197,8 @@ def gen_fwd(cfg: Cfg, g: int) -> str:
     a("#pragma unroll")
     a(f"  for (int k = 0; k < CPL; ++k)\n#pragma unroll\n    for (int i = 0; i < {len(outs)}; ++i) acc[k][i] = 0.f;")
     a(f"  const int64_t XS = int64_t({cfg.NX}) * C, WS = int64_t({cfg.NP}) * C;")
-    a("  const int beg = row_ptr[n], end = row_ptr[n + 1];")
-    a("  for (int t = beg; t < end; ++t) {")
-    a("    const int e = perm[t], s = snd[t];")
-    a(f"    const float* __restrict__ Ye = Y + int64_t(e) * {cfg.NY};")
-    for c in ys:
-        a(f"    const float y{c} = Ye[{c}];")
-    a("    const float* __restrict__ xs = x + int64_t(s) * XS;")
-    a("    const float* __restrict__ we = w + int64_t(e) * WS;")
-    a(f"    float xv[CPL][{len(xs)}], wv[CPL][{len(ps)}];")
-    a("#pragma unroll")
-    a("    for (int k = 0; k < CPL; ++k) {")
-    for c in xs:
-        a(f"      xv[k][{xi[c]}] = ok[k] ? xs[{c} * C + cc[k]] : 0.f;")
-    for j, p in enumerate(ps):
-        a(f"      wv[k][{j}] = ok[k] ? __builtin_nontemporal_load(we + {p['k']} * C + cc[k]) : 0.f;")
-    a("    }")
+    _emit_edge_loop_head(a, cfg, ps, xs, ys, xi)
+    a("    (void)e; (void)s;")
     # uniform coupling matrices M_p[m3][m1]
     for j, p in enumerate(ps):
         c = p["c"]
@@ -197,9 +240,7 @@ def gen_fwd(cfg: Cfg, g: int) -> str:
 
 def gen_bwd(cfg: Cfg, g: int) -> str:
     ps = cfg.groups[g]
-    xs = _uniq([p["o1"] + m for p in ps for m in range(2 * p["l1"] + 1)])
-    ys = _uniq([p["o2"] + m for p in ps for m in range(2 * p["l2"] + 1)])
-    outs = [p["o3"] + m for p in ps for m in range(2 * p["l3"] + 1)]
+    xs, ys, outs = _group_layout(ps)
     xi = {c: i for i, c in enumerate(xs)}
     oi = {c: i for i, c in enumerate(outs)}
     V = 1
@@ -211,19 +252,19 @@ def gen_bwd(cfg: Cfg, g: int) -> str:
     a(f"template <int CPL>\n__global__ void __launch_bounds__(64) {name}(const float* __restrict__ x, "
       "const float* __restrict__ Y, const float* __restrict__ w, const float* __restrict__ gout, "
       "const int32_t* __restrict__ row_ptr, const int32_t* __restrict__ perm, const int32_t* __restrict__ snd, "
-      "int64_t N, int C, float* __restrict__ gx, float* __restrict__ gw, float* __restrict__ gyp, int npart) {")
+      "int64_t N, int C, float* __restrict__ gx, float* __restrict__ gw, float* __restrict__ gyp, int npart, "
+      "int pbase) {")
     a("  const int64_t n = xcd_node(blockIdx.x, gridDim.x);")
     a("  if (n >= N) return;")
     a("  const int lane = threadIdx.x;")
     a("  int cc[CPL]; bool ok[CPL];")
     a("#pragma unroll")
     a("  for (int k = 0; k < CPL; ++k) { cc[k] = blockIdx.y * (64 * CPL) + 64 * k + lane; ok[k] = cc[k] < C; }")
-    a(f"  const int pidx = {g} * gridDim.y + blockIdx.y;")
+    a("  const int pidx = pbase + blockIdx.y;")
     a(f"  const int64_t XS = int64_t({cfg.NX}) * C, WS = int64_t({cfg.NP}) * C;")
     a(f"  const float* __restrict__ gn = gout + n * int64_t({cfg.NO}) * C;")
-    # v_p[m1][m2] per channel, from g
     vnames = {}
-    a(f"  float v[CPL][{sum(1 for p in ps for m1 in range(2*p['l1']+1) for m2 in range(2*p['l2']+1) if np.any(np.abs(p['c'][m1, m2, :]) > EPS))}];")
+    a(f"  float v[CPL][{_v_count(ps)}];")
     a("#pragma unroll")
     a("  for (int k = 0; k < CPL; ++k) {")
     a(f"    float gv[{len(outs)}];")
@@ -244,29 +285,18 @@ def gen_bwd(cfg: Cfg, g: int) -> str:
                 vnames[(j, m1, m2)] = vi
                 vi += 1
     a("  }")
-    a("  const int beg = row_ptr[n], end = row_ptr[n + 1];")
-    a("  for (int t = beg; t < end; ++t) {")
-    a("    const int e = perm[t], s = snd[t];")
-    a(f"    const float* __restrict__ Ye = Y + int64_t(e) * {cfg.NY};")
-    for c in ys:
-        a(f"    const float y{c} = Ye[{c}];")
-    a("    const float* __restrict__ xs = x + int64_t(s) * XS;")
+    _emit_edge_loop_head(a, cfg, ps, xs, ys, xi)
     a("    float* __restrict__ gwe = gw ? gw + int64_t(e) * WS : nullptr;")
-    a("    const float* __restrict__ we = w + int64_t(e) * WS;")
     a(f"    float gy[{V}];")
     a("#pragma unroll")
     a(f"    for (int i = 0; i < {V}; ++i) gy[i] = 0.f;")
     a("#pragma unroll")
     a("    for (int k = 0; k < CPL; ++k) {")
-    a(f"      float xv[{len(xs)}], wv[{len(ps)}], gxl[{len(xs)}];")
+    a(f"      float gxl[{len(xs)}];")
     for c in xs:
-        a(f"      xv[{xi[c]}] = ok[k] ? xs[{c} * C + cc[k]] : 0.f;")
         a(f"      gxl[{xi[c]}] = 0.f;")
     for j, p in enumerate(ps):
-        a(f"      wv[{j}] = ok[k] ? __builtin_nontemporal_load(we + {p['k']} * C + cc[k]) : 0.f;")
-    for j, p in enumerate(ps):
         n1, n2 = 2 * p["l1"] + 1, 2 * p["l2"] + 1
-        # u[m1] = sum_m2 y v ; s[m2] = sum_m1 x v
         for m1 in range(n1):
             ts = [m2 for m2 in range(n2) if (j, m1, m2) in vnames]
             if not ts:
@@ -275,17 +305,17 @@ def gen_bwd(cfg: Cfg, g: int) -> str:
             for m2 in ts[1:]:
                 expr = f"fmaf(y{p['o2'] + m2}, v[k][{vnames[(j, m1, m2)]}], {expr})"
             a(f"      const float u{j}_{m1} = {expr};")
-            a(f"      gxl[{xi[p['o1'] + m1]}] = fmaf(wv[{j}], u{j}_{m1}, gxl[{xi[p['o1'] + m1]}]);")
+            a(f"      gxl[{xi[p['o1'] + m1]}] = fmaf(wv[k][{j}], u{j}_{m1}, gxl[{xi[p['o1'] + m1]}]);")
         svals = []
         for m2 in range(n2):
             ts = [m1 for m1 in range(n1) if (j, m1, m2) in vnames]
             if not ts:
                 continue
-            expr = f"xv[{xi[p['o1'] + ts[0]]}] * v[k][{vnames[(j, ts[0], m2)]}]"
+            expr = f"xv[k][{xi[p['o1'] + ts[0]]}] * v[k][{vnames[(j, ts[0], m2)]}]"
             for m1 in ts[1:]:
-                expr = f"fmaf(xv[{xi[p['o1'] + m1]}], v[k][{vnames[(j, m1, m2)]}], {expr})"
+                expr = f"fmaf(xv[k][{xi[p['o1'] + m1]}], v[k][{vnames[(j, m1, m2)]}], {expr})"
             a(f"      const float s{j}_{m2} = {expr};")
-            a(f"      gy[{p['o2'] + m2}] = fmaf(wv[{j}], s{j}_{m2}, gy[{p['o2'] + m2}]);")
+            a(f"      gy[{p['o2'] + m2}] = fmaf(wv[k][{j}], s{j}_{m2}, gy[{p['o2'] + m2}]);")
             svals.append(m2)
         if svals:
             expr = f"y{p['o2'] + svals[0]} * s{j}_{svals[0]}"
@@ -336,12 +366,18 @@ def generate() -> str:
             fns += ["nullptr"] * (4 - len(fns))
             out.append("  {" + ", ".join(fns) + "},")
         out.append("};")
-        out.append(f"static const TPBwdFn kTPBwd{cpl}[][4] = {{")
-        for cfg in cfgs:
-            fns = [f"tp_bwd_c{cfg.idx}_g{g}<{cpl}>" for g in range(len(cfg.groups))]
-            fns += ["nullptr"] * (4 - len(fns))
-            out.append("  {" + ", ".join(fns) + "},")
-        out.append("};")
+    # backward: one instantiation per group, channels per lane chosen by register budget
+    out.append("static const TPBwdFn kTPBwd[][4] = {")
+    for cfg in cfgs:
+        fns = [f"tp_bwd_c{cfg.idx}_g{g}<{bwd_cpl(ps)}>" for g, ps in enumerate(cfg.groups)]
+        fns += ["nullptr"] * (4 - len(fns))
+        out.append("  {" + ", ".join(fns) + "},")
+    out.append("};")
+    out.append("static const int kTPBwdCPL[][4] = {")
+    for cfg in cfgs:
+        cp = [str(bwd_cpl(ps)) for ps in cfg.groups] + ["0"] * (4 - len(cfg.groups))
+        out.append("  {" + ", ".join(cp) + "},")
+    out.append("};")
     return "\n".join(out) + "\n"
 
 

@@ -27,25 +27,67 @@ __device__ __forceinline__ int64_t xcd_node(int64_t b, int64_t nblocks) {
     return (b & 7) * per + (b >> 3);
 }
 
+// Cross-lane exchanges without LDS.  Stride 32 / 16: gfx950's permlane swaps
+// exchange the upper half of `x` with the lower half of `z` (per 64- or
+// 32-lane half), so x' + z' is, on every lane, the pair sum of the value that
+// lane keeps (x on the lower lanes, z on the upper).  Stride 8 / 4 / 2 / 1: DPP
+// row_mirror, row_half_mirror and quad_perm pair lane L with L^15, L^7, L^3,
+// L^1, which flip bit 3, 2, 1, 0 of the lane id respectively.
+__device__ __forceinline__ void pair_sum_swap32(float& x, float& z) {
+    auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(z), false, false);
+    x = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ void pair_sum_swap16(float& x, float& z) {
+    auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(z), false, false);
+    x = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+template <int OFF>
+__device__ __forceinline__ float dpp_partner(float v) {
+    static_assert(OFF == 8 || OFF == 4 || OFF == 2 || OFF == 1, "row-local stride");
+    return OFF == 8 ? dpp<0x140>(v) : OFF == 4 ? dpp<0x141>(v) : OFF == 2 ? dpp<0x1b>(v) : dpp<0xb1>(v);
+}
+
+template <int OFF, int CNT, int V>
+__device__ __forceinline__ void rs_step(float (&a)[V], int lane) {
+    if constexpr (CNT > 1) {
+        constexpr int h = CNT / 2;
+        if constexpr (OFF == 32 || OFF == 16) {
+#pragma unroll
+            for (int i = 0; i < h; ++i) {
+                if constexpr (OFF == 32) pair_sum_swap32(a[i], a[h + i]);
+                else pair_sum_swap16(a[i], a[h + i]);
+            }
+        } else {
+            const bool hi = (lane & OFF) != 0;
+#pragma unroll
+            for (int i = 0; i < h; ++i) {
+                const float keep = hi ? a[h + i] : a[i];
+                const float send = hi ? a[i] : a[h + i];
+                a[i] = keep + dpp_partner<OFF>(send);
+            }
+        }
+        rs_step<OFF / 2, h, V>(a, lane);
+    } else if constexpr (OFF >= 1) {
+        if constexpr (OFF == 32 || OFF == 16) {
+            float z = a[0];
+            if constexpr (OFF == 32) pair_sum_swap32(a[0], z);
+            else pair_sum_swap16(a[0], z);
+        } else {
+            a[0] += dpp_partner<OFF>(a[0]);
+        }
+        rs_step<OFF / 2, 1, V>(a, lane);
+    }
+}
+
 // Sum V per-lane values over the 64 lanes; returns one of the V sums, which one
 // given by reduce_scatter_index (lanes sharing an index hold the same sum).
 template <int V>
 __device__ __forceinline__ float wave_reduce_scatter(float (&a)[V], int lane) {
-    int off = 32;
-#pragma unroll
-    for (int cnt = V; cnt > 1; cnt >>= 1) {
-        const bool hi = (lane & off) != 0;
-        const int h = cnt >> 1;
-#pragma unroll
-        for (int i = 0; i < h; ++i) {
-            const float send = hi ? a[i] : a[h + i];
-            const float keep = hi ? a[h + i] : a[i];
-            a[i] = keep + __shfl_xor(send, off);
-        }
-        off >>= 1;
-    }
-#pragma unroll
-    for (; off >= 1; off >>= 1) a[0] += __shfl_xor(a[0], off);
+    rs_step<32, V, V>(a, lane);
     return a[0];
 }
 
@@ -67,7 +109,7 @@ struct TPConfigInfo {
 typedef void (*TPFwdFn)(const float*, const float*, const float*, const int32_t*, const int32_t*, const int32_t*,
                         int64_t, int, float*);
 typedef void (*TPBwdFn)(const float*, const float*, const float*, const float*, const int32_t*, const int32_t*,
-                        const int32_t*, int64_t, int, float*, float*, float*, int);
+                        const int32_t*, int64_t, int, float*, float*, float*, int, int);
 
 #include "tp_gen.inc"
 
@@ -91,6 +133,13 @@ int check_common(int config, int channels, int64_t N, int64_t E) {
 }
 
 dim3 node_grid(int64_t N, int cblocks) { return dim3(unsigned(8 * ceil_div(N > 0 ? N : 1, 8)), unsigned(cblocks)); }
+
+// grad_Y partial rows per edge: one per (backward group, channel block)
+int64_t bwd_partials(int config, int C) {
+    int64_t np = 0;
+    for (int g = 0; g < kTPConfigs[config].ngroups; ++g) np += ceil_div(C, 64 * kTPBwdCPL[config][g]);
+    return np;
+}
 
 }  // namespace
 }  // namespace mnx
@@ -140,8 +189,7 @@ int mnx_tp_fwd_f32(int32_t config, int32_t C, const float* x, const float* Y, co
 size_t mnx_tp_bwd_workspace_bytes(int32_t config, int32_t C, int64_t E) {
     if (config < 0 || config >= kNumTPConfigs || C <= 0 || E < 0) return 0;
     const TPConfigInfo& cfg = kTPConfigs[config];
-    const int64_t npart = int64_t(cfg.ngroups) * ceil_div(C, 64);
-    return size_t(E > 0 ? E : 1) * size_t(npart) * size_t(cfg.ny) * sizeof(float) + 256;
+    return size_t(E > 0 ? E : 1) * size_t(bwd_partials(config, C)) * size_t(cfg.ny) * sizeof(float) + 256;
 }
 
 int mnx_tp_bwd_f32(int32_t config, int32_t C, const float* x, const float* Y, const float* w, const float* gout,
@@ -153,8 +201,7 @@ int mnx_tp_bwd_f32(int32_t config, int32_t C, const float* x, const float* Y, co
     if (N == 0 || E == 0) return MNX_OK;
     MNX_REQUIRE(x && Y && w && gout && row_ptr && perm && snd, "null pointer argument");
     const TPConfigInfo& cfg = kTPConfigs[config];
-    const int cblocks = int(ceil_div(C, 64));
-    const int npart = cfg.ngroups * cblocks;
+    const int npart = int(bwd_partials(config, C));
     float* part = nullptr;
     if (gY) {
         const size_t need = mnx_tp_bwd_workspace_bytes(config, C, E);
@@ -164,12 +211,13 @@ int mnx_tp_bwd_f32(int32_t config, int32_t C, const float* x, const float* Y, co
         // out-of-range indices), so the buffer needs no clearing.
         part = static_cast<float*>(ws);
     }
-    const dim3 grid = node_grid(N, cblocks);
+    int pbase = 0;
     for (int g = 0; g < cfg.ngroups; ++g) {
-        TPBwdFn fn = kTPBwd1[config][g];
-        hipLaunchKernelGGL(fn, grid, dim3(64), 0, (hipStream_t)stream, x, Y, w, gout, row_ptr, perm, snd, N, C, gx,
-                           gw, part, npart);
+        const int cblocks = int(ceil_div(C, 64 * kTPBwdCPL[config][g]));
+        hipLaunchKernelGGL(kTPBwd[config][g], node_grid(N, cblocks), dim3(64), 0, (hipStream_t)stream, x, Y, w, gout,
+                           row_ptr, perm, snd, N, C, gx, gw, part, npart, pbase);
         MNX_CHECK_LAUNCH();
+        pbase += cblocks;
     }
     if (gY) {
         const int64_t tot = E * cfg.ny;

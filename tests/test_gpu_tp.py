@@ -94,10 +94,12 @@ def test_tp_empty_receivers_and_no_edges(ops):
     config = K.tp_config_id([0, 1], [0, 1], [0, 1])
     ei = torch.zeros((0, 2), dtype=torch.int64, device=DEV)
     row_ptr, perm, snd = ops.edge_csr(ei, N)
-    x = torch.randn(N, 4 * C, device=DEV)
-    out = ops.tp_scatter(x, torch.zeros((0, 4), device=DEV), torch.zeros((0, 5 * C), device=DEV), row_ptr, perm, snd,
-                         config, C)
-    assert out.shape == (N, 10 * C) and torch.all(out == 0)
+    num_paths, nx, ny, no = K.tp_config_info(config)
+    assert (num_paths, nx, ny, no) == (4, 4, 4, 8)
+    x = torch.randn(N, nx * C, device=DEV)
+    out = ops.tp_scatter(x, torch.zeros((0, ny), device=DEV), torch.zeros((0, num_paths * C), device=DEV), row_ptr,
+                         perm, snd, config, C)
+    assert out.shape == (N, no * C) and torch.all(out == 0)
 
 
 def test_edge_csr_rejects_out_of_range(ops):
