@@ -45,6 +45,9 @@ def parse():
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--unsorted", action="store_true", help="keep atoms in random order (no spatial sort)")
     p.add_argument("--seed", type=int, default=0)
+    p.add_argument("--kernels-only", action="store_true",
+                   help="profiling aid: a 1 GiB device copy (counter calibration), then 3 TP forward and "
+                        "3 TP backward launches; prints their event times")
     return p.parse_args()
 
 
@@ -149,6 +152,17 @@ def time_tp_kernels(step: EdgeStep, reps: int = 5):
     return tf, tb
 
 
+def measured_traffic(kernel: str):
+    """HBM bytes per launch (FETCH_SIZE x calibration + WRITE_SIZE) of `kernel` at config 3,
+    recorded from rocprofv3 --pmc runs in profiles/tp_scatter_config3_traffic.{json,md}."""
+    path = os.path.join(ROOT, "profiles", "tp_scatter_config3_traffic.json")
+    try:
+        rec = json.load(open(path))[kernel]
+        return int(rec["read_bytes"] + rec["write_bytes"])
+    except (OSError, KeyError, ValueError):
+        return None
+
+
 def tp_bytes(N, E, C, P=23, NX=16, NY=16, NO=99):
     """Algorithmic HBM bytes (each tensor once at its width; fp32, int32 CSR)."""
     csr = E * 8 + (N + 1) * 4
@@ -209,6 +223,14 @@ def main():
     pos, box, edge_index, vec, L = make_system(args.atoms, args.seed, not args.unsorted, dev)
     N, E = pos.shape[0], edge_index.shape[0]
     step = EdgeStep(N, edge_index, vec, args.channels, args.seed, dev)
+    if args.kernels_only:
+        src = torch.empty(1 << 28, dtype=torch.float32, device=dev).fill_(1.0)
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        tf, tb = time_tp_kernels(step, reps=3)
+        print(json.dumps({"copy_bytes": 2 * src.numel() * 4, "tp_fwd_ms": tf, "tp_bwd_ms": tb, "edges": E}))
+        return
     for _ in range(args.warmup):
         step.step()
     torch.cuda.synchronize()
@@ -224,9 +246,10 @@ def main():
     bf, bb = tp_bytes(N, E, args.channels)
     dom_t, dom_b, dom_name = (tb, bb, "tp_scatter_bwd") if tb >= tf else (tf, bf, "tp_scatter_fwd")
     achieved = dom_b / (dom_t * 1e-3) / 1e9
+    traffic = measured_traffic(dom_name) if args.channels == 128 and args.atoms == 50_000 else None
     roof = {
         "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-        "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None, "kernel": dom_name,
+        "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic, "kernel": dom_name,
         "kernel_ms": round(dom_t, 3), "algorithmic_bytes": dom_b,
         "other": {"tp_scatter_fwd_ms": round(tf, 3), "tp_scatter_fwd_GBs": round(bf / (tf * 1e-3) / 1e9, 1),
                   "tp_scatter_bwd_ms": round(tb, 3), "tp_scatter_bwd_GBs": round(bb / (tb * 1e-3) / 1e9, 1)},
