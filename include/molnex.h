@@ -153,6 +153,54 @@ int mnx_tp_bwd_f32(int32_t config, int32_t channels, const float* x, const float
                    int64_t num_edges, float* grad_x, float* grad_Y, float* grad_w,
                    void* workspace, size_t workspace_bytes, mnx_stream_t stream);
 
+/* ------------------------------------------------------------------------ */
+/* Particle-mesh Ewald (replaces torch.ops.molix.pme_reciprocal and           */
+/* pme_direct: molix_library.cpp:29-41, CPU pme_cpu.cpp:95-458, CUDA          */
+/* pme_cuda.cu:106-523).  box: device 3x3 lower-triangular cell.  The caller  */
+/* runs the 3-D real FFTs (rocFFT) between the stages:                        */
+/*   spread -> rfftn -> convolve (energy)   and   irfftn(norm=forward) -> gather */
+/* Spline orders 3..8 (the reference CUDA path: 4, 5).                        */
+/* ------------------------------------------------------------------------ */
+/* grid[gx][gy][gz] (overwritten) = sum_atoms q sqrt(coulomb) B(x) B(y) B(z)  (pme_cpu.cpp:240-256) */
+int mnx_pme_spread_f32(const float* pos, const float* charges, const float* box, int64_t num_atoms,
+                       int32_t gx, int32_t gy, int32_t gz, int32_t order, double coulomb, float* grid,
+                       mnx_stream_t stream);
+int mnx_pme_spread_f64(const double* pos, const double* charges, const double* box, int64_t num_atoms,
+                       int32_t gx, int32_t gy, int32_t gz, int32_t order, double coulomb, double* grid,
+                       mnx_stream_t stream);
+/* In place on the half spectrum cgrid[gx][gy][gz/2+1] (interleaved re, im):
+ * G *= exp(-pi^2 m^2/alpha^2) / (pi V m^2 xm ym zm), m = 0 term zeroed;
+ * *energy = 1/2 sum scale |G|^2 eterm before the multiply (pme_cpu.cpp:263-294, 378). */
+size_t mnx_pme_convolve_workspace_bytes(int32_t gx, int32_t gy, int32_t gz);
+int mnx_pme_convolve_f32(float* cgrid, const float* box, int32_t gx, int32_t gy, int32_t gz, double alpha,
+                         const float* xmoduli, const float* ymoduli, const float* zmoduli,
+                         float* energy, void* workspace, size_t workspace_bytes, mnx_stream_t stream);
+int mnx_pme_convolve_f64(double* cgrid, const double* box, int32_t gx, int32_t gy, int32_t gz,
+                         double alpha, const double* xmoduli, const double* ymoduli,
+                         const double* zmoduli, double* energy, void* workspace,
+                         size_t workspace_bytes, mnx_stream_t stream);
+/* From the back-transformed grid: dE/dpos [n][3] and dE/dq [n] (pme_cpu.cpp:311-343). */
+int mnx_pme_gather_f32(const float* pos, const float* charges, const float* box, int64_t num_atoms,
+                       const float* grid, int32_t gx, int32_t gy, int32_t gz, int32_t order,
+                       double coulomb, float* dpos, float* dq, mnx_stream_t stream);
+int mnx_pme_gather_f64(const double* pos, const double* charges, const double* box, int64_t num_atoms,
+                       const double* grid, int32_t gx, int32_t gy, int32_t gz, int32_t order,
+                       double coulomb, double* dpos, double* dq, mnx_stream_t stream);
+/* Real-space sum over a pair list neighbors[2][num_pairs] (i = -1 padding skipped) minus the
+ * erf term of excluded pairs; exclusions[n][max_excl] descending, -1 padded (pme_cpu.cpp:95-164).
+ * *energy, dpos [n][3], dq [n] are overwritten. */
+size_t mnx_pme_direct_workspace_bytes(int64_t num_atoms, int64_t num_pairs);
+int mnx_pme_direct_f32(const float* pos, const float* charges, int64_t num_atoms, const int32_t* neighbors,
+                       int64_t num_pairs, const float* deltas, const float* distances,
+                       const int32_t* exclusions, int32_t max_excl, double alpha, double coulomb,
+                       float* energy, float* dpos, float* dq, void* workspace, size_t workspace_bytes,
+                       mnx_stream_t stream);
+int mnx_pme_direct_f64(const double* pos, const double* charges, int64_t num_atoms,
+                       const int32_t* neighbors, int64_t num_pairs, const double* deltas,
+                       const double* distances, const int32_t* exclusions, int32_t max_excl,
+                       double alpha, double coulomb, double* energy, double* dpos, double* dq,
+                       void* workspace, size_t workspace_bytes, mnx_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -378,3 +378,166 @@ def _tp_backward(ctx, grad_out):
 
 
 tp_scatter.register_autograd(_tp_backward, setup_context=_tp_setup)
+
+
+# ---------------------------------------------------------------------------
+# Particle-mesh Ewald (reference schemas, molix_library.cpp:29-41)
+# ---------------------------------------------------------------------------
+
+_PME_RECIP_SCHEMA = ("(Tensor positions, Tensor charges, Tensor box_vectors, Scalar gridx, Scalar gridy, "
+                     "Scalar gridz, Scalar order, Scalar alpha, Scalar coulomb, Tensor xmoduli, Tensor ymoduli, "
+                     "Tensor zmoduli) -> Tensor")
+_PME_DIRECT_SCHEMA = ("(Tensor positions, Tensor charges, Tensor neighbors, Tensor deltas, Tensor distances, "
+                      "Tensor exclusions, Scalar alpha, Scalar coulomb) -> Tensor")
+
+
+def _fsuffix(t: Tensor) -> str:
+    if t.dtype == torch.float64:
+        return "f64"
+    if t.dtype == torch.float32:
+        return "f32"
+    raise TypeError(f"PME needs float32 or float64 tensors, got {t.dtype}")
+
+
+def _pme_recip_energy(positions, charges, box, gx, gy, gz, order, alpha, coulomb, xm, ym, zm):
+    """spread -> rfftn (rocFFT) -> convolve; returns (energy, convolved half spectrum)."""
+    lib = _lib.load()
+    sfx = _fsuffix(positions)
+    dt, dev = positions.dtype, positions.device
+    pos = positions.detach().contiguous()
+    q = charges.detach().to(dt).contiguous()
+    b = box.detach().to(device=dev, dtype=dt).contiguous()
+    mods = [m.detach().to(device=dev, dtype=dt).contiguous() for m in (xm, ym, zm)]
+    for m, g in zip(mods, (gx, gy, gz)):
+        if m.numel() < g:
+            raise ValueError("moduli shorter than the grid")
+    grid = torch.empty((gx, gy, gz), dtype=dt, device=dev)
+    check(getattr(lib, f"mnx_pme_spread_{sfx}")(ptr(pos), ptr(q), ptr(b), pos.shape[0], gx, gy, gz, order,
+                                                float(coulomb), ptr(grid), _stream(pos)), "pme spread")
+    spec = torch.fft.rfftn(grid).contiguous()
+    energy = torch.empty((), dtype=dt, device=dev)
+    ws = _ws(lib.mnx_pme_convolve_workspace_bytes(gx, gy, gz), dev)
+    check(getattr(lib, f"mnx_pme_convolve_{sfx}")(ptr(torch.view_as_real(spec)), ptr(b), gx, gy, gz, float(alpha),
+                                                  ptr(mods[0]), ptr(mods[1]), ptr(mods[2]), ptr(energy), ptr(ws),
+                                                  ws.numel(), _stream(pos)), "pme convolve")
+    return energy, spec, pos, q, b
+
+
+@torch.library.custom_op("molix::pme_reciprocal", mutates_args=(), device_types="cuda", schema=_PME_RECIP_SCHEMA)
+def pme_reciprocal(positions, charges, box_vectors, gridx, gridy, gridz, order, alpha, coulomb, xmoduli, ymoduli,
+                   zmoduli):
+    """Reciprocal-space PME energy (reference ``pme_cpu.cpp:220-296,378``): B-spline spread on the GPU,
+    rocFFT real-to-complex transform, influence-function convolution with the energy sum."""
+    _require_gpu("pme_reciprocal", positions, charges, box_vectors)
+    e, *_ = _pme_recip_energy(positions, charges, box_vectors, int(gridx), int(gridy), int(gridz), int(order),
+                              alpha, coulomb, xmoduli, ymoduli, zmoduli)
+    return e
+
+
+@pme_reciprocal.register_fake
+def _(positions, charges, box_vectors, gridx, gridy, gridz, order, alpha, coulomb, xmoduli, ymoduli, zmoduli):
+    return positions.new_empty(())
+
+
+@torch.library.custom_op("molix::pme_reciprocal_backward", mutates_args=(), device_types="cuda")
+def pme_reciprocal_backward(positions: Tensor, charges: Tensor, box_vectors: Tensor, gridx: int, gridy: int,
+                            gridz: int, order: int, alpha: float, coulomb: float, xmoduli: Tensor, ymoduli: Tensor,
+                            zmoduli: Tensor) -> tuple[Tensor, Tensor]:
+    """(dE/dpos, dE/dq): recompute the convolved spectrum, irfftn(norm='forward'), gather
+    (reference backward ``pme_cpu.cpp:392-430``)."""
+    lib = _lib.load()
+    _, spec, pos, q, b = _pme_recip_energy(positions, charges, box_vectors, gridx, gridy, gridz, order, alpha,
+                                           coulomb, xmoduli, ymoduli, zmoduli)
+    real = torch.fft.irfftn(spec, s=(gridx, gridy, gridz), norm="forward").contiguous()
+    dpos = torch.empty_like(pos)
+    dq = torch.empty_like(q)
+    check(getattr(lib, f"mnx_pme_gather_{_fsuffix(pos)}")(ptr(pos), ptr(q), ptr(b), pos.shape[0], ptr(real), gridx,
+                                                          gridy, gridz, order, float(coulomb), ptr(dpos), ptr(dq),
+                                                          _stream(pos)), "pme gather")
+    return dpos, dq
+
+
+@pme_reciprocal_backward.register_fake
+def _(positions, charges, box_vectors, gridx, gridy, gridz, order, alpha, coulomb, xmoduli, ymoduli, zmoduli):
+    return torch.empty_like(positions), torch.empty_like(charges)
+
+
+def _pme_recip_setup(ctx, inputs, output):
+    ctx.save_for_backward(inputs[0], inputs[1], inputs[2], inputs[9], inputs[10], inputs[11])
+    ctx.args = tuple(inputs[3:9])
+
+
+def _pme_recip_bwd(ctx, grad):
+    pos, q, box, xm, ym, zm = ctx.saved_tensors
+    gx, gy, gz, order, alpha, coulomb = ctx.args
+    dpos, dq = pme_reciprocal_backward(pos, q, box, int(gx), int(gy), int(gz), int(order), float(alpha),
+                                       float(coulomb), xm, ym, zm)
+    return (dpos * grad, (dq * grad).to(q.dtype)) + (None,) * 10
+
+
+pme_reciprocal.register_autograd(_pme_recip_bwd, setup_context=_pme_recip_setup)
+
+
+def _pme_direct_run(positions, charges, neighbors, deltas, distances, exclusions, alpha, coulomb):
+    lib = _lib.load()
+    sfx = _fsuffix(positions)
+    dt, dev = positions.dtype, positions.device
+    pos = positions.detach().contiguous()
+    q = charges.detach().to(dt).contiguous()
+    nb = neighbors.to(torch.int32).contiguous()
+    dl = deltas.detach().to(dt).contiguous()
+    ds = distances.detach().to(dt).contiguous()
+    ex = exclusions.to(device=dev, dtype=torch.int32).contiguous()
+    n, P = pos.shape[0], nb.shape[1]
+    if ex.ndim != 2 or (ex.numel() and ex.shape[0] != n):
+        raise ValueError("exclusions must be (num_atoms, max_exclusions)")
+    max_excl = ex.shape[1] if ex.numel() else 0
+    energy = torch.empty((), dtype=dt, device=dev)
+    dpos = torch.empty_like(pos)
+    dq = torch.empty_like(q)
+    ws = _ws(lib.mnx_pme_direct_workspace_bytes(n, P), dev)
+    check(getattr(lib, f"mnx_pme_direct_{sfx}")(ptr(pos), ptr(q), n, ptr(nb), P, ptr(dl), ptr(ds), ptr(ex), max_excl,
+                                                float(alpha), float(coulomb), ptr(energy), ptr(dpos), ptr(dq), ptr(ws),
+                                                ws.numel(), _stream(pos)), "pme direct")
+    return energy, dpos, dq
+
+
+@torch.library.custom_op("molix::pme_direct", mutates_args=(), device_types="cuda", schema=_PME_DIRECT_SCHEMA)
+def pme_direct(positions, charges, neighbors, deltas, distances, exclusions, alpha, coulomb):
+    """Real-space PME energy over a pair list minus excluded pairs (reference ``pme_cpu.cpp:95-216``).
+    Like the reference, the gradient w.r.t. positions is the analytic one through the pair
+    geometry (deltas / distances are treated as functions of positions, ``pme_cpu.cpp:208-215``)."""
+    _require_gpu("pme_direct", positions, charges, neighbors)
+    e, _, _ = _pme_direct_run(positions, charges, neighbors, deltas, distances, exclusions, alpha, coulomb)
+    return e
+
+
+@pme_direct.register_fake
+def _(positions, charges, neighbors, deltas, distances, exclusions, alpha, coulomb):
+    return positions.new_empty(())
+
+
+@torch.library.custom_op("molix::pme_direct_backward", mutates_args=(), device_types="cuda")
+def pme_direct_backward(positions: Tensor, charges: Tensor, neighbors: Tensor, deltas: Tensor, distances: Tensor,
+                        exclusions: Tensor, alpha: float, coulomb: float) -> tuple[Tensor, Tensor]:
+    _, dpos, dq = _pme_direct_run(positions, charges, neighbors, deltas, distances, exclusions, alpha, coulomb)
+    return dpos, dq
+
+
+@pme_direct_backward.register_fake
+def _(positions, charges, neighbors, deltas, distances, exclusions, alpha, coulomb):
+    return torch.empty_like(positions), torch.empty_like(charges)
+
+
+def _pme_direct_setup(ctx, inputs, output):
+    ctx.save_for_backward(*inputs[:6])
+    ctx.args = (float(inputs[6]), float(inputs[7]))
+
+
+def _pme_direct_bwd(ctx, grad):
+    dpos, dq = pme_direct_backward(*ctx.saved_tensors, *ctx.args)
+    q = ctx.saved_tensors[1]
+    return (dpos * grad, (dq * grad).to(q.dtype)) + (None,) * 6
+
+
+pme_direct.register_autograd(_pme_direct_bwd, setup_context=_pme_direct_setup)
