@@ -201,6 +201,20 @@ int mnx_pme_direct_f64(const double* pos, const double* charges, int64_t num_ato
                        double alpha, double coulomb, double* energy, double* dpos, double* dq,
                        void* workspace, size_t workspace_bytes, mnx_stream_t stream);
 
+/* ------------------------------------------------------------------------ */
+/* Symmetric contraction of scalar channels, as the reference configures it  */
+/* (cuet.SymmetricContraction("{D}x0e" -> "{D}x0e", original_mace=True),     */
+/* src/molrep/interaction/symmetric_contraction.py:90-109):                  */
+/*   out[n][c] = sum_{k=1..nu} W[types[n]][k-1][c] x[n][c]^k                 */
+/* W [S][nu][D], S <= 16, nu <= 4.  grad_W is accumulated (zero it first).   */
+/* ------------------------------------------------------------------------ */
+int mnx_sc_scalar_fwd_f32(const float* x, const int64_t* types, const float* W, int64_t num_nodes,
+                          int32_t channels, int32_t num_elements, int32_t degree, float* out,
+                          mnx_stream_t stream);
+int mnx_sc_scalar_bwd_f32(const float* x, const int64_t* types, const float* W, const float* grad_out,
+                          int64_t num_nodes, int32_t channels, int32_t num_elements, int32_t degree,
+                          float* grad_x, float* grad_W, mnx_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -52,6 +52,8 @@ SIGNATURES = {
                                      vp]),
     "mnx_pme_direct_f64": (C.c_int, [vp, vp, c_i64, vp, c_i64, vp, vp, vp, c_i32, c_f64, c_f64, vp, vp, vp, vp, c_sz,
                                      vp]),
+    "mnx_sc_scalar_fwd_f32": (C.c_int, [vp, vp, vp, c_i64, c_i32, c_i32, c_i32, vp, vp]),
+    "mnx_sc_scalar_bwd_f32": (C.c_int, [vp, vp, vp, vp, c_i64, c_i32, c_i32, c_i32, vp, vp, vp]),
 }
 
 

@@ -1,0 +1,15 @@
+"""Global dtypes, mirroring molix.config (src/molix/config.py:13-20).
+
+The HIP kernels compute in fp32 (the north-star path); modules bake
+``config.ftype`` at construction like the reference (e.g. linear.py:89).
+"""
+
+import torch
+
+
+class _Config:
+    ftype: torch.dtype = torch.float32
+    itype: torch.dtype = torch.int64
+
+
+config = _Config()

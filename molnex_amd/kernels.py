@@ -541,3 +541,62 @@ def _pme_direct_bwd(ctx, grad):
 
 
 pme_direct.register_autograd(_pme_direct_bwd, setup_context=_pme_direct_setup)
+
+
+# ---------------------------------------------------------------------------
+# Symmetric contraction of scalar channels (symmetric_contraction.py:90-109)
+# ---------------------------------------------------------------------------
+
+
+@torch.library.custom_op("molix::symmetric_contraction_scalar", mutates_args=(), device_types="cuda")
+def symmetric_contraction_scalar(x: Tensor, atom_types: Tensor, weight: Tensor) -> Tensor:
+    """``out[n, c] = sum_k weight[z_n, k, c] x[n, c]^(k+1)``; weight ``(S, degree, D)``."""
+    _require_gpu("symmetric_contraction_scalar", x, atom_types, weight)
+    S, nu, D = weight.shape
+    xs = _f32_rows(x, D, "x")
+    z = atom_types.to(torch.int64).contiguous()
+    w = weight.contiguous()
+    out = torch.empty_like(xs)
+    check(_lib.load().mnx_sc_scalar_fwd_f32(ptr(xs), ptr(z), ptr(w), xs.shape[0], D, S, nu, ptr(out), _stream(xs)),
+          "symmetric_contraction_scalar")
+    return out.reshape(x.shape)
+
+
+@symmetric_contraction_scalar.register_fake
+def _(x, atom_types, weight):
+    return torch.empty_like(x)
+
+
+@torch.library.custom_op("molix::symmetric_contraction_scalar_backward", mutates_args=(), device_types="cuda")
+def symmetric_contraction_scalar_backward(grad: Tensor, x: Tensor, atom_types: Tensor, weight: Tensor,
+                                          need_x: bool, need_w: bool) -> tuple[Tensor, Tensor]:
+    S, nu, D = weight.shape
+    xs = _f32_rows(x, D, "x")
+    g = _f32_rows(grad, D, "grad")
+    z = atom_types.to(torch.int64).contiguous()
+    w = weight.contiguous()
+    gx = torch.empty_like(xs) if need_x else xs.new_empty(0)
+    gw = torch.zeros_like(w) if need_w else w.new_empty(0)
+    check(_lib.load().mnx_sc_scalar_bwd_f32(ptr(xs), ptr(z), ptr(w), ptr(g), xs.shape[0], D, S, nu, ptr(gx), ptr(gw),
+                                            _stream(xs)), "symmetric_contraction_scalar backward")
+    return gx.reshape(x.shape) if need_x else gx, gw
+
+
+@symmetric_contraction_scalar_backward.register_fake
+def _(grad, x, atom_types, weight, need_x, need_w):
+    return (torch.empty_like(x) if need_x else x.new_empty(0), torch.empty_like(weight) if need_w else
+            weight.new_empty(0))
+
+
+def _sc_setup(ctx, inputs, output):
+    ctx.save_for_backward(*inputs)
+
+
+def _sc_bwd(ctx, grad):
+    x, z, w = ctx.saved_tensors
+    nx, _, nw = ctx.needs_input_grad
+    gx, gw = symmetric_contraction_scalar_backward(grad.contiguous(), x, z, w, nx, nw)
+    return (gx if nx else None), None, (gw if nw else None)
+
+
+symmetric_contraction_scalar.register_autograd(_sc_bwd, setup_context=_sc_setup)

@@ -1,0 +1,120 @@
+"""Channelwise tensor-product convolution (src/molrep/interaction/tensor_product.py:33-149)
+on the fused HIP gather / TP / scatter kernels.
+
+``ConvTP`` keeps the reference constructor, ``forward(node_features,
+edge_angular, edge_index, tp_weights)``, ``weight_numel``, ``config`` and a
+``cue_tp`` attribute with ``irreps_in1`` / ``irreps_in2`` / ``irreps_out`` /
+``weight_numel`` (tests/test_molzoo/test_mace.py:412-422).
+"""
+
+from __future__ import annotations
+
+import torch
+import torch.nn as nn
+from pydantic import BaseModel
+
+from ... import kernels as K
+from ...irreps import ChannelwiseTPDescriptor, Irrep, Irreps
+from ...irreps import irreps_from_l_max as _irreps_from_l_max
+from ...irreps import sh_irreps_from_l_max as _sh_irreps_from_l_max
+
+
+class ConvTPSpec(BaseModel):
+    in_irreps: str
+    out_irreps: str
+    sh_irreps: str
+
+
+def _natural_ls(irreps: Irreps, what: str) -> list[int]:
+    ls = []
+    for b in irreps:
+        if b.ir.p != (-1) ** b.ir.l:
+            raise ValueError(f"{what}: only natural-parity irreps (0e, 1o, 2e, 3o) are supported, got {b.ir}")
+        ls.append(b.ir.l)
+    if ls != sorted(set(ls)):
+        raise ValueError(f"{what}: irreps must be in ascending l with one block per l, got {irreps}")
+    return ls
+
+
+class EdgeGraph:
+    """Receiver CSR of one edge list, built once and reused by every layer."""
+
+    def __init__(self, edge_index: torch.Tensor, num_nodes: int):
+        self.edge_index = edge_index
+        self.num_nodes = num_nodes
+        self.row_ptr, self.perm, self.senders = torch.ops.molix.edge_csr(edge_index, num_nodes)
+
+
+_graph_cache: dict = {}
+
+
+def edge_graph(edge_index: torch.Tensor, num_nodes: int) -> EdgeGraph:
+    key = (edge_index.data_ptr(), edge_index.shape[0], num_nodes, edge_index._version, edge_index.device)
+    g = _graph_cache.get(key)
+    if g is None or g.edge_index is not edge_index:
+        _graph_cache.clear()
+        g = EdgeGraph(edge_index, num_nodes)
+        _graph_cache[key] = g
+    return g
+
+
+class ChannelWiseTensorProduct(nn.Module):
+    """Channelwise TP x (mul x ir1) (x) Y (1 x ir2) -> mul x ir3 with per-edge weights,
+    gathered from senders and summed into receivers (ir_mul layout)."""
+
+    def __init__(self, irreps_in1, irreps_in2, irreps_out_filter):
+        super().__init__()
+        self.descriptor = ChannelwiseTPDescriptor(irreps_in1, irreps_in2, irreps_out_filter)
+        self.irreps_in1 = self.descriptor.irreps_in1
+        self.irreps_in2 = self.descriptor.irreps_in2
+        self.irreps_out = self.descriptor.irreps_out
+        self.weight_numel = self.descriptor.weight_numel
+        self.channels = self.descriptor.mul
+        in_ls = _natural_ls(self.irreps_in1, "irreps_in1")
+        sh_ls = _natural_ls(self.irreps_in2, "irreps_in2")
+        out_ls = sorted({b.ir.l for b in Irreps(irreps_out_filter)
+                         if b.ir.p == (-1) ** b.ir.l and any(p.l3 == b.ir.l for p in self.descriptor.paths)})
+        self.config_id = K.tp_config_id(in_ls, sh_ls, out_ls)
+        if self.config_id < 0:
+            raise ValueError(f"no compiled tensor-product kernel for in l={in_ls}, sh l={sh_ls}, out l={out_ls}")
+        num_paths, nx, ny, no = K.tp_config_info(self.config_id)
+        if num_paths != self.descriptor.num_paths or no * self.channels != self.irreps_out.dim:
+            raise RuntimeError("compiled tensor-product configuration does not match the path descriptor")
+
+    def forward(self, x, y, weight, indices_1=None, indices_out=None, size_out=None):
+        num_nodes = int(size_out) if size_out is not None else x.shape[0]
+        edge_index = torch.stack([indices_1, indices_out], dim=1)
+        g = edge_graph(edge_index, num_nodes)
+        return self.apply_graph(x, y, weight, g)
+
+    def apply_graph(self, x, y, weight, g: EdgeGraph):
+        return torch.ops.molix.tp_scatter(x, y, weight, g.row_ptr, g.perm, g.senders, self.config_id, self.channels)
+
+
+class ConvTP(nn.Module):
+    """Channelwise tensor product for equivariant message passing, fused with the
+    gather from senders (edge_index[:, 0]) and the scatter-sum into receivers
+    (edge_index[:, 1])."""
+
+    def __init__(self, *, in_irreps: str, out_irreps: str, sh_irreps: str):
+        super().__init__()
+        self.config = ConvTPSpec(in_irreps=in_irreps, out_irreps=out_irreps, sh_irreps=sh_irreps)
+        self.cue_tp = ChannelWiseTensorProduct(Irreps(in_irreps), Irreps(sh_irreps), Irreps(out_irreps))
+        self.weight_numel = self.cue_tp.weight_numel
+
+    def forward(self, node_features: torch.Tensor, edge_angular: torch.Tensor, edge_index: torch.Tensor,
+                tp_weights: torch.Tensor) -> torch.Tensor:
+        g = edge_graph(edge_index, node_features.shape[0])
+        return self.cue_tp.apply_graph(node_features, edge_angular, tp_weights, g)
+
+
+def irreps_from_l_max(l_max: int, hidden_dim: int) -> str:
+    return _irreps_from_l_max(l_max, hidden_dim)
+
+
+def sh_irreps_from_l_max(l_max: int) -> str:
+    return _sh_irreps_from_l_max(l_max)
+
+
+__all__ = ["ConvTP", "ConvTPSpec", "ChannelWiseTensorProduct", "irreps_from_l_max", "sh_irreps_from_l_max",
+           "EdgeGraph", "edge_graph", "Irrep"]

@@ -1,0 +1,176 @@
+"""MACE encoder (src/molzoo/mace.py:65-576) assembled from the HIP-backed modules.
+
+Same constructor, attribute names (``embedding``, ``initial_projection``,
+``interactions.i.{conv_tp, node_linear, radial_mlp, linear}``, ``products``,
+``projections``, ``element_updates``, ``layer_norms``), in/out keys and
+per-layer output ``(n_nodes, num_interactions, num_features)`` as the
+reference.  ``forward`` takes the reference's GraphBatch (any mapping that
+answers ``td["atoms", "Z"]`` or ``td["atoms"]["Z"]``) or keyword tensors.
+"""
+
+from __future__ import annotations
+
+import torch
+import torch.nn as nn
+from pydantic import BaseModel, ConfigDict, Field
+
+from ..config import config
+from ..irreps import Irreps
+from ..molrep.embedding.angular import SphericalHarmonics
+from ..molrep.embedding.cutoff import CosineCutoff, PolynomialCutoff
+from ..molrep.embedding.node import ContinuousEmbeddingSpec, DiscreteEmbeddingSpec, JointEmbedding
+from ..molrep.embedding.radial import BesselRBF
+from ..molrep.interaction.element_update import ElementUpdate
+from ..molrep.interaction.linear import Linear
+from ..molrep.interaction.radial_mlp import RadialWeightMLP
+from ..molrep.interaction.tensor_product import ConvTP, irreps_from_l_max, sh_irreps_from_l_max
+from ..molrep.readout.product_head import ProductHead
+
+
+def _get(td, group: str, key: str):
+    try:
+        return td[group, key]
+    except (KeyError, TypeError):
+        return td[group][key]
+
+
+def _set(td, group: str, key: str, value):
+    try:
+        td[group, key] = value
+    except (KeyError, TypeError):
+        td[group][key] = value
+
+
+class EmbeddingSpec(BaseModel):
+    model_config = ConfigDict(arbitrary_types_allowed=True)
+    node_attr_specs: list[DiscreteEmbeddingSpec | ContinuousEmbeddingSpec] = Field(..., min_length=1)
+    num_features: int = Field(..., gt=0)
+    r_max: float = Field(..., gt=0.0)
+    num_bessel: int = Field(8, gt=0)
+    l_max: int = Field(2, ge=0)
+
+
+class EmbeddingBlock(nn.Module):
+    """Node embedding, harmonics of the edge direction, Bessel x cutoff (mace.py:88-184)."""
+
+    def __init__(self, *, node_attr_specs, num_features: int, r_max: float, num_bessel: int = 8, l_max: int = 2,
+                 cutoff: str = "cosine"):
+        super().__init__()
+        self.config = EmbeddingSpec(node_attr_specs=node_attr_specs, num_features=num_features, r_max=r_max,
+                                    num_bessel=num_bessel, l_max=l_max)
+        self.node_embedding = JointEmbedding(embedding_specs=node_attr_specs, out_dim=num_features)
+        self.radial_embedding = BesselRBF(r_cut=r_max, num_radial=num_bessel)
+        self.spherical_harmonics = SphericalHarmonics(l_max=l_max)
+        self.cutoff_fn = CosineCutoff(r_cut=r_max) if cutoff == "cosine" else PolynomialCutoff(r_cut=r_max)
+
+    def forward(self, Z, bond_dist, bond_diff):
+        node_feats = self.node_embedding(Z=Z)
+        edge_dir = bond_diff / (bond_dist.unsqueeze(-1) + 1e-8)
+        edge_attrs = self.spherical_harmonics(edge_dir)
+        edge_feats = self.radial_embedding(bond_dist) * self.cutoff_fn(bond_dist).unsqueeze(-1)
+        return node_feats, edge_attrs, edge_feats
+
+
+class InteractionSpec(BaseModel):
+    model_config = ConfigDict(arbitrary_types_allowed=True)
+    num_features: int = Field(..., gt=0)
+    num_bessel: int = Field(8, gt=0)
+    l_max: int = Field(2, ge=0)
+    avg_num_neighbors: float = Field(1.0, gt=0.0)
+
+
+class InteractionBlock(nn.Module):
+    """node_linear -> radial MLP -> ConvTP (gather, TP, scatter) -> / avg_num_neighbors -> linear
+    (mace.py:210-337)."""
+
+    def __init__(self, *, num_features: int, num_bessel: int = 8, l_max: int = 2, avg_num_neighbors: float = 1.0):
+        super().__init__()
+        self.config = InteractionSpec(num_features=num_features, num_bessel=num_bessel, l_max=l_max,
+                                      avg_num_neighbors=avg_num_neighbors)
+        irreps_str = irreps_from_l_max(l_max, num_features)
+        self.conv_tp = ConvTP(in_irreps=irreps_str, out_irreps=irreps_str, sh_irreps=sh_irreps_from_l_max(l_max))
+        tp_out_irreps = str(self.conv_tp.cue_tp.irreps_out)
+        self.node_linear = Linear(Irreps(irreps_str), Irreps(irreps_str), dtype=config.ftype)
+        self.radial_mlp = RadialWeightMLP(in_dim=num_bessel, hidden_dim=num_features,
+                                          out_dim=self.conv_tp.weight_numel, num_layers=2)
+        self.linear = Linear(Irreps(tp_out_irreps), Irreps(irreps_str), dtype=config.ftype)
+        self.avg_num_neighbors = avg_num_neighbors
+
+    def forward(self, node_feats, edge_attrs, edge_feats, edge_index):
+        sc = node_feats
+        node_feats_up = self.node_linear(node_feats)
+        tp_weights = self.radial_mlp(edge_feats)
+        messages = self.conv_tp(node_features=node_feats_up, edge_angular=edge_attrs, edge_index=edge_index,
+                                tp_weights=tp_weights)
+        messages = messages / self.avg_num_neighbors
+        return self.linear(messages), sc
+
+
+class MACESpec(BaseModel):
+    model_config = ConfigDict(arbitrary_types_allowed=True)
+    node_attr_specs: list[DiscreteEmbeddingSpec | ContinuousEmbeddingSpec] = Field(..., min_length=1)
+    num_elements: int = Field(..., gt=0)
+    num_features: int = Field(..., gt=0)
+    r_max: float = Field(..., gt=0.0)
+    num_bessel: int = Field(8, gt=0)
+    l_max: int = Field(2, ge=0)
+    num_interactions: int = Field(2, gt=0)
+    correlation: int = Field(2, ge=1, le=3)
+    avg_num_neighbors: float = Field(1.0, gt=0.0)
+    layer_norm: bool = False
+
+
+class MACE(nn.Module):
+    in_keys = [("atoms", "Z"), ("atoms", "pos"), ("edges", "edge_index"), ("edges", "bond_diff"),
+               ("edges", "bond_dist")]
+    out_keys = [("atoms", "node_features")]
+
+    def __init__(self, *, node_attr_specs, num_elements: int, num_features: int, r_max: float, num_bessel: int = 8,
+                 l_max: int = 2, num_interactions: int = 2, correlation: int = 2, avg_num_neighbors: float = 1.0,
+                 layer_norm: bool = False, cutoff: str = "cosine"):
+        super().__init__()
+        self.config = MACESpec(node_attr_specs=node_attr_specs, num_elements=num_elements,
+                               num_features=num_features, r_max=r_max, num_bessel=num_bessel, l_max=l_max,
+                               num_interactions=num_interactions, correlation=correlation,
+                               avg_num_neighbors=avg_num_neighbors, layer_norm=layer_norm)
+        self.embedding = EmbeddingBlock(node_attr_specs=node_attr_specs, num_features=num_features, r_max=r_max,
+                                        num_bessel=num_bessel, l_max=l_max, cutoff=cutoff)
+        irreps_dim = Irreps(irreps_from_l_max(l_max, num_features)).dim
+        self.initial_projection = nn.Linear(num_features, irreps_dim, dtype=config.ftype)
+        self.interactions = nn.ModuleList([
+            InteractionBlock(num_features=num_features, num_bessel=num_bessel, l_max=l_max,
+                             avg_num_neighbors=avg_num_neighbors) for _ in range(num_interactions)])
+        self.products = nn.ModuleList([
+            ProductHead(hidden_dim=irreps_dim, out_dim=num_features, num_radial=num_bessel, l_max=l_max,
+                        max_body_order=correlation, num_species=num_elements) for _ in range(num_interactions)])
+        self.projections = nn.ModuleList([
+            nn.Linear(num_features, irreps_dim, dtype=config.ftype) for _ in range(num_interactions)])
+        self.element_updates = nn.ModuleList([
+            ElementUpdate(hidden_dim=irreps_dim, num_species=num_elements)
+            for _ in range(max(num_interactions - 1, 0))])
+        self.layer_norms = nn.ModuleList([
+            nn.LayerNorm(irreps_dim) if layer_norm else nn.Identity() for _ in range(max(num_interactions - 1, 0))])
+
+    def encode(self, Z, bond_dist, bond_diff, edge_index) -> torch.Tensor:
+        node_feats_init, edge_attrs, edge_feats = self.embedding(Z=Z, bond_dist=bond_dist, bond_diff=bond_diff)
+        node_feats = self.initial_projection(node_feats_init)
+        per_layer = []
+        for i in range(self.config.num_interactions):
+            msg, sc = self.interactions[i](node_feats=node_feats, edge_attrs=edge_attrs, edge_feats=edge_feats,
+                                           edge_index=edge_index)
+            h = self.products[i](node_features=msg, atom_types=Z)
+            per_layer.append(h)
+            h_proj = self.projections[i](h)
+            if i < self.config.num_interactions - 1:
+                node_feats = self.layer_norms[i](self.element_updates[i](h_prev=sc, m_curr=h_proj, atom_types=Z))
+            else:
+                node_feats = h_proj
+        return torch.stack(per_layer, dim=1)
+
+    def forward(self, td=None, *, Z=None, bond_dist=None, bond_diff=None, edge_index=None):
+        if td is None:
+            return self.encode(Z, bond_dist, bond_diff, edge_index)
+        feats = self.encode(_get(td, "atoms", "Z"), _get(td, "edges", "bond_dist"), _get(td, "edges", "bond_diff"),
+                            _get(td, "edges", "edge_index"))
+        _set(td, "atoms", "node_features", feats)
+        return td
