@@ -6,8 +6,10 @@ cuet.Linear calls of mace.py:270-291, element_update.py:101-109, node.py:153-159
 ``out[m, o] += sum_c W_bo[c, o] x_b[m, c] / sqrt(fan_in)`` with ``fan_in`` the
 total input multiplicity of that irrep (ir_mul layout, weights ~ N(0, 1)).
 With ``weight_classes`` the weights are external, one set per class, selected
-per row by ``weight_indices`` (cuet's indexed_linear).  Both run as GEMMs on
-the GPU (hipBLASLt through torch.matmul) over the ir_mul views.
+per row by ``weight_indices`` (cuet's indexed_linear).  Each output block is one
+GEMM (rows = (node, m), K = the concatenated channels of its source blocks) on
+the GPU through torch.mm (hipBLASLt); forward and backward are written out so
+every gradient slice is produced once.
 """
 
 from __future__ import annotations
@@ -51,20 +53,7 @@ class Linear(nn.Module):
 
     def _mix(self, x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
         """x (R, dim_in), w (weight_numel,) -> (R, dim_out)."""
-        R = x.shape[0]
-        outs = []
-        for off_o, mul_o, d, srcs, fan_in in self.plan:
-            if not srcs:
-                outs.append(x.new_zeros(R, d * mul_o))
-                continue
-            acc = None
-            for off_i, mul_i, wo in srcs:
-                xb = x[:, off_i:off_i + d * mul_i].reshape(R, d, mul_i)
-                wb = w[wo:wo + mul_i * mul_o].view(mul_i, mul_o)
-                y = torch.matmul(xb, wb)
-                acc = y if acc is None else acc + y
-            outs.append((acc * (1.0 / math.sqrt(fan_in))).reshape(R, d * mul_o))
-        return torch.cat(outs, dim=1) if len(outs) > 1 else outs[0]
+        return _BlockLinear.apply(x, w, self.plan, self.irreps_out.dim)
 
     def forward(self, x: torch.Tensor, weight: torch.Tensor | None = None,
                 weight_indices: torch.Tensor | None = None) -> torch.Tensor:
@@ -76,19 +65,107 @@ class Linear(nn.Module):
         else:
             if weight is None or weight_indices is None:
                 raise ValueError("indexed linear needs weight and weight_indices")
-            out = x2.new_empty(x2.shape[0], self.irreps_out.dim)
-            idx = weight_indices.reshape(-1)
-            for cls, rows in _class_rows(idx, self.weight_classes):
-                out[rows] = self._mix(x2[rows], weight[cls].reshape(-1))
+            out = _IndexedLinear.apply(x2, weight, weight_indices.reshape(-1), self)
         return out.reshape(*shape[:-1], self.irreps_out.dim)
+
+
+def _gather_rows(x, srcs, d):
+    """(R*d, K) rows (node, m), columns = the channels of every source block of one irrep."""
+    R = x.shape[0]
+    if len(srcs) == 1:
+        o, m, _ = srcs[0]
+        return x[:, o:o + d * m].reshape(R * d, m)
+    return torch.cat([x[:, o:o + d * m].reshape(R, d, m) for o, m, _ in srcs], dim=2).reshape(R * d, -1)
+
+
+def _block_forward(x, w, plan, dim_out):
+    R = x.shape[0]
+    out = x.new_empty(R, dim_out)
+    for off_o, mul_o, d, srcs, fan_in in plan:
+        if not srcs:
+            out[:, off_o:off_o + d * mul_o] = 0
+            continue
+        ws = torch.cat([w[wo:wo + m * mul_o].view(m, mul_o) for _, m, wo in srcs], dim=0)
+        y = torch.mm(_gather_rows(x, srcs, d), ws) * (1.0 / math.sqrt(fan_in))
+        out[:, off_o:off_o + d * mul_o] = y.view(R, d * mul_o)
+    return out
+
+
+def _block_backward(x, w, g, plan, need_x, need_w):
+    R = x.shape[0]
+    gx = x.new_zeros(x.shape) if need_x else None
+    gw = torch.zeros_like(w) if need_w else None
+    for off_o, mul_o, d, srcs, fan_in in plan:
+        if not srcs:
+            continue
+        s = 1.0 / math.sqrt(fan_in)
+        go = g[:, off_o:off_o + d * mul_o].reshape(R * d, mul_o)
+        if need_x:
+            ws = torch.cat([w[wo:wo + m * mul_o].view(m, mul_o) for _, m, wo in srcs], dim=0)
+            gxs = torch.mm(go, ws.t()) * s  # (R*d, K)
+            k0 = 0
+            for o, m, _ in srcs:
+                gx[:, o:o + d * m] += gxs[:, k0:k0 + m].reshape(R, d * m)
+                k0 += m
+        if need_w:
+            gws = torch.mm(_gather_rows(x, srcs, d).t(), go) * s  # (K, mul_o)
+            k0 = 0
+            for _, m, wo in srcs:
+                gw[wo:wo + m * mul_o] += gws[k0:k0 + m].reshape(-1)
+                k0 += m
+    return gx, gw
+
+
+class _BlockLinear(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x, w, plan, dim_out):
+        ctx.save_for_backward(x, w)
+        ctx.plan = plan
+        return _block_forward(x, w, plan, dim_out)
+
+    @staticmethod
+    def backward(ctx, g):
+        x, w = ctx.saved_tensors
+        gx, gw = _block_backward(x, w, g, ctx.plan, ctx.needs_input_grad[0], ctx.needs_input_grad[1])
+        return gx, gw, None, None
+
+
+class _IndexedLinear(torch.autograd.Function):
+    """Rows grouped by class, one block linear per class; gradients written per class rows."""
+
+    @staticmethod
+    def forward(ctx, x, weight, idx, lin):
+        groups = list(_class_rows(idx, lin.weight_classes))
+        if sum(len(r) for _, r in groups) != x.shape[0]:
+            raise ValueError("weight_indices must lie in [0, weight_classes)")
+        out = x.new_empty(x.shape[0], lin.irreps_out.dim)
+        for cls, rows in groups:
+            out[rows] = _block_forward(x[rows], weight[cls].reshape(-1), lin.plan, lin.irreps_out.dim)
+        ctx.save_for_backward(x, weight)
+        ctx.groups, ctx.lin = groups, lin
+        return out
+
+    @staticmethod
+    def backward(ctx, g):
+        x, weight = ctx.saved_tensors
+        need_x, need_w = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
+        gx = torch.empty_like(x) if need_x else None
+        gw = torch.zeros_like(weight) if need_w else None
+        for cls, rows in ctx.groups:
+            gxr, gwr = _block_backward(x[rows], weight[cls].reshape(-1), g[rows], ctx.lin.plan, need_x, need_w)
+            if need_x:
+                gx[rows] = gxr
+            if need_w:
+                gw[cls] = gwr.view_as(gw[cls])
+        return gx, gw, None, None
 
 
 def _class_rows(idx: torch.Tensor, num_classes: int):
     """Row indices of each class present (one host sync per call)."""
+    if idx.numel() and (int(idx.min()) < 0 or int(idx.max()) >= num_classes):
+        raise ValueError(f"weight_indices must lie in [0, {num_classes})")
     order = torch.argsort(idx, stable=True)
     counts = torch.bincount(idx, minlength=num_classes).tolist()
-    if len(counts) > num_classes:
-        raise ValueError(f"weight_indices has a value >= weight_classes ({num_classes})")
     start = 0
     for cls, c in enumerate(counts):
         if c:
