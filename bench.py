@@ -47,6 +47,8 @@ def parse():
     p.add_argument("--seed", type=int, default=0)
     p.add_argument("--workload", choices=["tp", "full"], default="tp",
                    help="tp: config 3 edge step (default, the headline line); full: config 5 energy + forces")
+    p.add_argument("--no-secondary", action="store_true",
+                   help="skip the secondary figures (config 2 neighbor list, config 5 energy + forces)")
     p.add_argument("--kernels-only", action="store_true",
                    help="profiling aid: a 1 GiB device copy (counter calibration), then 3 TP forward and "
                         "3 TP backward launches; prints their event times")
@@ -276,6 +278,34 @@ def full_step_bench(args, dev):
                        "atoms": n, "edges": int(edge_index.shape[0]), "channels": C}}
 
 
+def nlist_bench(dev, reps=5):
+    """directed cell list of 100k atoms in a periodic 100 A cube, rc 5 A.
+    Times the whole op (bin, count, scan, host read of the count, emit)."""
+    g = torch.Generator().manual_seed(2)
+    L = 100.0
+    pos = (torch.rand((100_000, 3), generator=g) * L).to(dev)
+    box = torch.eye(3, device=dev) * L
+    out = torch.ops.molix.neighbor_list(pos, 5.0, box, True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        out = torch.ops.molix.neighbor_list(pos, 5.0, box, True)
+    torch.cuda.synchronize()
+    dt = (time.perf_counter() - t0) / reps
+    E = out[0].shape[0]
+    return {"workload": "config 2: 100k atoms, periodic 100 A cube, rc 5 A, directed pairs + shifts",
+            "pairs": E, "ms": round(dt * 1e3, 3), "M_pairs_per_s": round(E / dt / 1e6, 1)}
+
+
+def secondary_figures(args, dev):
+    nl = nlist_bench(dev)
+    sub = argparse.Namespace(**{**vars(args), "steps": 3, "warmup": 2})
+    full = full_step_bench(sub, dev)
+    return {"config2_neighbor_list": nl,
+            "config5_energy_forces": {"atoms_per_s": full["value"], "ms_per_step": full["ms_per_step"],
+                                      "workload": full["config"]["workload"], "edges": full["config"]["edges"]}}
+
+
 def main():
     args = parse()
     if args.workload == "full":
@@ -325,8 +355,14 @@ def main():
         "other": {"tp_scatter_fwd_ms": round(tf, 3), "tp_scatter_fwd_GBs": round(bf / (tf * 1e-3) / 1e9, 1),
                   "tp_scatter_bwd_ms": round(tb, 3), "tp_scatter_bwd_GBs": round(bb / (tb * 1e-3) / 1e9, 1)},
     }
+    secondary = None
+    if not args.no_secondary:
+        del step
+        torch.cuda.empty_cache()
+        secondary = secondary_figures(args, dev)
     cpu = None
     if not args.no_cpu_baseline:
+        step = EdgeStep(N, edge_index, vec, args.channels, args.seed, dev)
         cpu = cpu_baseline(edge_index, step.vec, step.x, args.channels, step.mlp, step.mu, step.sigma, step.gout)
         cpu["cpu_model"] = platform.processor() or platform.machine()
     line = {
@@ -347,6 +383,7 @@ def main():
                    "spatially_sorted": not args.unsorted},
         "roofline": roof,
         "cpu_baseline": cpu,
+        "secondary": secondary,
     }
     print(json.dumps(line), flush=True)
 
