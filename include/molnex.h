@@ -215,6 +215,33 @@ int mnx_sc_scalar_bwd_f32(const float* x, const int64_t* types, const float* W, 
                           int64_t num_nodes, int32_t channels, int32_t num_elements, int32_t degree,
                           float* grad_x, float* grad_W, mnx_stream_t stream);
 
+/* ------------------------------------------------------------------------ */
+/* Equivariant symmetric contraction (the MACE product basis that the        */
+/* reference reaches through cuet.SymmetricContraction,                      */
+/* src/molrep/interaction/symmetric_contraction.py:94-109, here for irreps   */
+/* in = C x (0e+1o+..+l_in), out = C x (0e [+1o]), correlation 1..3):        */
+/*   out[n][L,M][c] = sum_{nu,k} W[types[n]][p(L,nu,k)][c]                   */
+/*                    sum_{i1..inu} U_{L,nu,k}[M][i1..inu] A[n][i1][c]..     */
+/* with the basis U of the library (symmetrised coupling chains,             */
+/* Gram-Schmidt in a fixed order).  ir_mul layouts: A [N][(l_in+1)^2][C],    */
+/* out [N][(L_out+1)^2][C]; W [S][paths][C].  Nodes with types outside       */
+/* [0, S) give zero output and zero grad_A.                                  */
+/* mnx_sc_config returns the config id (or -1); info = {dim_in, dim_out,     */
+/* paths, coefficients}.  Backward: order is a permutation of [0, N) that    */
+/* groups nodes by element (NULL = identity; only the number of atomics      */
+/* depends on it); grad_W is accumulated (zero it first); either gradient    */
+/* pointer may be NULL.                                                      */
+/* ------------------------------------------------------------------------ */
+int mnx_sc_config(int32_t l_in, int32_t l_out, int32_t correlation);
+int mnx_sc_config_info(int32_t config, int32_t* info);
+int mnx_sc_fwd_f32(int32_t config, const float* A, const int64_t* types, const float* W,
+                   int64_t num_nodes, int32_t channels, int32_t num_elements, float* out,
+                   mnx_stream_t stream);
+int mnx_sc_bwd_f32(int32_t config, const float* A, const int64_t* types, const float* W,
+                   const float* grad_out, const int32_t* order, int64_t num_nodes,
+                   int32_t channels, int32_t num_elements, float* grad_A, float* grad_W,
+                   mnx_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -54,6 +54,10 @@ SIGNATURES = {
                                      vp]),
     "mnx_sc_scalar_fwd_f32": (C.c_int, [vp, vp, vp, c_i64, c_i32, c_i32, c_i32, vp, vp]),
     "mnx_sc_scalar_bwd_f32": (C.c_int, [vp, vp, vp, vp, c_i64, c_i32, c_i32, c_i32, vp, vp, vp]),
+    "mnx_sc_config": (C.c_int, [c_i32, c_i32, c_i32]),
+    "mnx_sc_config_info": (C.c_int, [c_i32, vp]),
+    "mnx_sc_fwd_f32": (C.c_int, [c_i32, vp, vp, vp, c_i64, c_i32, c_i32, vp, vp]),
+    "mnx_sc_bwd_f32": (C.c_int, [c_i32, vp, vp, vp, vp, vp, c_i64, c_i32, c_i32, vp, vp, vp]),
 }
 
 

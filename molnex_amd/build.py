@@ -53,9 +53,10 @@ def _compile(src: str) -> str:
 
 def build(verbose: bool = True) -> str:
     sys.path.insert(0, os.path.dirname(PKG))
-    from molnex_amd.csrc import gen_tp
+    from molnex_amd.csrc import gen_sc, gen_tp
 
     gen_tp.main()
+    gen_sc.main()
     os.makedirs(BUILD, exist_ok=True)
     os.makedirs(LIBDIR, exist_ok=True)
     with cf.ThreadPoolExecutor(max_workers=min(8, len(SOURCES))) as ex:

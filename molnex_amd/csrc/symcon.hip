@@ -7,6 +7,13 @@
 // Forward: one thread per (node, channel), coalesced along channels.
 // Backward: grad_x in the same layout; grad_W reduced per (element, degree,
 // channel) in registers over a chunk of nodes, then one atomic per chunk.
+//
+// The general (equivariant) contraction -- irreps 0e+1o+..+l_in in, 0e (+1o)
+// out, correlation <= 3 -- runs the generated kernels of sc_gen.inc: one thread
+// per (node, channel) in the forward; the backward walks a chunk of nodes in a
+// caller-given order (nodes grouped by element) per channel, keeping the weight
+// gradient of the current element in registers and flushing it with one atomic
+// per path when the element changes.
 
 #include "common.h"
 
@@ -82,6 +89,10 @@ __global__ void k_sc_bwd(const float* __restrict__ x, const int64_t* __restrict_
     }
 }
 
+#include "sc_gen.inc"
+
+constexpr int kSCChunk = 16;
+
 }  // namespace
 }  // namespace mnx
 
@@ -114,6 +125,59 @@ int mnx_sc_scalar_bwd_f32(const float* x, const int64_t* types, const float* W, 
     const int64_t chunk = 256;
     hipLaunchKernelGGL(k_sc_bwd, dim3(unsigned(ceil_div(N, chunk)), unsigned(ceil_div(D, tb))), dim3(tb), 0,
                        (hipStream_t)stream, x, types, W, grad_out, N, D, S, nu, chunk, grad_x, grad_W);
+    MNX_CHECK_LAUNCH();
+    return MNX_OK;
+}
+
+int mnx_sc_config(int32_t l_in, int32_t l_out, int32_t correlation) {
+    clear_error();
+    for (int i = 0; i < kNumSCConfigs; ++i) {
+        const SCConfig& c = kSCConfigs[i];
+        if (c.l_in == l_in && c.l_out == l_out && c.nu == correlation) return i;
+    }
+    set_error(MNX_ERR_UNSUPPORTED, "no symmetric-contraction kernel for l_in %d, L_out %d, correlation %d (l_in 1..3, L_out 0..1, "
+              "correlation 1..3)", l_in, l_out, correlation);
+    return -1;
+}
+
+int mnx_sc_config_info(int32_t config, int32_t* info) {
+    clear_error();
+    MNX_REQUIRE(config >= 0 && config < kNumSCConfigs && info, "bad symmetric-contraction config %d", config);
+    const SCConfig& c = kSCConfigs[config];
+    info[0] = c.ni;
+    info[1] = c.no;
+    info[2] = c.paths;
+    info[3] = c.nnz;
+    return MNX_OK;
+}
+
+int mnx_sc_fwd_f32(int32_t config, const float* A, const int64_t* types, const float* W, int64_t N, int32_t C,
+                   int32_t S, float* out, mnx_stream_t stream) {
+    clear_error();
+    MNX_REQUIRE(config >= 0 && config < kNumSCConfigs, "bad symmetric-contraction config %d", config);
+    MNX_REQUIRE(N >= 0 && C > 0 && S > 0 && N * int64_t(C) < (int64_t(1) << 40), "bad sizes");
+    if (N == 0) return MNX_OK;
+    MNX_REQUIRE(A && types && W && out, "null pointer argument");
+    const int64_t threads = N * C;
+    hipLaunchKernelGGL(kSCFwd[config], dim3(unsigned(ceil_div(threads, int64_t(256)))), dim3(256), 0,
+                       (hipStream_t)stream, A, types, W, N, int(C), int(S), out);
+    MNX_CHECK_LAUNCH();
+    return MNX_OK;
+}
+
+int mnx_sc_bwd_f32(int32_t config, const float* A, const int64_t* types, const float* W, const float* grad_out,
+                   const int32_t* order, int64_t N, int32_t C, int32_t S, float* grad_A, float* grad_W,
+                   mnx_stream_t stream) {
+    clear_error();
+    MNX_REQUIRE(config >= 0 && config < kNumSCConfigs, "bad symmetric-contraction config %d", config);
+    MNX_REQUIRE(N >= 0 && N < (int64_t(1) << 31) && C > 0 && S > 0 && N * int64_t(C) < (int64_t(1) << 40),
+                "bad sizes");
+    if (N == 0 || (!grad_A && !grad_W)) return MNX_OK;
+    MNX_REQUIRE(A && types && W && grad_out, "null pointer argument");
+    const SCBwdFn fn = grad_A && grad_W ? kSCBwdAW[config] : grad_A ? kSCBwdA[config] : kSCBwdW[config];
+    const int64_t threads = ceil_div(N, int64_t(kSCChunk)) * C;
+    hipLaunchKernelGGL(fn, dim3(unsigned(ceil_div(threads, int64_t(256)))), dim3(256), 0, (hipStream_t)stream, A,
+                       types, W, grad_out, order, N, int(C), int(S), kSCChunk, grad_A, grad_W);
     MNX_CHECK_LAUNCH();
     return MNX_OK;
 }

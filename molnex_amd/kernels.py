@@ -600,3 +600,96 @@ def _sc_bwd(ctx, grad):
 
 
 symmetric_contraction_scalar.register_autograd(_sc_bwd, setup_context=_sc_setup)
+
+
+# ---------------------------------------------------------------------------
+# Equivariant symmetric contraction (MACE product basis; the reference reaches it
+# through cuet.SymmetricContraction, symmetric_contraction.py:94-109)
+# ---------------------------------------------------------------------------
+
+
+def sc_config_id(l_in: int, l_out: int, correlation: int) -> int:
+    cfg = int(_lib.load().mnx_sc_config(l_in, l_out, correlation))
+    if cfg < 0:
+        raise ValueError(_lib.load().mnx_last_error().decode())
+    return cfg
+
+
+def sc_config_info(config: int) -> tuple[int, int, int, int]:
+    """(dim_in, dim_out, paths, coefficients) per channel."""
+    info = (C.c_int32 * 4)()
+    check(_lib.load().mnx_sc_config_info(config, info), "sc_config_info")
+    return tuple(info)
+
+
+def _sc_shapes(x, weight, l_in, l_out, correlation):
+    cfg = sc_config_id(l_in, l_out, correlation)
+    ni, no, paths, _ = sc_config_info(cfg)
+    if weight.dim() != 3 or weight.shape[1] != paths:
+        raise ValueError(f"weight must be (num_elements, {paths}, channels), got {tuple(weight.shape)}")
+    S, _, Cc = weight.shape
+    if x.shape[-1] != ni * Cc:
+        raise ValueError(f"x last dim {x.shape[-1]} != {ni} x {Cc}")
+    return cfg, ni, no, S, Cc
+
+
+@torch.library.custom_op("molix::symmetric_contraction", mutates_args=(), device_types="cuda")
+def symmetric_contraction(x: Tensor, atom_types: Tensor, weight: Tensor, l_in: int, l_out: int,
+                          correlation: int) -> Tensor:
+    """B = sum_{nu<=correlation} U_nu . W[z] (x^{(x)nu}); x (N, (l_in+1)^2 C) ir_mul, weight
+    (S, paths, C) -> (N, (l_out+1)^2 C)."""
+    _require_gpu("symmetric_contraction", x, atom_types, weight)
+    cfg, ni, no, S, Cc = _sc_shapes(x, weight, l_in, l_out, correlation)
+    xs = _f32_rows(x, ni * Cc, "x")
+    z = atom_types.to(torch.int64).reshape(-1).contiguous()
+    w = weight.contiguous()
+    out = torch.empty((xs.shape[0], no * Cc), dtype=torch.float32, device=xs.device)
+    check(_lib.load().mnx_sc_fwd_f32(cfg, ptr(xs), ptr(z), ptr(w), xs.shape[0], Cc, S, ptr(out), _stream(xs)),
+          "symmetric_contraction")
+    return out.reshape(*x.shape[:-1], no * Cc)
+
+
+@symmetric_contraction.register_fake
+def _(x, atom_types, weight, l_in, l_out, correlation):
+    return x.new_empty(*x.shape[:-1], (l_out + 1) ** 2 * weight.shape[-1])
+
+
+@torch.library.custom_op("molix::symmetric_contraction_backward", mutates_args=(), device_types="cuda")
+def symmetric_contraction_backward(grad: Tensor, x: Tensor, atom_types: Tensor, weight: Tensor, l_in: int,
+                                   l_out: int, correlation: int, need_x: bool,
+                                   need_w: bool) -> tuple[Tensor, Tensor]:
+    cfg, ni, no, S, Cc = _sc_shapes(x, weight, l_in, l_out, correlation)
+    xs = _f32_rows(x, ni * Cc, "x")
+    g = _f32_rows(grad, no * Cc, "grad")
+    z = atom_types.to(torch.int64).reshape(-1).contiguous()
+    w = weight.contiguous()
+    # nodes grouped by element: one weight-gradient flush per element run
+    order = torch.argsort(z, stable=True).to(torch.int32) if need_w else None
+    gx = torch.empty_like(xs) if need_x else xs.new_empty(0)
+    gw = torch.zeros_like(w) if need_w else w.new_empty(0)
+    check(_lib.load().mnx_sc_bwd_f32(cfg, ptr(xs), ptr(z), ptr(w), ptr(g), ptr(order), xs.shape[0], Cc, S,
+                                     ptr(gx) if need_x else None, ptr(gw) if need_w else None, _stream(xs)),
+          "symmetric_contraction backward")
+    return (gx.reshape(x.shape) if need_x else gx), gw
+
+
+@symmetric_contraction_backward.register_fake
+def _(grad, x, atom_types, weight, l_in, l_out, correlation, need_x, need_w):
+    return (torch.empty_like(x) if need_x else x.new_empty(0),
+            torch.empty_like(weight) if need_w else weight.new_empty(0))
+
+
+def _scg_setup(ctx, inputs, output):
+    x, z, w, l_in, l_out, nu = inputs
+    ctx.save_for_backward(x, z, w)
+    ctx.cfg = (l_in, l_out, nu)
+
+
+def _scg_bwd(ctx, grad):
+    x, z, w = ctx.saved_tensors
+    nx, _, nw = ctx.needs_input_grad[:3]
+    gx, gw = symmetric_contraction_backward(grad.contiguous(), x, z, w, *ctx.cfg, nx, nw)
+    return (gx if nx else None), None, (gw if nw else None), None, None, None
+
+
+symmetric_contraction.register_autograd(_scg_bwd, setup_context=_scg_setup)

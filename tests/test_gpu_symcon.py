@@ -1,0 +1,136 @@
+"""GPU equivariant symmetric contraction vs the fp64 oracle, forward and backward.
+
+Every generated configuration (l_in 1..3, L_out 0..1, correlation 1..3) at
+small sizes, plus the config-4 shape (128 channels, 10 elements) on a node
+subset.  Tolerance (fp32 kernels vs fp64 oracle): norm-wise relative error
+<= 1e-5 and max-abs error <= 1e-4 * RMS(reference).  Gradients: the oracle's
+torch fp64 autograd.  Nodes with an element index outside [0, S) must give
+zero output and zero grad_A, and contribute nothing to grad_W.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from molnex_amd import kernels  # noqa: F401  (registers the molix ops)
+from oracle import symcon as O
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+CONFIGS = [(li, lo, nu) for li in (1, 2, 3) for lo in (0, 1) for nu in (1, 2, 3)]
+
+
+def assert_close(got, ref, what, rtol=1e-5):
+    got = np.asarray(got, np.float64)
+    ref = np.asarray(ref, np.float64)
+    nref = np.linalg.norm(ref)
+    if nref == 0:
+        assert np.abs(got).max(initial=0) == 0, what
+        return
+    err = np.linalg.norm(got - ref) / nref
+    rms = nref / np.sqrt(ref.size)
+    mx = np.abs(got - ref).max()
+    assert err <= rtol and mx <= rtol * rms * 10, f"{what}: rel {err:.2e}, max-abs {mx:.2e} (rms {rms:.2e})"
+
+
+def run_case(l_in, l_out, nu, N, C, S, seed, need=(True, True), invalid=True):
+    rng = np.random.default_rng(seed)
+    P = O.num_paths(l_in, l_out, nu)
+    A = rng.normal(size=(N, (l_in + 1) ** 2 * C)).astype(np.float32)
+    z = rng.integers(0, S, N)
+    if invalid and N > 4:
+        z[1], z[N // 2] = -1, S
+    W = (rng.normal(size=(S, P, C)) * 0.5).astype(np.float32)
+    g = rng.normal(size=(N, (l_out + 1) ** 2 * C)).astype(np.float32)
+
+    At = torch.from_numpy(A).double().requires_grad_(True)
+    Wt = torch.from_numpy(W).double().requires_grad_(True)
+    ref = O.contract(At, torch.from_numpy(z), Wt, l_in, l_out, nu)
+    ref_gA, ref_gW = torch.autograd.grad(ref, (At, Wt), torch.from_numpy(g).double())
+
+    Ad = torch.from_numpy(A).to(DEV).requires_grad_(need[0])
+    Wd = torch.from_numpy(W).to(DEV).requires_grad_(need[1])
+    zd = torch.from_numpy(z).to(DEV)
+    out = torch.ops.molix.symmetric_contraction(Ad, zd, Wd, l_in, l_out, nu)
+    torch.cuda.synchronize()
+    tag = f"l_in {l_in} L_out {l_out} nu {nu} N {N} C {C}"
+    assert_close(out.detach().cpu(), ref.detach(), f"out {tag}")
+    if invalid and N > 4:
+        assert out[1].abs().max().item() == 0 and out[N // 2].abs().max().item() == 0
+    if any(need):
+        grads = torch.autograd.grad(out, [t for t, n in zip((Ad, Wd), need) if n], torch.from_numpy(g).to(DEV))
+        torch.cuda.synchronize()
+        it = iter(grads)
+        if need[0]:
+            gA = next(it).cpu()
+            assert_close(gA, ref_gA, f"grad_A {tag}")
+            if invalid and N > 4:
+                assert gA[1].abs().max().item() == 0
+        if need[1]:
+            assert_close(next(it).cpu(), ref_gW, f"grad_W {tag}")
+
+
+@pytest.mark.parametrize("l_in,l_out,nu", CONFIGS)
+def test_sc_all_configs(l_in, l_out, nu):
+    run_case(l_in, l_out, nu, N=97, C=32, S=3, seed=l_in * 100 + l_out * 10 + nu)
+
+
+@pytest.mark.parametrize("need", [(True, False), (False, True)])
+def test_sc_single_gradient(need):
+    run_case(3, 1, 3, N=120, C=64, S=4, seed=7, need=need)
+
+
+def test_sc_odd_channels_and_tiny():
+    run_case(3, 1, 3, N=37, C=48, S=5, seed=11)
+    run_case(2, 1, 2, N=3, C=8, S=2, seed=12, invalid=False)
+
+
+def test_sc_config4_shape_subset():
+    # config 4's shape (128 channels, 10 elements, l <= 3 -> 0e + 1o, correlation 3) on 400 nodes
+    run_case(3, 1, 3, N=400, C=128, S=10, seed=4)
+
+
+def test_sc_empty_and_module():
+    from molnex_amd.molrep.interaction import EquivariantSymmetricContraction
+
+    m = EquivariantSymmetricContraction("16x0e+16x1o+16x2e+16x3o", "16x0e+16x1o", 3, 4).to(DEV)
+    x = torch.zeros(0, 16 * 16, device=DEV)
+    out = m(x, torch.zeros(0, dtype=torch.int64, device=DEV))
+    assert out.shape == (0, 64)
+    x = torch.randn(10, 256, device=DEV)
+    z = torch.randint(0, 4, (10,), device=DEV)
+    out = m(x, z)
+    ref = O.contract(x.cpu().double(), z.cpu(), m.weight.detach().cpu().double(), 3, 1, 3)
+    assert_close(out.detach().cpu(), ref, "module")
+
+
+def test_sc_element_runs_in_any_order():
+    """grad_W is the same whether or not the nodes arrive grouped by element (the op
+    groups them; the C ABI also accepts NULL order)."""
+    import ctypes
+
+    from molnex_amd import _lib
+    from molnex_amd import kernels as K
+
+    rng = np.random.default_rng(9)
+    N, C, S = 200, 32, 3
+    cfg = K.sc_config_id(3, 1, 3)
+    P = K.sc_config_info(cfg)[2]
+    A = torch.from_numpy(rng.normal(size=(N, 16 * C)).astype(np.float32)).to(DEV)
+    z = torch.from_numpy(rng.integers(0, S, N)).to(DEV)
+    W = torch.from_numpy(rng.normal(size=(S, P, C)).astype(np.float32)).to(DEV)
+    g = torch.from_numpy(rng.normal(size=(N, 4 * C)).astype(np.float32)).to(DEV)
+    lib = _lib.load()
+    res = []
+    for order in (None, torch.argsort(z, stable=True).to(torch.int32)):
+        gA = torch.empty_like(A)
+        gW = torch.zeros_like(W)
+        _lib.check(lib.mnx_sc_bwd_f32(cfg, A.data_ptr(), z.data_ptr(), W.data_ptr(), g.data_ptr(),
+                                      None if order is None else order.data_ptr(), N, C, S, gA.data_ptr(),
+                                      gW.data_ptr(), ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)),
+                   "sc bwd")
+        torch.cuda.synchronize()
+        res.append((gA.cpu(), gW.cpu()))
+    assert torch.equal(res[0][0], res[1][0])
+    assert_close(res[0][1], res[1][1].double(), "grad_W order")
