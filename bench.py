@@ -45,10 +45,12 @@ def parse():
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--unsorted", action="store_true", help="keep atoms in random order (no spatial sort)")
     p.add_argument("--seed", type=int, default=0)
-    p.add_argument("--workload", choices=["tp", "full"], default="tp",
+    p.add_argument("--workload", choices=["tp", "full", "sc"], default="tp",
                    help="tp: config 3 edge step (default, the headline line); full: config 5 energy + forces")
     p.add_argument("--no-secondary", action="store_true",
                    help="skip the secondary figures (config 2 neighbor list, config 5 energy + forces)")
+    p.add_argument("--literal", action="store_true",
+                   help="with --workload full: the literal MACE (hidden 128x0e+128x1o, polynomial cutoff)")
     p.add_argument("--kernels-only", action="store_true",
                    help="profiling aid: a 1 GiB device copy (counter calibration), then 3 TP forward and "
                         "3 TP backward launches; prints their event times")
@@ -240,9 +242,11 @@ def full_step_bench(args, dev):
     edge_index = torch.stack([j.long(), i.long()], 1)
     torch.manual_seed(args.seed)
     C = args.channels
+    literal = getattr(args, "literal", False)
     enc = MACE(node_attr_specs=[DiscreteEmbeddingSpec(input_key="Z", num_classes=10, emb_dim=C)], num_elements=10,
                num_features=C, r_max=5.0, num_bessel=8, l_max=3, num_interactions=2, correlation=3,
-               avg_num_neighbors=float(edge_index.shape[0]) / n)
+               avg_num_neighbors=float(edge_index.shape[0]) / n, cutoff="polynomial" if literal else "cosine",
+               hidden_irreps=f"{C}x0e+{C}x1o" if literal else None)
     model = EnergyForceModel(enc, C).to(dev)
     charge_head = ChargeHead(C, hidden_dim=64).to(dev)
     pme = PMEPotential(alpha=0.3, grid=(128, 128, 128), order=6, cutoff=5.0).to(dev)
@@ -274,7 +278,9 @@ def full_step_bench(args, dev):
             "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(dt * 1e3, 3),
             "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "fp32",
             "data": "synthetic (jittered lattice, random-init weights)",
-            "config": {"workload": "config 5: MACE as coded 128 ch l<=3 x2 layers + PME 128^3 order 6, 50k atoms",
+            "config": {"workload": ("config 5: MACE literal (hidden 128x0e+128x1o, polynomial cutoff, equivariant "
+                                    "product basis)" if literal else "config 5: MACE as coded 128 ch l<=3") +
+                                   " x2 layers + PME 128^3 order 6, 50k atoms",
                        "atoms": n, "edges": int(edge_index.shape[0]), "channels": C}}
 
 
@@ -297,25 +303,114 @@ def nlist_bench(dev, reps=5):
             "pairs": E, "ms": round(dt * 1e3, 3), "M_pairs_per_s": round(E / dt / 1e6, 1)}
 
 
+def sc_flops(l_in=3, l_out=1, nu=3):
+    """FLOPs per (node, channel) of the generated symmetric-contraction code, each distinct
+    pair product A_i A_j counted once (the compiler shares them between monomials and
+    product-rule terms): forward = monomials + one FMA per basis coefficient + the weight
+    mix; backward (both gradients) = monomials + per (monomial, path) h = coef . g, the
+    grad_W and grad-monomial FMAs + the product-rule FMAs."""
+    from molnex_amd.csrc.gen_sc import Cfg, config_list
+
+    c = Cfg(config_list().index((l_in, l_out, nu)), l_in, l_out, nu)
+    pairs = {m[:2] for m, _ in c.terms if len(m) >= 2} | {m[1:] for m, _ in c.terms if len(m) == 3} | \
+        {(m[0], m[2]) for m, _ in c.terms if len(m) == 3}
+    monos = len(pairs) + sum(1 for m, _ in c.terms if len(m) == 3)
+    accs = {(p, M) for _, ts in c.terms for p, M, _ in ts}
+    fwd = monos + 2 * c.nnz + 2 * len(accs)
+    bwd = monos
+    for mono, ts in c.terms:
+        per_path = {}
+        for p, _, _ in ts:
+            per_path[p] = per_path.get(p, 0) + 1
+        bwd += sum(2 * t - 1 + 4 for t in per_path.values())
+        for x in set(mono):
+            bwd += 1 if len(mono) == 1 else 2 + (1 if mono.count(x) > 1 else 0)
+    return fwd, bwd
+
+
+def sc_bench(dev, reps=10):
+    """equivariant symmetric contraction of 50k nodes, 128 x (0e+1o+2e+3o)
+    -> 128 x (0e+1o), correlation 3, 10 elements, then the 128 -> 128 channel mixing per (l, m);
+    forward and backward (grad wrt A and both weights).  Kernel times by HIP events."""
+    from molnex_amd import kernels as K
+    from molnex_amd.molrep.interaction import EquivariantSymmetricContraction, Linear
+
+    g = torch.Generator().manual_seed(4)
+    N, C, S = 50_000, 128, 10
+    A = torch.randn((N, 16 * C), generator=g).to(dev).requires_grad_(True)
+    z = torch.randint(0, S, (N,), generator=g).to(dev)
+    torch.manual_seed(4)
+    sc = EquivariantSymmetricContraction(f"{C}x0e+{C}x1o+{C}x2e+{C}x3o", f"{C}x0e+{C}x1o", 3, S).to(dev)
+    with torch.no_grad():
+        sc.weight.mul_(0.1)
+    mix = Linear(f"{C}x0e+{C}x1o", f"{C}x0e+{C}x1o").to(dev)
+    gout = torch.randn((N, 4 * C), generator=g).to(dev)
+
+    def step():
+        out = mix(sc(A, z))
+        out.backward(gout)
+
+    for _ in range(3):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        step()
+    torch.cuda.synchronize()
+    dt = (time.perf_counter() - t0) / reps
+    # the two contraction kernels alone
+    with torch.no_grad():
+        B = sc(A, z)
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
+    tf = tb = 0.0
+    for _ in range(reps):
+        ev[0].record()
+        torch.ops.molix.symmetric_contraction(A.detach(), z, sc.weight.detach(), 3, 1, 3)
+        ev[1].record()
+        K.symmetric_contraction_backward(gout, A.detach(), z, sc.weight.detach(), 3, 1, 3, True, True)
+        ev[3].record()
+        torch.cuda.synchronize()
+        tf += ev[0].elapsed_time(ev[1])
+        tb += ev[1].elapsed_time(ev[3])
+    tf, tb = tf / reps, tb / reps  # ms (the backward figure includes the element argsort)
+    ff, fb = sc_flops()
+    fwd_bytes = 4 * N * (16 * C + 4 * C) + 8 * N
+    return {"workload": "config 4: symmetric contraction 50k nodes, 128 x (0e+1o+2e+3o) -> 128 x (0e+1o), "
+                        "correlation 3, 10 elements, + 128->128 mixing; fwd + bwd",
+            "ms_per_step": round(dt * 1e3, 3), "nodes_per_s": round(N / dt, 1), "B_finite": bool(torch.isfinite(B).all()),
+            "sc_fwd_ms": round(tf, 4), "sc_bwd_ms": round(tb, 4),
+            "sc_fwd_TFLOPs": round(ff * N * C / (tf * 1e-3) / 1e12, 2),
+            "sc_bwd_TFLOPs": round(fb * N * C / (tb * 1e-3) / 1e12, 2),
+            "sc_fwd_GBs": round(fwd_bytes / (tf * 1e-3) / 1e9, 1),
+            "flops_per_node_channel": {"fwd": ff, "bwd": fb}}
+
+
 def secondary_figures(args, dev):
+    sc = sc_bench(dev)
     nl = nlist_bench(dev)
-    sub = argparse.Namespace(**{**vars(args), "steps": 3, "warmup": 2})
-    full = full_step_bench(sub, dev)
-    return {"config2_neighbor_list": nl,
-            "config5_energy_forces": {"atoms_per_s": full["value"], "ms_per_step": full["ms_per_step"],
-                                      "workload": full["config"]["workload"], "edges": full["config"]["edges"]}}
+    out = {"config2_neighbor_list": nl, "config4_symmetric_contraction": sc}
+    for key, lit in (("config5_energy_forces", False), ("config5_literal_energy_forces", True)):
+        sub = argparse.Namespace(**{**vars(args), "steps": 3, "warmup": 2, "literal": lit})
+        full = full_step_bench(sub, dev)
+        out[key] = {"atoms_per_s": full["value"], "ms_per_step": full["ms_per_step"],
+                    "workload": full["config"]["workload"], "edges": full["config"]["edges"]}
+        torch.cuda.empty_cache()
+    return out
 
 
 def main():
     args = parse()
-    if args.workload == "full":
-        dev = torch.device("cuda:0")
-        print(json.dumps(full_step_bench(args, dev)), flush=True)
-        return
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU; --gpus > 1 is not supported (see DESIGN.md, "
                                    "'More than one GPU')"}))
         sys.exit(2)
+    if args.workload == "full":
+        dev = torch.device("cuda:0")
+        print(json.dumps(full_step_bench(args, dev)), flush=True)
+        return
+    if args.workload == "sc":
+        print(json.dumps(sc_bench(torch.device("cuda:0"))), flush=True)
+        return
     if not torch.cuda.is_available():
         print(json.dumps({"error": "no GPU visible"}))
         sys.exit(1)

@@ -1,4 +1,4 @@
 from .basis_projection import BasisProjection
-from .product_head import ProductHead
+from .product_head import EquivariantProductHead, ProductHead
 
-__all__ = ["ProductHead", "BasisProjection"]
+__all__ = ["ProductHead", "EquivariantProductHead", "BasisProjection"]

@@ -1,5 +1,9 @@
 """Product head (src/molrep/readout/product_head.py:45-142): symmetric contraction ->
-identity projection -> nn.Linear(hidden_dim, out_dim)."""
+identity projection -> nn.Linear(hidden_dim, out_dim).
+
+``EquivariantProductHead`` is the literal MACE product block: the equivariant
+symmetric contraction (irreps_in -> irreps_out, per element, correlation <= 3)
+followed by an equivariant linear on irreps_out."""
 
 from __future__ import annotations
 
@@ -8,7 +12,8 @@ import torch.nn as nn
 from pydantic import BaseModel, Field
 
 from ...config import config
-from ..interaction.symmetric_contraction import SymmetricContraction
+from ..interaction.linear import Linear
+from ..interaction.symmetric_contraction import EquivariantSymmetricContraction, SymmetricContraction
 from .basis_projection import BasisProjection
 
 
@@ -36,3 +41,14 @@ class ProductHead(nn.Module):
     def forward(self, node_features: torch.Tensor, atom_types: torch.Tensor) -> torch.Tensor:
         basis = self.symmetric_contraction(node_features, atom_types)
         return self.linear(self.basis_projection(basis))
+
+
+class EquivariantProductHead(nn.Module):
+    def __init__(self, *, irreps_in: str, irreps_out: str, max_body_order: int, num_species: int):
+        super().__init__()
+        self.symmetric_contraction = EquivariantSymmetricContraction(irreps_in, irreps_out, max_body_order,
+                                                                     num_species, dtype=config.ftype)
+        self.linear = Linear(irreps_out, irreps_out, dtype=config.ftype)
+
+    def forward(self, node_features: torch.Tensor, atom_types: torch.Tensor) -> torch.Tensor:
+        return self.linear(self.symmetric_contraction(node_features, atom_types))

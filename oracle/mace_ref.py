@@ -52,11 +52,16 @@ def _irr(l_max, mul):
     return [(mul, l, (-1) ** l) for l in range(l_max + 1)]
 
 
-def conv_tp(x, Y, w, edge_index, num_nodes, l_max, C):
-    """Channelwise TP + scatter in fp64 (einsum per path; paths / layout per oracle.equivariant)."""
-    irr = "+".join(f"{C}x{l}{'e' if l % 2 == 0 else 'o'}" for l in range(l_max + 1))
-    sh = "+".join(f"{l}{'e' if l % 2 == 0 else 'o'}" for l in range(l_max + 1))
-    tp = EQ.ChannelwiseTP(irr, sh, irr, C)
+def _irr_str(ls, C=None):
+    return "+".join(f"{C}x{l}{'e' if l % 2 == 0 else 'o'}" if C else f"{l}{'e' if l % 2 == 0 else 'o'}"
+                    for l in ls)
+
+
+def conv_tp(x, Y, w, edge_index, num_nodes, l_max, C, in_ls=None):
+    """Channelwise TP + scatter in fp64 (einsum per path; paths / layout per oracle.equivariant);
+    input irreps ``C x in_ls`` (default l <= l_max), harmonics and output filter l <= l_max."""
+    ls = list(range(l_max + 1))
+    tp = EQ.ChannelwiseTP(_irr_str(in_ls if in_ls is not None else ls, C), _irr_str(ls), _irr_str(ls, C), C)
     E = Y.shape[0]
     xs = x.reshape(-1, tp.nx, C)
     w3 = w.reshape(E, len(tp.paths), C)
@@ -93,8 +98,90 @@ def linear(x, weight, blocks_in, blocks_out):
     return torch.cat(outs, dim=1)
 
 
+def _edge_embedding(cfg, pos, edge_index, l_max):
+    rc, nb_ = cfg["r_max"], cfg["num_bessel"]
+    bond_diff = pos[edge_index[:, 1]] - pos[edge_index[:, 0]]
+    bond_dist = bond_diff.norm(dim=-1).clamp(min=1e-6)
+    edge_dir = bond_diff / (bond_dist.unsqueeze(-1) + 1e-8)
+    Y = sh_torch(l_max, edge_dir)
+    freqs = torch.arange(1, nb_ + 1, dtype=torch.float64) * (math.pi / rc)
+    pref = math.sqrt(2.0 / rc)
+    rs = torch.linspace(1e-8, rc, 4096, dtype=torch.float32)
+    raw = (pref * torch.sin(rs[:, None] * freqs.float()) / (rs[:, None] + 1e-8))
+    mu, sig = raw.mean(0).double(), raw.std(0).clamp(min=1e-8).double()
+    phi = (pref * torch.sin(bond_dist[:, None] * freqs) / (bond_dist[:, None] + 1e-8) - mu) / sig
+    if cfg.get("cutoff", "cosine") == "polynomial":  # cutoff.py:138-161, p = 6
+        x = bond_dist / rc
+        fcut = torch.where(x < 1.0, 1.0 - 28.0 * x ** 6 + 48.0 * x ** 7 - 21.0 * x ** 8, torch.zeros_like(x))
+    else:  # cutoff.py:56-75
+        fcut = torch.where(bond_dist < rc, 0.5 * (torch.cos(math.pi * bond_dist / rc) + 1.0),
+                           torch.zeros_like(bond_dist))
+    return Y, phi * fcut[:, None]
+
+
+def _radial(t, p, edge_feats):
+    a = edge_feats
+    for j in (0, 2):
+        a = torch.nn.functional.silu(a @ t[p + f"radial_mlp.mlp.{j}.weight"].T + t[p + f"radial_mlp.mlp.{j}.bias"])
+    return a @ t[p + "radial_mlp.mlp.4.weight"].T + t[p + "radial_mlp.mlp.4.bias"]
+
+
+def _readout(t, per_layer, batch, num_graphs):
+    feats = torch.stack(per_layer, dim=1).mean(1)
+    e_atom = torch.nn.functional.silu(feats @ t["energy.mlp.0.weight"].T + t["energy.mlp.0.bias"])
+    e_atom = (e_atom @ t["energy.mlp.2.weight"].T + t["energy.mlp.2.bias"]).squeeze(-1)
+    return torch.zeros(num_graphs, dtype=torch.float64).index_add(0, batch, e_atom)
+
+
+def mace_energy_literal(sd: dict, cfg: dict, Z, pos, edge_index, batch, num_graphs):
+    """Per-graph energies (fp64) of the literal MACE configuration (hidden irreps
+    ``F x hidden_ls``, equivariant product basis and linears throughout)."""
+    from . import symcon as SC
+
+    t = {k: v.detach().to("cpu", torch.float64) for k, v in sd.items()}
+    F, L, l_max, nu = cfg["num_features"], cfg["num_interactions"], cfg["l_max"], cfg["correlation"]
+    hid = list(cfg["hidden_ls"])
+    blk = lambda ls: [(F, l, (-1) ** l) for l in ls]  # noqa: E731
+    Y, edge_feats = _edge_embedding(cfg, pos, edge_index, l_max)
+    emb = t["embedding.node_embedding.embedders.0.weight"][Z]
+    node = linear(emb, t["embedding.node_embedding.project.0.weight"], [(emb.shape[1], 0, 1)], [(F, 0, 1)])
+    h = linear(node, t["initial_projection.weight"], blk([0]), blk([0]))
+    target = list(range(l_max + 1))
+    per_layer = []
+    for i in range(L):
+        p = f"interactions.{i}."
+        in_ls = [0] if i == 0 else hid
+        out_ls = hid if i < L - 1 else [0]
+        sc = h
+        up = linear(h, t[p + "node_linear.weight"], blk(in_ls), blk(in_ls))
+        w = _radial(t, p, edge_feats)
+        msg, tp = conv_tp(up, Y, w, edge_index, pos.shape[0], l_max, F, in_ls=in_ls)
+        msg = msg / cfg["avg_num_neighbors"]
+        order = sorted(tp.out_pos, key=tp.out_pos.get)
+        m = linear(msg, t[p + "linear.weight"], [(F, tp.paths[k][4], tp.paths[k][5]) for k in order], blk(target))
+        B = SC.contract(m, Z, t[f"products.{i}.symmetric_contraction.weight"], l_max, max(out_ls), nu)
+        hp = linear(B, t[f"products.{i}.linear.weight"], blk(out_ls), blk(out_ls))
+        per_layer.append(hp[:, :F])
+        proj = linear(hp, t[f"projections.{i}.weight"], blk(out_ls), blk(out_ls))
+        if i < L - 1:
+            sc = torch.nn.functional.pad(sc, (0, proj.shape[1] - sc.shape[1]))
+            Wu = t[f"element_updates.{i}.weight"]
+            upd = torch.zeros_like(proj)
+            for s_ in range(Wu.shape[0]):
+                sel = Z == s_
+                if sel.any():
+                    upd[sel] = linear(proj[sel], Wu[s_], blk(out_ls), blk(out_ls))
+            h = sc + upd
+        else:
+            h = proj
+    return _readout(t, per_layer, batch, num_graphs)
+
+
 def mace_energy(sd: dict, cfg: dict, Z, pos, edge_index, batch, num_graphs):
-    """Per-graph energies (fp64) of the MACE-as-coded pipeline with the parameters ``sd``."""
+    """Per-graph energies (fp64) of the MACE-as-coded pipeline with the parameters ``sd``
+    (the literal configuration when ``cfg`` names ``hidden_ls``)."""
+    if cfg.get("hidden_ls") is not None:
+        return mace_energy_literal(sd, cfg, Z, pos, edge_index, batch, num_graphs)
     t = {k: v.detach().to("cpu", torch.float64) for k, v in sd.items()}
     F, L, l_max = cfg["num_features"], cfg["num_interactions"], cfg["l_max"]
     rc, nb_, nu = cfg["r_max"], cfg["num_bessel"], cfg["correlation"]

@@ -17,7 +17,8 @@ contraction densely:
 * basis: Gram-Schmidt over the candidates in that order (residual below 1e-6
   dropped), each vector keeping its candidate's orientation;
 * contraction: B[n, L, M, c] = sum_{nu,k} W[z_n, p, c] U_{L,nu,k}[M, i..] A[n, i, c]...
-  as a dense torch fp64 einsum (autograd gives the reference gradients).
+  in torch fp64, per (node, channel) row as the dense products A^{(x) nu} times the
+  flattened U (autograd gives the reference gradients).
 
 Pinned by (tests/test_oracle_symcon.py): the number of basis vectors equals the
 multiplicity of V_L in Sym^nu(V) from O(3) characters; orthonormality; slot
@@ -120,34 +121,40 @@ def num_paths(l_in, l_out, nu_max):
     return sum(len(U) for _, _, U in paths(l_in, l_out, nu_max))
 
 
-def contract(A, types, W, l_in, l_out, nu_max, parity_rule=True):
+def contract(A, types, W, l_in, l_out, nu_max, parity_rule=True, chunk=128):
     """A (N, (l_in+1)^2 * C) ir_mul, types (N,), W (S, paths, C) -> (N, (l_out+1)^2 * C) fp64 torch.
-    Nodes with types outside [0, S) give zeros."""
+    Nodes with types outside [0, S) give zeros.  Evaluated per row (node, channel) as the
+    dense products A^{(x) nu} (flattened) times the flattened basis, in node chunks."""
     N = A.shape[0]
     ni = (l_in + 1) ** 2
     C = A.shape[1] // ni
-    a = A.reshape(N, ni, C).to(torch.float64)
     S = W.shape[0]
     valid = (types >= 0) & (types < S)
     z = torch.where(valid, types, torch.zeros_like(types))
-    w = W.to(torch.float64)[z] * valid[:, None, None].to(torch.float64)  # (N, P, C)
-    outs = [None] * (l_out + 1)
-    p = 0
-    for L, nu, U in paths(l_in, l_out, nu_max, parity_rule):
-        Ut = torch.from_numpy(np.ascontiguousarray(U))
-        if nu == 1:
-            t = torch.einsum("kMi,nic->nkMc", Ut, a)
-        elif nu == 2:
-            t = torch.einsum("kMij,nic,njc->nkMc", Ut, a, a)
-        else:
-            t = torch.einsum("kMijl,nic,njc,nlc->nkMc", Ut, a, a, a)
-        y = (w[:, p:p + len(U), None, :] * t).sum(1)
-        outs[L] = y if outs[L] is None else outs[L] + y
-        p += len(U)
-    for L in range(l_out + 1):
-        if outs[L] is None:
-            outs[L] = a.new_zeros(N, 2 * L + 1, C)
-    return torch.cat([o.reshape(N, -1) for o in outs], dim=1)
+    w_all = W.to(torch.float64)[z] * valid[:, None, None].to(torch.float64)  # (N, P, C)
+    parts = paths(l_in, l_out, nu_max, parity_rule)
+    mats = [(L, nu, len(U), torch.from_numpy(np.ascontiguousarray(U.reshape(len(U) * (2 * L + 1), -1))))
+            for L, nu, U in parts]
+    chunks = []
+    for n0 in range(0, N, chunk):
+        n1 = min(N, n0 + chunk)
+        a = A[n0:n1].reshape(n1 - n0, ni, C).to(torch.float64).permute(0, 2, 1).reshape(-1, ni)  # rows (n, c)
+        w = w_all[n0:n1]
+        feats = {1: a}
+        if nu_max >= 2:
+            feats[2] = (a[:, :, None] * a[:, None, :]).reshape(a.shape[0], -1)
+        if nu_max >= 3:
+            feats[3] = (feats[2][:, :, None] * a[:, None, :]).reshape(a.shape[0], -1)
+        outs = [a.new_zeros(n1 - n0, C, 2 * L + 1) for L in range(l_out + 1)]
+        p = 0
+        for L, nu, r, Um in mats:
+            t = (feats[nu] @ Um.T).reshape(n1 - n0, C, r, 2 * L + 1)
+            outs[L] = outs[L] + (w[:, p:p + r, :].permute(0, 2, 1)[..., None] * t).sum(2)
+            p += r
+        chunks.append(torch.cat([o.permute(0, 2, 1).reshape(n1 - n0, -1) for o in outs], dim=1))
+    if not chunks:
+        return A.new_zeros(0, (l_out + 1) ** 2 * C, dtype=torch.float64)
+    return torch.cat(chunks, dim=0)
 
 
 def rotate(A, R, l_max, C):

@@ -32,38 +32,91 @@ def build(cfg, seed=0):
     from molnex_amd.molzoo import MACE
 
     torch.manual_seed(seed)
-    enc = MACE(node_attr_specs=[DiscreteEmbeddingSpec(input_key="Z", num_classes=cfg["num_elements"],
-                                                      emb_dim=cfg["num_features"])],
-               num_elements=cfg["num_elements"], num_features=cfg["num_features"], r_max=cfg["r_max"],
+    F = cfg["num_features"]
+    literal = cfg.get("hidden_ls") is not None
+    enc = MACE(node_attr_specs=[DiscreteEmbeddingSpec(input_key="Z", num_classes=cfg["num_elements"], emb_dim=F)],
+               num_elements=cfg["num_elements"], num_features=F, r_max=cfg["r_max"],
                num_bessel=cfg["num_bessel"], l_max=cfg["l_max"], num_interactions=cfg["num_interactions"],
-               correlation=cfg["correlation"], avg_num_neighbors=cfg["avg_num_neighbors"])
-    # keep the scalar polynomial of the product basis O(1) so fp32 stays well conditioned
+               correlation=cfg["correlation"], avg_num_neighbors=cfg["avg_num_neighbors"],
+               cutoff=cfg.get("cutoff", "cosine"),
+               hidden_irreps="+".join(f"{F}x{l}{'e' if l % 2 == 0 else 'o'}" for l in cfg["hidden_ls"])
+               if literal else None)
+    # keep the product basis polynomial O(1) so fp32 stays well conditioned
     with torch.no_grad():
         for p in enc.products:
-            p.symmetric_contraction.symmetric_contraction.weight.mul_(0.1)
-    return EnergyForceModel(enc, cfg["num_features"]).to(DEV)
+            sc = p.symmetric_contraction
+            (sc.weight if literal else sc.symmetric_contraction.weight).mul_(0.1)
+    return EnergyForceModel(enc, F).to(DEV)
 
 
 CFG1 = dict(num_elements=4, num_features=32, r_max=5.0, num_bessel=8, l_max=3, num_interactions=2, correlation=3,
             avg_num_neighbors=20.0)
 
 
+CFG1_LITERAL = dict(CFG1, cutoff="polynomial", hidden_ls=[0, 1])
+
+
 def test_config1_energy_forces_vs_fp64_oracle():
+    _config1_vs_oracle(CFG1)
+
+
+def test_config1_literal_energy_forces_vs_fp64_oracle():
+    """Literal MACE (hidden 32x0e+32x1o, polynomial cutoff, equivariant product basis)."""
+    _config1_vs_oracle(CFG1_LITERAL)
+
+
+def test_config1_literal_rotation_invariance():
+    """The literal configuration's per-atom scalar features (what the energy head reads) are
+    O(3)-invariant and its forces rotate with the positions (the reference's as-coded MACE is
+    not; its rotation tests are xfail).  The features' change under a rotation or inversion
+    must be negligible next to their change under a 0.05 A non-rigid jitter."""
+    from oracle import equivariant as EQ
+
+    pos, Z, batch = molecules(seed=2, n_mol=4)
+    ii, jj, _, _ = NL.directed_pairs(pos.astype(np.float32), 5.0, None)
+    ei = torch.tensor(np.stack([jj, ii], 1).astype(np.int64), device=DEV)
+    model = build(CFG1_LITERAL, seed=2)
+    Zt, bt = torch.tensor(Z, device=DEV), torch.tensor(batch, device=DEV)
+
+    def feats(p):
+        pt = torch.tensor(p, dtype=torch.float32, device=DEV)
+        d = pt[ei[:, 1]] - pt[ei[:, 0]]
+        with torch.no_grad():
+            return model.encoder(Z=Zt, bond_dist=d.norm(dim=-1), bond_diff=d, edge_index=ei).double().cpu()
+
+    h0 = feats(pos)
+    d_jit = (feats(pos + np.random.default_rng(7).normal(scale=0.05, size=pos.shape)) - h0).abs().max().item()
+    _, f0 = model(Zt, torch.tensor(pos, dtype=torch.float32, device=DEV), ei, bt, 4)
+    center = pos.reshape(4, 32, 3).mean(1, keepdims=True)
+    rel = pos.reshape(4, 32, 3) - center
+    for k, improper in ((5, False), (6, True)):
+        R = EQ.random_rotation(np.random.default_rng(k)) * (-1.0 if improper else 1.0)
+        pr = (rel @ R.T + center).reshape(-1, 3)
+        d_rot = (feats(pr) - h0).abs().max().item()
+        _, f1 = model(Zt, torch.tensor(pr, dtype=torch.float32, device=DEV), ei, bt, 4)
+        f0r = f0.detach().cpu().double() @ torch.tensor(R.T)
+        rel_f = ((f1.detach().cpu().double() - f0r).norm() / f0r.norm()).item()
+        print(f"improper={improper}: feature change {d_rot:.2e} (jitter {d_jit:.2e}, |h| {h0.abs().max():.2e}), "
+              f"force rel change {rel_f:.2e}")
+        assert d_rot <= 1e-3 * d_jit and rel_f <= 2e-4
+
+
+def _config1_vs_oracle(cfg):
     pos, Z, batch = molecules()
     # directed edges from the oracle neighbor list (the GPU list is checked bit-exactly elsewhere)
     ii, jj, _, _ = NL.directed_pairs(pos.astype(np.float32), 5.0, None)
     edge_index = np.stack([jj, ii], 1).astype(np.int64)
-    model = build(CFG1)
+    model = build(cfg)
     pt = torch.tensor(pos, dtype=torch.float32, device=DEV)
     e, f = model(torch.tensor(Z, device=DEV), pt, torch.tensor(edge_index, device=DEV),
                  torch.tensor(batch, device=DEV), 16)
     sd = {k.removeprefix("encoder."): v for k, v in model.state_dict().items()}
-    re, rf = mace_ref.energy_forces(sd, CFG1, torch.tensor(Z), torch.tensor(pos.astype(np.float32), dtype=torch.float64),
+    re, rf = mace_ref.energy_forces(sd, cfg, torch.tensor(Z), torch.tensor(pos.astype(np.float32), dtype=torch.float64),
                                     torch.tensor(edge_index), torch.tensor(batch), 16)
     e, f = e.detach().cpu().double(), f.detach().cpu().double()
     rel_e = ((e - re).abs() / re.abs()).max().item()
     rel_f = ((f - rf).norm() / rf.norm()).item()
-    print(f"config 1: energy rel err {rel_e:.2e}, force rel err {rel_f:.2e}, |E| ~ {re.abs().mean():.3f}")
+    print(f"config 1 ({'literal' if cfg.get('hidden_ls') else 'as coded'}): energy rel err {rel_e:.2e}, force rel err {rel_f:.2e}, |E| ~ {re.abs().mean():.3f}")
     assert rel_e <= 1e-5 and rel_f <= 1e-5
 
 
