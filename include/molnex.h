@@ -153,6 +153,19 @@ int mnx_tp_bwd_f32(int32_t config, int32_t channels, const float* x, const float
                    int64_t num_edges, float* grad_x, float* grad_Y, float* grad_w,
                    void* workspace, size_t workspace_bytes, mnx_stream_t stream);
 
+/* The same gradients, walked by sender, without atomics (bitwise reproducible):
+ * the CSR of edge_index[:, 0] (mnx_csr_build on the column-swapped edge list:
+ * s_row_ptr [N+1], s_perm = edge ids, s_receivers = their receivers).  grad_x,
+ * grad_Y and grad_w are overwritten (no zeroing needed).  Same results as
+ * mnx_tp_bwd_f32 up to fp32 summation order; slower on large graphs (weight rows
+ * are visited in sender order).  Replaces the same reference call (ConvTP
+ * backward, tensor_product.py:101-111). */
+int mnx_tp_bwd_sender_f32(int32_t config, int32_t channels, const float* x, const float* Y,
+                          const float* w, const float* grad_out, const int32_t* s_row_ptr,
+                          const int32_t* s_perm, const int32_t* s_receivers, int64_t num_nodes,
+                          int64_t num_edges, float* grad_x, float* grad_Y, float* grad_w,
+                          mnx_stream_t stream);
+
 /* ------------------------------------------------------------------------ */
 /* Particle-mesh Ewald (replaces torch.ops.molix.pme_reciprocal and           */
 /* pme_direct: molix_library.cpp:29-41, CPU pme_cpu.cpp:95-458, CUDA          */

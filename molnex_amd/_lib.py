@@ -40,6 +40,7 @@ SIGNATURES = {
     "mnx_tp_fwd_f32": (C.c_int, [c_i32, c_i32, vp, vp, vp, vp, vp, vp, c_i64, c_i64, vp, vp]),
     "mnx_tp_bwd_workspace_bytes": (c_sz, [c_i32, c_i32, c_i64]),
     "mnx_tp_bwd_f32": (C.c_int, [c_i32, c_i32, vp, vp, vp, vp, vp, vp, vp, c_i64, c_i64, vp, vp, vp, vp, c_sz, vp]),
+    "mnx_tp_bwd_sender_f32": (C.c_int, [c_i32, c_i32, vp, vp, vp, vp, vp, vp, vp, c_i64, c_i64, vp, vp, vp, vp]),
     "mnx_pme_spread_f32": (C.c_int, [vp, vp, vp, c_i64, c_i32, c_i32, c_i32, c_i32, c_f64, vp, vp]),
     "mnx_pme_spread_f64": (C.c_int, [vp, vp, vp, c_i64, c_i32, c_i32, c_i32, c_i32, c_f64, vp, vp]),
     "mnx_pme_convolve_workspace_bytes": (c_sz, [c_i32, c_i32, c_i32]),

@@ -10,6 +10,9 @@ import torch
 class _Config:
     ftype: torch.dtype = torch.float32
     itype: torch.dtype = torch.int64
+    # True: tensor-product backward walked by sender, without atomics (bitwise
+    # reproducible gradients, slower on large graphs)
+    deterministic: bool = False
 
 
 config = _Config()

@@ -199,10 +199,12 @@ def gen_fwd(cfg: Cfg, g: int) -> str:
     a(f"  const int64_t XS = int64_t({cfg.NX}) * C, WS = int64_t({cfg.NP}) * C;")
     _emit_edge_loop_head(a, cfg, ps, xs, ys, xi)
     a("    (void)e; (void)s;")
-    # uniform coupling matrices M_p[m3][m1]
+    # per output row (path j, m3): the wave-uniform coupling row M_j[m3][m1] = sum_m2 c y,
+    # used at once for every channel of the lane (short live ranges, no hoisted M table)
     for j, p in enumerate(ps):
         c = p["c"]
         for m3 in range(2 * p["l3"] + 1):
+            row = []
             for m1 in range(2 * p["l1"] + 1):
                 terms = [(m2, c[m1, m2, m3]) for m2 in range(2 * p["l2"] + 1) if abs(c[m1, m2, m3]) > EPS]
                 if not terms:
@@ -210,22 +212,21 @@ def gen_fwd(cfg: Cfg, g: int) -> str:
                 expr = f"{f32(terms[0][1])} * y{p['o2'] + terms[0][0]}"
                 for m2, v in terms[1:]:
                     expr = f"fmaf({f32(v)}, y{p['o2'] + m2}, {expr})"
-                a(f"    const float M{j}_{m3}_{m1} = {expr};")
-    a("#pragma unroll")
-    a("    for (int k = 0; k < CPL; ++k) {")
-    for j, p in enumerate(ps):
-        c = p["c"]
-        for m3 in range(2 * p["l3"] + 1):
-            m1s = [m1 for m1 in range(2 * p["l1"] + 1)
-                   if any(abs(c[m1, m2, m3]) > EPS for m2 in range(2 * p["l2"] + 1))]
-            if not m1s:
+                row.append((m1, expr))
+            if not row:
                 continue
-            expr = f"M{j}_{m3}_{m1s[0]} * xv[k][{xi[p['o1'] + m1s[0]]}]"
-            for m1 in m1s[1:]:
-                expr = f"fmaf(M{j}_{m3}_{m1}, xv[k][{xi[p['o1'] + m1]}], {expr})"
+            a("    {")
+            for m1, expr in row:
+                a(f"      const float M{m1} = {expr};")
             o = oi[p["o3"] + m3]
-            a(f"      acc[k][{o}] = fmaf(wv[k][{j}], {expr}, acc[k][{o}]);")
-    a("    }")
+            a("#pragma unroll")
+            a("      for (int k = 0; k < CPL; ++k) {")
+            expr = f"M{row[0][0]} * xv[k][{xi[p['o1'] + row[0][0]]}]"
+            for m1, _ in row[1:]:
+                expr = f"fmaf(M{m1}, xv[k][{xi[p['o1'] + m1]}], {expr})"
+            a(f"        acc[k][{o}] = fmaf(wv[k][{j}], {expr}, acc[k][{o}]);")
+            a("      }")
+            a("    }")
     a("  }")
     a(f"  float* __restrict__ on = out + n * int64_t({cfg.NO}) * C;")
     a("#pragma unroll")
@@ -339,6 +340,217 @@ def gen_bwd(cfg: Cfg, g: int) -> str:
     a("}")
     return "\n".join(L)
 
+# ---------------------------------------------------------------------------
+# Sender-major backward: one wavefront per (sender, channel block, path subgroup)
+# walks the sender's out-edges (sender CSR), so grad_x of the sender accumulates in
+# registers and is stored once -- no atomics.  Per sender and channel the table
+# N_p[m2][m3] = sum_m1 c[m1,m2,m3] x[m1] is formed once; per edge, with the
+# receiver's output gradient g gathered (read-only, cache resident):
+#   u_p[m1] = sum_m3 M_p[m3][m1] g_p[m3]  (M from the wave-uniform harmonics)
+#       -> grad_x[m1] += w_p u_p[m1]
+#   s_p[m2] = sum_m3 N_p[m2][m3] g_p[m3]
+#       -> grad_w_p = sum_m2 Y[m2] s_p[m2],  grad_Y[m2] += w_p s_p[m2] (channel sum)
+# Paths of one input l are split into subgroups whose per-channel register state
+# stays within SENDER_BUDGET; the first subgroup of an l stores grad_x, later ones add.
+# ---------------------------------------------------------------------------
+
+SENDER_BUDGET = 60
+
+
+def _npairs(p):
+    c = p["c"]
+    return [(m2, m3) for m2 in range(2 * p["l2"] + 1) for m3 in range(2 * p["l3"] + 1)
+            if np.any(np.abs(c[:, m2, m3]) > EPS)]
+
+
+def _sstate(ps):
+    nx = 2 * ps[0]["l1"] + 1
+    return sum(len(_npairs(p)) + 2 * (2 * p["l3"] + 1) + 2 for p in ps) + nx
+
+
+def sender_subgroups(cfg):
+    """[(paths, first_of_its_l)] in launch order."""
+    subs = []
+    for ps in cfg.groups:
+        cur, first = [], True
+        for p in ps:
+            if cur and _sstate(cur + [p]) > SENDER_BUDGET:
+                subs.append((cur, first))
+                cur, first = [p], False
+            else:
+                cur = cur + [p]
+        if cur:
+            subs.append((cur, first))
+    return subs
+
+
+def sender_cpl(ps) -> int:
+    return 2 if _sstate(ps) <= SENDER_BUDGET else 1
+
+
+def _sub_layout(ps):
+    xs = [ps[0]["o1"] + m for m in range(2 * ps[0]["l1"] + 1)]
+    ys = _uniq([p["o2"] + m for p in ps for m in range(2 * p["l2"] + 1)])
+    outs = [p["o3"] + m for p in ps for m in range(2 * p["l3"] + 1)]
+    return xs, ys, outs
+
+
+def gen_bwd_sender(cfg: Cfg, sg: int, ps, first: bool) -> str:
+    xs, ys, outs = _sub_layout(ps)
+    xi = {c: i for i, c in enumerate(xs)}
+    oi = {c: i for i, c in enumerate(outs)}
+    yi = {c: i for i, c in enumerate(ys)}
+    V = 1
+    while V < len(ys):
+        V *= 2
+    nidx = {}
+    for j, p in enumerate(ps):
+        for (m2, m3) in _npairs(p):
+            nidx[(j, m2, m3)] = len(nidx)
+    L = []
+    a = L.append
+    name = f"tp_bws_c{cfg.idx}_s{sg}"
+    a(f"template <int CPL>\n__global__ void __launch_bounds__(64) {name}(const float* __restrict__ x, "
+      "const float* __restrict__ Y, const float* __restrict__ w, const float* __restrict__ gout, "
+      "const int32_t* __restrict__ row_ptr, const int32_t* __restrict__ perm, const int32_t* __restrict__ rcv, "
+      "int64_t N, int C, float* __restrict__ gx, float* __restrict__ gw, float* __restrict__ gyp, int, int) {")
+    a("  const int64_t s = xcd_node(blockIdx.x, gridDim.x);")
+    a("  if (s >= N) return;")
+    a("  const int lane = threadIdx.x;")
+    a("  int cc[CPL]; bool ok[CPL];")
+    a("#pragma unroll")
+    a("  for (int k = 0; k < CPL; ++k) { cc[k] = blockIdx.y * (64 * CPL) + 64 * k + lane; ok[k] = cc[k] < C; }")
+    a(f"  const int64_t XS = int64_t({cfg.NX}) * C, WS = int64_t({cfg.NP}) * C, OS = int64_t({cfg.NO}) * C;")
+    a(f"  float nv[CPL][{max(len(nidx), 1)}], gxa[CPL][{len(xs)}];")
+    a("#pragma unroll")
+    a("  for (int k = 0; k < CPL; ++k) {")
+    a(f"    const float* __restrict__ xr = x + s * XS;")
+    for c in xs:
+        a(f"    const float x{xi[c]} = ok[k] ? xr[{c} * C + cc[k]] : 0.f;")
+    for (j, m2, m3), i in nidx.items():
+        p = ps[j]
+        terms = [(m1, p["c"][m1, m2, m3]) for m1 in range(2 * p["l1"] + 1) if abs(p["c"][m1, m2, m3]) > EPS]
+        expr = f"{f32(terms[0][1])} * x{xi[p['o1'] + terms[0][0]]}"
+        for m1, v in terms[1:]:
+            expr = f"fmaf({f32(v)}, x{xi[p['o1'] + m1]}, {expr})"
+        a(f"    nv[k][{i}] = {expr};")
+    for c in xs:
+        a(f"    gxa[k][{xi[c]}] = 0.f;")
+    a("  }")
+    a("  const int beg = row_ptr[s], end = row_ptr[s + 1];")
+    a("  int ne = 0, nr = 0;")
+    a("  " + " ".join(f"float ny{c} = 0.f;" for c in ys))
+    a(f"  float ngv[CPL][{len(outs)}], nwv[CPL][{len(ps)}];")
+
+    def prefetch(indent, t_expr):
+        a(f"{indent}{{")
+        a(f"{indent}  ne = perm[{t_expr}]; nr = rcv[{t_expr}];")
+        a(f"{indent}  const float* __restrict__ Yn = Y + int64_t(ne) * {cfg.NY};")
+        for c in ys:
+            a(f"{indent}  ny{c} = Yn[{c}];")
+        a(f"{indent}  const float* __restrict__ gn = gout + int64_t(nr) * OS;")
+        a(f"{indent}  const float* __restrict__ wn = w + int64_t(ne) * WS;")
+        a("#pragma unroll")
+        a(f"{indent}  for (int k = 0; k < CPL; ++k) {{")
+        for c in outs:
+            a(f"{indent}    ngv[k][{oi[c]}] = ok[k] ? gn[{c} * C + cc[k]] : 0.f;")
+        for j, p in enumerate(ps):
+            a(f"{indent}    nwv[k][{j}] = ok[k] ? __builtin_nontemporal_load(wn + {p['k']} * C + cc[k]) : 0.f;")
+        a(f"{indent}  }}")
+        a(f"{indent}}}")
+
+    a("  if (beg < end)")
+    prefetch("  ", "beg")
+    a("  for (int t = beg; t < end; ++t) {")
+    a("    const int e = ne;")
+    a("    " + " ".join(f"const float y{c} = ny{c};" for c in ys))
+    a(f"    float gv[CPL][{len(outs)}], wv[CPL][{len(ps)}];")
+    a("#pragma unroll")
+    a("    for (int k = 0; k < CPL; ++k) {")
+    a(f"#pragma unroll\n      for (int i = 0; i < {len(outs)}; ++i) gv[k][i] = ngv[k][i];")
+    a(f"#pragma unroll\n      for (int i = 0; i < {len(ps)}; ++i) wv[k][i] = nwv[k][i];")
+    a("    }")
+    a("    if (t + 1 < end)")
+    prefetch("    ", "t + 1")
+    a("    float* __restrict__ gwe = gw ? gw + int64_t(e) * WS : nullptr;")
+    a(f"    float gy[{V}];")
+    a("#pragma unroll")
+    a(f"    for (int i = 0; i < {V}; ++i) gy[i] = 0.f;")
+    a("#pragma unroll")
+    a("    for (int k = 0; k < CPL; ++k) {")
+    for j, p in enumerate(ps):
+        c = p["c"]
+        n1, n2, n3 = 2 * p["l1"] + 1, 2 * p["l2"] + 1, 2 * p["l3"] + 1
+        # u_j[m1] = sum_m3 M[m3][m1] g[m3]
+        for m1 in range(n1):
+            ents = []
+            for m3 in range(n3):
+                terms = [(m2, c[m1, m2, m3]) for m2 in range(n2) if abs(c[m1, m2, m3]) > EPS]
+                if not terms:
+                    continue
+                expr = f"{f32(terms[0][1])} * y{p['o2'] + terms[0][0]}"
+                for m2, v in terms[1:]:
+                    expr = f"fmaf({f32(v)}, y{p['o2'] + m2}, {expr})"
+                ents.append((m3, expr))
+            if not ents:
+                continue
+            a("      {")
+            for m3, expr in ents:
+                a(f"        const float M{m3} = {expr};")
+            uexpr = f"M{ents[0][0]} * gv[k][{oi[p['o3'] + ents[0][0]]}]"
+            for m3, _ in ents[1:]:
+                uexpr = f"fmaf(M{m3}, gv[k][{oi[p['o3'] + m3]}], {uexpr})"
+            a(f"        gxa[k][{xi[p['o1'] + m1]}] = fmaf(wv[k][{j}], {uexpr}, gxa[k][{xi[p['o1'] + m1]}]);")
+            a("      }")
+        # s_j[m2] = sum_m3 N[m2][m3] g[m3]
+        svals = []
+        for m2 in range(n2):
+            m3s = [m3 for m3 in range(n3) if (j, m2, m3) in nidx]
+            if not m3s:
+                continue
+            expr = f"nv[k][{nidx[(j, m2, m3s[0])]}] * gv[k][{oi[p['o3'] + m3s[0]]}]"
+            for m3 in m3s[1:]:
+                expr = f"fmaf(nv[k][{nidx[(j, m2, m3)]}], gv[k][{oi[p['o3'] + m3]}], {expr})"
+            a(f"      const float s{j}_{m2} = {expr};")
+            a(f"      gy[{yi[p['o2'] + m2]}] = fmaf(wv[k][{j}], s{j}_{m2}, gy[{yi[p['o2'] + m2]}]);")
+            svals.append(m2)
+        if svals:
+            expr = f"y{p['o2'] + svals[0]} * s{j}_{svals[0]}"
+            for m2 in svals[1:]:
+                expr = f"fmaf(y{p['o2'] + m2}, s{j}_{m2}, {expr})"
+        else:
+            expr = "0.f"
+        a(f"      if (gwe && ok[k]) __builtin_nontemporal_store({expr}, gwe + {p['k']} * C + cc[k]);")
+    a("    }")
+    # grad_Y accumulates in place (zeroed by the caller): one wave per (edge, component)
+    # when the channels fit one block, atomics otherwise
+    ymap = "{" + ", ".join(str(c) for c in ys) + "}"
+    a("    if (gyp) {")
+    a(f"      float r = wave_reduce_scatter<{V}>(gy, lane);")
+    a(f"      const int comp = reduce_scatter_index<{V}>(lane);")
+    a(f"      constexpr int ymap[{len(ys)}] = {ymap};")
+    a(f"      if ((lane & (64 / {V} - 1)) == 0 && comp < {len(ys)}) {{")
+    a(f"        float* __restrict__ dst = gyp + int64_t(e) * {cfg.NY} + ymap[comp];")
+    a("        if (gridDim.y == 1) *dst += r; else atomicAdd(dst, r);")
+    a("      }")
+    a("    }")
+    a("  }")
+    a("  if (gx) {")
+    a("#pragma unroll")
+    a("    for (int k = 0; k < CPL; ++k) {")
+    a("      if (!ok[k]) continue;")
+    a("      float* __restrict__ gxs = gx + s * XS;")
+    for c in xs:
+        if first:
+            a(f"      gxs[{c} * C + cc[k]] = gxa[k][{xi[c]}];")
+        else:
+            a(f"      gxs[{c} * C + cc[k]] += gxa[k][{xi[c]}];")
+    a("    }")
+    a("  }")
+    a("}")
+    return "\n".join(L)
+
+
 
 def generate() -> str:
     cfgs = [Cfg(i, *c) for i, c in enumerate(config_list())]
@@ -351,6 +563,9 @@ def generate() -> str:
             out.append(gen_fwd(cfg, g))
             out.append("")
             out.append(gen_bwd(cfg, g))
+            out.append("")
+        for sg, (ps, first) in enumerate(sender_subgroups(cfg)):
+            out.append(gen_bwd_sender(cfg, sg, ps, first))
             out.append("")
     # dispatch tables
     out.append("static const TPConfigInfo kTPConfigs[] = {")
@@ -376,6 +591,22 @@ def generate() -> str:
     out.append("static const int kTPBwdCPL[][4] = {")
     for cfg in cfgs:
         cp = [str(bwd_cpl(ps)) for ps in cfg.groups] + ["0"] * (4 - len(cfg.groups))
+        out.append("  {" + ", ".join(cp) + "},")
+    out.append("};")
+    # sender-major backward: subgroups, channels per lane, harmonics components per subgroup
+    subs = [sender_subgroups(cfg) for cfg in cfgs]
+    ms = max(len(x) for x in subs)
+    out.append(f"static constexpr int kTPMaxSub = {ms};")
+    out.append("static const int kTPBwSNum[] = {" + ", ".join(str(len(x)) for x in subs) + "};")
+    out.append(f"static const TPBwdFn kTPBwS[][{ms}] = {{")
+    for cfg, sl in zip(cfgs, subs):
+        fns = [f"tp_bws_c{cfg.idx}_s{sg}<{sender_cpl(ps)}>" for sg, (ps, _) in enumerate(sl)]
+        fns += ["nullptr"] * (ms - len(fns))
+        out.append("  {" + ", ".join(fns) + "},")
+    out.append("};")
+    out.append(f"static const int kTPBwSCPL[][{ms}] = {{")
+    for sl in subs:
+        cp = [str(sender_cpl(ps)) for ps, _ in sl] + ["0"] * (ms - len(sl))
         out.append("  {" + ", ".join(cp) + "},")
     out.append("};")
     return "\n".join(out) + "\n"

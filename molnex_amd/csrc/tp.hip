@@ -125,6 +125,11 @@ __global__ void k_reduce_partials(const float* __restrict__ part, int64_t E, int
     gY[idx] = s;
 }
 
+__global__ void k_zero(float* __restrict__ p, int64_t n) {
+    const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i < n) p[i] = 0.f;
+}
+
 int check_common(int config, int channels, int64_t N, int64_t E) {
     MNX_REQUIRE(config >= 0 && config < kNumTPConfigs, "invalid tp config %d", config);
     MNX_REQUIRE(channels > 0 && channels <= 4096, "channels out of range: %d", channels);
@@ -223,6 +228,33 @@ int mnx_tp_bwd_f32(int32_t config, int32_t C, const float* x, const float* Y, co
         const int64_t tot = E * cfg.ny;
         hipLaunchKernelGGL(k_reduce_partials, dim3(unsigned(ceil_div(tot, 256))), dim3(256), 0, (hipStream_t)stream,
                            part, E, npart, cfg.ny, gY);
+        MNX_CHECK_LAUNCH();
+    }
+    return MNX_OK;
+}
+
+int mnx_tp_bwd_sender_f32(int32_t config, int32_t C, const float* x, const float* Y, const float* w,
+                          const float* gout, const int32_t* s_row_ptr, const int32_t* s_perm,
+                          const int32_t* s_receivers, int64_t N, int64_t E, float* gx, float* gY, float* gw,
+                          mnx_stream_t stream) {
+    clear_error();
+    int rc = check_common(config, C, N, E);
+    if (rc) return rc;
+    if (N == 0) return MNX_OK;
+    MNX_REQUIRE(s_row_ptr && (E == 0 || (x && Y && w && gout && s_perm && s_receivers)), "null pointer argument");
+    const TPConfigInfo& cfg = kTPConfigs[config];
+    if (gY && E > 0) {  // accumulated in place by the subgroup kernels (a fill kernel: no memset node)
+        const int64_t n = E * cfg.ny;
+        hipLaunchKernelGGL(k_zero, dim3(unsigned(ceil_div(n, 256))), dim3(256), 0, (hipStream_t)stream, gY, n);
+        MNX_CHECK_LAUNCH();
+    }
+    // every (sender, component, channel) of grad_x is stored by the first subgroup of its
+    // input l (senders without edges store zeros) and accumulated by the later ones; each
+    // edge lies in one sender segment of the CSR (mnx_csr_build rejects out-of-range indices)
+    for (int g = 0; g < kTPBwSNum[config]; ++g) {
+        const int cblocks = int(ceil_div(C, 64 * kTPBwSCPL[config][g]));
+        hipLaunchKernelGGL(kTPBwS[config][g], node_grid(N, cblocks), dim3(64), 0, (hipStream_t)stream, x, Y, w,
+                           gout, s_row_ptr, s_perm, s_receivers, N, C, gx, gw, E > 0 ? gY : nullptr, 0, 0);
         MNX_CHECK_LAUNCH();
     }
     return MNX_OK;

@@ -307,8 +307,12 @@ def tp_config_info(config: int) -> tuple[int, int, int, int]:
 
 @torch.library.custom_op("molix::tp_scatter", mutates_args=(), device_types="cuda")
 def tp_scatter(x: Tensor, Y: Tensor, w: Tensor, row_ptr: Tensor, perm: Tensor, senders: Tensor, config: int,
-               channels: int) -> Tensor:
-    """``out[r] = sum_{e -> r} TP(x[send(e)], Y[e]; w[e])`` for a compiled configuration."""
+               channels: int, s_row_ptr: Tensor | None = None, s_perm: Tensor | None = None,
+               s_receivers: Tensor | None = None) -> Tensor:
+    """``out[r] = sum_{e -> r} TP(x[send(e)], Y[e]; w[e])`` for a compiled configuration.
+
+    ``(row_ptr, perm, senders)`` is the receiver CSR (``edge_csr``).  The optional sender CSR
+    (``edge_csr`` of the column-swapped edge list) selects the atomic-free backward."""
     _require_gpu("tp_scatter", x, Y, w, row_ptr)
     num_paths, nx, ny, no = tp_config_info(config)
     N = row_ptr.shape[0] - 1
@@ -318,6 +322,9 @@ def tp_scatter(x: Tensor, Y: Tensor, w: Tensor, row_ptr: Tensor, perm: Tensor, s
     ws_ = _f32_rows(w, num_paths * channels, "w")
     if xs.shape[0] != N or ws_.shape[0] != E or perm.shape[0] != E:
         raise ValueError("tp_scatter: inconsistent sizes of x / Y / w / CSR")
+    if s_row_ptr is not None and (s_row_ptr.shape[0] != N + 1 or s_perm is None or s_receivers is None
+                                  or s_perm.shape[0] != E or s_receivers.shape[0] != E):
+        raise ValueError("tp_scatter: inconsistent sender CSR")
     out = torch.empty((N, no * channels), dtype=torch.float32, device=xs.device)
     check(_lib.load().mnx_tp_fwd_f32(config, channels, ptr(xs), ptr(Ys), ptr(ws_), ptr(row_ptr), ptr(perm),
                                      ptr(senders), N, E, ptr(out), _stream(xs)), "tp_scatter")
@@ -325,7 +332,7 @@ def tp_scatter(x: Tensor, Y: Tensor, w: Tensor, row_ptr: Tensor, perm: Tensor, s
 
 
 @tp_scatter.register_fake
-def _(x, Y, w, row_ptr, perm, senders, config, channels):
+def _(x, Y, w, row_ptr, perm, senders, config, channels, s_row_ptr=None, s_perm=None, s_receivers=None):
     num_paths, nx, ny, no = tp_config_info(config)
     return x.new_empty((row_ptr.shape[0] - 1, no * channels))
 
@@ -333,8 +340,10 @@ def _(x, Y, w, row_ptr, perm, senders, config, channels):
 @torch.library.custom_op("molix::tp_scatter_backward", mutates_args=(), device_types="cuda")
 def tp_scatter_backward(grad_out: Tensor, x: Tensor, Y: Tensor, w: Tensor, row_ptr: Tensor, perm: Tensor,
                         senders: Tensor, config: int, channels: int, need_x: bool, need_Y: bool,
-                        need_w: bool) -> tuple[Tensor, Tensor, Tensor]:
-    """Gradients of ``<grad_out, tp_scatter(...)>`` w.r.t. x, Y, w (empty when not needed)."""
+                        need_w: bool, s_row_ptr: Tensor | None = None, s_perm: Tensor | None = None,
+                        s_receivers: Tensor | None = None) -> tuple[Tensor, Tensor, Tensor]:
+    """Gradients of ``<grad_out, tp_scatter(...)>`` w.r.t. x, Y, w (empty when not needed).
+    With the sender CSR the gradients are walked by sender (grad_x without atomics)."""
     lib = _lib.load()
     num_paths, nx, ny, no = tp_config_info(config)
     N = row_ptr.shape[0] - 1
@@ -344,27 +353,38 @@ def tp_scatter_backward(grad_out: Tensor, x: Tensor, Y: Tensor, w: Tensor, row_p
     wss = _f32_rows(w, num_paths * channels, "w")
     go = _f32_rows(grad_out, no * channels, "grad_out")
     dev = xs.device
-    gx = torch.zeros_like(xs) if need_x else xs.new_empty(0)
+    by_sender = s_row_ptr is not None
+    if need_x:
+        gx = torch.empty_like(xs) if by_sender else torch.zeros_like(xs)
+    else:
+        gx = xs.new_empty(0)
     gY = torch.empty_like(Ys) if need_Y else Ys.new_empty(0)
     gw = torch.empty_like(wss) if need_w else wss.new_empty(0)
-    ws = _ws(lib.mnx_tp_bwd_workspace_bytes(config, channels, E) if need_Y else 1, dev)
-    check(lib.mnx_tp_bwd_f32(config, channels, ptr(xs), ptr(Ys), ptr(wss), ptr(go), ptr(row_ptr), ptr(perm),
-                             ptr(senders), N, E, ptr(gx), ptr(gY), ptr(gw), ptr(ws), ws.numel(), _stream(xs)),
-          "tp_scatter backward")
+    if by_sender:
+        check(lib.mnx_tp_bwd_sender_f32(config, channels, ptr(xs), ptr(Ys), ptr(wss), ptr(go), ptr(s_row_ptr),
+                                        ptr(s_perm), ptr(s_receivers), N, E, ptr(gx), ptr(gY), ptr(gw),
+                                        _stream(xs)), "tp_scatter backward (by sender)")
+    else:
+        ws = _ws(lib.mnx_tp_bwd_workspace_bytes(config, channels, E) if need_Y else 1, dev)
+        check(lib.mnx_tp_bwd_f32(config, channels, ptr(xs), ptr(Ys), ptr(wss), ptr(go), ptr(row_ptr), ptr(perm),
+                                 ptr(senders), N, E, ptr(gx), ptr(gY), ptr(gw), ptr(ws), ws.numel(), _stream(xs)),
+              "tp_scatter backward")
     if E == 0:
         gY.zero_() if need_Y else None
     return gx, gY, gw
 
 
 @tp_scatter_backward.register_fake
-def _(grad_out, x, Y, w, row_ptr, perm, senders, config, channels, need_x, need_Y, need_w):
+def _(grad_out, x, Y, w, row_ptr, perm, senders, config, channels, need_x, need_Y, need_w, s_row_ptr=None,
+      s_perm=None, s_receivers=None):
     return (torch.empty_like(x) if need_x else x.new_empty(0), torch.empty_like(Y) if need_Y else Y.new_empty(0),
             torch.empty_like(w) if need_w else w.new_empty(0))
 
 
 def _tp_setup(ctx, inputs, output):
-    x, Y, w, row_ptr, perm, senders, config, channels = inputs
+    x, Y, w, row_ptr, perm, senders, config, channels, s_row_ptr, s_perm, s_receivers = inputs
     ctx.save_for_backward(x, Y, w, row_ptr, perm, senders)
+    ctx.sender_csr = (s_row_ptr, s_perm, s_receivers)
     ctx.config, ctx.channels = config, channels
 
 
@@ -372,9 +392,9 @@ def _tp_backward(ctx, grad_out):
     x, Y, w, row_ptr, perm, senders = ctx.saved_tensors
     nx, nY, nw = ctx.needs_input_grad[:3]
     gx, gY, gw = tp_scatter_backward(grad_out.contiguous(), x, Y, w, row_ptr, perm, senders, ctx.config,
-                                     ctx.channels, nx, nY, nw)
+                                     ctx.channels, nx, nY, nw, *ctx.sender_csr)
     return (gx.reshape(x.shape) if nx else None, gY.reshape(Y.shape) if nY else None,
-            gw.reshape(w.shape) if nw else None, None, None, None, None, None)
+            gw.reshape(w.shape) if nw else None, None, None, None, None, None, None, None, None)
 
 
 tp_scatter.register_autograd(_tp_backward, setup_context=_tp_setup)

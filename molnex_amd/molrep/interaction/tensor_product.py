@@ -14,6 +14,7 @@ import torch.nn as nn
 from pydantic import BaseModel
 
 from ... import kernels as K
+from ...config import config
 from ...irreps import ChannelwiseTPDescriptor, Irrep, Irreps
 from ...irreps import irreps_from_l_max as _irreps_from_l_max
 from ...irreps import sh_irreps_from_l_max as _sh_irreps_from_l_max
@@ -37,12 +38,19 @@ def _natural_ls(irreps: Irreps, what: str) -> list[int]:
 
 
 class EdgeGraph:
-    """Receiver CSR of one edge list, built once and reused by every layer."""
+    """Receiver CSR of one edge list, built once and reused by every layer; the sender CSR
+    (for the atomic-free backward, ``config.deterministic``) is built on first use."""
 
     def __init__(self, edge_index: torch.Tensor, num_nodes: int):
         self.edge_index = edge_index
         self.num_nodes = num_nodes
         self.row_ptr, self.perm, self.senders = torch.ops.molix.edge_csr(edge_index, num_nodes)
+        self._sender_csr = None
+
+    def sender_csr(self):
+        if self._sender_csr is None:
+            self._sender_csr = torch.ops.molix.edge_csr(self.edge_index.flip(1), self.num_nodes)
+        return self._sender_csr
 
 
 _graph_cache: dict = {}
@@ -88,7 +96,9 @@ class ChannelWiseTensorProduct(nn.Module):
         return self.apply_graph(x, y, weight, g)
 
     def apply_graph(self, x, y, weight, g: EdgeGraph):
-        return torch.ops.molix.tp_scatter(x, y, weight, g.row_ptr, g.perm, g.senders, self.config_id, self.channels)
+        extra = g.sender_csr() if config.deterministic else ()
+        return torch.ops.molix.tp_scatter(x, y, weight, g.row_ptr, g.perm, g.senders, self.config_id, self.channels,
+                                          *extra)
 
 
 class ConvTP(nn.Module):

@@ -55,19 +55,24 @@ def run_case(cfg, C, N, E, seed, ops):
     w = rng.normal(size=(E, len(tp.paths) * C)).astype(np.float32)
     ei = rng.integers(0, N, (E, 2))
     ei[: E // 10, 1] = 0  # one heavy receiver
+    ei[E // 10: E // 5, 0] = 1  # one heavy sender
     g = rng.normal(size=(N, tp.no * C)).astype(np.float32)
     config = K.tp_config_id(in_ls, sh_ls, out_ls)
     assert config >= 0
     xt, Yt, wt = (torch.tensor(a, device=DEV, requires_grad=True) for a in (x, Y, w))
-    row_ptr, perm, snd = ops.edge_csr(torch.tensor(ei, device=DEV), N)
-    out = ops.tp_scatter(xt, Yt, wt, row_ptr, perm, snd, config, C)
+    eit = torch.tensor(ei, device=DEV)
+    row_ptr, perm, snd = ops.edge_csr(eit, N)
+    scsr = ops.edge_csr(eit.flip(1), N)
     ref = tp.forward(x, Y, w, ei, N)
-    assert_close(out.detach().cpu().numpy(), ref, f"fwd {cfg} C={C}")
-    gx, gY, gw = torch.autograd.grad(out, (xt, Yt, wt), torch.tensor(g, device=DEV))
     rx, rY, rw = tp.backward(x, Y, w, ei, g)
-    assert_close(gx.cpu().numpy(), rx, f"grad_x {cfg} C={C}")
-    assert_close(gY.cpu().numpy(), rY, f"grad_Y {cfg} C={C}")
-    assert_close(gw.cpu().numpy(), rw, f"grad_w {cfg} C={C}")
+    # backward walked by receiver (grad_x atomics) and by sender (no atomics)
+    for tag, extra in (("by receiver", ()), ("by sender", scsr)):
+        out = ops.tp_scatter(xt, Yt, wt, row_ptr, perm, snd, config, C, *extra)
+        assert_close(out.detach().cpu().numpy(), ref, f"fwd {cfg} C={C}")
+        gx, gY, gw = torch.autograd.grad(out, (xt, Yt, wt), torch.tensor(g, device=DEV))
+        assert_close(gx.cpu().numpy(), rx, f"grad_x {cfg} C={C} {tag}")
+        assert_close(gY.cpu().numpy(), rY, f"grad_Y {cfg} C={C} {tag}")
+        assert_close(gw.cpu().numpy(), rw, f"grad_w {cfg} C={C} {tag}")
 
 
 @pytest.fixture(scope="module")
@@ -100,6 +105,12 @@ def test_tp_empty_receivers_and_no_edges(ops):
     out = ops.tp_scatter(x, torch.zeros((0, ny), device=DEV), torch.zeros((0, num_paths * C), device=DEV), row_ptr,
                          perm, snd, config, C)
     assert out.shape == (N, no * C) and torch.all(out == 0)
+    # backward with no edges, walked by sender: grad_x must come back all zero (stored, not accumulated)
+    xg = x.clone().requires_grad_(True)
+    out = ops.tp_scatter(xg, torch.zeros((0, ny), device=DEV), torch.zeros((0, num_paths * C), device=DEV), row_ptr,
+                         perm, snd, config, C, *ops.edge_csr(ei.flip(1), N))
+    (gx,) = torch.autograd.grad(out, (xg,), torch.ones_like(out))
+    assert torch.all(gx == 0)
 
 
 def test_edge_csr_rejects_out_of_range(ops):
@@ -121,3 +132,22 @@ def test_tp_deterministic_forward(ops):
     a = ops.tp_scatter(x, Y, w, *csr, config, C)
     b = ops.tp_scatter(x, Y, w, *csr, config, C)
     assert torch.equal(a, b)
+
+
+def test_tp_backward_by_sender_is_bitwise_reproducible(ops):
+    """The sender-walked backward has no atomics: two runs give identical gradients."""
+    from molnex_amd import kernels as K
+
+    rng = np.random.default_rng(10)
+    C, N, E = 128, 60, 1500
+    config = K.tp_config_id([0, 1, 2, 3], [0, 1, 2, 3], [0, 1, 2, 3])
+    x = torch.tensor(rng.normal(size=(N, 16 * C)), dtype=torch.float32, device=DEV)
+    Y = torch.tensor(rng.normal(size=(E, 16)), dtype=torch.float32, device=DEV)
+    w = torch.tensor(rng.normal(size=(E, 23 * C)), dtype=torch.float32, device=DEV)
+    g = torch.tensor(rng.normal(size=(N, 99 * C)), dtype=torch.float32, device=DEV)
+    ei = torch.tensor(rng.integers(0, N, (E, 2)), device=DEV)
+    csr, scsr = ops.edge_csr(ei, N), ops.edge_csr(ei.flip(1), N)
+    a = K.tp_scatter_backward(g, x, Y, w, *csr, config, C, True, True, True, *scsr)
+    b = K.tp_scatter_backward(g, x, Y, w, *csr, config, C, True, True, True, *scsr)
+    for u, v in zip(a, b):
+        assert torch.equal(u, v)
