@@ -45,8 +45,9 @@ def parse():
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--unsorted", action="store_true", help="keep atoms in random order (no spatial sort)")
     p.add_argument("--seed", type=int, default=0)
-    p.add_argument("--workload", choices=["tp", "full", "sc"], default="tp",
-                   help="tp: config 3 edge step (default, the headline line); full: config 5 energy + forces")
+    p.add_argument("--workload", choices=["tp", "full", "sc", "nl", "pme"], default="tp",
+                   help="tp: config 3 edge step (default, the headline line); full: config 5 energy + forces; "
+                        "sc / nl / pme: config 4, config 2, config 5's PME term alone")
     p.add_argument("--no-secondary", action="store_true",
                    help="skip the secondary figures (config 2 neighbor list, config 5 energy + forces)")
     p.add_argument("--literal", action="store_true",
@@ -215,6 +216,51 @@ def cpu_baseline(edge_index, vec, x, C, mlp, mu, sigma, gout, target_s=15.0, max
     }
 
 
+def lattice_positions(n: int, L: float, g: torch.Generator) -> torch.Tensor:
+    """Jittered cubic lattice in a periodic cube of side L: uniform density with every pair
+    >= 0.9 A apart, atoms in spatial (cell) order."""
+    k = math.ceil(n ** (1 / 3))
+    sites = torch.stack(torch.meshgrid(*[torch.arange(k)] * 3, indexing="ij"), -1).reshape(-1, 3).float()
+    sites = sites[torch.randperm(sites.shape[0], generator=g)[:n]]
+    a = L / k
+    pos = (sites + 0.5) * a + (torch.rand((n, 3), generator=g) - 0.5) * (a - 0.9)
+    cell = torch.floor(pos / (L / 16)).long().clamp(max=15)
+    return pos[torch.argsort((cell[:, 2] * 16 + cell[:, 1]) * 16 + cell[:, 0], stable=True)]
+
+
+def pme_bench(dev, reps=10):
+    """BASELINE config 5's long-range term alone: 50k atoms (jittered lattice, 0.1 A^-3), neutral
+    random charges, PME alpha 0.3, 128^3, order 6, real-space cutoff 5 A (half list built inside);
+    energy + forces by autograd."""
+    from molnex_amd.molpot import PMEPotential
+
+    n = 50_000
+    L = (n / 0.1) ** (1.0 / 3.0)
+    g = torch.Generator().manual_seed(5)
+    pos = lattice_positions(n, L, g).to(dev)
+    q = torch.randn(n, generator=g) * 0.3
+    q = (q - q.mean()).to(dev)
+    box = torch.eye(3, device=dev) * L
+    pme = PMEPotential(alpha=0.3, grid=(128, 128, 128), order=6, cutoff=5.0).to(dev)
+
+    def step():
+        p = pos.clone().requires_grad_(True)
+        e = pme(p, q, box)
+        (f,) = torch.autograd.grad(e, p)
+        return e, f
+
+    for _ in range(3):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        e, f = step()
+    torch.cuda.synchronize()
+    dt = (time.perf_counter() - t0) / reps
+    return {"workload": "config 5 PME term: 50k atoms, alpha 0.3, 128^3, order 6, rc 5 A, energy + forces",
+            "ms_per_step": round(dt * 1e3, 3), "energy_finite": bool(torch.isfinite(e).item())}
+
+
 def full_step_bench(args, dev):
     """MACE (as coded: 128 x (0e..3o), 2 layers, correlation 3) on 50k atoms in a
     periodic box with 10 elements, ChargeHead charges (per-system neutral) into PME (alpha 0.3, 128^3,
@@ -227,14 +273,7 @@ def full_step_bench(args, dev):
     n = args.atoms
     L = (n / 0.1) ** (1.0 / 3.0)
     g = torch.Generator().manual_seed(args.seed)
-    # jittered lattice: uniform density with every pair >= 0.9 A apart
-    k = math.ceil(n ** (1 / 3))
-    sites = torch.stack(torch.meshgrid(*[torch.arange(k)] * 3, indexing="ij"), -1).reshape(-1, 3).float()
-    sites = sites[torch.randperm(sites.shape[0], generator=g)[:n]]
-    a = L / k
-    pos = (sites + 0.5) * a + (torch.rand((n, 3), generator=g) - 0.5) * (a - 0.9)
-    cell = torch.floor(pos / (L / 16)).long().clamp(max=15)
-    pos = pos[torch.argsort((cell[:, 2] * 16 + cell[:, 1]) * 16 + cell[:, 0], stable=True)].to(dev)
+    pos = lattice_positions(n, L, g).to(dev)
     Z = torch.randint(0, 10, (n,), generator=g).to(dev)
     box = torch.eye(3, device=dev) * L
     # periodic images enter the recomputed bond vectors through the shifts: bond = pos[i] - pos[j] - shift
@@ -388,7 +427,8 @@ def sc_bench(dev, reps=10):
 def secondary_figures(args, dev):
     sc = sc_bench(dev)
     nl = nlist_bench(dev)
-    out = {"config2_neighbor_list": nl, "config4_symmetric_contraction": sc}
+    out = {"config2_neighbor_list": nl, "config4_symmetric_contraction": sc,
+           "config5_pme_term": pme_bench(dev)}
     for key, lit in (("config5_energy_forces", False), ("config5_literal_energy_forces", True)):
         sub = argparse.Namespace(**{**vars(args), "steps": 3, "warmup": 2, "literal": lit})
         full = full_step_bench(sub, dev)
@@ -408,8 +448,11 @@ def main():
         dev = torch.device("cuda:0")
         print(json.dumps(full_step_bench(args, dev)), flush=True)
         return
-    if args.workload == "sc":
-        print(json.dumps(sc_bench(torch.device("cuda:0"))), flush=True)
+    if args.workload in ("sc", "nl", "pme"):
+        import molnex_amd.kernels  # noqa: F401
+
+        fn = {"sc": sc_bench, "nl": nlist_bench, "pme": pme_bench}[args.workload]
+        print(json.dumps(fn(torch.device("cuda:0"))), flush=True)
         return
     if not torch.cuda.is_available():
         print(json.dumps({"error": "no GPU visible"}))

@@ -130,10 +130,55 @@ __device__ __forceinline__ void pair_geo(const T* __restrict__ pos, const T* __r
     g.shift[2] = s2;
 }
 
+// Acceptance of a candidate pair, decided as the reference decides it.  A cheap test
+// (minimum image through the reciprocal box diagonal, squared distance without the fma
+// chain) settles every candidate whose squared distance is clear of cutoff^2 by a relative
+// 1e-4 -- far more than the rounding difference between the two evaluations -- and the
+// exact reference arithmetic decides the rest (the band around the cutoff and zero
+// distance).  The two image choices can differ only where a fractional coordinate is
+// within rounding of 1/2, i.e. at about half a cell height of the box, which the cell list
+// keeps above the cutoff (>= 3 cells of width >= cutoff along every periodic axis).
 template <typename T>
-__device__ __forceinline__ bool accept(const T* pos, const T* box, int i, int j, bool periodic, T cutoff) {
+struct AcceptTest {
+    T inv[3];
+    T c2lo, c2hi, c2tiny;
+};
+
+// The all-pairs fallback (a periodic axis with < 3 cells) gets no cheap test: there the
+// half-box distance can be within the cutoff.
+template <typename T>
+__device__ __forceinline__ AcceptTest<T> accept_test(const T* box, bool periodic, bool brute, T cutoff) {
+    AcceptTest<T> a;
+    for (int k = 0; k < 3; ++k) a.inv[k] = periodic ? T(1) / box[4 * k] : T(0);
+    const T c2 = cutoff * cutoff;
+    a.c2lo = brute ? T(0) : c2 * T(0.9999);
+    a.c2hi = brute ? T(INFINITY) : c2 * T(1.0001);
+    a.c2tiny = c2 * T(1e-20);
+    return a;
+}
+
+template <typename T>
+__device__ __forceinline__ bool accept(const T* pos, const T* box, int i, int j, bool periodic, T cutoff,
+                                       const AcceptTest<T>& at) {
+    const int hi = i > j ? i : j, lo = i > j ? j : i;
+    T d0 = pos[3 * hi + 0] - pos[3 * lo + 0];
+    T d1 = pos[3 * hi + 1] - pos[3 * lo + 1];
+    T d2 = pos[3 * hi + 2] - pos[3 * lo + 2];
+    if (periodic) {
+#pragma unroll
+        for (int k = 2; k >= 0; --k) {
+            const T dk = k == 2 ? d2 : (k == 1 ? d1 : d0);
+            const T s = rint_(dk * at.inv[k]);
+            d0 = d0 - s * box[3 * k + 0];
+            d1 = d1 - s * box[3 * k + 1];
+            d2 = d2 - s * box[3 * k + 2];
+        }
+    }
+    const T r2 = d0 * d0 + d1 * d1 + d2 * d2;
+    if (r2 > at.c2hi) return false;
+    if (r2 < at.c2lo && r2 > at.c2tiny) return true;
     Geo<T> g;
-    pair_geo<T>(pos, box, i > j ? i : j, i > j ? j : i, periodic, false, g);
+    pair_geo<T>(pos, box, hi, lo, periodic, false, g);
     return g.dist <= cutoff && g.dist > T(0);
 }
 
@@ -299,30 +344,49 @@ __device__ __forceinline__ void for_candidates(const T* pos, int i, int64_t n, c
         }
         return;
     }
+    // lanes 0..26 fetch the atom range of neighbour cell (dz, dy, dx) = lane in base 3
+    // (all 27 in one round trip), a wave prefix sum flattens the ranges, and the lanes
+    // then sweep the ~27 x (atoms per cell) candidates contiguously
     int c[3];
     cell_coords<T>(pos, i, g, c);
-    for (int dz = -1; dz <= 1; ++dz) {
-        int z = c[2] + dz;
-        if (g.periodic) z = (z + g.n[2]) % g.n[2];
-        else if (z < 0 || z >= g.n[2]) continue;
-        for (int dy = -1; dy <= 1; ++dy) {
-            int y = c[1] + dy;
-            if (g.periodic) y = (y + g.n[1]) % g.n[1];
-            else if (y < 0 || y >= g.n[1]) continue;
-            for (int dx = -1; dx <= 1; ++dx) {
-                int x = c[0] + dx;
-                if (g.periodic) x = (x + g.n[0]) % g.n[0];
-                else if (x < 0 || x >= g.n[0]) continue;
-                const int cid = (z * g.n[1] + y) * g.n[0] + x;
-                const int b = cell_start[cid], e = cell_start[cid + 1];
-                for (int base = b; base < e; base += kWave) {
-                    const int k = base + lane;
-                    int j = k < e ? atoms_sorted[k] : -1;
-                    if (mode == MNX_NLIST_HALF ? j >= i : j == i) j = -1;
-                    f(j);
-                }
-            }
+    int rb = 0, rlen = 0;
+    if (lane < 27) {
+        int z = c[2] + lane / 9 - 1, y = c[1] + (lane / 3) % 3 - 1, x = c[0] + lane % 3 - 1;
+        bool in = true;
+        if (g.periodic) {
+            z = (z + g.n[2]) % g.n[2];
+            y = (y + g.n[1]) % g.n[1];
+            x = (x + g.n[0]) % g.n[0];
+        } else {
+            in = z >= 0 && z < g.n[2] && y >= 0 && y < g.n[1] && x >= 0 && x < g.n[0];
         }
+        if (in) {
+            const int cid = (z * g.n[1] + y) * g.n[0] + x;
+            rb = cell_start[cid];
+            rlen = cell_start[cid + 1] - rb;
+        }
+    }
+    int incl = rlen;  // inclusive prefix sum over lanes 0..31 (lanes >= 27 add 0)
+#pragma unroll
+    for (int o = 1; o < 32; o <<= 1) {
+        const int v = __shfl_up(incl, o, kWave);
+        if (lane >= o) incl += v;
+    }
+    const int total = __shfl(incl, 26, kWave);
+    for (int base = 0; base < total; base += kWave) {
+        const int k = base + lane;
+        // range r = number of ranges whose inclusive end is <= k (branch-free, all lanes)
+        int r = 0;
+#pragma unroll
+        for (int step = 16; step > 0; step >>= 1) {
+            const int probe = __shfl(incl, r + step - 1, kWave);
+            if (r + step <= 26 && probe <= k) r += step;
+        }
+        const int start = __shfl(rb, r, kWave);
+        const int first = __shfl(incl - rlen, r, kWave);
+        int j = k < total ? atoms_sorted[start + (k - first)] : -1;
+        if (mode == MNX_NLIST_HALF ? j >= i : j == i) j = -1;
+        f(j);
     }
 }
 
@@ -336,9 +400,10 @@ __global__ void __launch_bounds__(kWave) k_count(const T* __restrict__ pos, int6
     if (i >= n) return;
     const NlGrid g = *gp;
     const bool periodic = g.periodic;
+    const AcceptTest<T> at = accept_test<T>(box, periodic, g.brute != 0, cutoff);
     int count = 0;
     for_candidates<T>(pos, i, n, g, cell_start, atoms_sorted, mode, [&](int j) {
-        const bool ok = j >= 0 && accept<T>(pos, box, i, j, periodic, cutoff);
+        const bool ok = j >= 0 && accept<T>(pos, box, i, j, periodic, cutoff, at);
         count += __popcll(__ballot(ok));
     });
     if (threadIdx.x == 0) {
@@ -386,9 +451,10 @@ __global__ void __launch_bounds__(kWave) k_emit(const T* __restrict__ pos, int64
     const NlGrid g = *gp;
     const bool periodic = g.periodic;
     const int lane = threadIdx.x;
+    const AcceptTest<T> at = accept_test<T>(box, periodic, g.brute != 0, cutoff);
     int count = 0;
     for_candidates<T>(pos, i, n, g, cell_start, atoms_sorted, mode, [&](int j) {
-        const bool ok = j >= 0 && accept<T>(pos, box, i, j, periodic, cutoff);
+        const bool ok = j >= 0 && accept<T>(pos, box, i, j, periodic, cutoff, at);
         const uint64_t m = __ballot(ok);
         const int before = __popcll(m & ((uint64_t(1) << lane) - 1));
         if (ok && count + before < kNlCap) buf[count + before] = j;
