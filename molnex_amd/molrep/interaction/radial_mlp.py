@@ -1,10 +1,19 @@
-"""Radial weight MLP (src/molrep/interaction/radial_mlp.py:38-93): [Linear -> SiLU] x L -> Linear."""
+"""Radial weight MLP (src/molrep/interaction/radial_mlp.py:38-93): [Linear -> SiLU] x L -> Linear.
+
+The last layer maps every edge to ``weight_numel`` tensor-product weights (at 2.6 M edges
+and 2944 outputs a 30.8 GB result).  For many rows it runs as row chunks of 2^18 written
+straight into one output (hipBLASLt picks a faster kernel for chunk-sized problems: 11.4 ms
+instead of 14.0 ms at that size on MI355X), with an explicit backward doing the same.
+``.mlp`` stays the reference's ``Sequential`` so parameters and their names are unchanged.
+"""
 
 from __future__ import annotations
 
 import torch
 import torch.nn as nn
 from pydantic import BaseModel, ConfigDict, Field
+
+_CHUNK = 1 << 18
 
 
 class RadialWeightMLPSpec(BaseModel):
@@ -13,6 +22,39 @@ class RadialWeightMLPSpec(BaseModel):
     hidden_dim: int = Field(..., gt=0)
     out_dim: int = Field(..., gt=0)
     num_layers: int = Field(2, ge=1)
+
+
+class _ChunkedLinear(torch.autograd.Function):
+    """``x @ W^T + b`` over row chunks of ``_CHUNK``, each GEMM writing its slice of one output."""
+
+    @staticmethod
+    def forward(ctx, x, weight, bias):
+        out = x.new_empty(x.shape[0], weight.shape[0])
+        wt = weight.t()
+        for i in range(0, x.shape[0], _CHUNK):
+            if bias is None:
+                torch.mm(x[i:i + _CHUNK], wt, out=out[i:i + _CHUNK])
+            else:
+                torch.addmm(bias, x[i:i + _CHUNK], wt, out=out[i:i + _CHUNK])
+        ctx.save_for_backward(x, weight)
+        ctx.has_bias = bias is not None
+        return out
+
+    @staticmethod
+    def backward(ctx, g):
+        x, weight = ctx.saved_tensors
+        need_x, need_w, need_b = ctx.needs_input_grad
+        gx = x.new_empty(x.shape) if need_x else None
+        gw = torch.zeros_like(weight) if need_w else None
+        g = g.contiguous()
+        for i in range(0, x.shape[0], _CHUNK):
+            gi = g[i:i + _CHUNK]
+            if need_x:
+                torch.mm(gi, weight, out=gx[i:i + _CHUNK])
+            if need_w:
+                gw.addmm_(gi.t(), x[i:i + _CHUNK])
+        gb = g.sum(0) if (need_b and ctx.has_bias) else None
+        return gx, gw, gb
 
 
 class RadialWeightMLP(nn.Module):
@@ -29,4 +71,10 @@ class RadialWeightMLP(nn.Module):
         self.mlp = nn.Sequential(*layers)
 
     def forward(self, edge_feats: torch.Tensor) -> torch.Tensor:
-        return self.mlp(edge_feats)
+        h = edge_feats
+        for layer in self.mlp[:-1]:
+            h = layer(h)
+        last = self.mlp[-1]
+        if h.dim() == 2 and h.shape[0] > _CHUNK and h.is_cuda:
+            return _ChunkedLinear.apply(h, last.weight, last.bias)
+        return last(h)

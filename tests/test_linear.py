@@ -42,3 +42,25 @@ def test_indexed_linear_gradcheck():
     ref = torch.stack([x[i] @ W[z[i]].view(6, 6) / np.sqrt(6) for i in range(11)])
     np.testing.assert_allclose(out.detach().numpy(), ref.detach().numpy(), atol=1e-12)
     assert torch.autograd.gradcheck(lambda a, w: lin(a, weight=w, weight_indices=z), (x, W))
+
+
+def test_radial_mlp_chunked_last_layer_matches_dense(monkeypatch):
+    """The row-chunked last layer (used for large edge counts) equals the plain layer,
+    values and gradients, including a ragged final chunk."""
+    import torch.nn.functional as F
+
+    from molnex_amd.molrep.interaction import radial_mlp as R
+
+    monkeypatch.setattr(R, "_CHUNK", 7)
+    torch.manual_seed(0)
+    x = torch.randn(30, 5, dtype=torch.float64, requires_grad=True)
+    W = torch.randn(11, 5, dtype=torch.float64, requires_grad=True)
+    b = torch.randn(11, dtype=torch.float64, requires_grad=True)
+    g = torch.randn(30, 11, dtype=torch.float64)
+    out = R._ChunkedLinear.apply(x, W, b)
+    ref = F.linear(x, W, b)
+    assert torch.allclose(out, ref, atol=1e-12)
+    got = torch.autograd.grad(out, (x, W, b), g)
+    exp = torch.autograd.grad(ref, (x, W, b), g)
+    for a, e in zip(got, exp):
+        assert torch.allclose(a, e, atol=1e-12)
