@@ -69,6 +69,23 @@ class Linear(nn.Module):
         return out.reshape(*shape[:-1], self.irreps_out.dim)
 
 
+def _tn_mm(a, b):
+    """``a^T @ b`` for tall ``a``, ``b`` (rows >> columns).  hipBLASLt handles the single long
+    reduction poorly (456 us for 200k x 128 x 128 on MI355X); 32 batched slabs summed
+    afterwards run in 71 us."""
+    R = a.shape[0]
+    if R < (1 << 13) or not a.is_cuda:
+        return a.t() @ b
+    nc = 32
+    rows = R // nc
+    main = nc * rows
+    out = torch.bmm(a[:main].reshape(nc, rows, a.shape[1]).transpose(1, 2),
+                    b[:main].reshape(nc, rows, b.shape[1])).sum(0)
+    if main < R:
+        out += a[main:].t() @ b[main:]
+    return out
+
+
 def _gather_rows(x, srcs, d):
     """(R*d, K) rows (node, m), columns = the channels of every source block of one irrep."""
     R = x.shape[0]
@@ -93,8 +110,9 @@ def _block_forward(x, w, plan, dim_out):
 
 def _block_backward(x, w, g, plan, need_x, need_w):
     R = x.shape[0]
-    gx = x.new_zeros(x.shape) if need_x else None
+    gx = x.new_empty(x.shape) if need_x else None
     gw = torch.zeros_like(w) if need_w else None
+    written = set()  # input blocks whose grad_x slice already holds a contribution
     for off_o, mul_o, d, srcs, fan_in in plan:
         if not srcs:
             continue
@@ -105,14 +123,33 @@ def _block_backward(x, w, g, plan, need_x, need_w):
             gxs = torch.mm(go, ws.t()) * s  # (R*d, K)
             k0 = 0
             for o, m, _ in srcs:
-                gx[:, o:o + d * m] += gxs[:, k0:k0 + m].reshape(R, d * m)
+                part = gxs[:, k0:k0 + m].reshape(R, d * m)
+                if o in written:
+                    gx[:, o:o + d * m] += part
+                else:
+                    gx[:, o:o + d * m] = part
+                    written.add(o)
                 k0 += m
         if need_w:
-            gws = torch.mm(_gather_rows(x, srcs, d).t(), go) * s  # (K, mul_o)
+            gws = _tn_mm(_gather_rows(x, srcs, d), go) * s  # (K, mul_o)
             k0 = 0
             for _, m, wo in srcs:
                 gw[wo:wo + m * mul_o] += gws[k0:k0 + m].reshape(-1)
                 k0 += m
+    if need_x:
+        in_off = {}
+        for _, _, d, srcs, _ in plan:
+            for o, m, _ in srcs:
+                in_off[o] = d * m
+        # input blocks that feed no output get zero gradient
+        covered = sorted(written)
+        pos = 0
+        for o in covered:
+            if o > pos:
+                gx[:, pos:o] = 0
+            pos = o + in_off[o]
+        if pos < x.shape[1]:
+            gx[:, pos:] = 0
     return gx, gw
 
 

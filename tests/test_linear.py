@@ -64,3 +64,14 @@ def test_radial_mlp_chunked_last_layer_matches_dense(monkeypatch):
     exp = torch.autograd.grad(ref, (x, W, b), g)
     for a, e in zip(got, exp):
         assert torch.allclose(a, e, atol=1e-12)
+
+
+def test_linear_input_irrep_without_output_gets_zero_grad():
+    from molnex_amd.molrep.interaction import Linear
+
+    torch.manual_seed(1)
+    lin = Linear("4x0e+3x1o+2x2e", "5x0e+2x2e", dtype=torch.float64)
+    x = torch.randn(6, 4 + 9 + 10, dtype=torch.float64, requires_grad=True)
+    assert torch.autograd.gradcheck(lambda a, w: lin(a, weight=w), (x, lin.weight.detach().clone().requires_grad_()))
+    (gx,) = torch.autograd.grad(lin(x).sum(), (x,))
+    assert torch.all(gx[:, 4:13] == 0) and gx[:, :4].abs().sum() > 0
