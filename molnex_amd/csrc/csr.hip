@@ -4,6 +4,12 @@
 // (atomic slot claims), then each receiver's segment is sorted by edge id so
 // the result is deterministic.  Edges whose sender or receiver lies outside
 // [0, N) are left out and counted in *d_invalid.
+//
+// Edge lists that already come grouped by receiver in ascending order (the
+// neighbor list's output, and the reference's NeighborList task before it
+// appends the reversed edges) are detected on the device while counting: then
+// the CSR is the identity permutation and the placement and segment sort are
+// skipped, with no host synchronisation.
 
 #include "common.h"
 #include "scan.h"
@@ -16,6 +22,7 @@ struct CsrWs {
     int32_t* fill;
     int32_t* tiles;
     int32_t* invalid;
+    int32_t* unsorted;  // 0: all edges valid and grouped by receiver in ascending order
 };
 
 CsrWs carve_csr(void* base, size_t bytes, int64_t N, size_t* used) {
@@ -24,7 +31,8 @@ CsrWs carve_csr(void* base, size_t bytes, int64_t N, size_t* used) {
     w.counts = ws.take<int32_t>(N + 1);
     w.fill = ws.take<int32_t>(N + 1);
     w.tiles = ws.take<int32_t>(scan_workspace_elems(N + 1));
-    w.invalid = ws.take<int32_t>(1);
+    w.invalid = ws.take<int32_t>(2);  // [0] invalid count, [1] unsorted flag (cleared together)
+    w.unsorted = w.invalid + 1;
     *used = ws.used;
     return w;
 }
@@ -34,29 +42,44 @@ __device__ __forceinline__ bool edge_ok(const int64_t* ei, int64_t e, int64_t N)
     return s >= 0 && s < N && r >= 0 && r < N;
 }
 
+__global__ void k_fill_i32(int32_t* __restrict__ p, int64_t n) {
+    const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i < n) p[i] = 0;
+}
+
 __global__ void k_count_recv(const int64_t* __restrict__ ei, int64_t E, int64_t N, int32_t* __restrict__ counts,
-                             int32_t* __restrict__ invalid) {
+                             int32_t* __restrict__ invalid, int32_t* __restrict__ unsorted) {
     const int64_t e = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
     if (e >= E) return;
     if (!edge_ok(ei, e, N)) {
         atomicAdd(invalid, 1);
+        atomicOr(unsorted, 1);
         return;
     }
+    if (e > 0 && ei[2 * e + 1] < ei[2 * e - 1]) atomicOr(unsorted, 1);
     atomicAdd(&counts[ei[2 * e + 1]], 1);
 }
 
 __global__ void k_place_edges(const int64_t* __restrict__ ei, int64_t E, int64_t N, const int32_t* __restrict__ row_ptr,
-                              int32_t* __restrict__ fill, int32_t* __restrict__ perm) {
+                              int32_t* __restrict__ fill, int32_t* __restrict__ perm, int32_t* __restrict__ snd,
+                              const int32_t* __restrict__ unsorted) {
     const int64_t e = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
-    if (e >= E || !edge_ok(ei, e, N)) return;
+    if (e >= E) return;
+    if (*unsorted == 0) {  // grouped by receiver, all valid: CSR slot e holds edge e
+        perm[e] = int32_t(e);
+        if (snd) snd[e] = int32_t(ei[2 * e]);
+        return;
+    }
+    if (!edge_ok(ei, e, N)) return;
     const int64_t r = ei[2 * e + 1];
     perm[row_ptr[r] + atomicAdd(&fill[r], 1)] = int32_t(e);
 }
 
 __global__ void k_sort_segments(const int64_t* __restrict__ ei, int64_t N, const int32_t* __restrict__ row_ptr,
-                                int32_t* __restrict__ perm, int32_t* __restrict__ snd) {
+                                int32_t* __restrict__ perm, int32_t* __restrict__ snd,
+                                const int32_t* __restrict__ unsorted) {
     const int64_t r = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
-    if (r >= N) return;
+    if (r >= N || *unsorted == 0) return;
     const int b = row_ptr[r], e = row_ptr[r + 1];
     for (int k = b + 1; k < e; ++k) {
         const int v = perm[k];
@@ -97,13 +120,17 @@ int mnx_csr_build(const int64_t* edge_index, int64_t E, int64_t N, int32_t* row_
     size_t need = 0;
     CsrWs w = carve_csr(workspace, ws_bytes, N, &need);
     if (!workspace || ws_bytes < need) return set_error(MNX_ERR_WORKSPACE, "workspace %zu < %zu bytes", ws_bytes, need);
-    MNX_HIP_TRY(hipMemsetAsync(w.counts, 0, sizeof(int32_t) * (N + 1), stream));
-    MNX_HIP_TRY(hipMemsetAsync(w.fill, 0, sizeof(int32_t) * (N + 1), stream));
-    MNX_HIP_TRY(hipMemsetAsync(w.invalid, 0, sizeof(int32_t), stream));
     const int tb = 256;
+    // clear counters with fill kernels (no memset nodes if a caller captures this into a graph)
+    for (int32_t* p : {w.counts, w.fill}) {
+        hipLaunchKernelGGL(k_fill_i32, dim3(ceil_div(N + 1, tb)), dim3(tb), 0, stream, p, N + 1);
+        MNX_CHECK_LAUNCH();
+    }
+    hipLaunchKernelGGL(k_fill_i32, dim3(1), dim3(2), 0, stream, w.invalid, int64_t(2));  // invalid, unsorted
+    MNX_CHECK_LAUNCH();
     if (E > 0) {
         hipLaunchKernelGGL(k_count_recv, dim3(ceil_div(E, tb)), dim3(tb), 0, stream, edge_index, E, N, w.counts,
-                           w.invalid);
+                           w.invalid, w.unsorted);
         MNX_CHECK_LAUNCH();
     }
     // row_ptr[0..N] = exclusive scan of counts[0..N] (counts[N] == 0, so row_ptr[N] = valid edges)
@@ -111,10 +138,10 @@ int mnx_csr_build(const int64_t* edge_index, int64_t E, int64_t N, int32_t* row_
     if (rc) return rc;
     if (E > 0 && N > 0) {
         hipLaunchKernelGGL(k_place_edges, dim3(ceil_div(E, tb)), dim3(tb), 0, stream, edge_index, E, N, row_ptr,
-                           w.fill, perm);
+                           w.fill, perm, senders_sorted, w.unsorted);
         MNX_CHECK_LAUNCH();
         hipLaunchKernelGGL(k_sort_segments, dim3(ceil_div(N, tb)), dim3(tb), 0, stream, edge_index, N, row_ptr,
-                           perm, senders_sorted);
+                           perm, senders_sorted, w.unsorted);
         MNX_CHECK_LAUNCH();
     }
     if (d_invalid) {
