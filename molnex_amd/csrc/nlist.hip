@@ -29,6 +29,8 @@ namespace mnx {
 namespace {
 
 constexpr int kNlCap = 4096;  // max neighbours of one atom (LDS list per wave)
+constexpr int64_t kNlBlocks = 16384;  // grid-stride launches of the count / emit kernels
+constexpr int kCellParts = 4;          // wavefronts per cell (each takes every 4th atom of it)
 constexpr float kCellMargin = 1.0001f;
 
 struct NlGrid {
@@ -97,13 +99,10 @@ __device__ __forceinline__ double rint_(double a) { return rint(a); }
 __device__ __forceinline__ float sqrt_(float a) { return sqrtf(a); }
 __device__ __forceinline__ double sqrt_(double a) { return sqrt(a); }
 
-// Geometry of the pair (hi, lo) with hi > lo, in the reference's orientation.
+// Minimum image and distance of the difference vector d, the reference's arithmetic.
 template <typename T>
-__device__ __forceinline__ void pair_geo(const T* __restrict__ pos, const T* __restrict__ box, int hi, int lo,
-                                         bool periodic, bool want_shift, Geo<T>& g) {
-    T d0 = pos[3 * hi + 0] - pos[3 * lo + 0];
-    T d1 = pos[3 * hi + 1] - pos[3 * lo + 1];
-    T d2 = pos[3 * hi + 2] - pos[3 * lo + 2];
+__device__ __forceinline__ void geo_from_d(const T* __restrict__ box, T d0, T d1, T d2, bool periodic, bool want_shift,
+                                           Geo<T>& g) {
     T s0 = 0, s1 = 0, s2 = 0;
     if (periodic) {
 #pragma unroll
@@ -128,6 +127,14 @@ __device__ __forceinline__ void pair_geo(const T* __restrict__ pos, const T* __r
     g.shift[0] = s0;
     g.shift[1] = s1;
     g.shift[2] = s2;
+}
+
+// Geometry of the pair (hi, lo) with hi > lo, in the reference's orientation.
+template <typename T>
+__device__ __forceinline__ void pair_geo(const T* __restrict__ pos, const T* __restrict__ box, int hi, int lo,
+                                         bool periodic, bool want_shift, Geo<T>& g) {
+    geo_from_d<T>(box, pos[3 * hi + 0] - pos[3 * lo + 0], pos[3 * hi + 1] - pos[3 * lo + 1],
+                  pos[3 * hi + 2] - pos[3 * lo + 2], periodic, want_shift, g);
 }
 
 // Acceptance of a candidate pair, decided as the reference decides it.  A cheap test
@@ -157,13 +164,13 @@ __device__ __forceinline__ AcceptTest<T> accept_test(const T* box, bool periodic
     return a;
 }
 
+// Decision for the pair at positions a, b.  It does not depend on the order: a - b is the
+// exact negation of b - a, and the minimum image and the norm are symmetric in sign.
 template <typename T>
-__device__ __forceinline__ bool accept(const T* pos, const T* box, int i, int j, bool periodic, T cutoff,
-                                       const AcceptTest<T>& at) {
-    const int hi = i > j ? i : j, lo = i > j ? j : i;
-    T d0 = pos[3 * hi + 0] - pos[3 * lo + 0];
-    T d1 = pos[3 * hi + 1] - pos[3 * lo + 1];
-    T d2 = pos[3 * hi + 2] - pos[3 * lo + 2];
+__device__ __forceinline__ bool accept_xyz(const T* box, T ax, T ay, T az, T bx, T by, T bz, bool periodic, T cutoff,
+                                           const AcceptTest<T>& at) {
+    T d0 = ax - bx, d1 = ay - by, d2 = az - bz;
+    const T e0 = d0, e1 = d1, e2 = d2;
     if (periodic) {
 #pragma unroll
         for (int k = 2; k >= 0; --k) {
@@ -178,8 +185,15 @@ __device__ __forceinline__ bool accept(const T* pos, const T* box, int i, int j,
     if (r2 > at.c2hi) return false;
     if (r2 < at.c2lo && r2 > at.c2tiny) return true;
     Geo<T> g;
-    pair_geo<T>(pos, box, hi, lo, periodic, false, g);
+    geo_from_d<T>(box, e0, e1, e2, periodic, false, g);
     return g.dist <= cutoff && g.dist > T(0);
+}
+
+template <typename T>
+__device__ __forceinline__ bool accept(const T* pos, const T* box, int i, int j, bool periodic, T cutoff,
+                                       const AcceptTest<T>& at) {
+    return accept_xyz<T>(box, pos[3 * i], pos[3 * i + 1], pos[3 * i + 2], pos[3 * j], pos[3 * j + 1], pos[3 * j + 2],
+                         periodic, cutoff, at);
 }
 
 // ---------------------------------------------------------------------------
@@ -330,6 +344,56 @@ __global__ void k_sort_cells(const NlGrid* __restrict__ gp, const int32_t* __res
 // Candidate scan: one wavefront per atom
 // ---------------------------------------------------------------------------
 
+// Atom ranges of the 27 neighbour cells of cell (cx, cy, cz), flattened: lanes 0..26 hold
+// (begin, length) of neighbour cell (dz, dy, dx) = lane in base 3, fetched in one round trip,
+// and `incl` is the inclusive prefix sum of the lengths over lanes; `total` candidates in all.
+struct CellRanges {
+    int rb, rlen, incl, total;
+};
+
+__device__ __forceinline__ CellRanges cell_ranges(const NlGrid& g, int cx, int cy, int cz,
+                                                  const int32_t* __restrict__ cell_start, int lane) {
+    CellRanges cr{0, 0, 0, 0};
+    if (lane < 27) {
+        int z = cz + lane / 9 - 1, y = cy + (lane / 3) % 3 - 1, x = cx + lane % 3 - 1;
+        bool in = true;
+        if (g.periodic) {
+            z = (z + g.n[2]) % g.n[2];
+            y = (y + g.n[1]) % g.n[1];
+            x = (x + g.n[0]) % g.n[0];
+        } else {
+            in = z >= 0 && z < g.n[2] && y >= 0 && y < g.n[1] && x >= 0 && x < g.n[0];
+        }
+        if (in) {
+            const int cid = (z * g.n[1] + y) * g.n[0] + x;
+            cr.rb = cell_start[cid];
+            cr.rlen = cell_start[cid + 1] - cr.rb;
+        }
+    }
+    int incl = cr.rlen;  // lanes >= 27 add 0
+#pragma unroll
+    for (int o = 1; o < 32; o <<= 1) {
+        const int v = __shfl_up(incl, o, kWave);
+        if (lane >= o) incl += v;
+    }
+    cr.incl = incl;
+    cr.total = __shfl(incl, 26, kWave);
+    return cr;
+}
+
+// Candidate number k of the flattened ranges (-1 past the end); every lane must call it.
+__device__ __forceinline__ int cell_candidate(const CellRanges& cr, int k, const int32_t* __restrict__ atoms_sorted) {
+    int r = 0;  // number of ranges that end at or before k (branch-free search over 27 entries)
+#pragma unroll
+    for (int step = 16; step > 0; step >>= 1) {
+        const int probe = __shfl(cr.incl, r + step - 1, kWave);
+        if (r + step <= 26 && probe <= k) r += step;
+    }
+    const int start = __shfl(cr.rb, r, kWave);
+    const int first = __shfl(cr.incl - cr.rlen, r, kWave);
+    return k < cr.total ? atoms_sorted[start + (k - first)] : -1;
+}
+
 // Calls f(j) for every candidate j of atom i (each j at most once), lanes in parallel.
 template <typename T, typename F>
 __device__ __forceinline__ void for_candidates(const T* pos, int i, int64_t n, const NlGrid& g,
@@ -344,71 +408,38 @@ __device__ __forceinline__ void for_candidates(const T* pos, int i, int64_t n, c
         }
         return;
     }
-    // lanes 0..26 fetch the atom range of neighbour cell (dz, dy, dx) = lane in base 3
-    // (all 27 in one round trip), a wave prefix sum flattens the ranges, and the lanes
-    // then sweep the ~27 x (atoms per cell) candidates contiguously
     int c[3];
     cell_coords<T>(pos, i, g, c);
-    int rb = 0, rlen = 0;
-    if (lane < 27) {
-        int z = c[2] + lane / 9 - 1, y = c[1] + (lane / 3) % 3 - 1, x = c[0] + lane % 3 - 1;
-        bool in = true;
-        if (g.periodic) {
-            z = (z + g.n[2]) % g.n[2];
-            y = (y + g.n[1]) % g.n[1];
-            x = (x + g.n[0]) % g.n[0];
-        } else {
-            in = z >= 0 && z < g.n[2] && y >= 0 && y < g.n[1] && x >= 0 && x < g.n[0];
-        }
-        if (in) {
-            const int cid = (z * g.n[1] + y) * g.n[0] + x;
-            rb = cell_start[cid];
-            rlen = cell_start[cid + 1] - rb;
-        }
-    }
-    int incl = rlen;  // inclusive prefix sum over lanes 0..31 (lanes >= 27 add 0)
-#pragma unroll
-    for (int o = 1; o < 32; o <<= 1) {
-        const int v = __shfl_up(incl, o, kWave);
-        if (lane >= o) incl += v;
-    }
-    const int total = __shfl(incl, 26, kWave);
-    for (int base = 0; base < total; base += kWave) {
-        const int k = base + lane;
-        // range r = number of ranges whose inclusive end is <= k (branch-free, all lanes)
-        int r = 0;
-#pragma unroll
-        for (int step = 16; step > 0; step >>= 1) {
-            const int probe = __shfl(incl, r + step - 1, kWave);
-            if (r + step <= 26 && probe <= k) r += step;
-        }
-        const int start = __shfl(rb, r, kWave);
-        const int first = __shfl(incl - rlen, r, kWave);
-        int j = k < total ? atoms_sorted[start + (k - first)] : -1;
+    const CellRanges cr = cell_ranges(g, c[0], c[1], c[2], cell_start, lane);
+    for (int base = 0; base < cr.total; base += kWave) {
+        int j = cell_candidate(cr, base + lane, atoms_sorted);
         if (mode == MNX_NLIST_HALF ? j >= i : j == i) j = -1;
         f(j);
     }
 }
 
+// All-pairs fallback (a periodic axis with fewer than 3 cells): one wavefront per atom,
+// grid-stride; cell grids are handled by k_count_cells / k_emit_cells.
 template <typename T>
 __global__ void __launch_bounds__(kWave) k_count(const T* __restrict__ pos, int64_t n, const T* __restrict__ box,
                                                  T cutoff, int mode, NlGrid* __restrict__ gp,
                                                  const int32_t* __restrict__ cell_start,
                                                  const int32_t* __restrict__ atoms_sorted,
                                                  int32_t* __restrict__ counts) {
-    const int i = blockIdx.x;
-    if (i >= n) return;
     const NlGrid g = *gp;
+    if (!g.brute) return;
     const bool periodic = g.periodic;
-    const AcceptTest<T> at = accept_test<T>(box, periodic, g.brute != 0, cutoff);
-    int count = 0;
-    for_candidates<T>(pos, i, n, g, cell_start, atoms_sorted, mode, [&](int j) {
-        const bool ok = j >= 0 && accept<T>(pos, box, i, j, periodic, cutoff, at);
-        count += __popcll(__ballot(ok));
-    });
-    if (threadIdx.x == 0) {
-        counts[i] = count;
-        if (count > kNlCap) atomicExch(&gp->overflow, 1);
+    const AcceptTest<T> at = accept_test<T>(box, periodic, true, cutoff);
+    for (int i = blockIdx.x; i < n; i += gridDim.x) {
+        int count = 0;
+        for_candidates<T>(pos, i, n, g, cell_start, atoms_sorted, mode, [&](int j) {
+            const bool ok = j >= 0 && accept<T>(pos, box, i, j, periodic, cutoff, at);
+            count += __popcll(__ballot(ok));
+        });
+        if (threadIdx.x == 0) {
+            counts[i] = count;
+            if (count > kNlCap) atomicExch(&gp->overflow, 1);
+        }
     }
 }
 
@@ -436,6 +467,30 @@ __device__ void lds_sort(int32_t* buf, int len) {
     }
 }
 
+// Writes pair (i, j) at `slot` with the reference geometry (row = the larger index).
+template <typename T>
+__device__ __forceinline__ void write_pair(const T* __restrict__ pos, const T* __restrict__ box, bool periodic, int i,
+                                           int j, int64_t slot, int32_t* __restrict__ idx_i,
+                                           int32_t* __restrict__ idx_j, T* __restrict__ deltas,
+                                           T* __restrict__ dist, T* __restrict__ shifts) {
+    Geo<T> gg;
+    const bool flip = i < j;
+    pair_geo<T>(pos, box, flip ? j : i, flip ? i : j, periodic, shifts != nullptr, gg);
+    if (idx_i) idx_i[slot] = i;
+    if (idx_j) idx_j[slot] = j;
+    if (deltas) {
+        deltas[3 * slot + 0] = flip ? -gg.d[0] : gg.d[0];
+        deltas[3 * slot + 1] = flip ? -gg.d[1] : gg.d[1];
+        deltas[3 * slot + 2] = flip ? -gg.d[2] : gg.d[2];
+    }
+    if (dist) dist[slot] = gg.dist;
+    if (shifts) {
+        shifts[3 * slot + 0] = flip ? -gg.shift[0] : gg.shift[0];
+        shifts[3 * slot + 1] = flip ? -gg.shift[1] : gg.shift[1];
+        shifts[3 * slot + 2] = flip ? -gg.shift[2] : gg.shift[2];
+    }
+}
+
 template <typename T>
 __global__ void __launch_bounds__(kWave) k_emit(const T* __restrict__ pos, int64_t n, const T* __restrict__ box,
                                                 T cutoff, int mode, int layout, const NlGrid* __restrict__ gp,
@@ -446,43 +501,194 @@ __global__ void __launch_bounds__(kWave) k_emit(const T* __restrict__ pos, int64
                                                 T* __restrict__ deltas, T* __restrict__ dist,
                                                 T* __restrict__ shifts) {
     __shared__ int32_t buf[kNlCap];
-    const int i = blockIdx.x;
-    if (i >= n) return;
     const NlGrid g = *gp;
+    if (!g.brute) return;
     const bool periodic = g.periodic;
     const int lane = threadIdx.x;
-    const AcceptTest<T> at = accept_test<T>(box, periodic, g.brute != 0, cutoff);
-    int count = 0;
-    for_candidates<T>(pos, i, n, g, cell_start, atoms_sorted, mode, [&](int j) {
-        const bool ok = j >= 0 && accept<T>(pos, box, i, j, periodic, cutoff, at);
-        const uint64_t m = __ballot(ok);
-        const int before = __popcll(m & ((uint64_t(1) << lane) - 1));
-        if (ok && count + before < kNlCap) buf[count + before] = j;
-        count += __popcll(m);
-    });
-    if (count > kNlCap) count = kNlCap;  // flagged by k_count; host reports the error
-    __syncthreads();
-    lds_sort(buf, count);
-    const int64_t base = layout == MNX_NLIST_TRIANGULAR ? 0 : offsets[i];
-    for (int k = lane; k < count; k += kWave) {
-        const int j = buf[k];
-        const int64_t slot = layout == MNX_NLIST_TRIANGULAR ? int64_t(i) * (i - 1) / 2 + j : base + k;
-        if (slot >= capacity) continue;
-        Geo<T> gg;
-        const bool flip = i < j;
-        pair_geo<T>(pos, box, flip ? j : i, flip ? i : j, periodic, shifts != nullptr, gg);
-        if (idx_i) idx_i[slot] = i;
-        if (idx_j) idx_j[slot] = j;
-        if (deltas) {
-            deltas[3 * slot + 0] = flip ? -gg.d[0] : gg.d[0];
-            deltas[3 * slot + 1] = flip ? -gg.d[1] : gg.d[1];
-            deltas[3 * slot + 2] = flip ? -gg.d[2] : gg.d[2];
+    const AcceptTest<T> at = accept_test<T>(box, periodic, true, cutoff);
+    for (int i = blockIdx.x; i < n; i += gridDim.x) {
+        int count = 0;
+        __syncthreads();  // buf is reused across atoms
+        for_candidates<T>(pos, i, n, g, cell_start, atoms_sorted, mode, [&](int j) {
+            const bool ok = j >= 0 && accept<T>(pos, box, i, j, periodic, cutoff, at);
+            const uint64_t m = __ballot(ok);
+            const int before = __popcll(m & ((uint64_t(1) << lane) - 1));
+            if (ok && count + before < kNlCap) buf[count + before] = j;
+            count += __popcll(m);
+        });
+        if (count > kNlCap) count = kNlCap;  // flagged by k_count; host reports the error
+        __syncthreads();
+        lds_sort(buf, count);
+        const int64_t base = layout == MNX_NLIST_TRIANGULAR ? 0 : offsets[i];
+        for (int k = lane; k < count; k += kWave) {
+            const int j = buf[k];
+            const int64_t slot = layout == MNX_NLIST_TRIANGULAR ? int64_t(i) * (i - 1) / 2 + j : base + k;
+            if (slot < capacity) write_pair<T>(pos, box, periodic, i, j, slot, idx_i, idx_j, deltas, dist, shifts);
         }
-        if (dist) dist[slot] = gg.dist;
-        if (shifts) {
-            shifts[3 * slot + 0] = flip ? -gg.shift[0] : gg.shift[0];
-            shifts[3 * slot + 1] = flip ? -gg.shift[1] : gg.shift[1];
-            shifts[3 * slot + 2] = flip ? -gg.shift[2] : gg.shift[2];
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Cell grids: kCellParts wavefronts per cell, each taking every kCellParts-th atom of
+// the cell as a "centre".  All centres share the 27 neighbour cells, so each
+// candidate position is loaded once per wavefront and tested against all of its
+// centres (whose coordinates are wave-uniform).  Grid-stride over (cell, part); the
+// all-pairs fallback (k_count / k_emit) handles brute-force grids.
+// ---------------------------------------------------------------------------
+
+__device__ __forceinline__ int64_t cell_of_block(int64_t c, const NlGrid& g, int* cx, int* cy, int* cz) {
+    *cx = int(c % g.n[0]);
+    *cy = int((c / g.n[0]) % g.n[1]);
+    *cz = int(c / (int64_t(g.n[0]) * g.n[1]));
+    return c;
+}
+
+template <typename T>
+__global__ void __launch_bounds__(kWave) k_count_cells(const T* __restrict__ pos, const T* __restrict__ box, T cutoff,
+                                                       int mode, NlGrid* __restrict__ gp,
+                                                       const int32_t* __restrict__ cell_start,
+                                                       const int32_t* __restrict__ atoms_sorted,
+                                                       int32_t* __restrict__ counts) {
+    const NlGrid g = *gp;
+    if (g.brute) return;
+    const int lane = threadIdx.x;
+    const bool periodic = g.periodic;
+    const AcceptTest<T> at = accept_test<T>(box, periodic, false, cutoff);
+    for (int64_t v = blockIdx.x; v < g.ncells * kCellParts; v += gridDim.x) {
+        const int64_t c = v / kCellParts;
+        const int part = int(v - c * kCellParts);
+        const int cb = cell_start[c], ce = cell_start[c + 1];
+        const int ncent = (ce - cb - part + kCellParts - 1) / kCellParts;  // centres part, part + P, ...
+        if (ncent <= 0) continue;
+        int cx, cy, cz;
+        cell_of_block(c, g, &cx, &cy, &cz);
+        const CellRanges cr = cell_ranges(g, cx, cy, cz, cell_start, lane);
+        for (int q0 = 0; q0 < ncent; q0 += kWave) {
+            const int nq = ncent - q0 < kWave ? ncent - q0 : kWave;
+            const int my_i = lane < nq ? atoms_sorted[cb + part + (q0 + lane) * kCellParts] : -1;
+            int my_count = 0;
+            for (int base = 0; base < cr.total; base += kWave) {
+                const int j = cell_candidate(cr, base + lane, atoms_sorted);
+                const T jx = j >= 0 ? pos[3 * j] : T(0), jy = j >= 0 ? pos[3 * j + 1] : T(0),
+                        jz = j >= 0 ? pos[3 * j + 2] : T(0);
+                for (int q = 0; q < nq; ++q) {
+                    const int i = __builtin_amdgcn_readfirstlane(__shfl(my_i, q, kWave));
+                    const bool keep = j >= 0 && (mode == MNX_NLIST_HALF ? j < i : j != i);
+                    const bool ok = keep && accept_xyz<T>(box, pos[3 * i], pos[3 * i + 1], pos[3 * i + 2], jx, jy, jz,
+                                                          periodic, cutoff, at);
+                    const int cnt = __popcll(__ballot(ok));
+                    if (lane == q) my_count += cnt;
+                }
+            }
+            if (lane < nq) {
+                counts[my_i] = my_count;
+                if (my_count > kNlCap) atomicExch(&gp->overflow, 1);
+            }
+        }
+    }
+}
+
+template <typename T>
+__global__ void __launch_bounds__(kWave) k_emit_cells(const T* __restrict__ pos, const T* __restrict__ box, T cutoff,
+                                                      int mode, int layout, const NlGrid* __restrict__ gp,
+                                                      const int32_t* __restrict__ cell_start,
+                                                      const int32_t* __restrict__ atoms_sorted,
+                                                      const int32_t* __restrict__ counts,
+                                                      const int64_t* __restrict__ offsets, int64_t capacity,
+                                                      int32_t* __restrict__ idx_i, int32_t* __restrict__ idx_j,
+                                                      T* __restrict__ deltas, T* __restrict__ dist,
+                                                      T* __restrict__ shifts) {
+    __shared__ int32_t buf[kNlCap];  // accepted j of a batch of centres, one segment per centre
+    const NlGrid g = *gp;
+    if (g.brute) return;
+    const int lane = threadIdx.x;
+    const bool periodic = g.periodic;
+    const AcceptTest<T> at = accept_test<T>(box, periodic, false, cutoff);
+    for (int64_t v = blockIdx.x; v < g.ncells * kCellParts; v += gridDim.x) {
+        const int64_t c = v / kCellParts;
+        const int part = int(v - c * kCellParts);
+        const int cb = cell_start[c], ce = cell_start[c + 1];
+        const int ncent = (ce - cb - part + kCellParts - 1) / kCellParts;  // centres part, part + P, ...
+        if (ncent <= 0) continue;
+        int cx, cy, cz;
+        cell_of_block(c, g, &cx, &cy, &cz);
+        const CellRanges cr = cell_ranges(g, cx, cy, cz, cell_start, lane);
+        for (int q0 = 0; q0 < ncent;) {
+            // a batch of centres whose segments (counts, capped at kNlCap) fit the buffer
+            const int avail = ncent - q0 < kWave ? ncent - q0 : kWave;
+            const int my_i = lane < avail ? atoms_sorted[cb + part + (q0 + lane) * kCellParts] : -1;
+            const int my_cnt = lane < avail ? min(counts[my_i], kNlCap) : 0;
+            int incl = my_cnt;
+#pragma unroll
+            for (int o = 1; o < kWave; o <<= 1) {
+                const int v = __shfl_up(incl, o, kWave);
+                if (lane >= o) incl += v;
+            }
+            int nq = __popcll(__ballot(lane < avail && incl <= kNlCap));  // incl is non-decreasing
+            if (nq == 0) nq = 1;
+            const int my_off = incl - my_cnt;
+            int my_fill = 0;
+            __syncthreads();  // previous batch's segments fully read
+            for (int base = 0; base < cr.total; base += kWave) {
+                const int j = cell_candidate(cr, base + lane, atoms_sorted);
+                const T jx = j >= 0 ? pos[3 * j] : T(0), jy = j >= 0 ? pos[3 * j + 1] : T(0),
+                        jz = j >= 0 ? pos[3 * j + 2] : T(0);
+                for (int q = 0; q < nq; ++q) {
+                    const int i = __builtin_amdgcn_readfirstlane(__shfl(my_i, q, kWave));
+                    const int seg = __builtin_amdgcn_readfirstlane(__shfl(my_off, q, kWave));
+                    const int cap = __builtin_amdgcn_readfirstlane(__shfl(my_cnt, q, kWave));
+                    const int fill = __builtin_amdgcn_readfirstlane(__shfl(my_fill, q, kWave));
+                    const bool keep = j >= 0 && (mode == MNX_NLIST_HALF ? j < i : j != i);
+                    const bool ok = keep && accept_xyz<T>(box, pos[3 * i], pos[3 * i + 1], pos[3 * i + 2], jx, jy, jz,
+                                                          periodic, cutoff, at);
+                    const uint64_t m = __ballot(ok);
+                    const int before = __popcll(m & ((uint64_t(1) << lane) - 1));
+                    if (ok && fill + before < cap) buf[seg + fill + before] = j;
+                    if (lane == q) my_fill += __popcll(m);
+                }
+            }
+            __syncthreads();
+            // each centre's segment, ranked by j (the j are distinct), written at its offset
+            for (int q = 0; q < nq; ++q) {
+                const int i = __builtin_amdgcn_readfirstlane(__shfl(my_i, q, kWave));
+                const int seg = __builtin_amdgcn_readfirstlane(__shfl(my_off, q, kWave));
+                // entries actually written (equal to the count pass's unless it overflowed)
+                const int cap = __builtin_amdgcn_readfirstlane(__shfl(my_cnt, q, kWave));
+                const int got = __builtin_amdgcn_readfirstlane(__shfl(my_fill, q, kWave));
+                const int len = got < cap ? got : cap;
+                const int64_t obase = layout == MNX_NLIST_TRIANGULAR ? 0 : offsets[i];
+                if (len <= kWave) {
+                    // one element per lane, bitonic-sorted across the wavefront, written in order
+                    int v = lane < len ? buf[seg + lane] : INT32_MAX;
+#pragma unroll
+                    for (int size = 2; size <= kWave; size <<= 1) {
+#pragma unroll
+                        for (int stride = size >> 1; stride > 0; stride >>= 1) {
+                            const int other = __shfl_xor(v, stride, kWave);
+                            const bool up = (lane & size) == 0 || size == kWave;
+                            const bool low = (lane & stride) == 0;
+                            v = (low == up) ? min(v, other) : max(v, other);
+                        }
+                    }
+                    if (lane < len) {
+                        const int64_t slot =
+                            layout == MNX_NLIST_TRIANGULAR ? int64_t(i) * (i - 1) / 2 + v : obase + lane;
+                        if (slot < capacity) write_pair<T>(pos, box, periodic, i, v, slot, idx_i, idx_j, deltas, dist,
+                                                           shifts);
+                    }
+                } else {
+                    for (int k = lane; k < len; k += kWave) {
+                        const int v = buf[seg + k];
+                        int rank = 0;
+                        for (int t = 0; t < len; ++t) rank += buf[seg + t] < v ? 1 : 0;
+                        const int64_t slot =
+                            layout == MNX_NLIST_TRIANGULAR ? int64_t(i) * (i - 1) / 2 + v : obase + rank;
+                        if (slot < capacity) write_pair<T>(pos, box, periodic, i, v, slot, idx_i, idx_j, deltas, dist,
+                                                           shifts);
+                    }
+                }
+            }
+            q0 += nq;
         }
     }
 }
@@ -543,7 +749,11 @@ int nlist_count(const T* pos, int64_t n, double cutoff, const T* box, int mode, 
         hipLaunchKernelGGL(k_sort_cells, dim3(ceil_div(w.max_cells, tb)), dim3(tb), 0, stream, w.grid,
                            w.cell_start, w.atoms_sorted);
         MNX_CHECK_LAUNCH();
-        hipLaunchKernelGGL((k_count<T>), dim3(n), dim3(kWave), 0, stream, pos, n, box, T(cutoff), mode, w.grid,
+        const unsigned blocks = unsigned(std::min<int64_t>(std::max<int64_t>(n, w.max_cells * kCellParts), kNlBlocks));
+        hipLaunchKernelGGL((k_count_cells<T>), dim3(blocks), dim3(kWave), 0, stream, pos, box, T(cutoff), mode,
+                           w.grid, w.cell_start, w.atoms_sorted, w.counts);
+        MNX_CHECK_LAUNCH();
+        hipLaunchKernelGGL((k_count<T>), dim3(blocks), dim3(kWave), 0, stream, pos, n, box, T(cutoff), mode, w.grid,
                            w.cell_start, w.atoms_sorted, w.counts);
         MNX_CHECK_LAUNCH();
     }
@@ -580,7 +790,12 @@ int nlist_emit(const T* pos, int64_t n, double cutoff, const T* box, int mode, i
         MNX_CHECK_LAUNCH();
     }
     if (n > 0) {
-        hipLaunchKernelGGL((k_emit<T>), dim3(n), dim3(kWave), 0, stream, pos, n, box, T(cutoff), mode, layout,
+        const unsigned blocks = unsigned(std::min<int64_t>(std::max<int64_t>(n, w.max_cells * kCellParts), kNlBlocks));
+        hipLaunchKernelGGL((k_emit_cells<T>), dim3(blocks), dim3(kWave), 0, stream, pos, box, T(cutoff), mode, layout,
+                           w.grid, w.cell_start, w.atoms_sorted, w.counts, w.offsets, capacity, idx_i, idx_j, deltas,
+                           dist, shifts);
+        MNX_CHECK_LAUNCH();
+        hipLaunchKernelGGL((k_emit<T>), dim3(blocks), dim3(kWave), 0, stream, pos, n, box, T(cutoff), mode, layout,
                            w.grid, w.cell_start, w.atoms_sorted, w.offsets, capacity, idx_i, idx_j, deltas, dist,
                            shifts);
         MNX_CHECK_LAUNCH();
