@@ -174,13 +174,16 @@ int mnx_tp_bwd_sender_f32(int32_t config, int32_t channels, const float* x, cons
 /*   spread -> rfftn -> convolve (energy)   and   irfftn(norm=forward) -> gather */
 /* Spline orders 3..8 (the reference CUDA path: 4, 5).                        */
 /* ------------------------------------------------------------------------ */
-/* grid[gx][gy][gz] (overwritten) = sum_atoms q sqrt(coulomb) B(x) B(y) B(z)  (pme_cpu.cpp:240-256) */
+/* grid[gx][gy][gz] (overwritten) = sum_atoms q sqrt(coulomb) B(x) B(y) B(z)  (pme_cpu.cpp:240-256).
+ * Computed as a gather over 8^3-point mesh bricks with atoms binned by brick: no atomics, every
+ * point written once, a fixed summation order (deterministic). */
+size_t mnx_pme_spread_workspace_bytes(int64_t num_atoms, int32_t gx, int32_t gy, int32_t gz);
 int mnx_pme_spread_f32(const float* pos, const float* charges, const float* box, int64_t num_atoms,
                        int32_t gx, int32_t gy, int32_t gz, int32_t order, double coulomb, float* grid,
-                       mnx_stream_t stream);
+                       void* workspace, size_t workspace_bytes, mnx_stream_t stream);
 int mnx_pme_spread_f64(const double* pos, const double* charges, const double* box, int64_t num_atoms,
                        int32_t gx, int32_t gy, int32_t gz, int32_t order, double coulomb, double* grid,
-                       mnx_stream_t stream);
+                       void* workspace, size_t workspace_bytes, mnx_stream_t stream);
 /* In place on the half spectrum cgrid[gx][gy][gz/2+1] (interleaved re, im):
  * G *= exp(-pi^2 m^2/alpha^2) / (pi V m^2 xm ym zm), m = 0 term zeroed;
  * *energy = 1/2 sum scale |G|^2 eterm before the multiply (pme_cpu.cpp:263-294, 378). */
@@ -201,7 +204,9 @@ int mnx_pme_gather_f64(const double* pos, const double* charges, const double* b
                        double coulomb, double* dpos, double* dq, mnx_stream_t stream);
 /* Real-space sum over a pair list neighbors[2][num_pairs] (i = -1 padding skipped) minus the
  * erf term of excluded pairs; exclusions[n][max_excl] descending, -1 padded (pme_cpu.cpp:95-164).
- * *energy, dpos [n][3], dq [n] are overwritten. */
+ * *energy, dpos [n][3], dq [n] are overwritten; dpos and dq may both be NULL (energy only, no
+ * atomics).  The reference computes both in its forward (pme_cpu.cpp:168-205); the torch op
+ * here computes the energy in the forward and the derivatives in the backward. */
 size_t mnx_pme_direct_workspace_bytes(int64_t num_atoms, int64_t num_pairs);
 int mnx_pme_direct_f32(const float* pos, const float* charges, int64_t num_atoms, const int32_t* neighbors,
                        int64_t num_pairs, const float* deltas, const float* distances,
@@ -254,6 +259,28 @@ int mnx_sc_bwd_f32(int32_t config, const float* A, const int64_t* types, const f
                    const float* grad_out, const int32_t* order, int64_t num_nodes,
                    int32_t channels, int32_t num_elements, float* grad_A, float* grad_W,
                    mnx_stream_t stream);
+
+/* ------------------------------------------------------------------------ */
+/* Hidden stack of the radial weight MLP (replaces mlp[:-1] of               */
+/* RadialWeightMLP, src/molrep/interaction/radial_mlp.py:38-93:              */
+/* [Linear(in, hidden) -> SiLU] x layers) for the forward and the gradient   */
+/* with respect to the edge features.  raw parameters: per layer W_j         */
+/* [hidden][in_j] (torch.nn.Linear layout) then b_j [hidden], contiguous;    */
+/* mnx_radial_pack_f32 rearranges them once into frag                        */
+/* [mnx_radial_frag_floats(...)] floats (16-byte aligned), which the fwd and */
+/* bwd kernels read.  feats [E][kin], h [E][hidden], grad_feats [E][kin]     */
+/* (overwritten).  kin <= 64; hidden 32 or 64 with 1..4 layers, or 128 with  */
+/* 1..2 layers (else MNX_ERR_UNSUPPORTED; the size queries return -1).       */
+/* ------------------------------------------------------------------------ */
+int64_t mnx_radial_raw_floats(int32_t kin, int32_t hidden, int32_t layers);
+int64_t mnx_radial_frag_floats(int32_t kin, int32_t hidden, int32_t layers);
+int mnx_radial_pack_f32(const float* raw, int32_t kin, int32_t hidden, int32_t layers, float* frag,
+                        mnx_stream_t stream);
+int mnx_radial_fwd_f32(const float* feats, int64_t num_edges, int32_t kin, int32_t hidden,
+                       int32_t layers, const float* frag, float* h, mnx_stream_t stream);
+int mnx_radial_bwd_f32(const float* feats, int64_t num_edges, int32_t kin, int32_t hidden,
+                       int32_t layers, const float* frag, const float* grad_h, float* grad_feats,
+                       mnx_stream_t stream);
 
 #ifdef __cplusplus
 }

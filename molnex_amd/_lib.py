@@ -41,8 +41,9 @@ SIGNATURES = {
     "mnx_tp_bwd_workspace_bytes": (c_sz, [c_i32, c_i32, c_i64]),
     "mnx_tp_bwd_f32": (C.c_int, [c_i32, c_i32, vp, vp, vp, vp, vp, vp, vp, c_i64, c_i64, vp, vp, vp, vp, c_sz, vp]),
     "mnx_tp_bwd_sender_f32": (C.c_int, [c_i32, c_i32, vp, vp, vp, vp, vp, vp, vp, c_i64, c_i64, vp, vp, vp, vp]),
-    "mnx_pme_spread_f32": (C.c_int, [vp, vp, vp, c_i64, c_i32, c_i32, c_i32, c_i32, c_f64, vp, vp]),
-    "mnx_pme_spread_f64": (C.c_int, [vp, vp, vp, c_i64, c_i32, c_i32, c_i32, c_i32, c_f64, vp, vp]),
+    "mnx_pme_spread_workspace_bytes": (c_sz, [c_i64, c_i32, c_i32, c_i32]),
+    "mnx_pme_spread_f32": (C.c_int, [vp, vp, vp, c_i64, c_i32, c_i32, c_i32, c_i32, c_f64, vp, vp, c_sz, vp]),
+    "mnx_pme_spread_f64": (C.c_int, [vp, vp, vp, c_i64, c_i32, c_i32, c_i32, c_i32, c_f64, vp, vp, c_sz, vp]),
     "mnx_pme_convolve_workspace_bytes": (c_sz, [c_i32, c_i32, c_i32]),
     "mnx_pme_convolve_f32": (C.c_int, [vp, vp, c_i32, c_i32, c_i32, c_f64, vp, vp, vp, vp, vp, c_sz, vp]),
     "mnx_pme_convolve_f64": (C.c_int, [vp, vp, c_i32, c_i32, c_i32, c_f64, vp, vp, vp, vp, vp, c_sz, vp]),
@@ -59,6 +60,11 @@ SIGNATURES = {
     "mnx_sc_config_info": (C.c_int, [c_i32, vp]),
     "mnx_sc_fwd_f32": (C.c_int, [c_i32, vp, vp, vp, c_i64, c_i32, c_i32, vp, vp]),
     "mnx_sc_bwd_f32": (C.c_int, [c_i32, vp, vp, vp, vp, vp, c_i64, c_i32, c_i32, vp, vp, vp]),
+    "mnx_radial_raw_floats": (c_i64, [c_i32, c_i32, c_i32]),
+    "mnx_radial_frag_floats": (c_i64, [c_i32, c_i32, c_i32]),
+    "mnx_radial_pack_f32": (C.c_int, [vp, c_i32, c_i32, c_i32, vp, vp]),
+    "mnx_radial_fwd_f32": (C.c_int, [vp, c_i64, c_i32, c_i32, c_i32, vp, vp, vp]),
+    "mnx_radial_bwd_f32": (C.c_int, [vp, c_i64, c_i32, c_i32, c_i32, vp, vp, vp, vp]),
 }
 
 

@@ -9,12 +9,14 @@
 // spreading (:240-256), influence function and energy (:263-294), gather
 // (:311-343), direct sum with exclusions (:95-164).  The reference's CUDA path
 // (pme_cuda.cu:394,460) supports spline orders 4 and 5; these kernels take any
-// order 3..8.  Accumulations into the grid and per-atom derivatives use fp32 /
-// fp64 atomics; energies are reduced deterministically in fp64.
+// order 3..8.  The spread is a gather over mesh bricks (no atomics, fixed
+// summation order); the direct-space derivatives use fp32 / fp64 atomics, and
+// energies are reduced deterministically in fp64.
 
 #include <math.h>
 
 #include "common.h"
+#include "scan.h"
 
 namespace mnx {
 namespace {
@@ -42,11 +44,12 @@ __device__ __forceinline__ Recip<T> invert_box(const T* __restrict__ b) {
     return R;
 }
 
-// Grid origin and B-spline weights (and derivatives when dd != nullptr) of one atom.
+// Grid origin index and fractional offset of one atom along each axis (pme_cpu.cpp:37-60).
+// The index is clamped into [0, grid) so that a non-finite position cannot address
+// memory outside the mesh (its weights are then non-finite, as in the reference).
 template <typename T>
-__device__ __forceinline__ void spline(const T* __restrict__ pos, int64_t atom, const T* __restrict__ box,
-                                       const Recip<T>& R, const int grid[3], int order, int gidx[3],
-                                       T (&d)[kMaxOrder][3], T (*dd)[3]) {
+__device__ __forceinline__ void grid_coord(const T* __restrict__ pos, int64_t atom, const T* __restrict__ box,
+                                           const Recip<T>& R, const int grid[3], int gidx[3], T frac[3]) {
     T p[3] = {pos[3 * atom], pos[3 * atom + 1], pos[3 * atom + 2]};
     for (int i = 2; i >= 0; --i) {
         const T sc = floor(p[i] * R.r[i][i]);
@@ -56,8 +59,21 @@ __device__ __forceinline__ void spline(const T* __restrict__ pos, int64_t atom, 
         T t = p[0] * R.r[0][i] + p[1] * R.r[1][i] + p[2] * R.r[2][i];
         t = (t - floor(t)) * grid[i];
         const int ti = int(t);
-        const T dr = t - ti;
-        gidx[i] = ti % grid[i];
+        frac[i] = t - ti;
+        const int g = ti % grid[i];
+        gidx[i] = g < 0 ? 0 : (g < grid[i] ? g : grid[i] - 1);
+    }
+}
+
+// Grid origin and B-spline weights (and derivatives when dd != nullptr) of one atom.
+template <typename T>
+__device__ __forceinline__ void spline(const T* __restrict__ pos, int64_t atom, const T* __restrict__ box,
+                                       const Recip<T>& R, const int grid[3], int order, int gidx[3],
+                                       T (&d)[kMaxOrder][3], T (*dd)[3]) {
+    T frac[3];
+    grid_coord<T>(pos, atom, box, R, grid, gidx, frac);
+    for (int i = 0; i < 3; ++i) {
+        const T dr = frac[i];
         d[order - 1][i] = 0;
         d[1][i] = dr;
         d[0][i] = 1 - dr;
@@ -80,27 +96,184 @@ __device__ __forceinline__ void spline(const T* __restrict__ pos, int64_t atom, 
     }
 }
 
-// One wavefront lane per (atom, ix); each lane spreads its order^2 (iy, iz) points.
+// ---------------------------------------------------------------------------
+// Spreading as a gather over mesh bricks.  The mesh is cut into bricks of
+// kBrick^3 points (the last brick along an axis may be partial).  Atoms are
+// binned by the brick holding their spline origin, in ascending atom order
+// inside each brick.  One workgroup owns one brick: it stages the splines of
+// every atom whose origin lies in the brick or in the bricks that precede it
+// within order-1 points (cyclically).  Each lane owns one (y, z) column of the
+// brick, each of the four wavefronts sums a quarter of the staged atoms into
+// its lanes' columns, and the four partial sums are added in wave order and
+// stored once.  No atomics, every mesh point written exactly once (no
+// clearing pass), and a fixed summation order.
+// ---------------------------------------------------------------------------
+constexpr int kBrick = 8;          // mesh points per brick edge (>= kMaxOrder - 1)
+constexpr int kBrickThreads = 256; // two mesh points per thread
+constexpr int kBrickStage = 256;   // atom splines staged in LDS per pass
+constexpr int kAxisSrc = 3;        // source bricks per axis (see axis_sources)
+static_assert(kBrick * kBrick == kWave, "one lane per (y, z) column of a brick");
+static_assert(kBrickStage * 3 * kMaxOrder >= kBrickThreads * kBrick, "reduction fits the staging area");
+
+__device__ __forceinline__ int brick_of(const int gi[3], int nby, int nbz) {
+    return ((gi[0] / kBrick) * nby + gi[1] / kBrick) * nbz + gi[2] / kBrick;
+}
+
 template <typename T>
-__global__ void k_spread(const T* __restrict__ pos, const T* __restrict__ q, const T* __restrict__ box, int64_t n,
-                         int gx, int gy, int gz, int order, T sqrt_k, T* __restrict__ grid) {
-    const int64_t tid = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
-    const int64_t atom = tid / order;
-    const int ix = int(tid - atom * order);
-    if (atom >= n) return;
+__global__ void k_bin_count(const T* __restrict__ pos, const T* __restrict__ box, int64_t n, int gx, int gy, int gz,
+                            int nby, int nbz, int32_t* __restrict__ brick, int32_t* __restrict__ counts) {
+    const int64_t a = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (a >= n) return;
     const int G[3] = {gx, gy, gz};
     const Recip<T> R = invert_box<T>(box);
     int gi[3];
-    T d[kMaxOrder][3];
-    spline<T>(pos, atom, box, R, G, order, gi, d, nullptr);
-    const int x = (gi[0] + ix) % gx;
-    const T wx = q[atom] * sqrt_k * d[ix][0];
-    T* __restrict__ plane = grid + int64_t(x) * gy * gz;
-    for (int iy = 0; iy < order; ++iy) {
-        const int y = (gi[1] + iy) % gy;
-        const T wxy = wx * d[iy][1];
-        T* __restrict__ row = plane + int64_t(y) * gz;
-        for (int iz = 0; iz < order; ++iz) atomicAdd(row + (gi[2] + iz) % gz, wxy * d[iz][2]);
+    T frac[3];
+    grid_coord<T>(pos, a, box, R, G, gi, frac);
+    const int b = brick_of(gi, nby, nbz);
+    brick[a] = b;
+    atomicAdd(counts + b, 1);
+}
+
+__global__ void k_bin_place(const int32_t* __restrict__ brick, int64_t n, const int32_t* __restrict__ ptr,
+                            int32_t* __restrict__ fill, int32_t* __restrict__ slots) {
+    const int64_t a = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (a >= n) return;
+    const int b = brick[a];
+    slots[ptr[b] + atomicAdd(fill + b, 1)] = int32_t(a);
+}
+
+// Ascending atom order inside each brick: slot j moves to its rank within its brick.
+__global__ void k_bin_rank(const int32_t* __restrict__ brick, const int32_t* __restrict__ ptr,
+                           const int32_t* __restrict__ slots, int64_t n, int32_t* __restrict__ perm) {
+    const int64_t j = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (j >= n) return;
+    const int a = slots[j];
+    const int b = brick[a];
+    const int lo = ptr[b], hi = ptr[b + 1];
+    int r = 0;
+    for (int k = lo; k < hi; ++k) r += slots[k] < a;
+    perm[lo + r] = a;
+}
+
+// Bricks along one axis whose atoms reach destination brick b: b itself and the
+// bricks before it (cyclically) covering the order-1 points ahead of b's first
+// point.  Only the last brick of an axis can be partial, so three suffice.
+__device__ __forceinline__ int axis_sources(int b, int nb, int G, int order, int out[kAxisSrc]) {
+    int k = 0;
+    out[k++] = b;
+    int need = order - 1, cur = b;
+    while (need > 0 && k < kAxisSrc) {
+        cur = cur == 0 ? nb - 1 : cur - 1;
+        if (cur == b) break;
+        out[k++] = cur;
+        need -= min(kBrick, G - cur * kBrick);
+    }
+    return k;
+}
+
+template <typename T>
+__global__ void __launch_bounds__(kBrickThreads)
+    k_spread_bricks(const T* __restrict__ pos, const T* __restrict__ q, const T* __restrict__ box, int gx, int gy,
+                    int gz, int nbx, int nby, int nbz, int order, T sqrt_k, const int32_t* __restrict__ ptr,
+                    const int32_t* __restrict__ perm, T* __restrict__ grid) {
+    constexpr int kSrc = kAxisSrc * kAxisSrc * kAxisSrc;
+    __shared__ int s_src[kSrc];
+    __shared__ int s_off[kSrc + 1];
+    __shared__ int s_nsrc;
+    __shared__ int s_rel[kBrickStage];             // packed brick-relative origin, -1: misses the brick
+    __shared__ T s_w[kBrickStage][3 * kMaxOrder];  // [x weights * q sqrt(k) | y weights | z weights]
+    const int bid = blockIdx.x;
+    const int bz = bid % nbz, by = (bid / nbz) % nby, bx = bid / (nbz * nby);
+    if (threadIdx.x == 0) {
+        int sx[kAxisSrc], sy[kAxisSrc], sz[kAxisSrc];
+        const int nx = axis_sources(bx, nbx, gx, order, sx);
+        const int ny = axis_sources(by, nby, gy, order, sy);
+        const int nz = axis_sources(bz, nbz, gz, order, sz);
+        int k = 0, off = 0;
+        for (int i = 0; i < nx; ++i)
+            for (int j = 0; j < ny; ++j)
+                for (int l = 0; l < nz; ++l) {
+                    const int s = (sx[i] * nby + sy[j]) * nbz + sz[l];
+                    s_src[k] = s;
+                    s_off[k] = off;
+                    off += ptr[s + 1] - ptr[s];
+                    ++k;
+                }
+        s_off[k] = off;
+        s_nsrc = k;
+    }
+    __syncthreads();
+    const int total = s_off[s_nsrc];
+    const int G[3] = {gx, gy, gz};
+    const int S[3] = {bx * kBrick, by * kBrick, bz * kBrick};
+    const Recip<T> R = invert_box<T>(box);
+    const int t = threadIdx.x, lane = t & (kWave - 1), wave = t / kWave;
+    // lane -> (y, z) column of the brick; acc[x] for its 8 points along x
+    const int ly = lane >> 3, lz = lane & 7;
+    T acc[kBrick];
+    for (int x = 0; x < kBrick; ++x) acc[x] = 0;
+    for (int base = 0; base < total; base += kBrickStage) {
+        const int cnt = min(kBrickStage, total - base);
+        for (int c = t; c < cnt; c += kBrickThreads) {
+            const int g = base + c;
+            int s = 0;
+            while (s_off[s + 1] <= g) ++s;
+            const int atom = perm[ptr[s_src[s]] + (g - s_off[s])];
+            int gi[3];
+            T d[kMaxOrder][3];
+            spline<T>(pos, atom, box, R, G, order, gi, d, nullptr);
+            // origin relative to the brick start, cyclically in (-G, brick size); the atom
+            // reaches the brick along an axis iff that offset is > -order
+            int rel[3];
+            bool reach = true;
+            for (int a = 0; a < 3; ++a) {
+                int r = gi[a] - S[a];
+                r += r < 0 ? G[a] : 0;
+                if (r >= min(kBrick, G[a] - S[a])) r -= G[a];
+                reach = reach && r > -order;
+                rel[a] = r;
+            }
+            s_rel[c] = reach ? (rel[0] + 8) | ((rel[1] + 8) << 4) | ((rel[2] + 8) << 8) : -1;
+            if (reach) {
+                const T qs = q[atom] * sqrt_k;
+                for (int k = 0; k < order; ++k) {
+                    s_w[c][k] = qs * d[k][0];
+                    s_w[c][kMaxOrder + k] = d[k][1];
+                    s_w[c][2 * kMaxOrder + k] = d[k][2];
+                }
+            }
+        }
+        __syncthreads();
+        // wave w sums candidates w, w + 4, ... in order (wave-uniform skip of non-reaching ones)
+        for (int c = wave; c < cnt; c += kBrickThreads / kWave) {
+            const int pk = s_rel[c];
+            if (pk < 0) continue;
+            const int rx = (pk & 15) - 8, ry = ((pk >> 4) & 15) - 8, rz = (pk >> 8) - 8;
+            int dy = ly - ry;
+            dy += dy < 0 ? gy : 0;
+            int dz = lz - rz;
+            dz += dz < 0 ? gz : 0;
+            const bool in = dy < order && dz < order;
+            const T wyz = in ? s_w[c][kMaxOrder + dy] * s_w[c][2 * kMaxOrder + dz] : T(0);
+#pragma unroll
+            for (int x = 0; x < kBrick; ++x) {
+                int dx = x - rx;
+                dx += dx < 0 ? gx : 0;
+                if (dx < order) acc[x] += s_w[c][dx] * wyz;
+            }
+        }
+        __syncthreads();
+    }
+    // the four waves' partial sums, added in wave order (reuses the staging area)
+    T* red = &s_w[0][0];
+    for (int x = 0; x < kBrick; ++x) red[(wave * kBrick + x) * kWave + lane] = acc[x];
+    __syncthreads();
+    for (int i = t; i < kBrick * kWave; i += kBrickThreads) {
+        const int x = i / kWave, l = i % kWave;
+        T v = red[x * kWave + l];
+        for (int w = 1; w < kBrickThreads / kWave; ++w) v += red[(w * kBrick + x) * kWave + l];
+        const int px = S[0] + x, py = S[1] + (l >> 3), pz = S[2] + (l & 7);
+        if (px < gx && py < gy && pz < gz) grid[(int64_t(px) * gy + py) * gz + pz] = v;
     }
 }
 
@@ -202,41 +375,9 @@ __global__ void k_gather(const T* __restrict__ pos, const T* __restrict__ q, con
     dq[atom] = s * sqrt_k;
 }
 
-// Real-space pair sum over the given pair list minus excluded pairs (pme_cpu.cpp:110-135).
-template <typename T>
-__global__ void __launch_bounds__(kConvThreads) k_direct_pairs(const T* __restrict__ q, int64_t n,
-                                                               const int32_t* __restrict__ nb, int64_t P, const T* __restrict__ dl,
-                                                               const T* __restrict__ r, const int32_t* __restrict__ excl,
-                                                               int max_excl, T alpha, T coulomb,
-                                                               T* __restrict__ dpos, T* __restrict__ dq,
-                                                               double* __restrict__ partials) {
+// Block-wide fp64 sum of one value per thread into partials[blockIdx.x].
+__device__ __forceinline__ void block_partial(double e, double* __restrict__ partials) {
     __shared__ double red[kConvThreads];
-    const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
-    double e = 0.0;
-    if (i < P) {
-        const int a1 = nb[i], a2 = nb[P + i];
-        // -1 marks padding (reference); any other out-of-range index is skipped too
-        bool include = a1 > -1 && a1 < n && a2 >= 0 && a2 < n;
-        for (int j = 0; include && j < max_excl && excl[int64_t(a1) * max_excl + j] >= a2; ++j)
-            if (excl[int64_t(a1) * max_excl + j] == a2) include = false;
-        if (include) {
-            const T rr = r[i];
-            const T inv = T(1) / rr;
-            const T ar = alpha * rr;
-            const T ex = exp(-ar * ar);
-            const T ec = erfc(ar);
-            const T pref = coulomb * inv;
-            const T c1 = q[a1], c2 = q[a2];
-            e = double(pref * ec * c1 * c2);
-            atomicAdd(dq + a1, pref * ec * c2);
-            atomicAdd(dq + a2, pref * ec * c1);
-            const T dedr = pref * c1 * c2 * (ec + ar * ex * T(M_2_SQRTPI)) * inv * inv;
-            for (int k = 0; k < 3; ++k) {
-                atomicAdd(dpos + 3 * a1 + k, -dedr * dl[3 * i + k]);
-                atomicAdd(dpos + 3 * a2 + k, dedr * dl[3 * i + k]);
-            }
-        }
-    }
     red[threadIdx.x] = e;
     __syncthreads();
     for (int off = kConvThreads / 2; off > 0; off >>= 1) {
@@ -246,17 +387,94 @@ __global__ void __launch_bounds__(kConvThreads) k_direct_pairs(const T* __restri
     if (threadIdx.x == 0) partials[blockIdx.x] = red[0];
 }
 
+// Sum of v over this lane's run of equal keys, from this lane to the run's end
+// (the lanes of a run are contiguous; a run ends where the key changes).  After
+// the call the first lane of every run holds that run's total.  All 64 lanes
+// of the wavefront must take part.
+template <typename T, int K>
+__device__ __forceinline__ bool run_reduce(int key, T (&v)[K]) {
+    const int lane = threadIdx.x & (kWave - 1);
+    const int prev = __shfl_up(key, 1);
+    const bool head = lane == 0 || prev != key;
+    const unsigned long long heads = __ballot(head);
+    const unsigned long long above = lane == kWave - 1 ? 0ull : heads & (~0ull << (lane + 1));
+    const int end = above ? __builtin_ctzll(above) : kWave;
+    for (int off = 1; off < kWave; off <<= 1) {
+        const bool take = lane + off < end;
+        for (int k = 0; k < K; ++k) {
+            const T o = __shfl_down(v[k], off);
+            if (take) v[k] += o;
+        }
+    }
+    return head;
+}
+
+// Real-space pair sum over the given pair list minus excluded pairs (pme_cpu.cpp:110-135).
+// GRAD: also dE/dq and dE/dpos (pme_cpu.cpp:195-215).  Pair lists come grouped by
+// their first atom (the neighbor list's row order), so the first atom's four
+// derivative terms are summed over each run of equal rows in the wavefront and
+// added once per run; the second atom's terms are added per pair.
+template <typename T, bool GRAD>
+__global__ void __launch_bounds__(kConvThreads) k_direct_pairs(const T* __restrict__ q, int64_t n,
+                                                               const int32_t* __restrict__ nb, int64_t P, const T* __restrict__ dl,
+                                                               const T* __restrict__ r, const int32_t* __restrict__ excl,
+                                                               int max_excl, T alpha, T coulomb,
+                                                               T* __restrict__ dpos, T* __restrict__ dq,
+                                                               double* __restrict__ partials) {
+    const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    double e = 0.0;
+    int row = -1;
+    T g1[4] = {0, 0, 0, 0};  // d/dq and d/dpos of the pair's first atom
+    if (i < P) {
+        const int a1 = nb[i], a2 = nb[P + i];
+        // -1 marks padding (reference); any other out-of-range index is skipped too
+        bool include = a1 > -1 && a1 < n && a2 >= 0 && a2 < n;
+        if (include) row = a1;
+        for (int j = 0; include && j < max_excl && excl[int64_t(a1) * max_excl + j] >= a2; ++j)
+            if (excl[int64_t(a1) * max_excl + j] == a2) include = false;
+        if (include) {
+            const T rr = r[i];
+            const T inv = T(1) / rr;
+            const T ar = alpha * rr;
+            const T ec = erfc(ar);
+            const T pref = coulomb * inv;
+            const T c1 = q[a1], c2 = q[a2];
+            e = double(pref * ec * c1 * c2);
+            if (GRAD) {
+                const T ex = exp(-ar * ar);
+                const T dedr = pref * c1 * c2 * (ec + ar * ex * T(M_2_SQRTPI)) * inv * inv;
+                g1[0] = pref * ec * c2;
+                atomicAdd(dq + a2, pref * ec * c1);
+                for (int k = 0; k < 3; ++k) {
+                    const T f = dedr * dl[3 * i + k];
+                    g1[1 + k] = -f;
+                    atomicAdd(dpos + 3 * a2 + k, f);
+                }
+            }
+        }
+    }
+    if (GRAD) {
+        if (run_reduce<T, 4>(row, g1) && row >= 0) {
+            atomicAdd(dq + row, g1[0]);
+            for (int k = 0; k < 3; ++k) atomicAdd(dpos + 3 * row + k, g1[1 + k]);
+        }
+    }
+    block_partial(e, partials);
+}
+
 // Excluded pairs' erf term, removed from the reciprocal-space sum (pme_cpu.cpp:137-162).
-template <typename T>
+// One thread per atom a; a's own derivative terms are summed over its exclusions
+// and added once.
+template <typename T, bool GRAD>
 __global__ void __launch_bounds__(kConvThreads) k_direct_excl(const T* __restrict__ pos, const T* __restrict__ q,
                                                               int64_t n, const int32_t* __restrict__ excl,
                                                               int max_excl, T alpha, T coulomb,
                                                               T* __restrict__ dpos, T* __restrict__ dq,
                                                               double* __restrict__ partials) {
-    __shared__ double red[kConvThreads];
     const int64_t a = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
     double e = 0.0;
     if (a < n) {
+        T ga[4] = {0, 0, 0, 0};
         for (int j = 0; j < max_excl; ++j) {
             const int b = excl[a * max_excl + j];
             if (!(b > a)) break;
@@ -266,27 +484,33 @@ __global__ void __launch_bounds__(kConvThreads) k_direct_excl(const T* __restric
             const T rr = sqrt(dr[0] * dr[0] + dr[1] * dr[1] + dr[2] * dr[2]);
             const T inv = T(1) / rr;
             const T ar = alpha * rr;
-            const T ex = exp(-ar * ar);
             const T ef = erf(ar);
             const T pref = coulomb * inv;
             const T c1 = q[a], c2 = q[b];
             e -= double(pref * ef * c1 * c2);
-            atomicAdd(dq + a, -pref * ef * c2);
-            atomicAdd(dq + b, -pref * ef * c1);
-            const T dedr = pref * c1 * c2 * (ef - ar * ex * T(M_2_SQRTPI)) * inv * inv;
-            for (int k = 0; k < 3; ++k) {
-                atomicAdd(dpos + 3 * a + k, dedr * dr[k]);
-                atomicAdd(dpos + 3 * int64_t(b) + k, -dedr * dr[k]);
+            if (GRAD) {
+                const T ex = exp(-ar * ar);
+                const T dedr = pref * c1 * c2 * (ef - ar * ex * T(M_2_SQRTPI)) * inv * inv;
+                ga[0] -= pref * ef * c2;
+                atomicAdd(dq + b, -pref * ef * c1);
+                for (int k = 0; k < 3; ++k) {
+                    ga[1 + k] += dedr * dr[k];
+                    atomicAdd(dpos + 3 * int64_t(b) + k, -dedr * dr[k]);
+                }
             }
         }
+        if (GRAD && max_excl > 0) {
+            atomicAdd(dq + a, ga[0]);
+            for (int k = 0; k < 3; ++k) atomicAdd(dpos + 3 * a + k, ga[1 + k]);
+        }
     }
-    red[threadIdx.x] = e;
-    __syncthreads();
-    for (int off = kConvThreads / 2; off > 0; off >>= 1) {
-        if (threadIdx.x < off) red[threadIdx.x] += red[threadIdx.x + off];
-        __syncthreads();
-    }
-    if (threadIdx.x == 0) partials[blockIdx.x] = red[0];
+    block_partial(e, partials);
+}
+
+template <typename T>
+__global__ void k_fill(T* __restrict__ p, int64_t n) {
+    const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i < n) p[i] = T(0);
 }
 
 int check_grid(int gx, int gy, int gz, int order) {
@@ -296,18 +520,65 @@ int check_grid(int gx, int gy, int gz, int order) {
     return MNX_OK;
 }
 
+struct BrickWs {
+    int32_t *counts, *fill, *ptr, *tiles, *brick, *slots, *perm;
+};
+
+BrickWs carve_bricks(void* base, int64_t n, int64_t nbricks, size_t* used) {
+    Workspace ws{static_cast<char*>(base), 0};
+    BrickWs w;
+    w.counts = ws.take<int32_t>(nbricks + 1);
+    w.fill = ws.take<int32_t>(nbricks + 1);
+    w.ptr = ws.take<int32_t>(nbricks + 1);
+    w.tiles = ws.take<int32_t>(scan_workspace_elems(nbricks + 1));
+    w.brick = ws.take<int32_t>(n);
+    w.slots = ws.take<int32_t>(n);
+    w.perm = ws.take<int32_t>(n);
+    *used = ws.used;
+    return w;
+}
+
+int64_t brick_count(int g) { return ceil_div(g, kBrick); }
+
+size_t spread_ws(int64_t n, int gx, int gy, int gz) {
+    size_t used = 0;
+    carve_bricks(nullptr, n > 0 ? n : 0, brick_count(gx) * brick_count(gy) * brick_count(gz), &used);
+    return used + 256;
+}
+
 template <typename T>
 int spread(const T* pos, const T* q, const T* box, int64_t n, int gx, int gy, int gz, int order, double coulomb,
-           T* grid, hipStream_t s) {
+           T* grid, void* ws, size_t ws_bytes, hipStream_t s) {
     clear_error();
     int rc = check_grid(gx, gy, gz, order);
     if (rc) return rc;
+    MNX_REQUIRE(n >= 0 && n < (int64_t(1) << 31), "atom count out of range");
     MNX_REQUIRE(grid && box && (n == 0 || (pos && q)), "null pointer argument");
-    MNX_HIP_TRY(hipMemsetAsync(grid, 0, sizeof(T) * size_t(gx) * gy * gz, s));
-    if (n == 0) return MNX_OK;
-    const int64_t threads = n * order;
-    hipLaunchKernelGGL((k_spread<T>), dim3(ceil_div(threads, 256)), dim3(256), 0, s, pos, q, box, n, gx, gy, gz,
-                       order, T(sqrt(coulomb)), grid);
+    const int nbx = int(brick_count(gx)), nby = int(brick_count(gy)), nbz = int(brick_count(gz));
+    const int64_t nbricks = int64_t(nbx) * nby * nbz;
+    size_t need = 0;
+    BrickWs w = carve_bricks(ws, n, nbricks, &need);
+    if (!ws || ws_bytes < need) return set_error(MNX_ERR_WORKSPACE, "workspace %zu < %zu bytes", ws_bytes, need);
+    const int tb = 256;
+    for (int32_t* p : {w.counts, w.fill}) {
+        hipLaunchKernelGGL((k_fill<int32_t>), dim3(ceil_div(nbricks + 1, tb)), dim3(tb), 0, s, p, nbricks + 1);
+        MNX_CHECK_LAUNCH();
+    }
+    if (n > 0) {
+        hipLaunchKernelGGL((k_bin_count<T>), dim3(ceil_div(n, tb)), dim3(tb), 0, s, pos, box, n, gx, gy, gz, nby, nbz,
+                           w.brick, w.counts);
+        MNX_CHECK_LAUNCH();
+    }
+    rc = exclusive_scan<int32_t, int32_t>(w.counts, nbricks + 1, w.ptr, w.tiles, (int32_t*)nullptr, s);
+    if (rc) return rc;
+    if (n > 0) {
+        hipLaunchKernelGGL(k_bin_place, dim3(ceil_div(n, tb)), dim3(tb), 0, s, w.brick, n, w.ptr, w.fill, w.slots);
+        MNX_CHECK_LAUNCH();
+        hipLaunchKernelGGL(k_bin_rank, dim3(ceil_div(n, tb)), dim3(tb), 0, s, w.brick, w.ptr, w.slots, n, w.perm);
+        MNX_CHECK_LAUNCH();
+    }
+    hipLaunchKernelGGL((k_spread_bricks<T>), dim3(nbricks), dim3(kBrickThreads), 0, s, pos, q, box, gx, gy, gz, nbx,
+                       nby, nbz, order, T(sqrt(coulomb)), w.ptr, w.perm, grid);
     MNX_CHECK_LAUNCH();
     return MNX_OK;
 }
@@ -349,32 +620,47 @@ int gather(const T* pos, const T* q, const T* box, int64_t n, const T* grid, int
 
 size_t direct_ws(int64_t n, int64_t P) { return size_t(ceil_div(P > 0 ? P : 1, kConvThreads) + ceil_div(n > 0 ? n : 1, kConvThreads)) * sizeof(double); }
 
+template <typename T, bool GRAD>
+void launch_direct(const T* pos, const T* q, int64_t n, const int32_t* nb, int64_t P, const T* deltas, const T* dist,
+                   const int32_t* excl, int max_excl, double alpha, double coulomb, T* dpos, T* dq, double* part,
+                   int64_t b1, int64_t b2, hipStream_t s) {
+    if (b1 > 0)
+        hipLaunchKernelGGL((k_direct_pairs<T, GRAD>), dim3(b1), dim3(kConvThreads), 0, s, q, n, nb, P, deltas, dist,
+                           excl, max_excl, T(alpha), T(coulomb), dpos, dq, part);
+    if (b2 > 0)
+        hipLaunchKernelGGL((k_direct_excl<T, GRAD>), dim3(b2), dim3(kConvThreads), 0, s, pos, q, n, excl, max_excl,
+                           T(alpha), T(coulomb), dpos, dq, part + b1);
+}
+
 template <typename T>
 int direct(const T* pos, const T* q, int64_t n, const int32_t* nb, int64_t P, const T* deltas, const T* dist,
            const int32_t* excl, int max_excl, double alpha, double coulomb, T* energy, T* dpos, T* dq, void* ws,
            size_t ws_bytes, hipStream_t s) {
     clear_error();
     MNX_REQUIRE(n >= 0 && P >= 0 && max_excl >= 0, "sizes out of range");
-    MNX_REQUIRE(energy && (n == 0 || (pos && q && dpos && dq)), "null pointer argument");
+    MNX_REQUIRE(energy && (n == 0 || (pos && q)), "null pointer argument");
+    MNX_REQUIRE((dpos == nullptr) == (dq == nullptr), "dpos and dq must both be given or both be null");
     MNX_REQUIRE(max_excl == 0 || excl, "exclusions pointer is null");
+    MNX_REQUIRE(P == 0 || (nb && deltas && dist), "null pair-list pointer");
     if (!ws || ws_bytes < direct_ws(n, P)) return set_error(MNX_ERR_WORKSPACE, "workspace too small");
     double* part = static_cast<double*>(ws);
-    const int64_t b1 = ceil_div(P > 0 ? P : 1, kConvThreads), b2 = ceil_div(n > 0 ? n : 1, kConvThreads);
-    MNX_HIP_TRY(hipMemsetAsync(part, 0, sizeof(double) * (b1 + b2), s));
-    if (n > 0) {
-        MNX_HIP_TRY(hipMemsetAsync(dpos, 0, sizeof(T) * 3 * n, s));
-        MNX_HIP_TRY(hipMemsetAsync(dq, 0, sizeof(T) * n, s));
-    }
-    if (P > 0) {
-        hipLaunchKernelGGL((k_direct_pairs<T>), dim3(b1), dim3(kConvThreads), 0, s, q, n, nb, P, deltas, dist, excl,
-                           max_excl, T(alpha), T(coulomb), dpos, dq, part);
+    const int64_t b1 = P > 0 ? ceil_div(P, kConvThreads) : 0;
+    const int64_t b2 = (n > 0 && max_excl > 0) ? ceil_div(n, kConvThreads) : 0;
+    const bool grad = dpos != nullptr;
+    if (grad && n > 0) {
+        hipLaunchKernelGGL((k_fill<T>), dim3(ceil_div(3 * n, 256)), dim3(256), 0, s, dpos, 3 * n);
+        MNX_CHECK_LAUNCH();
+        hipLaunchKernelGGL((k_fill<T>), dim3(ceil_div(n, 256)), dim3(256), 0, s, dq, n);
         MNX_CHECK_LAUNCH();
     }
-    if (n > 0 && max_excl > 0) {
-        hipLaunchKernelGGL((k_direct_excl<T>), dim3(b2), dim3(kConvThreads), 0, s, pos, q, n, excl, max_excl,
-                           T(alpha), T(coulomb), dpos, dq, part + b1);
-        MNX_CHECK_LAUNCH();
-    }
+    if (grad)
+        launch_direct<T, true>(pos, q, n, nb, P, deltas, dist, excl, max_excl, alpha, coulomb, dpos, dq, part, b1, b2,
+                               s);
+    else
+        launch_direct<T, false>(pos, q, n, nb, P, deltas, dist, excl, max_excl, alpha, coulomb, dpos, dq, part, b1,
+                                b2, s);
+    MNX_CHECK_LAUNCH();
+    // every launched block wrote its partial; with no blocks the energy is 0
     hipLaunchKernelGGL((k_sum_partials<T>), dim3(1), dim3(1024), 0, s, part, b1 + b2, 1.0, energy);
     MNX_CHECK_LAUNCH();
     return MNX_OK;
@@ -387,13 +673,18 @@ using namespace mnx;
 
 extern "C" {
 
+size_t mnx_pme_spread_workspace_bytes(int64_t n, int32_t gx, int32_t gy, int32_t gz) {
+    return spread_ws(n, gx > 0 ? gx : 1, gy > 0 ? gy : 1, gz > 0 ? gz : 1);
+}
 int mnx_pme_spread_f32(const float* pos, const float* q, const float* box, int64_t n, int32_t gx, int32_t gy,
-                       int32_t gz, int32_t order, double coulomb, float* grid, mnx_stream_t s) {
-    return spread<float>(pos, q, box, n, gx, gy, gz, order, coulomb, grid, (hipStream_t)s);
+                       int32_t gz, int32_t order, double coulomb, float* grid, void* ws, size_t ws_bytes,
+                       mnx_stream_t s) {
+    return spread<float>(pos, q, box, n, gx, gy, gz, order, coulomb, grid, ws, ws_bytes, (hipStream_t)s);
 }
 int mnx_pme_spread_f64(const double* pos, const double* q, const double* box, int64_t n, int32_t gx, int32_t gy,
-                       int32_t gz, int32_t order, double coulomb, double* grid, mnx_stream_t s) {
-    return spread<double>(pos, q, box, n, gx, gy, gz, order, coulomb, grid, (hipStream_t)s);
+                       int32_t gz, int32_t order, double coulomb, double* grid, void* ws, size_t ws_bytes,
+                       mnx_stream_t s) {
+    return spread<double>(pos, q, box, n, gx, gy, gz, order, coulomb, grid, ws, ws_bytes, (hipStream_t)s);
 }
 size_t mnx_pme_convolve_workspace_bytes(int32_t gx, int32_t gy, int32_t gz) {
     return size_t(conv_blocks(gx, gy, gz)) * sizeof(double) + 256;

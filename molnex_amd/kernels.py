@@ -13,6 +13,7 @@ Ops
 ``molix::spherical_harmonics``  real SH l <= 3 (``cuet.SphericalHarmonics``)
 ``molix::edge_csr``             receiver CSR of an (E, 2) edge list
 ``molix::tp_scatter``           channelwise TP + scatter-sum (``cuet.ChannelWiseTensorProduct``)
+``molix::radial_hidden``        fused hidden stack of the radial weight MLP (gradient w.r.t. its input)
 """
 
 from __future__ import annotations
@@ -432,8 +433,10 @@ def _pme_recip_energy(positions, charges, box, gx, gy, gz, order, alpha, coulomb
         if m.numel() < g:
             raise ValueError("moduli shorter than the grid")
     grid = torch.empty((gx, gy, gz), dtype=dt, device=dev)
+    sws = _ws(lib.mnx_pme_spread_workspace_bytes(pos.shape[0], gx, gy, gz), dev)
     check(getattr(lib, f"mnx_pme_spread_{sfx}")(ptr(pos), ptr(q), ptr(b), pos.shape[0], gx, gy, gz, order,
-                                                float(coulomb), ptr(grid), _stream(pos)), "pme spread")
+                                                float(coulomb), ptr(grid), ptr(sws), sws.numel(), _stream(pos)),
+          "pme spread")
     spec = torch.fft.rfftn(grid).contiguous()
     energy = torch.empty((), dtype=dt, device=dev)
     ws = _ws(lib.mnx_pme_convolve_workspace_bytes(gx, gy, gz), dev)
@@ -498,7 +501,8 @@ def _pme_recip_bwd(ctx, grad):
 pme_reciprocal.register_autograd(_pme_recip_bwd, setup_context=_pme_recip_setup)
 
 
-def _pme_direct_run(positions, charges, neighbors, deltas, distances, exclusions, alpha, coulomb):
+def _pme_direct_run(positions, charges, neighbors, deltas, distances, exclusions, alpha, coulomb, grads=True):
+    """Energy, and (dE/dpos, dE/dq) when ``grads`` (else None, None: no derivative atomics)."""
     lib = _lib.load()
     sfx = _fsuffix(positions)
     dt, dev = positions.dtype, positions.device
@@ -513,11 +517,12 @@ def _pme_direct_run(positions, charges, neighbors, deltas, distances, exclusions
         raise ValueError("exclusions must be (num_atoms, max_exclusions)")
     max_excl = ex.shape[1] if ex.numel() else 0
     energy = torch.empty((), dtype=dt, device=dev)
-    dpos = torch.empty_like(pos)
-    dq = torch.empty_like(q)
+    dpos = torch.empty_like(pos) if grads else None
+    dq = torch.empty_like(q) if grads else None
     ws = _ws(lib.mnx_pme_direct_workspace_bytes(n, P), dev)
     check(getattr(lib, f"mnx_pme_direct_{sfx}")(ptr(pos), ptr(q), n, ptr(nb), P, ptr(dl), ptr(ds), ptr(ex), max_excl,
-                                                float(alpha), float(coulomb), ptr(energy), ptr(dpos), ptr(dq), ptr(ws),
+                                                float(alpha), float(coulomb), ptr(energy),
+                                                ptr(dpos), ptr(dq), ptr(ws),
                                                 ws.numel(), _stream(pos)), "pme direct")
     return energy, dpos, dq
 
@@ -528,7 +533,8 @@ def pme_direct(positions, charges, neighbors, deltas, distances, exclusions, alp
     Like the reference, the gradient w.r.t. positions is the analytic one through the pair
     geometry (deltas / distances are treated as functions of positions, ``pme_cpu.cpp:208-215``)."""
     _require_gpu("pme_direct", positions, charges, neighbors)
-    e, _, _ = _pme_direct_run(positions, charges, neighbors, deltas, distances, exclusions, alpha, coulomb)
+    e, _, _ = _pme_direct_run(positions, charges, neighbors, deltas, distances, exclusions, alpha, coulomb,
+                              grads=False)
     return e
 
 
@@ -713,3 +719,86 @@ def _scg_bwd(ctx, grad):
 
 
 symmetric_contraction.register_autograd(_scg_bwd, setup_context=_scg_setup)
+
+
+# ---------------------------------------------------------------------------
+# Radial weight MLP hidden stack
+# ---------------------------------------------------------------------------
+
+def radial_supported(kin: int, hidden: int, layers: int) -> bool:
+    """Whether the fused hidden-stack kernels are compiled for this shape."""
+    return _lib.load().mnx_radial_frag_floats(int(kin), int(hidden), int(layers)) > 0
+
+
+def _aligned16(t: Tensor) -> Tensor:
+    t = t.contiguous()
+    return t if t.data_ptr() % 16 == 0 else t.clone()
+
+
+def _radial_frag(params: Tensor, kin: int, hidden: int, layers: int) -> Tensor:
+    lib = _lib.load()
+    n = lib.mnx_radial_frag_floats(kin, hidden, layers)
+    if n < 0:
+        raise ValueError(f"radial_hidden: no kernel for in={kin}, hidden={hidden}, layers={layers}")
+    raw = params.detach().to(torch.float32).contiguous()
+    if raw.numel() != lib.mnx_radial_raw_floats(kin, hidden, layers):
+        raise ValueError("radial_hidden: parameter vector has the wrong length")
+    frag = torch.empty(n, dtype=torch.float32, device=raw.device)
+    check(lib.mnx_radial_pack_f32(ptr(raw), kin, hidden, layers, ptr(frag), _stream(raw)), "radial_hidden pack")
+    return frag
+
+
+@torch.library.custom_op("molix::radial_hidden", mutates_args=(), device_types="cuda")
+def radial_hidden(feats: Tensor, params: Tensor, kin: int, hidden: int, layers: int) -> Tensor:
+    """``mlp[:-1](feats)`` of ``RadialWeightMLP`` (``radial_mlp.py:38-93``: [Linear -> SiLU] x layers)
+    in one HIP kernel.  ``params`` = concatenated ``W_j.flatten(), b_j`` of the hidden Linears."""
+    _require_gpu("radial_hidden", feats, params)
+    if feats.dtype != torch.float32 or feats.dim() != 2 or feats.shape[1] != kin:
+        raise ValueError("radial_hidden: feats must be float32 (E, kin)")
+    f = feats.contiguous()
+    frag = _radial_frag(params, kin, hidden, layers)
+    out = f.new_empty(f.shape[0], hidden)
+    check(_lib.load().mnx_radial_fwd_f32(ptr(f), f.shape[0], kin, hidden, layers, ptr(frag), ptr(out), _stream(f)),
+          "radial_hidden")
+    return out
+
+
+@radial_hidden.register_fake
+def _(feats, params, kin, hidden, layers):
+    return feats.new_empty(feats.shape[0], hidden)
+
+
+@torch.library.custom_op("molix::radial_hidden_backward", mutates_args=(), device_types="cuda")
+def radial_hidden_backward(grad: Tensor, feats: Tensor, params: Tensor, kin: int, hidden: int,
+                           layers: int) -> Tensor:
+    """dL/dfeats of ``radial_hidden`` (forward recomputed in registers)."""
+    f = feats.contiguous()
+    g = _aligned16(grad.to(torch.float32))
+    frag = _radial_frag(params, kin, hidden, layers)
+    gf = torch.empty_like(f)
+    check(_lib.load().mnx_radial_bwd_f32(ptr(f), f.shape[0], kin, hidden, layers, ptr(frag), ptr(g), ptr(gf),
+                                         _stream(f)), "radial_hidden backward")
+    return gf
+
+
+@radial_hidden_backward.register_fake
+def _(grad, feats, params, kin, hidden, layers):
+    return torch.empty_like(feats)
+
+
+def _radial_setup(ctx, inputs, output):
+    feats, params, kin, hidden, layers = inputs
+    ctx.save_for_backward(feats, params)
+    ctx.cfg = (kin, hidden, layers)
+
+
+def _radial_bwd(ctx, grad):
+    feats, params = ctx.saved_tensors
+    if ctx.needs_input_grad[1]:
+        raise RuntimeError("molix::radial_hidden computes no parameter gradient; use the Sequential path "
+                           "when the radial MLP is trained")
+    gf = radial_hidden_backward(grad, feats, params, *ctx.cfg) if ctx.needs_input_grad[0] else None
+    return gf, None, None, None, None
+
+
+radial_hidden.register_autograd(_radial_bwd, setup_context=_radial_setup)

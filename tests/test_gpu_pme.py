@@ -93,3 +93,82 @@ def test_nacl_madelung_on_gpu(ops):
     e = float(e_dir) + float(e_rec) - k * alpha / math.sqrt(math.pi) * float(np.sum(q * q))
     madelung = -e / (len(q) / 2) / k
     assert abs(madelung - 1.747565) < 2e-5, madelung
+
+
+def _recip_gpu(ops, pos, q, box, grid, order, alpha, k, dtype):
+    mods = [torch.tensor(P.bspline_moduli(g_, order), dtype=dtype, device=DEV) for g_ in grid]
+    pt = torch.tensor(pos, dtype=dtype, device=DEV, requires_grad=True)
+    qt = torch.tensor(q, dtype=dtype, device=DEV, requires_grad=True)
+    e = ops.pme_reciprocal(pt, qt, torch.tensor(box, dtype=dtype, device=DEV), *grid, order, alpha, k, *mods)
+    gp, gq = torch.autograd.grad(e, (pt, qt))
+    return float(e), gp.cpu().numpy(), gq.cpu().numpy()
+
+
+@pytest.mark.parametrize("grid,order", [((5, 6, 7), 4), ((8, 8, 8), 8), ((9, 17, 24), 6), ((15, 16, 33), 5),
+                                        ((7, 30, 12), 3)])
+def test_reciprocal_mesh_shapes(ops, grid, order):
+    """Meshes smaller than one 8^3 brick, exact multiples, and partial last bricks (1..7 points),
+    in a triclinic cell, fp64 against the oracle."""
+    rng = np.random.default_rng(sum(grid) * 10 + order)
+    n = 300
+    box = np.array([[9.0, 0.0, 0.0], [1.5, 10.0, 0.0], [-2.0, 1.0, 11.0]])
+    frac = rng.uniform(-0.2, 1.2, (n, 3))  # also outside the cell: wrapped by the kernels
+    pos = frac @ box
+    q = rng.normal(size=n)
+    q -= q.mean()
+    alpha, k = 0.35, 138.935
+    e, gp, gq = _recip_gpu(ops, pos, q, box, grid, order, alpha, k, torch.float64)
+    mods = [P.bspline_moduli(g_, order) for g_ in grid]
+    re, rp, rq = P.reciprocal(pos, q, box, grid, order, alpha, k, mods)
+    assert abs(e - re) <= 1e-10 * abs(re), (e, re)
+    assert _rel(gp, rp) <= 1e-10
+    assert _rel(gq, rq) <= 1e-10
+
+
+def test_reciprocal_bitwise_reproducible(ops):
+    """The spread sums each mesh point in a fixed order: repeated runs agree bit for bit."""
+    rng = np.random.default_rng(11)
+    n, L = 4000, 35.0
+    pos = rng.uniform(0, L, (n, 3))
+    q = rng.normal(size=n)
+    q -= q.mean()
+    box = np.eye(3) * L
+    runs = [_recip_gpu(ops, pos, q, box, (40, 40, 40), 6, 0.3, 14.399645, torch.float32) for _ in range(3)]
+    for e, gp, gq in runs[1:]:
+        assert e == runs[0][0]
+        assert np.array_equal(gp, runs[0][1]) and np.array_equal(gq, runs[0][2])
+
+
+def test_direct_against_oracle_with_exclusions_and_padding(ops):
+    """Pair list in neighbor-list row order with -1 padding and exclusions; energy (energy-only
+    forward) and both derivatives (backward) against the fp64 oracle, fp32 and fp64."""
+    rng = np.random.default_rng(3)
+    n, L, rc = 900, 22.0, 6.0
+    pos = rng.uniform(0, L, (n, 3))
+    q = rng.normal(size=n)
+    q -= q.mean()
+    pt = torch.tensor(pos, device=DEV)
+    nb, d, dist, npairs = ops.get_neighbor_pairs(pt, rc, -1, torch.tensor(np.eye(3) * L, device=DEV))
+    nb, d, dist = nb.cpu().numpy(), d.cpu().numpy(), dist.cpu().numpy()
+    # symmetric exclusions from a random subset of listed pairs, descending, -1 padded
+    listed = np.flatnonzero(nb[0] >= 0)
+    sets = [set() for _ in range(n)]
+    for s in rng.choice(listed, size=600, replace=False):
+        a, b = int(nb[0][s]), int(nb[1][s])
+        if len(sets[a]) < 4 and len(sets[b]) < 4:
+            sets[a].add(b)
+            sets[b].add(a)
+    excl = -np.ones((n, 4), np.int32)
+    for i, s in enumerate(sets):
+        excl[i, :len(s)] = sorted(s, reverse=True)
+    alpha, k = 0.3, 14.399645
+    re, rp, rq = P.direct(pos, q, nb, d, dist, excl, alpha, k)
+    for dtype, tol in ((torch.float64, 1e-10), (torch.float32, 2e-5)):
+        p_ = torch.tensor(pos, dtype=dtype, device=DEV, requires_grad=True)
+        q_ = torch.tensor(q, dtype=dtype, device=DEV, requires_grad=True)
+        e = ops.pme_direct(p_, q_, torch.tensor(nb, device=DEV), torch.tensor(d, dtype=dtype, device=DEV),
+                           torch.tensor(dist, dtype=dtype, device=DEV), torch.tensor(excl, device=DEV), alpha, k)
+        gp, gq = torch.autograd.grad(e, (p_, q_))
+        assert abs(float(e) - re) <= tol * abs(re), (dtype, float(e), re)
+        assert _rel(gp.cpu().numpy(), rp) <= tol, dtype
+        assert _rel(gq.cpu().numpy(), rq) <= tol, dtype
