@@ -13,6 +13,9 @@ class _Config:
     # True: tensor-product backward walked by sender, without atomics (bitwise
     # reproducible gradients, slower on large graphs)
     deterministic: bool = False
+    # True: RadialWeightMLP runs its hidden stack as one fused HIP kernel when its
+    # parameters need no gradient (energy + forces); False: always the Sequential
+    fused_radial: bool = True
 
 
 config = _Config()

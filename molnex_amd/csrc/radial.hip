@@ -1,0 +1,368 @@
+// Hidden stack of the radial weight MLP, fused into one kernel per direction:
+//   h = silu(W_L ... silu(W_2 silu(W_1 f + b_1) + b_2) ... + b_L)
+// with f the (E, K) radial edge features and h (E, H) the input of the MLP's
+// last Linear (src/molrep/interaction/radial_mlp.py:38-93: [Linear(in, hidden) ->
+// SiLU] x num_layers, then Linear(hidden, out)).  The backward maps dL/dh to
+// dL/df, recomputing the forward in registers.
+//
+// One wavefront owns 32 edges.  Every layer is a v_mfma_f32_32x32x2f32 product
+// with the features on the M side and the 32 edges on the N side:
+//   out^T (H x 32) = W (H x K) . in^T (K x 32).
+// The D layout of an MFMA tile (lane l holds column l%32, i.e. one edge, and
+// rows 8*(r/4) + 4*(l/32) + r%4 in register r) is taken directly as the B
+// operand of the next layer by ordering the contraction index so that k-step s
+// of lane half h reads feature 8*(s/4) + 4*h + s%4 -- the feature that register
+// s%16 of tile s/16 holds.  Activations therefore stay in registers across
+// layers.  The weights are pre-arranged (k_radial_pack) in that k order,
+// "fragment" layout [tile][s/4][lane][s%4], so every A-operand read is one
+// coalesced 16-byte load per lane.
+
+#include "common.h"
+
+namespace mnx {
+namespace {
+
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kRadThreads = 256;  // four wavefronts, 32 edges each
+constexpr int kRadEdgesPerBlock = (kRadThreads / 64) * 32;
+constexpr int kRadMaxIn = 64;
+
+// Fragment buffer layout (floats): forward fragments of layers 0..L-1, backward
+// (transposed) fragments of layers 0..L-1, then the L x H biases.
+struct RadLayout {
+    int kin, kp, H, L;
+    __host__ __device__ int64_t fwd_size(int j) const {
+        return int64_t(H / 32) * ((j == 0 ? kp : H) / 8) * 256;
+    }
+    __host__ __device__ int64_t bwd_size(int j) const {
+        return int64_t(((j == 0 ? kp : H) + 31) / 32) * (H / 8) * 256;
+    }
+    __host__ __device__ int64_t fwd_off(int j) const {
+        int64_t o = 0;
+        for (int i = 0; i < j; ++i) o += fwd_size(i);
+        return o;
+    }
+    __host__ __device__ int64_t bwd_off(int j) const {
+        int64_t o = fwd_off(L);
+        for (int i = 0; i < j; ++i) o += bwd_size(i);
+        return o;
+    }
+    __host__ __device__ int64_t bias_off() const { return bwd_off(L); }
+    __host__ __device__ int64_t total() const { return bias_off() + int64_t(L) * H; }
+    // raw parameters: per layer W_j (H x K_j, row-major as torch.nn.Linear) then b_j (H)
+    __host__ __device__ int64_t raw_w(int j) const { return j == 0 ? 0 : int64_t(H) * kin + H + int64_t(j - 1) * (H * H + H); }
+    __host__ __device__ int64_t raw_b(int j) const { return raw_w(j) + int64_t(H) * (j == 0 ? kin : H); }
+    __host__ __device__ int64_t raw_total() const { return raw_w(L); }
+};
+
+// Builds the fragment buffer from the raw parameters; one thread per element.
+__global__ void k_radial_pack(const float* __restrict__ raw, RadLayout lay, float* __restrict__ frag) {
+    const int64_t idx = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (idx >= lay.total()) return;
+    float v = 0.f;
+    if (idx >= lay.bias_off()) {
+        const int64_t b = idx - lay.bias_off();
+        const int j = int(b / lay.H), m = int(b % lay.H);
+        v = raw[lay.raw_b(j) + m];
+    } else {
+        const bool bwd = idx >= lay.bwd_off(0);
+        int j = 0;
+        while (idx >= (bwd ? lay.bwd_off(j + 1) : lay.fwd_off(j + 1))) ++j;
+        const int64_t r = idx - (bwd ? lay.bwd_off(j) : lay.fwd_off(j));
+        const int kraw = j == 0 ? lay.kin : lay.H;
+        const int i = int(r % 4), lane = int((r / 4) % 64);
+        const int64_t rest = r / 256;
+        const int nq = bwd ? lay.H / 8 : (j == 0 ? lay.kp : lay.H) / 8;
+        const int q = int(rest % nq), t = int(rest / nq);
+        const int kstep = 8 * q + 4 * (lane / 32) + i;  // contraction index of this element
+        const int row = 32 * t + lane % 32;             // MFMA row (output feature, or input feature if bwd)
+        const float* W = raw + lay.raw_w(j);
+        if (!bwd) {
+            if (kstep < kraw) v = W[int64_t(row) * kraw + kstep];
+        } else {
+            if (row < kraw) v = W[int64_t(kstep) * kraw + row];
+        }
+    }
+    frag[idx] = v;
+}
+
+__device__ __forceinline__ float silu(float z) { return z / (1.f + expf(-z)); }
+
+__device__ __forceinline__ float silu_grad(float z) {
+    const float s = 1.f / (1.f + expf(-z));
+    return s * (1.f + z * (1.f - s));
+}
+
+__device__ __forceinline__ f32x4 frag4(const float* __restrict__ f, int t, int nq, int q, int lane) {
+    return *reinterpret_cast<const f32x4*>(f + ((int64_t(t) * nq + q) * 64 + lane) * 4);
+}
+
+// acc[t] += W(tile t) . in, contraction over K = 8 * NQ features held as in[s/16][s%16]
+template <int T, int NQ>
+__device__ __forceinline__ void mfma_layer(const float* __restrict__ f, const float (&in)[(NQ * 8) / 32 > 0 ? (NQ * 8) / 32 : 1][16],
+                                           f32x16 (&acc)[T], int lane) {
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) {
+#pragma unroll
+        for (int t = 0; t < T; ++t) {
+            const f32x4 a = frag4(f, t, NQ, q, lane);
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                acc[t] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i], in[q / 4][4 * (q % 4) + i], acc[t], 0, 0, 0);
+        }
+    }
+}
+
+// Layer 0: B operand read straight from the (E, kin) features; k-step 4q+i of lane half h = feature 8q+4h+i.
+template <int T>
+__device__ __forceinline__ void first_layer(const float* __restrict__ f, const float* __restrict__ feats, int64_t e,
+                                            bool valid, int kin, int kp, f32x16 (&acc)[T], int lane) {
+    const int nq = kp / 8, half = lane >> 5;
+    for (int q = 0; q < nq; ++q) {
+        float b[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int k = 8 * q + 4 * half + i;
+            b[i] = (valid && k < kin) ? feats[e * kin + k] : 0.f;
+        }
+#pragma unroll
+        for (int t = 0; t < T; ++t) {
+            const f32x4 a = frag4(f, t, nq, q, lane);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[t] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i], b[i], acc[t], 0, 0, 0);
+        }
+    }
+}
+
+template <int T>
+__device__ __forceinline__ void zero(f32x16 (&acc)[T]) {
+#pragma unroll
+    for (int t = 0; t < T; ++t)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[t][r] = 0.f;
+}
+
+// feature index of register r of tile t in lane half h
+__device__ __forceinline__ int dfeat(int t, int r, int half) { return 32 * t + 8 * (r / 4) + 4 * half + r % 4; }
+
+template <int H, int L>
+__global__ void __launch_bounds__(kRadThreads) k_radial_fwd(const float* __restrict__ feats, int64_t E, int kin,
+                                                            const float* __restrict__ frag, RadLayout lay,
+                                                            float* __restrict__ out) {
+    constexpr int T = H / 32;
+    const int lane = threadIdx.x & 63, half = lane >> 5;
+    const int64_t e0 = (int64_t(blockIdx.x) * (kRadThreads / 64) + threadIdx.x / 64) * 32;
+    if (e0 >= E) return;  // wave-uniform
+    const int64_t e = e0 + (lane & 31);
+    const bool valid = e < E;
+    const float* bias = frag + lay.bias_off();
+    f32x16 acc[T];
+    float act[T][16];
+    zero(acc);
+    first_layer<T>(frag + lay.fwd_off(0), feats, e, valid, kin, lay.kp, acc, lane);
+#pragma unroll
+    for (int j = 0; j < L; ++j) {
+        if (j > 0) {
+            zero(acc);
+            mfma_layer<T, H / 8>(frag + lay.fwd_off(j), act, acc, lane);
+        }
+#pragma unroll
+        for (int t = 0; t < T; ++t)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) act[t][r] = silu(acc[t][r] + bias[j * H + dfeat(t, r, half)]);
+    }
+    if (valid) {
+        float* o = out + e * H;
+#pragma unroll
+        for (int t = 0; t < T; ++t)
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const f32x4 v = {act[t][4 * g], act[t][4 * g + 1], act[t][4 * g + 2], act[t][4 * g + 3]};
+                *reinterpret_cast<f32x4*>(o + 32 * t + 8 * g + 4 * half) = v;
+            }
+    }
+}
+
+template <int H, int L>
+__global__ void __launch_bounds__(kRadThreads) k_radial_bwd(const float* __restrict__ feats, int64_t E, int kin,
+                                                            const float* __restrict__ frag, RadLayout lay,
+                                                            const float* __restrict__ grad_h,
+                                                            float* __restrict__ grad_feats) {
+    constexpr int T = H / 32;
+    const int lane = threadIdx.x & 63, half = lane >> 5;
+    const int64_t e0 = (int64_t(blockIdx.x) * (kRadThreads / 64) + threadIdx.x / 64) * 32;
+    if (e0 >= E) return;  // wave-uniform
+    const int64_t e = e0 + (lane & 31);
+    const bool valid = e < E;
+    const float* bias = frag + lay.bias_off();
+    // forward recompute, keeping the pre-activations z_j
+    float z[L][T][16];
+    float g[T][16];
+    f32x16 acc[T];
+    zero(acc);
+    first_layer<T>(frag + lay.fwd_off(0), feats, e, valid, kin, lay.kp, acc, lane);
+#pragma unroll
+    for (int j = 0; j < L; ++j) {
+        if (j > 0) {
+            zero(acc);
+            mfma_layer<T, H / 8>(frag + lay.fwd_off(j), g, acc, lane);  // g holds silu(z_{j-1})
+        }
+#pragma unroll
+        for (int t = 0; t < T; ++t)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                z[j][t][r] = acc[t][r] + bias[j * H + dfeat(t, r, half)];
+                g[t][r] = silu(z[j][t][r]);
+            }
+    }
+    // dL/dh in the D layout
+#pragma unroll
+    for (int t = 0; t < T; ++t)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            f32x4 v = {0.f, 0.f, 0.f, 0.f};
+            if (valid) v = *reinterpret_cast<const f32x4*>(grad_h + e * H + 32 * t + 8 * q + 4 * half);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) g[t][4 * q + i] = v[i];
+        }
+    // back through layers L-1 .. 1: g <- W_j^T (g * silu'(z_j))
+#pragma unroll
+    for (int j = L - 1; j >= 0; --j) {
+#pragma unroll
+        for (int t = 0; t < T; ++t)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) g[t][r] *= silu_grad(z[j][t][r]);
+        if (j == 0) break;
+        zero(acc);
+        mfma_layer<T, H / 8>(frag + lay.bwd_off(j), g, acc, lane);
+#pragma unroll
+        for (int t = 0; t < T; ++t)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) g[t][r] = acc[t][r];
+    }
+    // layer 0: dL/df^T (kp x 32) = W_0^T g, in ceil(kp / 32) row tiles
+    const int tiles0 = (lay.kp + 31) / 32;
+    for (int t0 = 0; t0 < tiles0; ++t0) {
+        f32x16 a0[1];
+        zero(a0);
+#pragma unroll
+        for (int q = 0; q < H / 8; ++q) {
+            const f32x4 a = frag4(frag + lay.bwd_off(0), t0, H / 8, q, lane);
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                a0[0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i], g[q / 4][4 * (q % 4) + i], a0[0], 0, 0, 0);
+        }
+        if (valid) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int k = dfeat(t0, r, half);
+                if (k < kin) grad_feats[e * kin + k] = a0[0][r];
+            }
+        }
+    }
+}
+
+RadLayout make_layout(int kin, int H, int L) { return RadLayout{kin, (kin + 7) & ~7, H, L}; }
+
+int check_shape(int kin, int H, int L) {
+    MNX_REQUIRE(kin > 0 && kin <= kRadMaxIn, "radial MLP input width %d not in [1, %d]", kin, kRadMaxIn);
+    const bool ok = ((H == 32 || H == 64) && L >= 1 && L <= 4) || (H == 128 && L >= 1 && L <= 2);
+    if (!ok)
+        return set_error(MNX_ERR_UNSUPPORTED,
+                         "radial MLP hidden stack %d x %d not compiled (32 or 64 wide up to 4 layers, 128 up to 2)", H,
+                         L);
+    return MNX_OK;
+}
+
+template <int H, int L>
+void launch_fwd(const float* feats, int64_t E, int kin, const float* frag, RadLayout lay, float* out, hipStream_t s) {
+    hipLaunchKernelGGL((k_radial_fwd<H, L>), dim3(ceil_div(E, kRadEdgesPerBlock)), dim3(kRadThreads), 0, s, feats, E,
+                       kin, frag, lay, out);
+}
+
+template <int H, int L>
+void launch_bwd(const float* feats, int64_t E, int kin, const float* frag, RadLayout lay, const float* gh, float* gf,
+                hipStream_t s) {
+    hipLaunchKernelGGL((k_radial_bwd<H, L>), dim3(ceil_div(E, kRadEdgesPerBlock)), dim3(kRadThreads), 0, s, feats, E,
+                       kin, frag, lay, gh, gf);
+}
+
+#define MNX_RAD_DISPATCH(FN, ...)                                     \
+    switch (H * 8 + L) {                                              \
+        case 32 * 8 + 1: FN<32, 1>(__VA_ARGS__); break;               \
+        case 32 * 8 + 2: FN<32, 2>(__VA_ARGS__); break;               \
+        case 32 * 8 + 3: FN<32, 3>(__VA_ARGS__); break;               \
+        case 32 * 8 + 4: FN<32, 4>(__VA_ARGS__); break;               \
+        case 64 * 8 + 1: FN<64, 1>(__VA_ARGS__); break;               \
+        case 64 * 8 + 2: FN<64, 2>(__VA_ARGS__); break;               \
+        case 64 * 8 + 3: FN<64, 3>(__VA_ARGS__); break;               \
+        case 64 * 8 + 4: FN<64, 4>(__VA_ARGS__); break;               \
+        case 128 * 8 + 1: FN<128, 1>(__VA_ARGS__); break;             \
+        default: FN<128, 2>(__VA_ARGS__); break;                      \
+    }
+
+}  // namespace
+}  // namespace mnx
+
+using namespace mnx;
+
+extern "C" {
+
+int64_t mnx_radial_raw_floats(int32_t kin, int32_t hidden, int32_t layers) {
+    if (check_shape(kin, hidden, layers)) return -1;
+    return make_layout(kin, hidden, layers).raw_total();
+}
+
+int64_t mnx_radial_frag_floats(int32_t kin, int32_t hidden, int32_t layers) {
+    if (check_shape(kin, hidden, layers)) return -1;
+    return make_layout(kin, hidden, layers).total();
+}
+
+int mnx_radial_pack_f32(const float* raw, int32_t kin, int32_t hidden, int32_t layers, float* frag,
+                        mnx_stream_t stream) {
+    clear_error();
+    int rc = check_shape(kin, hidden, layers);
+    if (rc) return rc;
+    MNX_REQUIRE(raw && frag, "null pointer argument");
+    const RadLayout lay = make_layout(kin, hidden, layers);
+    hipLaunchKernelGGL(k_radial_pack, dim3(ceil_div(lay.total(), 256)), dim3(256), 0, (hipStream_t)stream, raw, lay,
+                       frag);
+    MNX_CHECK_LAUNCH();
+    return MNX_OK;
+}
+
+int mnx_radial_fwd_f32(const float* feats, int64_t num_edges, int32_t kin, int32_t hidden, int32_t layers,
+                       const float* frag, float* out, mnx_stream_t stream) {
+    clear_error();
+    int rc = check_shape(kin, hidden, layers);
+    if (rc) return rc;
+    MNX_REQUIRE(num_edges >= 0 && num_edges < (int64_t(1) << 36), "edge count out of range");
+    if (num_edges == 0) return MNX_OK;
+    MNX_REQUIRE(feats && frag && out, "null pointer argument");
+    MNX_REQUIRE(((uintptr_t)frag | (uintptr_t)out) % 16 == 0, "frag and out must be 16-byte aligned");
+    const int H = hidden, L = layers;
+    const RadLayout lay = make_layout(kin, H, L);
+    MNX_RAD_DISPATCH(launch_fwd, feats, num_edges, kin, frag, lay, out, (hipStream_t)stream);
+    MNX_CHECK_LAUNCH();
+    return MNX_OK;
+}
+
+int mnx_radial_bwd_f32(const float* feats, int64_t num_edges, int32_t kin, int32_t hidden, int32_t layers,
+                       const float* frag, const float* grad_h, float* grad_feats, mnx_stream_t stream) {
+    clear_error();
+    int rc = check_shape(kin, hidden, layers);
+    if (rc) return rc;
+    MNX_REQUIRE(num_edges >= 0 && num_edges < (int64_t(1) << 36), "edge count out of range");
+    if (num_edges == 0) return MNX_OK;
+    MNX_REQUIRE(feats && frag && grad_h && grad_feats, "null pointer argument");
+    MNX_REQUIRE(((uintptr_t)frag | (uintptr_t)grad_h) % 16 == 0, "frag and grad_h must be 16-byte aligned");
+    const int H = hidden, L = layers;
+    const RadLayout lay = make_layout(kin, H, L);
+    MNX_RAD_DISPATCH(launch_bwd, feats, num_edges, kin, frag, lay, grad_h, grad_feats, (hipStream_t)stream);
+    MNX_CHECK_LAUNCH();
+    return MNX_OK;
+}
+
+}  // extern "C"

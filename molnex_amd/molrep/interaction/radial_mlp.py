@@ -5,6 +5,11 @@ and 2944 outputs a 30.8 GB result).  For many rows it runs as row chunks of 2^18
 straight into one output (hipBLASLt picks a faster kernel for chunk-sized problems: 11.4 ms
 instead of 14.0 ms at that size on MI355X), with an explicit backward doing the same.
 ``.mlp`` stays the reference's ``Sequential`` so parameters and their names are unchanged.
+
+When the hidden Linears' parameters need no gradient (energy + forces with fixed weights)
+the hidden stack ``[Linear -> SiLU] x num_layers`` runs as one fused HIP kernel
+(``molix::radial_hidden``, gradient w.r.t. the edge features only); otherwise, and for
+shapes the kernel does not cover, it runs as the ``Sequential``.
 """
 
 from __future__ import annotations
@@ -12,6 +17,9 @@ from __future__ import annotations
 import torch
 import torch.nn as nn
 from pydantic import BaseModel, ConfigDict, Field
+
+from ... import kernels
+from ...config import config
 
 _CHUNK = 1 << 18
 
@@ -70,10 +78,27 @@ class RadialWeightMLP(nn.Module):
         layers.append(nn.Linear(cur, out_dim))
         self.mlp = nn.Sequential(*layers)
 
+    def _fused_hidden(self, h: torch.Tensor) -> bool:
+        if not (config.fused_radial and h.is_cuda and h.dim() == 2 and h.dtype == torch.float32):
+            return False
+        hidden = list(self.mlp[:-1])
+        if not all(isinstance(m, nn.SiLU) for m in hidden[1::2]) or any(
+                not isinstance(m, nn.Linear) or m.bias is None for m in hidden[0::2]):
+            return False
+        if torch.is_grad_enabled() and any(p.requires_grad for p in self.mlp[:-1].parameters()):
+            return False
+        c = self.config
+        return kernels.radial_supported(c.in_dim, c.hidden_dim, c.num_layers)
+
     def forward(self, edge_feats: torch.Tensor) -> torch.Tensor:
         h = edge_feats
-        for layer in self.mlp[:-1]:
-            h = layer(h)
+        if self._fused_hidden(h):
+            c = self.config
+            raw = torch.cat([t.detach().reshape(-1) for m in self.mlp[:-1:2] for t in (m.weight, m.bias)])
+            h = kernels.radial_hidden(h, raw, c.in_dim, c.hidden_dim, c.num_layers)
+        else:
+            for layer in self.mlp[:-1]:
+                h = layer(h)
         last = self.mlp[-1]
         if h.dim() == 2 and h.shape[0] > _CHUNK and h.is_cuda:
             return _ChunkedLinear.apply(h, last.weight, last.bias)
