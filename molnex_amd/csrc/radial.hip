@@ -14,8 +14,8 @@
 // of lane half h reads feature 8*(s/4) + 4*h + s%4 -- the feature that register
 // s%16 of tile s/16 holds.  Activations therefore stay in registers across
 // layers.  The weights are pre-arranged (k_radial_pack) in that k order,
-// "fragment" layout [tile][s/4][lane][s%4], so every A-operand read is one
-// coalesced 16-byte load per lane.
+// "fragment" layout [tile][s/4][lane][s%4], staged through LDS, so every
+// A-operand read is one conflict-free 16-byte LDS read per lane.
 
 #include "common.h"
 
@@ -88,38 +88,77 @@ __global__ void k_radial_pack(const float* __restrict__ raw, RadLayout lay, floa
     frag[idx] = v;
 }
 
-__device__ __forceinline__ float silu(float z) { return z / (1.f + expf(-z)); }
+// sigmoid(z) = 1 / (1 + 2^(-z log2 e)) from the hardware exp2 and reciprocal (a few
+// ulp; the IEEE-exact expf and division would cost ~28 VALU instructions per
+// element, as much issue time as the MFMAs of a layer).  Saturates correctly:
+// z -> -inf gives 1/inf = 0, z -> +inf gives 1.
+__device__ __forceinline__ float sigmoid(float z) {
+    return __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(z * -1.4426950408889634f));
+}
+
+__device__ __forceinline__ float silu(float z) { return z * sigmoid(z); }
 
 __device__ __forceinline__ float silu_grad(float z) {
-    const float s = 1.f / (1.f + expf(-z));
+    const float s = sigmoid(z);
     return s * (1.f + z * (1.f - s));
 }
 
-__device__ __forceinline__ f32x4 frag4(const float* __restrict__ f, int t, int nq, int q, int lane) {
-    return *reinterpret_cast<const f32x4*>(f + ((int64_t(t) * nq + q) * 64 + lane) * 4);
+// Fragments reach the MFMAs through LDS: a workgroup stages up to kRadChunk
+// floats of one layer's fragments (whole output tiles) at a time and its four
+// wavefronts share them.
+constexpr int kRadChunk = 8192;  // floats (32 KB)
+
+struct RadShared {
+    f32x4 frag[kRadChunk / 4];
+    float bias[4 * 128];
+};
+
+// Copies n floats (a multiple of 4, 16-byte aligned) of fragments into LDS; the
+// caller brackets it with barriers.
+__device__ __forceinline__ void stage(const float* __restrict__ src, int n, f32x4* __restrict__ dst) {
+    const f32x4* s4 = reinterpret_cast<const f32x4*>(src);
+    for (int i = threadIdx.x; i < n / 4; i += kRadThreads) dst[i] = s4[i];
 }
 
-// acc[t] += W(tile t) . in, contraction over K = 8 * NQ features held as in[s/16][s%16]
+// acc[t] += W(tile t) . in over K = 8 * NQ features held as in[s/16][s%16]; the
+// layer's fragments f ([T][NQ][64 lanes][4]) are staged in chunks of whole tiles.
+// Every wavefront of the workgroup must call it (barriers inside).
 template <int T, int NQ>
-__device__ __forceinline__ void mfma_layer(const float* __restrict__ f, const float (&in)[(NQ * 8) / 32 > 0 ? (NQ * 8) / 32 : 1][16],
-                                           f32x16 (&acc)[T], int lane) {
+__device__ __forceinline__ void mfma_layer(const float* __restrict__ f, const float (&in)[NQ / 4][16],
+                                           f32x16 (&acc)[T], RadShared& sh, int lane) {
+    constexpr int kTileFloats = NQ * 256;
+    constexpr int kTPC = kRadChunk / kTileFloats < T ? kRadChunk / kTileFloats : T;  // tiles per chunk
+    static_assert(kTPC >= 1, "one output tile of fragments must fit the staging area");
 #pragma unroll
-    for (int q = 0; q < NQ; ++q) {
+    for (int t0 = 0; t0 < T; t0 += kTPC) {
+        __syncthreads();
+        stage(f + t0 * kTileFloats, (T - t0 < kTPC ? T - t0 : kTPC) * kTileFloats, sh.frag);
+        __syncthreads();
 #pragma unroll
-        for (int t = 0; t < T; ++t) {
-            const f32x4 a = frag4(f, t, NQ, q, lane);
+        for (int q = 0; q < NQ; ++q) {
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
-                acc[t] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i], in[q / 4][4 * (q % 4) + i], acc[t], 0, 0, 0);
+            for (int tt = 0; tt < kTPC; ++tt) {
+                if (t0 + tt < T) {
+                    const f32x4 a = sh.frag[(tt * NQ + q) * 64 + lane];
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                        acc[t0 + tt] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i], in[q / 4][4 * (q % 4) + i],
+                                                                           acc[t0 + tt], 0, 0, 0);
+                }
+            }
         }
     }
 }
 
-// Layer 0: B operand read straight from the (E, kin) features; k-step 4q+i of lane half h = feature 8q+4h+i.
+// Layer 0: B operand read straight from the (E, kin) features; k-step 4q+i of lane
+// half h = feature 8q+4h+i.  Its fragments (T x kp/8 blocks) fit one chunk.
 template <int T>
 __device__ __forceinline__ void first_layer(const float* __restrict__ f, const float* __restrict__ feats, int64_t e,
-                                            bool valid, int kin, int kp, f32x16 (&acc)[T], int lane) {
+                                            bool valid, int kin, int kp, f32x16 (&acc)[T], RadShared& sh, int lane) {
     const int nq = kp / 8, half = lane >> 5;
+    __syncthreads();
+    stage(f, T * nq * 256, sh.frag);
+    __syncthreads();
     for (int q = 0; q < nq; ++q) {
         float b[4];
 #pragma unroll
@@ -129,7 +168,7 @@ __device__ __forceinline__ void first_layer(const float* __restrict__ f, const f
         }
 #pragma unroll
         for (int t = 0; t < T; ++t) {
-            const f32x4 a = frag4(f, t, nq, q, lane);
+            const f32x4 a = sh.frag[(t * nq + q) * 64 + lane];
 #pragma unroll
             for (int i = 0; i < 4; ++i) acc[t] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i], b[i], acc[t], 0, 0, 0);
         }
@@ -147,31 +186,37 @@ __device__ __forceinline__ void zero(f32x16 (&acc)[T]) {
 // feature index of register r of tile t in lane half h
 __device__ __forceinline__ int dfeat(int t, int r, int half) { return 32 * t + 8 * (r / 4) + 4 * half + r % 4; }
 
+// Biases into LDS (read once per workgroup); visible after the next barrier.
+__device__ __forceinline__ void stage_bias(const float* __restrict__ b, int n, RadShared& sh) {
+    for (int i = threadIdx.x; i < n; i += kRadThreads) sh.bias[i] = b[i];
+}
+
+// Wavefronts past the last edge still run (all lanes invalid) because the
+// workgroup shares barriers; they store nothing.
 template <int H, int L>
 __global__ void __launch_bounds__(kRadThreads) k_radial_fwd(const float* __restrict__ feats, int64_t E, int kin,
                                                             const float* __restrict__ frag, RadLayout lay,
                                                             float* __restrict__ out) {
     constexpr int T = H / 32;
+    __shared__ RadShared sh;
     const int lane = threadIdx.x & 63, half = lane >> 5;
-    const int64_t e0 = (int64_t(blockIdx.x) * (kRadThreads / 64) + threadIdx.x / 64) * 32;
-    if (e0 >= E) return;  // wave-uniform
-    const int64_t e = e0 + (lane & 31);
+    const int64_t e = (int64_t(blockIdx.x) * (kRadThreads / 64) + threadIdx.x / 64) * 32 + (lane & 31);
     const bool valid = e < E;
-    const float* bias = frag + lay.bias_off();
+    stage_bias(frag + lay.bias_off(), L * H, sh);
     f32x16 acc[T];
     float act[T][16];
     zero(acc);
-    first_layer<T>(frag + lay.fwd_off(0), feats, e, valid, kin, lay.kp, acc, lane);
+    first_layer<T>(frag + lay.fwd_off(0), feats, e, valid, kin, lay.kp, acc, sh, lane);
 #pragma unroll
     for (int j = 0; j < L; ++j) {
         if (j > 0) {
             zero(acc);
-            mfma_layer<T, H / 8>(frag + lay.fwd_off(j), act, acc, lane);
+            mfma_layer<T, H / 8>(frag + lay.fwd_off(j), act, acc, sh, lane);
         }
 #pragma unroll
         for (int t = 0; t < T; ++t)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) act[t][r] = silu(acc[t][r] + bias[j * H + dfeat(t, r, half)]);
+            for (int r = 0; r < 16; ++r) act[t][r] = silu(acc[t][r] + sh.bias[j * H + dfeat(t, r, half)]);
     }
     if (valid) {
         float* o = out + e * H;
@@ -191,33 +236,35 @@ __global__ void __launch_bounds__(kRadThreads) k_radial_bwd(const float* __restr
                                                             const float* __restrict__ grad_h,
                                                             float* __restrict__ grad_feats) {
     constexpr int T = H / 32;
+    __shared__ RadShared sh;
     const int lane = threadIdx.x & 63, half = lane >> 5;
-    const int64_t e0 = (int64_t(blockIdx.x) * (kRadThreads / 64) + threadIdx.x / 64) * 32;
-    if (e0 >= E) return;  // wave-uniform
-    const int64_t e = e0 + (lane & 31);
+    const int64_t e = (int64_t(blockIdx.x) * (kRadThreads / 64) + threadIdx.x / 64) * 32 + (lane & 31);
     const bool valid = e < E;
-    const float* bias = frag + lay.bias_off();
-    // forward recompute, keeping the pre-activations z_j
-    float z[L][T][16];
+    stage_bias(frag + lay.bias_off(), L * H, sh);
+    // forward recompute, keeping the pre-activations z_0 .. z_{L-2}; the last
+    // layer's pre-activation stays in acc (its activation is not needed)
+    float z[L > 1 ? L - 1 : 1][T][16];
     float g[T][16];
     f32x16 acc[T];
     zero(acc);
-    first_layer<T>(frag + lay.fwd_off(0), feats, e, valid, kin, lay.kp, acc, lane);
+    first_layer<T>(frag + lay.fwd_off(0), feats, e, valid, kin, lay.kp, acc, sh, lane);
 #pragma unroll
     for (int j = 0; j < L; ++j) {
         if (j > 0) {
             zero(acc);
-            mfma_layer<T, H / 8>(frag + lay.fwd_off(j), g, acc, lane);  // g holds silu(z_{j-1})
+            mfma_layer<T, H / 8>(frag + lay.fwd_off(j), g, acc, sh, lane);  // g holds silu(z_{j-1})
         }
+        if (j < L - 1) {
 #pragma unroll
-        for (int t = 0; t < T; ++t)
+            for (int t = 0; t < T; ++t)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                z[j][t][r] = acc[t][r] + bias[j * H + dfeat(t, r, half)];
-                g[t][r] = silu(z[j][t][r]);
-            }
+                for (int r = 0; r < 16; ++r) {
+                    z[j][t][r] = acc[t][r] + sh.bias[j * H + dfeat(t, r, half)];
+                    g[t][r] = silu(z[j][t][r]);
+                }
+        }
     }
-    // dL/dh in the D layout
+    // g = dL/dh * silu'(z_{L-1}), dL/dh read in the D layout
 #pragma unroll
     for (int t = 0; t < T; ++t)
 #pragma unroll
@@ -225,31 +272,32 @@ __global__ void __launch_bounds__(kRadThreads) k_radial_bwd(const float* __restr
             f32x4 v = {0.f, 0.f, 0.f, 0.f};
             if (valid) v = *reinterpret_cast<const f32x4*>(grad_h + e * H + 32 * t + 8 * q + 4 * half);
 #pragma unroll
-            for (int i = 0; i < 4; ++i) g[t][4 * q + i] = v[i];
+            for (int i = 0; i < 4; ++i) {
+                const int r = 4 * q + i;
+                g[t][r] = v[i] * silu_grad(acc[t][r] + sh.bias[(L - 1) * H + dfeat(t, r, half)]);
+            }
         }
-    // back through layers L-1 .. 1: g <- W_j^T (g * silu'(z_j))
+    // back through layers L-1 .. 1: g <- (W_j^T g) * silu'(z_{j-1})
 #pragma unroll
-    for (int j = L - 1; j >= 0; --j) {
-#pragma unroll
-        for (int t = 0; t < T; ++t)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) g[t][r] *= silu_grad(z[j][t][r]);
-        if (j == 0) break;
+    for (int j = L - 1; j >= 1; --j) {
         zero(acc);
-        mfma_layer<T, H / 8>(frag + lay.bwd_off(j), g, acc, lane);
+        mfma_layer<T, H / 8>(frag + lay.bwd_off(j), g, acc, sh, lane);
 #pragma unroll
         for (int t = 0; t < T; ++t)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) g[t][r] = acc[t][r];
+            for (int r = 0; r < 16; ++r) g[t][r] = acc[t][r] * silu_grad(z[j - 1][t][r]);
     }
-    // layer 0: dL/df^T (kp x 32) = W_0^T g, in ceil(kp / 32) row tiles
+    // layer 0: dL/df^T (kp x 32) = W_0^T g, in ceil(kp / 32) <= 2 row tiles (one chunk)
     const int tiles0 = (lay.kp + 31) / 32;
+    __syncthreads();
+    stage(frag + lay.bwd_off(0), tiles0 * (H / 8) * 256, sh.frag);
+    __syncthreads();
     for (int t0 = 0; t0 < tiles0; ++t0) {
         f32x16 a0[1];
         zero(a0);
 #pragma unroll
         for (int q = 0; q < H / 8; ++q) {
-            const f32x4 a = frag4(frag + lay.bwd_off(0), t0, H / 8, q, lane);
+            const f32x4 a = sh.frag[(t0 * (H / 8) + q) * 64 + lane];
 #pragma unroll
             for (int i = 0; i < 4; ++i)
                 a0[0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i], g[q / 4][4 * (q % 4) + i], a0[0], 0, 0, 0);
