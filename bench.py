@@ -295,7 +295,7 @@ def full_step_bench(args, dev):
 
     def step():
         p = pos.detach().clone().requires_grad_(True)
-        bond_diff = p[edge_index[:, 1]] - p[edge_index[:, 0]] - shifts
+        bond_diff = torch.ops.molix.bond_vectors(p, edge_index, shifts)
         bond_dist = bond_diff.norm(dim=-1).clamp(min=1e-6)
         feats = enc(Z=Z, bond_dist=bond_dist, bond_diff=bond_diff, edge_index=edge_index)
         pooled = model.pool(feats)

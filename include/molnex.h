@@ -261,6 +261,19 @@ int mnx_sc_bwd_f32(int32_t config, const float* A, const int64_t* types, const f
                    mnx_stream_t stream);
 
 /* ------------------------------------------------------------------------ */
+/* Bond vectors diff[e] = pos[ei[e][1]] - pos[ei[e][0]] - shifts[e] (shifts  */
+/* may be NULL) for edge_index rows [sender, receiver], the reference's      */
+/* bond_diff = pos[target] - pos[source] (src/molix/data/tasks/              */
+/* neighbor_list.py:86-95), and its gradient grad_pos [n][3] (overwritten)   */
+/* = per atom, sum of grad_diff over its incoming minus its outgoing edges.  */
+/* Edges with an endpoint outside [0, n) give NaN and no gradient.           */
+/* ------------------------------------------------------------------------ */
+int mnx_bond_vectors_f32(const float* pos, int64_t num_atoms, const int64_t* edge_index,
+                         const float* shifts, int64_t num_edges, float* diff, mnx_stream_t stream);
+int mnx_bond_vectors_bwd_f32(const int64_t* edge_index, const float* grad_diff, int64_t num_edges,
+                             int64_t num_atoms, float* grad_pos, mnx_stream_t stream);
+
+/* ------------------------------------------------------------------------ */
 /* Hidden stack of the radial weight MLP (replaces mlp[:-1] of               */
 /* RadialWeightMLP, src/molrep/interaction/radial_mlp.py:38-93:              */
 /* [Linear(in, hidden) -> SiLU] x layers) for the forward and the gradient   */

@@ -14,6 +14,7 @@ Ops
 ``molix::edge_csr``             receiver CSR of an (E, 2) edge list
 ``molix::tp_scatter``           channelwise TP + scatter-sum (``cuet.ChannelWiseTensorProduct``)
 ``molix::radial_hidden``        fused hidden stack of the radial weight MLP (gradient w.r.t. its input)
+``molix::bond_vectors``         pos[receiver] - pos[sender] - shift per edge, with its position gradient
 """
 
 from __future__ import annotations
@@ -802,3 +803,65 @@ def _radial_bwd(ctx, grad):
 
 
 radial_hidden.register_autograd(_radial_bwd, setup_context=_radial_setup)
+
+
+# ---------------------------------------------------------------------------
+# Bond vectors
+# ---------------------------------------------------------------------------
+
+@torch.library.custom_op("molix::bond_vectors", mutates_args=(), device_types="cuda")
+def bond_vectors(positions: Tensor, edge_index: Tensor, shifts: Tensor | None = None) -> Tensor:
+    """``positions[edge_index[:, 1]] - positions[edge_index[:, 0]] - shifts`` for an (E, 2) edge list of
+    [sender, receiver] rows: the reference's ``bond_diff = pos[target] - pos[source]``
+    (``src/molix/data/tasks/neighbor_list.py:86-95``).  Backward: one kernel, receiver terms summed
+    over each wavefront's runs of equal receivers (neighbor-list order), sender terms atomically."""
+    _require_gpu("bond_vectors", positions, edge_index, shifts)
+    if positions.dtype != torch.float32:
+        raise TypeError("bond_vectors: positions must be float32")
+    pos = positions.detach().contiguous()
+    ei = edge_index.to(torch.int64).contiguous()
+    if ei.dim() != 2 or ei.shape[1] != 2:
+        raise ValueError("edge_index must be (E, 2)")
+    sh = None if shifts is None else shifts.detach().to(torch.float32).reshape(-1, 3).contiguous()
+    if sh is not None and sh.shape[0] != ei.shape[0]:
+        raise ValueError("shifts must be (E, 3)")
+    out = pos.new_empty(ei.shape[0], 3)
+    check(_lib.load().mnx_bond_vectors_f32(ptr(pos), pos.shape[0], ptr(ei), ptr(sh), ei.shape[0], ptr(out),
+                                           _stream(pos)), "bond_vectors")
+    return out
+
+
+@bond_vectors.register_fake
+def _(positions, edge_index, shifts=None):
+    return positions.new_empty(edge_index.shape[0], 3)
+
+
+@torch.library.custom_op("molix::bond_vectors_backward", mutates_args=(), device_types="cuda")
+def bond_vectors_backward(grad: Tensor, edge_index: Tensor, num_atoms: int) -> Tensor:
+    ei = edge_index.to(torch.int64).contiguous()
+    g = grad.to(torch.float32).contiguous()
+    gpos = g.new_empty(num_atoms, 3)
+    check(_lib.load().mnx_bond_vectors_bwd_f32(ptr(ei), ptr(g), ei.shape[0], num_atoms, ptr(gpos), _stream(g)),
+          "bond_vectors backward")
+    return gpos
+
+
+@bond_vectors_backward.register_fake
+def _(grad, edge_index, num_atoms):
+    return grad.new_empty(num_atoms, 3)
+
+
+def _bond_setup(ctx, inputs, output):
+    positions, edge_index = inputs[0], inputs[1]
+    ctx.save_for_backward(edge_index)
+    ctx.num_atoms = positions.shape[0]
+
+
+def _bond_bwd(ctx, grad):
+    (edge_index,) = ctx.saved_tensors
+    gpos = bond_vectors_backward(grad, edge_index, ctx.num_atoms) if ctx.needs_input_grad[0] else None
+    gsh = -grad if (len(ctx.needs_input_grad) > 2 and ctx.needs_input_grad[2]) else None
+    return gpos, None, gsh
+
+
+bond_vectors.register_autograd(_bond_bwd, setup_context=_bond_setup)

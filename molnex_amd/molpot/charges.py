@@ -6,6 +6,22 @@ import torch
 import torch.nn as nn
 
 
+class _PerGraph(torch.autograd.Function):
+    """``values[batch]`` whose backward is an ``index_add_`` (atomic) instead of the sort-based
+    accumulate of advanced indexing (~0.8 ms for 50k atoms into one graph)."""
+
+    @staticmethod
+    def forward(ctx, values, batch):
+        ctx.save_for_backward(batch)
+        ctx.n = values.shape[0]
+        return values.index_select(0, batch)
+
+    @staticmethod
+    def backward(ctx, g):
+        (batch,) = ctx.saved_tensors
+        return g.new_zeros(ctx.n).index_add_(0, batch, g), None
+
+
 class ChargeHead(nn.Module):
     def __init__(self, feature_dim: int, hidden_dim: int = 64, total_charge: float = 0.0):
         super().__init__()
@@ -20,4 +36,4 @@ class ChargeHead(nn.Module):
         s = torch.zeros(num_graphs, dtype=raw.dtype, device=raw.device).index_add_(0, batch, raw)
         cnt = torch.zeros(num_graphs, dtype=raw.dtype, device=raw.device).index_add_(0, batch, torch.ones_like(raw))
         shift = (self.total_charge - s) / cnt.clamp(min=1)
-        return {"charge": raw + shift[batch]}
+        return {"charge": raw + _PerGraph.apply(shift, batch)}

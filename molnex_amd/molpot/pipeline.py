@@ -1,13 +1,15 @@
 """Energy + forces composition around an encoder, as the reference composes it
 (tests/test_molzoo/test_symmetry.py:88-124): recompute bond vectors from
 positions (so autograd reaches them), encode, mean over layers, per-atom energy
-MLP, per-graph sum, forces = -dE/dpos."""
+MLP, per-graph sum, forces = -dE/dpos.  The bond vectors come from
+``molix::bond_vectors`` (one gather kernel forward, one kernel backward)."""
 
 from __future__ import annotations
 
 import torch
 import torch.nn as nn
 
+from .. import kernels
 from .derivation import EnergyAggregation, ForceDerivation
 from .heads import AtomicEnergyMLP
 from .pooling import LayerPooling
@@ -25,7 +27,7 @@ class EnergyForceModel(nn.Module):
     def forward(self, Z, pos, edge_index, batch, num_graphs: int, compute_forces: bool = True):
         if compute_forces and not pos.requires_grad:
             pos = pos.requires_grad_(True)
-        bond_diff = pos[edge_index[:, 1]] - pos[edge_index[:, 0]]
+        bond_diff = kernels.bond_vectors(pos, edge_index)
         bond_dist = bond_diff.norm(dim=-1).clamp(min=1e-6)
         feats = self.encoder(Z=Z, bond_dist=bond_dist, bond_diff=bond_diff, edge_index=edge_index)
         energy = self.aggregate(self.energy(self.pool(feats)), batch, num_graphs)

@@ -113,8 +113,9 @@ class InteractionBlock(nn.Module):
         tp_weights = self.radial_mlp(edge_feats)
         messages = self.conv_tp(node_features=node_feats_up, edge_angular=edge_attrs, edge_index=edge_index,
                                 tp_weights=tp_weights)
-        messages = messages / self.avg_num_neighbors
-        return self.linear(messages), sc
+        # linear(messages / avg) == linear(messages) / avg; scaling the linear's output
+        # touches (nodes x hidden) values instead of (nodes x TP-output) ones
+        return self.linear(messages) / self.avg_num_neighbors, sc
 
 
 class MACESpec(BaseModel):
