@@ -261,6 +261,23 @@ int mnx_sc_bwd_f32(int32_t config, const float* A, const int64_t* types, const f
                    mnx_stream_t stream);
 
 /* ------------------------------------------------------------------------ */
+/* Equivariant (ir_mul) block linear, one output irrep block per call        */
+/* (replaces the cuet.Linear of src/molrep/interaction/linear.py:43-105):    */
+/*   out[n*out_stride + out_off + i*out_comp + p] = sum_k A_k * w[k][p]       */
+/* for nodes n < R, components i < d, columns p < N, where k runs over the   */
+/* nseg input segments in order, segment s contributing seg_len[s] values    */
+/* a[n*a_stride + seg_col[s] + i*seg_comp[s] + 0..seg_len[s]-1].  w is       */
+/* (sum seg_len) x N row-major (weights pre-scaled by the caller); nseg = 0  */
+/* writes zeros.  seg_len multiples of 8; a_stride, seg_col, seg_comp        */
+/* multiples of 4; a 16-byte aligned; at most 8 segments.  Segment arrays    */
+/* are host memory.                                                          */
+/* ------------------------------------------------------------------------ */
+int mnx_block_linear_f32(const float* a, int64_t a_stride, int32_t nseg, const int64_t* seg_col,
+                         const int32_t* seg_comp, const int32_t* seg_len, const float* w, int32_t N,
+                         int64_t R, int32_t d, float* out, int64_t out_stride, int64_t out_off,
+                         int32_t out_comp, mnx_stream_t stream);
+
+/* ------------------------------------------------------------------------ */
 /* Bond vectors diff[e] = pos[ei[e][1]] - pos[ei[e][0]] - shifts[e] (shifts  */
 /* may be NULL) for edge_index rows [sender, receiver], the reference's      */
 /* bond_diff = pos[target] - pos[source] (src/molix/data/tasks/              */

@@ -1,0 +1,167 @@
+// Equivariant (ir_mul) block linear on MFMA: one output irrep block
+//   out[n][off + i*N + p] = sum_k A[(n, i)][k] * W[k][p]
+// where row (n, i) of A (node n, irrep component i < d) concatenates
+// segments of the input rows: segment s contributes len_s values starting at
+// a[n*stride + col_s + i*comp_s].  This is cuet.Linear / e3nn Linear in ir_mul
+// layout (src/molrep/interaction/linear.py:43-105): for an output block
+// mul_o x ir the segments are the input blocks of the same irrep and W their
+// stacked (mul_in x mul_o) weights, scaled by 1/sqrt(fan_in).  The gradient
+// with respect to an input block is the same product with the output-gradient
+// blocks as segments and the transposed weights.
+//
+// Each wavefront owns 32 rows (M side of v_mfma_f32_32x32x2f32) and up to 128
+// output columns (N side, NT tiles); A is read straight from the strided input
+// (16 bytes per lane, no gather copy), W is staged through LDS in 64-row
+// chunks in MFMA fragment order, and the D tiles are stored 128 contiguous
+// bytes per row into the output block.
+
+#include "common.h"
+
+namespace mnx {
+namespace {
+
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kLinThreads = 256;  // four wavefronts x 32 rows
+constexpr int kLinKC = 64;        // rows of W staged per pass
+constexpr int kLinMaxSeg = 8;
+
+struct LinSeg {
+    int64_t col;  // column of component 0
+    int32_t comp; // column step between components
+    int32_t len;  // values contributed (multiple of 8)
+};
+
+struct LinArgs {
+    const float* a;
+    int64_t a_stride;
+    int32_t nseg, K;
+    LinSeg seg[kLinMaxSeg];
+    const float* w;  // K x N row-major
+    int32_t N, d;
+    int64_t R;
+    float* out;
+    int64_t out_stride, out_off;
+    int32_t out_comp;
+};
+
+template <int NT>
+__global__ void __launch_bounds__(kLinThreads) k_block_linear(LinArgs p) {
+    __shared__ f32x4 sw[kLinKC / 8][NT][kWave];
+    const int lane = threadIdx.x & 63, half = lane >> 5, wave = threadIdx.x >> 6;
+    const int64_t rows = p.R * p.d;
+    const int64_t row0 = (int64_t(blockIdx.x) * (kLinThreads / kWave) + wave) * 32;
+    const int64_t row = row0 + (lane & 31);
+    const bool valid = row < rows;
+    const int64_t n = valid ? row / p.d : 0;
+    const int ci = valid ? int(row - n * p.d) : 0;
+    const float* arow = p.a + n * p.a_stride;
+    const int col0 = blockIdx.y * NT * 32;
+    f32x16 acc[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[t][r] = 0.f;
+    int seg = 0, seg_k0 = 0;  // segment holding k (wave-uniform walk)
+    for (int k0 = 0; k0 < p.K; k0 += kLinKC) {
+        __syncthreads();
+        for (int idx = threadIdx.x; idx < (kLinKC / 8) * NT * kWave; idx += kLinThreads) {
+            const int q = idx / (NT * kWave), t = (idx / kWave) % NT, ln = idx % kWave;
+            const int c = col0 + 32 * t + (ln & 31);
+            f32x4 v;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int k = k0 + 8 * q + 4 * (ln >> 5) + i;
+                v[i] = (k < p.K && c < p.N) ? p.w[int64_t(k) * p.N + c] : 0.f;
+            }
+            sw[q][t][ln] = v;
+        }
+        __syncthreads();
+        const int nq = min(kLinKC, p.K - k0) / 8;
+        for (int q = 0; q < nq; ++q) {
+            const int k = k0 + 8 * q;
+            while (k >= seg_k0 + p.seg[seg].len) {
+                seg_k0 += p.seg[seg].len;
+                ++seg;
+            }
+            f32x4 a = {0.f, 0.f, 0.f, 0.f};
+            if (valid)
+                a = *reinterpret_cast<const f32x4*>(arow + p.seg[seg].col + int64_t(ci) * p.seg[seg].comp +
+                                                    (k - seg_k0) + 4 * half);
+#pragma unroll
+            for (int t = 0; t < NT; ++t) {
+                const f32x4 b = sw[q][t][lane];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) acc[t] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i], b[i], acc[t], 0, 0, 0);
+            }
+        }
+    }
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+        const int c = col0 + 32 * t + (lane & 31);
+        if (c >= p.N) continue;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int64_t rr = row0 + 8 * (r / 4) + 4 * half + r % 4;
+            if (rr < rows) {
+                const int64_t nn = rr / p.d;
+                const int ii = int(rr - nn * p.d);
+                p.out[nn * p.out_stride + p.out_off + int64_t(ii) * p.out_comp + c] = acc[t][r];
+            }
+        }
+    }
+}
+
+}  // namespace
+}  // namespace mnx
+
+using namespace mnx;
+
+extern "C" {
+
+int mnx_block_linear_f32(const float* a, int64_t a_stride, int32_t nseg, const int64_t* seg_col,
+                         const int32_t* seg_comp, const int32_t* seg_len, const float* w, int32_t N, int64_t R,
+                         int32_t d, float* out, int64_t out_stride, int64_t out_off, int32_t out_comp,
+                         mnx_stream_t stream) {
+    clear_error();
+    MNX_REQUIRE(nseg >= 0 && nseg <= kLinMaxSeg, "segment count %d not in [0, %d]", nseg, kLinMaxSeg);
+    MNX_REQUIRE(R >= 0 && d >= 1 && N >= 1 && R * d < (int64_t(1) << 40), "sizes out of range");
+    if (R == 0) return MNX_OK;
+    MNX_REQUIRE(out && (nseg == 0 || (a && w && seg_col && seg_comp && seg_len)), "null pointer argument");
+    LinArgs p{};
+    p.a = a;
+    p.a_stride = a_stride;
+    p.nseg = nseg;
+    p.K = 0;
+    for (int s = 0; s < nseg; ++s) {
+        MNX_REQUIRE(seg_len[s] > 0 && seg_len[s] % 8 == 0 && seg_comp[s] % 4 == 0 && seg_col[s] % 4 == 0,
+                    "segment %d: length must be a positive multiple of 8, offsets multiples of 4", s);
+        p.seg[s] = LinSeg{seg_col[s], seg_comp[s], seg_len[s]};
+        p.K += seg_len[s];
+    }
+    MNX_REQUIRE(nseg == 0 || (a_stride % 4 == 0 && (uintptr_t)a % 16 == 0), "input rows must be 16-byte aligned");
+    p.w = w;
+    p.N = N;
+    p.d = d;
+    p.R = R;
+    p.out = out;
+    p.out_stride = out_stride;
+    p.out_off = out_off;
+    p.out_comp = out_comp;
+    const int64_t blocks = ceil_div(R * d, (kLinThreads / kWave) * 32);
+    MNX_REQUIRE(blocks < (int64_t(1) << 31), "too many rows");
+    const int nt = N >= 128 ? 4 : int(ceil_div(N, 32));
+    const dim3 grid(unsigned(blocks), unsigned(ceil_div(N, nt * 32)));
+    hipStream_t s = (hipStream_t)stream;
+    switch (nt) {
+        case 1: hipLaunchKernelGGL(k_block_linear<1>, grid, dim3(kLinThreads), 0, s, p); break;
+        case 2: hipLaunchKernelGGL(k_block_linear<2>, grid, dim3(kLinThreads), 0, s, p); break;
+        case 3: hipLaunchKernelGGL(k_block_linear<3>, grid, dim3(kLinThreads), 0, s, p); break;
+        default: hipLaunchKernelGGL(k_block_linear<4>, grid, dim3(kLinThreads), 0, s, p); break;
+    }
+    MNX_CHECK_LAUNCH();
+    return MNX_OK;
+}
+
+}  // extern "C"

@@ -10,6 +10,13 @@ per row by ``weight_indices`` (cuet's indexed_linear).  Each output block is one
 GEMM (rows = (node, m), K = the concatenated channels of its source blocks) on
 the GPU through torch.mm (hipBLASLt); forward and backward are written out so
 every gradient slice is produced once.
+
+On the GPU (float32, multiplicities that are multiples of 8) the blocks run in
+the HIP kernel ``mnx_block_linear_f32`` instead: rows (node, m) are read in
+place from the ir_mul input (no gather copy), the 1/sqrt(fan_in) scale is folded
+into the stacked weights and each output block is written directly; the input
+gradient is the same kernel on the output-gradient blocks with transposed
+weights.  Weight gradients (training) use the torch path below.
 """
 
 from __future__ import annotations
@@ -20,6 +27,7 @@ import torch
 import torch.nn as nn
 from pydantic import BaseModel
 
+from ... import _lib
 from ...config import config
 from ...irreps import Irreps
 
@@ -53,7 +61,23 @@ class Linear(nn.Module):
 
     def _mix(self, x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
         """x (R, dim_in), w (weight_numel,) -> (R, dim_out)."""
+        if x.is_cuda and x.dtype == torch.float32 and w.dtype == torch.float32 and self._hip_ok():
+            return _HipBlockLinear.apply(x, w, self)
         return _BlockLinear.apply(x, w, self.plan, self.irreps_out.dim)
+
+    def _hip_ok(self) -> bool:
+        """Shapes the HIP block kernel takes: every multiplicity a multiple of 8, at most 8
+        source blocks per output block and 8 consumers per input block."""
+        if not hasattr(self, "_hip_plan"):
+            ok = all(b.mul % 8 == 0 for b in self.irreps_in) and all(o.mul % 8 == 0 for o in self.irreps_out)
+            users = {}
+            for _, _, _, srcs, _ in self.plan:
+                ok = ok and len(srcs) <= 8
+                for o, _, _ in srcs:
+                    users[o] = users.get(o, 0) + 1
+            ok = ok and all(c <= 8 for c in users.values())
+            self._hip_plan = _hip_plan(self) if ok else None
+        return self._hip_plan is not None
 
     def forward(self, x: torch.Tensor, weight: torch.Tensor | None = None,
                 weight_indices: torch.Tensor | None = None) -> torch.Tensor:
@@ -151,6 +175,101 @@ def _block_backward(x, w, g, plan, need_x, need_w):
         if pos < x.shape[1]:
             gx[:, pos:] = 0
     return gx, gw
+
+
+def _hip_plan(lin: "Linear"):
+    """Launch descriptors and weight-stacking indices for the HIP block kernel.
+
+    fwd: per output block (out offset, mul_o, d, segments [(col, comp, len)], offset into the
+    stacked weights); the stacked weights are w[idx_f] * scale_f, block-major, each block
+    (sum of source muls) x mul_o row-major.
+    bwd: per input block (in offset, mul, d, segments over the output-gradient blocks, offset);
+    stacked w[idx_b] * scale_b, each block (sum of consumer mul_o) x mul row-major (W^T)."""
+    fwd, idx_f, sc_f, off = [], [], [], 0
+    consumers = {}
+    for off_o, mul_o, d, srcs, fan_in in lin.plan:
+        s = 1.0 / math.sqrt(fan_in) if srcs else 0.0
+        segs = []
+        for o, m, wo in srcs:
+            segs.append((o, m, m))
+            idx_f.append(torch.arange(wo, wo + m * mul_o))
+            sc_f.append(torch.full((m * mul_o,), s))
+            consumers.setdefault(o, []).append((off_o, mul_o, wo, s))
+        fwd.append((off_o, mul_o, d, segs, off))
+        off += sum(m for _, m, _ in srcs) * mul_o
+    bwd, idx_b, sc_b, off = [], [], [], 0
+    in_off = lin.irreps_in.offsets()
+    for ib, b in enumerate(lin.irreps_in):
+        o, m, d = in_off[ib], b.mul, b.ir.dim
+        segs = []
+        for off_o, mul_o, wo, s in consumers.get(o, []):
+            segs.append((off_o, mul_o, mul_o))
+            # W^T rows p, columns c: w[wo + c * mul_o + p]
+            idx_b.append((wo + torch.arange(m)[None, :] * mul_o + torch.arange(mul_o)[:, None]).reshape(-1))
+            sc_b.append(torch.full((mul_o * m,), s))
+        bwd.append((o, m, d, segs, off))
+        off += sum(mo for _, mo, _ in segs) * m
+    cat = lambda xs, dt: torch.cat(xs).to(dt) if xs else torch.zeros(0, dtype=dt)
+    return {"fwd": fwd, "bwd": bwd, "idx_f": cat(idx_f, torch.long), "sc_f": cat(sc_f, torch.float32),
+            "idx_b": cat(idx_b, torch.long), "sc_b": cat(sc_b, torch.float32), "dev": {}}
+
+
+def _hip_tables(hp, device):
+    key = str(device)
+    if key not in hp["dev"]:
+        hp["dev"][key] = tuple(hp[k].to(device) for k in ("idx_f", "sc_f", "idx_b", "sc_b"))
+    return hp["dev"][key]
+
+
+def _launch_blocks(a, a_stride, blocks, wstack, R, out, out_stride):
+    import ctypes as C
+
+    lib = _lib.load()
+    stream = torch.cuda.current_stream(a.device).cuda_stream
+    for off, mul, d, segs, woff in blocks:
+        n = len(segs)
+        cols = (C.c_int64 * max(n, 1))(*[sg[0] for sg in segs])
+        comps = (C.c_int32 * max(n, 1))(*[sg[1] for sg in segs])
+        lens = (C.c_int32 * max(n, 1))(*[sg[2] for sg in segs])
+        _lib.check(lib.mnx_block_linear_f32(a.data_ptr(), a_stride, n, cols, comps, lens,
+                                            wstack.data_ptr() + 4 * woff if wstack.numel() else None, mul, R, d,
+                                            out.data_ptr(), out_stride, off, mul, stream), "block linear")
+
+
+def _aligned(x: torch.Tensor) -> torch.Tensor:
+    x = x.contiguous()
+    return x if x.data_ptr() % 16 == 0 else x.clone()
+
+
+class _HipBlockLinear(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x, w, lin):
+        hp = lin._hip_plan
+        idx_f, sc_f, _, _ = _hip_tables(hp, x.device)
+        xs = _aligned(x)
+        ws = (w.index_select(0, idx_f) * sc_f).contiguous()
+        out = x.new_empty(x.shape[0], lin.irreps_out.dim)
+        _launch_blocks(xs, xs.shape[1], hp["fwd"], ws, xs.shape[0], out, out.shape[1])
+        ctx.save_for_backward(x, w)
+        ctx.lin = lin
+        return out
+
+    @staticmethod
+    def backward(ctx, g):
+        x, w = ctx.saved_tensors
+        lin = ctx.lin
+        need_x, need_w = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
+        gx = gw = None
+        g = _aligned(g)
+        if need_x:
+            hp = lin._hip_plan
+            _, _, idx_b, sc_b = _hip_tables(hp, x.device)
+            wb = (w.index_select(0, idx_b) * sc_b).contiguous()
+            gx = x.new_empty(x.shape)
+            _launch_blocks(g, g.shape[1], hp["bwd"], wb, x.shape[0], gx, gx.shape[1])
+        if need_w:
+            _, gw = _block_backward(x, w, g, lin.plan, False, True)
+        return gx, gw, None
 
 
 class _BlockLinear(torch.autograd.Function):
