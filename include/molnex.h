@@ -266,12 +266,17 @@ int mnx_sc_bwd_f32(int32_t config, const float* A, const int64_t* types, const f
 /*   out[n*out_stride + out_off + i*out_comp + p] = sum_k A_k * w[k][p]       */
 /* for nodes n < R, components i < d, columns p < N, where k runs over the   */
 /* nseg input segments in order, segment s contributing seg_len[s] values    */
-/* a[n*a_stride + seg_col[s] + i*seg_comp[s] + 0..seg_len[s]-1].  w is       */
-/* (sum seg_len) x N row-major (weights pre-scaled by the caller); nseg = 0  */
-/* writes zeros.  seg_len multiples of 8; a_stride, seg_col, seg_comp        */
-/* multiples of 4; a 16-byte aligned; at most 8 segments.  Segment arrays    */
-/* are host memory.                                                          */
+/* a[n*a_stride + seg_col[s] + i*seg_comp[s] + 0..seg_len[s]-1].  The K x N  */
+/* weights (K = sum seg_len, pre-scaled by the caller) come in the kernel's  */
+/* fragment order: with T = N >= 128 ? 4 : ceil(N/32) tiles, element         */
+/* [y][chunk][q][t][lane][i] (y < ceil(N/32T), chunk < ceil(K/64), q < 8,    */
+/* t < T, lane < 64, i < 4) holds W[64 chunk + 8q + 4(lane/32) + i]          */
+/* [32T y + 32t + lane%32], zero outside K x N; mnx_block_linear_frag_floats */
+/* gives its length.  nseg = 0 writes zeros.  seg_len multiples of 8;        */
+/* a_stride, seg_col, seg_comp multiples of 4; a and w 16-byte aligned; at   */
+/* most 8 segments.  Segment arrays are host memory.                        */
 /* ------------------------------------------------------------------------ */
+int64_t mnx_block_linear_frag_floats(int32_t K, int32_t N);
 int mnx_block_linear_f32(const float* a, int64_t a_stride, int32_t nseg, const int64_t* seg_col,
                          const int32_t* seg_comp, const int32_t* seg_len, const float* w, int32_t N,
                          int64_t R, int32_t d, float* out, int64_t out_stride, int64_t out_off,

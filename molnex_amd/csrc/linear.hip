@@ -11,9 +11,11 @@
 //
 // Each wavefront owns 32 rows (M side of v_mfma_f32_32x32x2f32) and up to 128
 // output columns (N side, NT tiles); A is read straight from the strided input
-// (16 bytes per lane, no gather copy), W is staged through LDS in 64-row
-// chunks in MFMA fragment order, and the D tiles are stored 128 contiguous
-// bytes per row into the output block.
+// (16 bytes per lane, no gather copy).  W arrives pre-arranged by the caller in
+// MFMA fragment order, [column group][64-row chunk][k/8][tile][lane][4] with zero
+// padding (mnx_block_linear_frag_floats gives its size), so each chunk is staged
+// into LDS with contiguous 16-byte copies shared by the workgroup's eight
+// wavefronts.  The D tiles are stored 128 contiguous bytes per row.
 
 #include "common.h"
 
@@ -23,7 +25,7 @@ namespace {
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int kLinThreads = 256;  // four wavefronts x 32 rows
+constexpr int kLinThreads = 512;  // eight wavefronts x 32 rows
 constexpr int kLinKC = 64;        // rows of W staged per pass
 constexpr int kLinMaxSeg = 8;
 
@@ -38,7 +40,7 @@ struct LinArgs {
     int64_t a_stride;
     int32_t nseg, K;
     LinSeg seg[kLinMaxSeg];
-    const float* w;  // K x N row-major
+    const float* w;  // fragment-ordered weights
     int32_t N, d;
     int64_t R;
     float* out;
@@ -64,19 +66,14 @@ __global__ void __launch_bounds__(kLinThreads) k_block_linear(LinArgs p) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[t][r] = 0.f;
     int seg = 0, seg_k0 = 0;  // segment holding k (wave-uniform walk)
+    constexpr int kChunk4 = (kLinKC / 8) * NT * kWave;  // float4s per staged chunk
+    const int nchunks = (p.K + kLinKC - 1) / kLinKC;
+    const f32x4* wsrc = reinterpret_cast<const f32x4*>(p.w) + int64_t(blockIdx.y) * nchunks * kChunk4;
+    f32x4* sw4 = &sw[0][0][0];
     for (int k0 = 0; k0 < p.K; k0 += kLinKC) {
         __syncthreads();
-        for (int idx = threadIdx.x; idx < (kLinKC / 8) * NT * kWave; idx += kLinThreads) {
-            const int q = idx / (NT * kWave), t = (idx / kWave) % NT, ln = idx % kWave;
-            const int c = col0 + 32 * t + (ln & 31);
-            f32x4 v;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int k = k0 + 8 * q + 4 * (ln >> 5) + i;
-                v[i] = (k < p.K && c < p.N) ? p.w[int64_t(k) * p.N + c] : 0.f;
-            }
-            sw[q][t][ln] = v;
-        }
+        for (int idx = threadIdx.x; idx < kChunk4; idx += kLinThreads) sw4[idx] = wsrc[idx];
+        wsrc += kChunk4;
         __syncthreads();
         const int nq = min(kLinKC, p.K - k0) / 8;
         for (int q = 0; q < nq; ++q) {
@@ -113,12 +110,21 @@ __global__ void __launch_bounds__(kLinThreads) k_block_linear(LinArgs p) {
     }
 }
 
+// output tiles of 32 columns per wavefront for N columns (the column-group width is 32 * this)
+int lin_tiles(int N) { return N >= 128 ? 4 : int(ceil_div(N, 32)); }
+
 }  // namespace
 }  // namespace mnx
 
 using namespace mnx;
 
 extern "C" {
+
+int64_t mnx_block_linear_frag_floats(int32_t K, int32_t N) {
+    if (K < 0 || N < 1) return -1;
+    const int nt = lin_tiles(N);
+    return ceil_div(N, nt * 32) * ceil_div(K, kLinKC) * int64_t(kLinKC / 8) * nt * kWave * 4;
+}
 
 int mnx_block_linear_f32(const float* a, int64_t a_stride, int32_t nseg, const int64_t* seg_col,
                          const int32_t* seg_comp, const int32_t* seg_len, const float* w, int32_t N, int64_t R,
@@ -141,6 +147,7 @@ int mnx_block_linear_f32(const float* a, int64_t a_stride, int32_t nseg, const i
         p.K += seg_len[s];
     }
     MNX_REQUIRE(nseg == 0 || (a_stride % 4 == 0 && (uintptr_t)a % 16 == 0), "input rows must be 16-byte aligned");
+    MNX_REQUIRE(nseg == 0 || (uintptr_t)w % 16 == 0, "weights must be 16-byte aligned");
     p.w = w;
     p.N = N;
     p.d = d;
@@ -151,7 +158,7 @@ int mnx_block_linear_f32(const float* a, int64_t a_stride, int32_t nseg, const i
     p.out_comp = out_comp;
     const int64_t blocks = ceil_div(R * d, (kLinThreads / kWave) * 32);
     MNX_REQUIRE(blocks < (int64_t(1) << 31), "too many rows");
-    const int nt = N >= 128 ? 4 : int(ceil_div(N, 32));
+    const int nt = lin_tiles(N);
     const dim3 grid(unsigned(blocks), unsigned(ceil_div(N, nt * 32)));
     hipStream_t s = (hipStream_t)stream;
     switch (nt) {

@@ -177,38 +177,87 @@ def _block_backward(x, w, g, plan, need_x, need_w):
     return gx, gw
 
 
-def _hip_plan(lin: "Linear"):
-    """Launch descriptors and weight-stacking indices for the HIP block kernel.
+def _lin_tiles(N: int) -> int:
+    """Output tiles of 32 columns per wavefront (``lin_tiles`` in csrc/linear.hip)."""
+    return 4 if N >= 128 else -(-N // 32)
 
-    fwd: per output block (out offset, mul_o, d, segments [(col, comp, len)], offset into the
-    stacked weights); the stacked weights are w[idx_f] * scale_f, block-major, each block
-    (sum of source muls) x mul_o row-major.
+
+def _frag_order(K: int, N: int):
+    """(k, c, valid) of every element of the kernel's weight layout
+    [column group][64-row chunk][k/8][tile][lane][4] (csrc/linear.hip)."""
+    nt = _lin_tiles(N)
+    Y, C = -(-N // (nt * 32)), -(-K // 64)
+    ar = torch.arange
+    y = ar(Y).view(-1, 1, 1, 1, 1, 1)
+    ch = ar(C).view(1, -1, 1, 1, 1, 1)
+    q = ar(8).view(1, 1, -1, 1, 1, 1)
+    t = ar(nt).view(1, 1, 1, -1, 1, 1)
+    ln = ar(64).view(1, 1, 1, 1, -1, 1)
+    i = ar(4).view(1, 1, 1, 1, 1, -1)
+    k, c = torch.broadcast_tensors(ch * 64 + 8 * q + 4 * (ln // 32) + i, y * nt * 32 + 32 * t + ln % 32)
+    k, c = k.reshape(-1), c.reshape(-1)
+    return k, c, (k < K) & (c < N)
+
+
+def _frag_block(rows, N):
+    """Gather indices and scales of one block's fragment-ordered weights.  ``rows`` lists the
+    stacked row segments (length, first flat index, step between rows, step between columns,
+    scale): W[k][c] = w[first + (k - k_seg) * row_step + c * col_step] * scale."""
+    K = sum(r[0] for r in rows)
+    k, c, valid = _frag_order(K, N)
+    base = torch.zeros(max(K, 1), dtype=torch.long)
+    cstep = torch.zeros(max(K, 1), dtype=torch.long)
+    scale = torch.zeros(max(K, 1))
+    k0 = 0
+    for length, first, row_step, col_step, sc in rows:
+        kk = torch.arange(length)
+        base[k0:k0 + length] = first + kk * row_step
+        cstep[k0:k0 + length] = col_step
+        scale[k0:k0 + length] = sc
+        k0 += length
+    kc = k.clamp(max=max(K - 1, 0))
+    idx = torch.where(valid, base[kc] + c * cstep[kc], torch.zeros_like(k))
+    sc = torch.where(valid, scale[kc], torch.zeros(()))
+    return idx, sc
+
+
+def _hip_plan(lin: "Linear"):
+    """Launch descriptors and fragment-ordered weight indices for the HIP block kernel.
+
+    fwd: per output block (out offset, mul_o, d, segments [(col, comp, len)], float offset of its
+    weights); the weights are w[idx_f] * scale_f with the stacked source weights (sum of source
+    muls) x mul_o in the kernel's fragment order.
     bwd: per input block (in offset, mul, d, segments over the output-gradient blocks, offset);
-    stacked w[idx_b] * scale_b, each block (sum of consumer mul_o) x mul row-major (W^T)."""
+    weights w[idx_b] * scale_b: the transposed blocks, (sum of consumer mul_o) x mul."""
     fwd, idx_f, sc_f, off = [], [], [], 0
     consumers = {}
     for off_o, mul_o, d, srcs, fan_in in lin.plan:
         s = 1.0 / math.sqrt(fan_in) if srcs else 0.0
-        segs = []
+        segs, rows = [], []
         for o, m, wo in srcs:
             segs.append((o, m, m))
-            idx_f.append(torch.arange(wo, wo + m * mul_o))
-            sc_f.append(torch.full((m * mul_o,), s))
+            rows.append((m, wo, mul_o, 1, s))  # W_src[c][p] = w[wo + c * mul_o + p]
             consumers.setdefault(o, []).append((off_o, mul_o, wo, s))
         fwd.append((off_o, mul_o, d, segs, off))
-        off += sum(m for _, m, _ in srcs) * mul_o
+        if segs:
+            i_, s_ = _frag_block(rows, mul_o)
+            idx_f.append(i_)
+            sc_f.append(s_)
+            off += i_.numel()
     bwd, idx_b, sc_b, off = [], [], [], 0
     in_off = lin.irreps_in.offsets()
     for ib, b in enumerate(lin.irreps_in):
         o, m, d = in_off[ib], b.mul, b.ir.dim
-        segs = []
+        segs, rows = [], []
         for off_o, mul_o, wo, s in consumers.get(o, []):
             segs.append((off_o, mul_o, mul_o))
-            # W^T rows p, columns c: w[wo + c * mul_o + p]
-            idx_b.append((wo + torch.arange(m)[None, :] * mul_o + torch.arange(mul_o)[:, None]).reshape(-1))
-            sc_b.append(torch.full((mul_o * m,), s))
+            rows.append((mul_o, wo, 1, mul_o, s))  # W^T[p][c] = w[wo + c * mul_o + p]
         bwd.append((o, m, d, segs, off))
-        off += sum(mo for _, mo, _ in segs) * m
+        if segs:
+            i_, s_ = _frag_block(rows, m)
+            idx_b.append(i_)
+            sc_b.append(s_)
+            off += i_.numel()
     cat = lambda xs, dt: torch.cat(xs).to(dt) if xs else torch.zeros(0, dtype=dt)
     return {"fwd": fwd, "bwd": bwd, "idx_f": cat(idx_f, torch.long), "sc_f": cat(sc_f, torch.float32),
             "idx_b": cat(idx_b, torch.long), "sc_b": cat(sc_b, torch.float32), "dev": {}}

@@ -97,3 +97,24 @@ def test_module_trains_through_sequential():
     assert not m._fused_hidden(feats)
     m(feats).sum().backward()
     assert m.mlp[0].weight.grad is not None
+
+
+def test_module_last_layer_trained_hidden_fused():
+    """Frozen hidden Linears with a trainable last Linear: hidden stack fused, last layer in torch,
+    its weight gradient intact."""
+    torch.manual_seed(0)
+    m = RadialWeightMLP(in_dim=8, hidden_dim=64, out_dim=40, num_layers=2).to(DEV)
+    for p in m.mlp[:-1].parameters():
+        p.requires_grad_(False)
+    feats = torch.randn(500, 8, device=DEV)
+    assert m._fused_hidden(feats)
+    out = m(feats)
+    out.square().sum().backward()
+    g1 = m.mlp[-1].weight.grad.clone()
+    m.mlp[-1].weight.grad = None
+    config.fused_radial = False
+    try:
+        m(feats).square().sum().backward()
+    finally:
+        config.fused_radial = True
+    assert _rel(g1, m.mlp[-1].weight.grad) <= 1e-5
