@@ -441,8 +441,8 @@ def secondary_figures(args, dev):
 def main():
     args = parse()
     if args.gpus != 1:
-        print(json.dumps({"error": "this build runs on one GPU; --gpus > 1 is not supported (see DESIGN.md, "
-                                   "'More than one GPU')"}))
+        print(json.dumps({"error": "this build runs on one GPU; --gpus > 1 is not supported (the path would "
+                                   "shard by space: owned atoms plus a halo of rc x interactions per GPU)"}))
         sys.exit(2)
     if args.workload == "full":
         dev = torch.device("cuda:0")

@@ -1,5 +1,5 @@
-"""Particle-mesh Ewald potential term (new: the reference has the ops but no module,
-src/molix/F/pot.py:11-14; SURVEY gap D4).
+"""Particle-mesh Ewald potential term (new: the reference has the ops but no module
+that combines them, src/molix/F/pot.py:11-14).
 
 E = E_direct(pairs within the real-space cutoff, minimum image)
   + E_reciprocal(B-spline order p on a gx x gy x gz mesh)
