@@ -13,10 +13,14 @@
 // the CUDA reference does not guarantee (atomicAdd slots, .cu:69).
 //
 // Layout of the work: atoms are binned into cells whose slab widths exceed the
-// cutoff (fractional coordinates for periodic cells), one wavefront per atom
-// scans the 27 neighbouring cells, compacts the accepted j with a ballot into
-// LDS, bitonic-sorts them there and writes its segment with coalesced stores.
-// This translation unit is compiled with -ffp-contract=off.
+// cutoff (fractional coordinates for periodic cells), each cell's atoms sorted by
+// id.  Four wavefronts share a cell (each takes every fourth atom of it as a
+// centre): they fetch the 27 neighbour cells' ranges in one round trip, load each
+// candidate once, test it against all of their centres, compact the accepted j
+// of each centre with a ballot into LDS, sort them in registers (bitonic, <= 64)
+// or by rank, and write each centre's segment with coalesced stores.  Grids with
+// fewer than 3 cells along a periodic axis use one wavefront per atom over all
+// atoms (brute mode).  This translation unit is compiled with -ffp-contract=off.
 
 #include <math.h>
 
