@@ -33,6 +33,7 @@ struct LinSeg {
     int64_t col;  // column of component 0
     int32_t comp; // column step between components
     int32_t len;  // values contributed (multiple of 8)
+    int32_t k0;   // first contraction index of the segment
 };
 
 struct LinArgs {
@@ -48,16 +49,22 @@ struct LinArgs {
     int32_t out_comp;
 };
 
-template <int NT>
+// NT: output tiles of 32 columns per wavefront; D: components per row group when it
+// is 1, 3, 5 or 7 (divisions by it become multiplies), 0 = read p.d.
+template <int NT, int D>
 __global__ void __launch_bounds__(kLinThreads) k_block_linear(LinArgs p) {
+    const int d = D ? D : p.d;
     __shared__ f32x4 sw[kLinKC / 8][NT][kWave];
     const int lane = threadIdx.x & 63, half = lane >> 5, wave = threadIdx.x >> 6;
-    const int64_t rows = p.R * p.d;
+    const int64_t rows = p.R * d;
     const int64_t row0 = (int64_t(blockIdx.x) * (kLinThreads / kWave) + wave) * 32;
     const int64_t row = row0 + (lane & 31);
     const bool valid = row < rows;
-    const int64_t n = valid ? row / p.d : 0;
-    const int ci = valid ? int(row - n * p.d) : 0;
+    // (node, component) of row0 once; rows within the tile follow in 32-bit arithmetic
+    const int64_t n0 = row0 / d;
+    const int c0 = int(row0 - n0 * d);
+    const int64_t n = n0 + (c0 + (lane & 31)) / d;
+    const int ci = (c0 + (lane & 31)) % d;
     const float* arow = p.a + n * p.a_stride;
     const int col0 = blockIdx.y * NT * 32;
     f32x16 acc[NT];
@@ -65,53 +72,81 @@ __global__ void __launch_bounds__(kLinThreads) k_block_linear(LinArgs p) {
     for (int t = 0; t < NT; ++t)
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[t][r] = 0.f;
-    int seg = 0, seg_k0 = 0;  // segment holding k (wave-uniform walk)
     constexpr int kChunk4 = (kLinKC / 8) * NT * kWave;  // float4s per staged chunk
     const int nchunks = (p.K + kLinKC - 1) / kLinKC;
     const f32x4* wsrc = reinterpret_cast<const f32x4*>(p.w) + int64_t(blockIdx.y) * nchunks * kChunk4;
     f32x4* sw4 = &sw[0][0][0];
+    // per segment, this lane's offset of contraction index k is base[s] + k (row-relative)
+    int32_t base[kLinMaxSeg];
+#pragma unroll
+    for (int sg = 0; sg < kLinMaxSeg; ++sg)
+        base[sg] = sg < p.nseg ? int32_t(p.seg[sg].col + int64_t(ci) * p.seg[sg].comp - p.seg[sg].k0 + 4 * half) : 0;
     for (int k0 = 0; k0 < p.K; k0 += kLinKC) {
+        // this chunk's A operands first (one 16-byte load per k-block of 8): their
+        // latency overlaps the weight staging below
+        f32x4 av[kLinKC / 8];
+#pragma unroll
+        for (int q = 0; q < kLinKC / 8; ++q) {
+            const int k = k0 + 8 * q;
+            int32_t off = 0;
+#pragma unroll
+            for (int sg = 0; sg < kLinMaxSeg; ++sg)  // k is wave-uniform: a scalar select chain
+                if (sg < p.nseg && k >= p.seg[sg].k0) off = base[sg];
+            av[q] = f32x4{0.f, 0.f, 0.f, 0.f};
+            if (valid && k < p.K) av[q] = *reinterpret_cast<const f32x4*>(arow + off + k);
+        }
         __syncthreads();
         for (int idx = threadIdx.x; idx < kChunk4; idx += kLinThreads) sw4[idx] = wsrc[idx];
         wsrc += kChunk4;
         __syncthreads();
         const int nq = min(kLinKC, p.K - k0) / 8;
-        for (int q = 0; q < nq; ++q) {
-            const int k = k0 + 8 * q;
-            while (k >= seg_k0 + p.seg[seg].len) {
-                seg_k0 += p.seg[seg].len;
-                ++seg;
-            }
-            f32x4 a = {0.f, 0.f, 0.f, 0.f};
-            if (valid)
-                a = *reinterpret_cast<const f32x4*>(arow + p.seg[seg].col + int64_t(ci) * p.seg[seg].comp +
-                                                    (k - seg_k0) + 4 * half);
 #pragma unroll
-            for (int t = 0; t < NT; ++t) {
-                const f32x4 b = sw[q][t][lane];
+        for (int q = 0; q < kLinKC / 8; ++q) {
+            if (q < nq) {
 #pragma unroll
-                for (int i = 0; i < 4; ++i) acc[t] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i], b[i], acc[t], 0, 0, 0);
+                for (int t = 0; t < NT; ++t) {
+                    const f32x4 b = sw[q][t][lane];
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                        acc[t] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[q][i], b[i], acc[t], 0, 0, 0);
+                }
             }
         }
+    }
+    // output row offsets of this lane's 16 accumulator registers
+    int64_t obase[16];
+    bool oval[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        const int o = 8 * (r / 4) + 4 * half + r % 4;
+        const int64_t nn = n0 + (c0 + o) / d;
+        const int ii = (c0 + o) % d;
+        oval[r] = row0 + o < rows;
+        obase[r] = nn * p.out_stride + p.out_off + int64_t(ii) * p.out_comp;
     }
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
         const int c = col0 + 32 * t + (lane & 31);
         if (c >= p.N) continue;
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const int64_t rr = row0 + 8 * (r / 4) + 4 * half + r % 4;
-            if (rr < rows) {
-                const int64_t nn = rr / p.d;
-                const int ii = int(rr - nn * p.d);
-                p.out[nn * p.out_stride + p.out_off + int64_t(ii) * p.out_comp + c] = acc[t][r];
-            }
-        }
+        for (int r = 0; r < 16; ++r)
+            if (oval[r]) p.out[obase[r] + c] = acc[t][r];
     }
 }
 
 // output tiles of 32 columns per wavefront for N columns (the column-group width is 32 * this)
 int lin_tiles(int N) { return N >= 128 ? 4 : int(ceil_div(N, 32)); }
+
+template <int NT>
+void launch_nt(int d, dim3 grid, hipStream_t s, const LinArgs& p) {
+    switch (d) {
+        case 1: hipLaunchKernelGGL((k_block_linear<NT, 1>), grid, dim3(kLinThreads), 0, s, p); break;
+        case 3: hipLaunchKernelGGL((k_block_linear<NT, 3>), grid, dim3(kLinThreads), 0, s, p); break;
+        case 5: hipLaunchKernelGGL((k_block_linear<NT, 5>), grid, dim3(kLinThreads), 0, s, p); break;
+        case 7: hipLaunchKernelGGL((k_block_linear<NT, 7>), grid, dim3(kLinThreads), 0, s, p); break;
+        default: hipLaunchKernelGGL((k_block_linear<NT, 0>), grid, dim3(kLinThreads), 0, s, p); break;
+    }
+}
 
 }  // namespace
 }  // namespace mnx
@@ -143,10 +178,13 @@ int mnx_block_linear_f32(const float* a, int64_t a_stride, int32_t nseg, const i
     for (int s = 0; s < nseg; ++s) {
         MNX_REQUIRE(seg_len[s] > 0 && seg_len[s] % 8 == 0 && seg_comp[s] % 4 == 0 && seg_col[s] % 4 == 0,
                     "segment %d: length must be a positive multiple of 8, offsets multiples of 4", s);
-        p.seg[s] = LinSeg{seg_col[s], seg_comp[s], seg_len[s]};
+        p.seg[s] = LinSeg{seg_col[s], seg_comp[s], seg_len[s], p.K};
         p.K += seg_len[s];
     }
     MNX_REQUIRE(nseg == 0 || (a_stride % 4 == 0 && (uintptr_t)a % 16 == 0), "input rows must be 16-byte aligned");
+    for (int s = 0; s < nseg; ++s)
+        MNX_REQUIRE(seg_col[s] + int64_t(d - 1) * seg_comp[s] + seg_len[s] < (int64_t(1) << 31),
+                    "segment %d exceeds 2^31 columns", s);
     MNX_REQUIRE(nseg == 0 || (uintptr_t)w % 16 == 0, "weights must be 16-byte aligned");
     p.w = w;
     p.N = N;
@@ -162,10 +200,10 @@ int mnx_block_linear_f32(const float* a, int64_t a_stride, int32_t nseg, const i
     const dim3 grid(unsigned(blocks), unsigned(ceil_div(N, nt * 32)));
     hipStream_t s = (hipStream_t)stream;
     switch (nt) {
-        case 1: hipLaunchKernelGGL(k_block_linear<1>, grid, dim3(kLinThreads), 0, s, p); break;
-        case 2: hipLaunchKernelGGL(k_block_linear<2>, grid, dim3(kLinThreads), 0, s, p); break;
-        case 3: hipLaunchKernelGGL(k_block_linear<3>, grid, dim3(kLinThreads), 0, s, p); break;
-        default: hipLaunchKernelGGL(k_block_linear<4>, grid, dim3(kLinThreads), 0, s, p); break;
+        case 1: launch_nt<1>(d, grid, s, p); break;
+        case 2: launch_nt<2>(d, grid, s, p); break;
+        case 3: launch_nt<3>(d, grid, s, p); break;
+        default: launch_nt<4>(d, grid, s, p); break;
     }
     MNX_CHECK_LAUNCH();
     return MNX_OK;
