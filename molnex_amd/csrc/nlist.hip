@@ -32,7 +32,9 @@
 namespace mnx {
 namespace {
 
-constexpr int kNlCap = 4096;  // max neighbours of one atom (LDS list per wave)
+constexpr int kNlCap = 4096;  // max neighbours of one atom (LDS list of the per-atom emit)
+constexpr int kEmitBuf = 1024; // LDS list per wavefront of the cell emit; atoms with more
+                               // neighbours are written by the per-atom emit
 constexpr int64_t kNlBlocks = 16384;  // grid-stride launches of the count / emit kernels
 constexpr int kCellParts = 4;          // wavefronts per cell (each takes every 4th atom of it)
 constexpr float kCellMargin = 1.0001f;
@@ -153,6 +155,7 @@ template <typename T>
 struct AcceptTest {
     T inv[3];
     T c2lo, c2hi, c2tiny;
+    T b[9];  // the box, held in registers for the cheap test
 };
 
 // The all-pairs fallback (a periodic axis with < 3 cells) gets no cheap test: there the
@@ -165,7 +168,19 @@ __device__ __forceinline__ AcceptTest<T> accept_test(const T* box, bool periodic
     a.c2lo = brute ? T(0) : c2 * T(0.9999);
     a.c2hi = brute ? T(INFINITY) : c2 * T(1.0001);
     a.c2tiny = c2 * T(1e-20);
+    for (int k = 0; k < 9; ++k) a.b[k] = periodic ? box[k] : T(0);
     return a;
+}
+
+// Value of lane q (wave-uniform q) broadcast to the wavefront through v_readlane.
+__device__ __forceinline__ int lane_value(int v, int q) { return __builtin_amdgcn_readlane(v, q); }
+__device__ __forceinline__ float lane_value(float v, int q) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), q));
+}
+__device__ __forceinline__ double lane_value(double v, int q) {
+    const long long b = __double_as_longlong(v);
+    const int lo = __builtin_amdgcn_readlane(int(b & 0xffffffff), q), hi = __builtin_amdgcn_readlane(int(b >> 32), q);
+    return __longlong_as_double((static_cast<long long>(hi) << 32) | static_cast<unsigned int>(lo));
 }
 
 // Decision for the pair at positions a, b.  It does not depend on the order: a - b is the
@@ -180,9 +195,9 @@ __device__ __forceinline__ bool accept_xyz(const T* box, T ax, T ay, T az, T bx,
         for (int k = 2; k >= 0; --k) {
             const T dk = k == 2 ? d2 : (k == 1 ? d1 : d0);
             const T s = rint_(dk * at.inv[k]);
-            d0 = d0 - s * box[3 * k + 0];
-            d1 = d1 - s * box[3 * k + 1];
-            d2 = d2 - s * box[3 * k + 2];
+            d0 = d0 - s * at.b[3 * k + 0];
+            d1 = d1 - s * at.b[3 * k + 1];
+            d2 = d2 - s * at.b[3 * k + 2];
         }
     }
     const T r2 = d0 * d0 + d1 * d1 + d2 * d2;
@@ -327,21 +342,18 @@ __global__ void k_place(int64_t n, const int32_t* __restrict__ cell_of, const in
     atoms_sorted[slot] = int32_t(i);
 }
 
-// Sort each cell's atom list ascending (deterministic order after atomic placement).
-__global__ void k_sort_cells(const NlGrid* __restrict__ gp, const int32_t* __restrict__ cell_start,
-                             int32_t* __restrict__ atoms_sorted) {
-    const int64_t c = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
-    if (c >= gp->ncells) return;
+// Each cell's atom list in ascending order (deterministic after the atomic placement into
+// `slots`): the atom in slot k moves to its rank within its cell.
+__global__ void k_rank_cells(int64_t n, const int32_t* __restrict__ cell_of, const int32_t* __restrict__ cell_start,
+                             const int32_t* __restrict__ slots, int32_t* __restrict__ atoms_sorted) {
+    const int64_t k = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (k >= n) return;
+    const int a = slots[k];
+    const int c = cell_of[a];
     const int b = cell_start[c], e = cell_start[c + 1];
-    for (int k = b + 1; k < e; ++k) {
-        int v = atoms_sorted[k];
-        int q = k - 1;
-        while (q >= b && atoms_sorted[q] > v) {
-            atoms_sorted[q + 1] = atoms_sorted[q];
-            --q;
-        }
-        atoms_sorted[q + 1] = v;
-    }
+    int r = 0;
+    for (int t = b; t < e; ++t) r += slots[t] < a;
+    atoms_sorted[b + r] = a;
 }
 
 // ---------------------------------------------------------------------------
@@ -500,17 +512,20 @@ __global__ void __launch_bounds__(kWave) k_emit(const T* __restrict__ pos, int64
                                                 T cutoff, int mode, int layout, const NlGrid* __restrict__ gp,
                                                 const int32_t* __restrict__ cell_start,
                                                 const int32_t* __restrict__ atoms_sorted,
+                                                const int32_t* __restrict__ counts,
                                                 const int64_t* __restrict__ offsets, int64_t capacity,
                                                 int32_t* __restrict__ idx_i, int32_t* __restrict__ idx_j,
                                                 T* __restrict__ deltas, T* __restrict__ dist,
                                                 T* __restrict__ shifts) {
     __shared__ int32_t buf[kNlCap];
     const NlGrid g = *gp;
-    if (!g.brute) return;
+    // brute grids: every atom; cell grids: the atoms the cell emit leaves (> kEmitBuf neighbours)
+    const bool only_big = !g.brute;
     const bool periodic = g.periodic;
     const int lane = threadIdx.x;
     const AcceptTest<T> at = accept_test<T>(box, periodic, true, cutoff);
     for (int i = blockIdx.x; i < n; i += gridDim.x) {
+        if (only_big && counts[i] <= kEmitBuf) continue;
         int count = 0;
         __syncthreads();  // buf is reused across atoms
         for_candidates<T>(pos, i, n, g, cell_start, atoms_sorted, mode, [&](int j) {
@@ -570,16 +585,18 @@ __global__ void __launch_bounds__(kWave) k_count_cells(const T* __restrict__ pos
         for (int q0 = 0; q0 < ncent; q0 += kWave) {
             const int nq = ncent - q0 < kWave ? ncent - q0 : kWave;
             const int my_i = lane < nq ? atoms_sorted[cb + part + (q0 + lane) * kCellParts] : -1;
+            const T mx = my_i >= 0 ? pos[3 * my_i] : T(0), my = my_i >= 0 ? pos[3 * my_i + 1] : T(0),
+                    mz = my_i >= 0 ? pos[3 * my_i + 2] : T(0);
             int my_count = 0;
             for (int base = 0; base < cr.total; base += kWave) {
                 const int j = cell_candidate(cr, base + lane, atoms_sorted);
                 const T jx = j >= 0 ? pos[3 * j] : T(0), jy = j >= 0 ? pos[3 * j + 1] : T(0),
                         jz = j >= 0 ? pos[3 * j + 2] : T(0);
                 for (int q = 0; q < nq; ++q) {
-                    const int i = __builtin_amdgcn_readfirstlane(__shfl(my_i, q, kWave));
+                    const int i = lane_value(my_i, q);
                     const bool keep = j >= 0 && (mode == MNX_NLIST_HALF ? j < i : j != i);
-                    const bool ok = keep && accept_xyz<T>(box, pos[3 * i], pos[3 * i + 1], pos[3 * i + 2], jx, jy, jz,
-                                                          periodic, cutoff, at);
+                    const bool ok = keep && accept_xyz<T>(box, lane_value(mx, q), lane_value(my, q), lane_value(mz, q),
+                                                          jx, jy, jz, periodic, cutoff, at);
                     const int cnt = __popcll(__ballot(ok));
                     if (lane == q) my_count += cnt;
                 }
@@ -602,7 +619,7 @@ __global__ void __launch_bounds__(kWave) k_emit_cells(const T* __restrict__ pos,
                                                       int32_t* __restrict__ idx_i, int32_t* __restrict__ idx_j,
                                                       T* __restrict__ deltas, T* __restrict__ dist,
                                                       T* __restrict__ shifts) {
-    __shared__ int32_t buf[kNlCap];  // accepted j of a batch of centres, one segment per centre
+    __shared__ int32_t buf[kEmitBuf];  // accepted j of a batch of centres, one segment per centre
     const NlGrid g = *gp;
     if (g.brute) return;
     const int lane = threadIdx.x;
@@ -618,17 +635,21 @@ __global__ void __launch_bounds__(kWave) k_emit_cells(const T* __restrict__ pos,
         cell_of_block(c, g, &cx, &cy, &cz);
         const CellRanges cr = cell_ranges(g, cx, cy, cz, cell_start, lane);
         for (int q0 = 0; q0 < ncent;) {
-            // a batch of centres whose segments (counts, capped at kNlCap) fit the buffer
+            // a batch of centres whose segments fit the buffer (kEmitBuf entries)
             const int avail = ncent - q0 < kWave ? ncent - q0 : kWave;
             const int my_i = lane < avail ? atoms_sorted[cb + part + (q0 + lane) * kCellParts] : -1;
-            const int my_cnt = lane < avail ? min(counts[my_i], kNlCap) : 0;
+            // centres with more than kEmitBuf neighbours take no buffer space here (per-atom emit)
+            const int cnt_i = lane < avail ? counts[my_i] : 0;
+            const int my_cnt = cnt_i > kEmitBuf ? 0 : cnt_i;
+            const T mx = my_i >= 0 ? pos[3 * my_i] : T(0), my = my_i >= 0 ? pos[3 * my_i + 1] : T(0),
+                    mz = my_i >= 0 ? pos[3 * my_i + 2] : T(0);
             int incl = my_cnt;
 #pragma unroll
             for (int o = 1; o < kWave; o <<= 1) {
                 const int v = __shfl_up(incl, o, kWave);
                 if (lane >= o) incl += v;
             }
-            int nq = __popcll(__ballot(lane < avail && incl <= kNlCap));  // incl is non-decreasing
+            int nq = __popcll(__ballot(lane < avail && incl <= kEmitBuf));  // incl is non-decreasing
             if (nq == 0) nq = 1;
             const int my_off = incl - my_cnt;
             int my_fill = 0;
@@ -638,13 +659,13 @@ __global__ void __launch_bounds__(kWave) k_emit_cells(const T* __restrict__ pos,
                 const T jx = j >= 0 ? pos[3 * j] : T(0), jy = j >= 0 ? pos[3 * j + 1] : T(0),
                         jz = j >= 0 ? pos[3 * j + 2] : T(0);
                 for (int q = 0; q < nq; ++q) {
-                    const int i = __builtin_amdgcn_readfirstlane(__shfl(my_i, q, kWave));
-                    const int seg = __builtin_amdgcn_readfirstlane(__shfl(my_off, q, kWave));
-                    const int cap = __builtin_amdgcn_readfirstlane(__shfl(my_cnt, q, kWave));
-                    const int fill = __builtin_amdgcn_readfirstlane(__shfl(my_fill, q, kWave));
+                    const int i = lane_value(my_i, q);
+                    const int seg = lane_value(my_off, q);
+                    const int cap = lane_value(my_cnt, q);
+                    const int fill = lane_value(my_fill, q);
                     const bool keep = j >= 0 && (mode == MNX_NLIST_HALF ? j < i : j != i);
-                    const bool ok = keep && accept_xyz<T>(box, pos[3 * i], pos[3 * i + 1], pos[3 * i + 2], jx, jy, jz,
-                                                          periodic, cutoff, at);
+                    const bool ok = keep && accept_xyz<T>(box, lane_value(mx, q), lane_value(my, q), lane_value(mz, q),
+                                                          jx, jy, jz, periodic, cutoff, at);
                     const uint64_t m = __ballot(ok);
                     const int before = __popcll(m & ((uint64_t(1) << lane) - 1));
                     if (ok && fill + before < cap) buf[seg + fill + before] = j;
@@ -654,11 +675,11 @@ __global__ void __launch_bounds__(kWave) k_emit_cells(const T* __restrict__ pos,
             __syncthreads();
             // each centre's segment, ranked by j (the j are distinct), written at its offset
             for (int q = 0; q < nq; ++q) {
-                const int i = __builtin_amdgcn_readfirstlane(__shfl(my_i, q, kWave));
-                const int seg = __builtin_amdgcn_readfirstlane(__shfl(my_off, q, kWave));
+                const int i = lane_value(my_i, q);
+                const int seg = lane_value(my_off, q);
                 // entries actually written (equal to the count pass's unless it overflowed)
-                const int cap = __builtin_amdgcn_readfirstlane(__shfl(my_cnt, q, kWave));
-                const int got = __builtin_amdgcn_readfirstlane(__shfl(my_fill, q, kWave));
+                const int cap = lane_value(my_cnt, q);
+                const int got = lane_value(my_fill, q);
                 const int len = got < cap ? got : cap;
                 const int64_t obase = layout == MNX_NLIST_TRIANGULAR ? 0 : offsets[i];
                 if (len <= kWave) {
@@ -747,11 +768,12 @@ int nlist_count(const T* pos, int64_t n, double cutoff, const T* box, int mode, 
     if (rc) return rc;
     if (n > 0) {
         const int tb = 256;
+        // place into `counts` (free until the count pass), then rank within each cell
         hipLaunchKernelGGL(k_place, dim3(ceil_div(n, tb)), dim3(tb), 0, stream, n, w.cell_of, w.cell_start,
-                           w.cell_fill, w.atoms_sorted);
+                           w.cell_fill, w.counts);
         MNX_CHECK_LAUNCH();
-        hipLaunchKernelGGL(k_sort_cells, dim3(ceil_div(w.max_cells, tb)), dim3(tb), 0, stream, w.grid,
-                           w.cell_start, w.atoms_sorted);
+        hipLaunchKernelGGL(k_rank_cells, dim3(ceil_div(n, tb)), dim3(tb), 0, stream, n, w.cell_of, w.cell_start,
+                           w.counts, w.atoms_sorted);
         MNX_CHECK_LAUNCH();
         const unsigned blocks = unsigned(std::min<int64_t>(std::max<int64_t>(n, w.max_cells * kCellParts), kNlBlocks));
         hipLaunchKernelGGL((k_count_cells<T>), dim3(blocks), dim3(kWave), 0, stream, pos, box, T(cutoff), mode,
@@ -800,8 +822,8 @@ int nlist_emit(const T* pos, int64_t n, double cutoff, const T* box, int mode, i
                            dist, shifts);
         MNX_CHECK_LAUNCH();
         hipLaunchKernelGGL((k_emit<T>), dim3(blocks), dim3(kWave), 0, stream, pos, n, box, T(cutoff), mode, layout,
-                           w.grid, w.cell_start, w.atoms_sorted, w.offsets, capacity, idx_i, idx_j, deltas, dist,
-                           shifts);
+                           w.grid, w.cell_start, w.atoms_sorted, w.counts, w.offsets, capacity, idx_i, idx_j, deltas,
+                           dist, shifts);
         MNX_CHECK_LAUNCH();
     }
     return MNX_OK;

@@ -129,3 +129,21 @@ def test_empty_and_single(ops):
         nb, d, dist, npairs = ops.get_neighbor_pairs(pos, 5.0, 4, torch.empty((0, 0), device=DEV))
         assert int(npairs.item()) == 0
         assert torch.all(nb == -1) and torch.all(torch.isnan(dist))
+
+
+def test_dense_cluster_beyond_cell_emit_buffer(ops):
+    """Atoms with more than 1024 neighbours on a cell grid (a dense cluster inside a periodic box):
+    their pair segments come from the per-atom emit, the rest from the cell emit; bit-exact."""
+    rng = np.random.default_rng(11)
+    L = 30.0
+    bg = rng.uniform(0, L, (8000, 3))
+    u = rng.normal(size=(1300, 3))
+    cluster = L / 2 + 2.0 * u / np.linalg.norm(u, axis=1, keepdims=True) * rng.uniform(0, 1, (1300, 1)) ** (1 / 3)
+    pos_np = np.concatenate([bg, cluster]).astype(np.float32)
+    box_np = np.eye(3, dtype=np.float32) * L
+    i, j, sh, d, dist = _directed_check(ops, pos_np, box_np, 5.0)
+    counts = np.bincount(i.cpu().numpy(), minlength=pos_np.shape[0])
+    assert counts.max() > 1024 and counts.max() <= 4096
+    # half list too (the reference layout)
+    ih, jh, _, _, _ = ops.neighbor_list(torch.from_numpy(pos_np).to(DEV), 5.0, torch.from_numpy(box_np).to(DEV), False)
+    assert ih.shape[0] * 2 == i.shape[0]
