@@ -45,7 +45,7 @@ struct NlGrid {
     int32_t n[3];
     int32_t ncells;
     int32_t overflow;  // set when an atom has more than kNlCap neighbours
-    int32_t pad;
+    int32_t nbig;      // atoms with more than kEmitBuf neighbours (listed in NlWs::big)
     double lo[3];
     double inv_w[3];
     double rinv[6];  // inverse of the lower-triangular cell: f_c = z*r5, ...
@@ -59,6 +59,7 @@ struct NlWs {
     int32_t* cell_fill;
     int32_t* atoms_sorted;
     int32_t* counts;
+    int32_t* big;
     int64_t* offsets;
     int64_t* total;
     int64_t* tiles64;
@@ -79,6 +80,7 @@ NlWs carve(void* base, size_t bytes, int64_t n, size_t* used) {
     w.cell_fill = ws.take<int32_t>(w.max_cells);
     w.atoms_sorted = ws.take<int32_t>(n > 0 ? n : 1);
     w.counts = ws.take<int32_t>(n > 0 ? n : 1);
+    w.big = ws.take<int32_t>(n > 0 ? n : 1);
     w.offsets = ws.take<int64_t>(n + 1);
     w.total = ws.take<int64_t>(1);
     w.tiles64 = ws.take<int64_t>(scan_workspace_elems(n));
@@ -512,20 +514,22 @@ __global__ void __launch_bounds__(kWave) k_emit(const T* __restrict__ pos, int64
                                                 T cutoff, int mode, int layout, const NlGrid* __restrict__ gp,
                                                 const int32_t* __restrict__ cell_start,
                                                 const int32_t* __restrict__ atoms_sorted,
-                                                const int32_t* __restrict__ counts,
+                                                const int32_t* __restrict__ big,
                                                 const int64_t* __restrict__ offsets, int64_t capacity,
                                                 int32_t* __restrict__ idx_i, int32_t* __restrict__ idx_j,
                                                 T* __restrict__ deltas, T* __restrict__ dist,
                                                 T* __restrict__ shifts) {
     __shared__ int32_t buf[kNlCap];
     const NlGrid g = *gp;
-    // brute grids: every atom; cell grids: the atoms the cell emit leaves (> kEmitBuf neighbours)
+    // brute grids: every atom; cell grids: the atoms the cell emit leaves (> kEmitBuf
+    // neighbours, listed by the count pass)
     const bool only_big = !g.brute;
+    const int64_t items = only_big ? g.nbig : n;
     const bool periodic = g.periodic;
     const int lane = threadIdx.x;
     const AcceptTest<T> at = accept_test<T>(box, periodic, true, cutoff);
-    for (int i = blockIdx.x; i < n; i += gridDim.x) {
-        if (only_big && counts[i] <= kEmitBuf) continue;
+    for (int64_t t = blockIdx.x; t < items; t += gridDim.x) {
+        const int i = only_big ? big[t] : int(t);
         int count = 0;
         __syncthreads();  // buf is reused across atoms
         for_candidates<T>(pos, i, n, g, cell_start, atoms_sorted, mode, [&](int j) {
@@ -567,7 +571,7 @@ __global__ void __launch_bounds__(kWave) k_count_cells(const T* __restrict__ pos
                                                        int mode, NlGrid* __restrict__ gp,
                                                        const int32_t* __restrict__ cell_start,
                                                        const int32_t* __restrict__ atoms_sorted,
-                                                       int32_t* __restrict__ counts) {
+                                                       int32_t* __restrict__ counts, int32_t* __restrict__ big) {
     const NlGrid g = *gp;
     if (g.brute) return;
     const int lane = threadIdx.x;
@@ -604,6 +608,7 @@ __global__ void __launch_bounds__(kWave) k_count_cells(const T* __restrict__ pos
             if (lane < nq) {
                 counts[my_i] = my_count;
                 if (my_count > kNlCap) atomicExch(&gp->overflow, 1);
+                if (my_count > kEmitBuf) big[atomicAdd(&gp->nbig, 1)] = my_i;
             }
         }
     }
@@ -777,7 +782,7 @@ int nlist_count(const T* pos, int64_t n, double cutoff, const T* box, int mode, 
         MNX_CHECK_LAUNCH();
         const unsigned blocks = unsigned(std::min<int64_t>(std::max<int64_t>(n, w.max_cells * kCellParts), kNlBlocks));
         hipLaunchKernelGGL((k_count_cells<T>), dim3(blocks), dim3(kWave), 0, stream, pos, box, T(cutoff), mode,
-                           w.grid, w.cell_start, w.atoms_sorted, w.counts);
+                           w.grid, w.cell_start, w.atoms_sorted, w.counts, w.big);
         MNX_CHECK_LAUNCH();
         hipLaunchKernelGGL((k_count<T>), dim3(blocks), dim3(kWave), 0, stream, pos, n, box, T(cutoff), mode, w.grid,
                            w.cell_start, w.atoms_sorted, w.counts);
@@ -822,7 +827,7 @@ int nlist_emit(const T* pos, int64_t n, double cutoff, const T* box, int mode, i
                            dist, shifts);
         MNX_CHECK_LAUNCH();
         hipLaunchKernelGGL((k_emit<T>), dim3(blocks), dim3(kWave), 0, stream, pos, n, box, T(cutoff), mode, layout,
-                           w.grid, w.cell_start, w.atoms_sorted, w.counts, w.offsets, capacity, idx_i, idx_j, deltas,
+                           w.grid, w.cell_start, w.atoms_sorted, w.big, w.offsets, capacity, idx_i, idx_j, deltas,
                            dist, shifts);
         MNX_CHECK_LAUNCH();
     }
