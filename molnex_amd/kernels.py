@@ -15,6 +15,7 @@ Ops
 ``molix::tp_scatter``           channelwise TP + scatter-sum (``cuet.ChannelWiseTensorProduct``)
 ``molix::radial_hidden``        fused hidden stack of the radial weight MLP (gradient w.r.t. its input)
 ``molix::bond_vectors``         pos[receiver] - pos[sender] - shift per edge, with its position gradient
+``molix::block_linear``         equivariant (ir_mul) block linear with pre-ordered weights (``cuet.Linear``)
 """
 
 from __future__ import annotations
@@ -803,6 +804,75 @@ def _radial_bwd(ctx, grad):
 
 
 radial_hidden.register_autograd(_radial_bwd, setup_context=_radial_setup)
+
+
+# ---------------------------------------------------------------------------
+# Equivariant block linear
+# ---------------------------------------------------------------------------
+
+def block_linear_desc(blocks) -> list[int]:
+    """Flat launch list of ``molix::block_linear``: per output block
+    ``out_off, mul, d, w_off, nseg`` followed by ``col, comp, len`` of each input segment."""
+    flat = []
+    for off, mul, d, segs, woff in blocks:
+        flat += [int(off), int(mul), int(d), int(woff), len(segs)]
+        for sg in segs:
+            flat += [int(v) for v in sg]
+    return flat
+
+
+def _parse_blocks(blocks: list[int]):
+    i = 0
+    while i < len(blocks):
+        if i + 5 > len(blocks):
+            raise ValueError("block_linear: truncated block list")
+        off, mul, d, woff, n = blocks[i:i + 5]
+        segs = blocks[i + 5:i + 5 + 3 * n]
+        if n < 0 or len(segs) != 3 * n:
+            raise ValueError("block_linear: truncated block list")
+        i += 5 + 3 * n
+        yield off, mul, d, woff, [tuple(segs[3 * s:3 * s + 3]) for s in range(n)]
+
+
+@torch.library.custom_op("molix::block_linear", mutates_args=(), device_types="cuda")
+def block_linear(a: Tensor, weights: Tensor, blocks: list[int], out_dim: int) -> Tensor:
+    """One ``mnx_block_linear_f32`` launch per output block of an ir_mul linear
+    (``src/molrep/interaction/linear.py:43-105``): ``blocks`` as built by ``block_linear_desc``,
+    ``weights`` the concatenated fragment-ordered (pre-scaled) weights of every block.  Every column
+    of the (R, out_dim) result must belong to exactly one block."""
+    _require_gpu("block_linear", a, weights)
+    if a.dtype != torch.float32 or weights.dtype != torch.float32 or a.dim() != 2:
+        raise TypeError("block_linear: a must be float32 (R, dim_in) and weights float32")
+    lib = _lib.load()
+    x = _aligned16(a)
+    w = _aligned16(weights.reshape(-1))
+    R, dim_in = x.shape
+    out = x.new_empty(R, out_dim)
+    covered = 0
+    for off, mul, d, woff, segs in _parse_blocks(blocks):
+        if off < 0 or off + d * mul > out_dim or mul <= 0 or d <= 0:
+            raise ValueError("block_linear: output block outside the result")
+        covered += d * mul
+        if any(c < 0 or ln <= 0 or c + (d - 1) * cp + ln > dim_in for c, cp, ln in segs):
+            raise ValueError("block_linear: input segment outside the input rows")
+        k = sum(ln for _, _, ln in segs)
+        if segs and (woff < 0 or woff + lib.mnx_block_linear_frag_floats(k, mul) > w.numel()):
+            raise ValueError("block_linear: block weights outside the weight vector")
+        n = len(segs)
+        cols = (C.c_int64 * max(n, 1))(*[sg[0] for sg in segs])
+        comps = (C.c_int32 * max(n, 1))(*[sg[1] for sg in segs])
+        lens = (C.c_int32 * max(n, 1))(*[sg[2] for sg in segs])
+        wp = w.data_ptr() + 4 * woff if segs else None
+        check(lib.mnx_block_linear_f32(ptr(x), dim_in, n, cols, comps, lens, wp, mul, R, d, ptr(out), out_dim, off,
+                                       mul, _stream(x)), "block_linear")
+    if covered != out_dim:
+        raise ValueError("block_linear: output blocks do not cover the result")
+    return out
+
+
+@block_linear.register_fake
+def _(a, weights, blocks, out_dim):
+    return a.new_empty(a.shape[0], out_dim)
 
 
 # ---------------------------------------------------------------------------

@@ -27,7 +27,7 @@ import torch
 import torch.nn as nn
 from pydantic import BaseModel
 
-from ... import _lib
+from ... import kernels as K
 from ...config import config
 from ...irreps import Irreps
 
@@ -58,6 +58,7 @@ class Linear(nn.Module):
             self.weight = nn.Parameter(torch.randn(1, self.weight_numel, dtype=dt))
         else:
             self.register_parameter("weight", None)
+        self._setup_hip()
 
     def _mix(self, x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
         """x (R, dim_in), w (weight_numel,) -> (R, dim_out)."""
@@ -66,18 +67,23 @@ class Linear(nn.Module):
         return _BlockLinear.apply(x, w, self.plan, self.irreps_out.dim)
 
     def _hip_ok(self) -> bool:
-        """Shapes the HIP block kernel takes: every multiplicity a multiple of 8, at most 8
-        source blocks per output block and 8 consumers per input block."""
-        if not hasattr(self, "_hip_plan"):
-            ok = all(b.mul % 8 == 0 for b in self.irreps_in) and all(o.mul % 8 == 0 for o in self.irreps_out)
-            users = {}
-            for _, _, _, srcs, _ in self.plan:
-                ok = ok and len(srcs) <= 8
-                for o, _, _ in srcs:
-                    users[o] = users.get(o, 0) + 1
-            ok = ok and all(c <= 8 for c in users.values())
-            self._hip_plan = _hip_plan(self) if ok else None
         return self._hip_plan is not None
+
+    def _setup_hip(self) -> None:
+        """Launch lists and fragment-order weight tables of the HIP block kernel, for shapes it
+        takes: every multiplicity a multiple of 8, at most 8 source blocks per output block and 8
+        consumers per input block.  The tables are non-persistent buffers, so they follow the
+        module's device and appear as constants when the module is traced."""
+        ok = all(b.mul % 8 == 0 for b in self.irreps_in) and all(o.mul % 8 == 0 for o in self.irreps_out)
+        users = {}
+        for _, _, _, srcs, _ in self.plan:
+            ok = ok and len(srcs) <= 8
+            for o, _, _ in srcs:
+                users[o] = users.get(o, 0) + 1
+        ok = ok and all(c <= 8 for c in users.values())
+        self._hip_plan = _hip_plan(self) if ok else None
+        for name in ("idx_f", "sc_f", "idx_b", "sc_b"):
+            self.register_buffer("_hip_" + name, self._hip_plan.pop(name) if ok else None, persistent=False)
 
     def forward(self, x: torch.Tensor, weight: torch.Tensor | None = None,
                 weight_indices: torch.Tensor | None = None) -> torch.Tensor:
@@ -259,46 +265,15 @@ def _hip_plan(lin: "Linear"):
             sc_b.append(s_)
             off += i_.numel()
     cat = lambda xs, dt: torch.cat(xs).to(dt) if xs else torch.zeros(0, dtype=dt)
-    return {"fwd": fwd, "bwd": bwd, "idx_f": cat(idx_f, torch.long), "sc_f": cat(sc_f, torch.float32),
-            "idx_b": cat(idx_b, torch.long), "sc_b": cat(sc_b, torch.float32), "dev": {}}
-
-
-def _hip_tables(hp, device):
-    key = str(device)
-    if key not in hp["dev"]:
-        hp["dev"][key] = tuple(hp[k].to(device) for k in ("idx_f", "sc_f", "idx_b", "sc_b"))
-    return hp["dev"][key]
-
-
-def _launch_blocks(a, a_stride, blocks, wstack, R, out, out_stride):
-    import ctypes as C
-
-    lib = _lib.load()
-    stream = torch.cuda.current_stream(a.device).cuda_stream
-    for off, mul, d, segs, woff in blocks:
-        n = len(segs)
-        cols = (C.c_int64 * max(n, 1))(*[sg[0] for sg in segs])
-        comps = (C.c_int32 * max(n, 1))(*[sg[1] for sg in segs])
-        lens = (C.c_int32 * max(n, 1))(*[sg[2] for sg in segs])
-        _lib.check(lib.mnx_block_linear_f32(a.data_ptr(), a_stride, n, cols, comps, lens,
-                                            wstack.data_ptr() + 4 * woff if wstack.numel() else None, mul, R, d,
-                                            out.data_ptr(), out_stride, off, mul, stream), "block linear")
-
-
-def _aligned(x: torch.Tensor) -> torch.Tensor:
-    x = x.contiguous()
-    return x if x.data_ptr() % 16 == 0 else x.clone()
+    return {"fwd": K.block_linear_desc(fwd), "bwd": K.block_linear_desc(bwd), "idx_f": cat(idx_f, torch.long),
+            "sc_f": cat(sc_f, torch.float32), "idx_b": cat(idx_b, torch.long), "sc_b": cat(sc_b, torch.float32)}
 
 
 class _HipBlockLinear(torch.autograd.Function):
     @staticmethod
     def forward(ctx, x, w, lin):
-        hp = lin._hip_plan
-        idx_f, sc_f, _, _ = _hip_tables(hp, x.device)
-        xs = _aligned(x)
-        ws = (w.index_select(0, idx_f) * sc_f).contiguous()
-        out = x.new_empty(x.shape[0], lin.irreps_out.dim)
-        _launch_blocks(xs, xs.shape[1], hp["fwd"], ws, xs.shape[0], out, out.shape[1])
+        ws = w.index_select(0, lin._hip_idx_f.to(w.device)) * lin._hip_sc_f.to(w.device)
+        out = torch.ops.molix.block_linear(x, ws, lin._hip_plan["fwd"], lin.irreps_out.dim)
         ctx.save_for_backward(x, w)
         ctx.lin = lin
         return out
@@ -309,13 +284,10 @@ class _HipBlockLinear(torch.autograd.Function):
         lin = ctx.lin
         need_x, need_w = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
         gx = gw = None
-        g = _aligned(g)
+        g = g.contiguous()
         if need_x:
-            hp = lin._hip_plan
-            _, _, idx_b, sc_b = _hip_tables(hp, x.device)
-            wb = (w.index_select(0, idx_b) * sc_b).contiguous()
-            gx = x.new_empty(x.shape)
-            _launch_blocks(g, g.shape[1], hp["bwd"], wb, x.shape[0], gx, gx.shape[1])
+            wb = w.index_select(0, lin._hip_idx_b.to(w.device)) * lin._hip_sc_b.to(w.device)
+            gx = torch.ops.molix.block_linear(g, wb, lin._hip_plan["bwd"], x.shape[1])
         if need_w:
             _, gw = _block_backward(x, w, g, lin.plan, False, True)
         return gx, gw, None

@@ -57,6 +57,10 @@ _graph_cache: dict = {}
 
 
 def edge_graph(edge_index: torch.Tensor, num_nodes: int) -> EdgeGraph:
+    """The EdgeGraph of ``edge_index``, cached on the tensor's storage and version so every layer of
+    one step shares it.  Under torch.compile / torch.export the CSR is built in the traced graph."""
+    if torch.compiler.is_compiling():
+        return EdgeGraph(edge_index, num_nodes)
     key = (edge_index.data_ptr(), edge_index.shape[0], num_nodes, edge_index._version, edge_index.device)
     g = _graph_cache.get(key)
     if g is None or g.edge_index is not edge_index:
