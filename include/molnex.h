@@ -317,6 +317,29 @@ int mnx_radial_bwd_f32(const float* feats, int64_t num_edges, int32_t kin, int32
                        int32_t layers, const float* frag, const float* grad_h, float* grad_feats,
                        mnx_stream_t stream);
 
+/* ------------------------------------------------------------------------ */
+/* Output layer of the radial weight MLP (the last Linear of                 */
+/* RadialWeightMLP, src/molrep/interaction/radial_mlp.py:38-93): per-edge    */
+/* tensor-product weights w[e][n] = sum_k h[e][k] W[n][k] + bias[n]          */
+/* (mnx_edge_weights_f32; bias may be NULL) and the input gradient           */
+/* grad_h[e][k] = sum_n grad_w[e][n] W[n][k] (mnx_edge_weights_bwd_f32,      */
+/* overwritten).  W is the torch.nn.Linear weight [N][K].  Products are      */
+/* fp32-accurate: each operand is split exactly into three bf16 parts and    */
+/* six partial products are accumulated in fp32 on the matrix cores.         */
+/* mnx_edge_weights_pack_f32 splits and arranges W once into frag            */
+/* [mnx_edge_weights_frag_elems(K, N, backward)] bf16 values (16-byte        */
+/* aligned), backward = 0 for the forward layout, 1 for the backward one.    */
+/* K in {16, 32, 64, 128} (else MNX_ERR_UNSUPPORTED; the size query returns  */
+/* -1); the backward needs N % 8 == 0; h and grad_w 16-byte aligned.         */
+/* ------------------------------------------------------------------------ */
+int64_t mnx_edge_weights_frag_elems(int32_t K, int32_t N, int32_t backward);
+int mnx_edge_weights_pack_f32(const float* weight, int32_t K, int32_t N, int32_t backward, uint16_t* frag,
+                              mnx_stream_t stream);
+int mnx_edge_weights_f32(const float* h, int64_t num_edges, int32_t K, const uint16_t* frag,
+                         const float* bias, int32_t N, float* w, mnx_stream_t stream);
+int mnx_edge_weights_bwd_f32(const float* grad_w, int64_t num_edges, int32_t N, const uint16_t* frag,
+                             int32_t K, float* grad_h, mnx_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

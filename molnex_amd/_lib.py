@@ -70,6 +70,10 @@ SIGNATURES = {
     "mnx_radial_pack_f32": (C.c_int, [vp, c_i32, c_i32, c_i32, vp, vp]),
     "mnx_radial_fwd_f32": (C.c_int, [vp, c_i64, c_i32, c_i32, c_i32, vp, vp, vp]),
     "mnx_radial_bwd_f32": (C.c_int, [vp, c_i64, c_i32, c_i32, c_i32, vp, vp, vp, vp]),
+    "mnx_edge_weights_frag_elems": (c_i64, [c_i32, c_i32, c_i32]),
+    "mnx_edge_weights_pack_f32": (C.c_int, [vp, c_i32, c_i32, c_i32, vp, vp]),
+    "mnx_edge_weights_f32": (C.c_int, [vp, c_i64, c_i32, vp, vp, c_i32, vp, vp]),
+    "mnx_edge_weights_bwd_f32": (C.c_int, [vp, c_i64, c_i32, vp, c_i32, vp, vp]),
 }
 
 

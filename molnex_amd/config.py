@@ -16,6 +16,9 @@ class _Config:
     # True: RadialWeightMLP runs its hidden stack as one fused HIP kernel when its
     # parameters need no gradient (energy + forces); False: always the Sequential
     fused_radial: bool = True
+    # True: RadialWeightMLP's last Linear (the per-edge tensor-product weights) runs as the
+    # split-bf16 matrix-core kernel molix::edge_weights; False: hipBLASLt fp32 GEMMs
+    edge_weights_kernel: bool = True
 
 
 config = _Config()

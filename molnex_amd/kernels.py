@@ -14,6 +14,7 @@ Ops
 ``molix::edge_csr``             receiver CSR of an (E, 2) edge list
 ``molix::tp_scatter``           channelwise TP + scatter-sum (``cuet.ChannelWiseTensorProduct``)
 ``molix::radial_hidden``        fused hidden stack of the radial weight MLP (gradient w.r.t. its input)
+``molix::edge_weights``         output layer of the radial weight MLP (per-edge TP weights), fp32-accurate split-bf16 MFMA
 ``molix::bond_vectors``         pos[receiver] - pos[sender] - shift per edge, with its position gradient
 ``molix::block_linear``         equivariant (ir_mul) block linear with pre-ordered weights (``cuet.Linear``)
 """
@@ -804,6 +805,100 @@ def _radial_bwd(ctx, grad):
 
 
 radial_hidden.register_autograd(_radial_bwd, setup_context=_radial_setup)
+
+
+# ---------------------------------------------------------------------------
+# Radial weight MLP output layer (per-edge tensor-product weights)
+# ---------------------------------------------------------------------------
+
+_EW_ROWS = 1 << 18
+
+
+def edge_weights_supported(in_dim: int, out_dim: int) -> bool:
+    """Whether ``molix::edge_weights`` (and its backward) take an in_dim -> out_dim Linear."""
+    return _lib.load().mnx_edge_weights_frag_elems(int(in_dim), int(out_dim), 1) > 0 and out_dim % 8 == 0
+
+
+def _ew_frag(weight: Tensor, backward: bool) -> Tensor:
+    lib = _lib.load()
+    N, K = weight.shape
+    n = lib.mnx_edge_weights_frag_elems(K, N, int(backward))
+    if n < 0:
+        raise ValueError(f"edge_weights: no kernel for a {K} -> {N} layer")
+    w = weight.detach().to(torch.float32).contiguous()
+    frag = torch.empty(n, dtype=torch.int16, device=w.device)
+    check(lib.mnx_edge_weights_pack_f32(ptr(w), K, N, int(backward), ptr(frag), _stream(w)), "edge_weights pack")
+    return frag
+
+
+@torch.library.custom_op("molix::edge_weights", mutates_args=(), device_types="cuda")
+def edge_weights(h: Tensor, weight: Tensor, bias: Tensor | None = None) -> Tensor:
+    """``h @ weight.T + bias``: the last Linear of ``RadialWeightMLP`` (``radial_mlp.py:38-93``) mapping
+    the (E, K) hidden activations to the (E, N) per-edge tensor-product weights.  fp32-accurate:
+    each operand split exactly into three bf16 parts, six partial products accumulated in fp32 on
+    the matrix cores."""
+    _require_gpu("edge_weights", h, weight, bias)
+    if h.dtype != torch.float32 or weight.dtype != torch.float32 or h.dim() != 2 or weight.dim() != 2:
+        raise TypeError("edge_weights: h (E, K) and weight (N, K) must be float32")
+    N, K = weight.shape
+    if h.shape[1] != K:
+        raise ValueError(f"edge_weights: h has {h.shape[1]} columns, weight expects {K}")
+    if bias is not None and (bias.dtype != torch.float32 or bias.shape != (N,)):
+        raise ValueError("edge_weights: bias must be float32 (N,)")
+    x = _aligned16(h)
+    frag = _ew_frag(weight, False)
+    out = x.new_empty(x.shape[0], N)
+    b = None if bias is None else bias.detach().contiguous()
+    check(_lib.load().mnx_edge_weights_f32(ptr(x), x.shape[0], K, ptr(frag), ptr(b), N, ptr(out), _stream(x)),
+          "edge_weights")
+    return out
+
+
+@edge_weights.register_fake
+def _(h, weight, bias=None):
+    return h.new_empty(h.shape[0], weight.shape[0])
+
+
+@torch.library.custom_op("molix::edge_weights_backward", mutates_args=(), device_types="cuda")
+def edge_weights_backward(grad: Tensor, weight: Tensor) -> Tensor:
+    """``grad @ weight``: dL/dh of ``edge_weights`` (same split-bf16 arithmetic)."""
+    N, K = weight.shape
+    if grad.dim() != 2 or grad.shape[1] != N:
+        raise ValueError("edge_weights_backward: grad must be (E, N)")
+    g = _aligned16(grad.to(torch.float32))
+    frag = _ew_frag(weight, True)
+    gh = g.new_empty(g.shape[0], K)
+    check(_lib.load().mnx_edge_weights_bwd_f32(ptr(g), g.shape[0], N, ptr(frag), K, ptr(gh), _stream(g)),
+          "edge_weights backward")
+    return gh
+
+
+@edge_weights_backward.register_fake
+def _(grad, weight):
+    return grad.new_empty(grad.shape[0], weight.shape[1])
+
+
+def _ew_setup(ctx, inputs, output):
+    h, weight, bias = inputs
+    ctx.save_for_backward(h, weight)
+    ctx.has_bias = bias is not None
+
+
+def _ew_bwd(ctx, grad):
+    h, weight = ctx.saved_tensors
+    need_h, need_w, need_b = ctx.needs_input_grad
+    grad = grad.contiguous()
+    gh = edge_weights_backward(grad, weight) if need_h else None
+    gw = None
+    if need_w:  # training: the (N, K) weight gradient as row-chunked hipBLASLt GEMMs
+        gw = torch.zeros_like(weight)
+        for i in range(0, h.shape[0], _EW_ROWS):
+            gw.addmm_(grad[i:i + _EW_ROWS].t(), h[i:i + _EW_ROWS])
+    gb = grad.sum(0) if (need_b and ctx.has_bias) else None
+    return gh, gw, gb
+
+
+edge_weights.register_autograd(_ew_bwd, setup_context=_ew_setup)
 
 
 # ---------------------------------------------------------------------------

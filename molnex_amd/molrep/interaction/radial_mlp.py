@@ -6,6 +6,10 @@ straight into one output (hipBLASLt picks a faster kernel for chunk-sized proble
 instead of 14.0 ms at that size on MI355X), with an explicit backward doing the same.
 ``.mlp`` stays the reference's ``Sequential`` so parameters and their names are unchanged.
 
+On the GPU in float32 the last Linear runs as ``molix::edge_weights`` (fp32-accurate products
+from three-way bf16 splits on the matrix cores, bound by the store of its output rather than by
+the fp32 matrix-core rate) for input widths 16/32/64/128.
+
 When the hidden Linears' parameters need no gradient (energy + forces with fixed weights)
 the hidden stack ``[Linear -> SiLU] x num_layers`` runs as one fused HIP kernel
 (``molix::radial_hidden``, gradient w.r.t. the edge features only); otherwise, and for
@@ -100,6 +104,10 @@ class RadialWeightMLP(nn.Module):
             for layer in self.mlp[:-1]:
                 h = layer(h)
         last = self.mlp[-1]
+        if (config.edge_weights_kernel and h.is_cuda and h.dim() == 2 and h.dtype == torch.float32
+                and last.weight.dtype == torch.float32
+                and kernels.edge_weights_supported(last.in_features, last.out_features)):
+            return kernels.edge_weights(h, last.weight, last.bias)
         if h.dim() == 2 and h.shape[0] > _CHUNK and h.is_cuda:
             return _ChunkedLinear.apply(h, last.weight, last.bias)
         return last(h)
