@@ -16,6 +16,18 @@
 // layers.  The weights are pre-arranged (k_radial_pack) in that k order,
 // "fragment" layout [tile][s/4][lane][s%4], staged through LDS, so every
 // A-operand read is one conflict-free 16-byte LDS read per lane.
+//
+// Layers with K = hidden inputs (every layer but the first, forward and
+// backward) run on the bf16 matrix cores with fp32-accurate products: each
+// operand is split exactly into three bf16 parts (x0 = bf16(x), x1 = bf16(x -
+// x0), x2 = bf16(x - x0 - x1)) and the six partial products x_i y_j with
+// i + j <= 2 are accumulated in fp32 by v_mfma_f32_32x32x16_bf16 (the dropped
+// terms are below 2^-25 |x y|), at 3/8 of the matrix-core cycles of fp32
+// MFMAs.  The D layout feeds these layers too: bf16 k-step q of lane half h,
+// element j, is feature 16q + 8(j/4) + 4h + j%4, i.e. registers 8(q%2) .. +7 of
+// tile q/2.  The weights of these layers are pre-split into three bf16 planes,
+// layout [q][tile][plane][lane][8].  The first layer (K = the few radial
+// features) stays on fp32 MFMAs.
 
 #include "common.h"
 
@@ -24,21 +36,26 @@ namespace {
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 
 constexpr int kRadThreads = 256;  // four wavefronts, 32 edges each
 constexpr int kRadEdgesPerBlock = (kRadThreads / 64) * 32;
 constexpr int kRadMaxIn = 64;
 
 // Fragment buffer layout (floats): forward fragments of layers 0..L-1, backward
-// (transposed) fragments of layers 0..L-1, then the L x H biases.
+// (transposed) fragments of layers 0..L-1, then the L x H biases.  Forward layer
+// 0 is fp32 ([tile][kp/8][lane][4]); every other block holds three bf16 planes,
+// [H/16][tiles][3][lane][8] (768 floats per k-step and tile).
+constexpr int kX3Block = 768;  // floats per (k-step, tile) of split-bf16 fragments
+
 struct RadLayout {
     int kin, kp, H, L;
+    __host__ __device__ int tiles_bwd(int j) const { return ((j == 0 ? kp : H) + 31) / 32; }
     __host__ __device__ int64_t fwd_size(int j) const {
-        return int64_t(H / 32) * ((j == 0 ? kp : H) / 8) * 256;
+        return j == 0 ? int64_t(H / 32) * (kp / 8) * 256 : int64_t(H / 32) * (H / 16) * kX3Block;
     }
-    __host__ __device__ int64_t bwd_size(int j) const {
-        return int64_t(((j == 0 ? kp : H) + 31) / 32) * (H / 8) * 256;
-    }
+    __host__ __device__ int64_t bwd_size(int j) const { return int64_t(tiles_bwd(j)) * (H / 16) * kX3Block; }
     __host__ __device__ int64_t fwd_off(int j) const {
         int64_t o = 0;
         for (int i = 0; i < j; ++i) o += fwd_size(i);
@@ -57,7 +74,22 @@ struct RadLayout {
     __host__ __device__ int64_t raw_total() const { return raw_w(L); }
 };
 
-// Builds the fragment buffer from the raw parameters; one thread per element.
+__device__ __forceinline__ void split3(float v, __bf16& b0, __bf16& b1, __bf16& b2) {
+    b0 = (__bf16)v;
+    float r = v - (float)b0;
+    b1 = (__bf16)r;
+    r -= (float)b1;
+    b2 = (__bf16)r;
+}
+
+__device__ __forceinline__ __bf16 split_part(float v, int p) {
+    __bf16 b0, b1, b2;
+    split3(v, b0, b1, b2);
+    return p == 0 ? b0 : (p == 1 ? b1 : b2);
+}
+
+// Builds the fragment buffer from the raw parameters; one thread per float
+// (two bf16 values in the split blocks).
 __global__ void k_radial_pack(const float* __restrict__ raw, RadLayout lay, float* __restrict__ frag) {
     const int64_t idx = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
     if (idx >= lay.total()) return;
@@ -66,24 +98,40 @@ __global__ void k_radial_pack(const float* __restrict__ raw, RadLayout lay, floa
         const int64_t b = idx - lay.bias_off();
         const int j = int(b / lay.H), m = int(b % lay.H);
         v = raw[lay.raw_b(j) + m];
+    } else if (idx < lay.fwd_off(1)) {
+        // forward layer 0, fp32 fragments [tile][q][lane][4]: k-step 4q+i of lane half h = feature 8q+4h+i
+        const int i = int(idx % 4), lane = int((idx / 4) % 64);
+        const int64_t rest = idx / 256;
+        const int nq = lay.kp / 8;
+        const int q = int(rest % nq), t = int(rest / nq);
+        const int k = 8 * q + 4 * (lane / 32) + i;
+        const int row = 32 * t + lane % 32;
+        if (k < lay.kin) v = raw[lay.raw_w(0) + int64_t(row) * lay.kin + k];
     } else {
         const bool bwd = idx >= lay.bwd_off(0);
-        int j = 0;
+        int j = bwd ? 0 : 1;
         while (idx >= (bwd ? lay.bwd_off(j + 1) : lay.fwd_off(j + 1))) ++j;
         const int64_t r = idx - (bwd ? lay.bwd_off(j) : lay.fwd_off(j));
-        const int kraw = j == 0 ? lay.kin : lay.H;
-        const int i = int(r % 4), lane = int((r / 4) % 64);
-        const int64_t rest = r / 256;
-        const int nq = bwd ? lay.H / 8 : (j == 0 ? lay.kp : lay.H) / 8;
-        const int q = int(rest % nq), t = int(rest / nq);
-        const int kstep = 8 * q + 4 * (lane / 32) + i;  // contraction index of this element
-        const int row = 32 * t + lane % 32;             // MFMA row (output feature, or input feature if bwd)
+        const int kraw = j == 0 ? lay.kin : lay.H;  // layer j's input width
+        const int tiles = bwd ? lay.tiles_bwd(j) : lay.H / 32;
         const float* W = raw + lay.raw_w(j);
-        if (!bwd) {
-            if (kstep < kraw) v = W[int64_t(row) * kraw + kstep];
-        } else {
-            if (row < kraw) v = W[int64_t(kstep) * kraw + row];
+        bf16x2 pair;
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            const int64_t e = 2 * r + u;  // bf16 element within the block
+            const int j8 = int(e % 8), lane = int((e / 8) % 64), p = int((e / 512) % 3);
+            const int t = int((e / 1536) % tiles), q = int(e / (1536 * int64_t(tiles)));
+            const int row = 32 * t + lane % 32;                                // A row
+            const int f = 16 * q + 8 * (j8 / 4) + 4 * (lane / 32) + j8 % 4;  // contraction feature
+            float w = 0.f;
+            if (!bwd) {
+                if (row < lay.H && f < lay.H) w = W[int64_t(row) * kraw + f];  // W_j[out][in]
+            } else {
+                if (row < kraw && f < lay.H) w = W[int64_t(f) * kraw + row];   // W_j^T
+            }
+            pair[u] = split_part(w, p);
         }
+        v = __builtin_bit_cast(float, pair);
     }
     frag[idx] = v;
 }
@@ -120,32 +168,48 @@ __device__ __forceinline__ void stage(const float* __restrict__ src, int n, f32x
     for (int i = threadIdx.x; i < n / 4; i += kRadThreads) dst[i] = s4[i];
 }
 
-// acc[t] += W(tile t) . in over K = 8 * NQ features held as in[s/16][s%16]; the
-// layer's fragments f ([T][NQ][64 lanes][4]) are staged in chunks of whole tiles.
-// Every wavefront of the workgroup must call it (barriers inside).
+// acc[t] += W(tile t) . in over K = 16 * NQ features held in the D layout as
+// in[q/2][8(q%2) + j] for k-step q (split-bf16 products, see the top of the
+// file).  The layer's fragments f ([NQ][T][3][64 lanes][8 bf16]) are staged in
+// chunks of whole k-steps, so each k-step's activations are split once.  Every
+// wavefront of the workgroup must call it (barriers inside).
 template <int T, int NQ>
-__device__ __forceinline__ void mfma_layer(const float* __restrict__ f, const float (&in)[NQ / 4][16],
+__device__ __forceinline__ void mfma_layer(const float* __restrict__ f, const float (&in)[NQ / 2][16],
                                            f32x16 (&acc)[T], RadShared& sh, int lane) {
-    constexpr int kTileFloats = NQ * 256;
-    constexpr int kTPC = kRadChunk / kTileFloats < T ? kRadChunk / kTileFloats : T;  // tiles per chunk
-    static_assert(kTPC >= 1, "one output tile of fragments must fit the staging area");
+    constexpr int kStep = T * kX3Block;  // floats per k-step
+    constexpr int kQPC = kRadChunk / kStep < NQ ? kRadChunk / kStep : NQ;  // k-steps per chunk
+    static_assert(kQPC >= 1, "one k-step of fragments must fit the staging area");
 #pragma unroll
-    for (int t0 = 0; t0 < T; t0 += kTPC) {
+    for (int q0 = 0; q0 < NQ; q0 += kQPC) {
         __syncthreads();
-        stage(f + t0 * kTileFloats, (T - t0 < kTPC ? T - t0 : kTPC) * kTileFloats, sh.frag);
+        stage(f + q0 * kStep, (NQ - q0 < kQPC ? NQ - q0 : kQPC) * kStep, sh.frag);
         __syncthreads();
 #pragma unroll
-        for (int q = 0; q < NQ; ++q) {
+        for (int qq = 0; qq < kQPC; ++qq) {
+            const int q = q0 + qq;
+            if (q >= NQ) break;
+            bf16x8 b0, b1, b2;
 #pragma unroll
-            for (int tt = 0; tt < kTPC; ++tt) {
-                if (t0 + tt < T) {
-                    const f32x4 a = sh.frag[(tt * NQ + q) * 64 + lane];
-#pragma unroll
-                    for (int i = 0; i < 4; ++i)
-                        acc[t0 + tt] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i], in[q / 4][4 * (q % 4) + i],
-                                                                           acc[t0 + tt], 0, 0, 0);
-                }
+            for (int j = 0; j < 8; ++j) {
+                __bf16 x0, x1, x2;
+                split3(in[q / 2][8 * (q % 2) + j], x0, x1, x2);
+                b0[j] = x0;
+                b1[j] = x1;
+                b2[j] = x2;
             }
+            auto a = [&](int t, int p) { return __builtin_bit_cast(bf16x8, sh.frag[((qq * T + t) * 3 + p) * 64 + lane]); };
+#pragma unroll
+            for (int t = 0; t < T; ++t) acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a(t, 2), b0, acc[t], 0, 0, 0);
+#pragma unroll
+            for (int t = 0; t < T; ++t) acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a(t, 1), b1, acc[t], 0, 0, 0);
+#pragma unroll
+            for (int t = 0; t < T; ++t) acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a(t, 0), b2, acc[t], 0, 0, 0);
+#pragma unroll
+            for (int t = 0; t < T; ++t) acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a(t, 1), b0, acc[t], 0, 0, 0);
+#pragma unroll
+            for (int t = 0; t < T; ++t) acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a(t, 0), b1, acc[t], 0, 0, 0);
+#pragma unroll
+            for (int t = 0; t < T; ++t) acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a(t, 0), b0, acc[t], 0, 0, 0);
         }
     }
 }
@@ -211,7 +275,7 @@ __global__ void __launch_bounds__(kRadThreads) k_radial_fwd(const float* __restr
     for (int j = 0; j < L; ++j) {
         if (j > 0) {
             zero(acc);
-            mfma_layer<T, H / 8>(frag + lay.fwd_off(j), act, acc, sh, lane);
+            mfma_layer<T, H / 16>(frag + lay.fwd_off(j), act, acc, sh, lane);
         }
 #pragma unroll
         for (int t = 0; t < T; ++t)
@@ -228,6 +292,19 @@ __global__ void __launch_bounds__(kRadThreads) k_radial_fwd(const float* __restr
                 *reinterpret_cast<f32x4*>(o + 32 * t + 8 * g + 4 * half) = v;
             }
     }
+}
+
+template <int T0>
+__device__ __forceinline__ void store_grad_feats(const f32x16 (&a0)[T0], float* __restrict__ grad_feats, int64_t e,
+                                                 bool valid, int kin, int half) {
+    if (!valid) return;
+#pragma unroll
+    for (int t = 0; t < T0; ++t)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int k = dfeat(t, r, half);
+            if (k < kin) grad_feats[e * kin + k] = a0[t][r];
+        }
 }
 
 template <int H, int L>
@@ -252,7 +329,7 @@ __global__ void __launch_bounds__(kRadThreads) k_radial_bwd(const float* __restr
     for (int j = 0; j < L; ++j) {
         if (j > 0) {
             zero(acc);
-            mfma_layer<T, H / 8>(frag + lay.fwd_off(j), g, acc, sh, lane);  // g holds silu(z_{j-1})
+            mfma_layer<T, H / 16>(frag + lay.fwd_off(j), g, acc, sh, lane);  // g holds silu(z_{j-1})
         }
         if (j < L - 1) {
 #pragma unroll
@@ -281,34 +358,23 @@ __global__ void __launch_bounds__(kRadThreads) k_radial_bwd(const float* __restr
 #pragma unroll
     for (int j = L - 1; j >= 1; --j) {
         zero(acc);
-        mfma_layer<T, H / 8>(frag + lay.bwd_off(j), g, acc, sh, lane);
+        mfma_layer<T, H / 16>(frag + lay.bwd_off(j), g, acc, sh, lane);
 #pragma unroll
         for (int t = 0; t < T; ++t)
 #pragma unroll
             for (int r = 0; r < 16; ++r) g[t][r] = acc[t][r] * silu_grad(z[j - 1][t][r]);
     }
-    // layer 0: dL/df^T (kp x 32) = W_0^T g, in ceil(kp / 32) <= 2 row tiles (one chunk)
-    const int tiles0 = (lay.kp + 31) / 32;
-    __syncthreads();
-    stage(frag + lay.bwd_off(0), tiles0 * (H / 8) * 256, sh.frag);
-    __syncthreads();
-    for (int t0 = 0; t0 < tiles0; ++t0) {
+    // layer 0: dL/df^T (kp x 32) = W_0^T g, in ceil(kp / 32) <= 2 row tiles
+    if (lay.tiles_bwd(0) == 1) {
         f32x16 a0[1];
         zero(a0);
-#pragma unroll
-        for (int q = 0; q < H / 8; ++q) {
-            const f32x4 a = sh.frag[(t0 * (H / 8) + q) * 64 + lane];
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-                a0[0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i], g[q / 4][4 * (q % 4) + i], a0[0], 0, 0, 0);
-        }
-        if (valid) {
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int k = dfeat(t0, r, half);
-                if (k < kin) grad_feats[e * kin + k] = a0[0][r];
-            }
-        }
+        mfma_layer<1, H / 16>(frag + lay.bwd_off(0), g, a0, sh, lane);
+        store_grad_feats(a0, grad_feats, e, valid, kin, half);
+    } else {
+        f32x16 a0[2];
+        zero(a0);
+        mfma_layer<2, H / 16>(frag + lay.bwd_off(0), g, a0, sh, lane);
+        store_grad_feats(a0, grad_feats, e, valid, kin, half);
     }
 }
 
