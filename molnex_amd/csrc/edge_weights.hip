@@ -218,10 +218,17 @@ __global__ __launch_bounds__(kEwFwdThreads) void k_ew_fwd(const float* __restric
                 const int n = (s * SC + t0 + u) * 32 + (lane & 31);
                 if (n >= N) continue;
                 const float b = sBias[buf][(t0 + u) * 32 + (lane & 31)];
+                float* o = out + (row0 + 4 * (lane >> 5)) * N + n;
+                if (row0 + 32 <= E) {  // whole row block valid: no per-row branches
 #pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    const int64_t row = row0 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-                    if (row < E) __builtin_nontemporal_store(acc[u][r] + b, out + row * N + n);
+                    for (int r = 0; r < 16; ++r)
+                        __builtin_nontemporal_store(acc[u][r] + b, o + int64_t(8 * (r >> 2) + (r & 3)) * N);
+                } else {
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) {
+                        const int64_t row = row0 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                        if (row < E) __builtin_nontemporal_store(acc[u][r] + b, o + int64_t(8 * (r >> 2) + (r & 3)) * N);
+                    }
                 }
             }
         }
