@@ -741,6 +741,17 @@ __global__ void k_pad(int64_t from_host, const int64_t* __restrict__ from_dev, i
     }
 }
 
+// Zeroes the per-cell counters and the grid header.
+__global__ void k_nl_clear(int32_t* __restrict__ cell_count, int32_t* __restrict__ cell_fill, int64_t ncells,
+                           int32_t* __restrict__ grid_words, int64_t ngrid) {
+    const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i < ncells) {
+        cell_count[i] = 0;
+        cell_fill[i] = 0;
+    }
+    if (i < ngrid) grid_words[i] = 0;
+}
+
 // *d_total = pair count, or -1 when some atom exceeded kNlCap neighbours.
 __global__ void k_report_total(const NlGrid* __restrict__ gp, const int64_t* __restrict__ total,
                                int64_t* __restrict__ d_total) {
@@ -758,9 +769,14 @@ int nlist_count(const T* pos, int64_t n, double cutoff, const T* box, int mode, 
     size_t need = 0;
     NlWs w = carve(ws, ws_bytes, n, &need);
     if (ws_bytes < need || !ws) return set_error(MNX_ERR_WORKSPACE, "workspace %zu < %zu bytes", ws_bytes, need);
-    MNX_HIP_TRY(hipMemsetAsync(w.cell_count, 0, sizeof(int32_t) * w.max_cells, stream));
-    MNX_HIP_TRY(hipMemsetAsync(w.cell_fill, 0, sizeof(int32_t) * w.max_cells, stream));
-    MNX_HIP_TRY(hipMemsetAsync(w.grid, 0, sizeof(NlGrid), stream));
+    {
+        // cleared by a kernel rather than hipMemsetAsync, so the sequence can sit in a captured HIP graph
+        const int64_t ng = int64_t(sizeof(NlGrid) / sizeof(int32_t));
+        const int64_t m = w.max_cells > ng ? w.max_cells : ng;
+        hipLaunchKernelGGL(k_nl_clear, dim3(ceil_div(m, 256)), dim3(256), 0, stream, w.cell_count, w.cell_fill,
+                           int64_t(w.max_cells), reinterpret_cast<int32_t*>(w.grid), ng);
+        MNX_CHECK_LAUNCH();
+    }
     hipLaunchKernelGGL((k_grid_setup<T>), dim3(1), dim3(1024), 0, stream, pos, n, box, cutoff, w.max_cells, w.grid);
     MNX_CHECK_LAUNCH();
     if (n > 0) {
