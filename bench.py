@@ -159,6 +159,37 @@ def time_tp_kernels(step: EdgeStep, reps: int = 5):
     return tf, tb
 
 
+def time_edge_weight_kernels(step: EdgeStep, reps: int = 5):
+    """Average duration of the radial MLP's output-layer kernels (molix::edge_weights forward and
+    input-gradient backward) at the step's shapes; HIP events on the current stream."""
+    K = step.K
+    with torch.no_grad():
+        r = torch.linalg.vector_norm(step.vec, dim=-1)
+        h = K.radial_hidden(bessel_cutoff(r, 5.0, 8, step.mu, step.sigma).contiguous(),
+                            torch.cat([t.reshape(-1) for m in step.mlp.mlp[:-1:2] for t in (m.weight, m.bias)]),
+                            8, 64, 2)
+    last = step.mlp.mlp[-1]
+    gw = torch.randn(h.shape[0], last.out_features, device=h.device)
+    fwd, bwd = [], []
+    for i in range(reps + 1):
+        e = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
+        e[0].record()
+        w = K.edge_weights(h, last.weight, last.bias)
+        e[1].record()
+        e[2].record()
+        K.edge_weights_backward(gw, last.weight)
+        e[3].record()
+        del w
+        if i:
+            fwd.append(e[:2])
+            bwd.append(e[2:])
+    torch.cuda.synchronize()
+    tf = sum(a.elapsed_time(b) for a, b in fwd) / reps
+    tb = sum(a.elapsed_time(b) for a, b in bwd) / reps
+    nbytes = 4 * h.shape[0] * (h.shape[1] + last.out_features)  # each direction: one E x K and one E x N tensor
+    return tf, tb, nbytes
+
+
 def measured_traffic(kernel: str):
     """HBM bytes per launch (FETCH_SIZE x calibration + WRITE_SIZE) of `kernel` at config 3,
     recorded from rocprofv3 --pmc runs in profiles/tp_scatter_config3_traffic.{json,md}."""
@@ -176,6 +207,30 @@ def tp_bytes(N, E, C, P=23, NX=16, NY=16, NO=99):
     fwd = 4 * (E * P * C + N * NO * C + N * NX * C + E * NY) + csr
     bwd = 4 * (2 * E * P * C + N * NO * C + 2 * N * NX * C + 2 * E * NY) + csr
     return fwd, bwd
+
+
+def mace_step_bytes(enc, N, E):
+    """Algorithmic HBM bytes of one energy + forces step of `enc` (fp32, each tensor once per kernel):
+    per interaction layer the radial MLP hidden stack (fwd: features in, h out; bwd: features and
+    grad_h in, grad_features out), its output layer (fwd: h in, per-edge weights out; bwd: their
+    gradient in, grad_h out) and the TP + scatter forward and backward (tp_bytes); once per step the
+    harmonics (vectors in, 16 components out, and back) and the bond vectors (positions and edge
+    list in, vectors out, and back).  Node-level kernels (linears, contraction, element updates, PME
+    on 50k atoms) move < 2 % of these bytes and are left out."""
+    from molnex_amd import kernels as K
+
+    total = 2 * (4 * E * 3 + 4 * E * 16) + 4 * E * 3  # harmonics fwd + bwd
+    total += 2 * (8 * E * 2 + 4 * E * 3 + 4 * N * 3)  # bond vectors fwd + bwd
+    for blk in enc.interactions:
+        P, NX, NY, NO = K.tp_config_info(blk.conv_tp.cue_tp.config_id)
+        C = blk.conv_tp.cue_tp.channels
+        rc = blk.radial_mlp.config
+        kin, H = rc.in_dim, rc.hidden_dim
+        tf, tb = tp_bytes(N, E, C, P, NX, NY, NO)
+        w = 4 * E * P * C
+        total += 4 * E * (kin + H) + (4 * E * H + w) + tf  # forward
+        total += tb + (w + 4 * E * H) + 4 * E * (kin + H + kin)  # backward
+    return total
 
 
 def cpu_baseline(edge_index, vec, x, C, mlp, mu, sigma, gout, target_s=15.0, max_edges=120_000):
@@ -313,7 +368,13 @@ def full_step_bench(args, dev):
         step()
     torch.cuda.synchronize()
     dt = (time.perf_counter() - t0) / args.steps
+    nbytes = mace_step_bytes(enc, n, int(edge_index.shape[0]))
+    achieved = nbytes / dt / 1e9
+    roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None, "kernel": "whole step",
+            "algorithmic_bytes": nbytes}
     return {"metric": "atoms/s energy+forces (MACE + PME)", "value": round(n / dt, 1), "unit": "atoms/s",
+            "roofline": roof,
             "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(dt * 1e3, 3),
             "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "fp32",
             "data": "synthetic (jittered lattice, random-init weights)",
@@ -435,7 +496,8 @@ def secondary_figures(args, dev):
         sub = argparse.Namespace(**{**vars(args), "steps": 3, "warmup": 2, "literal": lit})
         full = full_step_bench(sub, dev)
         out[key] = {"atoms_per_s": full["value"], "ms_per_step": full["ms_per_step"],
-                    "workload": full["config"]["workload"], "edges": full["config"]["edges"]}
+                    "workload": full["config"]["workload"], "edges": full["config"]["edges"],
+                    "hbm_frac": full["roofline"]["frac"], "algorithmic_GB": round(full["roofline"]["algorithmic_bytes"] / 1e9, 2)}
         torch.cuda.empty_cache()
     return out
 
@@ -484,6 +546,7 @@ def main():
     value = E * args.steps / dt / 1e6
 
     tf, tb = time_tp_kernels(step)
+    ewf, ewb, ew_bytes = time_edge_weight_kernels(step)
     bf, bb = tp_bytes(N, E, args.channels)
     dom_t, dom_b, dom_name = (tb, bb, "tp_scatter_bwd") if tb >= tf else (tf, bf, "tp_scatter_fwd")
     achieved = dom_b / (dom_t * 1e-3) / 1e9
@@ -493,7 +556,9 @@ def main():
         "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic, "kernel": dom_name,
         "kernel_ms": round(dom_t, 3), "algorithmic_bytes": dom_b,
         "other": {"tp_scatter_fwd_ms": round(tf, 3), "tp_scatter_fwd_GBs": round(bf / (tf * 1e-3) / 1e9, 1),
-                  "tp_scatter_bwd_ms": round(tb, 3), "tp_scatter_bwd_GBs": round(bb / (tb * 1e-3) / 1e9, 1)},
+                  "tp_scatter_bwd_ms": round(tb, 3), "tp_scatter_bwd_GBs": round(bb / (tb * 1e-3) / 1e9, 1),
+                  "edge_weights_fwd_ms": round(ewf, 3), "edge_weights_fwd_GBs": round(ew_bytes / (ewf * 1e-3) / 1e9, 1),
+                  "edge_weights_bwd_ms": round(ewb, 3), "edge_weights_bwd_GBs": round(ew_bytes / (ewb * 1e-3) / 1e9, 1)},
     }
     secondary = None
     if not args.no_secondary:
