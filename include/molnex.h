@@ -269,10 +269,12 @@ int mnx_sc_bwd_f32(int32_t config, const float* A, const int64_t* types, const f
 /* a[n*a_stride + seg_col[s] + i*seg_comp[s] + 0..seg_len[s]-1].  The K x N  */
 /* weights (K = sum seg_len, pre-scaled by the caller) come in the kernel's  */
 /* fragment order: with T = N >= 128 ? 4 : ceil(N/32) tiles, element         */
-/* [y][chunk][q][t][lane][i] (y < ceil(N/32T), chunk < ceil(K/64), q < 8,    */
-/* t < T, lane < 64, i < 4) holds W[64 chunk + 8q + 4(lane/32) + i]          */
+/* [y][chunk][q][t][lane][i] (y < ceil(N/32T), chunk < ceil(K/64), q < 4,    */
+/* t < T, lane < 64, i < 8) holds W[64 chunk + 16q + 8(lane/32) + i]         */
 /* [32T y + 32t + lane%32], zero outside K x N; mnx_block_linear_frag_floats */
-/* gives its length.  nseg = 0 writes zeros.  seg_len multiples of 8;        */
+/* gives its length.  Products are fp32-accurate (three-way bf16 splits of   */
+/* both operands, six partial products accumulated in fp32 on the matrix    */
+/* cores).  nseg = 0 writes zeros.  seg_len multiples of 8;                  */
 /* a_stride, seg_col, seg_comp multiples of 4; a and w 16-byte aligned; at   */
 /* most 8 segments.  Segment arrays are host memory.                        */
 /* ------------------------------------------------------------------------ */

@@ -9,13 +9,20 @@
 // with respect to an input block is the same product with the output-gradient
 // blocks as segments and the transposed weights.
 //
-// Each wavefront owns 32 rows (M side of v_mfma_f32_32x32x2f32) and up to 128
+// Each wavefront owns 32 rows (M side of v_mfma_f32_32x32x16_bf16) and up to 128
 // output columns (N side, NT tiles); A is read straight from the strided input
-// (16 bytes per lane, no gather copy).  W arrives pre-arranged by the caller in
-// MFMA fragment order, [column group][64-row chunk][k/8][tile][lane][4] with zero
-// padding (mnx_block_linear_frag_floats gives its size), so each chunk is staged
-// into LDS with contiguous 16-byte copies shared by the workgroup's eight
-// wavefronts.  The D tiles are stored 128 contiguous bytes per row.
+// (32 bytes per lane and k-step, no gather copy).  W arrives pre-arranged by the
+// caller in MFMA fragment order, [column group][64-row chunk][k/16][tile][lane][8]
+// (lane l holds W[16q + 8(l/32) + j][32t + l%32]) with zero padding
+// (mnx_block_linear_frag_floats gives its size); each chunk is staged into LDS
+// by the workgroup's eight wavefronts, split there into three bf16 planes.
+//
+// Arithmetic: fp32-accurate products on the bf16 matrix cores.  Each fp32
+// operand x is split exactly into x0 = bf16(x), x1 = bf16(x - x0),
+// x2 = bf16(x - x0 - x1); the six partial products x_i y_j with i + j <= 2 are
+// accumulated in fp32, smallest first (the dropped terms are below 2^-25 |x y|),
+// at 3/8 of the matrix-core cycles of fp32 MFMAs.  The D tiles are stored 128
+// contiguous bytes per row.
 
 #include "common.h"
 
@@ -24,6 +31,20 @@ namespace {
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ void split3(float v, __bf16& b0, __bf16& b1, __bf16& b2) {
+    b0 = (__bf16)v;
+    float r = v - (float)b0;
+    b1 = (__bf16)r;
+    r -= (float)b1;
+    b2 = (__bf16)r;
+}
+
+__device__ __forceinline__ f32x16 mfma_bf16(const bf16x8& a, const bf16x8& b, const f32x16& c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
 
 constexpr int kLinThreads = 512;  // eight wavefronts x 32 rows
 constexpr int kLinKC = 64;        // rows of W staged per pass
@@ -53,8 +74,9 @@ struct LinArgs {
 // is 1, 3, 5 or 7 (divisions by it become multiplies), 0 = read p.d.
 template <int NT, int D>
 __global__ void __launch_bounds__(kLinThreads) k_block_linear(LinArgs p) {
+    constexpr int KQ = kLinKC / 16;  // bf16 k-steps per staged chunk
     const int d = D ? D : p.d;
-    __shared__ f32x4 sw[kLinKC / 8][NT][kWave];
+    __shared__ bf16x8 sw[3][KQ][NT][kWave];
     const int lane = threadIdx.x & 63, half = lane >> 5, wave = threadIdx.x >> 6;
     const int64_t rows = p.R * d;
     const int64_t row0 = (int64_t(blockIdx.x) * (kLinThreads / kWave) + wave) * 32;
@@ -72,44 +94,77 @@ __global__ void __launch_bounds__(kLinThreads) k_block_linear(LinArgs p) {
     for (int t = 0; t < NT; ++t)
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[t][r] = 0.f;
-    constexpr int kChunk4 = (kLinKC / 8) * NT * kWave;  // float4s per staged chunk
+    constexpr int kChunk4 = KQ * NT * kWave * 2;  // fp32 float4s per staged chunk
     const int nchunks = (p.K + kLinKC - 1) / kLinKC;
     const f32x4* wsrc = reinterpret_cast<const f32x4*>(p.w) + int64_t(blockIdx.y) * nchunks * kChunk4;
-    f32x4* sw4 = &sw[0][0][0];
+    bf16x4* sw4 = reinterpret_cast<bf16x4*>(&sw[0][0][0][0]);
     // per segment, this lane's offset of contraction index k is base[s] + k (row-relative)
     int32_t base[kLinMaxSeg];
 #pragma unroll
     for (int sg = 0; sg < kLinMaxSeg; ++sg)
-        base[sg] = sg < p.nseg ? int32_t(p.seg[sg].col + int64_t(ci) * p.seg[sg].comp - p.seg[sg].k0 + 4 * half) : 0;
+        base[sg] = sg < p.nseg ? int32_t(p.seg[sg].col + int64_t(ci) * p.seg[sg].comp - p.seg[sg].k0) : 0;
     for (int k0 = 0; k0 < p.K; k0 += kLinKC) {
-        // this chunk's A operands first (one 16-byte load per k-block of 8): their
+        // this chunk's A operands first (8 consecutive values per lane and k-step): their
         // latency overlaps the weight staging below
-        f32x4 av[kLinKC / 8];
+        f32x4 av[KQ][2];
 #pragma unroll
-        for (int q = 0; q < kLinKC / 8; ++q) {
-            const int k = k0 + 8 * q;
+        for (int q = 0; q < KQ; ++q) {
+            const int k = k0 + 16 * q + 8 * half;
             int32_t off = 0;
 #pragma unroll
-            for (int sg = 0; sg < kLinMaxSeg; ++sg)  // k is wave-uniform: a scalar select chain
+            for (int sg = 0; sg < kLinMaxSeg; ++sg)
                 if (sg < p.nseg && k >= p.seg[sg].k0) off = base[sg];
-            av[q] = f32x4{0.f, 0.f, 0.f, 0.f};
-            if (valid && k < p.K) av[q] = *reinterpret_cast<const f32x4*>(arow + off + k);
+            av[q][0] = av[q][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+            if (valid && k < p.K) {
+                av[q][0] = *reinterpret_cast<const f32x4*>(arow + off + k);
+                av[q][1] = *reinterpret_cast<const f32x4*>(arow + off + k + 4);
+            }
         }
         __syncthreads();
-        for (int idx = threadIdx.x; idx < kChunk4; idx += kLinThreads) sw4[idx] = wsrc[idx];
+        // stage and split the chunk: fp32 float4 idx = ((q * NT + t) * 64 + lane) * 2 + h holds
+        // elements 4h..4h+3 of lane `lane`'s fragment; plane p goes to sw[p][q][t][lane]
+        for (int idx = threadIdx.x; idx < kChunk4; idx += kLinThreads) {
+            const f32x4 v = wsrc[idx];
+            bf16x4 b0, b1, b2;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                __bf16 x0, x1, x2;
+                split3(v[i], x0, x1, x2);
+                b0[i] = x0;
+                b1[i] = x1;
+                b2[i] = x2;
+            }
+            sw4[idx] = b0;
+            sw4[kChunk4 + idx] = b1;
+            sw4[2 * kChunk4 + idx] = b2;
+        }
         wsrc += kChunk4;
         __syncthreads();
-        const int nq = min(kLinKC, p.K - k0) / 8;
+        const int nq = (min(kLinKC, p.K - k0) + 15) / 16;
 #pragma unroll
-        for (int q = 0; q < kLinKC / 8; ++q) {
+        for (int q = 0; q < KQ; ++q) {
             if (q < nq) {
+                bf16x8 a0, a1, a2;
 #pragma unroll
-                for (int t = 0; t < NT; ++t) {
-                    const f32x4 b = sw[q][t][lane];
-#pragma unroll
-                    for (int i = 0; i < 4; ++i)
-                        acc[t] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[q][i], b[i], acc[t], 0, 0, 0);
+                for (int j = 0; j < 8; ++j) {
+                    __bf16 x0, x1, x2;
+                    split3(j < 4 ? av[q][0][j] : av[q][1][j - 4], x0, x1, x2);
+                    a0[j] = x0;
+                    a1[j] = x1;
+                    a2[j] = x2;
                 }
+#pragma unroll
+                for (int t = 0; t < NT; ++t) acc[t] = mfma_bf16(a2, sw[0][q][t][lane], acc[t]);
+#pragma unroll
+                for (int t = 0; t < NT; ++t) acc[t] = mfma_bf16(a1, sw[1][q][t][lane], acc[t]);
+#pragma unroll
+                for (int t = 0; t < NT; ++t) acc[t] = mfma_bf16(a0, sw[2][q][t][lane], acc[t]);
+#pragma unroll
+                for (int t = 0; t < NT; ++t) acc[t] = mfma_bf16(a1, sw[0][q][t][lane], acc[t]);
+#pragma unroll
+                for (int t = 0; t < NT; ++t) acc[t] = mfma_bf16(a0, sw[1][q][t][lane], acc[t]);
+#pragma unroll
+                for (int t = 0; t < NT; ++t) acc[t] = mfma_bf16(a0, sw[0][q][t][lane], acc[t]);
             }
         }
     }
@@ -158,7 +213,7 @@ extern "C" {
 int64_t mnx_block_linear_frag_floats(int32_t K, int32_t N) {
     if (K < 0 || N < 1) return -1;
     const int nt = lin_tiles(N);
-    return ceil_div(N, nt * 32) * ceil_div(K, kLinKC) * int64_t(kLinKC / 8) * nt * kWave * 4;
+    return ceil_div(N, nt * 32) * ceil_div(K, kLinKC) * int64_t(kLinKC / 16) * nt * kWave * 8;
 }
 
 int mnx_block_linear_f32(const float* a, int64_t a_stride, int32_t nseg, const int64_t* seg_col,

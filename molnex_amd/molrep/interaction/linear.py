@@ -12,7 +12,7 @@ the GPU through torch.mm (hipBLASLt); forward and backward are written out so
 every gradient slice is produced once.
 
 On the GPU (float32, multiplicities that are multiples of 8) the blocks run in
-the HIP kernel ``mnx_block_linear_f32`` instead: rows (node, m) are read in
+the HIP kernel ``mnx_block_linear_f32`` instead (fp32-accurate split-bf16 matrix-core products): rows (node, m) are read in
 place from the ir_mul input (no gather copy), the 1/sqrt(fan_in) scale is folded
 into the stacked weights and each output block is written directly; the input
 gradient is the same kernel on the output-gradient blocks with transposed
@@ -190,17 +190,18 @@ def _lin_tiles(N: int) -> int:
 
 def _frag_order(K: int, N: int):
     """(k, c, valid) of every element of the kernel's weight layout
-    [column group][64-row chunk][k/8][tile][lane][4] (csrc/linear.hip)."""
+    [column group][64-row chunk][k/16][tile][lane][8] (csrc/linear.hip): lane l of k-step q
+    holds W[16q + 8(l/32) + j][32t + l%32], the bf16 MFMA B operand."""
     nt = _lin_tiles(N)
     Y, C = -(-N // (nt * 32)), -(-K // 64)
     ar = torch.arange
     y = ar(Y).view(-1, 1, 1, 1, 1, 1)
     ch = ar(C).view(1, -1, 1, 1, 1, 1)
-    q = ar(8).view(1, 1, -1, 1, 1, 1)
+    q = ar(4).view(1, 1, -1, 1, 1, 1)
     t = ar(nt).view(1, 1, 1, -1, 1, 1)
     ln = ar(64).view(1, 1, 1, 1, -1, 1)
-    i = ar(4).view(1, 1, 1, 1, 1, -1)
-    k, c = torch.broadcast_tensors(ch * 64 + 8 * q + 4 * (ln // 32) + i, y * nt * 32 + 32 * t + ln % 32)
+    i = ar(8).view(1, 1, 1, 1, 1, -1)
+    k, c = torch.broadcast_tensors(ch * 64 + 16 * q + 8 * (ln // 32) + i, y * nt * 32 + 32 * t + ln % 32)
     k, c = k.reshape(-1), c.reshape(-1)
     return k, c, (k < K) & (c < N)
 
