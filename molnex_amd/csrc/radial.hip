@@ -154,10 +154,13 @@ __device__ __forceinline__ float silu_grad(float z) {
 // Fragments reach the MFMAs through LDS: a workgroup stages up to kRadChunk
 // floats of one layer's fragments (whole output tiles) at a time and its four
 // wavefronts share them.
-constexpr int kRadChunk = 8192;  // floats (32 KB)
+constexpr int kRadChunk = 8192;       // floats (32 KB)
+constexpr int kRadChunkWide = 24576;  // floats (96 KB): a whole 128-wide layer, for the backward
 
-struct RadShared {
-    f32x4 frag[kRadChunk / 4];
+template <int CH>
+struct RadSharedT {
+    static constexpr int kChunk = CH;
+    f32x4 frag[CH / 4];
     float bias[4 * 128];
 };
 
@@ -173,9 +176,10 @@ __device__ __forceinline__ void stage(const float* __restrict__ src, int n, f32x
 // file).  The layer's fragments f ([NQ][T][3][64 lanes][8 bf16]) are staged in
 // chunks of whole k-steps, so each k-step's activations are split once.  Every
 // wavefront of the workgroup must call it (barriers inside).
-template <int T, int NQ>
+template <int T, int NQ, class Sh>
 __device__ __forceinline__ void mfma_layer(const float* __restrict__ f, const float (&in)[NQ / 2][16],
-                                           f32x16 (&acc)[T], RadShared& sh, int lane) {
+                                           f32x16 (&acc)[T], Sh& sh, int lane) {
+    constexpr int kRadChunk = Sh::kChunk;
     constexpr int kStep = T * kX3Block;  // floats per k-step
     constexpr int kQPC = kRadChunk / kStep < NQ ? kRadChunk / kStep : NQ;  // k-steps per chunk
     static_assert(kQPC >= 1, "one k-step of fragments must fit the staging area");
@@ -216,9 +220,9 @@ __device__ __forceinline__ void mfma_layer(const float* __restrict__ f, const fl
 
 // Layer 0: B operand read straight from the (E, kin) features; k-step 4q+i of lane
 // half h = feature 8q+4h+i.  Its fragments (T x kp/8 blocks) fit one chunk.
-template <int T>
+template <int T, class Sh>
 __device__ __forceinline__ void first_layer(const float* __restrict__ f, const float* __restrict__ feats, int64_t e,
-                                            bool valid, int kin, int kp, f32x16 (&acc)[T], RadShared& sh, int lane) {
+                                            bool valid, int kin, int kp, f32x16 (&acc)[T], Sh& sh, int lane) {
     const int nq = kp / 8, half = lane >> 5;
     __syncthreads();
     stage(f, T * nq * 256, sh.frag);
@@ -251,7 +255,8 @@ __device__ __forceinline__ void zero(f32x16 (&acc)[T]) {
 __device__ __forceinline__ int dfeat(int t, int r, int half) { return 32 * t + 8 * (r / 4) + 4 * half + r % 4; }
 
 // Biases into LDS (read once per workgroup); visible after the next barrier.
-__device__ __forceinline__ void stage_bias(const float* __restrict__ b, int n, RadShared& sh) {
+template <class Sh>
+__device__ __forceinline__ void stage_bias(const float* __restrict__ b, int n, Sh& sh) {
     for (int i = threadIdx.x; i < n; i += kRadThreads) sh.bias[i] = b[i];
 }
 
@@ -262,7 +267,7 @@ __global__ void __launch_bounds__(kRadThreads) k_radial_fwd(const float* __restr
                                                             const float* __restrict__ frag, RadLayout lay,
                                                             float* __restrict__ out) {
     constexpr int T = H / 32;
-    __shared__ RadShared sh;
+    __shared__ RadSharedT<kRadChunk> sh;
     const int lane = threadIdx.x & 63, half = lane >> 5;
     const int64_t e = (int64_t(blockIdx.x) * (kRadThreads / 64) + threadIdx.x / 64) * 32 + (lane & 31);
     const bool valid = e < E;
@@ -313,7 +318,7 @@ __global__ void __launch_bounds__(kRadThreads) k_radial_bwd(const float* __restr
                                                             const float* __restrict__ grad_h,
                                                             float* __restrict__ grad_feats) {
     constexpr int T = H / 32;
-    __shared__ RadShared sh;
+    __shared__ RadSharedT<H == 128 ? kRadChunkWide : kRadChunk> sh;
     const int lane = threadIdx.x & 63, half = lane >> 5;
     const int64_t e = (int64_t(blockIdx.x) * (kRadThreads / 64) + threadIdx.x / 64) * 32 + (lane & 31);
     const bool valid = e < E;
