@@ -107,3 +107,23 @@ def test_module_matches_hipblaslt_path(hidden, out):
     (g64,) = torch.autograd.grad(w64, f64, gout.double())
     _check(w1, w64, w0)
     _check(g1, g64, g0)
+
+
+def test_edge_weights_config3_scale_sampled_rows():
+    """BASELINE config-3 shape (2.6 M edges, 64 -> 2944): sampled rows of the forward and of the
+    input gradient against float64."""
+    E, k, n = 2_618_418, 64, 2944
+    g = torch.Generator(device=DEV).manual_seed(3)
+    h = torch.randn(E, k, device=DEV, generator=g)
+    W = torch.randn(n, k, device=DEV, generator=g) / 8
+    b = torch.randn(n, device=DEV, generator=g)
+    rows = torch.randint(0, E, (256,), device=DEV, generator=g)
+    rows[-1] = E - 1
+    out = K.edge_weights(h, W, b)
+    ref = h[rows].double() @ W.double().t() + b.double()
+    _check(out[rows], ref, h[rows] @ W.t() + b)
+    del out
+    gw = torch.randn(E, n, device=DEV, generator=g)
+    gh = K.edge_weights_backward(gw, W)
+    ref = gw[rows].double() @ W.double()
+    _check(gh[rows], ref, gw[rows] @ W)
