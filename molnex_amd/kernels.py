@@ -879,14 +879,15 @@ def _(grad, weight):
 
 
 def _ew_setup(ctx, inputs, output):
-    h, weight, bias = inputs
+    h, weight = inputs[0], inputs[1]
     ctx.save_for_backward(h, weight)
-    ctx.has_bias = bias is not None
+    ctx.has_bias = len(inputs) > 2 and inputs[2] is not None
 
 
 def _ew_bwd(ctx, grad):
     h, weight = ctx.saved_tensors
-    need_h, need_w, need_b = ctx.needs_input_grad
+    need_h, need_w = ctx.needs_input_grad[:2]
+    need_b = len(ctx.needs_input_grad) > 2 and ctx.needs_input_grad[2]
     grad = grad.contiguous()
     gh = edge_weights_backward(grad, weight) if need_h else None
     gw = None
@@ -895,7 +896,7 @@ def _ew_bwd(ctx, grad):
         for i in range(0, h.shape[0], _EW_ROWS):
             gw.addmm_(grad[i:i + _EW_ROWS].t(), h[i:i + _EW_ROWS])
     gb = grad.sum(0) if (need_b and ctx.has_bias) else None
-    return gh, gw, gb
+    return (gh, gw, gb)[:len(ctx.needs_input_grad)]
 
 
 edge_weights.register_autograd(_ew_bwd, setup_context=_ew_setup)
@@ -1030,3 +1031,7 @@ def _bond_bwd(ctx, grad):
 
 
 bond_vectors.register_autograd(_bond_bwd, setup_context=_bond_setup)
+
+
+# second-order formulas (autograd of the backward ops): registered on import
+from . import second_order  # noqa: E402,F401

@@ -271,6 +271,8 @@ def _hip_plan(lin: "Linear"):
 
 
 class _HipBlockLinear(torch.autograd.Function):
+    """out = F(x, w): the blocks of ``lin`` on the HIP kernel."""
+
     @staticmethod
     def forward(ctx, x, w, lin):
         ws = w.index_select(0, lin._hip_idx_f.to(w.device)) * lin._hip_sc_f.to(w.device)
@@ -287,11 +289,35 @@ class _HipBlockLinear(torch.autograd.Function):
         gx = gw = None
         g = g.contiguous()
         if need_x:
-            wb = w.index_select(0, lin._hip_idx_b.to(w.device)) * lin._hip_sc_b.to(w.device)
-            gx = torch.ops.molix.block_linear(g, wb, lin._hip_plan["bwd"], x.shape[1])
+            gx = _HipBlockLinearT.apply(g, w, lin)
         if need_w:
             _, gw = _block_backward(x, w, g, lin.plan, False, True)
         return gx, gw, None
+
+
+class _HipBlockLinearT(torch.autograd.Function):
+    """gx = F^T(g, w), the input gradient of ``_HipBlockLinear`` (the same kernel with the
+    output-gradient blocks as segments and the transposed weights).  Its own backward (second
+    order) is F(ggx, w) for g and, since <ggx, F^T(g, w)> = <F(ggx, w), g>, the weight gradient
+    with x := ggx for w."""
+
+    @staticmethod
+    def forward(ctx, g, w, lin):
+        wb = w.index_select(0, lin._hip_idx_b.to(w.device)) * lin._hip_sc_b.to(w.device)
+        gx = torch.ops.molix.block_linear(g, wb, lin._hip_plan["bwd"], lin.irreps_in.dim)
+        ctx.save_for_backward(g, w)
+        ctx.lin = lin
+        return gx
+
+    @staticmethod
+    def backward(ctx, ggx):
+        g, w = ctx.saved_tensors
+        lin = ctx.lin
+        need_g, need_w = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
+        ggx = ggx.contiguous()
+        dg = _HipBlockLinear.apply(ggx, w, lin) if need_g else None
+        dw = _block_backward(ggx, w, g, lin.plan, False, True)[1] if need_w else None
+        return dg, dw, None
 
 
 class _BlockLinear(torch.autograd.Function):

@@ -1,0 +1,217 @@
+"""Second derivatives through the molix ops (force-matching training: the forces are taken with
+create_graph=True, as ForceDerivation does in training mode, force_derivation.py:38-43).
+
+Per op, with first-order gradients G = dL1/dθ of L1 = <g, op(θ)> and seeds s, the derivatives of
+L2 = <s, G> with respect to g and θ are compared with a float64 reference: for the multilinear ops
+(tensor product, block linear, output layer, bond vectors) the exact identities of multilinearity
+evaluated with the fp64 oracle / torch float64; for the pointwise polynomial ops (harmonics,
+contractions) torch float64 autograd of their restatements, whose forward is first checked against
+the kernel.  End to end: the gradient of an energy + force loss of MACE (as coded and literal)
+along random parameter directions against central differences of the loss.
+Tolerance 1e-5 relative (norm-wise) for the per-op checks; 1e-2 for the fp32 central differences.
+"""
+
+import copy
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import equivariant as O
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+ag = torch.autograd
+
+
+def _rel(a, b):
+    a, b = a.detach().double().cpu(), b.detach().double().cpu()
+    return float((a - b).norm() / b.norm().clamp_min(1e-300))
+
+
+@pytest.fixture(scope="module")
+def ops():
+    import molnex_amd.kernels  # noqa: F401
+
+    return torch.ops.molix
+
+
+def test_harmonics_second_order(ops):
+    from molnex_amd.second_order import sh_torch
+
+    g0 = torch.Generator().manual_seed(0)
+    v = torch.randn(300, 3, generator=g0, dtype=torch.float64)
+    v[0] = 0.0
+    g = torch.randn(300, 16, generator=g0, dtype=torch.float64)
+    s = torch.randn(300, 3, generator=g0, dtype=torch.float64)
+    assert _rel(ops.spherical_harmonics(v.float().to(DEV), 3), sh_torch(v, 3)) <= 1e-6
+    vd, gd = v.float().to(DEV).requires_grad_(True), g.float().to(DEV).requires_grad_(True)
+    (gv,) = ag.grad(ops.spherical_harmonics(vd, 3), vd, gd, create_graph=True)
+    dv, dg = ag.grad((gv * s.float().to(DEV)).sum(), (vd, gd))
+    v64, g64 = v.clone().requires_grad_(True), g.clone().requires_grad_(True)
+    (gv64,) = ag.grad(sh_torch(v64, 3), v64, g64, create_graph=True)
+    rv, rg = ag.grad((gv64 * s).sum(), (v64, g64))
+    assert _rel(dv, rv) <= 1e-5 and _rel(dg, rg) <= 1e-5
+
+
+def test_bond_vectors_second_order(ops):
+    g0 = torch.Generator().manual_seed(1)
+    pos = torch.randn(50, 3, generator=g0).to(DEV).requires_grad_(True)
+    ei = torch.randint(0, 50, (400, 2), generator=g0).to(DEV)
+    g = torch.randn(400, 3, generator=g0).to(DEV).requires_grad_(True)
+    s = torch.randn(50, 3, generator=g0).to(DEV)
+    (gp,) = ag.grad(ops.bond_vectors(pos, ei), pos, g, create_graph=True)
+    (dg,) = ag.grad((gp * s).sum(), g)
+    assert _rel(dg, s[ei[:, 1]] - s[ei[:, 0]]) <= 1e-6
+
+
+def test_edge_weights_second_order():
+    import molnex_amd.kernels as K
+
+    g0 = torch.Generator().manual_seed(2)
+    h, W = torch.randn(500, 64, generator=g0), torch.randn(96, 64, generator=g0) / 8
+    g, s = torch.randn(500, 96, generator=g0), torch.randn(500, 64, generator=g0)
+    hd, Wd, gd = (t.to(DEV).requires_grad_(True) for t in (h, W, g))
+    (gh,) = ag.grad(K.edge_weights(hd, Wd), hd, gd, create_graph=True)
+    dg, dW = ag.grad((gh * s.to(DEV)).sum(), (gd, Wd))
+    assert _rel(dg, s.double() @ W.double().t()) <= 1e-5
+    assert _rel(dW, g.double().t() @ s.double()) <= 1e-5
+
+
+@pytest.mark.parametrize("sender", [False, True])
+def test_tensor_product_second_order(ops, sender):
+    import molnex_amd.kernels as K
+
+    C, N, E = 8, 40, 300
+    ls = [0, 1, 2, 3]
+    irr = "0e + 1o + 2e + 3o"
+    tp = O.ChannelwiseTP(" + ".join(f"{C}x{t}" for t in irr.split(" + ")), irr, irr, C)
+    rng = np.random.default_rng(3)
+    x, Y, w = (rng.normal(size=s).astype(np.float32) for s in ((N, tp.nx * C), (E, tp.ny), (E, len(tp.paths) * C)))
+    g = rng.normal(size=(N, tp.no * C)).astype(np.float32)
+    sx, sY, sw = (rng.normal(size=a.shape).astype(np.float32) for a in (x, Y, w))
+    ei = rng.integers(0, N, (E, 2))
+    config = K.tp_config_id(ls, ls, ls)
+    eit = torch.tensor(ei, device=DEV)
+    csr = ops.edge_csr(eit, N)
+    extra = ops.edge_csr(eit.flip(1), N) if sender else ()
+    xt, Yt, wt, gt = (torch.tensor(a, device=DEV, requires_grad=True) for a in (x, Y, w, g))
+    out = ops.tp_scatter(xt, Yt, wt, *csr, config, C, *extra)
+    gx, gY, gw = ag.grad(out, (xt, Yt, wt), gt, create_graph=True)
+    L2 = sum((a * torch.tensor(b, device=DEV)).sum() for a, b in ((gx, sx), (gY, sY), (gw, sw)))
+    dg, dx, dY, dw = ag.grad(L2, (gt, xt, Yt, wt))
+    f = lambda a, b, c: tp.forward(a, b, c, ei, N)  # noqa: E731
+    b = lambda a, bb, c: tp.backward(a, bb, c, ei, g)  # noqa: E731
+    ref_g = f(sx, Y, w) + f(x, sY, w) + f(x, Y, sw)
+    ref_x = b(x, sY, w)[0] + b(x, Y, sw)[0]
+    ref_Y = b(sx, Y, w)[1] + b(x, Y, sw)[1]
+    ref_w = b(sx, Y, w)[2] + b(x, sY, w)[2]
+    for name, got, ref in (("g", dg, ref_g), ("x", dx, ref_x), ("Y", dY, ref_Y), ("w", dw, ref_w)):
+        assert _rel(got, torch.tensor(ref)) <= 1e-5, name
+
+
+def test_block_linear_second_order():
+    from molnex_amd.molrep.interaction.linear import Linear
+
+    torch.manual_seed(4)
+    lin = Linear("16x0e+8x0e+16x1o+8x2e", "32x0e+16x1o+8x2e").to(DEV)
+    x = torch.randn(70, lin.irreps_in.dim, device=DEV, requires_grad=True)
+    g = torch.randn(70, lin.irreps_out.dim, device=DEV, requires_grad=True)
+    s = torch.randn(70, lin.irreps_in.dim, device=DEV)
+    (gx,) = ag.grad(lin(x), x, g, create_graph=True)
+    dg, dw = ag.grad((gx * s).sum(), (g, lin.weight))
+    ref = copy.deepcopy(lin).double().cpu()
+    x64, g64 = x.detach().double().cpu().requires_grad_(True), g.detach().double().cpu().requires_grad_(True)
+    (gx64,) = ag.grad(ref(x64), x64, g64, create_graph=True)
+    rg, rw = ag.grad((gx64 * s.double().cpu()).sum(), (g64, ref.weight))
+    assert _rel(dg, rg) <= 1e-5 and _rel(dw, rw) <= 1e-5
+
+
+def test_scalar_contraction_second_order(ops):
+    from molnex_amd.second_order import sc_scalar_torch
+
+    g0 = torch.Generator().manual_seed(5)
+    x = torch.randn(60, 32, generator=g0)
+    z = torch.randint(0, 3, (60,), generator=g0)
+    w = torch.randn(3, 3, 32, generator=g0) * 0.3
+    g, sx, sw = torch.randn(60, 32, generator=g0), torch.randn(60, 32, generator=g0), torch.randn(3, 3, 32, generator=g0)
+    assert _rel(ops.symmetric_contraction_scalar(x.to(DEV), z.to(DEV), w.to(DEV)), sc_scalar_torch(x.double(), z, w.double())) <= 1e-6
+    xd, wd, gd = (t.to(DEV).requires_grad_(True) for t in (x, w, g))
+    gx, gw = ag.grad(ops.symmetric_contraction_scalar(xd, z.to(DEV), wd), (xd, wd), gd, create_graph=True)
+    d = ag.grad((gx * sx.to(DEV)).sum() + (gw * sw.to(DEV)).sum(), (gd, xd, wd))
+    x64, w64, g64 = (t.double().requires_grad_(True) for t in (x, w, g))
+    rx, rw = ag.grad(sc_scalar_torch(x64, z, w64), (x64, w64), g64, create_graph=True)
+    r = ag.grad((rx * sx.double()).sum() + (rw * sw.double()).sum(), (g64, x64, w64))
+    for a, b in zip(d, r):
+        assert _rel(a, b) <= 1e-5
+
+
+@pytest.mark.parametrize("l_in,l_out,nu", [(1, 1, 3), (3, 1, 3), (2, 0, 2)])
+def test_equivariant_contraction_second_order(ops, l_in, l_out, nu):
+    import molnex_amd.kernels as K
+    from molnex_amd.second_order import sc_torch
+
+    C, N, S = 8, 40, 3
+    paths = K.sc_config_info(K.sc_config_id(l_in, l_out, nu))[2]
+    g0 = torch.Generator().manual_seed(6 + l_in)
+    x = torch.randn(N, (l_in + 1) ** 2 * C, generator=g0) * 0.7
+    z = torch.randint(0, S, (N,), generator=g0)
+    w = torch.randn(S, paths, C, generator=g0) * 0.3
+    g = torch.randn(N, (l_out + 1) ** 2 * C, generator=g0)
+    sx, sw = torch.randn_like(x), torch.randn_like(w)
+    fwd = ops.symmetric_contraction(x.to(DEV), z.to(DEV), w.to(DEV), l_in, l_out, nu)
+    assert _rel(fwd, sc_torch(x.double(), z, w.double(), l_in, l_out, nu)) <= 1e-5
+    xd, wd, gd = (t.to(DEV).requires_grad_(True) for t in (x, w, g))
+    gx, gw = ag.grad(ops.symmetric_contraction(xd, z.to(DEV), wd, l_in, l_out, nu), (xd, wd), gd, create_graph=True)
+    d = ag.grad((gx * sx.to(DEV)).sum() + (gw * sw.to(DEV)).sum(), (gd, xd, wd))
+    x64, w64, g64 = (t.double().requires_grad_(True) for t in (x, w, g))
+    rx, rw = ag.grad(sc_torch(x64, z, w64, l_in, l_out, nu), (x64, w64), g64, create_graph=True)
+    r = ag.grad((rx * sx.double()).sum() + (rw * sw.double()).sum(), (g64, x64, w64))
+    for name, a, b in zip(("g", "x", "w"), d, r):
+        assert _rel(a, b) <= 1e-5, name
+
+
+@pytest.mark.parametrize("literal", [False, True])
+def test_mace_force_loss_gradient_vs_central_differences(literal):
+    """Training step of a force-matching loss: d(sum E^2 + sum F^2)/dθ along random directions of
+    all parameters against central differences of the loss (fp32)."""
+    from oracle import nlist as NL
+    from tests.test_gpu_mace import CFG1, CFG1_LITERAL, build, molecules
+
+    pos, Z, batch = molecules(seed=7, n_mol=2)
+    ii, jj, _, _ = NL.directed_pairs(pos.astype(np.float32), 5.0, None)
+    ei = torch.tensor(np.stack([jj, ii], 1).astype(np.int64), device=DEV)
+    model = build(CFG1_LITERAL if literal else CFG1, seed=7)
+    model.train()
+    Zt, bt = torch.tensor(Z, device=DEV), torch.tensor(batch, device=DEV)
+    p0 = torch.tensor(pos, dtype=torch.float32, device=DEV)
+    params = [q for q in model.parameters() if q.requires_grad]
+
+    def loss():
+        e, f = model(Zt, p0.clone(), ei, bt, 2)
+        return (e ** 2).sum() + (f ** 2).sum()
+
+    model.zero_grad()
+    loss().backward()
+    grads = [torch.zeros_like(q) if q.grad is None else q.grad.detach().clone() for q in params]
+    assert all(torch.isfinite(gq).all() for gq in grads)
+    gen = torch.Generator(device=DEV).manual_seed(8)
+    for _ in range(2):
+        dirs = [torch.randn(q.shape, device=DEV, generator=gen) for q in params]
+        scale = sum(float((d * d).sum()) for d in dirs) ** 0.5
+        dirs = [d / scale for d in dirs]
+        analytic = sum(float((gq * d).sum()) for gq, d in zip(grads, dirs))
+        eps = 2e-3
+        with torch.no_grad():
+            for q, d in zip(params, dirs):
+                q.add_(eps * d)
+        lp = float(loss())
+        with torch.no_grad():
+            for q, d in zip(params, dirs):
+                q.sub_(2 * eps * d)
+        lm = float(loss())
+        with torch.no_grad():
+            for q, d in zip(params, dirs):
+                q.add_(eps * d)
+        numeric = (lp - lm) / (2 * eps)
+        assert abs(analytic - numeric) <= 1e-2 * max(abs(numeric), 1e-3 * abs(float(loss()))), (analytic, numeric)
