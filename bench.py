@@ -384,6 +384,57 @@ def full_step_bench(args, dev):
                        "atoms": n, "edges": int(edge_index.shape[0]), "channels": C}}
 
 
+def train_step_bench(args, dev, steps=2, warmup=1):
+    """Force-matching training step on the config-5 literal MACE (50k atoms, 2.6 M edges): energy,
+    forces with create_graph (ForceDerivation in training mode), loss = E^2 + mean |F|^2, backward
+    to every parameter through the second-order formulas of the molix ops."""
+    from molnex_amd.molpot.pipeline import EnergyForceModel
+    from molnex_amd.molrep.embedding import DiscreteEmbeddingSpec
+    from molnex_amd.molzoo import MACE
+
+    n = args.atoms
+    L = (n / 0.1) ** (1.0 / 3.0)
+    g = torch.Generator().manual_seed(args.seed)
+    pos = lattice_positions(n, L, g).to(dev)
+    Z = torch.randint(0, 10, (n,), generator=g).to(dev)
+    box = torch.eye(3, device=dev) * L
+    i, j, shifts, _, _ = torch.ops.molix.neighbor_list(pos, 5.0, box, True)
+    edge_index = torch.stack([j.long(), i.long()], 1)
+    torch.manual_seed(args.seed)
+    C = args.channels
+    enc = MACE(node_attr_specs=[DiscreteEmbeddingSpec(input_key="Z", num_classes=10, emb_dim=C)], num_elements=10,
+               num_features=C, r_max=5.0, num_bessel=8, l_max=3, num_interactions=2, correlation=3,
+               avg_num_neighbors=float(edge_index.shape[0]) / n, cutoff="polynomial",
+               hidden_irreps=f"{C}x0e+{C}x1o")
+    model = EnergyForceModel(enc, C).to(dev)
+    model.train()
+    params = [q for q in model.parameters() if q.requires_grad]
+
+    def step():
+        p = pos.detach().clone().requires_grad_(True)
+        bond_diff = torch.ops.molix.bond_vectors(p, edge_index, shifts)
+        feats = enc(Z=Z, bond_dist=bond_diff.norm(dim=-1).clamp(min=1e-6), bond_diff=bond_diff,
+                    edge_index=edge_index)
+        e = model.aggregate(model.energy(model.pool(feats)), torch.zeros(n, dtype=torch.long, device=dev), 1)
+        f = model.forces(e, p)
+        loss = (e ** 2).sum() + (f ** 2).sum(-1).mean()
+        for q in params:
+            q.grad = None
+        loss.backward()
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    dt = (time.perf_counter() - t0) / steps
+    return {"workload": "config 5 literal MACE, force-matching training step (energy + forces with create_graph, "
+                        "loss backward to all parameters), 50k atoms", "ms_per_step": round(dt * 1e3, 3),
+            "atoms_per_s": round(n / dt, 1), "edges": int(edge_index.shape[0])}
+
+
 def nlist_bench(dev, reps=10, warmup=3):
     """directed cell list of 100k atoms in a periodic 100 A cube, rc 5 A.
     Times the whole op (bin, count, scan, host read of the count, emit) after warm-up calls
@@ -499,6 +550,8 @@ def secondary_figures(args, dev):
                     "workload": full["config"]["workload"], "edges": full["config"]["edges"],
                     "hbm_frac": full["roofline"]["frac"], "algorithmic_GB": round(full["roofline"]["algorithmic_bytes"] / 1e9, 2)}
         torch.cuda.empty_cache()
+    out["config5_literal_training_step"] = train_step_bench(args, dev)
+    torch.cuda.empty_cache()
     return out
 
 

@@ -192,7 +192,7 @@ K.tp_scatter_backward.register_autograd(_tp2_bwd, setup_context=_tp2_setup)
 
 def sc_scalar_torch(x: Tensor, z: Tensor, w: Tensor) -> Tensor:
     """``out[n, c] = sum_k w[z_n, k, c] x[n, c]^(k+1)`` (molix::symmetric_contraction_scalar)."""
-    wz = w[z.reshape(-1)]
+    wz = w.index_select(0, z.reshape(-1))
     xs = x.reshape(-1, w.shape[-1])
     out, p = torch.zeros_like(xs), xs
     for k in range(w.shape[1]):
@@ -233,7 +233,7 @@ def _sc_tables(l_in: int, l_out: int, nu: int, device: str, dtype: torch.dtype):
     return parts
 
 
-def sc_torch(x: Tensor, z: Tensor, w: Tensor, l_in: int, l_out: int, nu: int, rows: int = 4096) -> Tensor:
+def sc_torch(x: Tensor, z: Tensor, w: Tensor, l_in: int, l_out: int, nu: int, rows: int = 8192) -> Tensor:
     """``B[n, L, M, c] = sum_{nu, k} w[z_n, p, c] sum_q coef_k[M, q] prod_j A[n, q_j, c]``
     (molix::symmetric_contraction), in row chunks."""
     C = w.shape[-1]
@@ -243,12 +243,13 @@ def sc_torch(x: Tensor, z: Tensor, w: Tensor, l_in: int, l_out: int, nu: int, ro
     parts = _sc_tables(l_in, l_out, nu, str(x.device), x.dtype)
     chunks = []
     for i in range(0, A.shape[0], rows):
-        a, wz = A[i:i + rows], w[zz[i:i + rows]]
+        a, wz = A[i:i + rows], w.index_select(0, zz[i:i + rows])
         blocks = [a.new_zeros(a.shape[0], 2 * L + 1, C) for L in range(l_out + 1)]
         for p0, L, idx, coef in parts:
-            m = a[:, idx[:, 0]]
+            # index_select: its backward is an index_add, not a sort-based index_put
+            m = a.index_select(1, idx[:, 0])
             for j in range(1, idx.shape[1]):
-                m = m * a[:, idx[:, j]]
+                m = m * a.index_select(1, idx[:, j])
             P = torch.einsum("kmq,nqc->nkmc", coef, m)
             blocks[L] = blocks[L] + (wz[:, p0:p0 + coef.shape[0], None, :] * P).sum(1)
         chunks.append(torch.cat(blocks, dim=1))
