@@ -259,6 +259,17 @@ int mnx_sc_bwd_f32(int32_t config, const float* A, const int64_t* types, const f
                    const float* grad_out, const int32_t* order, int64_t num_nodes,
                    int32_t channels, int32_t num_elements, float* grad_A, float* grad_W,
                    mnx_stream_t stream);
+/* Second order of the contraction (force-matching training): with seeds   */
+/* seed_A [N][ni*C] and seed_W [S][paths][C] (either may be NULL: zero) on   */
+/* the first-order gradients of <grad_out, B>, the gradients of              */
+/* L2 = <seed_A, grad_A> + <seed_W, grad_W> with respect to grad_out         */
+/* (d_grad_out [N][no*C], overwritten), A (d_A, overwritten) and W (d_W,     */
+/* accumulated: zero it first); NULL outputs are skipped.  order as for     */
+/* mnx_sc_bwd_f32.  No counterpart in the reference's ops (cuequivariance    */
+/* provides it for symmetric_contraction.py:94-109).                        */
+int mnx_sc_bwd2_f32(int32_t config, const float* A, const int64_t* types, const float* W, const float* grad_out,
+                    const float* seed_A, const float* seed_W, const int32_t* order, int64_t N, int32_t C,
+                    int32_t S, float* d_grad_out, float* d_A, float* d_W, mnx_stream_t stream);
 
 /* ------------------------------------------------------------------------ */
 /* Equivariant (ir_mul) block linear, one output irrep block per call        */

@@ -60,6 +60,7 @@ SIGNATURES = {
     "mnx_sc_config_info": (C.c_int, [c_i32, vp]),
     "mnx_sc_fwd_f32": (C.c_int, [c_i32, vp, vp, vp, c_i64, c_i32, c_i32, vp, vp]),
     "mnx_sc_bwd_f32": (C.c_int, [c_i32, vp, vp, vp, vp, vp, c_i64, c_i32, c_i32, vp, vp, vp]),
+    "mnx_sc_bwd2_f32": (C.c_int, [c_i32, vp, vp, vp, vp, vp, vp, vp, c_i64, c_i32, c_i32, vp, vp, vp, vp]),
     "mnx_block_linear_frag_floats": (c_i64, [c_i32, c_i32]),
     "mnx_block_linear_f32": (C.c_int, [vp, c_i64, c_i32, vp, vp, vp, vp, c_i32, c_i64, c_i32, vp, c_i64, c_i64,
                                         c_i32, vp]),

@@ -226,6 +226,135 @@ def emit_bwd(c: Cfg) -> str:
     return "\n".join(L)
 
 
+def _dir_terms(mono):
+    """D = d mono along the seed s: [(count, x, rest)] with s_x * prod(a_rest), duplicates merged."""
+    acc = defaultdict(int)
+    for p in range(len(mono)):
+        rest = tuple(sorted(mono[r] for r in range(len(mono)) if r != p))
+        acc[(mono[p], rest)] += 1
+    return [(cnt, x, rest) for (x, rest), cnt in sorted(acc.items())]
+
+
+def _dir_deriv_terms(mono):
+    """d D / d a_y for D = sum_p s_{t_p} prod_{r != p} a_{t_r}: [(y, count, x, rest)] with
+    s_x * prod(a_rest) over ordered position pairs (p, q), p != q, y = t_q, duplicates merged."""
+    acc = defaultdict(int)
+    n = len(mono)
+    for p in range(n):
+        for q in range(n):
+            if p != q:
+                rest = tuple(sorted(mono[r] for r in range(n) if r not in (p, q)))
+                acc[(mono[q], mono[p], rest)] += 1
+    return [(y, cnt, x, rest) for (y, x, rest), cnt in sorted(acc.items())]
+
+
+def _prod(names):
+    return " * ".join(names) if names else "1.f"
+
+
+def emit_bwd2(c: Cfg) -> str:
+    """Second order: with first-order gradients gA, gW of <G, B> and seeds sA, sW,
+    L2 = <sA, gA> + <sW, gW> = sum_q H_q D_q + Hw_q m_q where D_q = d m_q along sA,
+    h_{k,q} = sum_M coef_k[M, q] G[M], H_q = sum_k W_k h_{k,q}, Hw_q = sum_k sW_k h_{k,q}:
+        dG[M] = sum_{q,k} coef_k[M, q] (W_k D_q + sW_k m_q)
+        dW_k  = sum_q h_{k,q} D_q
+        dA_y  = sum_q H_q dD_q/dA_y + Hw_q dm_q/dA_y."""
+    L = []
+    w = L.append
+    w(f"__global__ void __launch_bounds__(256) k_scg_bwd2_{c.idx}(const float* __restrict__ A, "
+      f"const int64_t* __restrict__ z, const float* __restrict__ W, const float* __restrict__ G, "
+      f"const float* __restrict__ sA, const float* __restrict__ sW, const int32_t* __restrict__ order, int64_t N, "
+      f"int C, int S, int chunk, float* __restrict__ dG, float* __restrict__ dA, float* __restrict__ dW) {{")
+    w("    const int64_t t = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;")
+    w("    const int64_t q = t / C;")
+    w("    const int c = int(t - q * C);")
+    w("    const int64_t s0 = q * chunk;")
+    w("    if (s0 >= N) return;")
+    w("    const int64_t s1 = s0 + chunk < N ? s0 + chunk : N;")
+    w("    const bool hasA = sA != nullptr, hasW = sW != nullptr;")
+    for p in range(c.paths):
+        w(f"    float dw{p} = 0.f;")
+    w("    int64_t ecur = -1;")
+    w("    for (int64_t s = s0; s < s1; ++s) {")
+    w("        const int64_t n = order ? int64_t(order[s]) : s;")
+    w("        const int64_t e = z[n];")
+    w("        if (dW && e != ecur) {")
+    w("            if (ecur >= 0 && ecur < S && hasA) {")
+    w(f"                float* wq = dW + ecur * ({c.paths} * int64_t(C)) + c;")
+    for p in range(c.paths):
+        w(f"                atomicAdd(wq + {p} * C, dw{p});")
+    w("            }")
+    for p in range(c.paths):
+        w(f"            dw{p} = 0.f;")
+    w("            ecur = e;")
+    w("        }")
+    w(f"        float* gq = dG ? dG + n * ({c.no} * int64_t(C)) + c : nullptr;")
+    w(f"        float* aq = dA ? dA + n * ({c.ni} * int64_t(C)) + c : nullptr;")
+    w("        if (e < 0 || e >= S) {")
+    w(f"            if (gq) for (int i = 0; i < {c.no}; ++i) gq[i * C] = 0.f;")
+    w(f"            if (aq) for (int i = 0; i < {c.ni}; ++i) aq[i * C] = 0.f;")
+    w("            continue;")
+    w("        }")
+    w(f"        const float* ap = A + n * ({c.ni} * int64_t(C)) + c;")
+    for i in c.used:
+        w(f"        const float a{i} = ap[{i} * C];")
+    w(f"        const float* sp = hasA ? sA + n * ({c.ni} * int64_t(C)) + c : nullptr;")
+    for i in c.used:
+        w(f"        const float s{i} = hasA ? sp[{i} * C] : 0.f;")
+    w(f"        const float* gp = G + n * ({c.no} * int64_t(C)) + c;")
+    for M in range(c.no):
+        w(f"        const float g{M} = gp[{M} * C];")
+    w(f"        const float* wp = W + e * ({c.paths} * int64_t(C)) + c;")
+    w(f"        const float* vp = hasW ? sW + e * ({c.paths} * int64_t(C)) + c : nullptr;")
+    for p in range(c.paths):
+        w(f"        const float w{p} = wp[{p} * C];")
+        w(f"        const float v{p} = hasW ? vp[{p} * C] : 0.f;")
+    for M in range(c.no):
+        w(f"        float dg{M} = 0.f;")
+    for i in range(c.ni):
+        w(f"        float d{i} = 0.f;")
+    for mono, ts in c.terms:
+        w("        {")
+        byp = defaultdict(list)
+        for p, M, v in ts:
+            byp[p].append((M, v))
+        w(f"            const float m = {_mono_expr(mono)};")
+        dterms = " + ".join((f"{float(cnt):.1f}f * " if cnt > 1 else "") + _prod([f"s{x}"] + [f"a{r}" for r in rest])
+                            for cnt, x, rest in _dir_terms(mono))
+        w(f"            const float D = {dterms};")
+        w("            float H = 0.f, Hw = 0.f;")
+        for p, lst in byp.items():
+            expr = f"{f32(lst[0][1])} * g{lst[0][0]}"
+            for M, v in lst[1:]:
+                expr = f"fmaf({f32(v)}, g{M}, {expr})"
+            w(f"            {{ const float h = {expr};")
+            w(f"              H = fmaf(w{p}, h, H); Hw = fmaf(v{p}, h, Hw); dw{p} = fmaf(h, D, dw{p}); }}")
+        for p, M, v in ts:
+            w(f"            dg{M} = fmaf({f32(v)}, fmaf(w{p}, D, v{p} * m), dg{M});")
+        for x, cnt, expr in _deriv_terms(mono):
+            val = "Hw" if expr is None else f"Hw * {expr}"
+            w(f"            d{x} = fmaf({float(cnt):.1f}f, {val}, d{x});")
+        for y, cnt, x, rest in _dir_deriv_terms(mono):
+            w(f"            d{y} = fmaf({float(cnt):.1f}f * H, {_prod([f's{x}'] + [f'a{r}' for r in rest])}, d{y});")
+        w("        }")
+    w("        if (gq) {")
+    for M in range(c.no):
+        w(f"            gq[{M} * C] = dg{M};")
+    w("        }")
+    w("        if (aq) {")
+    for i in range(c.ni):
+        w(f"            aq[{i} * C] = d{i};")
+    w("        }")
+    w("    }")
+    w("    if (dW && hasA && ecur >= 0 && ecur < S) {")
+    w(f"        float* wq = dW + ecur * ({c.paths} * int64_t(C)) + c;")
+    for p in range(c.paths):
+        w(f"        atomicAdd(wq + {p} * C, dw{p});")
+    w("    }")
+    w("}")
+    return "\n".join(L)
+
+
 def generate() -> str:
     cfgs = [Cfg(i, *t) for i, t in enumerate(config_list())]
     out = ["// Generated by molnex_amd/csrc/gen_sc.py -- do not edit.", ""]
@@ -233,6 +362,8 @@ def generate() -> str:
         out.append(emit_fwd(c))
         out.append("")
         out.append(emit_bwd(c))
+        out.append("")
+        out.append(emit_bwd2(c))
         out.append("")
     out.append("struct SCConfig { int l_in, l_out, nu, ni, no, paths, nnz; };")
     out.append("constexpr SCConfig kSCConfigs[] = {")
@@ -250,6 +381,9 @@ def generate() -> str:
         tw = "true" if gw else "false"
         out.append(f"constexpr SCBwdFn {name}[] = {{" +
                    ", ".join(f"k_scg_bwd_{c.idx}<{tb}, {tw}>" for c in cfgs) + "};")
+    out.append("using SCBwd2Fn = void (*)(const float*, const int64_t*, const float*, const float*, const float*, "
+               "const float*, const int32_t*, int64_t, int, int, int, float*, float*, float*);")
+    out.append("constexpr SCBwd2Fn kSCBwd2[] = {" + ", ".join(f"k_scg_bwd2_{c.idx}" for c in cfgs) + "};")
     return "\n".join(out) + "\n"
 
 

@@ -182,4 +182,21 @@ int mnx_sc_bwd_f32(int32_t config, const float* A, const int64_t* types, const f
     return MNX_OK;
 }
 
+int mnx_sc_bwd2_f32(int32_t config, const float* A, const int64_t* types, const float* W, const float* grad_out,
+                    const float* seed_A, const float* seed_W, const int32_t* order, int64_t N, int32_t C,
+                    int32_t S, float* d_grad_out, float* d_A, float* d_W, mnx_stream_t stream) {
+    clear_error();
+    MNX_REQUIRE(config >= 0 && config < kNumSCConfigs, "bad symmetric-contraction config %d", config);
+    MNX_REQUIRE(N >= 0 && N < (int64_t(1) << 31) && C > 0 && S > 0 && N * int64_t(C) < (int64_t(1) << 40),
+                "bad sizes");
+    if (N == 0 || (!d_grad_out && !d_A && !d_W)) return MNX_OK;
+    MNX_REQUIRE(A && types && W && grad_out, "null pointer argument");
+    const int64_t threads = ceil_div(N, int64_t(kSCChunk)) * C;
+    hipLaunchKernelGGL(kSCBwd2[config], dim3(unsigned(ceil_div(threads, int64_t(256)))), dim3(256), 0,
+                       (hipStream_t)stream, A, types, W, grad_out, seed_A, seed_W, order, N, int(C), int(S), kSCChunk,
+                       d_grad_out, d_A, d_W);
+    MNX_CHECK_LAUNCH();
+    return MNX_OK;
+}
+
 }  // extern "C"

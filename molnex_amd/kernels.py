@@ -708,6 +708,38 @@ def _(grad, x, atom_types, weight, l_in, l_out, correlation, need_x, need_w):
             torch.empty_like(weight) if need_w else weight.new_empty(0))
 
 
+@torch.library.custom_op("molix::symmetric_contraction_backward2", mutates_args=(), device_types="cuda")
+def symmetric_contraction_backward2(grad: Tensor, x: Tensor, atom_types: Tensor, weight: Tensor,
+                                    seed_x: Tensor | None, seed_w: Tensor | None, l_in: int, l_out: int,
+                                    correlation: int, need_grad: bool, need_x: bool,
+                                    need_w: bool) -> tuple[Tensor, Tensor, Tensor]:
+    """Second order of ``symmetric_contraction``: gradients of <seed_x, grad_x> + <seed_w, grad_w>
+    (the first-order gradients of <grad, B>) with respect to grad, x and weight (empty when not
+    needed)."""
+    cfg, ni, no, S, Cc = _sc_shapes(x, weight, l_in, l_out, correlation)
+    xs = _f32_rows(x, ni * Cc, "x")
+    g = _f32_rows(grad, no * Cc, "grad")
+    sx = None if seed_x is None else _f32_rows(seed_x, ni * Cc, "seed_x")
+    sw = None if seed_w is None else seed_w.to(torch.float32).contiguous()
+    z = atom_types.to(torch.int64).reshape(-1).contiguous()
+    w = weight.contiguous()
+    order = torch.argsort(z, stable=True).to(torch.int32) if need_w else None
+    dg = torch.empty_like(g) if need_grad else g.new_empty(0)
+    dx = torch.empty_like(xs) if need_x else xs.new_empty(0)
+    dw = torch.zeros_like(w) if need_w else w.new_empty(0)
+    check(_lib.load().mnx_sc_bwd2_f32(cfg, ptr(xs), ptr(z), ptr(w), ptr(g), ptr(sx), ptr(sw), ptr(order), xs.shape[0],
+                                      Cc, S, ptr(dg), ptr(dx), ptr(dw), _stream(xs)),
+          "symmetric_contraction second order")
+    return dg, dx, dw
+
+
+@symmetric_contraction_backward2.register_fake
+def _(grad, x, atom_types, weight, seed_x, seed_w, l_in, l_out, correlation, need_grad, need_x, need_w):
+    return (torch.empty_like(grad) if need_grad else grad.new_empty(0),
+            torch.empty_like(x) if need_x else x.new_empty(0),
+            torch.empty_like(weight) if need_w else weight.new_empty(0))
+
+
 def _scg_setup(ctx, inputs, output):
     x, z, w, l_in, l_out, nu = inputs
     ctx.save_for_backward(x, z, w)

@@ -15,9 +15,11 @@ each backward op; this module registers those formulas.
   ``bond_vectors`` (its gradient is a signed scatter whose adjoint is the gather itself) and the
   radial MLP's output layer (``edge_weights``: gh = g W, whose adjoints are h W^T and g^T h) work
   the same way.
-* The nonlinear pointwise ops (harmonics, the symmetric contractions) differentiate a torch
-  restatement of the same formula on the GPU (the harmonic polynomials; the product-basis
-  monomial tables of ``molnex_amd.symmetric``), used only on this second-order path.
+* The equivariant symmetric contraction has a generated second-order kernel
+  (``mnx_sc_bwd2_f32``: monomial values, directional derivatives along the seed and their
+  gradients, straight-line per configuration).  The harmonics and the scalar contraction, cheap
+  pointwise polynomials, differentiate torch restatements of the same formulas on the GPU;
+  ``sc_torch`` restates the equivariant contraction for the tests.
 
 The PME ops keep the reference's first-order-only autograd (pme_cpu.cpp:208-215).
 """
@@ -265,10 +267,13 @@ def _sc2_setup(ctx, inputs, output):
 
 def _sc2_bwd(ctx, ggx, ggw):
     g, x, z, w = ctx.saved_tensors
-    seeds = [_seed(ggx, ctx.need[0]), _seed(ggw, ctx.need[1])]
+    sx, sw = _seed(ggx, ctx.need[0]), _seed(ggw, ctx.need[1])
     ng, nx, _, nw = ctx.needs_input_grad[:4]
-    dg, dx, dw = _vjp_second(lambda xx, ww: sc_torch(xx, z, ww, *ctx.cfg), [x, w], g, seeds, [ng, nx, nw])
-    return dg, dx, None, dw, None, None, None, None, None
+    if (sx is None and sw is None) or not (ng or nx or nw):
+        return (None,) * 9
+    dg, dx, dw = K.symmetric_contraction_backward2(g.contiguous(), x, z, w, sx, sw, *ctx.cfg, ng, nx, nw)
+    return (dg.reshape(g.shape) if ng else None, dx.reshape(x.shape) if nx else None, None,
+            dw if nw else None, None, None, None, None, None)
 
 
 K.symmetric_contraction_backward.register_autograd(_sc2_bwd, setup_context=_sc2_setup)
