@@ -45,7 +45,7 @@ def parse():
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--unsorted", action="store_true", help="keep atoms in random order (no spatial sort)")
     p.add_argument("--seed", type=int, default=0)
-    p.add_argument("--workload", choices=["tp", "full", "sc", "nl", "pme"], default="tp",
+    p.add_argument("--workload", choices=["tp", "full", "sc", "nl", "pme", "train"], default="tp",
                    help="tp: config 3 edge step (default, the headline line); full: config 5 energy + forces; "
                         "sc / nl / pme: config 4, config 2, config 5's PME term alone")
     p.add_argument("--no-secondary", action="store_true",
@@ -564,6 +564,12 @@ def main():
     if args.workload == "full":
         dev = torch.device("cuda:0")
         print(json.dumps(full_step_bench(args, dev)), flush=True)
+        return
+    if args.workload == "train":
+        dev = torch.device("cuda:0")
+        out = train_step_bench(args, dev, steps=args.steps, warmup=args.warmup)
+        out["peak_GB"] = round(torch.cuda.max_memory_allocated() / 1e9, 1)
+        print(json.dumps(out), flush=True)
         return
     if args.workload in ("sc", "nl", "pme"):
         import molnex_amd.kernels  # noqa: F401
