@@ -183,7 +183,7 @@ def gen_fwd(cfg: Cfg, g: int) -> str:
     L = []
     a = L.append
     name = f"tp_fwd_c{cfg.idx}_g{g}"
-    a(f"template <int CPL>\n__global__ void __launch_bounds__(64) {name}(const float* __restrict__ x, "
+    a(f"template <int CPL, bool FULL>\n__global__ void __launch_bounds__(64) {name}(const float* __restrict__ x, "
       "const float* __restrict__ Y, const float* __restrict__ w, const int32_t* __restrict__ row_ptr, "
       "const int32_t* __restrict__ perm, const int32_t* __restrict__ snd, int64_t N, int C, "
       "float* __restrict__ out) {")
@@ -192,7 +192,7 @@ def gen_fwd(cfg: Cfg, g: int) -> str:
     a("  const int lane = threadIdx.x;")
     a("  int cc[CPL]; bool ok[CPL];")
     a("#pragma unroll")
-    a("  for (int k = 0; k < CPL; ++k) { cc[k] = blockIdx.y * (64 * CPL) + 64 * k + lane; ok[k] = cc[k] < C; }")
+    a("  for (int k = 0; k < CPL; ++k) { cc[k] = blockIdx.y * (64 * CPL) + 64 * k + lane; ok[k] = FULL || cc[k] < C; }")
     a(f"  float acc[CPL][{len(outs)}];")
     a("#pragma unroll")
     a(f"  for (int k = 0; k < CPL; ++k)\n#pragma unroll\n    for (int i = 0; i < {len(outs)}; ++i) acc[k][i] = 0.f;")
@@ -250,7 +250,7 @@ def gen_bwd(cfg: Cfg, g: int) -> str:
     L = []
     a = L.append
     name = f"tp_bwd_c{cfg.idx}_g{g}"
-    a(f"template <int CPL>\n__global__ void __launch_bounds__(64) {name}(const float* __restrict__ x, "
+    a(f"template <int CPL, bool FULL>\n__global__ void __launch_bounds__(64) {name}(const float* __restrict__ x, "
       "const float* __restrict__ Y, const float* __restrict__ w, const float* __restrict__ gout, "
       "const int32_t* __restrict__ row_ptr, const int32_t* __restrict__ perm, const int32_t* __restrict__ snd, "
       "int64_t N, int C, float* __restrict__ gx, float* __restrict__ gw, float* __restrict__ gyp, int npart, "
@@ -260,7 +260,7 @@ def gen_bwd(cfg: Cfg, g: int) -> str:
     a("  const int lane = threadIdx.x;")
     a("  int cc[CPL]; bool ok[CPL];")
     a("#pragma unroll")
-    a("  for (int k = 0; k < CPL; ++k) { cc[k] = blockIdx.y * (64 * CPL) + 64 * k + lane; ok[k] = cc[k] < C; }")
+    a("  for (int k = 0; k < CPL; ++k) { cc[k] = blockIdx.y * (64 * CPL) + 64 * k + lane; ok[k] = FULL || cc[k] < C; }")
     a("  const int pidx = pbase + blockIdx.y;")
     a(f"  const int64_t XS = int64_t({cfg.NX}) * C, WS = int64_t({cfg.NP}) * C;")
     a(f"  const float* __restrict__ gn = gout + n * int64_t({cfg.NO}) * C;")
@@ -574,20 +574,23 @@ def generate() -> str:
         out.append(f"  {{{im}, {sm}, {om}, {cfg.NP}, {cfg.NX}, {cfg.NY}, {cfg.NO}, {len(cfg.groups)}}},")
     out.append("};")
     out.append(f"static constexpr int kNumTPConfigs = {len(cfgs)};")
-    for cpl in (1, 2):
-        out.append(f"static const TPFwdFn kTPFwd{cpl}[][4] = {{")
+    # FULL: every lane's channels exist (C a multiple of 64 x CPL), no per-load guards
+    for full, tag in ((False, ""), (True, "F")):
+        fl = "true" if full else "false"
+        for cpl in (1, 2):
+            out.append(f"static const TPFwdFn kTPFwd{tag}{cpl}[][4] = {{")
+            for cfg in cfgs:
+                fns = [f"tp_fwd_c{cfg.idx}_g{g}<{cpl}, {fl}>" for g in range(len(cfg.groups))]
+                fns += ["nullptr"] * (4 - len(fns))
+                out.append("  {" + ", ".join(fns) + "},")
+            out.append("};")
+        # backward: one instantiation per group, channels per lane chosen by register budget
+        out.append(f"static const TPBwdFn kTPBwd{tag}[][4] = {{")
         for cfg in cfgs:
-            fns = [f"tp_fwd_c{cfg.idx}_g{g}<{cpl}>" for g in range(len(cfg.groups))]
+            fns = [f"tp_bwd_c{cfg.idx}_g{g}<{bwd_cpl(ps)}, {fl}>" for g, ps in enumerate(cfg.groups)]
             fns += ["nullptr"] * (4 - len(fns))
             out.append("  {" + ", ".join(fns) + "},")
         out.append("};")
-    # backward: one instantiation per group, channels per lane chosen by register budget
-    out.append("static const TPBwdFn kTPBwd[][4] = {")
-    for cfg in cfgs:
-        fns = [f"tp_bwd_c{cfg.idx}_g{g}<{bwd_cpl(ps)}>" for g, ps in enumerate(cfg.groups)]
-        fns += ["nullptr"] * (4 - len(fns))
-        out.append("  {" + ", ".join(fns) + "},")
-    out.append("};")
     out.append("static const int kTPBwdCPL[][4] = {")
     for cfg in cfgs:
         cp = [str(bwd_cpl(ps)) for ps in cfg.groups] + ["0"] * (4 - len(cfg.groups))

@@ -184,7 +184,8 @@ int mnx_tp_fwd_f32(int32_t config, int32_t C, const float* x, const float* Y, co
     const int cblocks = int(ceil_div(C, 64 * cpl));
     const dim3 grid = node_grid(N, cblocks);
     for (int g = 0; g < cfg.ngroups; ++g) {
-        TPFwdFn fn = cpl == 2 ? kTPFwd2[config][g] : kTPFwd1[config][g];
+        const bool full = C % (64 * cpl) == 0;
+        TPFwdFn fn = cpl == 2 ? (full ? kTPFwdF2 : kTPFwd2)[config][g] : (full ? kTPFwdF1 : kTPFwd1)[config][g];
         hipLaunchKernelGGL(fn, grid, dim3(64), 0, (hipStream_t)stream, x, Y, w, row_ptr, perm, snd, N, C, out);
         MNX_CHECK_LAUNCH();
     }
@@ -219,7 +220,9 @@ int mnx_tp_bwd_f32(int32_t config, int32_t C, const float* x, const float* Y, co
     int pbase = 0;
     for (int g = 0; g < cfg.ngroups; ++g) {
         const int cblocks = int(ceil_div(C, 64 * kTPBwdCPL[config][g]));
-        hipLaunchKernelGGL(kTPBwd[config][g], node_grid(N, cblocks), dim3(64), 0, (hipStream_t)stream, x, Y, w, gout,
+        const bool full = C % (64 * kTPBwdCPL[config][g]) == 0;
+        hipLaunchKernelGGL((full ? kTPBwdF : kTPBwd)[config][g], node_grid(N, cblocks), dim3(64), 0,
+                           (hipStream_t)stream, x, Y, w, gout,
                            row_ptr, perm, snd, N, C, gx, gw, part, npart, pbase);
         MNX_CHECK_LAUNCH();
         pbase += cblocks;
