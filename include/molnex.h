@@ -337,11 +337,14 @@ int mnx_radial_bwd_f32(const float* feats, int64_t num_edges, int32_t kin, int32
 /* (mnx_edge_weights_f32; bias may be NULL) and the input gradient           */
 /* grad_h[e][k] = sum_n grad_w[e][n] W[n][k] (mnx_edge_weights_bwd_f32,      */
 /* overwritten).  W is the torch.nn.Linear weight [N][K].  Products are      */
-/* fp32-accurate: each operand is split exactly into three bf16 parts and    */
-/* six partial products are accumulated in fp32 on the matrix cores.         */
-/* mnx_edge_weights_pack_f32 splits and arranges W once into frag            */
-/* [mnx_edge_weights_frag_elems(K, N, backward)] bf16 values (16-byte        */
-/* aligned), backward = 0 for the forward layout, 1 for the backward one.    */
+/* near-fp32 (relative error per product below 3 * 2^-22): rows of h and    */
+/* grad_w and output columns of W are scaled by powers of two, each scaled   */
+/* value is split into two fp16 parts and three partial products are        */
+/* accumulated in fp32 on the matrix cores; the scales are undone exactly.   */
+/* mnx_edge_weights_pack_f32 scales, splits and arranges W once into frag    */
+/* [mnx_edge_weights_frag_elems(K, N, backward)] 16-bit values (16-byte      */
+/* aligned: the fp16 planes, then the column scales as fp32), backward = 0  */
+/* for the forward layout, 1 for the backward one.                           */
 /* K in {16, 32, 64, 128} (else MNX_ERR_UNSUPPORTED; the size query returns  */
 /* -1); the backward needs N % 8 == 0; h and grad_w 16-byte aligned.         */
 /* ------------------------------------------------------------------------ */

@@ -17,7 +17,7 @@ class _Config:
     # parameters need no gradient (energy + forces); False: always the Sequential
     fused_radial: bool = True
     # True: RadialWeightMLP's last Linear (the per-edge tensor-product weights) runs as the
-    # split-bf16 matrix-core kernel molix::edge_weights; False: hipBLASLt fp32 GEMMs
+    # split-fp16 matrix-core kernel molix::edge_weights; False: hipBLASLt fp32 GEMMs
     edge_weights_kernel: bool = True
 
 

@@ -5,44 +5,52 @@
 // (the last Linear of src/molrep/interaction/radial_mlp.py:38-93; at 2.6 M edges
 // and N = 2944 the forward's result alone is 30.8 GB).
 //
-// Arithmetic: fp32-accurate products on the bf16 matrix cores.  Each fp32
-// operand a is split into three bf16 parts, a0 = bf16(a), a1 = bf16(a - a0),
-// a2 = bf16(a - a0 - a1) (round to nearest even; the differences are exact in
-// fp32), so that a = a0 + a1 + a2 + r with |r| <= 2^-27 |a|.  A product a*b is
-// taken as the six partial products a_i b_j with i + j <= 2; the dropped terms
-// are below 2^-25 |a b|, under the fp32 rounding of the sum itself.  Each
-// partial product is exact in the fp32 accumulator of v_mfma_f32_32x32x16_bf16,
-// and the six of them are accumulated smallest first.  Six bf16 MFMAs over
-// K = 16 take 3/8 of the matrix-core cycles of the eight fp32 MFMAs
-// (v_mfma_f32_32x32x2f32) over the same K, which takes the forward from the
-// fp32 matrix-core rate to the HBM store rate of its output.
+// Arithmetic: near-fp32 products on the fp16 matrix cores.  Operands are first
+// brought to a common power-of-two scale (each row of h and of the gradient
+// multiplied by 2^-e with 2^e <= its largest magnitude < 2^(e+1); each output
+// column of W likewise), then each scaled value a is split into two fp16 parts,
+// a0 = f16(a), a1 = f16(a - a0) (round to nearest even; the difference is exact
+// in fp32), so that a = a0 + a1 + r with |r| <= 2^-22 |a| (absolute 2^-25 of the
+// row's largest magnitude where a1 falls below the fp16 normal range).  A
+// product a*b is taken as a1 b0 + a0 b1 + a0 b0, smallest first, each exact in
+// the fp32 accumulator of v_mfma_f32_32x32x16_f16; the dropped a1 b1 and the
+// residuals are below 3 * 2^-22 |a b| per product, a few fp32 rounding units and
+// under the rounding of a K-term fp32 sum.  The scales are powers of two and
+// are undone exactly in the epilogue.  Three fp16 MFMAs per K = 16 take 3/16 of
+// the matrix-core cycles of the eight fp32 MFMAs (v_mfma_f32_32x32x2f32) over
+// the same K and half those of a three-way bf16 split (six products), which
+// matters where the layer is matrix-core bound (K = 128, and the clock held
+// down by matrix-core power).
 //
-// MFMA 32x32x16 bf16 operand layout: lane l holds A[l%32][8(l/32) + j] and
+// MFMA 32x32x16 operand layout: lane l holds A[l%32][8(l/32) + j] and
 // B[8(l/32) + j][l%32], j < 8; the accumulator's register r of lane l is
 // D[8(r/4) + 4(l/32) + r%4][l%32].
 //
 // Forward: a workgroup of eight wavefronts owns 256 edges (32 per wavefront,
-// their split rows of h held in registers for the whole kernel) and walks the N
-// columns in LDS stages of 24 KB of pre-split weights, double-buffered: a
-// stage's fragments are loaded into registers while the previous stage is
-// multiplied, so one barrier per stage suffices.  Results leave as
-// non-temporal stores, 128 contiguous bytes per row and half-wavefront (the
-// store pattern that reaches the HBM write rate; 32-byte pieces per row made
-// non-temporal stores five times slower on MI355X).
+// their scaled, split rows of h held in registers for the whole kernel) and
+// walks the N columns in LDS stages of 16 KB of pre-split weights,
+// double-buffered: a stage's fragments are loaded into registers while the
+// previous stage is multiplied, so one barrier per stage suffices.  Results
+// leave as non-temporal stores, 128 contiguous bytes per row and
+// half-wavefront (the store pattern that reaches the HBM write rate; 32-byte
+// pieces per row made non-temporal stores five times slower on MI355X).
 //
-// Backward: a wavefront owns 32 edges and all K output columns (in registers);
-// the E x N gradient streams in once (the next stage's rows loaded while the
-// current one is multiplied; ordinary cached loads, since each 128-byte line is
-// read by four 16-byte pieces and non-temporal loads of such pieces ran at 2/3
-// of the rate) and is split on the fly, the transposed weights come through the
-// same LDS stages.
+// Backward: a wavefront owns 32 edges and all K output columns (in registers),
+// computed transposed, D = W^T grad^T, so that each lane's accumulator column
+// is one edge; the E x N gradient streams in once (the next stage's rows loaded
+// while the current one is multiplied; ordinary cached loads, since each
+// 128-byte line is read by four 16-byte pieces and non-temporal loads of such
+// pieces ran at 2/3 of the rate) and is scaled and split on the fly.  A row's
+// scale is the running maximum over the stages seen so far: when it grows,
+// the accumulator is rescaled by the (exact) power of two.  The transposed
+// weights come through the same LDS stages.
 
 #include "common.h"
 
 namespace mnx {
 namespace {
 
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
@@ -50,15 +58,18 @@ constexpr int kEwFwdThreads = 512;                   // eight wavefronts
 constexpr int kEwFwdRows = (kEwFwdThreads / 64) * 32;  // edges per forward workgroup
 constexpr int kEwBwdThreads = 256;                   // four wavefronts
 constexpr int kEwBwdRows = (kEwBwdThreads / 64) * 32;  // edges per backward workgroup
-constexpr int kEwStageVec = 1536;                    // bf16x8 vectors per LDS stage (24 KB)
+constexpr int kEwStageVec = 1024;                    // f16x8 vectors per LDS stage (16 KB)
+constexpr int kEwNoExp = -127;                       // scale exponent of an all-zero row
 
-// Weight fragment layouts (bf16 elements, 8 per lane-vector).
+// Weight fragment layouts (fp16 elements, 8 per lane-vector), of W scaled by the
+// reciprocal of its column scale (forward: per output n; backward: per output k):
 //  forward, B = W^T (K x N): [stage][plane][q < KS][t < SC][lane][8] holds
 //    W[n][k], k = 16q + 8(lane/32) + j, n = 32(SC*stage + t) + lane%32;
-//  backward, B = W (N x K): [stage][plane][q < NQ][t < T][lane][8] holds
+//  backward, A = W^T (K x N): [stage][plane][q < NQ][t < T][lane][8] holds
 //    W[n][c], n = 16(NQ*stage + q) + 8(lane/32) + j, c = 32t + lane%32;
-// zero outside the matrix.  KS * SC = NQ * T = 8, so every stage is 3 * 8 * 64
-// vectors.
+// zero outside the matrix.  KS * SC = NQ * T = 8, so every stage is 2 * 8 * 64
+// vectors.  The planes are followed by the column scales as fp32 (N of them
+// forward, K backward), each a power of two.
 struct EwShape {
     int K, N;
     __host__ __device__ int ks() const { return K / 16; }
@@ -67,38 +78,74 @@ struct EwShape {
     __host__ __device__ int nq() const { return 8 / tiles_b(); }
     __host__ __device__ int stages_f() const { return (N + 32 * sc() - 1) / (32 * sc()); }
     __host__ __device__ int stages_b() const { return (N + 16 * nq() - 1) / (16 * nq()); }
-    __host__ __device__ int64_t elems_f() const { return int64_t(stages_f()) * kEwStageVec * 8; }
-    __host__ __device__ int64_t elems_b() const { return int64_t(stages_b()) * kEwStageVec * 8; }
+    __host__ __device__ int64_t planes(bool bwd) const {
+        return int64_t(bwd ? stages_b() : stages_f()) * kEwStageVec * 8;
+    }
+    // fp16 elements in all: the planes, then the scales (two fp16 slots per fp32)
+    __host__ __device__ int64_t elems(bool bwd) const { return planes(bwd) + 2 * int64_t(bwd ? K : N); }
 };
 
-__device__ __forceinline__ void split3(float v, __bf16& b0, __bf16& b1, __bf16& b2) {
-    b0 = (__bf16)v;
-    float r = v - (float)b0;
-    b1 = (__bf16)r;
-    r -= (float)b1;
-    b2 = (__bf16)r;
+// Exponent e with 2^e <= m < 2^(e+1), clamped so that 2^e and 2^-e are normal;
+// kEwNoExp for m == 0, 0 for inf/NaN (left to propagate).
+__device__ __forceinline__ int ew_exp(float m) {
+    if (m == 0.f) return kEwNoExp;
+    if (!(m <= 3.402823466e38f)) return 0;
+    return min(max(ilogbf(m), -126), 126);
 }
 
-__device__ __forceinline__ void split8(const f32x4& lo, const f32x4& hi, bf16x8& a0, bf16x8& a1, bf16x8& a2) {
+__device__ __forceinline__ void split8(const f32x4& lo, const f32x4& hi, float s, f16x8& a0, f16x8& a1) {
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-        __bf16 b0, b1, b2;
-        split3(j < 4 ? lo[j] : hi[j - 4], b0, b1, b2);
-        a0[j] = b0;
-        a1[j] = b1;
-        a2[j] = b2;
+        const float v = (j < 4 ? lo[j] : hi[j - 4]) * s;
+        const _Float16 h0 = (_Float16)v;
+        a0[j] = h0;
+        a1[j] = (_Float16)(v - (float)h0);
     }
 }
 
-__device__ __forceinline__ f32x16 mfma(const bf16x8& a, const bf16x8& b, const f32x16& c) {
-    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+__device__ __forceinline__ float absmax8(const f32x4& lo, const f32x4& hi, float m) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) m = fmaxf(m, fmaxf(fabsf(lo[j]), fabsf(hi[j])));
+    return m;
 }
 
-// One thread per fragment element (both layouts).
-__global__ void k_ew_pack(const float* __restrict__ W, EwShape sh, bool bwd, __bf16* __restrict__ frag) {
+__device__ __forceinline__ f32x16 mfma(const f16x8& a, const f16x8& b, const f32x16& c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+
+// Column scales: forward one thread per output n (max over its K weights); backward
+// one workgroup per output k (max over the N weights of column k).
+__global__ void k_ew_scales(const float* __restrict__ W, int K, int N, int bwd, float* __restrict__ scale) {
+    if (!bwd) {
+        const int n = blockIdx.x * blockDim.x + threadIdx.x;
+        if (n >= N) return;
+        float m = 0.f;
+        for (int k = 0; k < K; ++k) m = fmaxf(m, fabsf(W[int64_t(n) * K + k]));
+        const int e = ew_exp(m);
+        scale[n] = ldexpf(1.f, e == kEwNoExp ? 0 : e);
+        return;
+    }
+    __shared__ float part[256];
+    const int k = blockIdx.x;
+    float m = 0.f;
+    for (int n = threadIdx.x; n < N; n += blockDim.x) m = fmaxf(m, fabsf(W[int64_t(n) * K + k]));
+    part[threadIdx.x] = m;
+    __syncthreads();
+    for (int w = blockDim.x / 2; w > 0; w /= 2) {
+        if (threadIdx.x < w) part[threadIdx.x] = fmaxf(part[threadIdx.x], part[threadIdx.x + w]);
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) {
+        const int e = ew_exp(part[0]);
+        scale[k] = ldexpf(1.f, e == kEwNoExp ? 0 : e);
+    }
+}
+
+// One thread per fragment element (both layouts); the scales are already in place.
+__global__ void k_ew_pack(const float* __restrict__ W, EwShape sh, bool bwd, const float* __restrict__ scale,
+                          _Float16* __restrict__ frag) {
     const int64_t idx = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
-    const int64_t total = bwd ? sh.elems_b() : sh.elems_f();
-    if (idx >= total) return;
+    if (idx >= sh.planes(bwd)) return;
     const int j = int(idx % 8), lane = int((idx / 8) % 64);
     int64_t rest = idx / 512;
     int n, k, p;
@@ -108,8 +155,8 @@ __global__ void k_ew_pack(const float* __restrict__ W, EwShape sh, bool bwd, __b
         rest /= sc;
         const int q = int(rest % ks);
         rest /= ks;
-        p = int(rest % 3);
-        const int s = int(rest / 3);
+        p = int(rest % 2);
+        const int s = int(rest / 2);
         k = 16 * q + 8 * (lane / 32) + j;
         n = 32 * (sc * s + t) + lane % 32;
     } else {
@@ -118,61 +165,73 @@ __global__ void k_ew_pack(const float* __restrict__ W, EwShape sh, bool bwd, __b
         rest /= T;
         const int q = int(rest % nq);
         rest /= nq;
-        p = int(rest % 3);
-        const int s = int(rest / 3);
+        p = int(rest % 2);
+        const int s = int(rest / 2);
         n = 16 * (nq * s + q) + 8 * (lane / 32) + j;
         k = 32 * t + lane % 32;
     }
-    __bf16 part = (__bf16)0.f;
+    _Float16 part = (_Float16)0.f;
     if (n < sh.N && k < sh.K) {
-        __bf16 b0, b1, b2;
-        split3(W[int64_t(n) * sh.K + k], b0, b1, b2);
-        part = p == 0 ? b0 : (p == 1 ? b1 : b2);
+        const float v = ldexpf(W[int64_t(n) * sh.K + k], -ilogbf(scale[bwd ? k : n]));
+        const _Float16 h0 = (_Float16)v;
+        part = p == 0 ? h0 : (_Float16)(v - (float)h0);
     }
     frag[idx] = part;
 }
 
 template <int KS>
 __global__ __launch_bounds__(kEwFwdThreads) void k_ew_fwd(const float* __restrict__ h, int64_t E,
-                                                          const bf16x8* __restrict__ frag,
+                                                          const f16x8* __restrict__ frag,
+                                                          const float* __restrict__ colscale,
                                                           const float* __restrict__ bias, int N, int nstages,
                                                           float* __restrict__ out) {
     constexpr int K = 16 * KS, SC = 8 / KS;
     constexpr int PER = kEwStageVec / kEwFwdThreads;
     // Column tiles multiplied together: two independent accumulator chains keep the matrix
-    // core busy between dependent MFMAs (with one tile per stage, K = 128, a second chain
-    // costs more in registers than it gains).
+    // core busy between dependent MFMAs.
     constexpr int TP = SC >= 2 ? 2 : 1;
-    __shared__ bf16x8 sB[2][kEwStageVec];
-    __shared__ float sBias[2][SC * 32];
+    __shared__ f16x8 sB[2][kEwStageVec];
+    __shared__ float sBias[2][SC * 32], sCol[2][SC * 32];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int64_t row0 = int64_t(blockIdx.x) * kEwFwdRows + wave * 32;
 
-    bf16x8 a0[KS], a1[KS], a2[KS];
+    f16x8 a0[KS], a1[KS];
+    float rs[16];  // scales of the accumulator rows this lane holds
     {
         const int64_t row = row0 + (lane & 31);
         const bool ok = row < E;
         const float* src = h + (ok ? row : 0) * K + 8 * (lane >> 5);
+        f32x4 v[KS][2];
+        float m = 0.f;
 #pragma unroll
         for (int q = 0; q < KS; ++q) {
-            f32x4 lo = {0.f, 0.f, 0.f, 0.f}, hi = lo;
+            v[q][0] = v[q][1] = f32x4{0.f, 0.f, 0.f, 0.f};
             if (ok) {
-                lo = *reinterpret_cast<const f32x4*>(src + 16 * q);
-                hi = *reinterpret_cast<const f32x4*>(src + 16 * q + 4);
+                v[q][0] = *reinterpret_cast<const f32x4*>(src + 16 * q);
+                v[q][1] = *reinterpret_cast<const f32x4*>(src + 16 * q + 4);
             }
-            split8(lo, hi, a0[q], a1[q], a2[q]);
+            m = absmax8(v[q][0], v[q][1], m);
         }
+        m = fmaxf(m, __shfl_xor(m, 32));
+        int e = ew_exp(m);
+        if (e == kEwNoExp) e = 0;
+        const float si = ldexpf(1.f, -e), so = ldexpf(1.f, e);
+#pragma unroll
+        for (int q = 0; q < KS; ++q) split8(v[q][0], v[q][1], si, a0[q], a1[q]);
+#pragma unroll
+        for (int r = 0; r < 16; ++r) rs[r] = __shfl(so, 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3));
     }
 
-    bf16x8 pre[PER];
-    float pbias = 0.f;
+    f16x8 pre[PER];
+    float pbias = 0.f, pcol = 1.f;
     auto fetch = [&](int s) {
-        const bf16x8* src = frag + int64_t(s) * kEwStageVec + threadIdx.x;
+        const f16x8* src = frag + int64_t(s) * kEwStageVec + threadIdx.x;
 #pragma unroll
         for (int i = 0; i < PER; ++i) pre[i] = src[i * kEwFwdThreads];
         if (threadIdx.x < SC * 32) {
             const int n = s * SC * 32 + threadIdx.x;
             pbias = (bias && n < N) ? bias[n] : 0.f;
+            pcol = n < N ? colscale[n] : 1.f;
         }
     };
     fetch(0);
@@ -180,54 +239,49 @@ __global__ __launch_bounds__(kEwFwdThreads) void k_ew_fwd(const float* __restric
         const int buf = s & 1;
 #pragma unroll
         for (int i = 0; i < PER; ++i) sB[buf][threadIdx.x + i * kEwFwdThreads] = pre[i];
-        if (threadIdx.x < SC * 32) sBias[buf][threadIdx.x] = pbias;
+        if (threadIdx.x < SC * 32) {
+            sBias[buf][threadIdx.x] = pbias;
+            sCol[buf][threadIdx.x] = pcol;
+        }
         __syncthreads();
         if (s + 1 < nstages) fetch(s + 1);
-        const bf16x8* B = &sB[buf][lane];
-        auto bq = [&](int p, int q, int t) -> const bf16x8& { return B[((p * KS + q) * SC + t) * 64]; };
+        const f16x8* B = &sB[buf][lane];
+        auto bq = [&](int p, int q, int t) -> const f16x8& { return B[((p * KS + q) * SC + t) * 64]; };
 #pragma unroll
         for (int t0 = 0; t0 < SC; t0 += TP) {
             if ((s * SC + t0) * 32 >= N) break;
             f32x16 acc[2] = {f32x16{}, f32x16{}};
-            // accumulator and column tile of chain u
-            auto ai = [&](int, int u) { return u; };
             auto ti = [&](int u) { return TP == 2 ? t0 + u : t0; };
 #pragma unroll
             for (int q = 0; q < KS; ++q)
 #pragma unroll
                 for (int u = 0; u < TP; ++u) {
-                    f32x16& c = acc[ai(q, u)];
-                    c = mfma(a2[q], bq(0, q, ti(u)), c);
-                    c = mfma(a1[q], bq(1, q, ti(u)), c);
-                    c = mfma(a0[q], bq(2, q, ti(u)), c);
+                    acc[u] = mfma(a1[q], bq(0, q, ti(u)), acc[u]);
+                    acc[u] = mfma(a0[q], bq(1, q, ti(u)), acc[u]);
                 }
 #pragma unroll
             for (int q = 0; q < KS; ++q)
 #pragma unroll
-                for (int u = 0; u < TP; ++u) {
-                    f32x16& c = acc[ai(q, u)];
-                    c = mfma(a1[q], bq(0, q, ti(u)), c);
-                    c = mfma(a0[q], bq(1, q, ti(u)), c);
-                }
-#pragma unroll
-            for (int q = 0; q < KS; ++q)
-#pragma unroll
-                for (int u = 0; u < TP; ++u) acc[ai(q, u)] = mfma(a0[q], bq(0, q, ti(u)), acc[ai(q, u)]);
+                for (int u = 0; u < TP; ++u) acc[u] = mfma(a0[q], bq(0, q, ti(u)), acc[u]);
 #pragma unroll
             for (int u = 0; u < TP; ++u) {
                 const int n = (s * SC + t0 + u) * 32 + (lane & 31);
                 if (n >= N) continue;
                 const float b = sBias[buf][(t0 + u) * 32 + (lane & 31)];
+                const float cs = sCol[buf][(t0 + u) * 32 + (lane & 31)];
                 float* o = out + (row0 + 4 * (lane >> 5)) * N + n;
                 if (row0 + 32 <= E) {  // whole row block valid: no per-row branches
 #pragma unroll
                     for (int r = 0; r < 16; ++r)
-                        __builtin_nontemporal_store(acc[u][r] + b, o + int64_t(8 * (r >> 2) + (r & 3)) * N);
+                        __builtin_nontemporal_store(fmaf(acc[u][r] * rs[r], cs, b),
+                                                    o + int64_t(8 * (r >> 2) + (r & 3)) * N);
                 } else {
 #pragma unroll
                     for (int r = 0; r < 16; ++r) {
                         const int64_t row = row0 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-                        if (row < E) __builtin_nontemporal_store(acc[u][r] + b, o + int64_t(8 * (r >> 2) + (r & 3)) * N);
+                        if (row < E)
+                            __builtin_nontemporal_store(fmaf(acc[u][r] * rs[r], cs, b),
+                                                        o + int64_t(8 * (r >> 2) + (r & 3)) * N);
                     }
                 }
             }
@@ -237,11 +291,12 @@ __global__ __launch_bounds__(kEwFwdThreads) void k_ew_fwd(const float* __restric
 
 template <int T>
 __global__ __launch_bounds__(kEwBwdThreads) void k_ew_bwd(const float* __restrict__ gw, int64_t E, int N,
-                                                       const bf16x8* __restrict__ frag, int K, int nstages,
+                                                       const f16x8* __restrict__ frag,
+                                                       const float* __restrict__ colscale, int K, int nstages,
                                                        float* __restrict__ gh) {
     constexpr int NQ = 8 / T;
     constexpr int PER = kEwStageVec / kEwBwdThreads;
-    __shared__ bf16x8 sB[2][kEwStageVec];
+    __shared__ f16x8 sB[2][kEwStageVec];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int64_t row0 = int64_t(blockIdx.x) * kEwBwdRows + wave * 32;
     const int64_t arow = row0 + (lane & 31);
@@ -262,55 +317,72 @@ __global__ __launch_bounds__(kEwBwdThreads) void k_ew_bwd(const float* __restric
             ra[q][1] = hi;
         }
     };
-    bf16x8 pre[PER];
+    f16x8 pre[PER];
     auto fetch_b = [&](int s) {
-        const bf16x8* src = frag + int64_t(s) * kEwStageVec + threadIdx.x;
+        const f16x8* src = frag + int64_t(s) * kEwStageVec + threadIdx.x;
 #pragma unroll
         for (int i = 0; i < PER; ++i) pre[i] = src[i * kEwBwdThreads];
     };
 
+    // acc[t]: D = W^T grad^T, register r of lane l = gh[row0 + l%32][32t + 8(r/4) + 4(l/32) + r%4],
+    // in units of 2^ecur (this lane's row scale so far)
     f32x16 acc[T];
 #pragma unroll
     for (int t = 0; t < T; ++t) acc[t] = f32x16{};
+    int ecur = kEwNoExp;
     fetch_a(0);
     fetch_b(0);
     for (int s = 0; s < nstages; ++s) {
         const int buf = s & 1;
 #pragma unroll
         for (int i = 0; i < PER; ++i) sB[buf][threadIdx.x + i * kEwBwdThreads] = pre[i];
-        bf16x8 a0[NQ], a1[NQ], a2[NQ];
+        float m = 0.f;
 #pragma unroll
-        for (int q = 0; q < NQ; ++q) split8(ra[q][0], ra[q][1], a0[q], a1[q], a2[q]);
+        for (int q = 0; q < NQ; ++q) m = absmax8(ra[q][0], ra[q][1], m);
+        m = fmaxf(m, __shfl_xor(m, 32));
+        const int enew = max(ecur, ew_exp(m));
+        if (__ballot(enew != ecur)) {
+            const float f = ldexpf(1.f, ecur - enew);
+#pragma unroll
+            for (int t = 0; t < T; ++t) acc[t] *= f;
+        }
+        ecur = enew;
+        f16x8 g0[NQ], g1[NQ];
+        const float si = ldexpf(1.f, -ecur);
+#pragma unroll
+        for (int q = 0; q < NQ; ++q) split8(ra[q][0], ra[q][1], si, g0[q], g1[q]);
         __syncthreads();
         if (s + 1 < nstages) {
             fetch_a(s + 1);
             fetch_b(s + 1);
         }
-        const bf16x8* B = &sB[buf][lane];
-        auto bq = [&](int p, int q, int t) -> const bf16x8& { return B[((p * NQ + q) * T + t) * 64]; };
+        const f16x8* B = &sB[buf][lane];
+        auto wq = [&](int p, int q, int t) -> const f16x8& { return B[((p * NQ + q) * T + t) * 64]; };
 #pragma unroll
         for (int q = 0; q < NQ; ++q) {
 #pragma unroll
             for (int t = 0; t < T; ++t) {
-                acc[t] = mfma(a2[q], bq(0, q, t), acc[t]);
-                acc[t] = mfma(a1[q], bq(1, q, t), acc[t]);
-                acc[t] = mfma(a0[q], bq(2, q, t), acc[t]);
-                acc[t] = mfma(a1[q], bq(0, q, t), acc[t]);
-                acc[t] = mfma(a0[q], bq(1, q, t), acc[t]);
-                acc[t] = mfma(a0[q], bq(0, q, t), acc[t]);
+                acc[t] = mfma(wq(0, q, t), g1[q], acc[t]);
+                acc[t] = mfma(wq(1, q, t), g0[q], acc[t]);
+                acc[t] = mfma(wq(0, q, t), g0[q], acc[t]);
             }
         }
     }
+    if (!aok) return;
+    const float so = ldexpf(1.f, ecur == kEwNoExp ? 0 : ecur);
+    float* dst = gh + arow * K;
 #pragma unroll
-    for (int t = 0; t < T; ++t) {
-        const int c = 32 * t + (lane & 31);
-        if (c >= K) continue;
+    for (int t = 0; t < T; ++t)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const int64_t row = row0 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-            if (row < E) gh[row * K + c] = acc[t][r];
+        for (int r4 = 0; r4 < 4; ++r4) {
+            const int c = 32 * t + 8 * r4 + 4 * (lane >> 5);
+            if (c >= K) continue;
+            const f32x4 cs = *reinterpret_cast<const f32x4*>(colscale + c);
+            f32x4 v;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) v[i] = acc[t][4 * r4 + i] * so * cs[i];
+            *reinterpret_cast<f32x4*>(dst + c) = v;
         }
-    }
 }
 
 int check_ew(int32_t K, int32_t N) {
@@ -330,7 +402,7 @@ extern "C" {
 int64_t mnx_edge_weights_frag_elems(int32_t K, int32_t N, int32_t backward) {
     if (check_ew(K, N)) return -1;
     const EwShape sh{K, N};
-    return backward ? sh.elems_b() : sh.elems_f();
+    return sh.elems(backward != 0);
 }
 
 int mnx_edge_weights_pack_f32(const float* weight, int32_t K, int32_t N, int32_t backward, uint16_t* frag,
@@ -339,10 +411,19 @@ int mnx_edge_weights_pack_f32(const float* weight, int32_t K, int32_t N, int32_t
     int rc = check_ew(K, N);
     if (rc) return rc;
     MNX_REQUIRE(weight && frag, "null pointer argument");
+    MNX_REQUIRE((uintptr_t)frag % 16 == 0, "frag must be 16-byte aligned");
     const EwShape sh{K, N};
-    const int64_t total = backward ? sh.elems_b() : sh.elems_f();
-    hipLaunchKernelGGL(k_ew_pack, dim3(ceil_div(total, 256)), dim3(256), 0, (hipStream_t)stream, weight, sh,
-                       backward != 0, reinterpret_cast<__bf16*>(frag));
+    const bool bwd = backward != 0;
+    const int64_t total = sh.planes(bwd);
+    hipStream_t s = (hipStream_t)stream;
+    float* scale = reinterpret_cast<float*>(frag + total);
+    if (bwd)
+        hipLaunchKernelGGL(k_ew_scales, dim3(K), dim3(256), 0, s, weight, K, N, 1, scale);
+    else
+        hipLaunchKernelGGL(k_ew_scales, dim3(unsigned(ceil_div(N, 256))), dim3(256), 0, s, weight, K, N, 0, scale);
+    MNX_CHECK_LAUNCH();
+    hipLaunchKernelGGL(k_ew_pack, dim3(unsigned(ceil_div(total, 256))), dim3(256), 0, s, weight, sh, bwd, scale,
+                       reinterpret_cast<_Float16*>(frag));
     MNX_CHECK_LAUNCH();
     return MNX_OK;
 }
@@ -358,13 +439,14 @@ int mnx_edge_weights_f32(const float* h, int64_t num_edges, int32_t K, const uin
     MNX_REQUIRE(((uintptr_t)h | (uintptr_t)frag) % 16 == 0, "h and frag must be 16-byte aligned");
     const EwShape sh{K, N};
     const dim3 grid(unsigned(ceil_div(num_edges, kEwFwdRows))), block(kEwFwdThreads);
-    const bf16x8* f = reinterpret_cast<const bf16x8*>(frag);
+    const f16x8* f = reinterpret_cast<const f16x8*>(frag);
+    const float* cs = reinterpret_cast<const float*>(frag + sh.planes(false));
     hipStream_t s = (hipStream_t)stream;
     switch (K) {
-        case 16: hipLaunchKernelGGL(k_ew_fwd<1>, grid, block, 0, s, h, num_edges, f, bias, N, sh.stages_f(), out); break;
-        case 32: hipLaunchKernelGGL(k_ew_fwd<2>, grid, block, 0, s, h, num_edges, f, bias, N, sh.stages_f(), out); break;
-        case 64: hipLaunchKernelGGL(k_ew_fwd<4>, grid, block, 0, s, h, num_edges, f, bias, N, sh.stages_f(), out); break;
-        default: hipLaunchKernelGGL(k_ew_fwd<8>, grid, block, 0, s, h, num_edges, f, bias, N, sh.stages_f(), out); break;
+        case 16: hipLaunchKernelGGL(k_ew_fwd<1>, grid, block, 0, s, h, num_edges, f, cs, bias, N, sh.stages_f(), out); break;
+        case 32: hipLaunchKernelGGL(k_ew_fwd<2>, grid, block, 0, s, h, num_edges, f, cs, bias, N, sh.stages_f(), out); break;
+        case 64: hipLaunchKernelGGL(k_ew_fwd<4>, grid, block, 0, s, h, num_edges, f, cs, bias, N, sh.stages_f(), out); break;
+        default: hipLaunchKernelGGL(k_ew_fwd<8>, grid, block, 0, s, h, num_edges, f, cs, bias, N, sh.stages_f(), out); break;
     }
     MNX_CHECK_LAUNCH();
     return MNX_OK;
@@ -382,12 +464,13 @@ int mnx_edge_weights_bwd_f32(const float* grad_w, int64_t num_edges, int32_t N, 
     MNX_REQUIRE(((uintptr_t)grad_w | (uintptr_t)frag) % 16 == 0, "grad_w and frag must be 16-byte aligned");
     const EwShape sh{K, N};
     const dim3 grid(unsigned(ceil_div(num_edges, kEwBwdRows))), block(kEwBwdThreads);
-    const bf16x8* f = reinterpret_cast<const bf16x8*>(frag);
+    const f16x8* f = reinterpret_cast<const f16x8*>(frag);
+    const float* cs = reinterpret_cast<const float*>(frag + sh.planes(true));
     hipStream_t s = (hipStream_t)stream;
     switch (sh.tiles_b()) {
-        case 1: hipLaunchKernelGGL(k_ew_bwd<1>, grid, block, 0, s, grad_w, num_edges, N, f, K, sh.stages_b(), grad_h); break;
-        case 2: hipLaunchKernelGGL(k_ew_bwd<2>, grid, block, 0, s, grad_w, num_edges, N, f, K, sh.stages_b(), grad_h); break;
-        default: hipLaunchKernelGGL(k_ew_bwd<4>, grid, block, 0, s, grad_w, num_edges, N, f, K, sh.stages_b(), grad_h); break;
+        case 1: hipLaunchKernelGGL(k_ew_bwd<1>, grid, block, 0, s, grad_w, num_edges, N, f, cs, K, sh.stages_b(), grad_h); break;
+        case 2: hipLaunchKernelGGL(k_ew_bwd<2>, grid, block, 0, s, grad_w, num_edges, N, f, cs, K, sh.stages_b(), grad_h); break;
+        default: hipLaunchKernelGGL(k_ew_bwd<4>, grid, block, 0, s, grad_w, num_edges, N, f, cs, K, sh.stages_b(), grad_h); break;
     }
     MNX_CHECK_LAUNCH();
     return MNX_OK;

@@ -14,7 +14,7 @@ Ops
 ``molix::edge_csr``             receiver CSR of an (E, 2) edge list
 ``molix::tp_scatter``           channelwise TP + scatter-sum (``cuet.ChannelWiseTensorProduct``)
 ``molix::radial_hidden``        fused hidden stack of the radial weight MLP (gradient w.r.t. its input)
-``molix::edge_weights``         output layer of the radial weight MLP (per-edge TP weights), fp32-accurate split-bf16 MFMA
+``molix::edge_weights``         output layer of the radial weight MLP (per-edge TP weights), near-fp32 split-fp16 MFMA
 ``molix::bond_vectors``         pos[receiver] - pos[sender] - shift per edge, with its position gradient
 ``molix::block_linear``         equivariant (ir_mul) block linear with pre-ordered weights (``cuet.Linear``)
 """
@@ -893,7 +893,7 @@ def _(h, weight, bias=None):
 
 @torch.library.custom_op("molix::edge_weights_backward", mutates_args=(), device_types="cuda")
 def edge_weights_backward(grad: Tensor, weight: Tensor) -> Tensor:
-    """``grad @ weight``: dL/dh of ``edge_weights`` (same split-bf16 arithmetic)."""
+    """``grad @ weight``: dL/dh of ``edge_weights`` (same split-fp16 arithmetic)."""
     N, K = weight.shape
     if grad.dim() != 2 or grad.shape[1] != N:
         raise ValueError("edge_weights_backward: grad must be (E, N)")

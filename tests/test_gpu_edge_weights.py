@@ -1,7 +1,7 @@
 """Radial-MLP output layer (molix::edge_weights) vs the same Linear in float64.
 
-The kernel computes fp32-accurate products from three-way bf16 splits of both operands on the
-matrix cores.  Tolerance: norm-wise relative error at most 4x that of torch's own fp32 GEMM on
+The kernel computes near-fp32 products on the fp16 matrix cores (operands scaled by powers of two
+per row / output column and split into two fp16 parts, three partial products).  Tolerance: norm-wise relative error at most 4x that of torch's own fp32 GEMM on
 the same inputs (and at most 1e-5), max-abs at most 4x torch's or 1e-5 x RMS of the result, for the forward,
 the input gradient and the training gradients of weight and bias.
 """
