@@ -356,6 +356,31 @@ int mnx_edge_weights_f32(const float* h, int64_t num_edges, int32_t K, const uin
 int mnx_edge_weights_bwd_f32(const float* grad_w, int64_t num_edges, int32_t N, const uint16_t* frag,
                              int32_t K, float* grad_h, mnx_stream_t stream);
 
+/* ------------------------------------------------------------------------ */
+/* Per-edge channelwise tensor product with shared weights, no scatter: the  */
+/* layer product of Allegro (src/molzoo/allegro.py:352-359, applied at       */
+/* :457-458 to the scaled edge features and the aggregated harmonics of each */
+/* edge's source; there cuet.ChannelWiseTensorProduct with                   */
+/* shared_weights=True, followed by cuet.Linear(tp.irreps_out, irreps_in)).  */
+/*   out[e][o3 + m3][c] = w[p][c] sum cf_p[m1][m2][m3] x[e][o1+m1][c] Y[e][o2+m2] */
+/* config from mnx_tp_config with input, harmonics and output l all          */
+/* 0..l_max (only the paths whose output irrep is an input irrep are         */
+/* computed, the ones the projection reads); channels 8, 16, 32, 64 or 128.  */
+/* Layouts (ir_mul): x [E][NX * C], Y [E][NY], w [num_paths][C],             */
+/* out [E][NO * C] (mnx_tp_config_info gives NX, NY, NO, num_paths).         */
+/* The backward overwrites grad_x [E][NX * C], grad_Y [E][NY] and grad_w     */
+/* [num_paths][C] (each may be NULL); grad_w is summed over edges in a fixed */
+/* order (bitwise reproducible) through a workspace of                       */
+/* mnx_edge_tp_bwd_workspace_bytes bytes.                                    */
+/* ------------------------------------------------------------------------ */
+int mnx_edge_tp_fwd_f32(int32_t config, int32_t channels, const float* x, const float* Y,
+                        const float* w, int64_t num_edges, float* out, mnx_stream_t stream);
+size_t mnx_edge_tp_bwd_workspace_bytes(int32_t config, int32_t channels, int64_t num_edges);
+int mnx_edge_tp_bwd_f32(int32_t config, int32_t channels, const float* x, const float* Y,
+                        const float* w, const float* grad_out, int64_t num_edges, float* grad_x,
+                        float* grad_Y, float* grad_w, void* workspace, size_t workspace_bytes,
+                        mnx_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,128 @@
+// Per-edge channelwise tensor product with shared weights (Allegro's layer
+// product, src/molzoo/allegro.py:352-359,457-458): out[e] = TP(x[e], Y[e]; w),
+// no scatter.  The kernels are generated per configuration by gen_edge_tp.py
+// (edge_tp_gen.inc); configuration ids are those of mnx_tp_config.  Lanes hold
+// (edge, channel) pairs, 64 / min(C, 64) edges per wavefront.
+//
+// HBM traffic per edge: forward 4 (NX + NO) C + 4 NY bytes; backward
+// 4 (2 NX + NO) C + 8 NY bytes (plus one weight-gradient partial per
+// wavefront).
+
+#include "common.h"
+
+namespace mnx {
+namespace {
+
+struct ETPInfo {
+    int ok, np, nx, ny, no;
+};
+
+typedef void (*ETPFwdFn)(const float*, const float*, const float*, int64_t, int, float*);
+typedef void (*ETPBwdFn)(const float*, const float*, const float*, const float*, int64_t, int, float*, float*,
+                         float*);
+
+#include "edge_tp_gen.inc"
+
+constexpr int kETPThreads = 256;   // four wavefronts
+constexpr int kETPBwdWaves = 2048; // wavefronts of the backward grid (grid-stride over edges)
+
+// Sums the per-wavefront weight-gradient partials in a fixed order.
+__global__ void k_etp_reduce(const float* __restrict__ part, int64_t nparts, int64_t n, float* __restrict__ gw) {
+    const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    float s = 0.f;
+    for (int64_t b = 0; b < nparts; ++b) s += part[b * n + i];
+    gw[i] = s;
+}
+
+int etp_variant(int C) {
+    for (int v = 0; v < kETPNumVariants; ++v)
+        if (kETPVariantCW[v] * kETPVariantCPL[v] == C) return v;
+    return -1;
+}
+
+int etp_check(int32_t config, int32_t C, int64_t E, int* variant) {
+    MNX_REQUIRE(config >= 0 && config < kETPNumConfigs, "edge tensor product: config %d out of range", config);
+    if (!kETPInfo[config].ok)
+        return set_error(MNX_ERR_UNSUPPORTED,
+                         "edge tensor product: no per-edge kernel for config %d (input, harmonics and output l "
+                         "must all be 0..l_max)",
+                         config);
+    *variant = etp_variant(C);
+    if (*variant < 0)
+        return set_error(MNX_ERR_UNSUPPORTED, "edge tensor product: %d channels (8, 16, 32, 64 or 128 compiled)", C);
+    MNX_REQUIRE(E >= 0 && E < (int64_t(1) << 40), "edge count out of range");
+    return MNX_OK;
+}
+
+int64_t etp_bwd_waves(int64_t E, int C) {
+    const int64_t G = 64 / (C < 64 ? C : 64);
+    const int64_t groups = (E + G - 1) / G;
+    int64_t waves = groups < kETPBwdWaves ? groups : kETPBwdWaves;
+    return ((waves + 3) / 4) * 4;
+}
+
+}  // namespace
+}  // namespace mnx
+
+using namespace mnx;
+
+extern "C" {
+
+int mnx_edge_tp_fwd_f32(int32_t config, int32_t channels, const float* x, const float* Y, const float* w,
+                        int64_t num_edges, float* out, mnx_stream_t stream) {
+    clear_error();
+    int v = -1;
+    int rc = etp_check(config, channels, num_edges, &v);
+    if (rc) return rc;
+    if (num_edges == 0) return MNX_OK;
+    MNX_REQUIRE(x && Y && w && out, "null pointer argument");
+    const int64_t G = 64 / kETPVariantCW[v];
+    const int64_t blocks = ceil_div(ceil_div(num_edges, G), kETPThreads / 64);
+    hipLaunchKernelGGL(kETPFwd[config][v], dim3(unsigned(blocks)), dim3(kETPThreads), 0, (hipStream_t)stream, x, Y,
+                       w, num_edges, channels, out);
+    MNX_CHECK_LAUNCH();
+    return MNX_OK;
+}
+
+size_t mnx_edge_tp_bwd_workspace_bytes(int32_t config, int32_t channels, int64_t num_edges) {
+    int v = -1;
+    if (etp_check(config, channels, num_edges, &v)) return 0;
+    return size_t(etp_bwd_waves(num_edges, channels)) * kETPInfo[config].np * channels * sizeof(float);
+}
+
+int mnx_edge_tp_bwd_f32(int32_t config, int32_t channels, const float* x, const float* Y, const float* w,
+                        const float* grad_out, int64_t num_edges, float* grad_x, float* grad_Y, float* grad_w,
+                        void* workspace, size_t workspace_bytes, mnx_stream_t stream) {
+    clear_error();
+    int v = -1;
+    int rc = etp_check(config, channels, num_edges, &v);
+    if (rc) return rc;
+    hipStream_t s = (hipStream_t)stream;
+    const int64_t nw = int64_t(kETPInfo[config].np) * channels;
+    if (num_edges == 0) {
+        if (grad_w) {
+            // no edges: the weight gradient is zero (the reduction over no partials)
+            hipLaunchKernelGGL(k_etp_reduce, dim3(unsigned(ceil_div(nw, 256))), dim3(256), 0, s,
+                               static_cast<const float*>(nullptr), int64_t(0), nw, grad_w);
+            MNX_CHECK_LAUNCH();
+        }
+        return MNX_OK;
+    }
+    MNX_REQUIRE(x && Y && w && grad_out, "null pointer argument");
+    const int64_t waves = etp_bwd_waves(num_edges, channels);
+    const size_t need = size_t(waves) * nw * sizeof(float);
+    MNX_REQUIRE(workspace && workspace_bytes >= need, "edge tensor product backward: workspace of %zu bytes needed",
+                need);
+    float* part = static_cast<float*>(workspace);
+    hipLaunchKernelGGL(kETPBwd[config][v], dim3(unsigned(waves / 4)), dim3(kETPThreads), 0, s, grad_out, x, Y, w,
+                       num_edges, channels, grad_x, grad_Y, part);
+    MNX_CHECK_LAUNCH();
+    if (grad_w) {
+        hipLaunchKernelGGL(k_etp_reduce, dim3(unsigned(ceil_div(nw, 256))), dim3(256), 0, s, part, waves, nw, grad_w);
+        MNX_CHECK_LAUNCH();
+    }
+    return MNX_OK;
+}
+
+}  // extern "C"

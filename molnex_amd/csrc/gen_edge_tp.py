@@ -1,0 +1,231 @@
+"""Generates edge_tp_gen.inc: the per-edge channelwise tensor product with shared
+weights (no scatter) of Allegro's layers, forward and backward, one kernel per
+configuration and channel width.
+
+    out[e][o3 + m3][c] = w[p][c] * sum_{m1, m2} cf_p[m1][m2][m3] x[e][o1 + m1][c] Y[e][o2 + m2]
+
+(src/molzoo/allegro.py:352-359 builds it as cuet.ChannelWiseTensorProduct(irreps_in,
+sh_irreps, shared_weights=True); :457-458 applies it to the pre-scaled edge features
+and the aggregated neighbourhood harmonics of each edge's source).  Only the paths
+whose output irrep appears in irreps_in are computed: the projection that follows
+(:363-367, cuet.Linear(tp.irreps_out, irreps_in)) connects nothing else.
+
+Lane layout: a wavefront holds 64 / CW edges side by side, CW = min(C, 64) lanes
+per edge, one channel per lane (CPL = 2 channels per lane for C = 128), so small
+channel counts (Allegro's default is 16) still fill the wave.  Backward per lane
+and channel: v_p[m1][m2] = sum_m3 cf g[o3 + m3] (g the output gradient), then
+grad_x[m1] = sum_p w_p sum_m2 Y[m2] v_p[m1][m2] (stored once: x is per edge),
+grad_Y[m2] = sum_c sum_p w_p sum_m1 x[m1] v_p[m1][m2] (reduced over the CW lanes of
+the edge by xor shuffles), grad_w[p][c] = sum_e sum_m1 x[m1] (sum_m2 Y v)[m1]
+accumulated in registers over the edges a wavefront walks, reduced over its edge
+slots and written as one partial per wavefront (summed in a fixed order by a
+second kernel).
+"""
+
+from __future__ import annotations
+
+import os
+import sys
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.dirname(os.path.dirname(HERE)))
+
+from molnex_amd.csrc.gen_tp import EPS, Cfg, config_list, f32  # noqa: E402
+
+# (channels per edge slot, channels per lane): C = CW * CPL
+VARIANTS = ((8, 1), (16, 1), (32, 1), (64, 1), (64, 2))
+
+
+def supported(cfg: Cfg) -> bool:
+    """Allegro's product: input, harmonics and kept outputs all l = 0 .. l_max."""
+    return cfg.in_ls == cfg.sh_ls == cfg.out_ls
+
+
+def _fwd(cfg: Cfg) -> str:
+    L = []
+    a = L.append
+    NX, NY, NO, NP = cfg.NX, cfg.NY, cfg.NO, cfg.NP
+    a(f"template <int CW, int CPL>\n__global__ void __launch_bounds__(256) etp_fwd_c{cfg.idx}("
+      "const float* __restrict__ x, const float* __restrict__ Y, const float* __restrict__ w, int64_t E, int C, "
+      "float* __restrict__ out) {")
+    a("  constexpr int G = 64 / CW;")
+    a("  const int lane = threadIdx.x & 63;")
+    a("  const int64_t e = (int64_t(blockIdx.x) * 4 + (threadIdx.x >> 6)) * G + lane / CW;")
+    a("  if (e >= E) return;")
+    a("  const int c0 = lane % CW;")
+    a(f"  const float* __restrict__ Ye = Y + e * {NY};")
+    a("  " + " ".join(f"const float y{i} = Ye[{i}];" for i in range(NY)))
+    a(f"  const float* __restrict__ xe = x + e * ({NX} * int64_t(C));")
+    a(f"  float* __restrict__ oe = out + e * ({NO} * int64_t(C));")
+    a("#pragma unroll")
+    a("  for (int k = 0; k < CPL; ++k) {")
+    a("    const int c = c0 + 64 * k;")
+    a(f"    float xv[{NX}];")
+    a(f"#pragma unroll\n    for (int i = 0; i < {NX}; ++i) xv[i] = xe[i * C + c];")
+    for j, p in enumerate(cfg.paths):
+        cf = p["c"]
+        a("    {")
+        a(f"      const float wj = w[{j} * C + c];")
+        for m3 in range(2 * p["l3"] + 1):
+            row = []
+            for m1 in range(2 * p["l1"] + 1):
+                terms = [(m2, cf[m1, m2, m3]) for m2 in range(2 * p["l2"] + 1) if abs(cf[m1, m2, m3]) > EPS]
+                if not terms:
+                    continue
+                expr = f"{f32(terms[0][1])} * y{p['o2'] + terms[0][0]}"
+                for m2, v in terms[1:]:
+                    expr = f"fmaf({f32(v)}, y{p['o2'] + m2}, {expr})"
+                row.append((m1, expr))
+            o = p["o3"] + m3
+            if not row:
+                a(f"      oe[{o} * C + c] = 0.f;")
+                continue
+            s = f"({row[0][1]}) * xv[{p['o1'] + row[0][0]}]"
+            for m1, expr in row[1:]:
+                s = f"fmaf({expr}, xv[{p['o1'] + m1}], {s})"
+            a(f"      oe[{o} * C + c] = wj * ({s});")
+        a("    }")
+    a("  }")
+    a("}")
+    return "\n".join(L)
+
+
+def _bwd(cfg: Cfg) -> str:
+    L = []
+    a = L.append
+    NX, NY, NO, NP = cfg.NX, cfg.NY, cfg.NO, cfg.NP
+    a(f"template <int CW, int CPL>\n__global__ void __launch_bounds__(256) etp_bwd_c{cfg.idx}("
+      "const float* __restrict__ gout, const float* __restrict__ x, const float* __restrict__ Y, "
+      "const float* __restrict__ w, int64_t E, int C, float* __restrict__ gx, float* __restrict__ gY, "
+      "float* __restrict__ gw_part) {")
+    a("  constexpr int G = 64 / CW;")
+    a("  const int lane = threadIdx.x & 63, c0 = lane % CW;")
+    a("  const int64_t wave = int64_t(blockIdx.x) * 4 + (threadIdx.x >> 6), nwaves = int64_t(gridDim.x) * 4;")
+    a("  const int64_t ngroups = (E + G - 1) / G;")
+    a(f"  float wv[CPL][{NP}], gwa[CPL][{NP}];")
+    a("#pragma unroll")
+    a("  for (int k = 0; k < CPL; ++k)")
+    a("#pragma unroll")
+    a(f"    for (int j = 0; j < {NP}; ++j) {{ wv[k][j] = w[j * C + c0 + 64 * k]; gwa[k][j] = 0.f; }}")
+    a("  for (int64_t grp = wave; grp < ngroups; grp += nwaves) {")
+    a("    const int64_t e = grp * G + lane / CW;")
+    a("    const bool valid = e < E;")
+    a("    const int64_t es = valid ? e : 0;")
+    a(f"    const float* __restrict__ Ye = Y + es * {NY};")
+    a("    " + " ".join(f"const float y{i} = valid ? Ye[{i}] : 0.f;" for i in range(NY)))
+    a(f"    float gYp[{NY}];")
+    a(f"#pragma unroll\n    for (int i = 0; i < {NY}; ++i) gYp[i] = 0.f;")
+    a("#pragma unroll")
+    a("    for (int k = 0; k < CPL; ++k) {")
+    a("      const int c = c0 + 64 * k;")
+    a(f"      const float* __restrict__ xe = x + es * ({NX} * int64_t(C)) + c;")
+    a(f"      const float* __restrict__ ge = gout + es * ({NO} * int64_t(C)) + c;")
+    a(f"      float xv[{NX}], gv[{NO}], gxv[{NX}];")
+    a(f"#pragma unroll\n      for (int i = 0; i < {NX}; ++i) {{ xv[i] = valid ? xe[i * C] : 0.f; gxv[i] = 0.f; }}")
+    a(f"#pragma unroll\n      for (int i = 0; i < {NO}; ++i) gv[i] = valid ? ge[i * C] : 0.f;")
+    for j, p in enumerate(cfg.paths):
+        cf = p["c"]
+        a("      {")
+        a(f"        const float wj = wv[k][{j}];")
+        for m1 in range(2 * p["l1"] + 1):
+            vs = []
+            for m2 in range(2 * p["l2"] + 1):
+                terms = [(m3, cf[m1, m2, m3]) for m3 in range(2 * p["l3"] + 1) if abs(cf[m1, m2, m3]) > EPS]
+                if not terms:
+                    continue
+                expr = f"{f32(terms[0][1])} * gv[{p['o3'] + terms[0][0]}]"
+                for m3, v in terms[1:]:
+                    expr = f"fmaf({f32(v)}, gv[{p['o3'] + m3}], {expr})"
+                vs.append((m2, expr))
+            if not vs:
+                continue
+            xi = p["o1"] + m1
+            a("        {")
+            for m2, expr in vs:
+                a(f"          const float v{m2} = {expr};")
+            u = f"y{p['o2'] + vs[0][0]} * v{vs[0][0]}"
+            for m2, _ in vs[1:]:
+                u = f"fmaf(y{p['o2'] + m2}, v{m2}, {u})"
+            a(f"          const float u = {u};")
+            a(f"          gxv[{xi}] = fmaf(wj, u, gxv[{xi}]);")
+            a(f"          gwa[k][{j}] = fmaf(xv[{xi}], u, gwa[k][{j}]);")
+            a(f"          const float xw = xv[{xi}] * wj;")
+            for m2, _ in vs:
+                a(f"          gYp[{p['o2'] + m2}] = fmaf(xw, v{m2}, gYp[{p['o2'] + m2}]);")
+            a("        }")
+        a("      }")
+    a(f"      if (gx && valid) {{ float* __restrict__ gxe = gx + es * ({NX} * int64_t(C)) + c;")
+    a(f"#pragma unroll\n        for (int i = 0; i < {NX}; ++i) gxe[i * C] = gxv[i]; }}")
+    a("    }")
+    a("    if (gY) {")
+    a("#pragma unroll")
+    a(f"      for (int i = 0; i < {NY}; ++i) {{")
+    a("#pragma unroll")
+    a("        for (int s = 1; s < CW; s <<= 1) gYp[i] += __shfl_xor(gYp[i], s);")
+    a("      }")
+    a(f"      if (valid && c0 == 0) {{ float* __restrict__ gYe = gY + es * {NY};")
+    a(f"#pragma unroll\n        for (int i = 0; i < {NY}; ++i) gYe[i] = gYp[i]; }}")
+    a("    }")
+    a("  }")
+    a("  // one partial per wavefront: sum over its edge slots (lanes of equal channel)")
+    a("#pragma unroll")
+    a("  for (int k = 0; k < CPL; ++k)")
+    a("#pragma unroll")
+    a(f"    for (int j = 0; j < {NP}; ++j)")
+    a("#pragma unroll")
+    a("      for (int s = CW; s < 64; s <<= 1) gwa[k][j] += __shfl_xor(gwa[k][j], s);")
+    a("  if (lane < CW) {")
+    a(f"    float* __restrict__ pw = gw_part + wave * ({NP} * int64_t(C));")
+    a("#pragma unroll")
+    a("    for (int k = 0; k < CPL; ++k)")
+    a("#pragma unroll")
+    a(f"      for (int j = 0; j < {NP}; ++j) pw[j * C + c0 + 64 * k] = gwa[k][j];")
+    a("  }")
+    a("}")
+    return "\n".join(L)
+
+
+def generate() -> str:
+    cfgs = [Cfg(i, *c) for i, c in enumerate(config_list())]
+    out = ["// Generated by gen_edge_tp.py -- do not edit.", "// clang-format off", ""]
+    for cfg in cfgs:
+        if not supported(cfg):
+            continue
+        out.append(f"// config {cfg.idx}: l={cfg.in_ls}; {cfg.NP} paths, NX={cfg.NX} NY={cfg.NY} NO={cfg.NO}")
+        out.append(_fwd(cfg))
+        out.append("")
+        out.append(_bwd(cfg))
+        out.append("")
+    out.append(f"static constexpr int kETPNumConfigs = {len(cfgs)};")
+    out.append(f"static constexpr int kETPNumVariants = {len(VARIANTS)};")
+    out.append("static const int kETPVariantCW[] = {" + ", ".join(str(v[0]) for v in VARIANTS) + "};")
+    out.append("static const int kETPVariantCPL[] = {" + ", ".join(str(v[1]) for v in VARIANTS) + "};")
+    out.append("static const ETPInfo kETPInfo[] = {")
+    for cfg in cfgs:
+        out.append(f"  {{{int(supported(cfg))}, {cfg.NP}, {cfg.NX}, {cfg.NY}, {cfg.NO}}},")
+    out.append("};")
+    for kind in ("fwd", "bwd"):
+        typ = "ETPFwdFn" if kind == "fwd" else "ETPBwdFn"
+        out.append(f"static const {typ} kETP{kind.capitalize()}[][{len(VARIANTS)}] = {{")
+        for cfg in cfgs:
+            if supported(cfg):
+                fns = [f"etp_{kind}_c{cfg.idx}<{cw}, {cpl}>" for cw, cpl in VARIANTS]
+            else:
+                fns = ["nullptr"] * len(VARIANTS)
+            out.append("  {" + ", ".join(fns) + "},")
+        out.append("};")
+    return "\n".join(out) + "\n"
+
+
+def main():
+    path = os.path.join(HERE, "edge_tp_gen.inc")
+    text = generate()
+    old = open(path).read() if os.path.exists(path) else None
+    if old != text:
+        with open(path, "w") as f:
+            f.write(text)
+    return path
+
+
+if __name__ == "__main__":
+    print(main())

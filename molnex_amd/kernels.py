@@ -13,6 +13,7 @@ Ops
 ``molix::spherical_harmonics``  real SH l <= 3 (``cuet.SphericalHarmonics``)
 ``molix::edge_csr``             receiver CSR of an (E, 2) edge list
 ``molix::tp_scatter``           channelwise TP + scatter-sum (``cuet.ChannelWiseTensorProduct``)
+``molix::edge_tp``              per-edge channelwise TP with shared weights, no scatter (Allegro's layer product)
 ``molix::radial_hidden``        fused hidden stack of the radial weight MLP (gradient w.r.t. its input)
 ``molix::edge_weights``         output layer of the radial weight MLP (per-edge TP weights), near-fp32 split-fp16 MFMA
 ``molix::bond_vectors``         pos[receiver] - pos[sender] - shift per edge, with its position gradient
@@ -402,6 +403,82 @@ def _tp_backward(ctx, grad_out):
 
 
 tp_scatter.register_autograd(_tp_backward, setup_context=_tp_setup)
+
+
+def edge_tp_supported(config: int, channels: int) -> bool:
+    """Whether ``molix::edge_tp`` has a kernel for this configuration and channel count."""
+    return config >= 0 and _lib.load().mnx_edge_tp_bwd_workspace_bytes(config, channels, 1) > 0
+
+
+@torch.library.custom_op("molix::edge_tp", mutates_args=(), device_types="cuda")
+def edge_tp(x: Tensor, Y: Tensor, w: Tensor, config: int, channels: int) -> Tensor:
+    """``out[e] = TP(x[e], Y[e]; w)``: per-edge channelwise product with weights shared by all
+    edges (``w`` is ``(num_paths, C)``), no scatter -- Allegro's layer product
+    (src/molzoo/allegro.py:352-359,457-458)."""
+    _require_gpu("edge_tp", x, Y, w)
+    num_paths, nx, ny, no = tp_config_info(config)
+    E = Y.shape[0]
+    xs = _f32_rows(x, nx * channels, "x")
+    Ys = _f32_rows(Y, ny, "Y")
+    ws_ = _f32_rows(w, channels, "w")
+    if xs.shape[0] != E or ws_.shape[0] != num_paths:
+        raise ValueError("edge_tp: x must be (E, NX*C) and w (num_paths, C)")
+    out = torch.empty((E, no * channels), dtype=torch.float32, device=xs.device)
+    check(_lib.load().mnx_edge_tp_fwd_f32(config, channels, ptr(xs), ptr(Ys), ptr(ws_), E, ptr(out), _stream(xs)),
+          "edge_tp")
+    return out
+
+
+@edge_tp.register_fake
+def _(x, Y, w, config, channels):
+    num_paths, nx, ny, no = tp_config_info(config)
+    return x.new_empty((Y.shape[0], no * channels))
+
+
+@torch.library.custom_op("molix::edge_tp_backward", mutates_args=(), device_types="cuda")
+def edge_tp_backward(grad_out: Tensor, x: Tensor, Y: Tensor, w: Tensor, config: int, channels: int,
+                     need_x: bool, need_Y: bool, need_w: bool) -> tuple[Tensor, Tensor, Tensor]:
+    """Gradients of ``<grad_out, edge_tp(...)>`` w.r.t. x, Y and the shared w (empty when not
+    needed); the weight gradient is summed over edges in a fixed order."""
+    lib = _lib.load()
+    num_paths, nx, ny, no = tp_config_info(config)
+    E = Y.shape[0]
+    xs = _f32_rows(x, nx * channels, "x")
+    Ys = _f32_rows(Y, ny, "Y")
+    wss = _f32_rows(w, channels, "w")
+    go = _f32_rows(grad_out, no * channels, "grad_out")
+    gx = torch.empty_like(xs) if need_x else xs.new_empty(0)
+    gY = torch.empty_like(Ys) if need_Y else Ys.new_empty(0)
+    gw = torch.empty_like(wss) if need_w else wss.new_empty(0)
+    ws = _ws(max(int(lib.mnx_edge_tp_bwd_workspace_bytes(config, channels, E)), 1), xs.device)
+    check(lib.mnx_edge_tp_bwd_f32(config, channels, ptr(xs), ptr(Ys), ptr(wss), ptr(go), E,
+                                  ptr(gx) if need_x else None, ptr(gY) if need_Y else None,
+                                  ptr(gw) if need_w else None, ptr(ws), ws.numel(), _stream(xs)),
+          "edge_tp backward")
+    return gx, gY, gw
+
+
+@edge_tp_backward.register_fake
+def _(grad_out, x, Y, w, config, channels, need_x, need_Y, need_w):
+    return (torch.empty_like(x) if need_x else x.new_empty(0), torch.empty_like(Y) if need_Y else Y.new_empty(0),
+            torch.empty_like(w) if need_w else w.new_empty(0))
+
+
+def _etp_setup(ctx, inputs, output):
+    x, Y, w, config, channels = inputs
+    ctx.save_for_backward(x, Y, w)
+    ctx.config, ctx.channels = config, channels
+
+
+def _etp_backward(ctx, grad_out):
+    x, Y, w = ctx.saved_tensors
+    nx, nY, nw = ctx.needs_input_grad[:3]
+    gx, gY, gw = edge_tp_backward(grad_out.contiguous(), x, Y, w, ctx.config, ctx.channels, nx, nY, nw)
+    return (gx.reshape(x.shape) if nx else None, gY.reshape(Y.shape) if nY else None,
+            gw.reshape(w.shape) if nw else None, None, None)
+
+
+edge_tp.register_autograd(_etp_backward, setup_context=_etp_setup)
 
 
 # ---------------------------------------------------------------------------

@@ -1,0 +1,264 @@
+"""Allegro edge encoder (src/molzoo/allegro.py:1-642) on the HIP kernels.
+
+Same classes, constructor arguments, attribute names (``embedding.{radial_basis, cutoff_fn,
+spherical_harmonics, type_embedding, scalar_mlp, tensor_env}``, ``layers.i.{tp, tp_linear,
+env_embed, latent_mlp, tensor_env}``), in/out keys and output ``(n_edges, num_layers,
+num_scalar_features)`` as the reference.
+
+The layer product ``TP(env_w . V_ij, Y_agg(src))`` (allegro.py:352-359,457-458, a
+``cuet.ChannelWiseTensorProduct`` with shared internal weights) runs as ``molix::edge_tp``: one
+HIP kernel per direction, lanes holding (edge, channel) pairs so that the 8-16 channels Allegro
+uses still fill a 64-wide wavefront.  Its projection (allegro.py:363-367,
+``cuet.Linear(tp.irreps_out, irreps_in)``) connects only output blocks whose irrep is an input
+irrep, so only those paths are computed; the weight keeps one entry per path of the full product,
+in the reference's order, and the unused entries receive zero gradient as they do there.  The
+projection runs in the HIP block-linear kernel over the edges.  Because every irrep block of the
+tensor track has the same multiplicity, the ir_mul features are ``[sum_l (2l+1)][channel]`` and the
+per-channel scalings are one broadcast multiply.
+"""
+
+from __future__ import annotations
+
+import math
+
+import torch
+import torch.nn as nn
+from pydantic import BaseModel, ConfigDict, Field
+
+from .. import kernels as K
+from ..config import config
+from ..irreps import Irreps
+from ..molrep.embedding.angular import SphericalHarmonics
+from ..molrep.embedding.cutoff import PolynomialCutoff
+from ..molrep.embedding.radial import BesselRBF
+from ..molrep.interaction.linear import Linear
+from ..molrep.interaction.tensor_product import irreps_from_l_max, sh_irreps_from_l_max
+from .mace import _get, _set
+
+
+def _env_weight_harmonics(edge_angular, env_weights, l_max, num_tensor_features, irreps_dim):
+    """``Y_lm(e) * env(e, c)`` in ir_mul order (allegro.py:55-97): with uniform multiplicity the
+    layout is ``[m over all l][c]``, an outer product per edge."""
+    E = edge_angular.shape[0]
+    out = edge_angular.unsqueeze(-1) * env_weights.unsqueeze(-2)
+    return out.reshape(E, irreps_dim)
+
+
+def _scale_by_channel(tensor, scale, l_max, num_tensor_features):
+    """Scale every component of channel ``c`` by ``scale[e, c]`` (allegro.py:100-130)."""
+    E = tensor.shape[0]
+    return (tensor.reshape(E, -1, num_tensor_features) * scale.unsqueeze(-2)).reshape(E, -1)
+
+
+def _full_paths(in_irreps: Irreps, sh_irreps: Irreps):
+    """(l1, l2, l3, parity) of every path of the unfiltered channelwise product, in the weight
+    order of cuet.ChannelWiseTensorProduct (input block, harmonics block, l3 ascending)."""
+    paths = []
+    for b1 in in_irreps:
+        for b2 in sh_irreps:
+            for l3 in range(abs(b1.ir.l - b2.ir.l), b1.ir.l + b2.ir.l + 1):
+                paths.append((b1.ir.l, b2.ir.l, l3, b1.ir.p * b2.ir.p))
+    return paths
+
+
+class EdgeChannelWiseTensorProduct(nn.Module):
+    """Per-edge channelwise product ``F x (0..l_max) (x) (0..l_max)`` with one weight per path and
+    channel shared by all edges (``shared_weights=True, internal_weights=True``).  ``irreps_out``
+    lists the blocks the Allegro projection reads: the paths whose output irrep is an input irrep,
+    sorted by irrep (stable in path order)."""
+
+    def __init__(self, irreps_in, irreps_sh, *, dtype=None):
+        super().__init__()
+        self.irreps_in1 = Irreps(irreps_in)
+        self.irreps_in2 = Irreps(irreps_sh)
+        muls = {b.mul for b in self.irreps_in1}
+        if len(muls) != 1:
+            raise ValueError("EdgeChannelWiseTensorProduct needs one multiplicity for every input block")
+        self.channels = muls.pop()
+        ls = [b.ir.l for b in self.irreps_in1]
+        if ls != list(range(len(ls))) or [b.ir.l for b in self.irreps_in2] != ls:
+            raise ValueError("EdgeChannelWiseTensorProduct: input and harmonics must be l = 0..l_max, in order")
+        full = _full_paths(self.irreps_in1, self.irreps_in2)
+        kept_irreps = {(b.ir.l, b.ir.p) for b in self.irreps_in1}
+        kept = [k for k, (l1, l2, l3, p) in enumerate(full) if (l3, p) in kept_irreps]
+        self.num_paths_full = len(full)
+        self.weight_numel = len(full) * self.channels
+        self.register_buffer("kept_paths", torch.tensor(kept, dtype=torch.long), persistent=False)
+        self.config_id = K.tp_config_id(ls, ls, ls)
+        if self.config_id < 0 or not K.edge_tp_supported(self.config_id, self.channels):
+            raise ValueError(f"no per-edge tensor-product kernel for l_max={ls[-1]}, {self.channels} channels")
+        num_paths, nx, ny, no = K.tp_config_info(self.config_id)
+        if num_paths != len(kept):
+            raise RuntimeError("compiled per-edge product does not match the path enumeration")
+        order = sorted(range(len(kept)), key=lambda i: (full[kept[i]][2], 0, i))
+        self.irreps_out = Irreps(" + ".join(
+            f"{self.channels}x{full[kept[i]][2]}{'e' if full[kept[i]][3] == 1 else 'o'}" for i in order))
+        if self.irreps_out.dim != no * self.channels:
+            raise RuntimeError("compiled per-edge product output size mismatch")
+        dt = dtype if dtype is not None else config.ftype
+        self.weight = nn.Parameter(torch.randn(1, self.weight_numel, dtype=dt))
+
+    def forward(self, x: torch.Tensor, y: torch.Tensor) -> torch.Tensor:
+        w = self.weight.reshape(self.num_paths_full, self.channels).index_select(0, self.kept_paths)
+        return K.edge_tp(x, y, w, self.config_id, self.channels)
+
+
+class PairEmbedding(nn.Module):
+    """Two-body embedding on edges (allegro.py:137-249): Bessel x polynomial-cutoff radial
+    features, harmonics, concatenated source / destination type embeddings -> scalar MLP ->
+    per-channel environment weights -> initial tensor features."""
+
+    def __init__(self, *, num_elements: int, num_scalar_features: int, num_tensor_features: int, r_max: float,
+                 num_bessel: int = 8, l_max: int = 2, type_emb_dim: int = 16,
+                 scalar_mlp_hiddens: list[int] | None = None, poly_p: int = 6):
+        super().__init__()
+        self.num_scalar_features = num_scalar_features
+        self.num_tensor_features = num_tensor_features
+        self.l_max = l_max
+        self.radial_basis = BesselRBF(r_cut=r_max, num_radial=num_bessel)
+        self.cutoff_fn = PolynomialCutoff(r_cut=r_max, exponent=poly_p)
+        self.spherical_harmonics = SphericalHarmonics(l_max=l_max)
+        self.type_embedding = nn.Embedding(num_elements, type_emb_dim, dtype=config.ftype)
+        widths = [num_bessel + 2 * type_emb_dim]
+        widths += list(scalar_mlp_hiddens) if scalar_mlp_hiddens is not None else [num_scalar_features] * 2
+        widths.append(num_scalar_features)
+        layers: list[nn.Module] = []
+        for a, b in zip(widths[:-1], widths[1:]):
+            layers += [nn.Linear(a, b, dtype=config.ftype), nn.SiLU()]
+        self.scalar_mlp = nn.Sequential(*layers)
+        self.irreps_dim = Irreps(irreps_from_l_max(l_max, num_tensor_features)).dim
+        self.tensor_env = nn.Linear(num_scalar_features, num_tensor_features, dtype=config.ftype)
+
+    def forward(self, Z, bond_dist, bond_diff, edge_index):
+        src, dst = edge_index[:, 0], edge_index[:, 1]
+        edge_cutoff = self.cutoff_fn(bond_dist)
+        edge_radial = self.radial_basis(bond_dist) * edge_cutoff.unsqueeze(-1)
+        edge_angular = self.spherical_harmonics(bond_diff / (bond_dist.unsqueeze(-1) + 1e-8))
+        type_embed = torch.cat([self.type_embedding(Z[src]), self.type_embedding(Z[dst])], dim=-1)
+        scalar_features = self.scalar_mlp(torch.cat([edge_radial, type_embed], dim=-1))
+        env_weights = self.tensor_env(scalar_features)
+        tensor_features = _env_weight_harmonics(edge_angular, env_weights, self.l_max, self.num_tensor_features,
+                                                self.irreps_dim)
+        return scalar_features, tensor_features, edge_angular, edge_cutoff
+
+
+class AllegroLayer(nn.Module):
+    """One Allegro layer (allegro.py:252-480): env-scaled tensor track (x) neighbourhood-aggregated
+    harmonics of the edge's source, projection back to the tensor irreps, latent MLP on
+    ``[scalars, fresh invariants]`` with the residual ``a x + b MLP``, output env scaling."""
+
+    def __init__(self, *, num_scalar_features: int, num_tensor_features: int, l_max: int = 2,
+                 latent_mlp_hiddens: list[int] | None = None, latent_activation: type[nn.Module] | None = nn.SiLU,
+                 avg_num_neighbors: float | None = None, residual_alpha: float = 0.5):
+        super().__init__()
+        self.num_scalar_features = num_scalar_features
+        self.num_tensor_features = num_tensor_features
+        self.l_max = l_max
+        self.avg_num_neighbors = float(avg_num_neighbors) if avg_num_neighbors is not None else None
+        irreps = irreps_from_l_max(l_max, num_tensor_features)
+        sh_irreps = sh_irreps_from_l_max(l_max)
+        self.tp = EdgeChannelWiseTensorProduct(irreps, sh_irreps, dtype=config.ftype)
+        self.tp_linear = Linear(self.tp.irreps_out, irreps, dtype=config.ftype)
+        self.env_embed = nn.Linear(num_scalar_features, num_tensor_features, dtype=config.ftype)
+        widths = [num_scalar_features + num_tensor_features] + (list(latent_mlp_hiddens) if latent_mlp_hiddens else [])
+        layers: list[nn.Module] = []
+        for a, b in zip(widths[:-1], widths[1:]):
+            layers.append(nn.Linear(a, b, dtype=config.ftype))
+            if latent_activation is not None:
+                layers.append(latent_activation())
+        layers.append(nn.Linear(widths[-1], num_scalar_features, dtype=config.ftype))
+        self.latent_mlp = nn.Sequential(*layers)
+        self.tensor_env = nn.Linear(num_scalar_features, num_tensor_features, dtype=config.ftype)
+        norm = math.sqrt(1.0 + float(residual_alpha) ** 2)
+        self.residual_a = 1.0 / norm
+        self.residual_b = float(residual_alpha) / norm
+        self.irreps_dim = Irreps(irreps).dim
+        self._sh_dim = Irreps(sh_irreps).dim
+
+    def forward(self, scalar_features, tensor_features, edge_angular, edge_index, n_nodes: int):
+        F = self.num_tensor_features
+        src = edge_index[:, 0]
+        scaled_V = _scale_by_channel(tensor_features, self.env_embed(scalar_features), self.l_max, F)
+        node_Y = torch.zeros(n_nodes, self._sh_dim, dtype=tensor_features.dtype, device=tensor_features.device)
+        node_Y = node_Y.index_add(0, src, edge_angular)
+        if self.avg_num_neighbors is not None:
+            node_Y = node_Y / math.sqrt(self.avg_num_neighbors)
+        else:
+            count = torch.zeros(n_nodes, dtype=tensor_features.dtype, device=tensor_features.device)
+            count = count.index_add(0, src, torch.ones_like(src, dtype=tensor_features.dtype))
+            node_Y = node_Y / count.clamp(min=1.0).sqrt().unsqueeze(-1)
+        new_tensor = self.tp_linear(self.tp(scaled_V, node_Y[src]))
+        combined = torch.cat([scalar_features, new_tensor[:, :F]], dim=-1)
+        updated = self.residual_a * scalar_features + self.residual_b * self.latent_mlp(combined)
+        return updated, _scale_by_channel(new_tensor, self.tensor_env(updated), self.l_max, F)
+
+
+class AllegroSpec(BaseModel):
+    """Configuration of the Allegro encoder (allegro.py:487-503)."""
+
+    model_config = ConfigDict(arbitrary_types_allowed=True)
+
+    num_elements: int = Field(..., gt=0)
+    num_scalar_features: int = Field(64, gt=0)
+    num_tensor_features: int = Field(16, gt=0)
+    r_max: float = Field(..., gt=0.0)
+    num_bessel: int = Field(8, gt=0)
+    l_max: int = Field(2, ge=0)
+    num_layers: int = Field(2, gt=0)
+    poly_p: int = Field(6, ge=1)
+    scalar_mlp_hiddens: list[int] | None = None
+    latent_mlp_hiddens: list[int] | None = None
+    avg_num_neighbors: float | None = None
+    residual_alpha: float = 0.5
+
+
+class Allegro(nn.Module):
+    """Allegro equivariant edge encoder (allegro.py:506-642): pair embedding, ``num_layers``
+    Allegro layers, per-layer scalars times the cutoff envelope stacked into
+    ``edges.edge_features (n_edges, num_layers, num_scalar_features)``.  ``forward`` takes the
+    reference's GraphBatch (any mapping answering ``td["edges", "bond_dist"]`` or
+    ``td["edges"]["bond_dist"]``) or keyword tensors (then returns the features)."""
+
+    in_keys = [("atoms", "Z"), ("edges", "edge_index"), ("edges", "bond_diff"), ("edges", "bond_dist")]
+    out_keys = [("edges", "edge_features")]
+
+    def __init__(self, *, num_elements: int, num_scalar_features: int = 64, num_tensor_features: int = 16,
+                 r_max: float, num_bessel: int = 8, l_max: int = 2, num_layers: int = 2, poly_p: int = 6,
+                 scalar_mlp_hiddens: list[int] | None = None, latent_mlp_hiddens: list[int] | None = None,
+                 latent_activation: type[nn.Module] | None = nn.SiLU, avg_num_neighbors: float | None = None,
+                 residual_alpha: float = 0.5):
+        super().__init__()
+        self.config = AllegroSpec(num_elements=num_elements, num_scalar_features=num_scalar_features,
+                                  num_tensor_features=num_tensor_features, r_max=r_max, num_bessel=num_bessel,
+                                  l_max=l_max, num_layers=num_layers, poly_p=poly_p,
+                                  scalar_mlp_hiddens=scalar_mlp_hiddens, latent_mlp_hiddens=latent_mlp_hiddens,
+                                  avg_num_neighbors=avg_num_neighbors, residual_alpha=residual_alpha)
+        self.embedding = PairEmbedding(num_elements=num_elements, num_scalar_features=num_scalar_features,
+                                       num_tensor_features=num_tensor_features, r_max=r_max, num_bessel=num_bessel,
+                                       l_max=l_max, scalar_mlp_hiddens=scalar_mlp_hiddens, poly_p=poly_p)
+        self.layers = nn.ModuleList([
+            AllegroLayer(num_scalar_features=num_scalar_features, num_tensor_features=num_tensor_features,
+                         l_max=l_max, latent_mlp_hiddens=latent_mlp_hiddens, latent_activation=latent_activation,
+                         avg_num_neighbors=avg_num_neighbors, residual_alpha=residual_alpha)
+            for _ in range(num_layers)
+        ])
+
+    def encode(self, Z, bond_dist, bond_diff, edge_index):
+        scalars, tensors, edge_angular, edge_cutoff = self.embedding(Z, bond_dist, bond_diff, edge_index)
+        u = edge_cutoff.unsqueeze(-1)
+        per_layer = []
+        for layer in self.layers:
+            scalars, tensors = layer(scalars, tensors, edge_angular, edge_index, int(Z.shape[0]))
+            per_layer.append(scalars * u)
+        return torch.stack(per_layer, dim=1)
+
+    def forward(self, td=None, *, Z=None, bond_dist=None, bond_diff=None, edge_index=None):
+        if td is None:
+            return self.encode(Z, bond_dist, bond_diff, edge_index)
+        feats = self.encode(_get(td, "atoms", "Z"), _get(td, "edges", "bond_dist"), _get(td, "edges", "bond_diff"),
+                            _get(td, "edges", "edge_index"))
+        _set(td, "edges", "edge_features", feats)
+        return td
+
+
+__all__ = ["Allegro", "AllegroLayer", "AllegroSpec", "EdgeChannelWiseTensorProduct", "PairEmbedding"]

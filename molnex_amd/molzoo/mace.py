@@ -44,6 +44,9 @@ def _get(td, group: str, key: str):
 
 
 def _set(td, group: str, key: str, value):
+    if isinstance(td, dict):  # nested plain mappings: a tuple key would be stored as such
+        td[group][key] = value
+        return
     try:
         td[group, key] = value
     except (KeyError, TypeError):

@@ -1,0 +1,112 @@
+"""Allegro encoder on the HIP kernels (molzoo.allegro) vs its fp64 restatement
+(oracle/allegro_ref.py), plus the reference's own module checks
+(tests/test_molzoo/test_allegro.py: shapes, encoder contract, rotation invariance, compile).
+
+Tolerance: edge features and forces (-d/dpos of a fixed linear readout of the features) within
+1e-5 norm-wise relative error of float64.
+"""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import allegro_ref as AR
+from oracle import equivariant as EQ
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _system(n=40, rc=5.0, seed=0, box=9.0):
+    g = torch.Generator().manual_seed(seed)
+    pos = torch.rand(n, 3, generator=g, dtype=torch.float64) * box
+    Z = torch.randint(0, 3, (n,), generator=g)
+    d = pos[None, :, :] - pos[:, None, :]
+    r = d.norm(dim=-1)
+    src, dst = torch.nonzero((r < rc) & (r > 0), as_tuple=True)
+    return pos, Z, torch.stack([src, dst], 1), rc
+
+
+def _geometry(pos, edge_index):
+    diff = pos[edge_index[:, 1]] - pos[edge_index[:, 0]]
+    return diff, diff.norm(dim=-1)
+
+
+def _rel(a, b):
+    a, b = a.detach().double().cpu(), b.detach().double().cpu()
+    return float((a - b).norm() / b.norm())
+
+
+def _model(l_max, F, S, layers, avg=None, seed=1):
+    from molnex_amd.molzoo.allegro import Allegro
+
+    torch.manual_seed(seed)
+    m = Allegro(num_elements=3, num_scalar_features=S, num_tensor_features=F, r_max=5.0, l_max=l_max,
+                num_layers=layers, avg_num_neighbors=avg)
+    cfg = dict(l_max=l_max, num_tensor_features=F, num_layers=layers, r_max=5.0, num_bessel=8, poly_p=6,
+               residual_alpha=0.5, avg_num_neighbors=avg)
+    return m, cfg
+
+
+@pytest.mark.parametrize("l_max,F,S,layers,avg", [(2, 8, 16, 3, None), (2, 16, 64, 2, 12.0), (1, 16, 32, 2, None),
+                                                  (3, 8, 16, 2, None)])
+def test_allegro_matches_fp64_oracle(l_max, F, S, layers, avg):
+    pos, Z, ei, rc = _system()
+    m, cfg = _model(l_max, F, S, layers, avg)
+    mg = m.to(DEV)
+    readout = torch.randn(layers, S, dtype=torch.float64, generator=torch.Generator().manual_seed(2))
+
+    pg = pos.float().to(DEV).requires_grad_(True)
+    diff, dist = _geometry(pg, ei.to(DEV))
+    feats = mg(Z=Z.to(DEV), bond_dist=dist, bond_diff=diff, edge_index=ei.to(DEV))
+    (fg,) = torch.autograd.grad((feats * readout.float().to(DEV)).sum(), pg)
+
+    p64 = pos.clone().requires_grad_(True)
+    diff64, dist64 = _geometry(p64, ei)
+    ref = AR.allegro_features(m.state_dict(), cfg, Z, dist64, diff64, ei)
+    (f64,) = torch.autograd.grad((ref * readout).sum(), p64)
+    assert feats.shape == ref.shape == (ei.shape[0], layers, S)
+    assert _rel(feats, ref) <= 1e-5, _rel(feats, ref)
+    assert _rel(fg, f64) <= 1e-5, _rel(fg, f64)
+
+
+def test_allegro_rotation_invariant_and_contract():
+    """Scalar edge features are invariant under a rotation of the positions (the reference checks
+    rtol = atol = 1e-4; fp32 here stays far inside), and the GraphBatch contract writes
+    ``edges.edge_features`` of shape (n_edges, num_layers, num_scalar)."""
+    pos, Z, ei, rc = _system(seed=3)
+    m, _ = _model(2, 8, 16, 3)
+    m = m.to(DEV)
+    R = torch.from_numpy(EQ.random_rotation(np.random.default_rng(4)))
+    td = {"atoms": {"Z": Z.to(DEV)}, "edges": {"edge_index": ei.to(DEV)}}
+    diff, dist = _geometry(pos.float().to(DEV), ei.to(DEV))
+    td["edges"]["bond_diff"], td["edges"]["bond_dist"] = diff, dist
+    base = m(td)["edges"]["edge_features"]
+    assert base.shape == (ei.shape[0], 3, 16)
+    diff_r, dist_r = _geometry((pos @ R.T).float().to(DEV), ei.to(DEV))
+    rot = m(Z=Z.to(DEV), bond_dist=dist_r, bond_diff=diff_r, edge_index=ei.to(DEV))
+    assert _rel(rot, base) <= 1e-5
+    assert torch.allclose(base, rot, rtol=1e-4, atol=1e-4)
+
+
+def test_allegro_layer_shapes_and_compile():
+    from molnex_amd.molzoo.allegro import AllegroLayer, PairEmbedding
+
+    pos, Z, ei, rc = _system(seed=5)
+    diff, dist = _geometry(pos.float().to(DEV), ei.to(DEV))
+    torch.manual_seed(0)
+    emb = PairEmbedding(num_elements=3, num_scalar_features=16, num_tensor_features=8, r_max=5.0, l_max=2).to(DEV)
+    s, t, ang, cut = emb(Z.to(DEV), dist, diff, ei.to(DEV))
+    E = ei.shape[0]
+    assert s.shape == (E, 16) and t.shape == (E, emb.irreps_dim) and ang.shape == (E, 9) and cut.shape == (E,)
+    # the reference's polynomial in fp32 (same arithmetic here) cancels to about -2e-6 just inside
+    # r_cut (x = 0.999); it is exactly 0 from r_cut on
+    assert bool((cut >= -1e-5).all()) and bool((cut <= 1).all())
+    layer = AllegroLayer(num_scalar_features=16, num_tensor_features=8, l_max=2).to(DEV)
+    s2, t2 = layer(s, t, ang, ei.to(DEV), Z.shape[0])
+    assert s2.shape == s.shape and t2.shape == t.shape
+    compiled = torch.compile(layer, fullgraph=False)
+    s3, t3 = compiled(s, t, ang, ei.to(DEV), Z.shape[0])
+    assert _rel(s3, s2) <= 1e-6 and _rel(t3, t2) <= 1e-6
