@@ -45,9 +45,10 @@ def parse():
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--unsorted", action="store_true", help="keep atoms in random order (no spatial sort)")
     p.add_argument("--seed", type=int, default=0)
-    p.add_argument("--workload", choices=["tp", "full", "sc", "nl", "pme", "train"], default="tp",
+    p.add_argument("--workload", choices=["tp", "full", "sc", "nl", "pme", "train", "allegro"], default="tp",
                    help="tp: config 3 edge step (default, the headline line); full: config 5 energy + forces; "
-                        "sc / nl / pme: config 4, config 2, config 5's PME term alone")
+                        "sc / nl / pme: config 4, config 2, config 5's PME term alone; train: config 5 "
+                        "force-matching training step; allegro: Allegro energy + forces on the 50k-atom graph")
     p.add_argument("--no-secondary", action="store_true",
                    help="skip the secondary figures (config 2 neighbor list, config 5 energy + forces)")
     p.add_argument("--literal", action="store_true",
@@ -538,6 +539,81 @@ def sc_bench(dev, reps=10):
             "flops_per_node_channel": {"fwd": ff, "bwd": fb}}
 
 
+def allegro_bench(args, dev, steps=5, warmup=2, reps=5):
+    """Allegro encoder (src/molzoo/allegro.py, reference defaults: 64 scalar / 16 tensor channels,
+    l_max 2, 2 layers) on the config-3/5 graph (50k atoms, periodic, rc 5 A): edge features, a
+    fixed linear readout summed to an energy, forces by one backward to the positions.  Also the
+    molix::edge_tp kernels at the layer's shape, HIP events on the current stream; algorithmic bytes
+    per edge forward 4 (NX + NO) C + 4 NY, backward 4 (2 NX + NO) C + 8 NY (x, Y, out / grad once)."""
+    import molnex_amd.kernels as K
+    from molnex_amd.molzoo.allegro import Allegro
+
+    n = args.atoms
+    L = (n / 0.1) ** (1.0 / 3.0)
+    g = torch.Generator().manual_seed(args.seed)
+    pos = lattice_positions(n, L, g).to(dev)
+    Z = torch.randint(0, 10, (n,), generator=g).to(dev)
+    box = torch.eye(3, device=dev) * L
+    i, j, shifts, _, _ = torch.ops.molix.neighbor_list(pos, 5.0, box, True)
+    edge_index = torch.stack([j.long(), i.long()], 1)
+    E = int(edge_index.shape[0])
+    torch.manual_seed(args.seed)
+    enc = Allegro(num_elements=10, num_scalar_features=64, num_tensor_features=16, r_max=5.0, l_max=2,
+                  num_layers=2, avg_num_neighbors=E / n).to(dev)
+    for p in enc.parameters():
+        p.requires_grad_(False)
+    readout = torch.randn(2, 64, device=dev) / 8
+
+    def step():
+        p = pos.detach().clone().requires_grad_(True)
+        bond_diff = torch.ops.molix.bond_vectors(p, edge_index, shifts)
+        bond_dist = bond_diff.norm(dim=-1).clamp(min=1e-6)
+        feats = enc(Z=Z, bond_dist=bond_dist, bond_diff=bond_diff, edge_index=edge_index)
+        e = (feats * readout).sum()
+        (f,) = torch.autograd.grad(e, p)
+        return e, -f
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        e, f = step()
+    torch.cuda.synchronize()
+    dt = (time.perf_counter() - t0) / steps
+    finite = bool(torch.isfinite(f).all())
+    tp = enc.layers[0].tp
+    P, NX, NY, NO = K.tp_config_info(tp.config_id)
+    C = tp.channels
+    x = torch.randn(E, NX * C, device=dev)
+    Y = torch.randn(E, NY, device=dev)
+    w = torch.randn(P, C, device=dev)
+    gout = torch.randn(E, NO * C, device=dev)
+    fwd, bwd = [], []
+    for r in range(reps + 1):
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
+        ev[0].record()
+        K.edge_tp(x, Y, w, tp.config_id, C)
+        ev[1].record()
+        ev[2].record()
+        K.edge_tp_backward(gout, x, Y, w, tp.config_id, C, True, True, True)
+        ev[3].record()
+        if r:
+            fwd.append(ev[:2])
+            bwd.append(ev[2:])
+    torch.cuda.synchronize()
+    tf = sum(a.elapsed_time(b) for a, b in fwd) / reps
+    tb = sum(a.elapsed_time(b) for a, b in bwd) / reps
+    bf = E * (4 * (NX + NO) * C + 4 * NY)
+    bb = E * (4 * (2 * NX + NO) * C + 8 * NY)
+    return {"workload": "Allegro (64 scalar / 16 tensor ch, l_max 2, 2 layers) on 50k atoms, rc 5 A, energy + forces",
+            "edges": E, "ms_per_step": round(dt * 1e3, 3), "M_edges_per_s": round(E / dt / 1e6, 2),
+            "forces_finite": finite, "edge_tp_fwd_ms": round(tf, 3), "edge_tp_bwd_ms": round(tb, 3),
+            "edge_tp_fwd_GBs": round(bf / tf / 1e6, 1), "edge_tp_bwd_GBs": round(bb / tb / 1e6, 1),
+            "edge_tp_fwd_hbm_frac": round(bf / tf / 1e6 / HBM_PEAK_GBS, 4),
+            "edge_tp_bwd_hbm_frac": round(bb / tb / 1e6 / HBM_PEAK_GBS, 4)}
+
+
 def secondary_figures(args, dev):
     sc = sc_bench(dev)
     nl = nlist_bench(dev)
@@ -551,6 +627,8 @@ def secondary_figures(args, dev):
                     "hbm_frac": full["roofline"]["frac"], "algorithmic_GB": round(full["roofline"]["algorithmic_bytes"] / 1e9, 2)}
         torch.cuda.empty_cache()
     out["config5_literal_training_step"] = train_step_bench(args, dev)
+    torch.cuda.empty_cache()
+    out["allegro_energy_forces"] = allegro_bench(args, dev)
     torch.cuda.empty_cache()
     return out
 
@@ -570,6 +648,10 @@ def main():
         out = train_step_bench(args, dev, steps=args.steps, warmup=args.warmup)
         out["peak_GB"] = round(torch.cuda.max_memory_allocated() / 1e9, 1)
         print(json.dumps(out), flush=True)
+        return
+    if args.workload == "allegro":
+        print(json.dumps(allegro_bench(args, torch.device("cuda:0"), steps=args.steps, warmup=args.warmup)),
+              flush=True)
         return
     if args.workload in ("sc", "nl", "pme"):
         import molnex_amd.kernels  # noqa: F401
