@@ -51,7 +51,7 @@ int etp_check(int32_t config, int32_t C, int64_t E, int* variant) {
     *variant = etp_variant(C);
     if (*variant < 0)
         return set_error(MNX_ERR_UNSUPPORTED, "edge tensor product: %d channels (8, 16, 32, 64 or 128 compiled)", C);
-    MNX_REQUIRE(E >= 0 && E < (int64_t(1) << 40), "edge count out of range");
+    MNX_REQUIRE(E >= 0 && E < (int64_t(1) << 33), "edge count out of range");  // forward grid < 2^31 blocks
     return MNX_OK;
 }
 
