@@ -15,6 +15,7 @@ namespace {
 
 struct ETPInfo {
     int ok, np, nx, ny, no;
+    int fwd_groups;  // edge groups per forward wavefront
 };
 
 typedef void (*ETPFwdFn)(const float*, const float*, const float*, int64_t, int, float*);
@@ -26,13 +27,23 @@ typedef void (*ETPBwdFn)(const float*, const float*, const float*, const float*,
 constexpr int kETPThreads = 256;   // four wavefronts
 constexpr int kETPBwdWaves = 2048; // wavefronts of the backward grid (grid-stride over edges)
 
-// Sums the per-wavefront weight-gradient partials in a fixed order.
-__global__ void k_etp_reduce(const float* __restrict__ part, int64_t nparts, int64_t n, float* __restrict__ gw) {
-    const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
-    if (i >= n) return;
+constexpr int kETPReduceThreads = 256;
+
+// Sums the per-wavefront weight-gradient partials in a fixed order: one workgroup per output
+// value, each thread a fixed strided subset of the partials, then a fixed tree in LDS.
+__global__ void __launch_bounds__(kETPReduceThreads) k_etp_reduce(const float* __restrict__ part, int64_t nparts,
+                                                                  int64_t n, float* __restrict__ gw) {
+    __shared__ float red[kETPReduceThreads];
+    const int64_t i = blockIdx.x;
     float s = 0.f;
-    for (int64_t b = 0; b < nparts; ++b) s += part[b * n + i];
-    gw[i] = s;
+    for (int64_t b = threadIdx.x; b < nparts; b += kETPReduceThreads) s += part[b * n + i];
+    red[threadIdx.x] = s;
+    __syncthreads();
+    for (int w = kETPReduceThreads / 2; w > 0; w >>= 1) {
+        if (threadIdx.x < w) red[threadIdx.x] += red[threadIdx.x + w];
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) gw[i] = red[0];
 }
 
 int etp_variant(int C) {
@@ -78,7 +89,7 @@ int mnx_edge_tp_fwd_f32(int32_t config, int32_t channels, const float* x, const 
     if (num_edges == 0) return MNX_OK;
     MNX_REQUIRE(x && Y && w && out, "null pointer argument");
     const int64_t G = 64 / kETPVariantCW[v];
-    const int64_t blocks = ceil_div(ceil_div(num_edges, G), kETPThreads / 64);
+    const int64_t blocks = ceil_div(ceil_div(num_edges, G * kETPInfo[config].fwd_groups), kETPThreads / 64);
     hipLaunchKernelGGL(kETPFwd[config][v], dim3(unsigned(blocks)), dim3(kETPThreads), 0, (hipStream_t)stream, x, Y,
                        w, num_edges, channels, out);
     MNX_CHECK_LAUNCH();
@@ -103,7 +114,7 @@ int mnx_edge_tp_bwd_f32(int32_t config, int32_t channels, const float* x, const 
     if (num_edges == 0) {
         if (grad_w) {
             // no edges: the weight gradient is zero (the reduction over no partials)
-            hipLaunchKernelGGL(k_etp_reduce, dim3(unsigned(ceil_div(nw, 256))), dim3(256), 0, s,
+            hipLaunchKernelGGL(k_etp_reduce, dim3(unsigned(nw)), dim3(kETPReduceThreads), 0, s,
                                static_cast<const float*>(nullptr), int64_t(0), nw, grad_w);
             MNX_CHECK_LAUNCH();
         }
@@ -119,7 +130,7 @@ int mnx_edge_tp_bwd_f32(int32_t config, int32_t channels, const float* x, const 
                        num_edges, channels, grad_x, grad_Y, part);
     MNX_CHECK_LAUNCH();
     if (grad_w) {
-        hipLaunchKernelGGL(k_etp_reduce, dim3(unsigned(ceil_div(nw, 256))), dim3(256), 0, s, part, waves, nw, grad_w);
+        hipLaunchKernelGGL(k_etp_reduce, dim3(unsigned(nw)), dim3(kETPReduceThreads), 0, s, part, waves, nw, grad_w);
         MNX_CHECK_LAUNCH();
     }
     return MNX_OK;

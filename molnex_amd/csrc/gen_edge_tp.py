@@ -36,6 +36,12 @@ from molnex_amd.csrc.gen_tp import EPS, Cfg, config_list, f32  # noqa: E402
 VARIANTS = ((8, 1), (16, 1), (32, 1), (64, 1), (64, 2))
 
 
+def fwd_groups(cfg: Cfg) -> int:
+    """Edge groups per forward wavefront, their loads all in flight before any arithmetic: 2 up to
+    l_max = 2 (1.99 -> 1.39 ms at l_max 2, C = 16, 2.6 M edges), 1 for l_max = 3 (registers)."""
+    return 2 if cfg.NX <= 9 else 1
+
+
 def supported(cfg: Cfg) -> bool:
     """Allegro's product: input, harmonics and kept outputs all l = 0 .. l_max."""
     return cfg.in_ls == cfg.sh_ls == cfg.out_ls
@@ -45,46 +51,58 @@ def _fwd(cfg: Cfg) -> str:
     L = []
     a = L.append
     NX, NY, NO, NP = cfg.NX, cfg.NY, cfg.NO, cfg.NP
+    EPW = fwd_groups(cfg)
     a(f"template <int CW, int CPL>\n__global__ void __launch_bounds__(256) etp_fwd_c{cfg.idx}("
       "const float* __restrict__ x, const float* __restrict__ Y, const float* __restrict__ w, int64_t E, int C, "
       "float* __restrict__ out) {")
     a("  constexpr int G = 64 / CW;")
-    a("  const int lane = threadIdx.x & 63;")
-    a("  const int64_t e = (int64_t(blockIdx.x) * 4 + (threadIdx.x >> 6)) * G + lane / CW;")
-    a("  if (e >= E) return;")
-    a("  const int c0 = lane % CW;")
-    a(f"  const float* __restrict__ Ye = Y + e * {NY};")
-    a("  " + " ".join(f"const float y{i} = Ye[{i}];" for i in range(NY)))
-    a(f"  const float* __restrict__ xe = x + e * ({NX} * int64_t(C));")
-    a(f"  float* __restrict__ oe = out + e * ({NO} * int64_t(C));")
+    a("  const int lane = threadIdx.x & 63, c0 = lane % CW;")
+    a(f"  const int64_t e0 = (int64_t(blockIdx.x) * 4 + (threadIdx.x >> 6)) * ({EPW} * G) + lane / CW;")
+    a(f"  // {EPW} edge groups per wavefront: every load of all of them issued before any arithmetic")
+    a(f"  float y[{EPW}][{NY}], xv[{EPW}][CPL][{NX}];")
     a("#pragma unroll")
-    a("  for (int k = 0; k < CPL; ++k) {")
-    a("    const int c = c0 + 64 * k;")
-    a(f"    float xv[{NX}];")
-    a(f"#pragma unroll\n    for (int i = 0; i < {NX}; ++i) xv[i] = xe[i * C + c];")
+    a(f"  for (int q = 0; q < {EPW}; ++q) {{")
+    a("    const int64_t e = e0 + q * G;")
+    a("    if (e >= E) break;")
+    a(f"    const float* __restrict__ Ye = Y + e * {NY};")
+    a(f"    const float* __restrict__ xe = x + e * ({NX} * int64_t(C));")
+    a(f"#pragma unroll\n    for (int i = 0; i < {NY}; ++i) y[q][i] = Ye[i];")
+    a("#pragma unroll")
+    a("    for (int k = 0; k < CPL; ++k)")
+    a(f"#pragma unroll\n      for (int i = 0; i < {NX}; ++i) xv[q][k][i] = xe[i * C + c0 + 64 * k];")
+    a("  }")
+    a("#pragma unroll")
+    a(f"  for (int q = 0; q < {EPW}; ++q) {{")
+    a("    const int64_t e = e0 + q * G;")
+    a("    if (e >= E) break;")
+    a(f"    float* __restrict__ oe = out + e * ({NO} * int64_t(C));")
+    a("#pragma unroll")
+    a("    for (int k = 0; k < CPL; ++k) {")
+    a("      const int c = c0 + 64 * k;")
     for j, p in enumerate(cfg.paths):
         cf = p["c"]
-        a("    {")
-        a(f"      const float wj = w[{j} * C + c];")
+        a("      {")
+        a(f"        const float wj = w[{j} * C + c];")
         for m3 in range(2 * p["l3"] + 1):
             row = []
             for m1 in range(2 * p["l1"] + 1):
                 terms = [(m2, cf[m1, m2, m3]) for m2 in range(2 * p["l2"] + 1) if abs(cf[m1, m2, m3]) > EPS]
                 if not terms:
                     continue
-                expr = f"{f32(terms[0][1])} * y{p['o2'] + terms[0][0]}"
+                expr = f"{f32(terms[0][1])} * y[q][{p['o2'] + terms[0][0]}]"
                 for m2, v in terms[1:]:
-                    expr = f"fmaf({f32(v)}, y{p['o2'] + m2}, {expr})"
+                    expr = f"fmaf({f32(v)}, y[q][{p['o2'] + m2}], {expr})"
                 row.append((m1, expr))
             o = p["o3"] + m3
             if not row:
-                a(f"      oe[{o} * C + c] = 0.f;")
+                a(f"        oe[{o} * C + c] = 0.f;")
                 continue
-            s = f"({row[0][1]}) * xv[{p['o1'] + row[0][0]}]"
+            s = f"({row[0][1]}) * xv[q][k][{p['o1'] + row[0][0]}]"
             for m1, expr in row[1:]:
-                s = f"fmaf({expr}, xv[{p['o1'] + m1}], {s})"
-            a(f"      oe[{o} * C + c] = wj * ({s});")
-        a("    }")
+                s = f"fmaf({expr}, xv[q][k][{p['o1'] + m1}], {s})"
+            a(f"        oe[{o} * C + c] = wj * ({s});")
+        a("      }")
+    a("    }")
     a("  }")
     a("}")
     return "\n".join(L)
@@ -202,7 +220,7 @@ def generate() -> str:
     out.append("static const int kETPVariantCPL[] = {" + ", ".join(str(v[1]) for v in VARIANTS) + "};")
     out.append("static const ETPInfo kETPInfo[] = {")
     for cfg in cfgs:
-        out.append(f"  {{{int(supported(cfg))}, {cfg.NP}, {cfg.NX}, {cfg.NY}, {cfg.NO}}},")
+        out.append(f"  {{{int(supported(cfg))}, {cfg.NP}, {cfg.NX}, {cfg.NY}, {cfg.NO}, {fwd_groups(cfg)}}},")
     out.append("};")
     for kind in ("fwd", "bwd"):
         typ = "ETPFwdFn" if kind == "fwd" else "ETPBwdFn"
