@@ -315,8 +315,9 @@ int mnx_bond_vectors_bwd_f32(const int64_t* edge_index, const float* grad_diff, 
 /* with respect to the edge features.  raw parameters: per layer W_j         */
 /* [hidden][in_j] (torch.nn.Linear layout) then b_j [hidden], contiguous;    */
 /* mnx_radial_pack_f32 rearranges them once into frag                        */
-/* [mnx_radial_frag_floats(...)] floats (16-byte aligned), which the fwd and */
-/* bwd kernels read.  feats [E][kin], h [E][hidden], grad_feats [E][kin]     */
+/* [mnx_radial_frag_floats(...)] floats (16-byte aligned; hidden layers as   */
+/* power-of-two row scales and two fp16 planes of the scaled weights, for    */
+/* near-fp32 split-fp16 products), which the fwd and bwd kernels read.  feats [E][kin], h [E][hidden], grad_feats [E][kin]     */
 /* (overwritten).  kin <= 64; hidden 32 or 64 with 1..4 layers, or 128 with  */
 /* 1..2 layers (else MNX_ERR_UNSUPPORTED; the size queries return -1).       */
 /* ------------------------------------------------------------------------ */

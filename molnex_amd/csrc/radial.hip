@@ -18,16 +18,18 @@
 // A-operand read is one conflict-free 16-byte LDS read per lane.
 //
 // Layers with K = hidden inputs (every layer but the first, forward and
-// backward) run on the bf16 matrix cores with fp32-accurate products: each
-// operand is split exactly into three bf16 parts (x0 = bf16(x), x1 = bf16(x -
-// x0), x2 = bf16(x - x0 - x1)) and the six partial products x_i y_j with
-// i + j <= 2 are accumulated in fp32 by v_mfma_f32_32x32x16_bf16 (the dropped
-// terms are below 2^-25 |x y|), at 3/8 of the matrix-core cycles of fp32
-// MFMAs.  The D layout feeds these layers too: bf16 k-step q of lane half h,
-// element j, is feature 16q + 8(j/4) + 4h + j%4, i.e. registers 8(q%2) .. +7 of
-// tile q/2.  The weights of these layers are pre-split into three bf16 planes,
-// layout [q][tile][plane][lane][8].  The first layer (K = the few radial
-// features) stays on fp32 MFMAs.
+// backward) run on the fp16 matrix cores with near-fp32 products: each edge's
+// activation column and each weight row are brought to a power-of-two scale
+// (largest magnitude in [1, 2)), every scaled value v is split into two fp16
+// parts, v0 = f16(v), v1 = f16(v - v0) (|v - v0 - v1| <= 2^-22 |v|), and the
+// three partial products w1 v0 + w0 v1 + w0 v0 are accumulated in fp32 by
+// v_mfma_f32_32x32x16_f16 (the dropped terms are below 3 * 2^-22 |w v|); the
+// scales are undone exactly on the accumulator.  The D layout feeds these
+// layers too: fp16 k-step q of lane half h, element j, is feature
+// 16q + 8(j/4) + 4h + j%4, i.e. registers 8(q%2) .. +7 of tile q/2.  The weights
+// of these layers are pre-scaled and pre-split into two fp16 planes, layout
+// [q][tile][plane][lane][8], with one scale per output row.  The first layer
+// (K = the few radial features) stays on fp32 MFMAs.
 
 #include "common.h"
 
@@ -36,26 +38,28 @@ namespace {
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 
 constexpr int kRadThreads = 256;  // four wavefronts, 32 edges each
 constexpr int kRadEdgesPerBlock = (kRadThreads / 64) * 32;
 constexpr int kRadMaxIn = 64;
 
 // Fragment buffer layout (floats): forward fragments of layers 0..L-1, backward
-// (transposed) fragments of layers 0..L-1, then the L x H biases.  Forward layer
-// 0 is fp32 ([tile][kp/8][lane][4]); every other block holds three bf16 planes,
-// [H/16][tiles][3][lane][8] (768 floats per k-step and tile).
-constexpr int kX3Block = 768;  // floats per (k-step, tile) of split-bf16 fragments
+// (transposed) fragments of layers 0..L-1, the L x H biases, then the row scales
+// of the split blocks (forward layers 1..L-1: H each; backward layers 0..L-1:
+// 32 * tiles_bwd(j) each; powers of two).  Forward layer 0 is fp32
+// ([tile][kp/8][lane][4]); every other block holds two fp16 planes,
+// [H/16][tiles][2][lane][8] (512 floats per k-step and tile).
+constexpr int kX2Block = 512;  // floats per (k-step, tile) of split-fp16 fragments
 
 struct RadLayout {
     int kin, kp, H, L;
     __host__ __device__ int tiles_bwd(int j) const { return ((j == 0 ? kp : H) + 31) / 32; }
     __host__ __device__ int64_t fwd_size(int j) const {
-        return j == 0 ? int64_t(H / 32) * (kp / 8) * 256 : int64_t(H / 32) * (H / 16) * kX3Block;
+        return j == 0 ? int64_t(H / 32) * (kp / 8) * 256 : int64_t(H / 32) * (H / 16) * kX2Block;
     }
-    __host__ __device__ int64_t bwd_size(int j) const { return int64_t(tiles_bwd(j)) * (H / 16) * kX3Block; }
+    __host__ __device__ int64_t bwd_size(int j) const { return int64_t(tiles_bwd(j)) * (H / 16) * kX2Block; }
     __host__ __device__ int64_t fwd_off(int j) const {
         int64_t o = 0;
         for (int i = 0; i < j; ++i) o += fwd_size(i);
@@ -67,32 +71,58 @@ struct RadLayout {
         return o;
     }
     __host__ __device__ int64_t bias_off() const { return bwd_off(L); }
-    __host__ __device__ int64_t total() const { return bias_off() + int64_t(L) * H; }
+    // row scales: forward layer j >= 1, backward layer j
+    __host__ __device__ int64_t fscale_off(int j) const { return bias_off() + int64_t(L) * H + int64_t(j - 1) * H; }
+    __host__ __device__ int64_t bscale_off(int j) const {
+        int64_t o = bias_off() + int64_t(L) * H + int64_t(L - 1) * H;
+        for (int i = 0; i < j; ++i) o += 32 * tiles_bwd(i);
+        return o;
+    }
+    __host__ __device__ int64_t scales_total() const { return int64_t(L - 1) * H + (bscale_off(L) - bscale_off(0)); }
+    __host__ __device__ int64_t total() const { return bscale_off(L); }
     // raw parameters: per layer W_j (H x K_j, row-major as torch.nn.Linear) then b_j (H)
     __host__ __device__ int64_t raw_w(int j) const { return j == 0 ? 0 : int64_t(H) * kin + H + int64_t(j - 1) * (H * H + H); }
     __host__ __device__ int64_t raw_b(int j) const { return raw_w(j) + int64_t(H) * (j == 0 ? kin : H); }
     __host__ __device__ int64_t raw_total() const { return raw_w(L); }
 };
 
-__device__ __forceinline__ void split3(float v, __bf16& b0, __bf16& b1, __bf16& b2) {
-    b0 = (__bf16)v;
-    float r = v - (float)b0;
-    b1 = (__bf16)r;
-    r -= (float)b1;
-    b2 = (__bf16)r;
+// Exponent e with 2^e <= m < 2^(e+1), clamped so that 2^e and 2^-e are normal; 0 for
+// m == 0 and for inf/NaN (left to propagate).
+__device__ __forceinline__ int rad_exp(float m) {
+    if (!(m > 0.f) || !(m <= 3.402823466e38f)) return 0;
+    return min(max(ilogbf(m), -126), 126);
 }
 
-__device__ __forceinline__ __bf16 split_part(float v, int p) {
-    __bf16 b0, b1, b2;
-    split3(v, b0, b1, b2);
-    return p == 0 ? b0 : (p == 1 ? b1 : b2);
+// Row scales of the split blocks, one thread per row: forward layer j >= 1 row m is
+// W_j[m][:], backward layer j row m is column m of W_j (W_j^T[m][:]); rows past the
+// layer (padding of the last tile) get 1.
+__global__ void k_radial_scales(const float* __restrict__ raw, RadLayout lay, float* __restrict__ frag) {
+    const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    const int64_t n = lay.scales_total();
+    if (i >= n) return;
+    const int64_t o = lay.fscale_off(1) + i;
+    float m = 0.f;
+    if (o < lay.bscale_off(0)) {  // forward layer j >= 1
+        const int j = 1 + int(i / lay.H), row = int(i % lay.H);
+        const float* W = raw + lay.raw_w(j);
+        for (int f = 0; f < lay.H; ++f) m = fmaxf(m, fabsf(W[int64_t(row) * lay.H + f]));
+    } else {
+        int j = 0;
+        while (o >= lay.bscale_off(j + 1)) ++j;
+        const int row = int(o - lay.bscale_off(j));
+        const int kraw = j == 0 ? lay.kin : lay.H;
+        const float* W = raw + lay.raw_w(j);
+        if (row < kraw)
+            for (int f = 0; f < lay.H; ++f) m = fmaxf(m, fabsf(W[int64_t(f) * kraw + row]));
+    }
+    frag[o] = ldexpf(1.f, rad_exp(m));
 }
 
-// Builds the fragment buffer from the raw parameters; one thread per float
-// (two bf16 values in the split blocks).
+// Builds the fragment buffer from the raw parameters and the row scales (already in
+// place); one thread per float (two fp16 values in the split blocks).
 __global__ void k_radial_pack(const float* __restrict__ raw, RadLayout lay, float* __restrict__ frag) {
     const int64_t idx = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
-    if (idx >= lay.total()) return;
+    if (idx >= lay.fscale_off(1)) return;
     float v = 0.f;
     if (idx >= lay.bias_off()) {
         const int64_t b = idx - lay.bias_off();
@@ -115,12 +145,13 @@ __global__ void k_radial_pack(const float* __restrict__ raw, RadLayout lay, floa
         const int kraw = j == 0 ? lay.kin : lay.H;  // layer j's input width
         const int tiles = bwd ? lay.tiles_bwd(j) : lay.H / 32;
         const float* W = raw + lay.raw_w(j);
-        bf16x2 pair;
+        const float* scale = frag + (bwd ? lay.bscale_off(j) : lay.fscale_off(j));
+        f16x2 pair;
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
-            const int64_t e = 2 * r + u;  // bf16 element within the block
-            const int j8 = int(e % 8), lane = int((e / 8) % 64), p = int((e / 512) % 3);
-            const int t = int((e / 1536) % tiles), q = int(e / (1536 * int64_t(tiles)));
+            const int64_t e = 2 * r + u;  // fp16 element within the block
+            const int j8 = int(e % 8), lane = int((e / 8) % 64), p = int((e / 512) % 2);
+            const int t = int((e / 1024) % tiles), q = int(e / (1024 * int64_t(tiles)));
             const int row = 32 * t + lane % 32;                                // A row
             const int f = 16 * q + 8 * (j8 / 4) + 4 * (lane / 32) + j8 % 4;  // contraction feature
             float w = 0.f;
@@ -129,7 +160,9 @@ __global__ void k_radial_pack(const float* __restrict__ raw, RadLayout lay, floa
             } else {
                 if (row < kraw && f < lay.H) w = W[int64_t(f) * kraw + row];   // W_j^T
             }
-            pair[u] = split_part(w, p);
+            w = ldexpf(w, -ilogbf(scale[row]));
+            const _Float16 h0 = (_Float16)w;
+            pair[u] = p == 0 ? h0 : (_Float16)(w - (float)h0);
         }
         v = __builtin_bit_cast(float, pair);
     }
@@ -155,7 +188,7 @@ __device__ __forceinline__ float silu_grad(float z) {
 // floats of one layer's fragments (whole output tiles) at a time and its four
 // wavefronts share them.
 constexpr int kRadChunk = 8192;       // floats (32 KB)
-constexpr int kRadChunkWide = 24576;  // floats (96 KB): a whole 128-wide layer, for the backward
+constexpr int kRadChunkWide = 16384;  // floats (64 KB): a whole 128-wide layer, for the backward
 
 template <int CH>
 struct RadSharedT {
@@ -171,18 +204,28 @@ __device__ __forceinline__ void stage(const float* __restrict__ src, int n, f32x
     for (int i = threadIdx.x; i < n / 4; i += kRadThreads) dst[i] = s4[i];
 }
 
-// acc[t] += W(tile t) . in over K = 16 * NQ features held in the D layout as
-// in[q/2][8(q%2) + j] for k-step q (split-bf16 products, see the top of the
-// file).  The layer's fragments f ([NQ][T][3][64 lanes][8 bf16]) are staged in
-// chunks of whole k-steps, so each k-step's activations are split once.  Every
-// wavefront of the workgroup must call it (barriers inside).
+// acc[t] = W(tile t) . in over K = 16 * NQ features held in the D layout as
+// in[q/2][8(q%2) + j] for k-step q (split-fp16 products, see the top of the file),
+// acc zero on entry.  The layer's fragments f ([NQ][T][2][64 lanes][8 fp16]) are
+// staged in chunks of whole k-steps; rscale holds the layer's row scales.  The
+// lane's activations are scaled by their edge's power of two (largest magnitude
+// of the column in [1, 2)) before the split and the result by its inverse and the
+// row scales.  Every wavefront of the workgroup must call it (barriers inside).
 template <int T, int NQ, class Sh>
-__device__ __forceinline__ void mfma_layer(const float* __restrict__ f, const float (&in)[NQ / 2][16],
-                                           f32x16 (&acc)[T], Sh& sh, int lane) {
+__device__ __forceinline__ void mfma_layer(const float* __restrict__ f, const float* __restrict__ rscale,
+                                           const float (&in)[NQ / 2][16], f32x16 (&acc)[T], Sh& sh, int lane) {
     constexpr int kRadChunk = Sh::kChunk;
-    constexpr int kStep = T * kX3Block;  // floats per k-step
+    constexpr int kStep = T * kX2Block;  // floats per k-step
     constexpr int kQPC = kRadChunk / kStep < NQ ? kRadChunk / kStep : NQ;  // k-steps per chunk
     static_assert(kQPC >= 1, "one k-step of fragments must fit the staging area");
+    float m = 0.f;
+#pragma unroll
+    for (int t = 0; t < NQ / 2; ++t)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) m = fmaxf(m, fabsf(in[t][r]));
+    m = fmaxf(m, __shfl_xor(m, 32));
+    const int ex = rad_exp(m);
+    const float sinv = ldexpf(1.f, -ex);
 #pragma unroll
     for (int q0 = 0; q0 < NQ; q0 += kQPC) {
         __syncthreads();
@@ -192,30 +235,33 @@ __device__ __forceinline__ void mfma_layer(const float* __restrict__ f, const fl
         for (int qq = 0; qq < kQPC; ++qq) {
             const int q = q0 + qq;
             if (q >= NQ) break;
-            bf16x8 b0, b1, b2;
+            f16x8 b0, b1;
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
-                __bf16 x0, x1, x2;
-                split3(in[q / 2][8 * (q % 2) + j], x0, x1, x2);
-                b0[j] = x0;
-                b1[j] = x1;
-                b2[j] = x2;
+                const float v = in[q / 2][8 * (q % 2) + j] * sinv;
+                const _Float16 h0 = (_Float16)v;
+                b0[j] = h0;
+                b1[j] = (_Float16)(v - (float)h0);
             }
-            auto a = [&](int t, int p) { return __builtin_bit_cast(bf16x8, sh.frag[((qq * T + t) * 3 + p) * 64 + lane]); };
+            auto a = [&](int t, int p) { return __builtin_bit_cast(f16x8, sh.frag[((qq * T + t) * 2 + p) * 64 + lane]); };
 #pragma unroll
-            for (int t = 0; t < T; ++t) acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a(t, 2), b0, acc[t], 0, 0, 0);
+            for (int t = 0; t < T; ++t) acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a(t, 1), b0, acc[t], 0, 0, 0);
 #pragma unroll
-            for (int t = 0; t < T; ++t) acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a(t, 1), b1, acc[t], 0, 0, 0);
+            for (int t = 0; t < T; ++t) acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a(t, 0), b1, acc[t], 0, 0, 0);
 #pragma unroll
-            for (int t = 0; t < T; ++t) acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a(t, 0), b2, acc[t], 0, 0, 0);
-#pragma unroll
-            for (int t = 0; t < T; ++t) acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a(t, 1), b0, acc[t], 0, 0, 0);
-#pragma unroll
-            for (int t = 0; t < T; ++t) acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a(t, 0), b1, acc[t], 0, 0, 0);
-#pragma unroll
-            for (int t = 0; t < T; ++t) acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a(t, 0), b0, acc[t], 0, 0, 0);
+            for (int t = 0; t < T; ++t) acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a(t, 0), b0, acc[t], 0, 0, 0);
         }
     }
+    const float so = ldexpf(1.f, ex);
+    const int half = lane >> 5;
+#pragma unroll
+    for (int t = 0; t < T; ++t)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const f32x4 rs = *reinterpret_cast<const f32x4*>(rscale + 32 * t + 8 * g + 4 * half);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[t][4 * g + i] = acc[t][4 * g + i] * so * rs[i];
+        }
 }
 
 // Layer 0: B operand read straight from the (E, kin) features; k-step 4q+i of lane
@@ -280,7 +326,7 @@ __global__ void __launch_bounds__(kRadThreads) k_radial_fwd(const float* __restr
     for (int j = 0; j < L; ++j) {
         if (j > 0) {
             zero(acc);
-            mfma_layer<T, H / 16>(frag + lay.fwd_off(j), act, acc, sh, lane);
+            mfma_layer<T, H / 16>(frag + lay.fwd_off(j), frag + lay.fscale_off(j), act, acc, sh, lane);
         }
 #pragma unroll
         for (int t = 0; t < T; ++t)
@@ -334,7 +380,7 @@ __global__ void __launch_bounds__(kRadThreads) k_radial_bwd(const float* __restr
     for (int j = 0; j < L; ++j) {
         if (j > 0) {
             zero(acc);
-            mfma_layer<T, H / 16>(frag + lay.fwd_off(j), g, acc, sh, lane);  // g holds silu(z_{j-1})
+            mfma_layer<T, H / 16>(frag + lay.fwd_off(j), frag + lay.fscale_off(j), g, acc, sh, lane);  // g holds silu(z_{j-1})
         }
         if (j < L - 1) {
 #pragma unroll
@@ -363,7 +409,7 @@ __global__ void __launch_bounds__(kRadThreads) k_radial_bwd(const float* __restr
 #pragma unroll
     for (int j = L - 1; j >= 1; --j) {
         zero(acc);
-        mfma_layer<T, H / 16>(frag + lay.bwd_off(j), g, acc, sh, lane);
+        mfma_layer<T, H / 16>(frag + lay.bwd_off(j), frag + lay.bscale_off(j), g, acc, sh, lane);
 #pragma unroll
         for (int t = 0; t < T; ++t)
 #pragma unroll
@@ -373,12 +419,12 @@ __global__ void __launch_bounds__(kRadThreads) k_radial_bwd(const float* __restr
     if (lay.tiles_bwd(0) == 1) {
         f32x16 a0[1];
         zero(a0);
-        mfma_layer<1, H / 16>(frag + lay.bwd_off(0), g, a0, sh, lane);
+        mfma_layer<1, H / 16>(frag + lay.bwd_off(0), frag + lay.bscale_off(0), g, a0, sh, lane);
         store_grad_feats(a0, grad_feats, e, valid, kin, half);
     } else {
         f32x16 a0[2];
         zero(a0);
-        mfma_layer<2, H / 16>(frag + lay.bwd_off(0), g, a0, sh, lane);
+        mfma_layer<2, H / 16>(frag + lay.bwd_off(0), frag + lay.bscale_off(0), g, a0, sh, lane);
         store_grad_feats(a0, grad_feats, e, valid, kin, half);
     }
 }
@@ -445,9 +491,12 @@ int mnx_radial_pack_f32(const float* raw, int32_t kin, int32_t hidden, int32_t l
     int rc = check_shape(kin, hidden, layers);
     if (rc) return rc;
     MNX_REQUIRE(raw && frag, "null pointer argument");
+    MNX_REQUIRE((uintptr_t)frag % 16 == 0, "frag must be 16-byte aligned");
     const RadLayout lay = make_layout(kin, hidden, layers);
-    hipLaunchKernelGGL(k_radial_pack, dim3(ceil_div(lay.total(), 256)), dim3(256), 0, (hipStream_t)stream, raw, lay,
-                       frag);
+    hipStream_t s = (hipStream_t)stream;
+    hipLaunchKernelGGL(k_radial_scales, dim3(ceil_div(lay.scales_total(), 256)), dim3(256), 0, s, raw, lay, frag);
+    MNX_CHECK_LAUNCH();
+    hipLaunchKernelGGL(k_radial_pack, dim3(ceil_div(lay.fscale_off(1), 256)), dim3(256), 0, s, raw, lay, frag);
     MNX_CHECK_LAUNCH();
     return MNX_OK;
 }
