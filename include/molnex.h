@@ -369,17 +369,21 @@ int mnx_edge_weights_bwd_f32(const float* grad_w, int64_t num_edges, int32_t N, 
 /* computed, the ones the projection reads); channels 8, 16, 32, 64 or 128.  */
 /* Layouts (ir_mul): x [E][NX * C], Y [E][NY], w [num_paths][C],             */
 /* out [E][NO * C] (mnx_tp_config_info gives NX, NY, NO, num_paths).         */
-/* The backward overwrites grad_x [E][NX * C], grad_Y [E][NY] and grad_w     */
-/* [num_paths][C] (each may be NULL); grad_w is summed over edges in a fixed */
-/* order (bitwise reproducible) through a workspace of                       */
+/* x_scale [E][C] (or NULL) multiplies x channel by channel first (Allegro's */
+/* env weights, allegro.py:447-450).  The backward overwrites grad_x         */
+/* [E][NX * C], grad_Y [E][NY], grad_w [num_paths][C] and grad_x_scale       */
+/* [E][C] (each may be NULL); grad_w is summed over edges in a fixed order   */
+/* (bitwise reproducible) through a workspace of                             */
 /* mnx_edge_tp_bwd_workspace_bytes bytes.                                    */
 /* ------------------------------------------------------------------------ */
 int mnx_edge_tp_fwd_f32(int32_t config, int32_t channels, const float* x, const float* Y,
-                        const float* w, int64_t num_edges, float* out, mnx_stream_t stream);
+                        const float* w, const float* x_scale, int64_t num_edges, float* out,
+                        mnx_stream_t stream);
 size_t mnx_edge_tp_bwd_workspace_bytes(int32_t config, int32_t channels, int64_t num_edges);
 int mnx_edge_tp_bwd_f32(int32_t config, int32_t channels, const float* x, const float* Y,
-                        const float* w, const float* grad_out, int64_t num_edges, float* grad_x,
-                        float* grad_Y, float* grad_w, void* workspace, size_t workspace_bytes,
+                        const float* w, const float* x_scale, const float* grad_out,
+                        int64_t num_edges, float* grad_x, float* grad_Y, float* grad_w,
+                        float* grad_x_scale, void* workspace, size_t workspace_bytes,
                         mnx_stream_t stream);
 
 #ifdef __cplusplus

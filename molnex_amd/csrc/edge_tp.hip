@@ -1,6 +1,7 @@
 // Per-edge channelwise tensor product with shared weights (Allegro's layer
-// product, src/molzoo/allegro.py:352-359,457-458): out[e] = TP(x[e], Y[e]; w),
-// no scatter.  The kernels are generated per configuration by gen_edge_tp.py
+// product, src/molzoo/allegro.py:352-359,457-458): out[e] = TP(s[e] x[e], Y[e]; w),
+// no scatter, with an optional per-edge, per-channel scale s of x (the env
+// weights of allegro.py:447-450).  The kernels are generated per configuration by gen_edge_tp.py
 // (edge_tp_gen.inc); configuration ids are those of mnx_tp_config.  Lanes hold
 // (edge, channel) pairs, 64 / min(C, 64) edges per wavefront.
 //
@@ -18,9 +19,9 @@ struct ETPInfo {
     int fwd_groups;  // edge groups per forward wavefront
 };
 
-typedef void (*ETPFwdFn)(const float*, const float*, const float*, int64_t, int, float*);
-typedef void (*ETPBwdFn)(const float*, const float*, const float*, const float*, int64_t, int, float*, float*,
-                         float*);
+typedef void (*ETPFwdFn)(const float*, const float*, const float*, const float*, int64_t, int, float*);
+typedef void (*ETPBwdFn)(const float*, const float*, const float*, const float*, const float*, int64_t, int, float*,
+                         float*, float*, float*);
 
 #include "edge_tp_gen.inc"
 
@@ -81,7 +82,7 @@ using namespace mnx;
 extern "C" {
 
 int mnx_edge_tp_fwd_f32(int32_t config, int32_t channels, const float* x, const float* Y, const float* w,
-                        int64_t num_edges, float* out, mnx_stream_t stream) {
+                        const float* x_scale, int64_t num_edges, float* out, mnx_stream_t stream) {
     clear_error();
     int v = -1;
     int rc = etp_check(config, channels, num_edges, &v);
@@ -91,7 +92,7 @@ int mnx_edge_tp_fwd_f32(int32_t config, int32_t channels, const float* x, const 
     const int64_t G = 64 / kETPVariantCW[v];
     const int64_t blocks = ceil_div(ceil_div(num_edges, G * kETPInfo[config].fwd_groups), kETPThreads / 64);
     hipLaunchKernelGGL(kETPFwd[config][v], dim3(unsigned(blocks)), dim3(kETPThreads), 0, (hipStream_t)stream, x, Y,
-                       w, num_edges, channels, out);
+                       w, x_scale, num_edges, channels, out);
     MNX_CHECK_LAUNCH();
     return MNX_OK;
 }
@@ -103,8 +104,9 @@ size_t mnx_edge_tp_bwd_workspace_bytes(int32_t config, int32_t channels, int64_t
 }
 
 int mnx_edge_tp_bwd_f32(int32_t config, int32_t channels, const float* x, const float* Y, const float* w,
-                        const float* grad_out, int64_t num_edges, float* grad_x, float* grad_Y, float* grad_w,
-                        void* workspace, size_t workspace_bytes, mnx_stream_t stream) {
+                        const float* x_scale, const float* grad_out, int64_t num_edges, float* grad_x,
+                        float* grad_Y, float* grad_w, float* grad_x_scale, void* workspace, size_t workspace_bytes,
+                        mnx_stream_t stream) {
     clear_error();
     int v = -1;
     int rc = etp_check(config, channels, num_edges, &v);
@@ -127,7 +129,7 @@ int mnx_edge_tp_bwd_f32(int32_t config, int32_t channels, const float* x, const 
                 need);
     float* part = static_cast<float*>(workspace);
     hipLaunchKernelGGL(kETPBwd[config][v], dim3(unsigned(waves / 4)), dim3(kETPThreads), 0, s, grad_out, x, Y, w,
-                       num_edges, channels, grad_x, grad_Y, part);
+                       x_scale, num_edges, channels, grad_x, grad_Y, part, grad_x_scale);
     MNX_CHECK_LAUNCH();
     if (grad_w) {
         hipLaunchKernelGGL(k_etp_reduce, dim3(unsigned(nw)), dim3(kETPReduceThreads), 0, s, part, waves, nw, grad_w);

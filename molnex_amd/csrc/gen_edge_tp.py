@@ -10,6 +10,10 @@ and the aggregated neighbourhood harmonics of each edge's source).  Only the pat
 whose output irrep appears in irreps_in are computed: the projection that follows
 (:363-367, cuet.Linear(tp.irreps_out, irreps_in)) connects nothing else.
 
+An optional per-edge, per-channel scale xs[e][c] multiplies x first (Allegro's env weights,
+allegro.py:447-450: TP(s x) = s TP(x) channel by channel); its gradient is
+sum_m1 grad_(s x)[m1] x[m1] per edge and channel.
+
 Lane layout: a wavefront holds 64 / CW edges side by side, CW = min(C, 64) lanes
 per edge, one channel per lane (CPL = 2 channels per lane for C = 128), so small
 channel counts (Allegro's default is 16) still fill the wave.  Backward per lane
@@ -53,8 +57,8 @@ def _fwd(cfg: Cfg) -> str:
     NX, NY, NO, NP = cfg.NX, cfg.NY, cfg.NO, cfg.NP
     EPW = fwd_groups(cfg)
     a(f"template <int CW, int CPL>\n__global__ void __launch_bounds__(256) etp_fwd_c{cfg.idx}("
-      "const float* __restrict__ x, const float* __restrict__ Y, const float* __restrict__ w, int64_t E, int C, "
-      "float* __restrict__ out) {")
+      "const float* __restrict__ x, const float* __restrict__ Y, const float* __restrict__ w, "
+      "const float* __restrict__ xs, int64_t E, int C, float* __restrict__ out) {")
     a("  constexpr int G = 64 / CW;")
     a("  const int lane = threadIdx.x & 63, c0 = lane % CW;")
     a(f"  const int64_t e0 = (int64_t(blockIdx.x) * 4 + (threadIdx.x >> 6)) * ({EPW} * G) + lane / CW;")
@@ -69,7 +73,10 @@ def _fwd(cfg: Cfg) -> str:
     a(f"#pragma unroll\n    for (int i = 0; i < {NY}; ++i) y[q][i] = Ye[i];")
     a("#pragma unroll")
     a("    for (int k = 0; k < CPL; ++k)")
-    a(f"#pragma unroll\n      for (int i = 0; i < {NX}; ++i) xv[q][k][i] = xe[i * C + c0 + 64 * k];")
+    a("    {")
+    a("      const float sc = xs ? xs[e * C + c0 + 64 * k] : 1.f;")
+    a(f"#pragma unroll\n      for (int i = 0; i < {NX}; ++i) xv[q][k][i] = xe[i * C + c0 + 64 * k] * sc;")
+    a("    }")
     a("  }")
     a("#pragma unroll")
     a(f"  for (int q = 0; q < {EPW}; ++q) {{")
@@ -114,8 +121,8 @@ def _bwd(cfg: Cfg) -> str:
     NX, NY, NO, NP = cfg.NX, cfg.NY, cfg.NO, cfg.NP
     a(f"template <int CW, int CPL>\n__global__ void __launch_bounds__(256) etp_bwd_c{cfg.idx}("
       "const float* __restrict__ gout, const float* __restrict__ x, const float* __restrict__ Y, "
-      "const float* __restrict__ w, int64_t E, int C, float* __restrict__ gx, float* __restrict__ gY, "
-      "float* __restrict__ gw_part) {")
+      "const float* __restrict__ w, const float* __restrict__ xs, int64_t E, int C, float* __restrict__ gx, "
+      "float* __restrict__ gY, float* __restrict__ gw_part, float* __restrict__ gxs) {")
     a("  constexpr int G = 64 / CW;")
     a("  const int lane = threadIdx.x & 63, c0 = lane % CW;")
     a("  const int64_t wave = int64_t(blockIdx.x) * 4 + (threadIdx.x >> 6), nwaves = int64_t(gridDim.x) * 4;")
@@ -139,7 +146,9 @@ def _bwd(cfg: Cfg) -> str:
     a(f"      const float* __restrict__ xe = x + es * ({NX} * int64_t(C)) + c;")
     a(f"      const float* __restrict__ ge = gout + es * ({NO} * int64_t(C)) + c;")
     a(f"      float xv[{NX}], gv[{NO}], gxv[{NX}];")
-    a(f"#pragma unroll\n      for (int i = 0; i < {NX}; ++i) {{ xv[i] = valid ? xe[i * C] : 0.f; gxv[i] = 0.f; }}")
+    a("      const float sc = (xs && valid) ? xs[es * C + c] : 1.f;")
+    a(f"      float xr[{NX}];  // x as given; xv = sc * xr enters the product")
+    a(f"#pragma unroll\n      for (int i = 0; i < {NX}; ++i) {{ xr[i] = valid ? xe[i * C] : 0.f; xv[i] = xr[i] * sc; gxv[i] = 0.f; }}")
     a(f"#pragma unroll\n      for (int i = 0; i < {NO}; ++i) gv[i] = valid ? ge[i * C] : 0.f;")
     for j, p in enumerate(cfg.paths):
         cf = p["c"]
@@ -173,7 +182,12 @@ def _bwd(cfg: Cfg) -> str:
             a("        }")
         a("      }")
     a(f"      if (gx && valid) {{ float* __restrict__ gxe = gx + es * ({NX} * int64_t(C)) + c;")
-    a(f"#pragma unroll\n        for (int i = 0; i < {NX}; ++i) gxe[i * C] = gxv[i]; }}")
+    a(f"#pragma unroll\n        for (int i = 0; i < {NX}; ++i) gxe[i * C] = gxv[i] * sc; }}")
+    a("      if (gxs && valid) {")
+    a("        float t = 0.f;")
+    a(f"#pragma unroll\n        for (int i = 0; i < {NX}; ++i) t = fmaf(gxv[i], xr[i], t);")
+    a("        gxs[es * C + c] = t;")
+    a("      }")
     a("    }")
     a("    if (gY) {")
     a("#pragma unroll")

@@ -411,71 +411,82 @@ def edge_tp_supported(config: int, channels: int) -> bool:
 
 
 @torch.library.custom_op("molix::edge_tp", mutates_args=(), device_types="cuda")
-def edge_tp(x: Tensor, Y: Tensor, w: Tensor, config: int, channels: int) -> Tensor:
-    """``out[e] = TP(x[e], Y[e]; w)``: per-edge channelwise product with weights shared by all
-    edges (``w`` is ``(num_paths, C)``), no scatter -- Allegro's layer product
-    (src/molzoo/allegro.py:352-359,457-458)."""
-    _require_gpu("edge_tp", x, Y, w)
+def edge_tp(x: Tensor, Y: Tensor, w: Tensor, config: int, channels: int, x_scale: Tensor | None = None) -> Tensor:
+    """``out[e] = TP(s[e] * x[e], Y[e]; w)``: per-edge channelwise product with weights shared by
+    all edges (``w`` is ``(num_paths, C)``), no scatter -- Allegro's layer product
+    (src/molzoo/allegro.py:352-359,457-458); the optional ``x_scale`` ``(E, C)`` multiplies every
+    component of channel c of x[e] first (the env weights of allegro.py:447-450)."""
+    _require_gpu("edge_tp", x, Y, w, x_scale)
     num_paths, nx, ny, no = tp_config_info(config)
     E = Y.shape[0]
     xs = _f32_rows(x, nx * channels, "x")
     Ys = _f32_rows(Y, ny, "Y")
     ws_ = _f32_rows(w, channels, "w")
-    if xs.shape[0] != E or ws_.shape[0] != num_paths:
-        raise ValueError("edge_tp: x must be (E, NX*C) and w (num_paths, C)")
+    sc = None if x_scale is None else _f32_rows(x_scale, channels, "x_scale")
+    if xs.shape[0] != E or ws_.shape[0] != num_paths or (sc is not None and sc.shape[0] != E):
+        raise ValueError("edge_tp: x must be (E, NX*C), w (num_paths, C), x_scale (E, C)")
     out = torch.empty((E, no * channels), dtype=torch.float32, device=xs.device)
-    check(_lib.load().mnx_edge_tp_fwd_f32(config, channels, ptr(xs), ptr(Ys), ptr(ws_), E, ptr(out), _stream(xs)),
+    check(_lib.load().mnx_edge_tp_fwd_f32(config, channels, ptr(xs), ptr(Ys), ptr(ws_),
+                                          ptr(sc) if sc is not None else None, E, ptr(out), _stream(xs)),
           "edge_tp")
     return out
 
 
 @edge_tp.register_fake
-def _(x, Y, w, config, channels):
+def _(x, Y, w, config, channels, x_scale=None):
     num_paths, nx, ny, no = tp_config_info(config)
     return x.new_empty((Y.shape[0], no * channels))
 
 
 @torch.library.custom_op("molix::edge_tp_backward", mutates_args=(), device_types="cuda")
 def edge_tp_backward(grad_out: Tensor, x: Tensor, Y: Tensor, w: Tensor, config: int, channels: int,
-                     need_x: bool, need_Y: bool, need_w: bool) -> tuple[Tensor, Tensor, Tensor]:
-    """Gradients of ``<grad_out, edge_tp(...)>`` w.r.t. x, Y and the shared w (empty when not
-    needed); the weight gradient is summed over edges in a fixed order."""
+                     need_x: bool, need_Y: bool, need_w: bool, x_scale: Tensor | None = None,
+                     need_scale: bool = False) -> tuple[Tensor, Tensor, Tensor, Tensor]:
+    """Gradients of ``<grad_out, edge_tp(...)>`` w.r.t. x, Y, the shared w and x_scale (empty when
+    not needed); the weight gradient is summed over edges in a fixed order."""
     lib = _lib.load()
     num_paths, nx, ny, no = tp_config_info(config)
     E = Y.shape[0]
     xs = _f32_rows(x, nx * channels, "x")
     Ys = _f32_rows(Y, ny, "Y")
     wss = _f32_rows(w, channels, "w")
+    sc = None if x_scale is None else _f32_rows(x_scale, channels, "x_scale")
     go = _f32_rows(grad_out, no * channels, "grad_out")
     gx = torch.empty_like(xs) if need_x else xs.new_empty(0)
     gY = torch.empty_like(Ys) if need_Y else Ys.new_empty(0)
     gw = torch.empty_like(wss) if need_w else wss.new_empty(0)
+    need_scale = bool(need_scale and sc is not None)
+    gs = torch.empty_like(sc) if need_scale else xs.new_empty(0)
     ws = _ws(max(int(lib.mnx_edge_tp_bwd_workspace_bytes(config, channels, E)), 1), xs.device)
-    check(lib.mnx_edge_tp_bwd_f32(config, channels, ptr(xs), ptr(Ys), ptr(wss), ptr(go), E,
-                                  ptr(gx) if need_x else None, ptr(gY) if need_Y else None,
-                                  ptr(gw) if need_w else None, ptr(ws), ws.numel(), _stream(xs)),
+    check(lib.mnx_edge_tp_bwd_f32(config, channels, ptr(xs), ptr(Ys), ptr(wss), ptr(sc) if sc is not None else None,
+                                  ptr(go), E, ptr(gx) if need_x else None, ptr(gY) if need_Y else None,
+                                  ptr(gw) if need_w else None, ptr(gs) if need_scale else None, ptr(ws), ws.numel(),
+                                  _stream(xs)),
           "edge_tp backward")
-    return gx, gY, gw
+    return gx, gY, gw, gs
 
 
 @edge_tp_backward.register_fake
-def _(grad_out, x, Y, w, config, channels, need_x, need_Y, need_w):
+def _(grad_out, x, Y, w, config, channels, need_x, need_Y, need_w, x_scale=None, need_scale=False):
     return (torch.empty_like(x) if need_x else x.new_empty(0), torch.empty_like(Y) if need_Y else Y.new_empty(0),
-            torch.empty_like(w) if need_w else w.new_empty(0))
+            torch.empty_like(w) if need_w else w.new_empty(0),
+            torch.empty_like(x_scale) if (need_scale and x_scale is not None) else x.new_empty(0))
 
 
 def _etp_setup(ctx, inputs, output):
-    x, Y, w, config, channels = inputs
-    ctx.save_for_backward(x, Y, w)
+    x, Y, w, config, channels, x_scale = inputs
+    ctx.save_for_backward(x, Y, w, x_scale)
     ctx.config, ctx.channels = config, channels
 
 
 def _etp_backward(ctx, grad_out):
-    x, Y, w = ctx.saved_tensors
+    x, Y, w, x_scale = ctx.saved_tensors
     nx, nY, nw = ctx.needs_input_grad[:3]
-    gx, gY, gw = edge_tp_backward(grad_out.contiguous(), x, Y, w, ctx.config, ctx.channels, nx, nY, nw)
+    ns = x_scale is not None and ctx.needs_input_grad[5]
+    gx, gY, gw, gs = edge_tp_backward(grad_out.contiguous(), x, Y, w, ctx.config, ctx.channels, nx, nY, nw,
+                                      x_scale, ns)
     return (gx.reshape(x.shape) if nx else None, gY.reshape(Y.shape) if nY else None,
-            gw.reshape(w.shape) if nw else None, None, None)
+            gw.reshape(w.shape) if nw else None, None, None, gs.reshape(x_scale.shape) if ns else None)
 
 
 edge_tp.register_autograd(_etp_backward, setup_context=_etp_setup)

@@ -12,6 +12,7 @@ uses still fill a 64-wide wavefront.  Its projection (allegro.py:363-367,
 ``cuet.Linear(tp.irreps_out, irreps_in)``) connects only output blocks whose irrep is an input
 irrep, so only those paths are computed; the weight keeps one entry per path of the full product,
 in the reference's order, and the unused entries receive zero gradient as they do there.  The
+layer's env scaling of the tensor track before the product is fused into the same kernel.  The
 projection runs in the HIP block-linear kernel over the edges.  Because every irrep block of the
 tensor track has the same multiplicity, the ir_mul features are ``[sum_l (2l+1)][channel]`` and the
 per-channel scalings are one broadcast multiply.
@@ -98,9 +99,10 @@ class EdgeChannelWiseTensorProduct(nn.Module):
         dt = dtype if dtype is not None else config.ftype
         self.weight = nn.Parameter(torch.randn(1, self.weight_numel, dtype=dt))
 
-    def forward(self, x: torch.Tensor, y: torch.Tensor) -> torch.Tensor:
+    def forward(self, x: torch.Tensor, y: torch.Tensor, x_scale: torch.Tensor | None = None) -> torch.Tensor:
+        """``TP(x, y)``; with ``x_scale`` (E, C), ``TP(x_scale * x, y)`` channel by channel (fused)."""
         w = self.weight.reshape(self.num_paths_full, self.channels).index_select(0, self.kept_paths)
-        return K.edge_tp(x, y, w, self.config_id, self.channels)
+        return K.edge_tp(x, y, w, self.config_id, self.channels, x_scale)
 
 
 class PairEmbedding(nn.Module):
@@ -178,7 +180,6 @@ class AllegroLayer(nn.Module):
     def forward(self, scalar_features, tensor_features, edge_angular, edge_index, n_nodes: int):
         F = self.num_tensor_features
         src = edge_index[:, 0]
-        scaled_V = _scale_by_channel(tensor_features, self.env_embed(scalar_features), self.l_max, F)
         node_Y = torch.zeros(n_nodes, self._sh_dim, dtype=tensor_features.dtype, device=tensor_features.device)
         node_Y = node_Y.index_add(0, src, edge_angular)
         if self.avg_num_neighbors is not None:
@@ -187,7 +188,9 @@ class AllegroLayer(nn.Module):
             count = torch.zeros(n_nodes, dtype=tensor_features.dtype, device=tensor_features.device)
             count = count.index_add(0, src, torch.ones_like(src, dtype=tensor_features.dtype))
             node_Y = node_Y / count.clamp(min=1.0).sqrt().unsqueeze(-1)
-        new_tensor = self.tp_linear(self.tp(scaled_V, node_Y[src]))
+        # TP(env_w . V, Y_agg(src)): the per-channel env scaling (allegro.py:447-450) runs inside the
+        # product kernel, as TP(s x) = s TP(x) channel by channel
+        new_tensor = self.tp_linear(self.tp(tensor_features, node_Y[src], x_scale=self.env_embed(scalar_features)))
         combined = torch.cat([scalar_features, new_tensor[:, :F]], dim=-1)
         updated = self.residual_a * scalar_features + self.residual_b * self.latent_mlp(combined)
         return updated, _scale_by_channel(new_tensor, self.tensor_env(updated), self.l_max, F)

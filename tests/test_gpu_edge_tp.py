@@ -97,7 +97,7 @@ def test_edge_tp_empty_and_unsupported():
     Y = torch.zeros(0, NY, device=DEV)
     w = torch.randn(P, 16, device=DEV)
     assert K.edge_tp(x, Y, w, config, 16).shape == (0, NO * 16)
-    gx, gY, gw = K.edge_tp_backward(torch.zeros(0, NO * 16, device=DEV), x, Y, w, config, 16, True, True, True)
+    gx, gY, gw, _ = K.edge_tp_backward(torch.zeros(0, NO * 16, device=DEV), x, Y, w, config, 16, True, True, True)
     assert gx.shape == (0, NX * 16) and gY.shape == (0, NY) and torch.equal(gw, torch.zeros_like(w))
     assert not K.edge_tp_supported(config, 24)
     with pytest.raises(Exception):
@@ -105,3 +105,29 @@ def test_edge_tp_empty_and_unsupported():
                   config, 24)
     other = K.tp_config_id([0, 1], [0, 1, 2, 3], [0, 1])  # output filter differs from the input irreps
     assert not K.edge_tp_supported(other, 16)
+
+
+@pytest.mark.parametrize("l_max,C", [(2, 16), (1, 8), (3, 64)])
+def test_edge_tp_fused_channel_scale(l_max, C):
+    """``x_scale`` (E, C): the forward equals the product of the pre-scaled x bitwise (the same fp32
+    multiply in the kernel), the gradients match torch's scaling + unscaled product within 1e-6."""
+    import molnex_amd.kernels as K
+
+    E = 777
+    ls = list(range(l_max + 1))
+    config = K.tp_config_id(ls, ls, ls)
+    P, NX, NY, NO = K.tp_config_info(config)
+    g = torch.Generator(device=DEV).manual_seed(l_max + C)
+    x = torch.randn(E, NX * C, device=DEV, generator=g).requires_grad_(True)
+    s = torch.randn(E, C, device=DEV, generator=g).requires_grad_(True)
+    Y = torch.randn(E, NY, device=DEV, generator=g).requires_grad_(True)
+    w = torch.randn(P, C, device=DEV, generator=g).requires_grad_(True)
+    gout = torch.randn(E, NO * C, device=DEV, generator=g)
+    fused = K.edge_tp(x, Y, w, config, C, s)
+    ref = K.edge_tp((x.view(E, NX, C) * s.unsqueeze(1)).reshape(E, -1), Y, w, config, C)
+    assert torch.equal(fused, ref)
+    a = torch.autograd.grad(fused, (x, s, Y, w), gout)
+    b = torch.autograd.grad(ref, (x, s, Y, w), gout)
+    for name, u, v in zip(("x", "scale", "Y", "w"), a, b):
+        rel = float((u - v).norm() / v.norm())
+        assert rel <= 1e-6, (name, rel)
