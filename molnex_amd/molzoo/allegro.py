@@ -190,7 +190,9 @@ class AllegroLayer(nn.Module):
             node_Y = node_Y / count.clamp(min=1.0).sqrt().unsqueeze(-1)
         # TP(env_w . V, Y_agg(src)): the per-channel env scaling (allegro.py:447-450) runs inside the
         # product kernel, as TP(s x) = s TP(x) channel by channel
-        new_tensor = self.tp_linear(self.tp(tensor_features, node_Y[src], x_scale=self.env_embed(scalar_features)))
+        # index_select (backward: one index_add) rather than node_Y[src] (sort-based accumulating backward)
+        edge_node_Y = node_Y.index_select(0, src)
+        new_tensor = self.tp_linear(self.tp(tensor_features, edge_node_Y, x_scale=self.env_embed(scalar_features)))
         combined = torch.cat([scalar_features, new_tensor[:, :F]], dim=-1)
         updated = self.residual_a * scalar_features + self.residual_b * self.latent_mlp(combined)
         return updated, _scale_by_channel(new_tensor, self.tensor_env(updated), self.l_max, F)
