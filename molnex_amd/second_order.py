@@ -188,6 +188,63 @@ def _tp2_bwd(ctx, ggx, ggY, ggw):
 K.tp_scatter_backward.register_autograd(_tp2_bwd, setup_context=_tp2_setup)
 
 
+# per-edge product with shared weights (Allegro): out = TP(s x, Y; w) is multilinear in
+# (x, Y, w, s), so each second-order term is the forward or the backward with one factor replaced
+# by its incoming cotangent (as for the scatter product above)
+
+def _etp2_setup(ctx, inputs, output):
+    g, x, Y, w, config, channels, need_x, need_Y, need_w, x_scale, need_scale = inputs
+    ctx.save_for_backward(g, x, Y, w, x_scale)
+    ctx.cfg = (config, channels)
+    ctx.need = (need_x, need_Y, need_w, bool(need_scale and x_scale is not None))
+
+
+def _etp2_bwd(ctx, ggx, ggY, ggw, ggs):
+    g, x, Y, w, s = ctx.saved_tensors
+    cfg = ctx.cfg
+    live = lambda t, need: t if (need and t is not None and t.numel() > 0) else None  # noqa: E731
+    ggx, ggY, ggw = live(ggx, ctx.need[0]), live(ggY, ctx.need[1]), live(ggw, ctx.need[2])
+    ggs = live(ggs, ctx.need[3])
+    want_g, want_x, want_Y, want_w = ctx.needs_input_grad[:4]
+    want_s = s is not None and ctx.needs_input_grad[9]
+    xf = x.reshape(ggx.shape) if ggx is not None else x
+    dg = dx = dY = dw = ds = None
+
+    def acc(a, b):
+        return b if a is None else (a if b is None else a + b)
+
+    if want_g:
+        terms = []
+        if ggx is not None:
+            terms.append((ggx, Y, w, s))
+        if ggY is not None:
+            terms.append((x, ggY, w, s))
+        if ggw is not None:
+            terms.append((x, Y, ggw, s))
+        if ggs is not None:
+            terms.append((x, Y, w, ggs))
+        for xa, Ya, wa, sa in terms:
+            dg = acc(dg, K.edge_tp(xa, Ya, wa, *cfg, sa))
+    if ggx is not None and (want_Y or want_w or want_s):
+        _, bY, bw, bs = K.edge_tp_backward(g, ggx, Y, w, *cfg, False, want_Y, want_w, s, want_s)
+        dY, dw, ds = acc(dY, bY if want_Y else None), acc(dw, bw if want_w else None), acc(ds, bs if want_s else None)
+    if ggY is not None and (want_x or want_w or want_s):
+        bx, _, bw, bs = K.edge_tp_backward(g, xf, ggY, w, *cfg, want_x, False, want_w, s, want_s)
+        dx, dw, ds = acc(dx, bx if want_x else None), acc(dw, bw if want_w else None), acc(ds, bs if want_s else None)
+    if ggw is not None and (want_x or want_Y or want_s):
+        bx, bY, _, bs = K.edge_tp_backward(g, xf, Y, ggw, *cfg, want_x, want_Y, False, s, want_s)
+        dx, dY, ds = acc(dx, bx if want_x else None), acc(dY, bY if want_Y else None), acc(ds, bs if want_s else None)
+    if ggs is not None and (want_x or want_Y or want_w):
+        bx, bY, bw, _ = K.edge_tp_backward(g, xf, Y, w, *cfg, want_x, want_Y, want_w, ggs, False)
+        dx, dY, dw = acc(dx, bx if want_x else None), acc(dY, bY if want_Y else None), acc(dw, bw if want_w else None)
+    shape = lambda t, ref: None if t is None or ref is None else t.reshape(ref.shape)  # noqa: E731
+    return (shape(dg, g), shape(dx, x), shape(dY, Y), shape(dw, w), None, None, None, None, None,
+            shape(ds, s), None)
+
+
+K.edge_tp_backward.register_autograd(_etp2_bwd, setup_context=_etp2_setup)
+
+
 # ---------------------------------------------------------------------------
 # symmetric contractions
 # ---------------------------------------------------------------------------

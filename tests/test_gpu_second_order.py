@@ -217,3 +217,106 @@ def test_mace_force_loss_gradient_vs_central_differences(literal):
 
         numeric = (8 * (shifted(1) - shifted(-1)) - (shifted(2) - shifted(-2))) / (12 * eps)
         assert abs(analytic - numeric) <= 1e-2 * max(abs(numeric), 1e-3 * abs(float(loss()))), (analytic, numeric)
+
+
+def test_edge_tp_second_order_identities_vs_fp64_restatement():
+    """Second derivatives of the per-edge product with a channel scale (Allegro's layer product)
+    against torch float64 autograd of the einsum restatement in the oracle (allegro_ref.edge_tp):
+    d<r, grad(<g, TP(s x, Y; w)>)>/d(g, x, Y, w, s) for random cotangents r of every gradient."""
+    import molnex_amd.kernels as K
+    from oracle import allegro_ref as AR
+
+    E, C, l_max = 300, 8, 2
+    ls = list(range(l_max + 1))
+    config = K.tp_config_id(ls, ls, ls)
+    P, NX, NY, NO = K.tp_config_info(config)
+    full = [(l1, l2, l3) for l1 in ls for l2 in ls for l3 in range(abs(l1 - l2), l1 + l2 + 1)]
+    kept = [k for k, (l1, l2, l3) in enumerate(full) if (l1 + l2 + l3) % 2 == 0 and l3 <= l_max]
+    gen = torch.Generator().manual_seed(3)
+    x, Y, s, g = (torch.randn(*shape, generator=gen, dtype=torch.float64)
+                  for shape in ((E, NX * C), (E, NY), (E, C), (E, NO * C)))
+    wk = torch.randn(P, C, generator=gen, dtype=torch.float64)
+    rs = [torch.randn(*t.shape, generator=gen, dtype=torch.float64) for t in (x, Y, wk, s)]
+
+    def second(fn, prims):
+        prims = [p.clone().requires_grad_(True) for p in prims]
+        gg = g.clone().requires_grad_(True)
+        out = fn(*prims)
+        first = torch.autograd.grad((out * gg).sum(), prims, create_graph=True)
+        tot = sum((f * r).sum() for f, r in zip(first, rs))
+        return torch.autograd.grad(tot, [gg] + prims)
+
+    def ref_fn(xx, YY, ww, ss):
+        wfull = torch.zeros(len(full), C, dtype=torch.float64)
+        wfull = wfull.index_copy(0, torch.tensor(kept), ww)
+        xs = (xx.view(E, NX, C) * ss.unsqueeze(1)).reshape(E, -1)
+        return AR.edge_tp(xs, YY, wfull.reshape(1, -1), l_max, C)[0]
+
+    def hip_fn(xx, YY, ww, ss):
+        return K.edge_tp(xx, YY, ww, config, C, ss)
+
+    ref = second(ref_fn, [x, Y, wk, s])
+    # the HIP path in fp32 on the GPU: cotangents and primals cast once
+    g32 = g.float().to(DEV).requires_grad_(True)
+    prims = [t.float().to(DEV).requires_grad_(True) for t in (x, Y, wk, s)]
+    out = hip_fn(*prims)
+    first = torch.autograd.grad((out * g32).sum(), prims, create_graph=True)
+    tot = sum((f * r.float().to(DEV)).sum() for f, r in zip(first, rs))
+    got = torch.autograd.grad(tot, [g32] + prims)
+    for name, a, b in zip(("g", "x", "Y", "w", "s"), got, ref):
+        assert _rel(a, b) <= 1e-5, (name, _rel(a, b))
+
+
+def test_allegro_force_loss_gradient_vs_finite_differences():
+    """Force-matching training of the Allegro encoder: d(sum E^2 + sum F^2)/dθ (forces with
+    create_graph through molix::edge_tp's second-order formulas) along random directions of all
+    parameters against the 4-point central stencil of the loss (fp32)."""
+    from molnex_amd.molzoo.allegro import Allegro
+
+    g = torch.Generator().manual_seed(11)
+    n = 30
+    pos = torch.rand(n, 3, generator=g, dtype=torch.float64) * 8.0
+    Z = torch.randint(0, 3, (n,), generator=g).to(DEV)
+    r = (pos[None] - pos[:, None]).norm(dim=-1)
+    src, dst = torch.nonzero((r < 5.0) & (r > 0), as_tuple=True)
+    ei = torch.stack([src, dst], 1).to(DEV)
+    torch.manual_seed(12)
+    model = Allegro(num_elements=3, num_scalar_features=16, num_tensor_features=8, r_max=5.0, l_max=2,
+                    num_layers=2).to(DEV)
+    readout = torch.randn(2, 16, device=DEV, generator=torch.Generator(device=DEV).manual_seed(13)) / 4
+    p0 = pos.float().to(DEV)
+    params = [q for q in model.parameters() if q.requires_grad]
+
+    def loss():
+        p = p0.clone().requires_grad_(True)
+        diff = p[ei[:, 1]] - p[ei[:, 0]]
+        feats = model(Z=Z, bond_dist=diff.norm(dim=-1), bond_diff=diff, edge_index=ei)
+        e = (feats * readout).sum()
+        (f,) = torch.autograd.grad(e, p, create_graph=True)
+        return e ** 2 + (f ** 2).sum()
+
+    model.zero_grad()
+    loss().backward()
+    grads = [torch.zeros_like(q) if q.grad is None else q.grad.detach().clone() for q in params]
+    assert all(torch.isfinite(t).all() for t in grads)
+    gen = torch.Generator(device=DEV).manual_seed(14)
+    for _ in range(2):
+        dirs = [torch.randn(q.shape, device=DEV, generator=gen) for q in params]
+        scale = sum(float((d * d).sum()) for d in dirs) ** 0.5
+        dirs = [d / scale for d in dirs]
+        analytic = sum(float((gq * d).sum()) for gq, d in zip(grads, dirs))
+        eps = 5e-3
+
+        def shifted(t):
+            with torch.no_grad():
+                for q, d in zip(params, dirs):
+                    q.add_(t * eps * d)
+            val = float(loss())
+            with torch.no_grad():
+                for q, d in zip(params, dirs):
+                    q.sub_(t * eps * d)
+            return val
+
+        numeric = (8 * (shifted(1) - shifted(-1)) - (shifted(2) - shifted(-2))) / (12 * eps)
+        assert abs(analytic - numeric) <= 1e-2 * max(abs(numeric), 1e-3 * abs(float(loss()))), (analytic, numeric)
+
