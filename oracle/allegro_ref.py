@@ -12,7 +12,9 @@ a x + b MLP, and the output env scaling; per-layer scalars times the cutoff, sta
 Written with this oracle's pieces (harmonics as explicit polynomials, coupling tensors from the
 null-space construction of ``oracle.equivariant``, the product as one einsum per path, the
 equivariant linear per irrep block from ``oracle.mace_ref``); parameters are read by name from
-the product model's ``state_dict``.  Only the product's paths whose output irrep is an input
+the product model's ``state_dict``.  Pinned by: the pieces' own checks (``oracle.equivariant``,
+``oracle.mace_ref``), rotation invariance of the scalar edge features in float64 for l_max 1-3, and
+a planted output-block-order mistake that breaks it (tests/test_allegro_cpu.py).  Only the product's paths whose output irrep is an input
 irrep feed the projection (the reference's ``cuet.Linear(tp.irreps_out, irreps_in)`` connects
 nothing else), so only those are evaluated here; the weight rows are picked from the full path
 enumeration (input block, harmonics block, l3 ascending).
