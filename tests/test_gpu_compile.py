@@ -188,3 +188,47 @@ def test_exported_linear_matches_eager():
     ep = torch.export.export(lin, (x,), strict=False)
     assert any("block_linear" in str(n.target) for n in ep.graph.nodes)
     assert torch.allclose(ep.module()(x), ref, rtol=1e-6, atol=1e-6)
+
+
+def test_opcheck_edge_tp():
+    cfg = K.tp_config_id([0, 1, 2], [0, 1, 2], [0, 1, 2])
+    P, NX, NY, NO = K.tp_config_info(cfg)
+    E, C = 70, 16
+    g = torch.Generator(device=DEV).manual_seed(9)
+    x = torch.randn(E, NX * C, device=DEV, generator=g).requires_grad_(True)
+    Y = torch.randn(E, NY, device=DEV, generator=g).requires_grad_(True)
+    w = torch.randn(P, C, device=DEV, generator=g).requires_grad_(True)
+    s = torch.randn(E, C, device=DEV, generator=g).requires_grad_(True)
+    opcheck(ops.edge_tp.default, (x, Y, w, cfg, C, s))
+    opcheck(ops.edge_tp.default, (x, Y, w, cfg, C))
+    gout = torch.randn(E, NO * C, device=DEV, generator=g)
+    opcheck(ops.edge_tp_backward.default, (gout, x.detach(), Y.detach(), w.detach(), cfg, C, True, True, True,
+                                           s.detach(), True))
+
+
+def test_compiled_allegro_matches_eager():
+    """The Allegro encoder's energy + forces under torch.compile equal eager (the reference's
+    tests/test_molzoo/test_allegro.py:232-254 compile check)."""
+    from molnex_amd.molzoo.allegro import Allegro
+
+    pos, box, ei, shifts, deltas = _graph(n=50, L=8.0, seed=4)
+    Z = torch.randint(0, 3, (pos.shape[0],), device=DEV)
+    torch.manual_seed(5)
+    model = Allegro(num_elements=3, num_scalar_features=16, num_tensor_features=8, r_max=3.0, l_max=2,
+                    num_layers=2).to(DEV)
+    readout = torch.randn(2, 16, device=DEV)
+
+    def run(m):
+        p = pos.clone().requires_grad_(True)
+        diff = ops.bond_vectors(p, ei, shifts)
+        feats = m(Z=Z, bond_dist=diff.norm(dim=-1), bond_diff=diff, edge_index=ei)
+        e = (feats * readout).sum()
+        (f,) = torch.autograd.grad(e, p)
+        return e.detach(), f.detach()
+
+    e0, f0 = run(model)
+    e1, f1 = run(torch.compile(model, backend="eager", fullgraph=False))
+    rel_e = float((e0 - e1).abs() / e0.abs())
+    rel_f = float((f0 - f1).norm() / f0.norm())
+    # the source-harmonics and force scatters use atomics (summation order differs run to run)
+    assert rel_e <= 1e-6 and rel_f <= 1e-5, (rel_e, rel_f, float((f0 - f1).abs().max()))
