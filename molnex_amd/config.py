@@ -19,6 +19,10 @@ class _Config:
     # True: RadialWeightMLP's last Linear (the per-edge tensor-product weights) runs as the
     # split-fp16 matrix-core kernel molix::edge_weights; False: hipBLASLt fp32 GEMMs
     edge_weights_kernel: bool = True
+    # True: an EdgeGraph (the receiver CSR shared by a step's layers) checks once that every
+    # edge index lies in [0, num_nodes) -- one host synchronisation per graph; False: trust
+    # the indices like the reference's ops (src/molix/F/locality.py:3-5)
+    validate_edges: bool = True
 
 
 config = _Config()

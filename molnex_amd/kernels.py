@@ -268,10 +268,12 @@ spherical_harmonics.register_autograd(_sh_backward, setup_context=_sh_setup)
 
 
 @torch.library.custom_op("molix::edge_csr", mutates_args=(), device_types="cuda")
-def edge_csr(edge_index: Tensor, num_nodes: int) -> tuple[Tensor, Tensor, Tensor]:
+def edge_csr(edge_index: Tensor, num_nodes: int, validate: bool = True) -> tuple[Tensor, Tensor, Tensor]:
     """Receiver CSR of ``edge_index`` (E, 2) = [sender, receiver]: ``(row_ptr, perm, senders)``.
 
-    Raises if an index lies outside ``[0, num_nodes)``.
+    With ``validate`` (one host synchronisation) it raises if an index lies outside
+    ``[0, num_nodes)``; without it such edges are left out of the CSR unchecked, the
+    trusted-input convention of the reference's ops (``src/molix/F/locality.py:3-5``).
     """
     _require_gpu("edge_csr", edge_index)
     if edge_index.ndim != 2 or edge_index.shape[1] != 2:
@@ -287,13 +289,15 @@ def edge_csr(edge_index: Tensor, num_nodes: int) -> tuple[Tensor, Tensor, Tensor
     ws = _ws(lib.mnx_csr_workspace_bytes(num_nodes, E), dev)
     check(lib.mnx_csr_build(ptr(ei), E, num_nodes, ptr(row_ptr), ptr(perm), ptr(snd), ptr(invalid), ptr(ws),
                             ws.numel(), _stream(ei)), "edge_csr")
-    if E > 0 and int(invalid.item()) != 0:
-        raise ValueError(f"edge_index has {int(invalid.item())} edges with a node index outside [0, {num_nodes})")
+    if validate and E > 0:
+        bad = int(invalid.item())
+        if bad != 0:
+            raise ValueError(f"edge_index has {bad} edges with a node index outside [0, {num_nodes})")
     return row_ptr, perm, snd
 
 
 @edge_csr.register_fake
-def _(edge_index, num_nodes):
+def _(edge_index, num_nodes, validate=True):
     E = edge_index.shape[0]
     return (edge_index.new_empty((num_nodes + 1,), dtype=torch.int32),
             edge_index.new_empty((E,), dtype=torch.int32), edge_index.new_empty((E,), dtype=torch.int32))

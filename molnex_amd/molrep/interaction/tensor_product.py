@@ -38,22 +38,40 @@ def _natural_ls(irreps: Irreps, what: str) -> list[int]:
 
 
 class EdgeGraph:
-    """Receiver CSR of one edge list, built once and reused by every layer; the sender CSR
-    (for the atomic-free backward, ``config.deterministic``) is built on first use."""
+    """Receiver CSR of one edge list, built once and reused by every layer (its indices are
+    validated once, here: one host synchronisation per graph, when ``config.validate_edges``);
+    the sender CSR (for the atomic-free backward, ``config.deterministic``) is built on first
+    use."""
 
     def __init__(self, edge_index: torch.Tensor, num_nodes: int):
         self.edge_index = edge_index
         self.num_nodes = num_nodes
-        self.row_ptr, self.perm, self.senders = torch.ops.molix.edge_csr(edge_index, num_nodes)
+        self.row_ptr, self.perm, self.senders = torch.ops.molix.edge_csr(edge_index, num_nodes,
+                                                                         config.validate_edges)
         self._sender_csr = None
 
     def sender_csr(self):
         if self._sender_csr is None:
-            self._sender_csr = torch.ops.molix.edge_csr(self.edge_index.flip(1), self.num_nodes)
+            # same edges as the receiver CSR, already validated
+            self._sender_csr = torch.ops.molix.edge_csr(self.edge_index.flip(1), self.num_nodes, False)
         return self._sender_csr
 
 
 _graph_cache: dict = {}
+
+
+def _key(t: torch.Tensor):
+    return (t.data_ptr(), t.shape, t.stride(), t._version, t.device)
+
+
+def _cached_graph(key, sources, make) -> EdgeGraph:
+    g = _graph_cache.get(key)
+    if g is None or any(a is not b for a, b in zip(g._sources, sources)):
+        _graph_cache.clear()
+        g = make()
+        g._sources = sources
+        _graph_cache[key] = g
+    return g
 
 
 def edge_graph(edge_index: torch.Tensor, num_nodes: int) -> EdgeGraph:
@@ -61,13 +79,17 @@ def edge_graph(edge_index: torch.Tensor, num_nodes: int) -> EdgeGraph:
     one step shares it.  Under torch.compile / torch.export the CSR is built in the traced graph."""
     if torch.compiler.is_compiling():
         return EdgeGraph(edge_index, num_nodes)
-    key = (edge_index.data_ptr(), edge_index.shape[0], num_nodes, edge_index._version, edge_index.device)
-    g = _graph_cache.get(key)
-    if g is None or g.edge_index is not edge_index:
-        _graph_cache.clear()
-        g = EdgeGraph(edge_index, num_nodes)
-        _graph_cache[key] = g
-    return g
+    return _cached_graph(("ei", _key(edge_index), num_nodes), (edge_index,),
+                         lambda: EdgeGraph(edge_index, num_nodes))
+
+
+def edge_graph_from_indices(indices_1: torch.Tensor, indices_out: torch.Tensor, num_nodes: int) -> EdgeGraph:
+    """The EdgeGraph of separate sender / receiver index vectors (the cuet call form), cached on
+    both tensors so repeated calls with the same indices share one CSR."""
+    if torch.compiler.is_compiling():
+        return EdgeGraph(torch.stack([indices_1, indices_out], dim=1), num_nodes)
+    return _cached_graph(("pair", _key(indices_1), _key(indices_out), num_nodes), (indices_1, indices_out),
+                         lambda: EdgeGraph(torch.stack([indices_1, indices_out], dim=1), num_nodes))
 
 
 class ChannelWiseTensorProduct(nn.Module):
@@ -95,9 +117,7 @@ class ChannelWiseTensorProduct(nn.Module):
 
     def forward(self, x, y, weight, indices_1=None, indices_out=None, size_out=None):
         num_nodes = int(size_out) if size_out is not None else x.shape[0]
-        edge_index = torch.stack([indices_1, indices_out], dim=1)
-        g = edge_graph(edge_index, num_nodes)
-        return self.apply_graph(x, y, weight, g)
+        return self.apply_graph(x, y, weight, edge_graph_from_indices(indices_1, indices_out, num_nodes))
 
     def apply_graph(self, x, y, weight, g: EdgeGraph):
         extra = g.sender_csr() if config.deterministic else ()
@@ -131,4 +151,4 @@ def sh_irreps_from_l_max(l_max: int) -> str:
 
 
 __all__ = ["ConvTP", "ConvTPSpec", "ChannelWiseTensorProduct", "irreps_from_l_max", "sh_irreps_from_l_max",
-           "EdgeGraph", "edge_graph", "Irrep"]
+           "EdgeGraph", "edge_graph", "edge_graph_from_indices", "Irrep"]

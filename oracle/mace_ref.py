@@ -98,9 +98,16 @@ def linear(x, weight, blocks_in, blocks_out):
     return torch.cat(outs, dim=1)
 
 
-def _edge_embedding(cfg, pos, edge_index, l_max):
+def bond_vectors(pos, edge_index, shifts=None):
+    """pos[target] - pos[source] (src/molix/data/tasks/neighbor_list.py:86-89), minus the periodic
+    image offset of the source when ``shifts`` is given (bond = pos[i] - (pos[j] + shift))."""
+    d = pos[edge_index[:, 1]] - pos[edge_index[:, 0]]
+    return d if shifts is None else d - shifts
+
+
+def _edge_embedding(cfg, pos, edge_index, l_max, shifts=None):
     rc, nb_ = cfg["r_max"], cfg["num_bessel"]
-    bond_diff = pos[edge_index[:, 1]] - pos[edge_index[:, 0]]
+    bond_diff = bond_vectors(pos, edge_index, shifts)
     bond_dist = bond_diff.norm(dim=-1).clamp(min=1e-6)
     edge_dir = bond_diff / (bond_dist.unsqueeze(-1) + 1e-8)
     Y = sh_torch(l_max, edge_dir)
@@ -126,23 +133,35 @@ def _radial(t, p, edge_feats):
     return a @ t[p + "radial_mlp.mlp.4.weight"].T + t[p + "radial_mlp.mlp.4.bias"]
 
 
+def atom_energies(t, feats):
+    """Per-atom energy MLP on the layer-mean features (src/molpot/heads/heads.py:13-41)."""
+    e_atom = torch.nn.functional.silu(feats @ t["energy.mlp.0.weight"].T + t["energy.mlp.0.bias"])
+    return (e_atom @ t["energy.mlp.2.weight"].T + t["energy.mlp.2.bias"]).squeeze(-1)
+
+
 def _readout(t, per_layer, batch, num_graphs):
     feats = torch.stack(per_layer, dim=1).mean(1)
-    e_atom = torch.nn.functional.silu(feats @ t["energy.mlp.0.weight"].T + t["energy.mlp.0.bias"])
-    e_atom = (e_atom @ t["energy.mlp.2.weight"].T + t["energy.mlp.2.bias"]).squeeze(-1)
-    return torch.zeros(num_graphs, dtype=torch.float64).index_add(0, batch, e_atom)
+    return torch.zeros(num_graphs, dtype=torch.float64).index_add(0, batch, atom_energies(t, feats))
 
 
-def mace_energy_literal(sd: dict, cfg: dict, Z, pos, edge_index, batch, num_graphs):
+def _f64(sd: dict) -> dict:
+    return {k: v.detach().to("cpu", torch.float64) for k, v in sd.items()}
+
+
+def mace_energy_literal(sd: dict, cfg: dict, Z, pos, edge_index, batch, num_graphs, shifts=None):
     """Per-graph energies (fp64) of the literal MACE configuration (hidden irreps
     ``F x hidden_ls``, equivariant product basis and linears throughout)."""
+    t = _f64(sd)
+    return _readout(t, _layers_literal(t, cfg, Z, pos, edge_index, shifts), batch, num_graphs)
+
+
+def _layers_literal(t: dict, cfg: dict, Z, pos, edge_index, shifts=None):
     from . import symcon as SC
 
-    t = {k: v.detach().to("cpu", torch.float64) for k, v in sd.items()}
     F, L, l_max, nu = cfg["num_features"], cfg["num_interactions"], cfg["l_max"], cfg["correlation"]
     hid = list(cfg["hidden_ls"])
     blk = lambda ls: [(F, l, (-1) ** l) for l in ls]  # noqa: E731
-    Y, edge_feats = _edge_embedding(cfg, pos, edge_index, l_max)
+    Y, edge_feats = _edge_embedding(cfg, pos, edge_index, l_max, shifts)
     emb = t["embedding.node_embedding.embedders.0.weight"][Z]
     node = linear(emb, t["embedding.node_embedding.project.0.weight"], [(emb.shape[1], 0, 1)], [(F, 0, 1)])
     h = linear(node, t["initial_projection.weight"], blk([0]), blk([0]))
@@ -174,20 +193,26 @@ def mace_energy_literal(sd: dict, cfg: dict, Z, pos, edge_index, batch, num_grap
             h = sc + upd
         else:
             h = proj
-    return _readout(t, per_layer, batch, num_graphs)
+    return per_layer
 
 
-def mace_energy(sd: dict, cfg: dict, Z, pos, edge_index, batch, num_graphs):
+def mace_energy(sd: dict, cfg: dict, Z, pos, edge_index, batch, num_graphs, shifts=None):
     """Per-graph energies (fp64) of the MACE-as-coded pipeline with the parameters ``sd``
     (the literal configuration when ``cfg`` names ``hidden_ls``)."""
+    t = _f64(sd)
+    return _readout(t, mace_layers(t, cfg, Z, pos, edge_index, shifts), batch, num_graphs)
+
+
+def mace_layers(t: dict, cfg: dict, Z, pos, edge_index, shifts=None):
+    """Per-layer scalar features (the encoder output, mace.py:487-544) in fp64, from fp64
+    parameters ``t``; the literal configuration when ``cfg`` names ``hidden_ls``."""
     if cfg.get("hidden_ls") is not None:
-        return mace_energy_literal(sd, cfg, Z, pos, edge_index, batch, num_graphs)
-    t = {k: v.detach().to("cpu", torch.float64) for k, v in sd.items()}
+        return _layers_literal(t, cfg, Z, pos, edge_index, shifts)
     F, L, l_max = cfg["num_features"], cfg["num_interactions"], cfg["l_max"]
     rc, nb_, nu = cfg["r_max"], cfg["num_bessel"], cfg["correlation"]
     D = F * (l_max + 1) ** 2
     blocks = _irr(l_max, F)
-    bond_diff = pos[edge_index[:, 1]] - pos[edge_index[:, 0]]
+    bond_diff = bond_vectors(pos, edge_index, shifts)
     bond_dist = bond_diff.norm(dim=-1).clamp(min=1e-6)
     # embedding (mace.py:170-184)
     emb = t["embedding.node_embedding.embedders.0.weight"][Z]
@@ -235,14 +260,11 @@ def mace_energy(sd: dict, cfg: dict, Z, pos, edge_index, batch, num_graphs):
             h = sc + upd
         else:
             h = proj
-    feats = torch.stack(per_layer, dim=1).mean(1)
-    e_atom = torch.nn.functional.silu(feats @ t["energy.mlp.0.weight"].T + t["energy.mlp.0.bias"])
-    e_atom = (e_atom @ t["energy.mlp.2.weight"].T + t["energy.mlp.2.bias"]).squeeze(-1)
-    return torch.zeros(num_graphs, dtype=torch.float64).index_add(0, batch, e_atom)
+    return per_layer
 
 
-def energy_forces(sd, cfg, Z, pos, edge_index, batch, num_graphs):
+def energy_forces(sd, cfg, Z, pos, edge_index, batch, num_graphs, shifts=None):
     pos = pos.detach().to(torch.float64).requires_grad_(True)
-    e = mace_energy(sd, cfg, Z, pos, edge_index, batch, num_graphs)
+    e = mace_energy(sd, cfg, Z, pos, edge_index, batch, num_graphs, shifts)
     (g,) = torch.autograd.grad(e.sum(), pos)
     return e.detach(), -g
