@@ -108,6 +108,19 @@ int mnx_csr_build(const int64_t* edge_index, int64_t num_edges, int64_t num_node
                   int32_t* perm, int32_t* senders_sorted, int32_t* d_invalid, void* workspace,
                   size_t workspace_bytes, mnx_stream_t stream);
 
+/* The same CSR build without a workspace and without any allocation: no
+ * counterpart in the reference.  For callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc).  Its scratch (about 17 MB: per-receiver counters, scan
+ * tiles, flags) is one static device array per GPU, held until the process
+ * ends and cleared by fill kernels on every call; num_nodes above
+ * MNX_CSR_NOALLOC_MAX_NODES is rejected with MNX_ERR_INVALID.  All calls on
+ * one GPU share that array: calls that overlap on one GPU (concurrent
+ * streams or host threads) race and must be serialised by the caller. */
+#define MNX_CSR_NOALLOC_MAX_NODES 2097152
+int mnx_csr_build_noalloc(const int64_t* edge_index, int64_t num_edges, int64_t num_nodes, int32_t* row_ptr,
+                          int32_t* perm, int32_t* senders_sorted, int32_t* d_invalid, mnx_stream_t stream);
+
 /* ------------------------------------------------------------------------ */
 /* Real spherical harmonics, component normalisation, l <= 3, input vectors   */
 /* normalised inside (replaces cuet.SphericalHarmonics(ls, normalize=True),   */

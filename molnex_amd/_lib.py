@@ -33,6 +33,7 @@ SIGNATURES = {
     "mnx_nlist_backward_f64": (C.c_int, [vp, vp, vp, vp, vp, vp, c_i64, c_i64, vp, vp]),
     "mnx_csr_workspace_bytes": (c_sz, [c_i64, c_i64]),
     "mnx_csr_build": (C.c_int, [vp, c_i64, c_i64, vp, vp, vp, vp, vp, c_sz, vp]),
+    "mnx_csr_build_noalloc": (C.c_int, [vp, c_i64, c_i64, vp, vp, vp, vp, vp]),
     "mnx_sh_fwd_f32": (C.c_int, [vp, c_i64, c_i32, vp, vp]),
     "mnx_sh_bwd_f32": (C.c_int, [vp, vp, c_i64, c_i32, vp, vp]),
     "mnx_tp_config": (C.c_int, [c_i32, c_i32, c_i32]),

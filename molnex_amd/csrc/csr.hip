@@ -11,6 +11,8 @@
 // the CSR is the identity permutation and the placement and segment sort are
 // skipped, with no host synchronisation.
 
+#include <mutex>
+
 #include "common.h"
 #include "scan.h"
 
@@ -96,25 +98,44 @@ __global__ void k_sort_segments(const int64_t* __restrict__ ei, int64_t N, const
 
 __global__ void k_copy_invalid(const int32_t* __restrict__ src, int32_t* __restrict__ dst) { *dst = *src; }
 
-}  // namespace
-}  // namespace mnx
+// Allocation-free variant: the scratch (per-receiver counters, scan tiles,
+// flags) lives in one file-scope device array instead of a caller workspace.
+// Each device holds its own copy at its own address, found once per device
+// with hipGetSymbolAddress; host code uses that address, never the array's
+// name (which is only a host-side stand-in).  Every call on a device shares
+// the array, so calls that overlap on one device race.
+constexpr int64_t kNoallocMaxNodes = MNX_CSR_NOALLOC_MAX_NODES;
+constexpr size_t kAlign = 256;
+constexpr size_t align_up(size_t v) { return (v + kAlign - 1) & ~(kAlign - 1); }
+// counts, fill (N + 1 each), scan tiles, the two flags; the same carve as carve_csr
+constexpr size_t kNoallocScratchBytes =
+    align_up(sizeof(int32_t) * (kNoallocMaxNodes + 1)) * 2 +
+    align_up(sizeof(int32_t) * size_t((kNoallocMaxNodes + 1 + kScanTile - 1) / kScanTile)) + align_up(2 * sizeof(int32_t)) + kAlign;
 
-using namespace mnx;
+static __device__ __align__(256) unsigned char scratch[kNoallocScratchBytes];
 
-extern "C" {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
 
-size_t mnx_csr_workspace_bytes(int64_t N, int64_t E) {
-    (void)E;
-    size_t used = 0;
-    carve_csr(nullptr, 0, N < 0 ? 0 : N, &used);
-    return used + 256;
+int csr_scratch(void** out) {
+    int dev = -1;
+    MNX_HIP_TRY(hipGetDevice(&dev));
+    MNX_REQUIRE(dev >= 0 && dev < kMaxDevices, "device ordinal %d beyond %d", dev, kMaxDevices);
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void* p = nullptr;
+        MNX_HIP_TRY(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+        MNX_REQUIRE(p != nullptr, "hipGetSymbolAddress returned a null address");
+        g_scratch_ptr[dev] = p;
+    }
+    *out = g_scratch_ptr[dev];
+    return MNX_OK;
 }
 
-int mnx_csr_build(const int64_t* edge_index, int64_t E, int64_t N, int32_t* row_ptr, int32_t* perm,
-                  int32_t* senders_sorted, int32_t* d_invalid, void* workspace, size_t ws_bytes,
-                  mnx_stream_t stream_) {
-    clear_error();
-    hipStream_t stream = (hipStream_t)stream_;
+int csr_build(const int64_t* edge_index, int64_t E, int64_t N, int32_t* row_ptr, int32_t* perm,
+              int32_t* senders_sorted, int32_t* d_invalid, void* workspace, size_t ws_bytes,
+              hipStream_t stream) {
     MNX_REQUIRE(N >= 0 && N < (int64_t(1) << 31) && E >= 0 && E < (int64_t(1) << 31), "sizes out of range");
     MNX_REQUIRE(row_ptr && (E == 0 || (edge_index && perm)), "null pointer argument");
     size_t need = 0;
@@ -149,6 +170,40 @@ int mnx_csr_build(const int64_t* edge_index, int64_t E, int64_t N, int32_t* row_
         MNX_CHECK_LAUNCH();
     }
     return MNX_OK;
+}
+
+}  // namespace
+}  // namespace mnx
+
+using namespace mnx;
+
+extern "C" {
+
+size_t mnx_csr_workspace_bytes(int64_t N, int64_t E) {
+    (void)E;
+    size_t used = 0;
+    carve_csr(nullptr, 0, N < 0 ? 0 : N, &used);
+    return used + 256;
+}
+
+int mnx_csr_build(const int64_t* edge_index, int64_t E, int64_t N, int32_t* row_ptr, int32_t* perm,
+                  int32_t* senders_sorted, int32_t* d_invalid, void* workspace, size_t ws_bytes,
+                  mnx_stream_t stream) {
+    clear_error();
+    return csr_build(edge_index, E, N, row_ptr, perm, senders_sorted, d_invalid, workspace, ws_bytes,
+                     (hipStream_t)stream);
+}
+
+int mnx_csr_build_noalloc(const int64_t* edge_index, int64_t E, int64_t N, int32_t* row_ptr, int32_t* perm,
+                          int32_t* senders_sorted, int32_t* d_invalid, mnx_stream_t stream) {
+    clear_error();
+    MNX_REQUIRE(N >= 0 && N <= kNoallocMaxNodes, "num_nodes %lld exceeds the allocation-free limit of %lld",
+                (long long)N, (long long)kNoallocMaxNodes);
+    void* base = nullptr;
+    int rc = csr_scratch(&base);
+    if (rc) return rc;
+    return csr_build(edge_index, E, N, row_ptr, perm, senders_sorted, d_invalid, base, kNoallocScratchBytes,
+                     (hipStream_t)stream);
 }
 
 }  // extern "C"
