@@ -392,18 +392,22 @@ __device__ __forceinline__ void block_partial(double e, double* __restrict__ par
 // GRAD: also dE/dq and dE/dpos (pme_cpu.cpp:195-215).  Pair lists come grouped by
 // their first atom (the neighbor list's row order), so the first atom's four
 // derivative terms are summed over each run of equal rows in the wavefront and
-// added once per run; the second atom's terms are added per pair.
+// added once per run; the second atom's terms are added per pair.  Each pair's
+// terms are evaluated in fp64 whatever the storage type (erfc/exp/division in
+// double cost nothing next to the pair list's memory latency), so the fp32 path
+// differs from an fp64 evaluation only by its rounded inputs and the fp32
+// accumulation of the derivatives.
 template <typename T, bool GRAD>
 __global__ void __launch_bounds__(kConvThreads) k_direct_pairs(const T* __restrict__ q, int64_t n,
                                                                const int32_t* __restrict__ nb, int64_t P, const T* __restrict__ dl,
                                                                const T* __restrict__ r, const int32_t* __restrict__ excl,
-                                                               int max_excl, T alpha, T coulomb,
+                                                               int max_excl, double alpha, double coulomb,
                                                                T* __restrict__ dpos, T* __restrict__ dq,
                                                                double* __restrict__ partials) {
     const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
     double e = 0.0;
     int row = -1;
-    T g1[4] = {0, 0, 0, 0};  // d/dq and d/dpos of the pair's first atom
+    double g1[4] = {0, 0, 0, 0};  // d/dq and d/dpos of the pair's first atom
     if (i < P) {
         const int a1 = nb[i], a2 = nb[P + i];
         // -1 marks padding (reference); any other out-of-range index is skipped too
@@ -412,30 +416,30 @@ __global__ void __launch_bounds__(kConvThreads) k_direct_pairs(const T* __restri
         for (int j = 0; include && j < max_excl && excl[int64_t(a1) * max_excl + j] >= a2; ++j)
             if (excl[int64_t(a1) * max_excl + j] == a2) include = false;
         if (include) {
-            const T rr = r[i];
-            const T inv = T(1) / rr;
-            const T ar = alpha * rr;
-            const T ec = erfc(ar);
-            const T pref = coulomb * inv;
-            const T c1 = q[a1], c2 = q[a2];
-            e = double(pref * ec * c1 * c2);
+            const double rr = double(r[i]);
+            const double inv = 1.0 / rr;
+            const double ar = alpha * rr;
+            const double ec = erfc(ar);
+            const double pref = coulomb * inv;
+            const double c1 = double(q[a1]), c2 = double(q[a2]);
+            e = pref * ec * c1 * c2;
             if (GRAD) {
-                const T ex = exp(-ar * ar);
-                const T dedr = pref * c1 * c2 * (ec + ar * ex * T(M_2_SQRTPI)) * inv * inv;
+                const double ex = exp(-ar * ar);
+                const double dedr = pref * c1 * c2 * (ec + ar * ex * M_2_SQRTPI) * inv * inv;
                 g1[0] = pref * ec * c2;
-                atomicAdd(dq + a2, pref * ec * c1);
+                atomicAdd(dq + a2, T(pref * ec * c1));
                 for (int k = 0; k < 3; ++k) {
-                    const T f = dedr * dl[3 * i + k];
+                    const double f = dedr * double(dl[3 * i + k]);
                     g1[1 + k] = -f;
-                    atomicAdd(dpos + 3 * a2 + k, f);
+                    atomicAdd(dpos + 3 * a2 + k, T(f));
                 }
             }
         }
     }
     if (GRAD) {
-        if (run_reduce<T, 4>(row, g1) && row >= 0) {
-            atomicAdd(dq + row, g1[0]);
-            for (int k = 0; k < 3; ++k) atomicAdd(dpos + 3 * row + k, g1[1 + k]);
+        if (run_reduce<double, 4>(row, g1) && row >= 0) {
+            atomicAdd(dq + row, T(g1[0]));
+            for (int k = 0; k < 3; ++k) atomicAdd(dpos + 3 * row + k, T(g1[1 + k]));
         }
     }
     block_partial(e, partials);
@@ -443,44 +447,44 @@ __global__ void __launch_bounds__(kConvThreads) k_direct_pairs(const T* __restri
 
 // Excluded pairs' erf term, removed from the reciprocal-space sum (pme_cpu.cpp:137-162).
 // One thread per atom a; a's own derivative terms are summed over its exclusions
-// and added once.
+// and added once.  Pair terms in fp64 as above.
 template <typename T, bool GRAD>
 __global__ void __launch_bounds__(kConvThreads) k_direct_excl(const T* __restrict__ pos, const T* __restrict__ q,
                                                               int64_t n, const int32_t* __restrict__ excl,
-                                                              int max_excl, T alpha, T coulomb,
+                                                              int max_excl, double alpha, double coulomb,
                                                               T* __restrict__ dpos, T* __restrict__ dq,
                                                               double* __restrict__ partials) {
     const int64_t a = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
     double e = 0.0;
     if (a < n) {
-        T ga[4] = {0, 0, 0, 0};
+        double ga[4] = {0, 0, 0, 0};
         for (int j = 0; j < max_excl; ++j) {
             const int b = excl[a * max_excl + j];
             if (!(b > a)) break;
             if (b >= n) continue;
-            T dr[3];
-            for (int k = 0; k < 3; ++k) dr[k] = pos[3 * a + k] - pos[3 * int64_t(b) + k];
-            const T rr = sqrt(dr[0] * dr[0] + dr[1] * dr[1] + dr[2] * dr[2]);
-            const T inv = T(1) / rr;
-            const T ar = alpha * rr;
-            const T ef = erf(ar);
-            const T pref = coulomb * inv;
-            const T c1 = q[a], c2 = q[b];
-            e -= double(pref * ef * c1 * c2);
+            double dr[3];
+            for (int k = 0; k < 3; ++k) dr[k] = double(pos[3 * a + k]) - double(pos[3 * int64_t(b) + k]);
+            const double rr = sqrt(dr[0] * dr[0] + dr[1] * dr[1] + dr[2] * dr[2]);
+            const double inv = 1.0 / rr;
+            const double ar = alpha * rr;
+            const double ef = erf(ar);
+            const double pref = coulomb * inv;
+            const double c1 = double(q[a]), c2 = double(q[b]);
+            e -= pref * ef * c1 * c2;
             if (GRAD) {
-                const T ex = exp(-ar * ar);
-                const T dedr = pref * c1 * c2 * (ef - ar * ex * T(M_2_SQRTPI)) * inv * inv;
+                const double ex = exp(-ar * ar);
+                const double dedr = pref * c1 * c2 * (ef - ar * ex * M_2_SQRTPI) * inv * inv;
                 ga[0] -= pref * ef * c2;
-                atomicAdd(dq + b, -pref * ef * c1);
+                atomicAdd(dq + b, T(-pref * ef * c1));
                 for (int k = 0; k < 3; ++k) {
                     ga[1 + k] += dedr * dr[k];
-                    atomicAdd(dpos + 3 * int64_t(b) + k, -dedr * dr[k]);
+                    atomicAdd(dpos + 3 * int64_t(b) + k, T(-dedr * dr[k]));
                 }
             }
         }
         if (GRAD && max_excl > 0) {
-            atomicAdd(dq + a, ga[0]);
-            for (int k = 0; k < 3; ++k) atomicAdd(dpos + 3 * a + k, ga[1 + k]);
+            atomicAdd(dq + a, T(ga[0]));
+            for (int k = 0; k < 3; ++k) atomicAdd(dpos + 3 * a + k, T(ga[1 + k]));
         }
     }
     block_partial(e, partials);
@@ -605,10 +609,10 @@ void launch_direct(const T* pos, const T* q, int64_t n, const int32_t* nb, int64
                    int64_t b1, int64_t b2, hipStream_t s) {
     if (b1 > 0)
         hipLaunchKernelGGL((k_direct_pairs<T, GRAD>), dim3(b1), dim3(kConvThreads), 0, s, q, n, nb, P, deltas, dist,
-                           excl, max_excl, T(alpha), T(coulomb), dpos, dq, part);
+                           excl, max_excl, alpha, coulomb, dpos, dq, part);
     if (b2 > 0)
         hipLaunchKernelGGL((k_direct_excl<T, GRAD>), dim3(b2), dim3(kConvThreads), 0, s, pos, q, n, excl, max_excl,
-                           T(alpha), T(coulomb), dpos, dq, part + b1);
+                           alpha, coulomb, dpos, dq, part + b1);
 }
 
 template <typename T>

@@ -12,7 +12,8 @@ class NeighborList(nn.Module):
         self.pbc = pbc
 
     def forward(self, positions, cell):
-        return F.get_neighbor_pairs(positions, self.cutoff, box_vectors=cell if self.pbc else None)
+        # the reference passes the cell whatever pbc says (pbc only appears in the repr)
+        return F.get_neighbor_pairs(positions, self.cutoff, box_vectors=cell)
 
     def extra_repr(self):
         return f"cutoff={self.cutoff}, pbc={self.pbc}"

@@ -82,8 +82,10 @@ def edge_tp(V, Ye, weight, l_max, F):
 
 
 def allegro_features(sd: dict, cfg: dict, Z, bond_dist, bond_diff, edge_index):
-    """(E, num_layers, num_scalar_features) in float64 from the model's state_dict."""
-    t = {k: v.detach().double().cpu() for k, v in sd.items()}
+    """(E, num_layers, num_scalar_features) in float64 from the model's state_dict.  Entries that
+    already are float64 CPU tensors requiring grad are used as given (so autograd reaches them)."""
+    t = {k: v if (v.dtype == torch.float64 and v.device.type == "cpu" and v.requires_grad) else
+         v.detach().double().cpu() for k, v in sd.items()}
     l_max, F, nl = cfg["l_max"], cfg["num_tensor_features"], cfg["num_layers"]
     rc, nb, pp = cfg["r_max"], cfg["num_bessel"], cfg.get("poly_p", 6)
     alpha = cfg.get("residual_alpha", 0.5)

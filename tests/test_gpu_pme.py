@@ -29,25 +29,54 @@ def _t(a, grad=False):
     return torch.tensor(a, device=DEV, requires_grad=grad)
 
 
+def _run_case(ops, g, c, dtype):
+    pos = torch.tensor(g[c + "/positions"], dtype=dtype, device=DEV, requires_grad=True)
+    q = torch.tensor(g[c + "/charges"], dtype=dtype, device=DEV, requires_grad=True)
+    f = lambda k: torch.tensor(g[c + "/" + k], dtype=dtype, device=DEV)  # noqa: E731
+    if c.startswith("recip"):
+        grid = [int(v) for v in g[c + "/grid"]]
+        e = ops.pme_reciprocal(pos, q, f("box"), *grid, int(g[c + "/order"]), float(g[c + "/alpha"]),
+                               float(g[c + "/coulomb"]), f("xmoduli"), f("ymoduli"), f("zmoduli"))
+    else:
+        e = ops.pme_direct(pos, q, _t(g[c + "/neighbors"]), f("deltas"), f("distances"), _t(g[c + "/exclusions"]),
+                           float(g[c + "/alpha"]), float(g[c + "/coulomb"]))
+    gp, gq = torch.autograd.grad(e, (pos, q))
+    return float(e.detach()), gp.cpu().numpy(), gq.cpu().numpy()
+
+
+def _oracle_case(g, c):
+    """The fp64 oracle (pinned to the fp64 fixtures at 1e-10 in tests/test_oracle_pme.py) on the
+    case's inputs as stored."""
+    a = lambda k: np.asarray(g[c + "/" + k], np.float64)  # noqa: E731
+    if c.startswith("recip"):
+        return P.reciprocal(a("positions"), a("charges"), a("box"), [int(v) for v in g[c + "/grid"]],
+                            int(g[c + "/order"]), float(g[c + "/alpha"]), float(g[c + "/coulomb"]),
+                            [a("xmoduli"), a("ymoduli"), a("zmoduli")])
+    return P.direct(a("positions"), a("charges"), g[c + "/neighbors"], a("deltas"), a("distances"),
+                    g[c + "/exclusions"], float(g[c + "/alpha"]), float(g[c + "/coulomb"]))
+
+
 def test_pme_against_reference_fixtures(ops):
+    """fp64 cases: the reference op's own fp64 outputs at 1e-10.  Every case again in fp32 (inputs
+    rounded to fp32) against fp64 at 1e-5: the fp64 cases against the reference's fp64 outputs, the
+    fp32 cases against the fp64 oracle on their inputs (the stored fp32 outputs are the
+    reference's own fp32 evaluation and carry its rounding)."""
     g = np.load(GOLD)
     for c in g["cases"]:
-        pos = _t(g[c + "/positions"], True)
-        q = _t(g[c + "/charges"], True)
-        if c.startswith("recip"):
-            grid = [int(v) for v in g[c + "/grid"]]
-            e = ops.pme_reciprocal(pos, q, _t(g[c + "/box"]), *grid, int(g[c + "/order"]), float(g[c + "/alpha"]),
-                                   float(g[c + "/coulomb"]), _t(g[c + "/xmoduli"]), _t(g[c + "/ymoduli"]),
-                                   _t(g[c + "/zmoduli"]))
+        f64 = g[c + "/positions"].dtype == np.float64
+        if f64:
+            e, gp, gq = _run_case(ops, g, c, torch.float64)
+            ref_e = float(g[c + "/energy"])
+            assert abs(e - ref_e) <= 1e-10 * abs(ref_e), (c, e, ref_e)
+            assert _rel(gp, g[c + "/grad_positions"]) <= 1e-10, c
+            assert _rel(gq, g[c + "/grad_charges"]) <= 1e-10, c
+            ref = (ref_e, g[c + "/grad_positions"], g[c + "/grad_charges"])
         else:
-            e = ops.pme_direct(pos, q, _t(g[c + "/neighbors"]), _t(g[c + "/deltas"]), _t(g[c + "/distances"]),
-                               _t(g[c + "/exclusions"]), float(g[c + "/alpha"]), float(g[c + "/coulomb"]))
-        gp, gq = torch.autograd.grad(e, (pos, q))
-        tol = 1e-10 if pos.dtype == torch.float64 else 2e-5
-        ref_e = float(g[c + "/energy"])
-        assert abs(float(e) - ref_e) <= tol * abs(ref_e), (c, float(e), ref_e)
-        assert _rel(gp.cpu().numpy(), g[c + "/grad_positions"]) <= tol, c
-        assert _rel(gq.cpu().numpy(), g[c + "/grad_charges"]) <= tol, c
+            ref = _oracle_case(g, c)
+        e, gp, gq = _run_case(ops, g, c, torch.float32)
+        errs = (abs(e - ref[0]) / abs(ref[0]), _rel(gp, ref[1]), _rel(gq, ref[2]))
+        print(f"{c}: fp32 vs fp64 rel err energy {errs[0]:.2e}, d/dpos {errs[1]:.2e}, d/dq {errs[2]:.2e}")
+        assert max(errs) <= 1e-5, (c, errs)
 
 
 def test_config5_pme_scale(ops):
@@ -163,12 +192,14 @@ def test_direct_against_oracle_with_exclusions_and_padding(ops):
         excl[i, :len(s)] = sorted(s, reverse=True)
     alpha, k = 0.3, 14.399645
     re, rp, rq = P.direct(pos, q, nb, d, dist, excl, alpha, k)
-    for dtype, tol in ((torch.float64, 1e-10), (torch.float32, 2e-5)):
+    for dtype, tol in ((torch.float64, 1e-10), (torch.float32, 1e-5)):
         p_ = torch.tensor(pos, dtype=dtype, device=DEV, requires_grad=True)
         q_ = torch.tensor(q, dtype=dtype, device=DEV, requires_grad=True)
         e = ops.pme_direct(p_, q_, torch.tensor(nb, device=DEV), torch.tensor(d, dtype=dtype, device=DEV),
                            torch.tensor(dist, dtype=dtype, device=DEV), torch.tensor(excl, device=DEV), alpha, k)
         gp, gq = torch.autograd.grad(e, (p_, q_))
+        print(f"{dtype}: rel err energy {abs(float(e) - re) / abs(re):.2e}, d/dpos {_rel(gp.cpu().numpy(), rp):.2e}, "
+              f"d/dq {_rel(gq.cpu().numpy(), rq):.2e}")
         assert abs(float(e) - re) <= tol * abs(re), (dtype, float(e), re)
         assert _rel(gp.cpu().numpy(), rp) <= tol, dtype
         assert _rel(gq.cpu().numpy(), rq) <= tol, dtype

@@ -26,7 +26,7 @@ def _close(got, ref, what, rtol=1e-5):
     err = np.linalg.norm(got - ref) / nref
     mx = np.abs(got - ref).max()
     rms = nref / np.sqrt(ref.size)
-    assert err <= rtol and mx <= 10 * rtol * rms, f"{what}: rel {err:.2e}, max-abs {mx:.2e} (rms {rms:.2e})"
+    assert err <= rtol and mx <= rtol * rms, f"{what}: rel {err:.2e}, max-abs {mx:.2e} (rms {rms:.2e})"
 
 
 @pytest.fixture(scope="module")
