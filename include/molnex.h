@@ -122,6 +122,25 @@ int mnx_csr_build_noalloc(const int64_t* edge_index, int64_t num_edges, int64_t 
                           int32_t* perm, int32_t* senders_sorted, int32_t* d_invalid, mnx_stream_t stream);
 
 /* ------------------------------------------------------------------------ */
+/* Segment sums over a CSR (row_ptr / perm from mnx_csr_build of the rows'    */
+/* segment ids): replaces the scatter_add_ of molix.F.scatter_sum / batch_add */
+/* (src/molix/F/scatter.py:13-51) and MessageAggregation's neighbour sum      */
+/* (src/molrep/interaction/aggregation.py:93-117):                            */
+/*   out[n][:] = sum_{k in [row_ptr[n], row_ptr[n+1])} w[perm[k]] values[perm[k]][:] */
+/* values [num_rows][dim], weights [num_rows] or NULL (all ones), out          */
+/* [num_segments][dim] (overwritten; no atomics, a fixed summation order).    */
+/* ------------------------------------------------------------------------ */
+int mnx_segment_sum_f32(const float* values, int64_t num_rows, int32_t dim, const int32_t* row_ptr,
+                        const int32_t* perm, const float* weights, int64_t num_segments, float* out,
+                        mnx_stream_t stream);
+/* Its gradients: grad_values[r][:] = w[r] grad_out[index[r]][:] and grad_weights[r] =
+ * <values[r], grad_out[index[r]]> (either output may be NULL; rows whose index lies outside
+ * [0, num_segments) get zeros).  index: int64 [num_rows]. */
+int mnx_segment_sum_bwd_f32(const float* grad_out, const int64_t* index, const float* weights, const float* values,
+                            int64_t num_rows, int32_t dim, int64_t num_segments, float* grad_values,
+                            float* grad_weights, mnx_stream_t stream);
+
+/* ------------------------------------------------------------------------ */
 /* Real spherical harmonics, component normalisation, l <= 3, input vectors   */
 /* normalised inside (replaces cuet.SphericalHarmonics(ls, normalize=True),   */
 /* src/molrep/embedding/angular.py:89,104).  Output [n][(l_max+1)^2].         */
@@ -307,6 +326,22 @@ int mnx_block_linear_f32(const float* a, int64_t a_stride, int32_t nseg, const i
                          const int32_t* seg_comp, const int32_t* seg_len, const float* w, int32_t N,
                          int64_t R, int32_t d, float* out, int64_t out_stride, int64_t out_off,
                          int32_t out_comp, mnx_stream_t stream);
+/* The same block linear with one weight set per node class: the indexed     */
+/* linear of ElementUpdate (cuet.Linear(weight_classes=S,                     */
+/* method="indexed_linear"), src/molrep/interaction/element_update.py:        */
+/* 101-109,147-158).  Node n uses the weights of its class; the caller passes */
+/* the nodes grouped by class, order [R] (int32 node ids, classes ascending,  */
+/* ascending node id within a class, nodes whose class lies outside [0, S)    */
+/* last) and class_start [S + 2] (position in order where class s begins,     */
+/* s = 0..S, with s = S the out-of-range nodes, and class_start[S + 1] = R).  */
+/* w points at class 0's fragment-ordered weights (layout as above);         */
+/* consecutive classes are w_class_stride floats apart.  Out-of-range nodes  */
+/* get zero output.  No host synchronisation is needed to build the inputs.  */
+int mnx_indexed_block_linear_f32(const float* a, int64_t a_stride, int32_t nseg, const int64_t* seg_col,
+                                 const int32_t* seg_comp, const int32_t* seg_len, const float* w,
+                                 int64_t w_class_stride, int32_t num_classes, const int32_t* order,
+                                 const int32_t* class_start, int32_t N, int64_t R, int32_t d, float* out,
+                                 int64_t out_stride, int64_t out_off, int32_t out_comp, mnx_stream_t stream);
 
 /* ------------------------------------------------------------------------ */
 /* Bond vectors diff[e] = pos[ei[e][1]] - pos[ei[e][0]] - shifts[e] (shifts  */

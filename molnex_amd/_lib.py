@@ -34,6 +34,8 @@ SIGNATURES = {
     "mnx_csr_workspace_bytes": (c_sz, [c_i64, c_i64]),
     "mnx_csr_build": (C.c_int, [vp, c_i64, c_i64, vp, vp, vp, vp, vp, c_sz, vp]),
     "mnx_csr_build_noalloc": (C.c_int, [vp, c_i64, c_i64, vp, vp, vp, vp, vp]),
+    "mnx_segment_sum_f32": (C.c_int, [vp, c_i64, c_i32, vp, vp, vp, c_i64, vp, vp]),
+    "mnx_segment_sum_bwd_f32": (C.c_int, [vp, vp, vp, vp, c_i64, c_i32, c_i64, vp, vp, vp]),
     "mnx_sh_fwd_f32": (C.c_int, [vp, c_i64, c_i32, vp, vp]),
     "mnx_sh_bwd_f32": (C.c_int, [vp, vp, c_i64, c_i32, vp, vp]),
     "mnx_tp_config": (C.c_int, [c_i32, c_i32, c_i32]),
@@ -65,6 +67,8 @@ SIGNATURES = {
     "mnx_block_linear_frag_floats": (c_i64, [c_i32, c_i32]),
     "mnx_block_linear_f32": (C.c_int, [vp, c_i64, c_i32, vp, vp, vp, vp, c_i32, c_i64, c_i32, vp, c_i64, c_i64,
                                         c_i32, vp]),
+    "mnx_indexed_block_linear_f32": (C.c_int, [vp, c_i64, c_i32, vp, vp, vp, vp, c_i64, c_i32, vp, vp, c_i32,
+                                                c_i64, c_i32, vp, c_i64, c_i64, c_i32, vp]),
     "mnx_bond_vectors_f32": (C.c_int, [vp, c_i64, vp, vp, c_i64, vp, vp]),
     "mnx_bond_vectors_bwd_f32": (C.c_int, [vp, vp, c_i64, c_i64, vp, vp]),
     "mnx_radial_raw_floats": (c_i64, [c_i32, c_i32, c_i32]),

@@ -23,6 +23,16 @@
 // accumulated in fp32, smallest first (the dropped terms are below 2^-25 |x y|),
 // at 3/8 of the matrix-core cycles of fp32 MFMAs.  The D tiles are stored 128
 // contiguous bytes per row.
+//
+// Indexed mode (cuet.Linear(weight_classes=S, method="indexed_linear"),
+// src/molrep/interaction/element_update.py:101-109,147-158): every node has a
+// class (element) and its own weight set.  The caller groups the nodes by class
+// (`order`, ascending class, rows of an out-of-range class last) and passes the
+// class boundaries; workgroup b finds its class from those boundaries (each
+// class owns ceil(count * d / 256) consecutive workgroups), reads its rows
+// through `order` and uses the weights of its class.  The out-of-range class
+// writes zeros.  No host synchronisation: the grid is sized for the worst case
+// (one partial workgroup per class) and surplus workgroups exit at once.
 
 #include "common.h"
 
@@ -68,18 +78,47 @@ struct LinArgs {
     float* out;
     int64_t out_stride, out_off;
     int32_t out_comp;
+    // indexed mode
+    const int32_t* order;        // [R] node ids grouped by class
+    const int32_t* class_start;  // [S + 2] first position in order of classes 0..S (S = out of range)
+    int32_t S;
+    int64_t w_class_stride;      // floats between the weight sets of consecutive classes
 };
+
+constexpr int kLinRowsPerBlock = (kLinThreads / kWave) * 32;
 
 // NT: output tiles of 32 columns per wavefront; D: components per row group when it
 // is 1, 3, 5 or 7 (divisions by it become multiplies), 0 = read p.d.
-template <int NT, int D>
+template <int NT, int D, bool IDX>
 __global__ void __launch_bounds__(kLinThreads) k_block_linear(LinArgs p) {
     constexpr int KQ = kLinKC / 16;  // bf16 k-steps per staged chunk
     const int d = D ? D : p.d;
     __shared__ bf16x8 sw[3][KQ][NT][kWave];
     const int lane = threadIdx.x & 63, half = lane >> 5, wave = threadIdx.x >> 6;
-    const int64_t rows = p.R * d;
-    const int64_t row0 = (int64_t(blockIdx.x) * (kLinThreads / kWave) + wave) * 32;
+    int64_t row0, rows;
+    int K = p.K;
+    const float* wcls = p.w;
+    if (IDX) {
+        // this workgroup's class: classes 0..S (S = out of range, zeros) own consecutive runs of
+        // ceil(count * d / rows per block) workgroups
+        const int64_t b = blockIdx.x;
+        int64_t first = 0;
+        int cls = 0;
+        for (; cls <= p.S; ++cls) {
+            const int64_t cnt = int64_t(p.class_start[cls + 1] - p.class_start[cls]) * d;
+            const int64_t nb = (cnt + kLinRowsPerBlock - 1) / kLinRowsPerBlock;
+            if (b < first + nb) break;
+            first += nb;
+        }
+        if (cls > p.S) return;  // surplus workgroup (the grid is sized for the worst case)
+        row0 = int64_t(p.class_start[cls]) * d + (b - first) * kLinRowsPerBlock + wave * 32;
+        rows = int64_t(p.class_start[cls + 1]) * d;
+        if (cls == p.S) K = 0;  // out-of-range class: zero output
+        else wcls = p.w + int64_t(cls) * p.w_class_stride;
+    } else {
+        row0 = (int64_t(blockIdx.x) * (kLinThreads / kWave) + wave) * 32;
+        rows = p.R * d;
+    }
     const int64_t row = row0 + (lane & 31);
     const bool valid = row < rows;
     // (node, component) of row0 once; rows within the tile follow in 32-bit arithmetic
@@ -87,7 +126,8 @@ __global__ void __launch_bounds__(kLinThreads) k_block_linear(LinArgs p) {
     const int c0 = int(row0 - n0 * d);
     const int64_t n = n0 + (c0 + (lane & 31)) / d;
     const int ci = (c0 + (lane & 31)) % d;
-    const float* arow = p.a + n * p.a_stride;
+    const int64_t node = IDX ? (valid ? int64_t(p.order[n]) : 0) : n;
+    const float* arow = p.a + node * p.a_stride;
     const int col0 = blockIdx.y * NT * 32;
     f32x16 acc[NT];
 #pragma unroll
@@ -96,14 +136,14 @@ __global__ void __launch_bounds__(kLinThreads) k_block_linear(LinArgs p) {
         for (int r = 0; r < 16; ++r) acc[t][r] = 0.f;
     constexpr int kChunk4 = KQ * NT * kWave * 2;  // fp32 float4s per staged chunk
     const int nchunks = (p.K + kLinKC - 1) / kLinKC;
-    const f32x4* wsrc = reinterpret_cast<const f32x4*>(p.w) + int64_t(blockIdx.y) * nchunks * kChunk4;
+    const f32x4* wsrc = reinterpret_cast<const f32x4*>(wcls) + int64_t(blockIdx.y) * nchunks * kChunk4;
     bf16x4* sw4 = reinterpret_cast<bf16x4*>(&sw[0][0][0][0]);
     // per segment, this lane's offset of contraction index k is base[s] + k (row-relative)
     int32_t base[kLinMaxSeg];
 #pragma unroll
     for (int sg = 0; sg < kLinMaxSeg; ++sg)
         base[sg] = sg < p.nseg ? int32_t(p.seg[sg].col + int64_t(ci) * p.seg[sg].comp - p.seg[sg].k0) : 0;
-    for (int k0 = 0; k0 < p.K; k0 += kLinKC) {
+    for (int k0 = 0; k0 < K; k0 += kLinKC) {
         // this chunk's A operands first (8 consecutive values per lane and k-step): their
         // latency overlaps the weight staging below
         f32x4 av[KQ][2];
@@ -177,7 +217,8 @@ __global__ void __launch_bounds__(kLinThreads) k_block_linear(LinArgs p) {
         const int64_t nn = n0 + (c0 + o) / d;
         const int ii = (c0 + o) % d;
         oval[r] = row0 + o < rows;
-        obase[r] = nn * p.out_stride + p.out_off + int64_t(ii) * p.out_comp;
+        const int64_t on = IDX ? (oval[r] ? int64_t(p.order[nn]) : 0) : nn;
+        obase[r] = on * p.out_stride + p.out_off + int64_t(ii) * p.out_comp;
     }
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
@@ -192,39 +233,29 @@ __global__ void __launch_bounds__(kLinThreads) k_block_linear(LinArgs p) {
 // output tiles of 32 columns per wavefront for N columns (the column-group width is 32 * this)
 int lin_tiles(int N) { return N >= 128 ? 4 : int(ceil_div(N, 32)); }
 
-template <int NT>
+template <int NT, bool IDX>
 void launch_nt(int d, dim3 grid, hipStream_t s, const LinArgs& p) {
     switch (d) {
-        case 1: hipLaunchKernelGGL((k_block_linear<NT, 1>), grid, dim3(kLinThreads), 0, s, p); break;
-        case 3: hipLaunchKernelGGL((k_block_linear<NT, 3>), grid, dim3(kLinThreads), 0, s, p); break;
-        case 5: hipLaunchKernelGGL((k_block_linear<NT, 5>), grid, dim3(kLinThreads), 0, s, p); break;
-        case 7: hipLaunchKernelGGL((k_block_linear<NT, 7>), grid, dim3(kLinThreads), 0, s, p); break;
-        default: hipLaunchKernelGGL((k_block_linear<NT, 0>), grid, dim3(kLinThreads), 0, s, p); break;
+        case 1: hipLaunchKernelGGL((k_block_linear<NT, 1, IDX>), grid, dim3(kLinThreads), 0, s, p); break;
+        case 3: hipLaunchKernelGGL((k_block_linear<NT, 3, IDX>), grid, dim3(kLinThreads), 0, s, p); break;
+        case 5: hipLaunchKernelGGL((k_block_linear<NT, 5, IDX>), grid, dim3(kLinThreads), 0, s, p); break;
+        case 7: hipLaunchKernelGGL((k_block_linear<NT, 7, IDX>), grid, dim3(kLinThreads), 0, s, p); break;
+        default: hipLaunchKernelGGL((k_block_linear<NT, 0, IDX>), grid, dim3(kLinThreads), 0, s, p); break;
     }
 }
 
-}  // namespace
-}  // namespace mnx
-
-using namespace mnx;
-
-extern "C" {
-
-int64_t mnx_block_linear_frag_floats(int32_t K, int32_t N) {
-    if (K < 0 || N < 1) return -1;
-    const int nt = lin_tiles(N);
-    return ceil_div(N, nt * 32) * ceil_div(K, kLinKC) * int64_t(kLinKC / 16) * nt * kWave * 8;
-}
-
-int mnx_block_linear_f32(const float* a, int64_t a_stride, int32_t nseg, const int64_t* seg_col,
-                         const int32_t* seg_comp, const int32_t* seg_len, const float* w, int32_t N, int64_t R,
-                         int32_t d, float* out, int64_t out_stride, int64_t out_off, int32_t out_comp,
-                         mnx_stream_t stream) {
-    clear_error();
+// shared argument checks and launch of both entry points
+int block_linear(const float* a, int64_t a_stride, int32_t nseg, const int64_t* seg_col, const int32_t* seg_comp,
+                 const int32_t* seg_len, const float* w, int32_t N, int64_t R, int32_t d, float* out,
+                 int64_t out_stride, int64_t out_off, int32_t out_comp, const int32_t* order,
+                 const int32_t* class_start, int32_t S, int64_t w_class_stride, hipStream_t stream) {
     MNX_REQUIRE(nseg >= 0 && nseg <= kLinMaxSeg, "segment count %d not in [0, %d]", nseg, kLinMaxSeg);
     MNX_REQUIRE(R >= 0 && d >= 1 && N >= 1 && R * d < (int64_t(1) << 40), "sizes out of range");
     if (R == 0) return MNX_OK;
     MNX_REQUIRE(out && (nseg == 0 || (a && w && seg_col && seg_comp && seg_len)), "null pointer argument");
+    const bool idx = order != nullptr;
+    MNX_REQUIRE(!idx || (class_start && S >= 1 && S <= 4096 && w_class_stride >= 0 && w_class_stride % 4 == 0),
+                "indexed linear: bad class arguments");
     LinArgs p{};
     p.a = a;
     p.a_stride = a_stride;
@@ -249,19 +280,65 @@ int mnx_block_linear_f32(const float* a, int64_t a_stride, int32_t nseg, const i
     p.out_stride = out_stride;
     p.out_off = out_off;
     p.out_comp = out_comp;
-    const int64_t blocks = ceil_div(R * d, (kLinThreads / kWave) * 32);
+    p.order = order;
+    p.class_start = class_start;
+    p.S = S;
+    p.w_class_stride = w_class_stride;
+    // indexed: every class (and the out-of-range one) may end in a partial workgroup
+    const int64_t blocks = ceil_div(R * d, kLinRowsPerBlock) + (idx ? S + 1 : 0);
     MNX_REQUIRE(blocks < (int64_t(1) << 31), "too many rows");
     const int nt = lin_tiles(N);
     const dim3 grid(unsigned(blocks), unsigned(ceil_div(N, nt * 32)));
-    hipStream_t s = (hipStream_t)stream;
-    switch (nt) {
-        case 1: launch_nt<1>(d, grid, s, p); break;
-        case 2: launch_nt<2>(d, grid, s, p); break;
-        case 3: launch_nt<3>(d, grid, s, p); break;
-        default: launch_nt<4>(d, grid, s, p); break;
+    if (idx) {
+        switch (nt) {
+            case 1: launch_nt<1, true>(d, grid, stream, p); break;
+            case 2: launch_nt<2, true>(d, grid, stream, p); break;
+            case 3: launch_nt<3, true>(d, grid, stream, p); break;
+            default: launch_nt<4, true>(d, grid, stream, p); break;
+        }
+    } else {
+        switch (nt) {
+            case 1: launch_nt<1, false>(d, grid, stream, p); break;
+            case 2: launch_nt<2, false>(d, grid, stream, p); break;
+            case 3: launch_nt<3, false>(d, grid, stream, p); break;
+            default: launch_nt<4, false>(d, grid, stream, p); break;
+        }
     }
     MNX_CHECK_LAUNCH();
     return MNX_OK;
+}
+
+}  // namespace
+}  // namespace mnx
+
+using namespace mnx;
+
+extern "C" {
+
+int64_t mnx_block_linear_frag_floats(int32_t K, int32_t N) {
+    if (K < 0 || N < 1) return -1;
+    const int nt = lin_tiles(N);
+    return ceil_div(N, nt * 32) * ceil_div(K, kLinKC) * int64_t(kLinKC / 16) * nt * kWave * 8;
+}
+
+int mnx_block_linear_f32(const float* a, int64_t a_stride, int32_t nseg, const int64_t* seg_col,
+                         const int32_t* seg_comp, const int32_t* seg_len, const float* w, int32_t N, int64_t R,
+                         int32_t d, float* out, int64_t out_stride, int64_t out_off, int32_t out_comp,
+                         mnx_stream_t stream) {
+    clear_error();
+    return block_linear(a, a_stride, nseg, seg_col, seg_comp, seg_len, w, N, R, d, out, out_stride, out_off,
+                        out_comp, nullptr, nullptr, 0, 0, (hipStream_t)stream);
+}
+
+int mnx_indexed_block_linear_f32(const float* a, int64_t a_stride, int32_t nseg, const int64_t* seg_col,
+                                 const int32_t* seg_comp, const int32_t* seg_len, const float* w,
+                                 int64_t w_class_stride, int32_t num_classes, const int32_t* order,
+                                 const int32_t* class_start, int32_t N, int64_t R, int32_t d, float* out,
+                                 int64_t out_stride, int64_t out_off, int32_t out_comp, mnx_stream_t stream) {
+    clear_error();
+    MNX_REQUIRE(order && class_start, "indexed linear: order and class_start are required");
+    return block_linear(a, a_stride, nseg, seg_col, seg_comp, seg_len, w, N, R, d, out, out_stride, out_off,
+                        out_comp, order, class_start, num_classes, w_class_stride, (hipStream_t)stream);
 }
 
 }  // extern "C"

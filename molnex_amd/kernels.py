@@ -18,6 +18,8 @@ Ops
 ``molix::edge_weights``         output layer of the radial weight MLP (per-edge TP weights), near-fp32 split-fp16 MFMA
 ``molix::bond_vectors``         pos[receiver] - pos[sender] - shift per edge, with its position gradient
 ``molix::block_linear``         equivariant (ir_mul) block linear with pre-ordered weights (``cuet.Linear``)
+``molix::indexed_block_linear`` the block linear with one weight set per node class (ElementUpdate)
+``molix::segment_sum``          weighted segment sum of rows by segment id (scatter_sum / MessageAggregation)
 """
 
 from __future__ import annotations
@@ -1095,6 +1097,69 @@ def _(a, weights, blocks, out_dim):
     return a.new_empty(a.shape[0], out_dim)
 
 
+def class_groups(classes: Tensor, num_classes: int) -> tuple[Tensor, Tensor]:
+    """Nodes grouped by class without a host synchronisation: ``order`` (int32, classes ascending,
+    ascending node id within a class, out-of-range classes last) and ``class_start`` (int32,
+    ``num_classes + 2`` entries: where class s begins in ``order``, s = num_classes being the
+    out-of-range nodes)."""
+    c = classes.reshape(-1).to(torch.int64)
+    key = torch.where((c >= 0) & (c < num_classes), c, torch.full_like(c, num_classes))
+    order = torch.argsort(key, stable=True).to(torch.int32)
+    counts = torch.zeros(num_classes + 1, dtype=torch.int64, device=c.device).scatter_add_(0, key, torch.ones_like(key))
+    class_start = torch.cat([counts.new_zeros(1), torch.cumsum(counts, 0)]).to(torch.int32)
+    return order, class_start
+
+
+@torch.library.custom_op("molix::indexed_block_linear", mutates_args=(), device_types="cuda")
+def indexed_block_linear(a: Tensor, weights: Tensor, order: Tensor, class_start: Tensor, blocks: list[int],
+                         out_dim: int) -> Tensor:
+    """``block_linear`` with one weight set per node class (``cuet.Linear(weight_classes=S,
+    method="indexed_linear")``, ``src/molrep/interaction/element_update.py:101-109``): ``weights``
+    (S, F) holds every class's concatenated fragment-ordered weights, ``order`` / ``class_start``
+    come from ``class_groups``.  Nodes of an out-of-range class get zeros."""
+    _require_gpu("indexed_block_linear", a, weights, order, class_start)
+    if a.dtype != torch.float32 or weights.dtype != torch.float32 or a.dim() != 2 or weights.dim() != 2:
+        raise TypeError("indexed_block_linear: a must be float32 (R, dim_in) and weights float32 (S, F)")
+    lib = _lib.load()
+    x = _aligned16(a)
+    S, F = weights.shape
+    if F % 4:
+        raise ValueError("indexed_block_linear: per-class weight length must be a multiple of 4")
+    w = _aligned16(weights)
+    R, dim_in = x.shape
+    if order.shape[0] != R or class_start.shape[0] != S + 2:
+        raise ValueError("indexed_block_linear: order must be (R,) and class_start (S + 2,)")
+    od = order.to(torch.int32).contiguous()
+    cs = class_start.to(torch.int32).contiguous()
+    out = x.new_empty(R, out_dim)
+    covered = 0
+    for off, mul, d, woff, segs in _parse_blocks(blocks):
+        if off < 0 or off + d * mul > out_dim or mul <= 0 or d <= 0:
+            raise ValueError("indexed_block_linear: output block outside the result")
+        covered += d * mul
+        if any(c < 0 or ln <= 0 or c + (d - 1) * cp + ln > dim_in for c, cp, ln in segs):
+            raise ValueError("indexed_block_linear: input segment outside the input rows")
+        k = sum(ln for _, _, ln in segs)
+        if segs and (woff < 0 or woff + lib.mnx_block_linear_frag_floats(k, mul) > F):
+            raise ValueError("indexed_block_linear: block weights outside the per-class weights")
+        n = len(segs)
+        cols = (C.c_int64 * max(n, 1))(*[sg[0] for sg in segs])
+        comps = (C.c_int32 * max(n, 1))(*[sg[1] for sg in segs])
+        lens = (C.c_int32 * max(n, 1))(*[sg[2] for sg in segs])
+        wp = w.data_ptr() + 4 * woff if segs else None
+        check(lib.mnx_indexed_block_linear_f32(ptr(x), dim_in, n, cols, comps, lens, wp, F, S, ptr(od), ptr(cs),
+                                               mul, R, d, ptr(out), out_dim, off, mul, _stream(x)),
+              "indexed_block_linear")
+    if covered != out_dim:
+        raise ValueError("indexed_block_linear: output blocks do not cover the result")
+    return out
+
+
+@indexed_block_linear.register_fake
+def _(a, weights, order, class_start, blocks, out_dim):
+    return a.new_empty(a.shape[0], out_dim)
+
+
 # ---------------------------------------------------------------------------
 # Bond vectors
 # ---------------------------------------------------------------------------
@@ -1159,3 +1224,80 @@ bond_vectors.register_autograd(_bond_bwd, setup_context=_bond_setup)
 
 # second-order formulas (autograd of the backward ops): registered on import
 from . import second_order  # noqa: E402,F401
+
+
+# ---------------------------------------------------------------------------
+# Segment sums (molix.F.scatter_sum / batch_add, MessageAggregation)
+# ---------------------------------------------------------------------------
+
+
+def _segment_csr(index: Tensor, num_segments: int, validate: bool) -> tuple[Tensor, Tensor]:
+    """Rows grouped by segment id, ascending row id within a segment: (row_ptr, perm)."""
+    idx = index.to(torch.int64).reshape(-1)
+    row_ptr, perm, _ = edge_csr(torch.stack([idx, idx], dim=1), num_segments, validate)
+    return row_ptr, perm
+
+
+@torch.library.custom_op("molix::segment_sum", mutates_args=(), device_types="cuda")
+def segment_sum(values: Tensor, index: Tensor, num_segments: int, weights: Tensor | None = None,
+                validate: bool = True) -> Tensor:
+    """``out[n] = sum_{r: index[r] = n} weights[r] * values[r]`` for ``values`` (R, D), ``index`` (R,)
+    and ``weights`` (R,) or None: a CSR walk with no atomics and a fixed summation order.  With
+    ``validate`` (one host synchronisation) an index outside ``[0, num_segments)`` raises, as torch's
+    ``scatter_add_`` does; without it such rows are left out."""
+    _require_gpu("segment_sum", values, index, weights)
+    if values.dim() != 2:
+        raise ValueError(f"segment_sum: values must be (rows, D), got {tuple(values.shape)}")
+    v = _f32_rows(values, values.shape[1], "values")
+    if index.dim() != 1 or index.shape[0] != v.shape[0]:
+        raise ValueError(f"segment_sum: index must be ({v.shape[0]},), got {tuple(index.shape)}")
+    w = None if weights is None else _f32_rows(weights, 1, "weights").reshape(-1)
+    if w is not None and w.shape[0] != v.shape[0]:
+        raise ValueError("segment_sum: weights must have one entry per row")
+    out = v.new_empty(num_segments, v.shape[1])
+    row_ptr, perm = _segment_csr(index, num_segments, validate)
+    check(_lib.load().mnx_segment_sum_f32(ptr(v), v.shape[0], v.shape[1], ptr(row_ptr), ptr(perm), ptr(w),
+                                          num_segments, ptr(out), _stream(v)), "segment_sum")
+    return out
+
+
+@segment_sum.register_fake
+def _(values, index, num_segments, weights=None, validate=True):
+    return values.new_empty(num_segments, values.shape[1])
+
+
+@torch.library.custom_op("molix::segment_sum_backward", mutates_args=(), device_types="cuda")
+def segment_sum_backward(grad: Tensor, index: Tensor, values: Tensor, weights: Tensor | None, need_values: bool,
+                         need_weights: bool) -> tuple[Tensor, Tensor]:
+    g = _f32_rows(grad, grad.shape[-1], "grad")
+    v = _f32_rows(values, g.shape[1], "values")
+    idx = index.to(torch.int64).contiguous()
+    w = None if weights is None else _f32_rows(weights, 1, "weights").reshape(-1)
+    gv = torch.empty_like(v) if need_values else v.new_empty(0)
+    gw = v.new_empty(v.shape[0]) if (need_weights and w is not None) else v.new_empty(0)
+    check(_lib.load().mnx_segment_sum_bwd_f32(ptr(g), ptr(idx), ptr(w), ptr(v), v.shape[0], g.shape[1], g.shape[0],
+                                              ptr(gv), ptr(gw), _stream(g)), "segment_sum backward")
+    return gv, gw
+
+
+@segment_sum_backward.register_fake
+def _(grad, index, values, weights, need_values, need_weights):
+    return (torch.empty_like(values) if need_values else values.new_empty(0),
+            values.new_empty(values.shape[0]) if (need_weights and weights is not None) else values.new_empty(0))
+
+
+def _seg_setup(ctx, inputs, output):
+    values, index, num_segments, weights, validate = inputs
+    ctx.save_for_backward(values, index, weights)
+
+
+def _seg_backward(ctx, grad):
+    values, index, weights = ctx.saved_tensors
+    nig = ctx.needs_input_grad  # one flag per argument given (defaults left out)
+    nv, nw = nig[0], len(nig) > 3 and nig[3] and weights is not None
+    gv, gw = segment_sum_backward(grad.contiguous(), index, values, weights, nv, nw)
+    grads = [gv.reshape(values.shape) if nv else None, None, None, gw.reshape(weights.shape) if nw else None, None]
+    return tuple(grads[:len(nig)])
+
+
+segment_sum.register_autograd(_seg_backward, setup_context=_seg_setup)

@@ -95,7 +95,11 @@ class Linear(nn.Module):
         else:
             if weight is None or weight_indices is None:
                 raise ValueError("indexed linear needs weight and weight_indices")
-            out = _IndexedLinear.apply(x2, weight, weight_indices.reshape(-1), self)
+            idx = weight_indices.reshape(-1)
+            if x2.is_cuda and x2.dtype == torch.float32 and weight.dtype == torch.float32 and self._hip_ok():
+                out = _HipIndexedLinear.apply(x2, weight, K.class_groups(idx, self.weight_classes), idx, self)
+            else:
+                out = _IndexedLinear.apply(x2, weight, idx, self)
         return out.reshape(*shape[:-1], self.irreps_out.dim)
 
 
@@ -334,6 +338,63 @@ class _BlockLinear(torch.autograd.Function):
         return gx, gw, None, None
 
 
+def _indexed_weight_grad(x, g, weight, idx, lin):
+    """d<g, indexed linear(x)>/d weight, one block backward per class present (one host
+    synchronisation: training only); nodes of an out-of-range class contribute nothing."""
+    gw = torch.zeros_like(weight)
+    for cls, rows in _class_rows(idx, lin.weight_classes, strict=False):
+        gw[cls] = _block_backward(x[rows], weight[cls].reshape(-1), g[rows], lin.plan, False, True)[1].view_as(gw[cls])
+    return gw
+
+
+class _HipIndexedLinear(torch.autograd.Function):
+    """out = F_z(x, W): each node's rows through its class's weights on the HIP indexed block
+    kernel (nodes grouped by class on the device, no host synchronisation); the input gradient is
+    the same kernel with the transposed weights.  Weight gradients (training) take the per-class
+    torch path."""
+
+    @staticmethod
+    def forward(ctx, x, weight, groups, idx, lin):
+        ws = weight.index_select(1, lin._hip_idx_f.to(weight.device)) * lin._hip_sc_f.to(weight.device)
+        out = torch.ops.molix.indexed_block_linear(x, ws.contiguous(), *groups, lin._hip_plan["fwd"],
+                                                   lin.irreps_out.dim)
+        ctx.save_for_backward(x, weight, idx)
+        ctx.groups, ctx.lin = groups, lin
+        return out
+
+    @staticmethod
+    def backward(ctx, g):
+        x, weight, idx = ctx.saved_tensors
+        need_x, need_w = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
+        g = g.contiguous()
+        gx = _HipIndexedLinearT.apply(g, weight, ctx.groups, idx, ctx.lin) if need_x else None
+        gw = _indexed_weight_grad(x, g, weight, idx, ctx.lin) if need_w else None
+        return gx, gw, None, None, None
+
+
+class _HipIndexedLinearT(torch.autograd.Function):
+    """gx = F_z^T(g, W), the input gradient of ``_HipIndexedLinear``; its own backward (second
+    order) is F_z(ggx, W) for g and the weight gradient with x := ggx for W."""
+
+    @staticmethod
+    def forward(ctx, g, weight, groups, idx, lin):
+        wb = weight.index_select(1, lin._hip_idx_b.to(weight.device)) * lin._hip_sc_b.to(weight.device)
+        gx = torch.ops.molix.indexed_block_linear(g, wb.contiguous(), *groups, lin._hip_plan["bwd"],
+                                                  lin.irreps_in.dim)
+        ctx.save_for_backward(g, weight, idx)
+        ctx.groups, ctx.lin = groups, lin
+        return gx
+
+    @staticmethod
+    def backward(ctx, ggx):
+        g, weight, idx = ctx.saved_tensors
+        need_g, need_w = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
+        ggx = ggx.contiguous()
+        dg = _HipIndexedLinear.apply(ggx, weight, ctx.groups, idx, ctx.lin) if need_g else None
+        dw = _indexed_weight_grad(ggx, g, weight, idx, ctx.lin) if need_w else None
+        return dg, dw, None, None, None
+
+
 class _IndexedLinear(torch.autograd.Function):
     """Rows grouped by class, one block linear per class; gradients written per class rows."""
 
@@ -364,12 +425,15 @@ class _IndexedLinear(torch.autograd.Function):
         return gx, gw, None, None
 
 
-def _class_rows(idx: torch.Tensor, num_classes: int):
-    """Row indices of each class present (one host sync per call)."""
-    if idx.numel() and (int(idx.min()) < 0 or int(idx.max()) >= num_classes):
+def _class_rows(idx: torch.Tensor, num_classes: int, strict: bool = True):
+    """Row indices of each class present (one host sync per call).  ``strict``: an index outside
+    [0, num_classes) raises; otherwise such rows are left out."""
+    if strict and idx.numel() and (int(idx.min()) < 0 or int(idx.max()) >= num_classes):
         raise ValueError(f"weight_indices must lie in [0, {num_classes})")
+    if not strict:
+        idx = torch.where((idx >= 0) & (idx < num_classes), idx, torch.full_like(idx, num_classes))
     order = torch.argsort(idx, stable=True)
-    counts = torch.bincount(idx, minlength=num_classes).tolist()
+    counts = torch.bincount(idx, minlength=num_classes).tolist()[:num_classes]
     start = 0
     for cls, c in enumerate(counts):
         if c:
