@@ -11,7 +11,8 @@ node features and edge vectors.  Metric: M edges/s = E * steps / time.
 
 Prints one JSON line (the driver's contract) with a ``roofline`` object for the
 dominant HIP kernel (timed with HIP events on the stream it runs on) and a
-``cpu_baseline`` (the fp64 NumPy oracle on a bounded sample, rank 0, N=1).
+``cpu_baseline`` (the same step in torch on the host cores, fp32 and fp64, on a
+bounded sample of the graph; rank 0, N=1).
 
     python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu-baseline]
 """
@@ -19,6 +20,7 @@ dominant HIP kernel (timed with HIP events on the stream it runs on) and a
 from __future__ import annotations
 
 import argparse
+import copy
 import json
 import math
 import os
@@ -118,6 +120,9 @@ class EdgeStep:
             p.requires_grad_(False)
         self.mu, self.sigma = (t.to(dev) for t in bessel_stats(5.0, 8))
         self.gout = torch.randn((n_atoms, self.no * C), generator=g).to(dev)
+        from molnex_amd.config import config as mcfg
+
+        self.fused = mcfg.fused_weight_grad and self.K.tp_weight_grad_supported(self.config, C, 64)
 
     def step(self):
         ops = torch.ops.molix
@@ -125,8 +130,15 @@ class EdgeStep:
         row_ptr, perm, snd = ops.edge_csr(self.edge_index, self.N, False)
         Y = ops.spherical_harmonics(self.vec, 3)
         r = torch.linalg.vector_norm(self.vec, dim=-1)
-        w = self.mlp(bessel_cutoff(r, 5.0, 8, self.mu, self.sigma))
-        out = ops.tp_scatter(self.x, Y, w, row_ptr, perm, snd, self.config, self.C)
+        feats = bessel_cutoff(r, 5.0, 8, self.mu, self.sigma)
+        if self.fused:
+            # output layer + TP as one op: the backward forms the weight gradient in registers
+            last = self.mlp.mlp[-1]
+            out, _ = ops.radial_tp(self.x, Y, self.mlp.hidden(feats), last.weight, last.bias, row_ptr, perm, snd,
+                                   self.edge_index, self.config, self.C)
+        else:
+            w = self.mlp(feats)
+            out = ops.tp_scatter(self.x, Y, w, row_ptr, perm, snd, self.config, self.C)
         self.x.grad = None
         self.vec.grad = None
         out.backward(self.gout)
@@ -235,41 +247,86 @@ def mace_step_bytes(enc, N, E):
     return total
 
 
-def cpu_baseline(edge_index, vec, x, C, mlp, mu, sigma, gout, target_s=15.0, max_edges=120_000):
-    """fp64 NumPy oracle (oracle/equivariant.py) on a bounded sample: the edges of the
-    first receivers (in CSR order), fwd + bwd, in chunks until ~target_s of CPU work."""
-    from threadpoolctl import threadpool_limits
+def host_cores() -> int:
+    """Cores this process may use: its affinity set, capped by OMP_NUM_THREADS when that is set."""
+    n = len(os.sched_getaffinity(0))
+    env = os.environ.get("OMP_NUM_THREADS", "")
+    return max(1, min(n, int(env))) if env.isdigit() else n
 
-    from oracle import equivariant as O
 
-    irr = "0e+1o+2e+3o"
-    tp = O.ChannelwiseTP("+".join(f"{C}x{t}" for t in irr.split("+")), irr, irr, C)
-    order = torch.argsort(edge_index[:, 1], stable=True)[:max_edges]
-    with torch.no_grad():
-        v = vec.detach()[order]
-        Ys = O.sh(range(4), v.cpu().double().numpy())
-        ws = mlp(bessel_cutoff(torch.linalg.vector_norm(v, dim=-1), 5.0, 8, mu, sigma)).cpu().double().numpy()
-    ei = edge_index[order].cpu().numpy()
-    recv, ei[:, 1] = np.unique(ei[:, 1], return_inverse=True)
-    xn = x.detach().cpu().double().numpy()
-    gn = gout[torch.from_numpy(recv).to(gout.device)].cpu().double().numpy()
-    done, t_used, chunk = 0, 0.0, 4000
-    with threadpool_limits(1):
-        while t_used < target_s and done < len(ei):
-            sl = slice(done, done + chunk)
-            t0 = time.perf_counter()
-            tp.forward(xn, Ys[sl], ws[sl], ei[sl], len(recv))
-            tp.backward(xn, Ys[sl], ws[sl], ei[sl], gn)
-            t_used += time.perf_counter() - t0
-            done += len(Ys[sl])
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or platform.machine()
+
+
+def cpu_baseline(edge_index, vec, x, C, mlp, mu, sigma, gout, target_s=8.0, chunk_edges=5_000):
+    """The GPU line's step on the host cores, per dtype (fp32, then fp64), on a bounded sample:
+    harmonics + 8-Bessel x cosine cutoff -> the radial MLP -> channelwise TP + scatter, forward and
+    backward to the node features and the edge vectors (torch autograd through the oracle's torch
+    restatement, oracle/mace_ref.py: sh_torch, conv_tp), over receiver-ordered chunks of the
+    config-3 graph (each chunk: the edges of consecutive receivers, with their senders' rows) until
+    ~target_s of CPU time per dtype."""
+    from oracle import mace_ref
+
+    cores = host_cores()
+    prev = torch.get_num_threads()
+    torch.set_num_threads(cores)
+    order = torch.argsort(edge_index[:, 1], stable=True).cpu()
+    ei_all = edge_index.cpu()[order]
+    vec_all = vec.detach().cpu()[order]
+    rates = {}
+    try:
+        for dt in (torch.float32, torch.float64):
+            mlp_c = copy.deepcopy(mlp.mlp).cpu().to(dt)  # the plain Sequential: Linear/SiLU layers
+            mu_c, sig_c = mu.cpu().to(dt), sigma.cpu().to(dt)
+            done, t_used, start, warm = 0, 0.0, 0, True
+            while (t_used < target_s or warm) and start < len(ei_all):
+                ei = ei_all[start:start + chunk_edges]
+                # whole receivers only: stop at the last receiver boundary of the chunk
+                if start + chunk_edges < len(ei_all):
+                    last = int(ei[-1, 1])
+                    ei = ei[ei[:, 1] != last] if (ei[:, 1] != last).any() else ei
+                n_e = len(ei)
+                senders, s_loc = torch.unique(ei[:, 0], return_inverse=True)
+                recv, r_loc = torch.unique(ei[:, 1], return_inverse=True)
+                xs = x.detach()[senders.to(x.device)].cpu().to(dt).requires_grad_(True)
+                v = vec_all[start:start + n_e].to(dt).requires_grad_(True)
+                g = gout[recv.to(gout.device)].cpu().to(dt)
+                t0 = time.perf_counter()
+                r = torch.linalg.vector_norm(v, dim=-1)
+                Y = mace_ref.sh_torch(3, v)
+                w = mlp_c(bessel_cutoff(r, 5.0, 8, mu_c, sig_c))
+                out, _ = mace_ref.conv_tp(xs, Y, w, torch.stack([s_loc, r_loc], 1), len(recv), 3, C)
+                gx, gv = torch.autograd.grad(out, (xs, v), g)
+                dt_chunk = time.perf_counter() - t0
+                start += n_e
+                if warm:
+                    warm = False
+                    continue
+                t_used += dt_chunk
+                done += n_e
+            rates[dt] = (done / t_used / 1e6 if t_used else 0.0, done, t_used)
+    finally:
+        torch.set_num_threads(prev)
+    f32, f64 = rates[torch.float32], rates[torch.float64]
     return {
-        "value": round(done / t_used / 1e6, 6),
+        "value": round(f32[0], 6),
         "unit": "M edges/s",
-        "cores": 1,
+        "cores": cores,
         "kind": "port",
-        "sample": f"{done} edges of the config-3 graph (receiver-ordered prefix), channelwise TP + scatter "
-                  f"forward and backward in fp64 NumPy (oracle/equivariant.py), {t_used:.1f} s on 1 core; "
-                  f"harmonics and MLP weights precomputed",
+        "dtype": "fp32",
+        "fp64_value": round(f64[0], 6),
+        "cpu_model": cpu_model(),
+        "sample": f"the GPU line's step (harmonics, Bessel x cutoff, 8->64->64->{mlp.config.out_dim} SiLU MLP, channelwise "
+                  f"TP + scatter, backward to x and edge vectors) in torch on {cores} host cores over "
+                  f"receiver-ordered chunks of the config-3 graph: fp32 {f32[1]} edges in {f32[2]:.1f} s, fp64 "
+                  f"{f64[1]} edges in {f64[2]:.1f} s (after one warm-up chunk each)",
     }
 
 
@@ -349,6 +406,9 @@ def full_step_bench(args, dev):
     batch = torch.zeros(n, dtype=torch.long, device=dev)
     for p in list(model.parameters()) + list(charge_head.parameters()):
         p.requires_grad_(False)
+    # inference (energy + forces with a fixed model, no second derivatives): eval mode
+    model.eval()
+    charge_head.eval()
 
     def step():
         p = pos.detach().clone().requires_grad_(True)
@@ -615,11 +675,33 @@ def allegro_bench(args, dev, steps=5, warmup=2, reps=5):
             "edge_tp_bwd_hbm_frac": round(bb / tb / 1e6 / HBM_PEAK_GBS, 4)}
 
 
+def unsorted_bench(args, dev, steps=3, warmup=2):
+    """The headline step with the atoms left in random order (no spatial sort): the reference's data
+    path (collate.py:65-177) does not reorder atoms, so sender gathers then hit random rows."""
+    pos, box, edge_index, vec, L = make_system(args.atoms, args.seed, False, dev)
+    N, E = pos.shape[0], edge_index.shape[0]
+    step = EdgeStep(N, edge_index, vec, args.channels, args.seed, dev)
+    for _ in range(warmup):
+        step.step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step.step()
+    torch.cuda.synchronize()
+    dt = (time.perf_counter() - t0) / steps
+    tf, tb = time_tp_kernels(step, reps=3)
+    return {"workload": "config 3 with atoms in random order", "edges": E, "ms_per_step": round(dt * 1e3, 3),
+            "M_edges_per_s": round(E / dt / 1e6, 2), "tp_scatter_fwd_ms": round(tf, 3),
+            "tp_scatter_bwd_ms": round(tb, 3)}
+
+
 def secondary_figures(args, dev):
+    out = {"config3_unsorted_atoms": unsorted_bench(args, dev)}
+    torch.cuda.empty_cache()
     sc = sc_bench(dev)
     nl = nlist_bench(dev)
-    out = {"config2_neighbor_list": nl, "config4_symmetric_contraction": sc,
-           "config5_pme_term": pme_bench(dev)}
+    out.update({"config2_neighbor_list": nl, "config4_symmetric_contraction": sc,
+                "config5_pme_term": pme_bench(dev)})
     for key, lit in (("config5_energy_forces", False), ("config5_literal_energy_forces", True)):
         sub = argparse.Namespace(**{**vars(args), "steps": 3, "warmup": 2, "literal": lit})
         full = full_step_bench(sub, dev)
@@ -711,7 +793,6 @@ def main():
     if not args.no_cpu_baseline:
         step = EdgeStep(N, edge_index, vec, args.channels, args.seed, dev)
         cpu = cpu_baseline(edge_index, step.vec, step.x, args.channels, step.mlp, step.mu, step.sigma, step.gout)
-        cpu["cpu_model"] = platform.processor() or platform.machine()
     line = {
         "metric": "M edges/s TP+scatter (fwd+bwd wrt node features and edge vectors)",
         "value": round(value, 3),

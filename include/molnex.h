@@ -406,6 +406,28 @@ int mnx_edge_weights_bwd_f32(const float* grad_w, int64_t num_edges, int32_t N, 
                              int32_t K, float* grad_h, mnx_stream_t stream);
 
 /* ------------------------------------------------------------------------ */
+/* Fused weight gradient of the tensor product and the output layer of the    */
+/* radial weight MLP (the per-edge weights w[e] = W h[e] + b of               */
+/* src/molrep/interaction/radial_mlp.py:76-82 consumed by ConvTP,             */
+/* tensor_product.py:72-79,101-111):                                          */
+/*   grad_h[e][k] = sum_n gw[e][n] W[n][k],  n = p * C + c,                    */
+/*   gw[e][n] = d<grad_out, tp_scatter(x, Y, w)> / d w[e][n]                   */
+/* without materialising gw (E x num_paths*C): it is produced per edge in     */
+/* registers from x [N][NX*C], Y [E][NY], grad_out [N][NO*C] and the edge's   */
+/* sender / receiver (edge_index int64 [E][2], column 0 = sender) and         */
+/* multiplied on the matrix cores (near-fp32 split-fp16 products, as          */
+/* mnx_edge_weights_bwd_f32).  frag: W [num_paths*C][K] packed by             */
+/* mnx_edge_weights_pack_f32(..., backward = 1).  grad_h [E][K] overwritten.  */
+/* C a multiple of 16, K in {16, 32, 64, 128}.  Together with                 */
+/* mnx_tp_bwd_f32(..., grad_w = NULL) this replaces the TP backward's grad_w  */
+/* and mnx_edge_weights_bwd_f32.                                              */
+/* ------------------------------------------------------------------------ */
+int mnx_tp_weight_grad_f32(int32_t config, int32_t channels, const float* x, const float* Y,
+                           const float* grad_out, const int64_t* edge_index, int64_t num_nodes,
+                           int64_t num_edges, const uint16_t* frag, int32_t K, float* grad_h,
+                           mnx_stream_t stream);
+
+/* ------------------------------------------------------------------------ */
 /* Per-edge channelwise tensor product with shared weights, no scatter: the  */
 /* layer product of Allegro (src/molzoo/allegro.py:352-359, applied at       */
 /* :457-458 to the scaled edge features and the aggregated harmonics of each */

@@ -80,6 +80,7 @@ SIGNATURES = {
     "mnx_edge_weights_pack_f32": (C.c_int, [vp, c_i32, c_i32, c_i32, vp, vp]),
     "mnx_edge_weights_f32": (C.c_int, [vp, c_i64, c_i32, vp, vp, c_i32, vp, vp]),
     "mnx_edge_weights_bwd_f32": (C.c_int, [vp, c_i64, c_i32, vp, c_i32, vp, vp]),
+    "mnx_tp_weight_grad_f32": (C.c_int, [c_i32, c_i32, vp, vp, vp, vp, c_i64, c_i64, vp, c_i32, vp, vp]),
     "mnx_edge_tp_fwd_f32": (C.c_int, [c_i32, c_i32, vp, vp, vp, vp, c_i64, vp, vp]),
     "mnx_edge_tp_bwd_workspace_bytes": (c_sz, [c_i32, c_i32, c_i64]),
     "mnx_edge_tp_bwd_f32": (C.c_int, [c_i32, c_i32, vp, vp, vp, vp, vp, c_i64, vp, vp, vp, vp, vp, c_sz, vp]),

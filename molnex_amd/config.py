@@ -23,6 +23,12 @@ class _Config:
     # edge index lies in [0, num_nodes) -- one host synchronisation per graph; False: trust
     # the indices like the reference's ops (src/molix/F/locality.py:3-5)
     validate_edges: bool = True
+    # True: where the radial MLP's output layer is frozen and no second derivatives are taken
+    # (eval mode), it runs fused with the tensor product (molix::radial_tp): the backward forms
+    # the per-edge weight gradient in registers instead of writing and re-reading it.  Off by
+    # default: on MI355X the fused weight gradient is latency-bound on its per-lane gathers and
+    # slower than writing and re-reading the gradient, except for the 1-path-per-l products
+    fused_weight_grad: bool = False
 
 
 config = _Config()

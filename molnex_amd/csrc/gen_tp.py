@@ -615,13 +615,95 @@ def generate() -> str:
     return "\n".join(out) + "\n"
 
 
-def main():
-    path = os.path.join(HERE, "tp_gen.inc")
-    text = generate()
+# ---------------------------------------------------------------------------
+# Fused weight gradient (tp_gh.hip): per edge lane and path p, the gradient of the
+# per-edge weights for 8 consecutive channels,
+#   gw_p[c] = sum_m3 g[r][o3 + m3][c] * sum_m1 M_p[m3][m1] x[s][o1 + m1][c],
+#   M_p[m3][m1] = sum_m2 c_p[m1, m2, m3] Y[e][o2 + m2]
+# (the same quantity the receiver-walked backward stores as grad_w), produced in
+# registers for the matrix-core product with the output layer's weights.
+# ---------------------------------------------------------------------------
+
+
+def gen_grad_h(cfg: Cfg) -> str:
+    L = []
+    a = L.append
+    a(f"template <> struct TPGH<{cfg.idx}> {{")
+    a(f"  static constexpr int NX = {cfg.NX}, NY = {cfg.NY}, NO = {cfg.NO}, NP = {cfg.NP};")
+    a("  // gw[j] for path p, channels c + j (xr, gr already offset by c); y: the edge's harmonics")
+    a(f"  __device__ static __forceinline__ void gw(int p, const float* __restrict__ xr, "
+      f"const float* __restrict__ gr, int C, const float (&y)[{cfg.NY}], float (&out)[8]) {{")
+    a("    switch (p) {")
+    for p in cfg.paths:
+        c = p["c"]
+        n1, n3 = 2 * p["l1"] + 1, 2 * p["l3"] + 1
+        a(f"      case {p['k']}: {{")
+        a(f"        f32x4 xv[{n1}][2], gv[{n3}][2];")
+        for m1 in range(n1):
+            a(f"        xv[{m1}][0] = *reinterpret_cast<const f32x4*>(xr + {p['o1'] + m1} * C);")
+            a(f"        xv[{m1}][1] = *reinterpret_cast<const f32x4*>(xr + {p['o1'] + m1} * C + 4);")
+        for m3 in range(n3):
+            a(f"        gv[{m3}][0] = *reinterpret_cast<const f32x4*>(gr + {p['o3'] + m3} * C);")
+            a(f"        gv[{m3}][1] = *reinterpret_cast<const f32x4*>(gr + {p['o3'] + m3} * C + 4);")
+        rows = []
+        for m3 in range(n3):
+            row = []
+            for m1 in range(n1):
+                terms = [(m2, c[m1, m2, m3]) for m2 in range(2 * p["l2"] + 1) if abs(c[m1, m2, m3]) > EPS]
+                if not terms:
+                    continue
+                expr = f"{f32(terms[0][1])} * y[{p['o2'] + terms[0][0]}]"
+                for m2, v in terms[1:]:
+                    expr = f"fmaf({f32(v)}, y[{p['o2'] + m2}], {expr})"
+                a(f"        const float M{m3}_{m1} = {expr};")
+                row.append(m1)
+            rows.append(row)
+        a("#pragma unroll")
+        a("        for (int j = 0; j < 8; ++j) {")
+        a("          const int h = j >> 2, i = j & 3;")
+        a("          float acc = 0.f;")
+        for m3, row in enumerate(rows):
+            if not row:
+                continue
+            expr = f"M{m3}_{row[0]} * xv[{row[0]}][h][i]"
+            for m1 in row[1:]:
+                expr = f"fmaf(M{m3}_{m1}, xv[{m1}][h][i], {expr})"
+            a(f"          acc = fmaf(gv[{m3}][h][i], {expr}, acc);")
+        a("          out[j] = acc;")
+        a("        }")
+        a("      } break;")
+    a("      default:")
+    a("#pragma unroll")
+    a("        for (int j = 0; j < 8; ++j) out[j] = 0.f;")
+    a("    }")
+    a("  }")
+    a("};")
+    return "\n".join(L)
+
+
+def generate_gh() -> str:
+    cfgs = [Cfg(i, *c) for i, c in enumerate(config_list())]
+    out = ["// Generated by molnex_amd/csrc/gen_tp.py -- do not edit.",
+           "// Fused tensor-product weight gradient: per-path gw producers (TPGH<config>)."]
+    for cfg in cfgs:
+        out.append(f"// config {cfg.idx}: in l={cfg.in_ls} sh l={cfg.sh_ls} out l={cfg.out_ls}")
+        out.append(gen_grad_h(cfg))
+        out.append("")
+    out.append(f"static constexpr int kNumTPGHConfigs = {len(cfgs)};")
+    return "\n".join(out) + "\n"
+
+
+def _write(path, text):
     old = open(path).read() if os.path.exists(path) else None
     if old != text:
         with open(path, "w") as f:
             f.write(text)
+
+
+def main():
+    path = os.path.join(HERE, "tp_gen.inc")
+    _write(path, generate())
+    _write(os.path.join(HERE, "tp_gh_gen.inc"), generate_gh())
     return path
 
 

@@ -19,6 +19,7 @@ Ops
 ``molix::bond_vectors``         pos[receiver] - pos[sender] - shift per edge, with its position gradient
 ``molix::block_linear``         equivariant (ir_mul) block linear with pre-ordered weights (``cuet.Linear``)
 ``molix::indexed_block_linear`` the block linear with one weight set per node class (ElementUpdate)
+``molix::radial_tp``            radial-MLP output layer + tp_scatter, backward through ``molix::tp_weight_grad``
 ``molix::segment_sum``          weighted segment sum of rows by segment id (scatter_sum / MessageAggregation)
 """
 
@@ -1026,6 +1027,95 @@ def _ew_bwd(ctx, grad):
 
 
 edge_weights.register_autograd(_ew_bwd, setup_context=_ew_setup)
+
+
+# ---------------------------------------------------------------------------
+# Radial-MLP output layer + tensor product, with the fused weight gradient
+# ---------------------------------------------------------------------------
+
+
+def tp_weight_grad_supported(config: int, channels: int, hidden: int) -> bool:
+    """Whether ``molix::tp_weight_grad`` takes this configuration, channel count and hidden width."""
+    return config >= 0 and channels % 16 == 0 and hidden in (16, 32, 64, 128)
+
+
+@torch.library.custom_op("molix::tp_weight_grad", mutates_args=(), device_types="cuda")
+def tp_weight_grad(x: Tensor, Y: Tensor, grad_out: Tensor, edge_index: Tensor, weight: Tensor, config: int,
+                   channels: int) -> Tensor:
+    """``grad_h = gw @ weight`` for the per-edge weights ``w = h @ weight.T + b`` of a
+    ``tp_scatter``: the weight gradient ``gw = d<grad_out, tp_scatter(x, Y, w)>/dw`` is formed per
+    edge in registers and multiplied on the matrix cores, never written (``weight`` is the output
+    layer's (num_paths * C, K) matrix)."""
+    _require_gpu("tp_weight_grad", x, Y, grad_out, edge_index, weight)
+    num_paths, nx, ny, no = tp_config_info(config)
+    Nw, K = weight.shape
+    if Nw != num_paths * channels:
+        raise ValueError(f"tp_weight_grad: weight has {Nw} rows, the product has {num_paths} x {channels}")
+    xs = _aligned16(_f32_rows(x, nx * channels, "x"))
+    Ys = _f32_rows(Y, ny, "Y")
+    go = _aligned16(_f32_rows(grad_out, no * channels, "grad_out"))
+    ei = edge_index.to(torch.int64).contiguous()
+    if ei.dim() != 2 or ei.shape[1] != 2 or ei.shape[0] != Ys.shape[0] or go.shape[0] != xs.shape[0]:
+        raise ValueError("tp_weight_grad: inconsistent sizes of x / Y / grad_out / edge_index")
+    frag = _ew_frag(weight, True)
+    gh = xs.new_empty(Ys.shape[0], K)
+    check(_lib.load().mnx_tp_weight_grad_f32(config, channels, ptr(xs), ptr(Ys), ptr(go), ptr(ei), xs.shape[0],
+                                             Ys.shape[0], ptr(frag), K, ptr(gh), _stream(xs)), "tp_weight_grad")
+    return gh
+
+
+@tp_weight_grad.register_fake
+def _(x, Y, grad_out, edge_index, weight, config, channels):
+    return x.new_empty(Y.shape[0], weight.shape[1])
+
+
+@torch.library.custom_op("molix::radial_tp", mutates_args=(), device_types="cuda")
+def radial_tp(x: Tensor, Y: Tensor, h: Tensor, weight: Tensor, bias: Tensor | None, row_ptr: Tensor, perm: Tensor,
+              senders: Tensor, edge_index: Tensor, config: int, channels: int) -> tuple[Tensor, Tensor]:
+    """``tp_scatter(x, Y, w)`` with ``w = h @ weight.T + bias`` (the radial MLP's output layer,
+    ``radial_mlp.py:76-82``, feeding ConvTP, ``tensor_product.py:72-79,101-111``).  Returns
+    ``(out, w)``; ``w`` is kept for the backward, whose gradient with respect to ``h`` comes from
+    ``tp_weight_grad`` (the per-edge weight gradient is never materialised) and whose tensor-product
+    backward skips the weight gradient.  The output layer's parameters get no gradient here."""
+    w = edge_weights(h, weight, bias)
+    out = tp_scatter(x, Y, w, row_ptr, perm, senders, config, channels)
+    return out, w
+
+
+@radial_tp.register_fake
+def _(x, Y, h, weight, bias, row_ptr, perm, senders, edge_index, config, channels):
+    num_paths, nx, ny, no = tp_config_info(config)
+    return x.new_empty((row_ptr.shape[0] - 1, no * channels)), h.new_empty((h.shape[0], weight.shape[0]))
+
+
+def _rtp_setup(ctx, inputs, output):
+    x, Y, h, weight, bias, row_ptr, perm, senders, edge_index, config, channels = inputs
+    ctx.save_for_backward(x, Y, h, weight, output[1], row_ptr, perm, senders, edge_index)
+    ctx.config, ctx.channels = config, channels
+
+
+def _rtp_backward(ctx, g_out, g_w):
+    x, Y, h, weight, w, row_ptr, perm, senders, edge_index = ctx.saved_tensors
+    nig = ctx.needs_input_grad
+    if nig[3] or nig[4]:
+        raise RuntimeError("molix::radial_tp gives no gradient for the output layer's weight and bias; use the "
+                           "separate edge_weights + tp_scatter ops when they are trained")
+    need_x, need_Y, need_h = nig[0], nig[1], nig[2]
+    gx = gY = gh = None
+    if g_out is not None and (need_x or need_Y):
+        gx, gY, _ = tp_scatter_backward(g_out.contiguous(), x, Y, w, row_ptr, perm, senders, ctx.config,
+                                        ctx.channels, need_x, need_Y, False)
+        gx = gx.reshape(x.shape) if need_x else None
+        gY = gY.reshape(Y.shape) if need_Y else None
+    if need_h:
+        gh = (tp_weight_grad(x, Y, g_out.contiguous(), edge_index, weight, ctx.config, ctx.channels)
+              if g_out is not None else torch.zeros_like(h))
+        if g_w is not None:  # a caller that used the returned weights as well
+            gh = gh + edge_weights_backward(g_w.contiguous(), weight)
+    return gx, gY, gh, None, None, None, None, None, None, None, None
+
+
+radial_tp.register_autograd(_rtp_backward, setup_context=_rtp_setup)
 
 
 # ---------------------------------------------------------------------------

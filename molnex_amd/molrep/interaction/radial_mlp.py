@@ -94,15 +94,19 @@ class RadialWeightMLP(nn.Module):
         c = self.config
         return kernels.radial_supported(c.in_dim, c.hidden_dim, c.num_layers)
 
-    def forward(self, edge_feats: torch.Tensor) -> torch.Tensor:
+    def hidden(self, edge_feats: torch.Tensor) -> torch.Tensor:
+        """The activations fed to the output layer: ``mlp[:-1](edge_feats)``."""
         h = edge_feats
         if self._fused_hidden(h):
             c = self.config
             raw = torch.cat([t.detach().reshape(-1) for m in self.mlp[:-1:2] for t in (m.weight, m.bias)])
-            h = kernels.radial_hidden(h, raw, c.in_dim, c.hidden_dim, c.num_layers)
-        else:
-            for layer in self.mlp[:-1]:
-                h = layer(h)
+            return kernels.radial_hidden(h, raw, c.in_dim, c.hidden_dim, c.num_layers)
+        for layer in self.mlp[:-1]:
+            h = layer(h)
+        return h
+
+    def forward(self, edge_feats: torch.Tensor) -> torch.Tensor:
+        h = self.hidden(edge_feats)
         last = self.mlp[-1]
         if (config.edge_weights_kernel and h.is_cuda and h.dim() == 2 and h.dtype == torch.float32
                 and last.weight.dtype == torch.float32

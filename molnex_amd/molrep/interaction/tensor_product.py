@@ -141,6 +141,28 @@ class ConvTP(nn.Module):
         g = edge_graph(edge_index, node_features.shape[0])
         return self.cue_tp.apply_graph(node_features, edge_angular, tp_weights, g)
 
+    def forward_radial(self, node_features: torch.Tensor, edge_angular: torch.Tensor, edge_index: torch.Tensor,
+                       radial_mlp, edge_feats: torch.Tensor) -> torch.Tensor:
+        """``forward(..., tp_weights=radial_mlp(edge_feats))`` (the composition of mace.py:321-332).
+        When the output layer's parameters need no gradient (energy + forces with a fixed model) and
+        no second derivatives are taken (eval mode), its weights and the product run as
+        ``molix::radial_tp``, whose backward forms the per-edge weight gradient in registers
+        (``molix::tp_weight_grad``) instead of writing and re-reading it."""
+        last = radial_mlp.mlp[-1]
+        x = node_features
+        if (config.fused_weight_grad and not self.training and x.is_cuda and x.dtype == torch.float32
+                and not config.deterministic and not last.weight.requires_grad
+                and (last.bias is None or not last.bias.requires_grad)
+                and K.tp_weight_grad_supported(self.cue_tp.config_id, self.cue_tp.channels, last.in_features)
+                and K.edge_weights_supported(last.in_features, last.out_features)):
+            h = radial_mlp.hidden(edge_feats)
+            g = edge_graph(edge_index, x.shape[0])
+            out, _ = torch.ops.molix.radial_tp(x, edge_angular, h, last.weight, last.bias, g.row_ptr, g.perm,
+                                               g.senders, g.edge_index, self.cue_tp.config_id,
+                                               self.cue_tp.channels)
+            return out
+        return self.forward(x, edge_angular, edge_index, radial_mlp(edge_feats))
+
 
 def irreps_from_l_max(l_max: int, hidden_dim: int) -> str:
     return _irreps_from_l_max(l_max, hidden_dim)

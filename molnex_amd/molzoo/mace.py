@@ -113,9 +113,7 @@ class InteractionBlock(nn.Module):
     def forward(self, node_feats, edge_attrs, edge_feats, edge_index):
         sc = node_feats
         node_feats_up = self.node_linear(node_feats)
-        tp_weights = self.radial_mlp(edge_feats)
-        messages = self.conv_tp(node_features=node_feats_up, edge_angular=edge_attrs, edge_index=edge_index,
-                                tp_weights=tp_weights)
+        messages = self.conv_tp.forward_radial(node_feats_up, edge_attrs, edge_index, self.radial_mlp, edge_feats)
         # linear(messages / avg) == linear(messages) / avg; scaling the linear's output
         # touches (nodes x hidden) values instead of (nodes x TP-output) ones
         return self.linear(messages) / self.avg_num_neighbors, sc

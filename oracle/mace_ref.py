@@ -69,7 +69,7 @@ def conv_tp(x, Y, w, edge_index, num_nodes, l_max, C, in_ls=None):
     out = x.new_zeros(num_nodes, tp.no, C)
     for k, p in enumerate(tp.paths):
         s1, s2, s3 = tp._blocks(k)
-        cf = torch.from_numpy(np.ascontiguousarray(tp._coef(p)))
+        cf = torch.from_numpy(np.ascontiguousarray(tp._coef(p))).to(x.dtype)
         msg = torch.einsum("abc,eaC,eb,eC->ecC", cf, xs[:, s1][s], Y[:, s2], w3[:, k])
         out[:, s3] = out[:, s3].index_add(0, r, msg)
     return out.reshape(num_nodes, -1), tp
