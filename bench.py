@@ -561,7 +561,11 @@ def sc_bench(dev, reps=10):
     mix = Linear(f"{C}x0e+{C}x1o", f"{C}x0e+{C}x1o").to(dev)
     gout = torch.randn((N, 4 * C), generator=g).to(dev)
 
+    params = [A, *sc.parameters(), *mix.parameters()]
+
     def step():
+        for p in params:  # a training step's zero_grad(set_to_none=True): no accumulation adds
+            p.grad = None
         out = mix(sc(A, z))
         out.backward(gout)
 

@@ -140,6 +140,19 @@ int mnx_segment_sum_bwd_f32(const float* grad_out, const int64_t* index, const f
                             int64_t num_rows, int32_t dim, int64_t num_segments, float* grad_values,
                             float* grad_weights, mnx_stream_t stream);
 
+/* Nodes grouped by class (a stable counting sort; no atomics, no host sync):
+ * order [num_nodes] = node ids, classes ascending (classes outside
+ * [0, num_classes) last, as class num_classes), ascending node id within a
+ * class; class_start [num_classes + 2] = where each class begins in order.
+ * The grouping that cuet.Linear(weight_classes=S, method="indexed_linear")
+ * (src/molrep/interaction/element_update.py:101-109) and the per-element
+ * weights of cuet.SymmetricContraction (symmetric_contraction.py:100-109)
+ * need; replaces the torch.argsort of node elements. */
+#define MNX_CLASS_GROUPS_MAX_CLASSES 4096
+size_t mnx_class_groups_workspace_bytes(int64_t num_nodes, int32_t num_classes);
+int mnx_class_groups(const int64_t* classes, int64_t num_nodes, int32_t num_classes, int32_t* order,
+                     int32_t* class_start, void* workspace, size_t workspace_bytes, mnx_stream_t stream);
+
 /* ------------------------------------------------------------------------ */
 /* Real spherical harmonics, component normalisation, l <= 3, input vectors   */
 /* normalised inside (replaces cuet.SphericalHarmonics(ls, normalize=True),   */

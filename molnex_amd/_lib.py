@@ -35,6 +35,8 @@ SIGNATURES = {
     "mnx_csr_build": (C.c_int, [vp, c_i64, c_i64, vp, vp, vp, vp, vp, c_sz, vp]),
     "mnx_csr_build_noalloc": (C.c_int, [vp, c_i64, c_i64, vp, vp, vp, vp, vp]),
     "mnx_segment_sum_f32": (C.c_int, [vp, c_i64, c_i32, vp, vp, vp, c_i64, vp, vp]),
+    "mnx_class_groups_workspace_bytes": (c_sz, [c_i64, c_i32]),
+    "mnx_class_groups": (C.c_int, [vp, c_i64, c_i32, vp, vp, vp, c_sz, vp]),
     "mnx_segment_sum_bwd_f32": (C.c_int, [vp, vp, vp, vp, c_i64, c_i32, c_i64, vp, vp, vp]),
     "mnx_sh_fwd_f32": (C.c_int, [vp, c_i64, c_i32, vp, vp]),
     "mnx_sh_bwd_f32": (C.c_int, [vp, vp, c_i64, c_i32, vp, vp]),

@@ -120,6 +120,120 @@ __global__ void __launch_bounds__(kSegThreads) k_segment_sum_bwd(const float* __
     }
 }
 
+// ---------------------------------------------------------------------------
+// Class grouping: a stable counting sort of node ids by a small class id (the
+// element of each node; classes outside [0, S) form class S), giving the node
+// order and class boundaries that the element-indexed linear and the symmetric
+// contraction's weight gradient walk.  One wavefront per segment of
+// kGroupSeg consecutive nodes, 64 nodes per step in ascending order; within a
+// step each distinct class present is handled by one ballot (rank = number of
+// lower lanes of the same class), so the order within a class is ascending
+// node id.  Three launches: per-segment class counts, an exclusive scan of
+// the (class, segment) counts in class-major order, and the placement.  Every
+// workspace entry is written before it is read: no clearing is needed.
+// ---------------------------------------------------------------------------
+
+constexpr int kGroupSeg = 1024;
+constexpr int kGroupScanThreads = 1024;
+
+__device__ __forceinline__ int node_class(const int64_t* __restrict__ cls, int64_t i, int S) {
+    const int64_t c = cls[i];
+    return c >= 0 && c < S ? int(c) : S;
+}
+
+// fn(class, lanes of that class in this step, rank of this lane among them) for each distinct class
+// present among the active lanes of one 64-node step
+template <typename Fn>
+__device__ __forceinline__ void for_each_class(bool active, int c, Fn fn) {
+    const int lane = threadIdx.x & (kWave - 1);
+    const uint64_t below = (uint64_t(1) << lane) - 1;
+    uint64_t todo = __ballot(active);  // wave-uniform: the loop and the barriers inside fn are uniform
+    while (todo) {
+        const int first = __ffsll((unsigned long long)todo) - 1;
+        const int lc = __shfl(c, first);
+        const bool mine = active && c == lc;
+        const uint64_t mask = __ballot(mine);
+        fn(lc, __popcll(mask), mine, __popcll(mask & below));
+        todo &= ~mask;
+    }
+}
+
+__global__ void __launch_bounds__(kWave) k_group_count(const int64_t* __restrict__ cls, int64_t n, int S,
+                                                       int64_t nseg, int32_t* __restrict__ counts) {
+    extern __shared__ int32_t cnt[];
+    const int64_t seg = blockIdx.x;
+    for (int s = threadIdx.x; s <= S; s += kWave) cnt[s] = 0;
+    __syncthreads();
+    const int64_t b = seg * kGroupSeg, e = min(b + kGroupSeg, n);
+    for (int64_t i0 = b; i0 < e; i0 += kWave) {
+        const int64_t i = i0 + threadIdx.x;
+        const bool active = i < e;
+        const int c = active ? node_class(cls, i, S) : 0;
+        for_each_class(active, c, [&](int lc, int num, bool, int) {
+            if (threadIdx.x == 0) cnt[lc] += num;
+            __syncthreads();
+        });
+    }
+    __syncthreads();
+    for (int s = threadIdx.x; s <= S; s += kWave) counts[int64_t(s) * nseg + seg] = cnt[s];
+}
+
+// exclusive scan of counts[(S+1) * nseg] in place (one workgroup); class_start[s] = counts[s * nseg]
+// after the scan, class_start[S + 1] = n
+__global__ void __launch_bounds__(kGroupScanThreads) k_group_scan(int32_t* __restrict__ counts, int64_t len,
+                                                                  int64_t nseg, int S, int64_t n,
+                                                                  int32_t* __restrict__ class_start) {
+    __shared__ int32_t part[kGroupScanThreads];
+    const int t = threadIdx.x;
+    const int64_t per = (len + kGroupScanThreads - 1) / kGroupScanThreads;
+    const int64_t b = min(int64_t(t) * per, len), e = min(b + per, len);
+    int32_t sum = 0;
+    for (int64_t i = b; i < e; ++i) sum += counts[i];
+    part[t] = sum;
+    __syncthreads();
+    for (int off = 1; off < kGroupScanThreads; off <<= 1) {  // Hillis-Steele inclusive scan of the partials
+        const int32_t v = t >= off ? part[t - off] : 0;
+        __syncthreads();
+        part[t] += v;
+        __syncthreads();
+    }
+    int32_t run = part[t] - sum;
+    for (int64_t i = b; i < e; ++i) {
+        const int32_t v = counts[i];
+        counts[i] = run;
+        run += v;
+    }
+    __syncthreads();
+    if (nseg == 0) {
+        for (int s = t; s <= S + 1; s += kGroupScanThreads) class_start[s] = 0;
+        return;
+    }
+    for (int s = t; s <= S; s += kGroupScanThreads) class_start[s] = counts[int64_t(s) * nseg];
+    if (t == 0) class_start[S + 1] = int32_t(n);
+}
+
+__global__ void __launch_bounds__(kWave) k_group_place(const int64_t* __restrict__ cls, int64_t n, int S,
+                                                       int64_t nseg, const int32_t* __restrict__ offsets,
+                                                       int32_t* __restrict__ order) {
+    extern __shared__ int32_t base[];
+    const int64_t seg = blockIdx.x;
+    for (int s = threadIdx.x; s <= S; s += kWave) base[s] = offsets[int64_t(s) * nseg + seg];
+    __syncthreads();
+    const int64_t b = seg * kGroupSeg, e = min(b + kGroupSeg, n);
+    for (int64_t i0 = b; i0 < e; i0 += kWave) {
+        const int64_t i = i0 + threadIdx.x;
+        const bool active = i < e;
+        const int c = active ? node_class(cls, i, S) : 0;
+        for_each_class(active, c, [&](int lc, int num, bool mine, int rank) {
+            const int32_t at = base[lc];
+            if (mine) order[at + rank] = int32_t(i);
+            __syncthreads();
+            if (threadIdx.x == 0) base[lc] = at + num;
+            __syncthreads();
+        });
+    }
+}
+
 }  // namespace
 }  // namespace mnx
 
@@ -164,6 +278,40 @@ int mnx_segment_sum_bwd_f32(const float* grad_out, const int64_t* index, const f
                        stream, grad_out, index, weights, values, num_rows, int64_t(dim), num_segments, grad_values,
                        grad_weights);
     MNX_CHECK_LAUNCH();
+    return MNX_OK;
+}
+
+size_t mnx_class_groups_workspace_bytes(int64_t num_nodes, int32_t num_classes) {
+    if (num_nodes < 0 || num_classes < 0) return 0;
+    return size_t(ceil_div(num_nodes, int64_t(kGroupSeg))) * size_t(num_classes + 1) * sizeof(int32_t) + 256;
+}
+
+int mnx_class_groups(const int64_t* classes, int64_t num_nodes, int32_t num_classes, int32_t* order,
+                     int32_t* class_start, void* workspace, size_t workspace_bytes, mnx_stream_t stream_) {
+    clear_error();
+    hipStream_t stream = (hipStream_t)stream_;
+    MNX_REQUIRE(num_nodes >= 0 && num_nodes < (int64_t(1) << 31), "num_nodes out of range");
+    MNX_REQUIRE(num_classes >= 0 && num_classes <= MNX_CLASS_GROUPS_MAX_CLASSES, "num_classes %d not in [0, %d]",
+                num_classes, MNX_CLASS_GROUPS_MAX_CLASSES);
+    MNX_REQUIRE(class_start && (num_nodes == 0 || (classes && order)), "null pointer argument");
+    const size_t need = mnx_class_groups_workspace_bytes(num_nodes, num_classes);
+    MNX_REQUIRE(workspace && workspace_bytes >= need, "workspace %zu < %zu bytes", workspace_bytes, need);
+    const int64_t nseg = ceil_div(num_nodes, int64_t(kGroupSeg));
+    const size_t lds = size_t(num_classes + 1) * sizeof(int32_t);
+    int32_t* counts = static_cast<int32_t*>(workspace);
+    if (nseg > 0) {
+        hipLaunchKernelGGL(k_group_count, dim3(unsigned(nseg)), dim3(kWave), lds, stream, classes, num_nodes,
+                           int(num_classes), nseg, counts);
+        MNX_CHECK_LAUNCH();
+    }
+    hipLaunchKernelGGL(k_group_scan, dim3(1), dim3(kGroupScanThreads), 0, stream, counts,
+                       nseg * (num_classes + 1), nseg, int(num_classes), num_nodes, class_start);
+    MNX_CHECK_LAUNCH();
+    if (nseg > 0) {
+        hipLaunchKernelGGL(k_group_place, dim3(unsigned(nseg)), dim3(kWave), lds, stream, classes, num_nodes,
+                           int(num_classes), nseg, counts, order);
+        MNX_CHECK_LAUNCH();
+    }
     return MNX_OK;
 }
 

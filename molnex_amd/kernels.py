@@ -788,7 +788,7 @@ def symmetric_contraction_backward(grad: Tensor, x: Tensor, atom_types: Tensor, 
     z = atom_types.to(torch.int64).reshape(-1).contiguous()
     w = weight.contiguous()
     # nodes grouped by element: one weight-gradient flush per element run
-    order = torch.argsort(z, stable=True).to(torch.int32) if need_w else None
+    order = class_groups(z, S)[0] if need_w else None
     gx = torch.empty_like(xs) if need_x else xs.new_empty(0)
     gw = torch.zeros_like(w) if need_w else w.new_empty(0)
     check(_lib.load().mnx_sc_bwd_f32(cfg, ptr(xs), ptr(z), ptr(w), ptr(g), ptr(order), xs.shape[0], Cc, S,
@@ -818,7 +818,7 @@ def symmetric_contraction_backward2(grad: Tensor, x: Tensor, atom_types: Tensor,
     sw = None if seed_w is None else seed_w.to(torch.float32).contiguous()
     z = atom_types.to(torch.int64).reshape(-1).contiguous()
     w = weight.contiguous()
-    order = torch.argsort(z, stable=True).to(torch.int32) if need_w else None
+    order = class_groups(z, S)[0] if need_w else None
     dg = torch.empty_like(g) if need_grad else g.new_empty(0)
     dx = torch.empty_like(xs) if need_x else xs.new_empty(0)
     dw = torch.zeros_like(w) if need_w else w.new_empty(0)
@@ -1192,11 +1192,16 @@ def class_groups(classes: Tensor, num_classes: int) -> tuple[Tensor, Tensor]:
     ascending node id within a class, out-of-range classes last) and ``class_start`` (int32,
     ``num_classes + 2`` entries: where class s begins in ``order``, s = num_classes being the
     out-of-range nodes)."""
-    c = classes.reshape(-1).to(torch.int64)
-    key = torch.where((c >= 0) & (c < num_classes), c, torch.full_like(c, num_classes))
-    order = torch.argsort(key, stable=True).to(torch.int32)
-    counts = torch.zeros(num_classes + 1, dtype=torch.int64, device=c.device).scatter_add_(0, key, torch.ones_like(key))
-    class_start = torch.cat([counts.new_zeros(1), torch.cumsum(counts, 0)]).to(torch.int32)
+    if classes.device.type != "cuda":
+        raise RuntimeError(f"molix::class_groups runs on the GPU only (got a {classes.device} tensor)")
+    lib = _lib.load()
+    c = classes.reshape(-1).to(torch.int64).contiguous()
+    n = c.shape[0]
+    order = torch.empty(n, dtype=torch.int32, device=c.device)
+    class_start = torch.empty(num_classes + 2, dtype=torch.int32, device=c.device)
+    ws = _ws(lib.mnx_class_groups_workspace_bytes(n, num_classes), c.device)
+    check(lib.mnx_class_groups(ptr(c), n, num_classes, ptr(order), ptr(class_start), ptr(ws), ws.numel(),
+                               _stream(c)), "class_groups")
     return order, class_start
 
 
