@@ -31,6 +31,8 @@
 // [q][tile][plane][lane][8], with one scale per output row.  The first layer
 // (K = the few radial features) stays on fp32 MFMAs.
 
+#include <algorithm>
+
 #include "common.h"
 
 namespace mnx {
@@ -93,11 +95,12 @@ __device__ __forceinline__ int rad_exp(float m) {
     return min(max(ilogbf(m), -126), 126);
 }
 
-// Row scales of the split blocks, one thread per row: forward layer j >= 1 row m is
-// W_j[m][:], backward layer j row m is column m of W_j (W_j^T[m][:]); rows past the
-// layer (padding of the last tile) get 1.
+// Row scales of the split blocks, one wavefront per row: forward layer j >= 1 row m
+// is W_j[m][:], backward layer j row m is column m of W_j (W_j^T[m][:]); rows past
+// the layer (padding of the last tile) get 1.
 __global__ void k_radial_scales(const float* __restrict__ raw, RadLayout lay, float* __restrict__ frag) {
-    const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    const int lane = threadIdx.x & 63;
+    const int64_t i = (int64_t(blockIdx.x) * blockDim.x + threadIdx.x) >> 6;
     const int64_t n = lay.scales_total();
     if (i >= n) return;
     const int64_t o = lay.fscale_off(1) + i;
@@ -105,7 +108,7 @@ __global__ void k_radial_scales(const float* __restrict__ raw, RadLayout lay, fl
     if (o < lay.bscale_off(0)) {  // forward layer j >= 1
         const int j = 1 + int(i / lay.H), row = int(i % lay.H);
         const float* W = raw + lay.raw_w(j);
-        for (int f = 0; f < lay.H; ++f) m = fmaxf(m, fabsf(W[int64_t(row) * lay.H + f]));
+        for (int f = lane; f < lay.H; f += 64) m = fmaxf(m, fabsf(W[int64_t(row) * lay.H + f]));
     } else {
         int j = 0;
         while (o >= lay.bscale_off(j + 1)) ++j;
@@ -113,9 +116,11 @@ __global__ void k_radial_scales(const float* __restrict__ raw, RadLayout lay, fl
         const int kraw = j == 0 ? lay.kin : lay.H;
         const float* W = raw + lay.raw_w(j);
         if (row < kraw)
-            for (int f = 0; f < lay.H; ++f) m = fmaxf(m, fabsf(W[int64_t(f) * kraw + row]));
+            for (int f = lane; f < lay.H; f += 64) m = fmaxf(m, fabsf(W[int64_t(f) * kraw + row]));
     }
-    frag[o] = ldexpf(1.f, rad_exp(m));
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+    if (lane == 0) frag[o] = ldexpf(1.f, rad_exp(m));
 }
 
 // Builds the fragment buffer from the raw parameters and the row scales (already in
@@ -204,6 +209,62 @@ __device__ __forceinline__ void stage(const float* __restrict__ src, int n, f32x
     for (int i = threadIdx.x; i < n / 4; i += kRadThreads) dst[i] = s4[i];
 }
 
+// Exponent of the lane's activation column (largest magnitude over both lane
+// halves, i.e. the whole edge) for the split of a layer's B operand.
+template <int NQ>
+__device__ __forceinline__ int column_exp(const float (&in)[NQ / 2][16]) {
+    float m = 0.f;
+#pragma unroll
+    for (int t = 0; t < NQ / 2; ++t)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) m = fmaxf(m, fabsf(in[t][r]));
+    m = fmaxf(m, __shfl_xor(m, 32));
+    return rad_exp(m);
+}
+
+// k-steps q0 .. q0 + QN - 1 (those below NQ) of a split-fp16 layer: fragments fr
+// (LDS, k-step q0 first, [QN][T][2][64 lanes] f32x4 of 8 fp16), activations in
+// the D layout scaled by sinv before the split.
+template <int T, int NQ, int QN>
+__device__ __forceinline__ void mfma_steps(const f32x4* __restrict__ fr, int q0, const float (&in)[NQ / 2][16],
+                                           float sinv, f32x16 (&acc)[T], int lane) {
+#pragma unroll
+    for (int qq = 0; qq < QN; ++qq) {
+        const int q = q0 + qq;
+        if (q >= NQ) break;
+        f16x8 b0, b1;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const float v = in[q / 2][8 * (q % 2) + j] * sinv;
+            const _Float16 h0 = (_Float16)v;
+            b0[j] = h0;
+            b1[j] = (_Float16)(v - (float)h0);
+        }
+        auto a = [&](int t, int p) { return __builtin_bit_cast(f16x8, fr[((qq * T + t) * 2 + p) * 64 + lane]); };
+#pragma unroll
+        for (int t = 0; t < T; ++t) acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a(t, 1), b0, acc[t], 0, 0, 0);
+#pragma unroll
+        for (int t = 0; t < T; ++t) acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a(t, 0), b1, acc[t], 0, 0, 0);
+#pragma unroll
+        for (int t = 0; t < T; ++t) acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a(t, 0), b0, acc[t], 0, 0, 0);
+    }
+}
+
+// Undoes the column scale 2^-ex and the weight row scales rscale on the accumulator.
+template <int T>
+__device__ __forceinline__ void unscale(const float* __restrict__ rscale, int ex, f32x16 (&acc)[T], int lane) {
+    const float so = ldexpf(1.f, ex);
+    const int half = lane >> 5;
+#pragma unroll
+    for (int t = 0; t < T; ++t)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const f32x4 rs = *reinterpret_cast<const f32x4*>(rscale + 32 * t + 8 * g + 4 * half);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[t][4 * g + i] = acc[t][4 * g + i] * so * rs[i];
+        }
+}
+
 // acc[t] = W(tile t) . in over K = 16 * NQ features held in the D layout as
 // in[q/2][8(q%2) + j] for k-step q (split-fp16 products, see the top of the file),
 // acc zero on entry.  The layer's fragments f ([NQ][T][2][64 lanes][8 fp16]) are
@@ -218,50 +279,67 @@ __device__ __forceinline__ void mfma_layer(const float* __restrict__ f, const fl
     constexpr int kStep = T * kX2Block;  // floats per k-step
     constexpr int kQPC = kRadChunk / kStep < NQ ? kRadChunk / kStep : NQ;  // k-steps per chunk
     static_assert(kQPC >= 1, "one k-step of fragments must fit the staging area");
-    float m = 0.f;
-#pragma unroll
-    for (int t = 0; t < NQ / 2; ++t)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) m = fmaxf(m, fabsf(in[t][r]));
-    m = fmaxf(m, __shfl_xor(m, 32));
-    const int ex = rad_exp(m);
+    const int ex = column_exp<NQ>(in);
     const float sinv = ldexpf(1.f, -ex);
 #pragma unroll
     for (int q0 = 0; q0 < NQ; q0 += kQPC) {
         __syncthreads();
         stage(f + q0 * kStep, (NQ - q0 < kQPC ? NQ - q0 : kQPC) * kStep, sh.frag);
         __syncthreads();
-#pragma unroll
-        for (int qq = 0; qq < kQPC; ++qq) {
-            const int q = q0 + qq;
-            if (q >= NQ) break;
-            f16x8 b0, b1;
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const float v = in[q / 2][8 * (q % 2) + j] * sinv;
-                const _Float16 h0 = (_Float16)v;
-                b0[j] = h0;
-                b1[j] = (_Float16)(v - (float)h0);
-            }
-            auto a = [&](int t, int p) { return __builtin_bit_cast(f16x8, sh.frag[((qq * T + t) * 2 + p) * 64 + lane]); };
-#pragma unroll
-            for (int t = 0; t < T; ++t) acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a(t, 1), b0, acc[t], 0, 0, 0);
-#pragma unroll
-            for (int t = 0; t < T; ++t) acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a(t, 0), b1, acc[t], 0, 0, 0);
-#pragma unroll
-            for (int t = 0; t < T; ++t) acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a(t, 0), b0, acc[t], 0, 0, 0);
-        }
+        mfma_steps<T, NQ, kQPC>(sh.frag, q0, in, sinv, acc, lane);
     }
-    const float so = ldexpf(1.f, ex);
-    const int half = lane >> 5;
+    unscale<T>(rscale, ex, acc, lane);
+}
+
+// The same product with the whole layer's fragments resident in LDS (no barriers).
+// Software-pipelined one k-step ahead: the fragments of k-step q + 1 are read and
+// its activations split while the matrix cores work on k-step q (two register
+// buffers each).  At four row tiles a scheduling barrier per k-step keeps the
+// compiler from hoisting every k-step's reads to the top (which costs ~256
+// registers at one wavefront per SIMD); narrower layers leave it free.
+template <int T, int NQ>
+__device__ __forceinline__ void mfma_layer_res(const f32x4* __restrict__ fr, const float* __restrict__ rscale,
+                                               const float (&in)[NQ / 2][16], f32x16 (&acc)[T], int lane) {
+    const int ex = column_exp<NQ>(in);
+    const float sinv = ldexpf(1.f, -ex);
+    f32x4 buf[2][T][2];
+    f16x8 b0[2], b1[2];
+    auto fetch = [&](int q) {
 #pragma unroll
-    for (int t = 0; t < T; ++t)
+        for (int t = 0; t < T; ++t)
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
-            const f32x4 rs = *reinterpret_cast<const f32x4*>(rscale + 32 * t + 8 * g + 4 * half);
+            for (int p = 0; p < 2; ++p) buf[q & 1][t][p] = fr[((q * T + t) * 2 + p) * 64 + lane];
+    };
+    auto split = [&](int q) {
 #pragma unroll
-            for (int i = 0; i < 4; ++i) acc[t][4 * g + i] = acc[t][4 * g + i] * so * rs[i];
+        for (int j = 0; j < 8; ++j) {
+            const float v = in[q / 2][8 * (q % 2) + j] * sinv;
+            const _Float16 h0 = (_Float16)v;
+            b0[q & 1][j] = h0;
+            b1[q & 1][j] = (_Float16)(v - (float)h0);
         }
+    };
+    fetch(0);
+    split(0);
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) {
+        if (q + 1 < NQ) {
+            fetch(q + 1);
+            split(q + 1);
+        }
+        auto a = [&](int t, int p) { return __builtin_bit_cast(f16x8, buf[q & 1][t][p]); };
+#pragma unroll
+        for (int t = 0; t < T; ++t)
+            acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a(t, 1), b0[q & 1], acc[t], 0, 0, 0);
+#pragma unroll
+        for (int t = 0; t < T; ++t)
+            acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a(t, 0), b1[q & 1], acc[t], 0, 0, 0);
+#pragma unroll
+        for (int t = 0; t < T; ++t)
+            acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a(t, 0), b0[q & 1], acc[t], 0, 0, 0);
+        if constexpr (T >= 4) __builtin_amdgcn_sched_barrier(0);
+    }
+    unscale<T>(rscale, ex, acc, lane);
 }
 
 // Layer 0: B operand read straight from the (E, kin) features; k-step 4q+i of lane
@@ -283,6 +361,27 @@ __device__ __forceinline__ void first_layer(const float* __restrict__ f, const f
 #pragma unroll
         for (int t = 0; t < T; ++t) {
             const f32x4 a = sh.frag[(t * nq + q) * 64 + lane];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[t] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i], b[i], acc[t], 0, 0, 0);
+        }
+    }
+}
+
+// Layer 0 with its fragments resident in LDS at fr.
+template <int T>
+__device__ __forceinline__ void first_layer_res(const f32x4* __restrict__ fr, const float* __restrict__ feats,
+                                                int64_t e, bool valid, int kin, int kp, f32x16 (&acc)[T], int lane) {
+    const int nq = kp / 8, half = lane >> 5;
+    for (int q = 0; q < nq; ++q) {
+        float b[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int k = 8 * q + 4 * half + i;
+            b[i] = (valid && k < kin) ? feats[e * kin + k] : 0.f;
+        }
+#pragma unroll
+        for (int t = 0; t < T; ++t) {
+            const f32x4 a = fr[(t * nq + q) * 64 + lane];
 #pragma unroll
             for (int i = 0; i < 4; ++i) acc[t] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i], b[i], acc[t], 0, 0, 0);
         }
@@ -429,6 +528,168 @@ __global__ void __launch_bounds__(kRadThreads) k_radial_bwd(const float* __restr
     }
 }
 
+// ---------------------------------------------------------------------------
+// Resident variants, used when the padded input width is at most kRadResKp:
+// the fragments and biases one direction needs (at most ~153 KB, H = 128 with
+// two layers backward) are staged into LDS once per workgroup, and each
+// wavefront then walks groups of 32 edges, grid-strided, with no further
+// barriers -- the per-layer staging of the kernels above (a barrier and up to
+// 64 KB copied per layer and 128 edges) dominated at one wavefront per SIMD.
+// The grid is as many workgroups as fit the device at once.
+// ---------------------------------------------------------------------------
+
+constexpr int kRadResKp = 16;
+
+// A zero the compiler cannot see through, recomputed per edge group: offsetting the
+// bias and row-scale pointers by it keeps their loads at their uses (hoisted out of
+// the group loop they would hold ~270 registers for the whole kernel).
+__device__ __forceinline__ int opaque_zero() {
+    int z;
+    asm volatile("s_mov_b32 %0, 0" : "=s"(z));
+    return z;
+}
+
+template <int H, int L, bool BWD>
+constexpr int rad_res_floats() {
+    constexpr int T = H / 32;
+    int n = T * (kRadResKp / 8) * 256 + (L - 1) * T * (H / 16) * kX2Block + L * H;  // forward layers, biases
+    if (BWD) n += (H / 16) * kX2Block + (L - 1) * T * (H / 16) * kX2Block;  // backward layer 0 (one tile), 1..L-1
+    return n;
+}
+
+template <int H, int L>
+__global__ void __launch_bounds__(kRadThreads) k_radial_fwd_res(const float* __restrict__ feats, int64_t E, int kin,
+                                                                const float* __restrict__ frag, RadLayout lay,
+                                                                float* __restrict__ out) {
+    constexpr int T = H / 32;
+    __shared__ f32x4 res[rad_res_floats<H, L, false>() / 4];
+    const int nf = int(lay.fwd_off(L));  // forward fragments, then the biases
+    stage(frag, nf, res);
+    stage(frag + lay.bias_off(), L * H, res + nf / 4);
+    __syncthreads();
+    const float* bias = reinterpret_cast<const float*>(res) + nf;
+    const int lane = threadIdx.x & 63, half = lane >> 5;
+    const int64_t groups = (E + 31) / 32, stride = int64_t(gridDim.x) * (kRadThreads / 64);
+    for (int64_t grp = int64_t(blockIdx.x) * (kRadThreads / 64) + (threadIdx.x >> 6); grp < groups; grp += stride) {
+        const int64_t e = grp * 32 + (lane & 31);
+        const bool valid = e < E;
+        const int z0 = opaque_zero();
+        const float* bs = bias + z0;
+        const float* fs = frag + z0;
+        f32x16 acc[T];
+        float act[T][16];
+        zero(acc);
+        first_layer_res<T>(res, feats, e, valid, kin, lay.kp, acc, lane);
+#pragma unroll
+        for (int j = 0; j < L; ++j) {
+            if (j > 0) {
+                zero(acc);
+                mfma_layer_res<T, H / 16>(res + lay.fwd_off(j) / 4, fs + lay.fscale_off(j), act, acc, lane);
+            }
+#pragma unroll
+            for (int t = 0; t < T; ++t)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) act[t][r] = silu(acc[t][r] + bs[j * H + dfeat(t, r, half)]);
+        }
+        if (valid) {
+            float* o = out + e * H;
+#pragma unroll
+            for (int t = 0; t < T; ++t)
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    const f32x4 v = {act[t][4 * g], act[t][4 * g + 1], act[t][4 * g + 2], act[t][4 * g + 3]};
+                    *reinterpret_cast<f32x4*>(o + 32 * t + 8 * g + 4 * half) = v;
+                }
+        }
+    }
+}
+
+template <int H, int L>
+__global__ void __launch_bounds__(kRadThreads) k_radial_bwd_res(const float* __restrict__ feats, int64_t E, int kin,
+                                                                const float* __restrict__ frag, RadLayout lay,
+                                                                const float* __restrict__ grad_h,
+                                                                float* __restrict__ grad_feats) {
+    constexpr int T = H / 32;
+    __shared__ f32x4 res[rad_res_floats<H, L, true>() / 4];
+    stage(frag, int(lay.fscale_off(1)), res);  // both directions' fragments and the biases, as laid out in frag
+    __syncthreads();
+    const float* bias = reinterpret_cast<const float*>(res) + lay.bias_off();
+    const int lane = threadIdx.x & 63, half = lane >> 5;
+    const int64_t groups = (E + 31) / 32, stride = int64_t(gridDim.x) * (kRadThreads / 64);
+    for (int64_t grp = int64_t(blockIdx.x) * (kRadThreads / 64) + (threadIdx.x >> 6); grp < groups; grp += stride) {
+        const int64_t e = grp * 32 + (lane & 31);
+        const bool valid = e < E;
+        const int z0 = opaque_zero();
+        const float* bs = bias + z0;
+        const float* fs = frag + z0;
+        float z[L > 1 ? L - 1 : 1][T][16];
+        float g[T][16];
+        f32x16 acc[T];
+        zero(acc);
+        first_layer_res<T>(res, feats, e, valid, kin, lay.kp, acc, lane);
+#pragma unroll
+        for (int j = 0; j < L; ++j) {
+            if (j > 0) {
+                zero(acc);
+                mfma_layer_res<T, H / 16>(res + lay.fwd_off(j) / 4, fs + lay.fscale_off(j), g, acc, lane);
+            }
+            if (j < L - 1) {
+#pragma unroll
+                for (int t = 0; t < T; ++t)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) {
+                        z[j][t][r] = acc[t][r] + bs[j * H + dfeat(t, r, half)];
+                        g[t][r] = silu(z[j][t][r]);
+                    }
+            }
+        }
+        // g = dL/dh * silu'(z_{L-1}), dL/dh read in the D layout
+#pragma unroll
+        for (int t = 0; t < T; ++t)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const f32x4 v = valid ? *reinterpret_cast<const f32x4*>(grad_h + e * H + 32 * t + 8 * q + 4 * half)
+                                      : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int r = 4 * q + i;
+                    g[t][r] = v[i] * silu_grad(acc[t][r] + bs[(L - 1) * H + dfeat(t, r, half)]);
+                }
+            }
+#pragma unroll
+        for (int j = L - 1; j >= 1; --j) {
+            zero(acc);
+            mfma_layer_res<T, H / 16>(res + lay.bwd_off(j) / 4, fs + lay.bscale_off(j), g, acc, lane);
+#pragma unroll
+            for (int t = 0; t < T; ++t)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) g[t][r] = acc[t][r] * silu_grad(z[j - 1][t][r]);
+        }
+        f32x16 a0[1];  // kp <= 16: dL/df^T is one row tile
+        zero(a0);
+        mfma_layer_res<1, H / 16>(res + lay.bwd_off(0) / 4, fs + lay.bscale_off(0), g, a0, lane);
+        store_grad_feats(a0, grad_feats, e, valid, kin, half);
+    }
+}
+
+// Workgroups of a resident kernel that fit the device at once (per kernel, cached).
+template <class K>
+int resident_grid(K kernel, int64_t E) {
+    static int per_cu = -1;
+    static int cus = 0;
+    if (per_cu < 0) {
+        int dev = 0, n = 0, b = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+            hipOccupancyMaxActiveBlocksPerMultiprocessor(&b, kernel, kRadThreads, 0) != hipSuccess)
+            return -1;
+        cus = n;
+        per_cu = b;
+    }
+    const int64_t need = ceil_div(ceil_div(E, 32), kRadThreads / 64);
+    return int(std::min<int64_t>(need, int64_t(std::max(per_cu, 1)) * cus));
+}
+
 RadLayout make_layout(int kin, int H, int L) { return RadLayout{kin, (kin + 7) & ~7, H, L}; }
 
 int check_shape(int kin, int H, int L) {
@@ -443,15 +704,27 @@ int check_shape(int kin, int H, int L) {
 
 template <int H, int L>
 void launch_fwd(const float* feats, int64_t E, int kin, const float* frag, RadLayout lay, float* out, hipStream_t s) {
-    hipLaunchKernelGGL((k_radial_fwd<H, L>), dim3(ceil_div(E, kRadEdgesPerBlock)), dim3(kRadThreads), 0, s, feats, E,
-                       kin, frag, lay, out);
+    // resident only at 128 wide: narrower forwards are VALU-bound (SiLU) and run slightly
+    // faster per-layer staged, with more workgroups in flight
+    const int grid = H == 128 && lay.kp <= kRadResKp ? resident_grid(k_radial_fwd_res<H, L>, E) : 0;
+    if (grid > 0)
+        hipLaunchKernelGGL((k_radial_fwd_res<H, L>), dim3(grid), dim3(kRadThreads), 0, s, feats, E, kin, frag, lay,
+                           out);
+    else
+        hipLaunchKernelGGL((k_radial_fwd<H, L>), dim3(ceil_div(E, kRadEdgesPerBlock)), dim3(kRadThreads), 0, s, feats,
+                           E, kin, frag, lay, out);
 }
 
 template <int H, int L>
 void launch_bwd(const float* feats, int64_t E, int kin, const float* frag, RadLayout lay, const float* gh, float* gf,
                 hipStream_t s) {
-    hipLaunchKernelGGL((k_radial_bwd<H, L>), dim3(ceil_div(E, kRadEdgesPerBlock)), dim3(kRadThreads), 0, s, feats, E,
-                       kin, frag, lay, gh, gf);
+    const int grid = lay.kp <= kRadResKp ? resident_grid(k_radial_bwd_res<H, L>, E) : 0;
+    if (grid > 0)
+        hipLaunchKernelGGL((k_radial_bwd_res<H, L>), dim3(grid), dim3(kRadThreads), 0, s, feats, E, kin, frag, lay, gh,
+                           gf);
+    else
+        hipLaunchKernelGGL((k_radial_bwd<H, L>), dim3(ceil_div(E, kRadEdgesPerBlock)), dim3(kRadThreads), 0, s, feats,
+                           E, kin, frag, lay, gh, gf);
 }
 
 #define MNX_RAD_DISPATCH(FN, ...)                                     \
@@ -494,7 +767,7 @@ int mnx_radial_pack_f32(const float* raw, int32_t kin, int32_t hidden, int32_t l
     MNX_REQUIRE((uintptr_t)frag % 16 == 0, "frag must be 16-byte aligned");
     const RadLayout lay = make_layout(kin, hidden, layers);
     hipStream_t s = (hipStream_t)stream;
-    hipLaunchKernelGGL(k_radial_scales, dim3(ceil_div(lay.scales_total(), 256)), dim3(256), 0, s, raw, lay, frag);
+    hipLaunchKernelGGL(k_radial_scales, dim3(ceil_div(lay.scales_total(), 4)), dim3(256), 0, s, raw, lay, frag);
     MNX_CHECK_LAUNCH();
     hipLaunchKernelGGL(k_radial_pack, dim3(ceil_div(lay.fscale_off(1), 256)), dim3(256), 0, s, raw, lay, frag);
     MNX_CHECK_LAUNCH();

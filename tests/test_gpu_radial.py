@@ -36,9 +36,12 @@ def _ref(feats, Ws, bs):
     return h
 
 
+# input widths up to 16 run the LDS-resident grid-strided kernels (the large-E cases walk many
+# edge groups per wavefront), wider inputs the per-layer staged ones
 @pytest.mark.parametrize("kin,H,L,E", [(8, 64, 2, 1000), (8, 128, 2, 4099), (8, 128, 1, 77), (5, 32, 1, 33),
                                        (13, 64, 3, 31), (64, 32, 4, 100), (8, 64, 4, 257), (40, 64, 1, 64),
-                                       (8, 32, 2, 1)])
+                                       (8, 32, 2, 1), (8, 128, 2, 300_007), (16, 64, 2, 200_003),
+                                       (24, 128, 2, 5000)])
 def test_radial_hidden_matches_fp64(kin, H, L, E):
     g = torch.Generator().manual_seed(kin * 1000 + H * 10 + L)
     Ws, bs = _mlp_params(kin, H, L, g)
@@ -53,6 +56,8 @@ def test_radial_hidden_matches_fp64(kin, H, L, E):
     (gf64,) = torch.autograd.grad(h64, f64, gout.double())
     assert _rel(h.cpu(), h64) <= 1e-5
     assert _rel(gf.cpu(), gf64) <= 1e-5
+    for a, r in ((h.detach().cpu().double(), h64.detach()), (gf.cpu().double(), gf64)):
+        assert (a - r).abs().max() <= 1e-5 * r.pow(2).mean().sqrt()
 
 
 def test_radial_hidden_empty_and_unsupported():
