@@ -1187,13 +1187,8 @@ def _(a, weights, blocks, out_dim):
     return a.new_empty(a.shape[0], out_dim)
 
 
-def class_groups(classes: Tensor, num_classes: int) -> tuple[Tensor, Tensor]:
-    """Nodes grouped by class without a host synchronisation: ``order`` (int32, classes ascending,
-    ascending node id within a class, out-of-range classes last) and ``class_start`` (int32,
-    ``num_classes + 2`` entries: where class s begins in ``order``, s = num_classes being the
-    out-of-range nodes)."""
-    if classes.device.type != "cuda":
-        raise RuntimeError(f"molix::class_groups runs on the GPU only (got a {classes.device} tensor)")
+@torch.library.custom_op("molix::class_groups", mutates_args=(), device_types="cuda")
+def _class_groups_op(classes: Tensor, num_classes: int) -> tuple[Tensor, Tensor]:
     lib = _lib.load()
     c = classes.reshape(-1).to(torch.int64).contiguous()
     n = c.shape[0]
@@ -1203,6 +1198,22 @@ def class_groups(classes: Tensor, num_classes: int) -> tuple[Tensor, Tensor]:
     check(lib.mnx_class_groups(ptr(c), n, num_classes, ptr(order), ptr(class_start), ptr(ws), ws.numel(),
                                _stream(c)), "class_groups")
     return order, class_start
+
+
+@_class_groups_op.register_fake
+def _(classes, num_classes):
+    return (classes.new_empty(classes.numel(), dtype=torch.int32),
+            classes.new_empty(num_classes + 2, dtype=torch.int32))
+
+
+def class_groups(classes: Tensor, num_classes: int) -> tuple[Tensor, Tensor]:
+    """Nodes grouped by class without a host synchronisation: ``order`` (int32, classes ascending,
+    ascending node id within a class, out-of-range classes last) and ``class_start`` (int32,
+    ``num_classes + 2`` entries: where class s begins in ``order``, s = num_classes being the
+    out-of-range nodes)."""
+    if classes.device.type != "cuda":
+        raise RuntimeError(f"molix::class_groups runs on the GPU only (got a {classes.device} tensor)")
+    return _class_groups_op(classes, int(num_classes))
 
 
 @torch.library.custom_op("molix::indexed_block_linear", mutates_args=(), device_types="cuda")

@@ -53,6 +53,18 @@ def test_opcheck_tp_scatter():
     opcheck(ops.tp_scatter.default, (x, Y, w, row_ptr, perm, snd, cfg, C))
 
 
+def test_opcheck_class_groups():
+    z = torch.randint(-1, 7, (3000,), device=DEV)
+    opcheck(ops.class_groups.default, (z, 6), test_utils=("test_schema", "test_faketensor"))
+
+
+def test_opcheck_segment_sum():
+    idx = torch.randint(0, 40, (500,), device=DEV)
+    v = torch.randn(500, 12, device=DEV, requires_grad=True)
+    w = torch.randn(500, device=DEV, requires_grad=True)
+    opcheck(ops.segment_sum.default, (v, idx, 40, w, False))
+
+
 def test_opcheck_edge_csr():
     pos, box, ei, _, _ = _graph()
     opcheck(ops.edge_csr.default, (ei, pos.shape[0]), test_utils=("test_schema", "test_faketensor"))
