@@ -130,7 +130,8 @@ class EdgeStep:
         row_ptr, perm, snd = ops.edge_csr(self.edge_index, self.N, False)
         Y = ops.spherical_harmonics(self.vec, 3)
         r = torch.linalg.vector_norm(self.vec, dim=-1)
-        feats = bessel_cutoff(r, 5.0, 8, self.mu, self.sigma)
+        # 8-Bessel x cosine cutoff in one kernel each way (bessel_cutoff below is its torch form)
+        feats = ops.bessel_cutoff(r, 8, 5.0, 1e-8, self.mu, self.sigma, 1, 0)
         if self.fused:
             # output layer + TP as one op: the backward forms the weight gradient in registers
             last = self.mlp.mlp[-1]

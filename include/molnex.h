@@ -369,6 +369,22 @@ int mnx_bond_vectors_f32(const float* pos, int64_t num_atoms, const int64_t* edg
 int mnx_bond_vectors_bwd_f32(const int64_t* edge_index, const float* grad_diff, int64_t num_edges,
                              int64_t num_atoms, float* grad_pos, mnx_stream_t stream);
 
+/* Radial edge embedding of MACE: the Bessel basis times the cutoff envelope,
+ *   out[e][k] = c(r[e]) (phi_k(r[e]) - mu[k]) / sigma[k],
+ *   phi_k(r) = sqrt(2 / r_cut) sin((k+1) pi r / r_cut) / (r + eps),  k < num_radial,
+ * c = 1 (cutoff 0), 0.5 (cos(pi r / r_cut) + 1) (cutoff 1) or the polynomial
+ * envelope of the given exponent (cutoff 2), 0 for r >= r_cut; mu / sigma both
+ * NULL for the unnormalised basis.  out [num_edges][num_radial]; the backward
+ * gives grad_r [num_edges] from grad [num_edges][num_radial].  Replaces
+ * BesselRBF(r) * cutoff(r) (src/molrep/embedding/radial.py:36-148,
+ * cutoff.py:23-161, src/molzoo/mace.py:180-182).  num_radial <= 32. */
+int mnx_bessel_cutoff_f32(const float* r, int64_t num_edges, int32_t num_radial, double r_cut, double eps,
+                          const float* mu, const float* sigma, int32_t cutoff, int32_t exponent, float* out,
+                          mnx_stream_t stream);
+int mnx_bessel_cutoff_bwd_f32(const float* r, int64_t num_edges, int32_t num_radial, double r_cut, double eps,
+                              const float* mu, const float* sigma, int32_t cutoff, int32_t exponent,
+                              const float* grad, float* grad_r, mnx_stream_t stream);
+
 /* ------------------------------------------------------------------------ */
 /* Hidden stack of the radial weight MLP (replaces mlp[:-1] of               */
 /* RadialWeightMLP, src/molrep/interaction/radial_mlp.py:38-93:              */

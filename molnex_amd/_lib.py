@@ -73,6 +73,8 @@ SIGNATURES = {
                                                 c_i64, c_i32, vp, c_i64, c_i64, c_i32, vp]),
     "mnx_bond_vectors_f32": (C.c_int, [vp, c_i64, vp, vp, c_i64, vp, vp]),
     "mnx_bond_vectors_bwd_f32": (C.c_int, [vp, vp, c_i64, c_i64, vp, vp]),
+    "mnx_bessel_cutoff_f32": (C.c_int, [vp, c_i64, c_i32, c_f64, c_f64, vp, vp, c_i32, c_i32, vp, vp]),
+    "mnx_bessel_cutoff_bwd_f32": (C.c_int, [vp, c_i64, c_i32, c_f64, c_f64, vp, vp, c_i32, c_i32, vp, vp, vp]),
     "mnx_radial_raw_floats": (c_i64, [c_i32, c_i32, c_i32]),
     "mnx_radial_frag_floats": (c_i64, [c_i32, c_i32, c_i32]),
     "mnx_radial_pack_f32": (C.c_int, [vp, c_i32, c_i32, c_i32, vp, vp]),

@@ -4,6 +4,10 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <algorithm>
+#include <mutex>
+#include <unordered_map>
+
 #include "../../include/molnex.h"
 
 namespace mnx {
@@ -36,6 +40,28 @@ void clear_error();
 constexpr int kWave = 64;
 
 inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+// Workgroups of `threads` threads of `kernel` that the current device holds at once
+// (compute units x resident workgroups per unit, cached per kernel and device), capped
+// at `need`; -1 if the runtime cannot tell.  Grid size of persistent (grid-strided)
+// kernels.
+inline int64_t device_fill_grid(const void* kernel, int threads, int64_t need) {
+    static std::mutex mu;
+    static std::unordered_map<const void*, int> per_cu[64];
+    static int cus[64] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return -1;
+    std::lock_guard<std::mutex> lock(mu);
+    if (cus[dev] == 0 && hipDeviceGetAttribute(&cus[dev], hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+        return -1;
+    auto it = per_cu[dev].find(kernel);
+    if (it == per_cu[dev].end()) {
+        int b = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&b, kernel, threads, 0) != hipSuccess) return -1;
+        it = per_cu[dev].emplace(kernel, std::max(b, 1)).first;
+    }
+    return std::min<int64_t>(need, int64_t(it->second) * cus[dev]);
+}
 
 // Aligned bump allocator over a caller-provided workspace.
 struct Workspace {

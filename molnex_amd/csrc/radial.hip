@@ -31,8 +31,6 @@
 // [q][tile][plane][lane][8], with one scale per output row.  The first layer
 // (K = the few radial features) stays on fp32 MFMAs.
 
-#include <algorithm>
-
 #include "common.h"
 
 namespace mnx {
@@ -672,22 +670,11 @@ __global__ void __launch_bounds__(kRadThreads) k_radial_bwd_res(const float* __r
     }
 }
 
-// Workgroups of a resident kernel that fit the device at once (per kernel, cached).
+// Workgroups of a resident kernel: as many as fit the device at once.
 template <class K>
 int resident_grid(K kernel, int64_t E) {
-    static int per_cu = -1;
-    static int cus = 0;
-    if (per_cu < 0) {
-        int dev = 0, n = 0, b = 0;
-        if (hipGetDevice(&dev) != hipSuccess ||
-            hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-            hipOccupancyMaxActiveBlocksPerMultiprocessor(&b, kernel, kRadThreads, 0) != hipSuccess)
-            return -1;
-        cus = n;
-        per_cu = b;
-    }
     const int64_t need = ceil_div(ceil_div(E, 32), kRadThreads / 64);
-    return int(std::min<int64_t>(need, int64_t(std::max(per_cu, 1)) * cus));
+    return int(device_fill_grid(reinterpret_cast<const void*>(kernel), kRadThreads, need));
 }
 
 RadLayout make_layout(int kin, int H, int L) { return RadLayout{kin, (kin + 7) & ~7, H, L}; }

@@ -1328,6 +1328,76 @@ def _bond_bwd(ctx, grad):
 bond_vectors.register_autograd(_bond_bwd, setup_context=_bond_setup)
 
 
+# ---------------------------------------------------------------------------
+# Radial edge embedding (Bessel basis x cutoff envelope)
+# ---------------------------------------------------------------------------
+
+CUTOFF_KINDS = {"none": 0, "cosine": 1, "polynomial": 2}
+
+
+def _basis_args(r, mu, sigma, num_radial):
+    rr = r.detach().to(torch.float32).reshape(-1).contiguous()
+    m = None if mu is None else mu.detach().to(torch.float32).reshape(-1).contiguous()
+    s = None if sigma is None else sigma.detach().to(torch.float32).reshape(-1).contiguous()
+    if (m is None) != (s is None) or (m is not None and (m.numel() != num_radial or s.numel() != num_radial)):
+        raise ValueError("bessel_cutoff: mu and sigma must both be None or both have num_radial entries")
+    return rr, m, s
+
+
+@torch.library.custom_op("molix::bessel_cutoff", mutates_args=(), device_types="cuda")
+def bessel_cutoff(r: Tensor, num_radial: int, r_cut: float, eps: float, mu: Tensor | None, sigma: Tensor | None,
+                  cutoff: int, exponent: int) -> Tensor:
+    """``BesselRBF(r) * cutoff(r)[..., None]`` in one kernel (``radial.py:36-148``, ``cutoff.py:23-161``,
+    ``mace.py:180-182``): ``(r.shape..., num_radial)``.  ``cutoff``: 0 none, 1 cosine, 2 polynomial
+    (``exponent``); ``mu`` / ``sigma`` the basis normalisation or both None."""
+    _require_gpu("bessel_cutoff", r, mu, sigma)
+    rr, m, sg = _basis_args(r, mu, sigma, num_radial)
+    out = rr.new_empty(rr.shape[0], num_radial)
+    check(_lib.load().mnx_bessel_cutoff_f32(ptr(rr), rr.shape[0], num_radial, float(r_cut), float(eps), ptr(m),
+                                            ptr(sg), cutoff, exponent, ptr(out), _stream(rr)), "bessel_cutoff")
+    return out.reshape(*r.shape, num_radial)
+
+
+@bessel_cutoff.register_fake
+def _(r, num_radial, r_cut, eps, mu, sigma, cutoff, exponent):
+    return r.new_empty(*r.shape, num_radial, dtype=torch.float32)
+
+
+@torch.library.custom_op("molix::bessel_cutoff_backward", mutates_args=(), device_types="cuda")
+def bessel_cutoff_backward(grad: Tensor, r: Tensor, num_radial: int, r_cut: float, eps: float, mu: Tensor | None,
+                           sigma: Tensor | None, cutoff: int, exponent: int) -> Tensor:
+    rr, m, sg = _basis_args(r, mu, sigma, num_radial)
+    g = grad.to(torch.float32).reshape(-1, num_radial).contiguous()
+    gr = rr.new_empty(rr.shape[0])
+    check(_lib.load().mnx_bessel_cutoff_bwd_f32(ptr(rr), rr.shape[0], num_radial, float(r_cut), float(eps), ptr(m),
+                                                ptr(sg), cutoff, exponent, ptr(g), ptr(gr), _stream(rr)),
+          "bessel_cutoff backward")
+    return gr.reshape(r.shape)
+
+
+@bessel_cutoff_backward.register_fake
+def _(grad, r, num_radial, r_cut, eps, mu, sigma, cutoff, exponent):
+    return r.new_empty(r.shape, dtype=torch.float32)
+
+
+def _bc_setup(ctx, inputs, output):
+    r, num_radial, r_cut, eps, mu, sigma, cutoff, exponent = inputs
+    ctx.save_for_backward(r, mu, sigma)
+    ctx.args = (num_radial, r_cut, eps, cutoff, exponent)
+
+
+def _bc_bwd(ctx, grad):
+    r, mu, sigma = ctx.saved_tensors
+    n, r_cut, eps, cutoff, exponent = ctx.args
+    gr = None
+    if ctx.needs_input_grad[0]:
+        gr = bessel_cutoff_backward(grad.contiguous(), r, n, r_cut, eps, mu, sigma, cutoff, exponent).to(r.dtype)
+    return gr, None, None, None, None, None, None, None
+
+
+bessel_cutoff.register_autograd(_bc_bwd, setup_context=_bc_setup)
+
+
 # second-order formulas (autograd of the backward ops): registered on import
 from . import second_order  # noqa: E402,F401
 

@@ -60,3 +60,21 @@ class BesselRBF(nn.Module):
         if self.normalize:
             phi = (phi - self.mu) / self.sigma
         return phi
+
+
+def radial_edge_features(rbf: "BesselRBF", cutoff_fn: nn.Module, r: torch.Tensor) -> torch.Tensor:
+    """``rbf(r) * cutoff_fn(r)[..., None]`` (MACE's edge features, src/molzoo/mace.py:180-182): one
+    HIP kernel each way (``molix::bessel_cutoff``) for a BesselRBF with a cosine or polynomial
+    cutoff of the same radius on float32 GPU distances; the torch composition otherwise."""
+    from ... import kernels as K
+    from .cutoff import CosineCutoff, PolynomialCutoff
+
+    kind = 1 if isinstance(cutoff_fn, CosineCutoff) else 2 if isinstance(cutoff_fn, PolynomialCutoff) else -1
+    if (kind > 0 and isinstance(rbf, BesselRBF) and r.is_cuda and r.dtype == torch.float32
+            and rbf.config.num_radial <= 32 and float(cutoff_fn.r_cut) == rbf.r_cut):
+        exponent = cutoff_fn.exponent if kind == 2 else 0
+        mu, sigma = (rbf.mu, rbf.sigma) if rbf.normalize else (None, None)
+        return torch.ops.molix.bessel_cutoff(r, int(rbf.config.num_radial), rbf.r_cut, rbf.eps, mu, sigma, kind,
+                                             exponent)
+    return rbf(r) * cutoff_fn(r).unsqueeze(-1)
+

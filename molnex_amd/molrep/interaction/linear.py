@@ -53,6 +53,9 @@ class Linear(nn.Module):
             fan_in = sum(s[1] for s in srcs)
             self.plan.append((out_off[ob], o.mul, o.ir.dim, srcs, fan_in))
         self.weight_numel = woff
+        # a constant factor on the output, applied to the weights (F(x, w) s = F(x, s w): no extra
+        # pass over the output, gradients by autograd); not part of the state_dict
+        self.output_scale = 1.0
         dt = dtype if dtype is not None else config.ftype
         if internal_weights and weight_classes is None:
             self.weight = nn.Parameter(torch.randn(1, self.weight_numel, dtype=dt))
@@ -91,10 +94,14 @@ class Linear(nn.Module):
         x2 = x.reshape(-1, self.irreps_in.dim)
         if self.weight_classes is None:
             w = self.weight if weight is None else weight
+            if self.output_scale != 1.0:
+                w = w * self.output_scale
             out = self._mix(x2, w.reshape(-1))
         else:
             if weight is None or weight_indices is None:
                 raise ValueError("indexed linear needs weight and weight_indices")
+            if self.output_scale != 1.0:
+                weight = weight * self.output_scale
             idx = weight_indices.reshape(-1)
             if x2.is_cuda and x2.dtype == torch.float32 and weight.dtype == torch.float32 and self._hip_ok():
                 out = _HipIndexedLinear.apply(x2, weight, K.class_groups(idx, self.weight_classes), idx, self)

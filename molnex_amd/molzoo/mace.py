@@ -28,7 +28,7 @@ from ..irreps import Irreps
 from ..molrep.embedding.angular import SphericalHarmonics
 from ..molrep.embedding.cutoff import CosineCutoff, PolynomialCutoff
 from ..molrep.embedding.node import ContinuousEmbeddingSpec, DiscreteEmbeddingSpec, JointEmbedding
-from ..molrep.embedding.radial import BesselRBF
+from ..molrep.embedding.radial import BesselRBF, radial_edge_features
 from ..molrep.interaction.element_update import ElementUpdate
 from ..molrep.interaction.linear import Linear
 from ..molrep.interaction.radial_mlp import RadialWeightMLP
@@ -79,7 +79,7 @@ class EmbeddingBlock(nn.Module):
         node_feats = self.node_embedding(Z=Z)
         edge_dir = bond_diff / (bond_dist.unsqueeze(-1) + 1e-8)
         edge_attrs = self.spherical_harmonics(edge_dir)
-        edge_feats = self.radial_embedding(bond_dist) * self.cutoff_fn(bond_dist).unsqueeze(-1)
+        edge_feats = radial_edge_features(self.radial_embedding, self.cutoff_fn, bond_dist)
         return node_feats, edge_attrs, edge_feats
 
 
@@ -108,15 +108,16 @@ class InteractionBlock(nn.Module):
         self.radial_mlp = RadialWeightMLP(in_dim=num_bessel, hidden_dim=num_features,
                                           out_dim=self.conv_tp.weight_numel, num_layers=2)
         self.linear = Linear(Irreps(tp_out_irreps), Irreps(irreps_str), dtype=config.ftype)
+        # linear(messages) / avg_num_neighbors, with the division folded into the linear's weights
+        self.linear.output_scale = 1.0 / avg_num_neighbors
         self.avg_num_neighbors = avg_num_neighbors
 
     def forward(self, node_feats, edge_attrs, edge_feats, edge_index):
         sc = node_feats
         node_feats_up = self.node_linear(node_feats)
         messages = self.conv_tp.forward_radial(node_feats_up, edge_attrs, edge_index, self.radial_mlp, edge_feats)
-        # linear(messages / avg) == linear(messages) / avg; scaling the linear's output
-        # touches (nodes x hidden) values instead of (nodes x TP-output) ones
-        return self.linear(messages) / self.avg_num_neighbors, sc
+        # linear(messages / avg) == linear(messages) / avg == linear with weights / avg
+        return self.linear(messages), sc
 
 
 class MACESpec(BaseModel):

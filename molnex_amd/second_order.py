@@ -26,6 +26,7 @@ The PME ops keep the reference's first-order-only autograd (pme_cpu.cpp:208-215)
 
 from __future__ import annotations
 
+import math
 from functools import lru_cache
 
 import torch
@@ -96,6 +97,54 @@ def _sh2_bwd(ctx, ggv):
 
 
 K.spherical_harmonics_backward.register_autograd(_sh2_bwd, setup_context=_sh2_setup)
+
+
+# ---------------------------------------------------------------------------
+# radial edge embedding
+# ---------------------------------------------------------------------------
+
+def bessel_cutoff_torch(r: Tensor, num_radial: int, r_cut: float, eps: float, mu: Tensor | None,
+                        sigma: Tensor | None, cutoff: int, exponent: int) -> Tensor:
+    """The formula of ``molix::bessel_cutoff`` in torch (differentiable twice)."""
+    freqs = torch.arange(1, num_radial + 1, dtype=r.dtype, device=r.device) * (math.pi / r_cut)
+    rr = r.unsqueeze(-1)
+    phi = math.sqrt(2.0 / r_cut) * torch.sin(rr * freqs) / (rr + eps)
+    if mu is not None:
+        phi = (phi - mu.to(r.dtype)) / sigma.to(r.dtype)
+    if cutoff == 0:
+        return phi
+    if cutoff == 1:
+        c = 0.5 * (torch.cos(math.pi * (r / r_cut)) + 1.0)
+    else:
+        x = r / r_cut
+        g = torch.full_like(x, float((exponent + 1) * exponent // 2))
+        for k in range(exponent - 2, -1, -1):
+            g = g * x + float((k + 2) * (k + 1) // 2)
+        c = (1.0 - x) ** 3 * g
+    c = torch.where(r < r_cut, c, torch.zeros_like(c))
+    return phi * c.unsqueeze(-1)
+
+
+def _bc2_setup(ctx, inputs, output):
+    grad, r, num_radial, r_cut, eps, mu, sigma, cutoff, exponent = inputs
+    ctx.save_for_backward(grad, r, mu, sigma)
+    ctx.args = (num_radial, r_cut, eps, cutoff, exponent)
+
+
+def _bc2_bwd(ctx, ggr):
+    g, r, mu, sigma = ctx.saved_tensors
+    n, r_cut, eps, cutoff, exponent = ctx.args
+    ng, nr = ctx.needs_input_grad[:2]
+    # in fp64: the basis' derivatives cancel for small f r (the first-order kernel does the same)
+    seed = None if ggr is None else ggr.double()
+    dg, dr = _vjp_second(lambda rr: bessel_cutoff_torch(rr, n, r_cut, eps, mu, sigma, cutoff, exponent),
+                         [r.double()], g.double(), [seed], [ng, nr])
+    dg = None if dg is None else dg.to(g.dtype)
+    dr = None if dr is None else dr.to(r.dtype)
+    return dg, dr, None, None, None, None, None, None, None
+
+
+K.bessel_cutoff_backward.register_autograd(_bc2_bwd, setup_context=_bc2_setup)
 
 
 # ---------------------------------------------------------------------------

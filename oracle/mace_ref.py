@@ -111,19 +111,40 @@ def _edge_embedding(cfg, pos, edge_index, l_max, shifts=None):
     bond_dist = bond_diff.norm(dim=-1).clamp(min=1e-6)
     edge_dir = bond_diff / (bond_dist.unsqueeze(-1) + 1e-8)
     Y = sh_torch(l_max, edge_dir)
+    return Y, radial_features(bond_dist, rc, nb_, cfg.get("cutoff", "cosine"))
+
+
+def bessel_stats(rc, nb_):
+    """Shift / scale of the Bessel basis: mean and std of its fp32 values on 4096 points of
+    [1e-8, r_cut] (radial.py:117-147)."""
     freqs = torch.arange(1, nb_ + 1, dtype=torch.float64) * (math.pi / rc)
     pref = math.sqrt(2.0 / rc)
     rs = torch.linspace(1e-8, rc, 4096, dtype=torch.float32)
     raw = (pref * torch.sin(rs[:, None] * freqs.float()) / (rs[:, None] + 1e-8))
-    mu, sig = raw.mean(0).double(), raw.std(0).clamp(min=1e-8).double()
-    phi = (pref * torch.sin(bond_dist[:, None] * freqs) / (bond_dist[:, None] + 1e-8) - mu) / sig
-    if cfg.get("cutoff", "cosine") == "polynomial":  # cutoff.py:138-161, p = 6
+    return raw.mean(0).double(), raw.std(0).clamp(min=1e-8).double()
+
+
+def radial_features(bond_dist, rc, nb_, cutoff="cosine", p=6, normalize=True):
+    """MACE's edge features: the (normalised) Bessel basis times the cutoff envelope
+    (radial.py:36-148, cutoff.py:56-75 / 138-161, mace.py:180-182), in the dtype of bond_dist.  The
+    polynomial envelope in the expanded form of the reference,
+    1 - (p+1)(p+2)/2 x^p + p(p+2) x^(p+1) - p(p+1)/2 x^(p+2)."""
+    freqs = torch.arange(1, nb_ + 1, dtype=torch.float64) * (math.pi / rc)
+    pref = math.sqrt(2.0 / rc)
+    phi = pref * torch.sin(bond_dist[:, None] * freqs) / (bond_dist[:, None] + 1e-8)
+    if normalize:
+        mu, sig = bessel_stats(rc, nb_)
+        phi = (phi - mu) / sig
+    if cutoff == "polynomial":
         x = bond_dist / rc
-        fcut = torch.where(x < 1.0, 1.0 - 28.0 * x ** 6 + 48.0 * x ** 7 - 21.0 * x ** 8, torch.zeros_like(x))
-    else:  # cutoff.py:56-75
+        u = (1.0 - (p + 1) * (p + 2) / 2 * x ** p + p * (p + 2) * x ** (p + 1) - p * (p + 1) / 2 * x ** (p + 2))
+        fcut = torch.where(x < 1.0, u, torch.zeros_like(x))
+    elif cutoff == "cosine":
         fcut = torch.where(bond_dist < rc, 0.5 * (torch.cos(math.pi * bond_dist / rc) + 1.0),
                            torch.zeros_like(bond_dist))
-    return Y, phi * fcut[:, None]
+    else:
+        fcut = torch.ones_like(bond_dist)
+    return phi * fcut[:, None]
 
 
 def _radial(t, p, edge_feats):

@@ -42,6 +42,8 @@ def test_linear_forward_backward_vs_oracle(rows):
     ("128x0e+128x1o+128x0e+128x1o+64x2e", "128x0e+128x1o+32x2e", 777),  # two sources per output
     ("40x0e+24x1o", "24x0e+40x1o+16x2e", 333),                        # output block without source
     ("8x3o+16x3o", "200x3o", 65),                                      # N > 128: second column tile
+    ("128x0e+128x1o", "128x0e+128x1o", 120_001),     # weights resident in LDS, many row groups per workgroup
+    ("256x0e+256x1o+128x1o", "128x0e+128x1o", 60_000),  # K = 256 / 384: weight chunks streamed
 ])
 def test_hip_block_linear_matches_torch_blocks(irr_in, irr_out, rows):
     """The HIP block kernel (forward, input gradient) and the torch block GEMMs agree; weight
@@ -65,6 +67,8 @@ def test_hip_block_linear_matches_torch_blocks(irr_in, irr_out, rows):
     xd, wd = x.detach().double(), lin.weight.detach().double().reshape(-1)
     ref = L._block_forward(xd, wd, lin.plan, lin.irreps_out.dim)
     assert _rel(out.detach().cpu(), ref.cpu()) <= 1e-5
+    o = out.detach().cpu().double()
+    assert (o - ref.cpu()).abs().max() <= 1e-5 * ref.cpu().pow(2).mean().sqrt()
 
 
 def test_hip_block_linear_zero_rows_and_views():
