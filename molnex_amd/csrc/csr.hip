@@ -49,17 +49,31 @@ __global__ void k_fill_i32(int32_t* __restrict__ p, int64_t n) {
     if (i < n) p[i] = 0;
 }
 
+// Per-receiver edge counts, aggregated per wavefront: each run of equal receivers among a
+// wavefront's 64 consecutive edges adds its length with one atomic (receiver-grouped lists,
+// the common case, put ~52 consecutive edges on one counter, which per-edge atomics
+// serialise on), and the invalid-count / unsorted flags are set once per wavefront.
 __global__ void k_count_recv(const int64_t* __restrict__ ei, int64_t E, int64_t N, int32_t* __restrict__ counts,
                              int32_t* __restrict__ invalid, int32_t* __restrict__ unsorted) {
     const int64_t e = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
-    if (e >= E) return;
-    if (!edge_ok(ei, e, N)) {
-        atomicAdd(invalid, 1);
-        atomicOr(unsorted, 1);
-        return;
+    const int lane = threadIdx.x & (kWave - 1);
+    const bool in = e < E;
+    const bool ok = in && edge_ok(ei, e, N);
+    const int32_t key = ok ? int32_t(ei[2 * e + 1]) : -1;  // N < 2^31
+    const bool desc = ok && e > 0 && ei[2 * e + 1] < ei[2 * e - 1];
+    const uint64_t bad = __ballot(in && !ok), dsc = __ballot(desc), okm = __ballot(ok);
+    if (lane == 0) {
+        if (bad) atomicAdd(invalid, int32_t(__popcll(bad)));
+        if (bad || dsc) atomicOr(unsorted, 1);
     }
-    if (e > 0 && ei[2 * e + 1] < ei[2 * e - 1]) atomicOr(unsorted, 1);
-    atomicAdd(&counts[ei[2 * e + 1]], 1);
+    const int32_t prev = __shfl_up(key, 1);
+    const bool head = ok && (lane == 0 || key != prev);
+    const uint64_t stop = __ballot(head) | ~okm;  // a run ends before the next head or invalid lane
+    if (head) {
+        const uint64_t after = stop & ~((uint64_t(2) << lane) - 1);  // positions above this lane
+        const int end = after ? __ffsll((unsigned long long)after) - 1 : kWave;
+        atomicAdd(&counts[key], end - lane);
+    }
 }
 
 __global__ void k_place_edges(const int64_t* __restrict__ ei, int64_t E, int64_t N, const int32_t* __restrict__ row_ptr,
