@@ -123,6 +123,7 @@ class EdgeStep:
         from molnex_amd.config import config as mcfg
 
         self.fused = mcfg.fused_weight_grad and self.K.tp_weight_grad_supported(self.config, C, 64)
+        self.paired = mcfg.paired_radial
 
     def step(self):
         ops = torch.ops.molix
@@ -132,7 +133,15 @@ class EdgeStep:
         r = torch.linalg.vector_norm(self.vec, dim=-1)
         # 8-Bessel x cosine cutoff in one kernel each way (bessel_cutoff below is its torch form)
         feats = ops.bessel_cutoff(r, 8, 5.0, 1e-8, self.mu, self.sigma, 1, 0)
-        if self.fused:
+        pairs = self.K.EdgePairs.build(self.edge_index, self.N, row_ptr, perm, snd, feats.detach()) \
+            if self.paired else None
+        if pairs is not None:
+            # the output layer once per undirected pair (both directions have the same distance,
+            # hence the same weights); edge mode: every edge vector gets its own gradient
+            last = self.mlp.mlp[-1]
+            out, _ = ops.radial_tp_pairs(self.x, Y, self.mlp.hidden(feats), last.weight, last.bias, row_ptr, perm,
+                                         snd, pairs.wrow, pairs.pairs, self.config, self.C)
+        elif self.fused:
             # output layer + TP as one op: the backward forms the weight gradient in registers
             last = self.mlp.mlp[-1]
             out, _ = ops.radial_tp(self.x, Y, self.mlp.hidden(feats), last.weight, last.bias, row_ptr, perm, snd,
@@ -185,11 +194,13 @@ def time_edge_weight_kernels(step: EdgeStep, reps: int = 5):
                             8, 64, 2)
     last = step.mlp.mlp[-1]
     gw = torch.randn(h.shape[0], last.out_features, device=h.device)
+    # with the pairing the step's forward runs on one row per undirected pair (E / 2)
+    hf = h[: h.shape[0] // 2].contiguous() if step.paired else h
     fwd, bwd = [], []
     for i in range(reps + 1):
         e = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
         e[0].record()
-        w = K.edge_weights(h, last.weight, last.bias)
+        w = K.edge_weights(hf, last.weight, last.bias)
         e[1].record()
         e[2].record()
         K.edge_weights_backward(gw, last.weight)
@@ -201,8 +212,10 @@ def time_edge_weight_kernels(step: EdgeStep, reps: int = 5):
     torch.cuda.synchronize()
     tf = sum(a.elapsed_time(b) for a, b in fwd) / reps
     tb = sum(a.elapsed_time(b) for a, b in bwd) / reps
-    nbytes = 4 * h.shape[0] * (h.shape[1] + last.out_features)  # each direction: one E x K and one E x N tensor
-    return tf, tb, nbytes
+    # each direction: one rows x K and one rows x N tensor
+    nbytes_f = 4 * hf.shape[0] * (h.shape[1] + last.out_features)
+    nbytes_b = 4 * h.shape[0] * (h.shape[1] + last.out_features)
+    return tf, tb, nbytes_f, nbytes_b
 
 
 def measured_traffic(kernel: str):
@@ -775,7 +788,8 @@ def main():
     value = E * args.steps / dt / 1e6
 
     tf, tb = time_tp_kernels(step)
-    ewf, ewb, ew_bytes = time_edge_weight_kernels(step)
+    ewf, ewb, ewf_bytes, ewb_bytes = time_edge_weight_kernels(step)
+    step_paired = step.paired
     bf, bb = tp_bytes(N, E, args.channels)
     dom_t, dom_b, dom_name = (tb, bb, "tp_scatter_bwd") if tb >= tf else (tf, bf, "tp_scatter_fwd")
     achieved = dom_b / (dom_t * 1e-3) / 1e9
@@ -786,8 +800,8 @@ def main():
         "kernel_ms": round(dom_t, 3), "algorithmic_bytes": dom_b,
         "other": {"tp_scatter_fwd_ms": round(tf, 3), "tp_scatter_fwd_GBs": round(bf / (tf * 1e-3) / 1e9, 1),
                   "tp_scatter_bwd_ms": round(tb, 3), "tp_scatter_bwd_GBs": round(bb / (tb * 1e-3) / 1e9, 1),
-                  "edge_weights_fwd_ms": round(ewf, 3), "edge_weights_fwd_GBs": round(ew_bytes / (ewf * 1e-3) / 1e9, 1),
-                  "edge_weights_bwd_ms": round(ewb, 3), "edge_weights_bwd_GBs": round(ew_bytes / (ewb * 1e-3) / 1e9, 1)},
+                  "edge_weights_fwd_ms": round(ewf, 3), "edge_weights_fwd_GBs": round(ewf_bytes / (ewf * 1e-3) / 1e9, 1),
+                  "edge_weights_bwd_ms": round(ewb, 3), "edge_weights_bwd_GBs": round(ewb_bytes / (ewb * 1e-3) / 1e9, 1)},
     }
     secondary = None
     if not args.no_secondary:
@@ -813,7 +827,10 @@ def main():
         "data": "synthetic (seeded uniform periodic box, random-init MLP weights, N(0,1) node features)",
         "config": {"workload": "config 3: edge TP + scatter, 50k atoms, rc 5 A, 128 ch, l<=3, fwd+bwd",
                    "atoms": N, "edges": E, "channels": args.channels, "box_A": round(L, 3),
-                   "spatially_sorted": not args.unsorted},
+                   "spatially_sorted": not args.unsorted,
+                   "radial_output_layer": ("once per undirected pair (both directions have the same distance, "
+                                           "hence the same weights; per-edge gradients)" if step_paired
+                                           else "per directed edge")},
         "roofline": roof,
         "cpu_baseline": cpu,
         "secondary": secondary,

@@ -121,6 +121,22 @@ int mnx_csr_build(const int64_t* edge_index, int64_t num_edges, int64_t num_node
 int mnx_csr_build_noalloc(const int64_t* edge_index, int64_t num_edges, int64_t num_nodes, int32_t* row_ptr,
                           int32_t* perm, int32_t* senders_sorted, int32_t* d_invalid, mnx_stream_t stream);
 
+/* Reverse edges of a directed edge list, for work that depends on an edge only
+ * through per-edge features shared by the two directions of an undirected
+ * pair (the radial MLP of src/molrep/interaction/radial_mlp.py:38-93 evaluated
+ * per edge for ConvTP, tensor_product.py:72-79,101-111, sees only the
+ * distance).  rev[e] (int32 [E]) = the one edge e2 != e with edge_index[e2] =
+ * (edge_index[e][1], edge_index[e][0]) whose feats row [num_feats] equals
+ * feats[e] bit for bit; -1 if there is none or more than one, each such edge
+ * counted in d_bad[0] (device int32 [2], both words cleared by the caller;
+ * d_bad[1] is scratch).  row_ptr / perm / senders_sorted: the receiver CSR of
+ * edge_index (mnx_csr_build).  Binary search per edge when every receiver
+ * segment lists its senders in ascending order (checked on the device), a
+ * scan of the segment otherwise. */
+int mnx_edge_reverse(const int64_t* edge_index, int64_t num_edges, int64_t num_nodes, const int32_t* row_ptr,
+                     const int32_t* perm, const int32_t* senders_sorted, const float* feats, int32_t num_feats,
+                     int32_t* rev, int32_t* d_bad, mnx_stream_t stream);
+
 /* ------------------------------------------------------------------------ */
 /* Segment sums over a CSR (row_ptr / perm from mnx_csr_build of the rows'    */
 /* segment ids): replaces the scatter_add_ of molix.F.scatter_sum / batch_add */
@@ -210,6 +226,29 @@ int mnx_tp_bwd_sender_f32(int32_t config, int32_t channels, const float* x, cons
                           const int32_t* s_perm, const int32_t* s_receivers, int64_t num_nodes,
                           int64_t num_edges, float* grad_x, float* grad_Y, float* grad_w,
                           mnx_stream_t stream);
+
+/* The three calls above with the per-edge weights taken from row wrow[e] of w
+ * (int32 [E], any number of rows) instead of row e: edges whose weights are
+ * equal share one row, e.g. the two directions of an undirected pair, whose
+ * radial MLP inputs (the distance) are the same (the weights the reference
+ * computes per directed edge, radial_mlp.py:76-82, fed to ConvTP,
+ * tensor_product.py:72-79,101-111).  grad_w is still per directed edge
+ * ([E][num_paths*C]); summing it over the edges of a row is the caller's. */
+int mnx_tp_fwd_rows_f32(int32_t config, int32_t channels, const float* x, const float* Y,
+                        const float* w, const int32_t* wrow, const int32_t* row_ptr,
+                        const int32_t* perm, const int32_t* senders_sorted, int64_t num_nodes,
+                        int64_t num_edges, float* out, mnx_stream_t stream);
+int mnx_tp_bwd_rows_f32(int32_t config, int32_t channels, const float* x, const float* Y,
+                        const float* w, const int32_t* wrow, const float* grad_out,
+                        const int32_t* row_ptr, const int32_t* perm, const int32_t* senders_sorted,
+                        int64_t num_nodes, int64_t num_edges, float* grad_x, float* grad_Y,
+                        float* grad_w, void* workspace, size_t workspace_bytes, mnx_stream_t stream);
+int mnx_tp_bwd_sender_rows_f32(int32_t config, int32_t channels, const float* x, const float* Y,
+                               const float* w, const int32_t* wrow, const float* grad_out,
+                               const int32_t* s_row_ptr, const int32_t* s_perm,
+                               const int32_t* s_receivers, int64_t num_nodes, int64_t num_edges,
+                               float* grad_x, float* grad_Y, float* grad_w, mnx_stream_t stream);
+
 
 /* ------------------------------------------------------------------------ */
 /* Particle-mesh Ewald (replaces torch.ops.molix.pme_reciprocal and           */
@@ -433,6 +472,18 @@ int mnx_edge_weights_f32(const float* h, int64_t num_edges, int32_t K, const uin
                          const float* bias, int32_t N, float* w, mnx_stream_t stream);
 int mnx_edge_weights_bwd_f32(const float* grad_w, int64_t num_edges, int32_t N, const uint16_t* frag,
                              int32_t K, float* grad_h, mnx_stream_t stream);
+/* The forward on selected rows of h: w[i] = W h[rows[i]] + b for i < num_rows
+ * (rows int32 [num_rows]; NULL: rows[i] = i), e.g. the lead edge of each
+ * undirected pair (mnx_edge_reverse). */
+int mnx_edge_weights_rows_f32(const float* h, const int32_t* rows, int64_t num_rows, int32_t K,
+                              const uint16_t* frag, const float* bias, int32_t N, float* w, mnx_stream_t stream);
+/* The input gradient of a layer whose rows are shared by two directed edges
+ * (mnx_edge_reverse): grad_h[i][k] = sum_n (grad_w[pairs[i][0]][n] +
+ * grad_w[pairs[i][1]][n]) W[n][k] for the num_pairs rows of h, pairs int32
+ * [num_pairs][2], grad_w per directed edge.  With pairs = NULL it is
+ * mnx_edge_weights_bwd_f32 (num_pairs = num_edges). */
+int mnx_edge_weights_bwd_pairs_f32(const float* grad_w, const int32_t* pairs, int64_t num_pairs, int32_t N,
+                                   const uint16_t* frag, int32_t K, float* grad_h, mnx_stream_t stream);
 
 /* ------------------------------------------------------------------------ */
 /* Fused weight gradient of the tensor product and the output layer of the    */

@@ -46,6 +46,12 @@ SIGNATURES = {
     "mnx_tp_bwd_workspace_bytes": (c_sz, [c_i32, c_i32, c_i64]),
     "mnx_tp_bwd_f32": (C.c_int, [c_i32, c_i32, vp, vp, vp, vp, vp, vp, vp, c_i64, c_i64, vp, vp, vp, vp, c_sz, vp]),
     "mnx_tp_bwd_sender_f32": (C.c_int, [c_i32, c_i32, vp, vp, vp, vp, vp, vp, vp, c_i64, c_i64, vp, vp, vp, vp]),
+    "mnx_tp_fwd_rows_f32": (C.c_int, [c_i32, c_i32, vp, vp, vp, vp, vp, vp, vp, c_i64, c_i64, vp, vp]),
+    "mnx_tp_bwd_rows_f32": (C.c_int, [c_i32, c_i32, vp, vp, vp, vp, vp, vp, vp, vp, c_i64, c_i64, vp, vp, vp, vp,
+                                      c_sz, vp]),
+    "mnx_tp_bwd_sender_rows_f32": (C.c_int, [c_i32, c_i32, vp, vp, vp, vp, vp, vp, vp, vp, c_i64, c_i64, vp, vp,
+                                             vp, vp]),
+    "mnx_edge_reverse": (C.c_int, [vp, c_i64, c_i64, vp, vp, vp, vp, c_i32, vp, vp, vp]),
     "mnx_pme_spread_workspace_bytes": (c_sz, [c_i64, c_i32, c_i32, c_i32]),
     "mnx_pme_spread_f32": (C.c_int, [vp, vp, vp, c_i64, c_i32, c_i32, c_i32, c_i32, c_f64, vp, vp, c_sz, vp]),
     "mnx_pme_spread_f64": (C.c_int, [vp, vp, vp, c_i64, c_i32, c_i32, c_i32, c_i32, c_f64, vp, vp, c_sz, vp]),
@@ -84,6 +90,8 @@ SIGNATURES = {
     "mnx_edge_weights_pack_f32": (C.c_int, [vp, c_i32, c_i32, c_i32, vp, vp]),
     "mnx_edge_weights_f32": (C.c_int, [vp, c_i64, c_i32, vp, vp, c_i32, vp, vp]),
     "mnx_edge_weights_bwd_f32": (C.c_int, [vp, c_i64, c_i32, vp, c_i32, vp, vp]),
+    "mnx_edge_weights_bwd_pairs_f32": (C.c_int, [vp, vp, c_i64, c_i32, vp, c_i32, vp, vp]),
+    "mnx_edge_weights_rows_f32": (C.c_int, [vp, vp, c_i64, c_i32, vp, vp, c_i32, vp, vp]),
     "mnx_tp_weight_grad_f32": (C.c_int, [c_i32, c_i32, vp, vp, vp, vp, c_i64, c_i64, vp, c_i32, vp, vp]),
     "mnx_edge_tp_fwd_f32": (C.c_int, [c_i32, c_i32, vp, vp, vp, vp, c_i64, vp, vp]),
     "mnx_edge_tp_bwd_workspace_bytes": (c_sz, [c_i32, c_i32, c_i64]),

@@ -29,6 +29,11 @@ class _Config:
     # default: on MI355X the fused weight gradient is latency-bound on its per-lane gathers and
     # slower than writing and re-reading the gradient, except for the 1-path-per-l products
     fused_weight_grad: bool = False
+    # True: where the radial MLP's parameters are frozen and no second derivatives are taken (eval
+    # mode), the MLP and its output layer run once per undirected pair of opposite edges whose radial
+    # inputs are bit-identical (a neighbor list's pairs), and the tensor product reads each pair's
+    # weights for both directions (molix::radial_tp_pairs); graphs without such a pairing run per edge
+    paired_radial: bool = True
 
 
 config = _Config()

@@ -118,7 +118,8 @@ __global__ void k_ew_pack(const float* __restrict__ W, EwShape sh, bool bwd, con
 }
 
 template <int KS>
-__global__ __launch_bounds__(kEwFwdThreads) void k_ew_fwd(const float* __restrict__ h, int64_t E,
+__global__ __launch_bounds__(kEwFwdThreads) void k_ew_fwd(const float* __restrict__ h,
+                                                          const int32_t* __restrict__ hrows, int64_t E,
                                                           const f16x8* __restrict__ frag,
                                                           const float* __restrict__ colscale,
                                                           const float* __restrict__ bias, int N, int nstages,
@@ -138,7 +139,8 @@ __global__ __launch_bounds__(kEwFwdThreads) void k_ew_fwd(const float* __restric
     {
         const int64_t row = row0 + (lane & 31);
         const bool ok = row < E;
-        const float* src = h + (ok ? row : 0) * K + 8 * (lane >> 5);
+        const int64_t hrow = ok ? (hrows ? int64_t(hrows[row]) : row) : 0;  // output row -> row of h
+        const float* src = h + hrow * K + 8 * (lane >> 5);
         f32x4 v[KS][2];
         float m = 0.f;
 #pragma unroll
@@ -227,10 +229,13 @@ __global__ __launch_bounds__(kEwFwdThreads) void k_ew_fwd(const float* __restric
     }
 }
 
-template <int T>
+// PAIR: row i of the product is the sum of gradient rows pairs[i][0] and pairs[i][1] (the two
+// directed edges that share one row of weights), E the number of pairs.
+template <int T, bool PAIR>
 __global__ __launch_bounds__(kEwBwdThreads) void k_ew_bwd(const float* __restrict__ gw, int64_t E, int N,
                                                        const f16x8* __restrict__ frag,
                                                        const float* __restrict__ colscale, int K, int nstages,
+                                                       const int32_t* __restrict__ pairs,
                                                        float* __restrict__ gh) {
     constexpr int NQ = 8 / T;
     constexpr int PER = kEwStageVec / kEwBwdThreads;
@@ -239,7 +244,10 @@ __global__ __launch_bounds__(kEwBwdThreads) void k_ew_bwd(const float* __restric
     const int64_t row0 = int64_t(blockIdx.x) * kEwBwdRows + wave * 32;
     const int64_t arow = row0 + (lane & 31);
     const bool aok = arow < E;
-    const float* asrc = gw + (aok ? arow : 0) * N + 8 * (lane >> 5);
+    const int64_t src0 = PAIR ? (aok ? int64_t(pairs[2 * arow]) : 0) : (aok ? arow : 0);
+    const int64_t src1 = PAIR ? (aok ? int64_t(pairs[2 * arow + 1]) : 0) : 0;
+    const float* asrc = gw + src0 * N + 8 * (lane >> 5);
+    const float* bsrc = gw + src1 * N + 8 * (lane >> 5);
 
     f32x4 ra[NQ][2];
     auto fetch_a = [&](int s) {
@@ -250,6 +258,10 @@ __global__ __launch_bounds__(kEwBwdThreads) void k_ew_bwd(const float* __restric
             if (aok && n < N) {
                 lo = *reinterpret_cast<const f32x4*>(asrc + 16 * (NQ * s + q));
                 hi = *reinterpret_cast<const f32x4*>(asrc + 16 * (NQ * s + q) + 4);
+                if (PAIR) {
+                    lo += *reinterpret_cast<const f32x4*>(bsrc + 16 * (NQ * s + q));
+                    hi += *reinterpret_cast<const f32x4*>(bsrc + 16 * (NQ * s + q) + 4);
+                }
             }
             ra[q][0] = lo;
             ra[q][1] = hi;
@@ -368,6 +380,11 @@ int mnx_edge_weights_pack_f32(const float* weight, int32_t K, int32_t N, int32_t
 
 int mnx_edge_weights_f32(const float* h, int64_t num_edges, int32_t K, const uint16_t* frag, const float* bias,
                          int32_t N, float* out, mnx_stream_t stream) {
+    return mnx_edge_weights_rows_f32(h, nullptr, num_edges, K, frag, bias, N, out, stream);
+}
+
+int mnx_edge_weights_rows_f32(const float* h, const int32_t* rows, int64_t num_edges, int32_t K,
+                              const uint16_t* frag, const float* bias, int32_t N, float* out, mnx_stream_t stream) {
     clear_error();
     int rc = check_ew(K, N);
     if (rc) return rc;
@@ -381,10 +398,10 @@ int mnx_edge_weights_f32(const float* h, int64_t num_edges, int32_t K, const uin
     const float* cs = reinterpret_cast<const float*>(frag + sh.planes(false));
     hipStream_t s = (hipStream_t)stream;
     switch (K) {
-        case 16: hipLaunchKernelGGL(k_ew_fwd<1>, grid, block, 0, s, h, num_edges, f, cs, bias, N, sh.stages_f(), out); break;
-        case 32: hipLaunchKernelGGL(k_ew_fwd<2>, grid, block, 0, s, h, num_edges, f, cs, bias, N, sh.stages_f(), out); break;
-        case 64: hipLaunchKernelGGL(k_ew_fwd<4>, grid, block, 0, s, h, num_edges, f, cs, bias, N, sh.stages_f(), out); break;
-        default: hipLaunchKernelGGL(k_ew_fwd<8>, grid, block, 0, s, h, num_edges, f, cs, bias, N, sh.stages_f(), out); break;
+        case 16: hipLaunchKernelGGL(k_ew_fwd<1>, grid, block, 0, s, h, rows, num_edges, f, cs, bias, N, sh.stages_f(), out); break;
+        case 32: hipLaunchKernelGGL(k_ew_fwd<2>, grid, block, 0, s, h, rows, num_edges, f, cs, bias, N, sh.stages_f(), out); break;
+        case 64: hipLaunchKernelGGL(k_ew_fwd<4>, grid, block, 0, s, h, rows, num_edges, f, cs, bias, N, sh.stages_f(), out); break;
+        default: hipLaunchKernelGGL(k_ew_fwd<8>, grid, block, 0, s, h, rows, num_edges, f, cs, bias, N, sh.stages_f(), out); break;
     }
     MNX_CHECK_LAUNCH();
     return MNX_OK;
@@ -392,6 +409,11 @@ int mnx_edge_weights_f32(const float* h, int64_t num_edges, int32_t K, const uin
 
 int mnx_edge_weights_bwd_f32(const float* grad_w, int64_t num_edges, int32_t N, const uint16_t* frag, int32_t K,
                              float* grad_h, mnx_stream_t stream) {
+    return mnx_edge_weights_bwd_pairs_f32(grad_w, nullptr, num_edges, N, frag, K, grad_h, stream);
+}
+
+int mnx_edge_weights_bwd_pairs_f32(const float* grad_w, const int32_t* pairs, int64_t num_edges, int32_t N,
+                                   const uint16_t* frag, int32_t K, float* grad_h, mnx_stream_t stream) {
     clear_error();
     int rc = check_ew(K, N);
     if (rc) return rc;
@@ -405,11 +427,10 @@ int mnx_edge_weights_bwd_f32(const float* grad_w, int64_t num_edges, int32_t N, 
     const f16x8* f = reinterpret_cast<const f16x8*>(frag);
     const float* cs = reinterpret_cast<const float*>(frag + sh.planes(true));
     hipStream_t s = (hipStream_t)stream;
-    switch (sh.tiles_b()) {
-        case 1: hipLaunchKernelGGL(k_ew_bwd<1>, grid, block, 0, s, grad_w, num_edges, N, f, cs, K, sh.stages_b(), grad_h); break;
-        case 2: hipLaunchKernelGGL(k_ew_bwd<2>, grid, block, 0, s, grad_w, num_edges, N, f, cs, K, sh.stages_b(), grad_h); break;
-        default: hipLaunchKernelGGL(k_ew_bwd<4>, grid, block, 0, s, grad_w, num_edges, N, f, cs, K, sh.stages_b(), grad_h); break;
-    }
+    const int tiles = sh.tiles_b();
+    auto fn = pairs ? (tiles == 1 ? k_ew_bwd<1, true> : tiles == 2 ? k_ew_bwd<2, true> : k_ew_bwd<4, true>)
+                    : (tiles == 1 ? k_ew_bwd<1, false> : tiles == 2 ? k_ew_bwd<2, false> : k_ew_bwd<4, false>);
+    hipLaunchKernelGGL(fn, grid, block, 0, s, grad_w, num_edges, N, f, cs, K, sh.stages_b(), pairs, grad_h);
     MNX_CHECK_LAUNCH();
     return MNX_OK;
 }

@@ -6,6 +6,9 @@ coefficients of ``molnex_amd.irreps`` baked in as constants, so every register
 index is static.  Paths are split into groups by the l of irreps_in1; each
 group is one wavefront kernel per (receiver, channel block).
 
+Per-edge weights are read from row wrow[e] of w when wrow is given (edges that share
+their weights, e.g. the two directions of an undirected pair), else from row e.
+
 Forward (per edge, per channel):   out_p[m3] += w_p * sum_m1 M_p[m3][m1] x[m1]
   with the uniform matrix M_p[m3][m1] = sum_m2 c_p[m1,m2,m3] Y[m2].
 Backward (per receiver, per channel), with v_p[m1][m2] = sum_m3 c_p g_p[m3]
@@ -144,7 +147,7 @@ def _emit_prefetch(a, cfg, ps, xs, ys, xi, indent, t_expr, cpl_expr="CPL"):
     for c in ys:
         a(f"{indent}  ny{c} = Yn[{c}];")
     a(f"{indent}  const float* __restrict__ xn = x + int64_t(ns) * XS;")
-    a(f"{indent}  const float* __restrict__ wn = w + int64_t(ne) * WS;")
+    a(f"{indent}  const float* __restrict__ wn = w + int64_t(wrow ? wrow[ne] : ne) * WS;")
     a("#pragma unroll")
     a(f"{indent}  for (int k = 0; k < {cpl_expr}; ++k) {{")
     for c in xs:
@@ -185,8 +188,8 @@ def gen_fwd(cfg: Cfg, g: int) -> str:
     name = f"tp_fwd_c{cfg.idx}_g{g}"
     a(f"template <int CPL, bool FULL>\n__global__ void __launch_bounds__(64) {name}(const float* __restrict__ x, "
       "const float* __restrict__ Y, const float* __restrict__ w, const int32_t* __restrict__ row_ptr, "
-      "const int32_t* __restrict__ perm, const int32_t* __restrict__ snd, int64_t N, int C, "
-      "float* __restrict__ out) {")
+      "const int32_t* __restrict__ perm, const int32_t* __restrict__ snd, const int32_t* __restrict__ wrow, "
+      "int64_t N, int C, float* __restrict__ out) {")
     a("  const int64_t n = xcd_node(blockIdx.x, gridDim.x);")
     a("  if (n >= N) return;")
     a("  const int lane = threadIdx.x;")
@@ -253,6 +256,7 @@ def gen_bwd(cfg: Cfg, g: int) -> str:
     a(f"template <int CPL, bool FULL>\n__global__ void __launch_bounds__(64) {name}(const float* __restrict__ x, "
       "const float* __restrict__ Y, const float* __restrict__ w, const float* __restrict__ gout, "
       "const int32_t* __restrict__ row_ptr, const int32_t* __restrict__ perm, const int32_t* __restrict__ snd, "
+      "const int32_t* __restrict__ wrow, "
       "int64_t N, int C, float* __restrict__ gx, float* __restrict__ gw, float* __restrict__ gyp, int npart, "
       "int pbase) {")
     a("  const int64_t n = xcd_node(blockIdx.x, gridDim.x);")
@@ -413,6 +417,7 @@ def gen_bwd_sender(cfg: Cfg, sg: int, ps, first: bool) -> str:
     a(f"template <int CPL>\n__global__ void __launch_bounds__(64) {name}(const float* __restrict__ x, "
       "const float* __restrict__ Y, const float* __restrict__ w, const float* __restrict__ gout, "
       "const int32_t* __restrict__ row_ptr, const int32_t* __restrict__ perm, const int32_t* __restrict__ rcv, "
+      "const int32_t* __restrict__ wrow, "
       "int64_t N, int C, float* __restrict__ gx, float* __restrict__ gw, float* __restrict__ gyp, int, int) {")
     a("  const int64_t s = xcd_node(blockIdx.x, gridDim.x);")
     a("  if (s >= N) return;")
@@ -449,7 +454,7 @@ def gen_bwd_sender(cfg: Cfg, sg: int, ps, first: bool) -> str:
         for c in ys:
             a(f"{indent}  ny{c} = Yn[{c}];")
         a(f"{indent}  const float* __restrict__ gn = gout + int64_t(nr) * OS;")
-        a(f"{indent}  const float* __restrict__ wn = w + int64_t(ne) * WS;")
+        a(f"{indent}  const float* __restrict__ wn = w + int64_t(wrow ? wrow[ne] : ne) * WS;")
         a("#pragma unroll")
         a(f"{indent}  for (int k = 0; k < CPL; ++k) {{")
         for c in outs:

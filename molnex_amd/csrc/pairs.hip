@@ -1,0 +1,104 @@
+// Undirected pairs of a directed edge list.  The radial MLP's per-edge weights
+// (src/molrep/interaction/radial_mlp.py:76-82, fed to ConvTP,
+// src/molrep/interaction/tensor_product.py:72-79,101-111) depend on the edge
+// only through its radial features, and an edge s -> r and its reverse r -> s
+// have the same distance: a neighbor list emits bond vectors that are exact
+// negations of each other, so their features agree bit for bit.  Pairing the
+// two lets the MLP and its output run once per undirected pair.
+//
+// rev[e] = the one edge e2 != e with sender(e2) = receiver(e),
+// receiver(e2) = sender(e) and feats[e2] equal to feats[e] bit for bit (F
+// floats per edge); -1 when there is none or more than one (periodic images
+// of one pair at equal distances), and then *d_bad counts the edge.  The
+// candidates are the receiver-CSR segment of sender(e) (mnx_csr_build), one
+// thread per edge.  When every segment lists its senders in ascending order
+// (edge lists sorted by receiver and sender, as a neighbor list emits them;
+// checked by a first pass) the thread binary-searches its segment for the run
+// of sender receiver(e), else it scans the whole segment.
+
+#include "common.h"
+
+namespace mnx {
+namespace {
+
+// unsorted[0] = 1 if some receiver segment of the CSR lists a larger sender before a smaller one
+// (positions t, t + 1 of one segment: the same receiver).
+__global__ void k_segments_unsorted(const int64_t* __restrict__ ei, int64_t E, const int32_t* __restrict__ perm,
+                                    const int32_t* __restrict__ snd, int32_t* __restrict__ unsorted) {
+    const int64_t t = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (t + 1 >= E) return;
+    if (snd[t] > snd[t + 1] && ei[2 * int64_t(perm[t]) + 1] == ei[2 * int64_t(perm[t + 1]) + 1]) unsorted[0] = 1;
+}
+
+__global__ void k_edge_reverse(const int64_t* __restrict__ ei, int64_t E, int64_t N,
+                               const int32_t* __restrict__ row_ptr, const int32_t* __restrict__ perm,
+                               const int32_t* __restrict__ snd, const uint32_t* __restrict__ feats, int F,
+                               const int32_t* __restrict__ unsorted, int32_t* __restrict__ rev,
+                               int32_t* __restrict__ bad) {
+    const int64_t e = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (e >= E) return;
+    const int64_t s = ei[2 * e], r = ei[2 * e + 1];
+    int found = -1, count = 0;
+    if (s >= 0 && s < N && r >= 0 && r < N) {
+        const uint32_t* fe = feats + e * F;
+        int beg = row_ptr[s], end = row_ptr[s + 1];
+        if (!unsorted[0]) {  // first position with sender >= r
+            int lo = beg, hi = end;
+            while (lo < hi) {
+                const int mid = (lo + hi) >> 1;
+                if (snd[mid] < r) lo = mid + 1;
+                else hi = mid;
+            }
+            beg = lo;
+        }
+        for (int t = beg; t < end; ++t) {
+            if (snd[t] != r) {
+                if (!unsorted[0] && snd[t] > r) break;
+                continue;
+            }
+            const int e2 = perm[t];
+            if (e2 == e) continue;
+            const uint32_t* f2 = feats + int64_t(e2) * F;
+            bool same = true;
+            for (int k = 0; k < F; ++k) same = same && (f2[k] == fe[k]);
+            if (same) {
+                found = e2;
+                ++count;
+            }
+        }
+    }
+    rev[e] = count == 1 ? found : -1;
+    const uint64_t m = __ballot(count != 1);  // one atomic per wavefront
+    if (m && int(threadIdx.x & 63) == __ffsll((unsigned long long)m) - 1) atomicAdd(bad, int(__popcll(m)));
+}
+
+}  // namespace
+}  // namespace mnx
+
+using namespace mnx;
+
+extern "C" {
+
+int mnx_edge_reverse(const int64_t* edge_index, int64_t num_edges, int64_t num_nodes, const int32_t* row_ptr,
+                     const int32_t* perm, const int32_t* senders_sorted, const float* feats, int32_t num_feats,
+                     int32_t* rev, int32_t* d_bad, mnx_stream_t stream) {
+    clear_error();
+    MNX_REQUIRE(num_edges >= 0 && num_edges < (int64_t(1) << 31) && num_nodes >= 0 &&
+                    num_nodes < (int64_t(1) << 31), "sizes out of range");
+    MNX_REQUIRE(num_feats >= 0 && num_feats <= 1024, "feature width %d out of range", num_feats);
+    if (num_edges == 0) return MNX_OK;
+    MNX_REQUIRE(edge_index && row_ptr && perm && senders_sorted && rev && d_bad && (feats || num_feats == 0),
+                "null pointer argument");
+    const dim3 grid(unsigned(ceil_div(num_edges, 256)));
+    // d_bad[1] holds the segment-order flag (the caller clears both words)
+    hipLaunchKernelGGL(k_segments_unsorted, grid, dim3(256), 0, (hipStream_t)stream, edge_index, num_edges, perm,
+                       senders_sorted, d_bad + 1);
+    MNX_CHECK_LAUNCH();
+    hipLaunchKernelGGL(k_edge_reverse, grid, dim3(256), 0, (hipStream_t)stream, edge_index, num_edges, num_nodes,
+                       row_ptr, perm, senders_sorted, reinterpret_cast<const uint32_t*>(feats), num_feats,
+                       d_bad + 1, rev, d_bad);
+    MNX_CHECK_LAUNCH();
+    return MNX_OK;
+}
+
+}  // extern "C"

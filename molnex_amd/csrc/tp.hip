@@ -107,9 +107,9 @@ struct TPConfigInfo {
 };
 
 typedef void (*TPFwdFn)(const float*, const float*, const float*, const int32_t*, const int32_t*, const int32_t*,
-                        int64_t, int, float*);
+                        const int32_t*, int64_t, int, float*);
 typedef void (*TPBwdFn)(const float*, const float*, const float*, const float*, const int32_t*, const int32_t*,
-                        const int32_t*, int64_t, int, float*, float*, float*, int, int);
+                        const int32_t*, const int32_t*, int64_t, int, float*, float*, float*, int, int);
 
 #include "tp_gen.inc"
 
@@ -174,6 +174,12 @@ int mnx_tp_config_info(int32_t config, int32_t* info) {
 int mnx_tp_fwd_f32(int32_t config, int32_t C, const float* x, const float* Y, const float* w,
                    const int32_t* row_ptr, const int32_t* perm, const int32_t* snd, int64_t N, int64_t E,
                    float* out, mnx_stream_t stream) {
+    return mnx_tp_fwd_rows_f32(config, C, x, Y, w, nullptr, row_ptr, perm, snd, N, E, out, stream);
+}
+
+int mnx_tp_fwd_rows_f32(int32_t config, int32_t C, const float* x, const float* Y, const float* w,
+                        const int32_t* wrow, const int32_t* row_ptr, const int32_t* perm, const int32_t* snd,
+                        int64_t N, int64_t E, float* out, mnx_stream_t stream) {
     clear_error();
     int rc = check_common(config, C, N, E);
     if (rc) return rc;
@@ -186,7 +192,7 @@ int mnx_tp_fwd_f32(int32_t config, int32_t C, const float* x, const float* Y, co
     for (int g = 0; g < cfg.ngroups; ++g) {
         const bool full = C % (64 * cpl) == 0;
         TPFwdFn fn = cpl == 2 ? (full ? kTPFwdF2 : kTPFwd2)[config][g] : (full ? kTPFwdF1 : kTPFwd1)[config][g];
-        hipLaunchKernelGGL(fn, grid, dim3(64), 0, (hipStream_t)stream, x, Y, w, row_ptr, perm, snd, N, C, out);
+        hipLaunchKernelGGL(fn, grid, dim3(64), 0, (hipStream_t)stream, x, Y, w, row_ptr, perm, snd, wrow, N, C, out);
         MNX_CHECK_LAUNCH();
     }
     return MNX_OK;
@@ -201,6 +207,14 @@ size_t mnx_tp_bwd_workspace_bytes(int32_t config, int32_t C, int64_t E) {
 int mnx_tp_bwd_f32(int32_t config, int32_t C, const float* x, const float* Y, const float* w, const float* gout,
                    const int32_t* row_ptr, const int32_t* perm, const int32_t* snd, int64_t N, int64_t E,
                    float* gx, float* gY, float* gw, void* ws, size_t ws_bytes, mnx_stream_t stream) {
+    return mnx_tp_bwd_rows_f32(config, C, x, Y, w, nullptr, gout, row_ptr, perm, snd, N, E, gx, gY, gw, ws,
+                               ws_bytes, stream);
+}
+
+int mnx_tp_bwd_rows_f32(int32_t config, int32_t C, const float* x, const float* Y, const float* w,
+                        const int32_t* wrow, const float* gout, const int32_t* row_ptr, const int32_t* perm,
+                        const int32_t* snd, int64_t N, int64_t E, float* gx, float* gY, float* gw, void* ws,
+                        size_t ws_bytes, mnx_stream_t stream) {
     clear_error();
     int rc = check_common(config, C, N, E);
     if (rc) return rc;
@@ -223,7 +237,7 @@ int mnx_tp_bwd_f32(int32_t config, int32_t C, const float* x, const float* Y, co
         const bool full = C % (64 * kTPBwdCPL[config][g]) == 0;
         hipLaunchKernelGGL((full ? kTPBwdF : kTPBwd)[config][g], node_grid(N, cblocks), dim3(64), 0,
                            (hipStream_t)stream, x, Y, w, gout,
-                           row_ptr, perm, snd, N, C, gx, gw, part, npart, pbase);
+                           row_ptr, perm, snd, wrow, N, C, gx, gw, part, npart, pbase);
         MNX_CHECK_LAUNCH();
         pbase += cblocks;
     }
@@ -240,6 +254,14 @@ int mnx_tp_bwd_sender_f32(int32_t config, int32_t C, const float* x, const float
                           const float* gout, const int32_t* s_row_ptr, const int32_t* s_perm,
                           const int32_t* s_receivers, int64_t N, int64_t E, float* gx, float* gY, float* gw,
                           mnx_stream_t stream) {
+    return mnx_tp_bwd_sender_rows_f32(config, C, x, Y, w, nullptr, gout, s_row_ptr, s_perm, s_receivers, N, E, gx,
+                                      gY, gw, stream);
+}
+
+int mnx_tp_bwd_sender_rows_f32(int32_t config, int32_t C, const float* x, const float* Y, const float* w,
+                               const int32_t* wrow, const float* gout, const int32_t* s_row_ptr,
+                               const int32_t* s_perm, const int32_t* s_receivers, int64_t N, int64_t E, float* gx,
+                               float* gY, float* gw, mnx_stream_t stream) {
     clear_error();
     int rc = check_common(config, C, N, E);
     if (rc) return rc;
@@ -257,7 +279,7 @@ int mnx_tp_bwd_sender_f32(int32_t config, int32_t C, const float* x, const float
     for (int g = 0; g < kTPBwSNum[config]; ++g) {
         const int cblocks = int(ceil_div(C, 64 * kTPBwSCPL[config][g]));
         hipLaunchKernelGGL(kTPBwS[config][g], node_grid(N, cblocks), dim3(64), 0, (hipStream_t)stream, x, Y, w,
-                           gout, s_row_ptr, s_perm, s_receivers, N, C, gx, gw, E > 0 ? gY : nullptr, 0, 0);
+                           gout, s_row_ptr, s_perm, s_receivers, wrow, N, C, gx, gw, E > 0 ? gY : nullptr, 0, 0);
         MNX_CHECK_LAUNCH();
     }
     return MNX_OK;

@@ -20,6 +20,8 @@ Ops
 ``molix::block_linear``         equivariant (ir_mul) block linear with pre-ordered weights (``cuet.Linear``)
 ``molix::indexed_block_linear`` the block linear with one weight set per node class (ElementUpdate)
 ``molix::radial_tp``            radial-MLP output layer + tp_scatter, backward through ``molix::tp_weight_grad``
+``molix::edge_reverse``         the opposite edge of each edge (undirected pairs with identical radial inputs)
+``molix::radial_tp_pairs``      radial-MLP output layer once per undirected pair + tp_scatter over both directions
 ``molix::segment_sum``          weighted segment sum of rows by segment id (scatter_sum / MessageAggregation)
 """
 
@@ -317,14 +319,24 @@ def tp_config_info(config: int) -> tuple[int, int, int, int]:
     return tuple(info)
 
 
+def _check_wrow(wrow: Tensor | None, E: int, Ew: int, what: str) -> None:
+    if wrow is None:
+        if Ew != E:
+            raise ValueError(f"{what}: w has {Ew} rows for {E} edges")
+    elif wrow.dtype != torch.int32 or wrow.shape != (E,) or not wrow.is_contiguous():
+        raise ValueError(f"{what}: wrow must be a contiguous int32 ({E},) tensor")
+
+
 @torch.library.custom_op("molix::tp_scatter", mutates_args=(), device_types="cuda")
 def tp_scatter(x: Tensor, Y: Tensor, w: Tensor, row_ptr: Tensor, perm: Tensor, senders: Tensor, config: int,
                channels: int, s_row_ptr: Tensor | None = None, s_perm: Tensor | None = None,
-               s_receivers: Tensor | None = None) -> Tensor:
+               s_receivers: Tensor | None = None, wrow: Tensor | None = None) -> Tensor:
     """``out[r] = sum_{e -> r} TP(x[send(e)], Y[e]; w[e])`` for a compiled configuration.
 
     ``(row_ptr, perm, senders)`` is the receiver CSR (``edge_csr``).  The optional sender CSR
-    (``edge_csr`` of the column-swapped edge list) selects the atomic-free backward."""
+    (``edge_csr`` of the column-swapped edge list) selects the atomic-free backward.  With ``wrow``
+    (int32, one entry per edge) edge e takes its weights from row ``wrow[e]`` of ``w`` (rows shared
+    by edges with equal weights, e.g. the two directions of an undirected pair)."""
     _require_gpu("tp_scatter", x, Y, w, row_ptr)
     num_paths, nx, ny, no = tp_config_info(config)
     N = row_ptr.shape[0] - 1
@@ -332,19 +344,20 @@ def tp_scatter(x: Tensor, Y: Tensor, w: Tensor, row_ptr: Tensor, perm: Tensor, s
     xs = _f32_rows(x, nx * channels, "x")
     Ys = _f32_rows(Y, ny, "Y")
     ws_ = _f32_rows(w, num_paths * channels, "w")
-    if xs.shape[0] != N or ws_.shape[0] != E or perm.shape[0] != E:
-        raise ValueError("tp_scatter: inconsistent sizes of x / Y / w / CSR")
+    if xs.shape[0] != N or perm.shape[0] != E:
+        raise ValueError("tp_scatter: inconsistent sizes of x / Y / CSR")
+    _check_wrow(wrow, E, ws_.shape[0], "tp_scatter")
     if s_row_ptr is not None and (s_row_ptr.shape[0] != N + 1 or s_perm is None or s_receivers is None
                                   or s_perm.shape[0] != E or s_receivers.shape[0] != E):
         raise ValueError("tp_scatter: inconsistent sender CSR")
     out = torch.empty((N, no * channels), dtype=torch.float32, device=xs.device)
-    check(_lib.load().mnx_tp_fwd_f32(config, channels, ptr(xs), ptr(Ys), ptr(ws_), ptr(row_ptr), ptr(perm),
-                                     ptr(senders), N, E, ptr(out), _stream(xs)), "tp_scatter")
+    check(_lib.load().mnx_tp_fwd_rows_f32(config, channels, ptr(xs), ptr(Ys), ptr(ws_), ptr(wrow), ptr(row_ptr),
+                                          ptr(perm), ptr(senders), N, E, ptr(out), _stream(xs)), "tp_scatter")
     return out
 
 
 @tp_scatter.register_fake
-def _(x, Y, w, row_ptr, perm, senders, config, channels, s_row_ptr=None, s_perm=None, s_receivers=None):
+def _(x, Y, w, row_ptr, perm, senders, config, channels, s_row_ptr=None, s_perm=None, s_receivers=None, wrow=None):
     num_paths, nx, ny, no = tp_config_info(config)
     return x.new_empty((row_ptr.shape[0] - 1, no * channels))
 
@@ -353,9 +366,11 @@ def _(x, Y, w, row_ptr, perm, senders, config, channels, s_row_ptr=None, s_perm=
 def tp_scatter_backward(grad_out: Tensor, x: Tensor, Y: Tensor, w: Tensor, row_ptr: Tensor, perm: Tensor,
                         senders: Tensor, config: int, channels: int, need_x: bool, need_Y: bool,
                         need_w: bool, s_row_ptr: Tensor | None = None, s_perm: Tensor | None = None,
-                        s_receivers: Tensor | None = None) -> tuple[Tensor, Tensor, Tensor]:
+                        s_receivers: Tensor | None = None, wrow: Tensor | None = None) -> tuple[Tensor, Tensor, Tensor]:
     """Gradients of ``<grad_out, tp_scatter(...)>`` w.r.t. x, Y, w (empty when not needed).
-    With the sender CSR the gradients are walked by sender (grad_x without atomics)."""
+    With the sender CSR the gradients are walked by sender (grad_x without atomics).  With
+    ``wrow`` the weight gradient is per edge, (E, num_paths * C), not yet summed over the edges
+    that share a row of ``w``."""
     lib = _lib.load()
     num_paths, nx, ny, no = tp_config_info(config)
     N = row_ptr.shape[0] - 1
@@ -364,6 +379,7 @@ def tp_scatter_backward(grad_out: Tensor, x: Tensor, Y: Tensor, w: Tensor, row_p
     Ys = _f32_rows(Y, ny, "Y")
     wss = _f32_rows(w, num_paths * channels, "w")
     go = _f32_rows(grad_out, no * channels, "grad_out")
+    _check_wrow(wrow, E, wss.shape[0], "tp_scatter_backward")
     dev = xs.device
     by_sender = s_row_ptr is not None
     if need_x:
@@ -371,16 +387,16 @@ def tp_scatter_backward(grad_out: Tensor, x: Tensor, Y: Tensor, w: Tensor, row_p
     else:
         gx = xs.new_empty(0)
     gY = torch.empty_like(Ys) if need_Y else Ys.new_empty(0)
-    gw = torch.empty_like(wss) if need_w else wss.new_empty(0)
+    gw = wss.new_empty(E, num_paths * channels) if need_w else wss.new_empty(0)
     if by_sender:
-        check(lib.mnx_tp_bwd_sender_f32(config, channels, ptr(xs), ptr(Ys), ptr(wss), ptr(go), ptr(s_row_ptr),
-                                        ptr(s_perm), ptr(s_receivers), N, E, ptr(gx), ptr(gY), ptr(gw),
-                                        _stream(xs)), "tp_scatter backward (by sender)")
+        check(lib.mnx_tp_bwd_sender_rows_f32(config, channels, ptr(xs), ptr(Ys), ptr(wss), ptr(wrow), ptr(go),
+                                             ptr(s_row_ptr), ptr(s_perm), ptr(s_receivers), N, E, ptr(gx), ptr(gY),
+                                             ptr(gw), _stream(xs)), "tp_scatter backward (by sender)")
     else:
         ws = _ws(lib.mnx_tp_bwd_workspace_bytes(config, channels, E) if need_Y else 1, dev)
-        check(lib.mnx_tp_bwd_f32(config, channels, ptr(xs), ptr(Ys), ptr(wss), ptr(go), ptr(row_ptr), ptr(perm),
-                                 ptr(senders), N, E, ptr(gx), ptr(gY), ptr(gw), ptr(ws), ws.numel(), _stream(xs)),
-              "tp_scatter backward")
+        check(lib.mnx_tp_bwd_rows_f32(config, channels, ptr(xs), ptr(Ys), ptr(wss), ptr(wrow), ptr(go),
+                                      ptr(row_ptr), ptr(perm), ptr(senders), N, E, ptr(gx), ptr(gY), ptr(gw),
+                                      ptr(ws), ws.numel(), _stream(xs)), "tp_scatter backward")
     if E == 0:
         gY.zero_() if need_Y else None
     return gx, gY, gw
@@ -388,25 +404,27 @@ def tp_scatter_backward(grad_out: Tensor, x: Tensor, Y: Tensor, w: Tensor, row_p
 
 @tp_scatter_backward.register_fake
 def _(grad_out, x, Y, w, row_ptr, perm, senders, config, channels, need_x, need_Y, need_w, s_row_ptr=None,
-      s_perm=None, s_receivers=None):
+      s_perm=None, s_receivers=None, wrow=None):
     return (torch.empty_like(x) if need_x else x.new_empty(0), torch.empty_like(Y) if need_Y else Y.new_empty(0),
-            torch.empty_like(w) if need_w else w.new_empty(0))
+            w.new_empty(Y.shape[0], w.shape[1]) if need_w else w.new_empty(0))
 
 
 def _tp_setup(ctx, inputs, output):
-    x, Y, w, row_ptr, perm, senders, config, channels, s_row_ptr, s_perm, s_receivers = inputs
-    ctx.save_for_backward(x, Y, w, row_ptr, perm, senders)
+    x, Y, w, row_ptr, perm, senders, config, channels, s_row_ptr, s_perm, s_receivers, wrow = inputs
+    ctx.save_for_backward(x, Y, w, row_ptr, perm, senders, wrow)
     ctx.sender_csr = (s_row_ptr, s_perm, s_receivers)
     ctx.config, ctx.channels = config, channels
 
 
 def _tp_backward(ctx, grad_out):
-    x, Y, w, row_ptr, perm, senders = ctx.saved_tensors
+    x, Y, w, row_ptr, perm, senders, wrow = ctx.saved_tensors
     nx, nY, nw = ctx.needs_input_grad[:3]
     gx, gY, gw = tp_scatter_backward(grad_out.contiguous(), x, Y, w, row_ptr, perm, senders, ctx.config,
-                                     ctx.channels, nx, nY, nw, *ctx.sender_csr)
+                                     ctx.channels, nx, nY, nw, *ctx.sender_csr, wrow)
+    if nw and wrow is not None:  # sum the per-edge gradients over the edges that share a row
+        gw = torch.zeros(w.shape[0], gw.shape[1], dtype=gw.dtype, device=gw.device).index_add_(0, wrow.long(), gw)
     return (gx.reshape(x.shape) if nx else None, gY.reshape(Y.shape) if nY else None,
-            gw.reshape(w.shape) if nw else None, None, None, None, None, None, None, None, None)
+            gw.reshape(w.shape) if nw else None, None, None, None, None, None, None, None, None, None)
 
 
 tp_scatter.register_autograd(_tp_backward, setup_context=_tp_setup)
@@ -961,9 +979,10 @@ def _ew_frag(weight: Tensor, backward: bool) -> Tensor:
 @torch.library.custom_op("molix::edge_weights", mutates_args=(), device_types="cuda")
 def edge_weights(h: Tensor, weight: Tensor, bias: Tensor | None = None) -> Tensor:
     """``h @ weight.T + bias``: the last Linear of ``RadialWeightMLP`` (``radial_mlp.py:38-93``) mapping
-    the (E, K) hidden activations to the (E, N) per-edge tensor-product weights.  fp32-accurate:
-    each operand split exactly into three bf16 parts, six partial products accumulated in fp32 on
-    the matrix cores."""
+    the (E, K) hidden activations to the (E, N) per-edge tensor-product weights.  Near-fp32: rows of
+    h and columns of the weight are scaled by powers of two into [1, 2), each value is split into
+    two fp16 parts, and three partial products per pair are accumulated in fp32 on the matrix cores
+    (the scales are undone exactly)."""
     _require_gpu("edge_weights", h, weight, bias)
     if h.dtype != torch.float32 or weight.dtype != torch.float32 or h.dim() != 2 or weight.dim() != 2:
         raise TypeError("edge_weights: h (E, K) and weight (N, K) must be float32")
@@ -984,6 +1003,18 @@ def edge_weights(h: Tensor, weight: Tensor, bias: Tensor | None = None) -> Tenso
 @edge_weights.register_fake
 def _(h, weight, bias=None):
     return h.new_empty(h.shape[0], weight.shape[0])
+
+
+def _edge_weights_rows(h: Tensor, rows: Tensor, weight: Tensor, bias: Tensor | None) -> Tensor:
+    """``h[rows] @ weight.T + bias`` (rows int32), reading the selected rows of h in place."""
+    N, K = weight.shape
+    x = _aligned16(h.to(torch.float32))
+    frag = _ew_frag(weight, False)
+    out = x.new_empty(rows.shape[0], N)
+    b = None if bias is None else bias.detach().contiguous()
+    check(_lib.load().mnx_edge_weights_rows_f32(ptr(x), ptr(rows), rows.shape[0], K, ptr(frag), ptr(b), N,
+                                                ptr(out), _stream(x)), "edge_weights (rows)")
+    return out
 
 
 @torch.library.custom_op("molix::edge_weights_backward", mutates_args=(), device_types="cuda")
@@ -1092,6 +1123,8 @@ def _rtp_setup(ctx, inputs, output):
     x, Y, h, weight, bias, row_ptr, perm, senders, edge_index, config, channels = inputs
     ctx.save_for_backward(x, Y, h, weight, output[1], row_ptr, perm, senders, edge_index)
     ctx.config, ctx.channels = config, channels
+    # the returned weights usually get no gradient: pass None rather than an (E, N) zero tensor
+    ctx.set_materialize_grads(False)
 
 
 def _rtp_backward(ctx, g_out, g_w):
@@ -1116,6 +1149,170 @@ def _rtp_backward(ctx, g_out, g_w):
 
 
 radial_tp.register_autograd(_rtp_backward, setup_context=_rtp_setup)
+
+
+# ---------------------------------------------------------------------------
+# Undirected pairs: the radial MLP once per pair of opposite edges
+# ---------------------------------------------------------------------------
+
+
+@torch.library.custom_op("molix::edge_reverse", mutates_args=(), device_types="cuda")
+def edge_reverse(edge_index: Tensor, num_nodes: int, row_ptr: Tensor, perm: Tensor, senders: Tensor,
+                 feats: Tensor) -> tuple[Tensor, Tensor]:
+    """``(rev, bad)``: ``rev[e]`` (int32) is the edge that runs opposite to e (sender and receiver
+    swapped) with bit-identical features ``feats[e]`` (the radial inputs of the MLP), or -1 when there
+    is not exactly one; ``bad`` (int32, one element) counts the edges without a partner."""
+    _require_gpu("edge_reverse", edge_index, feats)
+    E = edge_index.shape[0]
+    f = feats.to(torch.float32).reshape(E, -1).contiguous()
+    ei = edge_index.to(torch.int64).contiguous()
+    rev = torch.empty(E, dtype=torch.int32, device=ei.device)
+    bad = torch.zeros(2, dtype=torch.int32, device=ei.device)
+    check(_lib.load().mnx_edge_reverse(ptr(ei), E, num_nodes, ptr(row_ptr), ptr(perm), ptr(senders), ptr(f),
+                                       f.shape[1], ptr(rev), ptr(bad), _stream(ei)), "edge_reverse")
+    return rev, bad[:1].clone()
+
+
+@edge_reverse.register_fake
+def _(edge_index, num_nodes, row_ptr, perm, senders, feats):
+    return (edge_index.new_empty((edge_index.shape[0],), dtype=torch.int32),
+            edge_index.new_empty((1,), dtype=torch.int32))
+
+
+class EdgePairs:
+    """The undirected pairs of a directed edge list whose two directions carry identical radial
+    features (a neighbor list's pairs: opposite bond vectors are exact negations).  ``pairs``
+    (int32, (E/2, 2)): the two edges of each pair, pair i led by its lower edge id, in ascending
+    order of that id; ``wrow`` (int32, (E,)): the pair of each edge; ``lead`` (int64, (E/2,)): the
+    lower edge of each pair.  ``build`` returns None unless every edge has exactly one partner
+    (one host synchronisation)."""
+
+    def __init__(self, pairs: Tensor, wrow: Tensor, lead: Tensor):
+        self.pairs, self.wrow, self.lead = pairs, wrow, lead
+
+    @staticmethod
+    def build(edge_index: Tensor, num_nodes: int, row_ptr: Tensor, perm: Tensor, senders: Tensor,
+              feats: Tensor) -> "EdgePairs | None":
+        E = edge_index.shape[0]
+        if E == 0 or E % 2:
+            return None
+        rev, bad = edge_reverse(edge_index, num_nodes, row_ptr, perm, senders, feats)
+        ids = torch.arange(E, device=rev.device, dtype=torch.int32)
+        back = rev[rev.clamp(min=0).long()]
+        broken = bad.sum() + ((rev >= 0) & (back != ids)).sum()
+        if int(broken.item()) != 0:
+            return None
+        # an involution without fixed points: every pair has one lead (its lower edge id), E/2 in all
+        lead_mask = ids < rev
+        rank = torch.cumsum(lead_mask.to(torch.int32), 0, dtype=torch.int32) - 1
+        slot = torch.where(lead_mask, rank, E // 2).long()  # non-leads go to a spare last slot
+        lead = torch.empty(E // 2 + 1, dtype=torch.int64, device=rev.device).scatter_(0, slot, ids.long())[:E // 2]
+        wrow = rank[torch.minimum(ids, rev).long()].contiguous()
+        pairs = torch.stack([lead.to(torch.int32), rev[lead]], dim=1).contiguous()
+        return EdgePairs(pairs, wrow, lead.contiguous())
+
+
+@torch.library.custom_op("molix::edge_weights_backward_pairs", mutates_args=(), device_types="cuda")
+def edge_weights_backward_pairs(grad: Tensor, pairs: Tensor, weight: Tensor) -> Tensor:
+    """``(grad[pairs[:, 0]] + grad[pairs[:, 1]]) @ weight``: dL/dh of an output layer applied once per
+    undirected pair, from the per-edge weight gradient (same split-fp16 arithmetic as
+    ``edge_weights_backward``, the two rows added as they are loaded)."""
+    N, K = weight.shape
+    if grad.dim() != 2 or grad.shape[1] != N:
+        raise ValueError("edge_weights_backward_pairs: grad must be (E, N)")
+    if pairs.dtype != torch.int32 or pairs.dim() != 2 or pairs.shape[1] != 2 or not pairs.is_contiguous():
+        raise ValueError("edge_weights_backward_pairs: pairs must be a contiguous int32 (P, 2) tensor")
+    g = _aligned16(grad.to(torch.float32))
+    frag = _ew_frag(weight, True)
+    gh = g.new_empty(pairs.shape[0], K)
+    check(_lib.load().mnx_edge_weights_bwd_pairs_f32(ptr(g), ptr(pairs), pairs.shape[0], N, ptr(frag), K, ptr(gh),
+                                                     _stream(g)), "edge_weights backward (pairs)")
+    return gh
+
+
+@edge_weights_backward_pairs.register_fake
+def _(grad, pairs, weight):
+    return grad.new_empty(pairs.shape[0], weight.shape[1])
+
+
+@torch.library.custom_op("molix::radial_tp_pairs", mutates_args=(), device_types="cuda")
+def radial_tp_pairs(x: Tensor, Y: Tensor, h: Tensor, weight: Tensor, bias: Tensor | None, row_ptr: Tensor,
+                    perm: Tensor, senders: Tensor, wrow: Tensor, pairs: Tensor, config: int,
+                    channels: int) -> tuple[Tensor, Tensor]:
+    """``(tp_scatter(x, Y, w[wrow]), w)`` with ``w = h @ weight.T + bias`` computed once per undirected
+    pair (``wrow`` maps every edge to its pair, ``pairs`` lists each pair's two edges, lead first:
+    ``EdgePairs``).  Equal to the output layer applied per directed edge (the reference's
+    composition, ``mace.py:321-329``, ``tensor_product.py:101-111``), since both directions of a pair
+    have the same radial inputs.  ``w`` (one row per pair) is returned for the backward.
+
+    ``h``, the radial MLP's hidden activations (``radial_mlp.py:76-82``), has one row per pair (its
+    lead edge's; pair mode) or one row per edge (edge mode).  In pair mode the backward adds the two
+    edges' weight gradients as it forms the output layer's input gradient
+    (``edge_weights_backward_pairs``): the gradient reaching each pair's radial inputs is the sum
+    of both directions', which leaves every function of the positions (energies, forces, virials)
+    as per edge.  In edge mode the forward uses the lead rows of ``h`` and the backward gives every
+    edge its own input gradient (``edge_weights_backward``), as the per-edge composition does."""
+    if h.shape[0] == pairs.shape[0]:
+        w = edge_weights(h, weight, bias)
+    else:  # the lead rows of h, read in place
+        w = _edge_weights_rows(h, pairs[:, 0].contiguous(), weight, bias)
+    return tp_scatter(x, Y, w, row_ptr, perm, senders, config, channels, wrow=wrow), w
+
+
+@radial_tp_pairs.register_fake
+def _(x, Y, h, weight, bias, row_ptr, perm, senders, wrow, pairs, config, channels):
+    num_paths, nx, ny, no = tp_config_info(config)
+    return x.new_empty((row_ptr.shape[0] - 1, no * channels)), h.new_empty((h.shape[0], weight.shape[0]))
+
+
+def _rtpp_setup(ctx, inputs, output):
+    x, Y, h, weight, bias, row_ptr, perm, senders, wrow, pairs, config, channels = inputs
+    ctx.save_for_backward(x, Y, h, weight, output[1], row_ptr, perm, senders, wrow, pairs)
+    ctx.config, ctx.channels, ctx.has_bias = config, channels, bias is not None
+    # the returned weights usually get no gradient: pass None rather than a (pairs, N) zero tensor
+    ctx.set_materialize_grads(False)
+
+
+def _rtpp_backward(ctx, g_out, g_w):
+    x, Y, h, weight, w, row_ptr, perm, senders, wrow, pairs = ctx.saved_tensors
+    nig = ctx.needs_input_grad
+    need_x, need_Y, need_h, need_W = nig[0], nig[1], nig[2], nig[3]
+    need_b = nig[4] and ctx.has_bias
+    gx = gY = gh = gW = gb = None
+    gw = None  # per-edge weight gradient, (E, N)
+    if g_out is not None and (need_x or need_Y or need_h or need_W or need_b):
+        gx, gY, gw = tp_scatter_backward(g_out.contiguous(), x, Y, w, row_ptr, perm, senders, ctx.config,
+                                         ctx.channels, need_x, need_Y, need_h or need_W or need_b, wrow=wrow)
+        gx = gx.reshape(x.shape) if need_x else None
+        gY = gY.reshape(Y.shape) if need_Y else None
+        if not (need_h or need_W or need_b):
+            gw = None
+    per_pair = h.shape[0] == pairs.shape[0]
+    lead = pairs[:, 0].long()
+    if need_h:
+        if gw is None:
+            gh = torch.zeros_like(h)
+        elif per_pair:
+            gh = edge_weights_backward_pairs(gw, pairs, weight)
+        else:
+            gh = edge_weights_backward(gw, weight)
+        if g_w is not None:  # a caller that used the returned per-pair weights as well
+            ghw = edge_weights_backward(g_w.contiguous(), weight)
+            gh = gh + ghw if per_pair else gh.index_add(0, lead, ghw)
+    if need_W or need_b:  # training: the per-pair weight gradient, then hipBLASLt GEMMs
+        gp = gw[lead] + gw[pairs[:, 1].long()] if gw is not None else torch.zeros_like(w)
+        if g_w is not None:
+            gp = gp + g_w
+        if need_W:
+            hl = h if per_pair else h.index_select(0, lead)
+            gW = torch.zeros_like(weight)
+            for i in range(0, hl.shape[0], _EW_ROWS):
+                gW.addmm_(gp[i:i + _EW_ROWS].t(), hl[i:i + _EW_ROWS])
+        gb = gp.sum(0) if need_b else None
+    return gx, gY, gh, gW, gb, None, None, None, None, None, None, None
+
+
+radial_tp_pairs.register_autograd(_rtpp_backward, setup_context=_rtpp_setup)
 
 
 # ---------------------------------------------------------------------------

@@ -49,6 +49,18 @@ class EdgeGraph:
         self.row_ptr, self.perm, self.senders = torch.ops.molix.edge_csr(edge_index, num_nodes,
                                                                          config.validate_edges)
         self._sender_csr = None
+        self._pairs = None  # (features tensor, its version, EdgePairs or None)
+
+    def pairs(self, feats: torch.Tensor):
+        """The undirected pairs of this graph whose two edges have bit-identical rows of ``feats``
+        (``kernels.EdgePairs``; None when some edge has no such partner), built once per features
+        tensor (one host synchronisation)."""
+        p = self._pairs
+        if p is None or p[0] is not feats or p[1] != feats._version:
+            built = K.EdgePairs.build(self.edge_index, self.num_nodes, self.row_ptr, self.perm, self.senders,
+                                      feats.detach())
+            self._pairs = p = (feats, feats._version, built)
+        return p[2]
 
     def sender_csr(self):
         if self._sender_csr is None:
@@ -144,12 +156,27 @@ class ConvTP(nn.Module):
     def forward_radial(self, node_features: torch.Tensor, edge_angular: torch.Tensor, edge_index: torch.Tensor,
                        radial_mlp, edge_feats: torch.Tensor) -> torch.Tensor:
         """``forward(..., tp_weights=radial_mlp(edge_feats))`` (the composition of mace.py:321-332).
-        When the output layer's parameters need no gradient (energy + forces with a fixed model) and
-        no second derivatives are taken (eval mode), its weights and the product run as
-        ``molix::radial_tp``, whose backward forms the per-edge weight gradient in registers
-        (``molix::tp_weight_grad``) instead of writing and re-reading it."""
+        When the MLP's parameters need no gradient (energy + forces with a fixed model) and no second
+        derivatives are taken (eval mode), and every edge has an opposite edge with bit-identical
+        radial features (a neighbor list's pairs), the MLP runs once per undirected pair and the
+        product reads each pair's weights for both directions (``molix::radial_tp_pairs``): the same
+        weights as per edge, half the MLP work and half the weight tensor.  Otherwise, with
+        ``config.fused_weight_grad``, the output layer and the product run as ``molix::radial_tp``,
+        whose backward forms the per-edge weight gradient in registers (``molix::tp_weight_grad``)."""
         last = radial_mlp.mlp[-1]
         x = node_features
+        if (config.paired_radial and not self.training and x.is_cuda and x.dtype == torch.float32
+                and edge_feats.dim() == 2 and not config.deterministic and not torch.compiler.is_compiling()
+                and not any(p.requires_grad for p in radial_mlp.parameters())
+                and K.edge_weights_supported(last.in_features, last.out_features)):
+            g = edge_graph(edge_index, x.shape[0])
+            pairs = g.pairs(edge_feats)
+            if pairs is not None:
+                h = radial_mlp.hidden(edge_feats.index_select(0, pairs.lead))
+                out, _ = torch.ops.molix.radial_tp_pairs(x, edge_angular, h, last.weight, last.bias, g.row_ptr,
+                                                         g.perm, g.senders, pairs.wrow, pairs.pairs,
+                                                         self.cue_tp.config_id, self.cue_tp.channels)
+                return out
         if (config.fused_weight_grad and not self.training and x.is_cuda and x.dtype == torch.float32
                 and not config.deterministic and not last.weight.requires_grad
                 and (last.bias is None or not last.bias.requires_grad)

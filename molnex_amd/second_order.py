@@ -195,7 +195,8 @@ K.edge_weights_backward.register_autograd(_ew2_bwd, setup_context=_ew2_setup)
 
 def _tp2_setup(ctx, inputs, output):
     (g, x, Y, w, row_ptr, perm, senders, config, channels, need_x, need_Y, need_w, s_row_ptr, s_perm,
-     s_receivers) = inputs
+     s_receivers, wrow) = inputs
+    ctx.shared_rows = wrow is not None
     ctx.save_for_backward(g, x, Y, w, row_ptr, perm, senders)
     ctx.sender_csr = (s_row_ptr, s_perm, s_receivers) if s_row_ptr is not None else ()
     ctx.cfg = (config, channels)
@@ -203,6 +204,9 @@ def _tp2_setup(ctx, inputs, output):
 
 
 def _tp2_bwd(ctx, ggx, ggY, ggw):
+    if ctx.shared_rows:
+        raise NotImplementedError("second derivatives of tp_scatter with shared weight rows (wrow) are not "
+                                  "implemented; use one weight row per edge when differentiating twice")
     g, x, Y, w, row_ptr, perm, senders = ctx.saved_tensors
     csr = (row_ptr, perm, senders)
     cfg, extra = ctx.cfg, ctx.sender_csr
@@ -231,7 +235,7 @@ def _tp2_bwd(ctx, ggx, ggY, ggw):
         bx, bY, _ = K.tp_scatter_backward(g, x, Y, ggw, *csr, *cfg, want_x, want_Y, False, *extra)
         dx, dY = acc(dx, bx if want_x else None), acc(dY, bY if want_Y else None)
     shape = lambda t, ref: None if t is None else t.reshape(ref.shape)  # noqa: E731
-    return (shape(dg, g), shape(dx, x), shape(dY, Y), shape(dw, w)) + (None,) * 11
+    return (shape(dg, g), shape(dx, x), shape(dY, Y), shape(dw, w)) + (None,) * 12
 
 
 K.tp_scatter_backward.register_autograd(_tp2_bwd, setup_context=_tp2_setup)

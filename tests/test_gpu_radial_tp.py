@@ -112,11 +112,12 @@ def test_mace_eval_mode_uses_fused_path_and_matches_oracle():
 
     from molnex_amd.config import config
 
-    prev, config.fused_weight_grad = config.fused_weight_grad, True
+    prev = config.fused_weight_grad, config.paired_radial
+    config.fused_weight_grad, config.paired_radial = True, False  # the per-pair path takes precedence
     try:
         _mace_eval_fused(CFG1, CFG1_LITERAL, build, molecules, mace_ref, NL)
     finally:
-        config.fused_weight_grad = prev
+        config.fused_weight_grad, config.paired_radial = prev
 
 
 def _mace_eval_fused(CFG1, CFG1_LITERAL, build, molecules, mace_ref, NL):
