@@ -1262,7 +1262,7 @@ def radial_tp_pairs(x: Tensor, Y: Tensor, h: Tensor, weight: Tensor, bias: Tenso
 @radial_tp_pairs.register_fake
 def _(x, Y, h, weight, bias, row_ptr, perm, senders, wrow, pairs, config, channels):
     num_paths, nx, ny, no = tp_config_info(config)
-    return x.new_empty((row_ptr.shape[0] - 1, no * channels)), h.new_empty((h.shape[0], weight.shape[0]))
+    return x.new_empty((row_ptr.shape[0] - 1, no * channels)), h.new_empty((pairs.shape[0], weight.shape[0]))
 
 
 def _rtpp_setup(ctx, inputs, output):

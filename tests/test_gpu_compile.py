@@ -53,6 +53,33 @@ def test_opcheck_tp_scatter():
     opcheck(ops.tp_scatter.default, (x, Y, w, row_ptr, perm, snd, cfg, C))
 
 
+def test_opcheck_pairs():
+    """The undirected-pair ops: edge_reverse, tp_scatter with a weight-row map, the pair-summing
+    output-layer backward, and radial_tp_pairs in pair and edge mode."""
+    pos, box, ei, shifts, _ = _graph()
+    N, C, Kh = pos.shape[0], 8, 16
+    bond = ops.bond_vectors(pos, ei, shifts)
+    feats = bond.norm(dim=-1, keepdim=True)
+    row_ptr, perm, snd = ops.edge_csr(ei, N)
+    opcheck(ops.edge_reverse.default, (ei, N, row_ptr, perm, snd, feats), test_utils=("test_schema", "test_faketensor"))
+    pr = K.EdgePairs.build(ei, N, row_ptr, perm, snd, feats)
+    assert pr is not None
+    E = ei.shape[0]
+    cfg = K.tp_config_id([0, 1], [0, 1], [0, 1])
+    P, nx, ny, no = K.tp_config_info(cfg)
+    x = torch.randn(N, nx * C, device=DEV, requires_grad=True)
+    Y = torch.randn(E, ny, device=DEV, requires_grad=True)
+    w = torch.randn(E // 2, P * C, device=DEV, requires_grad=True)
+    opcheck(ops.tp_scatter.default, (x, Y, w, row_ptr, perm, snd, cfg, C, None, None, None, pr.wrow))
+    W = torch.randn(P * C, Kh, device=DEV) * 0.3
+    gw = torch.randn(E, P * C, device=DEV)
+    opcheck(ops.edge_weights_backward_pairs.default, (gw, pr.pairs, W), test_utils=("test_schema", "test_faketensor"))
+    b = torch.randn(P * C, device=DEV)
+    for rows in (E // 2, E):  # pair mode, edge mode
+        h = torch.randn(rows, Kh, device=DEV, requires_grad=True)
+        opcheck(ops.radial_tp_pairs.default, (x, Y, h, W, b, row_ptr, perm, snd, pr.wrow, pr.pairs, cfg, C))
+
+
 def test_opcheck_class_groups():
     z = torch.randint(-1, 7, (3000,), device=DEV)
     opcheck(ops.class_groups.default, (z, 6), test_utils=("test_schema", "test_faketensor"))
