@@ -137,6 +137,20 @@ int mnx_edge_reverse(const int64_t* edge_index, int64_t num_edges, int64_t num_n
                      const int32_t* perm, const int32_t* senders_sorted, const float* feats, int32_t num_feats,
                      int32_t* rev, int32_t* d_bad, mnx_stream_t stream);
 
+/* The pairs themselves (num_edges even): after mnx_edge_reverse, the lead of
+ * each pair is its lower edge id; pair P (in ascending lead order) has
+ * lead[P] (int64 [E/2]) and pairs[P] = (lead, partner) (int32 [E/2][2]), and
+ * wrow[e] (int32 [E]) is the pair of edge e.  d_bad[0] (device int32 [2],
+ * both words cleared by the caller) counts edges without a partner or whose
+ * partner does not point back; when it is non-zero the outputs are not a
+ * pairing (every write stays inside them).  Workspace:
+ * mnx_edge_pairs_workspace_bytes. */
+size_t mnx_edge_pairs_workspace_bytes(int64_t num_edges);
+int mnx_edge_pairs(const int64_t* edge_index, int64_t num_edges, int64_t num_nodes, const int32_t* row_ptr,
+                   const int32_t* perm, const int32_t* senders_sorted, const float* feats, int32_t num_feats,
+                   int32_t* wrow, int64_t* lead, int32_t* pairs, int32_t* d_bad, void* workspace,
+                   size_t workspace_bytes, mnx_stream_t stream);
+
 /* ------------------------------------------------------------------------ */
 /* Segment sums over a CSR (row_ptr / perm from mnx_csr_build of the rows'    */
 /* segment ids): replaces the scatter_add_ of molix.F.scatter_sum / batch_add */

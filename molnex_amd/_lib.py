@@ -52,6 +52,8 @@ SIGNATURES = {
     "mnx_tp_bwd_sender_rows_f32": (C.c_int, [c_i32, c_i32, vp, vp, vp, vp, vp, vp, vp, vp, c_i64, c_i64, vp, vp,
                                              vp, vp]),
     "mnx_edge_reverse": (C.c_int, [vp, c_i64, c_i64, vp, vp, vp, vp, c_i32, vp, vp, vp]),
+    "mnx_edge_pairs_workspace_bytes": (c_sz, [c_i64]),
+    "mnx_edge_pairs": (C.c_int, [vp, c_i64, c_i64, vp, vp, vp, vp, c_i32, vp, vp, vp, vp, vp, c_sz, vp]),
     "mnx_pme_spread_workspace_bytes": (c_sz, [c_i64, c_i32, c_i32, c_i32]),
     "mnx_pme_spread_f32": (C.c_int, [vp, vp, vp, c_i64, c_i32, c_i32, c_i32, c_i32, c_f64, vp, vp, c_sz, vp]),
     "mnx_pme_spread_f64": (C.c_int, [vp, vp, vp, c_i64, c_i32, c_i32, c_i32, c_i32, c_f64, vp, vp, c_sz, vp]),

@@ -17,6 +17,7 @@
 // of sender receiver(e), else it scans the whole segment.
 
 #include "common.h"
+#include "scan.h"
 
 namespace mnx {
 namespace {
@@ -72,6 +73,41 @@ __global__ void k_edge_reverse(const int64_t* __restrict__ ei, int64_t E, int64_
     if (m && int(threadIdx.x & 63) == __ffsll((unsigned long long)m) - 1) atomicAdd(bad, int(__popcll(m)));
 }
 
+// Numbering of the pairs once rev is known: flag[e] = 1 for the lead (lower id) of each pair, and
+// bad[0] counts edges whose partner does not point back.
+__global__ void k_pair_flags(const int32_t* __restrict__ rev, int64_t E, int32_t* __restrict__ flag,
+                             int32_t* __restrict__ bad) {
+    const int64_t e = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (e >= E) return;
+    const int r = rev[e];
+    const bool ok = r >= 0 && r < E && rev[r] == int32_t(e);
+    flag[e] = ok && r > e ? 1 : 0;
+    const uint64_t m = __ballot(!ok);
+    if (m && int(threadIdx.x & 63) == __ffsll((unsigned long long)m) - 1) atomicAdd(bad, int(__popcll(m)));
+}
+
+// rank[e] = number of leads before e.  Pair rank[e] of lead e: lead[P] = e, pairs[P] = (e, rev[e]);
+// every edge's weight row is its lead's rank.  Writes stay inside the E/2 pair slots whatever rev
+// holds (bad[0] > 0 then tells the caller to discard them).
+__global__ void k_pair_place(const int32_t* __restrict__ rev, const int32_t* __restrict__ flag,
+                             const int32_t* __restrict__ rank, int64_t E, int32_t* __restrict__ wrow,
+                             int64_t* __restrict__ lead, int32_t* __restrict__ pairs) {
+    const int64_t e = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (e >= E) return;
+    const int64_t half = E / 2;
+    const int r = rev[e];
+    if (flag[e]) {
+        const int64_t P = rank[e];
+        if (P < half) {
+            lead[P] = e;
+            pairs[2 * P] = int32_t(e);
+            pairs[2 * P + 1] = r;
+        }
+    }
+    const int64_t m = (r >= 0 && r < e) ? r : e;
+    wrow[e] = rank[m] < half ? rank[m] : 0;
+}
+
 }  // namespace
 }  // namespace mnx
 
@@ -97,6 +133,42 @@ int mnx_edge_reverse(const int64_t* edge_index, int64_t num_edges, int64_t num_n
     hipLaunchKernelGGL(k_edge_reverse, grid, dim3(256), 0, (hipStream_t)stream, edge_index, num_edges, num_nodes,
                        row_ptr, perm, senders_sorted, reinterpret_cast<const uint32_t*>(feats), num_feats,
                        d_bad + 1, rev, d_bad);
+    MNX_CHECK_LAUNCH();
+    return MNX_OK;
+}
+
+size_t mnx_edge_pairs_workspace_bytes(int64_t num_edges) {
+    if (num_edges < 0) return 0;
+    const size_t e = size_t(num_edges > 0 ? num_edges : 1);
+    return 3 * (e * sizeof(int32_t) + 256) + scan_workspace_elems(num_edges) * sizeof(int32_t) + 2 * 256;
+}
+
+int mnx_edge_pairs(const int64_t* edge_index, int64_t num_edges, int64_t num_nodes, const int32_t* row_ptr,
+                   const int32_t* perm, const int32_t* senders_sorted, const float* feats, int32_t num_feats,
+                   int32_t* wrow, int64_t* lead, int32_t* pairs, int32_t* d_bad, void* workspace,
+                   size_t workspace_bytes, mnx_stream_t stream) {
+    clear_error();
+    MNX_REQUIRE(num_edges >= 0 && num_edges % 2 == 0, "edge count %lld must be even", (long long)num_edges);
+    if (num_edges == 0) return MNX_OK;
+    MNX_REQUIRE(wrow && lead && pairs && d_bad && workspace, "null pointer argument");
+    const size_t need = mnx_edge_pairs_workspace_bytes(num_edges);
+    if (workspace_bytes < need)
+        return set_error(MNX_ERR_WORKSPACE, "workspace %zu < %zu bytes", workspace_bytes, need);
+    Workspace ws{static_cast<char*>(workspace), workspace_bytes};
+    int32_t* rev = ws.take<int32_t>(size_t(num_edges));
+    int32_t* flag = ws.take<int32_t>(size_t(num_edges));
+    int32_t* rank = ws.take<int32_t>(size_t(num_edges));
+    int32_t* tiles = ws.take<int32_t>(scan_workspace_elems(num_edges));
+    int rc = mnx_edge_reverse(edge_index, num_edges, num_nodes, row_ptr, perm, senders_sorted, feats, num_feats, rev,
+                              d_bad, stream);
+    if (rc) return rc;
+    hipStream_t s = (hipStream_t)stream;
+    const dim3 grid(unsigned(ceil_div(num_edges, 256)));
+    hipLaunchKernelGGL(k_pair_flags, grid, dim3(256), 0, s, rev, num_edges, flag, d_bad);
+    MNX_CHECK_LAUNCH();
+    rc = exclusive_scan<int32_t, int32_t>(flag, num_edges, rank, tiles, nullptr, s);
+    if (rc) return rc;
+    hipLaunchKernelGGL(k_pair_place, grid, dim3(256), 0, s, rev, flag, rank, num_edges, wrow, lead, pairs);
     MNX_CHECK_LAUNCH();
     return MNX_OK;
 }

@@ -1196,20 +1196,22 @@ class EdgePairs:
         E = edge_index.shape[0]
         if E == 0 or E % 2:
             return None
-        rev, bad = edge_reverse(edge_index, num_nodes, row_ptr, perm, senders, feats)
-        ids = torch.arange(E, device=rev.device, dtype=torch.int32)
-        back = rev[rev.clamp(min=0).long()]
-        broken = bad.sum() + ((rev >= 0) & (back != ids)).sum()
-        if int(broken.item()) != 0:
+        _require_gpu("EdgePairs", edge_index, feats)
+        lib = _lib.load()
+        dev = edge_index.device
+        ei = edge_index.to(torch.int64).contiguous()
+        f = feats.detach().to(torch.float32).reshape(E, -1).contiguous()
+        wrow = torch.empty(E, dtype=torch.int32, device=dev)
+        lead = torch.empty(E // 2, dtype=torch.int64, device=dev)
+        pairs = torch.empty((E // 2, 2), dtype=torch.int32, device=dev)
+        bad = torch.zeros(2, dtype=torch.int32, device=dev)
+        ws = _ws(lib.mnx_edge_pairs_workspace_bytes(E), dev)
+        check(lib.mnx_edge_pairs(ptr(ei), E, num_nodes, ptr(row_ptr), ptr(perm), ptr(senders), ptr(f), f.shape[1],
+                                 ptr(wrow), ptr(lead), ptr(pairs), ptr(bad), ptr(ws), ws.numel(), _stream(ei)),
+              "edge pairs")
+        if int(bad[0].item()) != 0:
             return None
-        # an involution without fixed points: every pair has one lead (its lower edge id), E/2 in all
-        lead_mask = ids < rev
-        rank = torch.cumsum(lead_mask.to(torch.int32), 0, dtype=torch.int32) - 1
-        slot = torch.where(lead_mask, rank, E // 2).long()  # non-leads go to a spare last slot
-        lead = torch.empty(E // 2 + 1, dtype=torch.int64, device=rev.device).scatter_(0, slot, ids.long())[:E // 2]
-        wrow = rank[torch.minimum(ids, rev).long()].contiguous()
-        pairs = torch.stack([lead.to(torch.int32), rev[lead]], dim=1).contiguous()
-        return EdgePairs(pairs, wrow, lead.contiguous())
+        return EdgePairs(pairs, wrow, lead)
 
 
 @torch.library.custom_op("molix::edge_weights_backward_pairs", mutates_args=(), device_types="cuda")
