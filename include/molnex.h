@@ -145,6 +145,15 @@ int mnx_edge_reverse(const int64_t* edge_index, int64_t num_edges, int64_t num_n
  * partner does not point back; when it is non-zero the outputs are not a
  * pairing (every write stays inside them).  Workspace:
  * mnx_edge_pairs_workspace_bytes. */
+/* Rows of F floats by index (the radial features of each pair's lead edge,
+ * feeding the radial MLP of radial_mlp.py:38-93 once per pair):
+ * dst[i] = src[idx[i]] (gather) and dst[idx[i]] = src[i] (its adjoint for
+ * distinct indices; rows not indexed are left as they are); idx int64 [n]. */
+int mnx_gather_rows_f32(const float* src, const int64_t* idx, int64_t n, int32_t F, float* dst,
+                        mnx_stream_t stream);
+int mnx_scatter_rows_f32(const float* src, const int64_t* idx, int64_t n, int32_t F, float* dst,
+                         mnx_stream_t stream);
+
 size_t mnx_edge_pairs_workspace_bytes(int64_t num_edges);
 int mnx_edge_pairs(const int64_t* edge_index, int64_t num_edges, int64_t num_nodes, const int32_t* row_ptr,
                    const int32_t* perm, const int32_t* senders_sorted, const float* feats, int32_t num_feats,

@@ -108,6 +108,24 @@ __global__ void k_pair_place(const int32_t* __restrict__ rev, const int32_t* __r
     wrow[e] = rank[m] < half ? rank[m] : 0;
 }
 
+// dst[i][:] = src[idx[i]][:] (F floats per row), and its adjoint dst[idx[i]][:] = src[i][:]: one
+// thread per element (the rows of radial features are 32 bytes, too short for row-wise loops).
+__global__ void k_gather_rows(const float* __restrict__ src, const int64_t* __restrict__ idx, int64_t n, int F,
+                              float* __restrict__ dst) {
+    const int64_t t = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (t >= n * F) return;
+    const int64_t i = t / F;
+    dst[t] = src[idx[i] * F + (t - i * F)];
+}
+
+__global__ void k_scatter_rows(const float* __restrict__ src, const int64_t* __restrict__ idx, int64_t n, int F,
+                               float* __restrict__ dst) {
+    const int64_t t = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (t >= n * F) return;
+    const int64_t i = t / F;
+    dst[idx[i] * F + (t - i * F)] = src[t];
+}
+
 }  // namespace
 }  // namespace mnx
 
@@ -133,6 +151,30 @@ int mnx_edge_reverse(const int64_t* edge_index, int64_t num_edges, int64_t num_n
     hipLaunchKernelGGL(k_edge_reverse, grid, dim3(256), 0, (hipStream_t)stream, edge_index, num_edges, num_nodes,
                        row_ptr, perm, senders_sorted, reinterpret_cast<const uint32_t*>(feats), num_feats,
                        d_bad + 1, rev, d_bad);
+    MNX_CHECK_LAUNCH();
+    return MNX_OK;
+}
+
+int mnx_gather_rows_f32(const float* src, const int64_t* idx, int64_t n, int32_t F, float* dst,
+                        mnx_stream_t stream) {
+    clear_error();
+    MNX_REQUIRE(n >= 0 && F >= 1 && F <= 4096, "sizes out of range");
+    if (n == 0) return MNX_OK;
+    MNX_REQUIRE(src && idx && dst, "null pointer argument");
+    hipLaunchKernelGGL(k_gather_rows, dim3(unsigned(ceil_div(n * F, 256))), dim3(256), 0, (hipStream_t)stream, src, idx,
+                       n, F, dst);
+    MNX_CHECK_LAUNCH();
+    return MNX_OK;
+}
+
+int mnx_scatter_rows_f32(const float* src, const int64_t* idx, int64_t n, int32_t F, float* dst,
+                         mnx_stream_t stream) {
+    clear_error();
+    MNX_REQUIRE(n >= 0 && F >= 1 && F <= 4096, "sizes out of range");
+    if (n == 0) return MNX_OK;
+    MNX_REQUIRE(src && idx && dst, "null pointer argument");
+    hipLaunchKernelGGL(k_scatter_rows, dim3(unsigned(ceil_div(n * F, 256))), dim3(256), 0, (hipStream_t)stream, src,
+                       idx, n, F, dst);
     MNX_CHECK_LAUNCH();
     return MNX_OK;
 }

@@ -1214,6 +1214,69 @@ class EdgePairs:
         return EdgePairs(pairs, wrow, lead)
 
 
+@torch.library.custom_op("molix::gather_rows", mutates_args=(), device_types="cuda")
+def gather_rows(src: Tensor, idx: Tensor) -> Tensor:
+    """``src[idx]`` for a float32 (R, F) ``src`` and distinct int64 indices (the radial features of the
+    lead edge of each undirected pair); its backward scatters the gradient rows back."""
+    _require_gpu("gather_rows", src, idx)
+    if src.dtype != torch.float32 or src.dim() != 2 or idx.dtype != torch.int64 or idx.dim() != 1:
+        raise ValueError("gather_rows: src must be float32 (R, F), idx int64 (n,)")
+    s = src.contiguous()
+    i = idx.contiguous()
+    out = s.new_empty(i.shape[0], s.shape[1])
+    check(_lib.load().mnx_gather_rows_f32(ptr(s), ptr(i), i.shape[0], s.shape[1], ptr(out), _stream(s)),
+          "gather_rows")
+    return out
+
+
+@gather_rows.register_fake
+def _(src, idx):
+    return src.new_empty(idx.shape[0], src.shape[1])
+
+
+@torch.library.custom_op("molix::scatter_rows", mutates_args=(), device_types="cuda")
+def scatter_rows(grad: Tensor, idx: Tensor, num_rows: int) -> Tensor:
+    """The adjoint of ``gather_rows``: a (num_rows, F) tensor with ``grad[i]`` at row ``idx[i]``, zero
+    elsewhere (indices distinct)."""
+    g = grad.to(torch.float32).contiguous()
+    i = idx.contiguous()
+    out = torch.zeros(num_rows, g.shape[1], dtype=torch.float32, device=g.device)
+    check(_lib.load().mnx_scatter_rows_f32(ptr(g), ptr(i), i.shape[0], g.shape[1], ptr(out), _stream(g)),
+          "scatter_rows")
+    return out
+
+
+@scatter_rows.register_fake
+def _(grad, idx, num_rows):
+    return grad.new_empty(num_rows, grad.shape[1])
+
+
+def _gr_setup(ctx, inputs, output):
+    src, idx = inputs
+    ctx.save_for_backward(idx)
+    ctx.rows = src.shape[0]
+
+
+def _gr_backward(ctx, grad):
+    (idx,) = ctx.saved_tensors
+    return scatter_rows(grad, idx, ctx.rows), None
+
+
+gather_rows.register_autograd(_gr_backward, setup_context=_gr_setup)
+
+
+def _sr_setup(ctx, inputs, output):
+    ctx.save_for_backward(inputs[1])
+
+
+def _sr_backward(ctx, grad):
+    (idx,) = ctx.saved_tensors
+    return gather_rows(grad.contiguous(), idx), None, None
+
+
+scatter_rows.register_autograd(_sr_backward, setup_context=_sr_setup)
+
+
 @torch.library.custom_op("molix::edge_weights_backward_pairs", mutates_args=(), device_types="cuda")
 def edge_weights_backward_pairs(grad: Tensor, pairs: Tensor, weight: Tensor) -> Tensor:
     """``(grad[pairs[:, 0]] + grad[pairs[:, 1]]) @ weight``: dL/dh of an output layer applied once per

@@ -172,7 +172,7 @@ class ConvTP(nn.Module):
             g = edge_graph(edge_index, x.shape[0])
             pairs = g.pairs(edge_feats)
             if pairs is not None:
-                h = radial_mlp.hidden(edge_feats.index_select(0, pairs.lead))
+                h = radial_mlp.hidden(torch.ops.molix.gather_rows(edge_feats, pairs.lead))
                 out, _ = torch.ops.molix.radial_tp_pairs(x, edge_angular, h, last.weight, last.bias, g.row_ptr,
                                                          g.perm, g.senders, pairs.wrow, pairs.pairs,
                                                          self.cue_tp.config_id, self.cue_tp.channels)

@@ -75,6 +75,9 @@ def test_opcheck_pairs():
     gw = torch.randn(E, P * C, device=DEV)
     opcheck(ops.edge_weights_backward_pairs.default, (gw, pr.pairs, W), test_utils=("test_schema", "test_faketensor"))
     b = torch.randn(P * C, device=DEV)
+    f2 = torch.randn(E, 8, device=DEV, requires_grad=True)
+    opcheck(ops.gather_rows.default, (f2, pr.lead))
+    opcheck(ops.scatter_rows.default, (torch.randn(E // 2, 8, device=DEV, requires_grad=True), pr.lead, E))
     for rows in (E // 2, E):  # pair mode, edge mode
         h = torch.randn(rows, Kh, device=DEV, requires_grad=True)
         opcheck(ops.radial_tp_pairs.default, (x, Y, h, W, b, row_ptr, perm, snd, pr.wrow, pr.pairs, cfg, C))
