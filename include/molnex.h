@@ -145,6 +145,12 @@ int mnx_edge_reverse(const int64_t* edge_index, int64_t num_edges, int64_t num_n
  * partner does not point back; when it is non-zero the outputs are not a
  * pairing (every write stays inside them).  Workspace:
  * mnx_edge_pairs_workspace_bytes. */
+/* d_bad[0] (device int32, cleared by the caller) += the number of pairs
+ * (int32 [num_pairs][2], mnx_edge_pairs) whose two edges' feats rows differ in
+ * any bit: a pairing built once per edge list, checked again for new features. */
+int mnx_edge_pairs_verify(const int32_t* pairs, int64_t num_pairs, const float* feats, int32_t num_feats,
+                          int32_t* d_bad, mnx_stream_t stream);
+
 /* Rows of F floats by index (the radial features of each pair's lead edge,
  * feeding the radial MLP of radial_mlp.py:38-93 once per pair):
  * dst[i] = src[idx[i]] (gather) and dst[idx[i]] = src[i] (its adjoint for

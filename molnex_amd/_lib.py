@@ -54,6 +54,7 @@ SIGNATURES = {
     "mnx_edge_reverse": (C.c_int, [vp, c_i64, c_i64, vp, vp, vp, vp, c_i32, vp, vp, vp]),
     "mnx_edge_pairs_workspace_bytes": (c_sz, [c_i64]),
     "mnx_gather_rows_f32": (C.c_int, [vp, vp, c_i64, c_i32, vp, vp]),
+    "mnx_edge_pairs_verify": (C.c_int, [vp, c_i64, vp, c_i32, vp, vp]),
     "mnx_scatter_rows_f32": (C.c_int, [vp, vp, c_i64, c_i32, vp, vp]),
     "mnx_edge_pairs": (C.c_int, [vp, c_i64, c_i64, vp, vp, vp, vp, c_i32, vp, vp, vp, vp, vp, c_sz, vp]),
     "mnx_pme_spread_workspace_bytes": (c_sz, [c_i64, c_i32, c_i32, c_i32]),

@@ -108,6 +108,19 @@ __global__ void k_pair_place(const int32_t* __restrict__ rev, const int32_t* __r
     wrow[e] = rank[m] < half ? rank[m] : 0;
 }
 
+// bad[0] += number of pairs whose two edges' feature rows differ in any bit.
+__global__ void k_pairs_verify(const int32_t* __restrict__ pairs, int64_t P, const uint32_t* __restrict__ feats,
+                               int F, int32_t* __restrict__ bad) {
+    const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i >= P) return;
+    const uint32_t* a = feats + int64_t(pairs[2 * i]) * F;
+    const uint32_t* b = feats + int64_t(pairs[2 * i + 1]) * F;
+    bool same = true;
+    for (int k = 0; k < F; ++k) same = same && a[k] == b[k];
+    const uint64_t m = __ballot(!same);
+    if (m && int(threadIdx.x & 63) == __ffsll((unsigned long long)m) - 1) atomicAdd(bad, int(__popcll(m)));
+}
+
 // dst[i][:] = src[idx[i]][:] (F floats per row), and its adjoint dst[idx[i]][:] = src[i][:]: one
 // thread per element (the rows of radial features are 32 bytes, too short for row-wise loops).
 __global__ void k_gather_rows(const float* __restrict__ src, const int64_t* __restrict__ idx, int64_t n, int F,
@@ -175,6 +188,18 @@ int mnx_scatter_rows_f32(const float* src, const int64_t* idx, int64_t n, int32_
     MNX_REQUIRE(src && idx && dst, "null pointer argument");
     hipLaunchKernelGGL(k_scatter_rows, dim3(unsigned(ceil_div(n * F, 256))), dim3(256), 0, (hipStream_t)stream, src,
                        idx, n, F, dst);
+    MNX_CHECK_LAUNCH();
+    return MNX_OK;
+}
+
+int mnx_edge_pairs_verify(const int32_t* pairs, int64_t num_pairs, const float* feats, int32_t num_feats,
+                          int32_t* d_bad, mnx_stream_t stream) {
+    clear_error();
+    MNX_REQUIRE(num_pairs >= 0 && num_feats >= 0 && num_feats <= 1024, "sizes out of range");
+    if (num_pairs == 0) return MNX_OK;
+    MNX_REQUIRE(pairs && d_bad && (feats || num_feats == 0), "null pointer argument");
+    hipLaunchKernelGGL(k_pairs_verify, dim3(unsigned(ceil_div(num_pairs, 256))), dim3(256), 0, (hipStream_t)stream,
+                       pairs, num_pairs, reinterpret_cast<const uint32_t*>(feats), num_feats, d_bad);
     MNX_CHECK_LAUNCH();
     return MNX_OK;
 }

@@ -1213,6 +1213,16 @@ class EdgePairs:
             return None
         return EdgePairs(pairs, wrow, lead)
 
+    def holds_for(self, feats: Tensor) -> bool:
+        """Whether the two edges of every pair still have bit-identical rows of ``feats`` (one host
+        synchronisation; the pairing itself depends only on the edge list)."""
+        lib = _lib.load()
+        f = feats.detach().to(torch.float32).reshape(self.wrow.shape[0], -1).contiguous()
+        bad = torch.zeros(1, dtype=torch.int32, device=f.device)
+        check(lib.mnx_edge_pairs_verify(ptr(self.pairs), self.pairs.shape[0], ptr(f), f.shape[1], ptr(bad),
+                                        _stream(f)), "edge pairs verify")
+        return int(bad.item()) == 0
+
 
 @torch.library.custom_op("molix::gather_rows", mutates_args=(), device_types="cuda")
 def gather_rows(src: Tensor, idx: Tensor) -> Tensor:

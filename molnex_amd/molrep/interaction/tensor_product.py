@@ -53,12 +53,18 @@ class EdgeGraph:
 
     def pairs(self, feats: torch.Tensor):
         """The undirected pairs of this graph whose two edges have bit-identical rows of ``feats``
-        (``kernels.EdgePairs``; None when some edge has no such partner), built once per features
-        tensor (one host synchronisation)."""
+        (``kernels.EdgePairs``; None when some edge has no such partner).  Built on the first
+        features tensor; for later ones (new positions on the same edge list) the pairing is kept
+        if the features of every pair still agree, else rebuilt.  One host synchronisation per new
+        features tensor."""
         p = self._pairs
         if p is None or p[0] is not feats or p[1] != feats._version:
-            built = K.EdgePairs.build(self.edge_index, self.num_nodes, self.row_ptr, self.perm, self.senders,
-                                      feats.detach())
+            prev = p[2] if p is not None else None
+            if prev is not None and feats.shape[0] == prev.wrow.shape[0] and prev.holds_for(feats):
+                built = prev
+            else:
+                built = K.EdgePairs.build(self.edge_index, self.num_nodes, self.row_ptr, self.perm, self.senders,
+                                          feats.detach())
             self._pairs = p = (feats, feats._version, built)
         return p[2]
 

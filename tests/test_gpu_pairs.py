@@ -100,6 +100,29 @@ def test_no_pairing_when_partners_are_ambiguous_or_missing():
     assert pr is None
 
 
+def test_pairing_reused_for_new_positions():
+    """The pairing depends only on the edge list: new positions on the same edges keep it (checked on
+    the device), features that break a pair make the graph fall back to per-edge work."""
+    from molnex_amd.molrep.interaction.tensor_product import EdgeGraph
+
+    n, L = 300, (300 / 0.1) ** (1 / 3)
+    p, ei, bond = _system(n, L, seed=8)
+    box = torch.eye(3, device=DEV) * L
+    i, j, sh, _, _ = torch.ops.molix.neighbor_list(p, RC, box, True)
+    g = EdgeGraph(ei, n)
+    f1 = bond.norm(dim=-1, keepdim=True)
+    pr1 = g.pairs(f1)
+    assert pr1 is not None
+    p2 = p + 0.01 * torch.randn_like(p)  # same edge list, new positions
+    f2 = torch.ops.molix.bond_vectors(p2, ei, sh).norm(dim=-1, keepdim=True)
+    assert pr1.holds_for(f2)
+    assert g.pairs(f2) is pr1
+    f3 = f2.clone()
+    f3[5] += 1e-3
+    assert not pr1.holds_for(f3)
+    assert g.pairs(f3) is None
+
+
 def _irr(ls, C=None):
     return "+".join((f"{C}x" if C else "") + f"{l}{'e' if l % 2 == 0 else 'o'}" for l in ls)
 
