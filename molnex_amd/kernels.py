@@ -587,11 +587,18 @@ def pme_reciprocal_backward(positions: Tensor, charges: Tensor, box_vectors: Ten
     lib = _lib.load()
     _, spec, pos, q, b = _pme_recip_energy(positions, charges, box_vectors, gridx, gridy, gridz, order, alpha,
                                            coulomb, xmoduli, ymoduli, zmoduli)
-    real = torch.fft.irfftn(spec, s=(gridx, gridy, gridz), norm="forward").contiguous()
+    return _pme_recip_gather(spec, pos, q, b, gridx, gridy, gridz, order, coulomb)
+
+
+def _pme_recip_gather(spec, pos, q, b, gx, gy, gz, order, coulomb):
+    """irfftn(norm='forward') of the convolved half spectrum, then the B-spline gather of
+    (dE/dpos, dE/dq)."""
+    lib = _lib.load()
+    real = torch.fft.irfftn(spec, s=(gx, gy, gz), norm="forward").contiguous()
     dpos = torch.empty_like(pos)
     dq = torch.empty_like(q)
-    check(getattr(lib, f"mnx_pme_gather_{_fsuffix(pos)}")(ptr(pos), ptr(q), ptr(b), pos.shape[0], ptr(real), gridx,
-                                                          gridy, gridz, order, float(coulomb), ptr(dpos), ptr(dq),
+    check(getattr(lib, f"mnx_pme_gather_{_fsuffix(pos)}")(ptr(pos), ptr(q), ptr(b), pos.shape[0], ptr(real), gx, gy,
+                                                          gz, order, float(coulomb), ptr(dpos), ptr(dq),
                                                           _stream(pos)), "pme gather")
     return dpos, dq
 
@@ -615,6 +622,63 @@ def _pme_recip_bwd(ctx, grad):
 
 
 pme_reciprocal.register_autograd(_pme_recip_bwd, setup_context=_pme_recip_setup)
+
+
+@torch.library.custom_op("molix::pme_reciprocal_spectrum", mutates_args=(), device_types="cuda")
+def pme_reciprocal_spectrum(positions: Tensor, charges: Tensor, box_vectors: Tensor, gridx: int, gridy: int,
+                            gridz: int, order: int, alpha: float, coulomb: float, xmoduli: Tensor, ymoduli: Tensor,
+                            zmoduli: Tensor) -> tuple[Tensor, Tensor]:
+    """``molix::pme_reciprocal`` that also returns the convolved half spectrum (gridx, gridy,
+    gridz // 2 + 1), complex: its backward transforms that spectrum back and gathers, instead of
+    spreading and transforming the charges a second time (the reference's backward recomputes,
+    ``pme_cpu.cpp:392-430``).  The spectrum output carries no gradient."""
+    _require_gpu("pme_reciprocal_spectrum", positions, charges, box_vectors)
+    e, spec, *_ = _pme_recip_energy(positions, charges, box_vectors, int(gridx), int(gridy), int(gridz), int(order),
+                                    alpha, coulomb, xmoduli, ymoduli, zmoduli)
+    return e, spec
+
+
+@pme_reciprocal_spectrum.register_fake
+def _(positions, charges, box_vectors, gridx, gridy, gridz, order, alpha, coulomb, xmoduli, ymoduli, zmoduli):
+    cdt = torch.complex128 if positions.dtype == torch.float64 else torch.complex64
+    return positions.new_empty(()), positions.new_empty((gridx, gridy, gridz // 2 + 1), dtype=cdt)
+
+
+@torch.library.custom_op("molix::pme_reciprocal_gather", mutates_args=(), device_types="cuda")
+def pme_reciprocal_gather(positions: Tensor, charges: Tensor, box_vectors: Tensor, spectrum: Tensor, gridx: int,
+                          gridy: int, gridz: int, order: int, coulomb: float) -> tuple[Tensor, Tensor]:
+    """(dE/dpos, dE/dq) of ``molix::pme_reciprocal_spectrum`` from its spectrum output."""
+    _require_gpu("pme_reciprocal_gather", positions, charges, box_vectors, spectrum)
+    dt = positions.dtype
+    if spectrum.shape != (gridx, gridy, gridz // 2 + 1) or not spectrum.is_complex():
+        raise ValueError("pme_reciprocal_gather: spectrum must be complex (gridx, gridy, gridz // 2 + 1)")
+    pos = positions.detach().contiguous()
+    q = charges.detach().to(dt).contiguous()
+    b = box_vectors.detach().to(device=pos.device, dtype=dt).contiguous()
+    return _pme_recip_gather(spectrum, pos, q, b, int(gridx), int(gridy), int(gridz), int(order), coulomb)
+
+
+@pme_reciprocal_gather.register_fake
+def _(positions, charges, box_vectors, spectrum, gridx, gridy, gridz, order, coulomb):
+    return torch.empty_like(positions), torch.empty_like(charges)
+
+
+def _pme_spec_setup(ctx, inputs, output):
+    ctx.set_materialize_grads(False)
+    ctx.mark_non_differentiable(output[1])
+    ctx.save_for_backward(inputs[0], inputs[1], inputs[2], output[1])
+    ctx.args = (int(inputs[3]), int(inputs[4]), int(inputs[5]), int(inputs[6]), float(inputs[8]))
+
+
+def _pme_spec_bwd(ctx, grad, _grad_spec):
+    if grad is None:
+        return (None,) * 12
+    pos, q, box, spec = ctx.saved_tensors
+    dpos, dq = pme_reciprocal_gather(pos, q, box, spec, *ctx.args)
+    return (dpos * grad, (dq * grad).to(q.dtype)) + (None,) * 10
+
+
+pme_reciprocal_spectrum.register_autograd(_pme_spec_bwd, setup_context=_pme_spec_setup)
 
 
 def _pme_direct_run(positions, charges, neighbors, deltas, distances, exclusions, alpha, coulomb, grads=True):

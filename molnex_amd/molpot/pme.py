@@ -67,7 +67,9 @@ class PMEPotential(nn.Module):
             exclusions = torch.full((positions.shape[0], 1), -1, dtype=torch.int32, device=positions.device)
         e_dir = ops.pme_direct(positions, charges, nb, d, r, exclusions, self.alpha, self.coulomb)
         mods = [m.to(dt) for m in (self.xmoduli, self.ymoduli, self.zmoduli)]
-        e_rec = ops.pme_reciprocal(positions, charges, box.to(dt), *self.grid, self.order, self.alpha, self.coulomb,
-                                   *mods)
+        # the spectrum variant of molix::pme_reciprocal keeps the convolved spectrum for the
+        # backward, which then skips the second spread and forward transform
+        e_rec, _ = ops.pme_reciprocal_spectrum(positions, charges, box.to(dt), *self.grid, self.order, self.alpha,
+                                               self.coulomb, *mods)
         e_self = self.coulomb * self.alpha / math.sqrt(math.pi) * (charges * charges).sum()
         return e_dir + e_rec - e_self

@@ -71,7 +71,9 @@ def radial_edge_features(rbf: "BesselRBF", cutoff_fn: nn.Module, r: torch.Tensor
 
     kind = 1 if isinstance(cutoff_fn, CosineCutoff) else 2 if isinstance(cutoff_fn, PolynomialCutoff) else -1
     if (kind > 0 and isinstance(rbf, BesselRBF) and r.is_cuda and r.dtype == torch.float32
-            and rbf.config.num_radial <= 32 and float(cutoff_fn.r_cut) == rbf.r_cut):
+            and rbf.config.num_radial <= 32 and float(cutoff_fn.config.r_cut) == rbf.r_cut):
+        # the radius is compared on the spec, not on the module's device buffer: reading a GPU
+        # scalar back would synchronise the host once per forward
         exponent = cutoff_fn.exponent if kind == 2 else 0
         mu, sigma = (rbf.mu, rbf.sigma) if rbf.normalize else (None, None)
         return torch.ops.molix.bessel_cutoff(r, int(rbf.config.num_radial), rbf.r_cut, rbf.eps, mu, sigma, kind,

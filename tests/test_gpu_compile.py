@@ -126,6 +126,10 @@ def test_opcheck_pme():
                                      dist[keep].contiguous(), excl, 0.3, 14.399645))
     mods = [torch.tensor(P.bspline_moduli(16, 5), device=DEV) for _ in range(3)]
     opcheck(ops.pme_reciprocal.default, (pos64, q, box.double(), 16, 16, 16, 5, 0.3, 14.399645, *mods))
+    # the spectrum variant: the AOT check is left out, as its harness sums the real energy and
+    # the complex spectrum outputs into one accumulator
+    opcheck(ops.pme_reciprocal_spectrum.default, (pos64, q, box.double(), 16, 16, 16, 5, 0.3, 14.399645, *mods),
+            test_utils=("test_schema", "test_autograd_registration", "test_faketensor"))
 
 
 def test_opcheck_get_neighbor_pairs():

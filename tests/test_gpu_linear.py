@@ -79,3 +79,38 @@ def test_hip_block_linear_zero_rows_and_views():
     base = torch.randn(50, 65, device=DEV)
     xv = base[:, 1:]  # misaligned, strided view
     assert torch.allclose(lin(xv), lin(xv.contiguous()), rtol=1e-6, atol=1e-6)
+
+
+def test_hip_block_linear_dynamic_range():
+    """Rows of the input spanning 40 decades and weight columns spanning 24: every output element
+    (forward and input gradient) stays within the error bound of an fp32 GEMM, K u sum |a| |w|
+    (K <= 64 here, u = 2^-24), since each bf16 part of the three-way split carries the full fp32
+    exponent range (a scaled fp16 split would lose the small entries of a column that spans
+    many decades)."""
+    from molnex_amd.molrep.interaction import Linear
+    from molnex_amd.molrep.interaction import linear as L
+
+    torch.manual_seed(3)
+    lin = Linear("64x0e+32x1o", "32x0e+64x1o").to(DEV)
+    with torch.no_grad():
+        for off_o, mul_o, d, srcs, _ in lin.plan:
+            for o, m, wo in srcs:
+                blk = lin.weight.view(-1)[wo:wo + m * mul_o].view(m, mul_o)
+                blk *= torch.logspace(-12, 12, mul_o, device=DEV)
+    rows = 3000
+    x = torch.randn(rows, lin.irreps_in.dim, device=DEV)
+    x *= torch.logspace(-20, 20, rows, device=DEV)[torch.randperm(rows, device=DEV)].unsqueeze(1)
+    x.requires_grad_(True)
+    g = torch.randn(rows, lin.irreps_out.dim, device=DEV) * torch.logspace(-15, 15, rows, device=DEV).unsqueeze(1)
+    out = lin(x)
+    (gx,) = torch.autograd.grad(out, x, g)
+    xd, wd = x.detach().double(), lin.weight.detach().double().reshape(-1)
+    ref = L._block_forward(xd, wd, lin.plan, lin.irreps_out.dim)
+    gref = L._block_backward(xd, wd, g.double(), lin.plan, True, False)[0]
+    # per element, against the scale of an fp32 GEMM's rounding: the sum of |a| |w| products
+    bound = L._block_forward(xd.abs(), wd.abs(), lin.plan, lin.irreps_out.dim)
+    gbound = L._block_backward(xd.abs(), wd.abs(), g.double().abs(), lin.plan, True, False)[0]
+    for got, want, b in ((out.detach().double(), ref, bound), (gx.double(), gref, gbound)):
+        assert torch.isfinite(got).all()
+        err = ((got - want).abs() / b.clamp_min(1e-300)).max().item()
+        assert err <= 64 * 2.0 ** -24, err

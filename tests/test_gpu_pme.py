@@ -168,6 +168,39 @@ def test_reciprocal_bitwise_reproducible(ops):
         assert np.array_equal(gp, runs[0][1]) and np.array_equal(gq, runs[0][2])
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
+def test_reciprocal_spectrum_variant(ops, dtype):
+    """molix::pme_reciprocal_spectrum (the module's op: the backward reuses the forward's convolved
+    spectrum) gives the energy and both gradients of molix::pme_reciprocal (which recomputes it)
+    bit for bit, in a triclinic cell with a ragged mesh; its spectrum output is the half spectrum
+    and carries no gradient."""
+    rng = np.random.default_rng(5)
+    n, grid, order = 500, (12, 20, 15), 6
+    box = np.array([[14.0, 0.0, 0.0], [2.0, 13.0, 0.0], [-1.0, 1.5, 15.0]])
+    pos = rng.uniform(-0.1, 1.1, (n, 3)) @ box
+    q = rng.normal(size=n)
+    q -= q.mean()
+    mods = [torch.tensor(P.bspline_moduli(g_, order), dtype=dtype, device=DEV) for g_ in grid]
+    b = torch.tensor(box, dtype=dtype, device=DEV)
+    res = []
+    for op in (ops.pme_reciprocal, ops.pme_reciprocal_spectrum):
+        pt = torch.tensor(pos, dtype=dtype, device=DEV, requires_grad=True)
+        qt = torch.tensor(q, dtype=dtype, device=DEV, requires_grad=True)
+        out = op(pt, qt, b, *grid, order, 0.3, 14.399645, *mods)
+        e = out if op is ops.pme_reciprocal else out[0]
+        if op is ops.pme_reciprocal_spectrum:
+            assert out[1].shape == (grid[0], grid[1], grid[2] // 2 + 1) and out[1].is_complex()
+            assert not out[1].requires_grad
+        gp, gq = torch.autograd.grad(2.5 * e, (pt, qt))
+        res.append((e.item(), gp.cpu().numpy(), gq.cpu().numpy()))
+    assert res[0][0] == res[1][0]
+    assert np.array_equal(res[0][1], res[1][1]) and np.array_equal(res[0][2], res[1][2])
+    re, rp, rq = P.reciprocal(pos, q, box, grid, order, 0.3, 14.399645,
+                              [P.bspline_moduli(g_, order) for g_ in grid])
+    tol = 1e-10 if dtype == torch.float64 else 1e-5
+    assert abs(res[1][0] - re) <= tol * abs(re) and _rel(res[1][1], 2.5 * rp) <= tol
+
+
 def test_direct_against_oracle_with_exclusions_and_padding(ops):
     """Pair list in neighbor-list row order with -1 padding and exclusions; energy (energy-only
     forward) and both derivatives (backward) against the fp64 oracle, fp32 and fp64."""
