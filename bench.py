@@ -122,7 +122,7 @@ class EdgeStep:
         self.gout = torch.randn((n_atoms, self.no * C), generator=g).to(dev)
         from molnex_amd.config import config as mcfg
 
-        self.fused = mcfg.fused_weight_grad and self.K.tp_weight_grad_supported(self.config, C, 64)
+        self.fused = mcfg.fused_weight_grad is True and self.K.tp_weight_grad_supported(self.config, C, 64)
         self.paired = mcfg.paired_radial
 
     def step(self):
@@ -139,8 +139,11 @@ class EdgeStep:
             # the output layer once per undirected pair (both directions have the same distance,
             # hence the same weights); edge mode: every edge vector gets its own gradient
             last = self.mlp.mlp[-1]
+            # with config.fused_weight_grad = True: the input gradient without the per-edge weight
+            # gradient in memory (its work list costs one more synchronisation per step here)
+            batches = self.K.tp_gh_batches(row_ptr) if self.fused else None
             out, _ = ops.radial_tp_pairs(self.x, Y, self.mlp.hidden(feats), last.weight, last.bias, row_ptr, perm,
-                                         snd, pairs.wrow, pairs.pairs, self.config, self.C)
+                                         snd, pairs.wrow, pairs.pairs, self.config, self.C, batches)
         elif self.fused:
             # output layer + TP as one op: the backward forms the weight gradient in registers
             last = self.mlp.mlp[-1]

@@ -159,6 +159,11 @@ int mnx_gather_rows_f32(const float* src, const int64_t* idx, int64_t n, int32_t
                         mnx_stream_t stream);
 int mnx_scatter_rows_f32(const float* src, const int64_t* idx, int64_t n, int32_t F, float* dst,
                          mnx_stream_t stream);
+/* dst[i] = src[pairs[i][0]] + src[pairs[i][1]] for rows of F floats (F a multiple of 4, src and  */
+/* dst 16-byte aligned): the per-pair sum of per-edge rows (the output layer's input gradient     */
+/* of a pair from its two edges').  No counterpart in the reference (its MLP runs per edge).     */
+int mnx_pair_sum_rows_f32(const float* src, const int32_t* pairs, int64_t num_pairs, int32_t F, float* dst,
+                          mnx_stream_t stream);
 
 size_t mnx_edge_pairs_workspace_bytes(int64_t num_edges);
 int mnx_edge_pairs(const int64_t* edge_index, int64_t num_edges, int64_t num_nodes, const int32_t* row_ptr,
@@ -535,6 +540,22 @@ int mnx_tp_weight_grad_f32(int32_t config, int32_t channels, const float* x, con
                            const float* grad_out, const int64_t* edge_index, int64_t num_nodes,
                            int64_t num_edges, const uint16_t* frag, int32_t K, float* grad_h,
                            mnx_stream_t stream);
+/* The same grad_h for the edges of a receiver CSR (row_ptr, perm, senders as  */
+/* from mnx_csr_build), in batches of up to 32 consecutive edges of one      */
+/* receiver: batches [num_batches][2] = (receiver, first CSR slot), covering */
+/* every slot once.  A wavefront per batch stages its receiver's output       */
+/* gradient rows in LDS and forms gw from them and the senders' rows; the   */
+/* contraction runs group (paths sharing l1) by group, 16-channel chunk by   */
+/* chunk, path by path, so frag is W packed by mnx_edge_weights_pack_f32     */
+/* (backward) after permuting W's rows into that order:                      */
+/* mnx_tp_weight_grad_rows fills rows [num_paths * C] (host memory) with the */
+/* original row of each permuted one.  grad_h [num_edges][K] by edge id.     */
+int mnx_tp_weight_grad_rows(int32_t config, int32_t C, int32_t* rows);
+int mnx_tp_weight_grad_batched_f32(int32_t config, int32_t C, const float* x, const float* Y,
+                                   const float* grad_out, const int32_t* row_ptr, const int32_t* perm,
+                                   const int32_t* senders, const int32_t* batches, int64_t num_batches,
+                                   int64_t num_nodes, int64_t num_edges, const uint16_t* frag, int32_t K,
+                                   float* grad_h, mnx_stream_t stream);
 
 /* ------------------------------------------------------------------------ */
 /* Per-edge channelwise tensor product with shared weights, no scatter: the  */

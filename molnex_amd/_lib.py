@@ -56,6 +56,7 @@ SIGNATURES = {
     "mnx_gather_rows_f32": (C.c_int, [vp, vp, c_i64, c_i32, vp, vp]),
     "mnx_edge_pairs_verify": (C.c_int, [vp, c_i64, vp, c_i32, vp, vp]),
     "mnx_scatter_rows_f32": (C.c_int, [vp, vp, c_i64, c_i32, vp, vp]),
+    "mnx_pair_sum_rows_f32": (C.c_int, [vp, vp, c_i64, c_i32, vp, vp]),
     "mnx_edge_pairs": (C.c_int, [vp, c_i64, c_i64, vp, vp, vp, vp, c_i32, vp, vp, vp, vp, vp, c_sz, vp]),
     "mnx_pme_spread_workspace_bytes": (c_sz, [c_i64, c_i32, c_i32, c_i32]),
     "mnx_pme_spread_f32": (C.c_int, [vp, vp, vp, c_i64, c_i32, c_i32, c_i32, c_i32, c_f64, vp, vp, c_sz, vp]),
@@ -98,6 +99,9 @@ SIGNATURES = {
     "mnx_edge_weights_bwd_pairs_f32": (C.c_int, [vp, vp, c_i64, c_i32, vp, c_i32, vp, vp]),
     "mnx_edge_weights_rows_f32": (C.c_int, [vp, vp, c_i64, c_i32, vp, vp, c_i32, vp, vp]),
     "mnx_tp_weight_grad_f32": (C.c_int, [c_i32, c_i32, vp, vp, vp, vp, c_i64, c_i64, vp, c_i32, vp, vp]),
+    "mnx_tp_weight_grad_rows": (C.c_int, [c_i32, c_i32, vp]),
+    "mnx_tp_weight_grad_batched_f32": (C.c_int, [c_i32, c_i32, vp, vp, vp, vp, vp, vp, vp, c_i64, c_i64, c_i64, vp,
+                                                  c_i32, vp, vp]),
     "mnx_edge_tp_fwd_f32": (C.c_int, [c_i32, c_i32, vp, vp, vp, vp, c_i64, vp, vp]),
     "mnx_edge_tp_bwd_workspace_bytes": (c_sz, [c_i32, c_i32, c_i64]),
     "mnx_edge_tp_bwd_f32": (C.c_int, [c_i32, c_i32, vp, vp, vp, vp, vp, c_i64, vp, vp, vp, vp, vp, c_sz, vp]),

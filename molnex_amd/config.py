@@ -23,12 +23,13 @@ class _Config:
     # edge index lies in [0, num_nodes) -- one host synchronisation per graph; False: trust
     # the indices like the reference's ops (src/molix/F/locality.py:3-5)
     validate_edges: bool = True
-    # True: where the radial MLP's output layer is frozen and no second derivatives are taken
-    # (eval mode), it runs fused with the tensor product (molix::radial_tp): the backward forms
-    # the per-edge weight gradient in registers instead of writing and re-reading it.  Off by
-    # default: on MI355X the fused weight gradient is latency-bound on its per-lane gathers and
-    # slower than writing and re-reading the gradient, except for the 1-path-per-l products
-    fused_weight_grad: bool = False
+    # Where the radial MLP's output layer is frozen and no second derivatives are taken (eval mode),
+    # whether the backward forms the output layer's input gradient without writing the per-edge
+    # weight gradient (molix::tp_weight_grad_batched with the pairing, molix::radial_tp without it).
+    # False (default): never -- on MI355X it breaks even for products of scalar inputs and is slower
+    # for inputs with l >= 1 (its per-edge contraction is VALU-bound); None: scalar-input products
+    # only (a first interaction layer); True: every product
+    fused_weight_grad: bool | None = False
     # True: where the radial MLP's parameters are frozen and no second derivatives are taken (eval
     # mode), the MLP and its output layer run once per undirected pair of opposite edges whose radial
     # inputs are bit-identical (a neighbor list's pairs), and the tensor product reads each pair's

@@ -686,13 +686,172 @@ def gen_grad_h(cfg: Cfg) -> str:
     return "\n".join(L)
 
 
+# ---------------------------------------------------------------------------
+# Receiver-batched fused weight gradient (tp_gh.hip, k_tp_gh2): the contraction
+# index n = p*C + c of grad_h = gw W is walked group by group (paths sharing l1),
+# within a group by 16-channel chunk, within a chunk by path.  Per (group,
+# chunk) a lane holds its edge's sender rows of the group (n1 rows x 8 channels)
+# in registers, and the wavefront -- 32 edges of one receiver -- stages that
+# receiver's output-gradient rows of the group's paths (16 channels each) in
+# LDS; each k-step then forms gw for one path and 8 channels from registers and
+# LDS only.
+# ---------------------------------------------------------------------------
+
+
+def gh2_layout(cfg: Cfg):
+    """Per group: (paths, x row offset o1, n1, g rows [(path j, m3) -> LDS row], rows)."""
+    out = []
+    for ps in cfg.groups:
+        rows = []
+        for j, p in enumerate(ps):
+            for m3 in range(2 * p["l3"] + 1):
+                rows.append(p["o3"] + m3)
+        out.append(dict(paths=ps, o1=ps[0]["o1"], n1=2 * ps[0]["l1"] + 1, grows=rows))
+    return out
+
+
+def gh2_order(cfg: Cfg, C: int):
+    """W rows in the kernel's contraction order (the order of its k-steps' 16 rows each)."""
+    rows = []
+    for grp in gh2_layout(cfg):
+        for cc in range(C // 16):
+            for p in grp["paths"]:
+                rows.extend(range(p["k"] * C + 16 * cc, p["k"] * C + 16 * cc + 16))
+    return rows
+
+
+def gen_grad_h2(cfg: Cfg) -> str:
+    """TPGH2<cfg>::run: the whole contraction of k_tp_gh2 for one configuration, groups and paths
+    unrolled (every register index static), the 16-channel chunks a runtime loop.  Per chunk the
+    lane's sender rows and its share of the receiver's output-gradient rows for the next chunk are
+    loaded into registers while the current chunk's k-steps run; the gradient rows go to the
+    wavefront's LDS area (two buffers) at the end of the chunk.  Each k-step hands the lane's 8 gw
+    values to the caller's sink (S::step), which does the matrix-core part."""
+    lay = gh2_layout(cfg)
+    NG = len(lay)
+    gmax = max(len(g["grows"]) for g in lay)
+    L = []
+    a = L.append
+    a(f"template <> struct TPGH2<{cfg.idx}> {{")
+    a(f"  static constexpr int NG = {NG}, NX = {cfg.NX}, NY = {cfg.NY}, NO = {cfg.NO}, NP = {cfg.NP}, "
+      f"GROWS = {gmax};")
+    order = [p["k"] for g in lay for p in g["paths"]]
+    a(f"  static constexpr int GP[NG] = {{{', '.join(str(len(g['paths'])) for g in lay)}}};")
+    a(f"  static constexpr int ORDER[NP] = {{{', '.join(str(k) for k in order)}}};  // paths, group by group")
+    a("  template <class S>")
+    a("  __device__ static __forceinline__ void run(S& st, const float* __restrict__ xr, const float* __restrict__ grow,")
+    a(f"                                              int C, float* __restrict__ lds, int lane, bool eok, bool bok,")
+    a(f"                                              const float (&y)[{cfg.NY}]) {{")
+    a("    const int cpk = C >> 4;")
+    a("    const int hoff = 8 * (lane >> 5);")
+    a("    const f32x4 z4 = {0.f, 0.f, 0.f, 0.f};")
+    for gi, g in enumerate(lay):
+        n1, o1, rows = g["n1"], g["o1"], g["grows"]
+        nsh = -(-len(rows) * 4 // 64)  # this lane's shares of the gradient rows
+        a(f"    {{  // group {gi}: l1 = {g['paths'][0]['l1']}, {len(g['paths'])} paths, {len(rows)} gradient rows")
+        a("      " + " ".join(f"f32x4 a{m}, b{m}, na{m}, nb{m};" for m in range(n1)))
+        a("      " + " ".join(f"f32x4 gp{k}; int go{k} = -1;" for k in range(nsh)))
+        for k in range(nsh):
+            a(f"      if (lane + {64 * k} < {len(rows) * 4}) go{k} = kGH2Rows_c{cfg.idx}_g{gi}[(lane + {64 * k}) >> 2] * C + "
+              f"4 * ((lane + {64 * k}) & 3);")
+        # chunk 0: x and gradient rows directly
+        a("      if (eok) {")
+        for m in range(n1):
+            a(f"        a{m} = *reinterpret_cast<const f32x4*>(xr + {o1 + m} * C);")
+            a(f"        b{m} = *reinterpret_cast<const f32x4*>(xr + {o1 + m} * C + 4);")
+        a("      } else {")
+        a("        " + " ".join(f"a{m} = z4; b{m} = z4;" for m in range(n1)))
+        a("      }")
+        a("      if (bok) {")
+        for k in range(nsh):
+            a(f"        if (go{k} >= 0) *reinterpret_cast<f32x4*>(lds + 4 * (lane + {64 * k})) = "
+              f"*reinterpret_cast<const f32x4*>(grow + go{k});")
+        a("      }")
+        a("      for (int cc = 0; cc < cpk; ++cc) {")
+        a(f"        const float* __restrict__ gl = lds + (cc & 1) * {gmax * 16} + hoff;")
+        a("        const bool more = cc + 1 < cpk;")
+        a("        if (more && eok) {")
+        for m in range(n1):
+            a(f"          na{m} = *reinterpret_cast<const f32x4*>(xr + 16 * (cc + 1) + {o1 + m} * C);")
+            a(f"          nb{m} = *reinterpret_cast<const f32x4*>(xr + 16 * (cc + 1) + {o1 + m} * C + 4);")
+        a("        }")
+        a("        if (more && bok) {")
+        for k in range(nsh):
+            a(f"          if (go{k} >= 0) gp{k} = *reinterpret_cast<const f32x4*>(grow + 16 * (cc + 1) + go{k});")
+        a("        }")
+        base = 0
+        for j, p in enumerate(g["paths"]):
+            c = p["c"]
+            n3 = 2 * p["l3"] + 1
+            a(f"        {{  // path {p['k']}: ({p['l1']}, {p['l2']}) -> {p['l3']}")
+            a("          f32x4 o0 = z4, o1 = z4;")
+            a("          if (eok) {")
+            rws = []
+            for m3 in range(n3):
+                row = []
+                for m1 in range(n1):
+                    terms = [(m2, c[m1, m2, m3]) for m2 in range(2 * p["l2"] + 1) if abs(c[m1, m2, m3]) > EPS]
+                    if not terms:
+                        continue
+                    expr = f"{f32(terms[0][1])} * y[{p['o2'] + terms[0][0]}]"
+                    for m2, v in terms[1:]:
+                        expr = f"fmaf({f32(v)}, y[{p['o2'] + m2}], {expr})"
+                    a(f"            const float M{m3}_{m1} = {expr};")
+                    row.append(m1)
+                rws.append(row)
+            for m3, row in enumerate(rws):
+                if not row:
+                    continue
+                a("            {")
+                a(f"              const f32x4 g0 = *reinterpret_cast<const f32x4*>(gl + {(base + m3) * 16});")
+                a(f"              const f32x4 g1 = *reinterpret_cast<const f32x4*>(gl + {(base + m3) * 16 + 4});")
+                for q in range(8):
+                    h, i = q >> 2, q & 3
+                    xn = "ab"[h]
+                    expr = f"M{m3}_{row[0]} * {xn}{row[0]}[{i}]"
+                    for m1 in row[1:]:
+                        expr = f"fmaf(M{m3}_{m1}, {xn}{m1}[{i}], {expr})"
+                    a(f"              o{h}[{i}] = fmaf(g{h}[{i}], {expr}, o{h}[{i}]);")
+                a("            }")
+            a("          }")
+            a("          st.step(o0, o1);")
+            a("        }")
+            base += n3
+        a("        if (more) {")
+        a("          " + " ".join(f"a{m} = na{m}; b{m} = nb{m};" for m in range(n1)))
+        a("          if (bok) {")
+        a(f"            float* __restrict__ gn = lds + ((cc + 1) & 1) * {gmax * 16};")
+        for k in range(nsh):
+            a(f"            if (go{k} >= 0) *reinterpret_cast<f32x4*>(gn + 4 * (lane + {64 * k})) = gp{k};")
+        a("          }")
+        a("        }")
+        a("      }")
+        a("    }")
+    a("  }")
+    a("};")
+    return "\n".join(L)
+
+
+def gen_gh2_tables(cfg: Cfg) -> str:
+    """Constant-memory row lists of the groups' output-gradient rows (stage_g)."""
+    out = []
+    for gi, g in enumerate(gh2_layout(cfg)):
+        rows = g["grows"]
+        out.append(f"__constant__ int kGH2Rows_c{cfg.idx}_g{gi}[{len(rows)}] = "
+                   f"{{{', '.join(str(r) for r in rows)}}};")
+    return "\n".join(out)
+
+
 def generate_gh() -> str:
     cfgs = [Cfg(i, *c) for i, c in enumerate(config_list())]
     out = ["// Generated by molnex_amd/csrc/gen_tp.py -- do not edit.",
-           "// Fused tensor-product weight gradient: per-path gw producers (TPGH<config>)."]
+           "// Fused tensor-product weight gradient: per-path gw producers (TPGH<config>) and the",
+           "// receiver-batched form (TPGH2<config>)."]
     for cfg in cfgs:
         out.append(f"// config {cfg.idx}: in l={cfg.in_ls} sh l={cfg.sh_ls} out l={cfg.out_ls}")
         out.append(gen_grad_h(cfg))
+        out.append(gen_gh2_tables(cfg))
+        out.append(gen_grad_h2(cfg))
         out.append("")
     out.append(f"static constexpr int kNumTPGHConfigs = {len(cfgs)};")
     return "\n".join(out) + "\n"

@@ -139,6 +139,20 @@ __global__ void k_scatter_rows(const float* __restrict__ src, const int64_t* __r
     dst[idx[i] * F + (t - i * F)] = src[t];
 }
 
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// dst[i] = src[pairs[i][0]] + src[pairs[i][1]], one thread per 4 floats (F a multiple of 4).
+__global__ void k_pair_sum_rows(const float* __restrict__ src, const int32_t* __restrict__ pairs, int64_t n, int F4,
+                                float* __restrict__ dst) {
+    const int64_t t = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (t >= n * F4) return;
+    const int64_t i = t / F4;
+    const int f = int(t - i * F4);
+    const f32x4 a = reinterpret_cast<const f32x4*>(src)[int64_t(pairs[2 * i]) * F4 + f];
+    const f32x4 b = reinterpret_cast<const f32x4*>(src)[int64_t(pairs[2 * i + 1]) * F4 + f];
+    reinterpret_cast<f32x4*>(dst)[t] = a + b;
+}
+
 }  // namespace
 }  // namespace mnx
 
@@ -236,6 +250,19 @@ int mnx_edge_pairs(const int64_t* edge_index, int64_t num_edges, int64_t num_nod
     rc = exclusive_scan<int32_t, int32_t>(flag, num_edges, rank, tiles, nullptr, s);
     if (rc) return rc;
     hipLaunchKernelGGL(k_pair_place, grid, dim3(256), 0, s, rev, flag, rank, num_edges, wrow, lead, pairs);
+    MNX_CHECK_LAUNCH();
+    return MNX_OK;
+}
+
+int mnx_pair_sum_rows_f32(const float* src, const int32_t* pairs, int64_t num_pairs, int32_t F, float* dst,
+                          mnx_stream_t stream) {
+    clear_error();
+    MNX_REQUIRE(num_pairs >= 0 && F >= 0 && F % 4 == 0, "pair sum: F must be a multiple of 4");
+    if (num_pairs == 0 || F == 0) return MNX_OK;
+    MNX_REQUIRE(src && pairs && dst && (uintptr_t)src % 16 == 0 && (uintptr_t)dst % 16 == 0,
+                "pair sum: null or unaligned pointer");
+    hipLaunchKernelGGL(k_pair_sum_rows, dim3(unsigned(ceil_div(num_pairs * (F / 4), 256))), dim3(256), 0,
+                       (hipStream_t)stream, src, pairs, num_pairs, F / 4, dst);
     MNX_CHECK_LAUNCH();
     return MNX_OK;
 }

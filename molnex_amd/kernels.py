@@ -1374,10 +1374,95 @@ def _(grad, pairs, weight):
     return grad.new_empty(pairs.shape[0], weight.shape[1])
 
 
+@torch.library.custom_op("molix::pair_sum_rows", mutates_args=(), device_types="cuda")
+def pair_sum_rows(src: Tensor, pairs: Tensor) -> Tensor:
+    """``src[pairs[:, 0]] + src[pairs[:, 1]]`` for int32 (P, 2) pairs and rows of a multiple of 4 floats
+    (one kernel)."""
+    _require_gpu("pair_sum_rows", src, pairs)
+    if src.dtype != torch.float32 or src.dim() != 2 or src.shape[1] % 4:
+        raise ValueError("pair_sum_rows: src must be float32 (n, F) with F a multiple of 4")
+    s = _aligned16(src)
+    p = pairs.to(torch.int32).contiguous()
+    out = s.new_empty(p.shape[0], s.shape[1])
+    check(_lib.load().mnx_pair_sum_rows_f32(ptr(s), ptr(p), p.shape[0], s.shape[1], ptr(out), _stream(s)),
+          "pair_sum_rows")
+    return out
+
+
+@pair_sum_rows.register_fake
+def _(src, pairs):
+    return src.new_empty(pairs.shape[0], src.shape[1])
+
+
+def tp_gh_batches(row_ptr: Tensor) -> Tensor:
+    """The work list of ``tp_weight_grad_batched``: (receiver, first CSR slot) of every batch of up to 32
+    consecutive edges of one receiver, int32 (B, 2).  One host synchronisation (the batch count):
+    build it once per graph."""
+    rp = row_ptr.to(torch.int64)
+    n = rp.shape[0] - 1
+    nb = (rp[1:] - rp[:-1] + 31) // 32
+    total = int(nb.sum().item())
+    r = torch.repeat_interleave(torch.arange(n, device=rp.device), nb, output_size=total)
+    first = torch.cumsum(nb, 0) - nb
+    t0 = rp[:-1].index_select(0, r) + 32 * (torch.arange(total, device=rp.device) - first.index_select(0, r))
+    return torch.stack([r, t0], 1).to(torch.int32).contiguous()
+
+
+_GH2_ROWS: dict = {}
+
+
+def _gh2_frag(weight: Tensor, config: int, channels: int) -> Tensor:
+    """The output layer's W with its rows in ``tp_weight_grad_batched``'s contraction order, packed
+    as the backward fragment of ``edge_weights``."""
+    key = (config, channels, weight.device)
+    rows = _GH2_ROWS.get(key)
+    if rows is None:
+        num_paths = tp_config_info(config)[0]
+        host = (C.c_int32 * (num_paths * channels))()
+        check(_lib.load().mnx_tp_weight_grad_rows(config, channels, host), "tp_weight_grad rows")
+        rows = torch.tensor(list(host), dtype=torch.int64).to(weight.device)
+        _GH2_ROWS[key] = rows
+    return _ew_frag(weight.detach().index_select(0, rows), True)
+
+
+@torch.library.custom_op("molix::tp_weight_grad_batched", mutates_args=(), device_types="cuda")
+def tp_weight_grad_batched(x: Tensor, Y: Tensor, grad_out: Tensor, row_ptr: Tensor, perm: Tensor, senders: Tensor,
+                           batches: Tensor, weight: Tensor, config: int, channels: int) -> Tensor:
+    """``grad_h = gw @ weight`` per directed edge (as ``tp_weight_grad``) over the receiver CSR, one
+    wavefront per batch of ``tp_gh_batches``: the batch's receiver's output gradient is staged in LDS
+    and the sender rows are read once per 16-channel chunk, so the per-edge weight gradient ``gw``
+    is formed from registers and LDS and multiplied on the matrix cores without being written."""
+    _require_gpu("tp_weight_grad_batched", x, Y, grad_out, row_ptr, perm, senders, batches, weight)
+    num_paths, nx, ny, no = tp_config_info(config)
+    Nw, K = weight.shape
+    if Nw != num_paths * channels:
+        raise ValueError(f"tp_weight_grad_batched: weight has {Nw} rows, the product has {num_paths} x {channels}")
+    xs = _aligned16(_f32_rows(x, nx * channels, "x"))
+    Ys = _f32_rows(Y, ny, "Y")
+    go = _aligned16(_f32_rows(grad_out, no * channels, "grad_out"))
+    N, E = xs.shape[0], Ys.shape[0]
+    if (go.shape[0] != N or row_ptr.shape[0] != N + 1 or perm.shape[0] != E or senders.shape[0] != E
+            or batches.dim() != 2 or batches.shape[1] != 2):
+        raise ValueError("tp_weight_grad_batched: inconsistent sizes of x / Y / grad_out / CSR / batches")
+    rp, pm, sd = (t.to(torch.int32).contiguous() for t in (row_ptr, perm, senders))
+    bt = batches.to(torch.int32).contiguous()
+    frag = _gh2_frag(weight, config, channels)
+    gh = xs.new_empty(E, K)
+    check(_lib.load().mnx_tp_weight_grad_batched_f32(config, channels, ptr(xs), ptr(Ys), ptr(go), ptr(rp), ptr(pm),
+                                                     ptr(sd), ptr(bt), bt.shape[0], N, E, ptr(frag), K, ptr(gh),
+                                                     _stream(xs)), "tp_weight_grad_batched")
+    return gh
+
+
+@tp_weight_grad_batched.register_fake
+def _(x, Y, grad_out, row_ptr, perm, senders, batches, weight, config, channels):
+    return x.new_empty(Y.shape[0], weight.shape[1])
+
+
 @torch.library.custom_op("molix::radial_tp_pairs", mutates_args=(), device_types="cuda")
 def radial_tp_pairs(x: Tensor, Y: Tensor, h: Tensor, weight: Tensor, bias: Tensor | None, row_ptr: Tensor,
                     perm: Tensor, senders: Tensor, wrow: Tensor, pairs: Tensor, config: int,
-                    channels: int) -> tuple[Tensor, Tensor]:
+                    channels: int, batches: Tensor | None = None) -> tuple[Tensor, Tensor]:
     """``(tp_scatter(x, Y, w[wrow]), w)`` with ``w = h @ weight.T + bias`` computed once per undirected
     pair (``wrow`` maps every edge to its pair, ``pairs`` lists each pair's two edges, lead first:
     ``EdgePairs``).  Equal to the output layer applied per directed edge (the reference's
@@ -1390,7 +1475,12 @@ def radial_tp_pairs(x: Tensor, Y: Tensor, h: Tensor, weight: Tensor, bias: Tenso
     (``edge_weights_backward_pairs``): the gradient reaching each pair's radial inputs is the sum
     of both directions', which leaves every function of the positions (energies, forces, virials)
     as per edge.  In edge mode the forward uses the lead rows of ``h`` and the backward gives every
-    edge its own input gradient (``edge_weights_backward``), as the per-edge composition does."""
+    edge its own input gradient (``edge_weights_backward``), as the per-edge composition does.
+
+    With ``batches`` (``tp_gh_batches(row_ptr)``) and no output-layer parameter gradient, the backward
+    does not write the per-edge weight gradient: the tensor-product backward gives grad x and grad Y
+    only and ``tp_weight_grad_batched`` forms grad h per directed edge (summed over each pair's two
+    edges in pair mode)."""
     if h.shape[0] == pairs.shape[0]:
         w = edge_weights(h, weight, bias)
     else:  # the lead rows of h, read in place
@@ -1399,25 +1489,41 @@ def radial_tp_pairs(x: Tensor, Y: Tensor, h: Tensor, weight: Tensor, bias: Tenso
 
 
 @radial_tp_pairs.register_fake
-def _(x, Y, h, weight, bias, row_ptr, perm, senders, wrow, pairs, config, channels):
+def _(x, Y, h, weight, bias, row_ptr, perm, senders, wrow, pairs, config, channels, batches=None):
     num_paths, nx, ny, no = tp_config_info(config)
     return x.new_empty((row_ptr.shape[0] - 1, no * channels)), h.new_empty((pairs.shape[0], weight.shape[0]))
 
 
 def _rtpp_setup(ctx, inputs, output):
-    x, Y, h, weight, bias, row_ptr, perm, senders, wrow, pairs, config, channels = inputs
-    ctx.save_for_backward(x, Y, h, weight, output[1], row_ptr, perm, senders, wrow, pairs)
+    x, Y, h, weight, bias, row_ptr, perm, senders, wrow, pairs, config, channels = inputs[:12]
+    batches = inputs[12] if len(inputs) > 12 else None
+    ctx.save_for_backward(x, Y, h, weight, output[1], row_ptr, perm, senders, wrow, pairs, batches)
     ctx.config, ctx.channels, ctx.has_bias = config, channels, bias is not None
     # the returned weights usually get no gradient: pass None rather than a (pairs, N) zero tensor
     ctx.set_materialize_grads(False)
 
 
 def _rtpp_backward(ctx, g_out, g_w):
-    x, Y, h, weight, w, row_ptr, perm, senders, wrow, pairs = ctx.saved_tensors
+    x, Y, h, weight, w, row_ptr, perm, senders, wrow, pairs, batches = ctx.saved_tensors
     nig = ctx.needs_input_grad
     need_x, need_Y, need_h, need_W = nig[0], nig[1], nig[2], nig[3]
     need_b = nig[4] and ctx.has_bias
     gx = gY = gh = gW = gb = None
+    per_pair = h.shape[0] == pairs.shape[0]
+    if batches is not None and g_out is not None and need_h and not (need_W or need_b):
+        # grad h without the per-edge weight gradient in memory
+        go = g_out.contiguous()
+        if need_x or need_Y:
+            gx, gY, _ = tp_scatter_backward(go, x, Y, w, row_ptr, perm, senders, ctx.config, ctx.channels,
+                                            need_x, need_Y, False, wrow=wrow)
+            gx = gx.reshape(x.shape) if need_x else None
+            gY = gY.reshape(Y.shape) if need_Y else None
+        ghe = tp_weight_grad_batched(x, Y, go, row_ptr, perm, senders, batches, weight, ctx.config, ctx.channels)
+        gh = pair_sum_rows(ghe, pairs) if per_pair else ghe
+        if g_w is not None:
+            ghw = edge_weights_backward(g_w.contiguous(), weight)
+            gh = gh + ghw if per_pair else gh.index_add(0, pairs[:, 0].long(), ghw)
+        return gx, gY, gh, None, None, None, None, None, None, None, None, None, None
     gw = None  # per-edge weight gradient, (E, N)
     if g_out is not None and (need_x or need_Y or need_h or need_W or need_b):
         gx, gY, gw = tp_scatter_backward(g_out.contiguous(), x, Y, w, row_ptr, perm, senders, ctx.config,
@@ -1426,7 +1532,6 @@ def _rtpp_backward(ctx, g_out, g_w):
         gY = gY.reshape(Y.shape) if need_Y else None
         if not (need_h or need_W or need_b):
             gw = None
-    per_pair = h.shape[0] == pairs.shape[0]
     lead = pairs[:, 0].long()
     if need_h:
         if gw is None:
@@ -1448,7 +1553,7 @@ def _rtpp_backward(ctx, g_out, g_w):
             for i in range(0, hl.shape[0], _EW_ROWS):
                 gW.addmm_(gp[i:i + _EW_ROWS].t(), hl[i:i + _EW_ROWS])
         gb = gp.sum(0) if need_b else None
-    return gx, gY, gh, gW, gb, None, None, None, None, None, None, None
+    return gx, gY, gh, gW, gb, None, None, None, None, None, None, None, None
 
 
 radial_tp_pairs.register_autograd(_rtpp_backward, setup_context=_rtpp_setup)

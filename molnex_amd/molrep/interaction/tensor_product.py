@@ -50,6 +50,7 @@ class EdgeGraph:
                                                                          config.validate_edges)
         self._sender_csr = None
         self._pairs = None  # (features tensor, its version, EdgePairs or None)
+        self._gh_batches = None
 
     def pairs(self, feats: torch.Tensor):
         """The undirected pairs of this graph whose two edges have bit-identical rows of ``feats``
@@ -67,6 +68,13 @@ class EdgeGraph:
                                           feats.detach())
             self._pairs = p = (feats, feats._version, built)
         return p[2]
+
+    def gh_batches(self):
+        """Work list of the fused output-layer gradient (``kernels.tp_gh_batches``), built on first
+        use (one host synchronisation per graph)."""
+        if self._gh_batches is None:
+            self._gh_batches = K.tp_gh_batches(self.row_ptr)
+        return self._gh_batches
 
     def sender_csr(self):
         if self._sender_csr is None:
@@ -179,11 +187,18 @@ class ConvTP(nn.Module):
             pairs = g.pairs(edge_feats)
             if pairs is not None:
                 h = radial_mlp.hidden(torch.ops.molix.gather_rows(edge_feats, pairs.lead))
+                batches = None
+                fuse = config.fused_weight_grad
+                if fuse is None:  # automatic: products of scalar inputs only (see config.py)
+                    fuse = all(b.ir.l == 0 for b in self.cue_tp.irreps_in1)
+                if fuse and K.tp_weight_grad_supported(self.cue_tp.config_id, self.cue_tp.channels,
+                                                       last.in_features):
+                    batches = g.gh_batches()
                 out, _ = torch.ops.molix.radial_tp_pairs(x, edge_angular, h, last.weight, last.bias, g.row_ptr,
                                                          g.perm, g.senders, pairs.wrow, pairs.pairs,
-                                                         self.cue_tp.config_id, self.cue_tp.channels)
+                                                         self.cue_tp.config_id, self.cue_tp.channels, batches)
                 return out
-        if (config.fused_weight_grad and not self.training and x.is_cuda and x.dtype == torch.float32
+        if (config.fused_weight_grad is True and not self.training and x.is_cuda and x.dtype == torch.float32
                 and not config.deterministic and not last.weight.requires_grad
                 and (last.bias is None or not last.bias.requires_grad)
                 and K.tp_weight_grad_supported(self.cue_tp.config_id, self.cue_tp.channels, last.in_features)

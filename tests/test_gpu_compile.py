@@ -81,6 +81,19 @@ def test_opcheck_pairs():
     for rows in (E // 2, E):  # pair mode, edge mode
         h = torch.randn(rows, Kh, device=DEV, requires_grad=True)
         opcheck(ops.radial_tp_pairs.default, (x, Y, h, W, b, row_ptr, perm, snd, pr.wrow, pr.pairs, cfg, C))
+    # the fused input gradient (receiver batches; channels a multiple of 16)
+    C2 = 16
+    batches = K.tp_gh_batches(row_ptr)
+    x2 = torch.randn(N, nx * C2, device=DEV, requires_grad=True)
+    W2 = torch.randn(P * C2, Kh, device=DEV) * 0.3
+    b2 = torch.randn(P * C2, device=DEV)
+    for rows in (E // 2, E):
+        h = torch.randn(rows, Kh, device=DEV, requires_grad=True)
+        opcheck(ops.radial_tp_pairs.default, (x2, Y, h, W2, b2, row_ptr, perm, snd, pr.wrow, pr.pairs, cfg, C2,
+                                              batches))
+    g = torch.randn(N, no * C2, device=DEV)
+    opcheck(ops.tp_weight_grad_batched.default, (x2.detach(), Y.detach(), g, row_ptr, perm, snd, batches, W2, cfg,
+                                                 C2), test_utils=("test_schema", "test_faketensor"))
 
 
 def test_opcheck_class_groups():

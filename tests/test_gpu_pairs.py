@@ -213,6 +213,70 @@ def test_radial_tp_pairs_vs_per_edge_and_fp64(in_ls, sh_ls, out_ls, C, Kh):
         assert rel <= 1e-5 and mx <= 1e-4, name
 
 
+FUSED_CASES = [([0, 1, 2, 3], [0, 1, 2, 3], [0, 1, 2, 3], 64, 64),  # config 3 products
+               ([0], [0, 1, 2, 3], [0, 1, 2, 3], 128, 128),  # config 5 literal, layer 1
+               ([0, 1], [0, 1, 2, 3], [0, 1, 2, 3], 128, 128),  # config 5 literal, layer 2
+               ([0, 1], [0, 1, 2, 3], [0, 1], 32, 32)]
+
+
+@pytest.mark.parametrize("in_ls,sh_ls,out_ls,C,Kh", FUSED_CASES)
+def test_radial_tp_pairs_fused_input_gradient(in_ls, sh_ls, out_ls, C, Kh):
+    """The backward without the per-edge weight gradient in memory (work list of receiver batches,
+    molix::tp_weight_grad_batched) against the one that writes and re-reads it: the forward, grad_Y
+    bit-identical, grad_x within its atomic order, grad_h within 1e-5 (the same products summed in
+    another order); and against the fp64 oracle, pair and edge mode.  Receivers of degree above and
+    below 32 (batches that end inside a segment) and an atom without neighbours."""
+    n, L = 300, (300 / 0.1) ** (1 / 3)
+    p, ei, bond = _system(n, L, seed=7 * C + Kh)
+    n += 1  # one more node without edges (no batch)
+    pr, (row_ptr, perm, snd) = _pairs(ei, n, bond.norm(dim=-1, keepdim=True))
+    assert pr is not None
+    deg = (row_ptr[1:] - row_ptr[:-1]).cpu()
+    assert deg.max() > 32 and bool((deg % 32 != 0).any()) and deg[-1] == 0
+    batches = K.tp_gh_batches(row_ptr)
+    E = ei.shape[0]
+    cfg = K.tp_config_id(in_ls, sh_ls, out_ls)
+    P, NX, NY, NO = K.tp_config_info(cfg)
+    rng = np.random.default_rng(C + 3)
+    x = rng.normal(size=(n, NX * C)).astype(np.float32)
+    Y = torch.ops.molix.spherical_harmonics(bond, max(sh_ls))
+    hp = rng.normal(size=(E // 2, Kh)).astype(np.float32)
+    W = (rng.normal(size=(P * C, Kh)) / np.sqrt(Kh)).astype(np.float32)
+    b = (rng.normal(size=P * C) * 0.1).astype(np.float32)
+    g = rng.normal(size=(n, NO * C)).astype(np.float32)
+    t = lambda a, rg=False: torch.tensor(a, device=DEV, requires_grad=rg)  # noqa: E731
+    wrow = pr.wrow.long()
+    res = []
+    for bt in (None, batches):
+        xt, Yt, ht = t(x, True), Y.detach().clone().requires_grad_(True), t(hp, True)
+        out, _ = torch.ops.molix.radial_tp_pairs(xt, Yt, ht, t(W), t(b), row_ptr, perm, snd, pr.wrow, pr.pairs,
+                                                 cfg, C, bt)
+        res.append((out.detach(),) + torch.autograd.grad(out, (xt, Yt, ht), t(g)))
+    (out0, gx0, gY0, gh0), (out1, gx1, gY1, gh1) = res
+    assert torch.equal(out0, out1) and torch.equal(gY0, gY1)
+    for name, a, r in (("grad_x", gx1, gx0), ("grad_h", gh1, gh0)):
+        rel, mx = _stats(a.cpu(), r.cpu())
+        print(f"fused grad_h in={in_ls} C={C} K={Kh}: {name} vs unfused rel {rel:.2e}, max-abs {mx:.2e} RMS")
+        assert rel <= 1e-5 and mx <= 1e-5, (name, rel, mx)
+    # edge mode
+    hf = t(hp[wrow.cpu().numpy()], True)
+    out3, _ = torch.ops.molix.radial_tp_pairs(t(x), Y.detach(), hf, t(W), t(b), row_ptr, perm, snd, pr.wrow,
+                                              pr.pairs, cfg, C, batches)
+    (gh3,) = torch.autograd.grad(out3, (hf,), t(g))
+    # fp64 oracle (the isolated atom has no edges)
+    tp = O.ChannelwiseTP(_irr(in_ls, C), _irr(sh_ls), _irr(out_ls), C)
+    ei_np, Y64 = ei.cpu().numpy(), Y.detach().cpu().double().numpy()
+    wr = wrow.cpu().numpy()
+    w64 = (hp.astype(np.float64) @ W.T.astype(np.float64) + b)[wr]
+    _, _, rgw = tp.backward(x.astype(np.float64), Y64, w64, ei_np, g.astype(np.float64))
+    gwp = np.zeros((E // 2, P * C))
+    np.add.at(gwp, wr, rgw)
+    for name, a, r in (("grad_h pair", gh1, gwp @ W), ("grad_h edge", gh3, rgw @ W)):
+        rel, mx = _stats(a.detach().cpu(), r)
+        print(f"fused grad_h in={in_ls} C={C} K={Kh}: {name} vs fp64 rel {rel:.2e}, max-abs {mx:.2e} RMS")
+        assert rel <= 1e-5 and mx <= 1e-5, name
+
+
 def test_mace_eval_pairs_vs_per_edge_and_oracle(monkeypatch):
     """A frozen MACE (both variants, config-1 sizes) in eval mode takes the paired path; energies
     and forces against the same model per edge and against the fp64 oracle."""
@@ -246,6 +310,13 @@ def test_mace_eval_pairs_vs_per_edge_and_oracle(monkeypatch):
         rel_e = ((e - e2).abs().max() / e2.abs().max()).item()
         rel_f, mx_f = _stats(f.detach().cpu(), f2.detach().cpu())
         assert rel_e <= 1e-6 and rel_f <= 1e-6 and mx_f <= 1e-5, (rel_e, rel_f, mx_f)
+        # the same with the fused output-layer input gradient (no per-edge weight gradient in memory)
+        monkeypatch.setattr(config, "fused_weight_grad", True)
+        e3, f3 = model(*args)
+        monkeypatch.setattr(config, "fused_weight_grad", False)
+        rel_e = ((e3 - e).abs().max() / e.abs().max()).item()
+        rel_f, mx_f = _stats(f3.detach().cpu(), f.detach().cpu())
+        assert rel_e == 0 and rel_f <= 1e-6 and mx_f <= 1e-5, (rel_e, rel_f, mx_f)
         sd = {k.removeprefix("encoder."): v for k, v in model.state_dict().items()}
         re, rf = mace_ref.energy_forces(sd, cfg, torch.tensor(Z), torch.tensor(pos.astype(np.float32),
                                                                                 dtype=torch.float64),
