@@ -34,6 +34,9 @@
 // writes zeros.  No host synchronisation: the grid is sized for the worst case
 // (one partial workgroup per class) and surplus workgroups exit at once.
 
+#include <algorithm>
+#include <cstdlib>
+
 #include "common.h"
 
 namespace mnx {
@@ -230,6 +233,153 @@ __global__ void __launch_bounds__(kLinThreads) k_block_linear(LinArgs p) {
     }
 }
 
+// Resident form for K <= 128 (plain mode): a workgroup stages its column group's whole weight
+// block once, split into the three bf16 planes (at most 96 KB of LDS), then each wavefront walks
+// row tiles (tile = blockIdx.x * 8 + wave, stepping by the grid) without further barriers.  The
+// next tile's A operands are loaded k-step by k-step as soon as the current tile's k-step has been
+// split, so their latency runs under the current tile's matrix-core products.
+constexpr int kLinResMaxK = 128;
+
+template <int NT, int D>
+__global__ void __launch_bounds__(kLinThreads) k_block_linear_res(LinArgs p) {
+    constexpr int KQ = kLinResMaxK / 16;
+    const int d = D ? D : p.d;
+    __shared__ bf16x8 sw[3][KQ][NT][kWave];
+    const int lane = threadIdx.x & 63, half = lane >> 5, wave = threadIdx.x >> 6;
+    const int nq = (p.K + 15) / 16;
+    const int col0 = blockIdx.y * NT * 32;
+    {
+        // fp32 float4 idx = ((q * NT + t) * 64 + lane) * 2 + h of the column group's fragment
+        const int nchunks = (p.K + kLinKC - 1) / kLinKC;
+        const int n4 = nq * NT * kWave * 2;
+        const f32x4* wsrc = reinterpret_cast<const f32x4*>(p.w) + int64_t(blockIdx.y) * nchunks * (kLinKC / 16) * NT * kWave * 2;
+        bf16x4* sw4 = reinterpret_cast<bf16x4*>(&sw[0][0][0][0]);
+        constexpr int kPlane4 = KQ * NT * kWave * 2;  // bf16x4 per plane
+        for (int idx = threadIdx.x; idx < n4; idx += kLinThreads) {
+            const f32x4 v = wsrc[idx];
+            bf16x4 b0, b1, b2;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                __bf16 x0, x1, x2;
+                split3(v[i], x0, x1, x2);
+                b0[i] = x0;
+                b1[i] = x1;
+                b2[i] = x2;
+            }
+            sw4[idx] = b0;
+            sw4[kPlane4 + idx] = b1;
+            sw4[2 * kPlane4 + idx] = b2;
+        }
+        __syncthreads();
+    }
+    const int64_t rows = p.R * d;
+    const int64_t ntiles = (rows + 31) / 32;
+    const int64_t tstep = int64_t(gridDim.x) * (kLinThreads / kWave);
+    int32_t base[kLinMaxSeg];
+    // A operands of row tile `tile`: row pointer and per-segment offsets of this lane's row
+    auto locate = [&](int64_t tile, const float*& arow, bool& valid) {
+        const int64_t row0 = tile * 32;
+        const int64_t n0 = row0 / d;
+        const int c0 = int(row0 - n0 * d);
+        const int64_t n = n0 + (c0 + (lane & 31)) / d;
+        const int ci = (c0 + (lane & 31)) % d;
+        valid = row0 + (lane & 31) < rows;
+        arow = p.a + n * p.a_stride;
+#pragma unroll
+        for (int sg = 0; sg < kLinMaxSeg; ++sg)
+            base[sg] = sg < p.nseg ? int32_t(p.seg[sg].col + int64_t(ci) * p.seg[sg].comp - p.seg[sg].k0) : 0;
+    };
+    auto load_q = [&](const float* arow, bool valid, int q, f32x4 (&dst)[2]) {
+        const int k = 16 * q + 8 * half;
+        int32_t off = 0;
+#pragma unroll
+        for (int sg = 0; sg < kLinMaxSeg; ++sg)
+            if (sg < p.nseg && k >= p.seg[sg].k0) off = base[sg];
+        dst[0] = dst[1] = f32x4{0.f, 0.f, 0.f, 0.f};
+        if (valid && k < p.K) {
+            dst[0] = *reinterpret_cast<const f32x4*>(arow + off + k);
+            dst[1] = *reinterpret_cast<const f32x4*>(arow + off + k + 4);
+        }
+    };
+    int64_t tile = int64_t(blockIdx.x) * (kLinThreads / kWave) + wave;
+    if (tile >= ntiles) return;  // no barrier after this point
+    f32x4 av[KQ][2];
+    const float* arow;
+    bool valid;
+    locate(tile, arow, valid);
+#pragma unroll
+    for (int q = 0; q < KQ; ++q)
+        if (q < nq) load_q(arow, valid, q, av[q]);
+    for (; tile < ntiles; tile += tstep) {
+        const int64_t row0 = tile * 32;
+        const int64_t n0 = row0 / d;
+        const int c0 = int(row0 - n0 * d);
+        const int64_t next = tile + tstep;
+        const bool more = next < ntiles;
+        const float* arow_n = arow;
+        bool valid_n = false;
+        if (more) locate(next, arow_n, valid_n);
+        f32x16 acc[NT];
+#pragma unroll
+        for (int t = 0; t < NT; ++t)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[t][r] = 0.f;
+#pragma unroll
+        for (int q = 0; q < KQ; ++q) {
+            if (q < nq) {
+                bf16x8 a0, a1, a2;
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    __bf16 x0, x1, x2;
+                    split3(j < 4 ? av[q][0][j] : av[q][1][j - 4], x0, x1, x2);
+                    a0[j] = x0;
+                    a1[j] = x1;
+                    a2[j] = x2;
+                }
+                if (more) load_q(arow_n, valid_n, q, av[q]);
+#pragma unroll
+                for (int t = 0; t < NT; ++t) acc[t] = mfma_bf16(a2, sw[0][q][t][lane], acc[t]);
+#pragma unroll
+                for (int t = 0; t < NT; ++t) acc[t] = mfma_bf16(a1, sw[1][q][t][lane], acc[t]);
+#pragma unroll
+                for (int t = 0; t < NT; ++t) acc[t] = mfma_bf16(a0, sw[2][q][t][lane], acc[t]);
+#pragma unroll
+                for (int t = 0; t < NT; ++t) acc[t] = mfma_bf16(a1, sw[0][q][t][lane], acc[t]);
+#pragma unroll
+                for (int t = 0; t < NT; ++t) acc[t] = mfma_bf16(a0, sw[1][q][t][lane], acc[t]);
+#pragma unroll
+                for (int t = 0; t < NT; ++t) acc[t] = mfma_bf16(a0, sw[0][q][t][lane], acc[t]);
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int o = 8 * (r / 4) + 4 * half + r % 4;
+            if (row0 + o >= rows) continue;
+            const int64_t nn = n0 + (c0 + o) / d;
+            const int ii = (c0 + o) % d;
+            float* ob = p.out + nn * p.out_stride + p.out_off + int64_t(ii) * p.out_comp;
+#pragma unroll
+            for (int t = 0; t < NT; ++t) {
+                const int c = col0 + 32 * t + (lane & 31);
+                if (c < p.N) ob[c] = acc[t][r];
+            }
+        }
+        arow = arow_n;
+        valid = valid_n;
+    }
+}
+
+template <int NT>
+void launch_res(int d, dim3 grid, hipStream_t s, const LinArgs& p) {
+    switch (d) {
+        case 1: hipLaunchKernelGGL((k_block_linear_res<NT, 1>), grid, dim3(kLinThreads), 0, s, p); break;
+        case 3: hipLaunchKernelGGL((k_block_linear_res<NT, 3>), grid, dim3(kLinThreads), 0, s, p); break;
+        case 5: hipLaunchKernelGGL((k_block_linear_res<NT, 5>), grid, dim3(kLinThreads), 0, s, p); break;
+        case 7: hipLaunchKernelGGL((k_block_linear_res<NT, 7>), grid, dim3(kLinThreads), 0, s, p); break;
+        default: hipLaunchKernelGGL((k_block_linear_res<NT, 0>), grid, dim3(kLinThreads), 0, s, p); break;
+    }
+}
+
 // output tiles of 32 columns per wavefront for N columns (the column-group width is 32 * this)
 int lin_tiles(int N) { return N >= 128 ? 4 : int(ceil_div(N, 32)); }
 
@@ -242,6 +392,16 @@ void launch_nt(int d, dim3 grid, hipStream_t s, const LinArgs& p) {
         case 7: hipLaunchKernelGGL((k_block_linear<NT, 7, IDX>), grid, dim3(kLinThreads), 0, s, p); break;
         default: hipLaunchKernelGGL((k_block_linear<NT, 0, IDX>), grid, dim3(kLinThreads), 0, s, p); break;
     }
+}
+
+// the resident form unless the environment sets MNX_LIN_RESIDENT=0 (to compare with the chunked
+// kernel; both give bit-identical results)
+bool lin_resident() {
+    static const bool on = [] {
+        const char* e = std::getenv("MNX_LIN_RESIDENT");
+        return !(e && e[0] == '0');
+    }();
+    return on;
 }
 
 // shared argument checks and launch of both entry points
@@ -289,6 +449,18 @@ int block_linear(const float* a, int64_t a_stride, int32_t nseg, const int64_t* 
     MNX_REQUIRE(blocks < (int64_t(1) << 31), "too many rows");
     const int nt = lin_tiles(N);
     const dim3 grid(unsigned(blocks), unsigned(ceil_div(N, nt * 32)));
+    if (!idx && p.K > 0 && p.K <= kLinResMaxK && lin_resident()) {
+        // weights resident in LDS: one workgroup per CU walks row tiles
+        const dim3 rgrid(unsigned(std::min<int64_t>(blocks, 256)), grid.y);
+        switch (nt) {
+            case 1: launch_res<1>(d, rgrid, stream, p); break;
+            case 2: launch_res<2>(d, rgrid, stream, p); break;
+            case 3: launch_res<3>(d, rgrid, stream, p); break;
+            default: launch_res<4>(d, rgrid, stream, p); break;
+        }
+        MNX_CHECK_LAUNCH();
+        return MNX_OK;
+    }
     if (idx) {
         switch (nt) {
             case 1: launch_nt<1, true>(d, grid, stream, p); break;
