@@ -558,6 +558,42 @@ int mnx_tp_weight_grad_batched_f32(int32_t config, int32_t C, const float* x, co
                                    float* grad_h, mnx_stream_t stream);
 
 /* ------------------------------------------------------------------------ */
+/* Channelwise tensor product + scatter for irreps outside the compiled      */
+/* configurations, driven by a path table (replaces the same cuet call,      */
+/* cuet.ChannelWiseTensorProduct(irreps_in1, irreps_sh, irreps_out,          */
+/* layout=ir_mul, shared_weights=False, internal_weights=False) with         */
+/* indices_1 / indices_out / size_out, src/molrep/interaction/               */
+/* tensor_product.py:72-79,104-111, for any irreps with l <= 3: a            */
+/* multiplicity per input block, any parities, several blocks of one l).     */
+/*                                                                           */
+/* table (host memory, int32): [P, NX, NY, NO, NW] followed by P records     */
+/* [triple, xoff, yoff, ooff, woff, mul], with triple = mnx_tp_any_triple    */
+/* (l1, l2, l3) and the offsets in floats within a row of x [N][NX],         */
+/* Y [E][NY], out [N][NO] and w [E][NW]:                                     */
+/*   out[r][ooff + m3*mul + c] += w[e][woff + c] * sum_{m1,m2}                */
+/*       sqrt(2 l3 + 1) C[m1][m2][m3] x[s][xoff + m1*mul + c] Y[e][yoff + m2] */
+/* summed over the edges e = (s -> r).  The output blocks must tile the      */
+/* output row and the weight segments the weight row.  P <= 64, at most      */
+/* 65535 chunks of 64 channels over all paths.                               */
+/* ------------------------------------------------------------------------ */
+#define MNX_TP_ANY_MAX_PATHS 64
+/* Index of the coupling triple (l1, l2 -> l3), l <= 3, or -1. */
+int mnx_tp_any_triple(int32_t l1, int32_t l2, int32_t l3);
+/* out [N][NO] is overwritten. */
+int mnx_tp_any_fwd_f32(const int32_t* table, int32_t table_len, const float* x, const float* Y,
+                       const float* w, const int32_t* row_ptr, const int32_t* perm,
+                       const int32_t* senders_sorted, int64_t num_nodes, int64_t num_edges,
+                       float* out, mnx_stream_t stream);
+/* Gradients of <grad_out, out>: grad_x [N][NX] and grad_Y [E][NY] accumulated
+ * with atomics (zeroed by the caller), grad_w [E][NW] overwritten; any may be
+ * NULL. */
+int mnx_tp_any_bwd_f32(const int32_t* table, int32_t table_len, const float* x, const float* Y,
+                       const float* w, const float* grad_out, const int32_t* row_ptr,
+                       const int32_t* perm, const int32_t* senders_sorted, int64_t num_nodes,
+                       int64_t num_edges, float* grad_x, float* grad_Y, float* grad_w,
+                       mnx_stream_t stream);
+
+/* ------------------------------------------------------------------------ */
 /* Per-edge channelwise tensor product with shared weights, no scatter: the  */
 /* layer product of Allegro (src/molzoo/allegro.py:352-359, applied at       */
 /* :457-458 to the scaled edge features and the aggregated harmonics of each */

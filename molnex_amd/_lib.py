@@ -47,6 +47,9 @@ SIGNATURES = {
     "mnx_tp_bwd_f32": (C.c_int, [c_i32, c_i32, vp, vp, vp, vp, vp, vp, vp, c_i64, c_i64, vp, vp, vp, vp, c_sz, vp]),
     "mnx_tp_bwd_sender_f32": (C.c_int, [c_i32, c_i32, vp, vp, vp, vp, vp, vp, vp, c_i64, c_i64, vp, vp, vp, vp]),
     "mnx_tp_fwd_rows_f32": (C.c_int, [c_i32, c_i32, vp, vp, vp, vp, vp, vp, vp, c_i64, c_i64, vp, vp]),
+    "mnx_tp_any_triple": (C.c_int, [c_i32, c_i32, c_i32]),
+    "mnx_tp_any_fwd_f32": (C.c_int, [vp, c_i32, vp, vp, vp, vp, vp, vp, c_i64, c_i64, vp, vp]),
+    "mnx_tp_any_bwd_f32": (C.c_int, [vp, c_i32, vp, vp, vp, vp, vp, vp, vp, c_i64, c_i64, vp, vp, vp, vp]),
     "mnx_tp_bwd_rows_f32": (C.c_int, [c_i32, c_i32, vp, vp, vp, vp, vp, vp, vp, vp, c_i64, c_i64, vp, vp, vp, vp,
                                       c_sz, vp]),
     "mnx_tp_bwd_sender_rows_f32": (C.c_int, [c_i32, c_i32, vp, vp, vp, vp, vp, vp, vp, vp, c_i64, c_i64, vp, vp,

@@ -36,7 +36,7 @@ EXTRA = {
     # bit-exact reference geometry: no fused multiply-add contraction
     "nlist.hip": ["-ffp-contract=off"],
 }
-SOURCES = ["errors.cpp", "nlist.hip", "csr.hip", "sh.hip", "tp.hip", "pme.hip", "symcon.hip", "radial.hip", "edges.hip", "linear.hip", "edge_weights.hip", "edge_tp.hip", "segment.hip", "tp_gh.hip", "embed.hip", "pairs.hip"]
+SOURCES = ["errors.cpp", "nlist.hip", "csr.hip", "sh.hip", "tp.hip", "pme.hip", "symcon.hip", "radial.hip", "edges.hip", "linear.hip", "edge_weights.hip", "edge_tp.hip", "segment.hip", "tp_gh.hip", "embed.hip", "pairs.hip", "tp_any.hip"]
 
 
 def _compile(src: str) -> str:
@@ -53,11 +53,12 @@ def _compile(src: str) -> str:
 
 def build(verbose: bool = True) -> str:
     sys.path.insert(0, os.path.dirname(PKG))
-    from molnex_amd.csrc import gen_edge_tp, gen_sc, gen_tp
+    from molnex_amd.csrc import gen_edge_tp, gen_sc, gen_tp, gen_tp_any
 
     gen_tp.main()
     gen_sc.main()
     gen_edge_tp.main()
+    gen_tp_any.main()
     os.makedirs(BUILD, exist_ok=True)
     os.makedirs(LIBDIR, exist_ok=True)
     with cf.ThreadPoolExecutor(max_workers=min(8, len(SOURCES))) as ex:

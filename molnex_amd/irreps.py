@@ -207,13 +207,69 @@ def _sphere_quadrature():
 
 
 @lru_cache(maxsize=None)
+def _so3_quadrature():
+    """Rotations and weights (summing to 1) integrating polynomials of degree <= 9 in the entries
+    of R over SO(3) with the Haar measure: R = Rz(a) Ry(b) Rz(c), a and c on uniform 20-point
+    grids (exact for trigonometric degree < 20), b by 24-point Gauss-Legendre on [0, pi] with the
+    sin(b) density (an entire integrand of trigonometric degree <= 10: error at round-off)."""
+    n = 20
+    ang = 2 * np.pi * np.arange(n) / n
+    t, wt = np.polynomial.legendre.leggauss(24)
+    b = 0.5 * np.pi * (t + 1)
+    wb = wt * 0.25 * np.pi * np.sin(b)  # sums to 1 over [0, pi]
+    A, B, Cg = (g.ravel() for g in np.meshgrid(ang, b, ang, indexing="ij"))
+    W = np.repeat(wb[None, :, None], n, 0).repeat(n, 2).ravel() / (n * n)
+
+    def rz(a):
+        c, s = np.cos(a), np.sin(a)
+        o, z = np.ones_like(a), np.zeros_like(a)
+        return np.stack([np.stack([c, -s, z], -1), np.stack([s, c, z], -1), np.stack([z, z, o], -1)], -2)
+
+    def ry(a):
+        c, s = np.cos(a), np.sin(a)
+        o, z = np.ones_like(a), np.zeros_like(a)
+        return np.stack([np.stack([c, z, s], -1), np.stack([z, o, z], -1), np.stack([-s, z, c], -1)], -2)
+
+    return rz(A) @ ry(B) @ rz(Cg), W
+
+
+# probe directions of the odd-triple construction (any three non-coplanar unit vectors)
+_ODD_PROBES = (np.array([0.3, -0.5, 0.8]), np.array([-0.7, 0.2, 0.4]), np.array([0.1, 0.9, -0.3]))
+
+
+def _odd_coupling(l1: int, l2: int, l3: int) -> np.ndarray:
+    """Invariant tensor of a triple with odd ``l1 + l2 + l3`` (where the Gaunt integral vanishes,
+    e.g. the cross product of 1 x 1 -> 1): the Haar average of ``Y1(R u) Y2(R v) Y3(R w)`` over
+    SO(3) for three fixed directions, i.e. the projection of ``Y1(u) Y2(v) Y3(w)`` onto the
+    one-dimensional invariant subspace, rescaled to unit norm, with the sign that makes its first
+    entry (C order) above 1e-9 x max positive."""
+    R, W = _so3_quadrature()
+    u, v, w = (d / np.linalg.norm(d) for d in _ODD_PROBES)
+    g = np.einsum("k,ka,kb,kc->abc", W, sh_block(l1, R @ u), sh_block(l2, R @ v), sh_block(l3, R @ w))
+    nrm = np.linalg.norm(g)
+    if nrm < 1e-8:
+        raise RuntimeError(f"no invariant found for ({l1}, {l2}, {l3})")
+    g /= nrm
+    g[np.abs(g) < 1e-13] = 0.0
+    flat = g.ravel()
+    first = flat[np.flatnonzero(np.abs(flat) > 1e-9 * np.abs(flat).max())[0]]
+    return g if first > 0 else -g
+
+
+@lru_cache(maxsize=None)
 def coupling(l1: int, l2: int, l3: int) -> np.ndarray:
-    """Unit-norm real coupling tensor ``(2l1+1, 2l2+1, 2l3+1)``; zero if forbidden."""
+    """Unit-norm real coupling tensor ``(2l1+1, 2l2+1, 2l3+1)``; zero if forbidden.
+
+    Even ``l1 + l2 + l3``: the normalised Gaunt integral (sign: ``Σ G Y1(u) Y2(u) Y3(u) > 0``).
+    Odd sums (paths such as ``1o x 1o -> 1e`` that appear with non-natural parities): the
+    invariant of ``_odd_coupling`` (first non-zero entry positive)."""
     shape = (2 * l1 + 1, 2 * l2 + 1, 2 * l3 + 1)
-    if not (abs(l1 - l2) <= l3 <= l1 + l2) or (l1 + l2 + l3) % 2:
-        # odd l1+l2+l3 triples exist for O3 (e.g. 1o x 1o -> 1e) but the Gaunt
-        # integral vanishes there; none of the supported paths needs them.
+    if not (abs(l1 - l2) <= l3 <= l1 + l2):
         return np.zeros(shape)
+    if (l1 + l2 + l3) % 2:
+        g = _odd_coupling(l1, l2, l3)
+        g.setflags(write=False)
+        return g
     pts, w = _sphere_quadrature()
     y1, y2, y3 = sh_block(l1, pts), sh_block(l2, pts), sh_block(l3, pts)
     g = np.einsum("q,qa,qb,qc->abc", w, y1, y2, y3)
@@ -243,8 +299,10 @@ class ChannelwiseTPDescriptor:
     """Paths of ``x (mul x ir1) ⊗ Y (1 x ir2) -> mul x ir3`` with ir3 in a filter.
 
     Paths are enumerated in the order (block of in1, block of in2, l3 ascending);
-    the per-edge weight tensor is ``[path][channel]`` in that order.  Output
-    blocks are the path outputs stably sorted by irrep (one block per path).
+    the per-edge weight tensor holds one segment of ``mul`` channels per path in
+    that order (``[path][channel]`` for a uniform multiplicity).  Output blocks
+    are the path outputs stably sorted by irrep (one block per path, with the
+    multiplicity of the path's in1 block).
     Mirrors the construction used by ``ConvTP`` (``tensor_product.py:72-79``).
     """
 
@@ -253,9 +311,9 @@ class ChannelwiseTPDescriptor:
         self.irreps_in2 = Irreps(irreps_in2)
         filt = {b.ir for b in Irreps(irreps_out_filter)}
         muls = {b.mul for b in self.irreps_in1}
-        if len(muls) != 1:
-            raise ValueError("channelwise tensor product needs a uniform multiplicity in irreps_in1")
-        self.mul = muls.pop()
+        # the common multiplicity of irreps_in1, None when the blocks differ (each path then
+        # carries its input block's multiplicity)
+        self.mul = muls.pop() if len(muls) == 1 else None
         for b in self.irreps_in2:
             if b.mul != 1:
                 raise ValueError("irreps_in2 must have multiplicity 1 per block")
@@ -269,8 +327,8 @@ class ChannelwiseTPDescriptor:
         order = sorted(range(len(raw)), key=lambda k: (Irrep(raw[k][4], raw[k][5]).sort_key(), k))
         out_block_of = {k: pos for pos, k in enumerate(order)}
         self.paths = [TPPath(*r, out_block=out_block_of[k]) for k, r in enumerate(raw)]
-        self.irreps_out = Irreps([(self.mul, Irrep(raw[k][4], raw[k][5])) for k in order])
-        self.weight_numel = len(self.paths) * self.mul
+        self.irreps_out = Irreps([(self.irreps_in1[raw[k][0]].mul, Irrep(raw[k][4], raw[k][5])) for k in order])
+        self.weight_numel = sum(self.irreps_in1[r[0]].mul for r in raw)
         for p in self.paths:
             if max(p.l1, p.l2, p.l3) > L_MAX_SUPPORTED:
                 raise ValueError(f"l > {L_MAX_SUPPORTED} is not supported")

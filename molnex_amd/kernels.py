@@ -13,6 +13,7 @@ Ops
 ``molix::spherical_harmonics``  real SH l <= 3 (``cuet.SphericalHarmonics``)
 ``molix::edge_csr``             receiver CSR of an (E, 2) edge list
 ``molix::tp_scatter``           channelwise TP + scatter-sum (``cuet.ChannelWiseTensorProduct``)
+``molix::tp_any``               the same for any irreps (l <= 3), driven by a path table
 ``molix::edge_tp``              per-edge channelwise TP with shared weights, no scatter (Allegro's layer product)
 ``molix::radial_hidden``        fused hidden stack of the radial weight MLP (gradient w.r.t. its input)
 ``molix::edge_weights``         output layer of the radial weight MLP (per-edge TP weights), near-fp32 split-fp16 MFMA
@@ -428,6 +429,116 @@ def _tp_backward(ctx, grad_out):
 
 
 tp_scatter.register_autograd(_tp_backward, setup_context=_tp_setup)
+
+
+def tp_any_table(desc) -> list[int]:
+    """Path table of ``molix::tp_any`` for a ``ChannelwiseTPDescriptor``: ``[P, NX, NY, NO, NW]``
+    then per path ``[triple, x offset, Y offset, output offset, weight offset, multiplicity]`` (offsets
+    in floats within a row; ir_mul blocks; weight segments in path order; output blocks in the
+    descriptor's sorted order)."""
+    lib = _lib.load()
+    in1, in2, out = desc.irreps_in1, desc.irreps_in2, desc.irreps_out
+    off1, off2, off3 = in1.offsets(), in2.offsets(), out.offsets()
+    table = [desc.num_paths, in1.dim, in2.dim, out.dim, desc.weight_numel]
+    woff = 0
+    for p in desc.paths:
+        t = int(lib.mnx_tp_any_triple(p.l1, p.l2, p.l3))
+        if t < 0:
+            raise ValueError(f"tp_any: no coupling kernel for ({p.l1}, {p.l2} -> {p.l3})")
+        mul = in1[p.i1].mul
+        table += [t, off1[p.i1], off2[p.i2], off3[p.out_block], woff, mul]
+        woff += mul
+    return table
+
+
+def _any_dims(table: list[int]) -> tuple[int, int, int, int]:
+    return table[1], table[2], table[3], table[4]
+
+
+def _any_ctable(table: list[int]):
+    return (C.c_int32 * len(table))(*table), len(table)
+
+
+@torch.library.custom_op("molix::tp_any", mutates_args=(), device_types="cuda")
+def tp_any(x: Tensor, Y: Tensor, w: Tensor, row_ptr: Tensor, perm: Tensor, senders: Tensor,
+           table: list[int]) -> Tensor:
+    """``out[r] = sum_{e -> r} TP(x[send(e)], Y[e]; w[e])`` for any irreps with l <= 3, driven by the
+    path table of ``tp_any_table`` (the compiled ``tp_scatter`` configurations cover uniform
+    multiplicity, natural parity and one block per l)."""
+    _require_gpu("tp_any", x, Y, w, row_ptr)
+    nx, ny, no, nw = _any_dims(table)
+    N = row_ptr.shape[0] - 1
+    E = Y.shape[0]
+    if no == 0:  # no path survives the output filter
+        return torch.zeros((N, 0), dtype=torch.float32, device=x.device)
+    xs = _f32_rows(x, nx, "x")
+    Ys = _f32_rows(Y, ny, "Y")
+    ws_ = _f32_rows(w, nw, "w")
+    if xs.shape[0] != N or perm.shape[0] != E or senders.shape[0] != E or ws_.shape[0] != E:
+        raise ValueError("tp_any: inconsistent sizes of x / Y / w / CSR")
+    out = torch.empty((N, no), dtype=torch.float32, device=xs.device)
+    tb, n = _any_ctable(table)
+    check(_lib.load().mnx_tp_any_fwd_f32(tb, n, ptr(xs), ptr(Ys), ptr(ws_), ptr(row_ptr), ptr(perm), ptr(senders),
+                                         N, E, ptr(out), _stream(xs)), "tp_any")
+    return out
+
+
+@tp_any.register_fake
+def _(x, Y, w, row_ptr, perm, senders, table):
+    return x.new_empty((row_ptr.shape[0] - 1, table[3]))
+
+
+@torch.library.custom_op("molix::tp_any_backward", mutates_args=(), device_types="cuda")
+def tp_any_backward(grad_out: Tensor, x: Tensor, Y: Tensor, w: Tensor, row_ptr: Tensor, perm: Tensor,
+                    senders: Tensor, table: list[int], need_x: bool, need_Y: bool,
+                    need_w: bool) -> tuple[Tensor, Tensor, Tensor]:
+    """Gradients of ``<grad_out, tp_any(...)>`` w.r.t. x and Y (fp32 atomics) and w (empty when not
+    needed)."""
+    nx, ny, no, nw = _any_dims(table)
+    N = row_ptr.shape[0] - 1
+    E = Y.shape[0]
+    if no == 0:
+        return (torch.zeros_like(x) if need_x else x.new_empty(0), torch.zeros_like(Y) if need_Y else Y.new_empty(0),
+                w.new_zeros(E, 0) if need_w else w.new_empty(0))
+    xs = _f32_rows(x, nx, "x")
+    Ys = _f32_rows(Y, ny, "Y")
+    wss = _f32_rows(w, nw, "w")
+    go = _f32_rows(grad_out, no, "grad_out")
+    if (xs.shape[0] != N or go.shape[0] != N or wss.shape[0] != E or perm.shape[0] != E
+            or senders.shape[0] != E):
+        raise ValueError("tp_any_backward: inconsistent sizes of x / grad_out / w / CSR")
+    gx = torch.zeros_like(xs) if need_x else xs.new_empty(0)
+    gY = torch.zeros_like(Ys) if need_Y else Ys.new_empty(0)
+    gw = wss.new_empty(E, nw) if need_w else wss.new_empty(0)
+    tb, n = _any_ctable(table)
+    check(_lib.load().mnx_tp_any_bwd_f32(tb, n, ptr(xs), ptr(Ys), ptr(wss), ptr(go), ptr(row_ptr), ptr(perm),
+                                         ptr(senders), N, E, ptr(gx) if need_x else None,
+                                         ptr(gY) if need_Y else None, ptr(gw) if need_w else None, _stream(xs)),
+          "tp_any backward")
+    return gx, gY, gw
+
+
+@tp_any_backward.register_fake
+def _(grad_out, x, Y, w, row_ptr, perm, senders, table, need_x, need_Y, need_w):
+    return (torch.empty_like(x) if need_x else x.new_empty(0), torch.empty_like(Y) if need_Y else Y.new_empty(0),
+            w.new_empty(Y.shape[0], w.shape[1]) if need_w else w.new_empty(0))
+
+
+def _tp_any_setup(ctx, inputs, output):
+    x, Y, w, row_ptr, perm, senders, table = inputs
+    ctx.save_for_backward(x, Y, w, row_ptr, perm, senders)
+    ctx.table = table
+
+
+def _tp_any_bwd(ctx, grad_out):
+    x, Y, w, row_ptr, perm, senders = ctx.saved_tensors
+    nx, nY, nw = ctx.needs_input_grad[:3]
+    gx, gY, gw = tp_any_backward(grad_out.contiguous(), x, Y, w, row_ptr, perm, senders, ctx.table, nx, nY, nw)
+    return (gx.reshape(x.shape) if nx else None, gY.reshape(Y.shape) if nY else None,
+            gw.reshape(w.shape) if nw else None, None, None, None, None)
+
+
+tp_any.register_autograd(_tp_any_bwd, setup_context=_tp_any_setup)
 
 
 def edge_tp_supported(config: int, channels: int) -> bool:

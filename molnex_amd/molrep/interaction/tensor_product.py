@@ -26,14 +26,12 @@ class ConvTPSpec(BaseModel):
     sh_irreps: str
 
 
-def _natural_ls(irreps: Irreps, what: str) -> list[int]:
-    ls = []
-    for b in irreps:
-        if b.ir.p != (-1) ** b.ir.l:
-            raise ValueError(f"{what}: only natural-parity irreps (0e, 1o, 2e, 3o) are supported, got {b.ir}")
-        ls.append(b.ir.l)
-    if ls != sorted(set(ls)):
-        raise ValueError(f"{what}: irreps must be in ascending l with one block per l, got {irreps}")
+def _compiled_ls(irreps: Irreps) -> list[int] | None:
+    """The l's of ``irreps`` when it has the form of the compiled configurations (natural parity,
+    ascending l, one block per l), else None."""
+    ls = [b.ir.l for b in irreps]
+    if any(b.ir.p != (-1) ** b.ir.l for b in irreps) or ls != sorted(set(ls)):
+        return None
     return ls
 
 
@@ -130,22 +128,30 @@ class ChannelWiseTensorProduct(nn.Module):
         self.irreps_out = self.descriptor.irreps_out
         self.weight_numel = self.descriptor.weight_numel
         self.channels = self.descriptor.mul
-        in_ls = _natural_ls(self.irreps_in1, "irreps_in1")
-        sh_ls = _natural_ls(self.irreps_in2, "irreps_in2")
-        out_ls = sorted({b.ir.l for b in Irreps(irreps_out_filter)
-                         if b.ir.p == (-1) ** b.ir.l and any(p.l3 == b.ir.l for p in self.descriptor.paths)})
-        self.config_id = K.tp_config_id(in_ls, sh_ls, out_ls)
-        if self.config_id < 0:
-            raise ValueError(f"no compiled tensor-product kernel for in l={in_ls}, sh l={sh_ls}, out l={out_ls}")
-        num_paths, nx, ny, no = K.tp_config_info(self.config_id)
-        if num_paths != self.descriptor.num_paths or no * self.channels != self.irreps_out.dim:
-            raise RuntimeError("compiled tensor-product configuration does not match the path descriptor")
+        # the straight-line kernels compiled per configuration (uniform multiplicity, natural parity,
+        # one block per l), else the table-driven kernels of molix::tp_any (any irreps, l <= 3)
+        self.config_id = -1
+        self.any_table = None
+        in_ls, sh_ls = _compiled_ls(self.irreps_in1), _compiled_ls(self.irreps_in2)
+        out_irs = {b.ir for b in self.irreps_out}
+        if self.channels is not None and in_ls is not None and sh_ls is not None and all(
+                ir.p == (-1) ** ir.l for ir in out_irs):
+            out_ls = sorted({ir.l for ir in out_irs})
+            self.config_id = K.tp_config_id(in_ls, sh_ls, out_ls) if out_ls else -1
+        if self.config_id >= 0:
+            num_paths, nx, ny, no = K.tp_config_info(self.config_id)
+            if num_paths != self.descriptor.num_paths or no * self.channels != self.irreps_out.dim:
+                raise RuntimeError("compiled tensor-product configuration does not match the path descriptor")
+        else:
+            self.any_table = K.tp_any_table(self.descriptor)
 
     def forward(self, x, y, weight, indices_1=None, indices_out=None, size_out=None):
         num_nodes = int(size_out) if size_out is not None else x.shape[0]
         return self.apply_graph(x, y, weight, edge_graph_from_indices(indices_1, indices_out, num_nodes))
 
     def apply_graph(self, x, y, weight, g: EdgeGraph):
+        if self.config_id < 0:
+            return torch.ops.molix.tp_any(x, y, weight, g.row_ptr, g.perm, g.senders, self.any_table)
         extra = g.sender_csr() if config.deterministic else ()
         return torch.ops.molix.tp_scatter(x, y, weight, g.row_ptr, g.perm, g.senders, self.config_id, self.channels,
                                           *extra)
@@ -179,6 +185,8 @@ class ConvTP(nn.Module):
         whose backward forms the per-edge weight gradient in registers (``molix::tp_weight_grad``)."""
         last = radial_mlp.mlp[-1]
         x = node_features
+        if self.cue_tp.config_id < 0:  # table-driven product: no fused forms
+            return self.forward(x, edge_angular, edge_index, radial_mlp(edge_feats))
         if (config.paired_radial and not self.training and x.is_cuda and x.dtype == torch.float32
                 and edge_feats.dim() == 2 and not config.deterministic and not torch.compiler.is_compiling()
                 and not any(p.requires_grad for p in radial_mlp.parameters())

@@ -241,6 +241,46 @@ def _tp2_bwd(ctx, ggx, ggY, ggw):
 K.tp_scatter_backward.register_autograd(_tp2_bwd, setup_context=_tp2_setup)
 
 
+def _tpa2_setup(ctx, inputs, output):
+    g, x, Y, w, row_ptr, perm, senders, table, need_x, need_Y, need_w = inputs
+    ctx.save_for_backward(g, x, Y, w, row_ptr, perm, senders)
+    ctx.table = table
+    ctx.need = (need_x, need_Y, need_w)
+
+
+def _tpa2_bwd(ctx, ggx, ggY, ggw):
+    """The table-driven product is trilinear too: the same three forward and three backward terms."""
+    g, x, Y, w, row_ptr, perm, senders = ctx.saved_tensors
+    csr, tb = (row_ptr, perm, senders), ctx.table
+    live = lambda t, need: t if (need and t is not None and t.numel() > 0) else None  # noqa: E731
+    ggx, ggY, ggw = live(ggx, ctx.need[0]), live(ggY, ctx.need[1]), live(ggw, ctx.need[2])
+    want_g, want_x, want_Y, want_w = ctx.needs_input_grad[:4]
+    dg = dx = dY = dw = None
+    if want_g:
+        for a, b, c, seed in ((ggx, Y, w, ggx), (x, ggY, w, ggY), (x, Y, ggw, ggw)):
+            if seed is not None:
+                t = K.tp_any(a, b, c, *csr, tb)
+                dg = t if dg is None else dg + t
+
+    def acc(a, b):
+        return b if a is None else (a if b is None else a + b)
+
+    if ggx is not None and (want_Y or want_w):
+        _, bY, bw = K.tp_any_backward(g, ggx, Y, w, *csr, tb, False, want_Y, want_w)
+        dY, dw = acc(dY, bY if want_Y else None), acc(dw, bw if want_w else None)
+    if ggY is not None and (want_x or want_w):
+        bx, _, bw = K.tp_any_backward(g, x, ggY, w, *csr, tb, want_x, False, want_w)
+        dx, dw = acc(dx, bx if want_x else None), acc(dw, bw if want_w else None)
+    if ggw is not None and (want_x or want_Y):
+        bx, bY, _ = K.tp_any_backward(g, x, Y, ggw, *csr, tb, want_x, want_Y, False)
+        dx, dY = acc(dx, bx if want_x else None), acc(dY, bY if want_Y else None)
+    shape = lambda t, ref: None if t is None else t.reshape(ref.shape)  # noqa: E731
+    return (shape(dg, g), shape(dx, x), shape(dY, Y), shape(dw, w)) + (None,) * 7
+
+
+K.tp_any_backward.register_autograd(_tpa2_bwd, setup_context=_tpa2_setup)
+
+
 # per-edge product with shared weights (Allegro): out = TP(s x, Y; w) is multilinear in
 # (x, Y, w, s), so each second-order term is the forward or the backward with one factor replaced
 # by its incoming cotangent (as for the scatter product above)

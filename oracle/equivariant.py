@@ -35,7 +35,8 @@ def scatter_add(index, values, num):
     """out[index[e]] += values[e] (fp64, via a sparse incidence matrix)."""
     E = values.shape[0]
     inc = sp.csr_matrix((np.ones(E), (np.asarray(index), np.arange(E))), shape=(num, E))
-    return (inc @ values.reshape(E, -1)).reshape((num,) + values.shape[1:])
+    F = int(np.prod(values.shape[1:], dtype=np.int64))
+    return (inc @ values.reshape(E, F)).reshape((num,) + values.shape[1:])
 
 
 def _irrep_list(ls_or_str):
@@ -112,7 +113,9 @@ def wigner_d(l: int, R: np.ndarray) -> np.ndarray:
 
 @lru_cache(maxsize=None)
 def coupling(l1: int, l2: int, l3: int) -> np.ndarray:
-    """Unit-norm invariant tensor of l1 (x) l2 (x) l3; sign: sum C Y1(u)Y2(u)Y3(u) > 0."""
+    """Unit-norm invariant tensor of l1 (x) l2 (x) l3.  Sign: sum C Y1(u)Y2(u)Y3(u) > 0 for even
+    l1 + l2 + l3; for odd sums (where that sum vanishes identically) the first entry in C order
+    above 1e-9 x max is positive."""
     rng = np.random.default_rng(11)
     blocks = []
     for _ in range(3):
@@ -123,9 +126,13 @@ def coupling(l1: int, l2: int, l3: int) -> np.ndarray:
     _, s, vt = np.linalg.svd(M)
     c = vt[-1].reshape(2 * l1 + 1, 2 * l2 + 1, 2 * l3 + 1)
     assert s[-1] < 1e-8 and (len(s) < 2 or s[-2] > 1e-3), "invariant space is not one-dimensional"
+    c = c / np.linalg.norm(c)
+    if (l1 + l2 + l3) % 2:
+        flat = c.ravel()
+        return c * np.sign(flat[np.flatnonzero(np.abs(flat) > 1e-9 * np.abs(flat).max())[0]])
     u = np.array([0.3, -0.5, 0.8])
     val = np.einsum("abc,a,b,c->", c, real_sh(l1, u), real_sh(l2, u), real_sh(l3, u))
-    return c / np.linalg.norm(c) * np.sign(val)
+    return c * np.sign(val)
 
 
 def tp_paths(irreps_in1, irreps_in2, irreps_filter):
@@ -209,6 +216,66 @@ class ChannelwiseTP:
             q = np.matmul(xe * we, gr.transpose(0, 2, 1))  # (E, m1, m3) = sum_C x w g
             gY[:, s2] += np.einsum("abc,eac->eb", cf, q)
         return gx.reshape(x.shape), gY, gw.reshape(E, -1)
+
+
+class ChannelwiseTPMul:
+    """The channelwise product + scatter for any irreps: a multiplicity per block of in1 (path k of
+    in1 block b1 with multiplicity u takes the weights w[e, woff_k : woff_k + u] and writes an output
+    block of (2 l3 + 1) x u in ir_mul layout), any parities (paths 1o x 1o -> 1e included), several
+    blocks of one l.  Paths and the output order are those of ``tp_paths``; weight segments follow
+    the path order.  Restated per path with dense contractions, independently of the product's
+    path tables."""
+
+    def __init__(self, irreps_in1, irreps_in2, irreps_filter):
+        self.in1 = _irrep_list(irreps_in1)
+        self.in2 = _irrep_list(irreps_in2)
+        assert all(m == 1 for m, _, _ in self.in2)
+        self.paths, order = tp_paths(irreps_in1, irreps_in2, irreps_filter)
+        self.muls = [self.in1[p[0]][0] for p in self.paths]
+        self.off1 = _offsets([m * (2 * l + 1) for m, l, _ in self.in1])
+        self.off2 = _offsets([2 * l + 1 for _, l, _ in self.in2])
+        self.off3 = _offsets([(2 * self.paths[k][4] + 1) * self.muls[k] for k in order])
+        self.out_pos = {k: pos for pos, k in enumerate(order)}
+        self.offw = _offsets(self.muls)
+        self.nx, self.ny, self.no, self.nw = self.off1[-1], self.off2[-1], self.off3[-1], self.offw[-1]
+
+    def _parts(self, k, x, Y, w, N, E):
+        b1, b2, l1, l2, l3, _ = self.paths[k]
+        u = self.muls[k]
+        pos = self.out_pos[k]
+        xb = x[:, self.off1[b1]:self.off1[b1 + 1]].reshape(N, 2 * l1 + 1, u)
+        wk = w[:, self.offw[k]:self.offw[k + 1]]
+        cf = math.sqrt(2 * l3 + 1) * coupling(l1, l2, l3)
+        M = np.einsum("abc,eb->eca", cf, Y[:, self.off2[b2]:self.off2[b2 + 1]])  # (E, m3, m1)
+        return xb, wk, cf, M, slice(self.off3[pos], self.off3[pos + 1]), (2 * l3 + 1, u)
+
+    def forward(self, x, Y, w, edge_index, num_nodes):
+        x, Y, w = (np.asarray(a, np.float64) for a in (x, Y, w))
+        E = Y.shape[0]
+        s, r = edge_index[:, 0], edge_index[:, 1]
+        out = np.zeros((num_nodes, self.no))
+        for k in range(len(self.paths)):
+            xb, wk, _, M, s3, shp = self._parts(k, x, Y, w, x.shape[0], E)
+            msg = np.matmul(M, xb[s]) * wk[:, None, :]  # (E, m3, u)
+            out[:, s3] += scatter_add(r, msg, num_nodes).reshape(num_nodes, -1)
+        return out
+
+    def backward(self, x, Y, w, edge_index, grad_out):
+        x, Y, w, g = (np.asarray(a, np.float64) for a in (x, Y, w, grad_out))
+        N, E = x.shape[0], Y.shape[0]
+        s, r = edge_index[:, 0], edge_index[:, 1]
+        gx, gY, gw = np.zeros_like(x), np.zeros_like(Y), np.zeros_like(w)
+        for k in range(len(self.paths)):
+            b1, b2 = self.paths[k][:2]
+            xb, wk, cf, M, s3, shp = self._parts(k, x, Y, w, N, E)
+            gr = g[:, s3].reshape(-1, *shp)[r]  # (E, m3, u)
+            xe = xb[s]
+            uu = np.matmul(M.transpose(0, 2, 1), gr)  # (E, m1, u)
+            gw[:, self.offw[k]:self.offw[k + 1]] = (xe * uu).sum(1)
+            gx[:, self.off1[b1]:self.off1[b1 + 1]] += scatter_add(s, uu * wk[:, None, :], N).reshape(N, -1)
+            q = np.matmul(xe * wk[:, None, :], gr.transpose(0, 2, 1))  # (E, m1, m3)
+            gY[:, self.off2[b2]:self.off2[b2 + 1]] += np.einsum("abc,eac->eb", cf, q)
+        return gx, gY, gw
 
 
 def rotate_irreps(feat, R, irreps, channels, layout="ir_mul"):

@@ -53,6 +53,20 @@ def test_opcheck_tp_scatter():
     opcheck(ops.tp_scatter.default, (x, Y, w, row_ptr, perm, snd, cfg, C))
 
 
+def test_opcheck_tp_any():
+    from molnex_amd.irreps import ChannelwiseTPDescriptor
+
+    pos, box, ei, _, deltas = _graph()
+    N = pos.shape[0]
+    d = ChannelwiseTPDescriptor("8x0e + 4x1o + 4x1e", "0e + 1o", "0e + 0o + 1o + 1e")
+    table = K.tp_any_table(d)
+    row_ptr, perm, snd = ops.edge_csr(ei, N)
+    x = torch.randn(N, d.irreps_in1.dim, device=DEV, requires_grad=True)
+    Y = torch.randn(ei.shape[0], d.irreps_in2.dim, device=DEV, requires_grad=True)
+    w = torch.randn(ei.shape[0], d.weight_numel, device=DEV, requires_grad=True)
+    opcheck(ops.tp_any.default, (x, Y, w, row_ptr, perm, snd, table))
+
+
 def test_opcheck_pairs():
     """The undirected-pair ops: edge_reverse, tp_scatter with a weight-row map, the pair-summing
     output-layer backward, and radial_tp_pairs in pair and edge mode."""
