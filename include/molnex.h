@@ -594,6 +594,20 @@ int mnx_tp_any_bwd_f32(const int32_t* table, int32_t table_len, const float* x, 
                        mnx_stream_t stream);
 
 /* ------------------------------------------------------------------------ */
+/* C [M][N] = A^T B for tall operands A [K][M], B [K][N] (row strides lda,   */
+/* ldb >= the widths; K rows >> M, N): the weight gradients of the per-edge  */
+/* layers when training (dW = grad^T h over all edges of the radial MLP's    */
+/* output layer, src/molrep/interaction/radial_mlp.py:76-82, which torch's   */
+/* autograd computes as one GEMM over the edges), fp32-accurate on the bf16  */
+/* matrix cores, deterministic.  Workspace from                              */
+/* mnx_tall_tn_workspace_bytes (per-slab partial tiles); C is overwritten.   */
+/* ------------------------------------------------------------------------ */
+size_t mnx_tall_tn_workspace_bytes(int64_t K, int32_t M, int32_t N);
+int mnx_tall_tn_f32(const float* A, int64_t lda, const float* B, int64_t ldb, int64_t K, int32_t M,
+                    int32_t N, float* C, void* workspace, size_t workspace_bytes,
+                    mnx_stream_t stream);
+
+/* ------------------------------------------------------------------------ */
 /* Per-edge channelwise tensor product with shared weights, no scatter: the  */
 /* layer product of Allegro (src/molzoo/allegro.py:352-359, applied at       */
 /* :457-458 to the scaled edge features and the aggregated harmonics of each */

@@ -1131,8 +1131,6 @@ radial_hidden.register_autograd(_radial_bwd, setup_context=_radial_setup)
 # Radial weight MLP output layer (per-edge tensor-product weights)
 # ---------------------------------------------------------------------------
 
-_EW_ROWS = 1 << 18
-
 
 def edge_weights_supported(in_dim: int, out_dim: int) -> bool:
     """Whether ``molix::edge_weights`` (and its backward) take an in_dim -> out_dim Linear."""
@@ -1211,6 +1209,48 @@ def _(grad, weight):
     return grad.new_empty(grad.shape[0], weight.shape[1])
 
 
+def _rows_f32(t: Tensor, what: str) -> Tensor:
+    if t.dtype != torch.float32 or t.dim() != 2:
+        raise TypeError(f"{what} must be a 2-D float32 tensor")
+    return t if (t.stride(1) == 1 and t.stride(0) >= t.shape[1]) else t.contiguous()
+
+
+@torch.library.custom_op("molix::tall_tn", mutates_args=(), device_types="cuda")
+def tall_tn(a: Tensor, b: Tensor) -> Tensor:
+    """``a.T @ b`` for tall float32 ``a`` (K, M) and ``b`` (K, N), K >> M, N: a layer's weight
+    gradient summed over all edges, fp32-accurate on the bf16 matrix cores (split operands),
+    deterministic; rows may be strided."""
+    _require_gpu("tall_tn", a, b)
+    a2, b2 = _rows_f32(a, "a"), _rows_f32(b, "b")
+    if a2.shape[0] != b2.shape[0]:
+        raise ValueError(f"tall_tn: {a2.shape[0]} rows against {b2.shape[0]}")
+    K, M, N = a2.shape[0], a2.shape[1], b2.shape[1]
+    out = torch.empty((M, N), dtype=torch.float32, device=a2.device)
+    lib = _lib.load()
+    ws = _ws(lib.mnx_tall_tn_workspace_bytes(K, M, N), a2.device)
+    check(lib.mnx_tall_tn_f32(ptr(a2), a2.stride(0), ptr(b2), b2.stride(0), K, M, N, ptr(out), ptr(ws), ws.numel(),
+                              _stream(a2)), "tall_tn")
+    return out
+
+
+@tall_tn.register_fake
+def _(a, b):
+    return a.new_empty((a.shape[1], b.shape[1]))
+
+
+def _tall_setup(ctx, inputs, output):
+    ctx.save_for_backward(*inputs)
+
+
+def _tall_bwd(ctx, g):
+    a, b = ctx.saved_tensors
+    na, nb = ctx.needs_input_grad
+    return (b @ g.t() if na else None, a @ g if nb else None)
+
+
+tall_tn.register_autograd(_tall_bwd, setup_context=_tall_setup)
+
+
 def _ew_setup(ctx, inputs, output):
     h, weight = inputs[0], inputs[1]
     ctx.save_for_backward(h, weight)
@@ -1224,10 +1264,8 @@ def _ew_bwd(ctx, grad):
     grad = grad.contiguous()
     gh = edge_weights_backward(grad, weight) if need_h else None
     gw = None
-    if need_w:  # training: the (N, K) weight gradient as row-chunked hipBLASLt GEMMs
-        gw = torch.zeros_like(weight)
-        for i in range(0, h.shape[0], _EW_ROWS):
-            gw.addmm_(grad[i:i + _EW_ROWS].t(), h[i:i + _EW_ROWS])
+    if need_w:  # training: the (N, K) weight gradient summed over all rows
+        gw = tall_tn(grad, h)
     gb = grad.sum(0) if (need_b and ctx.has_bias) else None
     return (gh, gw, gb)[:len(ctx.needs_input_grad)]
 
@@ -1660,9 +1698,7 @@ def _rtpp_backward(ctx, g_out, g_w):
             gp = gp + g_w
         if need_W:
             hl = h if per_pair else h.index_select(0, lead)
-            gW = torch.zeros_like(weight)
-            for i in range(0, hl.shape[0], _EW_ROWS):
-                gW.addmm_(gp[i:i + _EW_ROWS].t(), hl[i:i + _EW_ROWS])
+            gW = tall_tn(gp, hl)
         gb = gp.sum(0) if need_b else None
     return gx, gY, gh, gW, gb, None, None, None, None, None, None, None, None
 

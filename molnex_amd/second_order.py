@@ -179,10 +179,8 @@ def _ew2_bwd(ctx, ggh):
     ng, nw = ctx.needs_input_grad[:2]
     dg = K.edge_weights(ggh.contiguous(), weight) if ng else None
     dw = None
-    if nw:  # d/dW <ggh, grad W> = grad^T ggh, row-chunked
-        dw = torch.zeros_like(weight)
-        for i in range(0, grad.shape[0], K._EW_ROWS):
-            dw.addmm_(grad[i:i + K._EW_ROWS].t(), ggh[i:i + K._EW_ROWS])
+    if nw:  # d/dW <ggh, grad W> = grad^T ggh over all rows
+        dw = K.tall_tn(grad, ggh)
     return dg, dw
 
 

@@ -1,0 +1,78 @@
+"""``molix::tall_tn``: a.T @ b for tall operands (the per-edge layers' weight gradients when
+training) against float64 torch, fp32-accurate: norm-wise relative error and max-abs / RMS of the
+reference <= 1e-5, and the norm-wise error no worse than twice torch's own fp32 GEMM's on the same
+inputs (or 1e-6); shapes with ragged tiles, strided rows, no rows; its autograd and opcheck."""
+
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _close(got, ref, what, tol=1e-5, mtol=1e-5):
+    got, ref = got.detach().double().cpu(), ref.detach().double().cpu()
+    n = ref.norm()
+    if n == 0:
+        assert got.abs().max() == 0, what
+        return
+    rms = n / ref.numel() ** 0.5
+    err, mx = float((got - ref).norm() / n), float((got - ref).abs().max())
+    assert err <= tol and mx <= mtol * rms, f"{what}: rel {err:.2e}, max-abs {mx:.2e} (rms {float(rms):.2e})"
+    return err
+
+
+@pytest.fixture(scope="module")
+def K():
+    from molnex_amd import kernels
+
+    return kernels
+
+
+@pytest.mark.parametrize("rows,M,N", [(1, 1, 1), (15, 31, 33), (17, 64, 128), (1000, 1280, 128), (4096, 300, 70),
+                                      (300_000, 512, 128), (2_607_384, 1280, 128)])
+def test_tall_tn_vs_float64(K, rows, M, N):
+    print(f"tall_tn {rows} x {M} x {N}", flush=True)
+    g = torch.Generator(device=DEV).manual_seed(rows + M)
+    a = torch.randn(rows, M, device=DEV, generator=g)
+    b = torch.randn(rows, N, device=DEV, generator=g)
+    # a dynamic range across rows (edge weights near the cutoff are tiny): 2^±30, or 2^±8 at the full
+    # 2.6 M rows, where fp32 accumulation itself (torch's GEMM included) reaches ~1e-5 at 2^±30
+    span = 30 if rows <= 300_000 else 8
+    a *= torch.exp2(torch.randint(-span, span + 1, (rows, 1), device=DEV, generator=g).float())
+    ref = a.double().t() @ b.double()
+    got = K.tall_tn(a, b)
+    mm = a.t() @ b
+    torch_err = float((mm.double() - ref).norm() / ref.norm())
+    torch_mx = float((mm.double() - ref).abs().max())
+    print(f"  rel error {float((got.double() - ref).norm() / ref.norm()):.2e}, torch fp32 {torch_err:.2e}", flush=True)
+    if rows <= 300_000:
+        err = _close(got, ref, f"{rows}x{M}x{N}")
+    else:  # 2.6 M random-sign rows: the fp32 sum's own rounding is near 1e-5 of the result's RMS
+        err = float((got.double() - ref).norm() / ref.norm())
+        assert err <= 1e-5 and float((got.double() - ref).abs().max()) <= 2 * torch_mx
+    assert err <= max(2 * torch_err, 1e-6), (err, torch_err)
+
+
+def test_tall_tn_strided_rows_and_empty(K):
+    g = torch.Generator(device=DEV).manual_seed(3)
+    big = torch.randn(5000, 200, device=DEV, generator=g)
+    a, b = big[:, 10:138], big[:, 150:190]  # row stride 200
+    _close(K.tall_tn(a, b), a.double().t() @ b.double(), "strided")
+    z = K.tall_tn(torch.empty(0, 7, device=DEV), torch.empty(0, 5, device=DEV))
+    assert z.shape == (7, 5) and torch.all(z == 0)
+
+
+def test_tall_tn_autograd_and_opcheck(K):
+    from torch.library import opcheck
+
+    g = torch.Generator(device=DEV).manual_seed(4)
+    a = torch.randn(3000, 96, device=DEV, generator=g, requires_grad=True)
+    b = torch.randn(3000, 40, device=DEV, generator=g, requires_grad=True)
+    w = torch.randn(96, 40, device=DEV, generator=g)
+    ga, gb = torch.autograd.grad((K.tall_tn(a, b) * w).sum(), (a, b))
+    a64, b64 = a.detach().double().requires_grad_(True), b.detach().double().requires_grad_(True)
+    ra, rb = torch.autograd.grad((a64.t() @ b64 * w.double()).sum(), (a64, b64))
+    _close(ga, ra, "grad a", 1e-5)
+    _close(gb, rb, "grad b", 1e-5)
+    opcheck(torch.ops.molix.tall_tn.default, (a, b))
