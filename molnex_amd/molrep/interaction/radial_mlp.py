@@ -13,7 +13,8 @@ the fp32 matrix-core rate) for input widths 16/32/64/128.
 When the hidden Linears' parameters need no gradient (energy + forces with fixed weights)
 the hidden stack ``[Linear -> SiLU] x num_layers`` runs as one fused HIP kernel
 (``molix::radial_hidden``, gradient w.r.t. the edge features only); otherwise, and for
-shapes the kernel does not cover, it runs as the ``Sequential``.
+shapes the kernel does not cover, it runs layer by layer, the Linears over many rows with their
+weight gradients (and those of second derivatives) on ``molix::tall_tn``.
 """
 
 from __future__ import annotations
@@ -69,6 +70,39 @@ class _ChunkedLinear(torch.autograd.Function):
         return gx, gw, gb
 
 
+_ROWS_MIN = 1 << 16
+
+
+class _RowsLinear(torch.autograd.Function):
+    """``x @ W^T + b`` over many rows (one per edge) whose weight gradient, summed over all rows, is
+    ``molix::tall_tn`` instead of one long hipBLASLt reduction.  The input gradient is this function
+    again (``g @ W``), so that second derivatives (force-matching training) also take the weight
+    gradient of that product through ``tall_tn``."""
+
+    @staticmethod
+    def forward(ctx, x, weight, bias):
+        ctx.save_for_backward(x, weight)
+        ctx.has_bias = bias is not None
+        return torch.addmm(bias, x, weight.t()) if bias is not None else x @ weight.t()
+
+    @staticmethod
+    def backward(ctx, g):
+        x, weight = ctx.saved_tensors
+        need_x, need_w, need_b = ctx.needs_input_grad
+        g = g.contiguous()
+        gx = _RowsLinear.apply(g, weight.t(), None) if need_x else None
+        gw = kernels.tall_tn(g, x) if need_w else None
+        gb = g.sum(0) if (need_b and ctx.has_bias) else None
+        return gx, gw, gb
+
+
+def _linear(layer: nn.Linear, h: torch.Tensor) -> torch.Tensor:
+    if (h.is_cuda and h.dim() == 2 and h.shape[0] >= _ROWS_MIN and h.dtype == torch.float32
+            and layer.weight.dtype == torch.float32 and torch.is_grad_enabled() and layer.weight.requires_grad):
+        return _RowsLinear.apply(h, layer.weight, layer.bias)
+    return layer(h)
+
+
 class RadialWeightMLP(nn.Module):
     def __init__(self, *, in_dim: int, hidden_dim: int, out_dim: int, num_layers: int = 2):
         super().__init__()
@@ -102,7 +136,7 @@ class RadialWeightMLP(nn.Module):
             raw = torch.cat([t.detach().reshape(-1) for m in self.mlp[:-1:2] for t in (m.weight, m.bias)])
             return kernels.radial_hidden(h, raw, c.in_dim, c.hidden_dim, c.num_layers)
         for layer in self.mlp[:-1]:
-            h = layer(h)
+            h = _linear(layer, h) if isinstance(layer, nn.Linear) else layer(h)
         return h
 
     def forward(self, edge_feats: torch.Tensor) -> torch.Tensor:

@@ -76,3 +76,32 @@ def test_tall_tn_autograd_and_opcheck(K):
     _close(ga, ra, "grad a", 1e-5)
     _close(gb, rb, "grad b", 1e-5)
     opcheck(torch.ops.molix.tall_tn.default, (a, b))
+
+
+def test_rows_linear_first_and_second_derivatives():
+    """The radial MLP's hidden Linear over many rows (weight gradients on tall_tn, also inside
+    second derivatives) against float64 torch: output, first derivatives with create_graph, and the
+    gradient of a loss on those derivatives."""
+    from molnex_amd.molrep.interaction import radial_mlp as R
+
+    g = torch.Generator(device=DEV).manual_seed(5)
+    rows = R._ROWS_MIN + 1234
+    lin = torch.nn.Linear(24, 40).to(DEV)
+    x = torch.randn(rows, 24, device=DEV, generator=g, requires_grad=True)
+    s = torch.randn(rows, 24, device=DEV, generator=g)
+    ref = torch.nn.Linear(24, 40).double().to(DEV)
+    ref.load_state_dict({k: v.double() for k, v in lin.state_dict().items()})
+    x64 = x.detach().double().requires_grad_(True)
+
+    def run(layer, xx, f):
+        y = f(layer, xx)
+        out = torch.nn.functional.silu(y)
+        (gx,) = torch.autograd.grad(out.square().sum(), xx, create_graph=True)
+        loss = (gx * s.to(gx.dtype)).sum() + out.sum()
+        return y, torch.autograd.grad(loss, (layer.weight, layer.bias, xx))
+
+    y, grads = run(lin, x, R._linear)
+    y64, grads64 = run(ref, x64, lambda layer, xx: layer(xx))
+    _close(y, y64, "rows linear output")
+    for a, b, name in zip(grads, grads64, ("weight", "bias", "x")):
+        _close(a, b, f"second-order grad {name}", 1e-5)
