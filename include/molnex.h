@@ -481,6 +481,14 @@ int mnx_radial_bwd_f32(const float* feats, int64_t num_edges, int32_t kin, int32
                        int32_t layers, const float* frag, const float* grad_h, float* grad_feats,
                        mnx_stream_t stream);
 
+/* Second derivative of the radial MLP's SiLU activations (nn.SiLU between   */
+/* the hidden Linears, src/molrep/interaction/radial_mlp.py:76-82, twice     */
+/* differentiated by a force-matching loss): for gx = g s'(x), s = SiLU,     */
+/* grad_x = gg g s''(x) and grad_grad_out = gg s'(x), elementwise over n     */
+/* values (16-byte aligned pointers; outputs overwritten).                   */
+int mnx_silu_bwd2_f32(const float* x, const float* grad, const float* grad_grad, int64_t n,
+                      float* grad_x, float* grad_grad_out, mnx_stream_t stream);
+
 /* ------------------------------------------------------------------------ */
 /* Output layer of the radial weight MLP (the last Linear of                 */
 /* RadialWeightMLP, src/molrep/interaction/radial_mlp.py:38-93): per-edge    */

@@ -1251,6 +1251,19 @@ def _tall_bwd(ctx, g):
 tall_tn.register_autograd(_tall_bwd, setup_context=_tall_setup)
 
 
+def silu_bwd2(x: Tensor, g: Tensor, gg: Tensor) -> tuple[Tensor, Tensor]:
+    """Adjoints of ``gx = g * silu'(x)`` for the seed ``gg``: ``(gg g silu''(x), gg silu'(x))``, one
+    fused pass (float32 CUDA tensors of one shape)."""
+    _require_gpu("silu_bwd2", x, g, gg)
+    xs, gs, ggs = (t.contiguous() for t in (x, g, gg))
+    if not (xs.dtype == gs.dtype == ggs.dtype == torch.float32) or not (xs.shape == gs.shape == ggs.shape):
+        raise ValueError("silu_bwd2: x, g and gg must be float32 tensors of one shape")
+    dx, dg = torch.empty_like(xs), torch.empty_like(xs)
+    check(_lib.load().mnx_silu_bwd2_f32(ptr(xs), ptr(gs), ptr(ggs), xs.numel(), ptr(dx), ptr(dg), _stream(xs)),
+          "silu_bwd2")
+    return dx, dg
+
+
 def _ew_setup(ctx, inputs, output):
     h, weight = inputs[0], inputs[1]
     ctx.save_for_backward(h, weight)

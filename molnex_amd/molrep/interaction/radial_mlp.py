@@ -14,7 +14,8 @@ When the hidden Linears' parameters need no gradient (energy + forces with fixed
 the hidden stack ``[Linear -> SiLU] x num_layers`` runs as one fused HIP kernel
 (``molix::radial_hidden``, gradient w.r.t. the edge features only); otherwise, and for
 shapes the kernel does not cover, it runs layer by layer, the Linears over many rows with their
-weight gradients (and those of second derivatives) on ``molix::tall_tn``.
+weight gradients (and those of second derivatives) on ``molix::tall_tn`` and the SiLUs' second
+derivatives in one fused pass (``kernels.silu_bwd2``).
 """
 
 from __future__ import annotations
@@ -96,10 +97,48 @@ class _RowsLinear(torch.autograd.Function):
         return gx, gw, gb
 
 
+class _SiLU(torch.autograd.Function):
+    """SiLU whose input gradient is ``_SiLUGrad``: the second derivatives of a force loss then take
+    one fused HIP pass (``kernels.silu_bwd2``) instead of torch's chain of elementwise kernels."""
+
+    @staticmethod
+    def forward(ctx, x):
+        ctx.save_for_backward(x)
+        return torch.nn.functional.silu(x)
+
+    @staticmethod
+    def backward(ctx, g):
+        (x,) = ctx.saved_tensors
+        return _SiLUGrad.apply(x, g)
+
+
+class _SiLUGrad(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x, g):
+        ctx.save_for_backward(x, g)
+        return torch.ops.aten.silu_backward(g, x)
+
+    @staticmethod
+    @torch.autograd.function.once_differentiable
+    def backward(ctx, gg):
+        x, g = ctx.saved_tensors
+        return kernels.silu_bwd2(x, g, gg)
+
+
+def _big_rows(h: torch.Tensor) -> bool:
+    return (h.is_cuda and h.dim() == 2 and h.shape[0] >= _ROWS_MIN and h.dtype == torch.float32
+            and torch.is_grad_enabled())
+
+
 def _linear(layer: nn.Linear, h: torch.Tensor) -> torch.Tensor:
-    if (h.is_cuda and h.dim() == 2 and h.shape[0] >= _ROWS_MIN and h.dtype == torch.float32
-            and layer.weight.dtype == torch.float32 and torch.is_grad_enabled() and layer.weight.requires_grad):
+    if _big_rows(h) and layer.weight.dtype == torch.float32 and layer.weight.requires_grad:
         return _RowsLinear.apply(h, layer.weight, layer.bias)
+    return layer(h)
+
+
+def _act(layer: nn.Module, h: torch.Tensor) -> torch.Tensor:
+    if isinstance(layer, nn.SiLU) and _big_rows(h) and h.requires_grad:
+        return _SiLU.apply(h)
     return layer(h)
 
 
@@ -136,7 +175,7 @@ class RadialWeightMLP(nn.Module):
             raw = torch.cat([t.detach().reshape(-1) for m in self.mlp[:-1:2] for t in (m.weight, m.bias)])
             return kernels.radial_hidden(h, raw, c.in_dim, c.hidden_dim, c.num_layers)
         for layer in self.mlp[:-1]:
-            h = _linear(layer, h) if isinstance(layer, nn.Linear) else layer(h)
+            h = _linear(layer, h) if isinstance(layer, nn.Linear) else _act(layer, h)
         return h
 
     def forward(self, edge_feats: torch.Tensor) -> torch.Tensor:
