@@ -19,8 +19,8 @@
 // operand order (double-buffered, one barrier per step); the wavefronts read
 // their operands from there, so each value is loaded and split once per
 // workgroup.  Each slab writes its
-// partial tile to a workspace [slab][M][N]; a second kernel sums the slabs in
-// slab order (deterministic, no atomics).  Slabs are sized so that the grid
+// partial tile to a workspace [slab][M][N]; a second kernel sums the slabs in a
+// fixed order (deterministic, no atomics).  Slabs are sized so that the grid
 // holds about four workgroups per CU.
 
 #include "common.h"
@@ -214,14 +214,23 @@ __global__ void __launch_bounds__(kTGThreads) k_tall_tn(const float* __restrict_
         }
 }
 
-// C[i] = sum_s part[s][i] in slab order (zeros when there are no slabs).
+// C[i] = sum_s part[s][i] (zeros when there are no slabs): eight partial sums over the slabs
+// s = j mod 8, so that eight loads are in flight, combined pairwise; a fixed order (deterministic).
 __global__ void __launch_bounds__(256) k_sum_slabs(const float* __restrict__ part, int64_t slabs, int64_t mn,
                                                    float* __restrict__ C) {
     const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
     if (i >= mn) return;
-    float s = 0.f;
-    for (int64_t z = 0; z < slabs; ++z) s += part[z * mn + i];
-    C[i] = s;
+    float s[8] = {};
+    int64_t z = 0;
+    for (; z + 8 <= slabs; z += 8) {
+        float v[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[j] = part[(z + j) * mn + i];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) s[j] += v[j];
+    }
+    for (int j = 0; z < slabs; ++z, ++j) s[j] += part[z * mn + i];
+    C[i] = ((s[0] + s[1]) + (s[2] + s[3])) + ((s[4] + s[5]) + (s[6] + s[7]));
 }
 
 struct TallPlan {
