@@ -14,14 +14,15 @@
 // tile 64 x 64, 2 x 2 MFMA tiles) over one slab of rows.  Per 16-row step each
 // thread loads 8 rows of one A column (and, for half the threads, of one B
 // column) through buffer descriptors (scalar row offsets: no per-load vector
-// address arithmetic; 64 consecutive columns per wavefront instruction) three
+// address arithmetic; 64 consecutive columns per wavefront instruction) two
 // steps ahead, splits them once and stores the three planes to LDS in MFMA
 // operand order (double-buffered, one barrier per step); the wavefronts read
 // their operands from there, so each value is loaded and split once per
-// workgroup.  Each slab writes its
-// partial tile to a workspace [slab][M][N]; a second kernel sums the slabs in a
-// fixed order (deterministic, no atomics).  Slabs are sized so that the grid
-// holds about four workgroups per CU.
+// workgroup.  Two workgroups fit a CU (at most 128 VGPRs and 72 KB of LDS
+// each), so one's products run while the other waits at its barrier.  Each slab
+// writes its partial tile to a workspace [slab][M][N]; a second kernel sums the
+// slabs in a fixed order (deterministic, no atomics).  Slabs are sized so that
+// the grid holds about four workgroups per CU.
 
 #include "common.h"
 
@@ -61,7 +62,7 @@ struct TGStage {
     bf16x8 b[3][2][kTGBN];
 };
 
-__global__ void __launch_bounds__(kTGThreads) k_tall_tn(const float* __restrict__ A, int64_t lda,
+__global__ void __launch_bounds__(kTGThreads, 4) k_tall_tn(const float* __restrict__ A, int64_t lda,
                                                         const float* __restrict__ B, int64_t ldb, int64_t K,
                                                         int M, int N, int64_t kslab, int mtiles, int ntiles,
                                                         int64_t slabs, float* __restrict__ part) {
@@ -141,55 +142,52 @@ __global__ void __launch_bounds__(kTGThreads) k_tall_tn(const float* __restrict_
         for (int u = 0; u < 2; ++u)
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[t][u][r] = 0.f;
-    // the six partial products, smallest first, each issued for the four independent accumulator
-    // tiles in turn (consecutive MFMAs never wait on each other's result)
+    // the six partial products, each issued for the four independent accumulator tiles in turn
+    // (consecutive MFMAs never wait on each other's result); grouped by A plane so that one A plane
+    // is live at a time: a2 b0, a1 b1, a1 b0, a0 b2, a0 b1, a0 b0 (the 2^-16-sized terms ahead of the
+    // 2^-8-sized ones except a0 b2, which follows a1 b0)
     auto products = [&](const TGStage& st) {
-        bf16x8 a[3][2], b[3][2];
+        bf16x8 b[3][2];
 #pragma unroll
         for (int q = 0; q < 3; ++q)
 #pragma unroll
-            for (int t = 0; t < 2; ++t) {
-                a[q][t] = st.a[q][half][wm * 64 + 32 * t + l32];
-                b[q][t] = st.b[q][half][wn * 64 + 32 * t + l32];
-            }
-        constexpr int PA[6] = {2, 1, 0, 1, 0, 0}, PB[6] = {0, 1, 2, 0, 1, 0};
+            for (int u = 0; u < 2; ++u) b[q][u] = st.b[q][half][wn * 64 + 32 * u + l32];
+        constexpr int PLANE[3] = {2, 1, 0};
+        constexpr int NB[3] = {1, 2, 3};  // partner B planes per A plane: b0 | b1, b0 | b2, b1, b0
+        constexpr int BP[3][3] = {{0, 0, 0}, {1, 0, 0}, {2, 1, 0}};
 #pragma unroll
-        for (int p = 0; p < 6; ++p)
+        for (int i = 0; i < 3; ++i) {
+            bf16x8 a[2];
 #pragma unroll
-            for (int t = 0; t < 2; ++t)
+            for (int t = 0; t < 2; ++t) a[t] = st.a[PLANE[i]][half][wm * 64 + 32 * t + l32];
 #pragma unroll
-                for (int u = 0; u < 2; ++u) acc[t][u] = tg_mfma(a[PA[p]][t], b[PB[p]][u], acc[t][u]);
+            for (int j = 0; j < NB[i]; ++j)
+#pragma unroll
+                for (int t = 0; t < 2; ++t)
+#pragma unroll
+                    for (int u = 0; u < 2; ++u) acc[t][u] = tg_mfma(a[t], b[BP[i][j]][u], acc[t][u]);
+        }
     };
 
     // Pipeline over the slab's full steps: step s is split into stage[s & 1] one iteration ahead
-    // of its products, from registers loaded two iterations before that (two register sets, so
-    // the loop is unrolled by two); one barrier per step.  The partial last step (if any) follows
-    // on its own.
+    // of its products and loaded one iteration before that; one barrier per step.  The partial
+    // last step (if any) follows on its own.
     const int64_t nfull = ke > kb ? (ke - kb) / 16 : 0;
-    float av0[8], bv0[8], av1[8], bv1[8];
-    if (nfull > 0) load_full(kb, av0, bv0);
-    if (nfull > 1) load_full(kb + 16, av1, bv1);
+    float av[8], bv[8];
     if (nfull > 0) {
-        put(stage[0], av0, bv0);
-        if (nfull > 2) load_full(kb + 32, av0, bv0);
+        load_full(kb, av, bv);
+        put(stage[0], av, bv);
+        if (nfull > 1) load_full(kb + 16, av, bv);
     }
     __syncthreads();
-    for (int64_t st = 0; st < nfull; st += 2) {
-        if (st + 1 < nfull) {  // step st + 1 from set 1, refilled with step st + 3
-            put(stage[1], av1, bv1);
-            if (st + 3 < nfull) load_full(kb + 16 * (st + 3), av1, bv1);
+    for (int64_t st = 0; st < nfull; ++st) {
+        if (st + 1 < nfull) {
+            put(stage[(st + 1) & 1], av, bv);
+            if (st + 2 < nfull) load_full(kb + 16 * (st + 2), av, bv);
         }
-        products(stage[0]);
-        __syncthreads();
-        if (st + 1 >= nfull) break;
-        if (st + 2 < nfull) {  // step st + 2 from set 0, refilled with step st + 4
-            put(stage[0], av0, bv0);
-            if (st + 4 < nfull) load_full(kb + 16 * (st + 4), av0, bv0);
-        }
-        products(stage[1]);
+        products(stage[st & 1]);
         __syncthreads();
     }
-    float av[8], bv[8];
     if (kb + 16 * nfull < ke) {
         load_tail(kb + 16 * nfull, av, bv);
         put(stage[0], av, bv);
