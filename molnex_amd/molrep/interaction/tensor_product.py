@@ -9,6 +9,8 @@ edge_angular, edge_index, tp_weights)``, ``weight_numel``, ``config`` and a
 
 from __future__ import annotations
 
+import warnings
+
 import torch
 import torch.nn as nn
 from pydantic import BaseModel
@@ -151,6 +153,10 @@ class ChannelWiseTensorProduct(nn.Module):
 
     def apply_graph(self, x, y, weight, g: EdgeGraph):
         if self.config_id < 0:
+            if config.deterministic:
+                warnings.warn("config.deterministic: the table-driven tensor product (irreps outside the compiled "
+                              "configurations) accumulates grad_x and grad_Y with atomics; its gradients are not "
+                              "bitwise reproducible", stacklevel=2)
             return torch.ops.molix.tp_any(x, y, weight, g.row_ptr, g.perm, g.senders, self.any_table)
         extra = g.sender_csr() if config.deterministic else ()
         return torch.ops.molix.tp_scatter(x, y, weight, g.row_ptr, g.perm, g.senders, self.config_id, self.channels,
