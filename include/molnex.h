@@ -608,11 +608,13 @@ int mnx_tp_any_bwd_f32(const int32_t* table, int32_t table_len, const float* x, 
 /* output layer, src/molrep/interaction/radial_mlp.py:76-82, which torch's   */
 /* autograd computes as one GEMM over the edges), fp32-accurate on the bf16  */
 /* matrix cores, deterministic.  Workspace from                              */
-/* mnx_tall_tn_workspace_bytes (per-slab partial tiles); C is overwritten.   */
+/* mnx_tall_tn_workspace_bytes (per-slab partial tiles); C is overwritten,   */
+/* and colsum_a [M] (may be NULL) receives the column sums of A (the bias    */
+/* gradient of the same layer) from the same pass.                           */
 /* ------------------------------------------------------------------------ */
 size_t mnx_tall_tn_workspace_bytes(int64_t K, int32_t M, int32_t N);
 int mnx_tall_tn_f32(const float* A, int64_t lda, const float* B, int64_t ldb, int64_t K, int32_t M,
-                    int32_t N, float* C, void* workspace, size_t workspace_bytes,
+                    int32_t N, float* C, float* colsum_a, void* workspace, size_t workspace_bytes,
                     mnx_stream_t stream);
 
 /* ------------------------------------------------------------------------ */

@@ -52,7 +52,7 @@ SIGNATURES = {
     "mnx_tp_any_bwd_f32": (C.c_int, [vp, c_i32, vp, vp, vp, vp, vp, vp, vp, c_i64, c_i64, vp, vp, vp, vp]),
     "mnx_tall_tn_workspace_bytes": (C.c_size_t, [c_i64, c_i32, c_i32]),
     "mnx_silu_bwd2_f32": (C.c_int, [vp, vp, vp, c_i64, vp, vp, vp]),
-    "mnx_tall_tn_f32": (C.c_int, [vp, c_i64, vp, c_i64, c_i64, c_i32, c_i32, vp, vp, C.c_size_t, vp]),
+    "mnx_tall_tn_f32": (C.c_int, [vp, c_i64, vp, c_i64, c_i64, c_i32, c_i32, vp, vp, vp, C.c_size_t, vp]),
     "mnx_tp_bwd_rows_f32": (C.c_int, [c_i32, c_i32, vp, vp, vp, vp, vp, vp, vp, vp, c_i64, c_i64, vp, vp, vp, vp,
                                       c_sz, vp]),
     "mnx_tp_bwd_sender_rows_f32": (C.c_int, [c_i32, c_i32, vp, vp, vp, vp, vp, vp, vp, vp, c_i64, c_i64, vp, vp,

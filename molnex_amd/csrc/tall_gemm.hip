@@ -21,8 +21,10 @@
 // workgroup.  Two workgroups fit a CU (at most 128 VGPRs and 72 KB of LDS
 // each), so one's products run while the other waits at its barrier.  Each slab
 // writes its partial tile to a workspace [slab][M][N]; a second kernel sums the
-// slabs in a fixed order (deterministic, no atomics).  Slabs are sized so that
-// the grid holds about four workgroups per CU.
+// slabs in a fixed order (deterministic, no atomics).  Optionally the loader
+// threads also sum their A columns (compensated), giving A's column sums (a
+// layer's bias gradient) from the same read.  Slabs are sized so that the grid
+// holds about four workgroups per CU.
 
 #include "common.h"
 
@@ -65,7 +67,8 @@ struct TGStage {
 __global__ void __launch_bounds__(kTGThreads, 4) k_tall_tn(const float* __restrict__ A, int64_t lda,
                                                         const float* __restrict__ B, int64_t ldb, int64_t K,
                                                         int M, int N, int64_t kslab, int mtiles, int ntiles,
-                                                        int64_t slabs, float* __restrict__ part) {
+                                                        int64_t slabs, float* __restrict__ part,
+                                                        float* __restrict__ cpart) {
     __shared__ TGStage stage[2];
     // XCD-aware order: workgroups are dealt round-robin over the 8 XCDs, so XCD x = b mod 8 takes
     // the contiguous item range starting at x * per, items ordered (slab, N tile, M tile): the M
@@ -121,7 +124,17 @@ __global__ void __launch_bounds__(kTGThreads, 4) k_tall_tn(const float* __restri
             bv[j] = kbb < ke && vb ? B[kbb * ldb + gb] : 0.f;
         }
     };
+    // column sums of A over this thread's rows (the bias gradient of the layer, when asked for):
+    // compensated, so that the long per-thread chain keeps fp32 accuracy
+    float csum = 0.f, ccomp = 0.f;
     auto put = [&](TGStage& st, const float (&av)[8], const float (&bv)[8]) {
+        if (cpart && tn == 0) {
+            const float t = ((av[0] + av[1]) + (av[2] + av[3])) + ((av[4] + av[5]) + (av[6] + av[7]));
+            const float yk = t - ccomp;
+            const float nk = csum + yk;
+            ccomp = (nk - csum) - yk;
+            csum = nk;
+        }
         bf16x8 x0, x1, x2;
         tg_split(av, x0, x1, x2);
         st.a[0][akh][am] = x0;
@@ -195,6 +208,7 @@ __global__ void __launch_bounds__(kTGThreads, 4) k_tall_tn(const float* __restri
         products(stage[0]);
     }
 
+    if (cpart && tn == 0 && va) cpart[(slab * 2 + akh) * M + ga] = csum;
     // D tile layout: lane holds rows 8 (r / 4) + 4 half + r % 4 of column l32
     const int m0 = tm * kTGBM + wm * 64, n0 = tn * kTGBN + wn * 64;
     float* dst = part + slab * M * N;
@@ -254,11 +268,11 @@ extern "C" {
 size_t mnx_tall_tn_workspace_bytes(int64_t K, int32_t M, int32_t N) {
     if (K <= 0 || M <= 0 || N <= 0) return 0;
     const TallPlan p = tall_plan(K, M, N);
-    return size_t(p.slabs) * size_t(M) * size_t(N) * sizeof(float);
+    return size_t(p.slabs) * (size_t(M) * size_t(N) + 2 * size_t(M)) * sizeof(float);
 }
 
 int mnx_tall_tn_f32(const float* A, int64_t lda, const float* B, int64_t ldb, int64_t K, int32_t M, int32_t N,
-                    float* C, void* workspace, size_t workspace_bytes, mnx_stream_t stream_) {
+                    float* C, float* colsum_a, void* workspace, size_t workspace_bytes, mnx_stream_t stream_) {
     clear_error();
     hipStream_t stream = (hipStream_t)stream_;
     MNX_REQUIRE(K >= 0 && M >= 0 && N >= 0, "tall_tn: sizes out of range");
@@ -268,6 +282,10 @@ int mnx_tall_tn_f32(const float* A, int64_t lda, const float* B, int64_t ldb, in
     if (K == 0) {
         k_sum_slabs<<<unsigned(ceil_div(mn, 256)), 256, 0, stream>>>(nullptr, 0, mn, C);
         MNX_CHECK_LAUNCH();
+        if (colsum_a) {
+            k_sum_slabs<<<unsigned(ceil_div(M, 256)), 256, 0, stream>>>(nullptr, 0, M, colsum_a);
+            MNX_CHECK_LAUNCH();
+        }
         return MNX_OK;
     }
     MNX_REQUIRE(A && B, "tall_tn: null input");
@@ -276,18 +294,23 @@ int mnx_tall_tn_f32(const float* A, int64_t lda, const float* B, int64_t ldb, in
     // byte offsets of a 16-row step stay in 32 bits (buffer descriptors)
     MNX_REQUIRE(lda <= (int64_t(1) << 25) && ldb <= (int64_t(1) << 25), "tall_tn: row strides above 2^25");
     const TallPlan p = tall_plan(K, M, N);
-    const size_t need = size_t(p.slabs) * size_t(mn) * sizeof(float);
+    const size_t need = size_t(p.slabs) * (size_t(mn) + 2 * size_t(M)) * sizeof(float);
     MNX_REQUIRE(workspace && workspace_bytes >= need, "tall_tn: workspace of %zu bytes, %zu needed",
                 workspace_bytes, need);
     float* part = static_cast<float*>(workspace);
     const int mt = int(ceil_div(M, kTGBM)), nt = int(ceil_div(N, kTGBN));
     const int64_t blocks = 8 * ceil_div(int64_t(mt) * nt * p.slabs, 8);
     MNX_REQUIRE(blocks < (int64_t(1) << 31), "tall_tn: %lld workgroups", (long long)blocks);
+    float* cpart = colsum_a ? part + size_t(p.slabs) * size_t(mn) : nullptr;
     k_tall_tn<<<unsigned(blocks), kTGThreads, 0, stream>>>(A, lda, B, ldb, K, M, N, p.kslab, mt, nt, p.slabs,
-                                                            part);
+                                                            part, cpart);
     MNX_CHECK_LAUNCH();
     k_sum_slabs<<<unsigned(ceil_div(mn, 256)), 256, 0, stream>>>(part, p.slabs, mn, C);
     MNX_CHECK_LAUNCH();
+    if (colsum_a) {
+        k_sum_slabs<<<unsigned(ceil_div(M, 256)), 256, 0, stream>>>(cpart, 2 * p.slabs, M, colsum_a);
+        MNX_CHECK_LAUNCH();
+    }
     return MNX_OK;
 }
 

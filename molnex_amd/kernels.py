@@ -1228,8 +1228,8 @@ def tall_tn(a: Tensor, b: Tensor) -> Tensor:
     out = torch.empty((M, N), dtype=torch.float32, device=a2.device)
     lib = _lib.load()
     ws = _ws(lib.mnx_tall_tn_workspace_bytes(K, M, N), a2.device)
-    check(lib.mnx_tall_tn_f32(ptr(a2), a2.stride(0), ptr(b2), b2.stride(0), K, M, N, ptr(out), ptr(ws), ws.numel(),
-                              _stream(a2)), "tall_tn")
+    check(lib.mnx_tall_tn_f32(ptr(a2), a2.stride(0), ptr(b2), b2.stride(0), K, M, N, ptr(out), None, ptr(ws),
+                              ws.numel(), _stream(a2)), "tall_tn")
     return out
 
 
@@ -1249,6 +1249,45 @@ def _tall_bwd(ctx, g):
 
 
 tall_tn.register_autograd(_tall_bwd, setup_context=_tall_setup)
+
+
+@torch.library.custom_op("molix::tall_tn_colsum", mutates_args=(), device_types="cuda")
+def tall_tn_colsum(a: Tensor, b: Tensor) -> tuple[Tensor, Tensor]:
+    """``(a.T @ b, a.sum(0))`` from one pass over ``a`` (``tall_tn`` with the column sums of ``a``:
+    a layer's weight and bias gradients)."""
+    _require_gpu("tall_tn_colsum", a, b)
+    a2, b2 = _rows_f32(a, "a"), _rows_f32(b, "b")
+    if a2.shape[0] != b2.shape[0]:
+        raise ValueError(f"tall_tn_colsum: {a2.shape[0]} rows against {b2.shape[0]}")
+    K, M, N = a2.shape[0], a2.shape[1], b2.shape[1]
+    out = torch.empty((M, N), dtype=torch.float32, device=a2.device)
+    cs = torch.empty((M,), dtype=torch.float32, device=a2.device)
+    lib = _lib.load()
+    ws = _ws(lib.mnx_tall_tn_workspace_bytes(K, M, N), a2.device)
+    check(lib.mnx_tall_tn_f32(ptr(a2), a2.stride(0), ptr(b2), b2.stride(0), K, M, N, ptr(out), ptr(cs), ptr(ws),
+                              ws.numel(), _stream(a2)), "tall_tn_colsum")
+    return out, cs
+
+
+@tall_tn_colsum.register_fake
+def _(a, b):
+    return a.new_empty((a.shape[1], b.shape[1])), a.new_empty((a.shape[1],))
+
+
+def _tallc_bwd(ctx, g, gc):
+    a, b = ctx.saved_tensors
+    na, nb = ctx.needs_input_grad
+    ga = gb = None
+    if na:
+        ga = b @ g.t() if g is not None else None
+        if gc is not None:
+            ga = gc.expand(a.shape[0], -1) if ga is None else ga + gc
+    if nb and g is not None:
+        gb = a @ g
+    return ga, gb
+
+
+tall_tn_colsum.register_autograd(_tallc_bwd, setup_context=_tall_setup)
 
 
 def silu_bwd2(x: Tensor, g: Tensor, gg: Tensor) -> tuple[Tensor, Tensor]:
@@ -1277,9 +1316,14 @@ def _ew_bwd(ctx, grad):
     grad = grad.contiguous()
     gh = edge_weights_backward(grad, weight) if need_h else None
     gw = None
-    if need_w:  # training: the (N, K) weight gradient summed over all rows
-        gw = tall_tn(grad, h)
-    gb = grad.sum(0) if (need_b and ctx.has_bias) else None
+    gb = None
+    if need_w:  # training: the (N, K) weight gradient summed over all rows (and the bias's)
+        if need_b and ctx.has_bias:
+            gw, gb = tall_tn_colsum(grad, h)
+        else:
+            gw = tall_tn(grad, h)
+    elif need_b and ctx.has_bias:
+        gb = grad.sum(0)
     return (gh, gw, gb)[:len(ctx.needs_input_grad)]
 
 

@@ -92,8 +92,14 @@ class _RowsLinear(torch.autograd.Function):
         need_x, need_w, need_b = ctx.needs_input_grad
         g = g.contiguous()
         gx = _RowsLinear.apply(g, weight.t(), None) if need_x else None
-        gw = kernels.tall_tn(g, x) if need_w else None
-        gb = g.sum(0) if (need_b and ctx.has_bias) else None
+        gw = gb = None
+        want_b = need_b and ctx.has_bias
+        if need_w and want_b:
+            gw, gb = kernels.tall_tn_colsum(g, x)
+        elif need_w:
+            gw = kernels.tall_tn(g, x)
+        elif want_b:
+            gb = g.sum(0)
         return gx, gw, gb
 
 

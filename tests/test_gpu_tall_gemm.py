@@ -150,3 +150,28 @@ def test_radial_mlp_hidden_second_order_many_rows():
 
     for a, b in zip(run(mlp, x), run(m64, x64)):
         _close(a, b, "hidden second order", 1e-5)
+
+
+def test_tall_tn_colsum(K):
+    """The column sums of a from the same pass (a layer's bias gradient) against float64, with a
+    ragged tail and columns beyond one tile; autograd of both outputs and opcheck."""
+    from torch.library import opcheck
+
+    g0 = torch.Generator(device=DEV).manual_seed(8)
+    for rows, M, N in ((300_001, 300, 64), (2_607_384, 1280, 128), (17, 5, 3)):
+        a = torch.randn(rows, M, device=DEV, generator=g0) + 0.5
+        b = torch.randn(rows, N, device=DEV, generator=g0)
+        c, s = K.tall_tn_colsum(a, b)
+        if rows <= 300_001:  # (the product at 2.6 M rows is checked by test_tall_tn_vs_float64)
+            _close(c, a.double().t() @ b.double(), f"colsum product {rows}")
+        _close(s, a.double().sum(0), f"colsum {rows}", 1e-6, 1e-6)
+    a = torch.randn(3000, 40, device=DEV, generator=g0, requires_grad=True)
+    b = torch.randn(3000, 24, device=DEV, generator=g0, requires_grad=True)
+    wc, ws = torch.randn(40, 24, device=DEV, generator=g0), torch.randn(40, device=DEV, generator=g0)
+    c, s = K.tall_tn_colsum(a, b)
+    ga, gb = torch.autograd.grad((c * wc).sum() + (s * ws).sum(), (a, b))
+    a64, b64 = a.detach().double().requires_grad_(True), b.detach().double().requires_grad_(True)
+    ra, rb = torch.autograd.grad((a64.t() @ b64 * wc.double()).sum() + (a64.sum(0) * ws.double()).sum(), (a64, b64))
+    _close(ga, ra, "colsum grad a", 1e-5)
+    _close(gb, rb, "colsum grad b", 1e-5)
+    opcheck(torch.ops.molix.tall_tn_colsum.default, (a, b))
