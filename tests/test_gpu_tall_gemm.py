@@ -175,3 +175,16 @@ def test_tall_tn_colsum(K):
     _close(ga, ra, "colsum grad a", 1e-5)
     _close(gb, rb, "colsum grad b", 1e-5)
     opcheck(torch.ops.molix.tall_tn_colsum.default, (a, b))
+
+
+def test_tall_tn_multi_tile_ragged_strided_colsum(K):
+    """Several 256 x 128 output tiles in both directions with ragged edges, a row count that leaves a
+    partial last step in every slab, row-strided views of both operands, and the column sums."""
+    g0 = torch.Generator(device=DEV).manual_seed(9)
+    rows = 100_003
+    big = torch.randn(rows, 700, device=DEV, generator=g0)
+    a, b = big[:, 3:336], big[:, 400:600]  # M = 333 (2 tiles), N = 200 (2 tiles), row stride 700
+    c, s = K.tall_tn_colsum(a, b)
+    _close(c, a.double().t() @ b.double(), "multi-tile product")
+    _close(s, a.double().sum(0), "multi-tile colsum", 1e-6, 1e-6)
+    _close(K.tall_tn(a, b), c, "tall_tn vs tall_tn_colsum product", 1e-7, 1e-7)
