@@ -183,3 +183,14 @@ def test_tp_any_config3_scale_matches_compiled(ops):
     gb = torch.autograd.grad(b, (x, Y, w), go)
     for u, v, name in zip(ga, gb, ("x", "Y", "w")):
         assert_close(u.cpu().numpy(), v.cpu().numpy(), f"grad_{name} at scale", rtol=1e-5)
+
+
+@pytest.mark.parametrize("in1,in2,filt", [
+    # harmonics-like operand with odd parity blocks only, outputs of both parities per l
+    ("4x1o + 6x2e", "1o + 2o", "0e + 0o + 1e + 1o + 2e + 2o + 3e + 3o"),
+    # one block of 200 channels (4 chunks of 64, ragged) next to a multiplicity-1 block
+    ("200x1e + 1x0o", "0e + 1o", "0o + 1o + 1e + 2o"),
+])
+def test_tp_any_more_irreps(ops, in1, in2, filt):
+    print(f"tp_any {in1} x {in2} -> {filt}", flush=True)
+    _check(ops, in1, in2, filt, N=30, E=250, seed=20)
