@@ -292,7 +292,7 @@ int mnx_tall_tn_f32(const float* A, int64_t lda, const float* B, int64_t ldb, in
     MNX_REQUIRE(lda >= M && ldb >= N, "tall_tn: row strides (%lld, %lld) below the widths (%d, %d)",
                 (long long)lda, (long long)ldb, M, N);
     // byte offsets of a 16-row step stay in 32 bits (buffer descriptors)
-    MNX_REQUIRE(lda <= (int64_t(1) << 25) && ldb <= (int64_t(1) << 25), "tall_tn: row strides above 2^25");
+    MNX_REQUIRE(lda < (int64_t(1) << 25) && ldb < (int64_t(1) << 25), "tall_tn: row strides of 2^25 or more");
     const TallPlan p = tall_plan(K, M, N);
     const size_t need = size_t(p.slabs) * (size_t(mn) + 2 * size_t(M)) * sizeof(float);
     MNX_REQUIRE(workspace && workspace_bytes >= need, "tall_tn: workspace of %zu bytes, %zu needed",
