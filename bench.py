@@ -240,16 +240,20 @@ def tp_bytes(N, E, C, P=23, NX=16, NY=16, NO=99):
     return fwd, bwd
 
 
-def mace_step_bytes(enc, N, E):
+def mace_step_bytes(enc, N, E, mlp_rows=None):
     """Algorithmic HBM bytes of one energy + forces step of `enc` (fp32, each tensor once per kernel):
     per interaction layer the radial MLP hidden stack (fwd: features in, h out; bwd: features and
-    grad_h in, grad_features out), its output layer (fwd: h in, per-edge weights out; bwd: their
-    gradient in, grad_h out) and the TP + scatter forward and backward (tp_bytes); once per step the
-    harmonics (vectors in, 16 components out, and back) and the bond vectors (positions and edge
-    list in, vectors out, and back).  Node-level kernels (linears, contraction, element updates, PME
-    on 50k atoms) move < 2 % of these bytes and are left out."""
+    grad_h in, grad_features out), its output layer (fwd: h in, weights out; bwd: the per-edge weight
+    gradient in, grad_h out) and the TP + scatter forward and backward (tp_bytes, per directed edge);
+    once per step the harmonics (vectors in, 16 components out, and back) and the bond vectors
+    (positions and edge list in, vectors out, and back).  ``mlp_rows``: the rows the radial MLP runs
+    on -- E per directed edge (the reference's form), E / 2 once per undirected pair (what MACE here
+    runs): the hidden stack, the output layer's input and its weights written then have E / 2 rows,
+    while the per-edge weight gradient it reads back stays E rows.  Node-level kernels (linears,
+    contraction, element updates, PME on 50k atoms) move < 2 % of these bytes and are left out."""
     from molnex_amd import kernels as K
 
+    R = E if mlp_rows is None else mlp_rows
     total = 2 * (4 * E * 3 + 4 * E * 16) + 4 * E * 3  # harmonics fwd + bwd
     total += 2 * (8 * E * 2 + 4 * E * 3 + 4 * N * 3)  # bond vectors fwd + bwd
     for blk in enc.interactions:
@@ -258,9 +262,8 @@ def mace_step_bytes(enc, N, E):
         rc = blk.radial_mlp.config
         kin, H = rc.in_dim, rc.hidden_dim
         tf, tb = tp_bytes(N, E, C, P, NX, NY, NO)
-        w = 4 * E * P * C
-        total += 4 * E * (kin + H) + (4 * E * H + w) + tf  # forward
-        total += tb + (w + 4 * E * H) + 4 * E * (kin + H + kin)  # backward
+        total += 4 * R * (kin + H) + 4 * R * (H + P * C) + tf  # forward
+        total += tb + 4 * E * P * C + 4 * R * H + 4 * R * (kin + H + kin)  # backward
     return total
 
 
@@ -452,11 +455,15 @@ def full_step_bench(args, dev):
         step()
     torch.cuda.synchronize()
     dt = (time.perf_counter() - t0) / args.steps
-    nbytes = mace_step_bytes(enc, n, int(edge_index.shape[0]))
+    E = int(edge_index.shape[0])
+    # the radial MLP runs once per undirected pair (E / 2 rows); the per-edge form beside it
+    nbytes = mace_step_bytes(enc, n, E, E // 2)
+    nbytes_edge = mace_step_bytes(enc, n, E)
     achieved = nbytes / dt / 1e9
     roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None, "kernel": "whole step",
-            "algorithmic_bytes": nbytes}
+            "algorithmic_bytes": nbytes, "algorithmic_bytes_mlp_per_edge": nbytes_edge,
+            "frac_mlp_per_edge": round(nbytes_edge / dt / 1e9 / HBM_PEAK_GBS, 4)}
     return {"metric": "atoms/s energy+forces (MACE + PME)", "value": round(n / dt, 1), "unit": "atoms/s",
             "roofline": roof,
             "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(dt * 1e3, 3),
@@ -735,7 +742,9 @@ def secondary_figures(args, dev):
         full = full_step_bench(sub, dev)
         out[key] = {"atoms_per_s": full["value"], "ms_per_step": full["ms_per_step"],
                     "workload": full["config"]["workload"], "edges": full["config"]["edges"],
-                    "hbm_frac": full["roofline"]["frac"], "algorithmic_GB": round(full["roofline"]["algorithmic_bytes"] / 1e9, 2)}
+                    "hbm_frac": full["roofline"]["frac"], "algorithmic_GB": round(full["roofline"]["algorithmic_bytes"] / 1e9, 2),
+                    "hbm_frac_mlp_per_edge": full["roofline"]["frac_mlp_per_edge"],
+                    "algorithmic_GB_mlp_per_edge": round(full["roofline"]["algorithmic_bytes_mlp_per_edge"] / 1e9, 2)}
         torch.cuda.empty_cache()
     out["config5_literal_training_step"] = train_step_bench(args, dev)
     torch.cuda.empty_cache()

@@ -139,15 +139,15 @@ def bwd_cpl(ps) -> int:
     return 2 if per_channel <= 60 else 1
 
 
-def _emit_prefetch(a, cfg, ps, xs, ys, xi, indent, t_expr, cpl_expr="CPL"):
-    """Load edge t_expr's ids, harmonics, sender row and weights into n* registers."""
+def _emit_prefetch(a, cfg, ps, xs, ys, xi, indent, cpl_expr="CPL"):
+    """Load the harmonics, sender row and weight row of the edge whose ids are (ne, ns, nw) into
+    the n* registers."""
     a(f"{indent}{{")
-    a(f"{indent}  ne = perm[{t_expr}]; ns = snd[{t_expr}];")
     a(f"{indent}  const float* __restrict__ Yn = Y + int64_t(ne) * {cfg.NY};")
     for c in ys:
         a(f"{indent}  ny{c} = Yn[{c}];")
     a(f"{indent}  const float* __restrict__ xn = x + int64_t(ns) * XS;")
-    a(f"{indent}  const float* __restrict__ wn = w + int64_t(wrow ? wrow[ne] : ne) * WS;")
+    a(f"{indent}  const float* __restrict__ wn = w + int64_t(nw) * WS;")
     a("#pragma unroll")
     a(f"{indent}  for (int k = 0; k < {cpl_expr}; ++k) {{")
     for c in xs:
@@ -158,13 +158,27 @@ def _emit_prefetch(a, cfg, ps, xs, ys, xi, indent, t_expr, cpl_expr="CPL"):
     a(f"{indent}}}")
 
 
+def _emit_ids(a, indent, t_expr, dst=("ie", "is", "iw")):
+    """Edge, sender and weight-row ids of CSR slot t_expr (wave-uniform scalar loads)."""
+    e, s_, w = dst
+    a(f"{indent}{e} = perm[{t_expr}]; {s_} = snd[{t_expr}]; {w} = wrow ? wrow[{e}] : {e};")
+
+
 def _emit_edge_loop_head(a, cfg, ps, xs, ys, xi):
+    """The receiver's CSR walk with a two-stage prefetch: the ids of edge t + 2 (including the
+    dependent weight-row lookup) are loaded while edge t is processed, and the rows of edge t + 1
+    are loaded at the top of iteration t from ids that are already in registers."""
     a("  const int beg = row_ptr[n], end = row_ptr[n + 1];")
-    a("  int ne = 0, ns = 0;")
+    a("  int ne = 0, ns = 0, nw = 0, ie = 0, is = 0, iw = 0;")
     a("  " + " ".join(f"float ny{c} = 0.f;" for c in ys))
     a(f"  float nxv[CPL][{len(xs)}], nwv[CPL][{len(ps)}];")
-    a("  if (beg < end)")
-    _emit_prefetch(a, cfg, ps, xs, ys, xi, "  ", "beg")
+    a("  if (beg < end) {")
+    _emit_ids(a, "    ", "beg", ("ne", "ns", "nw"))
+    _emit_prefetch(a, cfg, ps, xs, ys, xi, "    ")
+    a("  }")
+    a("  if (beg + 1 < end) {")
+    _emit_ids(a, "    ", "beg + 1")
+    a("  }")
     a("  for (int t = beg; t < end; ++t) {")
     a("    const int e = ne, s = ns;")
     a("    " + " ".join(f"const float y{c} = ny{c};" for c in ys))
@@ -174,8 +188,13 @@ def _emit_edge_loop_head(a, cfg, ps, xs, ys, xi):
     a(f"#pragma unroll\n      for (int i = 0; i < {len(xs)}; ++i) xv[k][i] = nxv[k][i];")
     a(f"#pragma unroll\n      for (int i = 0; i < {len(ps)}; ++i) wv[k][i] = nwv[k][i];")
     a("    }")
-    a("    if (t + 1 < end)")
-    _emit_prefetch(a, cfg, ps, xs, ys, xi, "    ", "t + 1")
+    a("    if (t + 1 < end) {")
+    a("      ne = ie; ns = is; nw = iw;")
+    _emit_prefetch(a, cfg, ps, xs, ys, xi, "      ")
+    a("      if (t + 2 < end) {")
+    _emit_ids(a, "        ", "t + 2")
+    a("      }")
+    a("    }")
 
 
 def gen_fwd(cfg: Cfg, g: int) -> str:

@@ -740,11 +740,14 @@ __device__ __forceinline__ void silu_bwd2_one(float x, float g, float gg, float&
     dx = gg * g * (sg * om * fmaf(x, om - sg, 2.f));
 }
 
+// VEC: 16-byte loads and stores (every pointer 16-byte aligned); otherwise four scalar elements
+// per thread (views at an offset that is not a multiple of four floats)
+template <bool VEC>
 __global__ void __launch_bounds__(256) k_silu_bwd2(const float* __restrict__ x, const float* __restrict__ g,
                                                    const float* __restrict__ gg, int64_t n, float* __restrict__ dx,
                                                    float* __restrict__ dg) {
     const int64_t i4 = (int64_t(blockIdx.x) * 256 + threadIdx.x) * 4;
-    if (i4 + 4 <= n) {
+    if (VEC && i4 + 4 <= n) {
         const float4 a = *reinterpret_cast<const float4*>(x + i4);
         const float4 b = *reinterpret_cast<const float4*>(g + i4);
         const float4 c = *reinterpret_cast<const float4*>(gg + i4);
@@ -756,7 +759,8 @@ __global__ void __launch_bounds__(256) k_silu_bwd2(const float* __restrict__ x, 
         *reinterpret_cast<float4*>(dx + i4) = ox;
         *reinterpret_cast<float4*>(dg + i4) = og;
     } else {
-        for (int64_t i = i4; i < n; ++i) silu_bwd2_one(x[i], g[i], gg[i], dx[i], dg[i]);
+        const int64_t end = i4 + 4 < n ? i4 + 4 : n;
+        for (int64_t i = i4; i < end; ++i) silu_bwd2_one(x[i], g[i], gg[i], dx[i], dg[i]);
     }
 }
 
@@ -832,11 +836,15 @@ int mnx_silu_bwd2_f32(const float* x, const float* grad, const float* grad_grad,
     MNX_REQUIRE(n >= 0, "silu_bwd2: n out of range");
     if (n == 0) return MNX_OK;
     MNX_REQUIRE(x && grad && grad_grad && grad_x && grad_grad_out, "null pointer argument");
+    bool aligned = true;
     for (const void* p : {(const void*)x, (const void*)grad, (const void*)grad_grad, (const void*)grad_x,
                           (const void*)grad_grad_out})
-        MNX_REQUIRE(reinterpret_cast<uintptr_t>(p) % 16 == 0, "silu_bwd2: pointers must be 16-byte aligned");
-    k_silu_bwd2<<<unsigned(ceil_div(ceil_div(n, 4), 256)), 256, 0, stream>>>(x, grad, grad_grad, n, grad_x,
-                                                                            grad_grad_out);
+        aligned = aligned && reinterpret_cast<uintptr_t>(p) % 16 == 0;
+    const unsigned blocks = unsigned(ceil_div(ceil_div(n, 4), 256));
+    if (aligned)
+        k_silu_bwd2<true><<<blocks, 256, 0, stream>>>(x, grad, grad_grad, n, grad_x, grad_grad_out);
+    else
+        k_silu_bwd2<false><<<blocks, 256, 0, stream>>>(x, grad, grad_grad, n, grad_x, grad_grad_out);
     MNX_CHECK_LAUNCH();
     return MNX_OK;
 }

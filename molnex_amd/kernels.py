@@ -1209,10 +1209,17 @@ def _(grad, weight):
     return grad.new_empty(grad.shape[0], weight.shape[1])
 
 
+# mnx_tall_tn_f32 takes row strides below 2^25 floats (its 16-row step offsets stay in 31 bits)
+_TALL_MAX_STRIDE = 1 << 25
+
+
 def _rows_f32(t: Tensor, what: str) -> Tensor:
+    """``t`` itself when its rows are unit-stride with a row stride the tall GEMM accepts, else a
+    contiguous copy (e.g. a column slice of a very wide tensor)."""
     if t.dtype != torch.float32 or t.dim() != 2:
         raise TypeError(f"{what} must be a 2-D float32 tensor")
-    return t if (t.stride(1) == 1 and t.stride(0) >= t.shape[1]) else t.contiguous()
+    ok = t.stride(1) == 1 and t.shape[1] <= t.stride(0) < _TALL_MAX_STRIDE
+    return t if ok else t.contiguous()
 
 
 @torch.library.custom_op("molix::tall_tn", mutates_args=(), device_types="cuda")

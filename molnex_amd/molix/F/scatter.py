@@ -7,8 +7,9 @@ The reduction axis is moved to the front and the remaining axes flattened into c
 ``dim`` reduces as one (rows, columns) segment sum.  ``index`` is the 1-D segment id of every slice
 along ``dim``; an index of ``src``'s rank whose entries only vary along ``dim`` (a broadcast view,
 or singleton axes elsewhere) is reduced to that 1-D form.  A full-rank index that varies along other
-axes is an element-wise scatter, not a segment sum: it goes to torch's GPU ``scatter_add``.
-GPU tensors only (the HIP op raises for CPU tensors)."""
+axes is an element-wise scatter, not a segment sum: it goes to torch's GPU ``scatter_add``, and so
+does a ``src`` that is not float32 (float64 models, half precision, integer counts), which the fp32
+kernel does not compute.  GPU tensors only (the HIP op raises for CPU tensors)."""
 
 from __future__ import annotations
 
@@ -37,11 +38,15 @@ def scatter_sum(src: Tensor, index: Tensor, dim: int = 0, dim_size: int | None =
     if dim_size is None:
         dim_size = int(index.max().item()) + 1 if index.numel() else 0
     ids = _segment_ids(index, src, dim)
-    if ids is None:
+    if ids is None or src.dtype != torch.float32:
         if src.device.type != "cuda":
             raise RuntimeError(f"scatter_sum runs on the GPU only (got a {src.device} tensor)")
         out_shape = list(src.shape)
         out_shape[dim] = dim_size
+        if ids is not None:  # a 1-D segment id per slice: broadcast it over the other axes
+            shape = [1] * src.dim()
+            shape[dim] = ids.shape[0]
+            index = ids.reshape(shape)
         return src.new_zeros(out_shape).scatter_add(dim, index.expand_as(src), src)
     moved = src.movedim(dim, 0)
     rows = moved.reshape(moved.shape[0], math.prod(moved.shape[1:]))

@@ -5,6 +5,8 @@ from __future__ import annotations
 import torch
 import torch.nn as nn
 
+from .derivation import _graph_totals
+
 
 class _PerGraph(torch.autograd.Function):
     """``values[batch]`` whose backward is an ``index_add_`` (atomic) instead of the sort-based
@@ -31,9 +33,11 @@ class ChargeHead(nn.Module):
     def forward(self, node_features: torch.Tensor, *, batch: torch.Tensor, num_graphs: int | None = None,
                 **kwargs) -> dict[str, torch.Tensor]:
         raw = self.mlp(node_features).squeeze(-1)
-        if num_graphs is None:
+        trusted = num_graphs is not None  # given: no host synchronisation, batch ids trusted
+        if not trusted:
             num_graphs = int(batch.max().item()) + 1
-        s = torch.zeros(num_graphs, dtype=raw.dtype, device=raw.device).index_add_(0, batch, raw)
-        cnt = torch.zeros(num_graphs, dtype=raw.dtype, device=raw.device).index_add_(0, batch, torch.ones_like(raw))
-        shift = (self.total_charge - s) / cnt.clamp(min=1)
+        # per-graph raw total and atom count in one segment-sum pass
+        r = raw.unsqueeze(-1)
+        both = _graph_totals(torch.cat([r, torch.ones_like(r)], dim=1), batch, num_graphs, trusted)
+        shift = (self.total_charge - both[:, 0]) / both[:, 1].clamp(min=1)
         return {"charge": raw + _PerGraph.apply(shift, batch)}

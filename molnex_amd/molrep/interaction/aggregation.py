@@ -5,7 +5,10 @@ weighted by a per-edge cutoff value, followed by an equivariant linear
 The sum is the ``molix::segment_sum`` HIP kernel over the targets' CSR (cutoff weights folded into
 the same pass, each node row summed in a fixed order and written once); the linear is
 ``EquivariantLinear`` on the block-linear kernel.  Edges are ``edge_index`` rows
-[source, target]."""
+[source, target].  Messages of another dtype than float32 (a float64 model) are summed by torch's
+``index_add`` on their device.  With ``n_nodes`` given there is no host synchronisation and the
+targets are trusted to lie in ``[0, n_nodes)``; without it the size is the largest node id + 1 and
+the ids are checked."""
 
 from __future__ import annotations
 
@@ -29,9 +32,15 @@ class MessageAggregation(nn.Module):
 
     def forward(self, messages: torch.Tensor, edge_index: torch.Tensor, edge_cutoff: torch.Tensor | None = None,
                 n_nodes: int | None = None) -> torch.Tensor:
-        if n_nodes is None:
+        trusted = n_nodes is not None
+        if not trusted:
             # the reference sizes the output by the largest node id in either column
             n_nodes = int(edge_index.max().item()) + 1 if edge_index.numel() else 0
         weights = edge_cutoff.reshape(-1) if (self.config.apply_cutoff and edge_cutoff is not None) else None
-        summed = torch.ops.molix.segment_sum(messages, edge_index[:, 1], int(n_nodes), weights)
+        target = edge_index[:, 1]
+        if messages.dtype == torch.float32 and messages.is_cuda:
+            summed = torch.ops.molix.segment_sum(messages, target, int(n_nodes), weights, not trusted)
+        else:
+            scaled = messages if weights is None else messages * weights.to(messages.dtype).unsqueeze(-1)
+            summed = messages.new_zeros(int(n_nodes), messages.shape[1]).index_add(0, target, scaled)
         return self.linear(summed)

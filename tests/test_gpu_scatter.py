@@ -120,3 +120,105 @@ def test_message_aggregation_vs_oracle(apply_cutoff):
         _close(gc, rc, 1e-5)
     else:
         assert gc is None
+
+
+def test_scatter_sum_other_dtypes():
+    """float64, half and integer src go to torch's scatter_add on the GPU (the fp32 kernel does
+    not compute them), with the reference's results."""
+    from molnex_amd.molix.F import batch_add, scatter_sum
+
+    g = torch.Generator().manual_seed(7)
+    idx = torch.randint(0, 9, (70,), generator=g)
+    src64 = torch.randn(70, 3, generator=g, dtype=torch.float64)
+    ref64 = torch.zeros(9, 3, dtype=torch.float64).index_add(0, idx, src64)
+    out64 = scatter_sum(src64.to(DEV), idx.to(DEV), 0, 9)
+    assert out64.dtype == torch.float64
+    assert torch.allclose(out64.cpu(), ref64, rtol=1e-14, atol=1e-14)
+    # along dim 1 with a 1-D index
+    src64t = src64.t().contiguous()
+    assert torch.allclose(scatter_sum(src64t.to(DEV), idx.to(DEV), 1, 9).cpu(), ref64.t(), rtol=1e-14, atol=1e-14)
+    counts = torch.randint(0, 5, (70,), generator=g)
+    outi = batch_add(counts.to(DEV), idx.to(DEV), 9)
+    assert outi.dtype == torch.int64
+    assert torch.equal(outi.cpu(), torch.zeros(9, dtype=torch.int64).index_add(0, idx, counts))
+    assert torch.equal(batch_add(counts.to(DEV), idx.to(DEV)).cpu()[: int(idx.max()) + 1],
+                       torch.zeros(9, dtype=torch.int64).index_add(0, idx, counts)[: int(idx.max()) + 1])
+    h = torch.randn(70, 4, generator=g).half()
+    outh = scatter_sum(h.to(DEV), idx.to(DEV), 0, 9)
+    assert outh.dtype == torch.float16
+    assert torch.allclose(outh.float().cpu(), torch.zeros(9, 4).index_add(0, idx, h.float()), atol=2e-2)
+
+
+def test_message_aggregation_float64():
+    from molnex_amd.molrep.interaction import MessageAggregation
+
+    torch.manual_seed(8)
+    irreps = "8x0e+8x1o"
+    blocks = [(8, 0, 1), (8, 1, -1)]
+    agg = MessageAggregation(irreps=irreps).to(DEV).double()
+    g = torch.Generator().manual_seed(9)
+    ei = torch.randint(0, 30, (400, 2), generator=g)
+    msg = torch.randn(400, 32, generator=g, dtype=torch.float64)
+    cut = torch.rand(400, generator=g, dtype=torch.float64)
+    out = agg(msg.to(DEV), ei.to(DEV), cut.to(DEV), n_nodes=30)
+    assert out.dtype == torch.float64
+    summed = torch.zeros(30, 32, dtype=torch.float64).index_add(0, ei[:, 1], msg * cut[:, None])
+    ref = mace_ref.linear(summed, agg.linear.linear.weight.detach().cpu(), blocks, blocks)
+    assert torch.allclose(out.cpu(), ref, rtol=1e-12, atol=1e-12)
+
+
+@pytest.mark.parametrize("pooling", ["sum", "mean"])
+def test_energy_aggregation_vs_fp64(pooling):
+    """Per-graph sum / mean of per-atom energies on the segment-sum kernel against an fp64
+    index_add (and a float64 model's energies through torch), empty graphs included."""
+    from molnex_amd.molpot import EnergyAggregation
+
+    g = torch.Generator().manual_seed(10)
+    batch = torch.sort(torch.randint(0, 12, (3000,), generator=g)).values
+    batch[batch == 5] = 6  # graph 5 has no atoms
+    e = torch.randn(3000, generator=g)
+    tot = torch.zeros(13, dtype=torch.float64).index_add(0, batch, e.double())
+    cnt = torch.zeros(13, dtype=torch.float64).index_add(0, batch, torch.ones(3000, dtype=torch.float64))
+    ref = tot if pooling == "sum" else tot / cnt.clamp(min=1)
+    agg = EnergyAggregation(pooling)
+    out = agg(e.to(DEV), batch.to(DEV), 13)
+    assert out.shape == (13,) and out.dtype == torch.float32
+    _close(out, ref, 1e-6)
+    assert float(out[5]) == 0.0
+    assert torch.equal(out, agg(e.to(DEV), batch.to(DEV), 13))  # fixed summation order
+    # num_graphs from the largest id (trailing graphs without atoms are not counted)
+    assert agg(e.to(DEV), batch.to(DEV)).shape == (int(batch.max()) + 1,)
+    out64 = agg(e.double().to(DEV), batch.to(DEV), 13)
+    assert out64.dtype == torch.float64 and torch.allclose(out64.cpu(), ref, rtol=1e-12, atol=1e-12)
+    # gradient: every atom of graph b receives dL/dE[b] (divided by the graph's count for mean)
+    eg = e.to(DEV).requires_grad_(True)
+    go = torch.randn(13, generator=g)
+    (ge,) = torch.autograd.grad(agg(eg, batch.to(DEV), 13), eg, go.to(DEV))
+    rg = go[batch] / (1.0 if pooling == "sum" else cnt.float()[batch])
+    assert torch.allclose(ge.cpu(), rg, rtol=1e-6, atol=1e-7)
+
+
+def test_aggregations_with_sizes_have_no_host_sync():
+    """With the sizes given, EnergyAggregation and MessageAggregation enqueue their work without a
+    device-to-host copy or synchronisation (torch's sync debug mode raises on one)."""
+    from molnex_amd.molpot import EnergyAggregation
+    from molnex_amd.molrep.interaction import MessageAggregation
+
+    g = torch.Generator().manual_seed(11)
+    batch = torch.sort(torch.randint(0, 4, (500,), generator=g)).values.to(DEV)
+    e = torch.randn(500, generator=g).to(DEV).requires_grad_(True)
+    agg = MessageAggregation(irreps="8x0e").to(DEV)
+    ei = torch.randint(0, 50, (300, 2), generator=g).to(DEV)
+    msg = torch.randn(300, 8, generator=g).to(DEV).requires_grad_(True)
+    cut = torch.rand(300, generator=g).to(DEV)
+    ea = EnergyAggregation("mean")
+    for sync_mode in (0, "error"):  # warm-up pass first (library load, lazy buffers)
+        torch.cuda.synchronize()
+        torch.cuda.set_sync_debug_mode(sync_mode)
+        try:
+            E = ea(e, batch, 4)
+            m = agg(msg, ei, cut, n_nodes=50)
+            ge, gm = torch.autograd.grad((E.sum(), m.sum()), (e, msg))
+        finally:
+            torch.cuda.set_sync_debug_mode(0)
+    assert torch.isfinite(ge).all() and torch.isfinite(gm).all()

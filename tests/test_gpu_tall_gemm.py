@@ -126,6 +126,37 @@ def test_silu_second_derivative_kernel(K):
         assert float(err.max()) <= 1e-5, (name, float(err.max()))
 
 
+def test_silu_second_derivative_offset_views(K):
+    """Views starting one float into their storage (not 16-byte aligned) take the scalar path and
+    agree bitwise with the aligned copies."""
+    g0 = torch.Generator(device=DEV).manual_seed(7)
+    base = [torch.randn(4099, device=DEV, generator=g0) for _ in range(3)]
+    views = [t[1:] for t in base]
+    assert all(v.data_ptr() % 16 for v in views)
+    dx, dg = K.silu_bwd2(*views)
+    ax, ag = K.silu_bwd2(*(v.clone() for v in views))
+    assert torch.equal(dx, ax) and torch.equal(dg, ag)
+
+
+def test_tall_tn_very_wide_row_stride(K):
+    """A column slice of a tensor whose rows are 2^25 + 128 floats apart (beyond the kernel's row
+    stride bound) is copied to contiguous rows instead of raising."""
+    g0 = torch.Generator(device=DEV).manual_seed(8)
+    rows = 16
+    wide = torch.empty(rows, (1 << 25) + 128, device=DEV)
+    a = wide[:, 64:128]
+    a.copy_(torch.randn(rows, 64, device=DEV, generator=g0))
+    b = torch.randn(rows, 32, device=DEV, generator=g0)
+    assert a.stride(0) >= 1 << 25
+    ref = a.double().t() @ b.double()
+    out = K.tall_tn(a, b)
+    _close(out, ref, "wide-stride tall_tn", 1e-6)
+    out2, cs = K.tall_tn_colsum(a, b)
+    _close(out2, ref, "wide-stride tall_tn_colsum", 1e-6)
+    _close(cs, a.double().sum(0), "wide-stride column sums", 1e-6)
+    del wide
+
+
 def test_radial_mlp_hidden_second_order_many_rows():
     """RadialWeightMLP's hidden stack over many rows when training (Linears on tall_tn, SiLUs with the
     fused second derivative) against the same module in float64: a force-style loss on the input

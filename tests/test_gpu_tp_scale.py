@@ -5,7 +5,7 @@ Checked on samples against the fp64 oracle evaluated on exactly the edges each v
 the outputs of sampled receivers and the weight / harmonic gradients of their edges, and the
 feature gradient of sampled senders (all their outgoing edges).  Over the whole graph, the
 receiver-walked backward (grad_x by atomics) must agree with the sender-walked one (no atomics).
-Tolerance as in test_gpu_tp.py: norm-wise relative 1e-5, max-abs 1e-4 x RMS.
+Tolerance as in test_gpu_tp.py: norm-wise relative 1e-5, max-abs 1e-5 x RMS.
 """
 
 import numpy as np
