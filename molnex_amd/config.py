@@ -35,6 +35,13 @@ class _Config:
     # inputs are bit-identical (a neighbor list's pairs), and the tensor product reads each pair's
     # weights for both directions (molix::radial_tp_pairs); graphs without such a pairing run per edge
     paired_radial: bool = True
+    # With paired_radial: True -- every new radial-features tensor on a graph (new positions) is
+    # checked on the device to keep its pairs bit-identical, with one host synchronisation to read
+    # the verdict (a failed check rebuilds the pairing); False -- the pairing found when the graph
+    # was first used is trusted for later positions.  That holds whenever the bond vectors of the
+    # two directions are exact negations, as molix::bond_vectors makes them from a neighbor list's
+    # antisymmetric shifts; it keeps an energy + forces step free of host synchronisation.
+    verify_pairs: bool = True
 
 
 config = _Config()

@@ -9,7 +9,9 @@
 // contiguous floats per lane when the row length allows 16-byte loads), the
 // segment's rows are walked in CSR order (ascending row id within a segment)
 // with four rows' loads in flight, and each output row is written once: no
-// atomics, a fixed summation order (bitwise reproducible).
+// atomics, a fixed summation order (bitwise reproducible).  Few long segments
+// (per-graph sums over large systems) take a workgroup each instead, whose
+// threads split the rows and combine them by a fixed tree (k_segment_sum_wg).
 //
 // Backward: grad_values[r][:] = w[r] * grad_out[index[r]][:] (a gather) and
 // grad_w[r] = <values[r], grad_out[index[r]]> (a dot product per row), one
@@ -88,6 +90,53 @@ __global__ void __launch_bounds__(kSegThreads) k_segment_sum(const float* __rest
     } else {
         out[seg * dim + col] = acc[0];
     }
+}
+
+// Few long segments (per-graph sums of a batch of large systems): one workgroup of 1024 threads per
+// (segment, block of DP columns).  Thread t owns column t % DP of the block and row slot t / DP; the
+// slots walk the segment's rows strided by their count, each adding its rows in ascending CSR
+// order (four loads in flight), and the slots are then combined by a fixed binary tree in LDS:
+// no atomics, a fixed summation order.
+constexpr int kWgThreads = 1024;
+
+template <int DP>
+__global__ void __launch_bounds__(kWgThreads) k_segment_sum_wg(const float* __restrict__ values, int64_t dim,
+                                                               const int32_t* __restrict__ row_ptr,
+                                                               const int32_t* __restrict__ perm,
+                                                               const float* __restrict__ w, int64_t col_blocks,
+                                                               float* __restrict__ out) {
+    constexpr int kSlots = kWgThreads / DP;
+    __shared__ float red[kWgThreads];
+    const int64_t seg = blockIdx.x / col_blocks;
+    const int64_t col = (blockIdx.x % col_blocks) * DP + threadIdx.x % DP;
+    const int slot = threadIdx.x / DP;
+    const bool active = col < dim;
+    const int b = row_ptr[seg], e = row_ptr[seg + 1];
+    float acc = 0.f;
+    int k = b + slot;
+    for (; k + 3 * kSlots < e; k += 4 * kSlots) {
+        float v[4], ws[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int row = perm[k + u * kSlots];
+            ws[u] = w ? w[row] : 1.f;
+            v[u] = active ? values[int64_t(row) * dim + col] : 0.f;
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) acc = fmaf(ws[u], v[u], acc);
+    }
+    for (; k < e; k += kSlots) {
+        const int row = perm[k];
+        acc = fmaf(w ? w[row] : 1.f, active ? values[int64_t(row) * dim + col] : 0.f, acc);
+    }
+    red[threadIdx.x] = acc;
+    __syncthreads();
+#pragma unroll
+    for (int half = kSlots / 2; half > 0; half >>= 1) {
+        if (slot < half) red[threadIdx.x] += red[threadIdx.x + half * DP];
+        __syncthreads();
+    }
+    if (slot == 0 && active) out[seg * dim + col] = red[threadIdx.x];
 }
 
 __device__ __forceinline__ float wave_sum(float v) {
@@ -249,6 +298,27 @@ int mnx_segment_sum_f32(const float* values, int64_t num_rows, int32_t dim, cons
     MNX_REQUIRE(num_rows >= 0 && num_segments >= 0 && dim >= 0, "sizes out of range");
     if (num_segments == 0 || dim == 0) return MNX_OK;
     MNX_REQUIRE(row_ptr && out && (num_rows == 0 || (values && perm)), "null pointer argument");
+    // few segments averaging 64 rows or more (e.g. one graph of a large system): a workgroup per
+    // segment and column block, since one wavefront per segment would leave the GPU nearly idle
+    int dp = 1;
+    while (dp < dim && dp < kWgThreads) dp *= 2;
+    const int64_t wg_blocks = num_segments * ceil_div(int64_t(dim), int64_t(dp));
+    if (wg_blocks <= 4096 && num_rows >= 64 * num_segments) {
+        const int64_t cb = ceil_div(int64_t(dim), int64_t(dp));
+        const dim3 g = dim3(unsigned(wg_blocks));
+#define MNX_SEG_WG(D)                                                                                      \
+    case D:                                                                                                \
+        hipLaunchKernelGGL(k_segment_sum_wg<D>, g, dim3(kWgThreads), 0, stream, values, int64_t(dim), row_ptr, \
+                           perm, weights, cb, out);                                                       \
+        break;
+        switch (dp) {
+            MNX_SEG_WG(1) MNX_SEG_WG(2) MNX_SEG_WG(4) MNX_SEG_WG(8) MNX_SEG_WG(16) MNX_SEG_WG(32) MNX_SEG_WG(64)
+            MNX_SEG_WG(128) MNX_SEG_WG(256) MNX_SEG_WG(512) MNX_SEG_WG(1024)
+        }
+#undef MNX_SEG_WG
+        MNX_CHECK_LAUNCH();
+        return MNX_OK;
+    }
     const bool vec = dim % 4 == 0 && reinterpret_cast<uintptr_t>(values) % 16 == 0 &&
                      reinterpret_cast<uintptr_t>(out) % 16 == 0;
     const int64_t per_block = vec ? kWave * 4 : kWave;

@@ -2050,8 +2050,6 @@ def _bc_bwd(ctx, grad):
 bessel_cutoff.register_autograd(_bc_bwd, setup_context=_bc_setup)
 
 
-# second-order formulas (autograd of the backward ops): registered on import
-from . import second_order  # noqa: E402,F401
 
 
 # ---------------------------------------------------------------------------
@@ -2129,3 +2127,7 @@ def _seg_backward(ctx, grad):
 
 
 segment_sum.register_autograd(_seg_backward, setup_context=_seg_setup)
+
+
+# second-order formulas (autograd of the backward ops): registered on import, after every op above
+from . import second_order  # noqa: E402,F401

@@ -56,12 +56,14 @@ class EdgeGraph:
         """The undirected pairs of this graph whose two edges have bit-identical rows of ``feats``
         (``kernels.EdgePairs``; None when some edge has no such partner).  Built on the first
         features tensor; for later ones (new positions on the same edge list) the pairing is kept
-        if the features of every pair still agree, else rebuilt.  One host synchronisation per new
-        features tensor."""
+        if the features of every pair still agree, else rebuilt: one host synchronisation per new
+        features tensor, or none with ``config.verify_pairs = False``, which trusts the first
+        pairing for later positions."""
         p = self._pairs
         if p is None or p[0] is not feats or p[1] != feats._version:
             prev = p[2] if p is not None else None
-            if prev is not None and feats.shape[0] == prev.wrow.shape[0] and prev.holds_for(feats):
+            if prev is not None and feats.shape[0] == prev.wrow.shape[0] and (
+                    not config.verify_pairs or prev.holds_for(feats)):
                 built = prev
             else:
                 built = K.EdgePairs.build(self.edge_index, self.num_nodes, self.row_ptr, self.perm, self.senders,

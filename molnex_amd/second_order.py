@@ -425,3 +425,40 @@ def _sc2_bwd(ctx, ggx, ggw):
 
 
 K.symmetric_contraction_backward.register_autograd(_sc2_bwd, setup_context=_sc2_setup)
+
+
+# ---------------------------------------------------------------------------
+# segment sums (per-graph energies, message aggregation)
+# ---------------------------------------------------------------------------
+# segment_sum_backward: gv[r] = w[r] g[idx[r]], gw[r] = <g[idx[r]], v[r]>; both linear in g, so
+# with the seeds (ggv, ggw):
+#   dL2/dg[s] = sum_{idx[r] = s} (w[r] ggv[r] + ggw[r] v[r])   (two segment sums)
+#   dL2/dv[r] = ggw[r] g[idx[r]]                               (the gather with weights ggw)
+#   dL2/dw[r] = <ggv[r], g[idx[r]]>                            (the per-row dot with values ggv)
+
+def _seg2_setup(ctx, inputs, output):
+    grad, index, values, weights, need_values, need_weights = inputs
+    ctx.save_for_backward(grad, index, values, weights)
+    ctx.num_segments = grad.shape[0]
+
+
+def _seg2_bwd(ctx, ggv, ggw):
+    grad, index, values, weights = ctx.saved_tensors
+    ng, _, nv, nw = (list(ctx.needs_input_grad) + [False] * 4)[:4]
+    has_v = ggv is not None and ggv.numel() > 0
+    has_w = ggw is not None and ggw.numel() > 0
+    dg = dv = dw = None
+    if ng:
+        dg = grad.new_zeros(grad.shape)
+        if has_v:
+            dg = dg + K.segment_sum(ggv.reshape(values.shape).contiguous(), index, ctx.num_segments, weights, False)
+        if has_w:
+            dg = dg + K.segment_sum(values, index, ctx.num_segments, ggw.reshape(-1).contiguous(), False)
+    if nv and has_w:
+        dv = K.segment_sum_backward(grad, index, values, ggw.reshape(-1).contiguous(), True, False)[0]
+    if nw and weights is not None and has_v:
+        dw = K.segment_sum_backward(grad, index, ggv.reshape(values.shape).contiguous(), weights, False, True)[1]
+    return dg, None, dv, dw, None, None
+
+
+K.segment_sum_backward.register_autograd(_seg2_bwd, setup_context=_seg2_setup)

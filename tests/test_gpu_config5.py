@@ -251,3 +251,40 @@ def test_config5_full_size_properties(literal):
     print(f"finite differences at {len(atoms)} atoms: rel err {rel:.2e} (|F| {np.linalg.norm(fd):.3g}); "
           f"along a random +-1 direction of all atoms: {fu:.6g} vs F.u {ref_u:.6g}, rel err {rel_u:.2e}")
     assert rel <= 1e-2 and rel_u <= 1e-2
+
+
+@pytest.mark.parametrize("literal", [True, False], ids=["literal", "as_coded"])
+def test_energy_forces_step_has_no_host_sync(literal):
+    """A whole MACE + ChargeHead + PME energy + forces step at new positions on a known graph, with
+    the graph count given and the first step's edge pairing trusted (config.verify_pairs = False),
+    enqueues without a device-to-host copy or synchronisation (torch's sync debug mode raises on
+    one); its energy and forces agree with the same step under the per-step pairing check."""
+    from molnex_amd.config import config
+    from molnex_amd.molpot import PMEPotential
+
+    n, C = 400, 32
+    pos, L = lattice(n, seed=5)
+    Z = np.random.default_rng(6).integers(0, 10, n)
+    model, head = build_models(10, C, literal, 30.0, seed=1)
+    pme = PMEPotential(alpha=ALPHA, grid=(32, 32, 32), order=ORDER, cutoff=RC).to(DEV)
+    system = System(pos, L, Z, model, head, pme)
+    pos_t = torch.tensor(pos, device=DEV)
+    moved = pos_t + 0.01 * torch.randn(pos_t.shape, generator=torch.Generator(device=DEV).manual_seed(7),
+                                       device=DEV)
+    prev = config.verify_pairs
+    try:
+        config.verify_pairs = False
+        system.energy_forces(pos_t)  # first step on the graph: CSR, pairing, lazy buffers
+        torch.cuda.synchronize()
+        torch.cuda.set_sync_debug_mode("error")
+        try:
+            e, f, *_ = system.energy_forces(moved)
+        finally:
+            torch.cuda.set_sync_debug_mode(0)
+        config.verify_pairs = True
+        e2, f2, *_ = system.energy_forces(moved.clone())
+    finally:
+        config.verify_pairs = prev
+    assert torch.isfinite(f).all()
+    assert abs(float(e) - float(e2)) <= 1e-6 * abs(float(e2))
+    assert float((f - f2).norm() / f2.norm()) <= 1e-6

@@ -7,6 +7,7 @@ import numpy as np
 import pytest
 import torch
 
+import molnex_amd.kernels  # noqa: F401  (registers torch.ops.molix.*)
 from oracle import equivariant as O
 from oracle import mace_ref
 
@@ -22,14 +23,19 @@ def _close(got, ref, tol=1e-6):
     assert (got - ref).norm() / den <= tol, float((got - ref).norm() / den)
 
 
-@pytest.mark.parametrize("rows,dim,num", [(1000, 128, 37), (777, 3, 50), (4096, 130, 9), (1, 8, 1), (300, 2048, 64)])
+@pytest.mark.parametrize("rows,dim,num", [(1000, 128, 37), (777, 3, 50), (4096, 130, 9), (1, 8, 1), (300, 2048, 64),
+                                          # few long segments (a workgroup per segment and column block)
+                                          (50000, 1, 1), (50000, 2, 1), (20000, 300, 3), (5000, 2048, 2),
+                                          (70000, 5, 16)])
 def test_segment_sum_matches_oracle(rows, dim, num):
     g = torch.Generator().manual_seed(rows + dim)
     v = torch.randn(rows, dim, generator=g)
     idx = torch.randint(0, num, (rows,), generator=g)
     w = torch.rand(rows, generator=g)
     out = torch.ops.molix.segment_sum(v.to(DEV), idx.to(DEV), num, w.to(DEV))
-    _close(out, O.scatter_add(idx.numpy(), (v.double() * w.double()[:, None]).numpy(), num))
+    # fp32 sums of thousands of rows per segment carry ~1e-6 of rounding: the 1e-5 contract there
+    tol = 1e-6 if rows <= 1000 * num else 1e-5
+    _close(out, O.scatter_add(idx.numpy(), (v.double() * w.double()[:, None]).numpy(), num), tol)
     out2 = torch.ops.molix.segment_sum(v.to(DEV), idx.to(DEV), num, w.to(DEV))
     assert torch.equal(out, out2)  # fixed summation order
 

@@ -65,6 +65,25 @@ def test_bond_vectors_second_order(ops):
     assert _rel(dg, s[ei[:, 1]] - s[ei[:, 0]]) <= 1e-6
 
 
+def test_segment_sum_second_order(ops):
+    """Weighted segment sum: second derivatives of <s, (gv, gw)> with respect to the output
+    gradient g, the values and the weights against float64 autograd of index_add."""
+    g0 = torch.Generator().manual_seed(12)
+    R, D, S = 700, 5, 31
+    idx = torch.randint(0, S, (R,), generator=g0)
+    v, w = torch.randn(R, D, generator=g0, dtype=torch.float64), torch.rand(R, generator=g0, dtype=torch.float64)
+    g = torch.randn(S, D, generator=g0, dtype=torch.float64)
+    sv, sw = torch.randn(R, D, generator=g0, dtype=torch.float64), torch.randn(R, generator=g0, dtype=torch.float64)
+    vd, wd, gd = (t.float().to(DEV).requires_grad_(True) for t in (v, w, g))
+    gv, gw = ag.grad(ops.segment_sum(vd, idx.to(DEV), S, wd), (vd, wd), gd, create_graph=True)
+    dv, dw, dg = ag.grad((gv * sv.float().to(DEV)).sum() + (gw * sw.float().to(DEV)).sum(), (vd, wd, gd))
+    v64, w64, g64 = (t.clone().requires_grad_(True) for t in (v, w, g))
+    out = torch.zeros(S, D, dtype=torch.float64).index_add(0, idx, v64 * w64[:, None])
+    gv64, gw64 = ag.grad(out, (v64, w64), g64, create_graph=True)
+    rv, rw, rg = ag.grad((gv64 * sv).sum() + (gw64 * sw).sum(), (v64, w64, g64))
+    assert _rel(dv, rv) <= 1e-6 and _rel(dw, rw) <= 1e-6 and _rel(dg, rg) <= 1e-6
+
+
 def test_edge_weights_second_order():
     import molnex_amd.kernels as K
 
