@@ -566,6 +566,32 @@ int mnx_tp_weight_grad_batched_f32(int32_t config, int32_t C, const float* x, co
                                    float* grad_h, mnx_stream_t stream);
 
 /* ------------------------------------------------------------------------ */
+/* Tensor-product backward fused with the output layer's input gradient      */
+/* (replaces the TP backward's grad_w output plus mnx_edge_weights_bwd_f32;  */
+/* the reference lets autograd write the per-edge weight gradient of        */
+/* cuet.ChannelWiseTensorProduct, tensor_product.py:72-79,101-111, and read */
+/* it back in the last Linear of RadialWeightMLP, radial_mlp.py:76-82):     */
+/*   grad_x, grad_Y as mnx_tp_bwd_rows_f32 (grad_x accumulated: zero it),  */
+/*   grad_h[e][k] = sum_n gw[e][n] W[n][k]   (grad_h [E][K] overwritten),   */
+/* with gw formed by the receiver walk and multiplied on the matrix cores   */
+/* from LDS, never written to memory.  W: the layer's weight                */
+/* [num_paths*C][K] fp32 (nn.Linear layout).  ny: the config's harmonics    */
+/* count (mnx_tp_config_info).  Supported when mnx_tp_bwd_gh_supported      */
+/* (C a multiple of 64, K in {64, 128}, every path group's W slice fits     */
+/* the LDS); the workspace holds the per-(group, channel block) partial     */
+/* rows of grad_h (summed in a fixed order by a last kernel) and W's        */
+/* pre-split fragments.  grad_Y may be NULL. */
+int mnx_tp_bwd_gh_supported(int32_t config, int32_t channels, int32_t K);
+size_t mnx_tp_bwd_gh_workspace_bytes(int32_t config, int32_t channels, int64_t num_edges, int32_t K,
+                                     int32_t ny);
+int mnx_tp_bwd_gh_rows_f32(int32_t config, int32_t channels, const float* x, const float* Y, const float* w,
+                           const int32_t* wrow, const float* grad_out, const int32_t* row_ptr,
+                           const int32_t* perm, const int32_t* senders_sorted, int64_t num_nodes,
+                           int64_t num_edges, int32_t ny, const float* W, int32_t K, float* grad_x,
+                           float* grad_Y, float* grad_h, void* workspace, size_t workspace_bytes,
+                           mnx_stream_t stream);
+
+/* ------------------------------------------------------------------------ */
 /* Channelwise tensor product + scatter for irreps outside the compiled      */
 /* configurations, driven by a path table (replaces the same cuet call,      */
 /* cuet.ChannelWiseTensorProduct(irreps_in1, irreps_sh, irreps_out,          */

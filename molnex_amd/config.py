@@ -30,6 +30,15 @@ class _Config:
     # for inputs with l >= 1 (its per-edge contraction is VALU-bound); None: scalar-input products
     # only (a first interaction layer); True: every product
     fused_weight_grad: bool | None = False
+    # True: with the radial MLP run once per undirected pair (paired_radial, eval mode), the tensor
+    # product's backward and the output layer's input gradient run as one pass
+    # (molix::tp_scatter_backward_gh: the per-edge weight gradient is multiplied on the matrix cores
+    # as it is formed, never written) wherever a kernel exists for the product and hidden width.
+    # False (default): on MI355X the fused pass is slower than the two kernels it replaces at every
+    # measured shape (config 3: 30.3-31.3 ms against 27.4-27.8 ms; the literal config-5 step 29.7-
+    # 30.6 ms against 27.6-28.7 ms), since its LDS staging and per-phase barriers cost the receiver
+    # walk more occupancy and issue time than the 30.8 GB weight-gradient stream it saves
+    tp_bwd_fused: bool = False
     # True: where the radial MLP's parameters are frozen and no second derivatives are taken (eval
     # mode), the MLP and its output layer run once per undirected pair of opposite edges whose radial
     # inputs are bit-identical (a neighbor list's pairs), and the tensor product reads each pair's

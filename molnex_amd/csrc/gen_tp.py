@@ -576,6 +576,292 @@ def gen_bwd_sender(cfg: Cfg, sg: int, ps, first: bool) -> str:
 
 
 
+# ---------------------------------------------------------------------------
+# Backward fused with the radial MLP output layer's input gradient
+#   grad_h[e][k] = sum_{p, c} gw[e][p][c] W[p*C + c][k]
+# without writing gw.  Persistent workgroups of NWAVE wavefronts; each wavefront
+# walks an equal share of the CSR slots (receivers change along the way: the
+# receiver's output gradient is folded into v again), one channel block of 64
+# per lane row (blockIdx.y).  Every SW edges per wavefront (a phase) the
+# workgroup has SLOTS = NWAVE * SW edges' gw rows (this group's P paths x 64
+# channels, fp32) in LDS; after a barrier each wavefront multiplies 16-row x
+# 16-column tiles of them by the group's slice of W (pre-split fp16 fragments,
+# LDS-resident for the whole kernel) on v_mfma_f32_16x16x32_f16, three products
+# per k-step (the split-fp16 scheme of edge_weights.hip: rows scaled by a power
+# of two from their largest magnitude, W columns likewise), and writes the tile
+# into a partial grad_h row per (group, channel block) at the edge's CSR slot;
+# a second barrier frees the staging for the next phase.
+# ---------------------------------------------------------------------------
+
+FUSED_LDS_BYTES = 160 * 1024
+FUSED_KH = (64, 128)
+
+
+def fused_lds(P: int, KH: int, nwave: int, sw: int) -> int:
+    """LDS bytes: the W slice, the staged gw rows (two fp16 planes, rows padded by 16 bytes) and
+    per-row exponents and CSR slots."""
+    slots = nwave * sw
+    return P * KH * 256 + 2 * slots * (P * 64 + 8) * 2 + slots * 8
+
+
+def fused_shape(ps, KH: int):
+    """(NWAVE, SW) of the fused backward for a group ``ps`` of paths and a hidden width KH, or None
+    when the group's W slice and the staging do not fit the LDS.  Groups whose folded output
+    gradient is small (at most 30 values per lane) fit four wavefronts per SIMD without spilling:
+    sixteen per workgroup; larger ones eight."""
+    P = len(ps)
+    for nw in ((16, 8) if _v_count(ps) <= 30 else (8,)):
+        # as many staged rows (slots) per phase as the LDS holds
+        for slots in range(128, 7, -8):
+            if slots % nw == 0 and fused_lds(P, KH, nw, slots // nw) <= FUSED_LDS_BYTES:
+                return nw, slots // nw
+    return None
+
+
+def gen_bwd_fused(cfg: Cfg, g: int) -> str:
+    ps = cfg.groups[g]
+    P = len(ps)
+    xs, ys, outs = _group_layout(ps)
+    xi = {c: i for i, c in enumerate(xs)}
+    oi = {c: i for i, c in enumerate(outs)}
+    V = 1
+    while V < cfg.NY:
+        V *= 2
+    L = []
+    a = L.append
+    name = f"tp_bwf_c{cfg.idx}_g{g}"
+    a(f"template <int NWAVE, int SW, int KH>\n__global__ void __launch_bounds__(64 * NWAVE, NWAVE / 4) {name}("
+      "const float* __restrict__ x, const float* __restrict__ Y, const float* __restrict__ w, "
+      "const float* __restrict__ gout, const int32_t* __restrict__ row_ptr, const int32_t* __restrict__ perm, "
+      "const int32_t* __restrict__ snd, const int32_t* __restrict__ wrow, int64_t N, int64_t E, int C, "
+      "float* __restrict__ gx, float* __restrict__ gyp, int npart, int pbase, const f16x8* __restrict__ wfrag, "
+      "const float* __restrict__ kscale, float* __restrict__ hpart) {")
+    a(f"  constexpr int P = {P}, SLOTS = NWAVE * SW, AST = P * 64 + 8, KSTEPS = P * 2, CT = KH / 16;")
+    a("  extern __shared__ __align__(16) unsigned char smem[];")
+    a("  f16x8* __restrict__ sW = reinterpret_cast<f16x8*>(smem);  // [CT][KSTEPS][2][64]")
+    a("  _Float16* __restrict__ sA = reinterpret_cast<_Float16*>(smem + P * KH * 256);  // [2][SLOTS][AST]")
+    a("  int* __restrict__ sE = reinterpret_cast<int*>(sA + 2 * SLOTS * AST);  // row exponents")
+    a("  int* __restrict__ sT = sE + SLOTS;  // CSR slot of each row, -1 if none")
+    a("  const int lane = threadIdx.x & 63;")
+    a("  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);")
+    a("  const int cb = blockIdx.y;")
+    a("  const int cc = cb * 64 + lane;")
+    a("  {  // this (group, channel block)'s W fragments, resident for the whole kernel")
+    a("    constexpr int NV = P * KH * 16;")
+    a("    const f16x8* __restrict__ src = wfrag + int64_t(cb) * NV;")
+    a("    for (int i = threadIdx.x; i < NV; i += 64 * NWAVE) sW[i] = src[i];")
+    a("  }")
+    a("  // this wavefront's share of the CSR slots; each XCD walks one contiguous range")
+    a("  const int64_t nwg = gridDim.x;")
+    a("  const int64_t lb = (blockIdx.x & 7) * (nwg >> 3) + (blockIdx.x >> 3);")
+    a("  const int64_t nwaves = nwg * NWAVE, wid = lb * NWAVE + wave;")
+    a("  const int t0 = int(wid * E / nwaves), t1 = int((wid + 1) * E / nwaves);")
+    a("  const int nph = int(((E + nwaves - 1) / nwaves + SW - 1) / SW);")
+    a(f"  const int64_t XS = int64_t({cfg.NX}) * C, WS = int64_t({cfg.NP}) * C;")
+    a("  // receiver of slot t0: the last n with row_ptr[n] <= t0")
+    a("  int n = 0, rend = 0;")
+    a("  if (t0 < t1) {")
+    a("    int lo = 0, hi = int(N);")
+    a("    while (hi - lo > 1) { const int mid = (lo + hi) >> 1; if (row_ptr[mid] <= t0) lo = mid; else hi = mid; }")
+    a("    n = lo; rend = row_ptr[n + 1];")
+    a("  }")
+    # folded output gradient of the current receiver
+    vnames = {}
+    nv = _v_count(ps)
+    a(f"  float v[{nv}];")
+
+    def emit_fold(indent):
+        a(f"{indent}{{")
+        a(f"{indent}  const float* __restrict__ gn = gout + int64_t(n) * {cfg.NO} * C;")
+        a(f"{indent}  float gv[{len(outs)}];")
+        for c in outs:
+            a(f"{indent}  gv[{oi[c]}] = gn[{c} * C + cc];")
+        vi = 0
+        for j, p in enumerate(ps):
+            c = p["c"]
+            for m1 in range(2 * p["l1"] + 1):
+                for m2 in range(2 * p["l2"] + 1):
+                    terms = [(m3, c[m1, m2, m3]) for m3 in range(2 * p["l3"] + 1) if abs(c[m1, m2, m3]) > EPS]
+                    if not terms:
+                        continue
+                    expr = f"{f32(terms[0][1])} * gv[{oi[p['o3'] + terms[0][0]]}]"
+                    for m3, val in terms[1:]:
+                        expr = f"fmaf({f32(val)}, gv[{oi[p['o3'] + m3]}], {expr})"
+                    a(f"{indent}  v[{vi}] = {expr};")
+                    vnames[(j, m1, m2)] = vi
+                    vi += 1
+        a(f"{indent}}}")
+
+    a(f"#pragma unroll\n  for (int i = 0; i < {nv}; ++i) v[i] = 0.f;")
+    a("  if (t0 < t1)")
+    emit_fold("  ")
+    # prefetch pipeline over [t0, t1)
+    a("  int ne = 0, ns = 0, nw = 0, ie = 0, is = 0, iw = 0;")
+    a("  " + " ".join(f"float ny{c} = 0.f;" for c in ys))
+    a(f"  float nxv[1][{len(xs)}], nwv[1][{len(ps)}];")
+    a("  if (t0 < t1) {")
+    _emit_ids(a, "    ", "t0", ("ne", "ns", "nw"))
+    _emit_prefetch_c(a, cfg, ps, xs, ys, xi, "    ")
+    a("  }")
+    a("  if (t0 + 1 < t1) {")
+    _emit_ids(a, "    ", "t0 + 1")
+    a("  }")
+    a("  int t = t0;")
+    a("  for (int ph = 0; ph < nph; ++ph) {")
+    a("    for (int i = 0; i < SW; ++i) {")
+    a("      const int slot = wave * SW + i;")
+    a("      _Float16* __restrict__ arow = sA + slot * AST;")
+    a("      if (t >= t1) {")
+    a("        if (lane == 0) { sT[slot] = -1; sE[slot] = 0; }")
+    a("        continue;")
+    a("      }")
+    a("      if (t == rend) {  // next receiver (skipping empty ones): fold its output gradient")
+    a("        do { ++n; rend = row_ptr[n + 1]; } while (rend == t);")
+    emit_fold("        ")
+    a("      }")
+    a("      const int e = ne, s = ns;")
+    a("      " + " ".join(f"const float y{c} = ny{c};" for c in ys))
+    a(f"      float xv[{len(xs)}], wv[{len(ps)}];")
+    a(f"#pragma unroll\n      for (int q = 0; q < {len(xs)}; ++q) xv[q] = nxv[0][q];")
+    a(f"#pragma unroll\n      for (int q = 0; q < {len(ps)}; ++q) wv[q] = nwv[0][q];")
+    a("      if (t + 1 < t1) {")
+    a("        ne = ie; ns = is; nw = iw;")
+    _emit_prefetch_c(a, cfg, ps, xs, ys, xi, "        ")
+    a("        if (t + 2 < t1) {")
+    _emit_ids(a, "          ", "t + 2")
+    a("        }")
+    a("      }")
+    a(f"      float gy[{V}];")
+    a(f"#pragma unroll\n      for (int q = 0; q < {V}; ++q) gy[q] = 0.f;")
+    a(f"      float gxl[{len(xs)}], gwv[{P}];")
+    for c in xs:
+        a(f"      gxl[{xi[c]}] = 0.f;")
+    for j, p in enumerate(ps):
+        n1, n2 = 2 * p["l1"] + 1, 2 * p["l2"] + 1
+        for m1 in range(n1):
+            ts = [m2 for m2 in range(n2) if (j, m1, m2) in vnames]
+            if not ts:
+                continue
+            expr = f"y{p['o2'] + ts[0]} * v[{vnames[(j, m1, ts[0])]}]"
+            for m2 in ts[1:]:
+                expr = f"fmaf(y{p['o2'] + m2}, v[{vnames[(j, m1, m2)]}], {expr})"
+            a(f"      const float u{j}_{m1} = {expr};")
+            a(f"      gxl[{xi[p['o1'] + m1]}] = fmaf(wv[{j}], u{j}_{m1}, gxl[{xi[p['o1'] + m1]}]);")
+        svals = []
+        for m2 in range(n2):
+            ts = [m1 for m1 in range(n1) if (j, m1, m2) in vnames]
+            if not ts:
+                continue
+            expr = f"xv[{xi[p['o1'] + ts[0]]}] * v[{vnames[(j, ts[0], m2)]}]"
+            for m1 in ts[1:]:
+                expr = f"fmaf(xv[{xi[p['o1'] + m1]}], v[{vnames[(j, m1, m2)]}], {expr})"
+            a(f"      const float s{j}_{m2} = {expr};")
+            a(f"      gy[{p['o2'] + m2}] = fmaf(wv[{j}], s{j}_{m2}, gy[{p['o2'] + m2}]);")
+            svals.append(m2)
+        if svals:
+            expr = f"y{p['o2'] + svals[0]} * s{j}_{svals[0]}"
+            for m2 in svals[1:]:
+                expr = f"fmaf(y{p['o2'] + m2}, s{j}_{m2}, {expr})"
+        else:
+            expr = "0.f"
+        a(f"      gwv[{j}] = {expr};")
+    a("      if (gx) {")
+    a("        float* __restrict__ gxs = gx + int64_t(s) * XS;")
+    for c in xs:
+        a(f"        atomicAdd(gxs + {c} * C + cc, gxl[{xi[c]}]);")
+    a("      }")
+    a("      if (gyp) {")
+    a(f"        float r = wave_reduce_scatter<{V}>(gy, lane);")
+    a(f"        const int comp = reduce_scatter_index<{V}>(lane);")
+    a(f"        if ((lane & (64 / {V} - 1)) == 0 && comp < {cfg.NY}) "
+      f"gyp[(int64_t(e) * npart + pbase + cb) * {cfg.NY} + comp] = r;")
+    a("      }")
+    a("      // gw row of this edge into the staging, scaled by the row's power of two and split")
+    a("      // into two fp16 parts (the matrix-core operand planes)")
+    a(f"      float m = fabsf(gwv[0]);")
+    a(f"#pragma unroll\n      for (int q = 1; q < {P}; ++q) m = fmaxf(m, fabsf(gwv[q]));")
+    a("      const int ex = ew_exp(wave_max(m));")
+    a("      const float sc = ldexpf(1.f, -ex);")
+    a(f"#pragma unroll\n      for (int q = 0; q < {P}; ++q) {{")
+    a("        const float v = gwv[q] * sc;")
+    a("        const _Float16 h0 = (_Float16)v;")
+    a("        arow[q * 64 + lane] = h0;")
+    a("        arow[SLOTS * AST + q * 64 + lane] = (_Float16)(v - (float)h0);")
+    a("      }")
+    a("      if (lane == 0) { sT[slot] = t; sE[slot] = ex; }")
+    a("      ++t;")
+    a("    }")
+    a("    __syncthreads();")
+    a("    fused_gh_tiles<P, NWAVE, SW, KH>(sW, sA, sE, sT, kscale, hpart + int64_t(cb) * E * KH, lane, wave);")
+    a("    __syncthreads();")
+    a("  }")
+    a("}")
+    return "\n".join(L)
+
+
+def _emit_prefetch_c(a, cfg, ps, xs, ys, xi, indent):
+    """_emit_prefetch for one channel per lane, channel ``cc`` (no guards: C % 64 == 0)."""
+    a(f"{indent}{{")
+    a(f"{indent}  const float* __restrict__ Yn = Y + int64_t(ne) * {cfg.NY};")
+    for c in ys:
+        a(f"{indent}  ny{c} = Yn[{c}];")
+    a(f"{indent}  const float* __restrict__ xn = x + int64_t(ns) * XS;")
+    a(f"{indent}  const float* __restrict__ wn = w + int64_t(nw) * WS;")
+    for c in xs:
+        a(f"{indent}  nxv[0][{xi[c]}] = xn[{c} * C + cc];")
+    for j, p in enumerate(ps):
+        a(f"{indent}  nwv[0][{j}] = __builtin_nontemporal_load(wn + {p['k']} * C + cc);")
+    a(f"{indent}}}")
+
+
+def fused_configs():
+    """(config index, group, KH, NWAVE, SW) of every fused backward instantiation."""
+    out = []
+    for i, c in enumerate(config_list()):
+        cfg = Cfg(i, *c)
+        for g, ps in enumerate(cfg.groups):
+            for KH in FUSED_KH:
+                sh = fused_shape(ps, KH)
+                if sh:
+                    out.append((i, g, KH, *sh))
+    return out
+
+
+def generate_fused() -> str:
+    cfgs = [Cfg(i, *c) for i, c in enumerate(config_list())]
+    out = ["// Generated by gen_tp.py -- do not edit.", "// clang-format off", ""]
+    for cfg in cfgs:
+        for g in range(len(cfg.groups)):
+            out.append(gen_bwd_fused(cfg, g))
+            out.append("")
+    inst = fused_configs()
+    out.append(f"static constexpr int kNumFusedKH = {len(FUSED_KH)};")
+    out.append("static constexpr int kFusedKH[] = {" + ", ".join(str(k) for k in FUSED_KH) + "};")
+    # per config and group: paths (weight-row indices), then per hidden width the kernel, its shape and LDS bytes
+    out.append("static const TPFusedGroup kTPFused[][4] = {")
+    for cfg in cfgs:
+        row = []
+        for g in range(4):
+            if g >= len(cfg.groups):
+                row.append("{0, {0}, {{nullptr, 0, 0, 0}, {nullptr, 0, 0, 0}}}")
+                continue
+            ps = cfg.groups[g]
+            pk = "{" + ", ".join(str(p["k"]) for p in ps) + "}"
+            ks = []
+            for KH in FUSED_KH:
+                sh = fused_shape(ps, KH)
+                if sh:
+                    nw, sw = sh
+                    ks.append(f"{{tp_bwf_c{cfg.idx}_g{g}<{nw}, {sw}, {KH}>, {nw}, {sw}, "
+                              f"{fused_lds(len(ps), KH, nw, sw)}}}")
+                else:
+                    ks.append("{nullptr, 0, 0, 0}")
+            row.append(f"{{{len(ps)}, {pk}, {{{', '.join(ks)}}}}}")
+        out.append("  {" + ", ".join(row) + "},")
+    out.append("};")
+    return "\n".join(out) + "\n"
+
+
 def generate() -> str:
     cfgs = [Cfg(i, *c) for i, c in enumerate(config_list())]
     out = ["// Generated by gen_tp.py -- do not edit.", "// clang-format off", ""]
@@ -887,6 +1173,7 @@ def main():
     path = os.path.join(HERE, "tp_gen.inc")
     _write(path, generate())
     _write(os.path.join(HERE, "tp_gh_gen.inc"), generate_gh())
+    _write(os.path.join(HERE, "tp_bwf_gen.inc"), generate_fused())
     return path
 
 

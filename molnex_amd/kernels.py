@@ -35,6 +35,7 @@ from torch import Tensor
 
 from . import _lib
 from ._lib import check, ptr
+from .config import config as _settings
 
 MNX_NLIST_HALF, MNX_NLIST_FULL = 0, 1
 MNX_NLIST_COMPACT, MNX_NLIST_TRIANGULAR = 0, 1
@@ -1672,6 +1673,51 @@ def _(x, Y, grad_out, row_ptr, perm, senders, batches, weight, config, channels)
     return x.new_empty(Y.shape[0], weight.shape[1])
 
 
+def tp_backward_gh_supported(config: int, channels: int, K: int) -> bool:
+    """Whether ``tp_scatter_backward_gh`` has a kernel for this product and hidden width."""
+    return config >= 0 and bool(_lib.load().mnx_tp_bwd_gh_supported(config, channels, K))
+
+
+@torch.library.custom_op("molix::tp_scatter_backward_gh", mutates_args=(), device_types="cuda")
+def tp_scatter_backward_gh(grad_out: Tensor, x: Tensor, Y: Tensor, w: Tensor, row_ptr: Tensor, perm: Tensor,
+                           senders: Tensor, wrow: Tensor | None, weight: Tensor, config: int, channels: int,
+                           need_x: bool, need_Y: bool) -> tuple[Tensor, Tensor, Tensor]:
+    """``(grad_x, grad_Y, grad_h)`` of ``<grad_out, tp_scatter(x, Y, w[wrow])>`` with ``w = h @ weight.T + b``:
+    the tensor-product backward fused with the output layer's input gradient ``grad_h = gw @ weight``
+    per directed edge, the per-edge weight gradient ``gw`` formed and multiplied on the matrix cores
+    without being written (``mnx_tp_bwd_gh_rows_f32``).  First order only (eval mode)."""
+    _require_gpu("tp_scatter_backward_gh", grad_out, x, Y, w, row_ptr, perm, senders, wrow, weight)
+    lib = _lib.load()
+    num_paths, nx, ny, no = tp_config_info(config)
+    Nw, K = weight.shape
+    if Nw != num_paths * channels:
+        raise ValueError(f"tp_scatter_backward_gh: weight has {Nw} rows, the product has {num_paths} x {channels}")
+    xs = _f32_rows(x, nx * channels, "x")
+    Ys = _f32_rows(Y, ny, "Y")
+    wss = _f32_rows(w, num_paths * channels, "w")
+    go = _f32_rows(grad_out, no * channels, "grad_out")
+    Wc = _f32_rows(weight, K, "weight")
+    N, E = row_ptr.shape[0] - 1, Ys.shape[0]
+    _check_wrow(wrow, E, wss.shape[0], "tp_scatter_backward_gh")
+    gx = torch.zeros_like(xs) if need_x else xs.new_empty(0)
+    gY = torch.empty_like(Ys) if need_Y else Ys.new_empty(0)
+    gh = xs.new_empty(E, K)
+    ws = _ws(lib.mnx_tp_bwd_gh_workspace_bytes(config, channels, E, K, ny), xs.device)
+    check(lib.mnx_tp_bwd_gh_rows_f32(config, channels, ptr(xs), ptr(Ys), ptr(wss), ptr(wrow), ptr(go), ptr(row_ptr),
+                                     ptr(perm), ptr(senders), N, E, ny, ptr(Wc), K, ptr(gx), ptr(gY), ptr(gh),
+                                     ptr(ws), ws.numel(), _stream(xs)), "tp_scatter backward (fused grad h)")
+    if E == 0:
+        gh.zero_()
+        gY.zero_() if need_Y else None
+    return gx, gY, gh
+
+
+@tp_scatter_backward_gh.register_fake
+def _(grad_out, x, Y, w, row_ptr, perm, senders, wrow, weight, config, channels, need_x, need_Y):
+    return (torch.empty_like(x) if need_x else x.new_empty(0), torch.empty_like(Y) if need_Y else Y.new_empty(0),
+            x.new_empty(Y.shape[0], weight.shape[1]))
+
+
 @torch.library.custom_op("molix::radial_tp_pairs", mutates_args=(), device_types="cuda")
 def radial_tp_pairs(x: Tensor, Y: Tensor, h: Tensor, weight: Tensor, bias: Tensor | None, row_ptr: Tensor,
                     perm: Tensor, senders: Tensor, wrow: Tensor, pairs: Tensor, config: int,
@@ -1732,6 +1778,19 @@ def _rtpp_backward(ctx, g_out, g_w):
             gx = gx.reshape(x.shape) if need_x else None
             gY = gY.reshape(Y.shape) if need_Y else None
         ghe = tp_weight_grad_batched(x, Y, go, row_ptr, perm, senders, batches, weight, ctx.config, ctx.channels)
+        gh = pair_sum_rows(ghe, pairs) if per_pair else ghe
+        if g_w is not None:
+            ghw = edge_weights_backward(g_w.contiguous(), weight)
+            gh = gh + ghw if per_pair else gh.index_add(0, pairs[:, 0].long(), ghw)
+        return gx, gY, gh, None, None, None, None, None, None, None, None, None, None
+    if (batches is None and _settings.tp_bwd_fused and g_out is not None and need_h and not (need_W or need_b)
+            and tp_backward_gh_supported(ctx.config, ctx.channels, weight.shape[1])):
+        # the tensor-product backward and the output layer's input gradient in one pass: the
+        # per-edge weight gradient is formed and consumed on chip
+        gx, gY, ghe = tp_scatter_backward_gh(g_out.contiguous(), x, Y, w, row_ptr, perm, senders, wrow, weight,
+                                             ctx.config, ctx.channels, need_x, need_Y)
+        gx = gx.reshape(x.shape) if need_x else None
+        gY = gY.reshape(Y.shape) if need_Y else None
         gh = pair_sum_rows(ghe, pairs) if per_pair else ghe
         if g_w is not None:
             ghw = edge_weights_backward(g_w.contiguous(), weight)
