@@ -124,17 +124,24 @@ class EdgeStep:
 
         self.fused = mcfg.fused_weight_grad is True and self.K.tp_weight_grad_supported(self.config, C, 64)
         self.paired = mcfg.paired_radial
+        self.graph = None  # (row_ptr, perm, senders, pairs), built on the first step
 
     def step(self):
         ops = torch.ops.molix
-        # indices come from the neighbor list (in range by construction): no validation sync
-        row_ptr, perm, snd = ops.edge_csr(self.edge_index, self.N, False)
         Y = ops.spherical_harmonics(self.vec, 3)
         r = torch.linalg.vector_norm(self.vec, dim=-1)
         # 8-Bessel x cosine cutoff in one kernel each way (bessel_cutoff below is its torch form)
         feats = ops.bessel_cutoff(r, 8, 5.0, 1e-8, self.mu, self.sigma, 1, 0)
-        pairs = self.K.EdgePairs.build(self.edge_index, self.N, row_ptr, perm, snd, feats.detach()) \
-            if self.paired else None
+        if self.graph is None:
+            # the receiver CSR and the undirected-edge pairing belong to the graph: built on its
+            # first step and kept, as an MD loop keeps its neighbor list between rebuilds (the
+            # pairing holds for any positions: a neighbor list's two directions have bond vectors
+            # that are exact negations).  Indices come from the neighbor list: no validation sync.
+            row_ptr, perm, snd = ops.edge_csr(self.edge_index, self.N, False)
+            pairs = self.K.EdgePairs.build(self.edge_index, self.N, row_ptr, perm, snd, feats.detach()) \
+                if self.paired else None
+            self.graph = (row_ptr, perm, snd, pairs)
+        row_ptr, perm, snd, pairs = self.graph
         if pairs is not None:
             # the output layer once per undirected pair (both directions have the same distance,
             # hence the same weights); edge mode: every edge vector gets its own gradient
@@ -849,7 +856,8 @@ def main():
                    "spatially_sorted": not args.unsorted,
                    "radial_output_layer": ("once per undirected pair (both directions have the same distance, "
                                            "hence the same weights; per-edge gradients)" if step_paired
-                                           else "per directed edge")},
+                                           else "per directed edge"),
+                   "graph": "receiver CSR and edge pairing built on the graph's first step and kept"},
         "roofline": roof,
         "cpu_baseline": cpu,
         "secondary": secondary,
