@@ -2,7 +2,8 @@
 // structure behind ConvTP's gather (indices_1) and scatter-sum (indices_out),
 // src/molrep/interaction/tensor_product.py:101-111.  Counting sort by receiver
 // (atomic slot claims), then each receiver's segment is sorted by edge id so
-// the result is deterministic.  Edges whose sender or receiver lies outside
+// the result is deterministic (a wavefront per segment: bitonic in registers up
+// to 64 edges, merge passes beyond).  Edges whose sender or receiver lies outside
 // [0, N) are left out and counted in *d_invalid.
 //
 // Edge lists that already come grouped by receiver in ascending order (the
@@ -25,6 +26,7 @@ struct CsrWs {
     int32_t* tiles;
     int32_t* invalid;
     int32_t* unsorted;  // 0: all edges valid and grouped by receiver in ascending order
+    int32_t* nlong;     // segments longer than one wavefront, listed for k_sort_long
 };
 
 CsrWs carve_csr(void* base, size_t bytes, int64_t N, size_t* used) {
@@ -33,8 +35,9 @@ CsrWs carve_csr(void* base, size_t bytes, int64_t N, size_t* used) {
     w.counts = ws.take<int32_t>(N + 1);
     w.fill = ws.take<int32_t>(N + 1);
     w.tiles = ws.take<int32_t>(scan_workspace_elems(N + 1));
-    w.invalid = ws.take<int32_t>(2);  // [0] invalid count, [1] unsorted flag (cleared together)
+    w.invalid = ws.take<int32_t>(3);  // [0] invalid count, [1] unsorted flag, [2] long segments (cleared together)
     w.unsorted = w.invalid + 1;
+    w.nlong = w.invalid + 2;
     *used = ws.used;
     return w;
 }
@@ -91,23 +94,130 @@ __global__ void k_place_edges(const int64_t* __restrict__ ei, int64_t E, int64_t
     perm[row_ptr[r] + atomicAdd(&fill[r], 1)] = int32_t(e);
 }
 
-__global__ void k_sort_segments(const int64_t* __restrict__ ei, int64_t N, const int32_t* __restrict__ row_ptr,
-                                int32_t* __restrict__ perm, int32_t* __restrict__ snd,
-                                const int32_t* __restrict__ unsorted) {
-    const int64_t r = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
-    if (r >= N || *unsorted == 0) return;
-    const int b = row_ptr[r], e = row_ptr[r + 1];
-    for (int k = b + 1; k < e; ++k) {
-        const int v = perm[k];
-        int q = k - 1;
-        while (q >= b && perm[q] > v) {
-            perm[q + 1] = perm[q];
-            --q;
+// Sorting each receiver's segment by edge id (the placement claims slots with atomics, in
+// arbitrary order).  k_sort_short: one wavefront per receiver; segments of up to 64 edges are
+// sorted in registers (bitonic network over the lanes) and written with their senders; longer
+// ones are appended to a list (in the `fill` array, free after the placement) for k_sort_long:
+// one wavefront per listed segment, grid-strided, which sorts runs of 64 in registers and merges
+// them pairwise (each element's output position = its rank in its run + the number of smaller
+// elements in the partner run, by binary search: edge ids are distinct) -- in LDS for segments
+// of up to kSortLds edges, else in global memory with the senders array as the second buffer.
+// O(n log^2 n) per segment instead of an insertion sort's O(n^2) on one thread.
+constexpr int kSortLds = 4096;
+
+__device__ __forceinline__ int bitonic64(int v, int lane) {
+#pragma unroll
+    for (int size = 2; size <= kWave; size <<= 1) {
+#pragma unroll
+        for (int stride = size >> 1; stride > 0; stride >>= 1) {
+            const int other = __shfl_xor(v, stride, kWave);
+            const bool up = (lane & size) == 0 || size == kWave;
+            const bool low = (lane & stride) == 0;
+            v = (low == up) ? min(v, other) : max(v, other);
         }
-        perm[q + 1] = v;
     }
-    if (snd)
-        for (int k = b; k < e; ++k) snd[k] = int32_t(ei[2 * int64_t(perm[k])]);
+    return v;
+}
+
+// number of entries of the sorted a[0..n) smaller than v
+__device__ __forceinline__ int count_below(const int32_t* a, int n, int v) {
+    int lo = 0, hi = n;
+    while (lo < hi) {
+        const int mid = (lo + hi) >> 1;
+        if (a[mid] < v) lo = mid + 1; else hi = mid;
+    }
+    return lo;
+}
+
+// one merge pass over a segment of len entries: runs of `run` from src merged pairwise into dst
+__device__ __forceinline__ void merge_pass(const int32_t* src, int32_t* dst, int len, int run, int lane) {
+    for (int k = lane; k < len; k += kWave) {
+        const int a0 = k / (2 * run) * (2 * run);
+        const int a1 = min(a0 + run, len), b1 = min(a0 + 2 * run, len);
+        const int v = src[k];
+        const int pos = k < a1 ? (k - a0) + count_below(src + a1, b1 - a1, v)
+                               : (k - a1) + count_below(src + a0, a1 - a0, v);
+        dst[a0 + pos] = v;
+    }
+}
+
+__global__ void __launch_bounds__(256) k_sort_short(const int64_t* __restrict__ ei, int64_t N,
+                                                    const int32_t* __restrict__ row_ptr, int32_t* __restrict__ perm,
+                                                    int32_t* __restrict__ snd, const int32_t* __restrict__ unsorted,
+                                                    int32_t* __restrict__ long_list, int32_t* __restrict__ nlong) {
+    const int64_t r = int64_t(blockIdx.x) * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & (kWave - 1);
+    if (r >= N || *unsorted == 0) return;
+    const int b = row_ptr[r], len = row_ptr[r + 1] - b;
+    if (len > kWave) {
+        if (lane == 0) long_list[atomicAdd(nlong, 1)] = int32_t(r);
+        return;
+    }
+    if (len == 0) return;
+    const int v = bitonic64(lane < len ? perm[b + lane] : INT32_MAX, lane);
+    if (lane < len) {
+        perm[b + lane] = v;
+        if (snd) snd[b + lane] = int32_t(ei[2 * int64_t(v)]);
+    }
+}
+
+__global__ void __launch_bounds__(kWave) k_sort_long(const int64_t* __restrict__ ei, const int32_t* __restrict__ row_ptr,
+                                                     int32_t* __restrict__ perm, int32_t* __restrict__ snd,
+                                                     const int32_t* __restrict__ long_list,
+                                                     const int32_t* __restrict__ nlong) {
+    __shared__ int32_t buf[2][kSortLds];
+    const int lane = threadIdx.x;
+    const int count = *nlong;
+    for (int li = blockIdx.x; li < count; li += gridDim.x) {
+        const int r = long_list[li];
+        const int b = row_ptr[r], len = row_ptr[r + 1] - b;
+        int32_t* seg = perm + b;
+        // runs of 64 in registers
+        for (int c0 = 0; c0 < len; c0 += kWave) {
+            const int v = bitonic64(c0 + lane < len ? seg[c0 + lane] : INT32_MAX, lane);
+            if (c0 + lane < len) {
+                if (len <= kSortLds) buf[0][c0 + lane] = v; else seg[c0 + lane] = v;
+            }
+        }
+        __syncthreads();
+        if (len <= kSortLds) {
+            int cur = 0;
+            for (int run = kWave; run < len; run *= 2) {
+                merge_pass(buf[cur], buf[cur ^ 1], len, run, lane);
+                cur ^= 1;
+                __syncthreads();
+            }
+            for (int k = lane; k < len; k += kWave) seg[k] = buf[cur][k];
+        } else if (snd) {
+            // merge passes in global memory, the senders array as the second buffer
+            int32_t* src = seg;
+            int32_t* dst = snd + b;
+            for (int run = kWave; run < len; run *= 2) {
+                merge_pass(src, dst, len, run, lane);
+                int32_t* t = src;
+                src = dst;
+                dst = t;
+                __syncthreads();
+            }
+            if (src != seg)
+                for (int k = lane; k < len; k += kWave) seg[k] = src[k];
+        } else if (lane == 0) {
+            // no second buffer: one lane merges the runs by insertion (runs are sorted already)
+            for (int k = kWave; k < len; ++k) {
+                const int v = seg[k];
+                int q = k - 1;
+                while (q >= 0 && seg[q] > v) {
+                    seg[q + 1] = seg[q];
+                    --q;
+                }
+                seg[q + 1] = v;
+            }
+        }
+        __syncthreads();
+        if (snd)
+            for (int k = lane; k < len; k += kWave) snd[b + k] = int32_t(ei[2 * int64_t(seg[k])]);
+        __syncthreads();
+    }
 }
 
 __global__ void k_copy_invalid(const int32_t* __restrict__ src, int32_t* __restrict__ dst) { *dst = *src; }
@@ -124,7 +234,7 @@ constexpr size_t align_up(size_t v) { return (v + kAlign - 1) & ~(kAlign - 1); }
 // counts, fill (N + 1 each), scan tiles, the two flags; the same carve as carve_csr
 constexpr size_t kNoallocScratchBytes =
     align_up(sizeof(int32_t) * (kNoallocMaxNodes + 1)) * 2 +
-    align_up(sizeof(int32_t) * size_t((kNoallocMaxNodes + 1 + kScanTile - 1) / kScanTile)) + align_up(2 * sizeof(int32_t)) + kAlign;
+    align_up(sizeof(int32_t) * size_t((kNoallocMaxNodes + 1 + kScanTile - 1) / kScanTile)) + align_up(3 * sizeof(int32_t)) + kAlign;
 
 static __device__ __align__(256) unsigned char scratch[kNoallocScratchBytes];
 
@@ -161,7 +271,7 @@ int csr_build(const int64_t* edge_index, int64_t E, int64_t N, int32_t* row_ptr,
         hipLaunchKernelGGL(k_fill_i32, dim3(ceil_div(N + 1, tb)), dim3(tb), 0, stream, p, N + 1);
         MNX_CHECK_LAUNCH();
     }
-    hipLaunchKernelGGL(k_fill_i32, dim3(1), dim3(2), 0, stream, w.invalid, int64_t(2));  // invalid, unsorted
+    hipLaunchKernelGGL(k_fill_i32, dim3(1), dim3(3), 0, stream, w.invalid, int64_t(3));  // invalid, unsorted, nlong
     MNX_CHECK_LAUNCH();
     if (E > 0) {
         hipLaunchKernelGGL(k_count_recv, dim3(ceil_div(E, tb)), dim3(tb), 0, stream, edge_index, E, N, w.counts,
@@ -175,8 +285,12 @@ int csr_build(const int64_t* edge_index, int64_t E, int64_t N, int32_t* row_ptr,
         hipLaunchKernelGGL(k_place_edges, dim3(ceil_div(E, tb)), dim3(tb), 0, stream, edge_index, E, N, row_ptr,
                            w.fill, perm, senders_sorted, w.unsorted);
         MNX_CHECK_LAUNCH();
-        hipLaunchKernelGGL(k_sort_segments, dim3(ceil_div(N, tb)), dim3(tb), 0, stream, edge_index, N, row_ptr,
-                           perm, senders_sorted, w.unsorted);
+        // the fill counters are done with after the placement: they hold the list of long segments
+        hipLaunchKernelGGL(k_sort_short, dim3(ceil_div(N, 4)), dim3(256), 0, stream, edge_index, N, row_ptr, perm,
+                           senders_sorted, w.unsorted, w.fill, w.nlong);
+        MNX_CHECK_LAUNCH();
+        hipLaunchKernelGGL(k_sort_long, dim3(unsigned(std::min<int64_t>(N, 2048))), dim3(kWave), 0, stream,
+                           edge_index, row_ptr, perm, senders_sorted, w.fill, w.nlong);
         MNX_CHECK_LAUNCH();
     }
     if (d_invalid) {
