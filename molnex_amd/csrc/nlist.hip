@@ -37,6 +37,8 @@ constexpr int kEmitBuf = 1024; // LDS list per wavefront of the cell emit; atoms
                                // neighbours are written by the per-atom emit
 constexpr int64_t kNlBlocks = 16384;  // grid-stride launches of the count / emit kernels
 constexpr int kCellParts = 4;          // wavefronts per cell (each takes every 4th atom of it)
+constexpr int kMaskChunks = 16;        // acceptance masks kept per centre: 16 x 64 candidates; cells
+                                       // with more candidates are tested again by the emit
 constexpr float kCellMargin = 1.0001f;
 
 struct NlGrid {
@@ -60,6 +62,7 @@ struct NlWs {
     int32_t* atoms_sorted;
     int32_t* counts;
     int32_t* big;
+    uint64_t* masks;  // per centre: the count pass's accept ballot of each 64-candidate chunk
     int64_t* offsets;
     int64_t* total;
     int64_t* tiles64;
@@ -81,6 +84,7 @@ NlWs carve(void* base, size_t bytes, int64_t n, size_t* used) {
     w.atoms_sorted = ws.take<int32_t>(n > 0 ? n : 1);
     w.counts = ws.take<int32_t>(n > 0 ? n : 1);
     w.big = ws.take<int32_t>(n > 0 ? n : 1);
+    w.masks = ws.take<uint64_t>(size_t(n > 0 ? n : 1) * kMaskChunks);
     w.offsets = ws.take<int64_t>(n + 1);
     w.total = ws.take<int64_t>(1);
     w.tiles64 = ws.take<int64_t>(scan_workspace_elems(n));
@@ -571,7 +575,8 @@ __global__ void __launch_bounds__(kWave) k_count_cells(const T* __restrict__ pos
                                                        int mode, NlGrid* __restrict__ gp,
                                                        const int32_t* __restrict__ cell_start,
                                                        const int32_t* __restrict__ atoms_sorted,
-                                                       int32_t* __restrict__ counts, int32_t* __restrict__ big) {
+                                                       int32_t* __restrict__ counts, int32_t* __restrict__ big,
+                                                       uint64_t* __restrict__ masks) {
     const NlGrid g = *gp;
     if (g.brute) return;
     const int lane = threadIdx.x;
@@ -592,6 +597,7 @@ __global__ void __launch_bounds__(kWave) k_count_cells(const T* __restrict__ pos
             const T mx = my_i >= 0 ? pos[3 * my_i] : T(0), my = my_i >= 0 ? pos[3 * my_i + 1] : T(0),
                     mz = my_i >= 0 ? pos[3 * my_i + 2] : T(0);
             int my_count = 0;
+            const bool keep_masks = cr.total <= kWave * kMaskChunks;  // wave-uniform
             for (int base = 0; base < cr.total; base += kWave) {
                 const int j = cell_candidate(cr, base + lane, atoms_sorted);
                 const T jx = j >= 0 ? pos[3 * j] : T(0), jy = j >= 0 ? pos[3 * j + 1] : T(0),
@@ -601,8 +607,11 @@ __global__ void __launch_bounds__(kWave) k_count_cells(const T* __restrict__ pos
                     const bool keep = j >= 0 && (mode == MNX_NLIST_HALF ? j < i : j != i);
                     const bool ok = keep && accept_xyz<T>(box, lane_value(mx, q), lane_value(my, q), lane_value(mz, q),
                                                           jx, jy, jz, periodic, cutoff, at);
-                    const int cnt = __popcll(__ballot(ok));
-                    if (lane == q) my_count += cnt;
+                    const uint64_t m = __ballot(ok);
+                    if (lane == q) {
+                        my_count += __popcll(m);
+                        if (keep_masks) masks[int64_t(my_i) * kMaskChunks + base / kWave] = m;
+                    }
                 }
             }
             if (lane < nq) {
@@ -620,6 +629,7 @@ __global__ void __launch_bounds__(kWave) k_emit_cells(const T* __restrict__ pos,
                                                       const int32_t* __restrict__ cell_start,
                                                       const int32_t* __restrict__ atoms_sorted,
                                                       const int32_t* __restrict__ counts,
+                                                      const uint64_t* __restrict__ masks,
                                                       const int64_t* __restrict__ offsets, int64_t capacity,
                                                       int32_t* __restrict__ idx_i, int32_t* __restrict__ idx_j,
                                                       T* __restrict__ deltas, T* __restrict__ dist,
@@ -659,18 +669,31 @@ __global__ void __launch_bounds__(kWave) k_emit_cells(const T* __restrict__ pos,
             const int my_off = incl - my_cnt;
             int my_fill = 0;
             __syncthreads();  // previous batch's segments fully read
+            // the count pass left each centre's accept ballots (the same candidates in the same
+            // order): reuse them instead of testing again, unless the cell had too many candidates
+            const bool use_masks = cr.total <= kWave * kMaskChunks;  // wave-uniform
             for (int base = 0; base < cr.total; base += kWave) {
                 const int j = cell_candidate(cr, base + lane, atoms_sorted);
-                const T jx = j >= 0 ? pos[3 * j] : T(0), jy = j >= 0 ? pos[3 * j + 1] : T(0),
-                        jz = j >= 0 ? pos[3 * j + 2] : T(0);
+                T jx = T(0), jy = T(0), jz = T(0);
+                if (!use_masks && j >= 0) {
+                    jx = pos[3 * j];
+                    jy = pos[3 * j + 1];
+                    jz = pos[3 * j + 2];
+                }
                 for (int q = 0; q < nq; ++q) {
                     const int i = lane_value(my_i, q);
                     const int seg = lane_value(my_off, q);
                     const int cap = lane_value(my_cnt, q);
                     const int fill = lane_value(my_fill, q);
-                    const bool keep = j >= 0 && (mode == MNX_NLIST_HALF ? j < i : j != i);
-                    const bool ok = keep && accept_xyz<T>(box, lane_value(mx, q), lane_value(my, q), lane_value(mz, q),
-                                                          jx, jy, jz, periodic, cutoff, at);
+                    bool ok;
+                    if (use_masks) {
+                        const uint64_t cm = masks[int64_t(__builtin_amdgcn_readfirstlane(i)) * kMaskChunks + base / kWave];
+                        ok = (cm >> lane) & 1;
+                    } else {
+                        const bool keep = j >= 0 && (mode == MNX_NLIST_HALF ? j < i : j != i);
+                        ok = keep && accept_xyz<T>(box, lane_value(mx, q), lane_value(my, q), lane_value(mz, q), jx,
+                                                   jy, jz, periodic, cutoff, at);
+                    }
                     const uint64_t m = __ballot(ok);
                     const int before = __popcll(m & ((uint64_t(1) << lane) - 1));
                     if (ok && fill + before < cap) buf[seg + fill + before] = j;
@@ -798,7 +821,7 @@ int nlist_count(const T* pos, int64_t n, double cutoff, const T* box, int mode, 
         MNX_CHECK_LAUNCH();
         const unsigned blocks = unsigned(std::min<int64_t>(std::max<int64_t>(n, w.max_cells * kCellParts), kNlBlocks));
         hipLaunchKernelGGL((k_count_cells<T>), dim3(blocks), dim3(kWave), 0, stream, pos, box, T(cutoff), mode,
-                           w.grid, w.cell_start, w.atoms_sorted, w.counts, w.big);
+                           w.grid, w.cell_start, w.atoms_sorted, w.counts, w.big, w.masks);
         MNX_CHECK_LAUNCH();
         hipLaunchKernelGGL((k_count<T>), dim3(blocks), dim3(kWave), 0, stream, pos, n, box, T(cutoff), mode, w.grid,
                            w.cell_start, w.atoms_sorted, w.counts);
@@ -839,8 +862,8 @@ int nlist_emit(const T* pos, int64_t n, double cutoff, const T* box, int mode, i
     if (n > 0) {
         const unsigned blocks = unsigned(std::min<int64_t>(std::max<int64_t>(n, w.max_cells * kCellParts), kNlBlocks));
         hipLaunchKernelGGL((k_emit_cells<T>), dim3(blocks), dim3(kWave), 0, stream, pos, box, T(cutoff), mode, layout,
-                           w.grid, w.cell_start, w.atoms_sorted, w.counts, w.offsets, capacity, idx_i, idx_j, deltas,
-                           dist, shifts);
+                           w.grid, w.cell_start, w.atoms_sorted, w.counts, w.masks, w.offsets, capacity, idx_i, idx_j,
+                           deltas, dist, shifts);
         MNX_CHECK_LAUNCH();
         hipLaunchKernelGGL((k_emit<T>), dim3(blocks), dim3(kWave), 0, stream, pos, n, box, T(cutoff), mode, layout,
                            w.grid, w.cell_start, w.atoms_sorted, w.big, w.offsets, capacity, idx_i, idx_j, deltas,
