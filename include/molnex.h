@@ -261,6 +261,22 @@ int mnx_tp_bwd_sender_f32(int32_t config, int32_t channels, const float* x, cons
                           int64_t num_edges, float* grad_x, float* grad_Y, float* grad_w,
                           mnx_stream_t stream);
 
+/* The backward one path group at a time (groups = paths sharing the l of irreps_in1;
+ * mnx_tp_group_paths fills bounds[0..ngroups] with their path ranges and returns ngroups): group
+ * `group`'s kernel of mnx_tp_bwd_rows_f32, writing grad_w for the group's columns
+ * [bounds[g] * C, bounds[g + 1] * C) and accumulating grad_x; its grad_Y partials go to the
+ * workspace (mnx_tp_bwd_workspace_bytes; NULL: no grad_Y), summed by mnx_tp_bwd_reduce_gy_f32
+ * once every group has run.  Lets a caller start consuming one group's grad_w (on another stream)
+ * while the next group runs. */
+int mnx_tp_group_paths(int32_t config, int32_t* bounds);
+int mnx_tp_bwd_group_rows_f32(int32_t config, int32_t channels, int32_t group, const float* x, const float* Y,
+                              const float* w, const int32_t* wrow, const float* grad_out, const int32_t* row_ptr,
+                              const int32_t* perm, const int32_t* senders_sorted, int64_t num_nodes,
+                              int64_t num_edges, float* grad_x, float* grad_w, void* workspace,
+                              size_t workspace_bytes, mnx_stream_t stream);
+int mnx_tp_bwd_reduce_gy_f32(int32_t config, int32_t channels, int64_t num_edges, const void* workspace,
+                             size_t workspace_bytes, float* grad_Y, mnx_stream_t stream);
+
 /* The three calls above with the per-edge weights taken from row wrow[e] of w
  * (int32 [E], any number of rows) instead of row e: edges whose weights are
  * equal share one row, e.g. the two directions of an undirected pair, whose
@@ -526,6 +542,14 @@ int mnx_edge_weights_rows_f32(const float* h, const int32_t* rows, int64_t num_r
  * mnx_edge_weights_bwd_f32 (num_pairs = num_edges). */
 int mnx_edge_weights_bwd_pairs_f32(const float* grad_w, const int32_t* pairs, int64_t num_pairs, int32_t N,
                                    const uint16_t* frag, int32_t K, float* grad_h, mnx_stream_t stream);
+/* The same over a column slice of the gradient: grad_w points at the slice's first column, rows
+ * ld floats apart (ld >= N, a multiple of 4), N the slice width and frag W's matching rows
+ * [N][K] packed for the backward; pairs may be NULL.  accumulate != 0 adds the product to grad_h
+ * instead of overwriting it, so slices taken in turn (e.g. as the tensor product's backward
+ * finishes each path group's columns) sum to the whole product in launch order. */
+int mnx_edge_weights_bwd_cols_f32(const float* grad_w, int64_t ld, const int32_t* pairs, int64_t num_rows,
+                                  int32_t N, const uint16_t* frag, int32_t K, float* grad_h, int32_t accumulate,
+                                  mnx_stream_t stream);
 
 /* ------------------------------------------------------------------------ */
 /* Fused weight gradient of the tensor product and the output layer of the    */

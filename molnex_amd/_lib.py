@@ -108,6 +108,11 @@ SIGNATURES = {
     "mnx_tp_weight_grad_rows": (C.c_int, [c_i32, c_i32, vp]),
     "mnx_tp_weight_grad_batched_f32": (C.c_int, [c_i32, c_i32, vp, vp, vp, vp, vp, vp, vp, c_i64, c_i64, c_i64, vp,
                                                   c_i32, vp, vp]),
+    "mnx_tp_group_paths": (C.c_int, [c_i32, vp]),
+    "mnx_tp_bwd_group_rows_f32": (C.c_int, [c_i32, c_i32, c_i32, vp, vp, vp, vp, vp, vp, vp, vp, c_i64, c_i64, vp, vp,
+                                             vp, c_sz, vp]),
+    "mnx_tp_bwd_reduce_gy_f32": (C.c_int, [c_i32, c_i32, c_i64, vp, c_sz, vp, vp]),
+    "mnx_edge_weights_bwd_cols_f32": (C.c_int, [vp, c_i64, vp, c_i64, c_i32, vp, c_i32, vp, c_i32, vp]),
     "mnx_tp_bwd_gh_supported": (C.c_int, [c_i32, c_i32, c_i32]),
     "mnx_tp_bwd_gh_workspace_bytes": (c_sz, [c_i32, c_i32, c_i64, c_i32, c_i32]),
     "mnx_tp_bwd_gh_rows_f32": (C.c_int, [c_i32, c_i32, vp, vp, vp, vp, vp, vp, vp, vp, c_i64, c_i64, c_i32, vp,

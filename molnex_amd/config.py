@@ -39,6 +39,14 @@ class _Config:
     # 30.6 ms against 27.6-28.7 ms), since its LDS staging and per-phase barriers cost the receiver
     # walk more occupancy and issue time than the 30.8 GB weight-gradient stream it saves
     tp_bwd_fused: bool = False
+    # True: with the radial MLP run once per undirected pair (eval mode), the tensor product's
+    # backward runs one path group at a time and each group's columns of the per-edge weight
+    # gradient are multiplied into the output layer's input gradient on a second stream while the
+    # next group runs (kernels.tp_backward_overlapped).  False (default): the whole backward, then
+    # the product; on MI355X the two streams' kernels barely co-reside (the backward's workgroups
+    # fill every compute unit's registers), so the overlap saved nothing (config 3 39.5 vs 39.1 ms,
+    # literal config 5 29.0 vs 28.6 ms)
+    tp_bwd_overlap: bool = False
     # True: where the radial MLP's parameters are frozen and no second derivatives are taken (eval
     # mode), the MLP and its output layer run once per undirected pair of opposite edges whose radial
     # inputs are bit-identical (a neighbor list's pairs), and the tensor product reads each pair's

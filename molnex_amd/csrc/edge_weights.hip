@@ -231,12 +231,14 @@ __global__ __launch_bounds__(kEwFwdThreads) void k_ew_fwd(const float* __restric
 
 // PAIR: row i of the product is the sum of gradient rows pairs[i][0] and pairs[i][1] (the two
 // directed edges that share one row of weights), E the number of pairs.
+// ld: the row stride of gw (N for a whole row; wider for a column slice); accumulate: gh += instead
+// of gh = (the partial products over column slices, added in launch order).
 template <int T, bool PAIR>
 __global__ __launch_bounds__(kEwBwdThreads) void k_ew_bwd(const float* __restrict__ gw, int64_t E, int N,
                                                        const f16x8* __restrict__ frag,
                                                        const float* __restrict__ colscale, int K, int nstages,
                                                        const int32_t* __restrict__ pairs,
-                                                       float* __restrict__ gh) {
+                                                       float* __restrict__ gh, int64_t ld, bool accumulate) {
     constexpr int NQ = 8 / T;
     constexpr int PER = kEwStageVec / kEwBwdThreads;
     __shared__ f16x8 sB[2][kEwStageVec];
@@ -246,8 +248,8 @@ __global__ __launch_bounds__(kEwBwdThreads) void k_ew_bwd(const float* __restric
     const bool aok = arow < E;
     const int64_t src0 = PAIR ? (aok ? int64_t(pairs[2 * arow]) : 0) : (aok ? arow : 0);
     const int64_t src1 = PAIR ? (aok ? int64_t(pairs[2 * arow + 1]) : 0) : 0;
-    const float* asrc = gw + src0 * N + 8 * (lane >> 5);
-    const float* bsrc = gw + src1 * N + 8 * (lane >> 5);
+    const float* asrc = gw + src0 * ld + 8 * (lane >> 5);
+    const float* bsrc = gw + src1 * ld + 8 * (lane >> 5);
 
     f32x4 ra[NQ][2];
     auto fetch_a = [&](int s) {
@@ -331,6 +333,7 @@ __global__ __launch_bounds__(kEwBwdThreads) void k_ew_bwd(const float* __restric
             f32x4 v;
 #pragma unroll
             for (int i = 0; i < 4; ++i) v[i] = acc[t][4 * r4 + i] * so * cs[i];
+            if (accumulate) v += *reinterpret_cast<const f32x4*>(dst + c);
             *reinterpret_cast<f32x4*>(dst + c) = v;
         }
 }
@@ -414,9 +417,17 @@ int mnx_edge_weights_bwd_f32(const float* grad_w, int64_t num_edges, int32_t N, 
 
 int mnx_edge_weights_bwd_pairs_f32(const float* grad_w, const int32_t* pairs, int64_t num_edges, int32_t N,
                                    const uint16_t* frag, int32_t K, float* grad_h, mnx_stream_t stream) {
+    return mnx_edge_weights_bwd_cols_f32(grad_w, N, pairs, num_edges, N, frag, K, grad_h, 0, stream);
+}
+
+int mnx_edge_weights_bwd_cols_f32(const float* grad_w, int64_t ld, const int32_t* pairs, int64_t num_edges,
+                                  int32_t N, const uint16_t* frag, int32_t K, float* grad_h, int32_t accumulate,
+                                  mnx_stream_t stream) {
     clear_error();
     int rc = check_ew(K, N);
     if (rc) return rc;
+    MNX_REQUIRE(ld >= N && ld % 4 == 0, "edge weights backward: row stride %lld below the width %d or not a "
+                "multiple of 4", (long long)ld, N);
     MNX_REQUIRE(N % 8 == 0, "edge weights backward: output width %d not a multiple of 8", N);
     MNX_REQUIRE(num_edges >= 0 && num_edges < (int64_t(1) << 36), "edge count out of range");
     if (num_edges == 0) return MNX_OK;
@@ -430,7 +441,8 @@ int mnx_edge_weights_bwd_pairs_f32(const float* grad_w, const int32_t* pairs, in
     const int tiles = sh.tiles_b();
     auto fn = pairs ? (tiles == 1 ? k_ew_bwd<1, true> : tiles == 2 ? k_ew_bwd<2, true> : k_ew_bwd<4, true>)
                     : (tiles == 1 ? k_ew_bwd<1, false> : tiles == 2 ? k_ew_bwd<2, false> : k_ew_bwd<4, false>);
-    hipLaunchKernelGGL(fn, grid, block, 0, s, grad_w, num_edges, N, f, cs, K, sh.stages_b(), pairs, grad_h);
+    hipLaunchKernelGGL(fn, grid, block, 0, s, grad_w, num_edges, N, f, cs, K, sh.stages_b(), pairs, grad_h, ld,
+                       accumulate != 0);
     MNX_CHECK_LAUNCH();
     return MNX_OK;
 }

@@ -906,6 +906,18 @@ def generate() -> str:
         cp = [str(bwd_cpl(ps)) for ps in cfg.groups] + ["0"] * (4 - len(cfg.groups))
         out.append("  {" + ", ".join(cp) + "},")
     out.append("};")
+    # path range of each group: groups hold consecutive paths (paths are enumerated by input block)
+    out.append("static const int kTPGroupPaths[][5] = {")
+    for cfg in cfgs:
+        bounds = [cfg.groups[0][0]["k"]]
+        for ps in cfg.groups:
+            ks = [p["k"] for p in ps]
+            assert ks == list(range(bounds[-1], bounds[-1] + len(ks))), "group paths must be consecutive"
+            bounds.append(bounds[-1] + len(ks))
+        assert bounds[0] == 0 and bounds[-1] == cfg.NP
+        bounds += [bounds[-1]] * (5 - len(bounds))
+        out.append("  {" + ", ".join(str(b) for b in bounds) + "},")
+    out.append("};")
     # sender-major backward: subgroups, channels per lane, harmonics components per subgroup
     subs = [sender_subgroups(cfg) for cfg in cfgs]
     ms = max(len(x) for x in subs)

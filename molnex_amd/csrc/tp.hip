@@ -176,6 +176,59 @@ int mnx_tp_bwd_rows_f32(int32_t config, int32_t C, const float* x, const float* 
     return MNX_OK;
 }
 
+int mnx_tp_group_paths(int32_t config, int32_t* bounds) {
+    clear_error();
+    MNX_REQUIRE(config >= 0 && config < kNumTPConfigs && bounds, "invalid tp config %d", config);
+    const int ng = kTPConfigs[config].ngroups;
+    for (int g = 0; g <= ng; ++g) bounds[g] = kTPGroupPaths[config][g];
+    return ng;
+}
+
+int mnx_tp_bwd_group_rows_f32(int32_t config, int32_t C, int32_t group, const float* x, const float* Y,
+                              const float* w, const int32_t* wrow, const float* gout, const int32_t* row_ptr,
+                              const int32_t* perm, const int32_t* snd, int64_t N, int64_t E, float* gx, float* gw,
+                              void* ws, size_t ws_bytes, mnx_stream_t stream) {
+    clear_error();
+    int rc = check_common(config, C, N, E);
+    if (rc) return rc;
+    const TPConfigInfo& cfg = kTPConfigs[config];
+    MNX_REQUIRE(group >= 0 && group < cfg.ngroups, "group %d not in [0, %d)", group, cfg.ngroups);
+    if (N == 0 || E == 0) return MNX_OK;
+    MNX_REQUIRE(x && Y && w && gout && row_ptr && perm && snd, "null pointer argument");
+    float* part = nullptr;
+    if (ws) {
+        const size_t need = mnx_tp_bwd_workspace_bytes(config, C, E);
+        if (ws_bytes < need) return set_error(MNX_ERR_WORKSPACE, "workspace %zu < %zu bytes", ws_bytes, need);
+        part = static_cast<float*>(ws);
+    }
+    int pbase = 0;
+    for (int g = 0; g < group; ++g) pbase += int(ceil_div(C, 64 * kTPBwdCPL[config][g]));
+    const int npart = int(bwd_partials(config, C));
+    const int cblocks = int(ceil_div(C, 64 * kTPBwdCPL[config][group]));
+    const bool full = C % (64 * kTPBwdCPL[config][group]) == 0;
+    hipLaunchKernelGGL((full ? kTPBwdF : kTPBwd)[config][group], node_grid(N, cblocks), dim3(64), 0,
+                       (hipStream_t)stream, x, Y, w, gout, row_ptr, perm, snd, wrow, N, C, gx, gw, part, npart, pbase);
+    MNX_CHECK_LAUNCH();
+    return MNX_OK;
+}
+
+int mnx_tp_bwd_reduce_gy_f32(int32_t config, int32_t C, int64_t E, const void* ws, size_t ws_bytes, float* gY,
+                             mnx_stream_t stream) {
+    clear_error();
+    int rc = check_common(config, C, 0, E);
+    if (rc) return rc;
+    if (E == 0) return MNX_OK;
+    MNX_REQUIRE(ws && gY, "null pointer argument");
+    const size_t need = mnx_tp_bwd_workspace_bytes(config, C, E);
+    if (ws_bytes < need) return set_error(MNX_ERR_WORKSPACE, "workspace %zu < %zu bytes", ws_bytes, need);
+    const TPConfigInfo& cfg = kTPConfigs[config];
+    const int64_t tot = E * cfg.ny;
+    hipLaunchKernelGGL(k_reduce_partials, dim3(unsigned(ceil_div(tot, 256))), dim3(256), 0, (hipStream_t)stream,
+                       static_cast<const float*>(ws), E, int(bwd_partials(config, C)), cfg.ny, gY);
+    MNX_CHECK_LAUNCH();
+    return MNX_OK;
+}
+
 int mnx_tp_bwd_sender_f32(int32_t config, int32_t C, const float* x, const float* Y, const float* w,
                           const float* gout, const int32_t* s_row_ptr, const int32_t* s_perm,
                           const int32_t* s_receivers, int64_t N, int64_t E, float* gx, float* gY, float* gw,

@@ -30,6 +30,8 @@ from __future__ import annotations
 
 import ctypes as C
 
+C_int32_5 = C.c_int32 * 5
+
 import torch
 from torch import Tensor
 
@@ -1673,6 +1675,83 @@ def _(x, Y, grad_out, row_ptr, perm, senders, batches, weight, config, channels)
     return x.new_empty(Y.shape[0], weight.shape[1])
 
 
+_AUX_STREAMS: dict = {}
+
+
+def _aux_stream(device: torch.device) -> torch.cuda.Stream:
+    """A second stream per device (default priority) for work that overlaps the current stream's."""
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    s = _AUX_STREAMS.get(idx)
+    if s is None:
+        s = _AUX_STREAMS[idx] = torch.cuda.Stream(device=idx)
+    return s
+
+
+def tp_backward_overlapped(grad_out: Tensor, x: Tensor, Y: Tensor, w: Tensor, row_ptr: Tensor, perm: Tensor,
+                           senders: Tensor, wrow: Tensor | None, weight: Tensor, pairs: Tensor | None, config: int,
+                           channels: int, need_x: bool, need_Y: bool) -> tuple[Tensor, Tensor, Tensor]:
+    """``(grad_x, grad_Y, grad_h)`` of ``<grad_out, tp_scatter(x, Y, w[wrow])>`` with ``w = h @ weight.T + b``:
+    the tensor product's backward runs one path group at a time on the current stream
+    (``mnx_tp_bwd_group_rows_f32``), and as each group's columns of the per-edge weight gradient are
+    written, a second stream multiplies them into ``grad_h`` (``mnx_edge_weights_bwd_cols_f32``,
+    accumulating over the groups in launch order) while the next group's backward runs: the
+    atomic-bound tensor-product backward and the memory-bound output-layer product overlap.
+    ``pairs``: ``grad_h`` per undirected pair (the two edges' rows added), else per edge."""
+    lib = _lib.load()
+    num_paths, nx, ny, no = tp_config_info(config)
+    Ch = channels
+    Nw, K = weight.shape
+    if Nw != num_paths * Ch:
+        raise ValueError(f"tp_backward_overlapped: weight has {Nw} rows, the product has {num_paths} x {Ch}")
+    xs = _f32_rows(x, nx * Ch, "x")
+    Ys = _f32_rows(Y, ny, "Y")
+    wss = _f32_rows(w, num_paths * Ch, "w")
+    go = _f32_rows(grad_out, no * Ch, "grad_out")
+    N, E = row_ptr.shape[0] - 1, Ys.shape[0]
+    _check_wrow(wrow, E, wss.shape[0], "tp_backward_overlapped")
+    dev = xs.device
+    gx = torch.zeros_like(xs) if need_x else xs.new_empty(0)
+    gY = torch.empty_like(Ys) if need_Y else Ys.new_empty(0)
+    gw = wss.new_empty(E, num_paths * Ch)
+    rows = pairs.shape[0] if pairs is not None else E
+    gh = xs.new_empty(rows, K)
+    if E == 0:
+        gY.zero_() if need_Y else None
+        return gx, gY, gh.zero_()
+    ws = _ws(lib.mnx_tp_bwd_workspace_bytes(config, Ch, E), dev) if need_Y else None
+    bounds = (C_int32_5)()
+    ng = lib.mnx_tp_group_paths(config, bounds)
+    if ng <= 0:
+        raise RuntimeError("tp_backward_overlapped: no path groups")
+    Wf = weight.detach().to(torch.float32).contiguous()
+    main, aux = torch.cuda.current_stream(dev), _aux_stream(dev)
+    ms, ax = main.cuda_stream, aux.cuda_stream
+    # largest groups first, so that the product left without overlap at the end is the smallest
+    order = sorted(range(ng), key=lambda g: -(bounds[g + 1] - bounds[g]))
+    frags = []
+    for i, g in enumerate(order):
+        p0, p1 = bounds[g], bounds[g + 1]
+        check(lib.mnx_tp_bwd_group_rows_f32(config, Ch, g, ptr(xs), ptr(Ys), ptr(wss), ptr(wrow), ptr(go),
+                                            ptr(row_ptr), ptr(perm), ptr(senders), N, E, ptr(gx) if need_x else None,
+                                            ptr(gw), ptr(ws), ws.numel() if ws is not None else 0, ms),
+              "tp_scatter backward (path group)")
+        frag = _ew_frag(Wf[p0 * Ch:p1 * Ch], True)
+        frags.append(frag)
+        ev = torch.cuda.Event()
+        ev.record(main)
+        aux.wait_event(ev)
+        check(lib.mnx_edge_weights_bwd_cols_f32(gw.data_ptr() + 4 * p0 * Ch, num_paths * Ch, ptr(pairs), rows,
+                                                (p1 - p0) * Ch, ptr(frag), K, ptr(gh), int(i > 0), ax),
+              "edge_weights backward (column slice)")
+    if need_Y:
+        check(lib.mnx_tp_bwd_reduce_gy_f32(config, Ch, E, ptr(ws), ws.numel(), ptr(gY), ms), "tp_scatter grad_Y")
+    # the current stream waits for the second one before anything here is freed, so the caching
+    # allocator (which reuses blocks in the current stream's order) cannot hand them out early
+    main.wait_stream(aux)
+    del frags
+    return gx, gY, gh
+
+
 def tp_backward_gh_supported(config: int, channels: int, K: int) -> bool:
     """Whether ``tp_scatter_backward_gh`` has a kernel for this product and hidden width."""
     return config >= 0 and bool(_lib.load().mnx_tp_bwd_gh_supported(config, channels, K))
@@ -1792,6 +1871,18 @@ def _rtpp_backward(ctx, g_out, g_w):
         gx = gx.reshape(x.shape) if need_x else None
         gY = gY.reshape(Y.shape) if need_Y else None
         gh = pair_sum_rows(ghe, pairs) if per_pair else ghe
+        if g_w is not None:
+            ghw = edge_weights_backward(g_w.contiguous(), weight)
+            gh = gh + ghw if per_pair else gh.index_add(0, pairs[:, 0].long(), ghw)
+        return gx, gY, gh, None, None, None, None, None, None, None, None, None, None
+    if (batches is None and _settings.tp_bwd_overlap and g_out is not None and need_h and not (need_W or need_b)
+            and ctx.channels % 8 == 0 and weight.shape[1] in (16, 32, 64, 128)):
+        # the tensor-product backward group by group, each group's weight-gradient columns
+        # multiplied into grad h on a second stream while the next group runs
+        gx, gY, gh = tp_backward_overlapped(g_out.contiguous(), x, Y, w, row_ptr, perm, senders, wrow, weight,
+                                            pairs if per_pair else None, ctx.config, ctx.channels, need_x, need_Y)
+        gx = gx.reshape(x.shape) if need_x else None
+        gY = gY.reshape(Y.shape) if need_Y else None
         if g_w is not None:
             ghw = edge_weights_backward(g_w.contiguous(), weight)
             gh = gh + ghw if per_pair else gh.index_add(0, pairs[:, 0].long(), ghw)
