@@ -234,7 +234,7 @@ __global__ __launch_bounds__(kEwFwdThreads) void k_ew_fwd(const float* __restric
 // ld: the row stride of gw (N for a whole row; wider for a column slice); accumulate: gh += instead
 // of gh = (the partial products over column slices, added in launch order).
 template <int T, bool PAIR>
-__global__ __launch_bounds__(kEwBwdThreads) void k_ew_bwd(const float* __restrict__ gw, int64_t E, int N,
+__global__ __launch_bounds__(kEwBwdThreads, T >= 2 ? 3 : 2) void k_ew_bwd(const float* __restrict__ gw, int64_t E, int N,
                                                        const f16x8* __restrict__ frag,
                                                        const float* __restrict__ colscale, int K, int nstages,
                                                        const int32_t* __restrict__ pairs,
