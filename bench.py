@@ -47,10 +47,12 @@ def parse():
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--unsorted", action="store_true", help="keep atoms in random order (no spatial sort)")
     p.add_argument("--seed", type=int, default=0)
-    p.add_argument("--workload", choices=["tp", "full", "sc", "nl", "pme", "train", "allegro"], default="tp",
+    p.add_argument("--workload", choices=["tp", "full", "sc", "nl", "pme", "train", "allegro", "tpgh"], default="tp",
                    help="tp: config 3 edge step (default, the headline line); full: config 5 energy + forces; "
                         "sc / nl / pme: config 4, config 2, config 5's PME term alone; train: config 5 "
-                        "force-matching training step; allegro: Allegro energy + forces on the 50k-atom graph")
+                        "force-matching training step; allegro: Allegro energy + forces on the 50k-atom graph; "
+                        "tpgh: the config-3 tensor-product backward fused with the output layer's input "
+                        "gradient against the unfused pair (off by default in the library)")
     p.add_argument("--no-secondary", action="store_true",
                    help="skip the secondary figures (config 2 neighbor list, config 5 energy + forces)")
     p.add_argument("--literal", action="store_true",
@@ -556,6 +558,47 @@ def nlist_bench(dev, reps=10, warmup=3):
             "pairs": E, "ms": round(dt * 1e3, 3), "M_pairs_per_s": round(E / dt / 1e6, 1)}
 
 
+def tp_gh_bench(dev, reps=5):
+    """The config-3 tensor-product backward in its two forms, event-timed on the same inputs:
+    unfused -- molix::tp_scatter_backward writing the per-edge weight gradient gw (E x 23*128),
+    then the output layer's input gradient gw W (molix::edge_weights backward, K 64) -- and fused,
+    molix::tp_scatter_backward_gh (gw staged in LDS and multiplied on the matrix cores, never
+    written)."""
+    import molnex_amd.kernels as K
+
+    torch.manual_seed(0)
+    pos, box, ei, vec, L = make_system(50_000, 0, True, dev)
+    N, E, C, Kh = pos.shape[0], ei.shape[0], 128, 64
+    ls = [0, 1, 2, 3]
+    cfg = K.tp_config_id(ls, ls, ls)
+    P, NX, NY, NO = K.tp_config_info(cfg)
+    row_ptr, perm, snd = torch.ops.molix.edge_csr(ei, N)
+    Y = torch.ops.molix.spherical_harmonics(vec, 3)
+    x = torch.randn(N, NX * C, device=dev)
+    w = torch.randn(E, P * C, device=dev)
+    W = torch.randn(P * C, Kh, device=dev) / Kh ** 0.5
+    g = torch.randn(N, NO * C, device=dev)
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(reps + 1)]
+    for i in range(reps + 1):
+        e = ev[i]
+        e[0].record()
+        _, _, gw = K.tp_scatter_backward(g, x, Y, w, row_ptr, perm, snd, cfg, C, True, True, True)
+        e[1].record()
+        K.edge_weights_backward(gw, W)
+        e[2].record()
+        del gw
+        K.tp_scatter_backward_gh(g, x, Y, w, row_ptr, perm, snd, None, W, cfg, C, True, True)
+        e[3].record()
+    torch.cuda.synchronize()
+    tb = sum(e[0].elapsed_time(e[1]) for e in ev[1:]) / reps
+    te = sum(e[1].elapsed_time(e[2]) for e in ev[1:]) / reps
+    tf = sum(e[2].elapsed_time(e[3]) for e in ev[1:]) / reps
+    return {"workload": "config 3 TP backward (50k atoms, 2.6 M edges, 128 x (0e+1o+2e+3o), K 64), "
+                        "fused with the output layer's input gradient vs unfused",
+            "edges": E, "unfused_tp_bwd_ms": round(tb, 3), "unfused_edge_weights_bwd_ms": round(te, 3),
+            "unfused_ms": round(tb + te, 3), "fused_ms": round(tf, 3)}
+
+
 def sc_flops(l_in=3, l_out=1, nu=3):
     """FLOPs per (node, channel) of the generated symmetric-contraction code, each distinct
     pair product A_i A_j counted once (the compiler shares them between monomials and
@@ -780,10 +823,10 @@ def main():
         print(json.dumps(allegro_bench(args, torch.device("cuda:0"), steps=args.steps, warmup=args.warmup)),
               flush=True)
         return
-    if args.workload in ("sc", "nl", "pme"):
+    if args.workload in ("sc", "nl", "pme", "tpgh"):
         import molnex_amd.kernels  # noqa: F401
 
-        fn = {"sc": sc_bench, "nl": nlist_bench, "pme": pme_bench}[args.workload]
+        fn = {"sc": sc_bench, "nl": nlist_bench, "pme": pme_bench, "tpgh": tp_gh_bench}[args.workload]
         print(json.dumps(fn(torch.device("cuda:0"))), flush=True)
         return
     if not torch.cuda.is_available():
