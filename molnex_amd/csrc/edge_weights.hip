@@ -233,7 +233,11 @@ __global__ __launch_bounds__(kEwFwdThreads) void k_ew_fwd(const float* __restric
 // directed edges that share one row of weights), E the number of pairs.
 // ld: the row stride of gw (N for a whole row; wider for a column slice); accumulate: gh += instead
 // of gh = (the partial products over column slices, added in launch order).
-template <int T, bool PAIR>
+// RAGGED: N is not a multiple of the stage width 16 NQ, so the last stage's loads are guarded;
+// otherwise every load is unconditional (rows past E read row 0, their results are not stored),
+// which keeps the loaded values in the registers the products read (a guarded load has to be
+// merged with the zero default: ~190 register moves per stage and wavefront).
+template <int T, bool PAIR, bool RAGGED>
 __global__ __launch_bounds__(kEwBwdThreads, T >= 2 ? 3 : 2) void k_ew_bwd(const float* __restrict__ gw, int64_t E, int N,
                                                        const f16x8* __restrict__ frag,
                                                        const float* __restrict__ colscale, int K, int nstages,
@@ -251,8 +255,25 @@ __global__ __launch_bounds__(kEwBwdThreads, T >= 2 ? 3 : 2) void k_ew_bwd(const 
     const float* asrc = gw + src0 * ld + 8 * (lane >> 5);
     const float* bsrc = gw + src1 * ld + 8 * (lane >> 5);
 
-    f32x4 ra[NQ][2];
-    auto fetch_a = [&](int s) {
+    // the gradient rows of two stages alternate between two register sets (the loop is unrolled
+    // by two, so that neither set is copied into the other at the loop's back edge)
+    using Rows = f32x4[NQ][2];
+    Rows ra, rb;
+    auto fetch_a = [&](Rows& r, int s) {
+        if (!RAGGED) {
+#pragma unroll
+            for (int q = 0; q < NQ; ++q) {
+                f32x4 lo = *reinterpret_cast<const f32x4*>(asrc + 16 * (NQ * s + q));
+                f32x4 hi = *reinterpret_cast<const f32x4*>(asrc + 16 * (NQ * s + q) + 4);
+                if (PAIR) {
+                    lo += *reinterpret_cast<const f32x4*>(bsrc + 16 * (NQ * s + q));
+                    hi += *reinterpret_cast<const f32x4*>(bsrc + 16 * (NQ * s + q) + 4);
+                }
+                r[q][0] = lo;
+                r[q][1] = hi;
+            }
+            return;
+        }
 #pragma unroll
         for (int q = 0; q < NQ; ++q) {
             const int n = 16 * (NQ * s + q) + 8 * (lane >> 5);
@@ -265,8 +286,8 @@ __global__ __launch_bounds__(kEwBwdThreads, T >= 2 ? 3 : 2) void k_ew_bwd(const 
                     hi += *reinterpret_cast<const f32x4*>(bsrc + 16 * (NQ * s + q) + 4);
                 }
             }
-            ra[q][0] = lo;
-            ra[q][1] = hi;
+            r[q][0] = lo;
+            r[q][1] = hi;
         }
     };
     f16x8 pre[PER];
@@ -282,15 +303,21 @@ __global__ __launch_bounds__(kEwBwdThreads, T >= 2 ? 3 : 2) void k_ew_bwd(const 
 #pragma unroll
     for (int t = 0; t < T; ++t) acc[t] = f32x16{};
     int ecur = kEwNoExp;
-    fetch_a(0);
-    fetch_b(0);
-    for (int s = 0; s < nstages; ++s) {
-        const int buf = s & 1;
+    // stage s: its rows in cur, W's fragments in pre (staged into LDS buffer buf); loads stage
+    // s + 1 into nxt and pre.  With two gradient rows per product row (PAIR) those loads are issued
+    // first, so that they have the whole stage to arrive (measured: K = 128, 1.44 -> 1.41 ms at
+    // 512 columns, 3.39 -> 3.31 ms at 1280); with one row per product row they wait until after the
+    // barrier (K = 64, 2944 columns: 6.80 ms, 7.12 ms when issued first)
+    auto stage = [&](int s, int buf, Rows& cur, Rows& nxt) {
 #pragma unroll
         for (int i = 0; i < PER; ++i) sB[buf][threadIdx.x + i * kEwBwdThreads] = pre[i];
+        if (PAIR && s + 1 < nstages) {
+            fetch_b(s + 1);
+            fetch_a(nxt, s + 1);
+        }
         float m = 0.f;
 #pragma unroll
-        for (int q = 0; q < NQ; ++q) m = absmax8(ra[q][0], ra[q][1], m);
+        for (int q = 0; q < NQ; ++q) m = absmax8(cur[q][0], cur[q][1], m);
         m = fmaxf(m, __shfl_xor(m, 32));
         const int enew = max(ecur, ew_exp(m));
         if (__ballot(enew != ecur)) {
@@ -302,10 +329,10 @@ __global__ __launch_bounds__(kEwBwdThreads, T >= 2 ? 3 : 2) void k_ew_bwd(const 
         f16x8 g0[NQ], g1[NQ];
         const float si = ldexpf(1.f, -ecur);
 #pragma unroll
-        for (int q = 0; q < NQ; ++q) split8(ra[q][0], ra[q][1], si, g0[q], g1[q]);
+        for (int q = 0; q < NQ; ++q) split8(cur[q][0], cur[q][1], si, g0[q], g1[q]);
         __syncthreads();
-        if (s + 1 < nstages) {
-            fetch_a(s + 1);
+        if (!PAIR && s + 1 < nstages) {
+            fetch_a(nxt, s + 1);
             fetch_b(s + 1);
         }
         const f16x8* B = &sB[buf][lane];
@@ -319,6 +346,12 @@ __global__ __launch_bounds__(kEwBwdThreads, T >= 2 ? 3 : 2) void k_ew_bwd(const 
                 acc[t] = mfma(wq(0, q, t), g0[q], acc[t]);
             }
         }
+    };
+    fetch_a(ra, 0);
+    fetch_b(0);
+    for (int s = 0; s < nstages; s += 2) {
+        stage(s, 0, ra, rb);
+        if (s + 1 < nstages) stage(s + 1, 1, rb, ra);
     }
     if (!aok) return;
     const float so = ldexpf(1.f, ecur == kEwNoExp ? 0 : ecur);
@@ -439,8 +472,15 @@ int mnx_edge_weights_bwd_cols_f32(const float* grad_w, int64_t ld, const int32_t
     const float* cs = reinterpret_cast<const float*>(frag + sh.planes(true));
     hipStream_t s = (hipStream_t)stream;
     const int tiles = sh.tiles_b();
-    auto fn = pairs ? (tiles == 1 ? k_ew_bwd<1, true> : tiles == 2 ? k_ew_bwd<2, true> : k_ew_bwd<4, true>)
-                    : (tiles == 1 ? k_ew_bwd<1, false> : tiles == 2 ? k_ew_bwd<2, false> : k_ew_bwd<4, false>);
+    // stage width 16 NQ = 128 / tiles columns
+    const bool ragged = N % (128 / tiles) != 0;
+    decltype(&k_ew_bwd<1, true, true>) fn;
+    if (ragged)
+        fn = pairs ? (tiles == 1 ? k_ew_bwd<1, true, true> : tiles == 2 ? k_ew_bwd<2, true, true> : k_ew_bwd<4, true, true>)
+                   : (tiles == 1 ? k_ew_bwd<1, false, true> : tiles == 2 ? k_ew_bwd<2, false, true> : k_ew_bwd<4, false, true>);
+    else
+        fn = pairs ? (tiles == 1 ? k_ew_bwd<1, true, false> : tiles == 2 ? k_ew_bwd<2, true, false> : k_ew_bwd<4, true, false>)
+                   : (tiles == 1 ? k_ew_bwd<1, false, false> : tiles == 2 ? k_ew_bwd<2, false, false> : k_ew_bwd<4, false, false>);
     hipLaunchKernelGGL(fn, grid, block, 0, s, grad_w, num_edges, N, f, cs, K, sh.stages_b(), pairs, grad_h, ld,
                        accumulate != 0);
     MNX_CHECK_LAUNCH();
