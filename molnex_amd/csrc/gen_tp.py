@@ -164,10 +164,12 @@ def _emit_ids(a, indent, t_expr, dst=("ie", "is", "iw")):
     a(f"{indent}{e} = perm[{t_expr}]; {s_} = snd[{t_expr}]; {w} = wrow ? wrow[{e}] : {e};")
 
 
-def _emit_edge_loop_head(a, cfg, ps, xs, ys, xi):
+def _emit_edge_loop_head(a, cfg, ps, xs, ys, xi, flush=None):
     """The receiver's CSR walk with a two-stage prefetch: the ids of edge t + 2 (including the
     dependent weight-row lookup) are loaded while edge t is processed, and the rows of edge t + 1
-    are loaded at the top of iteration t from ids that are already in registers."""
+    are loaded at the top of iteration t from ids that are already in registers.  `flush`: lines
+    emitted at the top of each iteration after the rows of edge t are taken and before the loads
+    of edge t + 1 are issued (the backward's deferred writes of edge t - 1)."""
     a("  const int beg = row_ptr[n], end = row_ptr[n + 1];")
     a("  int ne = 0, ns = 0, nw = 0, ie = 0, is = 0, iw = 0;")
     a("  " + " ".join(f"float ny{c} = 0.f;" for c in ys))
@@ -188,6 +190,8 @@ def _emit_edge_loop_head(a, cfg, ps, xs, ys, xi):
     a(f"#pragma unroll\n      for (int i = 0; i < {len(xs)}; ++i) xv[k][i] = nxv[k][i];")
     a(f"#pragma unroll\n      for (int i = 0; i < {len(ps)}; ++i) wv[k][i] = nwv[k][i];")
     a("    }")
+    for line in flush or []:
+        a(line)
     a("    if (t + 1 < end) {")
     a("      ne = ie; ns = is; nw = iw;")
     _emit_prefetch(a, cfg, ps, xs, ys, xi, "      ")
@@ -309,8 +313,35 @@ def gen_bwd(cfg: Cfg, g: int) -> str:
                 vnames[(j, m1, m2)] = vi
                 vi += 1
     a("  }")
-    _emit_edge_loop_head(a, cfg, ps, xs, ys, xi)
-    a("    float* __restrict__ gwe = gw ? gw + int64_t(e) * WS : nullptr;")
+    # Writes are deferred by one edge: edge t's weight gradient, grad_x atomics and grad_Y partial
+    # stay in registers (dgw, dgx, dgy) and are issued at the top of iteration t + 1, after the
+    # rows of edge t + 1 have arrived and before the loads of edge t + 2.  Waiting for loads with
+    # writes outstanding drains the whole vector memory counter (loads and writes retire out of
+    # order on gfx9), so writes issued after the next edge's loads -- the natural order -- made
+    # every iteration wait for its own atomics to complete.
+    flush = []
+    f = flush.append
+    f("    if (pend) {")
+    f("      float* __restrict__ gwe = gw ? gw + int64_t(de) * WS : nullptr;")
+    f("      float* __restrict__ gxs = gx ? gx + int64_t(ds) * XS : nullptr;")
+    f("#pragma unroll")
+    f("      for (int k = 0; k < CPL; ++k) {")
+    f("        if (!ok[k]) continue;")
+    for j, p in enumerate(ps):
+        f(f"        if (gwe) __builtin_nontemporal_store(dgw[k][{j}], gwe + {p['k']} * C + cc[k]);")
+    f("        if (gxs) {")
+    for c in xs:
+        f(f"          atomicAdd(gxs + {c} * C + cc[k], dgx[k][{xi[c]}]);")
+    f("        }")
+    f("      }")
+    f(f"      if (gyp && (lane & (64 / {V} - 1)) == 0 && dcomp < {cfg.NY}) "
+      f"gyp[(int64_t(de) * npart + pidx) * {cfg.NY} + dcomp] = dgy;")
+    f("    }")
+    a(f"  float dgw[CPL][{len(ps)}], dgx[CPL][{len(xs)}], dgy = 0.f;")
+    a(f"  const int dcomp = reduce_scatter_index<{V}>(lane);")
+    a("  int de = 0, ds = 0;")
+    a("  bool pend = false;")
+    _emit_edge_loop_head(a, cfg, ps, xs, ys, xi, flush)
     a(f"    float gy[{V}];")
     a("#pragma unroll")
     a(f"    for (int i = 0; i < {V}; ++i) gy[i] = 0.f;")
@@ -347,19 +378,15 @@ def gen_bwd(cfg: Cfg, g: int) -> str:
                 expr = f"fmaf(y{p['o2'] + m2}, s{j}_{m2}, {expr})"
         else:
             expr = "0.f"
-        a(f"      if (gwe && ok[k]) __builtin_nontemporal_store({expr}, gwe + {p['k']} * C + cc[k]);")
-    a("      if (gx && ok[k]) {")
-    a("        float* __restrict__ gxs = gx + int64_t(s) * XS;")
+        a(f"      dgw[k][{j}] = {expr};")
     for c in xs:
-        a(f"        atomicAdd(gxs + {c} * C + cc[k], gxl[{xi[c]}]);")
-    a("      }")
+        a(f"      dgx[k][{xi[c]}] = gxl[{xi[c]}];")
     a("    }")
-    a("    if (gyp) {")
-    a(f"      float r = wave_reduce_scatter<{V}>(gy, lane);")
-    a(f"      const int comp = reduce_scatter_index<{V}>(lane);")
-    a(f"      if ((lane & (64 / {V} - 1)) == 0 && comp < {cfg.NY}) gyp[(int64_t(e) * npart + pidx) * {cfg.NY} + comp] = r;")
-    a("    }")
+    a(f"    if (gyp) dgy = wave_reduce_scatter<{V}>(gy, lane);")
+    a("    de = e; ds = s; pend = true;")
     a("  }")
+    for line in flush:
+        a(line[2:] if line.startswith("  ") else line)
     a("}")
     return "\n".join(L)
 
