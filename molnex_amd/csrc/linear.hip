@@ -449,8 +449,11 @@ int block_linear(const float* a, int64_t a_stride, int32_t nseg, const int64_t* 
     MNX_REQUIRE(blocks < (int64_t(1) << 31), "too many rows");
     const int nt = lin_tiles(N);
     const dim3 grid(unsigned(blocks), unsigned(ceil_div(N, nt * 32)));
-    if (!idx && p.K > 0 && p.K <= kLinResMaxK && lin_resident()) {
-        // weights resident in LDS: one workgroup per CU walks row tiles
+    if (!idx && p.K > 0 && p.K <= kLinResMaxK && nt >= 2 && lin_resident()) {
+        // weights resident in LDS: one workgroup per CU walks row tiles.  Not for one column tile
+        // (N <= 32): there each wavefront's single accumulator chain is latency-bound at the
+        // resident grid's occupancy, and the chunked kernel's full grid is faster (Allegro's
+        // 16-channel projection over 2.6 M edges x 5 components: 576 vs 690 us)
         const dim3 rgrid(unsigned(std::min<int64_t>(blocks, 256)), grid.y);
         switch (nt) {
             case 1: launch_res<1>(d, rgrid, stream, p); break;
