@@ -2,7 +2,9 @@
 weights (no scatter) of Allegro's layers, forward and backward, one kernel per
 configuration and channel width.
 
-    out[e][o3 + m3][c] = w[p][c] * sum_{m1, m2} cf_p[m1][m2][m3] x[e][o1 + m1][c] Y[e][o2 + m2]
+    out[e][row(p, m3)][c] = w[p][c] * sum_{m1, m2} cf_p[m1][m2][m3] x[e][o1 + m1][c] Y[e][o2 + m2]
+
+with the rows of the paths that share an output irrep interleaved (out_row below)
 
 (src/molzoo/allegro.py:352-359 builds it as cuet.ChannelWiseTensorProduct(irreps_in,
 sh_irreps, shared_weights=True); :457-458 applies it to the pre-scaled edge features
@@ -17,7 +19,7 @@ sum_m1 grad_(s x)[m1] x[m1] per edge and channel.
 Lane layout: a wavefront holds 64 / CW edges side by side, CW = min(C, 64) lanes
 per edge, one channel per lane (CPL = 2 channels per lane for C = 128), so small
 channel counts (Allegro's default is 16) still fill the wave.  Backward per lane
-and channel: v_p[m1][m2] = sum_m3 cf g[o3 + m3] (g the output gradient), then
+and channel: v_p[m1][m2] = sum_m3 cf g[row(p, m3)] (g the output gradient), then
 grad_x[m1] = sum_p w_p sum_m2 Y[m2] v_p[m1][m2] (stored once: x is per edge),
 grad_Y[m2] = sum_c sum_p w_p sum_m1 x[m1] v_p[m1][m2] (reduced over the CW lanes of
 the edge by xor shuffles), grad_w[p][c] = sum_e sum_m1 x[m1] (sum_m2 Y v)[m1]
@@ -40,6 +42,27 @@ from molnex_amd.csrc.gen_tp import EPS, Cfg, config_list, f32  # noqa: E402
 VARIANTS = ((8, 1), (16, 1), (32, 1), (64, 1), (64, 2))
 
 
+def out_row(cfg: Cfg):
+    """Output row of (path k, m3).  The paths sharing an output irrep form one block of
+    multiplicity (paths x C), irrep component outermost: row = first row of the irrep's rows
+    + m3 * (paths of that irrep) + the path's rank among them (ascending path order), C channels
+    per row.  The projection after the product then reads one input segment per output irrep, and
+    its input gradient is one launch per irrep instead of one per path (the per-path blocks of the
+    irreps sorted by irrep, in the same path order, hold the same numbers with the rows permuted)."""
+    rows = {}
+    groups = {}
+    for p in sorted(cfg.paths, key=lambda p: p["o3"]):
+        groups.setdefault(p["l3"], []).append(p)
+    for l3, ps in groups.items():
+        base = min(p["o3"] for p in ps)
+        nb = len(ps)
+        assert max(p["o3"] for p in ps) == base + (nb - 1) * (2 * l3 + 1), "blocks of one irrep not adjacent"
+        for b, p in enumerate(ps):
+            for m3 in range(2 * l3 + 1):
+                rows[(p["k"], m3)] = base + m3 * nb + b
+    return rows
+
+
 def fwd_groups(cfg: Cfg) -> int:
     """Edge groups per forward wavefront, their loads all in flight before any arithmetic: 2 up to
     l_max = 2 (1.99 -> 1.39 ms at l_max 2, C = 16, 2.6 M edges), 1 for l_max = 3 (registers)."""
@@ -56,6 +79,7 @@ def _fwd(cfg: Cfg) -> str:
     a = L.append
     NX, NY, NO, NP = cfg.NX, cfg.NY, cfg.NO, cfg.NP
     EPW = fwd_groups(cfg)
+    rows = out_row(cfg)
     a(f"template <int CW, int CPL>\n__global__ void __launch_bounds__(256) etp_fwd_c{cfg.idx}("
       "const float* __restrict__ x, const float* __restrict__ Y, const float* __restrict__ w, "
       "const float* __restrict__ xs, int64_t E, int C, float* __restrict__ out) {")
@@ -100,7 +124,7 @@ def _fwd(cfg: Cfg) -> str:
                 for m2, v in terms[1:]:
                     expr = f"fmaf({f32(v)}, y[q][{p['o2'] + m2}], {expr})"
                 row.append((m1, expr))
-            o = p["o3"] + m3
+            o = rows[(p["k"], m3)]
             if not row:
                 a(f"        oe[{o} * C + c] = 0.f;")
                 continue
@@ -119,6 +143,7 @@ def _bwd(cfg: Cfg) -> str:
     L = []
     a = L.append
     NX, NY, NO, NP = cfg.NX, cfg.NY, cfg.NO, cfg.NP
+    rows = out_row(cfg)
     a(f"template <int CW, int CPL>\n__global__ void __launch_bounds__(256) etp_bwd_c{cfg.idx}("
       "const float* __restrict__ gout, const float* __restrict__ x, const float* __restrict__ Y, "
       "const float* __restrict__ w, const float* __restrict__ xs, int64_t E, int C, float* __restrict__ gx, "
@@ -160,9 +185,9 @@ def _bwd(cfg: Cfg) -> str:
                 terms = [(m3, cf[m1, m2, m3]) for m3 in range(2 * p["l3"] + 1) if abs(cf[m1, m2, m3]) > EPS]
                 if not terms:
                     continue
-                expr = f"{f32(terms[0][1])} * gv[{p['o3'] + terms[0][0]}]"
+                expr = f"{f32(terms[0][1])} * gv[{rows[(p['k'], terms[0][0])]}]"
                 for m3, v in terms[1:]:
-                    expr = f"fmaf({f32(v)}, gv[{p['o3'] + m3}], {expr})"
+                    expr = f"fmaf({f32(v)}, gv[{rows[(p['k'], m3)]}], {expr})"
                 vs.append((m2, expr))
             if not vs:
                 continue

@@ -549,12 +549,39 @@ def edge_tp_supported(config: int, channels: int) -> bool:
     return config >= 0 and _lib.load().mnx_edge_tp_bwd_workspace_bytes(config, channels, 1) > 0
 
 
+def edge_tp_out_rows(ls: list[int]) -> list[int]:
+    """Output layout of ``molix::edge_tp`` for input, harmonics and outputs l = ``ls``: entry i is the
+    row (C channels each) that holds row i of the per-path layout (one block per path, blocks
+    sorted by output irrep in path order, component-major within a block).  The kernel stores the
+    paths that share an output irrep as one block of multiplicity (paths x C), component
+    outermost: row = first row of the irrep + m3 * (its paths) + the path's rank among them."""
+    from .irreps import ChannelwiseTPDescriptor, Irreps
+
+    irr = Irreps(" + ".join(f"1x{l}{'e' if l % 2 == 0 else 'o'}" for l in ls))
+    d = ChannelwiseTPDescriptor(irr, irr, irr)
+    offs = [0]
+    for b in d.irreps_out:
+        offs.append(offs[-1] + b.ir.dim)
+    by_l = {}
+    for p in sorted(d.paths, key=lambda p: offs[p.out_block]):
+        by_l.setdefault(p.l3, []).append(p)
+    rows = [0] * offs[-1]
+    for l3, ps in by_l.items():
+        base = min(offs[p.out_block] for p in ps)
+        for b, p in enumerate(ps):
+            for m3 in range(2 * l3 + 1):
+                rows[offs[p.out_block] + m3] = base + m3 * len(ps) + b
+    return rows
+
+
 @torch.library.custom_op("molix::edge_tp", mutates_args=(), device_types="cuda")
 def edge_tp(x: Tensor, Y: Tensor, w: Tensor, config: int, channels: int, x_scale: Tensor | None = None) -> Tensor:
     """``out[e] = TP(s[e] * x[e], Y[e]; w)``: per-edge channelwise product with weights shared by
     all edges (``w`` is ``(num_paths, C)``), no scatter -- Allegro's layer product
     (src/molzoo/allegro.py:352-359,457-458); the optional ``x_scale`` ``(E, C)`` multiplies every
-    component of channel c of x[e] first (the env weights of allegro.py:447-450)."""
+    component of channel c of x[e] first (the env weights of allegro.py:447-450).  The paths of
+    one output irrep form one block of (paths x C) channels (``edge_tp_out_rows``), so the
+    projection that follows reads one input segment per irrep."""
     _require_gpu("edge_tp", x, Y, w, x_scale)
     num_paths, nx, ny, no = tp_config_info(config)
     E = Y.shape[0]

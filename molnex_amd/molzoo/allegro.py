@@ -66,7 +66,7 @@ class EdgeChannelWiseTensorProduct(nn.Module):
     """Per-edge channelwise product ``F x (0..l_max) (x) (0..l_max)`` with one weight per path and
     channel shared by all edges (``shared_weights=True, internal_weights=True``).  ``irreps_out``
     lists the blocks the Allegro projection reads: the paths whose output irrep is an input irrep,
-    sorted by irrep (stable in path order)."""
+    merged into one block per irrep (paths x C channels, in path order)."""
 
     def __init__(self, irreps_in, irreps_sh, *, dtype=None):
         super().__init__()
@@ -91,9 +91,15 @@ class EdgeChannelWiseTensorProduct(nn.Module):
         num_paths, nx, ny, no = K.tp_config_info(self.config_id)
         if num_paths != len(kept):
             raise RuntimeError("compiled per-edge product does not match the path enumeration")
-        order = sorted(range(len(kept)), key=lambda i: (full[kept[i]][2], 0, i))
+        # one block per output irrep, (paths of that irrep) x C channels, path-major in path order
+        # (molix::edge_tp's layout): the same numbers as per-path blocks sorted by irrep, with the
+        # projection's weights in the same flat order, and one projection segment per irrep
+        counts = {}
+        for k in kept:
+            l3, par = full[k][2], full[k][3]
+            counts[(l3, par)] = counts.get((l3, par), 0) + 1
         self.irreps_out = Irreps(" + ".join(
-            f"{self.channels}x{full[kept[i]][2]}{'e' if full[kept[i]][3] == 1 else 'o'}" for i in order))
+            f"{n * self.channels}x{l3}{'e' if par == 1 else 'o'}" for (l3, par), n in sorted(counts.items())))
         if self.irreps_out.dim != no * self.channels:
             raise RuntimeError("compiled per-edge product output size mismatch")
         dt = dtype if dtype is not None else config.ftype

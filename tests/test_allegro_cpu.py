@@ -27,7 +27,8 @@ def test_parameters_mirror_reference():
     layer = m.layers[0]
     # l_max 2: 19 paths of (0e+1o+2e) x (0e+1o+2e), 11 of them reach an input irrep
     assert layer.tp.weight.shape == (1, 19 * 8)
-    assert str(layer.tp.irreps_out).replace(" ", "").count("8x") == 11
+    # one block per output irrep: 3 x 0e, 4 x 1o, 4 x 2e paths of 8 channels
+    assert str(layer.tp.irreps_out).replace(" ", "") == "24x0e+32x1o+32x2e"
     assert layer.tp.irreps_out.dim == 35 * 8
     # projection: 3 x 0e, 4 x 1o, 4 x 2e input blocks of 8 channels onto 8 channels each
     assert layer.tp_linear.weight.numel() == (3 + 4 + 4) * 8 * 8

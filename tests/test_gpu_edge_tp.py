@@ -48,7 +48,19 @@ def oracle_case(l_max, C, E, seed):
     ref = tp.forward(x, Y, wb, ei, E)
     rx, rY, rw = tp.backward(x, Y, wb, ei, g)
     rw = rw.reshape(E, len(tp.paths), C).sum(0)
-    return ls, x, Y, w, g, ref, rx, rY, rw
+    return ls, x, Y, w, to_kernel_rows(g, ls, C), to_kernel_rows(ref, ls, C), rx, rY, rw
+
+
+def to_kernel_rows(a, ls, C):
+    """The oracle's per-path output rows in molix::edge_tp's layout (the paths of one output
+    irrep merged into one block, kernels.edge_tp_out_rows)."""
+    import molnex_amd.kernels as K
+
+    rows = K.edge_tp_out_rows(ls)
+    a = np.asarray(a).reshape(a.shape[0], len(rows), C)
+    out = np.empty_like(a)
+    out[:, rows] = a
+    return out.reshape(a.shape[0], -1)
 
 
 @pytest.mark.parametrize("l_max", [0, 1, 2, 3])

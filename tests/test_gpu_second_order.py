@@ -281,8 +281,11 @@ def test_edge_tp_second_order_identities_vs_fp64_restatement():
         xs = (xx.view(E, NX, C) * ss.unsqueeze(1)).reshape(E, -1)
         return AR.edge_tp(xs, YY, wfull.reshape(1, -1), l_max, C)[0]
 
+    rows = torch.tensor(K.edge_tp_out_rows(ls), device=DEV)
+
     def hip_fn(xx, YY, ww, ss):
-        return K.edge_tp(xx, YY, ww, config, C, ss)
+        # the kernel's rows (one block per output irrep) read back in the oracle's per-path order
+        return K.edge_tp(xx, YY, ww, config, C, ss).view(E, NO, C)[:, rows].reshape(E, -1)
 
     ref = second(ref_fn, [x, Y, wk, s])
     # the HIP path in fp32 on the GPU: cotangents and primals cast once
