@@ -45,6 +45,24 @@ def _env_weight_harmonics(edge_angular, env_weights, l_max, num_tensor_features,
     return out.reshape(E, irreps_dim)
 
 
+def _silu_stack(mlp: nn.Sequential, x: torch.Tensor) -> torch.Tensor:
+    """``mlp(x)`` for a stack of [Linear -> SiLU] layers of one width: one fused HIP kernel each way
+    (``molix::radial_hidden``, gradient w.r.t. x only) when the parameters need no gradient and the
+    shape is compiled (the pair embedding's scalar MLP, 40 -> 64 -> 64 -> 64 at the defaults: six
+    passes over (E, 64) activations in the torch form), else the modules themselves."""
+    lins, acts = list(mlp)[0::2], list(mlp)[1::2]
+    ok = (config.fused_radial and x.is_cuda and x.dim() == 2 and x.dtype == torch.float32 and len(lins) == len(acts)
+          and all(isinstance(m, nn.Linear) and m.bias is not None and m.weight.dtype == torch.float32 for m in lins)
+          and all(isinstance(m, nn.SiLU) for m in acts)
+          and len({m.out_features for m in lins}) == 1 and lins[0].in_features == x.shape[1]
+          and all(m.in_features == lins[0].out_features for m in lins[1:])
+          and not (torch.is_grad_enabled() and any(p.requires_grad for p in mlp.parameters())))
+    if ok and K.radial_supported(lins[0].in_features, lins[0].out_features, len(lins)):
+        raw = torch.cat([t.detach().reshape(-1) for m in lins for t in (m.weight, m.bias)])
+        return K.radial_hidden(x, raw, lins[0].in_features, lins[0].out_features, len(lins))
+    return mlp(x)
+
+
 def _scale_by_channel(tensor, scale, l_max, num_tensor_features):
     """Scale every component of channel ``c`` by ``scale[e, c]`` (allegro.py:100-130)."""
     E = tensor.shape[0]
@@ -143,7 +161,7 @@ class PairEmbedding(nn.Module):
         edge_radial = self.radial_basis(bond_dist) * edge_cutoff.unsqueeze(-1)
         edge_angular = self.spherical_harmonics(bond_diff / (bond_dist.unsqueeze(-1) + 1e-8))
         type_embed = torch.cat([self.type_embedding(Z[src]), self.type_embedding(Z[dst])], dim=-1)
-        scalar_features = self.scalar_mlp(torch.cat([edge_radial, type_embed], dim=-1))
+        scalar_features = _silu_stack(self.scalar_mlp, torch.cat([edge_radial, type_embed], dim=-1))
         env_weights = self.tensor_env(scalar_features)
         tensor_features = _env_weight_harmonics(edge_angular, env_weights, self.l_max, self.num_tensor_features,
                                                 self.irreps_dim)

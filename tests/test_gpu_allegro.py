@@ -72,6 +72,45 @@ def test_allegro_matches_fp64_oracle(l_max, F, S, layers, avg):
     assert _rel(fg, f64) <= 1e-5, _rel(fg, f64)
 
 
+@pytest.mark.parametrize("l_max,F,S,layers,avg", [(2, 16, 64, 2, 12.0), (1, 16, 32, 2, None)])
+def test_allegro_frozen_fused_scalar_mlp_vs_fp64_oracle(l_max, F, S, layers, avg):
+    """Parameters frozen (energy + forces in eval): the pair embedding's scalar MLP runs as the
+    fused hidden-stack kernel (molix::radial_hidden, 40 -> S -> S -> S with SiLU); features and
+    forces against the fp64 oracle and against the torch form."""
+    import molnex_amd.kernels as K
+    from molnex_amd.config import config
+
+    pos, Z, ei, rc = _system()
+    m, cfg = _model(l_max, F, S, layers, avg)
+    mg = m.to(DEV)
+    for p in mg.parameters():
+        p.requires_grad_(False)
+    assert K.radial_supported(8 + 2 * 16, S, 3)
+    readout = torch.randn(layers, S, dtype=torch.float64, generator=torch.Generator().manual_seed(2))
+
+    def run():
+        pg = pos.float().to(DEV).requires_grad_(True)
+        diff, dist = _geometry(pg, ei.to(DEV))
+        feats = mg(Z=Z.to(DEV), bond_dist=dist, bond_diff=diff, edge_index=ei.to(DEV))
+        (fg,) = torch.autograd.grad((feats * readout.float().to(DEV)).sum(), pg)
+        return feats, fg
+
+    feats, fg = run()
+    prev = config.fused_radial
+    config.fused_radial = False
+    try:
+        feats_t, fg_t = run()
+    finally:
+        config.fused_radial = prev
+    p64 = pos.clone().requires_grad_(True)
+    diff64, dist64 = _geometry(p64, ei)
+    ref = AR.allegro_features(m.state_dict(), cfg, Z, dist64, diff64, ei)
+    (f64,) = torch.autograd.grad((ref * readout).sum(), p64)
+    for a, b in ((feats, ref), (fg, f64), (feats_t, ref), (fg_t, f64)):
+        assert _rel(a, b) <= 1e-5, _rel(a, b)
+    assert _rel(feats, feats_t) <= 1e-5
+
+
 def test_allegro_rotation_invariant_and_contract():
     """Scalar edge features are invariant under a rotation of the positions (the reference checks
     rtol = atol = 1e-4; fp32 here stays far inside), and the GraphBatch contract writes
