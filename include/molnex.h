@@ -696,6 +696,31 @@ int mnx_edge_tp_bwd_f32(int32_t config, int32_t channels, const float* x, const 
                         float* grad_x_scale, void* workspace, size_t workspace_bytes,
                         mnx_stream_t stream);
 
+/* ------------------------------------------------------------------------ */
+/* Per-channel scaling of an ir_mul edge tensor (Allegro's output env        */
+/* scaling, src/molzoo/allegro.py:95-128 _scale_by_channel):                 */
+/*   out[e][d][c] = t[e][d][c] * s[e][c]  (t, out [E][D][F], s [E][F]),       */
+/* and its backward in one pass: grad_t = grad * s (broadcast over d),       */
+/* grad_s[e][c] = sum_d grad[e][d][c] t[e][d][c] (d ascending).  D in        */
+/* {1, 4, 9, 16}, F a multiple of 4, every pointer 16-byte aligned; NULL     */
+/* grad_t / grad_s are skipped.                                               */
+/* ------------------------------------------------------------------------ */
+int mnx_channel_scale_f32(const float* t, const float* s, int64_t E, int32_t D, int32_t F, float* out,
+                          mnx_stream_t stream);
+int mnx_channel_scale_bwd_f32(const float* grad, const float* t, const float* s, int64_t E, int32_t D, int32_t F,
+                              float* grad_t, float* grad_s, mnx_stream_t stream);
+/* Per-edge outer product of components and channels (the env-weighted      */
+/* harmonics of Allegro's pair embedding, src/molzoo/allegro.py:55-92):      */
+/*   out[e][d][c] = y[e][d] * s[e][c]  (y [E][D], s [E][F], out [E][D][F]);  */
+/* backward grad_y[e][d] = sum_c grad[e][d][c] s[e][c], grad_s[e][c] =        */
+/* sum_d grad[e][d][c] y[e][d], one pass.  D in {1, 4, 9, 16}; F a multiple  */
+/* of 4 with F / 4 a power of two <= 64 for the backward; s, out, grad and   */
+/* grad_s 16-byte aligned.                                                    */
+int mnx_channel_outer_f32(const float* y, const float* s, int64_t E, int32_t D, int32_t F, float* out,
+                          mnx_stream_t stream);
+int mnx_channel_outer_bwd_f32(const float* grad, const float* y, const float* s, int64_t E, int32_t D, int32_t F,
+                              float* grad_y, float* grad_s, mnx_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

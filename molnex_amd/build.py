@@ -36,7 +36,7 @@ EXTRA = {
     # bit-exact reference geometry: no fused multiply-add contraction
     "nlist.hip": ["-ffp-contract=off"],
 }
-SOURCES = ["errors.cpp", "nlist.hip", "csr.hip", "sh.hip", "tp.hip", "pme.hip", "symcon.hip", "radial.hip", "edges.hip", "linear.hip", "edge_weights.hip", "edge_tp.hip", "segment.hip", "tp_gh.hip", "embed.hip", "pairs.hip", "tp_any.hip", "tall_gemm.hip", "tp_fused.hip"]
+SOURCES = ["errors.cpp", "nlist.hip", "csr.hip", "sh.hip", "tp.hip", "pme.hip", "symcon.hip", "radial.hip", "edges.hip", "linear.hip", "edge_weights.hip", "edge_tp.hip", "segment.hip", "tp_gh.hip", "embed.hip", "pairs.hip", "tp_any.hip", "tall_gemm.hip", "tp_fused.hip", "chscale.hip"]
 
 
 def _compile(src: str) -> str:

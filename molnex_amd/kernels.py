@@ -2158,6 +2158,209 @@ bond_vectors.register_autograd(_bond_bwd, setup_context=_bond_setup)
 
 
 # ---------------------------------------------------------------------------
+# Per-channel scaling of an ir_mul edge tensor (Allegro's output env scaling)
+# ---------------------------------------------------------------------------
+
+
+def _cs_rows(t: Tensor, width: int, what: str) -> Tensor:
+    if t.dtype != torch.float32 or t.dim() != 2 or t.shape[1] != width:
+        raise ValueError(f"channel_scale: {what} must be float32 (E, {width})")
+    return _aligned16(t)
+
+
+@torch.library.custom_op("molix::channel_scale", mutates_args=(), device_types="cuda")
+def channel_scale(t: Tensor, s: Tensor, components: int) -> Tensor:
+    """``out[e][d][c] = t[e][d][c] * s[e][c]`` for an (E, D*F) ir_mul tensor and (E, F) scales: the
+    reference's ``_scale_by_channel`` (src/molzoo/allegro.py:95-128); one HIP pass each way (the
+    backward forms both gradients in one pass, ``mnx_channel_scale_bwd_f32``)."""
+    _require_gpu("channel_scale", t, s)
+    F = s.shape[1]
+    ts = _cs_rows(t, components * F, "t")
+    ss = _cs_rows(s, F, "s")
+    if ts.shape[0] != ss.shape[0]:
+        raise ValueError("channel_scale: t and s must have the same number of rows")
+    out = torch.empty_like(ts)
+    check(_lib.load().mnx_channel_scale_f32(ptr(ts), ptr(ss), ts.shape[0], components, F, ptr(out), _stream(ts)),
+          "channel_scale")
+    return out
+
+
+@channel_scale.register_fake
+def _(t, s, components):
+    return t.new_empty(t.shape)
+
+
+@torch.library.custom_op("molix::channel_scale_backward", mutates_args=(), device_types="cuda")
+def channel_scale_backward(grad: Tensor, t: Tensor, s: Tensor, components: int, need_t: bool,
+                           need_s: bool) -> tuple[Tensor, Tensor]:
+    """(grad * s, sum_d grad * t) of ``channel_scale`` in one pass; an empty tensor for a gradient
+    not requested."""
+    _require_gpu("channel_scale_backward", grad, t, s)
+    F = s.shape[1]
+    g = _cs_rows(grad, components * F, "grad")
+    ts = _cs_rows(t, components * F, "t")
+    ss = _cs_rows(s, F, "s")
+    gt = torch.empty_like(g) if need_t else g.new_empty(0)
+    gs = torch.empty_like(ss) if need_s else g.new_empty(0)
+    check(_lib.load().mnx_channel_scale_bwd_f32(ptr(g), ptr(ts), ptr(ss), g.shape[0], components, F,
+                                                ptr(gt) if need_t else None, ptr(gs) if need_s else None,
+                                                _stream(g)), "channel_scale backward")
+    return gt, gs
+
+
+@channel_scale_backward.register_fake
+def _(grad, t, s, components, need_t, need_s):
+    return (grad.new_empty(grad.shape) if need_t else grad.new_empty(0),
+            s.new_empty(s.shape) if need_s else s.new_empty(0))
+
+
+def _cs_setup(ctx, inputs, output):
+    t, s, components = inputs
+    ctx.save_for_backward(t, s)
+    ctx.components = components
+
+
+def _cs_bwd(ctx, grad):
+    t, s = ctx.saved_tensors
+    need_t, need_s = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
+    if not (need_t or need_s):
+        return None, None, None
+    gt, gs = channel_scale_backward(grad.contiguous(), t, s, ctx.components, need_t, need_s)
+    return (gt if need_t else None), (gs if need_s else None), None
+
+
+channel_scale.register_autograd(_cs_bwd, setup_context=_cs_setup)
+
+
+def _cs2_setup(ctx, inputs, output):
+    grad, t, s, components, need_t, need_s = inputs
+    ctx.save_for_backward(grad, t, s)
+    ctx.components = components
+    ctx.flags = (need_t, need_s)
+
+
+def _cs2_bwd(ctx, ggt, ggs):
+    """Second order: gt = g s and gs = sum_d g t are bilinear, so with cotangents (ggt, ggs)
+    d/dg = ggt s + t ggs, d/dt = g ggs, d/ds = sum_d ggt g -- the same two kernels."""
+    grad, t, s = ctx.saved_tensors
+    D = ctx.components
+    need_t, need_s = ctx.flags
+    has_t = need_t and ggt is not None and ggt.numel() > 0
+    has_s = need_s and ggs is not None and ggs.numel() > 0
+    dg = dt = ds = None
+    if ctx.needs_input_grad[0]:
+        dg = torch.zeros_like(grad)
+        if has_t:
+            dg = dg + channel_scale(ggt.contiguous(), s, D)
+        if has_s:
+            dg = dg + channel_scale(t, ggs.contiguous(), D)
+    if ctx.needs_input_grad[1] and has_s:
+        dt = channel_scale(grad, ggs.contiguous(), D)
+    if ctx.needs_input_grad[2] and has_t:
+        ds = channel_scale_backward(ggt.contiguous(), grad, s, D, False, True)[1]
+    return dg, dt, ds, None, None, None
+
+
+channel_scale_backward.register_autograd(_cs2_bwd, setup_context=_cs2_setup)
+
+
+CHANNEL_PRODUCT_COMPONENTS = (1, 4, 9, 16)
+
+
+@torch.library.custom_op("molix::channel_outer", mutates_args=(), device_types="cuda")
+def channel_outer(y: Tensor, s: Tensor) -> Tensor:
+    """``out[e][d][c] = y[e][d] * s[e][c]`` as an (E, D*F) ir_mul tensor: the env-weighted harmonics
+    of Allegro's pair embedding (src/molzoo/allegro.py:55-92); the backward forms both gradients in
+    one pass (``mnx_channel_outer_bwd_f32``)."""
+    _require_gpu("channel_outer", y, s)
+    if y.dtype != torch.float32 or y.dim() != 2:
+        raise ValueError("channel_outer: y must be float32 (E, D)")
+    E, D = y.shape
+    F = s.shape[1]
+    ys = y.contiguous()
+    ss = _cs_rows(s, F, "s")
+    if ss.shape[0] != E:
+        raise ValueError("channel_outer: y and s must have the same number of rows")
+    out = ys.new_empty(E, D * F)
+    check(_lib.load().mnx_channel_outer_f32(ptr(ys), ptr(ss), E, D, F, ptr(out), _stream(ys)), "channel_outer")
+    return out
+
+
+@channel_outer.register_fake
+def _(y, s):
+    return y.new_empty(y.shape[0], y.shape[1] * s.shape[1])
+
+
+@torch.library.custom_op("molix::channel_outer_backward", mutates_args=(), device_types="cuda")
+def channel_outer_backward(grad: Tensor, y: Tensor, s: Tensor, need_y: bool, need_s: bool) -> tuple[Tensor, Tensor]:
+    """(sum_c grad * s, sum_d grad * y) of ``channel_outer`` in one pass; an empty tensor for a
+    gradient not requested."""
+    _require_gpu("channel_outer_backward", grad, y, s)
+    E, D = y.shape
+    F = s.shape[1]
+    g = _cs_rows(grad, D * F, "grad")
+    ys = y.contiguous()
+    ss = _cs_rows(s, F, "s")
+    gy = torch.empty_like(ys) if need_y else g.new_empty(0)
+    gs = torch.empty_like(ss) if need_s else g.new_empty(0)
+    check(_lib.load().mnx_channel_outer_bwd_f32(ptr(g), ptr(ys), ptr(ss), E, D, F, ptr(gy) if need_y else None,
+                                                ptr(gs) if need_s else None, _stream(g)), "channel_outer backward")
+    return gy, gs
+
+
+@channel_outer_backward.register_fake
+def _(grad, y, s, need_y, need_s):
+    return (y.new_empty(y.shape) if need_y else y.new_empty(0), s.new_empty(s.shape) if need_s else s.new_empty(0))
+
+
+def _co_setup(ctx, inputs, output):
+    y, s = inputs
+    ctx.save_for_backward(y, s)
+
+
+def _co_bwd(ctx, grad):
+    y, s = ctx.saved_tensors
+    need_y, need_s = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
+    if not (need_y or need_s):
+        return None, None
+    gy, gs = channel_outer_backward(grad.contiguous(), y, s, need_y, need_s)
+    return (gy if need_y else None), (gs if need_s else None)
+
+
+channel_outer.register_autograd(_co_bwd, setup_context=_co_setup)
+
+
+def _co2_setup(ctx, inputs, output):
+    grad, y, s, need_y, need_s = inputs
+    ctx.save_for_backward(grad, y, s)
+    ctx.flags = (need_y, need_s)
+
+
+def _co2_bwd(ctx, ggy, ggs):
+    """Second order: gy = sum_c g s and gs = sum_d g y are bilinear, so with cotangents (ggy, ggs)
+    d/dg = ggy (x) s + y (x) ggs, d/dy = sum_c g ggs, d/ds = sum_d g ggy -- the same two kernels."""
+    grad, y, s = ctx.saved_tensors
+    need_y, need_s = ctx.flags
+    has_y = need_y and ggy is not None and ggy.numel() > 0
+    has_s = need_s and ggs is not None and ggs.numel() > 0
+    dg = dy = ds = None
+    if ctx.needs_input_grad[0]:
+        dg = torch.zeros_like(grad)
+        if has_y:
+            dg = dg + channel_outer(ggy.contiguous(), s)
+        if has_s:
+            dg = dg + channel_outer(y, ggs.contiguous())
+    if ctx.needs_input_grad[1] and has_s:
+        dy = channel_outer_backward(grad, y, ggs.contiguous(), True, False)[0]
+    if ctx.needs_input_grad[2] and has_y:
+        ds = channel_outer_backward(grad, ggy.contiguous(), s, False, True)[1]
+    return dg, dy, ds, None, None
+
+
+channel_outer_backward.register_autograd(_co2_bwd, setup_context=_co2_setup)
+
+
+# ---------------------------------------------------------------------------
 # Radial edge embedding (Bessel basis x cutoff envelope)
 # ---------------------------------------------------------------------------
 

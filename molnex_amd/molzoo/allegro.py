@@ -39,8 +39,13 @@ from .mace import _get, _set
 
 def _env_weight_harmonics(edge_angular, env_weights, l_max, num_tensor_features, irreps_dim):
     """``Y_lm(e) * env(e, c)`` in ir_mul order (allegro.py:55-97): with uniform multiplicity the
-    layout is ``[m over all l][c]``, an outer product per edge."""
-    E = edge_angular.shape[0]
+    layout is ``[m over all l][c]``, an outer product per edge (``molix::channel_outer`` on float32
+    GPU tensors: both gradients in one pass)."""
+    E, D = edge_angular.shape
+    F = env_weights.shape[1]
+    if (edge_angular.is_cuda and edge_angular.dtype == torch.float32 and env_weights.dtype == torch.float32
+            and D in K.CHANNEL_PRODUCT_COMPONENTS and F % 4 == 0 and (F // 4) & (F // 4 - 1) == 0 and F <= 256):
+        return K.channel_outer(edge_angular, env_weights)
     out = edge_angular.unsqueeze(-1) * env_weights.unsqueeze(-2)
     return out.reshape(E, irreps_dim)
 
@@ -64,9 +69,14 @@ def _silu_stack(mlp: nn.Sequential, x: torch.Tensor) -> torch.Tensor:
 
 
 def _scale_by_channel(tensor, scale, l_max, num_tensor_features):
-    """Scale every component of channel ``c`` by ``scale[e, c]`` (allegro.py:100-130)."""
-    E = tensor.shape[0]
-    return (tensor.reshape(E, -1, num_tensor_features) * scale.unsqueeze(-2)).reshape(E, -1)
+    """Scale every component of channel ``c`` by ``scale[e, c]`` (allegro.py:100-130): the
+    ``molix::channel_scale`` kernel (both gradients in one pass) for float32 GPU tensors."""
+    E, F = tensor.shape[0], num_tensor_features
+    if (tensor.is_cuda and tensor.dtype == torch.float32 and scale.dtype == torch.float32 and F % 4 == 0
+            and tensor.dim() == 2 and tensor.shape[1] % F == 0
+            and tensor.shape[1] // F in K.CHANNEL_PRODUCT_COMPONENTS):
+        return K.channel_scale(tensor, scale, tensor.shape[1] // F)
+    return (tensor.reshape(E, -1, F) * scale.unsqueeze(-2)).reshape(E, -1)
 
 
 def _full_paths(in_irreps: Irreps, sh_irreps: Irreps):

@@ -111,6 +111,54 @@ def test_allegro_frozen_fused_scalar_mlp_vs_fp64_oracle(l_max, F, S, layers, avg
     assert _rel(feats, feats_t) <= 1e-5
 
 
+def test_channel_scale_first_and_second_order_vs_fp64():
+    """molix::channel_scale (Allegro's output env scaling) against float64 torch: forward, both
+    gradients, and the second-order terms of the gradient (force-matching training)."""
+    import molnex_amd.kernels as K
+
+    g = torch.Generator().manual_seed(4)
+    E, D, F = 1037, 9, 16
+    t64, s64, w64 = (torch.randn(*sh, generator=g, dtype=torch.float64) for sh in ((E, D * F), (E, F), (E, D * F)))
+    r1, r2 = torch.randn(E, D * F, generator=g, dtype=torch.float64), torch.randn(E, F, generator=g,
+                                                                                   dtype=torch.float64)
+
+    def run(fn, t, s, w):
+        t, s, w = (a.clone().requires_grad_(True) for a in (t, s, w))
+        out = fn(t, s)
+        gt, gs = torch.autograd.grad((out * w).sum(), (t, s), create_graph=True)
+        tot = (gt * r1.to(gt)).sum() + (gs * r2.to(gs)).sum()
+        return (out,) + (gt, gs) + torch.autograd.grad(tot, (t, s, w))
+
+    ref = run(lambda t, s: (t.view(E, D, F) * s.unsqueeze(1)).reshape(E, -1), t64, s64, w64)
+    got = run(lambda t, s: K.channel_scale(t, s, D), *(a.float().to(DEV) for a in (t64, s64, w64)))
+    for name, a, b in zip(("out", "grad_t", "grad_s", "d2/dt", "d2/ds", "d2/dw"), got, ref):
+        assert _rel(a, b) <= 1e-6, (name, _rel(a, b))
+
+
+def test_channel_outer_first_and_second_order_vs_fp64():
+    """molix::channel_outer (the pair embedding's env-weighted harmonics) against float64 torch:
+    forward, both gradients and the second-order terms, D = 1, 4, 9, 16 and F = 4 .. 64."""
+    import molnex_amd.kernels as K
+
+    g = torch.Generator().manual_seed(5)
+    for E, D, F in ((517, 9, 16), (301, 16, 8), (64, 4, 64), (33, 1, 4)):
+        y64, s64, w64 = (torch.randn(*sh, generator=g, dtype=torch.float64) for sh in ((E, D), (E, F), (E, D * F)))
+        r1, r2 = torch.randn(E, D, generator=g, dtype=torch.float64), torch.randn(E, F, generator=g,
+                                                                                dtype=torch.float64)
+
+        def run(fn, y, s, w):
+            y, s, w = (a.clone().requires_grad_(True) for a in (y, s, w))
+            out = fn(y, s)
+            gy, gs = torch.autograd.grad((out * w).sum(), (y, s), create_graph=True)
+            tot = (gy * r1.to(gy)).sum() + (gs * r2.to(gs)).sum()
+            return (out, gy, gs) + torch.autograd.grad(tot, (y, s, w))
+
+        ref = run(lambda y, s: (y.unsqueeze(-1) * s.unsqueeze(-2)).reshape(E, -1), y64, s64, w64)
+        got = run(K.channel_outer, *(a.float().to(DEV) for a in (y64, s64, w64)))
+        for name, a, b in zip(("out", "grad_y", "grad_s", "d2/dy", "d2/ds", "d2/dw"), got, ref):
+            assert _rel(a, b) <= 1e-6, (E, D, F, name, _rel(a, b))
+
+
 def test_allegro_rotation_invariant_and_contract():
     """Scalar edge features are invariant under a rotation of the positions (the reference checks
     rtol = atol = 1e-4; fp32 here stays far inside), and the GraphBatch contract writes
