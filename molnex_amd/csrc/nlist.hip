@@ -39,6 +39,7 @@ constexpr int64_t kNlBlocks = 16384;  // grid-stride launches of the count / emi
 constexpr int kCellParts = 4;          // wavefronts per cell (each takes every 4th atom of it)
 constexpr int kMaskChunks = 16;        // acceptance masks kept per centre: 16 x 64 candidates; cells
                                        // with more candidates are tested again by the emit
+constexpr int kPreChunks = 8;          // candidate chunks a cell unit loads into registers at once
 constexpr float kCellMargin = 1.0001f;
 
 struct NlGrid {
@@ -53,6 +54,12 @@ struct NlGrid {
     double rinv[6];  // inverse of the lower-triangular cell: f_c = z*r5, ...
 };
 
+// Position moved into the primary cell, in cell order (screening test of the count pass).
+template <typename T>
+struct alignas(4 * sizeof(T)) PosW {
+    T x, y, z, w;
+};
+
 struct NlWs {
     NlGrid* grid;
     int32_t* cell_of;
@@ -63,6 +70,7 @@ struct NlWs {
     int32_t* counts;
     int32_t* big;
     uint64_t* masks;  // per centre: the count pass's accept ballot of each 64-candidate chunk
+    void* posw;       // PosW<T> per cell-ordered slot
     int64_t* offsets;
     int64_t* total;
     int64_t* tiles64;
@@ -85,6 +93,7 @@ NlWs carve(void* base, size_t bytes, int64_t n, size_t* used) {
     w.counts = ws.take<int32_t>(n > 0 ? n : 1);
     w.big = ws.take<int32_t>(n > 0 ? n : 1);
     w.masks = ws.take<uint64_t>(size_t(n > 0 ? n : 1) * kMaskChunks);
+    w.posw = ws.take<PosW<double>>(n > 0 ? n : 1);
     w.offsets = ws.take<int64_t>(n + 1);
     w.total = ws.take<int64_t>(1);
     w.tiles64 = ws.take<int64_t>(scan_workspace_elems(n));
@@ -183,10 +192,29 @@ __device__ __forceinline__ int lane_value(int v, int q) { return __builtin_amdgc
 __device__ __forceinline__ float lane_value(float v, int q) {
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), q));
 }
+__device__ __forceinline__ uint64_t lane_value(uint64_t v, int q) {
+    const uint32_t lo = __builtin_amdgcn_readlane(int(v & 0xffffffffu), q),
+                   hi = __builtin_amdgcn_readlane(int(v >> 32), q);
+    return (uint64_t(hi) << 32) | lo;
+}
 __device__ __forceinline__ double lane_value(double v, int q) {
     const long long b = __double_as_longlong(v);
     const int lo = __builtin_amdgcn_readlane(int(b & 0xffffffff), q), hi = __builtin_amdgcn_readlane(int(b >> 32), q);
     return __longlong_as_double((static_cast<long long>(hi) << 32) | static_cast<unsigned int>(lo));
+}
+
+// Value of lane (lane ^ s) for a power of two s < 64: DPP for 1, 2 (quad permutes) and 8
+// (rotation by 8 within a row of 16), the LDS crossbar without memory (ds_swizzle, xor
+// within 32 lanes) for 4 and 16, ds_bpermute for 32.
+__device__ __forceinline__ int lane_xor(int v, int s) {
+    switch (s) {
+        case 1: return __builtin_amdgcn_update_dpp(v, v, 0xB1, 0xF, 0xF, false);   // quad_perm [1,0,3,2]
+        case 2: return __builtin_amdgcn_update_dpp(v, v, 0x4E, 0xF, 0xF, false);   // quad_perm [2,3,0,1]
+        case 8: return __builtin_amdgcn_update_dpp(v, v, 0x128, 0xF, 0xF, false);  // row_ror:8
+        case 4: return __builtin_amdgcn_ds_swizzle(v, 0x101F);                     // and 31, xor 4
+        case 16: return __builtin_amdgcn_ds_swizzle(v, 0x401F);                    // and 31, xor 16
+        default: return __shfl_xor(v, s, kWave);
+    }
 }
 
 // Decision for the pair at positions a, b.  It does not depend on the order: a - b is the
@@ -349,9 +377,14 @@ __global__ void k_place(int64_t n, const int32_t* __restrict__ cell_of, const in
 }
 
 // Each cell's atom list in ascending order (deterministic after the atomic placement into
-// `slots`): the atom in slot k moves to its rank within its cell.
-__global__ void k_rank_cells(int64_t n, const int32_t* __restrict__ cell_of, const int32_t* __restrict__ cell_start,
-                             const int32_t* __restrict__ slots, int32_t* __restrict__ atoms_sorted) {
+// `slots`): the atom in slot k moves to its rank within its cell.  The same slot of `posw`
+// receives the atom's position moved into the primary cell (by whole box vectors, from the
+// fractional coordinates that binned it), which the count pass's screening test reads.
+template <typename T>
+__global__ void k_rank_cells(int64_t n, const T* __restrict__ pos, const T* __restrict__ box,
+                             const NlGrid* __restrict__ gp, const int32_t* __restrict__ cell_of,
+                             const int32_t* __restrict__ cell_start, const int32_t* __restrict__ slots,
+                             int32_t* __restrict__ atoms_sorted, PosW<T>* __restrict__ posw) {
     const int64_t k = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
     if (k >= n) return;
     const int a = slots[k];
@@ -360,6 +393,25 @@ __global__ void k_rank_cells(int64_t n, const int32_t* __restrict__ cell_of, con
     int r = 0;
     for (int t = b; t < e; ++t) r += slots[t] < a;
     atoms_sorted[b + r] = a;
+    const double x = pos[3 * a], y = pos[3 * a + 1], z = pos[3 * a + 2];
+    PosW<T> p;
+    if (gp->periodic) {
+        // the fractional coordinates of cell_coords; box rows (ax,0,0), (bx,by,0), (cx,cy,cz)
+        const NlGrid& g = *gp;
+        const double f2 = z * g.rinv[5];
+        const double f1 = (y - f2 * g.rinv[4]) * g.rinv[2];
+        const double f0 = (x - f1 * g.rinv[1] - f2 * g.rinv[3]) * g.rinv[0];
+        const double n0 = floor(f0), n1 = floor(f1), n2 = floor(f2);
+        p.x = T(x - n0 * double(box[0]) - n1 * double(box[3]) - n2 * double(box[6]));
+        p.y = T(y - n1 * double(box[4]) - n2 * double(box[7]));
+        p.z = T(z - n2 * double(box[8]));
+    } else {
+        p.x = T(x);
+        p.y = T(y);
+        p.z = T(z);
+    }
+    p.w = T(0);
+    posw[b + r] = p;
 }
 
 // ---------------------------------------------------------------------------
@@ -570,18 +622,43 @@ __device__ __forceinline__ int64_t cell_of_block(int64_t c, const NlGrid& g, int
     return c;
 }
 
-template <typename T>
+// Slot (index into the cell-ordered arrays) of candidate number k of the flattened ranges,
+// -1 past the end, and in *cell the neighbour-cell lane (0..26) it comes from; every lane must
+// call it.
+__device__ __forceinline__ int cell_candidate_slot(const CellRanges& cr, int k, int* cell) {
+    int r = 0;
+#pragma unroll
+    for (int step = 16; step > 0; step >>= 1) {
+        const int probe = __shfl(cr.incl, r + step - 1, kWave);
+        if (r + step <= 26 && probe <= k) r += step;
+    }
+    const int start = __shfl(cr.rb, r, kWave);
+    const int first = __shfl(cr.incl - cr.rlen, r, kWave);
+    *cell = r;
+    return k < cr.total ? start + (k - first) : -1;
+}
+
+// The count pass screens each (centre, candidate) pair by the squared distance between the
+// centre's position in the primary cell and the candidate's, moved by the box vectors that
+// wrap its neighbour cell next to the centre's cell.  With >= 3 cells of width >= the cutoff
+// along every periodic axis this is the minimum image for every pair within the cutoff (any
+// other image is more than twice the cutoff away).  Pairs clear of cutoff^2 by a relative
+// 1e-3 are settled by it -- the rounding of the wrapped positions is orders of magnitude
+// smaller -- and the reference arithmetic on the original positions decides the band and
+// zero distances, so the accepted set is the reference's.
+template <typename T, bool HALF>
 __global__ void __launch_bounds__(kWave) k_count_cells(const T* __restrict__ pos, const T* __restrict__ box, T cutoff,
-                                                       int mode, NlGrid* __restrict__ gp,
-                                                       const int32_t* __restrict__ cell_start,
+                                                       NlGrid* __restrict__ gp, const int32_t* __restrict__ cell_start,
                                                        const int32_t* __restrict__ atoms_sorted,
+                                                       const PosW<T>* __restrict__ posw,
                                                        int32_t* __restrict__ counts, int32_t* __restrict__ big,
                                                        uint64_t* __restrict__ masks) {
     const NlGrid g = *gp;
     if (g.brute) return;
     const int lane = threadIdx.x;
     const bool periodic = g.periodic;
-    const AcceptTest<T> at = accept_test<T>(box, periodic, false, cutoff);
+    const T c2 = cutoff * cutoff;
+    const T c2lo = c2 * T(0.999), c2hi = c2 * T(1.001), c2tiny = c2 * T(1e-20);
     for (int64_t v = blockIdx.x; v < g.ncells * kCellParts; v += gridDim.x) {
         const int64_t c = v / kCellParts;
         const int part = int(v - c * kCellParts);
@@ -591,22 +668,44 @@ __global__ void __launch_bounds__(kWave) k_count_cells(const T* __restrict__ pos
         int cx, cy, cz;
         cell_of_block(c, g, &cx, &cy, &cz);
         const CellRanges cr = cell_ranges(g, cx, cy, cz, cell_start, lane);
+        // lanes 0..26: the box vectors that bring neighbour cell `lane` next to this cell
+        T shx = T(0), shy = T(0), shz = T(0);
+        if (periodic && lane < 27) {
+            const int z = cz + lane / 9 - 1, y = cy + (lane / 3) % 3 - 1, x = cx + lane % 3 - 1;
+            const int wz = z < 0 ? -1 : (z >= g.n[2] ? 1 : 0), wy = y < 0 ? -1 : (y >= g.n[1] ? 1 : 0),
+                      wx = x < 0 ? -1 : (x >= g.n[0] ? 1 : 0);
+            shx = T(wx) * box[0] + T(wy) * box[3] + T(wz) * box[6];
+            shy = T(wy) * box[4] + T(wz) * box[7];
+            shz = T(wz) * box[8];
+        }
         for (int q0 = 0; q0 < ncent; q0 += kWave) {
             const int nq = ncent - q0 < kWave ? ncent - q0 : kWave;
-            const int my_i = lane < nq ? atoms_sorted[cb + part + (q0 + lane) * kCellParts] : -1;
-            const T mx = my_i >= 0 ? pos[3 * my_i] : T(0), my = my_i >= 0 ? pos[3 * my_i + 1] : T(0),
-                    mz = my_i >= 0 ? pos[3 * my_i + 2] : T(0);
+            const int my_slot = lane < nq ? cb + part + (q0 + lane) * kCellParts : -1;
+            const int my_i = my_slot >= 0 ? atoms_sorted[my_slot] : -1;
+            PosW<T> mp{T(0), T(0), T(0), T(0)};
+            if (my_slot >= 0) mp = posw[my_slot];
             int my_count = 0;
             const bool keep_masks = cr.total <= kWave * kMaskChunks;  // wave-uniform
             for (int base = 0; base < cr.total; base += kWave) {
-                const int j = cell_candidate(cr, base + lane, atoms_sorted);
-                const T jx = j >= 0 ? pos[3 * j] : T(0), jy = j >= 0 ? pos[3 * j + 1] : T(0),
-                        jz = j >= 0 ? pos[3 * j + 2] : T(0);
+                int r;
+                const int slot = cell_candidate_slot(cr, base + lane, &r);
+                const T sx = __shfl(shx, r, kWave), sy = __shfl(shy, r, kWave), sz = __shfl(shz, r, kWave);
+                const int j = slot >= 0 ? atoms_sorted[slot] : -1;
+                PosW<T> jp{T(0), T(0), T(0), T(0)};
+                if (slot >= 0) jp = posw[slot];
+                const T jx = jp.x + sx, jy = jp.y + sy, jz = jp.z + sz;
                 for (int q = 0; q < nq; ++q) {
                     const int i = lane_value(my_i, q);
-                    const bool keep = j >= 0 && (mode == MNX_NLIST_HALF ? j < i : j != i);
-                    const bool ok = keep && accept_xyz<T>(box, lane_value(mx, q), lane_value(my, q), lane_value(mz, q),
-                                                          jx, jy, jz, periodic, cutoff, at);
+                    const T dx = lane_value(mp.x, q) - jx, dy = lane_value(mp.y, q) - jy,
+                            dz = lane_value(mp.z, q) - jz;
+                    const T r2 = dx * dx + dy * dy + dz * dz;
+                    bool ok = j >= 0 && (HALF ? j < i : j != i) && !(r2 > c2hi);
+                    if (ok && !(r2 < c2lo && r2 > c2tiny)) {
+                        // the band around the cutoff and (near-)zero distances: reference arithmetic
+                        Geo<T> gg;
+                        pair_geo<T>(pos, box, i, j, periodic, false, gg);
+                        ok = gg.dist <= cutoff && gg.dist > T(0);
+                    }
                     const uint64_t m = __ballot(ok);
                     if (lane == q) {
                         my_count += __popcll(m);
@@ -649,6 +748,14 @@ __global__ void __launch_bounds__(kWave) k_emit_cells(const T* __restrict__ pos,
         int cx, cy, cz;
         cell_of_block(c, g, &cx, &cy, &cz);
         const CellRanges cr = cell_ranges(g, cx, cy, cz, cell_start, lane);
+        // as in the count pass: the candidate ids of up to kPreChunks chunks loaded at once
+        const int nchunks = (cr.total + kWave - 1) / kWave;  // wave-uniform
+        const bool pre = nchunks <= kPreChunks;               // implies the count pass kept the masks
+        int jr[kPreChunks];
+        if (pre) {
+#pragma unroll
+            for (int b = 0; b < kPreChunks; ++b) jr[b] = b < nchunks ? cell_candidate(cr, b * kWave + lane, atoms_sorted) : -1;
+        }
         for (int q0 = 0; q0 < ncent;) {
             // a batch of centres whose segments fit the buffer (kEmitBuf entries)
             const int avail = ncent - q0 < kWave ? ncent - q0 : kWave;
@@ -672,32 +779,62 @@ __global__ void __launch_bounds__(kWave) k_emit_cells(const T* __restrict__ pos,
             // the count pass left each centre's accept ballots (the same candidates in the same
             // order): reuse them instead of testing again, unless the cell had too many candidates
             const bool use_masks = cr.total <= kWave * kMaskChunks;  // wave-uniform
-            for (int base = 0; base < cr.total; base += kWave) {
-                const int j = cell_candidate(cr, base + lane, atoms_sorted);
-                T jx = T(0), jy = T(0), jz = T(0);
-                if (!use_masks && j >= 0) {
-                    jx = pos[3 * j];
-                    jy = pos[3 * j + 1];
-                    jz = pos[3 * j + 2];
-                }
+            // appends candidate j (accepted or not by this lane's `ok`) to centre q's segment
+            auto place = [&](int q, int j, bool ok) {
+                const int seg = lane_value(my_off, q);
+                const int cap = lane_value(my_cnt, q);
+                const int fill = lane_value(my_fill, q);
+                const uint64_t m = __ballot(ok);
+                const int before = __popcll(m & ((uint64_t(1) << lane) - 1));
+                if (ok && fill + before < cap) buf[seg + fill + before] = j;
+                if (lane == q) my_fill += __popcll(m);
+            };
+            if (pre) {
+                // each lane holds its own centre's ballots of every chunk; centre q's are read
+                // from lane q, and its segment is filled chunk after chunk with a uniform count
+                uint64_t mk[kPreChunks];
+#pragma unroll
+                for (int b = 0; b < kPreChunks; ++b)
+                    mk[b] = (b < nchunks && my_i >= 0) ? masks[int64_t(my_i) * kMaskChunks + b] : 0;
+                const uint64_t below = (uint64_t(1) << lane) - 1;
                 for (int q = 0; q < nq; ++q) {
-                    const int i = lane_value(my_i, q);
                     const int seg = lane_value(my_off, q);
                     const int cap = lane_value(my_cnt, q);
-                    const int fill = lane_value(my_fill, q);
-                    bool ok;
-                    if (use_masks) {
-                        const uint64_t cm = masks[int64_t(__builtin_amdgcn_readfirstlane(i)) * kMaskChunks + base / kWave];
-                        ok = (cm >> lane) & 1;
-                    } else {
-                        const bool keep = j >= 0 && (mode == MNX_NLIST_HALF ? j < i : j != i);
-                        ok = keep && accept_xyz<T>(box, lane_value(mx, q), lane_value(my, q), lane_value(mz, q), jx,
-                                                   jy, jz, periodic, cutoff, at);
+                    int fill = 0;
+#pragma unroll
+                    for (int b = 0; b < kPreChunks; ++b) {
+                        if (b < nchunks) {
+                            const uint64_t m = lane_value(mk[b], q);
+                            const int at = fill + __popcll(m & below);
+                            if (((m >> lane) & 1) && at < cap) buf[seg + at] = jr[b];
+                            fill += __popcll(m);
+                        }
                     }
-                    const uint64_t m = __ballot(ok);
-                    const int before = __popcll(m & ((uint64_t(1) << lane) - 1));
-                    if (ok && fill + before < cap) buf[seg + fill + before] = j;
-                    if (lane == q) my_fill += __popcll(m);
+                    if (lane == q) my_fill = fill;
+                }
+            } else {
+                for (int base = 0; base < cr.total; base += kWave) {
+                    const int j = cell_candidate(cr, base + lane, atoms_sorted);
+                    T jx = T(0), jy = T(0), jz = T(0);
+                    if (!use_masks && j >= 0) {
+                        jx = pos[3 * j];
+                        jy = pos[3 * j + 1];
+                        jz = pos[3 * j + 2];
+                    }
+                    for (int q = 0; q < nq; ++q) {
+                        const int i = lane_value(my_i, q);
+                        bool ok;
+                        if (use_masks) {
+                            const uint64_t cm =
+                                masks[int64_t(__builtin_amdgcn_readfirstlane(i)) * kMaskChunks + base / kWave];
+                            ok = (cm >> lane) & 1;
+                        } else {
+                            const bool keep = j >= 0 && (mode == MNX_NLIST_HALF ? j < i : j != i);
+                            ok = keep && accept_xyz<T>(box, lane_value(mx, q), lane_value(my, q), lane_value(mz, q),
+                                                       jx, jy, jz, periodic, cutoff, at);
+                        }
+                        place(q, j, ok);
+                    }
                 }
             }
             __syncthreads();
@@ -717,7 +854,7 @@ __global__ void __launch_bounds__(kWave) k_emit_cells(const T* __restrict__ pos,
                     for (int size = 2; size <= kWave; size <<= 1) {
 #pragma unroll
                         for (int stride = size >> 1; stride > 0; stride >>= 1) {
-                            const int other = __shfl_xor(v, stride, kWave);
+                            const int other = lane_xor(v, stride);
                             const bool up = (lane & size) == 0 || size == kWave;
                             const bool low = (lane & stride) == 0;
                             v = (low == up) ? min(v, other) : max(v, other);
@@ -816,12 +953,17 @@ int nlist_count(const T* pos, int64_t n, double cutoff, const T* box, int mode, 
         hipLaunchKernelGGL(k_place, dim3(ceil_div(n, tb)), dim3(tb), 0, stream, n, w.cell_of, w.cell_start,
                            w.cell_fill, w.counts);
         MNX_CHECK_LAUNCH();
-        hipLaunchKernelGGL(k_rank_cells, dim3(ceil_div(n, tb)), dim3(tb), 0, stream, n, w.cell_of, w.cell_start,
-                           w.counts, w.atoms_sorted);
+        PosW<T>* posw = static_cast<PosW<T>*>(w.posw);
+        hipLaunchKernelGGL((k_rank_cells<T>), dim3(ceil_div(n, tb)), dim3(tb), 0, stream, n, pos, box, w.grid,
+                           w.cell_of, w.cell_start, w.counts, w.atoms_sorted, posw);
         MNX_CHECK_LAUNCH();
         const unsigned blocks = unsigned(std::min<int64_t>(std::max<int64_t>(n, w.max_cells * kCellParts), kNlBlocks));
-        hipLaunchKernelGGL((k_count_cells<T>), dim3(blocks), dim3(kWave), 0, stream, pos, box, T(cutoff), mode,
-                           w.grid, w.cell_start, w.atoms_sorted, w.counts, w.big, w.masks);
+        if (mode == MNX_NLIST_HALF)
+            hipLaunchKernelGGL((k_count_cells<T, true>), dim3(blocks), dim3(kWave), 0, stream, pos, box, T(cutoff),
+                               w.grid, w.cell_start, w.atoms_sorted, posw, w.counts, w.big, w.masks);
+        else
+            hipLaunchKernelGGL((k_count_cells<T, false>), dim3(blocks), dim3(kWave), 0, stream, pos, box, T(cutoff),
+                               w.grid, w.cell_start, w.atoms_sorted, posw, w.counts, w.big, w.masks);
         MNX_CHECK_LAUNCH();
         hipLaunchKernelGGL((k_count<T>), dim3(blocks), dim3(kWave), 0, stream, pos, n, box, T(cutoff), mode, w.grid,
                            w.cell_start, w.atoms_sorted, w.counts);
