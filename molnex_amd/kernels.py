@@ -29,6 +29,7 @@ Ops
 from __future__ import annotations
 
 import ctypes as C
+import warnings
 
 C_int32_5 = C.c_int32 * 5
 
@@ -124,6 +125,12 @@ def get_neighbor_pairs(positions, cutoff, max_num_pairs, box_vectors):
     deltas = torch.empty((width, 3), dtype=pos.dtype, device=pos.device)
     distances = torch.empty((width,), dtype=pos.dtype, device=pos.device)
     ws, total = _nlist_run(pos, float(cutoff), box, MNX_NLIST_HALF)
+    if total > width:
+        # the reference's CPU path widens its outputs to every pair here; this op keeps the
+        # schema width as its CUDA path does, so say so once per call site
+        warnings.warn(f"get_neighbor_pairs: {total} pairs within the cutoff, max_num_pairs={width}: "
+                      "the outputs hold the first max_num_pairs pairs in (i, j) order, num_pairs the full "
+                      "count", RuntimeWarning, stacklevel=2)
     _nlist_emit(pos, float(cutoff), box, MNX_NLIST_HALF, layout, ws, width, neighbors[0], neighbors[1], deltas,
                 distances, None)
     num_pairs = torch.full((1,), total, dtype=torch.int32, device=pos.device)

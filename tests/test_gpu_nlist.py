@@ -2,6 +2,7 @@
 
 import math
 import os
+import warnings
 
 import numpy as np
 import pytest
@@ -35,9 +36,14 @@ def test_get_neighbor_pairs_matches_reference_fixtures(ops, gold):
         pos = torch.from_numpy(gold[c + "/positions"]).to(DEV)
         box = torch.from_numpy(gold[c + "/box"]).to(DEV)
         cut, mnp = float(gold[c + "/cutoff"]), int(gold[c + "/max_num_pairs"])
-        nb, d, dist, npairs = ops.get_neighbor_pairs(pos, cut, mnp, box)
+        with warnings.catch_warnings(record=True) as rec:
+            warnings.simplefilter("always")
+            nb, d, dist, npairs = ops.get_neighbor_pairs(pos, cut, mnp, box)
         ref_nb, ref_d, ref_dist = gold[c + "/neighbors"], gold[c + "/deltas"], gold[c + "/distances"]
         assert int(npairs.item()) == int(gold[c + "/num_pairs"][0]), c
+        # more pairs than max_num_pairs: a RuntimeWarning says the outputs are cut to the width
+        over = mnp != -1 and int(gold[c + "/num_pairs"][0]) > mnp
+        assert any(issubclass(r.category, RuntimeWarning) for r in rec) == over, c
         w = nb.shape[1]
         # the reference CPU path widens past max_num_pairs on overflow; this op
         # keeps the schema width (like the CUDA/meta paths) with the first pairs
