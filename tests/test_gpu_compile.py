@@ -303,5 +303,7 @@ def test_compiled_allegro_matches_eager():
     e1, f1 = run(torch.compile(model, backend="eager", fullgraph=False))
     rel_e = float((e0 - e1).abs() / e0.abs())
     rel_f = float((f0 - f1).norm() / f0.norm())
-    # the source-harmonics and force scatters use atomics (summation order differs run to run)
-    assert rel_e <= 1e-6 and rel_f <= 1e-5, (rel_e, rel_f, float((f0 - f1).abs().max()))
+    # the source-harmonics and force scatters use atomics (summation order differs run to run); the
+    # energy is a sum over every edge's features with cancellation, so its relative spread between
+    # runs reaches ~1e-6 of fp32 rounding
+    assert rel_e <= 5e-6 and rel_f <= 1e-5, (rel_e, rel_f, float((f0 - f1).abs().max()))
