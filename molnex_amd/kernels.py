@@ -1540,8 +1540,10 @@ class EdgePairs:
 
 @torch.library.custom_op("molix::gather_rows", mutates_args=(), device_types="cuda")
 def gather_rows(src: Tensor, idx: Tensor) -> Tensor:
-    """``src[idx]`` for a float32 (R, F) ``src`` and distinct int64 indices (the radial features of the
-    lead edge of each undirected pair); its backward scatters the gradient rows back."""
+    """``src[idx]`` for a float32 (R, F) ``src`` and int64 indices (the radial features of the lead
+    edge of each undirected pair; Allegro's type-pair embedding rows).  Its backward scatters the
+    gradient rows back without accumulation, so it needs distinct indices: callers with repeated
+    indices use it where ``src`` takes no gradient."""
     _require_gpu("gather_rows", src, idx)
     if src.dtype != torch.float32 or src.dim() != 2 or idx.dtype != torch.int64 or idx.dim() != 1:
         raise ValueError("gather_rows: src must be float32 (R, F), idx int64 (n,)")

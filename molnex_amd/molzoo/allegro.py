@@ -79,6 +79,30 @@ def _scale_by_channel(tensor, scale, l_max, num_tensor_features):
     return (tensor.reshape(E, -1, F) * scale.unsqueeze(-2)).reshape(E, -1)
 
 
+def _times_envelope(scalars: torch.Tensor, u: torch.Tensor) -> torch.Tensor:
+    """``scalars * u`` for an (E, F) ``scalars`` and the (E, 1) cutoff envelope ``u``: the outer
+    product kernel with one component (``molix::channel_outer``: the envelope's gradient, a sum
+    over the F channels, formed in the same pass as the scalars') for float32 GPU tensors."""
+    F = scalars.shape[-1]
+    if (scalars.is_cuda and scalars.dtype == torch.float32 and u.dtype == torch.float32 and scalars.dim() == 2
+            and u.shape == (scalars.shape[0], 1) and F % 4 == 0 and (F // 4) & (F // 4 - 1) == 0 and F <= 256):
+        return K.channel_outer(u, scalars)
+    return scalars * u
+
+
+def _type_pair_embedding(emb: nn.Embedding, zs: torch.Tensor, zd: torch.Tensor) -> torch.Tensor:
+    """``cat([emb(zs), emb(zd)], -1)``: with the table frozen (no gradient to it), one row gather
+    from the (types^2, 2 dim) table of all ordered type pairs (``molix::gather_rows``) instead of two
+    embedding lookups and a concatenation over the edges."""
+    w = emb.weight
+    if (w.is_cuda and w.dtype == torch.float32 and not (torch.is_grad_enabled() and w.requires_grad)
+            and emb.padding_idx is None and emb.max_norm is None):
+        S = w.shape[0]
+        table = torch.cat([w.repeat_interleave(S, 0), w.repeat(S, 1)], dim=1)
+        return K.gather_rows(table, zs.long() * S + zd.long())
+    return torch.cat([emb(zs), emb(zd)], dim=-1)
+
+
 def _full_paths(in_irreps: Irreps, sh_irreps: Irreps):
     """(l1, l2, l3, parity) of every path of the unfiltered channelwise product, in the weight
     order of cuet.ChannelWiseTensorProduct (input block, harmonics block, l3 ascending)."""
@@ -170,7 +194,7 @@ class PairEmbedding(nn.Module):
         edge_cutoff = self.cutoff_fn(bond_dist)
         edge_radial = self.radial_basis(bond_dist) * edge_cutoff.unsqueeze(-1)
         edge_angular = self.spherical_harmonics(bond_diff / (bond_dist.unsqueeze(-1) + 1e-8))
-        type_embed = torch.cat([self.type_embedding(Z[src]), self.type_embedding(Z[dst])], dim=-1)
+        type_embed = _type_pair_embedding(self.type_embedding, Z[src], Z[dst])
         scalar_features = _silu_stack(self.scalar_mlp, torch.cat([edge_radial, type_embed], dim=-1))
         env_weights = self.tensor_env(scalar_features)
         tensor_features = _env_weight_harmonics(edge_angular, env_weights, self.l_max, self.num_tensor_features,
@@ -228,7 +252,15 @@ class AllegroLayer(nn.Module):
         edge_node_Y = node_Y.index_select(0, src)
         new_tensor = self.tp_linear(self.tp(tensor_features, edge_node_Y, x_scale=self.env_embed(scalar_features)))
         combined = torch.cat([scalar_features, new_tensor[:, :F]], dim=-1)
-        updated = self.residual_a * scalar_features + self.residual_b * self.latent_mlp(combined)
+        # a x + b MLP(c): b folded into the last layer's weights, one add pass
+        mods = list(self.latent_mlp)
+        h = combined
+        for m in mods[:-1]:
+            h = m(h)
+        last = mods[-1]
+        mlp = nn.functional.linear(h, last.weight * self.residual_b,
+                                   last.bias * self.residual_b if last.bias is not None else None)
+        updated = torch.add(mlp, scalar_features, alpha=self.residual_a)
         return updated, _scale_by_channel(new_tensor, self.tensor_env(updated), self.l_max, F)
 
 
@@ -288,7 +320,7 @@ class Allegro(nn.Module):
         per_layer = []
         for layer in self.layers:
             scalars, tensors = layer(scalars, tensors, edge_angular, edge_index, int(Z.shape[0]))
-            per_layer.append(scalars * u)
+            per_layer.append(_times_envelope(scalars, u))
         return torch.stack(per_layer, dim=1)
 
     def forward(self, td=None, *, Z=None, bond_dist=None, bond_diff=None, edge_index=None):
