@@ -16,9 +16,11 @@
 // cutoff (fractional coordinates for periodic cells), each cell's atoms sorted by
 // id.  Four wavefronts share a cell (each takes every fourth atom of it as a
 // centre): they fetch the 27 neighbour cells' ranges in one round trip, load each
-// candidate once, test it against all of their centres, compact the accepted j
-// of each centre with a ballot into LDS, sort them in registers (bitonic, <= 64)
-// or by rank, and write each centre's segment with coalesced stores.  Grids with
+// candidate once and test it against all of their centres (count pass: a screening
+// distance on positions moved into the primary cell, the reference arithmetic near
+// the cutoff; the accept ballots are kept), then the emit pass compacts the accepted
+// j of each centre from the ballots into LDS, sorts them in registers (bitonic,
+// <= 64) or by rank, and writes each centre's segment with coalesced stores.  Grids with
 // fewer than 3 cells along a periodic axis use one wavefront per atom over all
 // atoms (brute mode).  This translation unit is compiled with -ffp-contract=off.
 
