@@ -1152,13 +1152,33 @@ def _radial_setup(ctx, inputs, output):
     ctx.cfg = (kin, hidden, layers)
 
 
+def _radial_torch(feats: Tensor, params: Tensor, kin: int, hidden: int, layers: int) -> Tensor:
+    """The hidden stack in tracked torch ops from the same flat parameters (W_j row-major, b_j)."""
+    z, off, k = feats, 0, kin
+    for _ in range(layers):
+        w = params[off:off + hidden * k].reshape(hidden, k)
+        b = params[off + hidden * k:off + hidden * k + hidden]
+        off += hidden * k + hidden
+        z = torch.nn.functional.silu(torch.nn.functional.linear(z, w, b))
+        k = hidden
+    return z
+
+
 def _radial_bwd(ctx, grad):
     feats, params = ctx.saved_tensors
     if ctx.needs_input_grad[1]:
         raise RuntimeError("molix::radial_hidden computes no parameter gradient; use the Sequential path "
                            "when the radial MLP is trained")
-    gf = radial_hidden_backward(grad, feats, params, *ctx.cfg) if ctx.needs_input_grad[0] else None
-    return gf, None, None, None, None
+    if not ctx.needs_input_grad[0]:
+        return None, None, None, None, None
+    if torch.is_grad_enabled() and feats.requires_grad:
+        # differentiated again (create_graph): the input gradient of the stack recomputed in
+        # tracked ops on the saved input, so that it stays a function of it
+        with torch.enable_grad():
+            (gf,) = torch.autograd.grad(_radial_torch(feats, params.detach(), *ctx.cfg), feats, grad,
+                                        create_graph=True)
+        return gf, None, None, None, None
+    return radial_hidden_backward(grad, feats, params, *ctx.cfg), None, None, None, None
 
 
 radial_hidden.register_autograd(_radial_bwd, setup_context=_radial_setup)

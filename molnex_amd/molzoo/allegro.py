@@ -103,6 +103,118 @@ def _type_pair_embedding(emb: nn.Embedding, zs: torch.Tensor, zd: torch.Tensor) 
     return torch.cat([emb(zs), emb(zd)], dim=-1)
 
 
+def _tail_torch(s, nt, lat, tenv, a, b, F):
+    """The layer tail in autograd-tracked ops: ``updated = a s + b latent([s, nt[:, :F]])`` and
+    the output env scaling of ``nt`` by ``tensor_env(updated)``."""
+    combined = torch.cat([s, nt[:, :F]], dim=-1)
+    mlp = nn.functional.linear(combined, lat.weight * b, lat.bias * b if lat.bias is not None else None)
+    updated = torch.add(mlp, s, alpha=a)
+    return updated, _scale_by_channel(nt, tenv(updated), None, F)
+
+
+class _LayerTail(torch.autograd.Function):
+    """The layer tail with frozen parameters (the energy + forces path) as GEMMs on row blocks:
+    ``updated = a s + s (b W_s)^T + nt[:, :F] (b W_t)^T + b c`` (W = [W_s W_t], c the latent
+    layer's weights and bias) without the concatenation, and a backward that forms ``nt``'s
+    gradient in place: the env scaling's backward (one pass for both gradients), then the latent
+    part added into the scalar columns, with no zero-filled slice gradient and no accumulation
+    pass.  Differentiated again (create_graph), the backward runs the same formulas in tracked
+    ops, with the env scale recomputed from the inputs."""
+
+    @staticmethod
+    def forward(ctx, s, nt, layer):
+        lat, tenv = layer.latent_mlp[0], layer.tensor_env
+        a, b, F = layer.residual_a, layer.residual_b, layer.num_tensor_features
+        ws = lat.weight[:, :s.shape[1]] * b
+        wt = lat.weight[:, s.shape[1]:] * b
+        upd = torch.addmm(lat.bias * b, s, ws.t())
+        upd.addmm_(nt[:, :F], wt.t())
+        upd.add_(s, alpha=a)
+        tv = torch.addmm(tenv.bias, upd, tenv.weight.t())
+        out = K.channel_scale(nt, tv, nt.shape[1] // F)
+        ctx.save_for_backward(s, nt, tv)
+        ctx.layer = layer
+        # an output nothing uses (the last layer's tensor track) arrives as None, not as zeros
+        ctx.set_materialize_grads(False)
+        return upd, out
+
+    @staticmethod
+    def backward(ctx, g_upd, g_out):
+        s, nt, tv = ctx.saved_tensors
+        layer = ctx.layer
+        lat, tenv = layer.latent_mlp[0], layer.tensor_env
+        a, b, F = layer.residual_a, layer.residual_b, layer.num_tensor_features
+        need_s, need_nt = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
+        ws = lat.weight[:, :s.shape[1]] * b
+        wt = lat.weight[:, s.shape[1]:] * b
+        if torch.is_grad_enabled():
+            # differentiated again (create_graph): the same gradient formulas in tracked ops, with
+            # the env scale recomputed from s and nt so that second derivatives reach them (not
+            # autograd.grad on a recomputed tail: nt itself depends on s through the layer's product)
+            with torch.enable_grad():
+                upd = torch.add(torch.addmm(lat.bias * b, torch.cat([s, nt[:, :F]], dim=1), lat.weight.t() * b), s,
+                                alpha=a)
+                tv_t = torch.addmm(tenv.bias, upd, tenv.weight.t())
+                if g_out is not None:
+                    g_nt, g_tv = K.channel_scale_backward(g_out.contiguous(), nt, tv_t, nt.shape[1] // F, True, True)
+                    g_lat = g_tv @ tenv.weight if g_upd is None else g_upd + g_tv @ tenv.weight
+                else:
+                    g_nt, g_lat = torch.zeros_like(nt), g_upd
+                if g_lat is None:
+                    return None, (g_nt if need_nt else None), None
+                g_s = a * g_lat + g_lat @ ws if need_s else None
+                if need_nt:
+                    g_nt = torch.cat([g_nt[:, :F] + g_lat @ wt, g_nt[:, F:]], dim=1)
+            return g_s, (g_nt if need_nt else None), None
+        if g_out is not None:
+            g_nt, g_tv = K.channel_scale_backward(g_out.contiguous(), nt, tv, nt.shape[1] // F, need_nt, True)
+            g_lat = torch.addmm(g_upd, g_tv, tenv.weight) if g_upd is not None else g_tv @ tenv.weight
+        else:
+            g_nt = torch.zeros_like(nt) if need_nt else None
+            g_lat = g_upd
+        if g_lat is None:
+            return None, g_nt if need_nt else None, None
+        g_s = torch.addmm(g_lat, g_lat, ws, beta=a) if need_s else None
+        if need_nt:
+            # the product into a contiguous block, then one strided add (an in-place product on
+            # the column slice would copy the slice out and back)
+            g_nt[:, :F] += g_lat @ wt
+        return g_s, (g_nt if need_nt else None), None
+
+
+def _layer_tail(layer, s, nt):
+    """``(updated, env-scaled nt)`` of an Allegro layer: ``_LayerTail`` when its parameters are
+    frozen and the shapes fit the kernels (float32 on the GPU, one latent layer), else the tracked
+    module form."""
+    mods = list(layer.latent_mlp)
+    F = layer.num_tensor_features
+    params = [p for m in (layer.latent_mlp, layer.tensor_env) for p in m.parameters()]
+    ok = (len(mods) == 1 and isinstance(mods[0], nn.Linear) and mods[0].bias is not None
+          and layer.tensor_env.bias is not None and s.is_cuda and s.dtype == torch.float32
+          and nt.dtype == torch.float32 and s.dim() == 2 and nt.dim() == 2 and F % 4 == 0
+          and nt.shape[1] % F == 0 and nt.shape[1] // F in K.CHANNEL_PRODUCT_COMPONENTS
+          and all(p.dtype == torch.float32 for p in params)
+          and not (torch.is_grad_enabled() and any(p.requires_grad for p in params)))
+    if ok:
+        return _LayerTail.apply(s.contiguous(), nt.contiguous(), layer)
+    return _tail_torch(s, nt, mods[0] if len(mods) == 1 else None, layer.tensor_env, layer.residual_a,
+                       layer.residual_b, F) if len(mods) == 1 else _tail_modules(layer, s, nt)
+
+
+def _tail_modules(layer, s, nt):
+    """The tail with a latent MLP of hidden layers: the modules, b folded into the last layer."""
+    F = layer.num_tensor_features
+    mods = list(layer.latent_mlp)
+    h = torch.cat([s, nt[:, :F]], dim=-1)
+    for m in mods[:-1]:
+        h = m(h)
+    last = mods[-1]
+    mlp = nn.functional.linear(h, last.weight * layer.residual_b,
+                               last.bias * layer.residual_b if last.bias is not None else None)
+    updated = torch.add(mlp, s, alpha=layer.residual_a)
+    return updated, _scale_by_channel(nt, layer.tensor_env(updated), None, F)
+
+
 def _full_paths(in_irreps: Irreps, sh_irreps: Irreps):
     """(l1, l2, l3, parity) of every path of the unfiltered channelwise product, in the weight
     order of cuet.ChannelWiseTensorProduct (input block, harmonics block, l3 ascending)."""
@@ -251,17 +363,8 @@ class AllegroLayer(nn.Module):
         # index_select (backward: one index_add) rather than node_Y[src] (sort-based accumulating backward)
         edge_node_Y = node_Y.index_select(0, src)
         new_tensor = self.tp_linear(self.tp(tensor_features, edge_node_Y, x_scale=self.env_embed(scalar_features)))
-        combined = torch.cat([scalar_features, new_tensor[:, :F]], dim=-1)
-        # a x + b MLP(c): b folded into the last layer's weights, one add pass
-        mods = list(self.latent_mlp)
-        h = combined
-        for m in mods[:-1]:
-            h = m(h)
-        last = mods[-1]
-        mlp = nn.functional.linear(h, last.weight * self.residual_b,
-                                   last.bias * self.residual_b if last.bias is not None else None)
-        updated = torch.add(mlp, scalar_features, alpha=self.residual_a)
-        return updated, _scale_by_channel(new_tensor, self.tensor_env(updated), self.l_max, F)
+        # a x + b MLP([x, scalar part of the new tensor]) and the output env scaling
+        return _layer_tail(self, scalar_features, new_tensor)
 
 
 class AllegroSpec(BaseModel):

@@ -111,6 +111,39 @@ def test_allegro_frozen_fused_scalar_mlp_vs_fp64_oracle(l_max, F, S, layers, avg
     assert _rel(feats, feats_t) <= 1e-5
 
 
+def test_allegro_frozen_tail_second_order_matches_module_form():
+    """Frozen parameters run each layer's tail as one autograd Function with a hand-written
+    backward; differentiating the forces again (create_graph) recomputes it in tracked ops.  The
+    forces and the position gradient of <forces, v> must match the module form (parameters
+    requiring gradients), and the first-order forces the fp64 oracle."""
+    pos, Z, ei, rc = _system(seed=3)
+    m, cfg = _model(2, 16, 64, 2, 12.0)
+    m = m.to(DEV)
+    readout = torch.randn(2, 64, generator=torch.Generator().manual_seed(4)).to(DEV)
+    v = torch.randn(pos.shape[0], 3, generator=torch.Generator().manual_seed(5)).to(DEV)
+
+    def run(frozen):
+        for p in m.parameters():
+            p.requires_grad_(not frozen)
+        pg = pos.float().to(DEV).requires_grad_(True)
+        diff, dist = _geometry(pg, ei.to(DEV))
+        feats = m(Z=Z.to(DEV), bond_dist=dist, bond_diff=diff, edge_index=ei.to(DEV))
+        (f,) = torch.autograd.grad((feats * readout).sum(), pg, create_graph=True)
+        (h,) = torch.autograd.grad((f * v).sum(), pg)
+        return f.detach(), h
+
+    f_fast, h_fast = run(True)
+    f_mod, h_mod = run(False)
+    assert _rel(f_fast, f_mod) <= 1e-5, _rel(f_fast, f_mod)
+    assert _rel(h_fast, h_mod) <= 1e-5, _rel(h_fast, h_mod)
+    p64 = pos.clone().requires_grad_(True)
+    diff64, dist64 = _geometry(p64, ei)
+    sd = {k: t.detach().cpu() for k, t in m.state_dict().items()}
+    ref = AR.allegro_features(sd, cfg, Z, dist64, diff64, ei)
+    (f64,) = torch.autograd.grad((ref * readout.double().cpu()).sum(), p64)
+    assert _rel(f_fast, f64) <= 1e-5, _rel(f_fast, f64)
+
+
 def test_channel_scale_first_and_second_order_vs_fp64():
     """molix::channel_scale (Allegro's output env scaling) against float64 torch: forward, both
     gradients, and the second-order terms of the gradient (force-matching training)."""
