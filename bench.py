@@ -689,8 +689,10 @@ def allegro_bench(args, dev, steps=5, warmup=2, reps=5):
     """Allegro encoder (src/molzoo/allegro.py, reference defaults: 64 scalar / 16 tensor channels,
     l_max 2, 2 layers) on the config-3/5 graph (50k atoms, periodic, rc 5 A): edge features, a
     fixed linear readout summed to an energy, forces by one backward to the positions.  Also the
-    molix::edge_tp kernels at the layer's shape, HIP events on the current stream; algorithmic bytes
-    per edge forward 4 (NX + NO) C + 4 NY, backward 4 (2 NX + NO) C + 8 NY (x, Y, out / grad once)."""
+    molix::edge_tp_proj kernels (the layer's product fused with its projection, which the frozen
+    encoder runs) at the layer's shape, HIP events on the current stream; algorithmic bytes per
+    edge forward 4 (NX + NI) C + 4 NY, backward 4 (2 NX + NI) C + 8 NY (x, Y, projected out / grad
+    once; NI = 9 projected components at l_max 2)."""
     import molnex_amd.kernels as K
     from molnex_amd.molzoo.allegro import Allegro
 
@@ -728,21 +730,25 @@ def allegro_bench(args, dev, steps=5, warmup=2, reps=5):
     torch.cuda.synchronize()
     dt = (time.perf_counter() - t0) / steps
     finite = bool(torch.isfinite(f).all())
-    tp = enc.layers[0].tp
+    layer = enc.layers[0]
+    tp = layer.tp
     P, NX, NY, NO = K.tp_config_info(tp.config_id)
     C = tp.channels
+    blocks = K.edge_tp_proj_blocks(tp.config_id)
+    NI = sum(2 * l + 1 for l, _, _, _ in blocks)
     x = torch.randn(E, NX * C, device=dev)
     Y = torch.randn(E, NY, device=dev)
     w = torch.randn(P, C, device=dev)
-    gout = torch.randn(E, NO * C, device=dev)
+    proj = layer.tp_linear.weight.reshape(-1, C) * layer._proj_scale
+    gout = torch.randn(E, NI * C, device=dev)
     fwd, bwd = [], []
     for r in range(reps + 1):
         ev = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
         ev[0].record()
-        K.edge_tp(x, Y, w, tp.config_id, C)
+        K.edge_tp_proj(x, Y, w, tp.config_id, proj)
         ev[1].record()
         ev[2].record()
-        K.edge_tp_backward(gout, x, Y, w, tp.config_id, C, True, True, True)
+        K.edge_tp_proj_backward(gout, x, Y, w, tp.config_id, proj, True, True, True)
         ev[3].record()
         if r:
             fwd.append(ev[:2])
@@ -750,14 +756,14 @@ def allegro_bench(args, dev, steps=5, warmup=2, reps=5):
     torch.cuda.synchronize()
     tf = sum(a.elapsed_time(b) for a, b in fwd) / reps
     tb = sum(a.elapsed_time(b) for a, b in bwd) / reps
-    bf = E * (4 * (NX + NO) * C + 4 * NY)
-    bb = E * (4 * (2 * NX + NO) * C + 8 * NY)
+    bf = E * (4 * (NX + NI) * C + 4 * NY)
+    bb = E * (4 * (2 * NX + NI) * C + 8 * NY)
     return {"workload": "Allegro (64 scalar / 16 tensor ch, l_max 2, 2 layers) on 50k atoms, rc 5 A, energy + forces",
             "edges": E, "ms_per_step": round(dt * 1e3, 3), "M_edges_per_s": round(E / dt / 1e6, 2),
-            "forces_finite": finite, "edge_tp_fwd_ms": round(tf, 3), "edge_tp_bwd_ms": round(tb, 3),
-            "edge_tp_fwd_GBs": round(bf / tf / 1e6, 1), "edge_tp_bwd_GBs": round(bb / tb / 1e6, 1),
-            "edge_tp_fwd_hbm_frac": round(bf / tf / 1e6 / HBM_PEAK_GBS, 4),
-            "edge_tp_bwd_hbm_frac": round(bb / tb / 1e6 / HBM_PEAK_GBS, 4)}
+            "forces_finite": finite, "edge_tp_proj_fwd_ms": round(tf, 3), "edge_tp_proj_bwd_ms": round(tb, 3),
+            "edge_tp_proj_fwd_GBs": round(bf / tf / 1e6, 1), "edge_tp_proj_bwd_GBs": round(bb / tb / 1e6, 1),
+            "edge_tp_proj_fwd_hbm_frac": round(bf / tf / 1e6 / HBM_PEAK_GBS, 4),
+            "edge_tp_proj_bwd_hbm_frac": round(bb / tb / 1e6 / HBM_PEAK_GBS, 4)}
 
 
 def unsorted_bench(args, dev, steps=3, warmup=2):

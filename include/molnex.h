@@ -697,6 +697,33 @@ int mnx_edge_tp_bwd_f32(int32_t config, int32_t channels, const float* x, const 
                         mnx_stream_t stream);
 
 /* ------------------------------------------------------------------------ */
+/* The same product fused with the projection after it (allegro.py:363-367,  */
+/* cuet.Linear(tp.irreps_out, irreps_in), applied at :465-466), 16 channels: */
+/*   out[e][I_l + m][c'] = sum_{b, c} proj[(J_l + b) * 16 + c][c']           */
+/*                          * TP_b(x_scale x, Y; w)[e][m][c]                 */
+/* for every projected irrep l = 0..l_max (I_l its first component, ir_mul), */
+/* b over the paths with output irrep l (J_l the first of them in the        */
+/* projection's row blocks).  mnx_edge_tp_proj_info writes, per projected    */
+/* irrep in row order, (l, paths, J_l, I_l) into blocks (4 ints each, at     */
+/* most 4 irreps) and returns their count (0: no fused kernel for config,   */
+/* -1: config out of range); out is [E][NI * 16] with NI =                   */
+/* sum (2l + 1).  proj is [num_paths * 16][16] (row J*16 + c: input channel  */
+/* c of path block J; the reference's weights of that irrep times its        */
+/* 1/sqrt(fan_in)).  No projection gradient; the backward's other outputs,   */
+/* workspace and order of summation are those of mnx_edge_tp_bwd_f32 with    */
+/* channels = 16 (mnx_edge_tp_bwd_workspace_bytes(config, 16, E) bytes).     */
+/* ------------------------------------------------------------------------ */
+int32_t mnx_edge_tp_proj_info(int32_t config, int32_t* blocks);
+int mnx_edge_tp_proj_fwd_f32(int32_t config, const float* x, const float* Y, const float* w,
+                             const float* x_scale, const float* proj, int64_t num_edges,
+                             float* out, mnx_stream_t stream);
+int mnx_edge_tp_proj_bwd_f32(int32_t config, const float* x, const float* Y, const float* w,
+                             const float* x_scale, const float* proj, const float* grad_out,
+                             int64_t num_edges, float* grad_x, float* grad_Y, float* grad_w,
+                             float* grad_x_scale, void* workspace, size_t workspace_bytes,
+                             mnx_stream_t stream);
+
+/* ------------------------------------------------------------------------ */
 /* Per-channel scaling of an ir_mul edge tensor (Allegro's output env        */
 /* scaling, src/molzoo/allegro.py:95-128 _scale_by_channel):                 */
 /*   out[e][d][c] = t[e][d][c] * s[e][c]  (t, out [E][D][F], s [E][F]),       */

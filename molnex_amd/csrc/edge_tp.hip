@@ -8,6 +8,14 @@
 // HBM traffic per edge: forward 4 (NX + NO) C + 4 NY bytes; backward
 // 4 (2 NX + NO) C + 8 NY bytes (plus one weight-gradient partial per
 // wavefront).
+//
+// mnx_edge_tp_proj_*: the product fused with the projection that follows it in each Allegro layer
+// (allegro.py:363-367, cuet.Linear(tp.irreps_out, irreps_in)) for 16 channels.  The product's NO
+// rows never reach HBM: each path's components are projected in registers (the 16 channels of
+// an edge rotated through its 16-lane row by DPP, weights staged in LDS) and only the
+// projected irreps (l = 0..l_max, 16 channels each) are written; the backward projects the
+// incoming gradient back the same way before the product's backward.  Per edge: forward
+// 4 (NX + NI) 16 + 4 NY bytes, backward 4 (2 NX + NI) 16 + 8 NY (NI = projected components).
 
 #include "common.h"
 
@@ -22,6 +30,22 @@ struct ETPInfo {
 typedef void (*ETPFwdFn)(const float*, const float*, const float*, const float*, int64_t, int, float*);
 typedef void (*ETPBwdFn)(const float*, const float*, const float*, const float*, const float*, int64_t, int, float*,
                          float*, float*, float*);
+// fused product + projection, 16 channels: (x, Y, w, xs, wp, E, out) and
+// (grad_proj, x, Y, w, xs, wp, E, gx, gY, gw_part, gxs)
+typedef void (*ETPFwdPFn)(const float*, const float*, const float*, const float*, const float*, int64_t, float*);
+typedef void (*ETPBwdPFn)(const float*, const float*, const float*, const float*, const float*, const float*, int64_t,
+                          float*, float*, float*, float*);
+
+// Lane i of each 16-lane row receives the value of lane (i - K) mod 16 of the same row
+// (DPP row_ror:K; one edge per row in the fused kernels).
+template <int K>
+__device__ __forceinline__ float ror16(float v) {
+    if constexpr (K == 0) {
+        return v;
+    } else {
+        return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x120 + K, 0xF, 0xF, true));
+    }
+}
 
 #include "edge_tp_gen.inc"
 
@@ -29,6 +53,7 @@ constexpr int kETPThreads = 256;   // four wavefronts
 constexpr int kETPBwdWaves = 2048; // wavefronts of the backward grid (grid-stride over edges)
 
 constexpr int kETPReduceThreads = 256;
+constexpr int kETPProjChannels = 16;  // channel count of the fused product + projection kernels
 
 // Sums the per-wavefront weight-gradient partials in a fixed order: one workgroup per output
 // value, each thread a fixed strided subset of the partials, then a fixed tree in LDS.
@@ -130,6 +155,71 @@ int mnx_edge_tp_bwd_f32(int32_t config, int32_t channels, const float* x, const 
     float* part = static_cast<float*>(workspace);
     hipLaunchKernelGGL(kETPBwd[config][v], dim3(unsigned(waves / 4)), dim3(kETPThreads), 0, s, grad_out, x, Y, w,
                        x_scale, num_edges, channels, grad_x, grad_Y, part, grad_x_scale);
+    MNX_CHECK_LAUNCH();
+    if (grad_w) {
+        hipLaunchKernelGGL(k_etp_reduce, dim3(unsigned(nw)), dim3(kETPReduceThreads), 0, s, part, waves, nw, grad_w);
+        MNX_CHECK_LAUNCH();
+    }
+    return MNX_OK;
+}
+
+int32_t mnx_edge_tp_proj_info(int32_t config, int32_t* blocks) {
+    clear_error();
+    if (config < 0 || config >= kETPNumConfigs) {
+        set_error(MNX_ERR_INVALID, "edge tensor product: config %d out of range", config);
+        return -1;
+    }
+    const int* b = kETPProjBlocks[config];
+    if (!kETPInfo[config].ok || b[0] == 0) {
+        set_error(MNX_ERR_UNSUPPORTED, "edge tensor product: no fused projection for config %d", config);
+        return 0;
+    }
+    if (blocks)
+        for (int i = 0; i < 4 * b[0]; ++i) blocks[i] = b[1 + i];
+    return b[0];
+}
+
+int mnx_edge_tp_proj_fwd_f32(int32_t config, const float* x, const float* Y, const float* w, const float* x_scale,
+                             const float* proj, int64_t num_edges, float* out, mnx_stream_t stream) {
+    clear_error();
+    int v = -1;
+    int rc = etp_check(config, kETPProjChannels, num_edges, &v);
+    if (rc) return rc;
+    if (num_edges == 0) return MNX_OK;
+    MNX_REQUIRE(x && Y && w && proj && out, "null pointer argument");
+    const int64_t blocks = ceil_div(ceil_div(num_edges, int64_t(4) * kETPInfo[config].fwd_groups), kETPThreads / 64);
+    hipLaunchKernelGGL(kETPFwdP[config], dim3(unsigned(blocks)), dim3(kETPThreads), 0, (hipStream_t)stream, x, Y, w,
+                       x_scale, proj, num_edges, out);
+    MNX_CHECK_LAUNCH();
+    return MNX_OK;
+}
+
+int mnx_edge_tp_proj_bwd_f32(int32_t config, const float* x, const float* Y, const float* w, const float* x_scale,
+                             const float* proj, const float* grad_out, int64_t num_edges, float* grad_x,
+                             float* grad_Y, float* grad_w, float* grad_x_scale, void* workspace,
+                             size_t workspace_bytes, mnx_stream_t stream) {
+    clear_error();
+    int v = -1;
+    int rc = etp_check(config, kETPProjChannels, num_edges, &v);
+    if (rc) return rc;
+    hipStream_t s = (hipStream_t)stream;
+    const int64_t nw = int64_t(kETPInfo[config].np) * kETPProjChannels;
+    if (num_edges == 0) {
+        if (grad_w) {
+            hipLaunchKernelGGL(k_etp_reduce, dim3(unsigned(nw)), dim3(kETPReduceThreads), 0, s,
+                               static_cast<const float*>(nullptr), int64_t(0), nw, grad_w);
+            MNX_CHECK_LAUNCH();
+        }
+        return MNX_OK;
+    }
+    MNX_REQUIRE(x && Y && w && proj && grad_out, "null pointer argument");
+    const int64_t waves = etp_bwd_waves(num_edges, kETPProjChannels);
+    const size_t need = size_t(waves) * nw * sizeof(float);
+    MNX_REQUIRE(workspace && workspace_bytes >= need,
+                "edge tensor product + projection backward: workspace of %zu bytes needed", need);
+    float* part = static_cast<float*>(workspace);
+    hipLaunchKernelGGL(kETPBwdP[config], dim3(unsigned(waves / 4)), dim3(kETPThreads), 0, s, grad_out, x, Y, w,
+                       x_scale, proj, num_edges, grad_x, grad_Y, part, grad_x_scale);
     MNX_CHECK_LAUNCH();
     if (grad_w) {
         hipLaunchKernelGGL(k_etp_reduce, dim3(unsigned(nw)), dim3(kETPReduceThreads), 0, s, part, waves, nw, grad_w);

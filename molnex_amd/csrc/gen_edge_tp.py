@@ -162,7 +162,7 @@ def _bwd(cfg: Cfg) -> str:
     a("    const bool valid = e < E;")
     a("    const int64_t es = valid ? e : 0;")
     a(f"    const float* __restrict__ Ye = Y + es * {NY};")
-    a("    " + " ".join(f"const float y{i} = valid ? Ye[{i}] : 0.f;" for i in range(NY)))
+    a("    " + " ".join(f"const float y{i} = Ye[{i}];" for i in range(NY)))
     a(f"    float gYp[{NY}];")
     a(f"#pragma unroll\n    for (int i = 0; i < {NY}; ++i) gYp[i] = 0.f;")
     a("#pragma unroll")
@@ -242,6 +242,292 @@ def _bwd(cfg: Cfg) -> str:
     return "\n".join(L)
 
 
+
+
+def proj_layout(cfg: Cfg):
+    """Blocks of the projection that follows the product (cuet.Linear(tp.irreps_out, irreps_in),
+    src/molzoo/allegro.py:363-367) for the fused kernels: per output irrep in merged-row order
+    (l3, its paths in rank order, first block index J0, the irrep's component offset O in the
+    projected rows, whose irreps are l = 0..l_max in order); and the projected components."""
+    rows = out_row(cfg)
+    groups = {}
+    for p in sorted(cfg.paths, key=lambda p: p["o3"]):
+        groups.setdefault(p["l3"], []).append(p)
+    offs, o = {}, 0
+    for l in sorted(groups):
+        offs[l] = o
+        o += 2 * l + 1
+    blocks, J = [], 0
+    for l3, ps in sorted(groups.items(), key=lambda kv: min(rows[(p["k"], 0)] for p in kv[1])):
+        blocks.append((l3, ps, J, offs[l3]))
+        J += len(ps)
+    return blocks, o
+
+
+def _row_terms(p, m3):
+    """[(m1, expr of Y)] of output component m3 of path p (Y in y[q][...])."""
+    cf = p["c"]
+    row = []
+    for m1 in range(2 * p["l1"] + 1):
+        terms = [(m2, cf[m1, m2, m3]) for m2 in range(2 * p["l2"] + 1) if abs(cf[m1, m2, m3]) > EPS]
+        if not terms:
+            continue
+        expr = f"{f32(terms[0][1])} * y[q][{p['o2'] + terms[0][0]}]"
+        for m2, v in terms[1:]:
+            expr = f"fmaf({f32(v)}, y[q][{p['o2'] + m2}], {expr})"
+        row.append((m1, expr))
+    return row
+
+
+def _stage_proj(a, cfg: Cfg, fwd: bool):
+    """LDS copy of the projection weights wp (rows J*16 + c, 16 columns) as sw[J][c][k] in rows of
+    20 floats (float4 reads of four k at once by the 16 lanes of a row hit distinct banks):
+    forward sw[J][c][k] = wp[J][c][(c + k) mod 16] w[j(J)][c] (the product's path weight of
+    channel c folded in, j(J) the compiled path of block row J), backward wp[J][c][(c - k) mod 16]."""
+    blocks, _ = proj_layout(cfg)
+    jidx = {p["k"]: j for j, p in enumerate(cfg.paths)}
+    a(f"  __shared__ __align__(16) float sw[{cfg.NP * 320}];")
+    a("  {")
+    a("    const int cc = threadIdx.x >> 4, k = threadIdx.x & 15;")
+    a(f"    const int src = cc * 16 + ((cc {'+' if fwd else '-'} k) & 15), dst = cc * 20 + k;")
+    for l3, ps, J0, O in blocks:
+        for b, p in enumerate(ps):
+            J = J0 + b
+            if fwd:
+                a(f"    sw[{J * 320} + dst] = wp[{J * 256} + src] * w[{jidx[p['k']]} * 16 + cc];")
+            else:
+                a(f"    sw[{J * 320} + dst] = wp[{J * 256} + src];")
+    a("  }")
+    a("  __syncthreads();")
+
+
+def _fwdp(cfg: Cfg) -> str:
+    """Product and projection in one pass (16 channels, one edge per 16-lane row).  Lane c holds
+    channel c of every path's output components t_b[m3] of an output irrep; for each offset k it
+    forms p_k = sum_b W[(J0 + b)*16 + c][(c + k) mod 16] t_b[m3] and the row rotation (DPP
+    row_ror:k: lane c' receives lane (c' - k) mod 16) delivers p_k to lane c + k, so that
+    acc[c'] = sum_k p_k[c' - k] = sum_{b, c} W[(J0 + b)*16 + c][c'] t_b[m3][c].  Only the
+    projected rows (irreps l = 0..l_max, 16 channels each) are written."""
+    L = []
+    a = L.append
+    NX, NY, NP = cfg.NX, cfg.NY, cfg.NP
+    EPW = fwd_groups(cfg)
+    blocks, ncomp = proj_layout(cfg)
+    a(f"__global__ void __launch_bounds__(256) etp_fwdp_c{cfg.idx}("
+      "const float* __restrict__ x, const float* __restrict__ Y, const float* __restrict__ w, "
+      "const float* __restrict__ xs, const float* __restrict__ wp, int64_t E, float* __restrict__ out) {")
+    _stage_proj(a, cfg, True)
+    a("  constexpr int G = 4, C = 16;")
+    a("  const int lane = threadIdx.x & 63, c0 = lane & 15;")
+    a(f"  const int64_t e0 = (int64_t(blockIdx.x) * 4 + (threadIdx.x >> 6)) * ({EPW} * G) + lane / 16;")
+    a("  const float4* __restrict__ sw4 = reinterpret_cast<const float4*>(sw) + c0 * 5;")
+    a(f"  float y[{EPW}][{NY}], xv[{EPW}][{NX}];")
+    a("#pragma unroll")
+    a(f"  for (int q = 0; q < {EPW}; ++q) {{")
+    a("    const int64_t e = e0 + q * G;")
+    a("    const int64_t es = e < E ? e : E - 1;  // rows past the end compute edge E - 1, unstored")
+    a(f"    const float* __restrict__ Ye = Y + es * {NY};")
+    a(f"    const float* __restrict__ xe = x + es * ({NX} * int64_t(C));")
+    a("#pragma unroll")
+    a(f"    for (int i = 0; i < {NY}; ++i) y[q][i] = Ye[i];")
+    a("    const float sc = xs ? xs[es * C + c0] : 1.f;")
+    a("#pragma unroll")
+    a(f"    for (int i = 0; i < {NX}; ++i) xv[q][i] = xe[i * C + c0] * sc;")
+    a("  }")
+    for l3, ps, J0, O in blocks:
+        M, nb = 2 * l3 + 1, len(ps)
+        a("  {")
+        a(f"    float t[{EPW}][{nb}][{M}], acc[{EPW}][{M}];")
+        a("#pragma unroll")
+        a(f"    for (int q = 0; q < {EPW}; ++q) {{")
+        for b, p in enumerate(ps):
+            for m3 in range(M):
+                row = _row_terms(p, m3)
+                if not row:
+                    a(f"      t[q][{b}][{m3}] = 0.f;")
+                    continue
+                sx = f"({row[0][1]}) * xv[q][{p['o1'] + row[0][0]}]"
+                for m1, expr in row[1:]:
+                    sx = f"fmaf({expr}, xv[q][{p['o1'] + m1}], {sx})"
+                a(f"      t[q][{b}][{m3}] = {sx};")
+        a("    }")
+        for kq in range(4):
+            # one group of four offsets at a time: the scheduler would otherwise issue every
+            # LDS read of the kernel up front and run out of registers
+            a("    __builtin_amdgcn_sched_barrier(0);")
+            a("    {")
+            for b in range(nb):
+                a(f"      const float4 v{b} = sw4[{(J0 + b) * 80 + kq}];")
+            for kk, comp in enumerate("xyzw"):
+                k = 4 * kq + kk
+                a("#pragma unroll")
+                a(f"      for (int q = 0; q < {EPW}; ++q)")
+                a("#pragma unroll")
+                a(f"        for (int m = 0; m < {M}; ++m) {{")
+                pe = f"v0.{comp} * t[q][0][m]"
+                for b in range(1, nb):
+                    pe = f"fmaf(v{b}.{comp}, t[q][{b}][m], {pe})"
+                if k == 0:
+                    a(f"          acc[q][m] = {pe};")
+                else:
+                    a(f"          acc[q][m] += ror16<{k}>({pe});")
+                a("        }")
+            a("    }")
+        # the sums complete here, before the guarded store (sunk into it, every rotated partial
+        # would stay live up to the store and the rotations could not fold into the adds)
+        a("#pragma unroll")
+        a(f"    for (int q = 0; q < {EPW}; ++q)")
+        a("#pragma unroll")
+        a(f"      for (int m = 0; m < {M}; ++m) asm volatile(\"\" : \"+v\"(acc[q][m]));")
+        a("#pragma unroll")
+        a(f"    for (int q = 0; q < {EPW}; ++q) {{")
+        a("      const int64_t e = e0 + q * G;")
+        a("      if (e < E) {")
+        a(f"        float* __restrict__ oe = out + e * {ncomp * 16} + {O * 16} + c0;")
+        a("#pragma unroll")
+        a(f"        for (int m = 0; m < {M}; ++m) oe[m * 16] = acc[q][m];")
+        a("      }")
+        a("    }")
+        a("  }")
+    a("}")
+    return "\n".join(L)
+
+
+def _bwdp(cfg: Cfg) -> str:
+    """Backward of ``_fwdp``.  Per output irrep, the gradient of each path's components is
+    projected back in registers: lane c accumulates s_b[m3][c] = sum_k W[(J0 + b)*16 + c][(c - k)
+    mod 16] g[m3][(c - k) mod 16] over the 16 rotations of the row (the rotated g shared by the
+    irrep's paths); then each of those paths' product backward as in ``_bwd`` (16 channels, one
+    channel per lane), so at most one irrep's path gradients are live at a time."""
+    L = []
+    a = L.append
+    NX, NY, NP = cfg.NX, cfg.NY, cfg.NP
+    blocks, ncomp = proj_layout(cfg)
+    jidx = {p["k"]: j for j, p in enumerate(cfg.paths)}
+    a(f"__global__ void __launch_bounds__(256) etp_bwdp_c{cfg.idx}("
+      "const float* __restrict__ gproj, const float* __restrict__ x, const float* __restrict__ Y, "
+      "const float* __restrict__ w, const float* __restrict__ xs, const float* __restrict__ wp, int64_t E, "
+      "float* __restrict__ gx, float* __restrict__ gY, float* __restrict__ gw_part, float* __restrict__ gxs) {")
+    _stage_proj(a, cfg, False)
+    a("  constexpr int G = 4, C = 16;")
+    a("  const int lane = threadIdx.x & 63, c = lane & 15;")
+    a("  const int64_t wave = int64_t(blockIdx.x) * 4 + (threadIdx.x >> 6), nwaves = int64_t(gridDim.x) * 4;")
+    a("  const int64_t ngroups = (E + G - 1) / G;")
+    a("  const float4* __restrict__ sw4 = reinterpret_cast<const float4*>(sw) + c * 5;")
+    a(f"  float wv[{NP}], gwa[{NP}];")
+    a("#pragma unroll")
+    a(f"  for (int j = 0; j < {NP}; ++j) {{ wv[j] = w[j * C + c]; gwa[j] = 0.f; }}")
+    a("  for (int64_t grp = wave; grp < ngroups; grp += nwaves) {")
+    a("    // the LDS weights are re-read every iteration (hoisted, they would not fit in registers)")
+    a("    asm volatile(\"\" ::: \"memory\");")
+    a("    const int64_t e = grp * G + lane / 16;")
+    a("    const bool valid = e < E;")
+    a("    const int64_t es = valid ? e : 0;")
+    a(f"    const float* __restrict__ Ye = Y + es * {NY};")
+    a("    " + " ".join(f"const float y{i} = Ye[{i}];" for i in range(NY)))
+    a(f"    float gYp[{NY}];")
+    a("#pragma unroll")
+    a(f"    for (int i = 0; i < {NY}; ++i) gYp[i] = 0.f;")
+    a(f"    const float* __restrict__ xe = x + es * ({NX} * int64_t(C)) + c;")
+    a(f"    const float* __restrict__ ge = gproj + es * {ncomp * 16} + c;")
+    a("    const float sc = xs ? xs[es * C + c] : 1.f;")
+    a(f"    float xr[{NX}], xv[{NX}], gxv[{NX}];  // x as given; xv = sc * xr enters the product")
+    a("#pragma unroll")
+    a(f"    for (int i = 0; i < {NX}; ++i) {{ xr[i] = xe[i * C]; xv[i] = xr[i] * sc; gxv[i] = 0.f; }}")
+    for l3, ps, J0, O in blocks:
+        M, nb = 2 * l3 + 1, len(ps)
+        a("    {")
+        a(f"      float gl[{M}], s[{nb}][{M}];")
+        a("#pragma unroll")
+        a(f"      for (int m = 0; m < {M}; ++m) {{ const float g = ge[({O} + m) * 16]; gl[m] = valid ? g : 0.f; }}")
+        a("#pragma unroll")
+        a(f"      for (int m = 0; m < {M}; ++m)")
+        a("#pragma unroll")
+        a(f"        for (int b = 0; b < {nb}; ++b) s[b][m] = 0.f;")
+        for kq in range(4):
+            a("      __builtin_amdgcn_sched_barrier(0);")
+            a("      {")
+            for b in range(nb):
+                a(f"        const float4 v{b} = sw4[{(J0 + b) * 80 + kq}];")
+            for kk, comp in enumerate("xyzw"):
+                k = 4 * kq + kk
+                a("#pragma unroll")
+                a(f"        for (int m = 0; m < {M}; ++m) {{")
+                a(f"          const float r = ror16<{k}>(gl[m]);")
+                for b in range(nb):
+                    a(f"          s[{b}][m] = fmaf(v{b}.{comp}, r, s[{b}][m]);")
+                a("        }")
+            a("      }")
+        a("      __builtin_amdgcn_sched_barrier(0);")
+        for b, p in enumerate(ps):
+            cf = p["c"]
+            j = jidx[p["k"]]
+            a("      {")
+            a(f"        const float wj = wv[{j}];")
+            for m1 in range(2 * p["l1"] + 1):
+                vs = []
+                for m2 in range(2 * p["l2"] + 1):
+                    terms = [(m3, cf[m1, m2, m3]) for m3 in range(M) if abs(cf[m1, m2, m3]) > EPS]
+                    if not terms:
+                        continue
+                    expr = f"{f32(terms[0][1])} * s[{b}][{terms[0][0]}]"
+                    for m3, v in terms[1:]:
+                        expr = f"fmaf({f32(v)}, s[{b}][{m3}], {expr})"
+                    vs.append((m2, expr))
+                if not vs:
+                    continue
+                xi = p["o1"] + m1
+                a("        {")
+                for m2, expr in vs:
+                    a(f"          const float v{m2} = {expr};")
+                u = f"y{p['o2'] + vs[0][0]} * v{vs[0][0]}"
+                for m2, _ in vs[1:]:
+                    u = f"fmaf(y{p['o2'] + m2}, v{m2}, {u})"
+                a(f"          const float u = {u};")
+                a(f"          gxv[{xi}] = fmaf(wj, u, gxv[{xi}]);")
+                a(f"          gwa[{j}] = fmaf(xv[{xi}], u, gwa[{j}]);")
+                a(f"          const float xw = xv[{xi}] * wj;")
+                for m2, _ in vs:
+                    a(f"          gYp[{p['o2'] + m2}] = fmaf(xw, v{m2}, gYp[{p['o2'] + m2}]);")
+                a("        }")
+            a("      }")
+        a("    }")
+    a(f"    if (gx && valid) {{ float* __restrict__ gxe = gx + es * ({NX} * int64_t(C)) + c;")
+    a("#pragma unroll")
+    a(f"      for (int i = 0; i < {NX}; ++i) gxe[i * C] = gxv[i] * sc; }}")
+    a("    if (gxs && valid) {")
+    a("      float t = 0.f;")
+    a("#pragma unroll")
+    a(f"      for (int i = 0; i < {NX}; ++i) t = fmaf(gxv[i], xr[i], t);")
+    a("      gxs[es * C + c] = t;")
+    a("    }")
+    a("    if (gY) {")
+    a("#pragma unroll")
+    a(f"      for (int i = 0; i < {NY}; ++i) {{")
+    a("        gYp[i] += ror16<8>(gYp[i]);  // every lane of the row ends with the row's sum")
+    a("        gYp[i] += ror16<4>(gYp[i]);")
+    a("        gYp[i] += ror16<2>(gYp[i]);")
+    a("        gYp[i] += ror16<1>(gYp[i]);")
+    a("      }")
+    a(f"      if (valid && c == 0) {{ float* __restrict__ gYe = gY + es * {NY};")
+    a("#pragma unroll")
+    a(f"        for (int i = 0; i < {NY}; ++i) gYe[i] = gYp[i]; }}")
+    a("    }")
+    a("  }")
+    a("  // one partial per wavefront: sum over its edge slots (lanes of equal channel)")
+    a("#pragma unroll")
+    a(f"  for (int j = 0; j < {NP}; ++j)")
+    a("#pragma unroll")
+    a("    for (int s2 = 16; s2 < 64; s2 <<= 1) gwa[j] += __shfl_xor(gwa[j], s2);")
+    a("  if (lane < 16) {")
+    a(f"    float* __restrict__ pw = gw_part + wave * ({NP} * int64_t(C));")
+    a("#pragma unroll")
+    a(f"    for (int j = 0; j < {NP}; ++j) pw[j * C + c] = gwa[j];")
+    a("  }")
+    a("}")
+    return "\n".join(L)
+
+
 def generate() -> str:
     cfgs = [Cfg(i, *c) for i, c in enumerate(config_list())]
     out = ["// Generated by gen_edge_tp.py -- do not edit.", "// clang-format off", ""]
@@ -253,6 +539,10 @@ def generate() -> str:
         out.append("")
         out.append(_bwd(cfg))
         out.append("")
+        out.append(_fwdp(cfg))
+        out.append("")
+        out.append(_bwdp(cfg))
+        out.append("")
     out.append(f"static constexpr int kETPNumConfigs = {len(cfgs)};")
     out.append(f"static constexpr int kETPNumVariants = {len(VARIANTS)};")
     out.append("static const int kETPVariantCW[] = {" + ", ".join(str(v[0]) for v in VARIANTS) + "};")
@@ -260,6 +550,23 @@ def generate() -> str:
     out.append("static const ETPInfo kETPInfo[] = {")
     for cfg in cfgs:
         out.append(f"  {{{int(supported(cfg))}, {cfg.NP}, {cfg.NX}, {cfg.NY}, {cfg.NO}, {fwd_groups(cfg)}}},")
+    out.append("};")
+    # fused product + projection (16 channels): kernels, projected components, projection blocks
+    out.append("static const ETPFwdPFn kETPFwdP[] = {" + ", ".join(
+        f"etp_fwdp_c{c.idx}" if supported(c) else "nullptr" for c in cfgs) + "};")
+    out.append("static const ETPBwdPFn kETPBwdP[] = {" + ", ".join(
+        f"etp_bwdp_c{c.idx}" if supported(c) else "nullptr" for c in cfgs) + "};")
+    out.append("static const int kETPProjComps[] = {" + ", ".join(
+        str(proj_layout(c)[1]) if supported(c) else "0" for c in cfgs) + "};")
+    out.append("static const int kETPProjBlocks[][4 * 4 + 1] = {")
+    for c in cfgs:
+        if supported(c):
+            bl = proj_layout(c)[0]
+            flat = [len(bl)] + [v for l3, ps, J0, O in bl for v in (l3, len(ps), J0, O)]
+        else:
+            flat = [0]
+        flat += [0] * (17 - len(flat))
+        out.append("  {" + ", ".join(str(v) for v in flat) + "},")
     out.append("};")
     for kind in ("fwd", "bwd"):
         typ = "ETPFwdFn" if kind == "fwd" else "ETPBwdFn"

@@ -15,6 +15,7 @@ Ops
 ``molix::tp_scatter``           channelwise TP + scatter-sum (``cuet.ChannelWiseTensorProduct``)
 ``molix::tp_any``               the same for any irreps (l <= 3), driven by a path table
 ``molix::edge_tp``              per-edge channelwise TP with shared weights, no scatter (Allegro's layer product)
+``molix::edge_tp_proj``         ``edge_tp`` (16 channels) and the projection after it in one pass (Allegro)
 ``molix::radial_hidden``        fused hidden stack of the radial weight MLP (gradient w.r.t. its input)
 ``molix::edge_weights``         output layer of the radial weight MLP (per-edge TP weights), near-fp32 split-fp16 MFMA
 ``molix::bond_vectors``         pos[receiver] - pos[sender] - shift per edge, with its position gradient
@@ -663,6 +664,157 @@ def _etp_backward(ctx, grad_out):
 
 
 edge_tp.register_autograd(_etp_backward, setup_context=_etp_setup)
+
+
+# the product fused with the projection after it (16 channels)
+
+def edge_tp_proj_blocks(config: int) -> tuple[tuple[int, int, int, int], ...]:
+    """Projected irreps of ``molix::edge_tp_proj`` for ``config``, in row order: (l, paths of output
+    irrep l, their first row block J in ``proj``, first projected component I); empty when the
+    configuration has no fused kernel."""
+    buf = (C.c_int32 * 16)()
+    n = int(_lib.load().mnx_edge_tp_proj_info(config, buf))
+    return tuple(tuple(int(v) for v in buf[4 * i:4 * i + 4]) for i in range(max(n, 0)))
+
+
+def edge_tp_proj_adjoint(g: Tensor, proj: Tensor, blocks) -> Tensor:
+    """Gradient of the product's rows (``molix::edge_tp``'s layout, 16 channels) from the gradient
+    of the projected rows: per irrep, ``G_l (E*M, 16) @ P_l^T`` with ``P_l`` its ``(paths*16, 16)``
+    rows of ``proj`` (tracked torch ops: the differentiable form of the fused backward)."""
+    E = g.shape[0]
+    parts = []
+    for l, nb, J, I in blocks:
+        M = 2 * l + 1
+        gb = g[:, I * 16:(I + M) * 16].reshape(E * M, 16)
+        parts.append((gb @ proj[J * 16:(J + nb) * 16].t()).reshape(E, M * nb * 16))
+    return torch.cat(parts, dim=1)
+
+
+def edge_tp_project(t: Tensor, proj: Tensor, blocks) -> Tensor:
+    """The projection alone on ``molix::edge_tp``'s output (16 channels): per irrep,
+    ``T_l (E*M, paths*16) @ P_l`` written at its projected rows.  ``edge_tp_proj`` computes
+    ``edge_tp_project(edge_tp(...), proj, blocks)`` in one pass."""
+    E = t.shape[0]
+    parts, row = [], 0
+    for l, nb, J, I in blocks:
+        M = 2 * l + 1
+        tb = t[:, row * 16:(row + M * nb) * 16].reshape(E * M, nb * 16)
+        parts.append((tb @ proj[J * 16:(J + nb) * 16]).reshape(E, M * 16))
+        row += M * nb
+    return torch.cat(parts, dim=1)
+
+
+def _proj_args(x, Y, w, config, proj, x_scale):
+    blocks = edge_tp_proj_blocks(config)
+    if not blocks:
+        raise ValueError(f"edge_tp_proj: no fused kernel for config {config}")
+    num_paths, nx, ny, no = tp_config_info(config)
+    E = Y.shape[0]
+    xs = _f32_rows(x, nx * 16, "x")
+    Ys = _f32_rows(Y, ny, "Y")
+    ws_ = _f32_rows(w, 16, "w")
+    pj = _f32_rows(proj, 16, "proj")
+    sc = None if x_scale is None else _f32_rows(x_scale, 16, "x_scale")
+    if (xs.shape[0] != E or ws_.shape[0] != num_paths or pj.shape[0] != num_paths * 16
+            or (sc is not None and sc.shape[0] != E)):
+        raise ValueError("edge_tp_proj: x must be (E, NX*16), w (num_paths, 16), proj (num_paths*16, 16), "
+                         "x_scale (E, 16)")
+    ni = sum(2 * l + 1 for l, _, _, _ in blocks)
+    return blocks, xs, Ys, ws_, pj, sc, ni
+
+
+@torch.library.custom_op("molix::edge_tp_proj", mutates_args=(), device_types="cuda")
+def edge_tp_proj(x: Tensor, Y: Tensor, w: Tensor, config: int, proj: Tensor,
+                 x_scale: Tensor | None = None) -> Tensor:
+    """``molix::edge_tp`` with 16 channels followed by the projection back to the input irreps
+    (src/molzoo/allegro.py:363-367,465-466: cuet.Linear(tp.irreps_out, irreps_in) on the product),
+    in one pass that never writes the product's rows: ``out`` (E, NI*16), irreps l = 0..l_max in
+    ir_mul.  ``proj`` (num_paths*16, 16) holds the projection's weights by row block
+    (``edge_tp_proj_blocks``: the paths of output irrep l are blocks J_l .. J_l + paths - 1, rows
+    J*16 + c for input channel c), scaled as applied."""
+    _require_gpu("edge_tp_proj", x, Y, w, proj, x_scale)
+    blocks, xs, Ys, ws_, pj, sc, ni = _proj_args(x, Y, w, config, proj, x_scale)
+    E = Ys.shape[0]
+    out = torch.empty((E, ni * 16), dtype=torch.float32, device=xs.device)
+    check(_lib.load().mnx_edge_tp_proj_fwd_f32(config, ptr(xs), ptr(Ys), ptr(ws_), ptr(sc) if sc is not None else None,
+                                               ptr(pj), E, ptr(out), _stream(xs)),
+          "edge_tp_proj")
+    return out
+
+
+@edge_tp_proj.register_fake
+def _(x, Y, w, config, proj, x_scale=None):
+    ni = sum(2 * l + 1 for l, _, _, _ in edge_tp_proj_blocks(config))
+    return x.new_empty((Y.shape[0], ni * 16))
+
+
+@torch.library.custom_op("molix::edge_tp_proj_backward", mutates_args=(), device_types="cuda")
+def edge_tp_proj_backward(grad_out: Tensor, x: Tensor, Y: Tensor, w: Tensor, config: int, proj: Tensor,
+                          need_x: bool, need_Y: bool, need_w: bool, x_scale: Tensor | None = None,
+                          need_scale: bool = False) -> tuple[Tensor, Tensor, Tensor, Tensor]:
+    """Gradients of ``<grad_out, edge_tp_proj(...)>`` w.r.t. x, Y, w and x_scale (empty when not
+    needed) in one pass: the projected gradient is taken back through the projection in registers,
+    then the product's backward; the weight gradient is summed over edges in a fixed order."""
+    lib = _lib.load()
+    blocks, xs, Ys, wss, pj, sc, ni = _proj_args(x, Y, w, config, proj, x_scale)
+    E = Ys.shape[0]
+    go = _f32_rows(grad_out, ni * 16, "grad_out")
+    gx = torch.empty_like(xs) if need_x else xs.new_empty(0)
+    gY = torch.empty_like(Ys) if need_Y else Ys.new_empty(0)
+    gw = torch.empty_like(wss) if need_w else wss.new_empty(0)
+    need_scale = bool(need_scale and sc is not None)
+    gs = torch.empty_like(sc) if need_scale else xs.new_empty(0)
+    ws = _ws(max(int(lib.mnx_edge_tp_bwd_workspace_bytes(config, 16, E)), 1), xs.device)
+    check(lib.mnx_edge_tp_proj_bwd_f32(config, ptr(xs), ptr(Ys), ptr(wss), ptr(sc) if sc is not None else None,
+                                       ptr(pj), ptr(go), E, ptr(gx) if need_x else None,
+                                       ptr(gY) if need_Y else None, ptr(gw) if need_w else None,
+                                       ptr(gs) if need_scale else None, ptr(ws), ws.numel(), _stream(xs)),
+          "edge_tp_proj backward")
+    return gx, gY, gw, gs
+
+
+@edge_tp_proj_backward.register_fake
+def _(grad_out, x, Y, w, config, proj, need_x, need_Y, need_w, x_scale=None, need_scale=False):
+    return (torch.empty_like(x) if need_x else x.new_empty(0), torch.empty_like(Y) if need_Y else Y.new_empty(0),
+            torch.empty_like(w) if need_w else w.new_empty(0),
+            torch.empty_like(x_scale) if (need_scale and x_scale is not None) else x.new_empty(0))
+
+
+def _etpp_setup(ctx, inputs, output):
+    x, Y, w, config, proj, x_scale = inputs
+    ctx.save_for_backward(x, Y, w, proj, x_scale)
+    ctx.config = config
+
+
+def _etpp_backward(ctx, grad_out):
+    x, Y, w, proj, x_scale = ctx.saved_tensors
+    config = ctx.config
+    nx, nY, nw = ctx.needs_input_grad[:3]
+    npj = ctx.needs_input_grad[4]
+    ns = x_scale is not None and ctx.needs_input_grad[5]
+    gp = None
+    if npj or torch.is_grad_enabled():
+        # the projection's weight gradient, or differentiated again (create_graph): the projection's
+        # adjoint in tracked ops, then molix::edge_tp's backward (which has second derivatives)
+        blocks = edge_tp_proj_blocks(config)
+        g_tp = edge_tp_proj_adjoint(grad_out, proj, blocks)
+        gx, gY, gw, gs = edge_tp_backward(g_tp.contiguous(), x, Y, w, config, 16, nx, nY, nw, x_scale, ns)
+        if npj:
+            t = edge_tp(x, Y, w, config, 16, x_scale)
+            E, parts, row = t.shape[0], [], 0
+            for l, nb, J, I in blocks:
+                M = 2 * l + 1
+                tb = t[:, row * 16:(row + M * nb) * 16].reshape(E * M, nb * 16)
+                parts.append(tb.t() @ grad_out[:, I * 16:(I + M) * 16].reshape(E * M, 16))
+                row += M * nb
+            gp = torch.cat(parts, dim=0).reshape(proj.shape)
+    else:
+        gx, gY, gw, gs = edge_tp_proj_backward(grad_out.contiguous(), x, Y, w, config, proj, nx, nY, nw, x_scale, ns)
+    return (gx.reshape(x.shape) if nx else None, gY.reshape(Y.shape) if nY else None,
+            gw.reshape(w.shape) if nw else None, None, gp, gs.reshape(x_scale.shape) if ns else None)
+
+
+edge_tp_proj.register_autograd(_etpp_backward, setup_context=_etpp_setup)
 
 
 # ---------------------------------------------------------------------------

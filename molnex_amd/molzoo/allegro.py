@@ -12,8 +12,10 @@ uses still fill a 64-wide wavefront.  Its projection (allegro.py:363-367,
 ``cuet.Linear(tp.irreps_out, irreps_in)``) connects only output blocks whose irrep is an input
 irrep, so only those paths are computed; the weight keeps one entry per path of the full product,
 in the reference's order, and the unused entries receive zero gradient as they do there.  The
-layer's env scaling of the tensor track before the product is fused into the same kernel.  The
-projection runs in the HIP block-linear kernel over the edges.  Because every irrep block of the
+layer's env scaling of the tensor track before the product is fused into the same kernel.  With
+16 channels and projection weights that take no gradient, the product and the projection run as
+one ``molix::edge_tp_proj`` pass per direction (the product's rows stay in registers); otherwise
+the projection runs in the HIP block-linear kernel over the edges.  Because every irrep block of the
 tensor track has the same multiplicity, the ir_mul features are ``[sum_l (2l+1)][channel]`` and the
 per-channel scalings are one broadcast multiply.
 """
@@ -314,6 +316,41 @@ class PairEmbedding(nn.Module):
         return scalar_features, tensor_features, edge_angular, edge_cutoff
 
 
+def _fused_projection_scale(tp: EdgeChannelWiseTensorProduct, lin: Linear) -> torch.Tensor | None:
+    """Per-row scale (1/sqrt(fan_in) of each projected irrep) that turns the projection's weight
+    vector, viewed as (paths*16, 16), into ``molix::edge_tp_proj``'s ``proj``; None when the fused
+    kernel does not apply (channels other than 16, or a projection whose weight blocks are not one
+    per product irrep, in the product's row order)."""
+    if tp.channels != 16 or lin.weight is None or lin.weight_classes is not None:
+        return None
+    blocks = K.edge_tp_proj_blocks(tp.config_id)
+    if not blocks or len(blocks) != len(lin.plan) or lin.weight_numel != tp.kept_paths.numel() * 256:
+        return None
+    scale, row = [], 0
+    for (l, nb, J, I), (off_o, mul_o, d, srcs, fan_in) in zip(blocks, lin.plan):
+        M = 2 * l + 1
+        if (mul_o != 16 or d != M or off_o != I * 16 or len(srcs) != 1
+                or srcs[0] != (row * 16, nb * 16, J * 256)):
+            return None
+        scale += [1.0 / math.sqrt(fan_in)] * (nb * 16)
+        row += M * nb
+    return torch.tensor(scale, dtype=lin.weight.dtype).unsqueeze(1)
+
+
+def _product_and_projection(layer, x, y, s):
+    """``tp_linear(tp(x, y, x_scale=s))`` (allegro.py:465-466).  With 16 channels, float32 on the
+    GPU and projection weights that take no gradient, one ``molix::edge_tp_proj`` pass: the
+    product's (E, paths x 16) rows per irrep are projected in registers and never reach memory."""
+    tp, lin = layer.tp, layer.tp_linear
+    sc = layer._proj_scale
+    if (sc is not None and x.is_cuda and x.dtype == torch.float32 and lin.weight.dtype == torch.float32
+            and not (torch.is_grad_enabled() and lin.weight.requires_grad)):
+        w = tp.weight.reshape(tp.num_paths_full, tp.channels).index_select(0, tp.kept_paths)
+        proj = lin.weight.reshape(-1, 16) * (sc * lin.output_scale if lin.output_scale != 1.0 else sc)
+        return K.edge_tp_proj(x, y, w, tp.config_id, proj, s)
+    return lin(tp(x, y, x_scale=s))
+
+
 class AllegroLayer(nn.Module):
     """One Allegro layer (allegro.py:252-480): env-scaled tensor track (x) neighbourhood-aggregated
     harmonics of the edge's source, projection back to the tensor irreps, latent MLP on
@@ -346,6 +383,7 @@ class AllegroLayer(nn.Module):
         self.residual_b = float(residual_alpha) / norm
         self.irreps_dim = Irreps(irreps).dim
         self._sh_dim = Irreps(sh_irreps).dim
+        self.register_buffer("_proj_scale", _fused_projection_scale(self.tp, self.tp_linear), persistent=False)
 
     def forward(self, scalar_features, tensor_features, edge_angular, edge_index, n_nodes: int):
         F = self.num_tensor_features
@@ -362,7 +400,7 @@ class AllegroLayer(nn.Module):
         # product kernel, as TP(s x) = s TP(x) channel by channel
         # index_select (backward: one index_add) rather than node_Y[src] (sort-based accumulating backward)
         edge_node_Y = node_Y.index_select(0, src)
-        new_tensor = self.tp_linear(self.tp(tensor_features, edge_node_Y, x_scale=self.env_embed(scalar_features)))
+        new_tensor = _product_and_projection(self, tensor_features, edge_node_Y, self.env_embed(scalar_features))
         # a x + b MLP([x, scalar part of the new tensor]) and the output env scaling
         return _layer_tail(self, scalar_features, new_tensor)
 

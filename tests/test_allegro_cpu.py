@@ -90,3 +90,45 @@ def test_oracle_invariance_catches_a_wrong_block_order(monkeypatch):
     a = _feats(m, cfg, pos, Z, ei)
     b = _feats(m, cfg, pos @ torch.from_numpy(R).T, Z, ei)
     assert float((a - b).abs().max()) > 1e-4 * float(a.abs().max())
+
+
+def test_fused_projection_layout_matches_oracle_linear():
+    """Host side of molix::edge_tp_proj (no GPU compute): the projected-irrep blocks the library
+    reports, the layer's per-row scales and the torch form of the projection (``edge_tp_project``,
+    whose adjoint is the fused backward's tracked form) against the oracle's equivariant linear on
+    the product's per-path blocks, for l_max 0..3."""
+    import molnex_amd.kernels as K
+    from oracle.mace_ref import linear as lin_ref
+
+    for l_max in range(4):
+        m = _model(l_max=l_max, F=16, S=8, layers=1)
+        layer = m.layers[0]
+        tp, lin = layer.tp, layer.tp_linear
+        blocks = K.edge_tp_proj_blocks(tp.config_id)
+        assert [b[0] for b in blocks] == list(range(l_max + 1))
+        muls = [b.mul // 16 for b in tp.irreps_out]
+        assert [b[1] for b in blocks] == muls
+        assert [b[2] for b in blocks] == list(np.cumsum([0] + muls[:-1]))
+        assert [b[3] for b in blocks] == [l * l for l in range(l_max + 1)]
+        scale = layer._proj_scale.reshape(-1)
+        assert torch.allclose(scale, torch.cat([torch.full((n * 16,), 1 / math.sqrt(n * 16)) for n in muls]))
+        # projection of a merged-layout product output vs the oracle linear on per-path blocks
+        ls = list(range(l_max + 1))
+        rows = K.edge_tp_out_rows(ls)
+        E = 5
+        g = torch.Generator().manual_seed(l_max)
+        t = torch.randn(E, len(rows), 16, generator=g, dtype=torch.float64)
+        per_path = t[:, rows, :].reshape(E, -1)
+        ds = EQ.ChannelwiseTP(AR._irr_str(ls, 16), AR._irr_str(ls), AR._irr_str(ls, 16), 16)
+        kept = sorted(range(len(ds.paths)), key=lambda k: ds.out_pos[k])
+        pblocks = [(16, ds.paths[k][4], ds.paths[k][5]) for k in kept]
+        w = lin.weight.detach().double()
+        ref = lin_ref(per_path, w, pblocks, [(16, l, (-1) ** l) for l in ls])
+        proj = w.reshape(-1, 16) * scale.double()[:, None]
+        got = K.edge_tp_project(t.reshape(E, -1), proj, blocks)
+        assert torch.allclose(got, ref, rtol=1e-6, atol=1e-6)  # the scales are float32
+        # adjoint: <G, P t> = <P^T G, t>
+        G = torch.randn(got.shape, generator=g, dtype=torch.float64)
+        lhs = (G * got).sum()
+        rhs = (K.edge_tp_proj_adjoint(G, proj, blocks) * t.reshape(E, -1)).sum()
+        assert torch.allclose(lhs, rhs, rtol=1e-12)
