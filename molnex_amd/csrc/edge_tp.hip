@@ -11,11 +11,14 @@
 //
 // mnx_edge_tp_proj_*: the product fused with the projection that follows it in each Allegro layer
 // (allegro.py:363-367, cuet.Linear(tp.irreps_out, irreps_in)) for 16 channels.  The product's NO
-// rows never reach HBM: each path's components are projected in registers (the 16 channels of
-// an edge rotated through its 16-lane row by DPP, weights staged in LDS) and only the
-// projected irreps (l = 0..l_max, 16 channels each) are written; the backward projects the
-// incoming gradient back the same way before the product's backward.  Per edge: forward
-// 4 (NX + NI) 16 + 4 NY bytes, backward 4 (2 NX + NI) 16 + 8 NY (NI = projected components).
+// rows never reach HBM.  Forward: a wavefront takes 16 edges at a time (lane = edge mod 16 and a
+// quarter of the channels), each path's components are the A operands of fp32 16x16x4
+// matrix-core products with the projection weights (staged once per workgroup in LDS, in operand
+// order), and only the projected irreps (l = 0..l_max, 16 channels each) are written.  Backward:
+// one edge per 16-lane row, channel c in lane c; the incoming gradient is taken back through the
+// projection by rotating it through the row (DPP) against LDS-staged weights, then the product's
+// backward.  Per edge: forward 4 (NX + NI) 16 + 4 NY bytes, backward 4 (2 NX + NI) 16 + 8 NY
+// (NI = projected components).
 
 #include "common.h"
 
@@ -35,6 +38,8 @@ typedef void (*ETPBwdFn)(const float*, const float*, const float*, const float*,
 typedef void (*ETPFwdPFn)(const float*, const float*, const float*, const float*, const float*, int64_t, float*);
 typedef void (*ETPBwdPFn)(const float*, const float*, const float*, const float*, const float*, const float*, int64_t,
                           float*, float*, float*, float*);
+
+typedef float f4 __attribute__((ext_vector_type(4)));  // one matrix-core accumulator / operand quad
 
 // Lane i of each 16-lane row receives the value of lane (i - K) mod 16 of the same row
 // (DPP row_ror:K; one edge per row in the fused kernels).
@@ -90,6 +95,15 @@ int etp_check(int32_t config, int32_t C, int64_t E, int* variant) {
         return set_error(MNX_ERR_UNSUPPORTED, "edge tensor product: %d channels (8, 16, 32, 64 or 128 compiled)", C);
     MNX_REQUIRE(E >= 0 && E < (int64_t(1) << 33), "edge count out of range");  // forward grid < 2^31 blocks
     return MNX_OK;
+}
+
+// Wavefronts of the fused product + projection forward: groups of 16 edges, grid-stride, at most
+// cap wavefronts (a multiple of 4: whole workgroups).
+constexpr int64_t kETPProjFwdWaves = 8192;
+int64_t etp_proj_waves(int64_t E, int64_t cap) {
+    const int64_t groups = (E + 15) / 16;
+    const int64_t waves = groups < cap ? groups : cap;
+    return ((waves + 3) / 4) * 4;
 }
 
 int64_t etp_bwd_waves(int64_t E, int C) {
@@ -187,9 +201,9 @@ int mnx_edge_tp_proj_fwd_f32(int32_t config, const float* x, const float* Y, con
     if (rc) return rc;
     if (num_edges == 0) return MNX_OK;
     MNX_REQUIRE(x && Y && w && proj && out, "null pointer argument");
-    const int64_t blocks = ceil_div(ceil_div(num_edges, int64_t(4) * kETPInfo[config].fwd_groups), kETPThreads / 64);
-    hipLaunchKernelGGL(kETPFwdP[config], dim3(unsigned(blocks)), dim3(kETPThreads), 0, (hipStream_t)stream, x, Y, w,
-                       x_scale, proj, num_edges, out);
+    const int64_t waves = etp_proj_waves(num_edges, kETPProjFwdWaves);
+    hipLaunchKernelGGL(kETPFwdP[config], dim3(unsigned(waves / 4)), dim3(kETPThreads), 0, (hipStream_t)stream, x, Y,
+                       w, x_scale, proj, num_edges, out);
     MNX_CHECK_LAUNCH();
     return MNX_OK;
 }

@@ -265,132 +265,127 @@ def proj_layout(cfg: Cfg):
 
 
 def _row_terms(p, m3):
-    """[(m1, expr of Y)] of output component m3 of path p (Y in y[q][...])."""
+    """[(m1, expr of Y)] of output component m3 of path p (Y in y[...])."""
     cf = p["c"]
     row = []
     for m1 in range(2 * p["l1"] + 1):
         terms = [(m2, cf[m1, m2, m3]) for m2 in range(2 * p["l2"] + 1) if abs(cf[m1, m2, m3]) > EPS]
         if not terms:
             continue
-        expr = f"{f32(terms[0][1])} * y[q][{p['o2'] + terms[0][0]}]"
+        expr = f"{f32(terms[0][1])} * y[{p['o2'] + terms[0][0]}]"
         for m2, v in terms[1:]:
-            expr = f"fmaf({f32(v)}, y[q][{p['o2'] + m2}], {expr})"
+            expr = f"fmaf({f32(v)}, y[{p['o2'] + m2}], {expr})"
         row.append((m1, expr))
     return row
 
 
-def _stage_proj(a, cfg: Cfg, fwd: bool):
-    """LDS copy of the projection weights wp (rows J*16 + c, 16 columns) as sw[J][c][k] in rows of
-    20 floats (float4 reads of four k at once by the 16 lanes of a row hit distinct banks):
-    forward sw[J][c][k] = wp[J][c][(c + k) mod 16] w[j(J)][c] (the product's path weight of
-    channel c folded in, j(J) the compiled path of block row J), backward wp[J][c][(c - k) mod 16]."""
+def _stage_proj(a, cfg: Cfg):
+    """LDS copy of the projection weights wp (rows J*16 + c, 16 columns) as the forward's matrix-core
+    B operands, sw[J][q][n][j] = wp[J][4q + j][n] w[j(J)][4q + j] (k = input channel 4 q + j,
+    column n = output channel; the product's path weight folded in, j(J) the compiled path of block
+    row J): lane l = 16 q + n reads its four j as one float4 at J*256 + 4 l."""
     blocks, _ = proj_layout(cfg)
     jidx = {p["k"]: j for j, p in enumerate(cfg.paths)}
-    a(f"  __shared__ __align__(16) float sw[{cfg.NP * 320}];")
+    a(f"  __shared__ __align__(16) float sw[{cfg.NP * 256}];")
     a("  {")
-    a("    const int cc = threadIdx.x >> 4, k = threadIdx.x & 15;")
-    a(f"    const int src = cc * 16 + ((cc {'+' if fwd else '-'} k) & 15), dst = cc * 20 + k;")
+    a("    const int q = threadIdx.x >> 6, n = (threadIdx.x >> 2) & 15, j = threadIdx.x & 3;")
+    a("    const int src = (4 * q + j) * 16 + n;")
     for l3, ps, J0, O in blocks:
         for b, p in enumerate(ps):
             J = J0 + b
-            if fwd:
-                a(f"    sw[{J * 320} + dst] = wp[{J * 256} + src] * w[{jidx[p['k']]} * 16 + cc];")
-            else:
-                a(f"    sw[{J * 320} + dst] = wp[{J * 256} + src];")
+            a(f"    sw[{J * 256} + threadIdx.x] = wp[{J * 256} + src] * w[{jidx[p['k']]} * 16 + 4 * q + j];")
     a("  }")
-    a("  __syncthreads();")
 
 
 def _fwdp(cfg: Cfg) -> str:
-    """Product and projection in one pass (16 channels, one edge per 16-lane row).  Lane c holds
-    channel c of every path's output components t_b[m3] of an output irrep; for each offset k it
-    forms p_k = sum_b W[(J0 + b)*16 + c][(c + k) mod 16] t_b[m3] and the row rotation (DPP
-    row_ror:k: lane c' receives lane (c' - k) mod 16) delivers p_k to lane c + k, so that
-    acc[c'] = sum_k p_k[c' - k] = sum_{b, c} W[(J0 + b)*16 + c][c'] t_b[m3][c].  Only the
+    """Product and projection in one pass (16 channels) on the matrix cores.  A wavefront walks
+    groups of 16 edges: lane l holds edge r = l mod 16 of the group and channels 4 q .. 4 q + 3
+    (q = l / 16).  Per output irrep, component m3 and path b, the product's values t_b[m3] are
+    exactly the A operand of four fp32 16x16x4 products (A[edge][k] = t_b[m3][edge][4 k + j]), whose
+    B operands are the projection weights of input channels 4 k + j (staged in LDS in operand
+    order); the 16x16 result holds out[edge 4 q + v][channel r] in lane l, register v.  Only the
     projected rows (irreps l = 0..l_max, 16 channels each) are written."""
     L = []
     a = L.append
-    NX, NY, NP = cfg.NX, cfg.NY, cfg.NP
-    EPW = fwd_groups(cfg)
+    NX, NY = cfg.NX, cfg.NY
     blocks, ncomp = proj_layout(cfg)
     a(f"__global__ void __launch_bounds__(256) etp_fwdp_c{cfg.idx}("
       "const float* __restrict__ x, const float* __restrict__ Y, const float* __restrict__ w, "
       "const float* __restrict__ xs, const float* __restrict__ wp, int64_t E, float* __restrict__ out) {")
-    _stage_proj(a, cfg, True)
-    a("  constexpr int G = 4, C = 16;")
-    a("  const int lane = threadIdx.x & 63, c0 = lane & 15;")
-    a(f"  const int64_t e0 = (int64_t(blockIdx.x) * 4 + (threadIdx.x >> 6)) * ({EPW} * G) + lane / 16;")
-    a("  const float4* __restrict__ sw4 = reinterpret_cast<const float4*>(sw) + c0 * 5;")
-    a(f"  float y[{EPW}][{NY}], xv[{EPW}][{NX}];")
-    a("#pragma unroll")
-    a(f"  for (int q = 0; q < {EPW}; ++q) {{")
-    a("    const int64_t e = e0 + q * G;")
-    a("    const int64_t es = e < E ? e : E - 1;  // rows past the end compute edge E - 1, unstored")
+    _stage_proj(a, cfg)
+    a("  __syncthreads();")
+    a("  const int lane = threadIdx.x & 63, r = lane & 15, q = lane >> 4;")
+    a("  const int64_t wave = int64_t(blockIdx.x) * 4 + (threadIdx.x >> 6), nwaves = int64_t(gridDim.x) * 4;")
+    a("  const int64_t ngroups = (E + 15) / 16;")
+    a("  const f4* __restrict__ sw4 = reinterpret_cast<const f4*>(sw) + lane;")
+    a("  for (int64_t grp = wave; grp < ngroups; grp += nwaves) {")
+    a("    asm volatile(\"\" ::: \"memory\");  // the LDS operands are re-read every group")
+    a("    const int64_t e = grp * 16 + r;")
+    a("    const int64_t es = e < E ? e : E - 1;  // edges past the end compute edge E - 1, unstored")
     a(f"    const float* __restrict__ Ye = Y + es * {NY};")
-    a(f"    const float* __restrict__ xe = x + es * ({NX} * int64_t(C));")
+    a(f"    float y[{NY}];")
     a("#pragma unroll")
-    a(f"    for (int i = 0; i < {NY}; ++i) y[q][i] = Ye[i];")
-    a("    const float sc = xs ? xs[es * C + c0] : 1.f;")
+    a(f"    for (int i = 0; i < {NY}; ++i) y[i] = Ye[i];")
+    a(f"    const f4* __restrict__ xe = reinterpret_cast<const f4*>(x + es * {NX * 16}) + q;")
+    a("    const f4 sc = xs ? *reinterpret_cast<const f4*>(xs + es * 16 + 4 * q) : f4{1.f, 1.f, 1.f, 1.f};")
+    a(f"    f4 xv[{NX}];")
     a("#pragma unroll")
-    a(f"    for (int i = 0; i < {NX}; ++i) xv[q][i] = xe[i * C + c0] * sc;")
-    a("  }")
+    a(f"    for (int i = 0; i < {NX}; ++i) xv[i] = xe[i * 4] * sc;")
     for l3, ps, J0, O in blocks:
-        M, nb = 2 * l3 + 1, len(ps)
-        a("  {")
-        a(f"    float t[{EPW}][{nb}][{M}], acc[{EPW}][{M}];")
+        M = 2 * l3 + 1
+        a("    {")
+        a(f"      f4 acc[{M}];")
         a("#pragma unroll")
-        a(f"    for (int q = 0; q < {EPW}; ++q) {{")
+        a(f"      for (int m = 0; m < {M}; ++m) acc[m] = f4{{0.f, 0.f, 0.f, 0.f}};")
         for b, p in enumerate(ps):
+            a("      __builtin_amdgcn_sched_barrier(0);  // one path at a time (register pressure)")
+            a("      {")
+            a(f"        const f4 bw = sw4[{(J0 + b) * 64}];")
+            a(f"        f4 t[{M}];")
             for m3 in range(M):
                 row = _row_terms(p, m3)
                 if not row:
-                    a(f"      t[q][{b}][{m3}] = 0.f;")
+                    a(f"        t[{m3}] = f4{{0.f, 0.f, 0.f, 0.f}};")
                     continue
-                sx = f"({row[0][1]}) * xv[q][{p['o1'] + row[0][0]}]"
+                sx = f"({row[0][1]}) * xv[{p['o1'] + row[0][0]}]"
                 for m1, expr in row[1:]:
-                    sx = f"fmaf({expr}, xv[q][{p['o1'] + m1}], {sx})"
-                a(f"      t[q][{b}][{m3}] = {sx};")
-        a("    }")
-        for kq in range(4):
-            # one group of four offsets at a time: the scheduler would otherwise issue every
-            # LDS read of the kernel up front and run out of registers
-            a("    __builtin_amdgcn_sched_barrier(0);")
-            a("    {")
-            for b in range(nb):
-                a(f"      const float4 v{b} = sw4[{(J0 + b) * 80 + kq}];")
-            for kk, comp in enumerate("xyzw"):
-                k = 4 * kq + kk
-                a("#pragma unroll")
-                a(f"      for (int q = 0; q < {EPW}; ++q)")
-                a("#pragma unroll")
-                a(f"        for (int m = 0; m < {M}; ++m) {{")
-                pe = f"v0.{comp} * t[q][0][m]"
-                for b in range(1, nb):
-                    pe = f"fmaf(v{b}.{comp}, t[q][{b}][m], {pe})"
-                if k == 0:
-                    a(f"          acc[q][m] = {pe};")
-                else:
-                    a(f"          acc[q][m] += ror16<{k}>({pe});")
-                a("        }")
-            a("    }")
-        # the sums complete here, before the guarded store (sunk into it, every rotated partial
-        # would stay live up to the store and the rotations could not fold into the adds)
+                    sx = f"({expr}) * xv[{p['o1'] + m1}] + {sx}"
+                a(f"        t[{m3}] = {sx};")
+            a("#pragma unroll")
+            a(f"        for (int m = 0; m < {M}; ++m) {{")
+            a("          acc[m] = __builtin_amdgcn_mfma_f32_16x16x4f32(t[m][0], bw[0], acc[m], 0, 0, 0);")
+            a("          acc[m] = __builtin_amdgcn_mfma_f32_16x16x4f32(t[m][1], bw[1], acc[m], 0, 0, 0);")
+            a("          acc[m] = __builtin_amdgcn_mfma_f32_16x16x4f32(t[m][2], bw[2], acc[m], 0, 0, 0);")
+            a("          acc[m] = __builtin_amdgcn_mfma_f32_16x16x4f32(t[m][3], bw[3], acc[m], 0, 0, 0);")
+            a("        }")
+            a("      }")
         a("#pragma unroll")
-        a(f"    for (int q = 0; q < {EPW}; ++q)")
+        a("      for (int v = 0; v < 4; ++v) {")
+        a("        const int64_t eo = grp * 16 + 4 * q + v;")
+        a("        if (eo < E) {")
+        a(f"          float* __restrict__ oe = out + eo * {ncomp * 16} + {O * 16} + r;")
         a("#pragma unroll")
-        a(f"      for (int m = 0; m < {M}; ++m) asm volatile(\"\" : \"+v\"(acc[q][m]));")
-        a("#pragma unroll")
-        a(f"    for (int q = 0; q < {EPW}; ++q) {{")
-        a("      const int64_t e = e0 + q * G;")
-        a("      if (e < E) {")
-        a(f"        float* __restrict__ oe = out + e * {ncomp * 16} + {O * 16} + c0;")
-        a("#pragma unroll")
-        a(f"        for (int m = 0; m < {M}; ++m) oe[m * 16] = acc[q][m];")
+        a(f"          for (int m = 0; m < {M}; ++m) oe[m * 16] = acc[m][v];")
+        a("        }")
         a("      }")
         a("    }")
-        a("  }")
+    a("  }")
     a("}")
     return "\n".join(L)
+
+
+def _stage_proj_rot(a, cfg: Cfg):
+    """LDS copy of the projection weights wp (rows J*16 + c, 16 columns) for the backward's row
+    rotations, sw[J][c][k] = wp[J][c][(c - k) mod 16] in rows of 20 floats (float4 reads of four k
+    at once by the 16 lanes of a row hit distinct banks)."""
+    a(f"  __shared__ __align__(16) float sw[{cfg.NP * 320}];")
+    a("  {")
+    a("    const int cc = threadIdx.x >> 4, k = threadIdx.x & 15;")
+    a("    const int src = cc * 16 + ((cc - k) & 15), dst = cc * 20 + k;")
+    for J in range(cfg.NP):
+        a(f"    sw[{J * 320} + dst] = wp[{J * 256} + src];")
+    a("  }")
+    a("  __syncthreads();")
 
 
 def _bwdp(cfg: Cfg) -> str:
@@ -408,7 +403,7 @@ def _bwdp(cfg: Cfg) -> str:
       "const float* __restrict__ gproj, const float* __restrict__ x, const float* __restrict__ Y, "
       "const float* __restrict__ w, const float* __restrict__ xs, const float* __restrict__ wp, int64_t E, "
       "float* __restrict__ gx, float* __restrict__ gY, float* __restrict__ gw_part, float* __restrict__ gxs) {")
-    _stage_proj(a, cfg, False)
+    _stage_proj_rot(a, cfg)
     a("  constexpr int G = 4, C = 16;")
     a("  const int lane = threadIdx.x & 63, c = lane & 15;")
     a("  const int64_t wave = int64_t(blockIdx.x) * 4 + (threadIdx.x >> 6), nwaves = int64_t(gridDim.x) * 4;")
