@@ -709,11 +709,13 @@ int mnx_edge_tp_bwd_f32(int32_t config, int32_t channels, const float* x, const 
 /* -1: config out of range); out is [E][NI * 16] with NI =                   */
 /* sum (2l + 1).  proj is [num_paths * 16][16] (row J*16 + c: input channel  */
 /* c of path block J; the reference's weights of that irrep times its        */
-/* 1/sqrt(fan_in)).  No projection gradient; the backward's other outputs,   */
-/* workspace and order of summation are those of mnx_edge_tp_bwd_f32 with    */
-/* channels = 16 (mnx_edge_tp_bwd_workspace_bytes(config, 16, E) bytes).     */
+/* 1/sqrt(fan_in)).  No projection gradient; the backward's other outputs   */
+/* and fixed order of summation are those of mnx_edge_tp_bwd_f32 with        */
+/* channels = 16, through a workspace of                                     */
+/* mnx_edge_tp_proj_bwd_workspace_bytes bytes (0: no fused kernel).          */
 /* ------------------------------------------------------------------------ */
 int32_t mnx_edge_tp_proj_info(int32_t config, int32_t* blocks);
+size_t mnx_edge_tp_proj_bwd_workspace_bytes(int32_t config, int64_t num_edges);
 int mnx_edge_tp_proj_fwd_f32(int32_t config, const float* x, const float* Y, const float* w,
                              const float* x_scale, const float* proj, int64_t num_edges,
                              float* out, mnx_stream_t stream);

@@ -764,7 +764,7 @@ def edge_tp_proj_backward(grad_out: Tensor, x: Tensor, Y: Tensor, w: Tensor, con
     gw = torch.empty_like(wss) if need_w else wss.new_empty(0)
     need_scale = bool(need_scale and sc is not None)
     gs = torch.empty_like(sc) if need_scale else xs.new_empty(0)
-    ws = _ws(max(int(lib.mnx_edge_tp_bwd_workspace_bytes(config, 16, E)), 1), xs.device)
+    ws = _ws(max(int(lib.mnx_edge_tp_proj_bwd_workspace_bytes(config, E)), 1), xs.device)
     check(lib.mnx_edge_tp_proj_bwd_f32(config, ptr(xs), ptr(Ys), ptr(wss), ptr(sc) if sc is not None else None,
                                        ptr(pj), ptr(go), E, ptr(gx) if need_x else None,
                                        ptr(gY) if need_Y else None, ptr(gw) if need_w else None,
