@@ -1418,6 +1418,29 @@ def _(grad, weight):
     return grad.new_empty(grad.shape[0], weight.shape[1])
 
 
+@torch.library.custom_op("molix::edge_weights_backward_acc", mutates_args=("out",), device_types="cuda")
+def edge_weights_backward_acc(grad: Tensor, weight: Tensor, out: Tensor) -> None:
+    """``out += grad @ weight`` in place (``out`` a contiguous (E, K) float32 tensor): the
+    input-gradient product of ``edge_weights`` accumulated into an existing gradient in the same
+    pass (``mnx_edge_weights_bwd_cols_f32`` with accumulation), instead of a product and an add."""
+    N, K = weight.shape
+    if grad.dim() != 2 or grad.shape[1] != N:
+        raise ValueError("edge_weights_backward_acc: grad must be (E, N)")
+    if (out.dtype != torch.float32 or out.shape != (grad.shape[0], K) or not out.is_contiguous()
+            or out.data_ptr() % 16 != 0):
+        raise ValueError("edge_weights_backward_acc: out must be a contiguous, 16-byte aligned float32 (E, K)")
+    g = _aligned16(grad.to(torch.float32))
+    frag = _ew_frag(weight, True)
+    check(_lib.load().mnx_edge_weights_bwd_cols_f32(ptr(g), N, None, g.shape[0], N, ptr(frag), K, ptr(out), 1,
+                                                    _stream(g)),
+          "edge_weights backward (accumulating)")
+
+
+@edge_weights_backward_acc.register_fake
+def _(grad, weight, out):
+    return None
+
+
 # mnx_tall_tn_f32 takes row strides below 2^25 floats (its 16-row step offsets stay in 31 bits)
 _TALL_MAX_STRIDE = 1 << 25
 

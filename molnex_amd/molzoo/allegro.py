@@ -114,24 +114,79 @@ def _tail_torch(s, nt, lat, tenv, a, b, F):
     return updated, _scale_by_channel(nt, tenv(updated), None, F)
 
 
+def _tail_weights(layer, S):
+    """(W_s, W_t, b c) of the frozen tail: ``updated = s W_s^T + nt[:, :F] W_t^T + b c`` with the
+    residual folded into the square block (``W_s = b W[:, :S] + a I``: ``a s`` needs no pass of its
+    own, forward or backward)."""
+    lat = layer.latent_mlp[0]
+    a, b = layer.residual_a, layer.residual_b
+    ws = torch.eye(S, dtype=lat.weight.dtype, device=lat.weight.device).mul_(a).add_(lat.weight[:, :S], alpha=b)
+    return ws, lat.weight[:, S:] * b, lat.bias * b
+
+
+def _row_linear(h, weight, bias=None):
+    """``h @ weight.T + bias`` on the split-fp16 row kernel (``molix::edge_weights``, fp32-accurate,
+    faster than hipBLASLt on these tall, narrow shapes) where it takes the shape, else ``addmm``."""
+    N, Kd = weight.shape
+    if h.is_contiguous() and K.edge_weights_supported(Kd, N):
+        return K.edge_weights(h, weight, bias)
+    return torch.addmm(bias, h, weight.t()) if bias is not None else h @ weight.t()
+
+
+def _row_grad(g, weight, out=None):
+    """``g @ weight`` (the input gradient of ``_row_linear``), or ``out += g @ weight`` in the same
+    pass when ``out`` is given."""
+    N, Kd = weight.shape
+    if K.edge_weights_supported(Kd, N) and (out is None or (out.is_contiguous() and out.data_ptr() % 16 == 0)):
+        if out is None:
+            return K.edge_weights_backward(g, weight)
+        K.edge_weights_backward_acc(g, weight, out)
+        return out
+    return g @ weight if out is None else out.add_(g @ weight)
+
+
+def _tail_grads_tracked(layer, s, nt, g_upd, g_out, need_s, need_nt):
+    """(grad s, grad nt) of the layer tail in tracked ops (for a backward that is differentiated
+    again), the env scale recomputed from s and nt so that second derivatives reach them.  Not
+    autograd.grad on a recomputed tail: nt itself depends on s through the layer's product."""
+    lat, tenv = layer.latent_mlp[0], layer.tensor_env
+    a, b, F = layer.residual_a, layer.residual_b, layer.num_tensor_features
+    ws = lat.weight[:, :s.shape[1]] * b
+    wt = lat.weight[:, s.shape[1]:] * b
+    with torch.enable_grad():
+        upd = torch.add(torch.addmm(lat.bias * b, torch.cat([s, nt[:, :F]], dim=1), lat.weight.t() * b), s, alpha=a)
+        tv_t = torch.addmm(tenv.bias, upd, tenv.weight.t())
+        if g_out is not None:
+            g_nt, g_tv = K.channel_scale_backward(g_out.contiguous(), nt, tv_t, nt.shape[1] // F, True, True)
+            g_lat = g_tv @ tenv.weight if g_upd is None else g_upd + g_tv @ tenv.weight
+        else:
+            g_nt, g_lat = torch.zeros_like(nt), g_upd
+        if g_lat is None:
+            return None, (g_nt if need_nt else None)
+        g_s = a * g_lat + g_lat @ ws if need_s else None
+        if need_nt:
+            g_nt = torch.cat([g_nt[:, :F] + g_lat @ wt, g_nt[:, F:]], dim=1)
+    return g_s, (g_nt if need_nt else None)
+
+
 class _LayerTail(torch.autograd.Function):
     """The layer tail with frozen parameters (the energy + forces path) as GEMMs on row blocks:
-    ``updated = a s + s (b W_s)^T + nt[:, :F] (b W_t)^T + b c`` (W = [W_s W_t], c the latent
-    layer's weights and bias) without the concatenation, and a backward that forms ``nt``'s
-    gradient in place: the env scaling's backward (one pass for both gradients), then the latent
-    part added into the scalar columns, with no zero-filled slice gradient and no accumulation
-    pass.  Differentiated again (create_graph), the backward runs the same formulas in tracked
-    ops, with the env scale recomputed from the inputs."""
+    ``updated = s W_s^T + nt[:, :F] W_t^T + b c`` (``_tail_weights``: the residual a s folded into
+    W_s) without the concatenation, and a backward that never forms the latent gradient: with
+    ``g_lat = g_upd + g_tv T`` (T the env layer's weight), ``g_s = g_upd W_s + g_tv (T W_s)`` and the
+    scalar columns of nt get ``g_upd W_t + g_tv (T W_t)``, two products each, the second accumulated
+    in the same pass.  The env scaling's backward gives nt's gradient in one pass for both
+    gradients; there is no zero-filled slice gradient and no accumulation pass.  Differentiated
+    again (create_graph), the backward runs the same formulas in tracked ops, with the env scale
+    recomputed from the inputs."""
 
     @staticmethod
     def forward(ctx, s, nt, layer):
-        lat, tenv = layer.latent_mlp[0], layer.tensor_env
-        a, b, F = layer.residual_a, layer.residual_b, layer.num_tensor_features
-        ws = lat.weight[:, :s.shape[1]] * b
-        wt = lat.weight[:, s.shape[1]:] * b
-        upd = torch.addmm(lat.bias * b, s, ws.t())
+        tenv = layer.tensor_env
+        F = layer.num_tensor_features
+        ws, wt, bc = _tail_weights(layer, s.shape[1])
+        upd = _row_linear(s, ws, bc)
         upd.addmm_(nt[:, :F], wt.t())
-        upd.add_(s, alpha=a)
         tv = torch.addmm(tenv.bias, upd, tenv.weight.t())
         out = K.channel_scale(nt, tv, nt.shape[1] // F)
         ctx.save_for_backward(s, nt, tv)
@@ -147,41 +202,126 @@ class _LayerTail(torch.autograd.Function):
         lat, tenv = layer.latent_mlp[0], layer.tensor_env
         a, b, F = layer.residual_a, layer.residual_b, layer.num_tensor_features
         need_s, need_nt = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
-        ws = lat.weight[:, :s.shape[1]] * b
-        wt = lat.weight[:, s.shape[1]:] * b
         if torch.is_grad_enabled():
-            # differentiated again (create_graph): the same gradient formulas in tracked ops, with
-            # the env scale recomputed from s and nt so that second derivatives reach them (not
-            # autograd.grad on a recomputed tail: nt itself depends on s through the layer's product)
+            # differentiated again (create_graph): the same gradient formulas in tracked ops
+            g_s, g_nt = _tail_grads_tracked(layer, s, nt, g_upd, g_out, need_s, need_nt)
+            return g_s, g_nt, None
+        g_s, g_nt = _tail_grads(layer, s, nt, tv, g_upd, g_out, need_s, need_nt)
+        return g_s, g_nt, None
+
+
+def _tail_grads(layer, s, nt, tv, g_upd, g_out, need_s, need_nt):
+    """(grad s, grad nt) of the frozen tail: with ``g_lat = g_upd + g_tv T`` (T the env layer's
+    weight), ``g_s = g_upd W_s + g_tv (T W_s)`` and the scalar columns of nt get
+    ``g_upd W_t + g_tv (T W_t)``: two products each, the second accumulated in the same pass, and the
+    latent gradient never formed."""
+    tenv, F = layer.tensor_env, layer.num_tensor_features
+    g_tv = None
+    if g_out is not None:
+        g_nt, g_tv = K.channel_scale_backward(g_out.contiguous(), nt, tv, nt.shape[1] // F, need_nt, True)
+    else:
+        g_nt = torch.zeros_like(nt) if need_nt else None
+    if g_upd is None and g_tv is None:
+        return None, (g_nt if need_nt else None)
+    ws, wt, _ = _tail_weights(layer, s.shape[1])
+    g_upd = g_upd.contiguous() if g_upd is not None else None
+
+    def through(w):
+        tw = tenv.weight @ w
+        if g_upd is None:
+            return _row_grad(g_tv, tw)
+        out = _row_grad(g_upd, w)
+        return _row_grad(g_tv, tw, out) if g_tv is not None else out
+
+    g_s = through(ws) if need_s else None
+    if need_nt:
+        g_nt[:, :F] += through(wt)
+    return g_s, (g_nt if need_nt else None)
+
+
+class _LayerFrozen(torch.autograd.Function):
+    """A whole layer with frozen parameters and the fused product + projection: env weights
+    ``x_scale = env_embed(s)``, ``nt = edge_tp_proj(V, Y_src, w, proj, x_scale)``, then the tail.
+    One Function so that the env layer's input gradient is accumulated into the scalars' gradient
+    in the same pass (``g_s += g_xs W_env``) instead of autograd summing two (E, S) gradients.
+    Differentiated again (create_graph), the backward runs tracked formulas: the tail's, the
+    projection's adjoint and ``molix::edge_tp``'s backward (which has second derivatives)."""
+
+    @staticmethod
+    def forward(ctx, s, V, eY, layer, w, proj):
+        ee, F = layer.env_embed, layer.num_tensor_features
+        xs = _row_linear(s, ee.weight, ee.bias)
+        nt = K.edge_tp_proj(V, eY, w, layer.tp.config_id, proj, xs)
+        tenv = layer.tensor_env
+        ws, wt, bc = _tail_weights(layer, s.shape[1])
+        upd = _row_linear(s, ws, bc)
+        upd.addmm_(nt[:, :F], wt.t())
+        tv = torch.addmm(tenv.bias, upd, tenv.weight.t())
+        out = K.channel_scale(nt, tv, nt.shape[1] // F)
+        ctx.save_for_backward(s, V, eY, w, proj, xs, nt, tv)
+        ctx.layer = layer
+        ctx.set_materialize_grads(False)
+        return upd, out
+
+    @staticmethod
+    def backward(ctx, g_upd, g_out):
+        s, V, eY, w, proj, xs, nt, tv = ctx.saved_tensors
+        layer = ctx.layer
+        ee, cfg = layer.env_embed, layer.tp.config_id
+        need_s, need_V, need_eY = ctx.needs_input_grad[:3]
+        if torch.is_grad_enabled():
+            # nt and the env weights recomputed in tracked ops, so that second derivatives reach
+            # V, the source harmonics and s through them
             with torch.enable_grad():
-                upd = torch.add(torch.addmm(lat.bias * b, torch.cat([s, nt[:, :F]], dim=1), lat.weight.t() * b), s,
-                                alpha=a)
-                tv_t = torch.addmm(tenv.bias, upd, tenv.weight.t())
-                if g_out is not None:
-                    g_nt, g_tv = K.channel_scale_backward(g_out.contiguous(), nt, tv_t, nt.shape[1] // F, True, True)
-                    g_lat = g_tv @ tenv.weight if g_upd is None else g_upd + g_tv @ tenv.weight
-                else:
-                    g_nt, g_lat = torch.zeros_like(nt), g_upd
-                if g_lat is None:
-                    return None, (g_nt if need_nt else None), None
-                g_s = a * g_lat + g_lat @ ws if need_s else None
-                if need_nt:
-                    g_nt = torch.cat([g_nt[:, :F] + g_lat @ wt, g_nt[:, F:]], dim=1)
-            return g_s, (g_nt if need_nt else None), None
-        if g_out is not None:
-            g_nt, g_tv = K.channel_scale_backward(g_out.contiguous(), nt, tv, nt.shape[1] // F, need_nt, True)
-            g_lat = torch.addmm(g_upd, g_tv, tenv.weight) if g_upd is not None else g_tv @ tenv.weight
-        else:
-            g_nt = torch.zeros_like(nt) if need_nt else None
-            g_lat = g_upd
-        if g_lat is None:
-            return None, g_nt if need_nt else None, None
-        g_s = torch.addmm(g_lat, g_lat, ws, beta=a) if need_s else None
-        if need_nt:
-            # the product into a contiguous block, then one strided add (an in-place product on
-            # the column slice would copy the slice out and back)
-            g_nt[:, :F] += g_lat @ wt
-        return g_s, (g_nt if need_nt else None), None
+                xs_t = nn.functional.linear(s, ee.weight, ee.bias)
+                nt_t = K.edge_tp_proj(V, eY, w, cfg, proj, xs_t)
+            g_s, g_nt = _tail_grads_tracked(layer, s, nt_t, g_upd, g_out, need_s, True)
+            if g_nt is None:
+                return g_s, None, None, None, None, None
+            with torch.enable_grad():
+                g_tp = K.edge_tp_proj_adjoint(g_nt, proj, K.edge_tp_proj_blocks(cfg))
+                gV, geY, _, g_xs = K.edge_tp_backward(g_tp.contiguous(), V, eY, w, cfg, 16, need_V, need_eY, False,
+                                                      xs_t, need_s)
+                if need_s:
+                    g_x = g_xs @ ee.weight
+                    g_s = g_x if g_s is None else g_s + g_x
+            return (g_s, gV.reshape(V.shape) if need_V else None, geY.reshape(eY.shape) if need_eY else None,
+                    None, None, None)
+        g_s, g_nt = _tail_grads(layer, s, nt, tv, g_upd, g_out, need_s, True)
+        if g_nt is None:
+            return g_s, None, None, None, None, None
+        gV, geY, _, g_xs = K.edge_tp_proj_backward(g_nt, V, eY, w, cfg, proj, need_V, need_eY, False, xs, need_s)
+        if need_s:
+            g_s = _row_grad(g_xs, ee.weight) if g_s is None else _row_grad(g_xs, ee.weight, g_s)
+        return (g_s, gV.reshape(V.shape) if need_V else None, geY.reshape(eY.shape) if need_eY else None,
+                None, None, None)
+
+
+def _tail_ok(layer, s, nt_dim):
+    mods = list(layer.latent_mlp)
+    F = layer.num_tensor_features
+    params = [p for m in (layer.latent_mlp, layer.tensor_env) for p in m.parameters()]
+    return (len(mods) == 1 and isinstance(mods[0], nn.Linear) and mods[0].bias is not None
+            and layer.tensor_env.bias is not None and s.is_cuda and s.dtype == torch.float32 and s.dim() == 2
+            and F % 4 == 0 and nt_dim % F == 0 and nt_dim // F in K.CHANNEL_PRODUCT_COMPONENTS
+            and all(p.dtype == torch.float32 for p in params)
+            and not (torch.is_grad_enabled() and any(p.requires_grad for p in params)))
+
+
+def _layer_frozen(layer, s, V, eY):
+    """The whole layer as ``_LayerFrozen`` when every parameter it reads is frozen and the fused
+    product + projection applies; None otherwise."""
+    tp, lin, ee = layer.tp, layer.tp_linear, layer.env_embed
+    params = [tp.weight, lin.weight, ee.weight] + ([ee.bias] if ee.bias is not None else [])
+    if (layer._proj_scale is None or ee.bias is None or not V.is_cuda or V.dtype != torch.float32
+            or any(p.dtype != torch.float32 for p in params)
+            or (torch.is_grad_enabled() and any(p.requires_grad for p in params))
+            or not _tail_ok(layer, s, layer.irreps_dim)):
+        return None
+    w = tp.weight.reshape(tp.num_paths_full, tp.channels).index_select(0, tp.kept_paths)
+    proj = lin.weight.reshape(-1, 16) * (layer._proj_scale * lin.output_scale if lin.output_scale != 1.0
+                                         else layer._proj_scale)
+    return _LayerFrozen.apply(s.contiguous(), V.contiguous(), eY.contiguous(), layer, w, proj)
 
 
 def _layer_tail(layer, s, nt):
@@ -190,14 +330,7 @@ def _layer_tail(layer, s, nt):
     module form."""
     mods = list(layer.latent_mlp)
     F = layer.num_tensor_features
-    params = [p for m in (layer.latent_mlp, layer.tensor_env) for p in m.parameters()]
-    ok = (len(mods) == 1 and isinstance(mods[0], nn.Linear) and mods[0].bias is not None
-          and layer.tensor_env.bias is not None and s.is_cuda and s.dtype == torch.float32
-          and nt.dtype == torch.float32 and s.dim() == 2 and nt.dim() == 2 and F % 4 == 0
-          and nt.shape[1] % F == 0 and nt.shape[1] // F in K.CHANNEL_PRODUCT_COMPONENTS
-          and all(p.dtype == torch.float32 for p in params)
-          and not (torch.is_grad_enabled() and any(p.requires_grad for p in params)))
-    if ok:
+    if nt.dtype == torch.float32 and nt.dim() == 2 and _tail_ok(layer, s, nt.shape[1]):
         return _LayerTail.apply(s.contiguous(), nt.contiguous(), layer)
     return _tail_torch(s, nt, mods[0] if len(mods) == 1 else None, layer.tensor_env, layer.residual_a,
                        layer.residual_b, F) if len(mods) == 1 else _tail_modules(layer, s, nt)
@@ -400,6 +533,9 @@ class AllegroLayer(nn.Module):
         # product kernel, as TP(s x) = s TP(x) channel by channel
         # index_select (backward: one index_add) rather than node_Y[src] (sort-based accumulating backward)
         edge_node_Y = node_Y.index_select(0, src)
+        fused = _layer_frozen(self, scalar_features, tensor_features, edge_node_Y)
+        if fused is not None:
+            return fused
         new_tensor = _product_and_projection(self, tensor_features, edge_node_Y, self.env_embed(scalar_features))
         # a x + b MLP([x, scalar part of the new tensor]) and the output env scaling
         return _layer_tail(self, scalar_features, new_tensor)
