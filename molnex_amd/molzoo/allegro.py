@@ -239,61 +239,98 @@ def _tail_grads(layer, s, nt, tv, g_upd, g_out, need_s, need_nt):
     return g_s, (g_nt if need_nt else None)
 
 
-class _LayerFrozen(torch.autograd.Function):
-    """A whole layer with frozen parameters and the fused product + projection: env weights
-    ``x_scale = env_embed(s)``, ``nt = edge_tp_proj(V, Y_src, w, proj, x_scale)``, then the tail.
-    One Function so that the env layer's input gradient is accumulated into the scalars' gradient
-    in the same pass (``g_s += g_xs W_env``) instead of autograd summing two (E, S) gradients.
-    Differentiated again (create_graph), the backward runs tracked formulas: the tail's, the
-    projection's adjoint and ``molix::edge_tp``'s backward (which has second derivatives)."""
+class _LayerChain(torch.autograd.Function):
+    """A whole layer with frozen parameters and the fused product + projection, its output env
+    scaling left to the next layer: env weights ``x_scale = env_embed(s)`` (times the previous
+    layer's output env weights ``tvp``, which scale the tensor track channel by channel and so fold
+    into the product's x_scale: TP(s (t x)) = (s t) TP(x)), ``nt = edge_tp_proj(V, Y_src, w, proj,
+    x_scale)``, the tail's ``updated`` and this layer's env weights ``tv = tensor_env(updated)``.
+    Returns (updated, nt, tv); the layer's tensor output is ``nt`` scaled by ``tv``, formed only
+    where a caller needs it.  One Function, so that the env layer's input gradient is accumulated
+    into the scalars' gradient in the same pass and the latent gradient is never formed.
+    Differentiated again (create_graph), the backward runs the same formulas in tracked ops (the
+    tail is linear in its inputs; the product's backward is ``molix::edge_tp``'s, which has second
+    derivatives)."""
 
     @staticmethod
-    def forward(ctx, s, V, eY, layer, w, proj):
-        ee, F = layer.env_embed, layer.num_tensor_features
+    def forward(ctx, s, V, tvp, eY, layer, w, proj):
+        ee, tenv, F = layer.env_embed, layer.tensor_env, layer.num_tensor_features
         xs = _row_linear(s, ee.weight, ee.bias)
-        nt = K.edge_tp_proj(V, eY, w, layer.tp.config_id, proj, xs)
-        tenv = layer.tensor_env
+        xe = xs * tvp if tvp is not None else xs
+        nt = K.edge_tp_proj(V, eY, w, layer.tp.config_id, proj, xe)
         ws, wt, bc = _tail_weights(layer, s.shape[1])
         upd = _row_linear(s, ws, bc)
         upd.addmm_(nt[:, :F], wt.t())
         tv = torch.addmm(tenv.bias, upd, tenv.weight.t())
-        out = K.channel_scale(nt, tv, nt.shape[1] // F)
-        ctx.save_for_backward(s, V, eY, w, proj, xs, nt, tv)
+        ctx.save_for_backward(s, V, tvp, eY, w, proj, xs, xe)
         ctx.layer = layer
         ctx.set_materialize_grads(False)
-        return upd, out
+        return upd, nt, tv
 
     @staticmethod
-    def backward(ctx, g_upd, g_out):
-        s, V, eY, w, proj, xs, nt, tv = ctx.saved_tensors
+    def backward(ctx, g_upd, g_nt, g_tv):
+        s, V, tvp, eY, w, proj, xs, xe = ctx.saved_tensors
         layer = ctx.layer
-        ee, cfg = layer.env_embed, layer.tp.config_id
-        need_s, need_V, need_eY = ctx.needs_input_grad[:3]
+        ee, tenv, cfg = layer.env_embed, layer.tensor_env, layer.tp.config_id
+        a, b, F = layer.residual_a, layer.residual_b, layer.num_tensor_features
+        need_s, need_V, need_tvp, need_eY = ctx.needs_input_grad[:4]
+        need_tvp = need_tvp and tvp is not None
+        nout = 7
+        if g_upd is None and g_nt is None and g_tv is None:
+            return (None,) * nout
         if torch.is_grad_enabled():
-            # nt and the env weights recomputed in tracked ops, so that second derivatives reach
-            # V, the source harmonics and s through them
+            lat = layer.latent_mlp[0]
             with torch.enable_grad():
                 xs_t = nn.functional.linear(s, ee.weight, ee.bias)
-                nt_t = K.edge_tp_proj(V, eY, w, cfg, proj, xs_t)
-            g_s, g_nt = _tail_grads_tracked(layer, s, nt_t, g_upd, g_out, need_s, True)
-            if g_nt is None:
-                return g_s, None, None, None, None, None
-            with torch.enable_grad():
+                xe_t = xs_t * tvp if tvp is not None else xs_t
+                g_lat = None
+                if g_upd is not None:
+                    g_lat = g_upd
+                if g_tv is not None:
+                    g_lat = g_tv @ tenv.weight if g_lat is None else g_lat + g_tv @ tenv.weight
+                g_s = None
+                if g_lat is not None:
+                    if need_s:
+                        g_s = a * g_lat + g_lat @ (lat.weight[:, :s.shape[1]] * b)
+                    cols = g_lat @ (lat.weight[:, s.shape[1]:] * b)
+                    base = g_nt if g_nt is not None else torch.zeros_like(V)
+                    g_nt = torch.cat([base[:, :F] + cols, base[:, F:]], dim=1)
                 g_tp = K.edge_tp_proj_adjoint(g_nt, proj, K.edge_tp_proj_blocks(cfg))
-                gV, geY, _, g_xs = K.edge_tp_backward(g_tp.contiguous(), V, eY, w, cfg, 16, need_V, need_eY, False,
-                                                      xs_t, need_s)
+                gV, geY, _, g_xe = K.edge_tp_backward(g_tp.contiguous(), V, eY, w, cfg, 16, need_V, need_eY, False,
+                                                      xe_t, need_s or need_tvp)
+                g_tvp = g_xe * xs_t if need_tvp else None
                 if need_s:
-                    g_x = g_xs @ ee.weight
+                    g_x = (g_xe * tvp if tvp is not None else g_xe) @ ee.weight
                     g_s = g_x if g_s is None else g_s + g_x
-            return (g_s, gV.reshape(V.shape) if need_V else None, geY.reshape(eY.shape) if need_eY else None,
+            return (g_s, gV.reshape(V.shape) if need_V else None, g_tvp, geY.reshape(eY.shape) if need_eY else None,
                     None, None, None)
-        g_s, g_nt = _tail_grads(layer, s, nt, tv, g_upd, g_out, need_s, True)
-        if g_nt is None:
-            return g_s, None, None, None, None, None
-        gV, geY, _, g_xs = K.edge_tp_proj_backward(g_nt, V, eY, w, cfg, proj, need_V, need_eY, False, xs, need_s)
+        g_s = None
+        if g_upd is not None or g_tv is not None:
+            ws, wt, _ = _tail_weights(layer, s.shape[1])
+            g_upd = g_upd.contiguous() if g_upd is not None else None
+            g_tv = g_tv.contiguous() if g_tv is not None else None
+
+            def through(wm):
+                # (g_upd + g_tv T) wm as g_upd wm + g_tv (T wm): the latent gradient is never formed
+                tw = tenv.weight @ wm
+                if g_upd is None:
+                    return _row_grad(g_tv, tw)
+                out = _row_grad(g_upd, wm)
+                return _row_grad(g_tv, tw, out) if g_tv is not None else out
+
+            g_s = through(ws) if need_s else None
+            cols = through(wt)
+            # the incoming gradient of nt is this Function's to consume (the next layer's backward
+            # made it): its scalar columns take the latent part in place
+            g_nt = g_nt.contiguous() if g_nt is not None else torch.zeros_like(V)
+            g_nt[:, :F] += cols
+        gV, geY, _, g_xe = K.edge_tp_proj_backward(g_nt, V, eY, w, cfg, proj, need_V, need_eY, False, xe,
+                                                   need_s or need_tvp)
+        g_tvp = g_xe * xs if need_tvp else None
         if need_s:
-            g_s = _row_grad(g_xs, ee.weight) if g_s is None else _row_grad(g_xs, ee.weight, g_s)
-        return (g_s, gV.reshape(V.shape) if need_V else None, geY.reshape(eY.shape) if need_eY else None,
+            g_x = g_xe * tvp if tvp is not None else g_xe
+            g_s = _row_grad(g_x, ee.weight) if g_s is None else _row_grad(g_x, ee.weight, g_s)
+        return (g_s, gV.reshape(V.shape) if need_V else None, g_tvp, geY.reshape(eY.shape) if need_eY else None,
                 None, None, None)
 
 
@@ -308,9 +345,9 @@ def _tail_ok(layer, s, nt_dim):
             and not (torch.is_grad_enabled() and any(p.requires_grad for p in params)))
 
 
-def _layer_frozen(layer, s, V, eY):
-    """The whole layer as ``_LayerFrozen`` when every parameter it reads is frozen and the fused
-    product + projection applies; None otherwise."""
+def _layer_chain(layer, s, V, tvp, eY):
+    """(updated, nt, tv) of ``_LayerChain`` when every parameter the layer reads is frozen and the
+    fused product + projection applies; None otherwise."""
     tp, lin, ee = layer.tp, layer.tp_linear, layer.env_embed
     params = [tp.weight, lin.weight, ee.weight] + ([ee.bias] if ee.bias is not None else [])
     if (layer._proj_scale is None or ee.bias is None or not V.is_cuda or V.dtype != torch.float32
@@ -321,7 +358,8 @@ def _layer_frozen(layer, s, V, eY):
     w = tp.weight.reshape(tp.num_paths_full, tp.channels).index_select(0, tp.kept_paths)
     proj = lin.weight.reshape(-1, 16) * (layer._proj_scale * lin.output_scale if lin.output_scale != 1.0
                                          else layer._proj_scale)
-    return _LayerFrozen.apply(s.contiguous(), V.contiguous(), eY.contiguous(), layer, w, proj)
+    return _LayerChain.apply(s.contiguous(), V.contiguous(), tvp.contiguous() if tvp is not None else None,
+                             eY.contiguous(), layer, w, proj)
 
 
 def _layer_tail(layer, s, nt):
@@ -518,24 +556,30 @@ class AllegroLayer(nn.Module):
         self._sh_dim = Irreps(sh_irreps).dim
         self.register_buffer("_proj_scale", _fused_projection_scale(self.tp, self.tp_linear), persistent=False)
 
-    def forward(self, scalar_features, tensor_features, edge_angular, edge_index, n_nodes: int):
-        F = self.num_tensor_features
+    def source_harmonics(self, edge_angular, edge_index, n_nodes: int):
+        """The harmonics of every edge summed onto its source node and normalised (1/sqrt of the
+        constant average neighbour count, or of the node's out-degree), gathered back per edge
+        (allegro.py:436-446); index_select (backward: one index_add) rather than node_Y[src]
+        (sort-based accumulating backward)."""
         src = edge_index[:, 0]
-        node_Y = torch.zeros(n_nodes, self._sh_dim, dtype=tensor_features.dtype, device=tensor_features.device)
-        node_Y = node_Y.index_add(0, src, edge_angular)
+        dt, dev = edge_angular.dtype, edge_angular.device
+        node_Y = torch.zeros(n_nodes, self._sh_dim, dtype=dt, device=dev).index_add(0, src, edge_angular)
         if self.avg_num_neighbors is not None:
             node_Y = node_Y / math.sqrt(self.avg_num_neighbors)
         else:
-            count = torch.zeros(n_nodes, dtype=tensor_features.dtype, device=tensor_features.device)
-            count = count.index_add(0, src, torch.ones_like(src, dtype=tensor_features.dtype))
+            count = torch.zeros(n_nodes, dtype=dt, device=dev).index_add(0, src, torch.ones_like(src, dtype=dt))
             node_Y = node_Y / count.clamp(min=1.0).sqrt().unsqueeze(-1)
+        return node_Y.index_select(0, src)
+
+    def forward(self, scalar_features, tensor_features, edge_angular, edge_index, n_nodes: int):
+        F = self.num_tensor_features
+        edge_node_Y = self.source_harmonics(edge_angular, edge_index, n_nodes)
+        chained = _layer_chain(self, scalar_features, tensor_features, None, edge_node_Y)
+        if chained is not None:
+            upd, nt, tv = chained
+            return upd, _scale_by_channel(nt, tv, self.l_max, F)
         # TP(env_w . V, Y_agg(src)): the per-channel env scaling (allegro.py:447-450) runs inside the
         # product kernel, as TP(s x) = s TP(x) channel by channel
-        # index_select (backward: one index_add) rather than node_Y[src] (sort-based accumulating backward)
-        edge_node_Y = node_Y.index_select(0, src)
-        fused = _layer_frozen(self, scalar_features, tensor_features, edge_node_Y)
-        if fused is not None:
-            return fused
         new_tensor = _product_and_projection(self, tensor_features, edge_node_Y, self.env_embed(scalar_features))
         # a x + b MLP([x, scalar part of the new tensor]) and the output env scaling
         return _layer_tail(self, scalar_features, new_tensor)
@@ -595,8 +639,17 @@ class Allegro(nn.Module):
         scalars, tensors, edge_angular, edge_cutoff = self.embedding(Z, bond_dist, bond_diff, edge_index)
         u = edge_cutoff.unsqueeze(-1)
         per_layer = []
+        tv = None  # the previous layer's output env weights when its scaling was left to this layer
         for layer in self.layers:
-            scalars, tensors = layer(scalars, tensors, edge_angular, edge_index, int(Z.shape[0]))
+            n = int(Z.shape[0])
+            chained = _layer_chain(layer, scalars, tensors, tv, layer.source_harmonics(edge_angular, edge_index, n))
+            if chained is not None:
+                scalars, tensors, tv = chained
+            else:
+                if tv is not None:
+                    tensors = _scale_by_channel(tensors, tv, layer.l_max, layer.num_tensor_features)
+                    tv = None
+                scalars, tensors = layer(scalars, tensors, edge_angular, edge_index, n)
             per_layer.append(_times_envelope(scalars, u))
         return torch.stack(per_layer, dim=1)
 

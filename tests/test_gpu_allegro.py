@@ -230,3 +230,35 @@ def test_allegro_layer_shapes_and_compile():
     compiled = torch.compile(layer, fullgraph=False)
     s3, t3 = compiled(s, t, ang, ei.to(DEV), Z.shape[0])
     assert _rel(s3, s2) <= 1e-6 and _rel(t3, t2) <= 1e-6
+
+
+def test_allegro_layer_called_alone_frozen_matches_module_form():
+    """One AllegroLayer called directly (its reference interface): frozen, it runs the whole-layer
+    Function and forms its tensor output from the returned env weights; outputs and the gradients
+    of scalars, tensor track and harmonics must match the module form (parameters requiring
+    gradients)."""
+    from molnex_amd.molzoo.allegro import AllegroLayer
+
+    pos, Z, ei, rc = _system(seed=6)
+    torch.manual_seed(3)
+    layer = AllegroLayer(num_scalar_features=32, num_tensor_features=16, l_max=2, avg_num_neighbors=10.0).to(DEV)
+    E, n = ei.shape[0], pos.shape[0]
+    g = torch.Generator().manual_seed(7)
+    s0 = torch.randn(E, 32, generator=g).to(DEV)
+    V0 = torch.randn(E, 9 * 16, generator=g).to(DEV)
+    Y0 = torch.randn(E, 9, generator=g).to(DEV)
+    rs = torch.randn(E, 32, generator=g).to(DEV)
+    rv = torch.randn(E, 9 * 16, generator=g).to(DEV)
+
+    def run(frozen):
+        for p in layer.parameters():
+            p.requires_grad_(not frozen)
+        s, V, Y = (t.clone().requires_grad_(True) for t in (s0, V0, Y0))
+        us, uv = layer(s, V, Y, ei.to(DEV), n)
+        grads = torch.autograd.grad((us * rs).sum() + (uv * rv).sum(), (s, V, Y))
+        return us.detach(), uv.detach(), grads
+
+    a = run(True)
+    b = run(False)
+    for x, y in zip(a[:2] + tuple(a[2]), b[:2] + tuple(b[2])):
+        assert _rel(x, y) <= 1e-5, _rel(x, y)

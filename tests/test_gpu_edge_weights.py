@@ -127,3 +127,21 @@ def test_edge_weights_config3_scale_sampled_rows():
     gh = K.edge_weights_backward(gw, W)
     ref = gw[rows].double() @ W.double()
     _check(gh[rows], ref, gw[rows] @ W)
+
+
+@pytest.mark.parametrize("n,k,e", [(64, 64, 1000), (16, 64, 777), (64, 16, 333), (16, 16, 5)])
+def test_edge_weights_backward_accumulating_matches_fp64(n, k, e):
+    """``out += grad @ weight`` in place (molix::edge_weights_backward_acc) against fp64, on an
+    ``out`` that already holds a gradient; the same product as edge_weights_backward, added."""
+    g = torch.Generator(device=DEV).manual_seed(n + k + e)
+    grad = torch.randn(e, n, device=DEV, generator=g)
+    weight = torch.randn(n, k, device=DEV, generator=g) / 4
+    out = torch.randn(e, k, device=DEV, generator=g)
+    ref = out.double() + grad.double() @ weight.double()
+    K.edge_weights_backward_acc(grad, weight, out)
+    err = float((out.double() - ref).norm() / ref.norm())
+    assert err <= 1e-6, err
+    prod = K.edge_weights_backward(grad, weight)
+    assert float((prod.double() - grad.double() @ weight.double()).norm() / (grad.double() @ weight.double()).norm()) <= 1e-6
+    with pytest.raises(ValueError):
+        K.edge_weights_backward_acc(grad, weight, torch.empty(e, k + 1, device=DEV))
