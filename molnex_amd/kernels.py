@@ -1420,19 +1420,24 @@ def _(grad, weight):
 
 @torch.library.custom_op("molix::edge_weights_backward_acc", mutates_args=("out",), device_types="cuda")
 def edge_weights_backward_acc(grad: Tensor, weight: Tensor, out: Tensor) -> None:
-    """``out += grad @ weight`` in place (``out`` a contiguous (E, K) float32 tensor): the
-    input-gradient product of ``edge_weights`` accumulated into an existing gradient in the same
-    pass (``mnx_edge_weights_bwd_cols_f32`` with accumulation), instead of a product and an add."""
+    """``out += grad @ weight`` in place (``out`` a contiguous (E, K) float32 tensor; ``grad`` may
+    be a column block of a wider tensor): the input-gradient product of ``edge_weights``
+    accumulated into an existing result in the same pass (``mnx_edge_weights_bwd_cols_f32`` with
+    accumulation), instead of a product and an add."""
     N, K = weight.shape
     if grad.dim() != 2 or grad.shape[1] != N:
         raise ValueError("edge_weights_backward_acc: grad must be (E, N)")
     if (out.dtype != torch.float32 or out.shape != (grad.shape[0], K) or not out.is_contiguous()
             or out.data_ptr() % 16 != 0):
         raise ValueError("edge_weights_backward_acc: out must be a contiguous, 16-byte aligned float32 (E, K)")
-    g = _aligned16(grad.to(torch.float32))
+    g = grad.to(torch.float32)
+    # rows may be strided (a column block of a wider tensor): unit column stride, a row stride that
+    # is a multiple of 4 floats and 16-byte aligned rows are read in place
+    if not (g.stride(1) == 1 and g.stride(0) >= N and g.stride(0) % 4 == 0 and g.data_ptr() % 16 == 0):
+        g = _aligned16(g)
     frag = _ew_frag(weight, True)
-    check(_lib.load().mnx_edge_weights_bwd_cols_f32(ptr(g), N, None, g.shape[0], N, ptr(frag), K, ptr(out), 1,
-                                                    _stream(g)),
+    check(_lib.load().mnx_edge_weights_bwd_cols_f32(ptr(g), g.stride(0), None, g.shape[0], N, ptr(frag), K,
+                                                    ptr(out), 1, _stream(g)),
           "edge_weights backward (accumulating)")
 
 

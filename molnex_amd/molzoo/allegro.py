@@ -142,7 +142,7 @@ def _row_grad(g, weight, out=None):
             return K.edge_weights_backward(g, weight)
         K.edge_weights_backward_acc(g, weight, out)
         return out
-    return g @ weight if out is None else out.add_(g @ weight)
+    return g @ weight if out is None else out.addmm_(g, weight)
 
 
 def _tail_grads_tracked(layer, s, nt, g_upd, g_out, need_s, need_nt):
@@ -259,8 +259,7 @@ class _LayerChain(torch.autograd.Function):
         xe = xs * tvp if tvp is not None else xs
         nt = K.edge_tp_proj(V, eY, w, layer.tp.config_id, proj, xe)
         ws, wt, bc = _tail_weights(layer, s.shape[1])
-        upd = _row_linear(s, ws, bc)
-        upd.addmm_(nt[:, :F], wt.t())
+        upd = _row_grad(nt[:, :F], wt.t().contiguous(), _row_linear(s, ws, bc))
         tv = torch.addmm(tenv.bias, upd, tenv.weight.t())
         ctx.save_for_backward(s, V, tvp, eY, w, proj, xs, xe)
         ctx.layer = layer
@@ -640,9 +639,13 @@ class Allegro(nn.Module):
         u = edge_cutoff.unsqueeze(-1)
         per_layer = []
         tv = None  # the previous layer's output env weights when its scaling was left to this layer
+        n = int(Z.shape[0])
+        src_Y = {}  # the source harmonics depend on the layer only through its normalisation
         for layer in self.layers:
-            n = int(Z.shape[0])
-            chained = _layer_chain(layer, scalars, tensors, tv, layer.source_harmonics(edge_angular, edge_index, n))
+            key = layer.avg_num_neighbors
+            if key not in src_Y:
+                src_Y[key] = layer.source_harmonics(edge_angular, edge_index, n)
+            chained = _layer_chain(layer, scalars, tensors, tv, src_Y[key])
             if chained is not None:
                 scalars, tensors, tv = chained
             else:
