@@ -207,8 +207,9 @@ size_t mnx_edge_tp_proj_bwd_workspace_bytes(int32_t config, int64_t num_edges) {
     return size_t(etp_proj_bwd_waves(num_edges)) * kETPInfo[config].np * kETPProjChannels * sizeof(float);
 }
 
-int mnx_edge_tp_proj_fwd_f32(int32_t config, const float* x, const float* Y, const float* w, const float* x_scale,
-                             const float* proj, int64_t num_edges, float* out, mnx_stream_t stream) {
+int mnx_edge_tp_proj_fwd_f32(int32_t config, const float* x, int32_t x_shared, const float* Y, const float* w,
+                             const float* x_scale, const float* proj, int64_t num_edges, float* out,
+                             mnx_stream_t stream) {
     clear_error();
     int v = -1;
     int rc = etp_check(config, kETPProjChannels, num_edges, &v);
@@ -216,15 +217,15 @@ int mnx_edge_tp_proj_fwd_f32(int32_t config, const float* x, const float* Y, con
     if (num_edges == 0) return MNX_OK;
     MNX_REQUIRE(x && Y && w && proj && out, "null pointer argument");
     const int64_t waves = etp_proj_waves(num_edges, kETPProjFwdWaves);
-    hipLaunchKernelGGL(kETPFwdP[config], dim3(unsigned(waves / 4)), dim3(kETPThreads), 0, (hipStream_t)stream, x, Y,
-                       w, x_scale, proj, num_edges, out);
+    hipLaunchKernelGGL(kETPFwdP[config][x_shared ? 1 : 0], dim3(unsigned(waves / 4)), dim3(kETPThreads), 0,
+                       (hipStream_t)stream, x, Y, w, x_scale, proj, num_edges, out);
     MNX_CHECK_LAUNCH();
     return MNX_OK;
 }
 
-int mnx_edge_tp_proj_bwd_f32(int32_t config, const float* x, const float* Y, const float* w, const float* x_scale,
-                             const float* proj, const float* grad_out, int64_t num_edges, float* grad_x,
-                             float* grad_Y, float* grad_w, float* grad_x_scale, void* workspace,
+int mnx_edge_tp_proj_bwd_f32(int32_t config, const float* x, int32_t x_shared, const float* Y, const float* w,
+                             const float* x_scale, const float* proj, const float* grad_out, int64_t num_edges,
+                             float* grad_x, float* grad_Y, float* grad_w, float* grad_x_scale, void* workspace,
                              size_t workspace_bytes, mnx_stream_t stream) {
     clear_error();
     int v = -1;
@@ -246,8 +247,8 @@ int mnx_edge_tp_proj_bwd_f32(int32_t config, const float* x, const float* Y, con
     MNX_REQUIRE(workspace && workspace_bytes >= need,
                 "edge tensor product + projection backward: workspace of %zu bytes needed", need);
     float* part = static_cast<float*>(workspace);
-    hipLaunchKernelGGL(kETPBwdP[config], dim3(unsigned(waves / 4)), dim3(kETPThreads), 0, s, grad_out, x, Y, w,
-                       x_scale, proj, num_edges, grad_x, grad_Y, part, grad_x_scale);
+    hipLaunchKernelGGL(kETPBwdP[config][x_shared ? 1 : 0], dim3(unsigned(waves / 4)), dim3(kETPThreads), 0, s,
+                       grad_out, x, Y, w, x_scale, proj, num_edges, grad_x, grad_Y, part, grad_x_scale);
     MNX_CHECK_LAUNCH();
     if (grad_w) {
         hipLaunchKernelGGL(k_etp_reduce, dim3(unsigned(nw)), dim3(kETPReduceThreads), 0, s, part, waves, nw, grad_w);

@@ -309,7 +309,7 @@ def _fwdp(cfg: Cfg) -> str:
     a = L.append
     NX, NY = cfg.NX, cfg.NY
     blocks, ncomp = proj_layout(cfg)
-    a(f"__global__ void __launch_bounds__(256) etp_fwdp_c{cfg.idx}("
+    a(f"template <bool XB>\n__global__ void __launch_bounds__(256) etp_fwdp_c{cfg.idx}("
       "const float* __restrict__ x, const float* __restrict__ Y, const float* __restrict__ w, "
       "const float* __restrict__ xs, const float* __restrict__ wp, int64_t E, float* __restrict__ out) {")
     _stage_proj(a, cfg)
@@ -326,11 +326,17 @@ def _fwdp(cfg: Cfg) -> str:
     a(f"    float y[{NY}];")
     a("#pragma unroll")
     a(f"    for (int i = 0; i < {NY}; ++i) y[i] = Ye[i];")
-    a(f"    const f4* __restrict__ xe = reinterpret_cast<const f4*>(x + es * {NX * 16}) + q;")
     a("    const f4 sc = xs ? *reinterpret_cast<const f4*>(xs + es * 16 + 4 * q) : f4{1.f, 1.f, 1.f, 1.f};")
     a(f"    f4 xv[{NX}];")
+    a("    if constexpr (XB) {  // x[e][i] shared by every channel")
+    a(f"      const float* __restrict__ xe = x + es * {NX};")
     a("#pragma unroll")
-    a(f"    for (int i = 0; i < {NX}; ++i) xv[i] = xe[i * 4] * sc;")
+    a(f"      for (int i = 0; i < {NX}; ++i) xv[i] = xe[i] * sc;")
+    a("    } else {")
+    a(f"      const f4* __restrict__ xe = reinterpret_cast<const f4*>(x + es * {NX * 16}) + q;")
+    a("#pragma unroll")
+    a(f"      for (int i = 0; i < {NX}; ++i) xv[i] = xe[i * 4] * sc;")
+    a("    }")
     for l3, ps, J0, O in blocks:
         M = 2 * l3 + 1
         a("    {")
@@ -399,7 +405,7 @@ def _bwdp(cfg: Cfg) -> str:
     NX, NY, NP = cfg.NX, cfg.NY, cfg.NP
     blocks, ncomp = proj_layout(cfg)
     jidx = {p["k"]: j for j, p in enumerate(cfg.paths)}
-    a(f"__global__ void __launch_bounds__(256) etp_bwdp_c{cfg.idx}("
+    a(f"template <bool XB>\n__global__ void __launch_bounds__(256) etp_bwdp_c{cfg.idx}("
       "const float* __restrict__ gproj, const float* __restrict__ x, const float* __restrict__ Y, "
       "const float* __restrict__ w, const float* __restrict__ xs, const float* __restrict__ wp, int64_t E, "
       "float* __restrict__ gx, float* __restrict__ gY, float* __restrict__ gw_part, float* __restrict__ gxs) {")
@@ -423,12 +429,13 @@ def _bwdp(cfg: Cfg) -> str:
     a(f"    float gYp[{NY}];")
     a("#pragma unroll")
     a(f"    for (int i = 0; i < {NY}; ++i) gYp[i] = 0.f;")
-    a(f"    const float* __restrict__ xe = x + es * ({NX} * int64_t(C)) + c;")
+    a(f"    const float* __restrict__ xe = XB ? x + es * {NX} : x + es * ({NX} * int64_t(C)) + c;")
+    a("    constexpr int XS = XB ? 1 : C;  // stride between x's components (x shared by the channels: 1)")
     a(f"    const float* __restrict__ ge = gproj + es * {ncomp * 16} + c;")
     a("    const float sc = xs ? xs[es * C + c] : 1.f;")
     a(f"    float xr[{NX}], xv[{NX}], gxv[{NX}];  // x as given; xv = sc * xr enters the product")
     a("#pragma unroll")
-    a(f"    for (int i = 0; i < {NX}; ++i) {{ xr[i] = xe[i * C]; xv[i] = xr[i] * sc; gxv[i] = 0.f; }}")
+    a(f"    for (int i = 0; i < {NX}; ++i) {{ xr[i] = xe[i * XS]; xv[i] = xr[i] * sc; gxv[i] = 0.f; }}")
     for l3, ps, J0, O in blocks:
         M, nb = 2 * l3 + 1, len(ps)
         a("    {")
@@ -487,9 +494,27 @@ def _bwdp(cfg: Cfg) -> str:
                 a("        }")
             a("      }")
         a("    }")
-    a(f"    if (gx && valid) {{ float* __restrict__ gxe = gx + es * ({NX} * int64_t(C)) + c;")
+    a("    if constexpr (XB) {  // grad of x shared by the channels: the row's sum over its 16 lanes")
+    a("      if (gx) {")
+    a(f"        float gxr[{NX}];")
     a("#pragma unroll")
-    a(f"      for (int i = 0; i < {NX}; ++i) gxe[i * C] = gxv[i] * sc; }}")
+    a(f"        for (int i = 0; i < {NX}; ++i) {{")
+    a("          float t = gxv[i] * sc;")
+    a("          t += ror16<8>(t);")
+    a("          t += ror16<4>(t);")
+    a("          t += ror16<2>(t);")
+    a("          t += ror16<1>(t);")
+    a("          gxr[i] = t;")
+    a("        }")
+    a(f"        if (valid && c == 0) {{ float* __restrict__ gxe = gx + es * {NX};")
+    a("#pragma unroll")
+    a(f"          for (int i = 0; i < {NX}; ++i) gxe[i] = gxr[i]; }}")
+    a("      }")
+    a("    } else if (gx && valid) {")
+    a(f"      float* __restrict__ gxe = gx + es * ({NX} * int64_t(C)) + c;")
+    a("#pragma unroll")
+    a(f"      for (int i = 0; i < {NX}; ++i) gxe[i * C] = gxv[i] * sc;")
+    a("    }")
     a("    if (gxs && valid) {")
     a("      float t = 0.f;")
     a("#pragma unroll")
@@ -547,10 +572,13 @@ def generate() -> str:
         out.append(f"  {{{int(supported(cfg))}, {cfg.NP}, {cfg.NX}, {cfg.NY}, {cfg.NO}, {fwd_groups(cfg)}}},")
     out.append("};")
     # fused product + projection (16 channels): kernels, projected components, projection blocks
-    out.append("static const ETPFwdPFn kETPFwdP[] = {" + ", ".join(
-        f"etp_fwdp_c{c.idx}" if supported(c) else "nullptr" for c in cfgs) + "};")
-    out.append("static const ETPBwdPFn kETPBwdP[] = {" + ", ".join(
-        f"etp_bwdp_c{c.idx}" if supported(c) else "nullptr" for c in cfgs) + "};")
+    # [config][x shared by the channels]
+    out.append("static const ETPFwdPFn kETPFwdP[][2] = {" + ", ".join(
+        f"{{etp_fwdp_c{c.idx}<false>, etp_fwdp_c{c.idx}<true>}}" if supported(c) else "{nullptr, nullptr}"
+        for c in cfgs) + "};")
+    out.append("static const ETPBwdPFn kETPBwdP[][2] = {" + ", ".join(
+        f"{{etp_bwdp_c{c.idx}<false>, etp_bwdp_c{c.idx}<true>}}" if supported(c) else "{nullptr, nullptr}"
+        for c in cfgs) + "};")
     out.append("static const int kETPProjComps[] = {" + ", ".join(
         str(proj_layout(c)[1]) if supported(c) else "0" for c in cfgs) + "};")
     out.append("static const int kETPProjBlocks[][4 * 4 + 1] = {")

@@ -710,17 +710,18 @@ def _proj_args(x, Y, w, config, proj, x_scale):
         raise ValueError(f"edge_tp_proj: no fused kernel for config {config}")
     num_paths, nx, ny, no = tp_config_info(config)
     E = Y.shape[0]
-    xs = _f32_rows(x, nx * 16, "x")
+    shared = x.dim() == 2 and x.shape[1] == nx  # one value per component for all channels
+    xs = _f32_rows(x, nx if shared else nx * 16, "x")
     Ys = _f32_rows(Y, ny, "Y")
     ws_ = _f32_rows(w, 16, "w")
     pj = _f32_rows(proj, 16, "proj")
     sc = None if x_scale is None else _f32_rows(x_scale, 16, "x_scale")
     if (xs.shape[0] != E or ws_.shape[0] != num_paths or pj.shape[0] != num_paths * 16
             or (sc is not None and sc.shape[0] != E)):
-        raise ValueError("edge_tp_proj: x must be (E, NX*16), w (num_paths, 16), proj (num_paths*16, 16), "
-                         "x_scale (E, 16)")
+        raise ValueError("edge_tp_proj: x must be (E, NX*16) or (E, NX), w (num_paths, 16), "
+                         "proj (num_paths*16, 16), x_scale (E, 16)")
     ni = sum(2 * l + 1 for l, _, _, _ in blocks)
-    return blocks, xs, Ys, ws_, pj, sc, ni
+    return blocks, xs, int(shared), Ys, ws_, pj, sc, ni
 
 
 @torch.library.custom_op("molix::edge_tp_proj", mutates_args=(), device_types="cuda")
@@ -731,13 +732,15 @@ def edge_tp_proj(x: Tensor, Y: Tensor, w: Tensor, config: int, proj: Tensor,
     in one pass that never writes the product's rows: ``out`` (E, NI*16), irreps l = 0..l_max in
     ir_mul.  ``proj`` (num_paths*16, 16) holds the projection's weights by row block
     (``edge_tp_proj_blocks``: the paths of output irrep l are blocks J_l .. J_l + paths - 1, rows
-    J*16 + c for input channel c), scaled as applied."""
+    J*16 + c for input channel c), scaled as applied.  ``x`` may also be (E, NX): one value per
+    component shared by all 16 channels (channel weights then come in through ``x_scale``)."""
     _require_gpu("edge_tp_proj", x, Y, w, proj, x_scale)
-    blocks, xs, Ys, ws_, pj, sc, ni = _proj_args(x, Y, w, config, proj, x_scale)
+    blocks, xs, shared, Ys, ws_, pj, sc, ni = _proj_args(x, Y, w, config, proj, x_scale)
     E = Ys.shape[0]
     out = torch.empty((E, ni * 16), dtype=torch.float32, device=xs.device)
-    check(_lib.load().mnx_edge_tp_proj_fwd_f32(config, ptr(xs), ptr(Ys), ptr(ws_), ptr(sc) if sc is not None else None,
-                                               ptr(pj), E, ptr(out), _stream(xs)),
+    check(_lib.load().mnx_edge_tp_proj_fwd_f32(config, ptr(xs), shared, ptr(Ys), ptr(ws_),
+                                               ptr(sc) if sc is not None else None, ptr(pj), E, ptr(out),
+                                               _stream(xs)),
           "edge_tp_proj")
     return out
 
@@ -756,7 +759,7 @@ def edge_tp_proj_backward(grad_out: Tensor, x: Tensor, Y: Tensor, w: Tensor, con
     needed) in one pass: the projected gradient is taken back through the projection in registers,
     then the product's backward; the weight gradient is summed over edges in a fixed order."""
     lib = _lib.load()
-    blocks, xs, Ys, wss, pj, sc, ni = _proj_args(x, Y, w, config, proj, x_scale)
+    blocks, xs, shared, Ys, wss, pj, sc, ni = _proj_args(x, Y, w, config, proj, x_scale)
     E = Ys.shape[0]
     go = _f32_rows(grad_out, ni * 16, "grad_out")
     gx = torch.empty_like(xs) if need_x else xs.new_empty(0)
@@ -765,8 +768,9 @@ def edge_tp_proj_backward(grad_out: Tensor, x: Tensor, Y: Tensor, w: Tensor, con
     need_scale = bool(need_scale and sc is not None)
     gs = torch.empty_like(sc) if need_scale else xs.new_empty(0)
     ws = _ws(max(int(lib.mnx_edge_tp_proj_bwd_workspace_bytes(config, E)), 1), xs.device)
-    check(lib.mnx_edge_tp_proj_bwd_f32(config, ptr(xs), ptr(Ys), ptr(wss), ptr(sc) if sc is not None else None,
-                                       ptr(pj), ptr(go), E, ptr(gx) if need_x else None,
+    check(lib.mnx_edge_tp_proj_bwd_f32(config, ptr(xs), shared, ptr(Ys), ptr(wss),
+                                       ptr(sc) if sc is not None else None, ptr(pj), ptr(go), E,
+                                       ptr(gx) if need_x else None,
                                        ptr(gY) if need_Y else None, ptr(gw) if need_w else None,
                                        ptr(gs) if need_scale else None, ptr(ws), ws.numel(), _stream(xs)),
           "edge_tp_proj backward")
@@ -778,6 +782,15 @@ def _(grad_out, x, Y, w, config, proj, need_x, need_Y, need_w, x_scale=None, nee
     return (torch.empty_like(x) if need_x else x.new_empty(0), torch.empty_like(Y) if need_Y else Y.new_empty(0),
             torch.empty_like(w) if need_w else w.new_empty(0),
             torch.empty_like(x_scale) if (need_scale and x_scale is not None) else x.new_empty(0))
+
+
+def _expand_shared_x(x: Tensor, config: int) -> Tensor:
+    """x (E, NX) shared by the 16 channels as the (E, NX*16) rows ``molix::edge_tp`` reads (tracked:
+    its gradient is the channel sum); other x unchanged."""
+    nx = tp_config_info(config)[1]
+    if x.dim() == 2 and x.shape[1] == nx:
+        return x.unsqueeze(-1).expand(x.shape[0], nx, 16).reshape(x.shape[0], nx * 16)
+    return x
 
 
 def _etpp_setup(ctx, inputs, output):
@@ -798,9 +811,12 @@ def _etpp_backward(ctx, grad_out):
         # adjoint in tracked ops, then molix::edge_tp's backward (which has second derivatives)
         blocks = edge_tp_proj_blocks(config)
         g_tp = edge_tp_proj_adjoint(grad_out, proj, blocks)
-        gx, gY, gw, gs = edge_tp_backward(g_tp.contiguous(), x, Y, w, config, 16, nx, nY, nw, x_scale, ns)
+        xf = _expand_shared_x(x, config)
+        gx, gY, gw, gs = edge_tp_backward(g_tp.contiguous(), xf, Y, w, config, 16, nx, nY, nw, x_scale, ns)
+        if nx and xf is not x:
+            gx = gx.reshape(x.shape[0], -1, 16).sum(-1)
         if npj:
-            t = edge_tp(x, Y, w, config, 16, x_scale)
+            t = edge_tp(xf, Y, w, config, 16, x_scale)
             E, parts, row = t.shape[0], [], 0
             for l, nb, J, I in blocks:
                 M = 2 * l + 1

@@ -241,7 +241,9 @@ def _tail_grads(layer, s, nt, tv, g_upd, g_out, need_s, need_nt):
 
 class _LayerChain(torch.autograd.Function):
     """A whole layer with frozen parameters and the fused product + projection, its output env
-    scaling left to the next layer: env weights ``x_scale = env_embed(s)`` (times the previous
+    scaling left to the next layer (the first layer's tensor track, harmonics times the embedding's
+    env weights, comes in the same way: V the (E, D) harmonics shared by the channels, tvp the env
+    weights): env weights ``x_scale = env_embed(s)`` (times the previous
     layer's output env weights ``tvp``, which scale the tensor track channel by channel and so fold
     into the product's x_scale: TP(s (t x)) = (s t) TP(x)), ``nt = edge_tp_proj(V, Y_src, w, proj,
     x_scale)``, the tail's ``updated`` and this layer's env weights ``tv = tensor_env(updated)``.
@@ -292,11 +294,14 @@ class _LayerChain(torch.autograd.Function):
                     if need_s:
                         g_s = a * g_lat + g_lat @ (lat.weight[:, :s.shape[1]] * b)
                     cols = g_lat @ (lat.weight[:, s.shape[1]:] * b)
-                    base = g_nt if g_nt is not None else torch.zeros_like(V)
+                    base = g_nt if g_nt is not None else V.new_zeros(V.shape[0], layer.irreps_dim)
                     g_nt = torch.cat([base[:, :F] + cols, base[:, F:]], dim=1)
                 g_tp = K.edge_tp_proj_adjoint(g_nt, proj, K.edge_tp_proj_blocks(cfg))
-                gV, geY, _, g_xe = K.edge_tp_backward(g_tp.contiguous(), V, eY, w, cfg, 16, need_V, need_eY, False,
+                Vf = K._expand_shared_x(V, cfg)
+                gV, geY, _, g_xe = K.edge_tp_backward(g_tp.contiguous(), Vf, eY, w, cfg, 16, need_V, need_eY, False,
                                                       xe_t, need_s or need_tvp)
+                if need_V and Vf is not V:
+                    gV = gV.reshape(V.shape[0], -1, 16).sum(-1)
                 g_tvp = g_xe * xs_t if need_tvp else None
                 if need_s:
                     g_x = (g_xe * tvp if tvp is not None else g_xe) @ ee.weight
@@ -321,7 +326,7 @@ class _LayerChain(torch.autograd.Function):
             cols = through(wt)
             # the incoming gradient of nt is this Function's to consume (the next layer's backward
             # made it): its scalar columns take the latent part in place
-            g_nt = g_nt.contiguous() if g_nt is not None else torch.zeros_like(V)
+            g_nt = g_nt.contiguous() if g_nt is not None else V.new_zeros(V.shape[0], layer.irreps_dim)
             g_nt[:, :F] += cols
         gV, geY, _, g_xe = K.edge_tp_proj_backward(g_nt, V, eY, w, cfg, proj, need_V, need_eY, False, xe,
                                                    need_s or need_tvp)
@@ -473,14 +478,19 @@ class PairEmbedding(nn.Module):
         self.irreps_dim = Irreps(irreps_from_l_max(l_max, num_tensor_features)).dim
         self.tensor_env = nn.Linear(num_scalar_features, num_tensor_features, dtype=config.ftype)
 
-    def forward(self, Z, bond_dist, bond_diff, edge_index):
+    def parts(self, Z, bond_dist, bond_diff, edge_index):
+        """(scalar features, env weights, harmonics, cutoff envelope): the embedding before the
+        tensor track ``harmonics x env weights`` is formed."""
         src, dst = edge_index[:, 0], edge_index[:, 1]
         edge_cutoff = self.cutoff_fn(bond_dist)
         edge_radial = self.radial_basis(bond_dist) * edge_cutoff.unsqueeze(-1)
         edge_angular = self.spherical_harmonics(bond_diff / (bond_dist.unsqueeze(-1) + 1e-8))
         type_embed = _type_pair_embedding(self.type_embedding, Z[src], Z[dst])
         scalar_features = _silu_stack(self.scalar_mlp, torch.cat([edge_radial, type_embed], dim=-1))
-        env_weights = self.tensor_env(scalar_features)
+        return scalar_features, self.tensor_env(scalar_features), edge_angular, edge_cutoff
+
+    def forward(self, Z, bond_dist, bond_diff, edge_index):
+        scalar_features, env_weights, edge_angular, edge_cutoff = self.parts(Z, bond_dist, bond_diff, edge_index)
         tensor_features = _env_weight_harmonics(edge_angular, env_weights, self.l_max, self.num_tensor_features,
                                                 self.irreps_dim)
         return scalar_features, tensor_features, edge_angular, edge_cutoff
@@ -635,10 +645,13 @@ class Allegro(nn.Module):
         ])
 
     def encode(self, Z, bond_dist, bond_diff, edge_index):
-        scalars, tensors, edge_angular, edge_cutoff = self.embedding(Z, bond_dist, bond_diff, edge_index)
+        emb = self.embedding
+        scalars, env0, edge_angular, edge_cutoff = emb.parts(Z, bond_dist, bond_diff, edge_index)
+        # the tensor track enters the first layer as the harmonics shared by the channels with the
+        # env weights as its channel scale (folded into the layer's product), when the layer takes it
+        tensors, tv = edge_angular, env0
         u = edge_cutoff.unsqueeze(-1)
         per_layer = []
-        tv = None  # the previous layer's output env weights when its scaling was left to this layer
         n = int(Z.shape[0])
         src_Y = {}  # the source harmonics depend on the layer only through its normalisation
         for layer in self.layers:
@@ -649,9 +662,12 @@ class Allegro(nn.Module):
             if chained is not None:
                 scalars, tensors, tv = chained
             else:
-                if tv is not None:
+                if tensors is edge_angular:  # first layer: form the tensor track
+                    tensors = _env_weight_harmonics(edge_angular, tv, emb.l_max, emb.num_tensor_features,
+                                                    emb.irreps_dim)
+                elif tv is not None:
                     tensors = _scale_by_channel(tensors, tv, layer.l_max, layer.num_tensor_features)
-                    tv = None
+                tv = None
                 scalars, tensors = layer(scalars, tensors, edge_angular, edge_index, n)
             per_layer.append(_times_envelope(scalars, u))
         return torch.stack(per_layer, dim=1)

@@ -190,3 +190,47 @@ def test_opcheck_edge_tp_proj():
     opcheck(ops.edge_tp_proj_backward.default, (gout, x.detach(), Y.detach(), w.detach(), tp.config_id,
                                                 proj.detach(), True, True, True, s.detach(), True))
     assert math.isfinite(float(gout.sum()))
+
+
+@pytest.mark.parametrize("l_max", [1, 2, 3])
+def test_edge_tp_proj_shared_x_matches_expanded(l_max):
+    """x given as (E, NX), one value per component shared by the 16 channels (the first layer's
+    harmonics, their channel weights in x_scale): forward and every gradient equal the op on the
+    expanded (E, NX*16) rows, x's gradient being the channel sum; also through the tracked form
+    (create_graph)."""
+    layer = _layer(l_max, seed=20 + l_max)
+    tp = layer.tp
+    P, NX, NY, NO = K.tp_config_info(tp.config_id)
+    E = 517
+    g = torch.Generator().manual_seed(30 + l_max)
+    xb = torch.randn(E, NX, generator=g).to(DEV)
+    Y = torch.randn(E, NY, generator=g).to(DEV)
+    s = (torch.rand(E, 16, generator=g) + 0.5).to(DEV)
+    w = tp.weight.detach().reshape(tp.num_paths_full, 16).index_select(0, tp.kept_paths)
+    proj = layer.tp_linear.weight.detach().reshape(-1, 16) * layer._proj_scale
+    R = torch.randn(E, (l_max + 1) ** 2 * 16, generator=g).to(DEV)
+
+    def run(shared, create_graph=False):
+        xa, Ya, sa, wa = (t.clone().requires_grad_(True) for t in (xb, Y, s, w))
+        x = xa if shared else xa.unsqueeze(-1).expand(E, NX, 16).reshape(E, NX * 16)
+        out = K.edge_tp_proj(x, Ya, wa, tp.config_id, proj, sa)
+        gr = torch.autograd.grad((out * R).sum(), (xa, Ya, sa, wa), create_graph=create_graph)
+        return out.detach(), gr
+
+    o1, g1 = run(True)
+    o2, g2 = run(False)
+    assert _rel(o1, o2) <= 1e-6
+    for a, b in zip(g1, g2):
+        assert a.shape == b.shape
+        assert _rel(a, b) <= 1e-5, _rel(a, b)
+    # second order through the tracked form: d<grad_x, v>/dY
+    v = torch.randn(E, NX, generator=g).to(DEV)
+    hs = []
+    for shared in (True, False):
+        xa, Ya = xb.clone().requires_grad_(True), Y.clone().requires_grad_(True)
+        x = xa if shared else xa.unsqueeze(-1).expand(E, NX, 16).reshape(E, NX * 16)
+        out = K.edge_tp_proj(x, Ya, w, tp.config_id, proj, s)
+        (gx,) = torch.autograd.grad((out * R).sum(), xa, create_graph=True)
+        (h,) = torch.autograd.grad((gx * v).sum(), Ya)
+        hs.append(h)
+    assert _rel(hs[0], hs[1]) <= 1e-5, _rel(hs[0], hs[1])
