@@ -547,11 +547,14 @@ __device__ __forceinline__ int opaque_zero() {
     return z;
 }
 
-template <int H, int L, bool BWD>
+// KP: the padded input width the LDS copy is sized for (kRadResKp, or 64 for the backward of
+// stacks up to 64 wide: the pair embedding's 40 inputs); the input gradient is ceil(KP / 32) row
+// tiles.
+template <int H, int L, bool BWD, int KP = kRadResKp>
 constexpr int rad_res_floats() {
     constexpr int T = H / 32;
-    int n = T * (kRadResKp / 8) * 256 + (L - 1) * T * (H / 16) * kX2Block + L * H;  // forward layers, biases
-    if (BWD) n += (H / 16) * kX2Block + (L - 1) * T * (H / 16) * kX2Block;  // backward layer 0 (one tile), 1..L-1
+    int n = T * (KP / 8) * 256 + (L - 1) * T * (H / 16) * kX2Block + L * H;  // forward layers, biases
+    if (BWD) n += ((KP + 31) / 32) * (H / 16) * kX2Block + (L - 1) * T * (H / 16) * kX2Block;  // backward 0, 1..L-1
     return n;
 }
 
@@ -602,13 +605,13 @@ __global__ void __launch_bounds__(kRadThreads) k_radial_fwd_res(const float* __r
     }
 }
 
-template <int H, int L>
+template <int H, int L, int KP>
 __global__ void __launch_bounds__(kRadThreads) k_radial_bwd_res(const float* __restrict__ feats, int64_t E, int kin,
                                                                 const float* __restrict__ frag, RadLayout lay,
                                                                 const float* __restrict__ grad_h,
                                                                 float* __restrict__ grad_feats) {
     constexpr int T = H / 32;
-    __shared__ f32x4 res[rad_res_floats<H, L, true>() / 4];
+    __shared__ f32x4 res[rad_res_floats<H, L, true, KP>() / 4];
     stage(frag, int(lay.fscale_off(1)), res);  // both directions' fragments and the biases, as laid out in frag
     __syncthreads();
     const float* bias = reinterpret_cast<const float*>(res) + lay.bias_off();
@@ -663,9 +666,10 @@ __global__ void __launch_bounds__(kRadThreads) k_radial_bwd_res(const float* __r
 #pragma unroll
                 for (int r = 0; r < 16; ++r) g[t][r] = acc[t][r] * silu_grad(z[j - 1][t][r]);
         }
-        f32x16 a0[1];  // kp <= 16: dL/df^T is one row tile
+        constexpr int T0 = (KP + 31) / 32;  // dL/df^T row tiles (the launch matches them to kp)
+        f32x16 a0[T0];
         zero(a0);
-        mfma_layer_res<1, H / 16>(res + lay.bwd_off(0) / 4, fs + lay.bscale_off(0), g, a0, lane);
+        mfma_layer_res<T0, H / 16>(res + lay.bwd_off(0) / 4, fs + lay.bscale_off(0), g, a0, lane);
         store_grad_feats(a0, grad_feats, e, valid, kin, half);
     }
 }
@@ -705,10 +709,18 @@ void launch_fwd(const float* feats, int64_t E, int kin, const float* frag, RadLa
 template <int H, int L>
 void launch_bwd(const float* feats, int64_t E, int kin, const float* frag, RadLayout lay, const float* gh, float* gf,
                 hipStream_t s) {
-    const int grid = lay.kp <= kRadResKp ? resident_grid(k_radial_bwd_res<H, L>, E) : 0;
-    if (grid > 0)
-        hipLaunchKernelGGL((k_radial_bwd_res<H, L>), dim3(grid), dim3(kRadThreads), 0, s, feats, E, kin, frag, lay, gh,
-                           gf);
+    // resident up to 16 inputs (one input-gradient tile), and for stacks up to 64 wide from 40 to 64
+    // inputs (two tiles: the LDS copy stays within ~130 KB)
+    const bool wide = H <= 64 && lay.kp > 32 && lay.kp <= 64;
+    const int grid = lay.kp <= kRadResKp ? resident_grid(k_radial_bwd_res<H, L, kRadResKp>, E)
+                     : wide             ? resident_grid(k_radial_bwd_res<H, L, (H <= 64 ? 64 : kRadResKp)>, E)
+                                        : 0;
+    if (grid > 0 && !wide)
+        hipLaunchKernelGGL((k_radial_bwd_res<H, L, kRadResKp>), dim3(grid), dim3(kRadThreads), 0, s, feats, E, kin,
+                           frag, lay, gh, gf);
+    else if (grid > 0)
+        hipLaunchKernelGGL((k_radial_bwd_res<H, L, (H <= 64 ? 64 : kRadResKp)>), dim3(grid), dim3(kRadThreads), 0, s,
+                           feats, E, kin, frag, lay, gh, gf);
     else
         hipLaunchKernelGGL((k_radial_bwd<H, L>), dim3(ceil_div(E, kRadEdgesPerBlock)), dim3(kRadThreads), 0, s, feats,
                            E, kin, frag, lay, gh, gf);

@@ -41,7 +41,8 @@ def _ref(feats, Ws, bs):
 @pytest.mark.parametrize("kin,H,L,E", [(8, 64, 2, 1000), (8, 128, 2, 4099), (8, 128, 1, 77), (5, 32, 1, 33),
                                        (13, 64, 3, 31), (64, 32, 4, 100), (8, 64, 4, 257), (40, 64, 1, 64),
                                        (8, 32, 2, 1), (8, 128, 2, 300_007), (16, 64, 2, 200_003),
-                                       (24, 128, 2, 5000)])
+                                       (24, 128, 2, 5000), (40, 64, 3, 5003), (33, 32, 2, 77),
+                                       (56, 64, 2, 20_011)])
 def test_radial_hidden_matches_fp64(kin, H, L, E):
     g = torch.Generator().manual_seed(kin * 1000 + H * 10 + L)
     Ws, bs = _mlp_params(kin, H, L, g)
