@@ -308,7 +308,7 @@ class _LayerChain(torch.autograd.Function):
                     g_s = g_x if g_s is None else g_s + g_x
             return (g_s, gV.reshape(V.shape) if need_V else None, g_tvp, geY.reshape(eY.shape) if need_eY else None,
                     None, None, None)
-        g_s = None
+        ws = None
         if g_upd is not None or g_tv is not None:
             ws, wt, _ = _tail_weights(layer, s.shape[1])
             g_upd = g_upd.contiguous() if g_upd is not None else None
@@ -322,7 +322,6 @@ class _LayerChain(torch.autograd.Function):
                 out = _row_grad(g_upd, wm)
                 return _row_grad(g_tv, tw, out) if g_tv is not None else out
 
-            g_s = through(ws) if need_s else None
             cols = through(wt)
             # the incoming gradient of nt is this Function's to consume (the next layer's backward
             # made it): its scalar columns take the latent part in place
@@ -331,9 +330,18 @@ class _LayerChain(torch.autograd.Function):
         gV, geY, _, g_xe = K.edge_tp_proj_backward(g_nt, V, eY, w, cfg, proj, need_V, need_eY, False, xe,
                                                    need_s or need_tvp)
         g_tvp = g_xe * xs if need_tvp else None
+        g_s = None
         if need_s:
+            # g_s = g_upd W_s + [g_tv | g_x] [T W_s ; W_env]: the two 16-wide gradients in one product
+            # accumulated into the first (one pass over the (E, S) result instead of two)
             g_x = g_xe * tvp if tvp is not None else g_xe
-            g_s = _row_grad(g_x, ee.weight) if g_s is None else _row_grad(g_x, ee.weight, g_s)
+            if g_tv is not None:
+                g_s = _row_grad(torch.cat([g_tv, g_x], dim=1), torch.cat([tenv.weight @ ws, ee.weight], dim=0),
+                                _row_grad(g_upd, ws) if g_upd is not None else None)
+            elif g_upd is not None:
+                g_s = _row_grad(g_x, ee.weight, _row_grad(g_upd, ws))
+            else:
+                g_s = _row_grad(g_x, ee.weight)
         return (g_s, gV.reshape(V.shape) if need_V else None, g_tvp, geY.reshape(eY.shape) if need_eY else None,
                 None, None, None)
 
