@@ -1421,10 +1421,15 @@ def edge_weights_backward(grad: Tensor, weight: Tensor) -> Tensor:
     N, K = weight.shape
     if grad.dim() != 2 or grad.shape[1] != N:
         raise ValueError("edge_weights_backward: grad must be (E, N)")
-    g = _aligned16(grad.to(torch.float32))
+    g = grad.to(torch.float32)
+    # rows may be strided (e.g. one layer's slice of a stacked gradient): read in place when the
+    # row stride is a multiple of 4 floats and the rows are 16-byte aligned
+    if not (g.stride(1) == 1 and g.stride(0) >= N and g.stride(0) % 4 == 0 and g.data_ptr() % 16 == 0):
+        g = _aligned16(g)
     frag = _ew_frag(weight, True)
     gh = g.new_empty(g.shape[0], K)
-    check(_lib.load().mnx_edge_weights_bwd_f32(ptr(g), g.shape[0], N, ptr(frag), K, ptr(gh), _stream(g)),
+    check(_lib.load().mnx_edge_weights_bwd_cols_f32(ptr(g), g.stride(0), None, g.shape[0], N, ptr(frag), K, ptr(gh),
+                                                    0, _stream(g)),
           "edge_weights backward")
     return gh
 

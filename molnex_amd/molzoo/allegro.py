@@ -311,7 +311,8 @@ class _LayerChain(torch.autograd.Function):
         ws = None
         if g_upd is not None or g_tv is not None:
             ws, wt, _ = _tail_weights(layer, s.shape[1])
-            g_upd = g_upd.contiguous() if g_upd is not None else None
+            # g_upd may be a strided slice of the stacked features' gradient: the row kernel reads it
+            # in place
             g_tv = g_tv.contiguous() if g_tv is not None else None
 
             def through(wm):
@@ -677,8 +678,11 @@ class Allegro(nn.Module):
                     tensors = _scale_by_channel(tensors, tv, layer.l_max, layer.num_tensor_features)
                 tv = None
                 scalars, tensors = layer(scalars, tensors, edge_angular, edge_index, n)
-            per_layer.append(_times_envelope(scalars, u))
-        return torch.stack(per_layer, dim=1)
+            per_layer.append(scalars)
+        # every layer's scalars times the cutoff envelope, in one pass over the stacked features (its
+        # backward reads one contiguous gradient; each layer then takes its slice in place)
+        stacked = torch.stack(per_layer, dim=1)
+        return _times_envelope(stacked.reshape(stacked.shape[0], -1), u).reshape(stacked.shape)
 
     def forward(self, td=None, *, Z=None, bond_dist=None, bond_diff=None, edge_index=None):
         if td is None:
