@@ -716,17 +716,20 @@ int mnx_edge_tp_bwd_f32(int32_t config, int32_t channels, const float* x, const 
 /* x_shared != 0: x is [E][NX], one value per component shared by all 16    */
 /* channels (x[e][i][c] = x[e][i], e.g. harmonics whose channel weights come */
 /* in through x_scale), and grad_x [E][NX] is the sum over the channels.     */
+/* x_scale2 [E][16] (or NULL) multiplies x_scale (the scale is their         */
+/* product); grad_x_scale2 is its gradient (either gradient may be NULL).    */
 /* ------------------------------------------------------------------------ */
 int32_t mnx_edge_tp_proj_info(int32_t config, int32_t* blocks);
 size_t mnx_edge_tp_proj_bwd_workspace_bytes(int32_t config, int64_t num_edges);
 int mnx_edge_tp_proj_fwd_f32(int32_t config, const float* x, int32_t x_shared, const float* Y,
-                             const float* w, const float* x_scale, const float* proj,
-                             int64_t num_edges, float* out, mnx_stream_t stream);
+                             const float* w, const float* x_scale, const float* x_scale2,
+                             const float* proj, int64_t num_edges, float* out, mnx_stream_t stream);
 int mnx_edge_tp_proj_bwd_f32(int32_t config, const float* x, int32_t x_shared, const float* Y,
-                             const float* w, const float* x_scale, const float* proj,
-                             const float* grad_out, int64_t num_edges, float* grad_x,
-                             float* grad_Y, float* grad_w, float* grad_x_scale, void* workspace,
-                             size_t workspace_bytes, mnx_stream_t stream);
+                             const float* w, const float* x_scale, const float* x_scale2,
+                             const float* proj, const float* grad_out, int64_t num_edges,
+                             float* grad_x, float* grad_Y, float* grad_w, float* grad_x_scale,
+                             float* grad_x_scale2, void* workspace, size_t workspace_bytes,
+                             mnx_stream_t stream);
 
 /* ------------------------------------------------------------------------ */
 /* Per-channel scaling of an ir_mul edge tensor (Allegro's output env        */

@@ -126,9 +126,9 @@ SIGNATURES = {
     "mnx_edge_tp_bwd_f32": (C.c_int, [c_i32, c_i32, vp, vp, vp, vp, vp, c_i64, vp, vp, vp, vp, vp, c_sz, vp]),
     "mnx_edge_tp_proj_info": (c_i32, [c_i32, vp]),
     "mnx_edge_tp_proj_bwd_workspace_bytes": (c_sz, [c_i32, c_i64]),
-    "mnx_edge_tp_proj_fwd_f32": (C.c_int, [c_i32, vp, c_i32, vp, vp, vp, vp, c_i64, vp, vp]),
-    "mnx_edge_tp_proj_bwd_f32": (C.c_int, [c_i32, vp, c_i32, vp, vp, vp, vp, vp, c_i64, vp, vp, vp, vp, vp, c_sz,
-                                           vp]),
+    "mnx_edge_tp_proj_fwd_f32": (C.c_int, [c_i32, vp, c_i32, vp, vp, vp, vp, vp, c_i64, vp, vp]),
+    "mnx_edge_tp_proj_bwd_f32": (C.c_int, [c_i32, vp, c_i32, vp, vp, vp, vp, vp, vp, c_i64, vp, vp, vp, vp, vp, vp,
+                                           c_sz, vp]),
 }
 
 

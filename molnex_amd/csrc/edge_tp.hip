@@ -33,11 +33,12 @@ struct ETPInfo {
 typedef void (*ETPFwdFn)(const float*, const float*, const float*, const float*, int64_t, int, float*);
 typedef void (*ETPBwdFn)(const float*, const float*, const float*, const float*, const float*, int64_t, int, float*,
                          float*, float*, float*);
-// fused product + projection, 16 channels: (x, Y, w, xs, wp, E, out) and
-// (grad_proj, x, Y, w, xs, wp, E, gx, gY, gw_part, gxs)
-typedef void (*ETPFwdPFn)(const float*, const float*, const float*, const float*, const float*, int64_t, float*);
-typedef void (*ETPBwdPFn)(const float*, const float*, const float*, const float*, const float*, const float*, int64_t,
-                          float*, float*, float*, float*);
+// fused product + projection, 16 channels: (x, Y, w, xs, xs2, wp, E, out) and
+// (grad_proj, x, Y, w, xs, xs2, wp, E, gx, gY, gw_part, gxs, gxs2)
+typedef void (*ETPFwdPFn)(const float*, const float*, const float*, const float*, const float*, const float*,
+                          int64_t, float*);
+typedef void (*ETPBwdPFn)(const float*, const float*, const float*, const float*, const float*, const float*,
+                          const float*, int64_t, float*, float*, float*, float*, float*);
 
 typedef float f4 __attribute__((ext_vector_type(4)));  // one matrix-core accumulator / operand quad
 
@@ -208,8 +209,8 @@ size_t mnx_edge_tp_proj_bwd_workspace_bytes(int32_t config, int64_t num_edges) {
 }
 
 int mnx_edge_tp_proj_fwd_f32(int32_t config, const float* x, int32_t x_shared, const float* Y, const float* w,
-                             const float* x_scale, const float* proj, int64_t num_edges, float* out,
-                             mnx_stream_t stream) {
+                             const float* x_scale, const float* x_scale2, const float* proj, int64_t num_edges,
+                             float* out, mnx_stream_t stream) {
     clear_error();
     int v = -1;
     int rc = etp_check(config, kETPProjChannels, num_edges, &v);
@@ -218,15 +219,15 @@ int mnx_edge_tp_proj_fwd_f32(int32_t config, const float* x, int32_t x_shared, c
     MNX_REQUIRE(x && Y && w && proj && out, "null pointer argument");
     const int64_t waves = etp_proj_waves(num_edges, kETPProjFwdWaves);
     hipLaunchKernelGGL(kETPFwdP[config][x_shared ? 1 : 0], dim3(unsigned(waves / 4)), dim3(kETPThreads), 0,
-                       (hipStream_t)stream, x, Y, w, x_scale, proj, num_edges, out);
+                       (hipStream_t)stream, x, Y, w, x_scale, x_scale2, proj, num_edges, out);
     MNX_CHECK_LAUNCH();
     return MNX_OK;
 }
 
 int mnx_edge_tp_proj_bwd_f32(int32_t config, const float* x, int32_t x_shared, const float* Y, const float* w,
-                             const float* x_scale, const float* proj, const float* grad_out, int64_t num_edges,
-                             float* grad_x, float* grad_Y, float* grad_w, float* grad_x_scale, void* workspace,
-                             size_t workspace_bytes, mnx_stream_t stream) {
+                             const float* x_scale, const float* x_scale2, const float* proj, const float* grad_out,
+                             int64_t num_edges, float* grad_x, float* grad_Y, float* grad_w, float* grad_x_scale,
+                             float* grad_x_scale2, void* workspace, size_t workspace_bytes, mnx_stream_t stream) {
     clear_error();
     int v = -1;
     int rc = etp_check(config, kETPProjChannels, num_edges, &v);
@@ -248,7 +249,8 @@ int mnx_edge_tp_proj_bwd_f32(int32_t config, const float* x, int32_t x_shared, c
                 "edge tensor product + projection backward: workspace of %zu bytes needed", need);
     float* part = static_cast<float*>(workspace);
     hipLaunchKernelGGL(kETPBwdP[config][x_shared ? 1 : 0], dim3(unsigned(waves / 4)), dim3(kETPThreads), 0, s,
-                       grad_out, x, Y, w, x_scale, proj, num_edges, grad_x, grad_Y, part, grad_x_scale);
+                       grad_out, x, Y, w, x_scale, x_scale2, proj, num_edges, grad_x, grad_Y, part, grad_x_scale,
+                       grad_x_scale2);
     MNX_CHECK_LAUNCH();
     if (grad_w) {
         hipLaunchKernelGGL(k_etp_reduce, dim3(unsigned(nw)), dim3(kETPReduceThreads), 0, s, part, waves, nw, grad_w);

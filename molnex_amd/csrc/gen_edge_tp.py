@@ -311,7 +311,8 @@ def _fwdp(cfg: Cfg) -> str:
     blocks, ncomp = proj_layout(cfg)
     a(f"template <bool XB>\n__global__ void __launch_bounds__(256) etp_fwdp_c{cfg.idx}("
       "const float* __restrict__ x, const float* __restrict__ Y, const float* __restrict__ w, "
-      "const float* __restrict__ xs, const float* __restrict__ wp, int64_t E, float* __restrict__ out) {")
+      "const float* __restrict__ xs, const float* __restrict__ xs2, const float* __restrict__ wp, int64_t E, "
+      "float* __restrict__ out) {")
     _stage_proj(a, cfg)
     a("  __syncthreads();")
     a("  const int lane = threadIdx.x & 63, r = lane & 15, q = lane >> 4;")
@@ -326,7 +327,8 @@ def _fwdp(cfg: Cfg) -> str:
     a(f"    float y[{NY}];")
     a("#pragma unroll")
     a(f"    for (int i = 0; i < {NY}; ++i) y[i] = Ye[i];")
-    a("    const f4 sc = xs ? *reinterpret_cast<const f4*>(xs + es * 16 + 4 * q) : f4{1.f, 1.f, 1.f, 1.f};")
+    a("    f4 sc = xs ? *reinterpret_cast<const f4*>(xs + es * 16 + 4 * q) : f4{1.f, 1.f, 1.f, 1.f};")
+    a("    if (xs2) sc *= *reinterpret_cast<const f4*>(xs2 + es * 16 + 4 * q);  // a second channel scale")
     a(f"    f4 xv[{NX}];")
     a("    if constexpr (XB) {  // x[e][i] shared by every channel")
     a(f"      const float* __restrict__ xe = x + es * {NX};")
@@ -407,8 +409,9 @@ def _bwdp(cfg: Cfg) -> str:
     jidx = {p["k"]: j for j, p in enumerate(cfg.paths)}
     a(f"template <bool XB>\n__global__ void __launch_bounds__(256) etp_bwdp_c{cfg.idx}("
       "const float* __restrict__ gproj, const float* __restrict__ x, const float* __restrict__ Y, "
-      "const float* __restrict__ w, const float* __restrict__ xs, const float* __restrict__ wp, int64_t E, "
-      "float* __restrict__ gx, float* __restrict__ gY, float* __restrict__ gw_part, float* __restrict__ gxs) {")
+      "const float* __restrict__ w, const float* __restrict__ xs, const float* __restrict__ xs2, "
+      "const float* __restrict__ wp, int64_t E, float* __restrict__ gx, float* __restrict__ gY, "
+      "float* __restrict__ gw_part, float* __restrict__ gxs, float* __restrict__ gxs2) {")
     _stage_proj_rot(a, cfg)
     a("  constexpr int G = 4, C = 16;")
     a("  const int lane = threadIdx.x & 63, c = lane & 15;")
@@ -432,7 +435,7 @@ def _bwdp(cfg: Cfg) -> str:
     a(f"    const float* __restrict__ xe = XB ? x + es * {NX} : x + es * ({NX} * int64_t(C)) + c;")
     a("    constexpr int XS = XB ? 1 : C;  // stride between x's components (x shared by the channels: 1)")
     a(f"    const float* __restrict__ ge = gproj + es * {ncomp * 16} + c;")
-    a("    const float sc = xs ? xs[es * C + c] : 1.f;")
+    a("    const float s1 = xs ? xs[es * C + c] : 1.f, s2 = xs2 ? xs2[es * C + c] : 1.f, sc = s1 * s2;")
     a(f"    float xr[{NX}], xv[{NX}], gxv[{NX}];  // x as given; xv = sc * xr enters the product")
     a("#pragma unroll")
     a(f"    for (int i = 0; i < {NX}; ++i) {{ xr[i] = xe[i * XS]; xv[i] = xr[i] * sc; gxv[i] = 0.f; }}")
@@ -515,11 +518,12 @@ def _bwdp(cfg: Cfg) -> str:
     a("#pragma unroll")
     a(f"      for (int i = 0; i < {NX}; ++i) gxe[i * C] = gxv[i] * sc;")
     a("    }")
-    a("    if (gxs && valid) {")
-    a("      float t = 0.f;")
+    a("    if ((gxs || gxs2) && valid) {")
+    a("      float t = 0.f;  // the gradient of the combined scale s1 s2")
     a("#pragma unroll")
     a(f"      for (int i = 0; i < {NX}; ++i) t = fmaf(gxv[i], xr[i], t);")
-    a("      gxs[es * C + c] = t;")
+    a("      if (gxs) gxs[es * C + c] = t * s2;")
+    a("      if (gxs2) gxs2[es * C + c] = t * s1;")
     a("    }")
     a("    if (gY) {")
     a("#pragma unroll")

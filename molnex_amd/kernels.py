@@ -704,7 +704,7 @@ def edge_tp_project(t: Tensor, proj: Tensor, blocks) -> Tensor:
     return torch.cat(parts, dim=1)
 
 
-def _proj_args(x, Y, w, config, proj, x_scale):
+def _proj_args(x, Y, w, config, proj, x_scale, x_scale2=None):
     blocks = edge_tp_proj_blocks(config)
     if not blocks:
         raise ValueError(f"edge_tp_proj: no fused kernel for config {config}")
@@ -716,37 +716,41 @@ def _proj_args(x, Y, w, config, proj, x_scale):
     ws_ = _f32_rows(w, 16, "w")
     pj = _f32_rows(proj, 16, "proj")
     sc = None if x_scale is None else _f32_rows(x_scale, 16, "x_scale")
+    sc2 = None if x_scale2 is None else _f32_rows(x_scale2, 16, "x_scale2")
     if (xs.shape[0] != E or ws_.shape[0] != num_paths or pj.shape[0] != num_paths * 16
-            or (sc is not None and sc.shape[0] != E)):
+            or (sc is not None and sc.shape[0] != E) or (sc2 is not None and sc2.shape[0] != E)):
         raise ValueError("edge_tp_proj: x must be (E, NX*16) or (E, NX), w (num_paths, 16), "
-                         "proj (num_paths*16, 16), x_scale (E, 16)")
+                         "proj (num_paths*16, 16), x_scale and x_scale2 (E, 16)")
     ni = sum(2 * l + 1 for l, _, _, _ in blocks)
-    return blocks, xs, int(shared), Ys, ws_, pj, sc, ni
+    return blocks, xs, int(shared), Ys, ws_, pj, sc, sc2, ni
 
 
 @torch.library.custom_op("molix::edge_tp_proj", mutates_args=(), device_types="cuda")
 def edge_tp_proj(x: Tensor, Y: Tensor, w: Tensor, config: int, proj: Tensor,
-                 x_scale: Tensor | None = None) -> Tensor:
+                 x_scale: Tensor | None = None, x_scale2: Tensor | None = None) -> Tensor:
     """``molix::edge_tp`` with 16 channels followed by the projection back to the input irreps
     (src/molzoo/allegro.py:363-367,465-466: cuet.Linear(tp.irreps_out, irreps_in) on the product),
     in one pass that never writes the product's rows: ``out`` (E, NI*16), irreps l = 0..l_max in
     ir_mul.  ``proj`` (num_paths*16, 16) holds the projection's weights by row block
     (``edge_tp_proj_blocks``: the paths of output irrep l are blocks J_l .. J_l + paths - 1, rows
     J*16 + c for input channel c), scaled as applied.  ``x`` may also be (E, NX): one value per
-    component shared by all 16 channels (channel weights then come in through ``x_scale``)."""
-    _require_gpu("edge_tp_proj", x, Y, w, proj, x_scale)
-    blocks, xs, shared, Ys, ws_, pj, sc, ni = _proj_args(x, Y, w, config, proj, x_scale)
+    component shared by all 16 channels (channel weights then come in through ``x_scale``).  An
+    optional ``x_scale2`` (E, 16) multiplies ``x_scale`` (the scale is their product, formed in the
+    kernel)."""
+    _require_gpu("edge_tp_proj", x, Y, w, proj, x_scale, x_scale2)
+    blocks, xs, shared, Ys, ws_, pj, sc, sc2, ni = _proj_args(x, Y, w, config, proj, x_scale, x_scale2)
     E = Ys.shape[0]
     out = torch.empty((E, ni * 16), dtype=torch.float32, device=xs.device)
     check(_lib.load().mnx_edge_tp_proj_fwd_f32(config, ptr(xs), shared, ptr(Ys), ptr(ws_),
-                                               ptr(sc) if sc is not None else None, ptr(pj), E, ptr(out),
+                                               ptr(sc) if sc is not None else None,
+                                               ptr(sc2) if sc2 is not None else None, ptr(pj), E, ptr(out),
                                                _stream(xs)),
           "edge_tp_proj")
     return out
 
 
 @edge_tp_proj.register_fake
-def _(x, Y, w, config, proj, x_scale=None):
+def _(x, Y, w, config, proj, x_scale=None, x_scale2=None):
     ni = sum(2 * l + 1 for l, _, _, _ in edge_tp_proj_blocks(config))
     return x.new_empty((Y.shape[0], ni * 16))
 
@@ -754,12 +758,14 @@ def _(x, Y, w, config, proj, x_scale=None):
 @torch.library.custom_op("molix::edge_tp_proj_backward", mutates_args=(), device_types="cuda")
 def edge_tp_proj_backward(grad_out: Tensor, x: Tensor, Y: Tensor, w: Tensor, config: int, proj: Tensor,
                           need_x: bool, need_Y: bool, need_w: bool, x_scale: Tensor | None = None,
-                          need_scale: bool = False) -> tuple[Tensor, Tensor, Tensor, Tensor]:
-    """Gradients of ``<grad_out, edge_tp_proj(...)>`` w.r.t. x, Y, w and x_scale (empty when not
-    needed) in one pass: the projected gradient is taken back through the projection in registers,
-    then the product's backward; the weight gradient is summed over edges in a fixed order."""
+                          need_scale: bool = False, x_scale2: Tensor | None = None,
+                          need_scale2: bool = False) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
+    """Gradients of ``<grad_out, edge_tp_proj(...)>`` w.r.t. x, Y, w, x_scale and x_scale2 (empty
+    when not needed) in one pass: the projected gradient is taken back through the projection in
+    registers, then the product's backward; the weight gradient is summed over edges in a fixed
+    order."""
     lib = _lib.load()
-    blocks, xs, shared, Ys, wss, pj, sc, ni = _proj_args(x, Y, w, config, proj, x_scale)
+    blocks, xs, shared, Ys, wss, pj, sc, sc2, ni = _proj_args(x, Y, w, config, proj, x_scale, x_scale2)
     E = Ys.shape[0]
     go = _f32_rows(grad_out, ni * 16, "grad_out")
     gx = torch.empty_like(xs) if need_x else xs.new_empty(0)
@@ -767,21 +773,26 @@ def edge_tp_proj_backward(grad_out: Tensor, x: Tensor, Y: Tensor, w: Tensor, con
     gw = torch.empty_like(wss) if need_w else wss.new_empty(0)
     need_scale = bool(need_scale and sc is not None)
     gs = torch.empty_like(sc) if need_scale else xs.new_empty(0)
+    need_scale2 = bool(need_scale2 and sc2 is not None)
+    gs2 = torch.empty_like(sc2) if need_scale2 else xs.new_empty(0)
     ws = _ws(max(int(lib.mnx_edge_tp_proj_bwd_workspace_bytes(config, E)), 1), xs.device)
     check(lib.mnx_edge_tp_proj_bwd_f32(config, ptr(xs), shared, ptr(Ys), ptr(wss),
-                                       ptr(sc) if sc is not None else None, ptr(pj), ptr(go), E,
-                                       ptr(gx) if need_x else None,
+                                       ptr(sc) if sc is not None else None, ptr(sc2) if sc2 is not None else None,
+                                       ptr(pj), ptr(go), E, ptr(gx) if need_x else None,
                                        ptr(gY) if need_Y else None, ptr(gw) if need_w else None,
-                                       ptr(gs) if need_scale else None, ptr(ws), ws.numel(), _stream(xs)),
+                                       ptr(gs) if need_scale else None, ptr(gs2) if need_scale2 else None,
+                                       ptr(ws), ws.numel(), _stream(xs)),
           "edge_tp_proj backward")
-    return gx, gY, gw, gs
+    return gx, gY, gw, gs, gs2
 
 
 @edge_tp_proj_backward.register_fake
-def _(grad_out, x, Y, w, config, proj, need_x, need_Y, need_w, x_scale=None, need_scale=False):
+def _(grad_out, x, Y, w, config, proj, need_x, need_Y, need_w, x_scale=None, need_scale=False, x_scale2=None,
+      need_scale2=False):
     return (torch.empty_like(x) if need_x else x.new_empty(0), torch.empty_like(Y) if need_Y else Y.new_empty(0),
             torch.empty_like(w) if need_w else w.new_empty(0),
-            torch.empty_like(x_scale) if (need_scale and x_scale is not None) else x.new_empty(0))
+            torch.empty_like(x_scale) if (need_scale and x_scale is not None) else x.new_empty(0),
+            torch.empty_like(x_scale2) if (need_scale2 and x_scale2 is not None) else x.new_empty(0))
 
 
 def _expand_shared_x(x: Tensor, config: int) -> Tensor:
@@ -794,29 +805,35 @@ def _expand_shared_x(x: Tensor, config: int) -> Tensor:
 
 
 def _etpp_setup(ctx, inputs, output):
-    x, Y, w, config, proj, x_scale = inputs
-    ctx.save_for_backward(x, Y, w, proj, x_scale)
+    x, Y, w, config, proj, x_scale, x_scale2 = inputs
+    ctx.save_for_backward(x, Y, w, proj, x_scale, x_scale2)
     ctx.config = config
 
 
 def _etpp_backward(ctx, grad_out):
-    x, Y, w, proj, x_scale = ctx.saved_tensors
+    x, Y, w, proj, x_scale, x_scale2 = ctx.saved_tensors
     config = ctx.config
     nx, nY, nw = ctx.needs_input_grad[:3]
     npj = ctx.needs_input_grad[4]
     ns = x_scale is not None and ctx.needs_input_grad[5]
-    gp = None
+    ns2 = x_scale2 is not None and ctx.needs_input_grad[6]
+    gp = gs2 = None
     if npj or torch.is_grad_enabled():
         # the projection's weight gradient, or differentiated again (create_graph): the projection's
         # adjoint in tracked ops, then molix::edge_tp's backward (which has second derivatives)
         blocks = edge_tp_proj_blocks(config)
         g_tp = edge_tp_proj_adjoint(grad_out, proj, blocks)
         xf = _expand_shared_x(x, config)
-        gx, gY, gw, gs = edge_tp_backward(g_tp.contiguous(), xf, Y, w, config, 16, nx, nY, nw, x_scale, ns)
+        sc = x_scale if x_scale2 is None else (x_scale2 if x_scale is None else x_scale * x_scale2)
+        gx, gY, gw, gsc = edge_tp_backward(g_tp.contiguous(), xf, Y, w, config, 16, nx, nY, nw, sc,
+                                           sc is not None and (ns or ns2))
+        gs = gsc * x_scale2 if (ns and x_scale2 is not None) else gsc
+        if ns2:
+            gs2 = gsc * x_scale if x_scale is not None else gsc
         if nx and xf is not x:
             gx = gx.reshape(x.shape[0], -1, 16).sum(-1)
         if npj:
-            t = edge_tp(xf, Y, w, config, 16, x_scale)
+            t = edge_tp(xf, Y, w, config, 16, sc)
             E, parts, row = t.shape[0], [], 0
             for l, nb, J, I in blocks:
                 M = 2 * l + 1
@@ -825,9 +842,11 @@ def _etpp_backward(ctx, grad_out):
                 row += M * nb
             gp = torch.cat(parts, dim=0).reshape(proj.shape)
     else:
-        gx, gY, gw, gs = edge_tp_proj_backward(grad_out.contiguous(), x, Y, w, config, proj, nx, nY, nw, x_scale, ns)
+        gx, gY, gw, gs, gs2 = edge_tp_proj_backward(grad_out.contiguous(), x, Y, w, config, proj, nx, nY, nw,
+                                                    x_scale, ns, x_scale2, ns2)
     return (gx.reshape(x.shape) if nx else None, gY.reshape(Y.shape) if nY else None,
-            gw.reshape(w.shape) if nw else None, None, gp, gs.reshape(x_scale.shape) if ns else None)
+            gw.reshape(w.shape) if nw else None, None, gp, gs.reshape(x_scale.shape) if ns else None,
+            gs2.reshape(x_scale2.shape) if ns2 else None)
 
 
 edge_tp_proj.register_autograd(_etpp_backward, setup_context=_etpp_setup)

@@ -258,19 +258,18 @@ class _LayerChain(torch.autograd.Function):
     def forward(ctx, s, V, tvp, eY, layer, w, proj):
         ee, tenv, F = layer.env_embed, layer.tensor_env, layer.num_tensor_features
         xs = _row_linear(s, ee.weight, ee.bias)
-        xe = xs * tvp if tvp is not None else xs
-        nt = K.edge_tp_proj(V, eY, w, layer.tp.config_id, proj, xe)
+        nt = K.edge_tp_proj(V, eY, w, layer.tp.config_id, proj, xs, tvp)  # the product scales by xs tvp
         ws, wt, bc = _tail_weights(layer, s.shape[1])
         upd = _row_grad(nt[:, :F], wt.t().contiguous(), _row_linear(s, ws, bc))
         tv = torch.addmm(tenv.bias, upd, tenv.weight.t())
-        ctx.save_for_backward(s, V, tvp, eY, w, proj, xs, xe)
+        ctx.save_for_backward(s, V, tvp, eY, w, proj, xs)
         ctx.layer = layer
         ctx.set_materialize_grads(False)
         return upd, nt, tv
 
     @staticmethod
     def backward(ctx, g_upd, g_nt, g_tv):
-        s, V, tvp, eY, w, proj, xs, xe = ctx.saved_tensors
+        s, V, tvp, eY, w, proj, xs = ctx.saved_tensors
         layer = ctx.layer
         ee, tenv, cfg = layer.env_embed, layer.tensor_env, layer.tp.config_id
         a, b, F = layer.residual_a, layer.residual_b, layer.num_tensor_features
@@ -328,14 +327,13 @@ class _LayerChain(torch.autograd.Function):
             # made it): its scalar columns take the latent part in place
             g_nt = g_nt.contiguous() if g_nt is not None else V.new_zeros(V.shape[0], layer.irreps_dim)
             g_nt[:, :F] += cols
-        gV, geY, _, g_xe = K.edge_tp_proj_backward(g_nt, V, eY, w, cfg, proj, need_V, need_eY, False, xe,
-                                                   need_s or need_tvp)
-        g_tvp = g_xe * xs if need_tvp else None
+        gV, geY, _, g_x, g_tvp = K.edge_tp_proj_backward(g_nt, V, eY, w, cfg, proj, need_V, need_eY, False, xs,
+                                                         need_s, tvp, need_tvp)
+        g_tvp = g_tvp if need_tvp else None
         g_s = None
         if need_s:
             # g_s = g_upd W_s + [g_tv | g_x] [T W_s ; W_env]: the two 16-wide gradients in one product
             # accumulated into the first (one pass over the (E, S) result instead of two)
-            g_x = g_xe * tvp if tvp is not None else g_xe
             if g_tv is not None:
                 g_s = _row_grad(torch.cat([g_tv, g_x], dim=1), torch.cat([tenv.weight @ ws, ee.weight], dim=0),
                                 _row_grad(g_upd, ws) if g_upd is not None else None)

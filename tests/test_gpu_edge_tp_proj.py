@@ -153,8 +153,8 @@ def test_edge_tp_proj_no_edges_and_reproducible_weight_gradient():
     ni = sum(2 * l + 1 for l, _, _, _ in K.edge_tp_proj_blocks(tp.config_id))
     x0, Y0 = torch.zeros(0, NX * 16, device=DEV), torch.zeros(0, NY, device=DEV)
     assert K.edge_tp_proj(x0, Y0, w, tp.config_id, proj).shape == (0, ni * 16)
-    _, _, gw, _ = K.edge_tp_proj_backward(torch.zeros(0, ni * 16, device=DEV), x0, Y0, w, tp.config_id, proj,
-                                          False, False, True)
+    _, _, gw, _, _ = K.edge_tp_proj_backward(torch.zeros(0, ni * 16, device=DEV), x0, Y0, w, tp.config_id, proj,
+                                             False, False, True)
     assert gw.shape == w.shape and not gw.any()
     g = torch.Generator(device=DEV).manual_seed(4)
     E = 200_003
@@ -189,6 +189,11 @@ def test_opcheck_edge_tp_proj():
     gout = torch.randn(E, ni * 16, device=DEV, generator=g)
     opcheck(ops.edge_tp_proj_backward.default, (gout, x.detach(), Y.detach(), w.detach(), tp.config_id,
                                                 proj.detach(), True, True, True, s.detach(), True))
+    s2 = (torch.rand(E, 16, device=DEV, generator=g) + 0.5).requires_grad_(True)
+    opcheck(ops.edge_tp_proj.default, (x, Y, w, tp.config_id, proj.detach(), s, s2))
+    opcheck(ops.edge_tp_proj_backward.default, (gout, x.detach(), Y.detach(), w.detach(), tp.config_id,
+                                                proj.detach(), True, True, True, s.detach(), True, s2.detach(),
+                                                True))
     assert math.isfinite(float(gout.sum()))
 
 
@@ -234,3 +239,31 @@ def test_edge_tp_proj_shared_x_matches_expanded(l_max):
         (h,) = torch.autograd.grad((gx * v).sum(), Ya)
         hs.append(h)
     assert _rel(hs[0], hs[1]) <= 1e-5, _rel(hs[0], hs[1])
+
+
+def test_edge_tp_proj_two_channel_scales_match_their_product():
+    """x_scale2 multiplies x_scale inside the kernels: forward and every gradient (both scales'
+    included) equal the op with the product as its one scale, first order and through the tracked
+    form (create_graph)."""
+    layer = _layer(2, seed=12)
+    tp = layer.tp
+    P, NX, NY, NO = K.tp_config_info(tp.config_id)
+    E = 733
+    g = torch.Generator().manual_seed(13)
+    x = torch.randn(E, NX * 16, generator=g).to(DEV)
+    Y = torch.randn(E, NY, generator=g).to(DEV)
+    s1 = (torch.rand(E, 16, generator=g) + 0.5).to(DEV)
+    s2 = (torch.rand(E, 16, generator=g) + 0.5).to(DEV)
+    w = tp.weight.detach().reshape(tp.num_paths_full, 16).index_select(0, tp.kept_paths)
+    proj = layer.tp_linear.weight.detach().reshape(-1, 16) * layer._proj_scale
+    R = torch.randn(E, 9 * 16, generator=g).to(DEV)
+    for create_graph in (False, True):
+        xa, Ya, a1, a2 = (t.clone().requires_grad_(True) for t in (x, Y, s1, s2))
+        out2 = K.edge_tp_proj(xa, Ya, w, tp.config_id, proj, a1, a2)
+        g2 = torch.autograd.grad((out2 * R).sum(), (xa, Ya, a1, a2), create_graph=create_graph)
+        xb, Yb, b1, b2 = (t.clone().requires_grad_(True) for t in (x, Y, s1, s2))
+        out1 = K.edge_tp_proj(xb, Yb, w, tp.config_id, proj, b1 * b2)
+        g1 = torch.autograd.grad((out1 * R).sum(), (xb, Yb, b1, b2), create_graph=create_graph)
+        assert _rel(out2, out1) <= 1e-6
+        for a, b in zip(g2, g1):
+            assert _rel(a, b) <= 1e-5, _rel(a, b)
