@@ -252,37 +252,43 @@ class _LayerChain(torch.autograd.Function):
     into the scalars' gradient in the same pass and the latent gradient is never formed.
     Differentiated again (create_graph), the backward runs the same formulas in tracked ops (the
     tail is linear in its inputs; the product's backward is ``molix::edge_tp``'s, which has second
-    derivatives)."""
+    derivatives).  With ``tvp_lin`` (the embedding's frozen env layer, for the first layer) the
+    env weights ``tvp = tvp_lin(s)`` of the same scalars are formed here, and their input gradient
+    joins the scalars' gradient in the same accumulating product."""
 
     @staticmethod
-    def forward(ctx, s, V, tvp, eY, layer, w, proj):
+    def forward(ctx, s, V, tvp, eY, layer, w, proj, tvp_lin=None):
         ee, tenv, F = layer.env_embed, layer.tensor_env, layer.num_tensor_features
+        if tvp_lin is not None:
+            tvp = torch.addmm(tvp_lin.bias, s, tvp_lin.weight.t())
         xs = _row_linear(s, ee.weight, ee.bias)
         nt = K.edge_tp_proj(V, eY, w, layer.tp.config_id, proj, xs, tvp)  # the product scales by xs tvp
         ws, wt, bc = _tail_weights(layer, s.shape[1])
         upd = _row_grad(nt[:, :F], wt.t().contiguous(), _row_linear(s, ws, bc))
         tv = torch.addmm(tenv.bias, upd, tenv.weight.t())
         ctx.save_for_backward(s, V, tvp, eY, w, proj, xs)
-        ctx.layer = layer
+        ctx.layer, ctx.tvp_lin = layer, tvp_lin
         ctx.set_materialize_grads(False)
         return upd, nt, tv
 
     @staticmethod
     def backward(ctx, g_upd, g_nt, g_tv):
         s, V, tvp, eY, w, proj, xs = ctx.saved_tensors
-        layer = ctx.layer
+        layer, tl = ctx.layer, ctx.tvp_lin
         ee, tenv, cfg = layer.env_embed, layer.tensor_env, layer.tp.config_id
         a, b, F = layer.residual_a, layer.residual_b, layer.num_tensor_features
         need_s, need_V, need_tvp, need_eY = ctx.needs_input_grad[:4]
-        need_tvp = need_tvp and tvp is not None
-        nout = 7
+        need_tvp = need_tvp and tvp is not None and tl is None
+        inner = tl is not None and need_s  # tvp formed here from s: its gradient joins g_s
+        nout = 8
         if g_upd is None and g_nt is None and g_tv is None:
             return (None,) * nout
         if torch.is_grad_enabled():
             lat = layer.latent_mlp[0]
             with torch.enable_grad():
                 xs_t = nn.functional.linear(s, ee.weight, ee.bias)
-                xe_t = xs_t * tvp if tvp is not None else xs_t
+                tvp_t = nn.functional.linear(s, tl.weight, tl.bias) if tl is not None else tvp
+                xe_t = xs_t * tvp_t if tvp_t is not None else xs_t
                 g_lat = None
                 if g_upd is not None:
                     g_lat = g_upd
@@ -301,12 +307,14 @@ class _LayerChain(torch.autograd.Function):
                                                       xe_t, need_s or need_tvp)
                 if need_V and Vf is not V:
                     gV = gV.reshape(V.shape[0], -1, 16).sum(-1)
-                g_tvp = g_xe * xs_t if need_tvp else None
+                g_tvp = g_xe * xs_t if need_tvp or inner else None
                 if need_s:
-                    g_x = (g_xe * tvp if tvp is not None else g_xe) @ ee.weight
+                    g_x = (g_xe * tvp_t if tvp_t is not None else g_xe) @ ee.weight
+                    if inner:
+                        g_x = g_x + g_tvp @ tl.weight
                     g_s = g_x if g_s is None else g_s + g_x
-            return (g_s, gV.reshape(V.shape) if need_V else None, g_tvp, geY.reshape(eY.shape) if need_eY else None,
-                    None, None, None)
+            return (g_s, gV.reshape(V.shape) if need_V else None, g_tvp if need_tvp else None,
+                    geY.reshape(eY.shape) if need_eY else None, None, None, None, None)
         ws = None
         if g_upd is not None or g_tv is not None:
             ws, wt, _ = _tail_weights(layer, s.shape[1])
@@ -328,21 +336,22 @@ class _LayerChain(torch.autograd.Function):
             g_nt = g_nt.contiguous() if g_nt is not None else V.new_zeros(V.shape[0], layer.irreps_dim)
             g_nt[:, :F] += cols
         gV, geY, _, g_x, g_tvp = K.edge_tp_proj_backward(g_nt, V, eY, w, cfg, proj, need_V, need_eY, False, xs,
-                                                         need_s, tvp, need_tvp)
-        g_tvp = g_tvp if need_tvp else None
+                                                         need_s, tvp, need_tvp or inner)
         g_s = None
         if need_s:
-            # g_s = g_upd W_s + [g_tv | g_x] [T W_s ; W_env]: the two 16-wide gradients in one product
-            # accumulated into the first (one pass over the (E, S) result instead of two)
+            # g_s = g_upd W_s + [g_tv | g_x | g_tvp] [T W_s ; W_env ; W_tvp]: the 16-wide gradients in
+            # one product accumulated into the first (one pass over the (E, S) result instead of
+            # one per gradient)
+            heads, mats = [g_x], [ee.weight]
             if g_tv is not None:
-                g_s = _row_grad(torch.cat([g_tv, g_x], dim=1), torch.cat([tenv.weight @ ws, ee.weight], dim=0),
-                                _row_grad(g_upd, ws) if g_upd is not None else None)
-            elif g_upd is not None:
-                g_s = _row_grad(g_x, ee.weight, _row_grad(g_upd, ws))
-            else:
-                g_s = _row_grad(g_x, ee.weight)
-        return (g_s, gV.reshape(V.shape) if need_V else None, g_tvp, geY.reshape(eY.shape) if need_eY else None,
-                None, None, None)
+                heads, mats = [g_tv] + heads, [tenv.weight @ ws] + mats
+            if inner:
+                heads, mats = heads + [g_tvp], mats + [tl.weight]
+            g_s = _row_grad(torch.cat(heads, dim=1) if len(heads) > 1 else heads[0],
+                            torch.cat(mats, dim=0) if len(mats) > 1 else mats[0],
+                            _row_grad(g_upd, ws) if g_upd is not None else None)
+        return (g_s, gV.reshape(V.shape) if need_V else None, g_tvp if need_tvp else None,
+                geY.reshape(eY.shape) if need_eY else None, None, None, None, None)
 
 
 def _tail_ok(layer, s, nt_dim):
@@ -356,9 +365,17 @@ def _tail_ok(layer, s, nt_dim):
             and not (torch.is_grad_enabled() and any(p.requires_grad for p in params)))
 
 
-def _layer_chain(layer, s, V, tvp, eY):
+def _env_lin_ok(lin, s):
+    """Whether ``lin`` (an env layer of the scalars ``s``) can run inside ``_LayerChain``."""
+    return (isinstance(lin, nn.Linear) and lin.bias is not None and lin.weight.dtype == torch.float32
+            and lin.bias.dtype == torch.float32 and lin.in_features == s.shape[1]
+            and not (torch.is_grad_enabled() and (lin.weight.requires_grad or lin.bias.requires_grad)))
+
+
+def _layer_chain(layer, s, V, tvp, eY, tvp_lin=None):
     """(updated, nt, tv) of ``_LayerChain`` when every parameter the layer reads is frozen and the
-    fused product + projection applies; None otherwise."""
+    fused product + projection applies; None otherwise.  ``tvp_lin``, given in place of ``tvp``,
+    is the env layer whose output on ``s`` is ``tvp`` (formed inside the Function when frozen)."""
     tp, lin, ee = layer.tp, layer.tp_linear, layer.env_embed
     params = [tp.weight, lin.weight, ee.weight] + ([ee.bias] if ee.bias is not None else [])
     if (layer._proj_scale is None or ee.bias is None or not V.is_cuda or V.dtype != torch.float32
@@ -369,8 +386,10 @@ def _layer_chain(layer, s, V, tvp, eY):
     w = tp.weight.reshape(tp.num_paths_full, tp.channels).index_select(0, tp.kept_paths)
     proj = lin.weight.reshape(-1, 16) * (layer._proj_scale * lin.output_scale if lin.output_scale != 1.0
                                          else layer._proj_scale)
+    if tvp_lin is not None and not _env_lin_ok(tvp_lin, s):
+        tvp, tvp_lin = tvp_lin(s), None
     return _LayerChain.apply(s.contiguous(), V.contiguous(), tvp.contiguous() if tvp is not None else None,
-                             eY.contiguous(), layer, w, proj)
+                             eY.contiguous(), layer, w, proj, tvp_lin)
 
 
 def _layer_tail(layer, s, nt):
@@ -485,16 +504,17 @@ class PairEmbedding(nn.Module):
         self.irreps_dim = Irreps(irreps_from_l_max(l_max, num_tensor_features)).dim
         self.tensor_env = nn.Linear(num_scalar_features, num_tensor_features, dtype=config.ftype)
 
-    def parts(self, Z, bond_dist, bond_diff, edge_index):
+    def parts(self, Z, bond_dist, bond_diff, edge_index, env=True):
         """(scalar features, env weights, harmonics, cutoff envelope): the embedding before the
-        tensor track ``harmonics x env weights`` is formed."""
+        tensor track ``harmonics x env weights`` is formed (env weights None with ``env=False``:
+        ``tensor_env`` of the scalar features, left to the caller)."""
         src, dst = edge_index[:, 0], edge_index[:, 1]
         edge_cutoff = self.cutoff_fn(bond_dist)
         edge_radial = self.radial_basis(bond_dist) * edge_cutoff.unsqueeze(-1)
         edge_angular = self.spherical_harmonics(bond_diff / (bond_dist.unsqueeze(-1) + 1e-8))
         type_embed = _type_pair_embedding(self.type_embedding, Z[src], Z[dst])
         scalar_features = _silu_stack(self.scalar_mlp, torch.cat([edge_radial, type_embed], dim=-1))
-        return scalar_features, self.tensor_env(scalar_features), edge_angular, edge_cutoff
+        return scalar_features, self.tensor_env(scalar_features) if env else None, edge_angular, edge_cutoff
 
     def forward(self, Z, bond_dist, bond_diff, edge_index):
         scalar_features, env_weights, edge_angular, edge_cutoff = self.parts(Z, bond_dist, bond_diff, edge_index)
@@ -653,10 +673,11 @@ class Allegro(nn.Module):
 
     def encode(self, Z, bond_dist, bond_diff, edge_index):
         emb = self.embedding
-        scalars, env0, edge_angular, edge_cutoff = emb.parts(Z, bond_dist, bond_diff, edge_index)
+        scalars, _, edge_angular, edge_cutoff = emb.parts(Z, bond_dist, bond_diff, edge_index, env=False)
         # the tensor track enters the first layer as the harmonics shared by the channels with the
-        # env weights as its channel scale (folded into the layer's product), when the layer takes it
-        tensors, tv = edge_angular, env0
+        # env weights as its channel scale (folded into the layer's product), when the layer takes
+        # it; the env weights are then formed inside the layer's Function (``env_lin``)
+        tensors, tv, env_lin = edge_angular, None, emb.tensor_env
         u = edge_cutoff.unsqueeze(-1)
         per_layer = []
         n = int(Z.shape[0])
@@ -665,10 +686,12 @@ class Allegro(nn.Module):
             key = layer.avg_num_neighbors
             if key not in src_Y:
                 src_Y[key] = layer.source_harmonics(edge_angular, edge_index, n)
-            chained = _layer_chain(layer, scalars, tensors, tv, src_Y[key])
+            chained = _layer_chain(layer, scalars, tensors, tv, src_Y[key], env_lin)
             if chained is not None:
                 scalars, tensors, tv = chained
             else:
+                if env_lin is not None:
+                    tv = env_lin(scalars)
                 if tensors is edge_angular:  # first layer: form the tensor track
                     tensors = _env_weight_harmonics(edge_angular, tv, emb.l_max, emb.num_tensor_features,
                                                     emb.irreps_dim)
@@ -676,6 +699,7 @@ class Allegro(nn.Module):
                     tensors = _scale_by_channel(tensors, tv, layer.l_max, layer.num_tensor_features)
                 tv = None
                 scalars, tensors = layer(scalars, tensors, edge_angular, edge_index, n)
+            env_lin = None
             per_layer.append(scalars)
         # every layer's scalars times the cutoff envelope, in one pass over the stacked features (its
         # backward reads one contiguous gradient; each layer then takes its slice in place)
