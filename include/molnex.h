@@ -755,6 +755,19 @@ int mnx_channel_outer_f32(const float* y, const float* s, int64_t E, int32_t D, 
                           mnx_stream_t stream);
 int mnx_channel_outer_bwd_f32(const float* grad, const float* y, const float* s, int64_t E, int32_t D, int32_t F,
                               float* grad_y, float* grad_s, mnx_stream_t stream);
+/* The same product with one component over a stack of L inputs (the cutoff */
+/* envelope on Allegro's per-layer scalar features and their stack,         */
+/* src/molzoo/allegro.py:628-641): s is a host array of L device pointers   */
+/* to [E][F] inputs; out[e][l][c] = y[e] * s_l[e][c] (out [E][L][F]);        */
+/* backward grad_s_l[e][c] = grad[e][l][c] y[e] (grad_s a host array of L   */
+/* device pointers, or NULL), grad_y[e] = sum_l sum_c grad[e][l][c]          */
+/* s_l[e][c] (NULL: not formed), one pass.  1 <= L <= 8; F a multiple of 4   */
+/* with F / 4 a power of two <= 64; every [E][F] and [E][L][F] array 16-byte */
+/* aligned.                                                                   */
+int mnx_channel_outer_stack_f32(const float* y, const float* const* s, int32_t L, int64_t E, int32_t F, float* out,
+                                mnx_stream_t stream);
+int mnx_channel_outer_stack_bwd_f32(const float* grad, const float* y, const float* const* s, int32_t L, int64_t E,
+                                    int32_t F, float* grad_y, float* const* grad_s, mnx_stream_t stream);
 
 #ifdef __cplusplus
 }

@@ -122,6 +122,8 @@ SIGNATURES = {
     "mnx_channel_scale_bwd_f32": (C.c_int, [vp, vp, vp, c_i64, c_i32, c_i32, vp, vp, vp]),
     "mnx_channel_outer_f32": (C.c_int, [vp, vp, c_i64, c_i32, c_i32, vp, vp]),
     "mnx_channel_outer_bwd_f32": (C.c_int, [vp, vp, vp, c_i64, c_i32, c_i32, vp, vp, vp]),
+    "mnx_channel_outer_stack_f32": (C.c_int, [vp, vp, c_i32, c_i64, c_i32, vp, vp]),
+    "mnx_channel_outer_stack_bwd_f32": (C.c_int, [vp, vp, vp, c_i32, c_i64, c_i32, vp, vp, vp]),
     "mnx_edge_tp_bwd_workspace_bytes": (c_sz, [c_i32, c_i32, c_i64]),
     "mnx_edge_tp_bwd_f32": (C.c_int, [c_i32, c_i32, vp, vp, vp, vp, vp, c_i64, vp, vp, vp, vp, vp, c_sz, vp]),
     "mnx_edge_tp_proj_info": (c_i32, [c_i32, vp]),

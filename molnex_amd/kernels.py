@@ -2609,6 +2609,69 @@ def _co2_bwd(ctx, ggy, ggs):
 channel_outer_backward.register_autograd(_co2_bwd, setup_context=_co2_setup)
 
 
+def _stack_args(y: Tensor, s, what: str):
+    L = len(s)
+    if not 1 <= L <= 8 or y.dtype != torch.float32 or y.numel() != (s[0].shape[0] if L else 0):
+        raise ValueError(f"{what}: y must be float32 with one entry per row and 1 to 8 inputs")
+    E, F = s[0].shape if s[0].dim() == 2 else (-1, -1)
+    if F < 4 or F % 4 or (F // 4) & (F // 4 - 1) or F > 256:
+        raise ValueError(f"{what}: inputs must be (E, F) with F / 4 a power of two <= 64")
+    ss = [_cs_rows(t, F, "s") for t in s]
+    if any(t.shape[0] != E for t in ss):
+        raise ValueError(f"{what}: inputs must all have the same number of rows")
+    return y.reshape(-1).contiguous(), ss, E, F
+
+
+def _ptr_array(ts) -> C.c_void_p:
+    return C.cast((C.c_void_p * len(ts))(*[t.data_ptr() for t in ts]), C.c_void_p)
+
+
+@torch.library.custom_op("molix::channel_outer_stack", mutates_args=(), device_types="cuda")
+def channel_outer_stack(y: Tensor, s: list[Tensor]) -> Tensor:
+    """``stack([y * s_l for s_l in s], 1)`` for a per-edge factor ``y`` (E rows of one entry) and
+    L (E, F) inputs, (E, L, F) in one pass: the cutoff envelope on Allegro's per-layer scalar
+    features and their stack (src/molzoo/allegro.py:628-641).  No autograd of its own; the
+    backward is ``channel_outer_stack_backward``."""
+    _require_gpu("channel_outer_stack", y, *s)
+    ys, ss, E, F = _stack_args(y, s, "channel_outer_stack")
+    out = ys.new_empty(E, len(ss), F)
+    check(_lib.load().mnx_channel_outer_stack_f32(ptr(ys), _ptr_array(ss), len(ss), E, F, ptr(out), _stream(ys)),
+          "channel_outer_stack")
+    return out
+
+
+@channel_outer_stack.register_fake
+def _(y, s):
+    return y.new_empty(s[0].shape[0], len(s), s[0].shape[1])
+
+
+@torch.library.custom_op("molix::channel_outer_stack_backward", mutates_args=(), device_types="cuda")
+def channel_outer_stack_backward(grad: Tensor, y: Tensor, s: list[Tensor], need_y: bool,
+                                 need_s: bool) -> list[Tensor]:
+    """``[grad y, grad s_0, ..., grad s_{L-1}]`` of ``channel_outer_stack`` in one pass: grad y
+    (shaped like ``y``) ``= sum_l sum_c grad[:, l, c] s_l[:, c]``, grad s_l ``= grad[:, l] y``;
+    empty tensors for gradients not requested."""
+    _require_gpu("channel_outer_stack_backward", grad, y, *s)
+    ys, ss, E, F = _stack_args(y, s, "channel_outer_stack_backward")
+    L = len(ss)
+    if grad.dtype != torch.float32 or tuple(grad.shape) != (E, L, F):
+        raise ValueError(f"channel_outer_stack_backward: grad must be float32 ({E}, {L}, {F})")
+    g = _aligned16(grad)
+    gy = torch.empty_like(ys) if need_y else g.new_empty(0)
+    gs = [torch.empty_like(t) for t in ss] if need_s else [g.new_empty(0) for _ in ss]
+    check(_lib.load().mnx_channel_outer_stack_bwd_f32(ptr(g), ptr(ys), _ptr_array(ss), L, E, F,
+                                                      ptr(gy) if need_y else None,
+                                                      _ptr_array(gs) if need_s else None, _stream(g)),
+          "channel_outer_stack backward")
+    return [gy.reshape(y.shape) if need_y else gy] + gs
+
+
+@channel_outer_stack_backward.register_fake
+def _(grad, y, s, need_y, need_s):
+    return ([y.new_empty(y.shape) if need_y else y.new_empty(0)]
+            + [t.new_empty(t.shape) if need_s else t.new_empty(0) for t in s])
+
+
 # ---------------------------------------------------------------------------
 # Radial edge embedding (Bessel basis x cutoff envelope)
 # ---------------------------------------------------------------------------

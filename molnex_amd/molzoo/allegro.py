@@ -92,6 +92,42 @@ def _times_envelope(scalars: torch.Tensor, u: torch.Tensor) -> torch.Tensor:
     return scalars * u
 
 
+class _EnvelopeStack(torch.autograd.Function):
+    """``stack([s_l * u for s_l in xs], 1)`` (allegro.py:628-641) as one pass each way
+    (``molix::channel_outer_stack``: the stack is never formed on its own, and the envelope's
+    gradient, a sum over layers and channels, comes in the same pass as the features').
+    Differentiated again (create_graph), the backward runs in tracked ops."""
+
+    @staticmethod
+    def forward(ctx, u, *xs):
+        ctx.save_for_backward(u, *xs)
+        return K.channel_outer_stack(u, list(xs))
+
+    @staticmethod
+    def backward(ctx, g):
+        u, *xs = ctx.saved_tensors
+        need_u, need_x = ctx.needs_input_grad[0], any(ctx.needs_input_grad[1:])
+        if torch.is_grad_enabled():
+            gx = [g[:, l] * u for l in range(len(xs))]
+            gu = sum((g[:, l] * x).sum(-1, keepdim=True) for l, x in enumerate(xs)) if need_u else None
+        else:
+            res = K.channel_outer_stack_backward(g.contiguous(), u, list(xs), need_u, need_x)
+            gu, gx = res[0], res[1:]
+        return (gu if need_u else None, *[gx[l] if ctx.needs_input_grad[1 + l] else None for l in range(len(xs))])
+
+
+def _envelope_stack(per_layer, u):
+    """``stack(per_layer, 1) * u[..., None]`` for (E, F) features and the (E, 1) envelope: one
+    pass with ``_EnvelopeStack`` for float32 GPU tensors, else the stack and ``_times_envelope``."""
+    F = per_layer[0].shape[-1]
+    if (u.is_cuda and u.dtype == torch.float32 and u.shape == (per_layer[0].shape[0], 1) and len(per_layer) <= 8
+            and F % 4 == 0 and (F // 4) & (F // 4 - 1) == 0 and F <= 256
+            and all(x.dtype == torch.float32 and x.dim() == 2 and x.shape == per_layer[0].shape for x in per_layer)):
+        return _EnvelopeStack.apply(u, *per_layer)
+    stacked = torch.stack(per_layer, dim=1)
+    return _times_envelope(stacked.reshape(stacked.shape[0], -1), u).reshape(stacked.shape)
+
+
 def _type_pair_embedding(emb: nn.Embedding, zs: torch.Tensor, zd: torch.Tensor) -> torch.Tensor:
     """``cat([emb(zs), emb(zd)], -1)``: with the table frozen (no gradient to it), one row gather
     from the (types^2, 2 dim) table of all ordered type pairs (``molix::gather_rows``) instead of two
@@ -701,10 +737,8 @@ class Allegro(nn.Module):
                 scalars, tensors = layer(scalars, tensors, edge_angular, edge_index, n)
             env_lin = None
             per_layer.append(scalars)
-        # every layer's scalars times the cutoff envelope, in one pass over the stacked features (its
-        # backward reads one contiguous gradient; each layer then takes its slice in place)
-        stacked = torch.stack(per_layer, dim=1)
-        return _times_envelope(stacked.reshape(stacked.shape[0], -1), u).reshape(stacked.shape)
+        # every layer's scalars times the cutoff envelope, written into the stack in one pass
+        return _envelope_stack(per_layer, u)
 
     def forward(self, td=None, *, Z=None, bond_dist=None, bond_diff=None, edge_index=None):
         if td is None:

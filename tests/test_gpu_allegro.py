@@ -192,6 +192,71 @@ def test_channel_outer_first_and_second_order_vs_fp64():
             assert _rel(a, b) <= 1e-6, (E, D, F, name, _rel(a, b))
 
 
+def test_envelope_stack_first_and_second_order_vs_fp64():
+    """The cutoff envelope written into the per-layer stack in one pass (molix::channel_outer_stack
+    and its one-pass backward, via the encoder's Function) against float64 torch: forward, the
+    gradients of the envelope and of every layer's features (non-contiguous and offset inputs
+    included), and the second-order terms (tracked backward); L = 1 .. 8, F = 4 .. 256."""
+    import molnex_amd.kernels as K
+    from molnex_amd.molzoo.allegro import _envelope_stack
+
+    g = torch.Generator().manual_seed(6)
+    for E, L, F in ((517, 2, 64), (301, 3, 16), (64, 1, 4), (33, 8, 256), (1, 2, 8)):
+        u64 = torch.rand(E, 1, generator=g, dtype=torch.float64)
+        xs64 = [torch.randn(E, F, generator=g, dtype=torch.float64) for _ in range(L)]
+        w64 = torch.randn(E, L, F, generator=g, dtype=torch.float64)
+        r = [torch.randn(E, F, generator=g, dtype=torch.float64) for _ in range(L)]
+        ru = torch.randn(E, 1, generator=g, dtype=torch.float64)
+
+        def run(fn, u, xs, w, second):
+            u = u.clone().requires_grad_(True)
+            xs = [x.clone().requires_grad_(True) for x in xs]
+            out = fn(xs, u)
+            grads = torch.autograd.grad((out * w).sum(), [u] + xs, create_graph=second)
+            if not second:
+                return (out,) + grads
+            tot = (grads[0] * ru.to(u)).sum() + sum((gx * rr.to(gx)).sum() for gx, rr in zip(grads[1:], r))
+            return (out,) + grads + torch.autograd.grad(tot, [u] + xs)
+
+        ref_fn = lambda xs, u: torch.stack(xs, 1) * u.unsqueeze(-1)  # noqa: E731
+        dev = (u64.float().to(DEV), [x.float().to(DEV) for x in xs64], w64.float().to(DEV))
+        for second in (False, True):
+            ref = run(ref_fn, u64, xs64, w64, second)
+            got = run(_envelope_stack, *dev, second)
+            assert len(got) == len(ref)
+            for k, (a, b) in enumerate(zip(got, ref)):
+                assert _rel(a, b) <= 2e-6, (E, L, F, second, k, _rel(a, b))
+        # inputs that are strided or offset views go through a contiguous, aligned copy
+        base = torch.randn(E, 2 * F + 1, generator=g).to(DEV)
+        xv = [base[:, 1:F + 1], base[:, F + 1:]] * ((L + 1) // 2)
+        xv = xv[:L]
+        out = K.channel_outer_stack(dev[0], xv)
+        assert _rel(out, torch.stack([x.double().cpu() for x in xv], 1) * u64.unsqueeze(-1)) <= 1e-6
+        res = K.channel_outer_stack_backward(dev[2], dev[0], xv, True, False)
+        assert res[0].shape == (E, 1) and all(t.numel() == 0 for t in res[1:])
+        ref_u = sum((w64[:, l] * xv[l].double().cpu()).sum(-1, keepdim=True) for l in range(L))
+        assert _rel(res[0], ref_u) <= 1e-6
+
+
+def test_envelope_stack_opcheck_and_errors():
+    import molnex_amd.kernels as K
+
+    g = torch.Generator().manual_seed(7)
+    u = torch.rand(37, 1, generator=g).to(DEV)
+    xs = [torch.randn(37, 16, generator=g).to(DEV) for _ in range(3)]
+    gr = torch.randn(37, 3, 16, generator=g).to(DEV)
+    torch.library.opcheck(torch.ops.molix.channel_outer_stack, (u, xs))
+    torch.library.opcheck(torch.ops.molix.channel_outer_stack_backward, (gr, u, xs, True, True))
+    empty = K.channel_outer_stack(u[:0], [x[:0] for x in xs])
+    assert empty.shape == (0, 3, 16)
+    with pytest.raises(ValueError):
+        K.channel_outer_stack(u, xs * 3)  # 9 inputs
+    with pytest.raises(ValueError):
+        K.channel_outer_stack(u, [torch.randn(37, 12, device=DEV)])  # F / 4 not a power of two
+    with pytest.raises(ValueError):
+        K.channel_outer_stack(u, [xs[0], xs[1][:36]])
+
+
 def test_allegro_rotation_invariant_and_contract():
     """Scalar edge features are invariant under a rotation of the positions (the reference checks
     rtol = atol = 1e-4; fp32 here stays far inside), and the GraphBatch contract writes
