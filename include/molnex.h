@@ -550,6 +550,13 @@ int mnx_edge_weights_bwd_pairs_f32(const float* grad_w, const int32_t* pairs, in
 int mnx_edge_weights_bwd_cols_f32(const float* grad_w, int64_t ld, const int32_t* pairs, int64_t num_rows,
                                   int32_t N, const uint16_t* frag, int32_t K, float* grad_h, int32_t accumulate,
                                   mnx_stream_t stream);
+/* The same written into (or, accumulate != 0, added to) a column block of a wider result:
+ * grad_h's rows ldh floats apart (ldh >= K, a multiple of 4; grad_h 16-byte aligned), e.g. the
+ * scalar columns of an edge tensor's gradient taking the latent layer's input gradient in place
+ * (src/molzoo/allegro.py:469-473).  mnx_edge_weights_bwd_cols_f32 is this with ldh = K. */
+int mnx_edge_weights_bwd_into_f32(const float* grad_w, int64_t ld, const int32_t* pairs, int64_t num_rows,
+                                  int32_t N, const uint16_t* frag, int32_t K, float* grad_h, int64_t ldh,
+                                  int32_t accumulate, mnx_stream_t stream);
 
 /* ------------------------------------------------------------------------ */
 /* Fused weight gradient of the tensor product and the output layer of the    */

@@ -113,6 +113,7 @@ SIGNATURES = {
                                              vp, c_sz, vp]),
     "mnx_tp_bwd_reduce_gy_f32": (C.c_int, [c_i32, c_i32, c_i64, vp, c_sz, vp, vp]),
     "mnx_edge_weights_bwd_cols_f32": (C.c_int, [vp, c_i64, vp, c_i64, c_i32, vp, c_i32, vp, c_i32, vp]),
+    "mnx_edge_weights_bwd_into_f32": (C.c_int, [vp, c_i64, vp, c_i64, c_i32, vp, c_i32, vp, c_i64, c_i32, vp]),
     "mnx_tp_bwd_gh_supported": (C.c_int, [c_i32, c_i32, c_i32]),
     "mnx_tp_bwd_gh_workspace_bytes": (c_sz, [c_i32, c_i32, c_i64, c_i32, c_i32]),
     "mnx_tp_bwd_gh_rows_f32": (C.c_int, [c_i32, c_i32, vp, vp, vp, vp, vp, vp, vp, vp, c_i64, c_i64, c_i32, vp,

@@ -231,8 +231,9 @@ __global__ __launch_bounds__(kEwFwdThreads) void k_ew_fwd(const float* __restric
 
 // PAIR: row i of the product is the sum of gradient rows pairs[i][0] and pairs[i][1] (the two
 // directed edges that share one row of weights), E the number of pairs.
-// ld: the row stride of gw (N for a whole row; wider for a column slice); accumulate: gh += instead
-// of gh = (the partial products over column slices, added in launch order).
+// ld: the row stride of gw (N for a whole row; wider for a column slice); ldh: the row stride of gh
+// (K, or wider when gh is a column block of a wider tensor); accumulate: gh += instead of gh = (the
+// partial products over column slices, added in launch order).
 // RAGGED: N is not a multiple of the stage width 16 NQ, so the last stage's loads are guarded;
 // otherwise every load is unconditional (rows past E read row 0, their results are not stored),
 // which keeps the loaded values in the registers the products read (a guarded load has to be
@@ -242,7 +243,8 @@ __global__ __launch_bounds__(kEwBwdThreads, T >= 2 ? 3 : 2) void k_ew_bwd(const 
                                                        const f16x8* __restrict__ frag,
                                                        const float* __restrict__ colscale, int K, int nstages,
                                                        const int32_t* __restrict__ pairs,
-                                                       float* __restrict__ gh, int64_t ld, bool accumulate) {
+                                                       float* __restrict__ gh, int64_t ld, int64_t ldh,
+                                                       bool accumulate) {
     constexpr int NQ = 8 / T;
     constexpr int PER = kEwStageVec / kEwBwdThreads;
     __shared__ f16x8 sB[2][kEwStageVec];
@@ -355,7 +357,7 @@ __global__ __launch_bounds__(kEwBwdThreads, T >= 2 ? 3 : 2) void k_ew_bwd(const 
     }
     if (!aok) return;
     const float so = ldexpf(1.f, ecur == kEwNoExp ? 0 : ecur);
-    float* dst = gh + arow * K;
+    float* dst = gh + arow * ldh;
 #pragma unroll
     for (int t = 0; t < T; ++t)
 #pragma unroll
@@ -456,16 +458,25 @@ int mnx_edge_weights_bwd_pairs_f32(const float* grad_w, const int32_t* pairs, in
 int mnx_edge_weights_bwd_cols_f32(const float* grad_w, int64_t ld, const int32_t* pairs, int64_t num_edges,
                                   int32_t N, const uint16_t* frag, int32_t K, float* grad_h, int32_t accumulate,
                                   mnx_stream_t stream) {
+    return mnx_edge_weights_bwd_into_f32(grad_w, ld, pairs, num_edges, N, frag, K, grad_h, K, accumulate, stream);
+}
+
+int mnx_edge_weights_bwd_into_f32(const float* grad_w, int64_t ld, const int32_t* pairs, int64_t num_edges,
+                                  int32_t N, const uint16_t* frag, int32_t K, float* grad_h, int64_t ldh,
+                                  int32_t accumulate, mnx_stream_t stream) {
     clear_error();
     int rc = check_ew(K, N);
     if (rc) return rc;
     MNX_REQUIRE(ld >= N && ld % 4 == 0, "edge weights backward: row stride %lld below the width %d or not a "
                 "multiple of 4", (long long)ld, N);
+    MNX_REQUIRE(ldh >= K && ldh % 4 == 0, "edge weights backward: output row stride %lld below the width %d or "
+                "not a multiple of 4", (long long)ldh, K);
     MNX_REQUIRE(N % 8 == 0, "edge weights backward: output width %d not a multiple of 8", N);
     MNX_REQUIRE(num_edges >= 0 && num_edges < (int64_t(1) << 36), "edge count out of range");
     if (num_edges == 0) return MNX_OK;
     MNX_REQUIRE(grad_w && frag && grad_h, "null pointer argument");
-    MNX_REQUIRE(((uintptr_t)grad_w | (uintptr_t)frag) % 16 == 0, "grad_w and frag must be 16-byte aligned");
+    MNX_REQUIRE(((uintptr_t)grad_w | (uintptr_t)frag | (uintptr_t)grad_h) % 16 == 0,
+                "grad_w, frag and grad_h must be 16-byte aligned");
     const EwShape sh{K, N};
     const dim3 grid(unsigned(ceil_div(num_edges, kEwBwdRows))), block(kEwBwdThreads);
     const f16x8* f = reinterpret_cast<const f16x8*>(frag);
@@ -481,7 +492,7 @@ int mnx_edge_weights_bwd_cols_f32(const float* grad_w, int64_t ld, const int32_t
     else
         fn = pairs ? (tiles == 1 ? k_ew_bwd<1, true, false> : tiles == 2 ? k_ew_bwd<2, true, false> : k_ew_bwd<4, true, false>)
                    : (tiles == 1 ? k_ew_bwd<1, false, false> : tiles == 2 ? k_ew_bwd<2, false, false> : k_ew_bwd<4, false, false>);
-    hipLaunchKernelGGL(fn, grid, block, 0, s, grad_w, num_edges, N, f, cs, K, sh.stages_b(), pairs, grad_h, ld,
+    hipLaunchKernelGGL(fn, grid, block, 0, s, grad_w, num_edges, N, f, cs, K, sh.stages_b(), pairs, grad_h, ld, ldh,
                        accumulate != 0);
     MNX_CHECK_LAUNCH();
     return MNX_OK;

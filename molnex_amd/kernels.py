@@ -1460,24 +1460,27 @@ def _(grad, weight):
 
 @torch.library.custom_op("molix::edge_weights_backward_acc", mutates_args=("out",), device_types="cuda")
 def edge_weights_backward_acc(grad: Tensor, weight: Tensor, out: Tensor) -> None:
-    """``out += grad @ weight`` in place (``out`` a contiguous (E, K) float32 tensor; ``grad`` may
-    be a column block of a wider tensor): the input-gradient product of ``edge_weights``
-    accumulated into an existing result in the same pass (``mnx_edge_weights_bwd_cols_f32`` with
+    """``out += grad @ weight`` in place (``out`` a float32 (E, K) tensor with unit column stride,
+    16-byte aligned rows a multiple of 4 floats apart, so a column block of a wider tensor too;
+    ``grad`` may be a column block as well): the input-gradient product of ``edge_weights``
+    accumulated into an existing result in the same pass (``mnx_edge_weights_bwd_into_f32`` with
     accumulation), instead of a product and an add."""
     N, K = weight.shape
     if grad.dim() != 2 or grad.shape[1] != N:
         raise ValueError("edge_weights_backward_acc: grad must be (E, N)")
-    if (out.dtype != torch.float32 or out.shape != (grad.shape[0], K) or not out.is_contiguous()
-            or out.data_ptr() % 16 != 0):
-        raise ValueError("edge_weights_backward_acc: out must be a contiguous, 16-byte aligned float32 (E, K)")
+    if (out.dtype != torch.float32 or out.shape != (grad.shape[0], K) or out.data_ptr() % 16 != 0
+            or (out.shape[0] > 1 and (out.stride(1) != 1 or out.stride(0) < K or out.stride(0) % 4 != 0))):
+        raise ValueError("edge_weights_backward_acc: out must be a float32 (E, K) with unit column stride and "
+                         "16-byte aligned rows a multiple of 4 floats apart")
     g = grad.to(torch.float32)
     # rows may be strided (a column block of a wider tensor): unit column stride, a row stride that
     # is a multiple of 4 floats and 16-byte aligned rows are read in place
     if not (g.stride(1) == 1 and g.stride(0) >= N and g.stride(0) % 4 == 0 and g.data_ptr() % 16 == 0):
         g = _aligned16(g)
     frag = _ew_frag(weight, True)
-    check(_lib.load().mnx_edge_weights_bwd_cols_f32(ptr(g), g.stride(0), None, g.shape[0], N, ptr(frag), K,
-                                                    ptr(out), 1, _stream(g)),
+    ldh = out.stride(0) if out.shape[0] > 1 else K
+    check(_lib.load().mnx_edge_weights_bwd_into_f32(ptr(g), g.stride(0), None, g.shape[0], N, ptr(frag), K,
+                                                    ptr(out), ldh, 1, _stream(g)),
           "edge_weights backward (accumulating)")
 
 

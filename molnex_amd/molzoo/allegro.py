@@ -171,9 +171,10 @@ def _row_linear(h, weight, bias=None):
 
 def _row_grad(g, weight, out=None):
     """``g @ weight`` (the input gradient of ``_row_linear``), or ``out += g @ weight`` in the same
-    pass when ``out`` is given."""
+    pass when ``out`` is given (a column block of a wider tensor too)."""
     N, Kd = weight.shape
-    if K.edge_weights_supported(Kd, N) and (out is None or (out.is_contiguous() and out.data_ptr() % 16 == 0)):
+    if K.edge_weights_supported(Kd, N) and (out is None or (out.data_ptr() % 16 == 0 and out.stride(1) == 1
+                                                            and out.stride(0) % 4 == 0)):
         if out is None:
             return K.edge_weights_backward(g, weight)
         K.edge_weights_backward_acc(g, weight, out)
@@ -293,7 +294,7 @@ class _LayerChain(torch.autograd.Function):
     joins the scalars' gradient in the same accumulating product."""
 
     @staticmethod
-    def forward(ctx, s, V, tvp, eY, layer, w, proj, tvp_lin=None):
+    def forward(ctx, s, V, tvp, eY, layer, w, proj, tvp_lin=None, need_tv=True):
         ee, tenv, F = layer.env_embed, layer.tensor_env, layer.num_tensor_features
         if tvp_lin is not None:
             tvp = torch.addmm(tvp_lin.bias, s, tvp_lin.weight.t())
@@ -301,7 +302,8 @@ class _LayerChain(torch.autograd.Function):
         nt = K.edge_tp_proj(V, eY, w, layer.tp.config_id, proj, xs, tvp)  # the product scales by xs tvp
         ws, wt, bc = _tail_weights(layer, s.shape[1])
         upd = _row_grad(nt[:, :F], wt.t().contiguous(), _row_linear(s, ws, bc))
-        tv = torch.addmm(tenv.bias, upd, tenv.weight.t())
+        # the last layer's env weights scale only its tensor output, which an encoder does not return
+        tv = torch.addmm(tenv.bias, upd, tenv.weight.t()) if need_tv else None
         ctx.save_for_backward(s, V, tvp, eY, w, proj, xs)
         ctx.layer, ctx.tvp_lin = layer, tvp_lin
         ctx.set_materialize_grads(False)
@@ -316,7 +318,7 @@ class _LayerChain(torch.autograd.Function):
         need_s, need_V, need_tvp, need_eY = ctx.needs_input_grad[:4]
         need_tvp = need_tvp and tvp is not None and tl is None
         inner = tl is not None and need_s  # tvp formed here from s: its gradient joins g_s
-        nout = 8
+        nout = 9
         if g_upd is None and g_nt is None and g_tv is None:
             return (None,) * nout
         if torch.is_grad_enabled():
@@ -350,7 +352,7 @@ class _LayerChain(torch.autograd.Function):
                         g_x = g_x + g_tvp @ tl.weight
                     g_s = g_x if g_s is None else g_s + g_x
             return (g_s, gV.reshape(V.shape) if need_V else None, g_tvp if need_tvp else None,
-                    geY.reshape(eY.shape) if need_eY else None, None, None, None, None)
+                    geY.reshape(eY.shape) if need_eY else None, None, None, None, None, None)
         ws = None
         if g_upd is not None or g_tv is not None:
             ws, wt, _ = _tail_weights(layer, s.shape[1])
@@ -358,19 +360,18 @@ class _LayerChain(torch.autograd.Function):
             # in place
             g_tv = g_tv.contiguous() if g_tv is not None else None
 
-            def through(wm):
-                # (g_upd + g_tv T) wm as g_upd wm + g_tv (T wm): the latent gradient is never formed
-                tw = tenv.weight @ wm
-                if g_upd is None:
-                    return _row_grad(g_tv, tw)
-                out = _row_grad(g_upd, wm)
-                return _row_grad(g_tv, tw, out) if g_tv is not None else out
+            def through(wm, out):
+                # out += (g_upd + g_tv T) wm as g_upd wm + g_tv (T wm): the latent gradient is never
+                # formed
+                if g_upd is not None:
+                    _row_grad(g_upd, wm, out)
+                if g_tv is not None:
+                    _row_grad(g_tv, tenv.weight @ wm, out)
 
-            cols = through(wt)
             # the incoming gradient of nt is this Function's to consume (the next layer's backward
-            # made it): its scalar columns take the latent part in place
+            # made it): its scalar columns take the latent part in place, in the products' own pass
             g_nt = g_nt.contiguous() if g_nt is not None else V.new_zeros(V.shape[0], layer.irreps_dim)
-            g_nt[:, :F] += cols
+            through(wt, g_nt[:, :F])
         gV, geY, _, g_x, g_tvp = K.edge_tp_proj_backward(g_nt, V, eY, w, cfg, proj, need_V, need_eY, False, xs,
                                                          need_s, tvp, need_tvp or inner)
         g_s = None
@@ -387,7 +388,7 @@ class _LayerChain(torch.autograd.Function):
                             torch.cat(mats, dim=0) if len(mats) > 1 else mats[0],
                             _row_grad(g_upd, ws) if g_upd is not None else None)
         return (g_s, gV.reshape(V.shape) if need_V else None, g_tvp if need_tvp else None,
-                geY.reshape(eY.shape) if need_eY else None, None, None, None, None)
+                geY.reshape(eY.shape) if need_eY else None, None, None, None, None, None)
 
 
 def _tail_ok(layer, s, nt_dim):
@@ -408,10 +409,11 @@ def _env_lin_ok(lin, s):
             and not (torch.is_grad_enabled() and (lin.weight.requires_grad or lin.bias.requires_grad)))
 
 
-def _layer_chain(layer, s, V, tvp, eY, tvp_lin=None):
+def _layer_chain(layer, s, V, tvp, eY, tvp_lin=None, need_tv=True):
     """(updated, nt, tv) of ``_LayerChain`` when every parameter the layer reads is frozen and the
     fused product + projection applies; None otherwise.  ``tvp_lin``, given in place of ``tvp``,
-    is the env layer whose output on ``s`` is ``tvp`` (formed inside the Function when frozen)."""
+    is the env layer whose output on ``s`` is ``tvp`` (formed inside the Function when frozen);
+    with ``need_tv`` false, tv is None (not formed)."""
     tp, lin, ee = layer.tp, layer.tp_linear, layer.env_embed
     params = [tp.weight, lin.weight, ee.weight] + ([ee.bias] if ee.bias is not None else [])
     if (layer._proj_scale is None or ee.bias is None or not V.is_cuda or V.dtype != torch.float32
@@ -425,7 +427,7 @@ def _layer_chain(layer, s, V, tvp, eY, tvp_lin=None):
     if tvp_lin is not None and not _env_lin_ok(tvp_lin, s):
         tvp, tvp_lin = tvp_lin(s), None
     return _LayerChain.apply(s.contiguous(), V.contiguous(), tvp.contiguous() if tvp is not None else None,
-                             eY.contiguous(), layer, w, proj, tvp_lin)
+                             eY.contiguous(), layer, w, proj, tvp_lin, need_tv)
 
 
 def _layer_tail(layer, s, nt):
@@ -718,11 +720,11 @@ class Allegro(nn.Module):
         per_layer = []
         n = int(Z.shape[0])
         src_Y = {}  # the source harmonics depend on the layer only through its normalisation
-        for layer in self.layers:
+        for k, layer in enumerate(self.layers):
             key = layer.avg_num_neighbors
             if key not in src_Y:
                 src_Y[key] = layer.source_harmonics(edge_angular, edge_index, n)
-            chained = _layer_chain(layer, scalars, tensors, tv, src_Y[key], env_lin)
+            chained = _layer_chain(layer, scalars, tensors, tv, src_Y[key], env_lin, k + 1 < len(self.layers))
             if chained is not None:
                 scalars, tensors, tv = chained
             else:

@@ -145,3 +145,14 @@ def test_edge_weights_backward_accumulating_matches_fp64(n, k, e):
     assert float((prod.double() - grad.double() @ weight.double()).norm() / (grad.double() @ weight.double()).norm()) <= 1e-6
     with pytest.raises(ValueError):
         K.edge_weights_backward_acc(grad, weight, torch.empty(e, k + 1, device=DEV))
+    # into a column block of a wider tensor (rows k + 12 floats apart, columns 4 .. 4 + k): the
+    # block takes the product, the columns either side stay as they were
+    wide = torch.randn(e, k + 12, device=DEV, generator=g)
+    before = wide.clone()
+    K.edge_weights_backward_acc(grad, weight, wide[:, 4:4 + k])
+    ref = before[:, 4:4 + k].double() + grad.double() @ weight.double()
+    err = float((wide[:, 4:4 + k].double() - ref).norm() / ref.norm())
+    assert err <= 1e-6, err
+    assert torch.equal(wide[:, :4], before[:, :4]) and torch.equal(wide[:, 4 + k:], before[:, 4 + k:])
+    with pytest.raises(ValueError):
+        K.edge_weights_backward_acc(grad, weight, wide[:, 2:2 + k])  # rows not 16-byte aligned
