@@ -291,7 +291,10 @@ class _LayerChain(torch.autograd.Function):
     tail is linear in its inputs; the product's backward is ``molix::edge_tp``'s, which has second
     derivatives).  With ``tvp_lin`` (the embedding's frozen env layer, for the first layer) the
     env weights ``tvp = tvp_lin(s)`` of the same scalars are formed here, and their input gradient
-    joins the scalars' gradient in the same accumulating product."""
+    joins the scalars' gradient in the same accumulating product.  The fourth output is ``s`` itself:
+    a caller that routes its other use of ``s`` through it (the encoder's stack of per-layer
+    features) hands that gradient to this backward, which accumulates its own products into it
+    instead of leaving autograd an extra pass to add the two."""
 
     @staticmethod
     def forward(ctx, s, V, tvp, eY, layer, w, proj, tvp_lin=None, need_tv=True):
@@ -307,10 +310,10 @@ class _LayerChain(torch.autograd.Function):
         ctx.save_for_backward(s, V, tvp, eY, w, proj, xs)
         ctx.layer, ctx.tvp_lin = layer, tvp_lin
         ctx.set_materialize_grads(False)
-        return upd, nt, tv
+        return upd, nt, tv, s
 
     @staticmethod
-    def backward(ctx, g_upd, g_nt, g_tv):
+    def backward(ctx, g_upd, g_nt, g_tv, g_pass):
         s, V, tvp, eY, w, proj, xs = ctx.saved_tensors
         layer, tl = ctx.layer, ctx.tvp_lin
         ee, tenv, cfg = layer.env_embed, layer.tensor_env, layer.tp.config_id
@@ -320,7 +323,7 @@ class _LayerChain(torch.autograd.Function):
         inner = tl is not None and need_s  # tvp formed here from s: its gradient joins g_s
         nout = 9
         if g_upd is None and g_nt is None and g_tv is None:
-            return (None,) * nout
+            return (g_pass,) + (None,) * (nout - 1)
         if torch.is_grad_enabled():
             lat = layer.latent_mlp[0]
             with torch.enable_grad():
@@ -351,6 +354,8 @@ class _LayerChain(torch.autograd.Function):
                     if inner:
                         g_x = g_x + g_tvp @ tl.weight
                     g_s = g_x if g_s is None else g_s + g_x
+                    if g_pass is not None:
+                        g_s = g_s + g_pass
             return (g_s, gV.reshape(V.shape) if need_V else None, g_tvp if need_tvp else None,
                     geY.reshape(eY.shape) if need_eY else None, None, None, None, None, None)
         ws = None
@@ -384,9 +389,13 @@ class _LayerChain(torch.autograd.Function):
                 heads, mats = [g_tv] + heads, [tenv.weight @ ws] + mats
             if inner:
                 heads, mats = heads + [g_tvp], mats + [tl.weight]
+            # the pass-through output's gradient (the same scalars' other use) is this Function's
+            # to consume: the products accumulate into it
+            acc = g_pass.contiguous() if g_pass is not None else None
+            if g_upd is not None:
+                acc = _row_grad(g_upd, ws, acc)
             g_s = _row_grad(torch.cat(heads, dim=1) if len(heads) > 1 else heads[0],
-                            torch.cat(mats, dim=0) if len(mats) > 1 else mats[0],
-                            _row_grad(g_upd, ws) if g_upd is not None else None)
+                            torch.cat(mats, dim=0) if len(mats) > 1 else mats[0], acc)
         return (g_s, gV.reshape(V.shape) if need_V else None, g_tvp if need_tvp else None,
                 geY.reshape(eY.shape) if need_eY else None, None, None, None, None, None)
 
@@ -410,7 +419,7 @@ def _env_lin_ok(lin, s):
 
 
 def _layer_chain(layer, s, V, tvp, eY, tvp_lin=None, need_tv=True):
-    """(updated, nt, tv) of ``_LayerChain`` when every parameter the layer reads is frozen and the
+    """(updated, nt, tv, s) of ``_LayerChain`` when every parameter the layer reads is frozen and the
     fused product + projection applies; None otherwise.  ``tvp_lin``, given in place of ``tvp``,
     is the env layer whose output on ``s`` is ``tvp`` (formed inside the Function when frozen);
     with ``need_tv`` false, tv is None (not formed)."""
@@ -650,7 +659,7 @@ class AllegroLayer(nn.Module):
         edge_node_Y = self.source_harmonics(edge_angular, edge_index, n_nodes)
         chained = _layer_chain(self, scalar_features, tensor_features, None, edge_node_Y)
         if chained is not None:
-            upd, nt, tv = chained
+            upd, nt, tv, _ = chained
             return upd, _scale_by_channel(nt, tv, self.l_max, F)
         # TP(env_w . V, Y_agg(src)): the per-channel env scaling (allegro.py:447-450) runs inside the
         # product kernel, as TP(s x) = s TP(x) channel by channel
@@ -726,7 +735,10 @@ class Allegro(nn.Module):
                 src_Y[key] = layer.source_harmonics(edge_angular, edge_index, n)
             chained = _layer_chain(layer, scalars, tensors, tv, src_Y[key], env_lin, k + 1 < len(self.layers))
             if chained is not None:
-                scalars, tensors, tv = chained
+                scalars_in = scalars
+                scalars, tensors, tv, passed = chained
+                if per_layer and per_layer[-1] is scalars_in:
+                    per_layer[-1] = passed  # the previous layer's features, routed through this Function
             else:
                 if env_lin is not None:
                     tv = env_lin(scalars)
